@@ -1,0 +1,260 @@
+"""Benchmark of the MI355X GoMLX backend hot path (one GPU).
+
+Prints ONE JSON line.  The headline workload is BASELINE.json configs[1]:
+RMSNorm over the last axis of x [8192, 4096] fp32 (gamma [4096], eps 1e-6) —
+one "step" is one RMSNorm launch over that batch, inputs resident in HBM.
+`value` is GB/s of algorithmic traffic (read x + gamma, write y).  The same line
+carries the other BASELINE workloads under "secondary" (softmax, bf16 RMSNorm,
+LayerNorm, bf16/fp32 DotGeneral, the attention composite), each with its own
+roofline fraction.
+
+Timing: W untimed warmup steps, then K steps bracketed by torch.cuda.synchronize()
+on both sides (wall clock -> ms_per_step), and HIP events recorded on the stream
+the kernels run on (-> average launch duration for "roofline").  Working sets
+below 1 GiB rotate through several input/output buffer sets so the 256 MB
+Infinity Cache cannot serve repeat reads (the rotation count is reported).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "go-darwinml_amd"))
+
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, GB/s
+BF16_PEAK_TFLOPS = 2500.0      # dense MFMA bf16
+FP32_PEAK_TFLOPS = 157.3       # dense MFMA fp32
+ROTATE_BYTES = 1 << 30         # >= 4x the 256 MB MALL per rotation round
+
+
+def parse():
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=200)
+    p.add_argument("--warmup", type=int, default=10)
+    p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    p.add_argument("--no-secondary", action="store_true")
+    p.add_argument("--only", default="", help="comma list of secondary case names")
+    return p.parse_args()
+
+
+class Case:
+    """One workload: `launch(i)` runs step i on the current stream."""
+
+    def __init__(self, name, launch, bytes_per_step=0, flops_per_step=0, bound="hbm",
+                 peak=HBM_PEAK_GBS, dtype="f32", rotation=1, config=None, kernel=""):
+        self.name, self.launch = name, launch
+        self.bytes, self.flops = bytes_per_step, flops_per_step
+        self.bound, self.peak, self.dtype = bound, peak, dtype
+        self.rotation, self.config, self.kernel = rotation, config or {}, kernel
+
+
+def time_case(case: Case, steps: int, warmup: int):
+    import torch
+    stream = torch.cuda.current_stream()
+    for i in range(warmup):
+        case.launch(i)
+    torch.cuda.synchronize()
+    ev0 = torch.cuda.Event(enable_timing=True)
+    ev1 = torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    ev0.record(stream)
+    for i in range(steps):
+        case.launch(i)
+    ev1.record(stream)
+    torch.cuda.synchronize()
+    wall_ms = (time.perf_counter() - t0) * 1e3
+    dev_ms = ev0.elapsed_time(ev1)
+    per_launch_s = dev_ms / steps / 1e3
+    if case.bound == "hbm":
+        achieved = case.bytes / per_launch_s / 1e9
+        unit = "GB/s"
+    else:
+        achieved = case.flops / per_launch_s / 1e12
+        unit = "TFLOP/s"
+    return {
+        "wall_ms": wall_ms,
+        "ms_per_step": wall_ms / steps,
+        "launch_us": per_launch_s * 1e6,
+        "roofline": {"bound": case.bound, "achieved": round(achieved, 2), "peak": case.peak,
+                     "unit": unit, "frac": round(achieved / case.peak, 4), "traffic": None},
+    }
+
+
+def rotation_for(nbytes):
+    return max(1, min(64, -(-ROTATE_BYTES // max(nbytes, 1))))
+
+
+def make_cases(only=None):
+    import torch
+    from gomlx_hip import ops
+
+    dev = torch.device("cuda:0")
+    g = torch.Generator(dev).manual_seed(2001)
+    cases = {}
+
+    def rms_case(dtype, tag):
+        rows, n = 8192, 4096
+        es = 4 if dtype == torch.float32 else 2
+        nbytes = (2 * rows * n + n) * es
+        rot = rotation_for(nbytes)
+        xs = [torch.randn((rows, n), device=dev, generator=g).to(dtype) for _ in range(rot)]
+        ys = [torch.empty_like(xs[0]) for _ in range(rot)]
+        gam = (torch.rand((n,), device=dev, generator=g) + 0.5).to(dtype)
+        return Case(f"rmsnorm_{tag}", lambda i: ops.rmsnorm(xs[i % rot], gam, 1e-6, out=ys[i % rot]),
+                    bytes_per_step=nbytes, dtype=tag, rotation=rot, kernel="rows_reg_kernel",
+                    config={"workload": f"RMSNorm last axis, x [8192,4096] {tag}, gamma [4096], eps 1e-6, fp32 statistics"})
+
+    def ln_case(dtype, tag):
+        rows, n = 8192, 4096
+        es = 4 if dtype == torch.float32 else 2
+        nbytes = (2 * rows * n + 2 * n) * es
+        rot = rotation_for(nbytes)
+        xs = [torch.randn((rows, n), device=dev, generator=g).to(dtype) for _ in range(rot)]
+        ys = [torch.empty_like(xs[0]) for _ in range(rot)]
+        gam = (torch.rand((n,), device=dev, generator=g) + 0.5).to(dtype)
+        bet = (torch.randn((n,), device=dev, generator=g) * 0.1).to(dtype)
+        return Case(f"layernorm_{tag}",
+                    lambda i: ops.layernorm(xs[i % rot], gam, bet, 1e-5, out=ys[i % rot]),
+                    bytes_per_step=nbytes, dtype=tag, rotation=rot, kernel="rows_reg_kernel",
+                    config={"workload": f"LayerNorm last axis, x [8192,4096] {tag}, eps 1e-5"})
+
+    def softmax_case():
+        rows, n = 4096, 1024
+        nbytes = 2 * rows * n * 4
+        rot = rotation_for(nbytes)
+        xs = [torch.randn((rows, n), device=dev, generator=g) * 2 for _ in range(rot)]
+        ys = [torch.empty_like(xs[0]) for _ in range(rot)]
+        return Case("softmax_f32", lambda i: ops.softmax(xs[i % rot], out=ys[i % rot]),
+                    bytes_per_step=nbytes, dtype="f32", rotation=rot, kernel="rows_reg_kernel",
+                    config={"workload": "Softmax last axis, x [4096,1024] fp32 ~ N(0, 2^2)"})
+
+    def dot_case(dtype, tag, peak):
+        B, M, K, N = 8, 2048, 4096, 4096
+        a = (torch.randn((B, M, K), device=dev, generator=g) * 0.125).to(dtype)
+        b = (torch.randn((B, K, N), device=dev, generator=g) * 0.125).to(dtype)
+        c = torch.empty((B, M, N), device=dev, dtype=dtype)
+        return Case(f"dot_general_{tag}", lambda i: ops.gemm(a, b, out=c),
+                    flops_per_step=2 * B * M * N * K, bound="mfma", peak=peak, dtype=tag,
+                    kernel="gemm_bf16_kernel" if tag == "bf16" else "gemm_f32_kernel",
+                    config={"workload": f"DotGeneral [8,2048,4096]x[8,4096,4096] lc=[2] lb=[0] rc=[1] rb=[0], {tag} in, fp32 accumulate, {tag} out"})
+
+    def attention_case():
+        Bh, S, D = 64, 2048, 128
+        q = torch.randn((Bh, S, D), device=dev, generator=g).to(torch.bfloat16)
+        k = torch.randn((Bh, S, D), device=dev, generator=g).to(torch.bfloat16)
+        v = torch.randn((Bh, S, D), device=dev, generator=g).to(torch.bfloat16)
+        s = torch.empty((Bh, S, S), device=dev, dtype=torch.bfloat16)
+        p = torch.empty_like(s)
+        o = torch.empty((Bh, S, D), device=dev, dtype=torch.bfloat16)
+        kt = k.transpose(1, 2)
+
+        def launch(i):
+            ops.gemm(q, kt, out=s)
+            ops.scale_mask_softmax(s, 1.0 / 128 ** 0.5, True, out=p)
+            ops.gemm(p, v, out=o)
+        return Case("attention_bf16", launch, flops_per_step=2 * 2 * Bh * S * S * D, bound="mfma",
+                    peak=BF16_PEAK_TFLOPS, dtype="bf16",
+                    kernel="gemm_bf16_kernel + rows_reg_kernel",
+                    config={"workload": "SDPA causal B4 H16 S2048 D128 bf16: DotGeneral -> fused scale+causal+softmax -> DotGeneral (flops: both GEMMs, full)"})
+
+    builders = {
+        "softmax_f32": softmax_case,
+        "rmsnorm_bf16": lambda: rms_case(torch.bfloat16, "bf16"),
+        "layernorm_f32": lambda: ln_case(torch.float32, "f32"),
+        "layernorm_bf16": lambda: ln_case(torch.bfloat16, "bf16"),
+        "dot_general_bf16": lambda: dot_case(torch.bfloat16, "bf16", BF16_PEAK_TFLOPS),
+        "dot_general_f32": lambda: dot_case(torch.float32, "f32", FP32_PEAK_TFLOPS),
+        "attention_bf16": attention_case,
+    }
+    primary = rms_case(torch.float32, "f32")
+    names = [n for n in builders if not only or n in only]
+    return primary, builders, names
+
+
+def cpu_baseline(seconds_target=10.0):
+    """The oracle's RMSNorm (C, OpenMP, fp64 accumulation) on the host cores, over a
+    bounded sample of the same workload: the first 2048 rows of an [8192, 4096]
+    fp32 input, repeated until ~seconds_target of CPU time has run."""
+    import numpy as np
+    sys.path.insert(0, ROOT)
+    from oracle import oracle as orc
+    from gomlx_hip import synth
+
+    rows, n = 2048, 4096
+    x = synth.normal(2001, (rows, n))
+    gam = synth.uniform_f32(2002, (n,), 0.5, 1.5)
+    orc.rmsnorm(x, gam, 1e-6)  # warm
+    reps, t0 = 0, time.perf_counter()
+    while time.perf_counter() - t0 < seconds_target:
+        orc.rmsnorm(x, gam, 1e-6)
+        reps += 1
+    dt = time.perf_counter() - t0
+    # fp32 in, fp64 out: count the algorithmic fp32 bytes (same unit as the GPU value)
+    nbytes = (2 * rows * n + n) * 4
+    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    return {"value": round(nbytes * reps / dt / 1e9, 3), "unit": "GB/s", "cores": threads,
+            "kind": "port",
+            "sample": f"oracle/oracle.c orc_rmsnorm (OpenMP, fp64 accumulate) on rows 0..2047 of "
+                      f"x [8192,4096] fp32, {reps} repetitions in {dt:.1f} s"}
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU only; --gpus must be 1",
+                          "n_gpus": args.gpus}))
+        sys.exit(2)
+    import torch
+    if not torch.cuda.is_available():
+        print(json.dumps({"error": "no GPU visible"}))
+        sys.exit(1)
+    from gomlx_hip import _lib
+    _lib.load()
+
+    only = set(filter(None, args.only.split(",")))
+    primary, builders, names = make_cases(only)
+    res = time_case(primary, args.steps, args.warmup)
+    secondary = []
+    if not args.no_secondary:
+        for name in names:
+            case = builders[name]()
+            steps = args.steps if case.bound == "hbm" else max(5, args.steps // 20)
+            r = time_case(case, steps, max(2, args.warmup // 2))
+            secondary.append({"name": name, "dtype": case.dtype, "steps": steps,
+                              "launch_us": round(r["launch_us"], 2),
+                              "value": r["roofline"]["achieved"], "unit": r["roofline"]["unit"],
+                              "roofline": r["roofline"], "rotation": case.rotation,
+                              "kernel": case.kernel, "config": case.config})
+            del case
+            torch.cuda.empty_cache()
+    cpu = None if args.no_cpu else cpu_baseline()
+    gbs = primary.bytes * args.steps / (res["wall_ms"] / 1e3) / 1e9
+    line = {
+        "metric": "softmax/RMSNorm GB/s (% HBM peak); bf16 DotGeneral TFLOP/s (% MFMA peak)",
+        "value": round(gbs, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(res["ms_per_step"], 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (torch.randn on device; inputs resident in HBM)",
+        "config": dict(primary.config, rotation=primary.rotation,
+                       kernel=primary.kernel, launch_us=round(res["launch_us"], 2)),
+        "roofline": res["roofline"],
+        "cpu_baseline": cpu,
+        "secondary": secondary,
+    }
+    print(json.dumps(line))
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,111 @@
+// Shared device/host helpers for the gomlx-hip kernels (gfx950, wave64).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "gomlx_hip.h"
+
+namespace ghip {
+
+// ---------------------------------------------------------------------------
+// bf16 stored as raw 16-bit patterns.  Conversion fp32 -> bf16 rounds to nearest
+// even (NaN kept quiet); bf16 -> fp32 is exact.
+// ---------------------------------------------------------------------------
+struct bf16_t {
+  uint16_t bits;
+};
+
+__device__ __host__ __forceinline__ float bf16_to_f32(uint16_t b) {
+  return __uint_as_float(static_cast<uint32_t>(b) << 16);
+}
+
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((u >> 16) | 0x40u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return static_cast<uint16_t>(u >> 16);
+}
+
+// Packs two fp32 into two bf16 (RNE) in one dword: lo in bits 0..15.
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  return static_cast<uint32_t>(f32_to_bf16(lo)) | (static_cast<uint32_t>(f32_to_bf16(hi)) << 16);
+}
+
+// ---------------------------------------------------------------------------
+// Element traits: how many elements one 16-byte vector holds and how to widen.
+// ---------------------------------------------------------------------------
+template <typename T> struct Elem;
+template <> struct Elem<float> {
+  static constexpr int kVec = 4;
+  __device__ static float load1(const float* p) { return *p; }
+  __device__ static void store1(float* p, float v) { *p = v; }
+};
+template <> struct Elem<bf16_t> {
+  static constexpr int kVec = 8;
+  __device__ static float load1(const bf16_t* p) { return bf16_to_f32(p->bits); }
+  __device__ static void store1(bf16_t* p, float v) { p->bits = f32_to_bf16(v); }
+};
+
+// Loads 16 bytes (kVec elements) and widens them to fp32.
+__device__ __forceinline__ void load_vec(const float* p, float* out) {
+  float4 v = *reinterpret_cast<const float4*>(p);
+  out[0] = v.x; out[1] = v.y; out[2] = v.z; out[3] = v.w;
+}
+__device__ __forceinline__ void load_vec(const bf16_t* p, float* out) {
+  uint4 v = *reinterpret_cast<const uint4*>(p);
+  uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    out[2 * i] = __uint_as_float(w[i] << 16);
+    out[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+  }
+}
+__device__ __forceinline__ void store_vec(float* p, const float* v) {
+  *reinterpret_cast<float4*>(p) = make_float4(v[0], v[1], v[2], v[3]);
+}
+__device__ __forceinline__ void store_vec(bf16_t* p, const float* v) {
+  uint4 o;
+  o.x = pack_bf16x2(v[0], v[1]);
+  o.y = pack_bf16x2(v[2], v[3]);
+  o.z = pack_bf16x2(v[4], v[5]);
+  o.w = pack_bf16x2(v[6], v[7]);
+  *reinterpret_cast<uint4*>(p) = o;
+}
+
+// ---------------------------------------------------------------------------
+// Wave64 reductions (butterfly over all 64 lanes; every lane gets the result).
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+  return v;
+}
+
+// exp(x) through the hardware base-2 exponential: exp(x) = 2^(x * log2(e)).
+__device__ __forceinline__ float fast_exp(float x) {
+  return exp2f(x * 1.4426950408889634f);
+}
+
+constexpr int kWave = 64;
+
+}  // namespace ghip
+
+// ---------------------------------------------------------------------------
+// Host-side error plumbing shared by every C entry point.
+// ---------------------------------------------------------------------------
+namespace ghip {
+int set_error(GHipError* err, int code, const char* fmt, ...);
+int check_hip(hipError_t e, GHipError* err, const char* what);
+}  // namespace ghip
+
+#define GHIP_CHECK(expr, err)                                      \
+  do {                                                             \
+    hipError_t _e = (expr);                                        \
+    if (_e != hipSuccess) return ghip::check_hip(_e, (err), #expr); \
+  } while (0)

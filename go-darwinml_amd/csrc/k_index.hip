@@ -1,0 +1,201 @@
+// Integer / indexing kernels: embedding gather, argmin/argmax, iota.
+// All three are bit-exact by construction (copies and integer arithmetic).
+#include "common.h"
+
+namespace ghip {
+
+// ---------------------------------------------------------------------------
+// Embedding gather: out[i] = table[clamp(ids[i])], one wave per output row,
+// 16-byte accesses when the row size and both base pointers allow it.
+// ---------------------------------------------------------------------------
+template <typename V>
+__global__ __launch_bounds__(256) void gather_rows_kernel(const V* __restrict__ table, int64_t nrows,
+                                                          int64_t row_vecs,
+                                                          const int32_t* __restrict__ ids, int64_t n,
+                                                          V* __restrict__ out) {
+  const int64_t r = static_cast<int64_t>(blockIdx.x) * 4 + threadIdx.x / kWave;
+  if (r >= n) return;
+  const int lane = threadIdx.x % kWave;
+  int64_t id = ids[r];
+  id = id < 0 ? 0 : (id > nrows - 1 ? nrows - 1 : id);
+  const V* src = table + id * row_vecs;
+  V* dst = out + r * row_vecs;
+  for (int64_t c = lane; c < row_vecs; c += kWave) dst[c] = src[c];
+}
+
+// ---------------------------------------------------------------------------
+// ArgMin / ArgMax along the middle axis of [outer, n, inner].
+// One thread per (outer, inner) output when inner > 1 (adjacent threads read
+// adjacent columns: coalesced); one wave per row when inner == 1.
+// Order: NaN beats everything (first NaN wins); among numbers the extreme value
+// wins and ties keep the lowest index.
+// ---------------------------------------------------------------------------
+struct ArgBest {
+  float v;
+  int64_t i;
+};
+
+__device__ __forceinline__ ArgBest arg_pick(ArgBest a, ArgBest b, bool is_min) {
+  // Returns the better of a and b (a and b from disjoint index sets).
+  const bool an = isnan(a.v), bn = isnan(b.v);
+  if (an || bn) {
+    if (an && bn) return a.i <= b.i ? a : b;
+    return an ? a : b;
+  }
+  if (a.v == b.v) return a.i <= b.i ? a : b;
+  const bool a_better = is_min ? (a.v < b.v) : (a.v > b.v);
+  return a_better ? a : b;
+}
+
+template <typename T, typename O>
+__global__ __launch_bounds__(256) void argminmax_cols_kernel(const T* __restrict__ x, int64_t outer,
+                                                             int64_t n, int64_t inner, int is_min,
+                                                             O* __restrict__ out) {
+  const int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (t >= outer * inner) return;
+  const int64_t o = t / inner, j = t % inner;
+  const T* xr = x + o * n * inner + j;
+  ArgBest best{Elem<T>::load1(xr), 0};
+  for (int64_t i = 1; i < n; ++i) best = arg_pick(best, ArgBest{Elem<T>::load1(xr + i * inner), i}, is_min);
+  out[t] = static_cast<O>(best.i);
+}
+
+template <typename T, typename O>
+__global__ __launch_bounds__(256) void argminmax_rows_kernel(const T* __restrict__ x, int64_t rows,
+                                                             int64_t n, int is_min,
+                                                             O* __restrict__ out) {
+  const int64_t r = static_cast<int64_t>(blockIdx.x) * 4 + threadIdx.x / kWave;
+  if (r >= rows) return;
+  const int lane = threadIdx.x % kWave;
+  const T* xr = x + r * n;
+  ArgBest best{is_min ? INFINITY : -INFINITY, INT64_MAX};
+  for (int64_t c = lane; c < n; c += kWave) best = arg_pick(best, ArgBest{Elem<T>::load1(xr + c), c}, is_min);
+  // The sentinel (index INT64_MAX) only survives in lanes that saw no element;
+  // a real +-inf ties with it and wins on its lower index.
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) {
+    ArgBest o{__shfl_xor(best.v, off, 64), __shfl_xor(best.i, off, 64)};
+    best = arg_pick(best, o, is_min);
+  }
+  if (lane == 0) out[r] = static_cast<O>(best.i);
+}
+
+// ---------------------------------------------------------------------------
+// Iota.
+// ---------------------------------------------------------------------------
+template <typename O>
+__global__ __launch_bounds__(256) void iota_kernel(O* __restrict__ out, int64_t total, int64_t n,
+                                                   int64_t inner) {
+  const int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (t >= total) return;
+  out[t] = static_cast<O>((t / inner) % n);
+}
+
+template <>
+__global__ __launch_bounds__(256) void iota_kernel<bf16_t>(bf16_t* __restrict__ out, int64_t total,
+                                                           int64_t n, int64_t inner) {
+  const int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (t >= total) return;
+  out[t].bits = f32_to_bf16(static_cast<float>((t / inner) % n));
+}
+
+static inline unsigned blocks_for(int64_t work, int per_block) {
+  return static_cast<unsigned>((work + per_block - 1) / per_block);
+}
+
+}  // namespace ghip
+
+using namespace ghip;
+
+extern "C" int ghip_gather_rows(const void* table, int64_t V, int64_t row_bytes,
+                                const int32_t* ids, int64_t n, void* out, void* stream,
+                                GHipError* err) {
+  if (V <= 0 || row_bytes <= 0 || n < 0)
+    return set_error(err, GHIP_ERR_INVALID_ARG, "gather_rows: bad sizes V=%lld row_bytes=%lld n=%lld",
+                     (long long)V, (long long)row_bytes, (long long)n);
+  if (n == 0) return GHIP_OK;
+  if (!table || !ids || !out) return set_error(err, GHIP_ERR_INVALID_ARG, "gather_rows: null pointer");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const unsigned grid = blocks_for(n, 4);
+  auto al = [](const void* p, unsigned a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; };
+  if (row_bytes % 16 == 0 && al(table, 16) && al(out, 16)) {
+    hipLaunchKernelGGL(gather_rows_kernel<uint4>, dim3(grid), dim3(256), 0, s,
+                       static_cast<const uint4*>(table), V, row_bytes / 16, ids, n,
+                       static_cast<uint4*>(out));
+  } else if (row_bytes % 4 == 0 && al(table, 4) && al(out, 4)) {
+    hipLaunchKernelGGL(gather_rows_kernel<uint32_t>, dim3(grid), dim3(256), 0, s,
+                       static_cast<const uint32_t*>(table), V, row_bytes / 4, ids, n,
+                       static_cast<uint32_t*>(out));
+  } else {
+    hipLaunchKernelGGL(gather_rows_kernel<uint8_t>, dim3(grid), dim3(256), 0, s,
+                       static_cast<const uint8_t*>(table), V, row_bytes, ids, n,
+                       static_cast<uint8_t*>(out));
+  }
+  GHIP_CHECK(hipGetLastError(), err);
+  return GHIP_OK;
+}
+
+template <typename T, typename O>
+static hipError_t launch_arg(const void* x, int64_t outer, int64_t n, int64_t inner, int is_min,
+                             void* out, hipStream_t s) {
+  if (inner == 1) {
+    hipLaunchKernelGGL((argminmax_rows_kernel<T, O>), dim3(blocks_for(outer, 4)), dim3(256), 0, s,
+                       static_cast<const T*>(x), outer, n, is_min, static_cast<O*>(out));
+  } else {
+    hipLaunchKernelGGL((argminmax_cols_kernel<T, O>), dim3(blocks_for(outer * inner, 256)),
+                       dim3(256), 0, s, static_cast<const T*>(x), outer, n, inner, is_min,
+                       static_cast<O*>(out));
+  }
+  return hipGetLastError();
+}
+
+extern "C" int ghip_argminmax(int dtype, const void* x, int64_t outer, int64_t n, int64_t inner,
+                              int is_min, int out_dtype, void* out, void* stream, GHipError* err) {
+  if (outer < 0 || n <= 0 || inner < 0)
+    return set_error(err, GHIP_ERR_INVALID_ARG, "argminmax: reduced axis must be non-empty");
+  if (outer * inner == 0) return GHIP_OK;
+  if (!x || !out) return set_error(err, GHIP_ERR_INVALID_ARG, "argminmax: null pointer");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  hipError_t e;
+  const bool o32 = out_dtype == GHIP_DTYPE_INT32, o64 = out_dtype == GHIP_DTYPE_INT64;
+  if (!o32 && !o64) return set_error(err, GHIP_ERR_UNSUPPORTED, "argminmax: output dtype %d", out_dtype);
+  if (dtype == GHIP_DTYPE_FLOAT32) {
+    e = o32 ? launch_arg<float, int32_t>(x, outer, n, inner, is_min, out, s)
+            : launch_arg<float, int64_t>(x, outer, n, inner, is_min, out, s);
+  } else if (dtype == GHIP_DTYPE_BFLOAT16) {
+    e = o32 ? launch_arg<bf16_t, int32_t>(x, outer, n, inner, is_min, out, s)
+            : launch_arg<bf16_t, int64_t>(x, outer, n, inner, is_min, out, s);
+  } else {
+    return set_error(err, GHIP_ERR_UNSUPPORTED, "argminmax: input dtype %d", dtype);
+  }
+  GHIP_CHECK(e, err);
+  return GHIP_OK;
+}
+
+extern "C" int ghip_iota(int dtype, void* out, int64_t outer, int64_t n, int64_t inner, void* stream,
+                         GHipError* err) {
+  if (outer < 0 || n < 0 || inner < 0) return set_error(err, GHIP_ERR_INVALID_ARG, "iota: negative size");
+  const int64_t total = outer * n * inner;
+  if (total == 0) return GHIP_OK;
+  if (!out) return set_error(err, GHIP_ERR_INVALID_ARG, "iota: null pointer");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const unsigned g = blocks_for(total, 256);
+  switch (dtype) {
+    case GHIP_DTYPE_INT32:
+      hipLaunchKernelGGL(iota_kernel<int32_t>, dim3(g), dim3(256), 0, s, static_cast<int32_t*>(out), total, n, inner);
+      break;
+    case GHIP_DTYPE_INT64:
+      hipLaunchKernelGGL(iota_kernel<int64_t>, dim3(g), dim3(256), 0, s, static_cast<int64_t*>(out), total, n, inner);
+      break;
+    case GHIP_DTYPE_FLOAT32:
+      hipLaunchKernelGGL(iota_kernel<float>, dim3(g), dim3(256), 0, s, static_cast<float*>(out), total, n, inner);
+      break;
+    case GHIP_DTYPE_BFLOAT16:
+      hipLaunchKernelGGL(iota_kernel<bf16_t>, dim3(g), dim3(256), 0, s, static_cast<bf16_t*>(out), total, n, inner);
+      break;
+    default:
+      return set_error(err, GHIP_ERR_UNSUPPORTED, "iota: dtype %d", dtype);
+  }
+  GHIP_CHECK(hipGetLastError(), err);
+  return GHIP_OK;
+}

@@ -1,0 +1,388 @@
+// Row kernels: softmax / log-softmax, attention-score softmax (scale + causal /
+// boolean mask), RMSNorm and LayerNorm over the last axis.
+//
+// All of them are HBM-bound: one read of x, one write of y (plus a [n] parameter
+// vector that stays in L2).  The fast path keeps a whole row in registers, so x is
+// read from HBM exactly once:
+//   * a row is split into 16-byte vectors; vector v of lane l covers elements
+//     [(v*L + l)*VEC, +VEC) where L is the number of lanes on the row, so each
+//     vector step of a wave touches one contiguous 1 KiB span (fully coalesced
+//     128-bit loads/stores);
+//   * rows up to 64*VEC*16 elements (4096 fp32 / 8192 bf16) get one wave each and
+//     reduce with cross-lane butterflies only (no LDS, no barriers);
+//   * longer rows (up to 4x that) get a 4-wave workgroup and one LDS exchange per
+//     reduction;
+//   * anything else (unaligned rows, n not a multiple of the vector width, or
+//     rows beyond the register budget) takes a generic multi-pass kernel.
+// Statistics are fp32 for both fp32 and bf16 I/O.
+#include <stdarg.h>
+
+#include "common.h"
+
+namespace ghip {
+
+enum RowOp { kSoftmax = 0, kLogSoftmax = 1, kRmsNorm = 2, kLayerNorm = 3, kMaskedSoftmax = 4 };
+
+struct RowParams {
+  const void* x;
+  void* y;
+  const void* gamma;
+  const void* beta;
+  const uint8_t* bmask;  // [sq, sk] keep-mask for kMaskedSoftmax (may be null)
+  int64_t rows;
+  int64_t n;
+  int64_t sq;            // rows per attention matrix (kMaskedSoftmax)
+  float eps;
+  float scale;
+  int causal;
+};
+
+template <int WPR>
+__device__ __forceinline__ float row_reduce_sum(float v, float* lds) {
+  v = wave_sum(v);
+  if constexpr (WPR == 1) {
+    return v;
+  } else {
+    const int w = threadIdx.x / kWave;
+    const int lane = threadIdx.x % kWave;
+    if (lane == 0) lds[w] = v;
+    __syncthreads();
+    float t = 0.f;
+#pragma unroll
+    for (int i = 0; i < WPR; ++i) t += lds[i];
+    __syncthreads();
+    return t;
+  }
+}
+
+template <int WPR>
+__device__ __forceinline__ float row_reduce_max(float v, float* lds) {
+  v = wave_max(v);
+  if constexpr (WPR == 1) {
+    return v;
+  } else {
+    const int w = threadIdx.x / kWave;
+    const int lane = threadIdx.x % kWave;
+    if (lane == 0) lds[w] = v;
+    __syncthreads();
+    float t = lds[0];
+#pragma unroll
+    for (int i = 1; i < WPR; ++i) t = fmaxf(t, lds[i]);
+    __syncthreads();
+    return t;
+  }
+}
+
+// One row per WPR waves; a 256-thread workgroup handles 4 / WPR rows.
+template <typename T, int OP, int NV, int WPR>
+__global__ __launch_bounds__(256) void rows_reg_kernel(RowParams p) {
+  constexpr int VEC = Elem<T>::kVec;
+  constexpr int LANES = kWave * WPR;
+  constexpr int ROWS_PER_BLOCK = 4 / WPR;
+  __shared__ float lds[4];
+
+  const int sub = threadIdx.x / LANES;  // row slot within the block
+  const int l = threadIdx.x % LANES;    // lane index within the row
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * ROWS_PER_BLOCK + sub;
+  // With WPR > 1 every thread of the block works on the same row, so the early
+  // exit below never splits a barrier.
+  if (row >= p.rows) return;
+  const int64_t n = p.n;
+  const T* xr = static_cast<const T*>(p.x) + row * n;
+  T* yr = static_cast<T*>(p.y) + row * n;
+
+  float v[NV][VEC];
+  bool live[NV];
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int64_t c0 = (static_cast<int64_t>(i) * LANES + l) * VEC;
+    live[i] = c0 < n;
+  }
+
+  if constexpr (OP == kSoftmax || OP == kLogSoftmax || OP == kMaskedSoftmax) {
+    const int64_t qrow = (OP == kMaskedSoftmax) ? (row % p.sq) : 0;
+    const uint8_t* mrow = (OP == kMaskedSoftmax && p.bmask) ? p.bmask + qrow * n : nullptr;
+    float mx = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const int64_t c0 = (static_cast<int64_t>(i) * LANES + l) * VEC;
+      // Causal: a vector whose first column is past the diagonal is fully masked
+      // and is never read from HBM.
+      const bool skip = (OP == kMaskedSoftmax) && p.causal && c0 > qrow;
+      if (live[i] && !skip) {
+        load_vec(xr + c0, v[i]);
+      } else {
+#pragma unroll
+        for (int j = 0; j < VEC; ++j) v[i][j] = -INFINITY;
+      }
+      if constexpr (OP == kMaskedSoftmax) {
+        if (live[i] && !skip) {
+#pragma unroll
+          for (int j = 0; j < VEC; ++j) {
+            float s = v[i][j] * p.scale;
+            if (p.causal && c0 + j > qrow) s = -INFINITY;
+            if (mrow && !mrow[c0 + j]) s = -INFINITY;
+            v[i][j] = s;
+          }
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < VEC; ++j) mx = fmaxf(mx, v[i][j]);
+    }
+    mx = row_reduce_max<WPR>(mx, lds);
+    float s = 0.f;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+#pragma unroll
+      for (int j = 0; j < VEC; ++j) {
+        if constexpr (OP == kLogSoftmax) {
+          s += fast_exp(v[i][j] - mx);
+        } else {
+          v[i][j] = fast_exp(v[i][j] - mx);
+          s += v[i][j];
+        }
+      }
+    }
+    s = row_reduce_sum<WPR>(s, lds);
+    if constexpr (OP == kLogSoftmax) {
+      const float shift = mx + logf(s);
+#pragma unroll
+      for (int i = 0; i < NV; ++i) {
+#pragma unroll
+        for (int j = 0; j < VEC; ++j) v[i][j] = v[i][j] - shift;
+      }
+    } else {
+      const float inv = 1.0f / s;
+#pragma unroll
+      for (int i = 0; i < NV; ++i) {
+#pragma unroll
+        for (int j = 0; j < VEC; ++j) v[i][j] *= inv;
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const int64_t c0 = (static_cast<int64_t>(i) * LANES + l) * VEC;
+      if (live[i]) store_vec(yr + c0, v[i]);
+    }
+  } else {
+    // RMSNorm / LayerNorm.
+    float s = 0.f;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const int64_t c0 = (static_cast<int64_t>(i) * LANES + l) * VEC;
+      if (live[i]) {
+        load_vec(xr + c0, v[i]);
+      } else {
+#pragma unroll
+        for (int j = 0; j < VEC; ++j) v[i][j] = 0.f;
+      }
+#pragma unroll
+      for (int j = 0; j < VEC; ++j) {
+        if constexpr (OP == kRmsNorm) s += v[i][j] * v[i][j];
+        else s += v[i][j];
+      }
+    }
+    s = row_reduce_sum<WPR>(s, lds);
+    const float inv_n = 1.0f / static_cast<float>(n);
+    float mean = 0.f, rstd;
+    if constexpr (OP == kRmsNorm) {
+      rstd = rsqrtf(s * inv_n + p.eps);
+    } else {
+      mean = s * inv_n;
+      float q = 0.f;
+#pragma unroll
+      for (int i = 0; i < NV; ++i) {
+        if (live[i]) {
+#pragma unroll
+          for (int j = 0; j < VEC; ++j) {
+            const float d = v[i][j] - mean;
+            q += d * d;
+          }
+        }
+      }
+      q = row_reduce_sum<WPR>(q, lds);
+      rstd = rsqrtf(q * inv_n + p.eps);
+    }
+    const T* g = static_cast<const T*>(p.gamma);
+    const T* b = static_cast<const T*>(p.beta);
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const int64_t c0 = (static_cast<int64_t>(i) * LANES + l) * VEC;
+      if (!live[i]) continue;
+      float gv[VEC], bv[VEC];
+      if (g) load_vec(g + c0, gv);
+      if (b) load_vec(b + c0, bv);
+#pragma unroll
+      for (int j = 0; j < VEC; ++j) {
+        float o = (v[i][j] - mean) * rstd;
+        if (g) o *= gv[j];
+        if (b) o += bv[j];
+        v[i][j] = o;
+      }
+      store_vec(yr + c0, v[i]);
+    }
+  }
+}
+
+// Generic fallback: one 256-thread workgroup per row, scalar accesses, several
+// passes over the row (the second and third normally hit L2).
+template <typename T, int OP>
+__global__ __launch_bounds__(256) void rows_generic_kernel(RowParams p) {
+  __shared__ float lds[4];
+  const int64_t row = blockIdx.x;
+  if (row >= p.rows) return;
+  const int64_t n = p.n;
+  const T* xr = static_cast<const T*>(p.x) + row * n;
+  T* yr = static_cast<T*>(p.y) + row * n;
+  const int t = threadIdx.x;
+
+  if constexpr (OP == kSoftmax || OP == kLogSoftmax || OP == kMaskedSoftmax) {
+    const int64_t qrow = (OP == kMaskedSoftmax) ? (row % p.sq) : 0;
+    const uint8_t* mrow = (OP == kMaskedSoftmax && p.bmask) ? p.bmask + qrow * n : nullptr;
+    auto val = [&](int64_t c) -> float {
+      float s = Elem<T>::load1(xr + c);
+      if constexpr (OP == kMaskedSoftmax) {
+        s *= p.scale;
+        if (p.causal && c > qrow) s = -INFINITY;
+        if (mrow && !mrow[c]) s = -INFINITY;
+      }
+      return s;
+    };
+    float mx = -INFINITY;
+    for (int64_t c = t; c < n; c += 256) mx = fmaxf(mx, val(c));
+    mx = row_reduce_max<4>(mx, lds);
+    float s = 0.f;
+    for (int64_t c = t; c < n; c += 256) s += fast_exp(val(c) - mx);
+    s = row_reduce_sum<4>(s, lds);
+    const float shift = mx + logf(s);
+    const float inv = 1.0f / s;
+    for (int64_t c = t; c < n; c += 256) {
+      const float d = val(c);
+      Elem<T>::store1(yr + c, OP == kLogSoftmax ? d - shift : fast_exp(d - mx) * inv);
+    }
+  } else {
+    float s = 0.f;
+    for (int64_t c = t; c < n; c += 256) {
+      const float a = Elem<T>::load1(xr + c);
+      s += (OP == kRmsNorm) ? a * a : a;
+    }
+    s = row_reduce_sum<4>(s, lds);
+    const float inv_n = 1.0f / static_cast<float>(n);
+    float mean = 0.f, rstd;
+    if constexpr (OP == kRmsNorm) {
+      rstd = rsqrtf(s * inv_n + p.eps);
+    } else {
+      mean = s * inv_n;
+      float q = 0.f;
+      for (int64_t c = t; c < n; c += 256) {
+        const float d = Elem<T>::load1(xr + c) - mean;
+        q += d * d;
+      }
+      q = row_reduce_sum<4>(q, lds);
+      rstd = rsqrtf(q * inv_n + p.eps);
+    }
+    const T* g = static_cast<const T*>(p.gamma);
+    const T* b = static_cast<const T*>(p.beta);
+    for (int64_t c = t; c < n; c += 256) {
+      float o = (Elem<T>::load1(xr + c) - mean) * rstd;
+      if (g) o *= Elem<T>::load1(g + c);
+      if (b) o += Elem<T>::load1(b + c);
+      Elem<T>::store1(yr + c, o);
+    }
+  }
+}
+
+static inline bool aligned16(const void* ptr) {
+  return (reinterpret_cast<uintptr_t>(ptr) & 15u) == 0;
+}
+
+template <typename T, int OP, int NV, int WPR>
+static hipError_t launch_reg(const RowParams& p, hipStream_t s) {
+  const int rows_per_block = 4 / WPR;
+  const int64_t blocks = (p.rows + rows_per_block - 1) / rows_per_block;
+  hipLaunchKernelGGL((rows_reg_kernel<T, OP, NV, WPR>), dim3(static_cast<unsigned>(blocks)),
+                     dim3(256), 0, s, p);
+  return hipGetLastError();
+}
+
+template <typename T, int OP>
+static hipError_t launch_rows(const RowParams& p, hipStream_t s) {
+  constexpr int VEC = Elem<T>::kVec;
+  if (p.rows == 0 || p.n == 0) return hipSuccess;
+  const bool vec_ok = (p.n % VEC == 0) && aligned16(p.x) && aligned16(p.y) &&
+                      (!p.gamma || aligned16(p.gamma)) && (!p.beta || aligned16(p.beta));
+  if (vec_ok) {
+    const int64_t w1 = (p.n + kWave * VEC - 1) / (kWave * VEC);    // vectors/lane, 1 wave
+    const int64_t w4 = (p.n + 4 * kWave * VEC - 1) / (4 * kWave * VEC);
+    if (w1 <= 1) return launch_reg<T, OP, 1, 1>(p, s);
+    if (w1 <= 2) return launch_reg<T, OP, 2, 1>(p, s);
+    if (w1 <= 4) return launch_reg<T, OP, 4, 1>(p, s);
+    if (w1 <= 8) return launch_reg<T, OP, 8, 1>(p, s);
+    if (w1 <= 16) return launch_reg<T, OP, 16, 1>(p, s);
+    if (w4 <= 8) return launch_reg<T, OP, 8, 4>(p, s);
+    if (w4 <= 16) return launch_reg<T, OP, 16, 4>(p, s);
+  }
+  hipLaunchKernelGGL((rows_generic_kernel<T, OP>), dim3(static_cast<unsigned>(p.rows)),
+                     dim3(256), 0, s, p);
+  return hipGetLastError();
+}
+
+template <int OP>
+static int dispatch_rows(int dtype, const RowParams& p, void* stream, GHipError* err,
+                         const char* what) {
+  if (p.rows < 0 || p.n < 0) return set_error(err, GHIP_ERR_INVALID_ARG, "%s: negative size", what);
+  if (p.rows > 0 && p.n > 0 && (!p.x || !p.y))
+    return set_error(err, GHIP_ERR_INVALID_ARG, "%s: null pointer", what);
+  if (p.rows > 0x7fffffffLL)
+    return set_error(err, GHIP_ERR_INVALID_ARG, "%s: too many rows (%lld)", what,
+                     static_cast<long long>(p.rows));
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  hipError_t e;
+  if (dtype == GHIP_DTYPE_FLOAT32) e = launch_rows<float, OP>(p, s);
+  else if (dtype == GHIP_DTYPE_BFLOAT16) e = launch_rows<bf16_t, OP>(p, s);
+  else return set_error(err, GHIP_ERR_UNSUPPORTED, "%s: dtype %d not supported", what, dtype);
+  if (e != hipSuccess) return check_hip(e, err, what);
+  return GHIP_OK;
+}
+
+}  // namespace ghip
+
+using namespace ghip;
+
+extern "C" int ghip_softmax_rows(int dtype, const void* x, void* y, int64_t rows, int64_t n,
+                                 int log_softmax, void* stream, GHipError* err) {
+  RowParams p{};
+  p.x = x; p.y = y; p.rows = rows; p.n = n;
+  if (log_softmax) return dispatch_rows<kLogSoftmax>(dtype, p, stream, err, "softmax_rows");
+  return dispatch_rows<kSoftmax>(dtype, p, stream, err, "softmax_rows");
+}
+
+extern "C" int ghip_scale_mask_softmax_rows(int dtype, const void* x, void* y, int64_t rows,
+                                            int64_t sq, int64_t sk, float scale, int causal,
+                                            const uint8_t* bmask, void* stream,
+                                            GHipError* err) {
+  if (sq <= 0 || (rows % sq) != 0)
+    return set_error(err, GHIP_ERR_INVALID_ARG,
+                     "scale_mask_softmax_rows: rows (%lld) must be a multiple of sq (%lld)",
+                     static_cast<long long>(rows), static_cast<long long>(sq));
+  RowParams p{};
+  p.x = x; p.y = y; p.rows = rows; p.n = sk; p.sq = sq; p.scale = scale;
+  p.causal = causal; p.bmask = bmask;
+  return dispatch_rows<kMaskedSoftmax>(dtype, p, stream, err, "scale_mask_softmax_rows");
+}
+
+extern "C" int ghip_rmsnorm_rows(int dtype, const void* x, const void* gamma, void* y,
+                                 int64_t rows, int64_t n, float eps, void* stream,
+                                 GHipError* err) {
+  RowParams p{};
+  p.x = x; p.y = y; p.gamma = gamma; p.rows = rows; p.n = n; p.eps = eps;
+  return dispatch_rows<kRmsNorm>(dtype, p, stream, err, "rmsnorm_rows");
+}
+
+extern "C" int ghip_layernorm_rows(int dtype, const void* x, const void* gamma, const void* beta,
+                                   void* y, int64_t rows, int64_t n, float eps, void* stream,
+                                   GHipError* err) {
+  RowParams p{};
+  p.x = x; p.y = y; p.gamma = gamma; p.beta = beta; p.rows = rows; p.n = n; p.eps = eps;
+  return dispatch_rows<kLayerNorm>(dtype, p, stream, err, "layernorm_rows");
+}

@@ -1,0 +1,156 @@
+"""Direct-op front end: device tensors in, device tensors out, via the C ABI.
+
+torch is used only as the allocator of device memory and as the source of the
+current HIP stream; every computation runs in libgomlx_hip.so.
+"""
+from __future__ import annotations
+
+import torch
+
+from . import _lib
+from ._lib import call
+
+_DT = {
+    torch.float32: _lib.DT_FLOAT32,
+    torch.bfloat16: _lib.DT_BFLOAT16,
+    torch.int32: _lib.DT_INT32,
+    torch.int64: _lib.DT_INT64,
+    torch.bool: _lib.DT_BOOL,
+    torch.uint8: _lib.DT_UINT8,
+}
+
+
+def dtype_code(dt: torch.dtype) -> int:
+    try:
+        return _DT[dt]
+    except KeyError:
+        raise TypeError(f"gomlx_hip: unsupported dtype {dt}") from None
+
+
+def _stream(stream=None) -> int:
+    if stream is None:
+        return torch.cuda.current_stream().cuda_stream
+    return int(stream)
+
+
+def _ptr(t):
+    return None if t is None else t.data_ptr()
+
+
+def _check_dev(*ts):
+    for t in ts:
+        if t is not None and not t.is_cuda:
+            raise ValueError("gomlx_hip ops take device tensors")
+
+
+def _rows(x: torch.Tensor):
+    if not x.is_contiguous():
+        raise ValueError("row kernels need a contiguous input")
+    n = x.shape[-1] if x.dim() else 1
+    return x.numel() // max(n, 1), n
+
+
+def softmax(x: torch.Tensor, log: bool = False, out=None, stream=None) -> torch.Tensor:
+    """Softmax (log-softmax) over the last axis."""
+    _check_dev(x)
+    rows, n = _rows(x)
+    y = torch.empty_like(x) if out is None else out
+    call("ghip_softmax_rows", dtype_code(x.dtype), x.data_ptr(), y.data_ptr(), rows, n,
+         int(log), _stream(stream))
+    return y
+
+
+def scale_mask_softmax(x: torch.Tensor, scale: float, causal: bool, bmask=None, out=None,
+                       stream=None) -> torch.Tensor:
+    """softmax(x * scale + mask) over the last axis of x [..., sq, sk]."""
+    _check_dev(x, bmask)
+    sq, sk = x.shape[-2], x.shape[-1]
+    rows = x.numel() // sk
+    y = torch.empty_like(x) if out is None else out
+    call("ghip_scale_mask_softmax_rows", dtype_code(x.dtype), x.data_ptr(), y.data_ptr(), rows,
+         sq, sk, float(scale), int(causal), _ptr(bmask), _stream(stream))
+    return y
+
+
+def rmsnorm(x: torch.Tensor, gamma=None, eps: float = 1e-6, out=None, stream=None):
+    _check_dev(x, gamma)
+    rows, n = _rows(x)
+    y = torch.empty_like(x) if out is None else out
+    call("ghip_rmsnorm_rows", dtype_code(x.dtype), x.data_ptr(), _ptr(gamma), y.data_ptr(),
+         rows, n, float(eps), _stream(stream))
+    return y
+
+
+def layernorm(x: torch.Tensor, gamma=None, beta=None, eps: float = 1e-5, out=None, stream=None):
+    _check_dev(x, gamma, beta)
+    rows, n = _rows(x)
+    y = torch.empty_like(x) if out is None else out
+    call("ghip_layernorm_rows", dtype_code(x.dtype), x.data_ptr(), _ptr(gamma), _ptr(beta),
+         y.data_ptr(), rows, n, float(eps), _stream(stream))
+    return y
+
+
+def gemm(a: torch.Tensor, b: torch.Tensor, out_dtype=None, out=None, stream=None):
+    """c[b] = a[b] @ b[b] for a [B,M,K] / [M,K], b [B,K,N] / [K,N]; any strides."""
+    _check_dev(a, b)
+    squeeze = a.dim() == 2
+    a3 = a.unsqueeze(0) if a.dim() == 2 else a
+    b3 = b.unsqueeze(0) if b.dim() == 2 else b
+    B, M, K = a3.shape
+    B2, K2, N = b3.shape
+    if K != K2 or (B2 != B and B2 != 1):
+        raise ValueError(f"gemm: shapes {tuple(a.shape)} x {tuple(b.shape)}")
+    odt = out_dtype or a.dtype
+    c = torch.empty((B, M, N), dtype=odt, device=a.device) if out is None else out.view(B, M, N)
+    sb_b = b3.stride(0) if B2 == B else 0
+    call("ghip_gemm_batched", dtype_code(a.dtype), dtype_code(odt), B, M, N, K,
+         a3.data_ptr(), a3.stride(0), a3.stride(1), a3.stride(2),
+         b3.data_ptr(), sb_b, b3.stride(1), b3.stride(2),
+         c.data_ptr(), c.stride(0), c.stride(1), c.stride(2), _stream(stream))
+    return c[0] if squeeze else c
+
+
+def gather_rows(table: torch.Tensor, ids: torch.Tensor, out=None, stream=None):
+    """out[i] = table[clamp(ids[i])] for an embedding table [V, ...]."""
+    _check_dev(table, ids)
+    if ids.dtype != torch.int32 or not ids.is_contiguous() or not table.is_contiguous():
+        raise ValueError("gather_rows: contiguous table and int32 ids required")
+    V = table.shape[0]
+    row_bytes = table[0].numel() * table.element_size()
+    o = torch.empty((ids.numel(),) + tuple(table.shape[1:]), dtype=table.dtype,
+                    device=table.device) if out is None else out
+    call("ghip_gather_rows", table.data_ptr(), V, row_bytes, ids.data_ptr(), ids.numel(),
+         o.data_ptr(), _stream(stream))
+    return o.view(tuple(ids.shape) + tuple(table.shape[1:])) if out is None else o
+
+
+def argminmax(x: torch.Tensor, axis: int, is_min: bool = False, out_dtype=torch.int32,
+              stream=None):
+    _check_dev(x)
+    if not x.is_contiguous():
+        raise ValueError("argminmax: contiguous input required")
+    ax = axis % x.dim()
+    outer = 1
+    for d in x.shape[:ax]:
+        outer *= d
+    inner = 1
+    for d in x.shape[ax + 1:]:
+        inner *= d
+    o = torch.empty(tuple(x.shape[:ax]) + tuple(x.shape[ax + 1:]), dtype=out_dtype,
+                    device=x.device)
+    call("ghip_argminmax", dtype_code(x.dtype), x.data_ptr(), outer, x.shape[ax], inner,
+         int(is_min), dtype_code(out_dtype), o.data_ptr(), _stream(stream))
+    return o
+
+
+def iota(shape, axis: int, dtype=torch.int32, device="cuda", stream=None):
+    o = torch.empty(tuple(shape), dtype=dtype, device=device)
+    ax = axis % len(shape)
+    outer = 1
+    for d in shape[:ax]:
+        outer *= d
+    inner = 1
+    for d in shape[ax + 1:]:
+        inner *= d
+    call("ghip_iota", dtype_code(dtype), o.data_ptr(), outer, shape[ax], inner, _stream(stream))
+    return o

@@ -1,0 +1,347 @@
+/*
+ * CPU oracle for the gomlx-hip backend — TEST INFRASTRUCTURE ONLY (see oracle.h).
+ *
+ * Each function cites the reference code whose semantics it restates.  The
+ * reference runs these ops inside Apple's MPSGraph (closed), and its intended
+ * parity target, GoMLX's pure-Go "simplego" backend, is an un-vendored module
+ * (github.com/gomlx/gomlx@v0.26.1-0.20260223064152-358aaf0bc270,
+ * mpsgraph/gomlx/go.mod:6), so what is restated here is the op semantics the
+ * reference's Go code and tests fix, computed in fp64.
+ */
+#include "oracle.h"
+
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+
+#define ORC_MAX_RANK 16
+
+/* ---------------------------------------------------------------------------
+ * Softmax / log-softmax.
+ * Reference: Function.FusedSoftmax (mpsgraph/gomlx/function.go:2276-2286)
+ * delegates to MPSGraph softMaxWithTensor:axis: (internal/bridge/bridge.m:1448-1461):
+ * y = exp(x - max) / sum(exp(x - max)) along `axis`, output shape = input shape.
+ * log-softmax has no reference op; it is x - max - log(sum(exp(x - max))).
+ * ------------------------------------------------------------------------- */
+void orc_softmax(const float* x, double* y, int64_t outer, int64_t n, int64_t inner,
+                 int log_, int mode) {
+#pragma omp parallel for collapse(2) schedule(static)
+  for (int64_t o = 0; o < outer; ++o) {
+    for (int64_t j = 0; j < inner; ++j) {
+      const float* xr = x + o * n * inner + j;
+      double* yr = y + o * n * inner + j;
+      double mx = -INFINITY;
+      for (int64_t i = 0; i < n; ++i) {
+        double v = xr[i * inner];
+        if (v > mx || isnan(v)) mx = v;
+      }
+      if (mode == ORC_MODE_F32SEQ) {
+        float mxf = (float)mx, s = 0.0f;
+        for (int64_t i = 0; i < n; ++i) s += expf(xr[i * inner] - mxf);
+        for (int64_t i = 0; i < n; ++i) {
+          float d = xr[i * inner] - mxf;
+          yr[i * inner] = log_ ? (double)(d - logf(s)) : (double)(expf(d) / s);
+        }
+      } else {
+        double s = 0.0;
+        for (int64_t i = 0; i < n; ++i) s += exp((double)xr[i * inner] - mx);
+        double ls = log(s);
+        for (int64_t i = 0; i < n; ++i) {
+          double d = (double)xr[i * inner] - mx;
+          yr[i * inner] = log_ ? d - ls : exp(d) / s;
+        }
+      }
+    }
+  }
+}
+
+/* ---------------------------------------------------------------------------
+ * LayerNorm.
+ * Reference: Function.FusedLayerNorm (mpsgraph/gomlx/function.go:2410-2565):
+ * mean = sum(x)/count (:2429-2452), diff = x - mean (:2455), var = sum(diff^2)/count
+ * (:2461-2473), normalized = diff * rsqrt(var + eps) (:2476-2496), then * gamma
+ * (:2533-2546) and + beta (:2549-2562).  Statistics here are fp64 (the reference
+ * keeps them in x's dtype, which the build deliberately does not copy).
+ * ------------------------------------------------------------------------- */
+void orc_layernorm(const float* x, const float* gamma, const float* beta, double* y,
+                   int64_t rows, int64_t n, double eps, int mode) {
+#pragma omp parallel for schedule(static)
+  for (int64_t r = 0; r < rows; ++r) {
+    const float* xr = x + r * n;
+    double* yr = y + r * n;
+    if (mode == ORC_MODE_F32SEQ) {
+      float s = 0.0f;
+      for (int64_t i = 0; i < n; ++i) s += xr[i];
+      float mean = s / (float)n, v = 0.0f;
+      for (int64_t i = 0; i < n; ++i) { float d = xr[i] - mean; v += d * d; }
+      float inv = 1.0f / sqrtf(v / (float)n + (float)eps);
+      for (int64_t i = 0; i < n; ++i) {
+        float o = (xr[i] - mean) * inv;
+        if (gamma) o *= gamma[i];
+        if (beta) o += beta[i];
+        yr[i] = o;
+      }
+    } else {
+      double s = 0.0;
+      for (int64_t i = 0; i < n; ++i) s += xr[i];
+      double mean = s / (double)n, v = 0.0;
+      for (int64_t i = 0; i < n; ++i) { double d = xr[i] - mean; v += d * d; }
+      double inv = 1.0 / sqrt(v / (double)n + eps);
+      for (int64_t i = 0; i < n; ++i) {
+        double o = ((double)xr[i] - mean) * inv;
+        if (gamma) o *= gamma[i];
+        if (beta) o += beta[i];
+        yr[i] = o;
+      }
+    }
+  }
+}
+
+/* ---------------------------------------------------------------------------
+ * RMSNorm: no reference op exists (mpsgraph/gomlx/capabilities.go:134-140 lists
+ * no RMSNorm); GoMLX graphs express it as the primitive chain Mul(x,x) ->
+ * ReduceSum (function.go:1184-1186) -> Div/Mul by 1/n -> Add eps (:808-810) ->
+ * Rsqrt (:686-688) -> Mul x -> Mul gamma (BroadcastInDim :1013-1042).
+ * ------------------------------------------------------------------------- */
+void orc_rmsnorm(const float* x, const float* gamma, double* y, int64_t rows, int64_t n,
+                 double eps, int mode) {
+#pragma omp parallel for schedule(static)
+  for (int64_t r = 0; r < rows; ++r) {
+    const float* xr = x + r * n;
+    double* yr = y + r * n;
+    if (mode == ORC_MODE_F32SEQ) {
+      float s = 0.0f;
+      for (int64_t i = 0; i < n; ++i) s += xr[i] * xr[i];
+      float inv = 1.0f / sqrtf(s / (float)n + (float)eps);
+      for (int64_t i = 0; i < n; ++i) {
+        float o = xr[i] * inv;
+        if (gamma) o *= gamma[i];
+        yr[i] = o;
+      }
+    } else {
+      double s = 0.0;
+      for (int64_t i = 0; i < n; ++i) s += (double)xr[i] * xr[i];
+      double inv = 1.0 / sqrt(s / (double)n + eps);
+      for (int64_t i = 0; i < n; ++i) {
+        double o = (double)xr[i] * inv;
+        if (gamma) o *= gamma[i];
+        yr[i] = o;
+      }
+    }
+  }
+}
+
+/* ---------------------------------------------------------------------------
+ * DotGeneral.
+ * Reference: dotGeneralOutputShape (mpsgraph/gomlx/dotgeneral.go:15-53) fixes the
+ * output order [batch (lhs batch-axes order)..., lhs free (ascending)..., rhs free
+ * (ascending)...] and dtype; classifyAxes (:186-227) pairs lhsContracting[i] with
+ * rhsContracting[i] and lhsBatch[i] with rhsBatch[i]; DotGeneral (:65-164) sums over
+ * the contracting axes.
+ * ------------------------------------------------------------------------- */
+static int in_list(int a, const int* l, int n) {
+  for (int i = 0; i < n; ++i) if (l[i] == a) return 1;
+  return 0;
+}
+
+/* Offsets (in elements) of every multi-index over `axes` (row-major over the
+ * listed axis order) for a tensor with row-major `dims`. */
+static int64_t* axis_offsets(const int64_t* dims, int rank, const int* axes, int naxes,
+                             int64_t* count_out) {
+  int64_t strides[ORC_MAX_RANK];
+  int64_t s = 1;
+  for (int i = rank - 1; i >= 0; --i) { strides[i] = s; s *= dims[i]; }
+  int64_t count = 1;
+  for (int i = 0; i < naxes; ++i) count *= dims[axes[i]];
+  int64_t* off = (int64_t*)malloc(sizeof(int64_t) * (size_t)(count > 0 ? count : 1));
+  for (int64_t c = 0; c < count; ++c) {
+    int64_t rem = c, o = 0;
+    for (int i = naxes - 1; i >= 0; --i) {
+      int64_t d = dims[axes[i]];
+      o += (rem % d) * strides[axes[i]];
+      rem /= d;
+    }
+    off[c] = o;
+  }
+  *count_out = count;
+  return off;
+}
+
+int orc_dot_general(const float* lhs, int lrank, const int64_t* ldims,
+                    const int* lcontract, int nlc, const int* lbatch, int nlb,
+                    const float* rhs, int rrank, const int64_t* rdims,
+                    const int* rcontract, int nrc, const int* rbatch, int nrb,
+                    double* out, int mode) {
+  if (nlc != nrc || nlb != nrb || lrank > ORC_MAX_RANK || rrank > ORC_MAX_RANK) return -1;
+  for (int i = 0; i < nlc; ++i)
+    if (ldims[lcontract[i]] != rdims[rcontract[i]]) return -1;
+  for (int i = 0; i < nlb; ++i)
+    if (ldims[lbatch[i]] != rdims[rbatch[i]]) return -1;
+  int lfree[ORC_MAX_RANK], rfree[ORC_MAX_RANK], nlf = 0, nrf = 0;
+  for (int i = 0; i < lrank; ++i)
+    if (!in_list(i, lcontract, nlc) && !in_list(i, lbatch, nlb)) lfree[nlf++] = i;
+  for (int i = 0; i < rrank; ++i)
+    if (!in_list(i, rcontract, nrc) && !in_list(i, rbatch, nrb)) rfree[nrf++] = i;
+  int64_t nb, nm, nk, nn, tmp;
+  int64_t* lb = axis_offsets(ldims, lrank, lbatch, nlb, &nb);
+  int64_t* lm = axis_offsets(ldims, lrank, lfree, nlf, &nm);
+  int64_t* lk = axis_offsets(ldims, lrank, lcontract, nlc, &nk);
+  int64_t* rb = axis_offsets(rdims, rrank, rbatch, nrb, &tmp);
+  int64_t* rn = axis_offsets(rdims, rrank, rfree, nrf, &nn);
+  int64_t* rk = axis_offsets(rdims, rrank, rcontract, nrc, &tmp);
+#pragma omp parallel for collapse(2) schedule(static)
+  for (int64_t b = 0; b < nb; ++b) {
+    for (int64_t m = 0; m < nm; ++m) {
+      const float* lp = lhs + lb[b] + lm[m];
+      for (int64_t n = 0; n < nn; ++n) {
+        const float* rp = rhs + rb[b] + rn[n];
+        double acc;
+        if (mode == ORC_MODE_F32SEQ) {
+          float s = 0.0f;
+          for (int64_t k = 0; k < nk; ++k) s += lp[lk[k]] * rp[rk[k]];
+          acc = s;
+        } else {
+          acc = 0.0;
+          for (int64_t k = 0; k < nk; ++k) acc += (double)lp[lk[k]] * (double)rp[rk[k]];
+        }
+        out[(b * nm + m) * nn + n] = acc;
+      }
+    }
+  }
+  free(lb); free(lm); free(lk); free(rb); free(rn); free(rk);
+  return 0;
+}
+
+/* Sampled entries of the canonical batched product (a size-independent check
+ * of a full-size DotGeneral: each sampled entry is an fp64 dot product). */
+void orc_dot_sampled(const float* a, int64_t sa_b, int64_t sa_m, int64_t sa_k,
+                     const float* b, int64_t sb_b, int64_t sb_k, int64_t sb_n, int64_t K,
+                     const int64_t* bs, const int64_t* ms, const int64_t* ns, int64_t count,
+                     double* out) {
+#pragma omp parallel for schedule(static)
+  for (int64_t i = 0; i < count; ++i) {
+    const float* ap = a + bs[i] * sa_b + ms[i] * sa_m;
+    const float* bp = b + bs[i] * sb_b + ns[i] * sb_n;
+    double acc = 0.0;
+    for (int64_t k = 0; k < K; ++k) acc += (double)ap[k * sa_k] * (double)bp[k * sb_k];
+    out[i] = acc;
+  }
+}
+
+/* ---------------------------------------------------------------------------
+ * Scaled dot-product attention.
+ * Reference: Function.FusedScaledDotProductAttention (mpsgraph/gomlx/function.go:
+ * 2669-2907): scores = DotGeneral(Q, K) contracting D with batch [B,H] (:2746-2753);
+ * scores *= scale (:2755-2770); causal keeps rowIota >= colIota over [Sq,Sk]
+ * (:2773-2790); boolean mask: Where(mask, scores, -inf) (:2847-2871); softmax over
+ * the last axis (:2880-2886); output = DotGeneral(P, V) (:2888-2897).  GQA repeats
+ * each KV head numHeads/numKVHeads times consecutively (repeatHeads :2911-2956),
+ * so query head h reads KV head h / (H / Hkv).
+ * ------------------------------------------------------------------------- */
+void orc_sdpa(const float* q, const float* k, const float* v, const uint8_t* mask,
+              int64_t B, int64_t H, int64_t Hkv, int64_t Sq, int64_t Sk, int64_t D,
+              double scale, int causal, double* out) {
+  int64_t rep = H / Hkv;
+#pragma omp parallel
+  {
+    double* p = (double*)malloc(sizeof(double) * (size_t)Sk);
+#pragma omp for collapse(3) schedule(static)
+    for (int64_t bb = 0; bb < B; ++bb)
+      for (int64_t h = 0; h < H; ++h)
+        for (int64_t i = 0; i < Sq; ++i) {
+          int64_t hk = h / rep;
+          const float* qr = q + ((bb * H + h) * Sq + i) * D;
+          const float* kb = k + (bb * Hkv + hk) * Sk * D;
+          const float* vb = v + (bb * Hkv + hk) * Sk * D;
+          double mx = -INFINITY;
+          for (int64_t j = 0; j < Sk; ++j) {
+            double s = 0.0;
+            for (int64_t d = 0; d < D; ++d) s += (double)qr[d] * (double)kb[j * D + d];
+            s *= scale;
+            int keep = 1;
+            if (causal && !(i >= j)) keep = 0;
+            if (mask && !mask[i * Sk + j]) keep = 0;
+            p[j] = keep ? s : -INFINITY;
+            if (p[j] > mx) mx = p[j];
+          }
+          double sum = 0.0;
+          for (int64_t j = 0; j < Sk; ++j) { p[j] = exp(p[j] - mx); sum += p[j]; }
+          double* orow = out + ((bb * H + h) * Sq + i) * D;
+          for (int64_t d = 0; d < D; ++d) orow[d] = 0.0;
+          for (int64_t j = 0; j < Sk; ++j) {
+            double w = p[j] / sum;
+            for (int64_t d = 0; d < D; ++d) orow[d] += w * (double)vb[j * D + d];
+          }
+        }
+    free(p);
+  }
+}
+
+/* ---------------------------------------------------------------------------
+ * Embedding gather.
+ * Reference: Function.Gather (mpsgraph/gomlx/gather.go:24-56) takes the
+ * embedding fast path gatherEmbeddingLookup (:61-203) when startIndexMap = [axis],
+ * sliceSizes[axis] = 1, axis collapsed and the other slice sizes full: the result
+ * is the indexed rows of the operand, in index order.  Out-of-range start indices
+ * are clamped into [0, V-1], XLA's Gather rule (the rule of the GoMLX graph
+ * layer; parity with simplego for out-of-range ids is otherwise unpinned).
+ * ------------------------------------------------------------------------- */
+void orc_gather_rows(const void* table, int64_t V, int64_t row_bytes, const int32_t* ids,
+                     int64_t n, void* out) {
+  const unsigned char* t = (const unsigned char*)table;
+  unsigned char* o = (unsigned char*)out;
+  for (int64_t i = 0; i < n; ++i) {
+    int64_t id = ids[i];
+    if (id < 0) id = 0;
+    if (id > V - 1) id = V - 1;
+    memcpy(o + i * row_bytes, t + id * row_bytes, (size_t)row_bytes);
+  }
+}
+
+/* ---------------------------------------------------------------------------
+ * ArgMinMax.
+ * Reference: Function.ArgMinMax (mpsgraph/gomlx/function.go:1204-1242): index of the
+ * max (min) along `axis`, with that axis removed from the output shape.  Tie and
+ * NaN rules are not fixed by the reference (MPSGraph decides); the rule used here
+ * is numpy's (first occurrence; NaN propagates as the extreme).
+ * ------------------------------------------------------------------------- */
+void orc_argminmax(const float* x, int64_t outer, int64_t n, int64_t inner, int is_min,
+                   int64_t* out) {
+  for (int64_t o = 0; o < outer; ++o)
+    for (int64_t j = 0; j < inner; ++j) {
+      const float* xr = x + o * n * inner + j;
+      int64_t best = 0;
+      float bv = xr[0];
+      if (!isnan(bv)) {
+        for (int64_t i = 1; i < n; ++i) {
+          float v = xr[i * inner];
+          if (isnan(v)) { best = i; break; }
+          if (is_min ? (v < bv) : (v > bv)) { bv = v; best = i; }
+        }
+      }
+      out[o * inner + j] = best;
+    }
+}
+
+/* ---------------------------------------------------------------------------
+ * Iota.
+ * Reference: Function.Iota (mpsgraph/gomlx/function.go:1127-1135) ->
+ * coordinateAlongAxis + cast (internal/bridge/bridge.m:237-259): the index along
+ * `iotaAxis`, converted to the output dtype.
+ * ------------------------------------------------------------------------- */
+void orc_iota(double* out, int64_t outer, int64_t n, int64_t inner) {
+  for (int64_t o = 0; o < outer; ++o)
+    for (int64_t i = 0; i < n; ++i)
+      for (int64_t j = 0; j < inner; ++j) out[(o * n + i) * inner + j] = (double)i;
+}
+
+void orc_f32_to_bf16(const float* x, uint16_t* y, int64_t n) {
+  for (int64_t i = 0; i < n; ++i) {
+    uint32_t u;
+    memcpy(&u, &x[i], 4);
+    if ((u & 0x7fffffffu) > 0x7f800000u) { y[i] = (uint16_t)((u >> 16) | 0x40); continue; }
+    uint32_t lsb = (u >> 16) & 1u;
+    u += 0x7fffu + lsb;
+    y[i] = (uint16_t)(u >> 16);
+  }
+}

@@ -1,0 +1,204 @@
+"""ctypes front end of the CPU oracle (oracle/oracle.c) — TEST INFRASTRUCTURE ONLY.
+
+Only tests/, ``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of bench.py
+import this module, as the checker.  Every function returns fp64 results computed
+by the C restatement; inputs are fp32 numpy arrays (bf16 data is passed widened,
+which is exact).
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB_PATH = os.path.join(_HERE, "_build", "liboracle.so")
+_lib = None
+
+MODE_F64 = 0
+MODE_F32SEQ = 1
+
+_f32p = np.ctypeslib.ndpointer(dtype=np.float32, flags="C_CONTIGUOUS")
+_f64p = np.ctypeslib.ndpointer(dtype=np.float64, flags="C_CONTIGUOUS")
+_i64p = np.ctypeslib.ndpointer(dtype=np.int64, flags="C_CONTIGUOUS")
+_i32p = np.ctypeslib.ndpointer(dtype=np.int32, flags="C_CONTIGUOUS")
+_u16p = np.ctypeslib.ndpointer(dtype=np.uint16, flags="C_CONTIGUOUS")
+_i64 = ctypes.c_int64
+_int = ctypes.c_int
+_vp = ctypes.c_void_p
+
+
+def build() -> str:
+    """Compile liboracle.so (gcc + OpenMP) and return its path."""
+    subprocess.run(["make", "-s", "-C", _HERE], check=True)
+    return _LIB_PATH
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(_LIB_PATH):
+            build()
+        L = ctypes.CDLL(_LIB_PATH)
+        L.orc_softmax.argtypes = [_f32p, _f64p, _i64, _i64, _i64, _int, _int]
+        L.orc_layernorm.argtypes = [_f32p, _vp, _vp, _f64p, _i64, _i64, ctypes.c_double, _int]
+        L.orc_rmsnorm.argtypes = [_f32p, _vp, _f64p, _i64, _i64, ctypes.c_double, _int]
+        L.orc_dot_general.argtypes = [_f32p, _int, _i64p, _vp, _int, _vp, _int,
+                                      _f32p, _int, _i64p, _vp, _int, _vp, _int, _f64p, _int]
+        L.orc_dot_general.restype = _int
+        L.orc_dot_sampled.argtypes = [_vp, _i64, _i64, _i64, _vp, _i64, _i64, _i64, _i64,
+                                      _i64p, _i64p, _i64p, _i64, _f64p]
+        L.orc_sdpa.argtypes = [_f32p, _f32p, _f32p, _vp, _i64, _i64, _i64, _i64, _i64, _i64,
+                               ctypes.c_double, _int, _f64p]
+        L.orc_gather_rows.argtypes = [_vp, _i64, _i64, _i32p, _i64, _vp]
+        L.orc_argminmax.argtypes = [_f32p, _i64, _i64, _i64, _int, _i64p]
+        L.orc_iota.argtypes = [_f64p, _i64, _i64, _i64]
+        L.orc_f32_to_bf16.argtypes = [_f32p, _u16p, _i64]
+        _lib = L
+    return _lib
+
+
+def _f32(x) -> np.ndarray:
+    return np.ascontiguousarray(np.asarray(x, dtype=np.float32))
+
+
+def _split(shape, axis):
+    axis = axis % len(shape)
+    outer = int(np.prod(shape[:axis], dtype=np.int64))
+    inner = int(np.prod(shape[axis + 1:], dtype=np.int64))
+    return outer, int(shape[axis]), inner
+
+
+def softmax(x, axis=-1, log=False, mode=MODE_F64) -> np.ndarray:
+    x = _f32(x)
+    y = np.empty(x.shape, np.float64)
+    outer, n, inner = _split(x.shape, axis)
+    lib().orc_softmax(x, y, outer, n, inner, int(log), mode)
+    return y
+
+
+def log_softmax(x, axis=-1, mode=MODE_F64) -> np.ndarray:
+    return softmax(x, axis, log=True, mode=mode)
+
+
+def _opt(a):
+    if a is None:
+        return None, None
+    a = _f32(a).reshape(-1)
+    return a, a.ctypes.data_as(ctypes.c_void_p)
+
+
+def layernorm(x, gamma=None, beta=None, eps=1e-5, mode=MODE_F64) -> np.ndarray:
+    """LayerNorm over the last axis; gamma/beta broadcast over it ([n] or [1, n])."""
+    x = _f32(x)
+    n = x.shape[-1]
+    g, gp = _opt(gamma)
+    b, bp = _opt(beta)
+    y = np.empty(x.shape, np.float64)
+    lib().orc_layernorm(x, gp, bp, y, x.size // n, n, eps, mode)
+    return y
+
+
+def rmsnorm(x, gamma=None, eps=1e-6, mode=MODE_F64) -> np.ndarray:
+    x = _f32(x)
+    n = x.shape[-1]
+    g, gp = _opt(gamma)
+    y = np.empty(x.shape, np.float64)
+    lib().orc_rmsnorm(x, gp, y, x.size // n, n, eps, mode)
+    return y
+
+
+def _int_arr(lst):
+    a = np.ascontiguousarray(np.asarray(list(lst), dtype=np.int32))
+    return a, (a.ctypes.data_as(ctypes.c_void_p) if a.size else None)
+
+
+def dot_general_shape(lshape, lc, lb, rshape, rc, rb):
+    """Output dims [batch..., lhs free..., rhs free...] (dotgeneral.go:15-53)."""
+    dims = [lshape[a] for a in lb]
+    dims += [d for i, d in enumerate(lshape) if i not in lc and i not in lb]
+    dims += [d for i, d in enumerate(rshape) if i not in rc and i not in rb]
+    return tuple(dims)
+
+
+def dot_general(lhs, lc, lb, rhs, rc, rb, mode=MODE_F64) -> np.ndarray:
+    lhs, rhs = _f32(lhs), _f32(rhs)
+    oshape = dot_general_shape(lhs.shape, lc, lb, rhs.shape, rc, rb)
+    out = np.empty(oshape, np.float64)
+    ld = np.asarray(lhs.shape, np.int64)
+    rd = np.asarray(rhs.shape, np.int64)
+    a1, p1 = _int_arr(lc)
+    a2, p2 = _int_arr(lb)
+    a3, p3 = _int_arr(rc)
+    a4, p4 = _int_arr(rb)
+    rc_ = lib().orc_dot_general(lhs, lhs.ndim, ld, p1, len(lc), p2, len(lb),
+                                rhs, rhs.ndim, rd, p3, len(rc), p4, len(rb), out, mode)
+    if rc_ != 0:
+        raise ValueError("orc_dot_general: invalid axes")
+    return out
+
+
+def dot_sampled(a, b, bs, ms, ns) -> np.ndarray:
+    """Sampled fp64 entries of C[b] = A[b] @ B[b] for A [B,M,K], B [B,K,N] (fp32)."""
+    a, b = _f32(a), _f32(b)
+    Bn, M, K = a.shape
+    _, K2, N = b.shape
+    assert K == K2
+    bs = np.ascontiguousarray(bs, np.int64)
+    ms = np.ascontiguousarray(ms, np.int64)
+    ns = np.ascontiguousarray(ns, np.int64)
+    out = np.empty(bs.shape, np.float64)
+    lib().orc_dot_sampled(a.ctypes.data, M * K, K, 1, b.ctypes.data, K * N, N, 1, K,
+                          bs, ms, ns, bs.size, out)
+    return out
+
+
+def sdpa(q, k, v, mask=None, scale=None, causal=False) -> np.ndarray:
+    """Attention in BHSD layout; q [B,H,Sq,D], k/v [B,Hkv,Sk,D]; mask bool [Sq,Sk]."""
+    q, k, v = _f32(q), _f32(k), _f32(v)
+    B, H, Sq, D = q.shape
+    _, Hkv, Sk, _ = k.shape
+    if scale is None:
+        scale = 1.0 / np.sqrt(D)
+    mp = None
+    if mask is not None:
+        m = np.ascontiguousarray(np.broadcast_to(np.asarray(mask, bool), (Sq, Sk)).astype(np.uint8))
+        mp = m.ctypes.data_as(ctypes.c_void_p)
+    out = np.empty((B, H, Sq, D), np.float64)
+    lib().orc_sdpa(q, k, v, mp, B, H, Hkv, Sq, Sk, D, float(scale), int(causal), out)
+    return out
+
+
+def gather_rows(table: np.ndarray, ids) -> np.ndarray:
+    table = np.ascontiguousarray(table)
+    ids = np.ascontiguousarray(np.asarray(ids, np.int32).reshape(-1))
+    V = table.shape[0]
+    row_bytes = table.nbytes // V
+    out = np.empty((ids.size,) + table.shape[1:], table.dtype)
+    lib().orc_gather_rows(table.ctypes.data, V, row_bytes, ids, ids.size, out.ctypes.data)
+    return out
+
+
+def argminmax(x, axis, is_min=False) -> np.ndarray:
+    x = _f32(x)
+    outer, n, inner = _split(x.shape, axis)
+    out = np.empty(outer * inner, np.int64)
+    lib().orc_argminmax(x, outer, n, inner, int(is_min), out)
+    ax = axis % x.ndim
+    return out.reshape(x.shape[:ax] + x.shape[ax + 1:])
+
+
+def iota(shape, axis) -> np.ndarray:
+    outer, n, inner = _split(tuple(shape), axis)
+    out = np.empty(tuple(shape), np.float64)
+    lib().orc_iota(out, outer, n, inner)
+    return out
+
+
+def f32_to_bf16_bits(x) -> np.ndarray:
+    x = _f32(x)
+    y = np.empty(x.shape, np.uint16)
+    lib().orc_f32_to_bf16(x.reshape(-1), y.reshape(-1), x.size)
+    return y

@@ -1,0 +1,104 @@
+"""Writes known_answers.json: the reference's own known-answer test vectors for
+the hot path, transcribed from mpsgraph/gomlx/mpsgraph_test.go (file:line in each
+entry).  Values are data (inputs and expected outputs), not code.  Closed forms
+the reference computes with math.Exp / math.Sqrt are evaluated here in fp64.
+
+Run:  python tests/golden/make_known_answers.py
+"""
+import json
+import math
+import os
+
+e1, e2, e3 = math.exp(1), math.exp(2), math.exp(3)
+s3 = math.exp(1.0 / math.sqrt(3.0))
+w0, w1 = s3 / (s3 + 1.0), 1.0 / (s3 + 1.0)
+
+CASES = {
+    "softmax": {
+        "source": "mpsgraph_test.go:1133-1190 (TestFusedSoftmax)",
+        "shape": [2, 3], "axis": 1, "tol": 1e-4,
+        "x": [1, 2, 3, 1, 1, 1],
+        "expected": [e1 / (e1 + e2 + e3), e2 / (e1 + e2 + e3), e3 / (e1 + e2 + e3),
+                     1 / 3, 1 / 3, 1 / 3],
+    },
+    "layernorm_basic": {
+        "source": "mpsgraph_test.go:2598-2609 (TestFusedLayerNorm/basic)",
+        "shape": [2, 4], "eps": 1e-5, "tol": 1e-3,
+        "x": [1, 2, 3, 4, 5, 6, 7, 8],
+        "expected": [-1.3416, -0.4472, 0.4472, 1.3416, -1.3416, -0.4472, 0.4472, 1.3416],
+    },
+    "layernorm_gamma_beta": {
+        "source": "mpsgraph_test.go:2611-2623 (TestFusedLayerNorm/with_gamma_beta)",
+        "shape": [2, 4], "eps": 1e-5, "tol": 1e-3,
+        "x": [1, 2, 3, 4, 5, 6, 7, 8], "gamma": [2, 2, 2, 2], "beta": [1, 1, 1, 1],
+        "gamma_shape": [1, 4],
+        "expected_first_row": [-1.6833, 0.1056, 1.8944, 3.6833],
+    },
+    "dot_simple": {
+        "source": "mpsgraph_test.go:496-545 (TestDotGeneral/SimpleMatMul)",
+        "lhs_shape": [2, 3], "rhs_shape": [3, 2], "lc": [1], "lb": [], "rc": [0], "rb": [],
+        "lhs": [1, 2, 3, 4, 5, 6], "rhs": [1, 2, 3, 4, 5, 6], "tol": 1e-4,
+        "expected": [22, 28, 49, 64],
+    },
+    "dot_batched": {
+        "source": "mpsgraph_test.go:547-595 (TestDotGeneral/BatchedMatMul)",
+        "lhs_shape": [2, 2, 3], "rhs_shape": [2, 3, 2], "lc": [2], "lb": [0], "rc": [1], "rb": [0],
+        "lhs": list(range(1, 13)), "rhs": list(range(1, 13)), "tol": 1e-3,
+        "expected": [22, 28, 49, 64, 220, 244, 301, 334],
+    },
+    "dot_bf16": {
+        "source": "mpsgraph_test.go:3141-3155 (TestBFloat16/matmul)",
+        "lhs_shape": [2, 2], "rhs_shape": [2, 2], "lc": [1], "lb": [], "rc": [0], "rb": [],
+        "lhs": [1, 2, 3, 4], "rhs": [5, 6, 7, 8], "tol": 1.0,
+        "expected": [19, 22, 43, 50],
+    },
+    "attention_dot_chain": {
+        "source": "mpsgraph_test.go:1638-1724 (TestTransformerBlock)",
+        "q": [1, 0, 0, 0, 1, 0], "k": [1, 0, 0, 0, 1, 0], "v": [10, 20, 30, 40, 50, 60],
+        "shape": [2, 3], "scale": 1.0 / math.sqrt(3.0), "tol": 1e-3,
+        "expected": [w0 * 10 + w1 * 40, w0 * 20 + w1 * 50, w0 * 30 + w1 * 60,
+                     w1 * 10 + w0 * 40, w1 * 20 + w0 * 50, w1 * 30 + w0 * 60],
+    },
+    "sdpa_causal": {
+        "source": "mpsgraph_test.go:2996-3015 (TestFusedScaledDotProductAttention/causal_mask)",
+        "shape": [1, 1, 3, 2], "scale": 1.0, "causal": True, "tol": 1e-3,
+        "q": [1, 0, 0, 1, 1, 1], "k": [1, 0, 0, 1, 1, 1], "v": [1, 0, 0, 1, 0.5, 0.5],
+        "expected_first_row": [1, 0],
+    },
+    "sdpa_bool_mask": {
+        "source": "mpsgraph_test.go:3036-3057 (TestFusedScaledDotProductAttention/boolean_mask)",
+        "shape": [1, 1, 2, 2], "scale": 1.0, "causal": False, "tol": 1e-3,
+        "q": [1, 0, 0, 1], "k": [1, 0, 0, 1], "v": [10, 20, 30, 40],
+        "mask": [True, False, True, True],
+        "expected_first_row": [10, 20],
+    },
+    "sdpa_basic_range": {
+        "source": "mpsgraph_test.go:2969-2994 (TestFusedScaledDotProductAttention/basic_BHSD)",
+        "shape": [1, 1, 2, 2], "scale": 1.0 / math.sqrt(2.0), "causal": False,
+        "q": [1, 0, 0, 1], "k": [1, 0, 0, 1], "v": [1, 0, 0, 1],
+        "expected_range": [-0.1, 1.1],
+    },
+    "gather_embedding": {
+        "source": "mpsgraph_test.go:599-674 (TestGather/EmbeddingLookup)",
+        "table_shape": [4, 3], "table": [10, 11, 12, 20, 21, 22, 30, 31, 32, 40, 41, 42],
+        "ids": [1, 3], "expected": [20, 21, 22, 40, 41, 42],
+    },
+    "argmax": {
+        "source": "mpsgraph_test.go:941-991 (TestArgMinMax)",
+        "shape": [2, 3], "axis": 1, "x": [1, 5, 3, 8, 2, 6], "expected": [1, 0],
+    },
+    "iota": {
+        "source": "mpsgraph_test.go:785-822 (TestIota)",
+        "shape": [2, 3], "axis": 1, "expected": [0, 1, 2, 0, 1, 2],
+    },
+    "convert_f32_i32": {
+        "source": "mpsgraph_test.go:1485-1532 (TestConvertDType)",
+        "x": [1.7, 2.3, -0.9], "expected": [1, 2, 0],
+    },
+}
+
+if __name__ == "__main__":
+    out = os.path.join(os.path.dirname(os.path.abspath(__file__)), "known_answers.json")
+    with open(out, "w") as f:
+        json.dump(CASES, f, indent=1)
+    print("wrote", out)

@@ -1,0 +1,55 @@
+"""The C ABI library loads and exports every entry point include/*.h declares
+(no compute: this runs on machines without a GPU)."""
+import ctypes
+import glob
+import os
+import re
+
+from gomlx_hip import _lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def declared_symbols():
+    names = set()
+    for h in glob.glob(os.path.join(ROOT, "include", "*.h")):
+        text = open(h).read()
+        text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+        names |= set(re.findall(r"\b(ghip_\w+)\s*\(", text))
+    return names
+
+
+def test_header_declares_entry_points():
+    names = declared_symbols()
+    for n in ["ghip_softmax_rows", "ghip_rmsnorm_rows", "ghip_layernorm_rows",
+              "ghip_gemm_batched", "ghip_gather_rows", "ghip_argminmax", "ghip_iota"]:
+        assert n in names
+
+
+def test_library_exports_every_declared_symbol():
+    L = _lib.load()
+    missing = [n for n in sorted(declared_symbols()) if not hasattr(L, n)]
+    assert not missing, f"not exported: {missing}"
+
+
+def test_python_signatures_cover_header():
+    # Every declared entry point has a ctypes signature, so no call goes untyped.
+    sigs = set(_lib.SIGNATURES) | {"ghip_version", "ghip_error_clear"}
+    extra = declared_symbols() - sigs
+    assert not extra, f"no ctypes signature for {sorted(extra)}"
+
+
+def test_version_string():
+    assert b"gfx950" in _lib.load().ghip_version()
+
+
+def test_error_path_without_gpu():
+    # Argument validation happens on the host before any HIP call.
+    import pytest
+    with pytest.raises(_lib.BackendError) as ei:
+        _lib.call("ghip_gemm_batched", _lib.DT_FLOAT32, _lib.DT_FLOAT32, 1, 4, 4, 4,
+                  None, 0, 0, 0, None, 0, 0, 0, None, 0, 0, 2, None)
+    assert ei.value.code == 1 and "sc_n" in str(ei.value)
+    with pytest.raises(_lib.BackendError) as ei:
+        _lib.call("ghip_softmax_rows", 99, None, None, 4, 4, 0, None)
+    assert ei.value.code in (1, 2)

@@ -1,0 +1,155 @@
+"""Parity of the batched GEMM (DotGeneral lowering target) against the oracle.
+
+Tolerances: bf16 inputs with bf16 output <= 1e-2 relative (north star, fp32
+reference); bf16 inputs with fp32 output and fp32 inputs <= 1e-4 relative
+(RMS-floored max elementwise error, conftest.rel_err)."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as orc
+from gomlx_hip import ops, synth
+from conftest import rel_err, norm_err
+
+pytestmark = pytest.mark.gpu
+
+
+def dev(a, d, dtype=torch.float32):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(d).to(dtype)
+
+
+@pytest.mark.parametrize("name", ["dot_simple", "dot_batched", "dot_bf16"])
+def test_known_answers(known, cuda, name):
+    c = known[name]
+    lhs = np.array(c["lhs"], np.float32).reshape(c["lhs_shape"])
+    rhs = np.array(c["rhs"], np.float32).reshape(c["rhs_shape"])
+    dt = torch.bfloat16 if name == "dot_bf16" else torch.float32
+    got = ops.gemm(dev(lhs, cuda, dt), dev(rhs, cuda, dt)).float().cpu().numpy()
+    assert np.max(np.abs(got.reshape(-1) - np.array(c["expected"]))) <= c["tol"]
+
+
+SHAPES = [  # (batch, M, N, K)
+    (1, 256, 256, 64),
+    (2, 512, 256, 128),
+    (1, 300, 200, 136),     # ragged tiles in M, N and K
+    (3, 128, 136, 72),
+    (1, 1024, 1024, 512),
+    (4, 64, 512, 256),
+    (1, 8, 8, 8),
+    (2, 520, 264, 1000),
+]
+
+
+@pytest.mark.parametrize("shape", SHAPES)
+@pytest.mark.parametrize("a_t", [False, True])
+@pytest.mark.parametrize("b_t", [False, True])
+def test_bf16_layouts(cuda, shape, a_t, b_t):
+    """Every operand majorness (K- or MN-contiguous) through strided views."""
+    B, M, N, K = shape
+    a = synth.round_bf16(synth.normal(3000 + M, (B, M, K), std=0.125))
+    b = synth.round_bf16(synth.normal(3100 + N, (B, K, N), std=0.125))
+    ta = dev(a, cuda, torch.bfloat16)
+    tb = dev(b, cuda, torch.bfloat16)
+    if a_t:  # same values, M-contiguous storage
+        ta = ta.transpose(1, 2).contiguous().transpose(1, 2)
+    if b_t:  # same values, K-contiguous storage
+        tb = tb.transpose(1, 2).contiguous().transpose(1, 2)
+    ref = orc.dot_general(a, [2], [0], b, [1], [0])
+    c32 = ops.gemm(ta, tb, out_dtype=torch.float32).cpu().numpy()
+    assert rel_err(c32, ref) <= 1e-4
+    c16 = ops.gemm(ta, tb).float().cpu().numpy()
+    assert rel_err(c16, ref) <= 1e-2
+
+
+@pytest.mark.parametrize("shape", SHAPES)
+@pytest.mark.parametrize("a_t", [False, True])
+@pytest.mark.parametrize("b_t", [False, True])
+def test_f32_layouts(cuda, shape, a_t, b_t):
+    B, M, N, K = shape
+    a = synth.normal(3200 + M, (B, M, K), std=0.125)
+    b = synth.normal(3300 + N, (B, K, N), std=0.125)
+    ta, tb = dev(a, cuda), dev(b, cuda)
+    if a_t:
+        ta = ta.transpose(1, 2).contiguous().transpose(1, 2)
+    if b_t:
+        tb = tb.transpose(1, 2).contiguous().transpose(1, 2)
+    c = ops.gemm(ta, tb).cpu().numpy()
+    assert rel_err(c, orc.dot_general(a, [2], [0], b, [1], [0])) <= 1e-4
+
+
+def test_generic_path_odd_strides(cuda):
+    """Shapes/strides the vector paths cannot address fall back to the generic kernel."""
+    a = synth.normal(3400, (2, 33, 19))
+    b = synth.normal(3401, (2, 19, 27))
+    c = ops.gemm(dev(a, cuda), dev(b, cuda)).cpu().numpy()
+    assert rel_err(c, orc.dot_general(a, [2], [0], b, [1], [0])) <= 1e-5
+    ab = synth.round_bf16(a)
+    bb = synth.round_bf16(b)
+    c = ops.gemm(dev(ab, cuda, torch.bfloat16), dev(bb, cuda, torch.bfloat16),
+                 out_dtype=torch.float32).cpu().numpy()
+    assert rel_err(c, orc.dot_general(ab, [2], [0], bb, [1], [0])) <= 1e-5
+
+
+def _sampled_check(ta, tb, c, count=4096, seed=0):
+    """Size-independent check of a full-size product: `count` random entries of c
+    against fp64 dot products computed on the host from the same input bytes."""
+    B, M, K = ta.shape
+    N = tb.shape[2]
+    rng = np.random.default_rng(seed)
+    bs = rng.integers(0, B, count)
+    ms = rng.integers(0, M, count)
+    ns = rng.integers(0, N, count)
+    a = ta.float().cpu().numpy()
+    b = tb.float().cpu().numpy()
+    ref = orc.dot_sampled(a, b, bs, ms, ns)
+    got = c.float().cpu().numpy()[bs, ms, ns]
+    return got, ref
+
+
+def test_dot_general_config_bf16(cuda):
+    """BASELINE config: A [8,2048,4096] x B [8,4096,4096], bf16, fp32 accumulate,
+    bf16 out; entries ~ N(0, 1/64)."""
+    g = torch.Generator(cuda).manual_seed(3001)
+    ta = (torch.randn((8, 2048, 4096), device=cuda, generator=g) * 0.125).to(torch.bfloat16)
+    tb = (torch.randn((8, 4096, 4096), device=cuda, generator=g) * 0.125).to(torch.bfloat16)
+    c = ops.gemm(ta, tb)
+    got, ref = _sampled_check(ta, tb, c)
+    assert rel_err(got, ref) <= 1e-2
+    assert norm_err(got, ref) <= 4e-3
+    c32 = ops.gemm(ta, tb, out_dtype=torch.float32)
+    got, ref = _sampled_check(ta, tb, c32, seed=1)
+    assert rel_err(got, ref) <= 1e-4
+
+
+def test_dot_general_config_f32(cuda):
+    g = torch.Generator(cuda).manual_seed(3002)
+    ta = torch.randn((8, 2048, 4096), device=cuda, generator=g) * 0.125
+    tb = torch.randn((8, 4096, 4096), device=cuda, generator=g) * 0.125
+    c = ops.gemm(ta, tb)
+    got, ref = _sampled_check(ta, tb, c)
+    assert rel_err(got, ref) <= 1e-4
+
+
+def test_attention_shapes_bf16(cuda):
+    """The two attention GEMMs at config shape: Q.K^T (rhs K-contiguous) and P.V."""
+    g = torch.Generator(cuda).manual_seed(4001)
+    q = torch.randn((64, 2048, 128), device=cuda, generator=g).to(torch.bfloat16)
+    k = torch.randn((64, 2048, 128), device=cuda, generator=g).to(torch.bfloat16)
+    s = ops.gemm(q, k.transpose(1, 2), out_dtype=torch.float32)
+    got, ref = _sampled_check(q, k.transpose(1, 2), s)
+    assert rel_err(got, ref) <= 1e-4
+    p = torch.softmax(s[:, :, :], dim=-1).to(torch.bfloat16)
+    v = torch.randn((64, 2048, 128), device=cuda, generator=g).to(torch.bfloat16)
+    o = ops.gemm(p, v, out_dtype=torch.float32)
+    got, ref = _sampled_check(p, v, o, seed=2)
+    assert rel_err(got, ref) <= 1e-4
+
+
+def test_empty_and_k0(cuda):
+    a = torch.empty((2, 0, 16), device=cuda)
+    b = torch.empty((2, 16, 8), device=cuda)
+    assert ops.gemm(a, b).shape == (2, 0, 8)
+    a = torch.empty((1, 4, 0), device=cuda)
+    b = torch.empty((1, 0, 8), device=cuda)
+    c = ops.gemm(a, b)
+    assert torch.count_nonzero(c).item() == 0

@@ -1,0 +1,224 @@
+"""Pins the CPU oracle: the reference's known answers, invariants, and
+independent textbook computations (numpy) chosen so that a dropped term, a
+wrong sign/index or a transposed operand fails."""
+import itertools
+
+import numpy as np
+import pytest
+
+from oracle import oracle as orc
+from gomlx_hip import synth
+from conftest import rel_err
+
+
+# ---------------------------------------------------------------- known answers
+def test_softmax_known_answer(known):
+    c = known["softmax"]
+    x = np.array(c["x"], np.float32).reshape(c["shape"])
+    y = orc.softmax(x, c["axis"])
+    assert np.max(np.abs(y.reshape(-1) - np.array(c["expected"]))) <= c["tol"]
+    y32 = orc.softmax(x, c["axis"], mode=orc.MODE_F32SEQ)
+    assert np.max(np.abs(y32.reshape(-1) - np.array(c["expected"]))) <= c["tol"]
+
+
+def test_layernorm_known_answers(known):
+    c = known["layernorm_basic"]
+    x = np.array(c["x"], np.float32).reshape(c["shape"])
+    y = orc.layernorm(x, eps=c["eps"])
+    assert np.max(np.abs(y.reshape(-1) - np.array(c["expected"]))) <= c["tol"]
+    c = known["layernorm_gamma_beta"]
+    x = np.array(c["x"], np.float32).reshape(c["shape"])
+    g = np.array(c["gamma"], np.float32).reshape(c["gamma_shape"])
+    b = np.array(c["beta"], np.float32).reshape(c["gamma_shape"])
+    y = orc.layernorm(x, g, b, eps=c["eps"])
+    assert np.max(np.abs(y[0] - np.array(c["expected_first_row"]))) <= c["tol"]
+
+
+@pytest.mark.parametrize("name", ["dot_simple", "dot_batched", "dot_bf16"])
+def test_dot_general_known_answers(known, name):
+    c = known[name]
+    lhs = np.array(c["lhs"], np.float32).reshape(c["lhs_shape"])
+    rhs = np.array(c["rhs"], np.float32).reshape(c["rhs_shape"])
+    y = orc.dot_general(lhs, c["lc"], c["lb"], rhs, c["rc"], c["rb"])
+    assert np.max(np.abs(y.reshape(-1) - np.array(c["expected"]))) <= min(c["tol"], 1e-9)
+
+
+def test_attention_chain_known_answer(known):
+    c = known["attention_dot_chain"]
+    q = np.array(c["q"], np.float32).reshape(1, 1, *c["shape"])
+    k = np.array(c["k"], np.float32).reshape(1, 1, *c["shape"])
+    v = np.array(c["v"], np.float32).reshape(1, 1, *c["shape"])
+    y = orc.sdpa(q, k, v, scale=c["scale"])
+    assert np.max(np.abs(y.reshape(-1) - np.array(c["expected"]))) <= c["tol"]
+
+
+def test_sdpa_known_answers(known):
+    c = known["sdpa_causal"]
+    sh = c["shape"]
+    q, k, v = (np.array(c[n], np.float32).reshape(sh) for n in "qkv")
+    y = orc.sdpa(q, k, v, scale=c["scale"], causal=True)
+    assert np.max(np.abs(y[0, 0, 0] - np.array(c["expected_first_row"]))) <= c["tol"]
+    c = known["sdpa_bool_mask"]
+    sh = c["shape"]
+    q, k, v = (np.array(c[n], np.float32).reshape(sh) for n in "qkv")
+    m = np.array(c["mask"], bool).reshape(sh[2], sh[3])
+    y = orc.sdpa(q, k, v, mask=m, scale=c["scale"])
+    assert np.max(np.abs(y[0, 0, 0] - np.array(c["expected_first_row"]))) <= c["tol"]
+    c = known["sdpa_basic_range"]
+    sh = c["shape"]
+    q, k, v = (np.array(c[n], np.float32).reshape(sh) for n in "qkv")
+    y = orc.sdpa(q, k, v, scale=c["scale"])
+    lo, hi = c["expected_range"]
+    assert np.all(y >= lo) and np.all(y <= hi)
+
+
+def test_gather_known_answer(known):
+    c = known["gather_embedding"]
+    t = np.array(c["table"], np.float32).reshape(c["table_shape"])
+    out = orc.gather_rows(t, c["ids"])
+    assert out.reshape(-1).tolist() == c["expected"]
+
+
+def test_argmax_iota_known_answers(known):
+    c = known["argmax"]
+    x = np.array(c["x"], np.float32).reshape(c["shape"])
+    assert orc.argminmax(x, c["axis"]).tolist() == c["expected"]
+    c = known["iota"]
+    assert orc.iota(c["shape"], c["axis"]).reshape(-1).tolist() == c["expected"]
+
+
+# ---------------------------------------------------------------- invariants / brute force
+def test_softmax_invariants_and_numpy():
+    x = synth.normal(7, (37, 53), std=3.0)
+    y = orc.softmax(x)
+    assert np.allclose(y.sum(-1), 1.0, atol=1e-12)
+    assert np.all(y > 0) and np.all(y <= 1)
+    y2 = orc.softmax(x + np.float32(5.0))   # shift invariance (5.0 is exact in fp32 here)
+    assert np.max(np.abs(y - y2)) < 1e-6
+    xd = x.astype(np.float64)
+    ref = np.exp(xd - xd.max(-1, keepdims=True))
+    ref /= ref.sum(-1, keepdims=True)
+    assert np.max(np.abs(y - ref)) < 1e-14
+    # middle-axis softmax equals last-axis softmax of the transposed tensor
+    x3 = synth.normal(8, (4, 9, 5))
+    ym = orc.softmax(x3, axis=1)
+    yt = orc.softmax(np.ascontiguousarray(x3.transpose(0, 2, 1)), axis=-1).transpose(0, 2, 1)
+    assert np.max(np.abs(ym - yt)) < 1e-14
+    ls = orc.log_softmax(x)
+    assert np.max(np.abs(ls - np.log(ref))) < 1e-12
+
+
+def test_layernorm_invariants():
+    x = synth.normal(11, (16, 256), std=3.0, mean=2.0)
+    y = orc.layernorm(x, eps=0.0)
+    assert np.max(np.abs(y.mean(-1))) < 1e-12
+    assert np.max(np.abs(y.var(-1) - 1.0)) < 1e-10
+    g = synth.uniform_f32(12, (256,), 0.5, 1.5)
+    b = synth.normal(13, (256,), std=0.1)
+    yg = orc.layernorm(x, g, b, eps=1e-5)
+    xd = x.astype(np.float64)
+    mu = xd.mean(-1, keepdims=True)
+    ref = (xd - mu) / np.sqrt(((xd - mu) ** 2).mean(-1, keepdims=True) + 1e-5) * g + b
+    assert np.max(np.abs(yg - ref)) < 1e-12
+
+
+def test_rmsnorm_invariants():
+    x = synth.normal(21, (16, 512), std=2.0)
+    y = orc.rmsnorm(x, eps=0.0)
+    assert np.max(np.abs((y ** 2).mean(-1) - 1.0)) < 1e-12
+    # scale invariance: rmsnorm(c x) == rmsnorm(x) when eps = 0
+    y4 = orc.rmsnorm(x * np.float32(4.0), eps=0.0)
+    assert np.max(np.abs(y - y4)) < 1e-12
+    # hand-computed row [3, 4]: rms = sqrt(12.5)
+    y = orc.rmsnorm(np.array([[3.0, 4.0]], np.float32), np.array([1.0, 2.0], np.float32), eps=0.0)
+    r = np.sqrt(12.5)
+    assert np.allclose(y, [[3 / r, 8 / r]], atol=1e-12)
+
+
+DOT_LAYOUTS = [
+    # (lhs shape, lc, lb, rhs shape, rc, rb)
+    ((5, 7), [1], [], (7, 3), [0], []),
+    ((5, 7), [1], [], (3, 7), [1], []),          # rhs transposed
+    ((7, 5), [0], [], (7, 3), [0], []),          # lhs transposed
+    ((2, 5, 7), [2], [0], (2, 7, 3), [1], [0]),  # DotGeneral config layout
+    ((2, 3, 5, 4), [3], [0, 1], (2, 3, 6, 4), [3], [0, 1]),  # attention Q.K^T
+    ((4, 2, 5, 3), [0, 3], [1], (3, 2, 4, 6), [2, 0], [1]),  # multi-contract, odd order
+]
+
+
+@pytest.mark.parametrize("layout", DOT_LAYOUTS)
+def test_dot_general_vs_einsum(layout):
+    ls, lc, lb, rs, rc, rb = layout
+    lhs = synth.normal(31, ls)
+    rhs = synth.normal(32, rs)
+    got = orc.dot_general(lhs, lc, lb, rhs, rc, rb)
+    letters = iter("abcdefghijklmnop")
+    lsub = [None] * len(ls)
+    rsub = [None] * len(rs)
+    for a, b in zip(lb, rb):
+        lsub[a] = rsub[b] = next(letters)
+    for a, b in zip(lc, rc):
+        lsub[a] = rsub[b] = next(letters)
+    for i in range(len(ls)):
+        if lsub[i] is None:
+            lsub[i] = next(letters)
+    for i in range(len(rs)):
+        if rsub[i] is None:
+            rsub[i] = next(letters)
+    out = [lsub[a] for a in lb] + [lsub[i] for i in range(len(ls)) if i not in lc and i not in lb] \
+        + [rsub[i] for i in range(len(rs)) if i not in rc and i not in rb]
+    spec = "".join(lsub) + "," + "".join(rsub) + "->" + "".join(out)
+    ref = np.einsum(spec, lhs.astype(np.float64), rhs.astype(np.float64))
+    assert got.shape == ref.shape
+    assert np.max(np.abs(got - ref)) < 1e-10
+
+
+def test_dot_sampled_matches_dot_general():
+    a = synth.normal(41, (2, 9, 13))
+    b = synth.normal(42, (2, 13, 11))
+    full = orc.dot_general(a, [2], [0], b, [1], [0])
+    idx = np.array(list(itertools.product(range(2), range(9), range(11))))
+    s = orc.dot_sampled(a, b, idx[:, 0], idx[:, 1], idx[:, 2])
+    assert np.max(np.abs(s - full.reshape(-1))) < 1e-12
+
+
+def test_sdpa_vs_numpy_gqa_causal():
+    B, H, Hkv, S, D = 2, 4, 2, 7, 5
+    q = synth.normal(51, (B, H, S, D))
+    k = synth.normal(52, (B, Hkv, S, D))
+    v = synth.normal(53, (B, Hkv, S, D))
+    got = orc.sdpa(q, k, v, causal=True, scale=0.3)
+    kr = np.repeat(k.astype(np.float64), H // Hkv, axis=1)
+    vr = np.repeat(v.astype(np.float64), H // Hkv, axis=1)
+    s = q.astype(np.float64) @ kr.transpose(0, 1, 3, 2) * 0.3
+    s = np.where(np.tril(np.ones((S, S), bool)), s, -np.inf)
+    p = np.exp(s - s.max(-1, keepdims=True))
+    p /= p.sum(-1, keepdims=True)
+    assert np.max(np.abs(got - p @ vr)) < 1e-12
+
+
+def test_argminmax_vs_numpy_and_rules():
+    x = synth.normal(61, (6, 17, 5))
+    for ax in range(3):
+        assert np.array_equal(orc.argminmax(x, ax), np.argmax(x, axis=ax))
+        assert np.array_equal(orc.argminmax(x, ax, is_min=True), np.argmin(x, axis=ax))
+    t = np.array([[1, 3, 3, 2], [np.nan, 1, np.nan, 5], [-np.inf, -np.inf, 0, 0]], np.float32)
+    assert orc.argminmax(t, 1).tolist() == [1, 0, 2]          # ties -> first, NaN wins
+    assert orc.argminmax(t, 1, is_min=True).tolist() == [0, 0, 0]
+
+
+def test_gather_clamps_out_of_range():
+    t = np.arange(12, dtype=np.float32).reshape(4, 3)
+    out = orc.gather_rows(t, [-5, 0, 3, 99])
+    assert out.tolist() == [t[0].tolist(), t[0].tolist(), t[3].tolist(), t[3].tolist()]
+
+
+def test_bf16_rounding_matches_numpy_port():
+    x = np.concatenate([synth.normal(71, (4096,), std=100.0),
+                        np.array([1.0 + 2 ** -8, 1.0 + 3 * 2 ** -8, np.inf, -np.inf, 0.0, -0.0],
+                                 np.float32)])
+    a = orc.f32_to_bf16_bits(x)
+    b = synth.to_bf16_bits(x)
+    assert np.array_equal(a, b)
+    # ties to even: 1 + 2^-8 -> 1.0, 1 + 3*2^-8 -> 1 + 2^-6
+    assert synth.bf16_bits_to_f32(a[4096:4098]).tolist() == [1.0, 1.0 + 2 ** -6]
