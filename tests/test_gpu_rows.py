@@ -15,6 +15,7 @@ from conftest import rel_err
 pytestmark = pytest.mark.gpu
 
 F32_TOL = 1e-5
+BF16_TOL = 2.0 ** -8 + 1e-5   # one bf16 rounding of the fp32 result
 
 
 def bf16_ulps(got_bf16: torch.Tensor, ref: np.ndarray) -> int:
@@ -149,7 +150,9 @@ def test_layernorm_config_bf16(cuda):
     b = synth.round_bf16(synth.normal(2003, (4096,), std=0.1))
     y = ops.layernorm(to_dev(x, cuda, torch.bfloat16), to_dev(g, cuda, torch.bfloat16),
                       to_dev(b, cuda, torch.bfloat16), 1e-5)
-    assert bf16_ulps(y, orc.layernorm(x, g, b, 1e-5)) <= 1
+    # x - mean (and beta) put outputs arbitrarily close to zero, where a ulp count is
+    # ill-conditioned: bound the RMS-floored relative error by one bf16 rounding.
+    assert rel_err(y.float().cpu().numpy(), orc.layernorm(x, g, b, 1e-5)) <= BF16_TOL
 
 
 def test_layernorm_known_answers(known, cuda):
