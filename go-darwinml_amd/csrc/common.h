@@ -17,7 +17,8 @@ struct bf16_t {
 };
 
 __device__ __host__ __forceinline__ float bf16_to_f32(uint16_t b) {
-  return __uint_as_float(static_cast<uint32_t>(b) << 16);
+  const uint32_t u = static_cast<uint32_t>(b) << 16;
+  return __builtin_bit_cast(float, u);
 }
 
 __device__ __forceinline__ uint16_t f32_to_bf16(float f) {

@@ -1,0 +1,212 @@
+// Graph IR, builder, lowering plan and executor of the GoMLX backend.
+//
+// Mirrors the reference backend's object model (mpsgraph/gomlx): a Backend owns
+// the device context (backend.go:22-27), a Builder owns one Function graph
+// (builder.go:16-24), Function methods append nodes with inferred shapes
+// (function.go), Compile lowers the graph to a launch plan (builder.go:72-109) and
+// an Executable runs it (executable.go:19-112).  Unlike the reference, which hands
+// the graph to MPSGraph, lowering and fusion happen here (graph_lower.cpp) and
+// every buffer stays in device memory.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <functional>
+#include <map>
+#include <memory>
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "gomlx_hip.h"
+
+struct GHipBackend;
+struct GHipBuilder;
+struct GHipFunction;
+struct GHipExecutable;
+struct GHipBuffer;
+
+namespace ghip {
+
+int dtype_size(int dt);
+bool dtype_is_float(int dt);
+bool dtype_is_int(int dt);      // signed or unsigned integer (not bool)
+bool dtype_is_unsigned(int dt);
+const char* dtype_name(int dt);
+
+struct Shape {
+  int dtype = GHIP_DTYPE_FLOAT32;
+  std::vector<int64_t> dims;
+  int rank() const { return static_cast<int>(dims.size()); }
+  int64_t size() const {
+    int64_t n = 1;
+    for (auto d : dims) n *= d;
+    return n;
+  }
+  size_t bytes() const { return static_cast<size_t>(size()) * dtype_size(dtype); }
+  bool operator==(const Shape& o) const { return dtype == o.dtype && dims == o.dims; }
+  bool operator!=(const Shape& o) const { return !(*this == o); }
+  std::string str() const;
+};
+
+std::vector<int64_t> contiguous_strides(const std::vector<int64_t>& dims);
+
+enum class Kind {
+  Param, Const, Iota, Unary, Binary, Compare, Where, Clamp, Convert,
+  Reshape, Transpose, Broadcast, Slice, Concat, Reverse,
+  Reduce, ArgMinMax, Dot, Gather, Softmax, LayerNorm, SDPA,
+};
+const char* kind_name(Kind k);
+
+struct Node {
+  Kind kind;
+  int sub = 0;                 // unary / binary / compare / reduce op code
+  Shape shape;
+  std::vector<int> in;         // operand value ids
+  std::vector<int64_t> a0, a1, a2, a3, a4;  // op attributes (see graph_build.cpp)
+  double f0 = 0.0;
+  int64_t i0 = 0, i1 = 0, i2 = 0, i3 = 0;
+  std::vector<uint8_t> data;   // Const payload
+  std::string name;            // Param name
+};
+
+bool is_elementwise(Kind k);
+
+}  // namespace ghip
+
+// ---------------------------------------------------------------------------
+// Public handle types (opaque in the C header).
+// ---------------------------------------------------------------------------
+struct GHipBackend {
+  int device = 0;
+  bool plan_only = false;
+  bool finalized = false;
+  hipStream_t stream = nullptr;
+  std::string device_name;
+  std::mutex mu;
+  // Caching device allocator: exact-size free lists (sizes rounded to 256 B).
+  std::multimap<size_t, void*> free_blocks;
+  size_t cached_bytes = 0;
+  int alloc(size_t bytes, void** out, GHipError* err);
+  void release(void* p, size_t bytes);
+  void trim();
+};
+
+struct GHipBuffer {
+  GHipBackend* backend = nullptr;
+  ghip::Shape shape;
+  void* ptr = nullptr;
+  size_t cap = 0;      // allocated bytes (>= shape.bytes())
+  bool valid = true;
+};
+
+struct GHipFunction {
+  GHipBuilder* builder = nullptr;
+  std::string name;
+  std::vector<ghip::Node> nodes;
+  std::vector<int> params;
+  std::vector<int> outputs;
+  bool returned = false;
+  int add(ghip::Node&& n) {
+    nodes.push_back(std::move(n));
+    return static_cast<int>(nodes.size()) - 1;
+  }
+};
+
+struct GHipBuilder {
+  GHipBackend* backend = nullptr;
+  std::string name;
+  std::unique_ptr<GHipFunction> main;
+  bool compiled = false;
+};
+
+namespace ghip {
+
+// A device view of a value: base slot + element offset + per-dim element strides.
+struct View {
+  int slot = -1;
+  int64_t offset = 0;
+  std::vector<int64_t> strides;
+  bool contiguous(const Shape& s) const;
+};
+
+// Execution-time state: one device pointer per memory slot.
+struct ExecState {
+  std::vector<char*> slot_ptr;
+  hipStream_t stream = nullptr;
+  char* ptr(const View& v, int dt) const { return slot_ptr[v.slot] + v.offset * dtype_size(dt); }
+};
+
+using StepFn = std::function<int(ExecState&, GHipError*)>;
+
+struct Step {
+  std::string desc;
+  StepFn run;
+};
+
+enum class SlotKind { Input, Const, Arena, Output };
+
+struct Slot {
+  SlotKind kind;
+  size_t bytes = 0;
+  int index = 0;          // input / output index
+  size_t arena_off = 0;   // Arena
+  void* const_ptr = nullptr;
+};
+
+struct Plan {
+  std::vector<Slot> slots;
+  std::vector<Step> steps;
+  size_t arena_bytes = 0;
+  std::vector<View> out_views;  // where each output value lives
+  std::vector<int> out_slot;    // output slot for each output
+  std::vector<std::string> log;
+  std::vector<std::vector<uint8_t>> const_data;  // per slot (Const slots only)
+};
+
+int lower(GHipBackend* be, GHipFunction* fn, Plan* plan, GHipError* err);
+
+// Generated elementwise kernels (rtc.cpp).
+struct RtcKernel {
+  hipModule_t module = nullptr;
+  hipFunction_t func = nullptr;
+};
+int rtc_get(GHipBackend* be, const std::string& src, const std::string& entry, RtcKernel* out,
+            GHipError* err);
+
+// Generic kernels (k_generic.hip).
+constexpr int kMaxRank = 8;
+// dst[...] = src[...] over `dims`, both sides addressed by element strides.
+struct CopyDesc {
+  int rank = 0;
+  int64_t dims[kMaxRank];
+  int64_t sst[kMaxRank];  // source strides
+  int64_t dst[kMaxRank];  // destination strides
+};
+int launch_strided_copy(int elem_bytes, const void* src, void* dst, const CopyDesc& d,
+                        hipStream_t s, GHipError* err);
+// out[o] = reduce over r of src[o-offset + r-offset]; out is contiguous over odims.
+struct ReduceDesc {
+  int orank = 0, rrank = 0;
+  int64_t odims[kMaxRank], ost[kMaxRank];
+  int64_t rdims[kMaxRank], rst[kMaxRank];
+};
+int launch_reduce(int dtype, int op, const void* src, const ReduceDesc& d, void* dst,
+                  hipStream_t s, GHipError* err);
+// Gather rows with int32 or int64 ids (clamped).
+int launch_gather_rows(const void* table, int64_t V, int64_t row_bytes, const void* ids,
+                       int id_dtype, int64_t n, void* out, hipStream_t s, GHipError* err);
+
+}  // namespace ghip
+
+struct GHipExecutable {
+  GHipBackend* backend = nullptr;
+  std::vector<ghip::Shape> in_shapes, out_shapes;
+  std::vector<std::string> in_names;
+  ghip::Plan plan;
+  std::vector<std::pair<void*, size_t>> owned_consts;
+  void* arena = nullptr;
+  size_t arena_cap = 0;
+  std::mutex mu;
+  bool finalized = false;
+};

@@ -1,0 +1,939 @@
+// Backend, buffers and graph construction (the backends.Function surface).
+//
+// Each ghip_fn_* call checks its operands, infers the output shape with the
+// XLA / GoMLX rules and appends one node; nothing touches the device until
+// Compile.  Errors follow the reference: graph-building calls return an error
+// (function.go wraps each with pkg/errors), never abort.
+#include <hip/hip_runtime.h>
+#include <stdarg.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include <algorithm>
+#include <set>
+#include <sstream>
+
+#include "common.h"
+#include "graph.h"
+
+using namespace ghip;
+
+namespace ghip {
+
+int dtype_size(int dt) {
+  switch (dt) {
+    case GHIP_DTYPE_BOOL: case GHIP_DTYPE_INT8: case GHIP_DTYPE_UINT8: return 1;
+    case GHIP_DTYPE_INT16: case GHIP_DTYPE_UINT16: case GHIP_DTYPE_FLOAT16:
+    case GHIP_DTYPE_BFLOAT16: return 2;
+    case GHIP_DTYPE_INT32: case GHIP_DTYPE_UINT32: case GHIP_DTYPE_FLOAT32: return 4;
+    case GHIP_DTYPE_INT64: case GHIP_DTYPE_UINT64: case GHIP_DTYPE_FLOAT64: return 8;
+    default: return 0;
+  }
+}
+bool dtype_is_float(int dt) {
+  return dt == GHIP_DTYPE_FLOAT16 || dt == GHIP_DTYPE_BFLOAT16 || dt == GHIP_DTYPE_FLOAT32 ||
+         dt == GHIP_DTYPE_FLOAT64;
+}
+bool dtype_is_unsigned(int dt) {
+  return dt == GHIP_DTYPE_UINT8 || dt == GHIP_DTYPE_UINT16 || dt == GHIP_DTYPE_UINT32 ||
+         dt == GHIP_DTYPE_UINT64;
+}
+bool dtype_is_int(int dt) {
+  return dt == GHIP_DTYPE_INT8 || dt == GHIP_DTYPE_INT16 || dt == GHIP_DTYPE_INT32 ||
+         dt == GHIP_DTYPE_INT64 || dtype_is_unsigned(dt);
+}
+const char* dtype_name(int dt) {
+  static const char* n[] = {"bool", "int8", "int16", "int32", "int64", "float16", "bfloat16",
+                            "float32", "float64", "uint8", "uint16", "uint32", "uint64"};
+  return (dt >= 0 && dt <= 12) ? n[dt] : "invalid";
+}
+
+std::string Shape::str() const {
+  std::ostringstream o;
+  o << "(" << dtype_name(dtype) << ")[";
+  for (size_t i = 0; i < dims.size(); ++i) o << (i ? " " : "") << dims[i];
+  o << "]";
+  return o.str();
+}
+
+std::vector<int64_t> contiguous_strides(const std::vector<int64_t>& dims) {
+  std::vector<int64_t> s(dims.size());
+  int64_t acc = 1;
+  for (int i = static_cast<int>(dims.size()) - 1; i >= 0; --i) {
+    s[i] = acc;
+    acc *= dims[i];
+  }
+  return s;
+}
+
+bool View::contiguous(const Shape& s) const {
+  auto c = contiguous_strides(s.dims);
+  for (int i = 0; i < s.rank(); ++i)
+    if (s.dims[i] != 1 && strides[i] != c[i]) return false;
+  return true;
+}
+
+const char* kind_name(Kind k) {
+  switch (k) {
+    case Kind::Param: return "Parameter"; case Kind::Const: return "Constant";
+    case Kind::Iota: return "Iota"; case Kind::Unary: return "Unary";
+    case Kind::Binary: return "Binary"; case Kind::Compare: return "Compare";
+    case Kind::Where: return "Where"; case Kind::Clamp: return "Clamp";
+    case Kind::Convert: return "ConvertDType"; case Kind::Reshape: return "Reshape";
+    case Kind::Transpose: return "Transpose"; case Kind::Broadcast: return "BroadcastInDim";
+    case Kind::Slice: return "Slice"; case Kind::Concat: return "Concatenate";
+    case Kind::Reverse: return "Reverse";
+    case Kind::Reduce: return "Reduce"; case Kind::ArgMinMax: return "ArgMinMax";
+    case Kind::Dot: return "DotGeneral"; case Kind::Gather: return "Gather";
+    case Kind::Softmax: return "FusedSoftmax"; case Kind::LayerNorm: return "FusedLayerNorm";
+    case Kind::SDPA: return "FusedScaledDotProductAttention";
+  }
+  return "?";
+}
+
+bool is_elementwise(Kind k) {
+  return k == Kind::Unary || k == Kind::Binary || k == Kind::Compare || k == Kind::Where ||
+         k == Kind::Clamp || k == Kind::Convert;
+}
+
+}  // namespace ghip
+
+// ===========================================================================
+// Backend and device allocator
+// ===========================================================================
+static size_t round_alloc(size_t b) { return (b + 255) & ~size_t(255); }
+
+int GHipBackend::alloc(size_t bytes, void** out, GHipError* err) {
+  bytes = round_alloc(bytes ? bytes : 1);
+  {
+    std::lock_guard<std::mutex> lk(mu);
+    auto it = free_blocks.find(bytes);
+    if (it != free_blocks.end()) {
+      *out = it->second;
+      free_blocks.erase(it);
+      cached_bytes -= bytes;
+      return GHIP_OK;
+    }
+  }
+  if (plan_only) return set_error(err, GHIP_ERR_STATE, "plan-only backend cannot allocate device memory");
+  hipSetDevice(device);
+  hipError_t e = hipMalloc(out, bytes);
+  if (e != hipSuccess) {
+    trim();
+    e = hipMalloc(out, bytes);
+  }
+  if (e != hipSuccess)
+    return set_error(err, GHIP_ERR_OOM, "device allocation of %zu bytes failed: %s", bytes,
+                     hipGetErrorString(e));
+  return GHIP_OK;
+}
+
+void GHipBackend::release(void* p, size_t bytes) {
+  if (!p) return;
+  std::lock_guard<std::mutex> lk(mu);
+  if (finalized) return;
+  bytes = round_alloc(bytes ? bytes : 1);
+  free_blocks.emplace(bytes, p);
+  cached_bytes += bytes;
+}
+
+void GHipBackend::trim() {
+  std::lock_guard<std::mutex> lk(mu);
+  if (plan_only) return;
+  hipSetDevice(device);
+  hipDeviceSynchronize();
+  for (auto& kv : free_blocks) hipFree(kv.second);
+  free_blocks.clear();
+  cached_bytes = 0;
+}
+
+extern "C" GHipBackend* ghip_backend_new(const char* config, GHipError* err) {
+  auto be = std::make_unique<GHipBackend>();
+  std::string cfg = config ? config : "";
+  if (cfg == "plan") {
+    be->plan_only = true;
+    be->device_name = "plan-only (no device)";
+    return be.release();
+  }
+  int dev = 0;
+  if (!cfg.empty()) {
+    const char* p = strstr(cfg.c_str(), "device=");
+    if (cfg.rfind("hip", 0) != 0 || (cfg != "hip" && !p)) {
+      set_error(err, GHIP_ERR_INVALID_ARG, "backend config \"%s\": expected \"hip:device=N\"", cfg.c_str());
+      return nullptr;
+    }
+    if (p) dev = atoi(p + 7);
+  }
+  int count = 0;
+  if (hipGetDeviceCount(&count) != hipSuccess || count == 0) {
+    set_error(err, GHIP_ERR_HIP, "no HIP device visible");
+    return nullptr;
+  }
+  if (dev < 0 || dev >= count) {
+    set_error(err, GHIP_ERR_INVALID_ARG, "device %d out of range (have %d)", dev, count);
+    return nullptr;
+  }
+  be->device = dev;
+  hipError_t e = hipSetDevice(dev);
+  if (e != hipSuccess) {
+    check_hip(e, err, "hipSetDevice");
+    return nullptr;
+  }
+  // Default-priority stream (no priority changes on this platform).
+  e = hipStreamCreateWithFlags(&be->stream, hipStreamNonBlocking);
+  if (e != hipSuccess) {
+    check_hip(e, err, "hipStreamCreate");
+    return nullptr;
+  }
+  hipDeviceProp_t prop;
+  if (hipGetDeviceProperties(&prop, dev) == hipSuccess) {
+    char buf[256];
+    snprintf(buf, sizeof buf, "%s (%s, %d CUs, %zu MiB)", prop.name, prop.gcnArchName,
+             prop.multiProcessorCount, static_cast<size_t>(prop.totalGlobalMem >> 20));
+    be->device_name = buf;
+  }
+  return be.release();
+}
+
+extern "C" void ghip_backend_finalize(GHipBackend* b) {
+  if (!b || b->finalized) return;
+  b->trim();
+  std::lock_guard<std::mutex> lk(b->mu);
+  b->finalized = true;
+  if (b->stream) {
+    hipSetDevice(b->device);
+    hipStreamSynchronize(b->stream);
+    hipStreamDestroy(b->stream);
+    b->stream = nullptr;
+  }
+}
+
+extern "C" int ghip_backend_is_finalized(GHipBackend* b) { return !b || b->finalized; }
+
+extern "C" int ghip_backend_description(GHipBackend* b, char* buf, size_t buflen) {
+  if (!b || !buf || !buflen) return -1;
+  return snprintf(buf, buflen, "HIP GPU backend (%s)", b->device_name.c_str());
+}
+
+extern "C" int ghip_backend_num_devices(GHipBackend* b) { return b && !b->plan_only ? 1 : 0; }
+extern "C" void* ghip_backend_stream(GHipBackend* b) { return b ? b->stream : nullptr; }
+
+// ===========================================================================
+// Buffers
+// ===========================================================================
+static bool make_shape(int dtype, const int64_t* dims, int rank, Shape* s, GHipError* err,
+                       const char* what) {
+  if (dtype_size(dtype) == 0) {
+    set_error(err, GHIP_ERR_INVALID_ARG, "%s: invalid dtype %d", what, dtype);
+    return false;
+  }
+  if (rank < 0 || rank > kMaxRank || (rank > 0 && !dims)) {
+    set_error(err, GHIP_ERR_INVALID_ARG, "%s: rank %d not supported (max %d)", what, rank, kMaxRank);
+    return false;
+  }
+  s->dtype = dtype;
+  s->dims.assign(dims, dims + rank);
+  for (auto d : s->dims)
+    if (d < 0) {
+      set_error(err, GHIP_ERR_INVALID_ARG, "%s: negative dimension", what);
+      return false;
+    }
+  return true;
+}
+
+static GHipBuffer* new_buffer(GHipBackend* b, const Shape& s, GHipError* err) {
+  auto buf = std::make_unique<GHipBuffer>();
+  buf->backend = b;
+  buf->shape = s;
+  buf->cap = s.bytes();
+  if (b->alloc(buf->cap, &buf->ptr, err) != GHIP_OK) return nullptr;
+  return buf.release();
+}
+
+extern "C" GHipBuffer* ghip_buffer_new(GHipBackend* b, int dtype, const int64_t* dims, int rank,
+                                       GHipError* err) {
+  if (!b || b->finalized) { set_error(err, GHIP_ERR_STATE, "buffer_new: backend finalized"); return nullptr; }
+  Shape s;
+  if (!make_shape(dtype, dims, rank, &s, err, "buffer_new")) return nullptr;
+  return new_buffer(b, s, err);
+}
+
+extern "C" GHipBuffer* ghip_buffer_from_host(GHipBackend* b, int dtype, const int64_t* dims,
+                                             int rank, const void* data, size_t nbytes,
+                                             GHipError* err) {
+  if (!b || b->finalized) { set_error(err, GHIP_ERR_STATE, "BufferFromFlatData: backend finalized"); return nullptr; }
+  Shape s;
+  if (!make_shape(dtype, dims, rank, &s, err, "BufferFromFlatData")) return nullptr;
+  if (nbytes != s.bytes()) {
+    set_error(err, GHIP_ERR_INVALID_ARG, "BufferFromFlatData: %zu bytes given for shape %s (%zu bytes)",
+              nbytes, s.str().c_str(), s.bytes());
+    return nullptr;
+  }
+  GHipBuffer* buf = new_buffer(b, s, err);
+  if (!buf) return nullptr;
+  if (nbytes) {
+    hipSetDevice(b->device);
+    hipError_t e = hipMemcpyAsync(buf->ptr, data, nbytes, hipMemcpyHostToDevice, b->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(b->stream);
+    if (e != hipSuccess) {
+      check_hip(e, err, "BufferFromFlatData copy");
+      b->release(buf->ptr, buf->cap);
+      delete buf;
+      return nullptr;
+    }
+  }
+  return buf;
+}
+
+extern "C" int ghip_buffer_to_host(GHipBuffer* buf, void* data, size_t nbytes, GHipError* err) {
+  if (!buf || !buf->valid) return set_error(err, GHIP_ERR_STATE, "BufferToFlatData: buffer finalized");
+  if (nbytes != buf->shape.bytes())
+    return set_error(err, GHIP_ERR_INVALID_ARG, "BufferToFlatData: %zu bytes for shape %s (%zu bytes)",
+                     nbytes, buf->shape.str().c_str(), buf->shape.bytes());
+  if (!nbytes) return GHIP_OK;
+  GHipBackend* b = buf->backend;
+  hipSetDevice(b->device);
+  GHIP_CHECK(hipMemcpyAsync(data, buf->ptr, nbytes, hipMemcpyDeviceToHost, b->stream), err);
+  GHIP_CHECK(hipStreamSynchronize(b->stream), err);
+  return GHIP_OK;
+}
+
+extern "C" int ghip_buffer_shape(GHipBuffer* buf, int* dtype, int64_t* dims, int max_rank) {
+  if (!buf || !buf->valid) return -1;
+  if (dtype) *dtype = buf->shape.dtype;
+  for (int i = 0; i < buf->shape.rank() && i < max_rank; ++i) dims[i] = buf->shape.dims[i];
+  return buf->shape.rank();
+}
+
+extern "C" void* ghip_buffer_device_ptr(GHipBuffer* buf) { return buf && buf->valid ? buf->ptr : nullptr; }
+
+extern "C" void ghip_buffer_finalize(GHipBuffer* buf) {
+  if (!buf) return;
+  if (buf->valid && buf->backend) {
+    // Work queued on the stream may still read this memory: wait before reuse.
+    hipSetDevice(buf->backend->device);
+    if (buf->backend->stream) hipStreamSynchronize(buf->backend->stream);
+    buf->backend->release(buf->ptr, buf->cap);
+  }
+  buf->valid = false;
+  delete buf;
+}
+
+// ===========================================================================
+// Builder
+// ===========================================================================
+extern "C" GHipBuilder* ghip_builder_new(GHipBackend* b, const char* name, GHipError* err) {
+  if (!b || b->finalized) { set_error(err, GHIP_ERR_STATE, "Builder: backend finalized"); return nullptr; }
+  auto bl = new GHipBuilder();
+  bl->backend = b;
+  bl->name = name ? name : "";
+  return bl;
+}
+
+extern "C" void ghip_builder_finalize(GHipBuilder* bl) { delete bl; }
+
+extern "C" GHipFunction* ghip_builder_main(GHipBuilder* bl) {
+  if (!bl) return nullptr;
+  if (!bl->main) {
+    bl->main = std::make_unique<GHipFunction>();
+    bl->main->builder = bl;
+    bl->main->name = "main";
+  }
+  return bl->main.get();
+}
+
+// ===========================================================================
+// Function: shape inference helpers
+// ===========================================================================
+namespace {
+
+struct Ctx {
+  GHipFunction* f;
+  GHipError* err;
+  const char* op;
+  bool ok = true;
+  int fail(int code, const char* fmt, ...) {
+    char buf[400];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    set_error(err, code, "%s: %s", op, buf);
+    ok = false;
+    return -1;
+  }
+  const Node* node(int v) {
+    if (!f) { fail(GHIP_ERR_INVALID_ARG, "null function"); return nullptr; }
+    if (f->returned) { fail(GHIP_ERR_STATE, "function already returned"); return nullptr; }
+    if (v < 0 || v >= static_cast<int>(f->nodes.size())) {
+      fail(GHIP_ERR_INVALID_ARG, "value %d does not belong to function %s", v, f->name.c_str());
+      return nullptr;
+    }
+    return &f->nodes[v];
+  }
+};
+
+// numpy-style broadcast of two shapes (equal dims, size-1 dims, or rank-0 scalars).
+bool broadcast_dims(const std::vector<int64_t>& a, const std::vector<int64_t>& b,
+                    std::vector<int64_t>* out) {
+  if (a.empty()) { *out = b; return true; }
+  if (b.empty()) { *out = a; return true; }
+  size_t r = std::max(a.size(), b.size());
+  out->assign(r, 1);
+  for (size_t i = 0; i < r; ++i) {
+    int64_t da = i < r - a.size() ? 1 : a[i - (r - a.size())];
+    int64_t db = i < r - b.size() ? 1 : b[i - (r - b.size())];
+    if (da != db && da != 1 && db != 1) return false;
+    (*out)[i] = da == 1 ? db : da;
+  }
+  return true;
+}
+
+bool normalize_axes(const int* axes, int n, int rank, std::vector<int64_t>* out) {
+  out->clear();
+  std::set<int64_t> seen;
+  for (int i = 0; i < n; ++i) {
+    int64_t a = axes[i] < 0 ? axes[i] + rank : axes[i];
+    if (a < 0 || a >= rank || seen.count(a)) return false;
+    seen.insert(a);
+    out->push_back(a);
+  }
+  return true;
+}
+
+}  // namespace
+
+#define FN_BEGIN(opname) Ctx c{f, err, opname}
+
+extern "C" GHipValue ghip_fn_parameter(GHipFunction* f, const char* name, int dtype,
+                                       const int64_t* dims, int rank, GHipError* err) {
+  FN_BEGIN("Parameter");
+  if (!f) return c.fail(GHIP_ERR_INVALID_ARG, "null function");
+  if (f->returned) return c.fail(GHIP_ERR_STATE, "function already returned");
+  Node n{Kind::Param};
+  if (!make_shape(dtype, dims, rank, &n.shape, err, "Parameter")) return -1;
+  n.name = name ? name : "";
+  n.i0 = static_cast<int64_t>(f->params.size());
+  int id = f->add(std::move(n));
+  f->params.push_back(id);
+  return id;
+}
+
+extern "C" GHipValue ghip_fn_constant(GHipFunction* f, int dtype, const int64_t* dims, int rank,
+                                      const void* data, size_t nbytes, GHipError* err) {
+  FN_BEGIN("Constant");
+  if (!f) return c.fail(GHIP_ERR_INVALID_ARG, "null function");
+  if (f->returned) return c.fail(GHIP_ERR_STATE, "function already returned");
+  Node n{Kind::Const};
+  if (!make_shape(dtype, dims, rank, &n.shape, err, "Constant")) return -1;
+  if (nbytes != n.shape.bytes())
+    return c.fail(GHIP_ERR_INVALID_ARG, "%zu bytes for shape %s", nbytes, n.shape.str().c_str());
+  if (nbytes && !data) return c.fail(GHIP_ERR_INVALID_ARG, "null data");
+  n.data.assign(static_cast<const uint8_t*>(data), static_cast<const uint8_t*>(data) + nbytes);
+  return f->add(std::move(n));
+}
+
+extern "C" GHipValue ghip_fn_iota(GHipFunction* f, int dtype, const int64_t* dims, int rank,
+                                  int axis, GHipError* err) {
+  FN_BEGIN("Iota");
+  if (!f) return c.fail(GHIP_ERR_INVALID_ARG, "null function");
+  Node n{Kind::Iota};
+  if (!make_shape(dtype, dims, rank, &n.shape, err, "Iota")) return -1;
+  if (dtype == GHIP_DTYPE_BOOL) return c.fail(GHIP_ERR_INVALID_ARG, "bool iota");
+  if (axis < 0) axis += rank;
+  if (axis < 0 || axis >= rank) return c.fail(GHIP_ERR_INVALID_ARG, "axis out of range");
+  n.i0 = axis;
+  return f->add(std::move(n));
+}
+
+extern "C" GHipValue ghip_fn_unary(GHipFunction* f, int op, GHipValue x, GHipError* err) {
+  FN_BEGIN("Unary");
+  const Node* a = c.node(x);
+  if (!a) return -1;
+  if (op < 0 || op >= GHIP_UNARY_COUNT) return c.fail(GHIP_ERR_INVALID_ARG, "bad unary op %d", op);
+  const int dt = a->shape.dtype;
+  Node n{Kind::Unary};
+  n.sub = op;
+  n.in = {x};
+  n.shape = a->shape;
+  switch (op) {
+    case GHIP_UNARY_SQRT: case GHIP_UNARY_RSQRT: case GHIP_UNARY_EXP: case GHIP_UNARY_EXPM1:
+    case GHIP_UNARY_LOG: case GHIP_UNARY_LOG1P: case GHIP_UNARY_SIN: case GHIP_UNARY_COS:
+    case GHIP_UNARY_TANH: case GHIP_UNARY_LOGISTIC: case GHIP_UNARY_ERF: case GHIP_UNARY_FLOOR:
+    case GHIP_UNARY_CEIL: case GHIP_UNARY_ROUND:
+      if (!dtype_is_float(dt)) return c.fail(GHIP_ERR_INVALID_ARG, "op %d needs a float operand, got %s", op, dtype_name(dt));
+      break;
+    case GHIP_UNARY_LOGICAL_NOT:
+      if (dt != GHIP_DTYPE_BOOL) return c.fail(GHIP_ERR_INVALID_ARG, "LogicalNot needs bool");
+      break;
+    case GHIP_UNARY_BITWISE_NOT:
+      if (!dtype_is_int(dt)) return c.fail(GHIP_ERR_INVALID_ARG, "BitwiseNot needs an integer");
+      break;
+    case GHIP_UNARY_IS_FINITE: case GHIP_UNARY_IS_NAN:
+      if (!dtype_is_float(dt)) return c.fail(GHIP_ERR_INVALID_ARG, "needs a float operand");
+      n.shape.dtype = GHIP_DTYPE_BOOL;
+      break;
+    case GHIP_UNARY_ABS: case GHIP_UNARY_NEG: case GHIP_UNARY_SIGN:
+      if (dt == GHIP_DTYPE_BOOL) return c.fail(GHIP_ERR_INVALID_ARG, "bool operand");
+      break;
+    default: break;
+  }
+  return f->add(std::move(n));
+}
+
+extern "C" GHipValue ghip_fn_binary(GHipFunction* f, int op, GHipValue lhs, GHipValue rhs,
+                                    GHipError* err) {
+  FN_BEGIN("Binary");
+  const Node* a = c.node(lhs);
+  if (!a) return -1;
+  const Node* b = c.node(rhs);
+  if (!b) return -1;
+  if (op < 0 || op >= GHIP_BINARY_COUNT) return c.fail(GHIP_ERR_INVALID_ARG, "bad binary op %d", op);
+  if (a->shape.dtype != b->shape.dtype)
+    return c.fail(GHIP_ERR_INVALID_ARG, "dtype mismatch %s vs %s", dtype_name(a->shape.dtype), dtype_name(b->shape.dtype));
+  const int dt = a->shape.dtype;
+  const bool logical = op == GHIP_BINARY_LOGICAL_AND || op == GHIP_BINARY_LOGICAL_OR || op == GHIP_BINARY_LOGICAL_XOR;
+  const bool bitwise = op >= GHIP_BINARY_BITWISE_AND;
+  if (logical && dt != GHIP_DTYPE_BOOL) return c.fail(GHIP_ERR_INVALID_ARG, "logical op needs bool");
+  if (bitwise && !dtype_is_int(dt)) return c.fail(GHIP_ERR_INVALID_ARG, "bitwise op needs integers");
+  if (!logical && !bitwise && dt == GHIP_DTYPE_BOOL) return c.fail(GHIP_ERR_INVALID_ARG, "arithmetic on bool");
+  if (op == GHIP_BINARY_ATAN2 && !dtype_is_float(dt)) return c.fail(GHIP_ERR_INVALID_ARG, "Atan2 needs floats");
+  Node n{Kind::Binary};
+  n.sub = op;
+  n.in = {lhs, rhs};
+  n.shape.dtype = dt;
+  if (!broadcast_dims(a->shape.dims, b->shape.dims, &n.shape.dims))
+    return c.fail(GHIP_ERR_INVALID_ARG, "incompatible shapes %s and %s", a->shape.str().c_str(), b->shape.str().c_str());
+  return f->add(std::move(n));
+}
+
+extern "C" GHipValue ghip_fn_compare(GHipFunction* f, int op, GHipValue lhs, GHipValue rhs,
+                                     GHipError* err) {
+  FN_BEGIN("Compare");
+  const Node* a = c.node(lhs);
+  if (!a) return -1;
+  const Node* b = c.node(rhs);
+  if (!b) return -1;
+  if (op < 0 || op >= GHIP_CMP_COUNT) return c.fail(GHIP_ERR_INVALID_ARG, "bad comparison %d", op);
+  if (a->shape.dtype != b->shape.dtype) return c.fail(GHIP_ERR_INVALID_ARG, "dtype mismatch");
+  Node n{Kind::Compare};
+  n.sub = op;
+  n.in = {lhs, rhs};
+  n.shape.dtype = GHIP_DTYPE_BOOL;
+  if (!broadcast_dims(a->shape.dims, b->shape.dims, &n.shape.dims))
+    return c.fail(GHIP_ERR_INVALID_ARG, "incompatible shapes %s and %s", a->shape.str().c_str(), b->shape.str().c_str());
+  return f->add(std::move(n));
+}
+
+extern "C" GHipValue ghip_fn_where(GHipFunction* f, GHipValue cond, GHipValue on_true,
+                                   GHipValue on_false, GHipError* err) {
+  FN_BEGIN("Where");
+  const Node* p = c.node(cond);
+  if (!p) return -1;
+  const Node* t = c.node(on_true);
+  if (!t) return -1;
+  const Node* e = c.node(on_false);
+  if (!e) return -1;
+  if (p->shape.dtype != GHIP_DTYPE_BOOL) return c.fail(GHIP_ERR_INVALID_ARG, "condition must be bool");
+  if (t->shape.dtype != e->shape.dtype) return c.fail(GHIP_ERR_INVALID_ARG, "branch dtypes differ");
+  Node n{Kind::Where};
+  n.in = {cond, on_true, on_false};
+  n.shape.dtype = t->shape.dtype;
+  std::vector<int64_t> d1;
+  if (!broadcast_dims(t->shape.dims, e->shape.dims, &d1) ||
+      !broadcast_dims(p->shape.dims, d1, &n.shape.dims))
+    return c.fail(GHIP_ERR_INVALID_ARG, "incompatible shapes");
+  return f->add(std::move(n));
+}
+
+extern "C" GHipValue ghip_fn_clamp(GHipFunction* f, GHipValue lo, GHipValue x, GHipValue hi,
+                                   GHipError* err) {
+  FN_BEGIN("Clamp");
+  const Node* l = c.node(lo);
+  if (!l) return -1;
+  const Node* v = c.node(x);
+  if (!v) return -1;
+  const Node* h = c.node(hi);
+  if (!h) return -1;
+  if (l->shape.dtype != v->shape.dtype || h->shape.dtype != v->shape.dtype)
+    return c.fail(GHIP_ERR_INVALID_ARG, "dtype mismatch");
+  std::vector<int64_t> tmp;
+  if (!broadcast_dims(l->shape.dims, v->shape.dims, &tmp) || tmp != v->shape.dims ||
+      !broadcast_dims(h->shape.dims, v->shape.dims, &tmp) || tmp != v->shape.dims)
+    return c.fail(GHIP_ERR_INVALID_ARG, "min/max must be scalars or x's shape");
+  Node n{Kind::Clamp};
+  n.in = {lo, x, hi};
+  n.shape = v->shape;
+  return f->add(std::move(n));
+}
+
+extern "C" GHipValue ghip_fn_convert_dtype(GHipFunction* f, GHipValue x, int dtype, GHipError* err) {
+  FN_BEGIN("ConvertDType");
+  const Node* a = c.node(x);
+  if (!a) return -1;
+  if (dtype_size(dtype) == 0) return c.fail(GHIP_ERR_INVALID_ARG, "invalid dtype %d", dtype);
+  Node n{Kind::Convert};
+  n.in = {x};
+  n.shape = a->shape;
+  n.shape.dtype = dtype;
+  return f->add(std::move(n));
+}
+
+extern "C" GHipValue ghip_fn_reshape(GHipFunction* f, GHipValue x, const int64_t* dims, int rank,
+                                     GHipError* err) {
+  FN_BEGIN("Reshape");
+  const Node* a = c.node(x);
+  if (!a) return -1;
+  Node n{Kind::Reshape};
+  if (!make_shape(a->shape.dtype, dims, rank, &n.shape, err, "Reshape")) return -1;
+  if (n.shape.size() != a->shape.size())
+    return c.fail(GHIP_ERR_INVALID_ARG, "cannot reshape %s to %s", a->shape.str().c_str(), n.shape.str().c_str());
+  n.in = {x};
+  return f->add(std::move(n));
+}
+
+extern "C" GHipValue ghip_fn_transpose(GHipFunction* f, GHipValue x, const int* perm, int rank,
+                                       GHipError* err) {
+  FN_BEGIN("Transpose");
+  const Node* a = c.node(x);
+  if (!a) return -1;
+  if (rank != a->shape.rank()) return c.fail(GHIP_ERR_INVALID_ARG, "permutation rank %d vs %d", rank, a->shape.rank());
+  std::vector<int64_t> p;
+  if (!normalize_axes(perm, rank, rank, &p)) return c.fail(GHIP_ERR_INVALID_ARG, "invalid permutation");
+  Node n{Kind::Transpose};
+  n.in = {x};
+  n.a0 = p;
+  n.shape.dtype = a->shape.dtype;
+  for (auto i : p) n.shape.dims.push_back(a->shape.dims[i]);
+  return f->add(std::move(n));
+}
+
+extern "C" GHipValue ghip_fn_broadcast_in_dim(GHipFunction* f, GHipValue x, const int64_t* dims,
+                                              int rank, const int* axes, int naxes, GHipError* err) {
+  FN_BEGIN("BroadcastInDim");
+  const Node* a = c.node(x);
+  if (!a) return -1;
+  Node n{Kind::Broadcast};
+  if (!make_shape(a->shape.dtype, dims, rank, &n.shape, err, "BroadcastInDim")) return -1;
+  if (naxes != a->shape.rank()) return c.fail(GHIP_ERR_INVALID_ARG, "%d axes for rank-%d operand", naxes, a->shape.rank());
+  std::vector<int64_t> ax;
+  if (!normalize_axes(axes, naxes, rank, &ax)) return c.fail(GHIP_ERR_INVALID_ARG, "invalid broadcast axes");
+  for (int i = 0; i < naxes; ++i) {
+    if (i > 0 && ax[i] <= ax[i - 1]) return c.fail(GHIP_ERR_INVALID_ARG, "broadcast axes must increase");
+    const int64_t d = a->shape.dims[i];
+    if (d != 1 && d != n.shape.dims[ax[i]])
+      return c.fail(GHIP_ERR_INVALID_ARG, "operand dim %d (%lld) vs output dim %lld", i, (long long)d,
+                    (long long)n.shape.dims[ax[i]]);
+  }
+  n.in = {x};
+  n.a0 = ax;
+  return f->add(std::move(n));
+}
+
+extern "C" GHipValue ghip_fn_reduce(GHipFunction* f, int op, GHipValue x, const int* axes, int naxes,
+                                    GHipError* err) {
+  FN_BEGIN("Reduce");
+  const Node* a = c.node(x);
+  if (!a) return -1;
+  if (op < 0 || op > GHIP_REDUCE_MIN) return c.fail(GHIP_ERR_INVALID_ARG, "bad reduce op %d", op);
+  if (a->shape.dtype == GHIP_DTYPE_BOOL) return c.fail(GHIP_ERR_INVALID_ARG, "bool reduction");
+  std::vector<int64_t> ax;
+  if (naxes == 0) {  // empty axes: reduce everything (function.go:1152-1158)
+    for (int i = 0; i < a->shape.rank(); ++i) ax.push_back(i);
+  } else if (!normalize_axes(axes, naxes, a->shape.rank(), &ax)) {
+    return c.fail(GHIP_ERR_INVALID_ARG, "invalid axes");
+  }
+  std::sort(ax.begin(), ax.end());
+  Node n{Kind::Reduce};
+  n.sub = op;
+  n.in = {x};
+  n.a0 = ax;
+  n.shape.dtype = a->shape.dtype;
+  for (int i = 0; i < a->shape.rank(); ++i)
+    if (!std::binary_search(ax.begin(), ax.end(), i)) n.shape.dims.push_back(a->shape.dims[i]);
+  return f->add(std::move(n));
+}
+
+extern "C" GHipValue ghip_fn_arg_min_max(GHipFunction* f, GHipValue x, int axis, int out_dtype,
+                                         int is_min, GHipError* err) {
+  FN_BEGIN("ArgMinMax");
+  const Node* a = c.node(x);
+  if (!a) return -1;
+  const int r = a->shape.rank();
+  if (axis < 0) axis += r;
+  if (axis < 0 || axis >= r) return c.fail(GHIP_ERR_INVALID_ARG, "axis out of range");
+  if (a->shape.dims[axis] == 0) return c.fail(GHIP_ERR_INVALID_ARG, "empty reduced axis");
+  if (out_dtype != GHIP_DTYPE_INT32 && out_dtype != GHIP_DTYPE_INT64)
+    return c.fail(GHIP_ERR_UNSUPPORTED, "output dtype %s", dtype_name(out_dtype));
+  if (!dtype_is_float(a->shape.dtype)) return c.fail(GHIP_ERR_UNSUPPORTED, "input dtype %s", dtype_name(a->shape.dtype));
+  Node n{Kind::ArgMinMax};
+  n.in = {x};
+  n.i0 = axis;
+  n.i1 = is_min ? 1 : 0;
+  n.shape.dtype = out_dtype;
+  for (int i = 0; i < r; ++i)
+    if (i != axis) n.shape.dims.push_back(a->shape.dims[i]);
+  return f->add(std::move(n));
+}
+
+extern "C" GHipValue ghip_fn_dot_general(GHipFunction* f, GHipValue lhs, const int* lc, int nlc,
+                                         const int* lb, int nlb, GHipValue rhs, const int* rc,
+                                         int nrc, const int* rb, int nrb, GHipError* err) {
+  FN_BEGIN("DotGeneral");
+  const Node* a = c.node(lhs);
+  if (!a) return -1;
+  const Node* b = c.node(rhs);
+  if (!b) return -1;
+  if (a->shape.dtype != b->shape.dtype) return c.fail(GHIP_ERR_INVALID_ARG, "dtype mismatch");
+  if (nlc != nrc || nlb != nrb) return c.fail(GHIP_ERR_INVALID_ARG, "axis count mismatch");
+  std::vector<int64_t> lca, lba, rca, rba;
+  std::vector<int> lall(lc, lc + nlc), rall(rc, rc + nrc);
+  lall.insert(lall.end(), lb, lb + nlb);
+  rall.insert(rall.end(), rb, rb + nrb);
+  std::vector<int64_t> tmp;
+  if (!normalize_axes(lall.data(), nlc + nlb, a->shape.rank(), &tmp) ||
+      !normalize_axes(rall.data(), nrc + nrb, b->shape.rank(), &tmp))
+    return c.fail(GHIP_ERR_INVALID_ARG, "invalid or repeated axes");
+  normalize_axes(lc, nlc, a->shape.rank(), &lca);
+  normalize_axes(lb, nlb, a->shape.rank(), &lba);
+  normalize_axes(rc, nrc, b->shape.rank(), &rca);
+  normalize_axes(rb, nrb, b->shape.rank(), &rba);
+  for (int i = 0; i < nlc; ++i)
+    if (a->shape.dims[lca[i]] != b->shape.dims[rca[i]]) return c.fail(GHIP_ERR_INVALID_ARG, "contracting dims differ");
+  for (int i = 0; i < nlb; ++i)
+    if (a->shape.dims[lba[i]] != b->shape.dims[rba[i]]) return c.fail(GHIP_ERR_INVALID_ARG, "batch dims differ");
+  if (!dtype_is_float(a->shape.dtype) || a->shape.dtype == GHIP_DTYPE_FLOAT16 || a->shape.dtype == GHIP_DTYPE_FLOAT64)
+    return c.fail(GHIP_ERR_UNSUPPORTED, "dtype %s (float32 and bfloat16 are lowered)", dtype_name(a->shape.dtype));
+  Node n{Kind::Dot};
+  n.in = {lhs, rhs};
+  n.a0 = lca; n.a1 = lba; n.a2 = rca; n.a3 = rba;
+  // Output: [batch..., lhs free..., rhs free...] (dotgeneral.go:15-53), lhs dtype.
+  n.shape.dtype = a->shape.dtype;
+  for (auto ax : lba) n.shape.dims.push_back(a->shape.dims[ax]);
+  for (int i = 0; i < a->shape.rank(); ++i)
+    if (std::find(lca.begin(), lca.end(), i) == lca.end() && std::find(lba.begin(), lba.end(), i) == lba.end())
+      n.shape.dims.push_back(a->shape.dims[i]);
+  for (int i = 0; i < b->shape.rank(); ++i)
+    if (std::find(rca.begin(), rca.end(), i) == rca.end() && std::find(rba.begin(), rba.end(), i) == rba.end())
+      n.shape.dims.push_back(b->shape.dims[i]);
+  if (n.shape.rank() > kMaxRank) return c.fail(GHIP_ERR_UNSUPPORTED, "output rank too large");
+  return f->add(std::move(n));
+}
+
+extern "C" GHipValue ghip_fn_gather(GHipFunction* f, GHipValue operand, GHipValue start_indices,
+                                    int index_vector_axis, const int* offset_output_axes, int n_offset,
+                                    const int* collapsed_slice_axes, int n_collapsed,
+                                    const int* start_index_map, int n_map, const int64_t* slice_sizes,
+                                    int n_sizes, int indices_are_sorted, GHipError* err) {
+  FN_BEGIN("Gather");
+  const Node* op = c.node(operand);
+  if (!op) return -1;
+  const Node* ix = c.node(start_indices);
+  if (!ix) return -1;
+  const int r = op->shape.rank(), ir = ix->shape.rank();
+  if (!dtype_is_int(ix->shape.dtype)) return c.fail(GHIP_ERR_INVALID_ARG, "indices must be integers");
+  if (n_sizes != r) return c.fail(GHIP_ERR_INVALID_ARG, "slice_sizes must have operand rank");
+  if (index_vector_axis < 0 || index_vector_axis > ir) return c.fail(GHIP_ERR_INVALID_ARG, "bad index_vector_axis");
+  const int64_t ivec = index_vector_axis < ir ? ix->shape.dims[index_vector_axis] : 1;
+  if (ivec != n_map) return c.fail(GHIP_ERR_INVALID_ARG, "index vector size %lld vs start_index_map %d", (long long)ivec, n_map);
+  for (int i = 0; i < r; ++i)
+    if (slice_sizes[i] < 0 || slice_sizes[i] > op->shape.dims[i]) return c.fail(GHIP_ERR_INVALID_ARG, "slice size out of range");
+  std::vector<int64_t> coll, omap, offs;
+  if (!normalize_axes(collapsed_slice_axes, n_collapsed, r, &coll) || !normalize_axes(start_index_map, n_map, r, &omap))
+    return c.fail(GHIP_ERR_INVALID_ARG, "invalid axes");
+  for (auto a : coll)
+    if (slice_sizes[a] != 1) return c.fail(GHIP_ERR_INVALID_ARG, "collapsed axes need slice size 1");
+  std::vector<int64_t> offset_dims;
+  for (int i = 0; i < r; ++i)
+    if (std::find(coll.begin(), coll.end(), i) == coll.end()) offset_dims.push_back(slice_sizes[i]);
+  if (static_cast<int>(offset_dims.size()) != n_offset) return c.fail(GHIP_ERR_INVALID_ARG, "offset_output_axes size");
+  std::vector<int64_t> batch_dims;
+  for (int i = 0; i < ir; ++i)
+    if (i != index_vector_axis) batch_dims.push_back(ix->shape.dims[i]);
+  const int orank = static_cast<int>(batch_dims.size()) + n_offset;
+  if (!normalize_axes(offset_output_axes, n_offset, orank, &offs)) return c.fail(GHIP_ERR_INVALID_ARG, "bad offset_output_axes");
+  Node n{Kind::Gather};
+  n.in = {operand, start_indices};
+  n.shape.dtype = op->shape.dtype;
+  n.shape.dims.assign(orank, 0);
+  size_t bi = 0, oi = 0;
+  for (int i = 0; i < orank; ++i) {
+    if (std::find(offs.begin(), offs.end(), i) != offs.end()) n.shape.dims[i] = offset_dims[oi++];
+    else n.shape.dims[i] = batch_dims[bi++];
+  }
+  n.i0 = index_vector_axis;
+  n.i1 = indices_are_sorted;
+  n.a0 = offs;
+  n.a1 = coll;
+  n.a2 = omap;
+  n.a3.assign(slice_sizes, slice_sizes + n_sizes);
+  return f->add(std::move(n));
+}
+
+extern "C" GHipValue ghip_fn_slice(GHipFunction* f, GHipValue x, const int64_t* starts,
+                                   const int64_t* limits, const int64_t* strides, int rank,
+                                   GHipError* err) {
+  FN_BEGIN("Slice");
+  const Node* a = c.node(x);
+  if (!a) return -1;
+  if (rank != a->shape.rank()) return c.fail(GHIP_ERR_INVALID_ARG, "rank mismatch");
+  Node n{Kind::Slice};
+  n.in = {x};
+  n.shape.dtype = a->shape.dtype;
+  for (int i = 0; i < rank; ++i) {
+    const int64_t st = strides ? strides[i] : 1;
+    if (starts[i] < 0 || limits[i] > a->shape.dims[i] || starts[i] > limits[i] || st <= 0)
+      return c.fail(GHIP_ERR_INVALID_ARG, "bad bounds on axis %d", i);
+    n.a0.push_back(starts[i]);
+    n.a1.push_back(limits[i]);
+    n.a2.push_back(st);
+    n.shape.dims.push_back((limits[i] - starts[i] + st - 1) / st);
+  }
+  return f->add(std::move(n));
+}
+
+extern "C" GHipValue ghip_fn_concatenate(GHipFunction* f, int axis, const GHipValue* operands, int cnt,
+                                         GHipError* err) {
+  FN_BEGIN("Concatenate");
+  if (cnt <= 0) return c.fail(GHIP_ERR_INVALID_ARG, "no operands");
+  const Node* first = c.node(operands[0]);
+  if (!first) return -1;
+  const int r = first->shape.rank();
+  if (axis < 0) axis += r;
+  if (axis < 0 || axis >= r) return c.fail(GHIP_ERR_INVALID_ARG, "axis out of range");
+  Node n{Kind::Concat};
+  n.shape = first->shape;
+  n.shape.dims[axis] = 0;
+  for (int i = 0; i < cnt; ++i) {
+    const Node* o = c.node(operands[i]);
+    if (!o) return -1;
+    if (o->shape.dtype != first->shape.dtype || o->shape.rank() != r) return c.fail(GHIP_ERR_INVALID_ARG, "operand %d mismatch", i);
+    for (int d = 0; d < r; ++d)
+      if (d != axis && o->shape.dims[d] != first->shape.dims[d]) return c.fail(GHIP_ERR_INVALID_ARG, "operand %d dims", i);
+    n.shape.dims[axis] += o->shape.dims[axis];
+    n.in.push_back(operands[i]);
+  }
+  n.i0 = axis;
+  return f->add(std::move(n));
+}
+
+extern "C" GHipValue ghip_fn_reverse(GHipFunction* f, GHipValue x, const int* axes, int naxes,
+                                     GHipError* err) {
+  FN_BEGIN("Reverse");
+  const Node* a = c.node(x);
+  if (!a) return -1;
+  std::vector<int64_t> ax;
+  if (!normalize_axes(axes, naxes, a->shape.rank(), &ax)) return c.fail(GHIP_ERR_INVALID_ARG, "invalid axes");
+  Node n{Kind::Reverse};
+  n.in = {x};
+  n.a0 = ax;
+  n.shape = a->shape;
+  return f->add(std::move(n));
+}
+
+extern "C" GHipValue ghip_fn_fused_softmax(GHipFunction* f, GHipValue x, int axis, GHipError* err) {
+  FN_BEGIN("FusedSoftmax");
+  const Node* a = c.node(x);
+  if (!a) return -1;
+  const int r = a->shape.rank();
+  if (axis < 0) axis += r;
+  if (axis < 0 || axis >= r) return c.fail(GHIP_ERR_INVALID_ARG, "axis out of range");
+  if (!dtype_is_float(a->shape.dtype)) return c.fail(GHIP_ERR_INVALID_ARG, "float input required");
+  Node n{Kind::Softmax};
+  n.in = {x};
+  n.i0 = axis;
+  n.shape = a->shape;
+  return f->add(std::move(n));
+}
+
+extern "C" GHipValue ghip_fn_fused_layer_norm(GHipFunction* f, GHipValue x, const int* axes, int naxes,
+                                              double epsilon, GHipValue gamma, GHipValue beta,
+                                              GHipError* err) {
+  FN_BEGIN("FusedLayerNorm");
+  const Node* a = c.node(x);
+  if (!a) return -1;
+  const int r = a->shape.rank();
+  std::vector<int64_t> ax;
+  if (!normalize_axes(axes, naxes, r, &ax) || naxes == 0)
+    return c.fail(GHIP_ERR_INVALID_ARG, "axis out of range for rank %d", r);  // function.go:2416-2427
+  std::sort(ax.begin(), ax.end());
+  if (!dtype_is_float(a->shape.dtype)) return c.fail(GHIP_ERR_INVALID_ARG, "float input required");
+  Node n{Kind::LayerNorm};
+  n.in = {x, gamma, beta};
+  n.a0 = ax;
+  n.f0 = epsilon;
+  n.shape = a->shape;
+  int64_t norm = 1;
+  for (auto d : ax) norm *= a->shape.dims[d];
+  for (int which = 1; which <= 2; ++which) {
+    const int v = n.in[which];
+    if (v < 0) continue;
+    const Node* p = c.node(v);
+    if (!p) return -1;
+    if (p->shape.dtype != a->shape.dtype) return c.fail(GHIP_ERR_INVALID_ARG, "gamma/beta dtype");
+    if (p->shape.size() != norm) return c.fail(GHIP_ERR_INVALID_ARG, "gamma/beta must cover the normalized axes");
+  }
+  return f->add(std::move(n));
+}
+
+extern "C" GHipValue ghip_fn_fused_sdpa(GHipFunction* f, GHipValue q, GHipValue k, GHipValue v,
+                                        GHipValue mask, int num_heads, int num_kv_heads, int layout,
+                                        double scale, int causal, GHipError* err) {
+  FN_BEGIN("FusedScaledDotProductAttention");
+  const Node* qn = c.node(q);
+  if (!qn) return -1;
+  const Node* kn = c.node(k);
+  if (!kn) return -1;
+  const Node* vn = c.node(v);
+  if (!vn) return -1;
+  if (qn->shape.rank() != 4) return c.fail(GHIP_ERR_INVALID_ARG, "query must have rank 4, got %d", qn->shape.rank());
+  if (num_heads <= 0 || num_kv_heads <= 0 || num_heads % num_kv_heads)
+    return c.fail(GHIP_ERR_INVALID_ARG, "numHeads (%d) must be positive and divisible by numKVHeads (%d)", num_heads, num_kv_heads);
+  if (layout != GHIP_LAYOUT_BHSD && layout != GHIP_LAYOUT_BSHD) return c.fail(GHIP_ERR_INVALID_ARG, "bad layout");
+  if (kn->shape.rank() != 4 || vn->shape.rank() != 4) return c.fail(GHIP_ERR_INVALID_ARG, "k/v must have rank 4");
+  if (qn->shape.dtype != kn->shape.dtype || qn->shape.dtype != vn->shape.dtype)
+    return c.fail(GHIP_ERR_INVALID_ARG, "q/k/v dtypes differ");
+  const int ha = layout == GHIP_LAYOUT_BHSD ? 1 : 2, sa = layout == GHIP_LAYOUT_BHSD ? 2 : 1;
+  if (qn->shape.dims[ha] != num_heads || kn->shape.dims[ha] != num_kv_heads || vn->shape.dims[ha] != num_kv_heads)
+    return c.fail(GHIP_ERR_INVALID_ARG, "head counts do not match the shapes");
+  if (kn->shape.dims[0] != qn->shape.dims[0] || kn->shape.dims[3] != qn->shape.dims[3] ||
+      kn->shape.dims[sa] != vn->shape.dims[sa] || vn->shape.dims[0] != qn->shape.dims[0])
+    return c.fail(GHIP_ERR_INVALID_ARG, "q/k/v shapes are inconsistent");
+  if (mask >= 0) {
+    const Node* m = c.node(mask);
+    if (!m) return -1;
+    if (m->shape.dtype != GHIP_DTYPE_BOOL && m->shape.dtype != qn->shape.dtype)
+      return c.fail(GHIP_ERR_INVALID_ARG, "mask must be bool or additive in q's dtype");
+  }
+  Node n{Kind::SDPA};
+  n.in = {q, k, v, mask};
+  n.i0 = num_heads;
+  n.i1 = num_kv_heads;
+  n.i2 = layout;
+  n.i3 = causal ? 1 : 0;
+  n.f0 = scale;
+  n.shape = qn->shape;
+  n.shape.dims[3] = vn->shape.dims[3];
+  return f->add(std::move(n));
+}
+
+extern "C" int ghip_fn_return(GHipFunction* f, const GHipValue* outputs, int cnt, GHipError* err) {
+  FN_BEGIN("Return");
+  if (!f) return c.fail(GHIP_ERR_INVALID_ARG, "null function");
+  if (f->returned) return set_error(err, GHIP_ERR_STATE, "Return: called twice");
+  for (int i = 0; i < cnt; ++i)
+    if (outputs[i] < 0 || outputs[i] >= static_cast<int>(f->nodes.size()))
+      return set_error(err, GHIP_ERR_INVALID_ARG, "Return: output %d is not a value of this function", i);
+  f->outputs.assign(outputs, outputs + cnt);
+  f->returned = true;
+  return GHIP_OK;
+}
+
+extern "C" int ghip_fn_value_shape(GHipFunction* f, GHipValue v, int* dtype, int64_t* dims, int max_rank) {
+  if (!f || v < 0 || v >= static_cast<int>(f->nodes.size())) return -1;
+  const Shape& s = f->nodes[v].shape;
+  if (dtype) *dtype = s.dtype;
+  for (int i = 0; i < s.rank() && i < max_rank; ++i) dims[i] = s.dims[i];
+  return s.rank();
+}

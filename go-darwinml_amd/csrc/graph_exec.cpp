@@ -1,0 +1,178 @@
+// Compile and Execute (builder.go:72-109, executable.go:19-112).
+//
+// Compile lowers the graph once (graph_lower.cpp) and uploads constants to
+// device memory owned by the executable.  Execute validates the inputs like the
+// reference (executable.go:54-68), allocates the outputs from the backend's
+// caching allocator, binds every plan slot to a device pointer (inputs, constants,
+// the executable's arena, outputs) and launches the steps on the backend stream.
+// It does not wait: buffers are device resident, and reading one back
+// (BufferToFlatData) or releasing one synchronises the stream.
+#include <hip/hip_runtime.h>
+#include <string.h>
+
+#include <algorithm>
+
+#include "common.h"
+#include "graph.h"
+
+using namespace ghip;
+
+extern "C" GHipExecutable* ghip_builder_compile(GHipBuilder* bl, GHipError* err) {
+  if (!bl) { set_error(err, GHIP_ERR_INVALID_ARG, "Compile: null builder"); return nullptr; }
+  if (bl->compiled) { set_error(err, GHIP_ERR_STATE, "Builder already compiled"); return nullptr; }
+  if (!bl->main) { set_error(err, GHIP_ERR_STATE, "Builder has no main function"); return nullptr; }
+  if (!bl->main->returned) { set_error(err, GHIP_ERR_STATE, "Main function has no Return() call"); return nullptr; }
+  GHipBackend* be = bl->backend;
+  if (!be || be->finalized) { set_error(err, GHIP_ERR_STATE, "Compile: backend finalized"); return nullptr; }
+  bl->compiled = true;
+  auto ex = std::make_unique<GHipExecutable>();
+  ex->backend = be;
+  GHipFunction* fn = bl->main.get();
+  for (int p : fn->params) {
+    ex->in_shapes.push_back(fn->nodes[p].shape);
+    ex->in_names.push_back(fn->nodes[p].name);
+  }
+  for (int o : fn->outputs) ex->out_shapes.push_back(fn->nodes[o].shape);
+  if (lower(be, fn, &ex->plan, err) != GHIP_OK) return nullptr;
+  if (!be->plan_only) {
+    hipSetDevice(be->device);
+    for (size_t s = 0; s < ex->plan.slots.size(); ++s) {
+      Slot& sl = ex->plan.slots[s];
+      if (sl.kind != SlotKind::Const) continue;
+      void* p = nullptr;
+      if (be->alloc(sl.bytes, &p, err) != GHIP_OK) {
+        ghip_exec_finalize(ex.release());
+        return nullptr;
+      }
+      ex->owned_consts.emplace_back(p, sl.bytes);
+      sl.const_ptr = p;
+      const auto& data = ex->plan.const_data[s];
+      if (!data.empty()) {
+        hipError_t e = hipMemcpyAsync(p, data.data(), data.size(), hipMemcpyHostToDevice, be->stream);
+        if (e == hipSuccess) e = hipStreamSynchronize(be->stream);
+        if (e != hipSuccess) {
+          check_hip(e, err, "Compile: constant upload");
+          ghip_exec_finalize(ex.release());
+          return nullptr;
+        }
+      }
+    }
+  }
+  return ex.release();
+}
+
+extern "C" int ghip_exec_num_inputs(GHipExecutable* e) { return e ? static_cast<int>(e->in_shapes.size()) : -1; }
+extern "C" int ghip_exec_num_outputs(GHipExecutable* e) { return e ? static_cast<int>(e->out_shapes.size()) : -1; }
+
+static int shape_out(const Shape& s, int* dtype, int64_t* dims, int max_rank) {
+  if (dtype) *dtype = s.dtype;
+  for (int i = 0; i < s.rank() && i < max_rank; ++i) dims[i] = s.dims[i];
+  return s.rank();
+}
+extern "C" int ghip_exec_input_shape(GHipExecutable* e, int i, int* dtype, int64_t* dims, int max_rank) {
+  if (!e || i < 0 || i >= static_cast<int>(e->in_shapes.size())) return -1;
+  return shape_out(e->in_shapes[i], dtype, dims, max_rank);
+}
+extern "C" int ghip_exec_output_shape(GHipExecutable* e, int i, int* dtype, int64_t* dims, int max_rank) {
+  if (!e || i < 0 || i >= static_cast<int>(e->out_shapes.size())) return -1;
+  return shape_out(e->out_shapes[i], dtype, dims, max_rank);
+}
+
+extern "C" size_t ghip_exec_plan(GHipExecutable* e, char* buf, size_t buflen) {
+  if (!e) return 0;
+  std::string s;
+  char head[160];
+  snprintf(head, sizeof head, "# %zu steps, arena %zu bytes\n", e->plan.steps.size(), e->plan.arena_bytes);
+  s += head;
+  for (auto& l : e->plan.log) s += l + "\n";
+  if (buf && buflen) {
+    const size_t n = std::min(buflen - 1, s.size());
+    memcpy(buf, s.data(), n);
+    buf[n] = '\0';
+  }
+  return s.size();
+}
+
+extern "C" int ghip_exec_execute(GHipExecutable* e, GHipBuffer* const* inputs, int n, const uint8_t* donate,
+                                 GHipBuffer** outputs, int nout, GHipError* err) {
+  (void)donate;  // inputs are never written; donation is accepted and ignored
+  if (!e || e->finalized) return set_error(err, GHIP_ERR_STATE, "Execute: executable finalized");
+  std::lock_guard<std::mutex> lk(e->mu);
+  GHipBackend* be = e->backend;
+  if (!be || be->finalized) return set_error(err, GHIP_ERR_STATE, "Execute: backend finalized");
+  if (be->plan_only) return set_error(err, GHIP_ERR_STATE, "Execute: plan-only backend has no device");
+  if (n != static_cast<int>(e->in_shapes.size()))
+    return set_error(err, GHIP_ERR_INVALID_ARG, "Execute: expected %zu inputs, got %d", e->in_shapes.size(), n);
+  if (nout != static_cast<int>(e->out_shapes.size()))
+    return set_error(err, GHIP_ERR_INVALID_ARG, "Execute: expected %zu outputs, got %d", e->out_shapes.size(), nout);
+  for (int i = 0; i < n; ++i) {
+    if (!inputs[i] || !inputs[i]->valid)
+      return set_error(err, GHIP_ERR_INVALID_ARG, "Execute: input #%d is not a valid buffer", i);
+    if (inputs[i]->shape != e->in_shapes[i])
+      return set_error(err, GHIP_ERR_INVALID_ARG, "Execute: input #%d shape mismatch: expected %s, got %s", i,
+                       e->in_shapes[i].str().c_str(), inputs[i]->shape.str().c_str());
+  }
+  hipSetDevice(be->device);
+  const Plan& plan = e->plan;
+  if (plan.arena_bytes > e->arena_cap) {
+    if (e->arena) {
+      hipStreamSynchronize(be->stream);
+      be->release(e->arena, e->arena_cap);
+      e->arena = nullptr;
+      e->arena_cap = 0;
+    }
+    if (be->alloc(plan.arena_bytes, &e->arena, err) != GHIP_OK) return err ? err->code : GHIP_ERR_OOM;
+    e->arena_cap = plan.arena_bytes;
+  }
+  std::vector<GHipBuffer*> outs(nout, nullptr);
+  auto cleanup = [&]() {
+    for (auto* b : outs)
+      if (b) ghip_buffer_finalize(b);
+  };
+  for (int i = 0; i < nout; ++i) {
+    outs[i] = ghip_buffer_new(be, e->out_shapes[i].dtype, e->out_shapes[i].dims.data(), e->out_shapes[i].rank(), err);
+    if (!outs[i]) {
+      cleanup();
+      return err ? err->code : GHIP_ERR_OOM;
+    }
+  }
+  ExecState st;
+  st.stream = be->stream;
+  st.slot_ptr.resize(plan.slots.size(), nullptr);
+  for (size_t s = 0; s < plan.slots.size(); ++s) {
+    const Slot& sl = plan.slots[s];
+    switch (sl.kind) {
+      case SlotKind::Input: st.slot_ptr[s] = static_cast<char*>(inputs[sl.index]->ptr); break;
+      case SlotKind::Const: st.slot_ptr[s] = static_cast<char*>(sl.const_ptr); break;
+      case SlotKind::Arena: st.slot_ptr[s] = static_cast<char*>(e->arena) + sl.arena_off; break;
+      case SlotKind::Output: st.slot_ptr[s] = static_cast<char*>(outs[sl.index]->ptr); break;
+    }
+  }
+  for (const Step& step : plan.steps) {
+    const int rc = step.run(st, err);
+    if (rc != GHIP_OK) {
+      if (err && err->message) {
+        std::string m = std::string("Execute: ") + step.desc + ": " + err->message;
+        set_error(err, rc, "%s", m.c_str());
+      }
+      hipStreamSynchronize(be->stream);
+      cleanup();
+      return rc;
+    }
+  }
+  for (int i = 0; i < nout; ++i) outputs[i] = outs[i];
+  return GHIP_OK;
+}
+
+extern "C" void ghip_exec_finalize(GHipExecutable* e) {
+  if (!e) return;
+  GHipBackend* be = e->backend;
+  if (be && !be->finalized && !be->plan_only) {
+    hipSetDevice(be->device);
+    hipStreamSynchronize(be->stream);
+    for (auto& pc : e->owned_consts) be->release(pc.first, pc.second);
+    if (e->arena) be->release(e->arena, e->arena_cap);
+  }
+  e->finalized = true;
+  delete e;
+}

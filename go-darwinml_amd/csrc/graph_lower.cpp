@@ -1,0 +1,1330 @@
+// Compile-time lowering: graph -> launch plan.
+//
+// What the reference leaves to MPSGraph's closed compiler (bridge.m:1112-1240) is
+// done here, explicitly:
+//   * Views, not copies: Reshape of contiguous data, Transpose, BroadcastInDim and
+//     Slice only rewrite (offset, strides).  Consumers that take strided operands
+//     (generated elementwise kernels, the GEMM, reductions) read through them;
+//     others get one strided-copy materialisation.
+//   * Pattern fusion into the hand-written row kernels: FusedSoftmax, the
+//     primitive softmax and log-softmax chains, the RMSNorm chain
+//     (x * rsqrt(mean(x^2) + eps) * gamma), FusedLayerNorm, and
+//     FusedScaledDotProductAttention = GEMM -> scale+mask+softmax -> GEMM.
+//   * DotGeneral -> batched MFMA GEMM with batch / free / contracting axis groups
+//     folded into single strides whenever the operand layout allows (no
+//     transposes, unlike dotgeneral.go:97-148), output [batch, lhs free, rhs free].
+//   * Elementwise clusters (Unary / Binary / Compare / Where / Clamp / Convert,
+//     plus Iota leaves and scalar constants inlined as literals) become one
+//     generated kernel each (rtc.cpp), so adjacent elementwise chains make one
+//     HBM round trip.
+//   * Intermediates live in one arena per executable; offsets come from a
+//     first-fit interval allocation over step lifetimes.
+#include <math.h>
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <algorithm>
+#include <set>
+#include <sstream>
+
+#include "common.h"
+#include "graph.h"
+
+namespace ghip {
+namespace {
+
+struct Fusion {
+  enum Kind { None, RmsNorm, Softmax, LogSoftmax } kind = None;
+  int x = -1, gamma = -1;
+  double eps = 0;
+};
+
+std::string fmt(const char* f, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, f);
+  vsnprintf(buf, sizeof buf, f, ap);
+  va_end(ap);
+  return buf;
+}
+
+struct Lowerer {
+  GHipBackend* be;
+  GHipFunction* fn;
+  Plan* plan;
+  GHipError* err;
+  std::vector<Node>& N;
+  std::vector<char> live;
+  std::vector<std::vector<int>> users;
+  std::vector<int> cluster;  // elementwise cluster id (= root node) or -1
+  std::vector<Fusion> fusion;
+  std::vector<char> have;
+  std::vector<View> views;
+  std::vector<std::vector<int>> reads, writes;  // per step: slots
+  std::vector<std::vector<uint8_t>> const_data;  // per slot (Const slots)
+  bool failed = false;
+
+  Lowerer(GHipBackend* b, GHipFunction* f, Plan* p, GHipError* e)
+      : be(b), fn(f), plan(p), err(e), N(f->nodes) {}
+
+  View bad() {
+    failed = true;
+    return View{};
+  }
+  View fail(int code, const char* what) {
+    if (!failed) set_error(err, code, "Compile: %s", what);
+    return bad();
+  }
+
+  // ------------------------------------------------------------------ slots
+  int new_slot(SlotKind k, size_t bytes, int index = 0) {
+    Slot s;
+    s.kind = k;
+    s.bytes = bytes;
+    s.index = index;
+    plan->slots.push_back(s);
+    const_data.emplace_back();
+    return static_cast<int>(plan->slots.size()) - 1;
+  }
+  View contig(int slot, const Shape& s) {
+    View v;
+    v.slot = slot;
+    v.strides = contiguous_strides(s.dims);
+    return v;
+  }
+  View fresh(const Shape& s) { return contig(new_slot(SlotKind::Arena, s.bytes()), s); }
+
+  void add_step(const std::string& desc, std::vector<int> r, std::vector<int> w, StepFn f) {
+    plan->steps.push_back(Step{desc, std::move(f)});
+    reads.push_back(std::move(r));
+    writes.push_back(std::move(w));
+  }
+
+  // ------------------------------------------------------------------ analysis
+  void analyse() {
+    const int n = static_cast<int>(N.size());
+    live.assign(n, 0);
+    users.assign(n, {});
+    std::vector<int> stack(fn->outputs.begin(), fn->outputs.end());
+    while (!stack.empty()) {
+      int v = stack.back();
+      stack.pop_back();
+      if (v < 0 || live[v]) continue;
+      live[v] = 1;
+      for (int o : N[v].in)
+        if (o >= 0) stack.push_back(o);
+    }
+    for (int v = 0; v < n; ++v)
+      if (live[v])
+        for (int o : N[v].in)
+          if (o >= 0) users[o].push_back(v);
+    fusion.assign(n, Fusion{});
+    for (int v = n - 1; v >= 0; --v)
+      if (live[v]) match_patterns(v);
+    build_clusters();
+  }
+
+  // ------------------------------------------------------------------ patterns
+  int strip_reshape(int v) {
+    while (v >= 0 && N[v].kind == Kind::Reshape) v = N[v].in[0];
+    return v;
+  }
+  // Scalar constant behind Reshape/Broadcast chains: returns true and its value.
+  bool scalar_const(int v, double* val) {
+    while (v >= 0 && (N[v].kind == Kind::Reshape || N[v].kind == Kind::Broadcast)) v = N[v].in[0];
+    if (v < 0 || N[v].kind != Kind::Const || N[v].shape.size() != 1) return false;
+    *val = const_as_double(N[v], 0);
+    return true;
+  }
+  static double const_as_double(const Node& c, int64_t i) {
+    const uint8_t* p = c.data.data() + i * dtype_size(c.shape.dtype);
+    switch (c.shape.dtype) {
+      case GHIP_DTYPE_FLOAT32: { float f; memcpy(&f, p, 4); return f; }
+      case GHIP_DTYPE_FLOAT64: { double d; memcpy(&d, p, 8); return d; }
+      case GHIP_DTYPE_BFLOAT16: { uint16_t b; memcpy(&b, p, 2); return bf16_to_f32(b); }
+      case GHIP_DTYPE_FLOAT16: { _Float16 h; memcpy(&h, p, 2); return static_cast<double>(h); }
+      case GHIP_DTYPE_INT8: { int8_t x; memcpy(&x, p, 1); return x; }
+      case GHIP_DTYPE_INT16: { int16_t x; memcpy(&x, p, 2); return x; }
+      case GHIP_DTYPE_INT32: { int32_t x; memcpy(&x, p, 4); return x; }
+      case GHIP_DTYPE_INT64: { int64_t x; memcpy(&x, p, 8); return static_cast<double>(x); }
+      case GHIP_DTYPE_UINT8: case GHIP_DTYPE_BOOL: { uint8_t x; memcpy(&x, p, 1); return x; }
+      case GHIP_DTYPE_UINT16: { uint16_t x; memcpy(&x, p, 2); return x; }
+      case GHIP_DTYPE_UINT32: { uint32_t x; memcpy(&x, p, 4); return x; }
+      case GHIP_DTYPE_UINT64: { uint64_t x; memcpy(&x, p, 8); return static_cast<double>(x); }
+      default: return NAN;
+    }
+  }
+  // v (shape == xs) broadcasts a per-row value along the last axis of xs; returns
+  // the per-row value (through reshapes) in *u.
+  bool row_broadcast(int v, const Shape& xs, int* u) {
+    const int r = xs.rank();
+    if (r == 0 || v < 0) return false;
+    const int64_t rows = xs.size() / std::max<int64_t>(xs.dims[r - 1], 1);
+    const Node& b = N[v];
+    int src = -1;
+    if (b.kind == Kind::Broadcast && b.shape.dims == xs.dims) {
+      const Node& s = N[b.in[0]];
+      const int sr = s.shape.rank();
+      bool ok = true;
+      for (int i = 0; i < sr; ++i) {
+        const int64_t ax = b.a0[i];
+        if (ax == r - 1) ok = ok && s.shape.dims[i] == 1;
+        else ok = ok && s.shape.dims[i] == xs.dims[ax];
+      }
+      // every non-last axis of xs must be covered (else it is broadcast too)
+      std::set<int64_t> cov(b.a0.begin(), b.a0.end());
+      for (int a = 0; a < r - 1; ++a) ok = ok && (cov.count(a) || xs.dims[a] == 1);
+      if (!ok) return false;
+      src = b.in[0];
+    } else if (b.shape.rank() == r && b.shape.dims[r - 1] == 1 && b.shape.size() == rows && xs.dims[r - 1] != 1) {
+      src = v;  // implicit numpy broadcast of a [..., 1] operand
+    } else {
+      return false;
+    }
+    if (N[src].shape.size() != rows) return false;
+    *u = strip_reshape(src);
+    return true;
+  }
+  // v is a [n]-vector broadcast along the leading axes of xs (gamma / beta).
+  bool col_broadcast(int v, const Shape& xs, int* g) {
+    const int r = xs.rank();
+    if (r == 0) return false;
+    const int64_t n = xs.dims[r - 1];
+    const Node& b = N[v];
+    if (b.kind == Kind::Broadcast && b.shape.dims == xs.dims) {
+      const Node& s = N[b.in[0]];
+      if (s.shape.size() != n) return false;
+      for (int i = 0; i < s.shape.rank(); ++i)
+        if (s.shape.dims[i] != 1 && b.a0[i] != r - 1) return false;
+      *g = b.in[0];
+      return true;
+    }
+    if (b.shape.size() == n && b.shape.rank() <= r && (b.shape.rank() == 0 ? false : b.shape.dims.back() == n)) {
+      *g = v;
+      return true;
+    }
+    return false;
+  }
+  bool is_binary(int v, int op) { return v >= 0 && N[v].kind == Kind::Binary && N[v].sub == op; }
+  bool is_unary(int v, int op) { return v >= 0 && N[v].kind == Kind::Unary && N[v].sub == op; }
+  bool is_last_axis_reduce(int v, int op, int x) {
+    if (v < 0 || N[v].kind != Kind::Reduce || N[v].sub != op || N[v].in[0] != x) return false;
+    const int r = N[x].shape.rank();
+    return N[v].a0.size() == 1 && N[v].a0[0] == r - 1;
+  }
+
+  // RMSNorm core: v = x * bcast(rsqrt(mean(x*x) + eps)).
+  bool rms_core(int v, int* xo, double* eps) {
+    if (!is_binary(v, GHIP_BINARY_MUL)) return false;
+    for (int o = 0; o < 2; ++o) {
+      const int x = N[v].in[o], rb = N[v].in[1 - o];
+      if (N[x].shape.dims != N[v].shape.dims || !dtype_is_float(N[x].shape.dtype)) continue;
+      int u;
+      if (!row_broadcast(rb, N[x].shape, &u) || !is_unary(u, GHIP_UNARY_RSQRT)) continue;
+      const int add = strip_reshape(N[u].in[0]);
+      if (!is_binary(add, GHIP_BINARY_ADD)) continue;
+      for (int p = 0; p < 2; ++p) {
+        double e;
+        if (!scalar_const(N[add].in[p], &e)) continue;
+        const int m = strip_reshape(N[add].in[1 - p]);
+        const double n = static_cast<double>(N[x].shape.dims.back());
+        int s = -1;
+        if (is_binary(m, GHIP_BINARY_MUL)) {
+          for (int q = 0; q < 2; ++q) {
+            double c;
+            if (scalar_const(N[m].in[q], &c) && fabs(c * n - 1.0) < 1e-5) s = strip_reshape(N[m].in[1 - q]);
+          }
+        } else if (is_binary(m, GHIP_BINARY_DIV)) {
+          double c;
+          if (scalar_const(N[m].in[1], &c) && fabs(c - n) < 1e-6 * n) s = strip_reshape(N[m].in[0]);
+        }
+        if (s < 0 || N[s].kind != Kind::Reduce || N[s].sub != GHIP_REDUCE_SUM) continue;
+        const int sq = N[s].in[0];
+        if (!is_last_axis_reduce(s, GHIP_REDUCE_SUM, sq)) continue;
+        bool square = is_binary(sq, GHIP_BINARY_MUL) && N[sq].in[0] == x && N[sq].in[1] == x;
+        double two;
+        square = square || (is_binary(sq, GHIP_BINARY_POW) && N[sq].in[0] == x && scalar_const(N[sq].in[1], &two) && two == 2.0);
+        if (!square) continue;
+        *xo = x;
+        *eps = e;
+        return true;
+      }
+    }
+    return false;
+  }
+
+  void match_patterns(int v) {
+    const Node& n = N[v];
+    if (n.kind != Kind::Binary) return;
+    // RMSNorm, with or without gamma.
+    if (n.sub == GHIP_BINARY_MUL && dtype_is_float(n.shape.dtype) && n.shape.rank() >= 1) {
+      int x, g;
+      double eps;
+      for (int o = 0; o < 2; ++o) {
+        if (col_broadcast(n.in[1 - o], n.shape, &g) && rms_core(n.in[o], &x, &eps)) {
+          fusion[v] = Fusion{Fusion::RmsNorm, x, g, eps};
+          return;
+        }
+      }
+      if (rms_core(v, &x, &eps)) {
+        fusion[v] = Fusion{Fusion::RmsNorm, x, -1, eps};
+        return;
+      }
+    }
+    // Softmax: exp(x - bmax) / bcast(sum(exp(x - bmax))).
+    if (n.sub == GHIP_BINARY_DIV && dtype_is_float(n.shape.dtype) && n.shape.rank() >= 1) {
+      const int e = n.in[0];
+      int s;
+      if (is_unary(e, GHIP_UNARY_EXP) && row_broadcast(n.in[1], n.shape, &s) &&
+          is_last_axis_reduce(s, GHIP_REDUCE_SUM, e)) {
+        int x;
+        if (shifted_by_max(N[e].in[0], &x)) {
+          fusion[v] = Fusion{Fusion::Softmax, x};
+          return;
+        }
+      }
+    }
+    // Log-softmax: (x - bmax) - bcast(log(sum(exp(x - bmax)))).
+    if (n.sub == GHIP_BINARY_SUB && dtype_is_float(n.shape.dtype) && n.shape.rank() >= 1) {
+      const int d = n.in[0];
+      int x, l;
+      if (shifted_by_max(d, &x) && row_broadcast(n.in[1], n.shape, &l) && is_unary(l, GHIP_UNARY_LOG)) {
+        const int s = strip_reshape(N[l].in[0]);
+        if (s >= 0 && N[s].kind == Kind::Reduce && is_unary(N[s].in[0], GHIP_UNARY_EXP) &&
+            N[N[s].in[0]].in[0] == d && is_last_axis_reduce(s, GHIP_REDUCE_SUM, N[s].in[0])) {
+          fusion[v] = Fusion{Fusion::LogSoftmax, x};
+          return;
+        }
+      }
+    }
+  }
+  // d = x - bcast(max(x, last axis)).
+  bool shifted_by_max(int d, int* xo) {
+    if (!is_binary(d, GHIP_BINARY_SUB)) return false;
+    const int x = N[d].in[0];
+    int m;
+    if (N[x].shape.dims != N[d].shape.dims) return false;
+    if (!row_broadcast(N[d].in[1], N[x].shape, &m)) return false;
+    if (!is_last_axis_reduce(m, GHIP_REDUCE_MAX, x)) return false;
+    *xo = x;
+    return true;
+  }
+
+  // ------------------------------------------------------------------ clusters
+  bool clusterable(int v) {
+    if (!live[v] || fusion[v].kind != Fusion::None) return false;
+    const Kind k = N[v].kind;
+    return is_elementwise(k);
+  }
+  void build_clusters() {
+    const int n = static_cast<int>(N.size());
+    cluster.assign(n, -1);
+    std::set<int> outs(fn->outputs.begin(), fn->outputs.end());
+    for (int v = n - 1; v >= 0; --v) {
+      if (!clusterable(v) || cluster[v] >= 0) continue;
+      cluster[v] = v;  // new root
+      std::vector<int> work{v};
+      while (!work.empty()) {
+        const int u = work.back();
+        work.pop_back();
+        for (int o : N[u].in) {
+          if (o < 0 || cluster[o] >= 0 || !clusterable(o) || outs.count(o)) continue;
+          if (N[o].shape.dims != N[v].shape.dims) continue;
+          bool all_in = true;
+          for (int w : users[o]) all_in = all_in && cluster[w] == v;
+          if (!all_in) continue;
+          cluster[o] = v;
+          work.push_back(o);
+        }
+      }
+    }
+  }
+
+  // ------------------------------------------------------------------ views
+  View get(int v) {
+    if (failed) return View{};
+    if (have[v]) return views[v];
+    View r;
+    const Node& n = N[v];
+    if (fusion[v].kind != Fusion::None) {
+      r = emit_fusion(v);
+    } else {
+      switch (n.kind) {
+        case Kind::Param: r = contig(new_slot(SlotKind::Input, n.shape.bytes(), static_cast<int>(n.i0)), n.shape); break;
+        case Kind::Const: {
+          r = contig(new_slot(SlotKind::Const, n.shape.bytes()), n.shape);
+          const_data[r.slot] = n.data;
+          break;
+        }
+        case Kind::Reshape: {
+          View s = get(n.in[0]);
+          if (failed) return bad();
+          s = materialize(s, N[n.in[0]].shape);
+          r = s;
+          r.strides = contiguous_strides(n.shape.dims);
+          break;
+        }
+        case Kind::Transpose: {
+          View s = get(n.in[0]);
+          if (failed) return bad();
+          r = s;
+          for (size_t i = 0; i < n.a0.size(); ++i) r.strides[i] = s.strides[n.a0[i]];
+          break;
+        }
+        case Kind::Broadcast: {
+          View s = get(n.in[0]);
+          if (failed) return bad();
+          r.slot = s.slot;
+          r.offset = s.offset;
+          r.strides.assign(n.shape.rank(), 0);
+          const Shape& ss = N[n.in[0]].shape;
+          for (int i = 0; i < ss.rank(); ++i)
+            if (ss.dims[i] != 1) r.strides[n.a0[i]] = s.strides[i];
+          break;
+        }
+        case Kind::Slice: {
+          View s = get(n.in[0]);
+          if (failed) return bad();
+          r = s;
+          for (int i = 0; i < n.shape.rank(); ++i) {
+            r.offset += n.a0[i] * s.strides[i];
+            r.strides[i] = s.strides[i] * n.a2[i];
+          }
+          break;
+        }
+        case Kind::Reverse: {  // negative-stride view
+          View s = get(n.in[0]);
+          if (failed) return bad();
+          r = s;
+          for (auto a : n.a0) {
+            r.offset += (n.shape.dims[a] - 1) * s.strides[a];
+            r.strides[a] = -s.strides[a];
+          }
+          break;
+        }
+        case Kind::Iota: r = emit_iota(v); break;
+        case Kind::Unary: case Kind::Binary: case Kind::Compare: case Kind::Where:
+        case Kind::Clamp: case Kind::Convert:
+          r = emit_cluster(cluster[v] == v ? v : -1, v);
+          break;
+        case Kind::Concat: r = emit_concat(v); break;
+        case Kind::Reduce: r = emit_reduce(v); break;
+        case Kind::ArgMinMax: r = emit_argminmax(v); break;
+        case Kind::Dot: r = emit_dot(v); break;
+        case Kind::Gather: r = emit_gather(v); break;
+        case Kind::Softmax: r = emit_softmax(v); break;
+        case Kind::LayerNorm: r = emit_layernorm(v); break;
+        case Kind::SDPA: r = emit_sdpa(v); break;
+      }
+    }
+    if (failed) return bad();
+    views[v] = r;
+    have[v] = 1;
+    return r;
+  }
+
+  CopyDesc copy_desc(const Shape& s, const View& src, const View& dst) {
+    CopyDesc d;
+    d.rank = s.rank();
+    for (int i = 0; i < d.rank; ++i) {
+      d.dims[i] = s.dims[i];
+      d.sst[i] = src.strides[i];
+      d.dst[i] = dst.strides[i];
+    }
+    return d;
+  }
+
+  void emit_copy(const Shape& s, const View& src, const View& dst, const char* why) {
+    const CopyDesc d = copy_desc(s, src, dst);
+    const int eb = dtype_size(s.dtype);
+    const int dt = s.dtype;
+    add_step(fmt("strided_copy %s %s", s.str().c_str(), why), {src.slot}, {dst.slot},
+             [=](ExecState& st, GHipError* e) {
+               return launch_strided_copy(eb, st.ptr(src, dt), st.ptr(dst, dt), d, st.stream, e);
+             });
+  }
+
+  View materialize(const View& src, const Shape& s, const char* why = "(materialise)") {
+    if (failed) return bad();
+    if (src.contiguous(s)) {
+      View r = src;
+      r.strides = contiguous_strides(s.dims);
+      return r;
+    }
+    View dst = fresh(s);
+    emit_copy(s, src, dst, why);
+    return dst;
+  }
+
+  // Permuted view helper: result dims[i] = dims[perm[i]].
+  static View permute(const View& v, const std::vector<int64_t>& perm) {
+    View r = v;
+    for (size_t i = 0; i < perm.size(); ++i) r.strides[i] = v.strides[perm[i]];
+    return r;
+  }
+  static Shape permute_shape(const Shape& s, const std::vector<int64_t>& perm) {
+    Shape r = s;
+    for (size_t i = 0; i < perm.size(); ++i) r.dims[i] = s.dims[perm[i]];
+    return r;
+  }
+  static std::vector<int64_t> inverse(const std::vector<int64_t>& p) {
+    std::vector<int64_t> q(p.size());
+    for (size_t i = 0; i < p.size(); ++i) q[p[i]] = static_cast<int64_t>(i);
+    return q;
+  }
+
+  // ------------------------------------------------------------------ row kernels
+  struct Vec {
+    bool present = false;
+    View view;
+    Shape shape;
+  };
+  Vec vec_of(int v) {
+    Vec r;
+    if (v < 0) return r;
+    r.present = true;
+    r.view = get(v);
+    r.shape = N[v].shape;
+    return r;
+  }
+  View emit_rows(int op, const Shape& xs, const View& xv, const Vec& gamma, const Vec& beta, double eps,
+                 const std::string& why) {
+    const int r = xs.rank();
+    const int64_t n = r ? xs.dims[r - 1] : 1;
+    const int64_t rows = n ? xs.size() / n : 0;
+    const int dt = xs.dtype;
+    if (dt != GHIP_DTYPE_FLOAT32 && dt != GHIP_DTYPE_BFLOAT16)
+      return fail(GHIP_ERR_UNSUPPORTED, "row kernels take float32 / bfloat16");
+    View x = materialize(xv, xs);
+    View g, b;
+    std::vector<int> rd{x.slot};
+    if (gamma.present) {
+      g = materialize(gamma.view, gamma.shape);
+      rd.push_back(g.slot);
+    }
+    if (beta.present) {
+      b = materialize(beta.view, beta.shape);
+      rd.push_back(b.slot);
+    }
+    if (failed) return bad();
+    View y = fresh(xs);
+    const bool hg = gamma.present, hb = beta.present;
+    const float fe = static_cast<float>(eps);
+    static const char* names[] = {"softmax_rows", "log_softmax_rows", "rmsnorm_rows", "layernorm_rows"};
+    add_step(fmt("%s %s rows=%lld n=%lld%s%s %s", names[op], dtype_name(dt), (long long)rows, (long long)n,
+                 hg ? " +gamma" : "", hb ? " +beta" : "", why.c_str()),
+             rd, {y.slot}, [=](ExecState& st, GHipError* e) {
+               const void* xp = st.ptr(x, dt);
+               void* yp = st.ptr(y, dt);
+               const void* gp = hg ? st.ptr(g, dt) : nullptr;
+               const void* bp = hb ? st.ptr(b, dt) : nullptr;
+               switch (op) {
+                 case 0: return ghip_softmax_rows(dt, xp, yp, rows, n, 0, st.stream, e);
+                 case 1: return ghip_softmax_rows(dt, xp, yp, rows, n, 1, st.stream, e);
+                 case 2: return ghip_rmsnorm_rows(dt, xp, gp, yp, rows, n, fe, st.stream, e);
+                 default: return ghip_layernorm_rows(dt, xp, gp, bp, yp, rows, n, fe, st.stream, e);
+               }
+             });
+    return y;
+  }
+
+  View emit_fusion(int v) {
+    const Fusion& f = fusion[v];
+    const Shape& xs = N[f.x].shape;
+    View xv = get(f.x);
+    if (failed) return bad();
+    switch (f.kind) {
+      case Fusion::RmsNorm: {
+        // gamma must be contiguous [n] data.
+        return emit_rows(2, xs, xv, vec_of(f.gamma), Vec{}, f.eps, "(fused primitive RMSNorm chain)");
+      }
+      case Fusion::Softmax: return emit_rows(0, xs, xv, Vec{}, Vec{}, 0, "(fused primitive softmax chain)");
+      case Fusion::LogSoftmax: return emit_rows(1, xs, xv, Vec{}, Vec{}, 0, "(fused primitive log-softmax chain)");
+      default: return fail(GHIP_ERR_STATE, "unknown fusion");
+    }
+  }
+
+  View emit_softmax(int v) {
+    const Node& n = N[v];
+    const Shape& xs = N[n.in[0]].shape;
+    View xv = get(n.in[0]);
+    if (failed) return bad();
+    const int r = xs.rank(), axis = static_cast<int>(n.i0);
+    if (axis == r - 1) return emit_rows(0, xs, xv, Vec{}, Vec{}, 0, "(FusedSoftmax)");
+    std::vector<int64_t> perm;
+    for (int i = 0; i < r; ++i)
+      if (i != axis) perm.push_back(i);
+    perm.push_back(axis);
+    View y = emit_rows(0, permute_shape(xs, perm), permute(xv, perm), Vec{}, Vec{}, 0, "(FusedSoftmax, axis moved last)");
+    if (failed) return bad();
+    return permute(y, inverse(perm));
+  }
+
+  View emit_layernorm(int v) {
+    const Node n = N[v];
+    const Shape xs = N[n.in[0]].shape;
+    View xv = get(n.in[0]);
+    if (failed) return bad();
+    const int r = xs.rank();
+    const int k = static_cast<int>(n.a0.size());
+    bool trailing = true;
+    for (int i = 0; i < k; ++i) trailing = trailing && n.a0[i] == r - k + i;
+    std::vector<int64_t> perm;
+    for (int i = 0; i < r; ++i)
+      if (std::find(n.a0.begin(), n.a0.end(), i) == n.a0.end()) perm.push_back(i);
+    for (auto a : n.a0) perm.push_back(a);
+    // Collapse to [rows, prod(normalized)] and run the row kernel.
+    Shape ps = permute_shape(xs, perm);
+    View pv = trailing ? xv : permute(xv, perm);
+    View x2 = materialize(pv, ps);
+    if (failed) return bad();
+    Shape flat = ps;
+    int64_t nn = 1;
+    for (int i = r - k; i < r; ++i) nn *= ps.dims[i];
+    flat.dims.assign(ps.dims.begin(), ps.dims.begin() + (r - k));
+    flat.dims.push_back(nn);
+    View fv = contig(x2.slot, flat);
+    fv.offset = x2.offset;
+    // gamma / beta of x's rank with non-normalized axes of size 1 follow x's
+    // permutation; lower-rank ones are already in normalized-axes order.
+    Vec gb[2] = {vec_of(n.in[1]), vec_of(n.in[2])};
+    for (int w = 0; w < 2; ++w) {
+      if (!gb[w].present || trailing || gb[w].shape.rank() != r) continue;
+      gb[w].view = materialize(permute(gb[w].view, perm), permute_shape(gb[w].shape, perm));
+      gb[w].shape = permute_shape(gb[w].shape, perm);
+    }
+    if (failed) return bad();
+    View y = emit_rows(3, flat, fv, gb[0], gb[1], n.f0, "(FusedLayerNorm)");
+    if (failed) return bad();
+    View yv = contig(y.slot, ps);
+    return trailing ? yv : permute(yv, inverse(perm));
+  }
+
+  // ------------------------------------------------------------------ iota / concat / reduce / arg
+  View emit_iota(int v) {
+    const Node& n = N[v];
+    const int dt = n.shape.dtype;
+    if (dt != GHIP_DTYPE_INT32 && dt != GHIP_DTYPE_INT64 && dt != GHIP_DTYPE_FLOAT32 && dt != GHIP_DTYPE_BFLOAT16)
+      return emit_cluster(-1, v);  // generated kernel handles the other dtypes
+    View y = fresh(n.shape);
+    int64_t outer = 1, inner = 1;
+    const int ax = static_cast<int>(n.i0);
+    for (int i = 0; i < ax; ++i) outer *= n.shape.dims[i];
+    for (int i = ax + 1; i < n.shape.rank(); ++i) inner *= n.shape.dims[i];
+    const int64_t len = n.shape.dims[ax];
+    add_step(fmt("iota %s axis=%d", n.shape.str().c_str(), ax), {}, {y.slot},
+             [=](ExecState& st, GHipError* e) { return ghip_iota(dt, st.ptr(y, dt), outer, len, inner, st.stream, e); });
+    return y;
+  }
+
+  View emit_concat(int v) {
+    const Node& n = N[v];
+    View y = fresh(n.shape);
+    int64_t off = 0;
+    const int ax = static_cast<int>(n.i0);
+    for (int o : n.in) {
+      View s = get(o);
+      if (failed) return bad();
+      View d = y;
+      d.offset = off * y.strides[ax];
+      emit_copy(N[o].shape, s, d, "(Concatenate)");
+      off += N[o].shape.dims[ax];
+    }
+    return y;
+  }
+
+  View emit_reduce(int v) {
+    const Node& n = N[v];
+    const Shape& xs = N[n.in[0]].shape;
+    View x = get(n.in[0]);
+    if (failed) return bad();
+    ReduceDesc d;
+    for (int i = 0; i < xs.rank(); ++i) {
+      if (std::find(n.a0.begin(), n.a0.end(), i) != n.a0.end()) {
+        d.rdims[d.rrank] = xs.dims[i];
+        d.rst[d.rrank++] = x.strides[i];
+      } else {
+        d.odims[d.orank] = xs.dims[i];
+        d.ost[d.orank++] = x.strides[i];
+      }
+    }
+    if (d.orank == 0) {  // scalar output
+      d.odims[0] = 1;
+      d.ost[0] = 0;
+      d.orank = 1;
+    }
+    if (d.rrank == 0) {
+      d.rdims[0] = 1;
+      d.rst[0] = 0;
+      d.rrank = 1;
+    }
+    View y = fresh(n.shape);
+    const int dt = xs.dtype, op = n.sub;
+    static const char* names[] = {"sum", "product", "max", "min"};
+    add_step(fmt("reduce_%s %s -> %s", names[op], xs.str().c_str(), n.shape.str().c_str()), {x.slot}, {y.slot},
+             [=](ExecState& st, GHipError* e) { return launch_reduce(dt, op, st.ptr(x, dt), d, st.ptr(y, dt), st.stream, e); });
+    return y;
+  }
+
+  View emit_argminmax(int v) {
+    const Node& n = N[v];
+    const Shape& xs = N[n.in[0]].shape;
+    if (xs.dtype != GHIP_DTYPE_FLOAT32 && xs.dtype != GHIP_DTYPE_BFLOAT16)
+      return fail(GHIP_ERR_UNSUPPORTED, "ArgMinMax lowers float32 / bfloat16 inputs");
+    View x = materialize(get(n.in[0]), xs);
+    if (failed) return bad();
+    const int ax = static_cast<int>(n.i0);
+    int64_t outer = 1, inner = 1;
+    for (int i = 0; i < ax; ++i) outer *= xs.dims[i];
+    for (int i = ax + 1; i < xs.rank(); ++i) inner *= xs.dims[i];
+    const int64_t len = xs.dims[ax];
+    View y = fresh(n.shape);
+    const int dt = xs.dtype, odt = n.shape.dtype, is_min = static_cast<int>(n.i1);
+    add_step(fmt("arg%s %s axis=%d", is_min ? "min" : "max", xs.str().c_str(), ax), {x.slot}, {y.slot},
+             [=](ExecState& st, GHipError* e) {
+               return ghip_argminmax(dt, st.ptr(x, dt), outer, len, inner, is_min, odt, st.ptr(y, odt), st.stream, e);
+             });
+    return y;
+  }
+
+  // ------------------------------------------------------------------ DotGeneral
+  // Merges `axes` (in flatten order) of a strided view into one (size, stride).
+  static bool merge(const Shape& s, const View& v, const std::vector<int64_t>& axes, int64_t* size, int64_t* stride) {
+    int64_t sz = 1, st = 0;
+    bool have_st = false;
+    // innermost-first
+    for (int i = static_cast<int>(axes.size()) - 1; i >= 0; --i) {
+      const int64_t a = axes[i], d = s.dims[a];
+      if (d == 1) continue;
+      if (!have_st) {
+        st = v.strides[a];
+        have_st = true;
+      } else if (v.strides[a] != st * sz) {
+        return false;
+      }
+      sz *= d;
+    }
+    if (!have_st) st = 0;
+    // size-1 dims were skipped: total size
+    int64_t total = 1;
+    for (auto a : axes) total *= s.dims[a];
+    *size = total;
+    *stride = st;
+    return true;
+  }
+
+  View emit_dot(int v) {
+    const Node& n = N[v];
+    const int L = n.in[0], R = n.in[1];
+    Shape ls = N[L].shape, rs = N[R].shape;
+    View lv = get(L), rv = get(R);
+    if (failed) return bad();
+    std::vector<int64_t> lfree, rfree;
+    for (int i = 0; i < ls.rank(); ++i)
+      if (std::find(n.a0.begin(), n.a0.end(), i) == n.a0.end() && std::find(n.a1.begin(), n.a1.end(), i) == n.a1.end())
+        lfree.push_back(i);
+    for (int i = 0; i < rs.rank(); ++i)
+      if (std::find(n.a2.begin(), n.a2.end(), i) == n.a2.end() && std::find(n.a3.begin(), n.a3.end(), i) == n.a3.end())
+        rfree.push_back(i);
+    int64_t B, sab, sbb, M, sam, K, sak, N_, sbn, K2, sbk, B2;
+    auto try_merge = [&]() {
+      return merge(ls, lv, n.a1, &B, &sab) && merge(ls, lv, lfree, &M, &sam) && merge(ls, lv, n.a0, &K, &sak) &&
+             merge(rs, rv, n.a3, &B2, &sbb) && merge(rs, rv, rfree, &N_, &sbn) && merge(rs, rv, n.a2, &K2, &sbk);
+    };
+    std::string how = "strides folded";
+    if (!try_merge()) {
+      // Materialise each operand in canonical [batch, free, contracting] order.
+      std::vector<int64_t> lp(n.a1.begin(), n.a1.end()), rp(n.a3.begin(), n.a3.end());
+      lp.insert(lp.end(), lfree.begin(), lfree.end());
+      lp.insert(lp.end(), n.a0.begin(), n.a0.end());
+      rp.insert(rp.end(), rfree.begin(), rfree.end());
+      rp.insert(rp.end(), n.a2.begin(), n.a2.end());
+      auto canon = [&](const Shape& s, const View& vw, const std::vector<int64_t>& p) {
+        View m = materialize(permute(vw, p), permute_shape(s, p), "(DotGeneral operand to [batch, free, contracting])");
+        // re-express as a view of the ORIGINAL axes
+        View back = m;
+        auto inv = inverse(p);
+        for (size_t i = 0; i < p.size(); ++i) back.strides[i] = m.strides[inv[i]];
+        return back;
+      };
+      lv = canon(ls, lv, lp);
+      rv = canon(rs, rv, rp);
+      if (failed) return bad();
+      how = "operands materialised";
+      if (!try_merge()) return fail(GHIP_ERR_STATE, "DotGeneral: stride merge failed after canonicalisation");
+    }
+    if (K != K2 || B != B2) return fail(GHIP_ERR_STATE, "DotGeneral: inconsistent sizes");
+    View y = fresh(n.shape);
+    const int dt = ls.dtype, odt = n.shape.dtype;
+    const int64_t scb = M * N_, scm = N_;
+    add_step(fmt("gemm_batched %s B=%lld M=%lld N=%lld K=%lld (%s; a strides b=%lld m=%lld k=%lld, b strides b=%lld k=%lld n=%lld)",
+                 dtype_name(dt), (long long)B, (long long)M, (long long)N_, (long long)K, how.c_str(), (long long)sab,
+                 (long long)sam, (long long)sak, (long long)sbb, (long long)sbk, (long long)sbn),
+             {lv.slot, rv.slot}, {y.slot}, [=](ExecState& st, GHipError* e) {
+               return ghip_gemm_batched(dt, odt, B, M, N_, K, st.ptr(lv, dt), sab, sam, sak, st.ptr(rv, dt), sbb, sbk, sbn,
+                                        st.ptr(y, odt), scb, scm, 1, st.stream, e);
+             });
+    return y;
+  }
+
+  // ------------------------------------------------------------------ Gather
+  View emit_gather(int v) {
+    const Node& n = N[v];
+    const Shape& os = N[n.in[0]].shape;
+    const Shape& is = N[n.in[1]].shape;
+    const int r = os.rank(), ir = is.rank();
+    const int ivax = static_cast<int>(n.i0);
+    // Embedding-lookup pattern (gather.go:61-98).
+    bool emb = n.a2.size() == 1 && n.a1.size() == 1 && n.a1[0] == n.a2[0] && n.a3[n.a2[0]] == 1 &&
+               (ivax == ir - 1 || ivax == ir);
+    const int g = emb ? static_cast<int>(n.a2[0]) : -1;
+    for (int i = 0; emb && i < r; ++i)
+      if (i != g && n.a3[i] != os.dims[i]) emb = false;
+    const int batch_rank = n.shape.rank() - static_cast<int>(n.a0.size());
+    for (size_t i = 0; emb && i < n.a0.size(); ++i)
+      if (n.a0[i] != batch_rank + static_cast<int64_t>(i)) emb = false;  // offset axes trailing
+    if (!emb) return fail(GHIP_ERR_UNSUPPORTED, "Gather: only the embedding-lookup form is lowered");
+    View tv = get(n.in[0]), iv = get(n.in[1]);
+    if (failed) return bad();
+    // Bring the gathered axis first, the rest in order: rows of the table.
+    std::vector<int64_t> perm{g};
+    for (int i = 0; i < r; ++i)
+      if (i != g) perm.push_back(i);
+    View tab = materialize(permute(tv, perm), permute_shape(os, perm), "(Gather table, gathered axis first)");
+    View ids = materialize(iv, is);
+    if (failed) return bad();
+    View y = fresh(n.shape);
+    const int64_t V = os.dims[g];
+    const int64_t row_bytes = V ? static_cast<int64_t>(os.bytes() / V) : 0;
+    const int64_t cnt = is.size() / (ivax < ir ? is.dims[ivax] : 1);
+    const int idt = is.dtype, tdt = os.dtype;
+    add_step(fmt("gather_rows table=%s ids=%s rows=%lld", os.str().c_str(), is.str().c_str(), (long long)cnt),
+             {tab.slot, ids.slot}, {y.slot}, [=](ExecState& st, GHipError* e) {
+               return launch_gather_rows(st.ptr(tab, tdt), V, row_bytes, st.ptr(ids, idt), idt, cnt, st.ptr(y, tdt), st.stream, e);
+             });
+    if (g != 0) {
+      // Output rows follow the permuted table: [batch..., other axes in order] — that
+      // is already the XLA output order for trailing offset axes.
+    }
+    return y;
+  }
+
+  // ------------------------------------------------------------------ SDPA
+  View emit_sdpa(int v) {
+    const Node& n = N[v];
+    const int qv_ = n.in[0], kv_ = n.in[1], vv_ = n.in[2], mv_ = n.in[3];
+    const int H = static_cast<int>(n.i0), Hkv = static_cast<int>(n.i1);
+    const bool bshd = n.i2 == GHIP_LAYOUT_BSHD;
+    const bool causal = n.i3 != 0;
+    const int dt = N[qv_].shape.dtype;
+    if (dt != GHIP_DTYPE_FLOAT32 && dt != GHIP_DTYPE_BFLOAT16) return fail(GHIP_ERR_UNSUPPORTED, "SDPA: float32 / bfloat16 only");
+    const std::vector<int64_t> to_bhsd{0, 2, 1, 3};
+    auto as_bhsd = [&](int id, Shape* s) {
+      View w = get(id);
+      *s = N[id].shape;
+      if (bshd) {
+        w = permute(w, to_bhsd);
+        *s = permute_shape(*s, to_bhsd);
+      }
+      return w;
+    };
+    Shape qs, ks, vs;
+    View q = as_bhsd(qv_, &qs), k = as_bhsd(kv_, &ks), vw = as_bhsd(vv_, &vs);
+    if (failed) return bad();
+    const int64_t B = qs.dims[0], Sq = qs.dims[2], D = qs.dims[3], Sk = ks.dims[2], Dv = vs.dims[3];
+    // GQA: repeat each KV head H/Hkv times (function.go:2731-2744) as a broadcast view.
+    auto repeat = [&](View w, Shape s) {
+      if (Hkv == H) return std::make_pair(w, s);
+      const int rep = H / Hkv;
+      Shape s5 = s;
+      s5.dims = {s.dims[0], s.dims[1], rep, s.dims[2], s.dims[3]};
+      View w5;
+      w5.slot = w.slot;
+      w5.offset = w.offset;
+      w5.strides = {w.strides[0], w.strides[1], 0, w.strides[2], w.strides[3]};
+      View m = materialize(w5, s5, "(SDPA repeat KV heads)");
+      Shape s4 = s;
+      s4.dims[1] = H;
+      View m4 = contig(m.slot, s4);
+      m4.offset = m.offset;
+      return std::make_pair(m4, s4);
+    };
+    auto kk = repeat(k, ks);
+    auto vvv = repeat(vw, vs);
+    k = kk.first; ks = kk.second;
+    vw = vvv.first; vs = vvv.second;
+    // Batch (b, h) must merge into one GEMM batch stride; else materialise BHSD.
+    auto bstride = [&](const View& w, const Shape& s) -> int64_t {
+      if (s.dims[1] == 1) return w.strides[0];
+      if (s.dims[0] == 1 || w.strides[0] == w.strides[1] * s.dims[1]) return w.strides[1];
+      return -1;
+    };
+    if (bstride(q, qs) < 0) q = materialize(q, qs, "(SDPA Q to BHSD)");
+    if (bstride(k, ks) < 0) k = materialize(k, ks, "(SDPA K to BHSD)");
+    if (bstride(vw, vs) < 0) vw = materialize(vw, vs, "(SDPA V to BHSD)");
+    // Mask: a boolean keep-mask that broadcasts over [B, H] (trailing [Sq, Sk]).
+    View mask;
+    bool has_mask = false;
+    if (mv_ >= 0) {
+      Shape ms = N[mv_].shape;
+      if (ms.dtype != GHIP_DTYPE_BOOL) return fail(GHIP_ERR_UNSUPPORTED, "SDPA: additive masks are not lowered yet");
+      View mw = get(mv_);
+      if (bshd && ms.rank() == 4) {  // rank-4 masks follow Q's layout (function.go:2709-2718)
+        mw = permute(mw, to_bhsd);
+        ms = permute_shape(ms, to_bhsd);
+      }
+      bool lead1 = ms.rank() >= 2;
+      for (int i = 0; lead1 && i < ms.rank() - 2; ++i) lead1 = ms.dims[i] == 1;
+      if (!lead1 || ms.dims[ms.rank() - 2] != Sq || ms.dims[ms.rank() - 1] != Sk)
+        return fail(GHIP_ERR_UNSUPPORTED, "SDPA: boolean mask must be [.., Sq, Sk] with unit leading dims");
+      Shape m2 = ms;
+      m2.dims = {Sq, Sk};
+      View m2v = mw;
+      m2v.strides = {mw.strides[ms.rank() - 2], mw.strides[ms.rank() - 1]};
+      mask = materialize(m2v, m2, "(SDPA mask)");
+      has_mask = true;
+    }
+    if (failed) return bad();
+    const int64_t BH = B * H;
+    Shape ss;
+    ss.dtype = dt;
+    ss.dims = {B, H, Sq, Sk};
+    View scores = fresh(ss);
+    View probs = fresh(ss);
+    Shape os;
+    os.dtype = dt;
+    os.dims = {B, H, Sq, Dv};
+    View out = fresh(os);
+    const int64_t qbs = bstride(q, qs), qms = q.strides[2], qks = q.strides[3];
+    const int64_t kbs = bstride(k, ks), kns = k.strides[2], kks = k.strides[3];
+    const int64_t vbs = bstride(vw, vs), vks = vw.strides[2], vns = vw.strides[3];
+    const float scale = static_cast<float>(n.f0);
+    add_step(fmt("gemm_batched %s B=%lld M=%lld N=%lld K=%lld (SDPA scores = Q.K^T)", dtype_name(dt), (long long)BH,
+                 (long long)Sq, (long long)Sk, (long long)D),
+             {q.slot, k.slot}, {scores.slot}, [=](ExecState& st, GHipError* e) {
+               return ghip_gemm_batched(dt, dt, BH, Sq, Sk, D, st.ptr(q, dt), qbs, qms, qks, st.ptr(k, dt), kbs, kks, kns,
+                                        st.ptr(scores, dt), Sq * Sk, Sk, 1, st.stream, e);
+             });
+    std::vector<int> rd{scores.slot};
+    if (has_mask) rd.push_back(mask.slot);
+    add_step(fmt("scale_mask_softmax_rows %s rows=%lld sk=%lld scale=%g causal=%d mask=%d", dtype_name(dt),
+                 (long long)(BH * Sq), (long long)Sk, n.f0, causal ? 1 : 0, has_mask ? 1 : 0),
+             rd, {probs.slot}, [=](ExecState& st, GHipError* e) {
+               const uint8_t* mp = has_mask ? reinterpret_cast<const uint8_t*>(st.ptr(mask, GHIP_DTYPE_BOOL)) : nullptr;
+               return ghip_scale_mask_softmax_rows(dt, st.ptr(scores, dt), st.ptr(probs, dt), BH * Sq, Sq, Sk, scale,
+                                                   causal ? 1 : 0, mp, st.stream, e);
+             });
+    add_step(fmt("gemm_batched %s B=%lld M=%lld N=%lld K=%lld (SDPA out = P.V)", dtype_name(dt), (long long)BH,
+                 (long long)Sq, (long long)Dv, (long long)Sk),
+             {probs.slot, vw.slot}, {out.slot}, [=](ExecState& st, GHipError* e) {
+               return ghip_gemm_batched(dt, dt, BH, Sq, Dv, Sk, st.ptr(probs, dt), Sq * Sk, Sk, 1, st.ptr(vw, dt), vbs, vks,
+                                        vns, st.ptr(out, dt), Sq * Dv, Dv, 1, st.stream, e);
+             });
+    return bshd ? permute(out, to_bhsd) : out;
+  }
+
+  // ------------------------------------------------------------------ elementwise codegen
+  View emit_cluster(int root, int v);
+  std::string ctype(int dt) {
+    switch (dt) {
+      case GHIP_DTYPE_BOOL: return "bool";
+      case GHIP_DTYPE_INT8: return "signed char";
+      case GHIP_DTYPE_INT16: return "short";
+      case GHIP_DTYPE_INT32: return "int";
+      case GHIP_DTYPE_INT64: return "long long";
+      case GHIP_DTYPE_UINT8: return "unsigned char";
+      case GHIP_DTYPE_UINT16: return "unsigned short";
+      case GHIP_DTYPE_UINT32: return "unsigned int";
+      case GHIP_DTYPE_UINT64: return "unsigned long long";
+      case GHIP_DTYPE_FLOAT64: return "double";
+      default: return "float";  // f16 / bf16 / f32 compute in fp32
+    }
+  }
+  std::string stype(int dt) {
+    switch (dt) {
+      case GHIP_DTYPE_BOOL: return "unsigned char";
+      case GHIP_DTYPE_BFLOAT16: return "unsigned short";
+      case GHIP_DTYPE_FLOAT16: return "_Float16";
+      default: return ctype(dt);
+    }
+  }
+  std::string load_expr(int dt, const std::string& e) {
+    if (dt == GHIP_DTYPE_BFLOAT16) return "bf2f(" + e + ")";
+    if (dt == GHIP_DTYPE_FLOAT16) return "(float)(" + e + ")";
+    if (dt == GHIP_DTYPE_BOOL) return "(" + e + " != 0)";
+    return e;
+  }
+  std::string store_expr(int dt, const std::string& e) {
+    if (dt == GHIP_DTYPE_BFLOAT16) return "f2bf(" + e + ")";
+    if (dt == GHIP_DTYPE_FLOAT16) return "(_Float16)(" + e + ")";
+    if (dt == GHIP_DTYPE_BOOL) return "(unsigned char)(" + e + ")";
+    return e;
+  }
+  std::string round_expr(int dt, const std::string& e) {
+    if (dt == GHIP_DTYPE_BFLOAT16) return "rbf(" + e + ")";
+    if (dt == GHIP_DTYPE_FLOAT16) return "rhf(" + e + ")";
+    return e;
+  }
+  std::string literal(int dt, double val) {
+    char b[64];
+    if (dt == GHIP_DTYPE_FLOAT64) snprintf(b, sizeof b, "%a", val);
+    else if (dtype_is_float(dt)) {
+      if (isnan(val)) return "__builtin_nanf(\"\")";
+      if (isinf(val)) return val > 0 ? "__builtin_inff()" : "(-__builtin_inff())";
+      snprintf(b, sizeof b, "%af", static_cast<float>(val));
+    } else if (dt == GHIP_DTYPE_BOOL) snprintf(b, sizeof b, "%s", val != 0 ? "true" : "false");
+    else snprintf(b, sizeof b, "((%s)%lldLL)", ctype(dt).c_str(), static_cast<long long>(val));
+    return b;
+  }
+  std::string int_limits(int dt, bool hi) {
+    switch (dt) {
+      case GHIP_DTYPE_INT8: return hi ? "127" : "-128";
+      case GHIP_DTYPE_INT16: return hi ? "32767" : "-32768";
+      case GHIP_DTYPE_INT32: return hi ? "2147483647" : "(-2147483647-1)";
+      case GHIP_DTYPE_INT64: return hi ? "9223372036854775807LL" : "(-9223372036854775807LL-1)";
+      case GHIP_DTYPE_UINT8: return hi ? "255" : "0";
+      case GHIP_DTYPE_UINT16: return hi ? "65535" : "0";
+      case GHIP_DTYPE_UINT32: return hi ? "4294967295u" : "0";
+      default: return hi ? "18446744073709551615ull" : "0";
+    }
+  }
+  std::string op_expr(const Node& n, const std::vector<std::string>& a, const std::vector<int>& adt);
+
+  // ------------------------------------------------------------------ outputs / memory
+  int finish();
+};
+
+// Expression for one elementwise node given operand expressions (compute types).
+std::string Lowerer::op_expr(const Node& n, const std::vector<std::string>& a, const std::vector<int>& adt) {
+  const int dt = n.shape.dtype;
+  const int it = adt.empty() ? dt : adt[0];
+  const bool fl = dtype_is_float(it);
+  const bool f64 = it == GHIP_DTYPE_FLOAT64;
+  const std::string T = ctype(dt);
+  auto fn1 = [&](const char* f32, const char* f64n) { return std::string(f64 ? f64n : f32) + "(" + a[0] + ")"; };
+  switch (n.kind) {
+    case Kind::Unary:
+      switch (n.sub) {
+        case GHIP_UNARY_ABS: return fl ? fn1("fabsf", "fabs") : (dtype_is_unsigned(it) ? a[0] : "(" + T + ")(" + a[0] + " < 0 ? -" + a[0] + " : " + a[0] + ")");
+        case GHIP_UNARY_NEG: return "(" + T + ")(-" + a[0] + ")";
+        case GHIP_UNARY_SQRT: return fn1("sqrtf", "sqrt");
+        case GHIP_UNARY_RSQRT: return f64 ? "(1.0 / sqrt(" + a[0] + "))" : "rsqrtf(" + a[0] + ")";
+        case GHIP_UNARY_EXP: return fn1("expf", "exp");
+        case GHIP_UNARY_EXPM1: return fn1("expm1f", "expm1");
+        case GHIP_UNARY_LOG: return fn1("logf", "log");
+        case GHIP_UNARY_LOG1P: return fn1("log1pf", "log1p");
+        case GHIP_UNARY_SIN: return fn1("sinf", "sin");
+        case GHIP_UNARY_COS: return fn1("cosf", "cos");
+        case GHIP_UNARY_TANH: return fn1("tanhf", "tanh");
+        case GHIP_UNARY_LOGISTIC: return f64 ? "(1.0 / (1.0 + exp(-" + a[0] + ")))" : "(1.0f / (1.0f + expf(-" + a[0] + ")))";
+        case GHIP_UNARY_ERF: return fn1("erff", "erf");
+        case GHIP_UNARY_FLOOR: return fn1("floorf", "floor");
+        case GHIP_UNARY_CEIL: return fn1("ceilf", "ceil");
+        case GHIP_UNARY_ROUND: return fn1("rintf", "rint");  // round half to even
+        case GHIP_UNARY_SIGN:
+          if (fl) return "(" + a[0] + " > 0 ? (" + T + ")1 : (" + a[0] + " < 0 ? (" + T + ")-1 : " + a[0] + "))";
+          return "(" + T + ")(" + a[0] + " > 0 ? 1 : (" + a[0] + " < 0 ? -1 : 0))";
+        case GHIP_UNARY_LOGICAL_NOT: return "(!" + a[0] + ")";
+        case GHIP_UNARY_BITWISE_NOT: return "(" + T + ")(~" + a[0] + ")";
+        case GHIP_UNARY_IS_FINITE: return "(bool)isfinite(" + a[0] + ")";
+        case GHIP_UNARY_IS_NAN: return "(bool)isnan(" + a[0] + ")";
+        default: return a[0];
+      }
+    case Kind::Binary: {
+      const std::string& x = a[0];
+      const std::string& y = a[1];
+      const int bits = dtype_size(it) * 8;
+      switch (n.sub) {
+        case GHIP_BINARY_ADD: return "(" + T + ")(" + x + " + " + y + ")";
+        case GHIP_BINARY_SUB: return "(" + T + ")(" + x + " - " + y + ")";
+        case GHIP_BINARY_MUL: return "(" + T + ")(" + x + " * " + y + ")";
+        case GHIP_BINARY_DIV:
+          if (fl) return "(" + x + " / " + y + ")";
+          if (dtype_is_unsigned(it)) return "(" + T + ")(" + y + " == 0 ? (" + T + ")~(" + T + ")0 : " + x + " / " + y + ")";
+          return "(" + T + ")(" + y + " == 0 ? (" + T + ")-1 : ((" + y + " == -1 && " + x + " == " + int_limits(it, false) + ") ? " + x + " : " + x + " / " + y + "))";
+        case GHIP_BINARY_REM:
+          if (fl) return std::string(f64 ? "fmod(" : "fmodf(") + x + ", " + y + ")";
+          if (dtype_is_unsigned(it)) return "(" + T + ")(" + y + " == 0 ? " + x + " : " + x + " % " + y + ")";
+          return "(" + T + ")(" + y + " == 0 ? " + x + " : (" + y + " == -1 ? 0 : " + x + " % " + y + "))";
+        case GHIP_BINARY_POW:
+          if (fl) return std::string(f64 ? "pow(" : "powf(") + x + ", " + y + ")";
+          return "(" + T + ")ipow((long long)" + x + ", (long long)" + y + ")";
+        case GHIP_BINARY_MAX: return fl ? "fmax_nan(" + x + ", " + y + ")" : "(" + x + " > " + y + " ? " + x + " : " + y + ")";
+        case GHIP_BINARY_MIN: return fl ? "fmin_nan(" + x + ", " + y + ")" : "(" + x + " < " + y + " ? " + x + " : " + y + ")";
+        case GHIP_BINARY_ATAN2: return std::string(f64 ? "atan2(" : "atan2f(") + x + ", " + y + ")";
+        case GHIP_BINARY_LOGICAL_AND: return "(" + x + " && " + y + ")";
+        case GHIP_BINARY_LOGICAL_OR: return "(" + x + " || " + y + ")";
+        case GHIP_BINARY_LOGICAL_XOR: return "(" + x + " != " + y + ")";
+        case GHIP_BINARY_BITWISE_AND: return "(" + T + ")(" + x + " & " + y + ")";
+        case GHIP_BINARY_BITWISE_OR: return "(" + T + ")(" + x + " | " + y + ")";
+        case GHIP_BINARY_BITWISE_XOR: return "(" + T + ")(" + x + " ^ " + y + ")";
+        case GHIP_BINARY_SHIFT_LEFT:
+          return "(" + T + ")((" + y + " < 0 || " + y + " >= " + std::to_string(bits) + ") ? 0 : (" + T + ")(" + x + " << " + y + "))";
+        case GHIP_BINARY_SHIFT_RIGHT_ARITHMETIC:
+          if (dtype_is_unsigned(it)) return "(" + T + ")((" + y + " >= " + std::to_string(bits) + ") ? 0 : (" + x + " >> " + y + "))";
+          return "(" + T + ")((" + y + " < 0 || " + y + " >= " + std::to_string(bits) + ") ? (" + x + " < 0 ? -1 : 0) : (" + x + " >> " + y + "))";
+        default: {  // logical right shift: shift the unsigned bit pattern
+          static const char* ut[] = {"", "unsigned char", "unsigned short", "", "unsigned int", "", "", "", "unsigned long long"};
+          const std::string U = ut[dtype_size(it)];
+          return "(" + T + ")((" + y + " < 0 || " + y + " >= " + std::to_string(bits) + ") ? 0 : (" + U + ")((" + U + ")" + x + " >> " + y + "))";
+        }
+      }
+    }
+    case Kind::Compare: {
+      static const char* ops[] = {"==", "!=", ">", ">=", "<", "<="};
+      return "(" + a[0] + " " + ops[n.sub] + " " + a[1] + ")";
+    }
+    case Kind::Where: return "(" + a[0] + " ? " + a[1] + " : " + a[2] + ")";
+    case Kind::Clamp:
+      if (fl) return "fmin_nan(fmax_nan(" + a[1] + ", " + a[0] + "), " + a[2] + ")";
+      return "(" + a[1] + " < " + a[0] + " ? " + a[0] + " : (" + a[1] + " > " + a[2] + " ? " + a[2] + " : " + a[1] + "))";
+    case Kind::Convert: {
+      const int src = it;
+      if (dt == GHIP_DTYPE_BOOL) return "(" + a[0] + " != 0)";
+      if (dtype_is_float(dt)) return "(" + T + ")(" + a[0] + ")";
+      if (dtype_is_float(src))  // truncate toward zero, saturating; NaN -> 0
+        return "(" + T + ")((" + a[0] + " != " + a[0] + ") ? 0 : ((" + a[0] + ") <= (" + ctype(src) + ")" + int_limits(dt, false) +
+               " ? " + int_limits(dt, false) + " : ((" + a[0] + ") >= (" + ctype(src) + ")" + int_limits(dt, true) + " ? " +
+               int_limits(dt, true) + " : (" + T + ")(" + a[0] + "))))";
+      return "(" + T + ")(" + a[0] + ")";
+    }
+    default: return a.empty() ? "0" : a[0];
+  }
+}
+
+View Lowerer::emit_cluster(int root, int v) {
+  // Members: root's cluster (or, for a value requested outside its cluster, the
+  // value alone plus any Iota leaves) in node order.
+  std::vector<int> mem;
+  if (root >= 0) {
+    for (int u = 0; u <= root; ++u)
+      if (cluster[u] == root) mem.push_back(u);
+  } else {
+    mem.push_back(v);
+  }
+  const Shape& os = N[v].shape;
+  std::set<int> inset(mem.begin(), mem.end());
+  // Inputs: operands outside the cluster (scalar constants become literals;
+  // Iota operands of the cluster's shape are computed from the index).
+  struct In {
+    int value;
+    View view;
+    std::vector<int64_t> eff;  // effective strides over os.dims
+    bool linear;
+  };
+  std::vector<In> ins;
+  std::map<int, std::string> expr;  // value -> C expression
+  std::ostringstream body;
+  bool need_idx = false;
+  std::vector<std::string> idx_names;
+  for (int d = 0; d < os.rank(); ++d) idx_names.push_back("d" + std::to_string(d));
+  auto iota_expr = [&](int u) {
+    need_idx = true;
+    return "((" + ctype(N[u].shape.dtype) + ")" + idx_names[N[u].i0] + ")";
+  };
+  for (int u : mem) {
+    for (int o : N[u].in) {
+      if (o < 0 || inset.count(o) || expr.count(o)) continue;
+      double c;
+      if (scalar_const(o, &c) && (dtype_is_float(N[o].shape.dtype) || fabs(c) < 9007199254740992.0)) {
+        expr[o] = literal(N[o].shape.dtype, c);
+        continue;
+      }
+      if (N[o].kind == Kind::Iota && N[o].shape.dims == os.dims) {
+        expr[o] = iota_expr(o);
+        continue;
+      }
+      View w = get(o);
+      if (failed) return bad();
+      In in{o, w, {}, true};
+      // right-aligned implicit broadcast to os.dims
+      const Shape& s = N[o].shape;
+      const int off = os.rank() - s.rank();
+      in.eff.assign(os.rank(), 0);
+      for (int d = 0; d < s.rank(); ++d)
+        if (s.dims[d] != 1) in.eff[off + d] = w.strides[d];
+      auto cs = contiguous_strides(os.dims);
+      for (int d = 0; d < os.rank(); ++d)
+        if (os.dims[d] != 1 && in.eff[d] != cs[d]) in.linear = false;
+      if (!in.linear) need_idx = true;
+      const int k = static_cast<int>(ins.size());
+      std::string off_e = "i";
+      if (!in.linear) {
+        off_e = "0";
+        for (int d = 0; d < os.rank(); ++d)
+          if (in.eff[d] != 0 && os.dims[d] != 1) off_e += " + " + idx_names[d] + " * " + std::to_string(in.eff[d]) + "LL";
+      }
+      body << "    const " << ctype(s.dtype) << " in" << k << " = "
+           << load_expr(s.dtype, "((const " + stype(s.dtype) + "*)p_in" + std::to_string(k) + ")[" + off_e + "]") << ";\n";
+      expr[o] = "in" + std::to_string(k);
+      ins.push_back(in);
+    }
+    if (failed) return bad();
+    const Node& n = N[u];
+    std::vector<std::string> a;
+    std::vector<int> adt;
+    for (int o : n.in) {
+      a.push_back(expr[o]);
+      adt.push_back(N[o].shape.dtype);
+    }
+    std::string e;
+    if (n.kind == Kind::Iota) e = iota_expr(u);
+    else {
+      // Where / Clamp: the dtype driving op semantics is the value operands'.
+      std::vector<int> sem = adt;
+      if (n.kind == Kind::Where) sem = {adt[1]};
+      if (n.kind == Kind::Clamp) sem = {adt[1]};
+      e = op_expr(n, a, sem);
+    }
+    const std::string name = "v" + std::to_string(u);
+    body << "    const " << ctype(n.shape.dtype) << " " << name << " = " << round_expr(n.shape.dtype, e) << ";\n";
+    expr[u] = name;
+  }
+  std::ostringstream src;
+  src << R"(typedef unsigned short u16;
+__device__ __forceinline__ float bf2f(u16 b) { return __uint_as_float(((unsigned)b) << 16); }
+__device__ __forceinline__ u16 f2bf(float f) {
+  unsigned u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (u16)((u >> 16) | 0x40u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (u16)(u >> 16);
+}
+__device__ __forceinline__ float rbf(float f) { return bf2f(f2bf(f)); }
+__device__ __forceinline__ float rhf(float f) { return (float)(_Float16)f; }
+template <typename T> __device__ __forceinline__ T fmax_nan(T a, T b) { return (a > b || a != a) ? a : b; }
+template <typename T> __device__ __forceinline__ T fmin_nan(T a, T b) { return (a < b || a != a) ? a : b; }
+__device__ __forceinline__ long long ipow(long long b, long long e) {
+  if (e < 0) return b == 1 ? 1 : (b == -1 ? ((e & 1) ? -1 : 1) : 0);
+  long long r = 1;
+  while (e) { if (e & 1) r *= b; b *= b; e >>= 1; }
+  return r;
+}
+extern "C" __global__ void __launch_bounds__(256) fused(
+)";
+  for (size_t k = 0; k < ins.size(); ++k) src << "    const void* __restrict__ p_in" << k << ",\n";
+  src << "    void* __restrict__ p_out, long long n) {\n";
+  src << "  for (long long i = (long long)blockIdx.x * 256 + threadIdx.x; i < n; i += (long long)gridDim.x * 256) {\n";
+  if (need_idx) {
+    src << "    long long q = i;\n";
+    for (int d = os.rank() - 1; d >= 0; --d) {
+      src << "    const long long " << idx_names[d] << " = q % " << os.dims[d] << "LL;";
+      if (d > 0) src << " q /= " << os.dims[d] << "LL;";
+      src << "\n";
+    }
+  }
+  src << body.str();
+  src << "    ((" << stype(os.dtype) << "*)p_out)[i] = " << store_expr(os.dtype, expr[v]) << ";\n  }\n}\n";
+  const std::string code = src.str();
+  RtcKernel kern;
+  if (rtc_get(be, code, "fused", &kern, err) != GHIP_OK) return bad();
+  View y = fresh(os);
+  const int64_t total = os.size();
+  std::vector<int> rd;
+  std::vector<View> in_views;
+  std::vector<int> in_dt;
+  for (auto& in : ins) {
+    rd.push_back(in.view.slot);
+    in_views.push_back(in.view);
+    in_dt.push_back(N[in.value].shape.dtype);
+  }
+  std::ostringstream d;
+  d << "fused_elementwise " << os.str() << " ops=" << mem.size() << " inputs=" << ins.size() << " [";
+  for (size_t i = 0; i < mem.size(); ++i) {
+    const Node& n = N[mem[i]];
+    d << (i ? "," : "") << kind_name(n.kind);
+    if (n.kind == Kind::Unary || n.kind == Kind::Binary || n.kind == Kind::Compare) d << "#" << n.sub;
+  }
+  d << "]";
+  const int odt = os.dtype;
+  add_step(d.str(), rd, {y.slot}, [=](ExecState& st, GHipError* e) -> int {
+    if (total == 0) return GHIP_OK;
+    std::vector<void*> ptrs(in_views.size());
+    std::vector<void*> args;
+    for (size_t k = 0; k < in_views.size(); ++k) ptrs[k] = st.ptr(in_views[k], in_dt[k]);
+    void* outp = st.ptr(y, odt);
+    long long nn = total;
+    for (size_t k = 0; k < ptrs.size(); ++k) args.push_back(&ptrs[k]);
+    args.push_back(&outp);
+    args.push_back(&nn);
+    int64_t g = (total + 255) / 256;
+    if (g > 16384) g = 16384;
+    hipError_t h = hipModuleLaunchKernel(kern.func, static_cast<unsigned>(g), 1, 1, 256, 1, 1, 0, st.stream, args.data(), nullptr);
+    if (h != hipSuccess) return check_hip(h, e, "generated elementwise kernel launch");
+    return GHIP_OK;
+  });
+  return y;
+}
+
+int Lowerer::finish() {
+  // Outputs: reuse the producing arena slot when the value is a dense,
+  // exclusively-owned buffer; otherwise copy into a fresh output slot.
+  std::set<int> converted;
+  const int nout = static_cast<int>(fn->outputs.size());
+  plan->out_slot.assign(nout, -1);
+  for (int i = 0; i < nout; ++i) {
+    const int v = fn->outputs[i];
+    View w = get(v);
+    if (failed) return err ? err->code : GHIP_ERR_STATE;
+    const Shape& s = N[v].shape;
+    Slot& sl = plan->slots[w.slot];
+    if (sl.kind == SlotKind::Arena && w.offset == 0 && w.contiguous(s) && sl.bytes == s.bytes() && !converted.count(w.slot)) {
+      sl.kind = SlotKind::Output;
+      sl.index = i;
+      converted.insert(w.slot);
+      plan->out_slot[i] = w.slot;
+    } else {
+      View o = contig(new_slot(SlotKind::Output, s.bytes(), i), s);
+      emit_copy(s, w, o, "(copy to output)");
+      plan->out_slot[i] = o.slot;
+    }
+  }
+  // Arena: first-fit offsets over [first write, last use] step intervals.
+  const int ns = static_cast<int>(plan->slots.size());
+  std::vector<int> first(ns, INT32_MAX), last(ns, -1);
+  for (size_t st = 0; st < plan->steps.size(); ++st) {
+    for (int s : writes[st]) { first[s] = std::min(first[s], static_cast<int>(st)); last[s] = std::max(last[s], static_cast<int>(st)); }
+    for (int s : reads[st]) { first[s] = std::min(first[s], static_cast<int>(st)); last[s] = std::max(last[s], static_cast<int>(st)); }
+  }
+  std::vector<int> order;
+  for (int s = 0; s < ns; ++s)
+    if (plan->slots[s].kind == SlotKind::Arena && last[s] >= 0) order.push_back(s);
+  std::sort(order.begin(), order.end(), [&](int a, int b) { return plan->slots[a].bytes > plan->slots[b].bytes; });
+  struct Placed { size_t off, end; int first, last; };
+  std::vector<Placed> placed;
+  size_t arena = 0;
+  for (int s : order) {
+    const size_t sz = (plan->slots[s].bytes + 255) & ~size_t(255);
+    std::vector<std::pair<size_t, size_t>> busy;
+    for (auto& p : placed)
+      if (!(p.last < first[s] || last[s] < p.first)) busy.emplace_back(p.off, p.end);
+    std::sort(busy.begin(), busy.end());
+    size_t off = 0;
+    for (auto& b : busy) {
+      if (off + sz <= b.first) break;
+      off = std::max(off, b.second);
+    }
+    plan->slots[s].arena_off = off;
+    placed.push_back(Placed{off, off + sz, first[s], last[s]});
+    arena = std::max(arena, off + sz);
+  }
+  plan->arena_bytes = arena;
+  for (auto& st : plan->steps) plan->log.push_back(st.desc);
+  return GHIP_OK;
+}
+
+}  // namespace
+
+int lower(GHipBackend* be, GHipFunction* fn, Plan* plan, GHipError* err) {
+  Lowerer L(be, fn, plan, err);
+  L.have.assign(fn->nodes.size(), 0);
+  L.views.assign(fn->nodes.size(), View{});
+  L.analyse();
+  int rc = L.finish();
+  if (rc != GHIP_OK) return rc;
+  // Const payloads travel with the plan (uploaded by Compile).
+  plan->const_data = std::move(L.const_data);
+  return GHIP_OK;
+}
+
+}  // namespace ghip

@@ -1,0 +1,79 @@
+// Run-time compilation of generated kernels (fused elementwise clusters).
+//
+// Compile turns each elementwise cluster into HIP source (graph_lower.cpp) and
+// this file compiles it once per process with hipRTC for gfx950, caching the
+// loaded module by source text, so identical clusters across graphs share one
+// code object.  A plan-only backend compiles (which validates the generated
+// source) but never loads modules.
+#include <hip/hip_runtime.h>
+#include <hip/hiprtc.h>
+
+#include <map>
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "common.h"
+#include "graph.h"
+
+namespace ghip {
+
+namespace {
+struct Entry {
+  std::vector<char> code;
+  RtcKernel k;
+  bool loaded = false;
+};
+std::mutex g_mu;
+std::map<std::string, Entry> g_cache;
+
+// Options: gfx950, -O3, and packed-fp32 VALU ops disabled (they are not used
+// anywhere in this library).
+const char* kOpts[] = {"--offload-arch=gfx950", "-O3", "-std=c++17", "-Xclang", "-target-feature",
+                       "-Xclang", "-packed-fp32-ops"};
+}  // namespace
+
+int rtc_get(GHipBackend* be, const std::string& src, const std::string& entry, RtcKernel* out,
+            GHipError* err) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  Entry& e = g_cache[src];
+  if (e.code.empty()) {
+    hiprtcProgram prog;
+    if (hiprtcCreateProgram(&prog, src.c_str(), "fused.hip", 0, nullptr, nullptr) != HIPRTC_SUCCESS) {
+      g_cache.erase(src);
+      return set_error(err, GHIP_ERR_HIP, "hiprtcCreateProgram failed");
+    }
+    const hiprtcResult rc = hiprtcCompileProgram(prog, sizeof(kOpts) / sizeof(kOpts[0]), kOpts);
+    if (rc != HIPRTC_SUCCESS) {
+      size_t n = 0;
+      hiprtcGetProgramLogSize(prog, &n);
+      std::string log(n + 1, '\0');
+      hiprtcGetProgramLog(prog, &log[0]);
+      hiprtcDestroyProgram(&prog);
+      g_cache.erase(src);
+      return set_error(err, GHIP_ERR_HIP, "generated kernel failed to compile: %s\n--- source ---\n%s",
+                       log.c_str(), src.c_str());
+    }
+    size_t n = 0;
+    hiprtcGetCodeSize(prog, &n);
+    e.code.resize(n);
+    hiprtcGetCode(prog, e.code.data());
+    hiprtcDestroyProgram(&prog);
+  }
+  if (be->plan_only) {
+    *out = RtcKernel{};
+    return GHIP_OK;
+  }
+  if (!e.loaded) {
+    hipSetDevice(be->device);
+    hipError_t h = hipModuleLoadData(&e.k.module, e.code.data());
+    if (h != hipSuccess) return check_hip(h, err, "hipModuleLoadData(generated kernel)");
+    h = hipModuleGetFunction(&e.k.func, e.k.module, entry.c_str());
+    if (h != hipSuccess) return check_hip(h, err, "hipModuleGetFunction(generated kernel)");
+    e.loaded = true;
+  }
+  *out = e.k;
+  return GHIP_OK;
+}
+
+}  // namespace ghip

@@ -1,0 +1,101 @@
+"""The BASELINE workloads as GoMLX graphs, built through the backend API.
+
+Each builder emits the ops a GoMLX graph program sends to a backend for that
+workload (the same primitive / fused ops the reference backend receives), so
+running them exercises the full Builder -> Compile -> Execute path.
+"""
+from __future__ import annotations
+
+import numpy as np
+
+from .backend import AxesLayout, Backend, dtypes, make_shape
+
+
+def rms_norm(f, x, gamma, eps: float):
+    """RMSNorm as the primitive chain GoMLX emits (no fused backend op exists):
+    x * rsqrt(ReduceSum(x*x, -1) / n + eps) * gamma."""
+    s = f.OpShape(x)
+    dt, dims = s.dtype, s.dims
+    n = dims[-1]
+    rows = dims[:-1]
+    ss = f.ReduceSum(f.Mul(x, x), len(dims) - 1)
+    inv_n = f.Constant(np.array(1.0 / n, np.float32), dtype=dt)
+    mean = f.Mul(ss, f.BroadcastInDim(inv_n, make_shape(dt, *rows), []))
+    e = f.Constant(np.array(eps, np.float32), dtype=dt)
+    r = f.Rsqrt(f.Add(mean, f.BroadcastInDim(e, make_shape(dt, *rows), [])))
+    rb = f.BroadcastInDim(r, make_shape(dt, *dims), list(range(len(dims) - 1)))
+    y = f.Mul(x, rb)
+    if gamma is not None:
+        y = f.Mul(y, f.BroadcastInDim(gamma, make_shape(dt, *dims), [len(dims) - 1]))
+    return y
+
+
+def softmax_chain(f, x):
+    """Softmax over the last axis as the primitive chain (max, sub, exp, sum, div)."""
+    s = f.OpShape(x)
+    r = len(s.dims)
+    m = f.ReduceMax(x, r - 1)
+    e = f.Exp(f.Sub(x, f.BroadcastInDim(m, s, list(range(r - 1)))))
+    z = f.ReduceSum(e, r - 1)
+    return f.Div(e, f.BroadcastInDim(z, s, list(range(r - 1))))
+
+
+def dense(f, x, w):
+    """x [..., din] @ w [din, dout] -> [..., dout] (DotGeneral, no batch axes)."""
+    rx = len(f.OpShape(x).dims)
+    return f.DotGeneral(x, [rx - 1], [], w, [0], [])
+
+
+class TransformerBlockConfig:
+    def __init__(self, batch=8, seq=1024, vocab=32000, d_model=2048, heads=16, head_dim=128,
+                 ffn=8192, eps=1e-6, dtype=dtypes.BFloat16):
+        self.batch, self.seq, self.vocab = batch, seq, vocab
+        self.d_model, self.heads, self.head_dim, self.ffn = d_model, heads, head_dim, ffn
+        self.eps, self.dtype = eps, dtype
+
+    def flops(self) -> int:
+        """Algorithmic flops of the block forward (GEMMs + full attention matrices)."""
+        T, d, f = self.batch * self.seq, self.d_model, self.ffn
+        S, H, Dh = self.seq, self.heads, self.head_dim
+        proj = 2 * T * d * d * 4          # Q, K, V, O
+        attn = 2 * 2 * self.batch * H * S * S * Dh
+        ffn = 2 * T * d * f * 3           # gate, up, down
+        return proj + attn + ffn
+
+    def param_shapes(self):
+        dt, d, f = self.dtype, self.d_model, self.ffn
+        return [
+            ("ids", make_shape(dtypes.Int32, self.batch, self.seq)),
+            ("embedding", make_shape(dt, self.vocab, d)),
+            ("g_attn", make_shape(dt, d)),
+            ("wq", make_shape(dt, d, d)), ("wk", make_shape(dt, d, d)),
+            ("wv", make_shape(dt, d, d)), ("wo", make_shape(dt, d, d)),
+            ("g_ffn", make_shape(dt, d)),
+            ("w_gate", make_shape(dt, d, f)), ("w_up", make_shape(dt, d, f)),
+            ("w_down", make_shape(dt, f, d)),
+        ]
+
+
+def transformer_block(backend: Backend, cfg: TransformerBlockConfig):
+    """Decoder-only block forward:
+    embedding gather -> RMSNorm -> 16-head causal attention -> residual ->
+    RMSNorm -> SwiGLU FFN -> residual.  Returns the compiled Executable."""
+    b = backend.Builder("transformer_block")
+    f = b.Main()
+    P = {name: f.Parameter(name, shape) for name, shape in cfg.param_shapes()}
+    B, S, d, H, Dh = cfg.batch, cfg.seq, cfg.d_model, cfg.heads, cfg.head_dim
+    ids = f.Reshape(P["ids"], B, S, 1)
+    x = f.Gather(P["embedding"], ids, 2, [2], [0], [0], [1, d], False)      # [B, S, d]
+    h = rms_norm(f, x, P["g_attn"], cfg.eps)
+    q = f.Reshape(dense(f, h, P["wq"]), B, S, H, Dh)
+    k = f.Reshape(dense(f, h, P["wk"]), B, S, H, Dh)
+    v = f.Reshape(dense(f, h, P["wv"]), B, S, H, Dh)
+    a = f.FusedScaledDotProductAttention(q, k, v, None, H, H, AxesLayout.BSHD, Dh ** -0.5, True)
+    x2 = f.Add(x, dense(f, f.Reshape(a, B, S, d), P["wo"]))
+    h2 = rms_norm(f, x2, P["g_ffn"], cfg.eps)
+    gate = dense(f, h2, P["w_gate"])
+    up = dense(f, h2, P["w_up"])
+    act = f.Mul(f.Mul(gate, f.Logistic(gate)), up)                          # SiLU(gate) * up
+    out = f.Add(x2, dense(f, act, P["w_down"]))
+    f.Return([out])
+    return b.Compile()

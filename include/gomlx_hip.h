@@ -133,6 +133,156 @@ int ghip_argminmax(int dtype, const void* x, int64_t outer, int64_t n, int64_t i
 int ghip_iota(int dtype, void* out, int64_t outer, int64_t n, int64_t inner, void* stream,
               GHipError* err);
 
+/* ===========================================================================
+ * Graph API: the GoMLX backends plugin surface (Backend / Builder / Function /
+ * Executable / Buffer) as a C ABI a cgo layer binds one-to-one.  It replaces the
+ * MPSGraph context / tensor / exec calls of bridge.h (context :48-53, op
+ * constructors :55-156, compile :159-163, execute :167-172).
+ *
+ * Values are small integer ids inside their Function (GHipValue, -1 = none);
+ * every constructor returns the new id or -1 with err filled.  Shapes follow
+ * XLA / GoMLX semantics (the upstream shapeinference rules).  Compile lowers the
+ * whole graph once: it fuses softmax / RMSNorm / LayerNorm / attention patterns
+ * into the row kernels above, DotGeneral into the batched GEMM with operand
+ * transposes folded into strides, and chains of elementwise ops into generated
+ * kernels (hipRTC, gfx950).  Execute launches the plan on the backend's stream
+ * with device-resident buffers and synchronizes once at the end.
+ * ======================================================================== */
+typedef struct GHipBackend GHipBackend;
+typedef struct GHipBuilder GHipBuilder;
+typedef struct GHipFunction GHipFunction;
+typedef struct GHipExecutable GHipExecutable;
+typedef struct GHipBuffer GHipBuffer;
+typedef int32_t GHipValue;
+
+/* Unary ops (backends.Function Abs ... Identity, function.go:658-782). */
+enum {
+  GHIP_UNARY_ABS = 0, GHIP_UNARY_NEG, GHIP_UNARY_SQRT, GHIP_UNARY_RSQRT, GHIP_UNARY_EXP,
+  GHIP_UNARY_EXPM1, GHIP_UNARY_LOG, GHIP_UNARY_LOG1P, GHIP_UNARY_SIN, GHIP_UNARY_COS,
+  GHIP_UNARY_TANH, GHIP_UNARY_LOGISTIC, GHIP_UNARY_ERF, GHIP_UNARY_FLOOR, GHIP_UNARY_CEIL,
+  GHIP_UNARY_ROUND, GHIP_UNARY_SIGN, GHIP_UNARY_LOGICAL_NOT, GHIP_UNARY_BITWISE_NOT,
+  GHIP_UNARY_IS_FINITE, GHIP_UNARY_IS_NAN, GHIP_UNARY_IDENTITY, GHIP_UNARY_COUNT
+};
+/* Binary ops (function.go:788-903). */
+enum {
+  GHIP_BINARY_ADD = 0, GHIP_BINARY_SUB, GHIP_BINARY_MUL, GHIP_BINARY_DIV, GHIP_BINARY_REM,
+  GHIP_BINARY_POW, GHIP_BINARY_MAX, GHIP_BINARY_MIN, GHIP_BINARY_ATAN2,
+  GHIP_BINARY_LOGICAL_AND, GHIP_BINARY_LOGICAL_OR, GHIP_BINARY_LOGICAL_XOR,
+  GHIP_BINARY_BITWISE_AND, GHIP_BINARY_BITWISE_OR, GHIP_BINARY_BITWISE_XOR,
+  GHIP_BINARY_SHIFT_LEFT, GHIP_BINARY_SHIFT_RIGHT_ARITHMETIC, GHIP_BINARY_SHIFT_RIGHT_LOGICAL,
+  GHIP_BINARY_COUNT
+};
+/* Comparisons (function.go:923-963); results are Bool. */
+enum {
+  GHIP_CMP_EQ = 0, GHIP_CMP_NE, GHIP_CMP_GT, GHIP_CMP_GE, GHIP_CMP_LT, GHIP_CMP_LE, GHIP_CMP_COUNT
+};
+/* Reductions; numbering is the reference's MPSGraphReduceType (bridge.h:40-45). */
+enum { GHIP_REDUCE_SUM = 0, GHIP_REDUCE_PRODUCT = 1, GHIP_REDUCE_MAX = 2, GHIP_REDUCE_MIN = 3 };
+/* Attention axes layout (backends.AxesLayout). */
+enum { GHIP_LAYOUT_BHSD = 0, GHIP_LAYOUT_BSHD = 1 };
+
+/* --- Backend (mpsgraph/gomlx/backend.go:22-167) ------------------------- */
+/* New (backend.go:33-43).  config: "" or "hip:device=N"; "plan" builds a
+ * backend that compiles (lowers, generates kernels) but cannot execute — it
+ * needs no GPU and exists so the lowering can be inspected anywhere. */
+GHipBackend* ghip_backend_new(const char* config, GHipError* err);
+void ghip_backend_finalize(GHipBackend* b);               /* Finalize (:80-92) */
+int ghip_backend_is_finalized(GHipBackend* b);            /* IsFinalized (:95-99) */
+int ghip_backend_description(GHipBackend* b, char* buf, size_t buflen); /* Description */
+int ghip_backend_num_devices(GHipBackend* b);             /* NumDevices (:57) */
+void* ghip_backend_stream(GHipBackend* b);                /* stream Execute uses */
+
+/* --- Buffers (buffer.go:20-119, DataInterface backend.go:103-167) ------- */
+/* BufferFromFlatData: device buffer of `shape` holding a copy of host `data`. */
+GHipBuffer* ghip_buffer_from_host(GHipBackend* b, int dtype, const int64_t* dims, int rank,
+                                  const void* data, size_t nbytes, GHipError* err);
+/* NewSharedBuffer (device memory, contents undefined). */
+GHipBuffer* ghip_buffer_new(GHipBackend* b, int dtype, const int64_t* dims, int rank,
+                            GHipError* err);
+/* BufferToFlatData: copies the buffer into host `data` (nbytes must match). */
+int ghip_buffer_to_host(GHipBuffer* buf, void* data, size_t nbytes, GHipError* err);
+/* BufferShape: writes dtype and up to max_rank dims; returns the rank (-1: bad buffer). */
+int ghip_buffer_shape(GHipBuffer* buf, int* dtype, int64_t* dims, int max_rank);
+/* BufferData: the device pointer (zero-copy; valid until finalize). */
+void* ghip_buffer_device_ptr(GHipBuffer* buf);
+void ghip_buffer_finalize(GHipBuffer* buf);               /* BufferFinalize */
+
+/* --- Builder (builder.go:16-109) ---------------------------------------- */
+GHipBuilder* ghip_builder_new(GHipBackend* b, const char* name, GHipError* err);
+void ghip_builder_finalize(GHipBuilder* bl);
+GHipFunction* ghip_builder_main(GHipBuilder* bl);         /* Main (:50-55) */
+/* Compile (:72-91): errors on a second call, without Main, or without Return. */
+GHipExecutable* ghip_builder_compile(GHipBuilder* bl, GHipError* err);
+
+/* --- Function (function.go, dotgeneral.go, gather.go) ------------------ */
+GHipValue ghip_fn_parameter(GHipFunction* f, const char* name, int dtype, const int64_t* dims,
+                            int rank, GHipError* err);                  /* :285-295 */
+GHipValue ghip_fn_constant(GHipFunction* f, int dtype, const int64_t* dims, int rank,
+                           const void* data, size_t nbytes, GHipError* err); /* :298-334 */
+GHipValue ghip_fn_iota(GHipFunction* f, int dtype, const int64_t* dims, int rank, int axis,
+                       GHipError* err);                                 /* :1127-1135 */
+GHipValue ghip_fn_unary(GHipFunction* f, int op, GHipValue x, GHipError* err);
+GHipValue ghip_fn_binary(GHipFunction* f, int op, GHipValue lhs, GHipValue rhs, GHipError* err);
+GHipValue ghip_fn_compare(GHipFunction* f, int op, GHipValue lhs, GHipValue rhs, GHipError* err);
+GHipValue ghip_fn_where(GHipFunction* f, GHipValue cond, GHipValue on_true, GHipValue on_false,
+                        GHipError* err);                                /* :1044-1058 */
+GHipValue ghip_fn_clamp(GHipFunction* f, GHipValue lo, GHipValue x, GHipValue hi,
+                        GHipError* err);                                /* :1060-1072 */
+GHipValue ghip_fn_convert_dtype(GHipFunction* f, GHipValue x, int dtype, GHipError* err);
+GHipValue ghip_fn_reshape(GHipFunction* f, GHipValue x, const int64_t* dims, int rank,
+                          GHipError* err);                              /* :969-981 */
+GHipValue ghip_fn_transpose(GHipFunction* f, GHipValue x, const int* perm, int rank,
+                            GHipError* err);                            /* :983-996 */
+GHipValue ghip_fn_broadcast_in_dim(GHipFunction* f, GHipValue x, const int64_t* dims, int rank,
+                                   const int* axes, int naxes, GHipError* err); /* :1013-1042 */
+GHipValue ghip_fn_reduce(GHipFunction* f, int op, GHipValue x, const int* axes, int naxes,
+                         GHipError* err);                               /* :1147-1198 */
+GHipValue ghip_fn_arg_min_max(GHipFunction* f, GHipValue x, int axis, int out_dtype, int is_min,
+                              GHipError* err);                          /* :1204-1242 */
+GHipValue ghip_fn_dot_general(GHipFunction* f, GHipValue lhs, const int* lhs_contracting,
+                              int nlc, const int* lhs_batch, int nlb, GHipValue rhs,
+                              const int* rhs_contracting, int nrc, const int* rhs_batch,
+                              int nrb, GHipError* err);                 /* dotgeneral.go:65-164 */
+GHipValue ghip_fn_gather(GHipFunction* f, GHipValue operand, GHipValue start_indices,
+                         int index_vector_axis, const int* offset_output_axes, int n_offset,
+                         const int* collapsed_slice_axes, int n_collapsed,
+                         const int* start_index_map, int n_map, const int64_t* slice_sizes,
+                         int n_sizes, int indices_are_sorted, GHipError* err); /* gather.go:24-56 */
+GHipValue ghip_fn_slice(GHipFunction* f, GHipValue x, const int64_t* starts, const int64_t* limits,
+                        const int64_t* strides, int rank, GHipError* err);  /* :1074-1091 */
+GHipValue ghip_fn_concatenate(GHipFunction* f, int axis, const GHipValue* operands, int n,
+                              GHipError* err);                          /* :1093-1113 */
+GHipValue ghip_fn_reverse(GHipFunction* f, GHipValue x, const int* axes, int naxes,
+                          GHipError* err);                              /* :1115-1125 */
+GHipValue ghip_fn_fused_softmax(GHipFunction* f, GHipValue x, int axis, GHipError* err); /* :2276 */
+/* gamma / beta may be -1 (absent). */
+GHipValue ghip_fn_fused_layer_norm(GHipFunction* f, GHipValue x, const int* axes, int naxes,
+                                   double epsilon, GHipValue gamma, GHipValue beta,
+                                   GHipError* err);                     /* :2410-2565 */
+/* mask may be -1; layout GHIP_LAYOUT_*. */
+GHipValue ghip_fn_fused_sdpa(GHipFunction* f, GHipValue q, GHipValue k, GHipValue v,
+                             GHipValue mask, int num_heads, int num_kv_heads, int layout,
+                             double scale, int causal, GHipError* err); /* :2669-2907 */
+int ghip_fn_return(GHipFunction* f, const GHipValue* outputs, int n, GHipError* err); /* :337-345 */
+/* OpShape (builder.go:63-69): dtype + dims of a value; returns rank or -1. */
+int ghip_fn_value_shape(GHipFunction* f, GHipValue v, int* dtype, int64_t* dims, int max_rank);
+
+/* --- Executable (executable.go:19-112) ---------------------------------- */
+int ghip_exec_num_inputs(GHipExecutable* e);
+int ghip_exec_num_outputs(GHipExecutable* e);
+int ghip_exec_input_shape(GHipExecutable* e, int i, int* dtype, int64_t* dims, int max_rank);
+int ghip_exec_output_shape(GHipExecutable* e, int i, int* dtype, int64_t* dims, int max_rank);
+/* Execute (:50-112): validates count and shapes of `inputs`, runs the plan, and
+ * returns `nout` new output buffers (owned by the caller).  donate may be NULL;
+ * a donated input buffer may be reused for an output of identical shape.
+ * Calls on one executable are serialized. */
+int ghip_exec_execute(GHipExecutable* e, GHipBuffer* const* inputs, int n, const uint8_t* donate,
+                      GHipBuffer** outputs, int nout, GHipError* err);
+/* Human-readable lowering plan (one line per launch), for inspection / tests.
+ * Returns the full length; writes at most buflen-1 chars. */
+size_t ghip_exec_plan(GHipExecutable* e, char* buf, size_t buflen);
+void ghip_exec_finalize(GHipExecutable* e);
+
 #ifdef __cplusplus
 }
 #endif

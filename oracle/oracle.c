@@ -189,24 +189,33 @@ int orc_dot_general(const float* lhs, int lrank, const int64_t* ldims,
   int64_t* rb = axis_offsets(rdims, rrank, rbatch, nrb, &tmp);
   int64_t* rn = axis_offsets(rdims, rrank, rfree, nrf, &nn);
   int64_t* rk = axis_offsets(rdims, rrank, rcontract, nrc, &tmp);
-#pragma omp parallel for collapse(2) schedule(static)
-  for (int64_t b = 0; b < nb; ++b) {
-    for (int64_t m = 0; m < nm; ++m) {
-      const float* lp = lhs + lb[b] + lm[m];
-      for (int64_t n = 0; n < nn; ++n) {
-        const float* rp = rhs + rb[b] + rn[n];
-        double acc;
-        if (mode == ORC_MODE_F32SEQ) {
-          float s = 0.0f;
-          for (int64_t k = 0; k < nk; ++k) s += lp[lk[k]] * rp[rk[k]];
-          acc = s;
-        } else {
-          acc = 0.0;
-          for (int64_t k = 0; k < nk; ++k) acc += (double)lp[lk[k]] * (double)rp[rk[k]];
+  /* k-outer / n-inner so rows of rhs stream; each output still accumulates its
+   * terms in k order (sequentially for ORC_MODE_F32SEQ). */
+#pragma omp parallel
+  {
+    double* acc = (double*)malloc(sizeof(double) * (size_t)(nn > 0 ? nn : 1));
+    float* acc32 = (float*)malloc(sizeof(float) * (size_t)(nn > 0 ? nn : 1));
+#pragma omp for collapse(2) schedule(static)
+    for (int64_t b = 0; b < nb; ++b) {
+      for (int64_t m = 0; m < nm; ++m) {
+        const float* lp = lhs + lb[b] + lm[m];
+        for (int64_t n = 0; n < nn; ++n) { acc[n] = 0.0; acc32[n] = 0.0f; }
+        for (int64_t k = 0; k < nk; ++k) {
+          const float* rp = rhs + rb[b] + rk[k];
+          if (mode == ORC_MODE_F32SEQ) {
+            const float a = lp[lk[k]];
+            for (int64_t n = 0; n < nn; ++n) acc32[n] += a * rp[rn[n]];
+          } else {
+            const double a = lp[lk[k]];
+            for (int64_t n = 0; n < nn; ++n) acc[n] += a * (double)rp[rn[n]];
+          }
         }
-        out[(b * nm + m) * nn + n] = acc;
+        double* o = out + (b * nm + m) * nn;
+        for (int64_t n = 0; n < nn; ++n) o[n] = mode == ORC_MODE_F32SEQ ? (double)acc32[n] : acc[n];
       }
     }
+    free(acc);
+    free(acc32);
   }
   free(lb); free(lm); free(lk); free(rb); free(rn); free(rk);
   return 0;

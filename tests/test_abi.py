@@ -34,7 +34,8 @@ def test_library_exports_every_declared_symbol():
 
 def test_python_signatures_cover_header():
     # Every declared entry point has a ctypes signature, so no call goes untyped.
-    sigs = set(_lib.SIGNATURES) | {"ghip_version", "ghip_error_clear"}
+    from gomlx_hip import backend
+    sigs = set(_lib.SIGNATURES) | set(backend._GRAPH_SIGS) | {"ghip_version", "ghip_error_clear"}
     extra = declared_symbols() - sigs
     assert not extra, f"no ctypes signature for {sorted(extra)}"
 

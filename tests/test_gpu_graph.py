@@ -1,0 +1,419 @@
+"""Graph API on the GPU: Builder -> Compile -> Execute through the C ABI.
+
+The first block mirrors the reference's own backend tests
+(mpsgraph/gomlx/mpsgraph_test.go, cited per test) with the same inputs,
+expected values and tolerances; the rest checks fused lowerings and the
+transformer block against the CPU oracle."""
+import math
+
+import numpy as np
+import pytest
+
+from oracle import oracle as orc
+from gomlx_hip import synth
+from gomlx_hip.backend import AxesLayout, Backend, BackendError, dtypes, make_shape
+from gomlx_hip import graphs
+from conftest import rel_err, norm_err
+
+pytestmark = pytest.mark.gpu
+
+F32, BF16, I32, I64 = dtypes.Float32, dtypes.BFloat16, dtypes.Int32, dtypes.Int64
+
+
+@pytest.fixture(scope="module")
+def be(cuda):
+    b = Backend("")
+    yield b
+    b.Finalize()
+
+
+def run(be, build, inputs, name="t"):
+    """build(f, params) -> list of outputs; inputs: list of (np array, Shape)."""
+    b = be.Builder(name)
+    f = b.Main()
+    params = [f.Parameter(f"p{i}", s) for i, (_, s) in enumerate(inputs)]
+    outs = build(f, *params)
+    f.Return(outs)
+    ex = b.Compile()
+    bufs = [be.BufferFromFlatData(0, a, s) for a, s in inputs]
+    res = ex.Execute(bufs, None, 0)
+    out = []
+    for r in res:
+        s = be.BufferShape(r)
+        a = be.BufferToFlatData(r).reshape(s.dims)
+        if s.dtype == BF16:
+            a = synth.bf16_bits_to_f32(a)
+        out.append(a)
+    ex.Finalize()
+    return out
+
+
+def close(got, want, tol):
+    assert np.max(np.abs(np.asarray(got, np.float64).reshape(-1) - np.asarray(want, np.float64).reshape(-1))) <= tol
+
+
+# ------------------------------------------------------------ reference Tier A mirrors
+def test_backend_creation(be):                                    # :27-42
+    assert be.Name() == "hip" and be.NumDevices() == 1
+    assert "gfx950" in be.Description()
+
+
+def test_buffer_operations(be):                                   # :44-81
+    s = make_shape(F32, 2, 3)
+    buf = be.BufferFromFlatData(0, np.arange(1, 7, dtype=np.float32), s)
+    assert be.BufferShape(buf) == s
+    assert be.BufferToFlatData(buf).tolist() == [1, 2, 3, 4, 5, 6]
+    be.BufferFinalize(buf)
+    with pytest.raises(BackendError):
+        be.BufferFromFlatData(0, np.zeros(5, np.float32), s)     # size mismatch
+
+
+def test_add_operation(be):                                       # :223-239
+    s = make_shape(F32, 2, 3)
+    (y,) = run(be, lambda f, x, y: [f.Add(x, y)],
+               [(np.array([1, 2, 3, 4, 5, 6], np.float32), s), (np.array([10, 20, 30, 40, 50, 60], np.float32), s)])
+    close(y, [11, 22, 33, 44, 55, 66], 1e-5)
+
+
+@pytest.mark.parametrize("name,inp,exp,tol", [                    # :241-276
+    ("Abs", [-1, 2, -3, 4], [1, 2, 3, 4], 1e-5),
+    ("Neg", [-1, 2, -3, 4], [1, -2, 3, -4], 1e-5),
+    ("Sqrt", [1, 4, 9, 16], [1, 2, 3, 4], 1e-5),
+    ("Exp", [0, 1], [1, math.e], 1e-5),
+    ("Log", [1, math.e], [0, 1], 1e-4),
+    ("Tanh", [0, 1], [0, math.tanh(1)], 1e-5),
+])
+def test_unary_operations(be, name, inp, exp, tol):
+    x = np.array(inp, np.float32)
+    (y,) = run(be, lambda f, a: [getattr(f, name)(a)], [(x, make_shape(F32, len(inp)))])
+    close(y, exp, tol)
+
+
+@pytest.mark.parametrize("name,exp,tol", [                        # :278-324
+    ("Add", [13, 25, 40, 48], 1e-5), ("Sub", [7, 15, 20, 32], 1e-5), ("Mul", [30, 100, 300, 320], 1e-5),
+    ("Div", [10 / 3, 4, 3, 5], 1e-4), ("Max", [10, 20, 30, 40], 1e-5), ("Min", [3, 5, 10, 8], 1e-5),
+])
+def test_binary_operations(be, name, exp, tol):
+    s = make_shape(F32, 4)
+    (y,) = run(be, lambda f, a, b: [getattr(f, name)(a, b)],
+               [(np.array([10, 20, 30, 40], np.float32), s), (np.array([3, 5, 10, 8], np.float32), s)])
+    close(y, exp, tol)
+
+
+def test_reshape_constant_reduce(be):                             # :326-487
+    (r,) = run(be, lambda f, x: [f.Reshape(x, 3, 2)], [(np.arange(6, dtype=np.float32), make_shape(F32, 2, 3))])
+    assert r.shape == (3, 2) and r.reshape(-1).tolist() == list(range(6))
+    (c,) = run(be, lambda f, x: [f.Add(x, f.Constant(np.array([10, 20, 30], np.float32), 3))],
+               [(np.array([1, 2, 3], np.float32), make_shape(F32, 3))])
+    close(c, [11, 22, 33], 1e-5)
+    x = np.array([1, 2, 3, 4, 5, 6], np.float32)
+    s, p, mx, mn = run(be, lambda f, a: [f.ReduceSum(a, 1), f.ReduceProduct(a, 1), f.ReduceMax(a, 0), f.ReduceMin(a)],
+                       [(x, make_shape(F32, 2, 3))])
+    close(s, [6, 15], 1e-5)
+    close(p, [6, 120], 1e-5)                                       # :1318-1365
+    close(mx, [4, 5, 6], 0)
+    close(mn, [1], 0)
+
+
+def test_dot_general_known_answers(be, known):                    # :489-596
+    for name in ("dot_simple", "dot_batched"):
+        c = known[name]
+        (y,) = run(be, lambda f, a, b: [f.DotGeneral(a, c["lc"], c["lb"], b, c["rc"], c["rb"])],
+                   [(np.array(c["lhs"], np.float32), make_shape(F32, *c["lhs_shape"])),
+                    (np.array(c["rhs"], np.float32), make_shape(F32, *c["rhs_shape"]))])
+        close(y, c["expected"], c["tol"])
+
+
+def test_gather_known_answer(be, known):                          # :599-674
+    c = known["gather_embedding"]
+    (y,) = run(be, lambda f, t, i: [f.Gather(t, i, 1, [1], [0], [0], [1, 3], False)],
+               [(np.array(c["table"], np.float32), make_shape(F32, 4, 3)),
+                (np.array(c["ids"], np.int32), make_shape(I32, 2, 1))])
+    assert y.reshape(-1).tolist() == c["expected"]
+
+
+def test_slice_concat_broadcast_reverse_transpose(be):            # :677-876, :1269-1316, :1535-1582
+    x = np.arange(12, dtype=np.float32)
+    (s,) = run(be, lambda f, a: [f.Slice(a, [1, 1], [3, 3], [1, 1])], [(x, make_shape(F32, 3, 4))])
+    close(s, [5, 6, 9, 10], 0)  # arange(12) (the reference fills 1..12 and expects [6,7,10,11])
+    (c,) = run(be, lambda f, a, b: [f.Concatenate(1, a, b)],
+               [(np.array([1, 2, 3, 4], np.float32), make_shape(F32, 2, 2)),
+                (np.array([5, 6, 7, 8, 9, 10], np.float32), make_shape(F32, 2, 3))])
+    close(c, [1, 2, 5, 6, 7, 3, 4, 8, 9, 10], 0)
+    (b,) = run(be, lambda f, a: [f.BroadcastInDim(a, make_shape(F32, 2, 3), [1])],
+               [(np.array([10, 20, 30], np.float32), make_shape(F32, 3))])
+    close(b, [10, 20, 30, 10, 20, 30], 0)
+    v = np.array([1, 2, 3, 4, 5, 6], np.float32)
+    r, t = run(be, lambda f, a: [f.Reverse(a, 1), f.Transpose(a, 1, 0)], [(v, make_shape(F32, 2, 3))])
+    close(r, [3, 2, 1, 6, 5, 4], 0)
+    close(t, [1, 4, 2, 5, 3, 6], 0)
+
+
+def test_iota_argmax_convert(be, known):                          # :785-822, :941-991, :1485-1532
+    b = be.Builder("iota")
+    f = b.Main()
+    f.Return([f.Iota(make_shape(F32, 2, 3), 1)])
+    ex = b.Compile()
+    (out,) = ex.Execute([], None, 0)
+    assert be.BufferToFlatData(out).tolist() == known["iota"]["expected"]
+    (a,) = run(be, lambda f, x: [f.ArgMinMax(x, 1, I32, False)],
+               [(np.array([1, 5, 3, 8, 2, 6], np.float32), make_shape(F32, 2, 3))])
+    assert a.tolist() == [1, 0]
+    (cv,) = run(be, lambda f, x: [f.ConvertDType(x, I32)], [(np.array([1.7, 2.3, -0.9], np.float32), make_shape(F32, 3))])
+    assert cv.tolist() == [1, 2, 0]
+
+
+def test_comparisons_and_where(be):                               # :1367-1483
+    s = make_shape(F32, 4)
+    l, r = np.array([1, 2, 3, 4], np.float32), np.array([2, 2, 2, 2], np.float32)
+    outs = run(be, lambda f, a, b: [f.Equal(a, b), f.NotEqual(a, b), f.GreaterThan(a, b), f.LessThan(a, b),
+                                    f.GreaterOrEqual(a, b), f.LessOrEqual(a, b)], [(l, s), (r, s)])
+    for got, want in zip(outs, [l == r, l != r, l > r, l < r, l >= r, l <= r]):
+        assert got.astype(bool).tolist() == want.tolist()
+    (w,) = run(be, lambda f, c, t, e: [f.Where(c, t, e)],
+               [(np.array([True, False, True, False]), make_shape(dtypes.Bool, 4)),
+                (np.array([10, 20, 30, 40], np.float32), s), (np.array([1, 2, 3, 4], np.float32), s)])
+    close(w, [10, 2, 30, 4], 0)
+
+
+def test_multiple_outputs_and_chained_ops(be):                    # :1584-1634, :1727-1803
+    s = make_shape(F32, 3)
+    a, d = run(be, lambda f, x, y: [f.Add(x, y), f.Sub(x, y)],
+               [(np.array([10, 20, 30], np.float32), s), (np.array([1, 2, 3], np.float32), s)])
+    close(a, [11, 22, 33], 1e-5)
+    close(d, [9, 18, 27], 1e-5)
+    x = np.array([1.0, 2.0, 3.0, 4.0], np.float32)
+    w = np.array([0.5, -0.5, 1.0, -1.0], np.float32)
+    bb = np.array([0.1, 0.2, -0.1, 0.0], np.float32)
+    (y,) = run(be, lambda f, xx: [f.Logistic(f.Add(f.Mul(xx, f.Constant(w, 4)), f.Constant(bb, 4)))],
+               [(x, make_shape(F32, 4))])
+    close(y, 1 / (1 + np.exp(-(x.astype(np.float64) * w + bb))), 1e-5)
+
+
+def test_transformer_block_attention_chain(be, known):            # :1638-1724
+    c = known["attention_dot_chain"]
+    s = make_shape(F32, 2, 3)
+
+    def build(f, q, k, v):
+        scores = f.DotGeneral(q, [1], [], k, [1], [])
+        sc = f.Constant(np.array([c["scale"]], np.float32), 1)
+        scores = f.Mul(scores, f.BroadcastInDim(sc, make_shape(F32, 2, 2), [1]))
+        w = f.FusedSoftmax(scores, 1)
+        return [f.DotGeneral(w, [1], [], v, [0], [])]
+    (y,) = run(be, build, [(np.array(c["q"], np.float32), s), (np.array(c["k"], np.float32), s),
+                           (np.array(c["v"], np.float32), s)])
+    close(y, c["expected"], c["tol"])
+
+
+def test_int64_and_uint8(be):                                     # :2746-2804
+    (a,) = run(be, lambda f, x, y: [f.Add(x, y)], [(np.array([1, 2, 3], np.int64), make_shape(I64, 3)),
+                                                   (np.array([10, 20, 30], np.int64), make_shape(I64, 3))])
+    assert a.tolist() == [11, 22, 33]
+    (cv,) = run(be, lambda f, x: [f.ConvertDType(x, I64)], [(np.array([1.5, 2.7, -3.2], np.float32), make_shape(F32, 3))])
+    assert cv.tolist() == [1, 2, -3]
+    (u,) = run(be, lambda f, x, y: [f.Add(x, y)], [(np.array([250, 3], np.uint8), make_shape(dtypes.Uint8, 2)),
+                                                   (np.array([10, 4], np.uint8), make_shape(dtypes.Uint8, 2))])
+    assert u.tolist() == [4, 7]  # wraps like Go's uint8
+
+
+# ------------------------------------------------------------ reference Tier D mirrors
+def test_fused_softmax_known_answer(be, known):                   # :1133-1190
+    c = known["softmax"]
+    (y,) = run(be, lambda f, x: [f.FusedSoftmax(x, 1)], [(np.array(c["x"], np.float32), make_shape(F32, 2, 3))])
+    close(y, c["expected"], c["tol"])
+
+
+def test_fused_layer_norm_known_answers(be, known):               # :2595-2623
+    c = known["layernorm_basic"]
+    (y,) = run(be, lambda f, x: [f.FusedLayerNorm(x, [-1], c["eps"])],
+               [(np.array(c["x"], np.float32), make_shape(F32, 2, 4))])
+    close(y, c["expected"], c["tol"])
+    c = known["layernorm_gamma_beta"]
+    (y,) = run(be, lambda f, x, g, b: [f.FusedLayerNorm(x, [-1], c["eps"], g, b)],
+               [(np.array(c["x"], np.float32), make_shape(F32, 2, 4)),
+                (np.array(c["gamma"], np.float32), make_shape(F32, 1, 4)),
+                (np.array(c["beta"], np.float32), make_shape(F32, 1, 4))])
+    close(y[0], c["expected_first_row"], c["tol"])
+
+
+def test_fused_sdpa_known_answers(be, known):                     # :2966-3058
+    c = known["sdpa_causal"]
+    sh = make_shape(F32, *c["shape"])
+    (y,) = run(be, lambda f, q, k, v: [f.FusedScaledDotProductAttention(q, k, v, None, 1, 1, AxesLayout.BHSD, c["scale"], True)],
+               [(np.array(c[n], np.float32), sh) for n in "qkv"])
+    close(y[0, 0, 0], c["expected_first_row"], c["tol"])
+    c = known["sdpa_bool_mask"]
+    sh = make_shape(F32, *c["shape"])
+    (y,) = run(be, lambda f, q, k, v, m: [f.FusedScaledDotProductAttention(q, k, v, m, 1, 1, AxesLayout.BHSD, 1.0, False)],
+               [(np.array(c[n], np.float32), sh) for n in "qkv"] +
+               [(np.array(c["mask"], bool), make_shape(dtypes.Bool, 1, 1, 2, 2))])
+    close(y[0, 0, 0], c["expected_first_row"], c["tol"])
+    c = known["sdpa_basic_range"]
+    (y,) = run(be, lambda f, q, k, v: [f.FusedScaledDotProductAttention(q, k, v, None, 1, 1, AxesLayout.BSHD, c["scale"], False)],
+               [(np.array(c[n], np.float32), make_shape(F32, 1, 2, 1, 2)) for n in "qkv"])
+    assert y.shape == (1, 2, 1, 2) and np.all(y > -0.1) and np.all(y < 1.1)
+
+
+def test_bfloat16_add_and_matmul(be):                             # :3128-3156
+    (y,) = run(be, lambda f, x: [f.ConvertDType(f.Add(f.ConvertDType(x, BF16), f.ConvertDType(x, BF16)), F32)],
+               [(np.array([1, 2, 3, 4], np.float32), make_shape(F32, 4))])
+    close(y, [2, 4, 6, 8], 0.1)
+
+    def mm(f, a, b):
+        c = f.DotGeneral(f.ConvertDType(a, BF16), [1], [], f.ConvertDType(b, BF16), [0], [])
+        return [f.ConvertDType(c, F32)]
+    (y,) = run(be, mm, [(np.array([1, 2, 3, 4], np.float32), make_shape(F32, 2, 2)),
+                        (np.array([5, 6, 7, 8], np.float32), make_shape(F32, 2, 2))])
+    close(y, [19, 22, 43, 50], 1.0)
+
+
+# ------------------------------------------------------------ fused lowerings vs the oracle
+def test_graph_softmax_chain_and_rmsnorm_chain(be):
+    x = synth.normal(1001, (4096, 1024), std=2.0)
+    y1, y2 = run(be, lambda f, a: [graphs.softmax_chain(f, a), f.FusedSoftmax(a, -1)], [(x, make_shape(F32, 4096, 1024))])
+    ref = orc.softmax(x)
+    assert rel_err(y1, ref) <= 1e-5 and rel_err(y2, ref) <= 1e-5
+    x = synth.normal(2001, (512, 4096))
+    g = synth.uniform_f32(2002, (4096,), 0.5, 1.5)
+    (y,) = run(be, lambda f, a, gg: [graphs.rms_norm(f, a, gg, 1e-6)],
+               [(x, make_shape(F32, 512, 4096)), (g, make_shape(F32, 4096))])
+    assert rel_err(y, orc.rmsnorm(x, g, 1e-6)) <= 1e-5
+
+
+def test_graph_dot_general_layouts(be):
+    a = synth.round_bf16(synth.normal(3001, (2, 64, 96), std=0.125))
+    b = synth.round_bf16(synth.normal(3002, (96, 2, 80), std=0.125))
+    # contracting lhs axis 2 with rhs axis 0, batch lhs 0 / rhs 1 (rhs layout needs a stride fold)
+    (y,) = run(be, lambda f, x, w: [f.DotGeneral(x, [2], [0], w, [0], [1])],
+               [(a, make_shape(BF16, 2, 64, 96)), (b, make_shape(BF16, 96, 2, 80))])
+    assert rel_err(y, orc.dot_general(a, [2], [0], b, [0], [1])) <= 1e-2
+    c = synth.normal(3003, (4, 3, 5, 6))
+    d = synth.normal(3004, (6, 4, 7, 5))
+    (y,) = run(be, lambda f, x, w: [f.DotGeneral(x, [3, 2], [0], w, [0, 3], [1])],
+               [(c, make_shape(F32, 4, 3, 5, 6)), (d, make_shape(F32, 6, 4, 7, 5))])
+    assert rel_err(y, orc.dot_general(c, [3, 2], [0], d, [0, 3], [1])) <= 1e-5
+
+
+@pytest.mark.parametrize("layout", [AxesLayout.BHSD, AxesLayout.BSHD])
+def test_graph_sdpa_gqa_causal(be, layout):
+    B, H, Hkv, S, D = 2, 8, 2, 128, 64
+    q = synth.normal(4001, (B, H, S, D))
+    k = synth.normal(4002, (B, Hkv, S, D))
+    v = synth.normal(4003, (B, Hkv, S, D))
+    ref = orc.sdpa(q, k, v, scale=D ** -0.5, causal=True)
+    t = (lambda a: np.ascontiguousarray(a.transpose(0, 2, 1, 3))) if layout == AxesLayout.BSHD else (lambda a: a)
+    (y,) = run(be, lambda f, qq, kk, vv: [f.FusedScaledDotProductAttention(qq, kk, vv, None, H, Hkv, layout, D ** -0.5, True)],
+               [(t(q), make_shape(F32, *t(q).shape)), (t(k), make_shape(F32, *t(k).shape)), (t(v), make_shape(F32, *t(v).shape))])
+    if layout == AxesLayout.BSHD:
+        y = y.transpose(0, 2, 1, 3)
+    assert rel_err(y, ref) <= 1e-4
+
+
+def test_graph_elementwise_semantics(be):
+    x = np.array([-2.5, -0.5, 0.5, 1.5, 2.5, np.nan, np.inf, -np.inf], np.float32)
+    s = make_shape(F32, 8)
+    outs = run(be, lambda f, a: [f.Round(a), f.Sign(a), f.Floor(a), f.IsNaN(a), f.IsFinite(a),
+                                 f.ConvertDType(a, I32)], [(x, s)])
+    assert np.array_equal(outs[0], np.rint(x), equal_nan=True)
+    assert np.array_equal(outs[1], np.sign(x), equal_nan=True)
+    assert np.array_equal(outs[2], np.floor(x), equal_nan=True)
+    assert outs[3].astype(bool).tolist() == np.isnan(x).tolist()
+    assert outs[4].astype(bool).tolist() == np.isfinite(x).tolist()
+    assert outs[5].tolist() == [-2, 0, 0, 1, 2, 0, 2147483647, -2147483648]
+    i = np.array([7, -7, 7, -7, 5], np.int32)
+    j = np.array([2, 2, -2, -2, 0], np.int32)
+    d, r, sh = run(be, lambda f, a, b: [f.Div(a, b), f.Rem(a, b), f.ShiftRightLogical(a, f.Abs(b))],
+                   [(i, make_shape(I32, 5)), (j, make_shape(I32, 5))])
+    assert d.tolist() == [3, -3, -3, 3, -1]          # truncating division; x/0 = -1
+    assert r.tolist() == [1, -1, 1, -1, 5]           # sign of the dividend; x%0 = x
+    assert sh.tolist() == [1, (np.uint32(-7 & 0xFFFFFFFF) >> 2).astype(np.int32), 1,
+                           (np.uint32(-7 & 0xFFFFFFFF) >> 2).astype(np.int32), 5]
+
+
+def test_execute_errors(be):                                      # executable.go:54-68
+    b = be.Builder("err")
+    f = b.Main()
+    x = f.Parameter("x", make_shape(F32, 3))
+    f.Return([f.Exp(x)])
+    ex = b.Compile()
+    with pytest.raises(BackendError, match="expected 1 inputs"):
+        ex.Execute([], None, 0)
+    bad = be.BufferFromFlatData(0, np.zeros(4, np.float32), make_shape(F32, 4))
+    with pytest.raises(BackendError, match="shape mismatch"):
+        ex.Execute([bad], None, 0)
+
+
+# ------------------------------------------------------------ transformer block
+def _bf(a):
+    return synth.round_bf16(np.asarray(a, np.float32))
+
+
+def _tb_reference(cfg, P, emulate_bf16=True):
+    """Block forward composed from oracle primitives in fp64; with emulate_bf16
+    every op output the graph holds in bf16 is rounded to bf16 (the graph's
+    semantics), with the fused RMSNorm / attention softmax rounded once."""
+    r = _bf if emulate_bf16 else (lambda a: np.asarray(a, np.float64))
+    B, S, d, H, Dh = cfg.batch, cfg.seq, cfg.d_model, cfg.heads, cfg.head_dim
+    x = orc.gather_rows(P["embedding"], P["ids"].reshape(-1)).reshape(B, S, d).astype(np.float64)
+    h = r(orc.rmsnorm(x.astype(np.float32), P["g_attn"], cfg.eps))
+    def proj(a, w):
+        return r(orc.dot_general(np.asarray(a, np.float32), [a.ndim - 1], [], w, [0], []))
+    q, k, v = (proj(h, P[w]).reshape(B, S, H, Dh).transpose(0, 2, 1, 3) for w in ("wq", "wk", "wv"))
+    if emulate_bf16:
+        s = r(orc.dot_general(np.ascontiguousarray(q, np.float32), [3], [0, 1], np.ascontiguousarray(k, np.float32), [3], [0, 1]))
+        p = orc.softmax(np.where(np.tril(np.ones((S, S), bool)), s * (Dh ** -0.5), -np.inf).astype(np.float32))
+        a = r(orc.dot_general(r(p).astype(np.float32), [3], [0, 1], np.ascontiguousarray(v, np.float32), [2], [0, 1]))
+    else:
+        a = orc.sdpa(q, k, v, scale=Dh ** -0.5, causal=True)
+    a = a.transpose(0, 2, 1, 3).reshape(B, S, d)
+    x2 = r(x + proj(a, P["wo"]))
+    h2 = r(orc.rmsnorm(np.asarray(x2, np.float32), P["g_ffn"], cfg.eps))
+    gate, up = proj(h2, P["w_gate"]), proj(h2, P["w_up"])
+    act = r(r(gate * r(1.0 / (1.0 + np.exp(-gate)))) * up)
+    return r(x2 + proj(act, P["w_down"]))
+
+
+def _tb_inputs(cfg, seed=5001):
+    P = {"ids": synth.uniform_int(seed, (cfg.batch, cfg.seq), 0, cfg.vocab)}
+    for i, (name, shape) in enumerate(cfg.param_shapes()[1:]):
+        if name.startswith("g_"):
+            P[name] = np.ones(shape.dims, np.float32)
+        else:
+            P[name] = _bf(synth.normal(seed + 1 + i, shape.dims, std=0.02))
+    return P
+
+
+def _tb_run(be, cfg, P):
+    ex = graphs.transformer_block(be, cfg)
+    bufs = [be.BufferFromFlatData(0, P[name], shape) for name, shape in cfg.param_shapes()]
+    (out,) = ex.Execute(bufs, None, 0)
+    y = synth.bf16_bits_to_f32(be.BufferToFlatData(out)).reshape(cfg.batch, cfg.seq, cfg.d_model)
+    return ex, y
+
+
+def test_transformer_block_small_vs_oracle(be):
+    cfg = graphs.TransformerBlockConfig(batch=2, seq=128, vocab=1000, d_model=256, heads=2, head_dim=128, ffn=1024)
+    P = _tb_inputs(cfg)
+    ex, y = _tb_run(be, cfg, P)
+    assert "rmsnorm_rows" in ex.Plan() and "scale_mask_softmax_rows" in ex.Plan()
+    emu = _tb_reference(cfg, P, emulate_bf16=True)
+    exact = _tb_reference(cfg, P, emulate_bf16=False)
+    # Same rounding points as the graph: differences are isolated bf16 rounding
+    # flips (fp32 vs fp64 accumulation at a rounding boundary), which stay small in
+    # norm; a few ulps elementwise where residual sums cancel.
+    assert norm_err(y, emu) <= 3e-3
+    assert rel_err(y, emu) <= 4e-2
+    assert norm_err(y, exact) <= 1e-2       # against fp64 truth (no intermediate rounding)
+
+
+def test_transformer_block_config_sampled(be):
+    """BASELINE configs[4] end to end (ids [8,1024], d_model 2048, 16 heads,
+    FFN 8192), checked on batch row 0 against the oracle composition."""
+    cfg = graphs.TransformerBlockConfig()
+    P = _tb_inputs(cfg)
+    ex, y = _tb_run(be, cfg, P)
+    assert np.all(np.isfinite(y))
+    one = graphs.TransformerBlockConfig(batch=1)
+    P1 = dict(P, ids=P["ids"][:1])
+    exact = _tb_reference(one, P1, emulate_bf16=False)
+    assert norm_err(y[:1], exact) <= 1e-2

@@ -1,0 +1,167 @@
+"""Graph API host logic on the plan-only backend (no GPU): shape inference,
+error paths the reference's Go code returns, and the lowering decisions."""
+import numpy as np
+import pytest
+
+from gomlx_hip.backend import AxesLayout, Backend, BackendError, dtypes, make_shape
+from gomlx_hip import graphs
+
+
+@pytest.fixture(scope="module")
+def be():
+    b = Backend("plan")
+    yield b
+    b.Finalize()
+
+
+F32 = dtypes.Float32
+BF16 = dtypes.BFloat16
+
+
+def test_backend_identity(be):
+    assert be.Name() == "hip"
+    assert "plan-only" in be.Description()
+    assert be.NumDevices() == 0
+    with pytest.raises(BackendError):
+        Backend("mpsgraph:whatever")
+
+
+def test_shape_inference(be):
+    f = be.Builder("shapes").Main()
+    x = f.Parameter("x", make_shape(F32, 2, 3, 4))
+    assert f.OpShape(f.Transpose(x, 2, 0, 1)).dims == (4, 2, 3)
+    assert f.OpShape(f.ReduceSum(x, 1)).dims == (2, 4)
+    assert f.OpShape(f.ReduceMax(x)).dims == ()
+    assert f.OpShape(f.ArgMinMax(x, 2, dtypes.Int32, False)) == make_shape(dtypes.Int32, 2, 3)
+    assert f.OpShape(f.GreaterThan(x, x)).dtype == dtypes.Bool
+    y = f.Parameter("y", make_shape(F32, 5, 4, 7))
+    # DotGeneral output order [batch..., lhs free..., rhs free...] (dotgeneral.go:15-53)
+    assert f.OpShape(f.DotGeneral(x, [2], [], y, [1], [])).dims == (2, 3, 5, 7)
+    z = f.Parameter("z", make_shape(F32, 2, 4, 6))
+    assert f.OpShape(f.DotGeneral(x, [2], [0], z, [1], [0])).dims == (2, 3, 6)
+    assert f.OpShape(f.Slice(x, [0, 1, 0], [2, 3, 4], [1, 1, 2])).dims == (2, 2, 2)
+    assert f.OpShape(f.Concatenate(1, x, x)).dims == (2, 6, 4)
+    emb = f.Parameter("emb", make_shape(BF16, 100, 16))
+    ids = f.Parameter("ids", make_shape(dtypes.Int32, 3, 5, 1))
+    assert f.OpShape(f.Gather(emb, ids, 2, [2], [0], [0], [1, 16])).dims == (3, 5, 16)
+    q = f.Parameter("q", make_shape(BF16, 2, 4, 8, 16))
+    kv = f.Parameter("kv", make_shape(BF16, 2, 2, 8, 16))
+    o = f.FusedScaledDotProductAttention(q, kv, kv, None, 4, 2, AxesLayout.BHSD, 0.25, True)
+    assert f.OpShape(o).dims == (2, 4, 8, 16)
+
+
+def test_build_errors(be):
+    f = be.Builder("errors").Main()
+    x = f.Parameter("x", make_shape(F32, 2, 3))
+    i = f.Parameter("i", make_shape(dtypes.Int32, 2, 3))
+    with pytest.raises(BackendError, match="dtype mismatch"):
+        f.Add(x, i)
+    with pytest.raises(BackendError):
+        f.Reshape(x, 7)
+    with pytest.raises(BackendError):
+        f.DotGeneral(x, [1], [], x, [1], [0])
+    q = f.Parameter("q", make_shape(F32, 2, 3, 4))
+    with pytest.raises(BackendError, match="rank 4"):  # function.go:2695-2697
+        f.FusedScaledDotProductAttention(q, q, q, None, 1, 1, AxesLayout.BHSD, 1.0, False)
+    with pytest.raises(BackendError, match="divisible"):
+        q4 = f.Parameter("q4", make_shape(F32, 1, 3, 2, 4))
+        f.FusedScaledDotProductAttention(q4, q4, q4, None, 3, 2, AxesLayout.BHSD, 1.0, False)
+    with pytest.raises(BackendError, match="out of range"):  # function.go:2420-2424
+        f.FusedLayerNorm(x, [5], 1e-5)
+
+
+def test_compile_state_errors(be):
+    b = be.Builder("state")
+    with pytest.raises(BackendError, match="no main"):      # builder.go:76-78
+        b.Compile()
+    b = be.Builder("state2")
+    f = b.Main()
+    f.Parameter("x", make_shape(F32, 2))
+    with pytest.raises(BackendError, match="Return"):       # builder.go:79-81
+        b.Compile()
+    x = f.Parameter("y", make_shape(F32, 2))
+    f.Return([f.Neg(x)])
+    b.Compile()
+    with pytest.raises(BackendError, match="already compiled"):  # builder.go:73-75
+        b.Compile()
+
+
+def plan_of(be, build):
+    b = be.Builder("p")
+    f = b.Main()
+    outs = build(f)
+    f.Return(outs)
+    return b.Compile().Plan()
+
+
+def test_rmsnorm_chain_is_fused(be):
+    def build(f):
+        x = f.Parameter("x", make_shape(BF16, 64, 256))
+        g = f.Parameter("g", make_shape(BF16, 256))
+        return [graphs.rms_norm(f, x, g, 1e-6)]
+    p = plan_of(be, build)
+    assert "rmsnorm_rows bfloat16 rows=64 n=256 +gamma" in p
+    assert "reduce" not in p and "fused_elementwise" not in p
+
+
+def test_softmax_chain_and_fused_softmax(be):
+    def build(f):
+        x = f.Parameter("x", make_shape(F32, 4096, 1024))
+        return [graphs.softmax_chain(f, x), f.FusedSoftmax(x, 1)]
+    p = plan_of(be, build)
+    assert p.count("softmax_rows float32 rows=4096 n=1024") == 2
+    assert "reduce" not in p
+
+
+def test_softmax_other_axis_moves_axis_last(be):
+    def build(f):
+        x = f.Parameter("x", make_shape(F32, 8, 16, 32))
+        return [f.FusedSoftmax(x, 1)]
+    p = plan_of(be, build)
+    assert "softmax_rows float32 rows=256 n=16" in p
+
+
+def test_dot_general_folds_transposes(be):
+    def build(f):
+        a = f.Parameter("a", make_shape(BF16, 8, 2048, 4096))
+        b = f.Parameter("b", make_shape(BF16, 8, 4096, 4096))
+        bt = f.Transpose(b, 0, 2, 1)                    # [8, N, K] view of the same data
+        return [f.DotGeneral(a, [2], [0], b, [1], [0]), f.DotGeneral(a, [2], [0], bt, [2], [0])]
+    p = plan_of(be, build)
+    assert p.count("strides folded") == 2 and "strided_copy" not in p
+    assert "arena 0 bytes" in p  # both products written straight into the outputs
+
+
+def test_elementwise_chain_is_one_kernel(be):
+    def build(f):
+        x = f.Parameter("x", make_shape(F32, 128, 64))
+        w = f.Parameter("w", make_shape(F32, 64))
+        c = f.Constant(np.array(0.5, np.float32))
+        y = f.Logistic(f.Add(f.Mul(x, f.BroadcastInDim(w, make_shape(F32, 128, 64), [1])),
+                             f.BroadcastInDim(c, make_shape(F32, 128, 64), [])))
+        return [y]
+    p = plan_of(be, build)
+    assert p.count("fused_elementwise") == 1 and "ops=3 inputs=2" in p
+
+
+def test_transformer_block_plan(be):
+    e = graphs.transformer_block(be, graphs.TransformerBlockConfig(batch=2, seq=64, vocab=100,
+                                                                   d_model=128, heads=2, head_dim=64,
+                                                                   ffn=256))
+    p = e.Plan()
+    assert p.count("rmsnorm_rows") == 2
+    assert p.count("gemm_batched") == 9
+    assert "scale_mask_softmax_rows" in p and "causal=1" in p
+    assert "gather_rows" in p
+    assert e.Outputs()[0].dims == (2, 64, 128)
+    assert [s.dims for s in e.Inputs()][:2] == [(2, 64), (100, 128)]
+
+
+def test_plan_backend_cannot_execute(be):
+    b = be.Builder("noexec")
+    f = b.Main()
+    x = f.Parameter("x", make_shape(F32, 4))
+    f.Return([f.Exp(x)])
+    e = b.Compile()
+    with pytest.raises(BackendError):
+        be.BufferFromFlatData(0, np.zeros(4, np.float32), make_shape(F32, 4))
