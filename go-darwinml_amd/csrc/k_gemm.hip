@@ -1,31 +1,40 @@
 // Batched GEMM for DotGeneral: c[b] = a[b] (M x K) * b[b] (K x N), fp32 accumulate.
 //
-// bf16 path (the MFMA path the metric is quoted on):
-//   * v_mfma_f32_32x32x16_bf16 (gfx950): every lane feeds 8 consecutive-k bf16 of
-//     one row (A) / one column (B), so both operand tiles live in LDS K-major:
-//     tile[row][64 k] with the 16-byte chunk index XOR-swizzled by (row & 7); a
-//     fragment read is one ds_read_b128 per lane and 8 consecutive lanes hit 8
-//     different chunks (no bank conflicts).
-//   * K-contiguous operands are copied to LDS with 16-byte loads/stores.
-//     MN-contiguous operands (e.g. rhs [K, N] row-major, the DotGeneral config)
-//     are loaded as 4(k) x 8(mn) blocks with 16-byte loads and transposed in
-//     registers (byte permutes) into four-k 8-byte LDS stores — no transpose pass
-//     over HBM, unlike the reference's two materialized rhs transposes
-//     (dotgeneral.go:116-145).
-//   * Two LDS stages: the global loads of k-tile t+1 are in flight while the MFMAs
-//     of tile t run; one barrier per k-tile.
+// bf16 path (the MFMA path the metric is quoted on), gfx950:
+//   * v_mfma_f32_32x32x16_bf16.  Each lane feeds 8 consecutive-k bf16 of one
+//     row of A / one column of B.  The MFMA is issued with the operands swapped
+//     (B fragment first), so each lane's accumulators hold 4 consecutive output
+//     columns and the epilogue stores 8 bytes (bf16) / 16 bytes (fp32) per lane.
+//   * Global -> LDS without a VGPR round trip: buffer_load_dwordx4 ... lds puts
+//     16 bytes per lane straight into LDS.  Out-of-range lanes are given an
+//     offset past the buffer's end and read zeros, which pads ragged M/N/K edges.
+//   * K-contiguous operand tiles live in LDS as [rows][64 k] with 16-byte chunks
+//     XOR-swizzled per row; fragments are one ds_read_b128 per lane.
+//     MN-contiguous operand tiles (e.g. rhs [K, N] row-major, the DotGeneral
+//     config) stay [64 k][rows] as in memory and are read with the gfx950
+//     transpose read ds_read_b64_tr_b16, so no transpose ever touches HBM or
+//     VGPRs (the reference materializes two rhs transposes, dotgeneral.go:116-145).
+//     Both swizzles are bank-conflict free for 8- and 16-lane LDS phases.
+//   * Two LDS stages of 64-deep k-tiles: the loads of tile t+2 are issued right
+//     after the barrier that retires tile t, so one tile of MFMA work covers the
+//     load latency.  The loads are issued as inline asm so the compiler does not
+//     wait on them before unrelated LDS reads; waits are explicit.
 //   * Workgroup -> tile mapping is XCD-aware: consecutive workgroup ids land on
 //     different XCDs (round robin), so ids are remapped to give each XCD a
 //     contiguous run of tiles, ordered in GROUP_M-row groups for L2 reuse.
 // fp32 path: v_mfma_f32_32x32x2f32 with MN-major LDS tiles (one float per lane).
-// Anything the vector paths cannot address (odd strides, unaligned bases) runs a
-// generic LDS-tiled kernel.
+// Anything the vector paths cannot address (odd strides, unaligned bases,
+// negative strides, > 2 GiB per batch slice) runs a generic LDS-tiled kernel.
 #include "common.h"
+
+#define GHIP_LDS __attribute__((address_space(3)))
 
 namespace ghip {
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
+typedef int i32x4_t __attribute__((ext_vector_type(4)));
 
 struct GemmParams {
   const void* a;
@@ -36,6 +45,8 @@ struct GemmParams {
   int64_t sc_b, sc_m;
   int64_t batch, M, N, K;
   int tiles_m, tiles_n;
+  uint32_t a_extent, b_extent;  // bytes addressable from one batch slice's base
+  int vec_c;                    // C rows allow 4-element vector stores
 };
 
 template <typename OutT>
@@ -63,109 +74,155 @@ __device__ __forceinline__ void map_tile(int64_t bid, int64_t total, int tiles_m
 }
 
 // ---------------------------------------------------------------------------
-// bf16 operand tile loader: R rows (m or n) x 64 k, LDS layout [R][64] K-major,
-// 16-byte chunks swizzled by (row & 7).
+// bf16 operand tiles: R rows (m for A, n for B) x 64 k, loaded into LDS by
+// buffer_load ... lds.
 // ---------------------------------------------------------------------------
 constexpr int kBK = 64;
+constexpr uint32_t kOffOOB = 0x80000000u;  // past any buffer this path accepts
 
-__device__ __forceinline__ int swz(int row, int chunk) { return (chunk ^ (row & 7)); }
+// K-contiguous LDS tile [R][64]: 16-byte chunk kc of row r sits at slot
+// kc ^ swz_k(r), so 8 (or 16) consecutive rows reading the same kc land in
+// distinct 16-byte bank groups of a 128-byte (or 256-byte) bank period.
+__device__ __forceinline__ int swz_k(int r) { return (r & 7) ^ ((r >> 3) & 1); }
+// MN-contiguous LDS tile [64][R]: chunk j of k-row k sits at slot j ^ swz_n(k),
+// swz_n = {0, 6, 10, 12}[k & 3] (a nibble table): the 4 k-rows x 32 bytes read
+// by 16 lanes of a transpose read, and the 4 x 64 bytes read by 32 lanes, land
+// in distinct bank groups.
+__device__ __forceinline__ int swz_n(int k) { return (0xCA60u >> ((k & 3) * 4)) & 15u; }
 
-template <int R, int T, bool KCONTIG>
-struct TileLoader {
-  // K-contiguous: R*8 chunks of 16 B.  MN-contiguous: (64/4)*(R/8) blocks of
-  // 4 k-rows x 8 mn (four 16 B loads each).
-  static constexpr int kUnits = KCONTIG ? R * 8 : (kBK / 4) * (R / 8);
-  static constexpr int kPer = (kUnits + T - 1) / T;
-  static constexpr int kRegs = KCONTIG ? kPer : kPer * 4;
-  uint4 r[kRegs];
+// Raw buffer descriptor (stride 0): reads at byte offsets >= `bytes` return 0.
+__device__ __forceinline__ i32x4_t make_rsrc(const void* base, uint32_t bytes) {
+  const uint64_t b = reinterpret_cast<uint64_t>(base);
+  i32x4_t r;
+  r.x = __builtin_amdgcn_readfirstlane(static_cast<int>(b));
+  r.y = __builtin_amdgcn_readfirstlane(static_cast<int>((b >> 32) & 0xffff));
+  r.z = __builtin_amdgcn_readfirstlane(static_cast<int>(bytes));
+  r.w = 0x00020000;
+  return r;
+}
 
-  // base: operand pointer at (row0, k0) of this tile for batch bb.
-  // s_row / s_k: element strides; rows_left / k_left: valid extent from (row0,k0).
-  __device__ __forceinline__ void load(const uint16_t* base, int64_t s_row, int64_t s_k,
-                                       int64_t rows_left, int64_t k_left, int tid) {
-#pragma unroll
-    for (int i = 0; i < kPer; ++i) {
-      const int u = tid + i * T;
-      if constexpr (KCONTIG) {
-        const int row = u >> 3, kc = u & 7;
-        const bool ok = (u < kUnits) && row < rows_left && kc * 8 < k_left;
-        r[i] = ok ? *reinterpret_cast<const uint4*>(base + row * s_row + kc * 8)
-                  : make_uint4(0, 0, 0, 0);
-      } else {
-        const int rg = u % (R / 8), kg = u / (R / 8);
-        const bool rok = (u < kUnits) && rg * 8 < rows_left;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int k = kg * 4 + j;
-          const bool ok = rok && k < k_left;
-          r[i * 4 + j] = ok ? *reinterpret_cast<const uint4*>(base + k * s_k + rg * 8)
-                            : make_uint4(0, 0, 0, 0);
-        }
-      }
-    }
+// 16 bytes per lane from buffer offset voff straight into LDS at lds + lane*16.
+__device__ __forceinline__ void dma16(i32x4_t rsrc, const void* lds, uint32_t voff) {
+  const uint32_t la = static_cast<uint32_t>(reinterpret_cast<uintptr_t>((GHIP_LDS const void*)lds));
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+               ::"s"(__builtin_amdgcn_readfirstlane(la)), "v"(voff), "s"(rsrc)
+               : "memory", "m0");
+}
+
+// Wave-instruction i of a wave fills LDS bytes [blk*1024, blk*1024 + 1024),
+// blk = wave * kPerWave + i; lane l writes bytes l*16 .. l*16+15 of that block, so
+// the swizzle is applied by choosing which global chunk each lane fetches.
+template <int R, bool KC, int NW>
+struct OperandTile {
+  static constexpr int kInstr = R * kBK * 2 / 1024;
+  static constexpr int kPerWave = kInstr / NW;
+  static_assert(kInstr % NW == 0 && kPerWave % 2 == 0, "tile must split evenly over waves");
+  static constexpr int kCPR = KC ? kBK / 8 : R / 8;  // 16-byte chunks per LDS row
+  static constexpr int kRPI = 64 / kCPR;             // LDS rows per instruction
+  static_assert(KC || R >= 128, "MN-major tiles need >= 16 chunks per LDS row");
+
+  // The swizzle depends on the parity of the instruction only: byte offsets of
+  // this lane's chunk for even / odd i; instruction i adds (i & ~1) * step.
+  uint32_t voff[2];
+  uint32_t step;
+  int mn_valid;
+
+  __device__ __forceinline__ static int row_of(int wave, int i, int lane) {
+    return (wave * kPerWave + i) * kRPI + lane / kCPR;
   }
-
-  __device__ __forceinline__ void store(uint16_t* lds, int tid) const {
+  __device__ __forceinline__ static int chunk_of(int wave, int i, int lane) {
+    const int r = row_of(wave, i, lane);
+    return KC ? (lane % kCPR) ^ swz_k(r) : (lane % kCPR) ^ swz_n(r);
+  }
+  // s_mn / s_k: element strides of the operand along its rows (m or n) and k.
+  __device__ __forceinline__ void init(int wave, int lane, int64_t s_mn, int64_t s_k, int64_t valid) {
+    mn_valid = valid > R ? R : static_cast<int>(valid);
 #pragma unroll
-    for (int i = 0; i < kPer; ++i) {
-      const int u = tid + i * T;
-      if (u >= kUnits) continue;
-      if constexpr (KCONTIG) {
-        const int row = u >> 3, kc = u & 7;
-        *reinterpret_cast<uint4*>(lds + row * kBK + swz(row, kc) * 8) = r[i];
-      } else {
-        const int rg = u % (R / 8), kg = u / (R / 8);
-        const uint32_t w0[4] = {r[i * 4 + 0].x, r[i * 4 + 0].y, r[i * 4 + 0].z, r[i * 4 + 0].w};
-        const uint32_t w1[4] = {r[i * 4 + 1].x, r[i * 4 + 1].y, r[i * 4 + 1].z, r[i * 4 + 1].w};
-        const uint32_t w2[4] = {r[i * 4 + 2].x, r[i * 4 + 2].y, r[i * 4 + 2].z, r[i * 4 + 2].w};
-        const uint32_t w3[4] = {r[i * 4 + 3].x, r[i * 4 + 3].y, r[i * 4 + 3].z, r[i * 4 + 3].w};
-        const int kc = kg >> 1, half = kg & 1;
+    for (int par = 0; par < 2; ++par) {
+      const int r = row_of(wave, par, lane);
+      const int c = chunk_of(wave, par, lane);
+      voff[par] = KC ? static_cast<uint32_t>((r * s_mn + c * 8) * 2)
+                     : static_cast<uint32_t>((r * s_k + c * 8) * 2);
+    }
+    step = static_cast<uint32_t>(kRPI * (KC ? s_mn : s_k) * 2);
+  }
+  // full: the whole tile lies inside the operand; otherwise out-of-range rows and
+  // k-chunks read zeros.
+  __device__ __forceinline__ void issue(i32x4_t rs, uint16_t* lds, int wave, int lane, bool full,
+                                        int k_left) const {
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          // Column e of the 4x8 block: k = kg*4 .. kg*4+3 of row rg*8+e.
-          const int d = e >> 1;
-          uint32_t lo, hi;
-          if (e & 1) {
-            lo = (w0[d] >> 16) | (w1[d] & 0xffff0000u);
-            hi = (w2[d] >> 16) | (w3[d] & 0xffff0000u);
-          } else {
-            lo = (w0[d] & 0xffffu) | (w1[d] << 16);
-            hi = (w2[d] & 0xffffu) | (w3[d] << 16);
-          }
-          const int row = rg * 8 + e;
-          *reinterpret_cast<uint2*>(lds + row * kBK + swz(row, kc) * 8 + half * 4) =
-              make_uint2(lo, hi);
-        }
-      }
+    for (int i = 0; i < kPerWave; ++i) {
+      const uint32_t v = voff[i & 1] + static_cast<uint32_t>(i & ~1) * step;
+      const int r = row_of(wave, i, lane);
+      const int c = chunk_of(wave, i, lane);
+      const bool ok = KC ? (r < mn_valid && c * 8 < k_left) : (r < k_left && c * 8 < mn_valid);
+      dma16(rs, lds + (wave * kPerWave + i) * 512, (full || ok) ? v : kOffOOB);
     }
   }
 };
 
+// Fragment of a 32-row (A) / 32-column (B) block for k16 step s: lane l gets 8
+// consecutive k (8*(l/32) .. +8) of row/column l % 32.
+__device__ __forceinline__ bf16x8_t frag_kc(const uint16_t* lds, int rbase, int s, int lane) {
+  const int row = rbase + (lane & 31);
+  const int slot = (2 * s + (lane >> 5)) ^ swz_k(row);
+  return *reinterpret_cast<const bf16x8_t*>(lds + row * kBK + slot * 8);
+}
+// Same fragment from an MN-major tile: ds_read_b64_tr_b16 hands lane j of each
+// 16-lane group element j of the four 4-element rows its group points at, so
+// lanes address 4 k-rows x 16 columns and receive 4 consecutive k of one column.
+template <int R>
+__device__ __forceinline__ bf16x8_t frag_mn(const uint16_t* lds, int nbase, int s, int lane) {
+  const int kl = 16 * s + 8 * (lane >> 5) + ((lane & 15) >> 2);
+  const int nl = nbase + 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+  const uint16_t* p0 = lds + kl * R + (((nl >> 3) ^ swz_n(kl)) * 8) + (nl & 7);
+  const uint16_t* p1 = p0 + 4 * R;  // k + 4 keeps k & 3, hence the swizzle
+  bf16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((GHIP_LDS bf16x4_t*)(p0));
+  bf16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((GHIP_LDS bf16x4_t*)(p1));
+  return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+}
+
 template <int BM, int BN, int WM, int WN, bool A_K, bool B_K, typename OutT>
-__global__ __launch_bounds__(WM * WN * 64) void gemm_bf16_kernel(GemmParams p) {
-  constexpr int T = WM * WN * 64;
+__global__ __launch_bounds__(WM* WN * 64, 1) void gemm_bf16_kernel(GemmParams p) {
+  constexpr int NW = WM * WN;
   constexpr int TM = BM / WM, TN = BN / WN;  // wave tile
   constexpr int FM = TM / 32, FN = TN / 32;  // 32x32 MFMA blocks per wave
-  static_assert(FM >= 1 && FN >= 1, "wave tile too small");
-  __shared__ __attribute__((aligned(16))) uint16_t lds[2][(BM + BN) * kBK];
+  constexpr int NS = kBK / 16;               // k16 steps per k-tile
+  using TA = OperandTile<BM, A_K, NW>;
+  using TB = OperandTile<BN, B_K, NW>;
+  constexpr int LPW = TA::kPerWave + TB::kPerWave;  // loads per wave per k-tile
+  __shared__ __attribute__((aligned(1024))) uint16_t sa[2][BM * kBK];
+  __shared__ __attribute__((aligned(1024))) uint16_t sb[2][BN * kBK];
 
-  const int tid = threadIdx.x;
-  const int lane = tid & 63, wave = tid >> 6;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int wm = wave / WN, wn = wave % WN;
 
   int64_t bb;
   int tm, tn;
-  const int64_t total = p.batch * p.tiles_m * p.tiles_n;
-  map_tile(blockIdx.x, total, p.tiles_m, p.tiles_n, bb, tm, tn);
+  map_tile(blockIdx.x, p.batch * p.tiles_m * p.tiles_n, p.tiles_m, p.tiles_n, bb, tm, tn);
   const int64_t m0 = static_cast<int64_t>(tm) * BM, n0 = static_cast<int64_t>(tn) * BN;
+  const uint16_t* A0 = static_cast<const uint16_t*>(p.a) + bb * p.sa_b + m0 * p.sa_m;
+  const uint16_t* B0 = static_cast<const uint16_t*>(p.b) + bb * p.sb_b + n0 * p.sb_n;
+  const uint32_t a_left0 = p.a_extent - static_cast<uint32_t>(m0 * p.sa_m * 2);
+  const uint32_t b_left0 = p.b_extent - static_cast<uint32_t>(n0 * p.sb_n * 2);
 
-  const uint16_t* A = static_cast<const uint16_t*>(p.a) + bb * p.sa_b + m0 * p.sa_m;
-  const uint16_t* B = static_cast<const uint16_t*>(p.b) + bb * p.sb_b + n0 * p.sb_n;
-  const int64_t s_am = p.sa_m, s_ak = p.sa_k;
-  const int64_t rows_a = p.M - m0, rows_b = p.N - n0;
+  TA ta;
+  TB tb;
+  ta.init(wave, lane, p.sa_m, p.sa_k, p.M - m0);
+  tb.init(wave, lane, p.sb_n, p.sb_k, p.N - n0);
+  const bool mn_full = m0 + BM <= p.M && n0 + BN <= p.N;
+  const int KT = static_cast<int>((p.K + kBK - 1) / kBK);
 
-  TileLoader<BM, T, A_K> la;
-  TileLoader<BN, T, B_K> lb;
+  auto issue = [&](int kt, int st) {
+    const int64_t k0 = static_cast<int64_t>(kt) * kBK;
+    const int k_left = static_cast<int>(p.K - k0 < kBK ? p.K - k0 : kBK);
+    const bool full = mn_full && k_left == kBK;
+    ta.issue(make_rsrc(A0 + k0 * p.sa_k, a_left0 - static_cast<uint32_t>(k0 * p.sa_k * 2)), sa[st],
+             wave, lane, full, k_left);
+    tb.issue(make_rsrc(B0 + k0 * p.sb_k, b_left0 - static_cast<uint32_t>(k0 * p.sb_k * 2)), sb[st],
+             wave, lane, full, k_left);
+  };
 
   f32x16_t acc[FM][FN];
 #pragma unroll
@@ -175,70 +232,90 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_bf16_kernel(GemmParams p) {
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
 
-  const int KT = static_cast<int>((p.K + kBK - 1) / kBK);
-  la.load(A, s_am, s_ak, rows_a, p.K, tid);
-  lb.load(B, p.sb_n, p.sb_k, rows_b, p.K, tid);
-  la.store(lds[0], tid);
-  lb.store(lds[0] + BM * kBK, tid);
-  __syncthreads();
+  bf16x8_t fa[2][FM], fb[2][FN];
+  auto read = [&](int st, int s, int buf) {
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+      fa[buf][i] = A_K ? frag_kc(sa[st], wm * TM + i * 32, s, lane)
+                       : frag_mn<BM>(sa[st], wm * TM + i * 32, s, lane);
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+      fb[buf][j] = B_K ? frag_kc(sb[st], wn * TN + j * 32, s, lane)
+                       : frag_mn<BN>(sb[st], wn * TN + j * 32, s, lane);
+  };
+  auto mfma = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+      for (int j = 0; j < FN; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb[buf][j], fa[buf][i], acc[i][j], 0, 0, 0);
+  };
 
-  const int frow = lane & 31;  // row (A) / column (B) inside a 32-block
-  const int kgrp = lane >> 5;  // which 8-k half of a 16-k MFMA step
-
-  for (int kt = 0; kt < KT; ++kt) {
-    const int cur = kt & 1;
-    const bool more = kt + 1 < KT;
-    if (more) {
-      const int64_t k0 = static_cast<int64_t>(kt + 1) * kBK;
-      la.load(A + k0 * s_ak, s_am, s_ak, rows_a, p.K - k0, tid);
-      lb.load(B + k0 * p.sb_k, p.sb_n, p.sb_k, rows_b, p.K - k0, tid);
-    }
-    const uint16_t* As = lds[cur];
-    const uint16_t* Bs = lds[cur] + BM * kBK;
-#pragma unroll
-    for (int s = 0; s < kBK / 16; ++s) {
-      const int kc = s * 2 + kgrp;
-      bf16x8_t af[FM], bfr[FN];
-#pragma unroll
-      for (int i = 0; i < FM; ++i) {
-        const int row = wm * TM + i * 32 + frow;
-        uint4 v = *reinterpret_cast<const uint4*>(As + row * kBK + swz(row, kc) * 8);
-        af[i] = __builtin_bit_cast(bf16x8_t, v);
-      }
-#pragma unroll
-      for (int j = 0; j < FN; ++j) {
-        const int row = wn * TN + j * 32 + frow;
-        uint4 v = *reinterpret_cast<const uint4*>(Bs + row * kBK + swz(row, kc) * 8);
-        bfr[j] = __builtin_bit_cast(bf16x8_t, v);
-      }
-#pragma unroll
-      for (int i = 0; i < FM; ++i)
-#pragma unroll
-        for (int j = 0; j < FN; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bfr[j], acc[i][j], 0, 0, 0);
-    }
-    if (more) {
-      la.store(lds[cur ^ 1], tid);
-      lb.store(lds[cur ^ 1] + BM * kBK, tid);
-    }
-    __syncthreads();
+  // Prologue: tiles 0 and 1 in flight, wait for tile 0.
+  issue(0, 0);
+  if (KT > 1) {
+    issue(1, 1);
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(LPW) : "memory");
+  } else {
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   }
+  __syncthreads();
+  read(0, 0, 0);
 
-  // Epilogue: acc[i][j][v] is C[row, col] with col = lane % 32 and
-  // row = (v / 4) * 8 + (lane / 32) * 4 + v % 4 inside the 32x32 block.
+  // Tile kt lives in stage kt & 1.  At its last k16 step: wait for tile kt+1,
+  // barrier (everyone has finished reading stage kt & 1), refill that stage with
+  // tile kt+2, fetch step 0 of tile kt+1, then run the last MFMAs of tile kt.
+  auto tile = [&](int kt, int st) {
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+      const int buf = s & 1;
+      if (s + 1 < NS) {
+        read(st, s + 1, buf ^ 1);
+      } else {
+        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+        if (kt + 2 < KT) issue(kt + 2, st);
+        if (kt + 1 < KT) read(st ^ 1, 0, buf ^ 1);
+      }
+      mfma(buf);
+    }
+  };
+  for (int kt = 0; kt < KT; kt += 2) {
+    tile(kt, 0);
+    if (kt + 1 < KT) tile(kt + 1, 1);
+  }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+
+  // acc[i][j] holds the transposed 32x32 block: lane l, value v ->
+  // row m = l % 32, columns n = (v / 4) * 8 + (l / 32) * 4 + v % 4.
   OutT* C = static_cast<OutT*>(p.c) + bb * p.sc_b;
 #pragma unroll
-  for (int i = 0; i < FM; ++i)
+  for (int i = 0; i < FM; ++i) {
+    const int64_t m = m0 + wm * TM + i * 32 + (lane & 31);
+    if (m >= p.M) continue;
 #pragma unroll
     for (int j = 0; j < FN; ++j) {
-      const int64_t col = n0 + wn * TN + j * 32 + frow;
-      if (col >= p.N) continue;
 #pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        const int64_t row = m0 + wm * TM + i * 32 + (v >> 2) * 8 + kgrp * 4 + (v & 3);
-        if (row < p.M) store_out<OutT>(C + row * p.sc_m + col, acc[i][j][v]);
+      for (int q = 0; q < 4; ++q) {
+        const int64_t n = n0 + wn * TN + j * 32 + q * 8 + (lane >> 5) * 4;
+        OutT* dst = C + m * p.sc_m + n;
+        if (p.vec_c && n + 3 < p.N) {
+          if constexpr (sizeof(OutT) == 2) {
+            *reinterpret_cast<uint2*>(dst) =
+                make_uint2(pack_bf16x2(acc[i][j][q * 4 + 0], acc[i][j][q * 4 + 1]),
+                           pack_bf16x2(acc[i][j][q * 4 + 2], acc[i][j][q * 4 + 3]));
+          } else {
+            *reinterpret_cast<float4*>(dst) = make_float4(acc[i][j][q * 4 + 0], acc[i][j][q * 4 + 1],
+                                                          acc[i][j][q * 4 + 2], acc[i][j][q * 4 + 3]);
+          }
+        } else {
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            if (n + e < p.N) store_out<OutT>(dst + e, acc[i][j][q * 4 + e]);
+        }
       }
     }
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -448,15 +525,28 @@ static int majorness(const void* base, int64_t s_b, int64_t s_mn, int64_t s_k, i
   return -1;
 }
 
+// Bytes spanned by one batch slice of an operand with non-negative strides.
+static int64_t slice_bytes(int64_t rows, int64_t s_row, int64_t K, int64_t s_k, int64_t es) {
+  return ((rows - 1) * s_row + (K - 1) * s_k + 1) * es;
+}
+
 template <typename OutT>
 static hipError_t dispatch_bf16(GemmParams p, hipStream_t s) {
   const int ma = majorness(p.a, p.sa_b, p.sa_m, p.sa_k, p.M, p.K, 8, p.batch);
   const int mb = majorness(p.b, p.sb_b, p.sb_n, p.sb_k, p.N, p.K, 8, p.batch);
-  if (ma < 0 || mb < 0) return launch_generic<bf16_t, OutT>(p, s);
+  const bool nonneg = p.sa_b >= 0 && p.sa_m >= 0 && p.sa_k >= 0 && p.sb_b >= 0 && p.sb_k >= 0 &&
+                      p.sb_n >= 0;
+  const int64_t ea = slice_bytes(p.M, p.sa_m, p.K, p.sa_k, 2);
+  const int64_t eb = slice_bytes(p.N, p.sb_n, p.K, p.sb_k, 2);
+  if (ma < 0 || mb < 0 || !nonneg || ea >= (int64_t{1} << 31) || eb >= (int64_t{1} << 31))
+    return launch_generic<bf16_t, OutT>(p, s);
+  p.a_extent = static_cast<uint32_t>(ea);
+  p.b_extent = static_cast<uint32_t>(eb);
+  p.vec_c = (p.sc_m % 4 == 0) && (p.sc_b % 4 == 0 || p.batch == 1) &&
+            (reinterpret_cast<uintptr_t>(p.c) % (4 * sizeof(OutT)) == 0);
   const int64_t t256 = p.batch * ((p.M + 255) / 256) * ((p.N + 255) / 256);
-  const int64_t t256x128 = p.batch * ((p.M + 255) / 256) * ((p.N + 127) / 128);
-  if (p.M >= 256 && p.N >= 256 && t256 >= 256) return launch_bf16<256, 256, 2, 4, OutT>(p, ma, mb, s);
-  if (p.M >= 256 && t256x128 >= 256) return launch_bf16<256, 128, 4, 2, OutT>(p, ma, mb, s);
+  if (p.M >= 256 && p.N >= 256 && t256 >= 128) return launch_bf16<256, 256, 2, 4, OutT>(p, ma, mb, s);
+  if (p.M >= 256 && p.N >= 128) return launch_bf16<256, 128, 2, 2, OutT>(p, ma, mb, s);
   return launch_bf16<128, 128, 2, 2, OutT>(p, ma, mb, s);
 }
 
