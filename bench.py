@@ -13,6 +13,10 @@ on both sides (wall clock -> ms_per_step), and HIP events recorded on the stream
 the kernels run on (-> average launch duration for "roofline").  Working sets
 below 1 GiB rotate through several input/output buffer sets so the 256 MB
 Infinity Cache cannot serve repeat reads (the rotation count is reported).
+HBM-bound cases launch their steps from a captured HIP graph (one graph holds a
+whole rotation cycle and is replayed), so microsecond kernels run back to back
+instead of waiting on the Python launch path; the graph is built, replayed once
+and checked against an eager launch before timing.
 """
 from __future__ import annotations
 
@@ -39,32 +43,75 @@ def parse():
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--no-secondary", action="store_true")
     p.add_argument("--only", default="", help="comma list of secondary case names")
+    p.add_argument("--eager", action="store_true",
+                   help="launch every step from Python (no HIP graph); for counter collection")
+    p.add_argument("--copy-ref", type=int, default=0, metavar="MIB",
+                   help="only run a plain device copy of MIB MiB (read + write) `steps` times: "
+                        "the reference kernel that scales FETCH_SIZE / WRITE_SIZE to bytes")
     return p.parse_args()
 
 
 class Case:
-    """One workload: `launch(i)` runs step i on the current stream."""
+    """One workload: `launch(i)` runs step i on the current stream; `out(i)` is the
+    tensor step i writes (used to check a graph replay against eager launches)."""
 
     def __init__(self, name, launch, bytes_per_step=0, flops_per_step=0, bound="hbm",
-                 peak=HBM_PEAK_GBS, dtype="f32", rotation=1, config=None, kernel=""):
+                 peak=HBM_PEAK_GBS, dtype="f32", rotation=1, config=None, kernel="",
+                 out=None):
         self.name, self.launch = name, launch
         self.bytes, self.flops = bytes_per_step, flops_per_step
         self.bound, self.peak, self.dtype = bound, peak, dtype
         self.rotation, self.config, self.kernel = rotation, config or {}, kernel
+        self.out = out
 
 
-def time_case(case: Case, steps: int, warmup: int):
+def graph_runner(case: Case, steps: int):
+    """Captures one rotation cycle of launches (at least 16) into a HIP graph.
+    Returns (replay, launches_per_replay) or None when the case has no output to
+    check.  The first replay is compared bit for bit with eager launches."""
+    import torch
+    if case.out is None:
+        return None
+    per = case.rotation * max(1, -(-16 // case.rotation))
+    for i in range(per):
+        case.launch(i)
+    torch.cuda.synchronize()
+    eager = [case.out(i).clone() for i in range(case.rotation)]
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for i in range(per):
+            case.launch(i)
+    for i in range(case.rotation):
+        case.out(i).zero_()
+    g.replay()
+    torch.cuda.synchronize()
+    for i in range(case.rotation):
+        if not torch.equal(case.out(i), eager[i]):
+            raise RuntimeError(f"{case.name}: graph replay differs from eager launches")
+    return g.replay, per
+
+
+def time_case(case: Case, steps: int, warmup: int, eager: bool = False):
     import torch
     stream = torch.cuda.current_stream()
-    for i in range(warmup):
-        case.launch(i)
+    runner = graph_runner(case, steps) if case.bound == "hbm" and not eager else None
+    if runner is not None:
+        replay, per = runner
+        reps = max(1, -(-steps // per))
+        steps = reps * per
+        work = lambda: [replay() for _ in range(reps)]  # noqa: E731
+        for _ in range(max(1, warmup // per)):
+            replay()
+    else:
+        work = lambda: [case.launch(i) for i in range(steps)]  # noqa: E731
+        for i in range(warmup):
+            case.launch(i)
     torch.cuda.synchronize()
     ev0 = torch.cuda.Event(enable_timing=True)
     ev1 = torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()
     ev0.record(stream)
-    for i in range(steps):
-        case.launch(i)
+    work()
     ev1.record(stream)
     torch.cuda.synchronize()
     wall_ms = (time.perf_counter() - t0) * 1e3
@@ -77,12 +124,27 @@ def time_case(case: Case, steps: int, warmup: int):
         achieved = case.flops / per_launch_s / 1e12
         unit = "TFLOP/s"
     return {
+        "steps": steps,
+        "graph": runner is not None,
         "wall_ms": wall_ms,
         "ms_per_step": wall_ms / steps,
         "launch_us": per_launch_s * 1e6,
         "roofline": {"bound": case.bound, "achieved": round(achieved, 2), "peak": case.peak,
                      "unit": unit, "frac": round(achieved / case.peak, 4), "traffic": None},
     }
+
+
+def measured_traffic(kernel_key):
+    """HBM bytes per launch of a kernel from the committed counter summary
+    (profiles/traffic.json: FETCH_SIZE / WRITE_SIZE scaled by a copy of known
+    size), or None when that kernel has not been measured."""
+    path = os.path.join(ROOT, "profiles", "traffic.json")
+    try:
+        with open(path) as f:
+            entry = json.load(f).get(kernel_key)
+    except (OSError, ValueError):
+        return None
+    return None if entry is None else entry["traffic_bytes"]
 
 
 def rotation_for(nbytes):
@@ -107,6 +169,7 @@ def make_cases(only=None):
         gam = (torch.rand((n,), device=dev, generator=g) + 0.5).to(dtype)
         return Case(f"rmsnorm_{tag}", lambda i: ops.rmsnorm(xs[i % rot], gam, 1e-6, out=ys[i % rot]),
                     bytes_per_step=nbytes, dtype=tag, rotation=rot, kernel="rows_reg_kernel",
+                    out=lambda i: ys[i % rot],
                     config={"workload": f"RMSNorm last axis, x [8192,4096] {tag}, gamma [4096], eps 1e-6, fp32 statistics"})
 
     def ln_case(dtype, tag):
@@ -121,6 +184,7 @@ def make_cases(only=None):
         return Case(f"layernorm_{tag}",
                     lambda i: ops.layernorm(xs[i % rot], gam, bet, 1e-5, out=ys[i % rot]),
                     bytes_per_step=nbytes, dtype=tag, rotation=rot, kernel="rows_reg_kernel",
+                    out=lambda i: ys[i % rot],
                     config={"workload": f"LayerNorm last axis, x [8192,4096] {tag}, eps 1e-5"})
 
     def softmax_case():
@@ -131,6 +195,7 @@ def make_cases(only=None):
         ys = [torch.empty_like(xs[0]) for _ in range(rot)]
         return Case("softmax_f32", lambda i: ops.softmax(xs[i % rot], out=ys[i % rot]),
                     bytes_per_step=nbytes, dtype="f32", rotation=rot, kernel="rows_reg_kernel",
+                    out=lambda i: ys[i % rot],
                     config={"workload": "Softmax last axis, x [4096,1024] fp32 ~ N(0, 2^2)"})
 
     def dot_case(dtype, tag, peak):
@@ -203,6 +268,20 @@ def cpu_baseline(seconds_target=10.0):
                       f"x [8192,4096] fp32, {reps} repetitions in {dt:.1f} s"}
 
 
+def copy_reference(mib: int, steps: int):
+    """A plain device-to-device copy of `mib` MiB, `steps` times: its FETCH_SIZE /
+    WRITE_SIZE counters per dispatch, divided by mib * 1024, give the factor that
+    turns those counters into bytes for the kernels measured beside it."""
+    import torch
+    n = mib * (1 << 20) // 4
+    x = torch.ones(n, device="cuda", dtype=torch.float32)
+    y = torch.empty_like(x)
+    for _ in range(steps):
+        y.copy_(x)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_ref_mib": mib, "steps": steps}))
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -217,15 +296,19 @@ def main():
     _lib.load()
 
     only = set(filter(None, args.only.split(",")))
+    if args.copy_ref:
+        copy_reference(args.copy_ref, args.steps)
+        return
     primary, builders, names = make_cases(only)
-    res = time_case(primary, args.steps, args.warmup)
+    res = time_case(primary, args.steps, args.warmup, args.eager)
     secondary = []
     if not args.no_secondary:
         for name in names:
             case = builders[name]()
             steps = args.steps if case.bound == "hbm" else max(5, args.steps // 20)
-            r = time_case(case, steps, max(2, args.warmup // 2))
-            secondary.append({"name": name, "dtype": case.dtype, "steps": steps,
+            r = time_case(case, steps, max(2, args.warmup // 2), args.eager)
+            secondary.append({"name": name, "dtype": case.dtype, "steps": r["steps"],
+                              "graph": r["graph"],
                               "launch_us": round(r["launch_us"], 2),
                               "value": r["roofline"]["achieved"], "unit": r["roofline"]["unit"],
                               "roofline": r["roofline"], "rotation": case.rotation,
@@ -233,13 +316,13 @@ def main():
             del case
             torch.cuda.empty_cache()
     cpu = None if args.no_cpu else cpu_baseline()
-    gbs = primary.bytes * args.steps / (res["wall_ms"] / 1e3) / 1e9
+    gbs = primary.bytes * res["steps"] / (res["wall_ms"] / 1e3) / 1e9
     line = {
         "metric": "softmax/RMSNorm GB/s (% HBM peak); bf16 DotGeneral TFLOP/s (% MFMA peak)",
         "value": round(gbs, 2),
         "unit": "GB/s",
         "n_gpus": 1,
-        "steps": args.steps,
+        "steps": res["steps"],
         "warmup": args.warmup,
         "ms_per_step": round(res["ms_per_step"], 5),
         "higher_is_better": True,
@@ -247,9 +330,9 @@ def main():
         "vs_baseline": None,
         "dtype": "f32",
         "data": "synthetic (torch.randn on device; inputs resident in HBM)",
-        "config": dict(primary.config, rotation=primary.rotation,
+        "config": dict(primary.config, rotation=primary.rotation, graph=res["graph"],
                        kernel=primary.kernel, launch_us=round(res["launch_us"], 2)),
-        "roofline": res["roofline"],
+        "roofline": dict(res["roofline"], traffic=measured_traffic("rows_reg_kernel<float, 2, 4, 4>")),
         "cpu_baseline": cpu,
         "secondary": secondary,
     }
