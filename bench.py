@@ -209,23 +209,18 @@ def make_cases(only=None):
                     config={"workload": f"DotGeneral [8,2048,4096]x[8,4096,4096] lc=[2] lb=[0] rc=[1] rb=[0], {tag} in, fp32 accumulate, {tag} out"})
 
     def attention_case():
-        Bh, S, D = 64, 2048, 128
-        q = torch.randn((Bh, S, D), device=dev, generator=g).to(torch.bfloat16)
-        k = torch.randn((Bh, S, D), device=dev, generator=g).to(torch.bfloat16)
-        v = torch.randn((Bh, S, D), device=dev, generator=g).to(torch.bfloat16)
-        s = torch.empty((Bh, S, S), device=dev, dtype=torch.bfloat16)
-        p = torch.empty_like(s)
-        o = torch.empty((Bh, S, D), device=dev, dtype=torch.bfloat16)
-        kt = k.transpose(1, 2)
-
-        def launch(i):
-            ops.gemm(q, kt, out=s)
-            ops.scale_mask_softmax(s, 1.0 / 128 ** 0.5, True, out=p)
-            ops.gemm(p, v, out=o)
-        return Case("attention_bf16", launch, flops_per_step=2 * 2 * Bh * S * S * D, bound="mfma",
-                    peak=BF16_PEAK_TFLOPS, dtype="bf16",
-                    kernel="gemm_bf16_kernel + rows_reg_kernel",
-                    config={"workload": "SDPA causal B4 H16 S2048 D128 bf16: DotGeneral -> fused scale+causal+softmax -> DotGeneral (flops: both GEMMs, full)"})
+        B, H, S, D = 4, 16, 2048, 128
+        q = torch.randn((B, H, S, D), device=dev, generator=g).to(torch.bfloat16)
+        k = torch.randn((B, H, S, D), device=dev, generator=g).to(torch.bfloat16)
+        v = torch.randn((B, H, S, D), device=dev, generator=g).to(torch.bfloat16)
+        o = torch.empty_like(q)
+        return Case("attention_bf16", lambda i: ops.sdpa(q, k, v, D ** -0.5, True, out=o),
+                    flops_per_step=2 * 2 * B * H * S * S * D, bound="mfma",
+                    peak=BF16_PEAK_TFLOPS, dtype="bf16", kernel="sdpa_fwd_kernel",
+                    config={"workload": "SDPA causal B4 H16 S2048 D128 bf16, one fused kernel "
+                                        "(Q.K^T, scale, causal mask, online softmax, P.V); flops "
+                                        "counted for both products over the full S x S matrix, "
+                                        "the causal half above the diagonal is skipped"})
 
     builders = {
         "softmax_f32": softmax_case,

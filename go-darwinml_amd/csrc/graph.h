@@ -196,6 +196,10 @@ int launch_reduce(int dtype, int op, const void* src, const ReduceDesc& d, void*
 // Gather rows with int32 or int64 ids (clamped).
 int launch_gather_rows(const void* table, int64_t V, int64_t row_bytes, const void* ids,
                        int id_dtype, int64_t n, void* out, hipStream_t s, GHipError* err);
+// Whether the fused attention kernel (ghip_sdpa_fwd) takes these operands; strides
+// in elements ordered (batch, head, sequence), head dim contiguous.
+bool sdpa_fused_supported(int dtype, int64_t H, int64_t Hkv, int64_t Sq, int64_t Sk, int64_t D,
+                          const int64_t* qs, const int64_t* ks, const int64_t* vs, const int64_t* os);
 
 }  // namespace ghip
 

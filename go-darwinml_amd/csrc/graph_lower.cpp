@@ -25,6 +25,7 @@
 #include <string.h>
 
 #include <algorithm>
+#include <array>
 #include <set>
 #include <sstream>
 
@@ -833,6 +834,37 @@ struct Lowerer {
     View q = as_bhsd(qv_, &qs), k = as_bhsd(kv_, &ks), vw = as_bhsd(vv_, &vs);
     if (failed) return bad();
     const int64_t B = qs.dims[0], Sq = qs.dims[2], D = qs.dims[3], Sk = ks.dims[2], Dv = vs.dims[3];
+    // One fused kernel when there is no mask operand and the operands fit it: Q, K,
+    // V are read through their views (BHSD or BSHD, GQA heads shared in place) and
+    // the output is written in the layout the graph expects.
+    if (mv_ < 0 && D == Dv && q.strides[3] == 1 && k.strides[3] == 1 && vw.strides[3] == 1) {
+      Shape os;
+      os.dtype = dt;
+      os.dims = {B, H, Sq, Dv};
+      // Output slot in the caller's layout; o_view is its BHSD view.
+      Shape os_layout = bshd ? permute_shape(os, to_bhsd) : os;
+      View out_l = fresh(os_layout);
+      View ov = bshd ? permute(out_l, to_bhsd) : out_l;
+      const int64_t qst[3] = {q.strides[0], q.strides[1], q.strides[2]};
+      const int64_t kst[3] = {k.strides[0], k.strides[1], k.strides[2]};
+      const int64_t vst[3] = {vw.strides[0], vw.strides[1], vw.strides[2]};
+      const int64_t ost[3] = {ov.strides[0], ov.strides[1], ov.strides[2]};
+      const bool al = q.offset % 8 == 0 && k.offset % 8 == 0 && vw.offset % 8 == 0 && ov.offset % 4 == 0;
+      if (al && sdpa_fused_supported(dt, H, Hkv, Sq, Sk, D, qst, kst, vst, ost)) {
+        const float scale = static_cast<float>(n.f0);
+        std::array<int64_t, 3> aq{qst[0], qst[1], qst[2]}, ak{kst[0], kst[1], kst[2]},
+            av{vst[0], vst[1], vst[2]}, ao{ost[0], ost[1], ost[2]};
+        add_step(fmt("sdpa_fwd %s B=%lld H=%lld Hkv=%d Sq=%lld Sk=%lld D=%lld causal=%d (fused attention)",
+                     dtype_name(dt), (long long)B, (long long)H, Hkv, (long long)Sq, (long long)Sk, (long long)D,
+                     causal ? 1 : 0),
+                 {q.slot, k.slot, vw.slot}, {ov.slot}, [=](ExecState& st, GHipError* e) {
+                   return ghip_sdpa_fwd(dt, st.ptr(q, dt), st.ptr(k, dt), st.ptr(vw, dt), st.ptr(ov, dt), B, H, Hkv,
+                                        Sq, Sk, D, aq.data(), ak.data(), av.data(), ao.data(), scale, causal ? 1 : 0,
+                                        st.stream, e);
+                 });
+        return out_l;
+      }
+    }
     // GQA: repeat each KV head H/Hkv times (function.go:2731-2744) as a broadcast view.
     auto repeat = [&](View w, Shape s) {
       if (Hkv == H) return std::make_pair(w, s);

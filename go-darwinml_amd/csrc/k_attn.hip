@@ -1,0 +1,331 @@
+// Fused scaled-dot-product attention (forward), the single-kernel lowering of
+// Function.FusedScaledDotProductAttention (mpsgraph/gomlx/function.go:2669-2907):
+//   out = softmax(scale * Q K^T  [causal: -inf where key > query]) V
+// for bf16 Q/K/V/O with head dim 128, fp32 softmax statistics and accumulation.
+// GQA reads KV head h / (H / Hkv) directly (function.go:2911-2956 repeats it).
+//
+// Never materialises the [B, H, Sq, Sk] scores (the composite path writes and
+// re-reads them: 1 GiB of bf16 traffic at B4 H16 S2048).  Per workgroup: 128
+// queries (4 waves x 32); K and V stream through LDS in 64-key tiles:
+//   * everything is computed transposed: S^T = K Q^T and O^T = V^T P^T with
+//     v_mfma_f32_32x32x16_bf16, so each lane owns one query column -- its running
+//     max, running sum and output rescale stay in the lane (one cross-half-wave
+//     exchange per tile for the max);
+//   * Q stays in registers for the whole kernel (B operand of S^T);
+//   * the softmaxed S^T accumulators become the bf16 B operand of the second MFMA
+//     without leaving registers: the 16 values a lane holds for key step s are
+//     keys 16s + {0..3, 8..11} + 4 * (lane / 32), and V^T is read in that same key
+//     order with two ds_read_b64_tr_b16 per fragment;
+//   * K / V tiles arrive by buffer_load ... lds (16 B per lane, out-of-range keys
+//     read zeros) into two LDS stages, XOR-swizzled so the ds_read_b128 (K) and
+//     transpose reads (V) are bank-conflict free;
+//   * causal: tiles past a workgroup's last query are never loaded, a wave skips
+//     the tiles past its own last query, and only diagonal tiles apply the
+//     element mask; query blocks run longest-first.
+#include "common.h"
+
+#define GHIP_ALDS __attribute__((address_space(3)))
+
+namespace ghip {
+namespace attn {
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+typedef int i32x4_t __attribute__((ext_vector_type(4)));
+
+struct Params {
+  const void* q;
+  const void* k;
+  const void* v;
+  void* o;
+  int64_t q_sb, q_sh, q_ss;  // element strides of batch, head, sequence (d stride 1)
+  int64_t k_sb, k_sh, k_ss;
+  int64_t v_sb, v_sh, v_ss;
+  int64_t o_sb, o_sh, o_ss;
+  int B, H, Hkv, Sq, Sk;
+  float scale_log2;             // softmax scale * log2(e)
+  int causal;
+  uint32_t k_extent, v_extent;  // bytes addressable from one (batch, kv head) slice
+};
+
+constexpr int kD = 128;     // head dim
+constexpr int kBKV = 64;    // keys per tile
+constexpr int kQW = 32;     // queries per wave
+constexpr int kWaves = 4;   // waves per workgroup
+constexpr int kBQ = kQW * kWaves;
+constexpr uint32_t kOffOOB = 0x80000000u;
+
+__device__ __forceinline__ i32x4_t make_rsrc(const void* base, uint32_t bytes) {
+  const uint64_t b = reinterpret_cast<uint64_t>(base);
+  i32x4_t r;
+  r.x = __builtin_amdgcn_readfirstlane(static_cast<int>(b));
+  r.y = __builtin_amdgcn_readfirstlane(static_cast<int>((b >> 32) & 0xffff));
+  r.z = __builtin_amdgcn_readfirstlane(static_cast<int>(bytes));
+  r.w = 0x00020000;
+  return r;
+}
+// 16 bytes per lane from buffer offset voff straight into LDS at lds + lane*16.
+__device__ __forceinline__ void dma16(i32x4_t rsrc, const void* lds, uint32_t voff) {
+  const uint32_t la = static_cast<uint32_t>(reinterpret_cast<uintptr_t>((GHIP_ALDS const void*)lds));
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+               ::"s"(__builtin_amdgcn_readfirstlane(la)), "v"(voff), "s"(rsrc)
+               : "memory", "m0");
+}
+
+// LDS tiles are [64 keys][128 d] bf16: 256-byte rows of 16 chunks of 16 B.
+// K: chunk kc of key row r sits at slot kc ^ (r & 15), so the 16 (8) rows of a
+// ds_read_b128 phase land in distinct bank groups.
+__device__ __forceinline__ int swz_k(int r) { return r & 15; }
+// V: chunk j of key row r sits at slot j ^ {0, 6, 10, 12}[r & 3] (a transpose read
+// touches 4 consecutive rows x 2-4 chunks).
+__device__ __forceinline__ int swz_v(int r) { return (0xCA60u >> ((r & 3) * 4)) & 15u; }
+
+// One 16 KiB tile = 16 wave-instructions of 1 KiB (4 key rows each), 4 per wave.
+// Lane l of instruction blk fills bytes l*16.. of LDS block blk, so the swizzle is
+// applied by choosing the global chunk it fetches.
+template <bool IS_V>
+__device__ __forceinline__ void load_tile(i32x4_t rs, uint16_t* lds, int wave, int lane,
+                                          int keys_left, int64_t s_ss) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int blk = wave * 4 + i;
+    const int r = blk * 4 + lane / 16;
+    const int c = lane % 16;
+    const int chunk = IS_V ? (c ^ swz_v(r)) : (c ^ swz_k(r));
+    const uint32_t off = static_cast<uint32_t>((static_cast<int64_t>(r) * s_ss + chunk * 8) * 2);
+    dma16(rs, lds + blk * 512, r < keys_left ? off : kOffOOB);
+  }
+}
+
+// K fragment (A operand of S^T = K Q^T): key row kb*32 + lane%32, d = 16s + 8*(lane/32).
+__device__ __forceinline__ bf16x8_t frag_k(const uint16_t* lds, int kb, int s, int lane) {
+  const int row = kb * 32 + (lane & 31);
+  const int slot = (2 * s + (lane >> 5)) ^ swz_k(row);
+  return *reinterpret_cast<const bf16x8_t*>(lds + row * kD + slot * 8);
+}
+// V^T fragment (A operand of O^T = V^T P^T), d block db, key step s: lane
+// (d = 32 db + lane%32, h = lane/32) gets keys 16s + 4h + {0..3} and
+// 16s + 8 + 4h + {0..3}.  ds_read_b64_tr_b16 hands lane j of each 16-lane group
+// element j of the four 4-element rows the group points at.
+__device__ __forceinline__ bf16x8_t frag_v(const uint16_t* lds, int db, int s, int lane) {
+  const int kl = 16 * s + 4 * (lane >> 5) + ((lane & 15) >> 2);
+  const int nl = db * 32 + 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+  const uint16_t* p0 = lds + kl * kD + (((nl >> 3) ^ swz_v(kl)) * 8) + (nl & 7);
+  const uint16_t* p1 = p0 + 8 * kD;  // key + 8 keeps key & 3, hence the swizzle
+  bf16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((GHIP_ALDS bf16x4_t*)(p0));
+  bf16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((GHIP_ALDS bf16x4_t*)(p1));
+  return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+}
+
+__global__ __launch_bounds__(256, 2) void sdpa_fwd_kernel(Params p) {
+  __shared__ __attribute__((aligned(1024))) uint16_t sk[2][kBKV * kD];
+  __shared__ __attribute__((aligned(1024))) uint16_t sv[2][kBKV * kD];
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int h2 = lane >> 5;  // half of the wave
+  const int nqb = (p.Sq + kBQ - 1) / kBQ;
+  const int qb = p.causal ? (nqb - 1 - static_cast<int>(blockIdx.x % nqb))
+                          : static_cast<int>(blockIdx.x % nqb);
+  const int bh = blockIdx.x / nqb;
+  const int b = bh / p.H, h = bh % p.H;
+  const int hk = h / (p.H / p.Hkv);
+  const int q0 = qb * kBQ;
+  const int qw = q0 + wave * kQW;    // first query of this wave
+  const int qi = qw + (lane & 31);   // this lane's query
+
+  const uint16_t* Q = static_cast<const uint16_t*>(p.q) + b * p.q_sb + h * p.q_sh;
+  const uint16_t* Kb = static_cast<const uint16_t*>(p.k) + b * p.k_sb + hk * p.k_sh;
+  const uint16_t* Vb = static_cast<const uint16_t*>(p.v) + b * p.v_sb + hk * p.v_sh;
+
+  // Q fragments (B operand of S^T): query qi, d = 16s + 8*h2 .. +8.
+  bf16x8_t qf[kD / 16];
+#pragma unroll
+  for (int s = 0; s < kD / 16; ++s) {
+    if (qi < p.Sq)
+      qf[s] = *reinterpret_cast<const bf16x8_t*>(Q + static_cast<int64_t>(qi) * p.q_ss + 16 * s + 8 * h2);
+    else
+      qf[s] = bf16x8_t{};
+  }
+
+  const int kv_end = p.causal ? min(p.Sk, q0 + kBQ) : p.Sk;
+  const int ntiles = (kv_end + kBKV - 1) / kBKV;
+
+  auto issue = [&](int t, int st) {
+    const int64_t key0 = static_cast<int64_t>(t) * kBKV;
+    const int left = static_cast<int>(p.Sk - key0);
+    const uint32_t dk = static_cast<uint32_t>(key0 * p.k_ss * 2);
+    const uint32_t dv = static_cast<uint32_t>(key0 * p.v_ss * 2);
+    load_tile<false>(make_rsrc(Kb + key0 * p.k_ss, p.k_extent - dk), sk[st], wave, lane, left, p.k_ss);
+    load_tile<true>(make_rsrc(Vb + key0 * p.v_ss, p.v_extent - dv), sv[st], wave, lane, left, p.v_ss);
+  };
+
+  f32x16_t o[kD / 32];
+#pragma unroll
+  for (int db = 0; db < kD / 32; ++db)
+#pragma unroll
+    for (int v = 0; v < 16; ++v) o[db][v] = 0.f;
+  float m = -INFINITY;  // running max (log2 units) of query qi
+  float l = 0.f;        // running sum over this half-wave's keys
+
+  if (ntiles > 0) issue(0, 0);
+  if (ntiles > 1) issue(1, 1);
+  for (int t = 0; t < ntiles; ++t) {
+    const int st = t & 1;
+    // 8 loads per wave per tile: leave tile t+1's in flight.
+    if (t + 1 < ntiles) asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+    else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    const int key0 = t * kBKV;
+    // Causal: a wave whose last query precedes the tile's first key has nothing to
+    // do here (it still takes part in the barriers and loads).
+    const bool active = !p.causal || key0 <= qw + kQW - 1;
+    if (active) {
+      f32x16_t s0, s1;
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        s0[v] = 0.f;
+        s1[v] = 0.f;
+      }
+#pragma unroll
+      for (int s = 0; s < kD / 16; ++s) {
+        s0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(frag_k(sk[st], 0, s, lane), qf[s], s0, 0, 0, 0);
+        s1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(frag_k(sk[st], 1, s, lane), qf[s], s1, 0, 0, 0);
+      }
+      // s{kb}[v] is key key0 + 32 kb + (v/4)*8 + 4 h2 + v%4 for query qi.
+      const bool need_mask = (p.causal && key0 + kBKV - 1 > qw) || key0 + kBKV > p.Sk;
+      float mx = -INFINITY;
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int kr = (v >> 2) * 8 + 4 * h2 + (v & 3);
+        float a = s0[v] * p.scale_log2, c = s1[v] * p.scale_log2;
+        if (need_mask) {
+          const int ka = key0 + kr, kc = key0 + 32 + kr;
+          if (ka >= p.Sk || (p.causal && ka > qi)) a = -INFINITY;
+          if (kc >= p.Sk || (p.causal && kc > qi)) c = -INFINITY;
+        }
+        s0[v] = a;
+        s1[v] = c;
+        mx = fmaxf(mx, fmaxf(a, c));
+      }
+      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+      const float mnew = fmaxf(m, mx);
+      // A query with nothing unmasked yet keeps m = -inf; 0 is then the base.
+      const float base = mnew == -INFINITY ? 0.f : mnew;
+      const float alpha = exp2f(m - base);
+      m = mnew;
+      float ls = 0.f;
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const float e0 = exp2f(s0[v] - base), e1 = exp2f(s1[v] - base);
+        ls += e0 + e1;
+        s0[v] = e0;
+        s1[v] = e1;
+      }
+      l = l * alpha + ls;
+#pragma unroll
+      for (int db = 0; db < kD / 32; ++db)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) o[db][v] *= alpha;
+      // P^T operand of key step s: s{s/2}[8 (s%2) .. +8] rounded to bf16.
+      bf16x8_t pb[4];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        pb[0][e] = static_cast<__bf16>(s0[e]);
+        pb[1][e] = static_cast<__bf16>(s0[8 + e]);
+        pb[2][e] = static_cast<__bf16>(s1[e]);
+        pb[3][e] = static_cast<__bf16>(s1[8 + e]);
+      }
+#pragma unroll
+      for (int s = 0; s < kBKV / 16; ++s)
+#pragma unroll
+        for (int db = 0; db < kD / 32; ++db)
+          o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(frag_v(sv[st], db, s, lane), pb[s], o[db], 0, 0, 0);
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (t + 2 < ntiles) issue(t + 2, st);
+  }
+
+  // o[db][v] is d = 32 db + (v/4)*8 + 4 h2 + v%4 of query qi.
+  const float lt = l + __shfl_xor(l, 32, 64);
+  const float inv = lt > 0.f ? 1.0f / lt : 0.f;
+  if (qi < p.Sq) {
+    uint16_t* O = static_cast<uint16_t*>(p.o) + b * p.o_sb + h * p.o_sh + static_cast<int64_t>(qi) * p.o_ss;
+#pragma unroll
+    for (int db = 0; db < kD / 32; ++db)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int d = db * 32 + g * 8 + 4 * h2;
+        *reinterpret_cast<uint2*>(O + d) =
+            make_uint2(pack_bf16x2(o[db][g * 4 + 0] * inv, o[db][g * 4 + 1] * inv),
+                       pack_bf16x2(o[db][g * 4 + 2] * inv, o[db][g * 4 + 3] * inv));
+      }
+  }
+}
+
+}  // namespace attn
+
+// Whether ghip_sdpa_fwd takes these operands (checked again, with the pointers,
+// by the entry point).  Strides are in elements, ordered (batch, head, sequence);
+// the head dim must be contiguous.
+bool sdpa_fused_supported(int dtype, int64_t H, int64_t Hkv, int64_t Sq, int64_t Sk, int64_t D,
+                          const int64_t* qs, const int64_t* ks, const int64_t* vs, const int64_t* os) {
+  if (dtype != GHIP_DTYPE_BFLOAT16 || D != attn::kD || Hkv <= 0 || H % Hkv != 0) return false;
+  if (Sq <= 0 || Sk <= 0 || Sq > (int64_t{1} << 30) || Sk > (int64_t{1} << 30)) return false;
+  for (const int64_t* s : {qs, ks, vs})
+    for (int i = 0; i < 3; ++i)
+      if (s[i] < 0 || s[i] % 8 != 0) return false;
+  for (int i = 0; i < 3; ++i)
+    if (os[i] < 0 || os[i] % 4 != 0) return false;
+  // One (batch, kv head) slice of K / V must fit the 2 GiB buffer-offset range.
+  if (((Sk - 1) * ks[2] + D) * 2 >= (int64_t{1} << 31)) return false;
+  if (((Sk - 1) * vs[2] + D) * 2 >= (int64_t{1} << 31)) return false;
+  return true;
+}
+
+}  // namespace ghip
+
+using namespace ghip;
+
+extern "C" int ghip_sdpa_fwd(int dtype, const void* q, const void* k, const void* v, void* o,
+                             int64_t B, int64_t H, int64_t Hkv, int64_t Sq, int64_t Sk, int64_t D,
+                             const int64_t* q_strides, const int64_t* k_strides,
+                             const int64_t* v_strides, const int64_t* o_strides, float scale,
+                             int causal, void* stream, GHipError* err) {
+  if (B < 0 || H <= 0 || Hkv <= 0 || Sq < 0 || Sk < 0 || D <= 0)
+    return set_error(err, GHIP_ERR_INVALID_ARG, "sdpa_fwd: bad sizes");
+  if (H % Hkv != 0)
+    return set_error(err, GHIP_ERR_INVALID_ARG, "sdpa_fwd: num_heads (%lld) must be a multiple of num_kv_heads (%lld)",
+                     static_cast<long long>(H), static_cast<long long>(Hkv));
+  if (!q_strides || !k_strides || !v_strides || !o_strides)
+    return set_error(err, GHIP_ERR_INVALID_ARG, "sdpa_fwd: null strides");
+  if (B == 0 || Sq == 0) return GHIP_OK;
+  if (!q || !k || !v || !o) return set_error(err, GHIP_ERR_INVALID_ARG, "sdpa_fwd: null pointer");
+  if (!sdpa_fused_supported(dtype, H, Hkv, Sq, Sk, D, q_strides, k_strides, v_strides, o_strides))
+    return set_error(err, GHIP_ERR_UNSUPPORTED,
+                     "sdpa_fwd: needs bfloat16, head dim 128, non-negative strides that are multiples of 8 "
+                     "(4 for the output) and < 2 GiB per K/V head");
+  auto al = [](const void* ptr, uintptr_t a) { return (reinterpret_cast<uintptr_t>(ptr) & (a - 1)) == 0; };
+  if (!al(q, 16) || !al(k, 16) || !al(v, 16) || !al(o, 8))
+    return set_error(err, GHIP_ERR_UNSUPPORTED, "sdpa_fwd: q/k/v must be 16-byte aligned, o 8-byte aligned");
+  const int64_t nqb = (Sq + attn::kBQ - 1) / attn::kBQ;
+  if (nqb * B * H > 0x7fffffffLL) return set_error(err, GHIP_ERR_INVALID_ARG, "sdpa_fwd: problem too large");
+  attn::Params p{};
+  p.q = q; p.k = k; p.v = v; p.o = o;
+  p.q_sb = q_strides[0]; p.q_sh = q_strides[1]; p.q_ss = q_strides[2];
+  p.k_sb = k_strides[0]; p.k_sh = k_strides[1]; p.k_ss = k_strides[2];
+  p.v_sb = v_strides[0]; p.v_sh = v_strides[1]; p.v_ss = v_strides[2];
+  p.o_sb = o_strides[0]; p.o_sh = o_strides[1]; p.o_ss = o_strides[2];
+  p.B = static_cast<int>(B); p.H = static_cast<int>(H); p.Hkv = static_cast<int>(Hkv);
+  p.Sq = static_cast<int>(Sq); p.Sk = static_cast<int>(Sk);
+  p.scale_log2 = scale * 1.4426950408889634f;
+  p.causal = causal ? 1 : 0;
+  p.k_extent = static_cast<uint32_t>(((Sk - 1) * p.k_ss + D) * 2);
+  p.v_extent = static_cast<uint32_t>(((Sk - 1) * p.v_ss + D) * 2);
+  hipLaunchKernelGGL(attn::sdpa_fwd_kernel, dim3(static_cast<unsigned>(nqb * B * H)), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), p);
+  GHIP_CHECK(hipGetLastError(), err);
+  return GHIP_OK;
+}

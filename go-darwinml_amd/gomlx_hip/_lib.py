@@ -48,6 +48,9 @@ SIGNATURES = {
     "ghip_argminmax": [_int, _vp, _i64, _i64, _i64, _int, _int, _vp, _vp, _errp],
     "ghip_iota": [_int, _vp, _i64, _i64, _i64, _vp, _errp],
     "ghip_device_name": [_int, ctypes.c_char_p, ctypes.c_size_t, _errp],
+    "ghip_sdpa_fwd": [_int, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64,
+                      ctypes.POINTER(_i64), ctypes.POINTER(_i64), ctypes.POINTER(_i64),
+                      ctypes.POINTER(_i64), _f32, _int, _vp, _errp],
 }
 
 _lib = None

@@ -110,6 +110,28 @@ def gemm(a: torch.Tensor, b: torch.Tensor, out_dtype=None, out=None, stream=None
     return c[0] if squeeze else c
 
 
+def _strides3(t: torch.Tensor):
+    """(batch, head, sequence) element strides of a [B, H, S, D] view."""
+    import ctypes
+    if t.stride(3) != 1:
+        raise ValueError("sdpa: the head dim must be contiguous")
+    return (ctypes.c_int64 * 3)(t.stride(0), t.stride(1), t.stride(2))
+
+
+def sdpa(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: float, causal: bool,
+         out=None, stream=None):
+    """Fused attention: q [B,H,Sq,D], k / v [B,Hkv,Sk,D] (any strides with a contiguous
+    head dim, e.g. BSHD storage viewed as BHSD) -> out [B,H,Sq,D]."""
+    _check_dev(q, k, v)
+    B, H, Sq, D = q.shape
+    _, Hkv, Sk, _ = k.shape
+    o = torch.empty((B, H, Sq, D), dtype=q.dtype, device=q.device) if out is None else out
+    call("ghip_sdpa_fwd", dtype_code(q.dtype), q.data_ptr(), k.data_ptr(), v.data_ptr(),
+         o.data_ptr(), B, H, Hkv, Sq, Sk, D, _strides3(q), _strides3(k), _strides3(v),
+         _strides3(o), float(scale), int(causal), _stream(stream))
+    return o
+
+
 def gather_rows(table: torch.Tensor, ids: torch.Tensor, out=None, stream=None):
     """out[i] = table[clamp(ids[i])] for an embedding table [V, ...]."""
     _check_dev(table, ids)

@@ -114,6 +114,23 @@ int ghip_gemm_batched(int ab_dtype, int c_dtype, int64_t batch, int64_t M, int64
                       int64_t sc_b, int64_t sc_m, int64_t sc_n, void* stream,
                       GHipError* err);
 
+/* Fused attention forward, the one-kernel lowering of
+ * Function.FusedScaledDotProductAttention (function.go:2669-2907; the composite
+ * it replaces is DotGeneral -> scale -> causal Where -> FusedSoftmax -> DotGeneral,
+ * :2746-2897):
+ *   o[b, h, i, :] = sum_j softmax_j(scale * q[b,h,i,:].k[b,hk,j,:] [j > i masked
+ *                   when causal]) v[b, hk, j, :],   hk = h / (H / Hkv)  (GQA, :2911-2956)
+ * Operands are addressed by ELEMENT strides (batch, head, sequence) with the head
+ * dim contiguous, so BHSD and BSHD layouts both work without copies.  Supported:
+ * dtype BFLOAT16, D == 128, strides multiples of 8 (4 for o), q/k/v 16-byte and o
+ * 8-byte aligned; anything else returns GHIP_ERR_UNSUPPORTED (the graph lowering
+ * then uses the composite).  Softmax statistics and accumulation are fp32. */
+int ghip_sdpa_fwd(int dtype, const void* q, const void* k, const void* v, void* o,
+                  int64_t B, int64_t H, int64_t Hkv, int64_t Sq, int64_t Sk, int64_t D,
+                  const int64_t* q_strides, const int64_t* k_strides, const int64_t* v_strides,
+                  const int64_t* o_strides, float scale, int causal, void* stream,
+                  GHipError* err);
+
 /* Embedding lookup: out[i, :] = table[clamp(ids[i], 0, V-1), :] (row_bytes per
  * row, copied bit-exactly).  Replaces the gather fast path
  * (gather.go:61-203 -> mpsgraph_gather_along_axis, bridge.m:764-782). */
