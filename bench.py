@@ -57,12 +57,13 @@ class Case:
 
     def __init__(self, name, launch, bytes_per_step=0, flops_per_step=0, bound="hbm",
                  peak=HBM_PEAK_GBS, dtype="f32", rotation=1, config=None, kernel="",
-                 out=None):
+                 out=None, stream=None):
         self.name, self.launch = name, launch
         self.bytes, self.flops = bytes_per_step, flops_per_step
         self.bound, self.peak, self.dtype = bound, peak, dtype
         self.rotation, self.config, self.kernel = rotation, config or {}, kernel
         self.out = out
+        self.stream = stream  # stream the kernels run on when it is not torch's
 
 
 def graph_runner(case: Case, steps: int):
@@ -93,7 +94,7 @@ def graph_runner(case: Case, steps: int):
 
 def time_case(case: Case, steps: int, warmup: int, eager: bool = False):
     import torch
-    stream = torch.cuda.current_stream()
+    stream = case.stream or torch.cuda.current_stream()
     runner = graph_runner(case, steps) if case.bound == "hbm" and not eager else None
     if runner is not None:
         replay, per = runner
@@ -107,12 +108,14 @@ def time_case(case: Case, steps: int, warmup: int, eager: bool = False):
         for i in range(warmup):
             case.launch(i)
     torch.cuda.synchronize()
+    stream.synchronize()
     ev0 = torch.cuda.Event(enable_timing=True)
     ev1 = torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()
     ev0.record(stream)
     work()
     ev1.record(stream)
+    stream.synchronize()
     torch.cuda.synchronize()
     wall_ms = (time.perf_counter() - t0) * 1e3
     dev_ms = ev0.elapsed_time(ev1)
@@ -222,6 +225,40 @@ def make_cases(only=None):
                                         "counted for both products over the full S x S matrix, "
                                         "the causal half above the diagonal is skipped"})
 
+    def transformer_case():
+        """BASELINE configs[4] through the graph API: Builder -> Compile -> Execute of
+        the whole decoder block (gather, RMSNorm, QKV/O projections, fused causal
+        attention, residual, RMSNorm, SwiGLU FFN, residual) on the backend's stream."""
+        import numpy as np
+        from gomlx_hip import graphs, synth
+        from gomlx_hip.backend import Backend
+        be = Backend("")
+        cfg = graphs.TransformerBlockConfig()
+        ex = graphs.transformer_block(be, cfg)
+        bufs = []
+        for i, (name, shape) in enumerate(cfg.param_shapes()):
+            if name == "ids":
+                host = synth.uniform_int(5001, (cfg.batch, cfg.seq), 0, cfg.vocab)
+            elif name.startswith("g_"):
+                host = np.ones(shape.dims, np.float32)
+            else:
+                host = synth.round_bf16(synth.normal(5002 + i, shape.dims, std=0.02))
+            bufs.append(be.BufferFromFlatData(0, host, shape))
+        stream = torch.cuda.ExternalStream(be.stream())
+
+        def launch(i):
+            (y,) = ex.Execute(bufs, None, 0)
+            be.BufferFinalize(y)  # back to the caching allocator; stream order protects reuse
+        case = Case("transformer_block_bf16", launch, flops_per_step=cfg.flops(), bound="mfma",
+                    peak=BF16_PEAK_TFLOPS, dtype="bf16", kernel="graph Execute (all kernels)",
+                    stream=stream,
+                    config={"workload": "decoder block B8 S1024 d2048 H16 Dh128 FFN 8192 bf16 "
+                                        "(configs[4]) through Builder/Compile/Execute; flops: "
+                                        "projections + both attention products over the full "
+                                        "S x S matrices", "steps_in_plan": ex.Plan().count("\n")})
+        case.keep = (be, ex, bufs)  # keep the backend alive while timing
+        return case
+
     builders = {
         "softmax_f32": softmax_case,
         "rmsnorm_bf16": lambda: rms_case(torch.bfloat16, "bf16"),
@@ -230,6 +267,7 @@ def make_cases(only=None):
         "dot_general_bf16": lambda: dot_case(torch.bfloat16, "bf16", BF16_PEAK_TFLOPS),
         "dot_general_f32": lambda: dot_case(torch.float32, "f32", FP32_PEAK_TFLOPS),
         "attention_bf16": attention_case,
+        "transformer_block_bf16": transformer_case,
     }
     primary = rms_case(torch.float32, "f32")
     names = [n for n in builders if not only or n in only]
