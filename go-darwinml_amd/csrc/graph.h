@@ -199,7 +199,8 @@ int launch_gather_rows(const void* table, int64_t V, int64_t row_bytes, const vo
 // Whether the fused attention kernel (ghip_sdpa_fwd) takes these operands; strides
 // in elements ordered (batch, head, sequence), head dim contiguous.
 bool sdpa_fused_supported(int dtype, int64_t H, int64_t Hkv, int64_t Sq, int64_t Sk, int64_t D,
-                          const int64_t* qs, const int64_t* ks, const int64_t* vs, const int64_t* os);
+                          const int64_t* qs, const int64_t* ks, const int64_t* vs, const int64_t* os,
+                          float scale);
 
 }  // namespace ghip
 

@@ -850,8 +850,8 @@ struct Lowerer {
       const int64_t vst[3] = {vw.strides[0], vw.strides[1], vw.strides[2]};
       const int64_t ost[3] = {ov.strides[0], ov.strides[1], ov.strides[2]};
       const bool al = q.offset % 8 == 0 && k.offset % 8 == 0 && vw.offset % 8 == 0 && ov.offset % 4 == 0;
-      if (al && sdpa_fused_supported(dt, H, Hkv, Sq, Sk, D, qst, kst, vst, ost)) {
-        const float scale = static_cast<float>(n.f0);
+      const float scale = static_cast<float>(n.f0);
+      if (al && sdpa_fused_supported(dt, H, Hkv, Sq, Sk, D, qst, kst, vst, ost, scale)) {
         std::array<int64_t, 3> aq{qst[0], qst[1], qst[2]}, ak{kst[0], kst[1], kst[2]},
             av{vst[0], vst[1], vst[2]}, ao{ost[0], ost[1], ost[2]};
         add_step(fmt("sdpa_fwd %s B=%lld H=%lld Hkv=%d Sq=%lld Sk=%lld D=%lld causal=%d (fused attention)",

@@ -151,6 +151,9 @@ __global__ __launch_bounds__(256, 2) void sdpa_fwd_kernel(Params p) {
 
   const int kv_end = p.causal ? min(p.Sk, q0 + kBQ) : p.Sk;
   const int ntiles = (kv_end + kBKV - 1) / kBKV;
+  // scale_log2 > 0, so the running max is kept on the raw scores and the scale
+  // is folded into one FMA per exponent: exp2(s * c - m * c).
+  const float c = p.scale_log2;
 
   auto issue = [&](int t, int st) {
     const int64_t key0 = static_cast<int64_t>(t) * kBKV;
@@ -166,86 +169,91 @@ __global__ __launch_bounds__(256, 2) void sdpa_fwd_kernel(Params p) {
   for (int db = 0; db < kD / 32; ++db)
 #pragma unroll
     for (int v = 0; v < 16; ++v) o[db][v] = 0.f;
-  float m = -INFINITY;  // running max (log2 units) of query qi
+  float m = -INFINITY;  // running max of the raw scores of query qi
   float l = 0.f;        // running sum over this half-wave's keys
 
-  if (ntiles > 0) issue(0, 0);
-  if (ntiles > 1) issue(1, 1);
-  for (int t = 0; t < ntiles; ++t) {
-    const int st = t & 1;
-    // 8 loads per wave per tile: leave tile t+1's in flight.
-    if (t + 1 < ntiles) asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
-    else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  // One barrier per tile: at the top of tile t every wave has finished tile t-1,
+  // so once tile t has landed, stage (t+1) & 1 can take tile t+1.
+  auto tile = [&](int t, int st) {
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
+    if (t + 1 < ntiles) issue(t + 1, st ^ 1);
     const int key0 = t * kBKV;
     // Causal: a wave whose last query precedes the tile's first key has nothing to
     // do here (it still takes part in the barriers and loads).
-    const bool active = !p.causal || key0 <= qw + kQW - 1;
-    if (active) {
-      f32x16_t s0, s1;
+    if (p.causal && key0 > qw + kQW - 1) return;
+    f32x16_t s0, s1;
 #pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        s0[v] = 0.f;
-        s1[v] = 0.f;
-      }
+    for (int v = 0; v < 16; ++v) {
+      s0[v] = 0.f;
+      s1[v] = 0.f;
+    }
 #pragma unroll
-      for (int s = 0; s < kD / 16; ++s) {
-        s0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(frag_k(sk[st], 0, s, lane), qf[s], s0, 0, 0, 0);
-        s1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(frag_k(sk[st], 1, s, lane), qf[s], s1, 0, 0, 0);
-      }
-      // s{kb}[v] is key key0 + 32 kb + (v/4)*8 + 4 h2 + v%4 for query qi.
-      const bool need_mask = (p.causal && key0 + kBKV - 1 > qw) || key0 + kBKV > p.Sk;
-      float mx = -INFINITY;
+    for (int s = 0; s < kD / 16; ++s) {
+      s0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(frag_k(sk[st], 0, s, lane), qf[s], s0, 0, 0, 0);
+      s1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(frag_k(sk[st], 1, s, lane), qf[s], s1, 0, 0, 0);
+    }
+    // s{kb}[v] is key key0 + 32 kb + (v/4)*8 + 4 h2 + v%4 for query qi; only the
+    // diagonal tile(s) and a ragged last tile need the element mask.
+    if ((p.causal && key0 + kBKV - 1 > qw) || key0 + kBKV > p.Sk) {
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
         const int kr = (v >> 2) * 8 + 4 * h2 + (v & 3);
-        float a = s0[v] * p.scale_log2, c = s1[v] * p.scale_log2;
-        if (need_mask) {
-          const int ka = key0 + kr, kc = key0 + 32 + kr;
-          if (ka >= p.Sk || (p.causal && ka > qi)) a = -INFINITY;
-          if (kc >= p.Sk || (p.causal && kc > qi)) c = -INFINITY;
-        }
-        s0[v] = a;
-        s1[v] = c;
-        mx = fmaxf(mx, fmaxf(a, c));
+        const int ka = key0 + kr, kc = key0 + 32 + kr;
+        if (ka >= p.Sk || (p.causal && ka > qi)) s0[v] = -INFINITY;
+        if (kc >= p.Sk || (p.causal && kc > qi)) s1[v] = -INFINITY;
       }
-      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-      const float mnew = fmaxf(m, mx);
-      // A query with nothing unmasked yet keeps m = -inf; 0 is then the base.
-      const float base = mnew == -INFINITY ? 0.f : mnew;
-      const float alpha = exp2f(m - base);
-      m = mnew;
-      float ls = 0.f;
+    }
+    float mx = -INFINITY;
 #pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        const float e0 = exp2f(s0[v] - base), e1 = exp2f(s1[v] - base);
-        ls += e0 + e1;
-        s0[v] = e0;
-        s1[v] = e1;
-      }
-      l = l * alpha + ls;
+    for (int v = 0; v < 16; ++v) mx = fmaxf(mx, fmaxf(s0[v], s1[v]));
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    const float mnew = fmaxf(m, mx);
+    // A query with nothing unmasked yet keeps m = -inf and exponent offset 0.
+    const float nb = mnew == -INFINITY ? 0.f : -mnew * c;
+    // v_exp_f32 directly: weights below 2^-126 flush to zero.
+    const float alpha = __builtin_amdgcn_exp2f(__builtin_fmaf(m, c, nb));
+    m = mnew;
+    float ls = 0.f;
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+      const float e0 = __builtin_amdgcn_exp2f(__builtin_fmaf(s0[v], c, nb));
+      const float e1 = __builtin_amdgcn_exp2f(__builtin_fmaf(s1[v], c, nb));
+      ls += e0 + e1;
+      s0[v] = e0;
+      s1[v] = e1;
+    }
+    l = l * alpha + ls;
+    // The output rescale is a no-op unless some lane's max moved.
+    if (__builtin_amdgcn_ballot_w64(alpha != 1.f)) {
 #pragma unroll
       for (int db = 0; db < kD / 32; ++db)
 #pragma unroll
         for (int v = 0; v < 16; ++v) o[db][v] *= alpha;
-      // P^T operand of key step s: s{s/2}[8 (s%2) .. +8] rounded to bf16.
-      bf16x8_t pb[4];
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        pb[0][e] = static_cast<__bf16>(s0[e]);
-        pb[1][e] = static_cast<__bf16>(s0[8 + e]);
-        pb[2][e] = static_cast<__bf16>(s1[e]);
-        pb[3][e] = static_cast<__bf16>(s1[8 + e]);
-      }
-#pragma unroll
-      for (int s = 0; s < kBKV / 16; ++s)
-#pragma unroll
-        for (int db = 0; db < kD / 32; ++db)
-          o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(frag_v(sv[st], db, s, lane), pb[s], o[db], 0, 0, 0);
     }
+    // P^T operand of key step s: s{s/2}[8 (s%2) .. +8] rounded to bf16.
+    bf16x8_t pb[4];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      pb[0][e] = static_cast<__bf16>(s0[e]);
+      pb[1][e] = static_cast<__bf16>(s0[8 + e]);
+      pb[2][e] = static_cast<__bf16>(s1[e]);
+      pb[3][e] = static_cast<__bf16>(s1[8 + e]);
+    }
+#pragma unroll
+    for (int s = 0; s < kBKV / 16; ++s)
+#pragma unroll
+      for (int db = 0; db < kD / 32; ++db)
+        o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(frag_v(sv[st], db, s, lane), pb[s], o[db], 0, 0, 0);
+    // This stage's LDS reads complete before the next barrier, after which it is
+    // refilled.
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-    __syncthreads();
-    if (t + 2 < ntiles) issue(t + 2, st);
+  };
+
+  if (ntiles > 0) issue(0, 0);
+  for (int t = 0; t < ntiles; t += 2) {
+    tile(t, 0);
+    if (t + 1 < ntiles) tile(t + 1, 1);
   }
 
   // o[db][v] is d = 32 db + (v/4)*8 + 4 h2 + v%4 of query qi.
@@ -271,8 +279,10 @@ __global__ __launch_bounds__(256, 2) void sdpa_fwd_kernel(Params p) {
 // by the entry point).  Strides are in elements, ordered (batch, head, sequence);
 // the head dim must be contiguous.
 bool sdpa_fused_supported(int dtype, int64_t H, int64_t Hkv, int64_t Sq, int64_t Sk, int64_t D,
-                          const int64_t* qs, const int64_t* ks, const int64_t* vs, const int64_t* os) {
+                          const int64_t* qs, const int64_t* ks, const int64_t* vs, const int64_t* os,
+                          float scale) {
   if (dtype != GHIP_DTYPE_BFLOAT16 || D != attn::kD || Hkv <= 0 || H % Hkv != 0) return false;
+  if (!(scale > 0.f) || !(scale < 1e30f)) return false;  // positive and finite
   if (Sq <= 0 || Sk <= 0 || Sq > (int64_t{1} << 30) || Sk > (int64_t{1} << 30)) return false;
   for (const int64_t* s : {qs, ks, vs})
     for (int i = 0; i < 3; ++i)
@@ -303,10 +313,10 @@ extern "C" int ghip_sdpa_fwd(int dtype, const void* q, const void* k, const void
     return set_error(err, GHIP_ERR_INVALID_ARG, "sdpa_fwd: null strides");
   if (B == 0 || Sq == 0) return GHIP_OK;
   if (!q || !k || !v || !o) return set_error(err, GHIP_ERR_INVALID_ARG, "sdpa_fwd: null pointer");
-  if (!sdpa_fused_supported(dtype, H, Hkv, Sq, Sk, D, q_strides, k_strides, v_strides, o_strides))
+  if (!sdpa_fused_supported(dtype, H, Hkv, Sq, Sk, D, q_strides, k_strides, v_strides, o_strides, scale))
     return set_error(err, GHIP_ERR_UNSUPPORTED,
-                     "sdpa_fwd: needs bfloat16, head dim 128, non-negative strides that are multiples of 8 "
-                     "(4 for the output) and < 2 GiB per K/V head");
+                     "sdpa_fwd: needs bfloat16, head dim 128, a positive finite scale, non-negative strides "
+                     "that are multiples of 8 (4 for the output) and < 2 GiB per K/V head");
   auto al = [](const void* ptr, uintptr_t a) { return (reinterpret_cast<uintptr_t>(ptr) & (a - 1)) == 0; };
   if (!al(q, 16) || !al(k, 16) || !al(v, 16) || !al(o, 8))
     return set_error(err, GHIP_ERR_UNSUPPORTED, "sdpa_fwd: q/k/v must be 16-byte aligned, o 8-byte aligned");

@@ -97,3 +97,6 @@ def test_sdpa_rejects_unsupported(cuda):
     k = torch.zeros((1, 2, 16, 128), device=cuda, dtype=torch.bfloat16)
     with pytest.raises(BackendError):
         ops.sdpa(q, k, k, 1.0, False)  # 3 heads over 2 KV heads
+    q = torch.zeros((1, 2, 16, 128), device=cuda, dtype=torch.bfloat16)
+    with pytest.raises(BackendError):
+        ops.sdpa(q, q, q, -0.5, False)  # negative scale: composite path only
