@@ -8,7 +8,10 @@ carries the other BASELINE workloads under "secondary" (softmax, bf16 RMSNorm,
 LayerNorm, bf16/fp32 DotGeneral, the attention composite), each with its own
 roofline fraction.
 
-Timing: W untimed warmup steps, then K steps bracketed by torch.cuda.synchronize()
+Timing: W untimed warmup steps plus at least 0.25 s of sustained untimed launches
+(the GPU clock settles only under sustained load; a cold first burst of bf16
+GEMMs runs ~10% slower), then K steps (raised so the timed region holds at least
+30 ms of device work) bracketed by torch.cuda.synchronize()
 on both sides (wall clock -> ms_per_step), and HIP events recorded on the stream
 the kernels run on (-> average launch duration for "roofline").  Working sets
 below 1 GiB rotate through several input/output buffer sets so the 256 MB
@@ -92,21 +95,42 @@ def graph_runner(case: Case, steps: int):
     return g.replay, per
 
 
+MIN_WARM_S = 0.25   # sustained warm-up before each timed region
+MIN_TIMED_S = 0.03  # minimum device time inside each timed region
+
+
 def time_case(case: Case, steps: int, warmup: int, eager: bool = False):
     import torch
     stream = case.stream or torch.cuda.current_stream()
     runner = graph_runner(case, steps) if case.bound == "hbm" and not eager else None
     if runner is not None:
         replay, per = runner
-        reps = max(1, -(-steps // per))
-        steps = reps * per
-        work = lambda: [replay() for _ in range(reps)]  # noqa: E731
+        once = lambda i: replay()  # noqa: E731
         for _ in range(max(1, warmup // per)):
             replay()
     else:
-        work = lambda: [case.launch(i) for i in range(steps)]  # noqa: E731
+        per = 1
+        once = case.launch
         for i in range(warmup):
             case.launch(i)
+    # The clock settles only after some 100 ms of sustained load: keep warming up
+    # until that much wall time has passed, and size the timed region to at least
+    # MIN_TIMED_S of work (never fewer steps than asked for).
+    stream.synchronize()
+    n, t0 = 0, time.perf_counter()
+    while time.perf_counter() - t0 < MIN_WARM_S:
+        for _ in range(4):
+            once(n)
+            n += 1
+        stream.synchronize()
+    est = (time.perf_counter() - t0) / (n * per)
+    steps = max(steps, int(MIN_TIMED_S / est) + 1)
+    reps = max(1, -(-steps // per))
+    steps = reps * per
+    if runner is not None:
+        work = lambda: [replay() for _ in range(reps)]  # noqa: E731
+    else:
+        work = lambda: [case.launch(i) for i in range(steps)]  # noqa: E731
     torch.cuda.synchronize()
     stream.synchronize()
     ev0 = torch.cuda.Event(enable_timing=True)

@@ -21,16 +21,30 @@ __device__ __host__ __forceinline__ float bf16_to_f32(uint16_t b) {
   return __builtin_bit_cast(float, u);
 }
 
+// Round to nearest even; a NaN keeps its sign and upper payload bits and comes
+// out quiet.  On gfx950 this is exactly v_cvt_pk_bf16_f32 (the device path:
+// one instruction per pair of values); the integer formulation (host path) is
+// the definition both are tested against.
 __device__ __forceinline__ uint16_t f32_to_bf16(float f) {
-  uint32_t u = __float_as_uint(f);
+#if defined(__HIP_DEVICE_COMPILE__)
+  return __builtin_bit_cast(uint16_t, static_cast<__bf16>(f));
+#else
+  uint32_t u = __builtin_bit_cast(uint32_t, f);
   if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((u >> 16) | 0x40u);
   u += 0x7fffu + ((u >> 16) & 1u);
   return static_cast<uint16_t>(u >> 16);
+#endif
 }
 
 // Packs two fp32 into two bf16 (RNE) in one dword: lo in bits 0..15.
 __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+  const bf16x2_t v = {static_cast<__bf16>(lo), static_cast<__bf16>(hi)};
+  return __builtin_bit_cast(uint32_t, v);
+#else
   return static_cast<uint32_t>(f32_to_bf16(lo)) | (static_cast<uint32_t>(f32_to_bf16(hi)) << 16);
+#endif
 }
 
 // ---------------------------------------------------------------------------

@@ -22,14 +22,17 @@
 #include <math.h>
 #include <stdarg.h>
 #include <stdio.h>
+#include <stdlib.h>
 #include <string.h>
 
 #include <algorithm>
 #include <array>
+#include <map>
 #include <set>
 #include <sstream>
 
 #include "common.h"
+#include "gemm_bf16_dev.h"
 #include "graph.h"
 
 namespace ghip {
@@ -40,6 +43,30 @@ struct Fusion {
   int x = -1, gamma = -1;
   double eps = 0;
 };
+
+// Helpers shared by every generated elementwise kernel: bf16 / f16 rounding
+// (round to nearest even, NaN kept quiet; for bf16 gfx950's v_cvt_pk_bf16_f32,
+// which computes exactly that), NaN-propagating min/max, integer pow.
+const char kRtcPrelude[] = R"(typedef unsigned short u16;
+__device__ __forceinline__ float bf2f(u16 b) { return __uint_as_float(((unsigned)b) << 16); }
+__device__ __forceinline__ u16 f2bf(float f) { return __builtin_bit_cast(u16, (__bf16)f); }
+__device__ __forceinline__ float rbf(float f) { return bf2f(f2bf(f)); }
+__device__ __forceinline__ float rhf(float f) { return (float)(_Float16)f; }
+template <typename T> __device__ __forceinline__ T fmax_nan(T a, T b) { return (a > b || a != a) ? a : b; }
+template <typename T> __device__ __forceinline__ T fmin_nan(T a, T b) { return (a < b || a != a) ? a : b; }
+__device__ __forceinline__ long long ipow(long long b, long long e) {
+  if (e < 0) return b == 1 ? 1 : (b == -1 ? ((e & 1) ? -1 : 1) : 0);
+  long long r = 1;
+  while (e) { if (e & 1) r *= b; b *= b; e >>= 1; }
+  return r;
+}
+)";
+
+// Text of gemm_bf16_dev.h (the bf16 MFMA GEMM core), compiled with hipRTC in
+// front of generated epilogues.
+const char kGemmDevSrc[] =
+#include "gemm_bf16_dev.inc"
+    ;
 
 std::string fmt(const char* f, ...) {
   char buf[512];
@@ -715,12 +742,24 @@ struct Lowerer {
     return true;
   }
 
-  View emit_dot(int v) {
+  // A DotGeneral folded to one batched GEMM: operand views and (batch, M, N, K)
+  // sizes with one stride per axis group.
+  struct DotPlan {
+    View lv, rv;
+    int64_t B = 0, sab = 0, sbb = 0, M = 0, sam = 0, K = 0, sak = 0, N = 0, sbn = 0, sbk = 0;
+    int nbatch = 0, nlfree = 0;  // output dims: [batch (nbatch), lhs free (nlfree), rhs free]
+    std::string how;
+  };
+
+  // Folds Dot node v's axis groups into single strides.  Operands whose groups
+  // do not fold are materialised in [batch, free, contracting] order, unless
+  // allow_copy is false (then returns false with no step emitted).
+  bool plan_dot(int v, bool allow_copy, DotPlan* d) {
     const Node& n = N[v];
     const int L = n.in[0], R = n.in[1];
     Shape ls = N[L].shape, rs = N[R].shape;
     View lv = get(L), rv = get(R);
-    if (failed) return bad();
+    if (failed) return false;
     std::vector<int64_t> lfree, rfree;
     for (int i = 0; i < ls.rank(); ++i)
       if (std::find(n.a0.begin(), n.a0.end(), i) == n.a0.end() && std::find(n.a1.begin(), n.a1.end(), i) == n.a1.end())
@@ -735,6 +774,7 @@ struct Lowerer {
     };
     std::string how = "strides folded";
     if (!try_merge()) {
+      if (!allow_copy) return false;
       // Materialise each operand in canonical [batch, free, contracting] order.
       std::vector<int64_t> lp(n.a1.begin(), n.a1.end()), rp(n.a3.begin(), n.a3.end());
       lp.insert(lp.end(), lfree.begin(), lfree.end());
@@ -751,16 +791,39 @@ struct Lowerer {
       };
       lv = canon(ls, lv, lp);
       rv = canon(rs, rv, rp);
-      if (failed) return bad();
+      if (failed) return false;
       how = "operands materialised";
-      if (!try_merge()) return fail(GHIP_ERR_STATE, "DotGeneral: stride merge failed after canonicalisation");
+      if (!try_merge()) {
+        fail(GHIP_ERR_STATE, "DotGeneral: stride merge failed after canonicalisation");
+        return false;
+      }
     }
-    if (K != K2 || B != B2) return fail(GHIP_ERR_STATE, "DotGeneral: inconsistent sizes");
+    if (K != K2 || B != B2) {
+      fail(GHIP_ERR_STATE, "DotGeneral: inconsistent sizes");
+      return false;
+    }
+    d->lv = lv;
+    d->rv = rv;
+    d->B = B; d->sab = sab; d->sbb = sbb; d->M = M; d->sam = sam; d->K = K; d->sak = sak;
+    d->N = N_; d->sbn = sbn; d->sbk = sbk;
+    d->nbatch = static_cast<int>(n.a1.size());
+    d->nlfree = static_cast<int>(lfree.size());
+    d->how = how;
+    return true;
+  }
+
+  View emit_dot(int v) {
+    const Node& n = N[v];
+    DotPlan d;
+    if (!plan_dot(v, true, &d)) return bad();
+    const View lv = d.lv, rv = d.rv;
+    const int64_t B = d.B, sab = d.sab, sbb = d.sbb, M = d.M, sam = d.sam, K = d.K, sak = d.sak, N_ = d.N,
+                  sbn = d.sbn, sbk = d.sbk;
     View y = fresh(n.shape);
-    const int dt = ls.dtype, odt = n.shape.dtype;
+    const int dt = N[n.in[0]].shape.dtype, odt = n.shape.dtype;
     const int64_t scb = M * N_, scm = N_;
     add_step(fmt("gemm_batched %s B=%lld M=%lld N=%lld K=%lld (%s; a strides b=%lld m=%lld k=%lld, b strides b=%lld k=%lld n=%lld)",
-                 dtype_name(dt), (long long)B, (long long)M, (long long)N_, (long long)K, how.c_str(), (long long)sab,
+                 dtype_name(dt), (long long)B, (long long)M, (long long)N_, (long long)K, d.how.c_str(), (long long)sab,
                  (long long)sam, (long long)sak, (long long)sbb, (long long)sbk, (long long)sbn),
              {lv.slot, rv.slot}, {y.slot}, [=](ExecState& st, GHipError* e) {
                return ghip_gemm_batched(dt, odt, B, M, N_, K, st.ptr(lv, dt), sab, sam, sak, st.ptr(rv, dt), sbb, sbk, sbn,
@@ -768,6 +831,17 @@ struct Lowerer {
              });
     return y;
   }
+
+  // ------------------------------------------------------------------ GEMM epilogue fusion
+  // An elementwise cluster whose inputs include one DotGeneral (or two that share
+  // the left operand and all sizes) consumed only inside the cluster runs as
+  // one GEMM whose epilogue evaluates the cluster: the Dot results never touch
+  // HBM.  The Dot value enters the epilogue rounded to the Dot's dtype, and the
+  // members' code is the same generated code the stand-alone cluster kernel
+  // runs, so fused and unfused plans give bit-identical results.
+  bool fuse_epilogues = true;
+  View emit_gemm_epilogue(int v, const std::vector<int>& mem, bool* fused);
+  std::string member_stmt(int u, std::map<int, std::string>& expr, const std::string& name);
 
   // ------------------------------------------------------------------ Gather
   View emit_gather(int v) {
@@ -1125,6 +1199,24 @@ std::string Lowerer::op_expr(const Node& n, const std::vector<std::string>& a, c
   }
 }
 
+// Statement computing elementwise member u (in its compute type, rounded to its
+// dtype) from the expressions of its operands; records u's expression.
+std::string Lowerer::member_stmt(int u, std::map<int, std::string>& expr, const std::string& name) {
+  const Node& n = N[u];
+  std::vector<std::string> a;
+  std::vector<int> adt;
+  for (int o : n.in) {
+    a.push_back(expr[o]);
+    adt.push_back(N[o].shape.dtype);
+  }
+  // Where / Clamp: the dtype driving op semantics is the value operands'.
+  std::vector<int> sem = adt;
+  if (n.kind == Kind::Where) sem = {adt[1]};
+  if (n.kind == Kind::Clamp) sem = {adt[1]};
+  expr[u] = name;
+  return "    const " + ctype(n.shape.dtype) + " " + name + " = " + round_expr(n.shape.dtype, op_expr(n, a, sem)) + ";\n";
+}
+
 View Lowerer::emit_cluster(int root, int v) {
   // Members: root's cluster (or, for a value requested outside its cluster, the
   // value alone plus any Iota leaves) in node order.
@@ -1132,6 +1224,12 @@ View Lowerer::emit_cluster(int root, int v) {
   if (root >= 0) {
     for (int u = 0; u <= root; ++u)
       if (cluster[u] == root) mem.push_back(u);
+    if (fuse_epilogues) {
+      bool fused = false;
+      View y = emit_gemm_epilogue(v, mem, &fused);
+      if (failed) return bad();
+      if (fused) return y;
+    }
   } else {
     mem.push_back(v);
   }
@@ -1193,46 +1291,16 @@ View Lowerer::emit_cluster(int root, int v) {
       ins.push_back(in);
     }
     if (failed) return bad();
-    const Node& n = N[u];
-    std::vector<std::string> a;
-    std::vector<int> adt;
-    for (int o : n.in) {
-      a.push_back(expr[o]);
-      adt.push_back(N[o].shape.dtype);
+    if (N[u].kind == Kind::Iota) {
+      const std::string name = "v" + std::to_string(u);
+      body << "    const " << ctype(N[u].shape.dtype) << " " << name << " = " << round_expr(N[u].shape.dtype, iota_expr(u)) << ";\n";
+      expr[u] = name;
+    } else {
+      body << member_stmt(u, expr, "v" + std::to_string(u));
     }
-    std::string e;
-    if (n.kind == Kind::Iota) e = iota_expr(u);
-    else {
-      // Where / Clamp: the dtype driving op semantics is the value operands'.
-      std::vector<int> sem = adt;
-      if (n.kind == Kind::Where) sem = {adt[1]};
-      if (n.kind == Kind::Clamp) sem = {adt[1]};
-      e = op_expr(n, a, sem);
-    }
-    const std::string name = "v" + std::to_string(u);
-    body << "    const " << ctype(n.shape.dtype) << " " << name << " = " << round_expr(n.shape.dtype, e) << ";\n";
-    expr[u] = name;
   }
   std::ostringstream src;
-  src << R"(typedef unsigned short u16;
-__device__ __forceinline__ float bf2f(u16 b) { return __uint_as_float(((unsigned)b) << 16); }
-__device__ __forceinline__ u16 f2bf(float f) {
-  unsigned u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return (u16)((u >> 16) | 0x40u);
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return (u16)(u >> 16);
-}
-__device__ __forceinline__ float rbf(float f) { return bf2f(f2bf(f)); }
-__device__ __forceinline__ float rhf(float f) { return (float)(_Float16)f; }
-template <typename T> __device__ __forceinline__ T fmax_nan(T a, T b) { return (a > b || a != a) ? a : b; }
-template <typename T> __device__ __forceinline__ T fmin_nan(T a, T b) { return (a < b || a != a) ? a : b; }
-__device__ __forceinline__ long long ipow(long long b, long long e) {
-  if (e < 0) return b == 1 ? 1 : (b == -1 ? ((e & 1) ? -1 : 1) : 0);
-  long long r = 1;
-  while (e) { if (e & 1) r *= b; b *= b; e >>= 1; }
-  return r;
-}
-extern "C" __global__ void __launch_bounds__(256) fused(
+  src << kRtcPrelude << R"(extern "C" __global__ void __launch_bounds__(256) fused(
 )";
   for (size_t k = 0; k < ins.size(); ++k) src << "    const void* __restrict__ p_in" << k << ",\n";
   src << "    void* __restrict__ p_out, long long n) {\n";
@@ -1285,6 +1353,244 @@ extern "C" __global__ void __launch_bounds__(256) fused(
     if (h != hipSuccess) return check_hip(h, e, "generated elementwise kernel launch");
     return GHIP_OK;
   });
+  return y;
+}
+
+// Compile-time image of the run-time checks ghip_gemm_batched makes before it
+// takes the bf16 MFMA path (slot bases are 256-byte aligned, so a view's base is
+// 16-byte aligned iff its element offset is a multiple of 8).
+static int mfma_majorness(int64_t offset, int64_t s_b, int64_t s_mn, int64_t s_k, int64_t MN, int64_t K,
+                          int64_t batch) {
+  if (offset % 8 != 0) return -1;
+  const bool b_ok = batch == 1 || s_b % 8 == 0;
+  if (s_k == 1 && K % 8 == 0 && (MN == 1 || s_mn % 8 == 0) && b_ok) return 1;
+  if (s_mn == 1 && MN % 8 == 0 && (K == 1 || s_k % 8 == 0) && b_ok) return 0;
+  return -1;
+}
+
+View Lowerer::emit_gemm_epilogue(int v, const std::vector<int>& mem, bool* fused) {
+  *fused = false;
+  const Shape& os = N[v].shape;
+  std::set<int> inset(mem.begin(), mem.end());
+  std::set<int> outs(fn->outputs.begin(), fn->outputs.end());
+  // Dot inputs, in first-use order.
+  std::vector<int> dots;
+  for (int u : mem) {
+    if (N[u].kind == Kind::Iota) return View{};
+    for (int o : N[u].in)
+      if (o >= 0 && !inset.count(o) && N[o].kind == Kind::Dot &&
+          std::find(dots.begin(), dots.end(), o) == dots.end())
+        dots.push_back(o);
+  }
+  if (dots.empty() || dots.size() > 2) return View{};
+  for (int d : dots) {
+    const Node& n = N[d];
+    if (!live[d] || have[d] || outs.count(d) || fusion[d].kind != Fusion::None) return View{};
+    if (n.shape.dims != os.dims) return View{};
+    for (int w : users[d])
+      if (!inset.count(w)) return View{};
+    if (N[n.in[0]].shape.dtype != GHIP_DTYPE_BFLOAT16 || N[n.in[1]].shape.dtype != GHIP_DTYPE_BFLOAT16) return View{};
+    if (n.shape.dtype != GHIP_DTYPE_BFLOAT16 && n.shape.dtype != GHIP_DTYPE_FLOAT32) return View{};
+  }
+  if (dots.size() == 2) {
+    const Node& a = N[dots[0]];
+    const Node& b = N[dots[1]];
+    if (a.in[0] != b.in[0] || a.shape.dtype != b.shape.dtype || N[a.in[1]].shape.dims != N[b.in[1]].shape.dims ||
+        a.a0 != b.a0 || a.a1 != b.a1 || a.a2 != b.a2 || a.a3 != b.a3)
+      return View{};
+  }
+  const int NB = static_cast<int>(dots.size());
+  DotPlan dp[2];
+  for (int k = 0; k < NB; ++k) {
+    if (!plan_dot(dots[k], false, &dp[k])) return View{};  // (failed is checked by the caller)
+  }
+  const DotPlan& d = dp[0];
+  if (NB == 2 && (dp[1].sbb != d.sbb || dp[1].sbk != d.sbk || dp[1].sbn != d.sbn)) return View{};
+  // The bf16 MFMA path's operand conditions, decided here because the fused
+  // kernel has no generic fallback.
+  if (d.B > 65535 || d.M == 0 || d.N == 0 || d.K == 0) return View{};
+  if (d.sab < 0 || d.sam < 0 || d.sak < 0 || d.sbb < 0 || d.sbk < 0 || d.sbn < 0) return View{};
+  const int ma = mfma_majorness(d.lv.offset, d.sab, d.sam, d.sak, d.M, d.K, d.B);
+  int mb = mfma_majorness(d.rv.offset, d.sbb, d.sbn, d.sbk, d.N, d.K, d.B);
+  if (NB == 2 && mfma_majorness(dp[1].rv.offset, d.sbb, d.sbn, d.sbk, d.N, d.K, d.B) != mb) mb = -1;
+  if (ma < 0 || mb < 0) return View{};
+  const int64_t ea = ((d.M - 1) * d.sam + (d.K - 1) * d.sak + 1) * 2;
+  const int64_t eb = ((d.N - 1) * d.sbn + (d.K - 1) * d.sbk + 1) * 2;
+  if (ea >= (int64_t{1} << 31) || eb >= (int64_t{1} << 31)) return View{};
+
+  // Extra operands: each must fold to one stride per (batch, m, n) group of the
+  // output dims [batch (nbatch), lhs free (nlfree), rhs free].
+  std::vector<int64_t> gb, gm, gn;
+  for (int i = 0; i < os.rank(); ++i)
+    (i < d.nbatch ? gb : i < d.nbatch + d.nlfree ? gm : gn).push_back(i);
+  struct In {
+    View view;
+    int dt;
+    int64_t sb, sm, sn;
+    bool vin;  // 4-element vector loads: unit n stride, rows and base 4-element aligned
+  };
+  std::vector<In> ins;
+  std::map<int, std::string> expr;
+  for (int k = 0; k < NB; ++k) expr[dots[k]] = round_expr(N[dots[k]].shape.dtype, k == 0 ? "acc0[e]" : "acc1[e]");
+  std::ostringstream body;
+  for (size_t ui = 0; ui < mem.size(); ++ui) {
+    const int u = mem[ui];
+    for (int o : N[u].in) {
+      if (o < 0 || inset.count(o) || expr.count(o)) continue;
+      double c;
+      if (scalar_const(o, &c) && (dtype_is_float(N[o].shape.dtype) || fabs(c) < 9007199254740992.0)) {
+        expr[o] = literal(N[o].shape.dtype, c);
+        continue;
+      }
+      if (N[o].kind == Kind::Iota || static_cast<int>(ins.size()) == kEpiMaxIn) return View{};
+      View w = get(o);
+      if (failed) return View{};
+      const Shape& s = N[o].shape;
+      View eff;
+      eff.slot = w.slot;
+      eff.offset = w.offset;
+      eff.strides.assign(os.rank(), 0);
+      const int off = os.rank() - s.rank();
+      for (int i = 0; i < s.rank(); ++i)
+        if (s.dims[i] != 1) eff.strides[off + i] = w.strides[i];
+      In in{w, s.dtype, 0, 0, 0, false};
+      int64_t sz;
+      if (!merge(os, eff, gb, &sz, &in.sb) || !merge(os, eff, gm, &sz, &in.sm) || !merge(os, eff, gn, &sz, &in.sn))
+        return View{};
+      in.vin = in.sn == 1 && (in.sm % 4 == 0 || d.M == 1) && (in.sb % 4 == 0 || d.B == 1) && w.offset % 4 == 0;
+      const int k = static_cast<int>(ins.size());
+      const std::string ks = std::to_string(k);
+      body << "      const " << ctype(s.dtype) << " in" << ks << " = " << load_expr(s.dtype, "pr.x" + ks + "[e]") << ";\n";
+      expr[o] = "in" + ks;
+      ins.push_back(in);
+    }
+    body << "  " << member_stmt(u, expr, "t" + std::to_string(ui));
+  }
+
+  // Tile shape: the precompiled kernels' choice for one operand; with two, a
+  // 256 x (2 x 128) tile does the MMA work of one 256 x 256 tile.
+  int BM = 128, BN = 128, WM = 2, WN = 2;
+  const int64_t t256 = d.B * ((d.M + 255) / 256) * ((d.N + 255) / 256);
+  if (NB == 1) {
+    if (d.M >= 256 && d.N >= 256 && t256 >= 128) BM = 256, BN = 256, WM = 2, WN = 4;
+    else if (d.M >= 256 && d.N >= 128) BM = 256, BN = 128, WM = 2, WN = 2;
+  } else if (d.M >= 256 && d.N >= 128) {
+    BM = 256, BN = 128, WM = 2, WN = 4;
+  }
+  const int nt = WM * WN * 64;
+  const int odt = os.dtype;
+  std::ostringstream src;
+  src << kGemmDevSrc << "\n" << kRtcPrelude;
+  // Pre: the 4 raw elements of each extra operand for one call, loaded by
+  // prefetch() ahead of the stores of the previous row block.  FULL: the
+  // tile lies inside the output, so no column bounds checks.
+  const bool vec = d.N % 4 == 0;
+  src << "namespace ghip {\nstruct GenEpi {\n  struct Pre {";
+  for (size_t k = 0; k < ins.size(); ++k) src << " " << stype(ins[k].dt) << " x" << k << "[4];";
+  src << " };\n  EpiArgs a;\n"
+      << "  template <bool FULL>\n"
+      << "  __device__ __forceinline__ void prefetch(int64_t bb, int64_t m, int64_t n, Pre& pr) const {\n";
+  for (size_t k = 0; k < ins.size(); ++k) {
+    const std::string T = stype(ins[k].dt), ks = std::to_string(k);
+    src << "    {\n      const " << T << "* src = (const " << T << "*)a.in[" << ks << "] + bb * a.s_b[" << ks
+        << "] + m * a.s_m[" << ks << "] + n * a.s_n[" << ks << "];\n";
+    if (ins[k].vin)
+      src << "      if (FULL || n + 3 < a.N) {\n"
+          << "        struct __attribute__((aligned(4 * sizeof(" << T << ")))) V { " << T << " x[4]; };\n"
+          << "        const V w = *(const V*)src;\n"
+          << "#pragma unroll\n        for (int e = 0; e < 4; ++e) pr.x" << ks << "[e] = w.x[e];\n"
+          << "      } else {\n";
+    else
+      src << "      {\n";
+    src << "#pragma unroll\n        for (int e = 0; e < 4; ++e) pr.x" << ks << "[e] = (FULL || n + e < a.N) ? src[e * a.s_n[" << ks
+        << "]] : (" << T << ")0;\n      }\n    }\n";
+  }
+  src << "  }\n"
+      << "  template <bool FULL>\n"
+      << "  __device__ __forceinline__ void store(int64_t bb, int64_t m, int64_t n, const float* acc0,\n"
+      << "                                        const float* acc1, const Pre& pr) const {\n"
+      << "    " << ctype(odt) << " r[4];\n"
+      << "#pragma unroll\n    for (int e = 0; e < 4; ++e) {\n      const int64_t nn = n + e;\n"
+      << "      if (!FULL && nn >= a.N) { r[e] = 0; continue; }\n"
+      << body.str()
+      << "      r[e] = " << expr[v] << ";\n    }\n"
+      << "    " << stype(odt) << "* o = (" << stype(odt) << "*)a.out + bb * a.so_b + m * a.so_m + n;\n";
+  if (vec)
+    src << "    if (FULL || n + 3 < a.N) {\n"
+        << "      struct __attribute__((aligned(4 * sizeof(" << stype(odt) << ")))) V { " << stype(odt) << " x[4]; } w;\n"
+        << "#pragma unroll\n      for (int e = 0; e < 4; ++e) w.x[e] = " << store_expr(odt, "r[e]") << ";\n"
+        << "      *(V*)o = w;\n      return;\n    }\n";
+  src << "#pragma unroll\n    for (int e = 0; e < 4; ++e)\n      if (FULL || n + e < a.N) o[e] = " << store_expr(odt, "r[e]")
+      << ";\n  }\n};\n}  // namespace ghip\n";
+  src << "extern \"C\" __global__ void __launch_bounds__(" << nt << ", 1) gemm_epilogue(ghip::GemmParams p, ghip::EpiArgs a) {\n"
+      << "  const ghip::GenEpi epi{a};\n"
+      << "  ghip::gemm_bf16_body<" << BM << ", " << BN << ", " << WM << ", " << WN << ", " << (ma ? "true" : "false") << ", "
+      << (mb ? "true" : "false") << ", " << NB << ">(p, epi);\n}\n";
+  RtcKernel kern;
+  if (rtc_get(be, src.str(), "gemm_epilogue", &kern, err) != GHIP_OK) {
+    failed = true;
+    return View{};
+  }
+
+  View y = fresh(os);
+  GemmParams gp{};
+  gp.sa_b = d.sab; gp.sa_m = d.sam; gp.sa_k = d.sak;
+  gp.sb_b = d.sbb; gp.sb_k = d.sbk; gp.sb_n = d.sbn;
+  gp.batch = d.B; gp.M = d.M; gp.N = d.N; gp.K = d.K;
+  gp.tiles_m = static_cast<int>((d.M + BM - 1) / BM);
+  gp.tiles_n = static_cast<int>((d.N + BN - 1) / BN);
+  gp.a_extent = static_cast<uint32_t>(ea);
+  gp.b_extent = static_cast<uint32_t>(eb);
+  const int64_t blocks = d.B * gp.tiles_m * gp.tiles_n;
+  const int64_t so_b = d.M * d.N, so_m = d.N;
+  const View lv = d.lv, rv0 = d.rv, rv1 = dp[NB - 1].rv;
+  std::vector<int> rd{lv.slot, rv0.slot};
+  if (NB == 2) rd.push_back(rv1.slot);
+  for (auto& in : ins) rd.push_back(in.view.slot);
+  std::ostringstream desc;
+  desc << fmt("gemm_batched+epilogue bf16 B=%lld M=%lld N=%lld K=%lld dots=%d tile=%dx%d (%s) ops=%zu inputs=%zu [",
+              (long long)d.B, (long long)d.M, (long long)d.N, (long long)d.K, NB, BM, BN * NB, d.how.c_str(), mem.size(),
+              ins.size());
+  for (size_t i = 0; i < mem.size(); ++i) {
+    const Node& n = N[mem[i]];
+    desc << (i ? "," : "") << kind_name(n.kind);
+    if (n.kind == Kind::Unary || n.kind == Kind::Binary || n.kind == Kind::Compare) desc << "#" << n.sub;
+  }
+  desc << "]";
+  add_step(desc.str(), rd, {y.slot}, [=](ExecState& st, GHipError* e) -> int {
+    GemmParams p = gp;
+    p.a = st.ptr(lv, GHIP_DTYPE_BFLOAT16);
+    p.b = st.ptr(rv0, GHIP_DTYPE_BFLOAT16);
+    p.b1 = st.ptr(rv1, GHIP_DTYPE_BFLOAT16);
+    p.c = st.ptr(y, odt);
+    if ((reinterpret_cast<uintptr_t>(p.a) | reinterpret_cast<uintptr_t>(p.b) | reinterpret_cast<uintptr_t>(p.b1)) & 15u)
+      return set_error(e, GHIP_ERR_STATE, "fused GEMM epilogue: operand base not 16-byte aligned");
+    EpiArgs a{};
+    for (size_t k = 0; k < ins.size(); ++k) {
+      const int es = dtype_size(ins[k].dt);
+      a.in[k] = st.ptr(ins[k].view, ins[k].dt);
+      a.s_b[k] = ins[k].sb;
+      a.s_m[k] = ins[k].sm;
+      a.s_n[k] = ins[k].sn;
+      a.vin[k] = ins[k].vin;
+      if (ins[k].vin && reinterpret_cast<uintptr_t>(a.in[k]) % (4 * es) != 0)
+        return set_error(e, GHIP_ERR_STATE, "fused GEMM epilogue: operand %zu not %d-byte aligned", k, 4 * es);
+    }
+    a.out = p.c;
+    a.so_b = so_b;
+    a.so_m = so_m;
+    a.N = p.N;
+    a.vec = vec;
+    if (vec && reinterpret_cast<uintptr_t>(p.c) % (4 * dtype_size(odt)) != 0)
+      return set_error(e, GHIP_ERR_STATE, "fused GEMM epilogue: output not %d-byte aligned", 4 * dtype_size(odt));
+    void* args[] = {&p, &a};
+    hipError_t h = hipModuleLaunchKernel(kern.func, static_cast<unsigned>(blocks), 1, 1, nt, 1, 1, 0, st.stream, args,
+                                         nullptr);
+    if (h != hipSuccess) return check_hip(h, e, "fused GEMM epilogue launch");
+    return GHIP_OK;
+  });
+  for (int k = 0; k < NB; ++k) have[dots[k]] = 1;  // consumed here; never materialised
+  *fused = true;
   return y;
 }
 
@@ -1349,6 +1655,10 @@ int Lowerer::finish() {
 
 int lower(GHipBackend* be, GHipFunction* fn, Plan* plan, GHipError* err) {
   Lowerer L(be, fn, plan, err);
+  // GHIP_EPILOGUE_FUSION=0 keeps every DotGeneral a stand-alone GEMM (the
+  // unfused plan the fused one is checked against).
+  const char* ef = getenv("GHIP_EPILOGUE_FUSION");
+  L.fuse_epilogues = !(ef && ef[0] == '0');
   L.have.assign(fn->nodes.size(), 0);
   L.views.assign(fn->nodes.size(), View{});
   L.analyse();

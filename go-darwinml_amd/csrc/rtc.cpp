@@ -8,6 +8,10 @@
 #include <hip/hip_runtime.h>
 #include <hip/hiprtc.h>
 
+#include <stdio.h>
+#include <stdlib.h>
+
+#include <functional>
 #include <map>
 #include <mutex>
 #include <string>
@@ -38,6 +42,16 @@ int rtc_get(GHipBackend* be, const std::string& src, const std::string& entry, R
   std::lock_guard<std::mutex> lk(g_mu);
   Entry& e = g_cache[src];
   if (e.code.empty()) {
+    // GHIP_RTC_DUMP=<dir>: keep a copy of every generated source (for reading
+    // the generated code and its ISA offline).
+    if (const char* dir = getenv("GHIP_RTC_DUMP")) {
+      const std::string path = std::string(dir) + "/" + entry + "_" +
+                               std::to_string(std::hash<std::string>()(src)) + ".hip";
+      if (FILE* f = fopen(path.c_str(), "w")) {
+        fwrite(src.data(), 1, src.size(), f);
+        fclose(f);
+      }
+    }
     hiprtcProgram prog;
     if (hiprtcCreateProgram(&prog, src.c_str(), "fused.hip", 0, nullptr, nullptr) != HIPRTC_SUCCESS) {
       g_cache.erase(src);

@@ -343,6 +343,24 @@ def test_execute_errors(be):                                      # executable.g
         ex.Execute([bad], None, 0)
 
 
+def test_bf16_rounding_all_upper_halves(be):
+    """fp32 -> bf16 in generated kernels (gfx950 v_cvt_pk_bf16_f32) against the
+    oracle's integer round-to-nearest-even: every one of the 2^16 upper halves
+    (all signs, exponents, mantissa tops: zeros, denormals, carries into the
+    exponent, overflow to inf, every NaN payload) with lower halves that are
+    exact, below / at / above the tie, and odd/even-tie cases, bit for bit."""
+    hi = np.arange(1 << 16, dtype=np.uint32) << np.uint32(16)
+    lo = np.array([0, 1, 0x3FFF, 0x7FFF, 0x8000, 0x8001, 0xBFFF, 0xFFFF, 0x4000, 0xC000, 0x0002, 0x7FFE,
+                   0x1234, 0x9ABC, 0x5555, 0xAAAA], np.uint32)
+    u = (hi[:, None] | lo[None, :]).reshape(-1)
+    x = u.view(np.float32)
+    s = make_shape(F32, x.size)
+    (y,) = run(be, lambda f, a: [f.ConvertDType(a, BF16)], [(x, s)])
+    want = orc.f32_to_bf16_bits(x)
+    got = synth.to_bf16_bits(y)  # y holds the bf16 values widened exactly to fp32
+    assert np.array_equal(got, want)
+
+
 # ------------------------------------------------------------ transformer block
 def _bf(a):
     return synth.round_bf16(np.asarray(a, np.float32))

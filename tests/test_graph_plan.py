@@ -144,14 +144,21 @@ def test_elementwise_chain_is_one_kernel(be):
     assert p.count("fused_elementwise") == 1 and "ops=3 inputs=2" in p
 
 
-def test_transformer_block_plan(be):
-    e = graphs.transformer_block(be, graphs.TransformerBlockConfig(batch=2, seq=64, vocab=100,
-                                                                   d_model=128, heads=2, head_dim=64,
-                                                                   ffn=256))
+def test_transformer_block_plan(be, monkeypatch):
+    cfg = graphs.TransformerBlockConfig(batch=2, seq=64, vocab=100, d_model=128, heads=2, head_dim=64, ffn=256)
+    e = graphs.transformer_block(be, cfg)
     p = e.Plan()
     assert p.count("rmsnorm_rows") == 2
-    assert p.count("gemm_batched") == 9
+    # Q, K, V and the two attention products stay plain GEMMs; the residual adds
+    # and SiLU(gate) * up run as GEMM epilogues (gate and up in one kernel).
+    assert p.count("gemm_batched bfloat16") == 5
+    assert p.count("gemm_batched+epilogue") == 3 and p.count("dots=2") == 1
+    assert "fused_elementwise" not in p
     assert "scale_mask_softmax_rows" in p and "causal=1" in p
+    monkeypatch.setenv("GHIP_EPILOGUE_FUSION", "0")
+    u = graphs.transformer_block(be, cfg).Plan()
+    assert u.count("gemm_batched bfloat16") == 9 and "gemm_batched+epilogue" not in u
+    assert u.count("fused_elementwise") == 3
     assert "gather_rows" in p
     assert e.Outputs()[0].dims == (2, 64, 128)
     assert [s.dims for s in e.Inputs()][:2] == [(2, 64), (100, 128)]
