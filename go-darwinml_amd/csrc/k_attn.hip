@@ -16,12 +16,16 @@
 //     without leaving registers: the 16 values a lane holds for key step s are
 //     keys 16s + {0..3, 8..11} + 4 * (lane / 32), and V^T is read in that same key
 //     order with two ds_read_b64_tr_b16 per fragment;
-//   * K / V tiles arrive by buffer_load ... lds (16 B per lane, out-of-range keys
-//     read zeros) into two LDS stages, XOR-swizzled so the ds_read_b128 (K) and
-//     transpose reads (V) are bank-conflict free;
+//   * K / V tiles arrive by buffer_load ... lds (16 B per lane; keys past Sk lie
+//     beyond the buffer descriptor's extent and read zeros) into two LDS stages,
+//     XOR-swizzled so the ds_read_b128 (K) and transpose reads (V) are
+//     bank-conflict free;
+//   * the output rescale of the online softmax is lazy: the reference max moves
+//     only when a tile's max exceeds it by more than 2^8 (exponents stay <= 2^8);
 //   * causal: tiles past a workgroup's last query are never loaded, a wave skips
 //     the tiles past its own last query, and only diagonal tiles apply the
-//     element mask; query blocks run longest-first.
+//     element mask; the grid runs all (batch, head) pairs of the last query block
+//     first, so the longest workgroups start first.
 #include "common.h"
 
 #define GHIP_ALDS __attribute__((address_space(3)))
@@ -54,7 +58,7 @@ constexpr int kBKV = 64;    // keys per tile
 constexpr int kQW = 32;     // queries per wave
 constexpr int kWaves = 4;   // waves per workgroup
 constexpr int kBQ = kQW * kWaves;
-constexpr uint32_t kOffOOB = 0x80000000u;
+constexpr float kLazyLog2 = 8.f;  // the reference max may trail the true max by 2^8
 
 __device__ __forceinline__ i32x4_t make_rsrc(const void* base, uint32_t bytes) {
   const uint64_t b = reinterpret_cast<uint64_t>(base);
@@ -65,12 +69,11 @@ __device__ __forceinline__ i32x4_t make_rsrc(const void* base, uint32_t bytes) {
   r.w = 0x00020000;
   return r;
 }
-// 16 bytes per lane from buffer offset voff straight into LDS at lds + lane*16.
-__device__ __forceinline__ void dma16(i32x4_t rsrc, const void* lds, uint32_t voff) {
-  const uint32_t la = static_cast<uint32_t>(reinterpret_cast<uintptr_t>((GHIP_ALDS const void*)lds));
+// 16 bytes per lane from buffer offset voff straight into LDS byte address
+// la + lane*16 (la wave-uniform).
+__device__ __forceinline__ void dma16(i32x4_t rsrc, uint32_t la, uint32_t voff) {
   asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
-               ::"s"(__builtin_amdgcn_readfirstlane(la)), "v"(voff), "s"(rsrc)
-               : "memory", "m0");
+               ::"s"(la), "v"(voff), "s"(rsrc) : "memory", "m0");
 }
 
 // LDS tiles are [64 keys][128 d] bf16: 256-byte rows of 16 chunks of 16 B.
@@ -80,23 +83,6 @@ __device__ __forceinline__ int swz_k(int r) { return r & 15; }
 // V: chunk j of key row r sits at slot j ^ {0, 6, 10, 12}[r & 3] (a transpose read
 // touches 4 consecutive rows x 2-4 chunks).
 __device__ __forceinline__ int swz_v(int r) { return (0xCA60u >> ((r & 3) * 4)) & 15u; }
-
-// One 16 KiB tile = 16 wave-instructions of 1 KiB (4 key rows each), 4 per wave.
-// Lane l of instruction blk fills bytes l*16.. of LDS block blk, so the swizzle is
-// applied by choosing the global chunk it fetches.
-template <bool IS_V>
-__device__ __forceinline__ void load_tile(i32x4_t rs, uint16_t* lds, int wave, int lane,
-                                          int keys_left, int64_t s_ss) {
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int blk = wave * 4 + i;
-    const int r = blk * 4 + lane / 16;
-    const int c = lane % 16;
-    const int chunk = IS_V ? (c ^ swz_v(r)) : (c ^ swz_k(r));
-    const uint32_t off = static_cast<uint32_t>((static_cast<int64_t>(r) * s_ss + chunk * 8) * 2);
-    dma16(rs, lds + blk * 512, r < keys_left ? off : kOffOOB);
-  }
-}
 
 // K fragment (A operand of S^T = K Q^T): key row kb*32 + lane%32, d = 16s + 8*(lane/32).
 __device__ __forceinline__ bf16x8_t frag_k(const uint16_t* lds, int kb, int s, int lane) {
@@ -119,16 +105,19 @@ __device__ __forceinline__ bf16x8_t frag_v(const uint16_t* lds, int db, int s, i
 }
 
 __global__ __launch_bounds__(256, 2) void sdpa_fwd_kernel(Params p) {
-  __shared__ __attribute__((aligned(1024))) uint16_t sk[2][kBKV * kD];
-  __shared__ __attribute__((aligned(1024))) uint16_t sv[2][kBKV * kD];
+  // [stage][K | V][64 keys x 128 d]
+  __shared__ __attribute__((aligned(1024))) uint16_t smem[2][2][kBKV * kD];
+  const uint32_t lds0 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>((GHIP_ALDS void*)&smem[0][0][0]));
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int h2 = lane >> 5;  // half of the wave
   const int nqb = (p.Sq + kBQ - 1) / kBQ;
-  const int qb = p.causal ? (nqb - 1 - static_cast<int>(blockIdx.x % nqb))
-                          : static_cast<int>(blockIdx.x % nqb);
-  const int bh = blockIdx.x / nqb;
+  const int nbh = p.B * p.H;
+  // Longest first over the whole grid: every (batch, head) of the last query
+  // block, then of the one before it, ... (causal: later blocks see more keys).
+  const int qb = p.causal ? (nqb - 1 - static_cast<int>(blockIdx.x / nbh)) : static_cast<int>(blockIdx.x / nbh);
+  const int bh = blockIdx.x % nbh;
   const int b = bh / p.H, h = bh % p.H;
   const int hk = h / (p.H / p.Hkv);
   const int q0 = qb * kBQ;
@@ -155,13 +144,28 @@ __global__ __launch_bounds__(256, 2) void sdpa_fwd_kernel(Params p) {
   // is folded into one FMA per exponent: exp2(s * c - m * c).
   const float c = p.scale_log2;
 
+  // Per-lane byte offsets of this wave's 4 K and 4 V DMA instructions within a
+  // tile (instruction i fills key rows 4 (4 wave + i) .. +4, 16 lanes per row).
+  // Keys past Sk lie beyond the descriptor's extent and read zeros.
+  uint32_t koff[4], voff[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int r = (wave * 4 + i) * 4 + lane / 16;
+    const int cc = lane % 16;
+    koff[i] = static_cast<uint32_t>((static_cast<int64_t>(r) * p.k_ss + (cc ^ swz_k(r)) * 8) * 2);
+    voff[i] = static_cast<uint32_t>((static_cast<int64_t>(r) * p.v_ss + (cc ^ swz_v(r)) * 8) * 2);
+  }
+  const uint32_t kstep = static_cast<uint32_t>(kBKV * p.k_ss * 2), vstep = static_cast<uint32_t>(kBKV * p.v_ss * 2);
   auto issue = [&](int t, int st) {
-    const int64_t key0 = static_cast<int64_t>(t) * kBKV;
-    const int left = static_cast<int>(p.Sk - key0);
-    const uint32_t dk = static_cast<uint32_t>(key0 * p.k_ss * 2);
-    const uint32_t dv = static_cast<uint32_t>(key0 * p.v_ss * 2);
-    load_tile<false>(make_rsrc(Kb + key0 * p.k_ss, p.k_extent - dk), sk[st], wave, lane, left, p.k_ss);
-    load_tile<true>(make_rsrc(Vb + key0 * p.v_ss, p.v_extent - dv), sv[st], wave, lane, left, p.v_ss);
+    const uint32_t dk = static_cast<uint32_t>(t) * kstep, dv = static_cast<uint32_t>(t) * vstep;
+    const i32x4_t rk = make_rsrc(reinterpret_cast<const char*>(Kb) + dk, p.k_extent - dk);
+    const i32x4_t rv = make_rsrc(reinterpret_cast<const char*>(Vb) + dv, p.v_extent - dv);
+    const uint32_t lk = lds0 + static_cast<uint32_t>(st) * (2 * kBKV * kD * 2) + wave * 4 * 1024;
+    const uint32_t lv = lk + kBKV * kD * 2;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) dma16(rk, lk + i * 1024, koff[i]);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) dma16(rv, lv + i * 1024, voff[i]);
   };
 
   f32x16_t o[kD / 32];
@@ -169,7 +173,7 @@ __global__ __launch_bounds__(256, 2) void sdpa_fwd_kernel(Params p) {
   for (int db = 0; db < kD / 32; ++db)
 #pragma unroll
     for (int v = 0; v < 16; ++v) o[db][v] = 0.f;
-  float m = -INFINITY;  // running max of the raw scores of query qi
+  float m = -INFINITY;  // reference max (raw scores) the exponents are taken against
   float l = 0.f;        // running sum over this half-wave's keys
 
   // One barrier per tile: at the top of tile t every wave has finished tile t-1,
@@ -182,6 +186,8 @@ __global__ __launch_bounds__(256, 2) void sdpa_fwd_kernel(Params p) {
     // Causal: a wave whose last query precedes the tile's first key has nothing to
     // do here (it still takes part in the barriers and loads).
     if (p.causal && key0 > qw + kQW - 1) return;
+    const uint16_t* sk = &smem[st][0][0];
+    const uint16_t* sv = &smem[st][1][0];
     f32x16_t s0, s1;
 #pragma unroll
     for (int v = 0; v < 16; ++v) {
@@ -190,30 +196,44 @@ __global__ __launch_bounds__(256, 2) void sdpa_fwd_kernel(Params p) {
     }
 #pragma unroll
     for (int s = 0; s < kD / 16; ++s) {
-      s0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(frag_k(sk[st], 0, s, lane), qf[s], s0, 0, 0, 0);
-      s1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(frag_k(sk[st], 1, s, lane), qf[s], s1, 0, 0, 0);
+      s0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(frag_k(sk, 0, s, lane), qf[s], s0, 0, 0, 0);
+      s1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(frag_k(sk, 1, s, lane), qf[s], s1, 0, 0, 0);
     }
-    // s{kb}[v] is key key0 + 32 kb + (v/4)*8 + 4 h2 + v%4 for query qi; only the
-    // diagonal tile(s) and a ragged last tile need the element mask.
+    // s{kb}[v] is key key0 + 32 kb + 4 h2 + kv, kv = (v/4)*8 + v%4, for query qi;
+    // only the diagonal tile(s) and a ragged last tile need the element mask:
+    // visible iff kv (+32 for s1) < lim.
     if ((p.causal && key0 + kBKV - 1 > qw) || key0 + kBKV > p.Sk) {
+      const int lim = min(p.Sk, p.causal ? qi + 1 : p.Sk) - key0 - 4 * h2;
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
-        const int kr = (v >> 2) * 8 + 4 * h2 + (v & 3);
-        const int ka = key0 + kr, kc = key0 + 32 + kr;
-        if (ka >= p.Sk || (p.causal && ka > qi)) s0[v] = -INFINITY;
-        if (kc >= p.Sk || (p.causal && kc > qi)) s1[v] = -INFINITY;
+        const int kv = (v >> 2) * 8 + (v & 3);
+        s0[v] = kv < lim ? s0[v] : -INFINITY;
+        s1[v] = kv + 32 < lim ? s1[v] : -INFINITY;
       }
     }
+    // v_max3_f32 directly: fmaxf would first quiet every MFMA result with a
+    // second v_max (MFMA results are never signaling NaNs).
     float mx = -INFINITY;
 #pragma unroll
-    for (int v = 0; v < 16; ++v) mx = fmaxf(mx, fmaxf(s0[v], s1[v]));
+    for (int v = 0; v < 16; ++v) asm("v_max3_f32 %0, %1, %2, %3" : "=v"(mx) : "v"(mx), "v"(s0[v]), "v"(s1[v]));
     mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-    const float mnew = fmaxf(m, mx);
+    // Lazy rescale: the reference max only moves (with o and l rescaled) when
+    // some lane's tile max exceeds it by more than kLazyLog2, so exponents stay
+    // <= 2^kLazyLog2 and the 64 multiplies of the rescale are rare.  The result
+    // o / l does not depend on the reference chosen.
+    if (__builtin_amdgcn_ballot_w64((mx - m) * c > kLazyLog2)) {
+      const float mnew = fmaxf(m, mx);
+      // v_exp_f32 directly: weights below 2^-126 flush to zero.
+      const float alpha = mnew == -INFINITY ? 1.f : __builtin_amdgcn_exp2f((m - mnew) * c);
+      m = mnew;
+      l *= alpha;
+#pragma unroll
+      for (int db = 0; db < kD / 32; ++db)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) o[db][v] *= alpha;
+    }
     // A query with nothing unmasked yet keeps m = -inf and exponent offset 0.
-    const float nb = mnew == -INFINITY ? 0.f : -mnew * c;
-    // v_exp_f32 directly: weights below 2^-126 flush to zero.
-    const float alpha = __builtin_amdgcn_exp2f(__builtin_fmaf(m, c, nb));
-    m = mnew;
+    const float nb = m == -INFINITY ? 0.f : -m * c;
     float ls = 0.f;
 #pragma unroll
     for (int v = 0; v < 16; ++v) {
@@ -223,14 +243,7 @@ __global__ __launch_bounds__(256, 2) void sdpa_fwd_kernel(Params p) {
       s0[v] = e0;
       s1[v] = e1;
     }
-    l = l * alpha + ls;
-    // The output rescale is a no-op unless some lane's max moved.
-    if (__builtin_amdgcn_ballot_w64(alpha != 1.f)) {
-#pragma unroll
-      for (int db = 0; db < kD / 32; ++db)
-#pragma unroll
-        for (int v = 0; v < 16; ++v) o[db][v] *= alpha;
-    }
+    l += ls;
     // P^T operand of key step s: s{s/2}[8 (s%2) .. +8] rounded to bf16.
     bf16x8_t pb[4];
 #pragma unroll
@@ -244,7 +257,7 @@ __global__ __launch_bounds__(256, 2) void sdpa_fwd_kernel(Params p) {
     for (int s = 0; s < kBKV / 16; ++s)
 #pragma unroll
       for (int db = 0; db < kD / 32; ++db)
-        o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(frag_v(sv[st], db, s, lane), pb[s], o[db], 0, 0, 0);
+        o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(frag_v(sv, db, s, lane), pb[s], o[db], 0, 0, 0);
     // This stage's LDS reads complete before the next barrier, after which it is
     // refilled.
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
