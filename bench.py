@@ -60,9 +60,12 @@ class Case:
 
     def __init__(self, name, launch, bytes_per_step=0, flops_per_step=0, bound="hbm",
                  peak=HBM_PEAK_GBS, dtype="f32", rotation=1, config=None, kernel="",
-                 out=None, stream=None):
+                 out=None, stream=None, executed_flops_per_step=None):
         self.name, self.launch = name, launch
         self.bytes, self.flops = bytes_per_step, flops_per_step
+        # MFMA work actually executed when it is less than the algorithmic flops
+        # (causal attention skips the masked half of the score matrix).
+        self.executed_flops = executed_flops_per_step
         self.bound, self.peak, self.dtype = bound, peak, dtype
         self.rotation, self.config, self.kernel = rotation, config or {}, kernel
         self.out = out
@@ -243,6 +246,7 @@ def make_cases(only=None):
         o = torch.empty_like(q)
         return Case("attention_bf16", lambda i: ops.sdpa(q, k, v, D ** -0.5, True, out=o),
                     flops_per_step=2 * 2 * B * H * S * S * D, bound="mfma",
+                    executed_flops_per_step=2 * 2 * B * H * D * S * (S + 1) // 2,
                     peak=BF16_PEAK_TFLOPS, dtype="bf16", kernel="sdpa_fwd_kernel",
                     config={"workload": "SDPA causal B4 H16 S2048 D128 bf16, one fused kernel "
                                         "(Q.K^T, scale, causal mask, online softmax, P.V); flops "
@@ -273,7 +277,9 @@ def make_cases(only=None):
         def launch(i):
             (y,) = ex.Execute(bufs, None, 0)
             be.BufferFinalize(y)  # back to the caching allocator; stream order protects reuse
+        S, causal_attn = cfg.seq, 2 * 2 * cfg.batch * cfg.heads * cfg.seq * cfg.seq * cfg.head_dim
         case = Case("transformer_block_bf16", launch, flops_per_step=cfg.flops(), bound="mfma",
+                    executed_flops_per_step=cfg.flops() - causal_attn + causal_attn * (S + 1) // (2 * S),
                     peak=BF16_PEAK_TFLOPS, dtype="bf16", kernel="graph Execute (all kernels)",
                     stream=stream,
                     config={"workload": "decoder block B8 S1024 d2048 H16 Dh128 FFN 8192 bf16 "
@@ -364,12 +370,18 @@ def main():
             case = builders[name]()
             steps = args.steps if case.bound == "hbm" else max(5, args.steps // 20)
             r = time_case(case, steps, max(2, args.warmup // 2), args.eager)
-            secondary.append({"name": name, "dtype": case.dtype, "steps": r["steps"],
-                              "graph": r["graph"],
-                              "launch_us": round(r["launch_us"], 2),
-                              "value": r["roofline"]["achieved"], "unit": r["roofline"]["unit"],
-                              "roofline": r["roofline"], "rotation": case.rotation,
-                              "kernel": case.kernel, "config": case.config})
+            entry = {"name": name, "dtype": case.dtype, "steps": r["steps"],
+                     "graph": r["graph"],
+                     "launch_us": round(r["launch_us"], 2),
+                     "value": r["roofline"]["achieved"], "unit": r["roofline"]["unit"],
+                     "roofline": r["roofline"], "rotation": case.rotation,
+                     "kernel": case.kernel, "config": case.config}
+            if case.executed_flops:
+                # MFMA utilisation by the work actually executed (causal half only)
+                ex_tf = r["roofline"]["achieved"] * case.executed_flops / case.flops
+                entry["executed"] = {"achieved": round(ex_tf, 2), "unit": "TFLOP/s",
+                                     "frac": round(ex_tf / case.peak, 4)}
+            secondary.append(entry)
             del case
             torch.cuda.empty_cache()
     cpu = None if args.no_cpu else cpu_baseline()

@@ -3,7 +3,7 @@
 // bf16 path (the MFMA path the metric is quoted on): the core lives in
 // gemm_bf16_dev.h (shared with the Compile-time generated epilogue GEMMs); the
 // kernels here instantiate it with a plain store epilogue.
-// fp32 path: v_mfma_f32_32x32x2f32 with MN-major LDS tiles (one float per lane).
+// fp32 path: v_mfma_f32_32x32x2f32 over LDS-DMA tiles (below).
 // Anything the vector paths cannot address (odd strides, unaligned bases,
 // negative strides, > 2 GiB per batch slice) runs a generic LDS-tiled kernel.
 #include "common.h"
@@ -53,77 +53,119 @@ __global__ __launch_bounds__(WM* WN * 64, 1) void gemm_bf16_kernel(GemmParams p)
 }
 
 // ---------------------------------------------------------------------------
-// fp32 MFMA path: 128x128x32 tiles, 4 waves (2x2, 64x64 each),
-// v_mfma_f32_32x32x2f32.  LDS tiles are MN-major [k][row] so a fragment read is
-// 32 consecutive floats.
+// fp32 MFMA path: v_mfma_f32_32x32x2f32, 32-deep k-tiles by buffer_load ... lds
+// (two stages), operands swapped like the bf16 path so a lane stores 4 adjacent
+// columns.  K-contiguous tiles are [rows][32 k] with 16-byte chunks XOR-swizzled
+// per row; one ds_read_b128 hands a lane the 4 k of 4 consecutive MFMA steps
+// (lanes 0-31 take k = 8g + e, lanes 32-63 k = 8g + 4 + e at step e: both operands
+// use the same k order, so the contraction is unchanged).  MN-contiguous tiles
+// stay [32 k][rows] and are read one k per step (ds_read_b32, 128 contiguous
+// bytes per half-wave).
 // ---------------------------------------------------------------------------
 constexpr int kBK32 = 32;
 
-template <int R, int T, bool KCONTIG>
-struct TileLoaderF32 {
-  // K-contiguous: float4 along k for one row; LD = R + 1 (scalar LDS writes).
-  // MN-contiguous: float4 along rows for one k; LD = R + 4 (vector LDS writes).
-  static constexpr int kLD = KCONTIG ? R + 1 : R + 4;
-  static constexpr int kUnits = R * kBK32 / 4;
-  static constexpr int kPer = (kUnits + T - 1) / T;
-  float4 r[kPer];
+// 32-bit LDS address form of dma16 (the generic-pointer form costs SGPRs here).
+__device__ __forceinline__ void dma16_la(i32x4_t rsrc, uint32_t la, uint32_t voff) {
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+               ::"s"(la), "v"(voff), "s"(rsrc) : "memory", "m0");
+}
 
-  __device__ __forceinline__ void load(const float* base, int64_t s_row, int64_t s_k,
-                                       int64_t rows_left, int64_t k_left, int tid) {
+// R rows x 32 k fp32 tile, split over NW waves in 1 KiB DMA instructions.
+template <int R, bool KC, int NW>
+struct TileF32 {
+  static constexpr int kInstr = R * kBK32 * 4 / 1024;
+  static constexpr int kPerWave = kInstr / NW;
+  static_assert(kInstr % NW == 0, "tile must split evenly over waves");
+  static_assert(KC || (R >= 16 && R <= 256), "MN-major: 1..4 k-rows per instruction");
+  uint32_t voff[kPerWave];
+  int rowv[kPerWave], kv[kPerWave];  // first row / k each lane's chunk holds
+
+  __device__ __forceinline__ void init(int wave, int lane, int64_t s_mn, int64_t s_k) {
 #pragma unroll
-    for (int i = 0; i < kPer; ++i) {
-      const int u = tid + i * T;
-      if constexpr (KCONTIG) {
-        const int row = u / (kBK32 / 4), kc = u % (kBK32 / 4);
-        const bool ok = u < kUnits && row < rows_left && kc * 4 < k_left;
-        r[i] = ok ? *reinterpret_cast<const float4*>(base + row * s_row + kc * 4)
-                  : make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int i = 0; i < kPerWave; ++i) {
+      const int blk = wave * kPerWave + i;
+      if constexpr (KC) {  // 8 rows of 8 chunks per instruction; slot pc holds chunk pc ^ (r & 7)
+        const int r = blk * 8 + lane / 8, c = (lane % 8) ^ (r & 7);
+        rowv[i] = r;
+        kv[i] = c * 4;
+        voff[i] = static_cast<uint32_t>((r * s_mn + c * 4) * 4);
       } else {
-        const int rg = u % (R / 4), k = u / (R / 4);
-        const bool ok = u < kUnits && rg * 4 < rows_left && k < k_left;
-        r[i] = ok ? *reinterpret_cast<const float4*>(base + k * s_k + rg * 4)
-                  : make_float4(0.f, 0.f, 0.f, 0.f);
+        constexpr int kCPR = R / 4, kRPI = 64 / kCPR;  // chunks per k-row, k-rows per instruction
+        const int k = blk * kRPI + lane / kCPR, ch = lane % kCPR;
+        rowv[i] = ch * 4;
+        kv[i] = k;
+        voff[i] = static_cast<uint32_t>((k * s_k + ch * 4) * 4);
       }
     }
   }
-  __device__ __forceinline__ void store(float* lds, int tid) const {
+  __device__ __forceinline__ void issue(i32x4_t rs, uint32_t lds, int wave, bool full, int rows_left,
+                                        int k_left) const {
 #pragma unroll
-    for (int i = 0; i < kPer; ++i) {
-      const int u = tid + i * T;
-      if (u >= kUnits) continue;
-      if constexpr (KCONTIG) {
-        const int row = u / (kBK32 / 4), kc = u % (kBK32 / 4);
-        lds[(kc * 4 + 0) * kLD + row] = r[i].x;
-        lds[(kc * 4 + 1) * kLD + row] = r[i].y;
-        lds[(kc * 4 + 2) * kLD + row] = r[i].z;
-        lds[(kc * 4 + 3) * kLD + row] = r[i].w;
-      } else {
-        const int rg = u % (R / 4), k = u / (R / 4);
-        *reinterpret_cast<float4*>(lds + k * kLD + rg * 4) = r[i];
-      }
+    for (int i = 0; i < kPerWave; ++i) {
+      const bool ok = rowv[i] < rows_left && kv[i] < k_left;
+      dma16_la(rs, lds + (wave * kPerWave + i) * 1024, (full || ok) ? voff[i] : kOffOOB);
     }
   }
 };
 
-template <bool A_K, bool B_K, typename OutT>
-__global__ __launch_bounds__(256) void gemm_f32_kernel(GemmParams p) {
-  constexpr int BM = 128, BN = 128, T = 256, WN = 2;
-  constexpr int TM = 64, TN = 64, FM = 2, FN = 2;
-  using LA = TileLoaderF32<BM, T, A_K>;
-  using LB = TileLoaderF32<BN, T, B_K>;
-  constexpr int SA = kBK32 * LA::kLD, SB = kBK32 * LB::kLD;
-  __shared__ __attribute__((aligned(16))) float lds[2][SA + SB];
+// K-contiguous fragment, group g (k 8g .. 8g+7) of the 32-row block at rbase.
+__device__ __forceinline__ float4 frag_f32_kc(const float* lds, int rbase, int g, int lane) {
+  const int r = rbase + (lane & 31);
+  const int c = (2 * g + (lane >> 5)) ^ (r & 7);
+  return *reinterpret_cast<const float4*>(lds + r * kBK32 + c * 4);
+}
+// MN-contiguous fragment at step e of group g.
+template <int R>
+__device__ __forceinline__ float frag_f32_mn(const float* lds, int rbase, int g, int e, int lane) {
+  return lds[(8 * g + 4 * (lane >> 5) + e) * R + rbase + (lane & 31)];
+}
+__device__ __forceinline__ float f4_at(const float4& v, int e) {
+  return e == 0 ? v.x : e == 1 ? v.y : e == 2 ? v.z : v.w;
+}
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+template <int BM, int BN, int WM, int WN, bool A_K, bool B_K, typename OutT>
+__global__ __launch_bounds__(WM* WN * 64, (WM * WN == 4 ? 2 : 1)) void gemm_f32_kernel(GemmParams p) {
+  constexpr int NW = WM * WN;
+  constexpr int TM = BM / WM, TN = BN / WN;
+  constexpr int FM = TM / 32, FN = TN / 32;
+  using TA = TileF32<BM, A_K, NW>;
+  using TB = TileF32<BN, B_K, NW>;
+  constexpr int LPW = TA::kPerWave + TB::kPerWave;
+  constexpr int SA = BM * kBK32, SB = BN * kBK32;  // floats per stage
+  __shared__ __attribute__((aligned(1024))) float smem[2][SA + SB];
+  const uint32_t lds0 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>((GHIP_LDS void*)&smem[0][0]));
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int wm = wave / WN, wn = wave % WN;
   int64_t bb;
   int tm, tn;
   map_tile(blockIdx.x, p.batch * p.tiles_m * p.tiles_n, p.tiles_m, p.tiles_n, bb, tm, tn);
   const int64_t m0 = static_cast<int64_t>(tm) * BM, n0 = static_cast<int64_t>(tn) * BN;
-  const float* A = static_cast<const float*>(p.a) + bb * p.sa_b + m0 * p.sa_m;
-  const float* B = static_cast<const float*>(p.b) + bb * p.sb_b + n0 * p.sb_n;
-  LA la;
-  LB lb;
+  const float* A0 = static_cast<const float*>(p.a) + bb * p.sa_b + m0 * p.sa_m;
+  const float* B0 = static_cast<const float*>(p.b) + bb * p.sb_b + n0 * p.sb_n;
+  const uint32_t a_left0 = p.a_extent - static_cast<uint32_t>(m0 * p.sa_m * 4);
+  const uint32_t b_left0 = p.b_extent - static_cast<uint32_t>(n0 * p.sb_n * 4);
+  TA ta;
+  TB tb;
+  ta.init(wave, lane, p.sa_m, p.sa_k);
+  tb.init(wave, lane, p.sb_n, p.sb_k);
+  const int rows_a = static_cast<int>(p.M - m0 < BM ? p.M - m0 : BM);
+  const int rows_b = static_cast<int>(p.N - n0 < BN ? p.N - n0 : BN);
+  const bool mn_full = m0 + BM <= p.M && n0 + BN <= p.N;
+  const int KT = static_cast<int>((p.K + kBK32 - 1) / kBK32);
+
+  auto issue = [&](int kt, int st) {
+    const int64_t k0 = static_cast<int64_t>(kt) * kBK32;
+    const int k_left = static_cast<int>(p.K - k0 < kBK32 ? p.K - k0 : kBK32);
+    const bool full = mn_full && k_left == kBK32;
+    const uint32_t la = lds0 + static_cast<uint32_t>(st) * (SA + SB) * 4;
+    ta.issue(make_rsrc(A0 + k0 * p.sa_k, a_left0 - static_cast<uint32_t>(k0 * p.sa_k * 4)), la, wave, full,
+             rows_a, k_left);
+    tb.issue(make_rsrc(B0 + k0 * p.sb_k, b_left0 - static_cast<uint32_t>(k0 * p.sb_k * 4)), la + SA * 4, wave,
+             full, rows_b, k_left);
+  };
+
   f32x16_t acc[FM][FN];
 #pragma unroll
   for (int i = 0; i < FM; ++i)
@@ -132,56 +174,76 @@ __global__ __launch_bounds__(256) void gemm_f32_kernel(GemmParams p) {
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
 
-  const int KT = static_cast<int>((p.K + kBK32 - 1) / kBK32);
-  la.load(A, p.sa_m, p.sa_k, p.M - m0, p.K, tid);
-  lb.load(B, p.sb_n, p.sb_k, p.N - n0, p.K, tid);
-  la.store(lds[0], tid);
-  lb.store(lds[0] + SA, tid);
-  __syncthreads();
-  const int frow = lane & 31, kk = lane >> 5;
-  for (int kt = 0; kt < KT; ++kt) {
-    const int cur = kt & 1;
-    const bool more = kt + 1 < KT;
-    if (more) {
-      const int64_t k0 = static_cast<int64_t>(kt + 1) * kBK32;
-      la.load(A + k0 * p.sa_k, p.sa_m, p.sa_k, p.M - m0, p.K - k0, tid);
-      lb.load(B + k0 * p.sb_k, p.sb_n, p.sb_k, p.N - n0, p.K - k0, tid);
-    }
-    const float* As = lds[cur];
-    const float* Bs = lds[cur] + SA;
+  auto compute = [&](int st) {
+    const float* As = &smem[st][0];
+    const float* Bs = &smem[st][SA];
 #pragma unroll
-    for (int s = 0; s < kBK32 / 2; ++s) {
-      const int k = s * 2 + kk;
-      float af[FM], bfv[FN];
+    for (int g = 0; g < kBK32 / 8; ++g) {
+      float4 a4[FM], b4[FN];
+      if constexpr (A_K) {
 #pragma unroll
-      for (int i = 0; i < FM; ++i) af[i] = As[k * LA::kLD + wm * TM + i * 32 + frow];
+        for (int i = 0; i < FM; ++i) a4[i] = frag_f32_kc(As, wm * TM + i * 32, g, lane);
+      }
+      if constexpr (B_K) {
 #pragma unroll
-      for (int j = 0; j < FN; ++j) bfv[j] = Bs[k * LB::kLD + wn * TN + j * 32 + frow];
+        for (int j = 0; j < FN; ++j) b4[j] = frag_f32_kc(Bs, wn * TN + j * 32, g, lane);
+      }
 #pragma unroll
-      for (int i = 0; i < FM; ++i)
+      for (int e = 0; e < 4; ++e) {
+        float af[FM], bf[FN];
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+          af[i] = A_K ? f4_at(a4[i], e) : frag_f32_mn<BM>(As, wm * TM + i * 32, g, e, lane);
 #pragma unroll
         for (int j = 0; j < FN; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(af[i], bfv[j], acc[i][j], 0, 0, 0);
-    }
-    if (more) {
-      la.store(lds[cur ^ 1], tid);
-      lb.store(lds[cur ^ 1] + SA, tid);
-    }
-    __syncthreads();
-  }
-  OutT* C = static_cast<OutT*>(p.c) + bb * p.sc_b;
+          bf[j] = B_K ? f4_at(b4[j], e) : frag_f32_mn<BN>(Bs, wn * TN + j * 32, g, e, lane);
 #pragma unroll
-  for (int i = 0; i < FM; ++i)
+        for (int i = 0; i < FM; ++i)
 #pragma unroll
-    for (int j = 0; j < FN; ++j) {
-      const int64_t col = n0 + wn * TN + j * 32 + frow;
-      if (col >= p.N) continue;
-#pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        const int64_t row = m0 + wm * TM + i * 32 + (v >> 2) * 8 + kk * 4 + (v & 3);
-        if (row < p.M) store_out<OutT>(C + row * p.sc_m + col, acc[i][j][v]);
+          for (int j = 0; j < FN; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(bf[j], af[i], acc[i][j], 0, 0, 0);
       }
     }
+  };
+
+  // Prologue: tiles 0 and 1 in flight, wait for tile 0.
+  issue(0, 0);
+  if (KT > 1) {
+    issue(1, 1);
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(LPW) : "memory");
+  } else {
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  }
+  __syncthreads();
+  for (int kt = 0; kt < KT; ++kt) {
+    const int st = kt & 1;
+    compute(st);
+    // Every wave is done with stage st and tile kt+1 has landed; tile kt+2 refills st.
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (kt + 2 < KT) issue(kt + 2, st);
+  }
+
+  // acc[i][j]: lane l, value v -> row m = l % 32 of block i, columns
+  // n = (v / 4) * 8 + (l / 32) * 4 + v % 4 of block j.
+  const StoreEpi<OutT> epi{static_cast<OutT*>(p.c), p.sc_b, p.sc_m, p.N, p.vec_c};
+  const typename StoreEpi<OutT>::Pre none{};
+#pragma unroll
+  for (int i = 0; i < FM; ++i) {
+    const int64_t m = m0 + wm * TM + i * 32 + (lane & 31);
+    if (m >= p.M) continue;
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int64_t n = n0 + wn * TN + j * 32 + q * 8 + (lane >> 5) * 4;
+        if (n >= p.N) continue;
+        float v[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] = acc[i][j][q * 4 + e];
+        epi.template store<false>(bb, m, n, v, v, none);
+      }
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -228,15 +290,15 @@ static hipError_t launch_bf16(GemmParams p, bool a_k, bool b_k, hipStream_t s) {
   return hipGetLastError();
 }
 
-template <typename OutT>
+template <int BM, int BN, int WM, int WN, typename OutT>
 static hipError_t launch_f32(GemmParams p, bool a_k, bool b_k, hipStream_t s) {
-  p.tiles_m = static_cast<int>((p.M + 127) / 128);
-  p.tiles_n = static_cast<int>((p.N + 127) / 128);
-  const dim3 grid(static_cast<unsigned>(p.batch * p.tiles_m * p.tiles_n)), block(256);
-  if (a_k && b_k) hipLaunchKernelGGL((gemm_f32_kernel<true, true, OutT>), grid, block, 0, s, p);
-  else if (a_k) hipLaunchKernelGGL((gemm_f32_kernel<true, false, OutT>), grid, block, 0, s, p);
-  else if (b_k) hipLaunchKernelGGL((gemm_f32_kernel<false, true, OutT>), grid, block, 0, s, p);
-  else hipLaunchKernelGGL((gemm_f32_kernel<false, false, OutT>), grid, block, 0, s, p);
+  p.tiles_m = static_cast<int>((p.M + BM - 1) / BM);
+  p.tiles_n = static_cast<int>((p.N + BN - 1) / BN);
+  const dim3 grid(static_cast<unsigned>(p.batch * p.tiles_m * p.tiles_n)), block(WM * WN * 64);
+  if (a_k && b_k) hipLaunchKernelGGL((gemm_f32_kernel<BM, BN, WM, WN, true, true, OutT>), grid, block, 0, s, p);
+  else if (a_k) hipLaunchKernelGGL((gemm_f32_kernel<BM, BN, WM, WN, true, false, OutT>), grid, block, 0, s, p);
+  else if (b_k) hipLaunchKernelGGL((gemm_f32_kernel<BM, BN, WM, WN, false, true, OutT>), grid, block, 0, s, p);
+  else hipLaunchKernelGGL((gemm_f32_kernel<BM, BN, WM, WN, false, false, OutT>), grid, block, 0, s, p);
   return hipGetLastError();
 }
 
@@ -288,8 +350,19 @@ template <typename OutT>
 static hipError_t dispatch_f32(GemmParams p, hipStream_t s) {
   const int ma = majorness(p.a, p.sa_b, p.sa_m, p.sa_k, p.M, p.K, 4, p.batch);
   const int mb = majorness(p.b, p.sb_b, p.sb_n, p.sb_k, p.N, p.K, 4, p.batch);
-  if (ma < 0 || mb < 0) return launch_generic<float, OutT>(p, s);
-  return launch_f32<OutT>(p, ma, mb, s);
+  const bool nonneg = p.sa_b >= 0 && p.sa_m >= 0 && p.sa_k >= 0 && p.sb_b >= 0 && p.sb_k >= 0 &&
+                      p.sb_n >= 0;
+  const int64_t ea = slice_bytes(p.M, p.sa_m, p.K, p.sa_k, 4);
+  const int64_t eb = slice_bytes(p.N, p.sb_n, p.K, p.sb_k, 4);
+  if (ma < 0 || mb < 0 || !nonneg || ea >= (int64_t{1} << 31) || eb >= (int64_t{1} << 31))
+    return launch_generic<float, OutT>(p, s);
+  p.a_extent = static_cast<uint32_t>(ea);
+  p.b_extent = static_cast<uint32_t>(eb);
+  p.vec_c = (p.sc_m % 4 == 0) && (p.sc_b % 4 == 0 || p.batch == 1) &&
+            (reinterpret_cast<uintptr_t>(p.c) % (4 * sizeof(OutT)) == 0);
+  const int64_t t256 = p.batch * ((p.M + 255) / 256) * ((p.N + 255) / 256);
+  if (p.M >= 256 && p.N >= 256 && t256 >= 128) return launch_f32<256, 256, 2, 4, OutT>(p, ma, mb, s);
+  return launch_f32<128, 128, 2, 2, OutT>(p, ma, mb, s);
 }
 
 }  // namespace ghip

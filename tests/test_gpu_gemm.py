@@ -77,6 +77,22 @@ def test_f32_layouts(cuda, shape, a_t, b_t):
     assert rel_err(c, orc.dot_general(a, [2], [0], b, [1], [0])) <= 1e-4
 
 
+@pytest.mark.parametrize("a_t", [False, True])
+@pytest.mark.parametrize("b_t", [False, True])
+def test_f32_layouts_large_tiles(cuda, a_t, b_t):
+    """Big enough for the 256 x 256 fp32 tiles (>= 128 of them), ragged M, N, K."""
+    g = torch.Generator(cuda).manual_seed(3401)
+    ta = torch.randn((2, 2056, 140), device=cuda, generator=g) * 0.125
+    tb = torch.randn((2, 140, 2060), device=cuda, generator=g) * 0.125
+    if a_t:
+        ta = ta.transpose(1, 2).contiguous().transpose(1, 2)
+    if b_t:
+        tb = tb.transpose(1, 2).contiguous().transpose(1, 2)
+    c = ops.gemm(ta, tb)
+    got, ref = _sampled_check(ta, tb, c, seed=7)
+    assert rel_err(got, ref) <= 1e-4
+
+
 def test_generic_path_odd_strides(cuda):
     """Shapes/strides the vector paths cannot address fall back to the generic kernel."""
     a = synth.normal(3400, (2, 33, 19))
