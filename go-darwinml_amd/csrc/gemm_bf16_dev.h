@@ -215,12 +215,18 @@ struct BoolC {
   static constexpr bool value = B;
 };
 
-// One BM x BN output tile per workgroup of WM x WN waves.  For every 4 adjacent
-// outputs a lane owns, calls epi.store<FULL>(bb, m, n, v0, v1, pre) with m < M
-// and columns n .. n+3 (with FULL false the ones >= N must be ignored; FULL
-// true: the whole tile lies inside the output): v0[e] = (A.B)[bb, m, n+e] in
-// fp32, v1[e] the same element of A.B1 when NB == 2 (else v1 == v0), and `pre`
-// what epi.prefetch<FULL>(bb, m, n, pre) loaded for the same outputs.
+// One BM x BN output tile per workgroup of WM x WN waves.  The epilogue functor:
+//   Stage                        how one product value is held in LDS (uint16_t:
+//                                bf16 bits; float: fp32)
+//   static Stage stage(float)    fp32 accumulator -> staged value
+//   Pre, prefetch<FULL>(bb, m, n, Pre&)
+//                                loads the epilogue's own operands for a row chunk
+//   store<FULL>(bb, m, n, const Stage* v0, const Stage* v1, const Pre&)
+//                                finishes CH = 16 / sizeof(Stage) consecutive
+//                                outputs (bb, m, n .. n+CH-1) of row m < M: v0 from
+//                                A.B, v1 from A.B1 when NB == 2 (else v1 == v0);
+//                                FULL: the whole tile lies inside the output (no
+//                                column bounds), else columns >= N are ignored.
 template <int BM, int BN, int WM, int WN, bool A_K, bool B_K, int NB, class Epi>
 __device__ __forceinline__ void gemm_bf16_body(const GemmParams& p, const Epi& epi) {
   static_assert(NB == 1 || NB == 2, "one or two right operands");
@@ -231,8 +237,12 @@ __device__ __forceinline__ void gemm_bf16_body(const GemmParams& p, const Epi& e
   using TA = OperandTile<BM, A_K, NW>;
   using TB = OperandTile<BN, B_K, NW>;
   constexpr int LPW = TA::kPerWave + NB * TB::kPerWave;  // loads per wave per k-tile
-  __shared__ __attribute__((aligned(1024))) uint16_t sa[2][BM * kBK];
-  __shared__ __attribute__((aligned(1024))) uint16_t sb[2][NB * BN * kBK];
+  // Two stages of the A and B tiles; after the main loop the same memory stages
+  // the output tile for the epilogue.
+  constexpr int kLdsBytes = 2 * BM * kBK * 2 + 2 * NB * BN * kBK * 2;
+  __shared__ __attribute__((aligned(1024))) uint16_t smem[kLdsBytes / 2];
+  uint16_t(*sa)[BM * kBK] = reinterpret_cast<uint16_t(*)[BM * kBK]>(smem);
+  uint16_t(*sb)[NB * BN * kBK] = reinterpret_cast<uint16_t(*)[NB * BN * kBK]>(smem + 2 * BM * kBK);
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -331,44 +341,90 @@ __device__ __forceinline__ void gemm_bf16_body(const GemmParams& p, const Epi& e
   }
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
-  // acc[i][j] holds the transposed 32x32 block: lane l, value v ->
-  // row m = l % 32, columns n = (v / 4) * 8 + (l / 32) * 4 + v % 4.
-  // The epilogue's own operands for 32-row block i+1 are fetched (prefetch)
-  // before block i's outputs are stored, so their loads overlap instead of each
-  // waiting behind the previous store.  Tiles inside the output (all but the
-  // ragged edge) run a copy with no per-lane bounds checks, which keeps those
-  // loads and stores free of divergent branches.
+  // Epilogue through LDS.  acc[i][j] holds the transposed 32x32 block: lane l,
+  // value v -> row m = l % 32, columns n = (v / 4) * 8 + (l / 32) * 4 + v % 4, so
+  // storing it directly writes 16 bytes into each of 32 rows per instruction.
+  // Instead the tile is staged in LDS (as Epi::Stage values, 16-byte chunk c of
+  // row r at slot c ^ (r % chunks-per-row)) and read back row-wise: each lane
+  // takes CH = 16 / sizeof(Stage) consecutive columns of one row, so a wave
+  // instruction covers whole rows.  Tiles whose stage exceeds the LDS take 2
+  // passes of half the rows.  The epilogue's own operands for the next row
+  // chunk are fetched (prefetch) before the current chunk is stored.
+  using Stage = typename Epi::Stage;
+  constexpr int ES = sizeof(Stage);
+  constexpr int CH = 16 / ES;
+  constexpr int kStageBytes = NB * BM * BN * ES;
+  constexpr int P = kStageBytes <= kLdsBytes ? 1 : 2;  // passes
+  static_assert(kStageBytes <= P * kLdsBytes && BM % (32 * P) == 0,
+                "stage must fit the LDS in at most 2 passes of whole 32-row blocks");
+  constexpr int PR = BM / P;          // rows per pass
+  constexpr int CPR = BN * ES / 16;   // 16-byte chunks per staged row (per product)
+  constexpr int NT = NW * 64;
+  static_assert((CPR & (CPR - 1)) == 0 && NT % CPR == 0 && PR % (NT / CPR) == 0, "row-chunk split");
+  constexpr int RPI = NT / CPR;  // rows per read iteration
+  constexpr int NIT = PR / RPI;  // read iterations per pass
+  Stage* stg = reinterpret_cast<Stage*>(smem);
+  auto slot = [](int r, int c) { return c ^ (r & (CPR - 1)); };
+
   auto epilogue = [&](auto full_c) {
     constexpr bool FULL = decltype(full_c)::value;
-    typename Epi::Pre pre[2][FN][4];
-    auto prefetch = [&](int i, int slot) {
-      const int64_t m = m0 + wm * TM + i * 32 + (lane & 31);
-      if (!FULL && m >= p.M) return;
 #pragma unroll
-      for (int j = 0; j < FN; ++j)
+    for (int pass = 0; pass < P; ++pass) {
+      // LDS is free: every wave has finished its main-loop reads (or the
+      // previous pass's row reads).
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      __syncthreads();
 #pragma unroll
-        for (int q = 0; q < 4; ++q)
-          epi.template prefetch<FULL>(bb, m, n0 + wn * TN + j * 32 + q * 8 + (lane >> 5) * 4, pre[slot][j][q]);
-    };
-    prefetch(0, 0);
+      for (int i = 0; i < FM; ++i) {
+        const int r = wm * TM + i * 32 + (lane & 31);
+        if ((wm * TM + i * 32) / PR != pass) continue;  // uniform over the wave
+        const int rl = r - pass * PR;
 #pragma unroll
-    for (int i = 0; i < FM; ++i) {
-      if (i + 1 < FM) prefetch(i + 1, (i + 1) & 1);
-      const int64_t m = m0 + wm * TM + i * 32 + (lane & 31);
-      if (!FULL && m >= p.M) continue;
+        for (int h = 0; h < NB; ++h)
 #pragma unroll
-      for (int j = 0; j < FN; ++j) {
+          for (int j = 0; j < FN; ++j)
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const int64_t n = n0 + wn * TN + j * 32 + q * 8 + (lane >> 5) * 4;
-          float v0[4], v1[4];
+            for (int q = 0; q < 4; ++q) {
+              const int n = wn * TN + j * 32 + q * 8 + (lane >> 5) * 4;
+              Stage w[4];
 #pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            v0[e] = acc[i][j][q * 4 + e];
-            v1[e] = acc[i][(NB - 1) * FN + j][q * 4 + e];
-          }
-          epi.template store<FULL>(bb, m, n, v0, v1, pre[i & 1][j][q]);
+              for (int e = 0; e < 4; ++e) w[e] = Epi::stage(acc[i][h * FN + j][q * 4 + e]);
+              const int c = n * ES / 16, off = (n * ES) % 16;
+              char* dst = reinterpret_cast<char*>(stg + (h * PR + rl) * BN) + slot(rl, c) * 16 + off;
+              if constexpr (ES == 2) {
+                struct __attribute__((aligned(8))) W8 { Stage x[4]; };
+                *reinterpret_cast<W8*>(dst) = W8{{w[0], w[1], w[2], w[3]}};
+              } else {
+                struct __attribute__((aligned(16))) W16 { Stage x[4]; };
+                *reinterpret_cast<W16*>(dst) = W16{{w[0], w[1], w[2], w[3]}};
+              }
+            }
+      }
+      __syncthreads();
+      const int t = threadIdx.x;
+      const int cl = t % CPR;
+      const int64_t n = n0 + cl * CH;
+      typename Epi::Pre pre[2];
+      auto row_of = [&](int it) { return pass * PR + it * RPI + t / CPR; };
+      if (FULL || m0 + row_of(0) < p.M) epi.template prefetch<FULL>(bb, m0 + row_of(0), n, pre[0]);
+#pragma unroll
+      for (int it = 0; it < NIT; ++it) {
+        if (it + 1 < NIT && (FULL || m0 + row_of(it + 1) < p.M))
+          epi.template prefetch<FULL>(bb, m0 + row_of(it + 1), n, pre[(it + 1) & 1]);
+        const int rl = it * RPI + t / CPR;
+        const int64_t m = m0 + pass * PR + rl;
+        if (!FULL && m >= p.M) continue;
+        Stage v0[CH], v1[CH];
+        struct __attribute__((aligned(16))) C16 { Stage x[CH]; };
+        const C16 a0 = *reinterpret_cast<const C16*>(reinterpret_cast<const char*>(stg + rl * BN) + slot(rl, cl) * 16);
+        const C16 a1 = *reinterpret_cast<const C16*>(reinterpret_cast<const char*>(stg + ((NB - 1) * PR + rl) * BN) +
+                                                     slot(rl, cl) * 16);
+#pragma unroll
+        for (int e = 0; e < CH; ++e) {
+          v0[e] = a0.x[e];
+          v1[e] = a1.x[e];
         }
+        epi.template store<FULL>(bb, m, n, v0, v1, pre[it & 1]);
       }
     }
   };

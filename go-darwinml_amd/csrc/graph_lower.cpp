@@ -1431,7 +1431,13 @@ View Lowerer::emit_gemm_epilogue(int v, const std::vector<int>& mem, bool* fused
   };
   std::vector<In> ins;
   std::map<int, std::string> expr;
-  for (int k = 0; k < NB; ++k) expr[dots[k]] = round_expr(N[dots[k]].shape.dtype, k == 0 ? "acc0[e]" : "acc1[e]");
+  // The GEMM stages each product in the Dot's own dtype (bf16 bits, or fp32), so
+  // the value read back is exactly what the stand-alone Dot would have stored.
+  const int dot_dt = N[dots[0]].shape.dtype;
+  const bool stage_bf16 = dot_dt == GHIP_DTYPE_BFLOAT16;
+  const int CH = stage_bf16 ? 8 : 4;  // outputs per epilogue call (16 staged bytes)
+  for (int k = 0; k < NB; ++k) expr[dots[k]] = stage_bf16 ? (k == 0 ? "bf2f(acc0[e])" : "bf2f(acc1[e])")
+                                                           : (k == 0 ? "acc0[e]" : "acc1[e]");
   std::ostringstream body;
   for (size_t ui = 0; ui < mem.size(); ++ui) {
     const int u = mem[ui];
@@ -1457,7 +1463,7 @@ View Lowerer::emit_gemm_epilogue(int v, const std::vector<int>& mem, bool* fused
       int64_t sz;
       if (!merge(os, eff, gb, &sz, &in.sb) || !merge(os, eff, gm, &sz, &in.sm) || !merge(os, eff, gn, &sz, &in.sn))
         return View{};
-      in.vin = in.sn == 1 && (in.sm % 4 == 0 || d.M == 1) && (in.sb % 4 == 0 || d.B == 1) && w.offset % 4 == 0;
+      in.vin = in.sn == 1 && (in.sm % CH == 0 || d.M == 1) && (in.sb % CH == 0 || d.B == 1) && w.offset % CH == 0;
       const int k = static_cast<int>(ins.size());
       const std::string ks = std::to_string(k);
       body << "      const " << ctype(s.dtype) << " in" << ks << " = " << load_expr(s.dtype, "pr.x" + ks + "[e]") << ";\n";
@@ -1481,46 +1487,52 @@ View Lowerer::emit_gemm_epilogue(int v, const std::vector<int>& mem, bool* fused
   const int odt = os.dtype;
   std::ostringstream src;
   src << kGemmDevSrc << "\n" << kRtcPrelude;
-  // Pre: the 4 raw elements of each extra operand for one call, loaded by
-  // prefetch() ahead of the stores of the previous row block.  FULL: the
+  // Pre: the CH raw elements of each extra operand for one call (one row chunk),
+  // loaded by prefetch() ahead of the stores of the previous chunk.  FULL: the
   // tile lies inside the output, so no column bounds checks.
-  const bool vec = d.N % 4 == 0;
-  src << "namespace ghip {\nstruct GenEpi {\n  struct Pre {";
-  for (size_t k = 0; k < ins.size(); ++k) src << " " << stype(ins[k].dt) << " x" << k << "[4];";
+  const bool vec = d.N % CH == 0;
+  const std::string CHs = std::to_string(CH);
+  src << "namespace ghip {\nstruct GenEpi {\n  using Stage = " << (stage_bf16 ? "unsigned short" : "float") << ";\n"
+      << "  __device__ __forceinline__ static Stage stage(float v) { return " << (stage_bf16 ? "f2bf(v)" : "v")
+      << "; }\n  struct Pre {";
+  for (size_t k = 0; k < ins.size(); ++k) src << " " << stype(ins[k].dt) << " x" << k << "[" << CH << "];";
   src << " };\n  EpiArgs a;\n"
       << "  template <bool FULL>\n"
       << "  __device__ __forceinline__ void prefetch(int64_t bb, int64_t m, int64_t n, Pre& pr) const {\n";
   for (size_t k = 0; k < ins.size(); ++k) {
     const std::string T = stype(ins[k].dt), ks = std::to_string(k);
+    const int vbytes = std::min(CH * dtype_size(ins[k].dt), 16);
     src << "    {\n      const " << T << "* src = (const " << T << "*)a.in[" << ks << "] + bb * a.s_b[" << ks
         << "] + m * a.s_m[" << ks << "] + n * a.s_n[" << ks << "];\n";
     if (ins[k].vin)
-      src << "      if (FULL || n + 3 < a.N) {\n"
-          << "        struct __attribute__((aligned(4 * sizeof(" << T << ")))) V { " << T << " x[4]; };\n"
+      src << "      if (FULL || n + " << CH - 1 << " < a.N) {\n"
+          << "        struct __attribute__((aligned(" << vbytes << "))) V { " << T << " x[" << CHs << "]; };\n"
           << "        const V w = *(const V*)src;\n"
-          << "#pragma unroll\n        for (int e = 0; e < 4; ++e) pr.x" << ks << "[e] = w.x[e];\n"
+          << "#pragma unroll\n        for (int e = 0; e < " << CHs << "; ++e) pr.x" << ks << "[e] = w.x[e];\n"
           << "      } else {\n";
     else
       src << "      {\n";
-    src << "#pragma unroll\n        for (int e = 0; e < 4; ++e) pr.x" << ks << "[e] = (FULL || n + e < a.N) ? src[e * a.s_n[" << ks
+    src << "#pragma unroll\n        for (int e = 0; e < " << CHs << "; ++e) pr.x" << ks << "[e] = (FULL || n + e < a.N) ? src[e * a.s_n[" << ks
         << "]] : (" << T << ")0;\n      }\n    }\n";
   }
   src << "  }\n"
       << "  template <bool FULL>\n"
-      << "  __device__ __forceinline__ void store(int64_t bb, int64_t m, int64_t n, const float* acc0,\n"
-      << "                                        const float* acc1, const Pre& pr) const {\n"
-      << "    " << ctype(odt) << " r[4];\n"
-      << "#pragma unroll\n    for (int e = 0; e < 4; ++e) {\n      const int64_t nn = n + e;\n"
+      << "  __device__ __forceinline__ void store(int64_t bb, int64_t m, int64_t n, const Stage* acc0,\n"
+      << "                                        const Stage* acc1, const Pre& pr) const {\n"
+      << "    " << ctype(odt) << " r[" << CH << "];\n"
+      << "#pragma unroll\n    for (int e = 0; e < " << CHs << "; ++e) {\n      const int64_t nn = n + e;\n"
       << "      if (!FULL && nn >= a.N) { r[e] = 0; continue; }\n"
       << body.str()
       << "      r[e] = " << expr[v] << ";\n    }\n"
       << "    " << stype(odt) << "* o = (" << stype(odt) << "*)a.out + bb * a.so_b + m * a.so_m + n;\n";
-  if (vec)
-    src << "    if (FULL || n + 3 < a.N) {\n"
-        << "      struct __attribute__((aligned(4 * sizeof(" << stype(odt) << ")))) V { " << stype(odt) << " x[4]; } w;\n"
-        << "#pragma unroll\n      for (int e = 0; e < 4; ++e) w.x[e] = " << store_expr(odt, "r[e]") << ";\n"
+  if (vec) {
+    const int obytes = std::min(CH * dtype_size(odt), 16);
+    src << "    if (FULL || n + " << CH - 1 << " < a.N) {\n"
+        << "      struct __attribute__((aligned(" << obytes << "))) V { " << stype(odt) << " x[" << CHs << "]; } w;\n"
+        << "#pragma unroll\n      for (int e = 0; e < " << CHs << "; ++e) w.x[e] = " << store_expr(odt, "r[e]") << ";\n"
         << "      *(V*)o = w;\n      return;\n    }\n";
-  src << "#pragma unroll\n    for (int e = 0; e < 4; ++e)\n      if (FULL || n + e < a.N) o[e] = " << store_expr(odt, "r[e]")
+  }
+  src << "#pragma unroll\n    for (int e = 0; e < " << CHs << "; ++e)\n      if (FULL || n + e < a.N) o[e] = " << store_expr(odt, "r[e]")
       << ";\n  }\n};\n}  // namespace ghip\n";
   src << "extern \"C\" __global__ void __launch_bounds__(" << nt << ", 1) gemm_epilogue(ghip::GemmParams p, ghip::EpiArgs a) {\n"
       << "  const ghip::GenEpi epi{a};\n"
@@ -1573,16 +1585,17 @@ View Lowerer::emit_gemm_epilogue(int v, const std::vector<int>& mem, bool* fused
       a.s_m[k] = ins[k].sm;
       a.s_n[k] = ins[k].sn;
       a.vin[k] = ins[k].vin;
-      if (ins[k].vin && reinterpret_cast<uintptr_t>(a.in[k]) % (4 * es) != 0)
-        return set_error(e, GHIP_ERR_STATE, "fused GEMM epilogue: operand %zu not %d-byte aligned", k, 4 * es);
+      const int va = std::min(CH * es, 16);
+      if (ins[k].vin && reinterpret_cast<uintptr_t>(a.in[k]) % va != 0)
+        return set_error(e, GHIP_ERR_STATE, "fused GEMM epilogue: operand %zu not %d-byte aligned", k, va);
     }
     a.out = p.c;
     a.so_b = so_b;
     a.so_m = so_m;
     a.N = p.N;
     a.vec = vec;
-    if (vec && reinterpret_cast<uintptr_t>(p.c) % (4 * dtype_size(odt)) != 0)
-      return set_error(e, GHIP_ERR_STATE, "fused GEMM epilogue: output not %d-byte aligned", 4 * dtype_size(odt));
+    if (vec && reinterpret_cast<uintptr_t>(p.c) % std::min(CH * dtype_size(odt), 16) != 0)
+      return set_error(e, GHIP_ERR_STATE, "fused GEMM epilogue: output not aligned for %d-element stores", CH);
     void* args[] = {&p, &a};
     hipError_t h = hipModuleLaunchKernel(kern.func, static_cast<unsigned>(blocks), 1, 1, nt, 1, 1, 0, st.stream, args,
                                          nullptr);

@@ -18,30 +18,54 @@ __device__ __forceinline__ void store_out<float>(float* p, float v) { *p = v; }
 template <>
 __device__ __forceinline__ void store_out<bf16_t>(bf16_t* p, float v) { p->bits = f32_to_bf16(v); }
 
-// Epilogue of the precompiled bf16 kernels: store 4 adjacent outputs, one 8-byte
-// (bf16) / 16-byte (fp32) store when the row allows it.
+// Epilogue of the precompiled bf16 kernels: the output value itself is staged
+// (bf16 bits or fp32) and a row chunk is one 16-byte store.
 template <typename OutT>
-struct StoreEpi {
+struct StoreEpi;
+template <>
+struct StoreEpi<bf16_t> {
+  using Stage = uint16_t;
   struct Pre {};
-  OutT* c;
+  bf16_t* c;
   int64_t sc_b, sc_m, N;
   int vec;
+  __device__ __forceinline__ static Stage stage(float v) { return f32_to_bf16(v); }
   template <bool FULL>
   __device__ __forceinline__ void prefetch(int64_t, int64_t, int64_t, Pre&) const {}
   template <bool FULL>
-  __device__ __forceinline__ void store(int64_t bb, int64_t m, int64_t n, const float* v, const float*,
+  __device__ __forceinline__ void store(int64_t bb, int64_t m, int64_t n, const Stage* v, const Stage*,
                                         const Pre&) const {
-    OutT* dst = c + bb * sc_b + m * sc_m + n;
+    uint16_t* dst = reinterpret_cast<uint16_t*>(c + bb * sc_b + m * sc_m + n);
+    if (vec && (FULL || n + 7 < N)) {
+      *reinterpret_cast<uint4*>(dst) = make_uint4(v[0] | (uint32_t(v[1]) << 16), v[2] | (uint32_t(v[3]) << 16),
+                                                 v[4] | (uint32_t(v[5]) << 16), v[6] | (uint32_t(v[7]) << 16));
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        if (FULL || n + e < N) dst[e] = v[e];
+    }
+  }
+};
+template <>
+struct StoreEpi<float> {
+  using Stage = float;
+  struct Pre {};
+  float* c;
+  int64_t sc_b, sc_m, N;
+  int vec;
+  __device__ __forceinline__ static Stage stage(float v) { return v; }
+  template <bool FULL>
+  __device__ __forceinline__ void prefetch(int64_t, int64_t, int64_t, Pre&) const {}
+  template <bool FULL>
+  __device__ __forceinline__ void store(int64_t bb, int64_t m, int64_t n, const Stage* v, const Stage*,
+                                        const Pre&) const {
+    float* dst = c + bb * sc_b + m * sc_m + n;
     if (vec && (FULL || n + 3 < N)) {
-      if constexpr (sizeof(OutT) == 2) {
-        *reinterpret_cast<uint2*>(dst) = make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
-      } else {
-        *reinterpret_cast<float4*>(dst) = make_float4(v[0], v[1], v[2], v[3]);
-      }
+      *reinterpret_cast<float4*>(dst) = make_float4(v[0], v[1], v[2], v[3]);
     } else {
 #pragma unroll
       for (int e = 0; e < 4; ++e)
-        if (n + e < N) store_out<OutT>(dst + e, v[e]);
+        if (FULL || n + e < N) dst[e] = v[e];
     }
   }
 };
@@ -226,8 +250,7 @@ __global__ __launch_bounds__(WM* WN * 64, (WM * WN == 4 ? 2 : 1)) void gemm_f32_
 
   // acc[i][j]: lane l, value v -> row m = l % 32 of block i, columns
   // n = (v / 4) * 8 + (l / 32) * 4 + v % 4 of block j.
-  const StoreEpi<OutT> epi{static_cast<OutT*>(p.c), p.sc_b, p.sc_m, p.N, p.vec_c};
-  const typename StoreEpi<OutT>::Pre none{};
+  OutT* C = static_cast<OutT*>(p.c) + bb * p.sc_b;
 #pragma unroll
   for (int i = 0; i < FM; ++i) {
     const int64_t m = m0 + wm * TM + i * 32 + (lane & 31);
@@ -241,7 +264,17 @@ __global__ __launch_bounds__(WM* WN * 64, (WM * WN == 4 ? 2 : 1)) void gemm_f32_
         float v[4];
 #pragma unroll
         for (int e = 0; e < 4; ++e) v[e] = acc[i][j][q * 4 + e];
-        epi.template store<false>(bb, m, n, v, v, none);
+        OutT* dst = C + m * p.sc_m + n;
+        if (p.vec_c && n + 3 < p.N) {
+          if constexpr (sizeof(OutT) == 2)
+            *reinterpret_cast<uint2*>(dst) = make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
+          else
+            *reinterpret_cast<float4*>(dst) = make_float4(v[0], v[1], v[2], v[3]);
+        } else {
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            if (n + e < p.N) store_out<OutT>(dst + e, v[e]);
+        }
       }
   }
 }
@@ -338,8 +371,9 @@ static hipError_t dispatch_bf16(GemmParams p, hipStream_t s) {
     return launch_generic<bf16_t, OutT>(p, s);
   p.a_extent = static_cast<uint32_t>(ea);
   p.b_extent = static_cast<uint32_t>(eb);
-  p.vec_c = (p.sc_m % 4 == 0) && (p.sc_b % 4 == 0 || p.batch == 1) &&
-            (reinterpret_cast<uintptr_t>(p.c) % (4 * sizeof(OutT)) == 0);
+  constexpr int64_t kV = 16 / sizeof(OutT);  // elements per 16-byte store
+  p.vec_c = (p.sc_m % kV == 0) && (p.sc_b % kV == 0 || p.batch == 1) &&
+            (reinterpret_cast<uintptr_t>(p.c) % 16 == 0);
   const int64_t t256 = p.batch * ((p.M + 255) / 256) * ((p.N + 255) / 256);
   if (p.M >= 256 && p.N >= 256 && t256 >= 128) return launch_bf16<256, 256, 2, 4, OutT>(p, ma, mb, s);
   if (p.M >= 256 && p.N >= 128) return launch_bf16<256, 128, 2, 2, OutT>(p, ma, mb, s);
