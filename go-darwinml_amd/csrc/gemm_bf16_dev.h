@@ -129,12 +129,12 @@ __device__ __forceinline__ i32x4_t make_rsrc(const void* base, uint32_t bytes) {
   return r;
 }
 
-// 16 bytes per lane from buffer offset voff straight into LDS at lds + lane*16.
-__device__ __forceinline__ void dma16(i32x4_t rsrc, const void* lds, uint32_t voff) {
-  const uint32_t la = static_cast<uint32_t>(reinterpret_cast<uint64_t>((GHIP_LDS const void*)lds));
+// 16 bytes per lane from buffer offset voff straight into LDS byte address
+// la + lane*16 (la wave-uniform; a 32-bit LDS address, so no generic-pointer
+// conversion is needed per load).
+__device__ __forceinline__ void dma16(i32x4_t rsrc, uint32_t la, uint32_t voff) {
   asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
-               ::"s"(__builtin_amdgcn_readfirstlane(la)), "v"(voff), "s"(rsrc)
-               : "memory", "m0");
+               ::"s"(la), "v"(voff), "s"(rsrc) : "memory", "m0");
 }
 
 // Wave-instruction i of a wave fills LDS bytes [blk*1024, blk*1024 + 1024),
@@ -174,17 +174,22 @@ struct OperandTile {
     }
     step = static_cast<uint32_t>(kRPI * (KC ? s_mn : s_k) * 2);
   }
-  // full: the whole tile lies inside the operand; otherwise out-of-range rows and
-  // k-chunks read zeros.
-  __device__ __forceinline__ void issue(i32x4_t rs, uint16_t* lds, int wave, int lane, bool full,
-                                        int k_left) const {
+  // lds: LDS byte address of the tile.  FULL: the whole tile lies inside the
+  // operand (no per-lane masks); otherwise out-of-range rows and k-chunks read
+  // zeros.
+  template <bool FULL>
+  __device__ __forceinline__ void issue(i32x4_t rs, uint32_t lds, int wave, int lane, int k_left) const {
 #pragma unroll
     for (int i = 0; i < kPerWave; ++i) {
       const uint32_t v = voff[i & 1] + static_cast<uint32_t>(i & ~1) * step;
-      const int r = row_of(wave, i, lane);
-      const int c = chunk_of(wave, i, lane);
-      const bool ok = KC ? (r < mn_valid && c * 8 < k_left) : (r < k_left && c * 8 < mn_valid);
-      dma16(rs, lds + (wave * kPerWave + i) * 512, (full || ok) ? v : kOffOOB);
+      if constexpr (FULL) {
+        dma16(rs, lds + (wave * kPerWave + i) * 1024, v);
+      } else {
+        const int r = row_of(wave, i, lane);
+        const int c = chunk_of(wave, i, lane);
+        const bool ok = KC ? (r < mn_valid && c * 8 < k_left) : (r < k_left && c * 8 < mn_valid);
+        dma16(rs, lds + (wave * kPerWave + i) * 1024, ok ? v : kOffOOB);
+      }
     }
   }
 };
@@ -265,16 +270,25 @@ __device__ __forceinline__ void gemm_bf16_body(const GemmParams& p, const Epi& e
   const bool mn_full = m0 + BM <= p.M && n0 + BN <= p.N;
   const int KT = static_cast<int>((p.K + kBK - 1) / kBK);
 
+  const uint32_t lds_a = static_cast<uint32_t>(reinterpret_cast<uint64_t>((GHIP_LDS void*)smem));
+  const uint32_t lds_b = lds_a + 2 * BM * kBK * 2;
   auto issue = [&](int kt, int st) {
     const int64_t k0 = static_cast<int64_t>(kt) * kBK;
     const int k_left = static_cast<int>(p.K - k0 < kBK ? p.K - k0 : kBK);
-    const bool full = mn_full && k_left == kBK;
     const uint32_t b_left = b_left0 - static_cast<uint32_t>(k0 * p.sb_k * 2);
-    ta.issue(make_rsrc(A0 + k0 * p.sa_k, a_left0 - static_cast<uint32_t>(k0 * p.sa_k * 2)), sa[st],
-             wave, lane, full, k_left);
-    tb.issue(make_rsrc(B0 + k0 * p.sb_k, b_left), sb[st], wave, lane, full, k_left);
-    if constexpr (NB == 2)
-      tb.issue(make_rsrc(B1 + k0 * p.sb_k, b_left), sb[st] + BN * kBK, wave, lane, full, k_left);
+    const i32x4_t ra = make_rsrc(A0 + k0 * p.sa_k, a_left0 - static_cast<uint32_t>(k0 * p.sa_k * 2));
+    const i32x4_t rb = make_rsrc(B0 + k0 * p.sb_k, b_left);
+    const uint32_t la = lds_a + st * (BM * kBK * 2), lb = lds_b + st * (NB * BN * kBK * 2);
+    if (mn_full && k_left == kBK) {
+      ta.template issue<true>(ra, la, wave, lane, k_left);
+      tb.template issue<true>(rb, lb, wave, lane, k_left);
+      if constexpr (NB == 2) tb.template issue<true>(make_rsrc(B1 + k0 * p.sb_k, b_left), lb + BN * kBK * 2, wave, lane, k_left);
+    } else {
+      ta.template issue<false>(ra, la, wave, lane, k_left);
+      tb.template issue<false>(rb, lb, wave, lane, k_left);
+      if constexpr (NB == 2)
+        tb.template issue<false>(make_rsrc(B1 + k0 * p.sb_k, b_left), lb + BN * kBK * 2, wave, lane, k_left);
+    }
   };
 
   f32x16_t acc[FM][NB * FN];
