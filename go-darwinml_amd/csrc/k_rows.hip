@@ -212,22 +212,27 @@ __global__ __launch_bounds__(256) void rows_reg_kernel(RowParams p) {
       const int64_t c0 = (static_cast<int64_t>(i) * LANES + l) * VEC;
       v[i] = live[i] ? ld_nt(xr + c0) : make_uint4(0, 0, 0, 0);
     }
-    float s = 0.f;
-#pragma unroll
-    for (int i = 0; i < NV; ++i) {
-      float f[VEC];
-      unpack(v[i], f, T{});
-#pragma unroll
-      for (int j = 0; j < VEC; ++j) s += (OP == kRmsNorm) ? f[j] * f[j] : f[j];
-    }
-    s = row_reduce_sum<WPR>(s, lds, 0);
     const float inv_n = 1.0f / static_cast<float>(n);
     float mean = 0.f, rstd;
-    if constexpr (OP == kRmsNorm) {
-      rstd = rsqrtf(s * inv_n + p.eps);
-    } else {
-      mean = s * inv_n;
-      float q = 0.f;
+    if constexpr (OP == kLayerNorm && WPR > 1) {
+      // Each wave reduces its part of the row to (count, mean, M2) in registers
+      // and one LDS exchange combines the WPR parts (Chan, Golub and LeVeque's
+      // pairwise update: M2 = sum M2_w + n_w (mean_w - mean)^2), instead of a
+      // reduction for the mean followed by a second one for the variance.
+      float cnt = 0.f, sw = 0.f;
+#pragma unroll
+      for (int i = 0; i < NV; ++i) {
+        if (!live[i]) continue;
+        float f[VEC];
+        unpack(v[i], f, T{});
+        cnt += VEC;
+#pragma unroll
+        for (int j = 0; j < VEC; ++j) sw += f[j];
+      }
+      cnt = wave_sum(cnt);
+      sw = wave_sum(sw);
+      const float mw = cnt > 0.f ? sw / cnt : 0.f;
+      float qw = 0.f;
 #pragma unroll
       for (int i = 0; i < NV; ++i) {
         if (!live[i]) continue;
@@ -235,12 +240,58 @@ __global__ __launch_bounds__(256) void rows_reg_kernel(RowParams p) {
         unpack(v[i], f, T{});
 #pragma unroll
         for (int j = 0; j < VEC; ++j) {
-          const float d = f[j] - mean;
-          q += d * d;
+          const float d = f[j] - mw;
+          qw += d * d;
         }
       }
-      q = row_reduce_sum<WPR>(q, lds, 1);
-      rstd = rsqrtf(q * inv_n + p.eps);
+      qw = wave_sum(qw);
+      const int w = threadIdx.x / kWave, first = (w / WPR) * WPR;
+      if ((threadIdx.x % kWave) == 0) {
+        lds[0][w] = cnt;
+        lds[1][w] = mw;
+        lds[2][w] = qw;
+      }
+      __syncthreads();
+      float sum = 0.f;
+#pragma unroll
+      for (int k = 0; k < WPR; ++k) sum += lds[0][first + k] * lds[1][first + k];
+      mean = sum * inv_n;
+      float m2 = 0.f;
+#pragma unroll
+      for (int k = 0; k < WPR; ++k) {
+        const float d = lds[1][first + k] - mean;
+        m2 += lds[2][first + k] + lds[0][first + k] * d * d;
+      }
+      rstd = rsqrtf(m2 * inv_n + p.eps);
+    } else {
+      float s = 0.f;
+#pragma unroll
+      for (int i = 0; i < NV; ++i) {
+        float f[VEC];
+        unpack(v[i], f, T{});
+#pragma unroll
+        for (int j = 0; j < VEC; ++j) s += (OP == kRmsNorm) ? f[j] * f[j] : f[j];
+      }
+      s = row_reduce_sum<WPR>(s, lds, 0);
+      if constexpr (OP == kRmsNorm) {
+        rstd = rsqrtf(s * inv_n + p.eps);
+      } else {
+        mean = s * inv_n;
+        float q = 0.f;
+#pragma unroll
+        for (int i = 0; i < NV; ++i) {
+          if (!live[i]) continue;
+          float f[VEC];
+          unpack(v[i], f, T{});
+#pragma unroll
+          for (int j = 0; j < VEC; ++j) {
+            const float d = f[j] - mean;
+            q += d * d;
+          }
+        }
+        q = row_reduce_sum<WPR>(q, lds, 1);
+        rstd = rsqrtf(q * inv_n + p.eps);
+      }
     }
     const T* g = static_cast<const T*>(p.gamma);
     const T* b = static_cast<const T*>(p.beta);
