@@ -918,6 +918,213 @@ extern "C" GHipValue ghip_fn_fused_sdpa(GHipFunction* f, GHipValue q, GHipValue 
   return f->add(std::move(n));
 }
 
+// ===========================================================================
+// Composite fused ops.  The reference builds these from primitive MPSGraph ops
+// (function.go:2288-2408, 2567-2667, 2976-3075); here they are built from this
+// Function's own primitives in the same order, so the lowering sees ordinary
+// DotGeneral + elementwise graphs and fuses bias / activation / slicing into the
+// GEMM epilogue like any other chain.
+// ===========================================================================
+namespace {
+
+// fp32 -> bf16 / f16 bits, round to nearest even (NaN quiet).
+uint16_t host_f32_to_bf16(float f) {
+  uint32_t u;
+  memcpy(&u, &f, 4);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((u >> 16) | 0x40u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return static_cast<uint16_t>(u >> 16);
+}
+
+// makeScalarConst (function.go:210-231): the value is taken as float32 and then
+// converted to dt.  The conversion happens here, at build time, so the constant
+// reaches the lowering as one literal of dt.
+GHipValue scalar_const(GHipFunction* f, int dt, double val, GHipError* err) {
+  const float v32 = static_cast<float>(val);
+  uint8_t buf[8];
+  size_t nb = 0;
+  switch (dt) {
+    case GHIP_DTYPE_FLOAT32: memcpy(buf, &v32, 4); nb = 4; break;
+    case GHIP_DTYPE_FLOAT64: { const double d = v32; memcpy(buf, &d, 8); nb = 8; break; }
+    case GHIP_DTYPE_BFLOAT16: { const uint16_t h = host_f32_to_bf16(v32); memcpy(buf, &h, 2); nb = 2; break; }
+    case GHIP_DTYPE_FLOAT16: { const _Float16 h = static_cast<_Float16>(v32); memcpy(buf, &h, 2); nb = 2; break; }
+    default: set_error(err, GHIP_ERR_INVALID_ARG, "scalar constant: dtype %s is not a float", dtype_name(dt)); return -1;
+  }
+  return ghip_fn_constant(f, dt, nullptr, 0, buf, nb, err);
+}
+
+// Prefixes err's message with "<op>: " (errors.Wrap in the reference).
+GHipValue wrap(GHipValue v, GHipError* err, const char* op) {
+  if (v < 0 && err && err->message) {
+    std::string m = std::string(op) + ": " + err->message;
+    set_error(err, err->code, "%s", m.c_str());
+  }
+  return v;
+}
+
+// bias broadcast over the trailing axes of `shape_of` and added (function.go:2601-2618).
+GHipValue add_trailing_bias(GHipFunction* f, GHipValue v, GHipValue bias, GHipError* err) {
+  const Shape rs = f->nodes[v].shape;
+  const Shape bs = f->nodes[bias].shape;
+  if (bs.rank() > rs.rank()) {
+    set_error(err, GHIP_ERR_INVALID_ARG, "bias rank %d exceeds result rank %d", bs.rank(), rs.rank());
+    return -1;
+  }
+  std::vector<int> axes(bs.rank());
+  for (int i = 0; i < bs.rank(); ++i) axes[i] = rs.rank() - bs.rank() + i;
+  const GHipValue b = ghip_fn_broadcast_in_dim(f, bias, rs.dims.data(), rs.rank(), axes.data(), bs.rank(), err);
+  if (b < 0) return -1;
+  return ghip_fn_binary(f, GHIP_BINARY_ADD, v, b, err);
+}
+
+// x [..., din] . w [din, ...] contracting x's last axis with w's first.
+GHipValue dense_dot(GHipFunction* f, GHipValue x, GHipValue w, GHipError* err) {
+  const int lc = f->nodes[x].shape.rank() - 1, rc = 0;
+  return ghip_fn_dot_general(f, x, &lc, 1, nullptr, 0, w, &rc, 1, nullptr, 0, err);
+}
+
+}  // namespace
+
+extern "C" GHipValue ghip_fn_fused_gelu(GHipFunction* f, GHipValue x, int exact, GHipError* err) {
+  FN_BEGIN("FusedGelu");
+  const Node* a = c.node(x);
+  if (!a) return -1;
+  const int dt = a->shape.dtype;
+  if (!dtype_is_float(dt)) return c.fail(GHIP_ERR_INVALID_ARG, "float input required, got %s", dtype_name(dt));
+  auto K = [&](double v) { return scalar_const(f, dt, v, err); };
+  auto mul = [&](GHipValue p, GHipValue q) { return p < 0 || q < 0 ? -1 : ghip_fn_binary(f, GHIP_BINARY_MUL, p, q, err); };
+  auto add = [&](GHipValue p, GHipValue q) { return p < 0 || q < 0 ? -1 : ghip_fn_binary(f, GHIP_BINARY_ADD, p, q, err); };
+  auto un = [&](int op, GHipValue p) { return p < 0 ? -1 : ghip_fn_unary(f, op, p, err); };
+  GHipValue r;
+  if (exact) {
+    // x * 0.5 * (1 + erf(x / sqrt(2))), evaluated as (0.5 x) (1 + erf(x (1/sqrt 2))).
+    const GHipValue half = K(0.5), inv_sqrt2 = K(0.7071067811865475), one = K(1.0);
+    const GHipValue e = un(GHIP_UNARY_ERF, mul(x, inv_sqrt2));
+    r = mul(mul(half, x), add(one, e));
+  } else {
+    // 0.5 x (1 + tanh(sqrt(2/pi) (x + 0.044715 x^3))), sqrt(2/pi) as the reference writes it.
+    const GHipValue half = K(0.5), one = K(1.0), coeff = K(0.044715), s2pi = K(0.7978845608);
+    const GHipValue x3 = mul(mul(x, x), x);
+    const GHipValue inner = add(x, mul(coeff, x3));
+    const GHipValue th = un(GHIP_UNARY_TANH, mul(s2pi, inner));
+    r = mul(mul(half, x), add(one, th));
+  }
+  return wrap(r, err, "FusedGelu");
+}
+
+extern "C" GHipValue ghip_fn_fused_dense(GHipFunction* f, GHipValue x, GHipValue weight, GHipValue bias,
+                                         int activation, GHipError* err) {
+  FN_BEGIN("FusedDense");
+  const Node* xn = c.node(x);
+  if (!xn) return -1;
+  const Node* wn = c.node(weight);
+  if (!wn) return -1;
+  if (bias >= 0 && !c.node(bias)) return -1;
+  if (xn->shape.rank() < 1 || wn->shape.rank() < 2)
+    return c.fail(GHIP_ERR_INVALID_ARG, "x must have rank >= 1 (got %d), weight must have rank >= 2 (got %d)",
+                  xn->shape.rank(), wn->shape.rank());
+  const int64_t in_features = xn->shape.dims.back();
+  if (in_features != wn->shape.dims[0])
+    return c.fail(GHIP_ERR_INVALID_ARG, "x's last dim (%lld) must match weight's first dim (%lld)",
+                  static_cast<long long>(in_features), static_cast<long long>(wn->shape.dims[0]));
+  if (activation < GHIP_ACTIVATION_NONE || activation > GHIP_ACTIVATION_TANH)
+    return c.fail(GHIP_ERR_INVALID_ARG, "unsupported activation type %d", activation);
+  GHipValue r = wrap(dense_dot(f, x, weight, err), err, "FusedDense: DotGeneral");
+  if (r < 0) return -1;
+  if (bias >= 0) {
+    r = wrap(add_trailing_bias(f, r, bias, err), err, "FusedDense: bias");
+    if (r < 0) return -1;
+  }
+  const int dt = f->nodes[r].shape.dtype;
+  switch (activation) {
+    case GHIP_ACTIVATION_GELU:
+      return wrap(ghip_fn_fused_gelu(f, r, 0, err), err, "FusedDense: GELU activation");
+    case GHIP_ACTIVATION_RELU: {
+      const GHipValue zero = scalar_const(f, dt, 0.0, err);
+      return wrap(zero < 0 ? -1 : ghip_fn_binary(f, GHIP_BINARY_MAX, r, zero, err), err, "FusedDense: ReLU");
+    }
+    case GHIP_ACTIVATION_SILU: {
+      const GHipValue s = ghip_fn_unary(f, GHIP_UNARY_LOGISTIC, r, err);
+      return wrap(s < 0 ? -1 : ghip_fn_binary(f, GHIP_BINARY_MUL, r, s, err), err, "FusedDense: SiLU");
+    }
+    case GHIP_ACTIVATION_TANH:
+      return wrap(ghip_fn_unary(f, GHIP_UNARY_TANH, r, err), err, "FusedDense: Tanh");
+    default:
+      return r;
+  }
+}
+
+extern "C" int ghip_fn_fused_qkv_projection(GHipFunction* f, GHipValue x, GHipValue w_qkv, GHipValue bias_q,
+                                            GHipValue bias_k, GHipValue bias_v, int query_dim, int key_value_dim,
+                                            GHipValue* query, GHipValue* key, GHipValue* value, GHipError* err) {
+  FN_BEGIN("FusedAttentionQKVProjection");
+  auto code = [&]() { return err && err->code ? err->code : GHIP_ERR_INVALID_ARG; };
+  if (!query || !key || !value) {
+    c.fail(GHIP_ERR_INVALID_ARG, "null output pointer");
+    return GHIP_ERR_INVALID_ARG;
+  }
+  *query = *key = *value = -1;
+  const Node* xn = c.node(x);
+  if (!xn || !c.node(w_qkv)) return code();
+  for (GHipValue b : {bias_q, bias_k, bias_v})
+    if (b >= 0 && !c.node(b)) return code();
+  if (xn->shape.rank() < 1) {
+    c.fail(GHIP_ERR_INVALID_ARG, "x must have rank >= 1, got %d", xn->shape.rank());
+    return GHIP_ERR_INVALID_ARG;
+  }
+  if (query_dim < 0 || key_value_dim < 0) {
+    c.fail(GHIP_ERR_INVALID_ARG, "negative queryDim (%d) or keyValueDim (%d)", query_dim, key_value_dim);
+    return GHIP_ERR_INVALID_ARG;
+  }
+  const int64_t q = query_dim, kv = key_value_dim;
+  const int64_t lo[3] = {0, q, q + kv}, hi[3] = {q, q + kv, q + 2 * kv};
+  const char* what[3] = {"FusedAttentionQKVProjection: slice Q", "FusedAttentionQKVProjection: slice K",
+                         "FusedAttentionQKVProjection: slice V"};
+  auto slice_last = [&](GHipValue t, int64_t a, int64_t b, const char* msg) -> GHipValue {
+    const Shape ts = f->nodes[t].shape;
+    const int r = ts.rank();
+    std::vector<int64_t> st(r, 0), lim = ts.dims, str(r, 1);
+    st[r - 1] = a;
+    lim[r - 1] = b;
+    return wrap(ghip_fn_slice(f, t, st.data(), lim.data(), str.data(), r, err), err, msg);
+  };
+  GHipValue out[3] = {-1, -1, -1};
+  const bool any_bias = bias_q >= 0 || bias_k >= 0 || bias_v >= 0;
+  if (any_bias && f->nodes[w_qkv].shape.rank() >= 2) {
+    // With biases: one product per output over the matching columns of wQKV.
+    // Every output element is the same K-sum as in x . wQKV (the GEMM's
+    // summation order does not depend on N), and each product's bias add runs
+    // in its GEMM epilogue instead of as a separate pass over a strided slice.
+    for (int i = 0; i < 3; ++i) {
+      const GHipValue ws = slice_last(w_qkv, lo[i], hi[i], what[i]);
+      if (ws < 0) return code();
+      out[i] = wrap(dense_dot(f, x, ws, err), err, "FusedAttentionQKVProjection: DotGeneral");
+      if (out[i] < 0) return code();
+    }
+  } else {
+    // One product x . wQKV -> [..., queryDim + 2 keyValueDim], sliced on its last
+    // axis (zero-copy views of the product).
+    const GHipValue comb = wrap(dense_dot(f, x, w_qkv, err), err, "FusedAttentionQKVProjection: DotGeneral");
+    if (comb < 0) return code();
+    for (int i = 0; i < 3; ++i) {
+      out[i] = slice_last(comb, lo[i], hi[i], what[i]);
+      if (out[i] < 0) return code();
+    }
+  }
+  const GHipValue biases[3] = {bias_q, bias_k, bias_v};
+  const char* names[3] = {"FusedAttentionQKVProjection: biasQ", "FusedAttentionQKVProjection: biasK",
+                          "FusedAttentionQKVProjection: biasV"};
+  for (int i = 0; i < 3; ++i) {
+    if (biases[i] < 0) continue;
+    out[i] = wrap(add_trailing_bias(f, out[i], biases[i], err), err, names[i]);
+    if (out[i] < 0) return code();
+  }
+  *query = out[0];
+  *key = out[1];
+  *value = out[2];
+  return GHIP_OK;
+}
+
 extern "C" int ghip_fn_return(GHipFunction* f, const GHipValue* outputs, int cnt, GHipError* err) {
   FN_BEGIN("Return");
   if (!f) return c.fail(GHIP_ERR_INVALID_ARG, "null function");

@@ -122,6 +122,10 @@ _GRAPH_SIGS = {
     "ghip_fn_fused_softmax": ([_vp, _int, _int, _errp], _int),
     "ghip_fn_fused_layer_norm": ([_vp, _int, _intp, _int, _dbl, _int, _int, _errp], _int),
     "ghip_fn_fused_sdpa": ([_vp, _int, _int, _int, _int, _int, _int, _int, _dbl, _int, _errp], _int),
+    "ghip_fn_fused_gelu": ([_vp, _int, _int, _errp], _int),
+    "ghip_fn_fused_dense": ([_vp, _int, _int, _int, _int, _errp], _int),
+    "ghip_fn_fused_qkv_projection": ([_vp, _int, _int, _int, _int, _int, _int, _int, _intp, _intp,
+                                      _intp, _errp], _int),
     "ghip_fn_return": ([_vp, _intp, _int, _errp], _int),
     "ghip_fn_value_shape": ([_vp, _int, _intp, _i64p, _int], _int),
     "ghip_exec_num_inputs": ([_vp], _int),
@@ -465,6 +469,24 @@ class Function:
                                        causal: bool, options=None) -> Value:
         return self._call("ghip_fn_fused_sdpa", query.id, key.id, value.id, _vid(mask), num_heads,
                           num_kv_heads, axes_layout, float(scale), int(causal))
+
+    def FusedGelu(self, x, exact: bool) -> Value:
+        return self._call("ghip_fn_fused_gelu", x.id, int(exact))
+
+    def FusedDense(self, x, weight, bias, activation: int) -> Value:
+        return self._call("ghip_fn_fused_dense", x.id, weight.id, _vid(bias), int(activation))
+
+    def FusedAttentionQKVProjection(self, x, w_qkv, bias_q, bias_k, bias_v, query_dim: int,
+                                    key_value_dim: int):
+        """Returns (query, key, value)."""
+        out = [ctypes.c_int(-1) for _ in range(3)]
+        err = GHipError(0, None)
+        rc = _L().ghip_fn_fused_qkv_projection(self.handle, x.id, w_qkv.id, _vid(bias_q), _vid(bias_k),
+                                                _vid(bias_v), int(query_dim), int(key_value_dim),
+                                                *(ctypes.byref(o) for o in out), ctypes.byref(err))
+        if rc != 0:
+            _raise(err, rc)
+        return tuple(Value(self, o.value) for o in out)
 
 
 def _add_unary(name, code):

@@ -281,6 +281,30 @@ GHipValue ghip_fn_fused_layer_norm(GHipFunction* f, GHipValue x, const int* axes
 GHipValue ghip_fn_fused_sdpa(GHipFunction* f, GHipValue q, GHipValue k, GHipValue v,
                              GHipValue mask, int num_heads, int num_kv_heads, int layout,
                              double scale, int causal, GHipError* err); /* :2669-2907 */
+/* Composite fused ops, built from the primitives above in the order the
+ * reference composes them, so the lowering fuses them like any other chain
+ * (bias / activation / slicing run in the GEMM epilogue).
+ * FusedGelu (:2288-2408): exact = x/2 (1 + erf(x/sqrt 2)); otherwise the tanh
+ * approximation with the reference's constants. */
+GHipValue ghip_fn_fused_gelu(GHipFunction* f, GHipValue x, int exact, GHipError* err);
+/* backends.ActivationType values FusedDense takes (names as in GoMLX; a cgo
+ * binding maps GoMLX's constants onto these by name). */
+enum {
+  GHIP_ACTIVATION_NONE = 0, GHIP_ACTIVATION_GELU, GHIP_ACTIVATION_RELU, GHIP_ACTIVATION_SILU,
+  GHIP_ACTIVATION_TANH
+};
+/* FusedDense (:2567-2667): x [..., din] . weight [din, ...] + bias (broadcast over
+ * the trailing axes; -1 = none), then the activation (GELU = tanh approximation,
+ * as the reference calls FusedGelu with exact = false). */
+GHipValue ghip_fn_fused_dense(GHipFunction* f, GHipValue x, GHipValue weight, GHipValue bias,
+                              int activation, GHipError* err);
+/* FusedAttentionQKVProjection (:2976-3075): x . wQKV sliced on the last axis into
+ * [0, qdim), [qdim, qdim+kvdim), [qdim+kvdim, qdim+2 kvdim), each plus its bias
+ * (-1 = none).  Writes the three values; returns GHIP_OK or the error code. */
+int ghip_fn_fused_qkv_projection(GHipFunction* f, GHipValue x, GHipValue w_qkv, GHipValue bias_q,
+                                 GHipValue bias_k, GHipValue bias_v, int query_dim,
+                                 int key_value_dim, GHipValue* query, GHipValue* key,
+                                 GHipValue* value, GHipError* err);
 int ghip_fn_return(GHipFunction* f, const GHipValue* outputs, int n, GHipError* err); /* :337-345 */
 /* OpShape (builder.go:63-69): dtype + dims of a value; returns rank or -1. */
 int ghip_fn_value_shape(GHipFunction* f, GHipValue v, int* dtype, int64_t* dims, int max_rank);

@@ -344,6 +344,31 @@ void orc_iota(double* out, int64_t outer, int64_t n, int64_t inner) {
       for (int64_t j = 0; j < inner; ++j) out[(o * n + i) * inner + j] = (double)i;
 }
 
+/* ---------------------------------------------------------------------------
+ * Activations of FusedDense / FusedGelu.
+ * Reference: Function.FusedGelu (mpsgraph/gomlx/function.go:2288-2408):
+ *   exact:  x * 0.5 * (1 + erf(x / sqrt 2));
+ *   approx: 0.5 * x * (1 + tanh(0.7978845608 * (x + 0.044715 x^3)));
+ * FusedDense (function.go:2620-2664): GELU is the approximate form, ReLU
+ * max(x, 0), SiLU x * sigmoid(x), Tanh tanh(x).
+ * ------------------------------------------------------------------------- */
+void orc_activation(const double* x, double* y, int64_t n, int act) {
+#pragma omp parallel for schedule(static)
+  for (int64_t i = 0; i < n; ++i) {
+    const double v = x[i];
+    double r = v;
+    switch (act) {
+      case ORC_ACT_GELU: r = 0.5 * v * (1.0 + tanh(0.7978845608 * (v + 0.044715 * v * v * v))); break;
+      case ORC_ACT_GELU_EXACT: r = 0.5 * v * (1.0 + erf(v * 0.7071067811865475)); break;
+      case ORC_ACT_RELU: r = isnan(v) ? v : (v > 0.0 ? v : 0.0); break;
+      case ORC_ACT_SILU: r = v / (1.0 + exp(-v)); break;
+      case ORC_ACT_TANH: r = tanh(v); break;
+      default: break;
+    }
+    y[i] = r;
+  }
+}
+
 void orc_f32_to_bf16(const float* x, uint16_t* y, int64_t n) {
   for (int64_t i = 0; i < n; ++i) {
     uint32_t u;

@@ -30,6 +30,11 @@
  *   orc_argminmax    reference known answer (mpsgraph_test.go:973-990),
  *                    numpy.argmax/argmin on tie-free data.
  *   orc_iota         reference known answer (mpsgraph_test.go:795-821).
+ *   orc_activation   reference known answers for GELU (mpsgraph_test.go:2645-2656)
+ *                    and ReLU through FusedDense (:2841-2852); odd-part identity
+ *                    g(x) - g(-x) = x for both GELU forms; exact GELU against
+ *                    x * Phi(x) from the normal CDF (scipy); tanh approximation
+ *                    within 1e-3 of exact; SiLU against x / (1 + e^-x).
  */
 #ifndef GOMLX_HIP_ORACLE_H
 #define GOMLX_HIP_ORACLE_H
@@ -91,6 +96,13 @@ void orc_argminmax(const float* x, int64_t outer, int64_t n, int64_t inner, int 
 
 /* Iota: out viewed as [outer, n, inner], out[o, i, j] = i. */
 void orc_iota(double* out, int64_t outer, int64_t n, int64_t inner);
+
+/* Activation functions of FusedDense / FusedGelu in fp64, elementwise over n
+ * values: ORC_ACT_NONE, ORC_ACT_GELU (tanh approximation), ORC_ACT_RELU,
+ * ORC_ACT_SILU, ORC_ACT_TANH, ORC_ACT_GELU_EXACT. */
+enum { ORC_ACT_NONE = 0, ORC_ACT_GELU = 1, ORC_ACT_RELU = 2, ORC_ACT_SILU = 3, ORC_ACT_TANH = 4,
+       ORC_ACT_GELU_EXACT = 5 };
+void orc_activation(const double* x, double* y, int64_t n, int act);
 
 /* fp32 -> bf16 (round to nearest even; NaN stays NaN), as 16-bit patterns. */
 void orc_f32_to_bf16(const float* x, uint16_t* y, int64_t n);

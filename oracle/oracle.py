@@ -56,6 +56,7 @@ def lib():
         L.orc_argminmax.argtypes = [_f32p, _i64, _i64, _i64, _int, _i64p]
         L.orc_iota.argtypes = [_f64p, _i64, _i64, _i64]
         L.orc_f32_to_bf16.argtypes = [_f32p, _u16p, _i64]
+        L.orc_activation.argtypes = [_f64p, _f64p, _i64, _int]
         _lib = L
     return _lib
 
@@ -195,6 +196,42 @@ def iota(shape, axis) -> np.ndarray:
     out = np.empty(tuple(shape), np.float64)
     lib().orc_iota(out, outer, n, inner)
     return out
+
+
+ACT_NONE, ACT_GELU, ACT_RELU, ACT_SILU, ACT_TANH, ACT_GELU_EXACT = range(6)
+
+
+def activation(x, act: int) -> np.ndarray:
+    """FusedDense / FusedGelu activations in fp64 (function.go:2288-2408, 2620-2664)."""
+    x = np.ascontiguousarray(np.asarray(x, np.float64))
+    y = np.empty_like(x)
+    lib().orc_activation(x.reshape(-1), y.reshape(-1), x.size, int(act))
+    return y
+
+
+def gelu(x, exact: bool) -> np.ndarray:
+    """FusedGelu (function.go:2288-2408)."""
+    return activation(x, ACT_GELU_EXACT if exact else ACT_GELU)
+
+
+def dense(x, w, bias=None, act: int = ACT_NONE) -> np.ndarray:
+    """FusedDense (function.go:2567-2667): x's last axis contracted with w's first,
+    plus bias broadcast over the trailing axes, then the activation."""
+    x = _f32(x)
+    y = dot_general(x, [x.ndim - 1], [], w, [0], [])
+    if bias is not None:
+        y = y + np.asarray(bias, np.float64)
+    return activation(y, act)
+
+
+def qkv_projection(x, w, bq, bk, bv, query_dim: int, key_value_dim: int):
+    """FusedAttentionQKVProjection (function.go:2976-3075): x . w sliced on the last
+    axis into Q [0, q), K [q, q+kv), V [q+kv, q+2kv), each plus its bias."""
+    x = _f32(x)
+    y = dot_general(x, [x.ndim - 1], [], w, [0], [])
+    q, kv = query_dim, key_value_dim
+    outs = [y[..., :q], y[..., q:q + kv], y[..., q + kv:q + 2 * kv]]
+    return tuple(o if b is None else o + np.asarray(b, np.float64) for o, b in zip(outs, (bq, bk, bv)))
 
 
 def f32_to_bf16_bits(x) -> np.ndarray:

@@ -95,6 +95,47 @@ CASES = {
         "source": "mpsgraph_test.go:1485-1532 (TestConvertDType)",
         "x": [1.7, 2.3, -0.9], "expected": [1, 2, 0],
     },
+    "gelu": {
+        "source": "mpsgraph_test.go:2645-2656 (TestFusedGelu)",
+        "x": [0.0, 1.0, -1.0, 3.0], "tol": 1e-3,
+        "expected": [0.0, 0.8413, -0.1587, 2.9960],
+    },
+    "dense_no_bias": {
+        "source": "mpsgraph_test.go:2809-2825 (TestFusedDense/no_activation_no_bias)",
+        "x_shape": [2, 3], "x": [1, 2, 3, 4, 5, 6],
+        "w_shape": [3, 4], "w": [1, 0, 0, 0, 0, 1, 0, 0, 0, 0, 1, 0],
+        "activation": "none", "tol": 1e-4,
+        "expected": [1, 2, 3, 0, 4, 5, 6, 0],
+    },
+    "dense_bias": {
+        "source": "mpsgraph_test.go:2827-2839 (TestFusedDense/with_bias)",
+        "x_shape": [2, 2], "x": [1, 0, 0, 1],
+        "w_shape": [2, 2], "w": [2, 0, 0, 3], "bias": [10, 20],
+        "activation": "none", "tol": 1e-4,
+        "expected": [12, 20, 10, 23],
+    },
+    "dense_relu": {
+        "source": "mpsgraph_test.go:2841-2852 (TestFusedDense/relu_activation)",
+        "x_shape": [2, 2], "x": [1, -1, -1, 1],
+        "w_shape": [2, 2], "w": [1, 0, 0, 1],
+        "activation": "relu", "tol": 1e-4,
+        "expected": [1, 0, 0, 1],
+    },
+    "qkv_identity": {
+        "source": "mpsgraph_test.go:2900-2931 (TestFusedAttentionQKVProjection/identity_weights)",
+        "x_shape": [2, 6], "x": list(range(1, 13)),
+        "w_shape": [6, 6], "w": [1.0 if i % 7 == 0 else 0.0 for i in range(36)],
+        "query_dim": 2, "key_value_dim": 2, "tol": 1e-4,
+        "q": [1, 2, 7, 8], "k": [3, 4, 9, 10], "v": [5, 6, 11, 12],
+    },
+    "qkv_biases": {
+        "source": "mpsgraph_test.go:2933-2962 (TestFusedAttentionQKVProjection/with_biases)",
+        "x_shape": [1, 4], "x": [1, 2, 3, 4],
+        "w_shape": [4, 6], "w": [1.0 if i in (0, 7, 14, 21) else 0.0 for i in range(24)],
+        "bias_q": [10, 20], "bias_k": [100, 200], "bias_v": [1000, 2000],
+        "query_dim": 2, "key_value_dim": 2, "tol": 1e-4,
+        "q": [11, 22], "k": [103, 204], "v": [1000, 2000],
+    },
 }
 
 if __name__ == "__main__":

@@ -1,0 +1,178 @@
+"""FusedGelu, FusedDense and FusedAttentionQKVProjection on the GPU.
+
+The reference builds these from primitive ops (function.go:2288-2408,
+2567-2667, 2976-3075); here they are composites of this backend's primitives
+whose bias / activation run in the GEMM epilogue.  Checked against the
+reference's own known answers (mpsgraph_test.go:2645-2656, 2805-2962), against
+the CPU oracle at transformer-sized shapes, and bit-for-bit against the
+unfused plan (GHIP_EPILOGUE_FUSION=0)."""
+import os
+
+import numpy as np
+import pytest
+
+from oracle import oracle as orc
+from gomlx_hip import synth
+from gomlx_hip.backend import ActivationType, Backend, BackendError, dtypes, make_shape
+from conftest import rel_err
+
+pytestmark = pytest.mark.gpu
+
+F32, BF16 = dtypes.Float32, dtypes.BFloat16
+ACTS = {"none": ActivationType.NONE, "gelu": ActivationType.GELU, "relu": ActivationType.RELU,
+        "silu": ActivationType.SILU, "tanh": ActivationType.TANH}
+ORC_ACTS = {"none": orc.ACT_NONE, "gelu": orc.ACT_GELU, "relu": orc.ACT_RELU,
+            "silu": orc.ACT_SILU, "tanh": orc.ACT_TANH}
+
+
+@pytest.fixture(scope="module")
+def be(cuda):
+    b = Backend("")
+    yield b
+    b.Finalize()
+
+
+def run(be, build, inputs, fuse=True):
+    """Returns (plan text, [(dtype, raw array)]) for build(f, *params)."""
+    old = os.environ.get("GHIP_EPILOGUE_FUSION")
+    os.environ["GHIP_EPILOGUE_FUSION"] = "1" if fuse else "0"
+    try:
+        b = be.Builder("fd")
+        f = b.Main()
+        params = [f.Parameter(f"p{i}", s) for i, (_, s) in enumerate(inputs)]
+        f.Return(list(build(f, *params)))
+        ex = b.Compile()
+    finally:
+        if old is None:
+            del os.environ["GHIP_EPILOGUE_FUSION"]
+        else:
+            os.environ["GHIP_EPILOGUE_FUSION"] = old
+    plan = ex.Plan()
+    bufs = [be.BufferFromFlatData(0, a, s) for a, s in inputs]
+    outs = []
+    for r in ex.Execute(bufs, None, 0):
+        s = be.BufferShape(r)
+        outs.append((s.dtype, be.BufferToFlatData(r).reshape(s.dims).copy()))
+    ex.Finalize()
+    return plan, outs
+
+
+def as_f(o):
+    dt, a = o
+    return synth.bf16_bits_to_f32(a) if dt == BF16 else a.astype(np.float64)
+
+
+# ------------------------------------------------------------ reference known answers
+def test_fused_gelu_known_answer(be, known):                      # mpsgraph_test.go:2645-2656
+    c = known["gelu"]
+    for exact in (False, True):
+        _, (y,) = run(be, lambda f, x: [f.FusedGelu(x, exact)], [(np.array(c["x"], np.float32), make_shape(F32, 4))])
+        assert np.max(np.abs(as_f(y) - c["expected"])) <= c["tol"]
+        assert np.max(np.abs(as_f(y) - orc.gelu(np.array(c["x"]), exact))) <= 1e-6
+
+
+@pytest.mark.parametrize("name", ["dense_no_bias", "dense_bias", "dense_relu"])
+def test_fused_dense_known_answers(be, known, name):              # mpsgraph_test.go:2805-2852
+    c = known[name]
+    ins = [(np.array(c["x"], np.float32), make_shape(F32, *c["x_shape"])),
+           (np.array(c["w"], np.float32), make_shape(F32, *c["w_shape"]))]
+    if "bias" in c:
+        ins.append((np.array(c["bias"], np.float32), make_shape(F32, len(c["bias"]))))
+    _, (y,) = run(be, lambda f, x, w, *b: [f.FusedDense(x, w, b[0] if b else None, ACTS[c["activation"]])], ins)
+    assert np.max(np.abs(as_f(y).reshape(-1) - c["expected"])) <= c["tol"]
+
+
+@pytest.mark.parametrize("name", ["qkv_identity", "qkv_biases"])
+def test_fused_qkv_known_answers(be, known, name):                # mpsgraph_test.go:2896-2962
+    c = known[name]
+    ins = [(np.array(c["x"], np.float32), make_shape(F32, *c["x_shape"])),
+           (np.array(c["w"], np.float32), make_shape(F32, *c["w_shape"]))]
+    nb = 0
+    if "bias_q" in c:
+        for k in ("bias_q", "bias_k", "bias_v"):
+            ins.append((np.array(c[k], np.float32), make_shape(F32, len(c[k]))))
+        nb = 3
+
+    def build(f, x, w, *b):
+        bq, bk, bv = b if nb else (None, None, None)
+        return f.FusedAttentionQKVProjection(x, w, bq, bk, bv, c["query_dim"], c["key_value_dim"])
+
+    _, outs = run(be, build, ins)
+    for o, key in zip(outs, "qkv"):
+        assert np.max(np.abs(as_f(o).reshape(-1) - c[key])) <= c["tol"]
+
+
+def test_fused_dense_errors(be):
+    b = be.Builder("err")
+    f = b.Main()
+    x = f.Parameter("x", make_shape(F32, 2, 3))
+    with pytest.raises(BackendError, match="must match weight's first dim"):
+        f.FusedDense(x, f.Parameter("w", make_shape(F32, 4, 3)), None, ActivationType.NONE)
+    with pytest.raises(BackendError, match="weight must have rank >= 2"):
+        f.FusedDense(x, f.Parameter("w1", make_shape(F32, 3)), None, ActivationType.NONE)
+    with pytest.raises(BackendError, match="unsupported activation type 7"):
+        f.FusedDense(x, f.Parameter("w2", make_shape(F32, 3, 3)), None, 7)
+    with pytest.raises(BackendError, match="slice V"):
+        f.FusedAttentionQKVProjection(x, f.Parameter("w3", make_shape(F32, 3, 5)), None, None, None, 2, 2)
+    b.Finalize()
+
+
+# ------------------------------------------------------------ transformer-sized, vs oracle
+def _bf16_input(shape, scale, seed):
+    a = np.random.default_rng(seed).standard_normal(shape).astype(np.float32) * scale
+    return synth.round_bf16(a)
+
+
+@pytest.mark.parametrize("act", ["none", "gelu", "relu", "silu", "tanh"])
+def test_fused_dense_bf16_vs_oracle(be, act):
+    M, K, N = 1000, 512, 776           # ragged M and N: partial tiles on both axes
+    x = _bf16_input((2, M // 2, K), 1.0, 11)
+    w = _bf16_input((K, N), K ** -0.5, 12)
+    bias = _bf16_input((N,), 0.5, 13)
+    ins = [(synth.to_bf16_bits(x), make_shape(BF16, 2, M // 2, K)),
+           (synth.to_bf16_bits(w), make_shape(BF16, K, N)),
+           (synth.to_bf16_bits(bias), make_shape(BF16, N))]
+    build = lambda f, xx, ww, bb: [f.FusedDense(xx, ww, bb, ACTS[act])]
+    plan, (y,) = run(be, build, ins)
+    assert "gemm_batched+epilogue" in plan and "fused_elementwise" not in plan, plan
+    ref = orc.dense(x, w, bias, ORC_ACTS[act])
+    # bf16 product, bias add and activation steps each round to bf16
+    assert rel_err(as_f(y), ref) <= 3e-2
+    _, (y0,) = run(be, build, ins, fuse=False)
+    assert np.array_equal(y[1], y0[1]), "fused epilogue differs from the unfused plan"
+
+
+def test_fused_gelu_exact_bf16_chain(be):
+    x = _bf16_input((64, 1000), 2.0, 21)
+    ins = [(synth.to_bf16_bits(x), make_shape(BF16, 64, 1000))]
+    plan, (y,) = run(be, lambda f, xx: [f.FusedGelu(xx, True)], ins)
+    assert plan.count("fused_elementwise") == 1, plan      # one generated kernel for the chain
+    assert rel_err(as_f(y), orc.gelu(x, True)) <= 3e-2
+
+
+@pytest.mark.parametrize("with_bias", [False, True])
+def test_fused_qkv_bf16_vs_oracle(be, with_bias):
+    T, d, q, kv = 1024, 512, 512, 256      # grouped-query sizes: K/V narrower than Q
+    x = _bf16_input((4, T // 4, d), 1.0, 31)
+    w = _bf16_input((d, q + 2 * kv), d ** -0.5, 32)
+    ins = [(synth.to_bf16_bits(x), make_shape(BF16, 4, T // 4, d)),
+           (synth.to_bf16_bits(w), make_shape(BF16, d, q + 2 * kv))]
+    bs = [None, None, None]
+    if with_bias:
+        bs = [_bf16_input((n,), 0.5, 40 + i) for i, n in enumerate((q, kv, kv))]
+        ins += [(synth.to_bf16_bits(b), make_shape(BF16, b.size)) for b in bs]
+
+    def build(f, xx, ww, *b):
+        bb = b if with_bias else (None, None, None)
+        return f.FusedAttentionQKVProjection(xx, ww, bb[0], bb[1], bb[2], q, kv)
+
+    plan, outs = run(be, build, ins)
+    assert "fused_elementwise" not in plan, plan
+    refs = orc.qkv_projection(x, w, bs[0], bs[1], bs[2], q, kv)
+    for o, r, n in zip(outs, refs, (q, kv, kv)):
+        assert o[1].shape == (4, T // 4, n)
+        assert rel_err(as_f(o), r) <= 2e-2
+    if with_bias:
+        _, outs0 = run(be, build, ins, fuse=False)
+        for o, o0 in zip(outs, outs0):
+            assert np.array_equal(o[1], o0[1])

@@ -222,3 +222,59 @@ def test_bf16_rounding_matches_numpy_port():
     assert np.array_equal(a, b)
     # ties to even: 1 + 2^-8 -> 1.0, 1 + 3*2^-8 -> 1 + 2^-6
     assert synth.bf16_bits_to_f32(a[4096:4098]).tolist() == [1.0, 1.0 + 2 ** -6]
+
+
+# ---------------------------------------------------------------- FusedGelu / FusedDense / QKV
+def test_gelu_known_answer(known):
+    c = known["gelu"]
+    x = np.array(c["x"])
+    for exact in (False, True):
+        assert np.max(np.abs(orc.gelu(x, exact) - np.array(c["expected"]))) <= c["tol"]
+
+
+def test_activation_identities():
+    from scipy.special import erf, ndtr
+    x = np.linspace(-8, 8, 4001)
+    for act in (orc.ACT_GELU, orc.ACT_GELU_EXACT):
+        g = orc.activation(x, act)
+        # odd part: g(x) - g(-x) = x for x*Phi(x) and for its tanh approximation
+        assert np.max(np.abs(g - orc.activation(-x, act) - x)) < 1e-12
+    ex = orc.gelu(x, True)
+    assert np.max(np.abs(ex - x * ndtr(x))) < 1e-12               # x * Phi(x), normal CDF
+    assert np.max(np.abs(ex - 0.5 * x * (1 + erf(x / np.sqrt(2))))) < 1e-12
+    assert np.max(np.abs(orc.gelu(x, False) - ex)) < 1e-3          # tanh form tracks the exact one
+    assert np.max(np.abs(orc.activation(x, orc.ACT_SILU) - x / (1 + np.exp(-x)))) < 1e-12
+    assert np.array_equal(orc.activation(x, orc.ACT_RELU), np.maximum(x, 0))
+    assert np.max(np.abs(orc.activation(x, orc.ACT_TANH) - np.tanh(x))) < 1e-15
+    assert np.array_equal(orc.activation(x, orc.ACT_NONE), x)
+
+
+@pytest.mark.parametrize("name", ["dense_no_bias", "dense_bias", "dense_relu"])
+def test_dense_known_answers(known, name):
+    c = known[name]
+    x = np.array(c["x"], np.float32).reshape(c["x_shape"])
+    w = np.array(c["w"], np.float32).reshape(c["w_shape"])
+    act = {"none": orc.ACT_NONE, "relu": orc.ACT_RELU}[c["activation"]]
+    y = orc.dense(x, w, c.get("bias"), act)
+    assert np.max(np.abs(y.reshape(-1) - np.array(c["expected"]))) <= c["tol"]
+
+
+def test_dense_against_numpy():
+    rng = np.random.default_rng(5)
+    x = rng.standard_normal((3, 5, 7)).astype(np.float32)
+    w = rng.standard_normal((7, 2, 4)).astype(np.float32)   # rank-3 weight: trailing dims kept
+    b = rng.standard_normal((2, 4)).astype(np.float32)
+    y = orc.dense(x, w, b, orc.ACT_TANH)
+    ref = np.tanh(np.tensordot(x.astype(np.float64), w.astype(np.float64), axes=([2], [0])) + b)
+    assert y.shape == (3, 5, 2, 4) and np.max(np.abs(y - ref)) < 1e-12
+
+
+@pytest.mark.parametrize("name", ["qkv_identity", "qkv_biases"])
+def test_qkv_projection_known_answers(known, name):
+    c = known[name]
+    x = np.array(c["x"], np.float32).reshape(c["x_shape"])
+    w = np.array(c["w"], np.float32).reshape(c["w_shape"])
+    outs = orc.qkv_projection(x, w, c.get("bias_q"), c.get("bias_k"), c.get("bias_v"),
+                              c["query_dim"], c["key_value_dim"])
+    for o, key in zip(outs, "qkv"):
+        assert np.max(np.abs(o.reshape(-1) - np.array(c[key]))) <= c["tol"]
