@@ -77,6 +77,50 @@ std::string fmt(const char* f, ...) {
   return buf;
 }
 
+// Strides that present a strided view of dims `od` (strides `os`, row-major
+// element order) as dims `nd` without moving data, when they exist: every run of
+// old dims that the new dims regroup must be laid out as one row-major block
+// (os[k] == od[k+1] * os[k+1] inside the run).  Size-1 dims impose nothing.
+static bool reshape_strides(const std::vector<int64_t>& od, const std::vector<int64_t>& os,
+                            const std::vector<int64_t>& nd, std::vector<int64_t>* ns) {
+  std::vector<int64_t> d, st;
+  int64_t total = 1;
+  for (size_t i = 0; i < od.size(); ++i) {
+    total *= od[i];
+    if (od[i] != 1) d.push_back(od[i]), st.push_back(os[i]);
+  }
+  ns->assign(nd.size(), 1);
+  if (total == 0) {
+    *ns = contiguous_strides(nd);
+    return true;
+  }
+  size_t i = 0, j = 0;
+  const size_t n_old = d.size(), n_new = nd.size();
+  while (i < n_old && j < n_new) {
+    const size_t i0 = i, j0 = j;
+    int64_t po = d[i], pn = nd[j];
+    while (po != pn) {
+      if (pn < po) {
+        if (++j >= n_new) return false;
+        pn *= nd[j];
+      } else {
+        if (++i >= n_old) return false;
+        po *= d[i];
+      }
+    }
+    for (size_t k = i0; k < i; ++k)
+      if (st[k] != d[k + 1] * st[k + 1]) return false;
+    (*ns)[j] = st[i];
+    for (size_t k = j; k > j0; --k) (*ns)[k - 1] = (*ns)[k] * nd[k];
+    ++i;
+    ++j;
+  }
+  if (i != n_old) return false;
+  for (; j < n_new; ++j)
+    if (nd[j] != 1) return false;
+  return true;
+}
+
 struct Lowerer {
   GHipBackend* be;
   GHipFunction* fn;
@@ -388,9 +432,15 @@ struct Lowerer {
         case Kind::Reshape: {
           View s = get(n.in[0]);
           if (failed) return bad();
-          s = materialize(s, N[n.in[0]].shape);
-          r = s;
-          r.strides = contiguous_strides(n.shape.dims);
+          std::vector<int64_t> st;
+          if (reshape_strides(N[n.in[0]].shape.dims, s.strides, n.shape.dims, &st)) {
+            r = s;  // zero-copy: the new dims group the old ones without crossing a stride break
+            r.strides = st;
+          } else {
+            s = materialize(s, N[n.in[0]].shape);
+            r = s;
+            r.strides = contiguous_strides(n.shape.dims);
+          }
           break;
         }
         case Kind::Transpose: {

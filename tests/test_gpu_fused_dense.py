@@ -176,3 +176,30 @@ def test_fused_qkv_bf16_vs_oracle(be, with_bias):
         _, outs0 = run(be, build, ins, fuse=False)
         for o, o0 in zip(outs, outs0):
             assert np.array_equal(o[1], o0[1])
+
+
+def test_qkv_views_feed_fused_attention(be):
+    """QKV without biases: Q/K/V are column views of one product; splitting their last
+    axis into heads is a view too, so the fused attention kernel reads them in place."""
+    B, S, d, H, Hkv, D = 2, 256, 512, 4, 2, 128
+    q_dim, kv_dim = H * D, Hkv * D
+    x = _bf16_input((B, S, d), 1.0, 51)
+    w = _bf16_input((d, q_dim + 2 * kv_dim), d ** -0.5, 52)
+    ins = [(synth.to_bf16_bits(x), make_shape(BF16, B, S, d)),
+           (synth.to_bf16_bits(w), make_shape(BF16, d, q_dim + 2 * kv_dim))]
+
+    def build(f, xx, ww):
+        q, k, v = f.FusedAttentionQKVProjection(xx, ww, None, None, None, q_dim, kv_dim)
+        heads = lambda t, h: f.Reshape(t, B, S, h, D)
+        return [f.FusedScaledDotProductAttention(heads(q, H), heads(k, Hkv), heads(v, Hkv), None, H, Hkv,
+                                                 1, D ** -0.5, True)]   # 1 = BSHD
+
+    plan, (y,) = run(be, build, ins)
+    assert "strided_copy" not in plan and "fused attention" in plan, plan
+    qr, kr, vr = (synth.round_bf16(o.astype(np.float32)) for o in orc.qkv_projection(x, w, None, None, None, q_dim, kv_dim))
+    bhsd = lambda t, h: np.ascontiguousarray(t.reshape(B, S, h, D).transpose(0, 2, 1, 3))
+    ref = orc.sdpa(bhsd(qr, H), bhsd(kr, Hkv), bhsd(vr, Hkv), scale=D ** -0.5, causal=True).transpose(0, 2, 1, 3)
+    got = as_f(y)
+    assert got.shape == (B, S, H, D)
+    assert np.linalg.norm(got - ref) / np.linalg.norm(ref) <= 1e-2
+    assert rel_err(got, ref) <= 2.5e-2

@@ -492,3 +492,18 @@ def test_transformer_block_config_sampled(be):
     P1 = dict(P, ids=P["ids"][:1])
     exact = _tb_reference(one, P1, emulate_bf16=False)
     assert norm_err(y[:1], exact) <= 1e-2
+
+
+def test_reshape_of_strided_views(be):
+    """Reshapes of reversed, transposed and broadcast views (zero-copy where the
+    stride runs allow it, one copy otherwise) give numpy's results."""
+    x = np.arange(24, dtype=np.float32).reshape(6, 4) * 0.5 - 3
+    (a, b, c) = run(be, lambda f, p: [f.ReduceSum(f.Reshape(f.Reverse(p, 0), 2, 3, 4), 0),
+                                      f.Add(f.Reshape(f.Transpose(p, 1, 0), 24), f.Reshape(p, 24)),
+                                      f.Mul(f.Reshape(f.BroadcastInDim(f.Reshape(f.Slice(p, [0, 1], [6, 2]), 6), make_shape(F32, 2, 6, 3), [1]), 4, 9),
+                                            f.Reshape(f.BroadcastInDim(f.Slice(p, [0, 0], [6, 3]), make_shape(F32, 2, 6, 3), [1, 2]), 4, 9))],
+                    [(x, make_shape(F32, 6, 4))])
+    assert np.array_equal(a, x[::-1].reshape(2, 3, 4).sum(0))
+    assert np.array_equal(b, x.T.reshape(24) + x.reshape(24))
+    want = (np.broadcast_to(x[:, 1][None, :, None], (2, 6, 3)) * np.broadcast_to(x[None, :, :3], (2, 6, 3))).reshape(4, 9)
+    assert np.array_equal(c, want)

@@ -172,3 +172,46 @@ def test_plan_backend_cannot_execute(be):
     e = b.Compile()
     with pytest.raises(BackendError):
         be.BufferFromFlatData(0, np.zeros(4, np.float32), make_shape(F32, 4))
+
+
+def _plan(be, build, shapes):
+    b = be.Builder("p")
+    f = b.Main()
+    ps = [f.Parameter(f"p{i}", s) for i, s in enumerate(shapes)]
+    f.Return(build(f, *ps))
+    return b.Compile().Plan()
+
+
+def test_reshape_of_strided_views_is_zero_copy(be):
+    # Splitting the last axis of a column slice: a view (no copy) feeding SDPA.
+    def build(f, x, w):
+        q, k, v = f.FusedAttentionQKVProjection(x, w, None, None, None, 512, 256)
+        heads = lambda t, h: f.Reshape(t, 2, 64, h, 128)
+        return [f.FusedScaledDotProductAttention(heads(q, 4), heads(k, 2), heads(v, 2), None, 4, 2,
+                                                 AxesLayout.BSHD, 0.125, True)]
+    plan = _plan(be, build, [make_shape(BF16, 2, 64, 256), make_shape(BF16, 256, 1024)])
+    assert "strided_copy" not in plan and "materialise" not in plan, plan
+    assert plan.count("gemm_batched") == 1 and "N=1024" in plan and "fused attention" in plan, plan
+    # Merging axes that a transpose separated cannot be a view: one copy.
+    def merged(f, x):
+        t = f.Reshape(f.Transpose(x, 1, 0), 12)
+        return [f.Add(t, t)]
+    plan = _plan(be, merged, [make_shape(F32, 3, 4)])
+    assert plan.count("strided_copy") == 1, plan
+    # Reshape of a reversed / broadcast view that keeps the stride runs stays a view.
+    plan = _plan(be, lambda f, x: [f.ReduceSum(f.Reshape(f.Reverse(x, 0), 2, 3, 4), 0)], [make_shape(F32, 6, 4)])
+    assert "strided_copy" not in plan, plan
+
+
+def test_fused_dense_and_qkv_plans(be):
+    plan = _plan(be, lambda f, x, w, b: [f.FusedDense(x, w, b, 1)],
+                 [make_shape(BF16, 4, 128, 256), make_shape(BF16, 256, 512), make_shape(BF16, 512)])
+    assert plan.count("gemm_batched+epilogue") == 1 and "fused_elementwise" not in plan, plan
+    plan = _plan(be, lambda f, x, w, bq, bk, bv: list(f.FusedAttentionQKVProjection(x, w, bq, bk, bv, 256, 128)),
+                 [make_shape(BF16, 4, 128, 256), make_shape(BF16, 256, 512), make_shape(BF16, 256),
+                  make_shape(BF16, 128), make_shape(BF16, 128)])
+    assert plan.count("gemm_batched+epilogue") == 3 and "fused_elementwise" not in plan, plan
+    f = be.Builder("e").Main()
+    x = f.Parameter("x", make_shape(F32, 2, 3))
+    with pytest.raises(BackendError, match="FusedGelu: float input required"):
+        f.FusedGelu(f.Parameter("i", make_shape(dtypes.Int32, 3)), False)
