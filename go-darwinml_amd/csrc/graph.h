@@ -55,6 +55,7 @@ enum class Kind {
   Param, Const, Iota, Unary, Binary, Compare, Where, Clamp, Convert,
   Reshape, Transpose, Broadcast, Slice, Concat, Reverse,
   Reduce, ArgMinMax, Dot, Gather, Softmax, LayerNorm, SDPA,
+  DynSlice, DynUpdate, Scatter,
 };
 const char* kind_name(Kind k);
 
@@ -196,6 +197,41 @@ int launch_reduce(int dtype, int op, const void* src, const ReduceDesc& d, void*
 // Gather rows with int32 or int64 ids (clamped).
 int launch_gather_rows(const void* table, int64_t V, int64_t row_bytes, const void* ids,
                        int id_dtype, int64_t n, void* out, hipStream_t s, GHipError* err);
+// Window copy at run-time starts (DynamicSlice: window on the source side,
+// at_dst = 0; DynamicUpdateSlice: window on the destination side, at_dst = 1).
+// Starts are integer scalars in device memory, clamped to [0, dims - win].
+struct DynDesc {
+  int rank = 0;
+  int64_t dims[kMaxRank];   // operand dims (the side the window lives in)
+  int64_t win[kMaxRank];    // window dims
+  int64_t sst[kMaxRank];    // source strides
+  int64_t dst[kMaxRank];    // destination strides
+  const void* start[kMaxRank];
+  int sdt[kMaxRank];        // start dtypes
+};
+int launch_window_copy(int elem_bytes, const void* src, void* dst, const DynDesc& d, int at_dst, hipStream_t s,
+                       GHipError* err);
+// XLA scatter into `acc` (dtype scatter_acc_dtype(dtype), contiguous operand
+// dims): one thread per update element.
+struct ScatterDesc {
+  int ur = 0;                  // updates rank
+  int64_t udims[kMaxRank], ust[kMaxRank];
+  int uwin_od[kMaxRank];       // operand dim of each window dim of updates; -1: scatter dim
+  int64_t ibatch_st[kMaxRank]; // scatter dims: element stride in the indices tensor
+  int nidx = 0;                // index vector length
+  int64_t ivec_st = 0;         // element stride of the index vector axis
+  int sato[kMaxRank];          // operand dim of each index vector component
+  int r = 0;                   // operand rank
+  int64_t odims[kMaxRank], ost[kMaxRank], wsize[kMaxRank];
+  int idx_dt = 0, idx_es = 0;
+};
+int scatter_acc_dtype(int dtype);
+int launch_scatter(int dtype, int mode, const void* updates, const void* indices, void* acc, const ScatterDesc& d,
+                   hipStream_t s, GHipError* err);
+// dst (contiguous) = convert(src viewed through d.sst); widening / narrowing pairs
+// used around scatter accumulators.
+int launch_convert(int src_dt, int dst_dt, const void* src, void* dst, const CopyDesc& d, hipStream_t s,
+                   GHipError* err);
 // Whether the fused attention kernel (ghip_sdpa_fwd) takes these operands; strides
 // in elements ordered (batch, head, sequence), head dim contiguous.
 bool sdpa_fused_supported(int dtype, int64_t H, int64_t Hkv, int64_t Sq, int64_t Sk, int64_t D,

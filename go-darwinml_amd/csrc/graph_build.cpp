@@ -88,6 +88,8 @@ const char* kind_name(Kind k) {
     case Kind::Dot: return "DotGeneral"; case Kind::Gather: return "Gather";
     case Kind::Softmax: return "FusedSoftmax"; case Kind::LayerNorm: return "FusedLayerNorm";
     case Kind::SDPA: return "FusedScaledDotProductAttention";
+    case Kind::DynSlice: return "DynamicSlice"; case Kind::DynUpdate: return "DynamicUpdateSlice";
+    case Kind::Scatter: return "Scatter";
   }
   return "?";
 }
@@ -915,6 +917,143 @@ extern "C" GHipValue ghip_fn_fused_sdpa(GHipFunction* f, GHipValue q, GHipValue 
   n.f0 = scale;
   n.shape = qn->shape;
   n.shape.dims[3] = vn->shape.dims[3];
+  return f->add(std::move(n));
+}
+
+// ===========================================================================
+// DynamicSlice / DynamicUpdateSlice (function.go:1571-1621) and ScatterSum /
+// ScatterMax / ScatterMin (gather.go:441-640).
+// ===========================================================================
+namespace {
+// Start indices: one integer scalar value per operand axis.
+bool check_starts(Ctx& c, const GHipValue* starts, int n, int rank) {
+  if (n != rank) {
+    c.fail(GHIP_ERR_INVALID_ARG, "%d start indices for a rank-%d operand", n, rank);
+    return false;
+  }
+  for (int i = 0; i < n; ++i) {
+    const Node* s = c.node(starts[i]);
+    if (!s) return false;
+    if (!dtype_is_int(s->shape.dtype) || s->shape.rank() != 0) {
+      c.fail(GHIP_ERR_INVALID_ARG, "startIndex[%d] must be an integer scalar, got %s", i, s->shape.str().c_str());
+      return false;
+    }
+  }
+  return true;
+}
+}  // namespace
+
+extern "C" GHipValue ghip_fn_dynamic_slice(GHipFunction* f, GHipValue operand, const GHipValue* starts, int nstarts,
+                                           const int64_t* sizes, int nsizes, GHipError* err) {
+  FN_BEGIN("DynamicSlice");
+  const Node* a = c.node(operand);
+  if (!a) return -1;
+  const int r = a->shape.rank();
+  if (!check_starts(c, starts, nstarts, r)) return -1;
+  if (nsizes != r) return c.fail(GHIP_ERR_INVALID_ARG, "%d slice sizes for a rank-%d operand", nsizes, r);
+  Node n{Kind::DynSlice};
+  n.shape.dtype = a->shape.dtype;
+  for (int i = 0; i < r; ++i) {
+    if (sizes[i] < 0 || sizes[i] > a->shape.dims[i])
+      return c.fail(GHIP_ERR_INVALID_ARG, "slice size %lld out of [0, %lld] on axis %d", (long long)sizes[i],
+                    (long long)a->shape.dims[i], i);
+    n.shape.dims.push_back(sizes[i]);
+  }
+  n.in.push_back(operand);
+  n.in.insert(n.in.end(), starts, starts + nstarts);
+  return f->add(std::move(n));
+}
+
+extern "C" GHipValue ghip_fn_dynamic_update_slice(GHipFunction* f, GHipValue operand, GHipValue update,
+                                                  const GHipValue* starts, int nstarts, GHipError* err) {
+  FN_BEGIN("DynamicUpdateSlice");
+  const Node* a = c.node(operand);
+  if (!a) return -1;
+  const Node* u = c.node(update);
+  if (!u) return -1;
+  const int r = a->shape.rank();
+  if (u->shape.dtype != a->shape.dtype)
+    return c.fail(GHIP_ERR_INVALID_ARG, "update dtype %s differs from operand %s", dtype_name(u->shape.dtype),
+                  dtype_name(a->shape.dtype));
+  if (u->shape.rank() != r) return c.fail(GHIP_ERR_INVALID_ARG, "update rank %d vs operand rank %d", u->shape.rank(), r);
+  for (int i = 0; i < r; ++i)
+    if (u->shape.dims[i] > a->shape.dims[i])
+      return c.fail(GHIP_ERR_INVALID_ARG, "update dim %lld exceeds operand dim %lld on axis %d",
+                    (long long)u->shape.dims[i], (long long)a->shape.dims[i], i);
+  if (!check_starts(c, starts, nstarts, r)) return -1;
+  Node n{Kind::DynUpdate};
+  n.shape = a->shape;
+  n.in = {operand, update};
+  n.in.insert(n.in.end(), starts, starts + nstarts);
+  return f->add(std::move(n));
+}
+
+extern "C" GHipValue ghip_fn_scatter(GHipFunction* f, int mode, GHipValue operand, GHipValue indices,
+                                     GHipValue updates, int index_vector_axis, const int* update_window_axes,
+                                     int n_uwa, const int* inserted_window_axes, int n_iwa,
+                                     const int* scatter_axes_to_operand_axes, int n_sato, int indices_are_sorted,
+                                     int unique_indices, GHipError* err) {
+  static const char* names[] = {"ScatterSum", "ScatterMax", "ScatterMin"};
+  if (mode < GHIP_SCATTER_SUM || mode > GHIP_SCATTER_MIN) {
+    set_error(err, GHIP_ERR_INVALID_ARG, "Scatter: bad mode %d", mode);
+    return -1;
+  }
+  FN_BEGIN(names[mode]);
+  const Node* op = c.node(operand);
+  if (!op) return -1;
+  const Node* ix = c.node(indices);
+  if (!ix) return -1;
+  const Node* up = c.node(updates);
+  if (!up) return -1;
+  const int r = op->shape.rank(), ir = ix->shape.rank(), ur = up->shape.rank();
+  if (!dtype_is_int(ix->shape.dtype)) return c.fail(GHIP_ERR_INVALID_ARG, "indices must be integers");
+  if (up->shape.dtype != op->shape.dtype) return c.fail(GHIP_ERR_INVALID_ARG, "updates dtype differs from operand");
+  if (op->shape.dtype == GHIP_DTYPE_BOOL) return c.fail(GHIP_ERR_INVALID_ARG, "bool operand");
+  if (index_vector_axis < 0 || index_vector_axis > ir) return c.fail(GHIP_ERR_INVALID_ARG, "bad indexVectorAxis %d", index_vector_axis);
+  const int64_t ivec = index_vector_axis < ir ? ix->shape.dims[index_vector_axis] : 1;
+  if (ivec != n_sato)
+    return c.fail(GHIP_ERR_INVALID_ARG, "index vector size %lld vs %d scatterAxesToOperandAxes", (long long)ivec, n_sato);
+  std::vector<int64_t> uwa, iwa, sato;
+  if (!normalize_axes(update_window_axes, n_uwa, ur, &uwa)) return c.fail(GHIP_ERR_INVALID_ARG, "invalid updateWindowAxes");
+  if (!normalize_axes(inserted_window_axes, n_iwa, r, &iwa)) return c.fail(GHIP_ERR_INVALID_ARG, "invalid insertedWindowAxes");
+  if (!normalize_axes(scatter_axes_to_operand_axes, n_sato, r, &sato))
+    return c.fail(GHIP_ERR_INVALID_ARG, "invalid scatterAxesToOperandAxes");
+  if (!std::is_sorted(uwa.begin(), uwa.end()) || !std::is_sorted(iwa.begin(), iwa.end()))
+    return c.fail(GHIP_ERR_INVALID_ARG, "window axes must be sorted");
+  if (n_uwa + n_iwa != r)
+    return c.fail(GHIP_ERR_INVALID_ARG, "%d update window axes + %d inserted axes != operand rank %d", n_uwa, n_iwa, r);
+  const int nbatch = ir - (index_vector_axis < ir ? 1 : 0);
+  if (ur != n_uwa + nbatch)
+    return c.fail(GHIP_ERR_INVALID_ARG, "updates rank %d != %d window axes + %d scatter axes", ur, n_uwa, nbatch);
+  // Window axes of updates map, in order, onto the operand axes not inserted.
+  int wi = 0;
+  for (int d = 0; d < r; ++d) {
+    if (std::find(iwa.begin(), iwa.end(), d) != iwa.end()) continue;
+    const int64_t ws = up->shape.dims[uwa[wi++]];
+    if (ws > op->shape.dims[d])
+      return c.fail(GHIP_ERR_INVALID_ARG, "update window size %lld exceeds operand dim %lld (axis %d)", (long long)ws,
+                    (long long)op->shape.dims[d], d);
+  }
+  // Scatter axes of updates match the index batch axes, in order.
+  int bi = 0;
+  for (int d = 0; d < ur; ++d) {
+    if (std::find(uwa.begin(), uwa.end(), d) != uwa.end()) continue;
+    if (bi == index_vector_axis) ++bi;
+    if (up->shape.dims[d] != ix->shape.dims[bi])
+      return c.fail(GHIP_ERR_INVALID_ARG, "updates scatter dim %d (%lld) != indices batch dim %d (%lld)", d,
+                    (long long)up->shape.dims[d], bi, (long long)ix->shape.dims[bi]);
+    ++bi;
+  }
+  Node n{Kind::Scatter};
+  n.sub = mode;
+  n.in = {operand, indices, updates};
+  n.shape = op->shape;
+  n.i0 = index_vector_axis;
+  n.i1 = indices_are_sorted;
+  n.i2 = unique_indices;
+  n.a0 = uwa;
+  n.a1 = iwa;
+  n.a2 = sato;
   return f->add(std::move(n));
 }
 

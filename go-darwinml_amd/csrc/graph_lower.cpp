@@ -494,6 +494,9 @@ struct Lowerer {
         case Kind::Softmax: r = emit_softmax(v); break;
         case Kind::LayerNorm: r = emit_layernorm(v); break;
         case Kind::SDPA: r = emit_sdpa(v); break;
+        case Kind::DynSlice: r = emit_dyn_slice(v); break;
+        case Kind::DynUpdate: r = emit_dyn_update(v); break;
+        case Kind::Scatter: r = emit_scatter(v); break;
       }
     }
     if (failed) return bad();
@@ -763,6 +766,146 @@ struct Lowerer {
              [=](ExecState& st, GHipError* e) {
                return ghip_argminmax(dt, st.ptr(x, dt), outer, len, inner, is_min, odt, st.ptr(y, odt), st.stream, e);
              });
+    return y;
+  }
+
+  // ------------------------------------------------------------------ DynamicSlice / UpdateSlice / Scatter
+  // Views of the run-time start scalars in[first..] (read by the kernels).
+  bool start_views(const Node& n, int first, std::vector<View>* sv, std::vector<int>* sdt, std::vector<int>* rd) {
+    for (size_t k = first; k < n.in.size(); ++k) {
+      sv->push_back(get(n.in[k]));
+      sdt->push_back(N[n.in[k]].shape.dtype);
+      rd->push_back(sv->back().slot);
+    }
+    return !failed;
+  }
+
+  View emit_dyn_slice(int v) {
+    const Node n = N[v];
+    const Shape os = N[n.in[0]].shape;
+    if (os.rank() > kMaxRank) return fail(GHIP_ERR_UNSUPPORTED, "DynamicSlice: rank > 8");
+    View src = get(n.in[0]);
+    std::vector<View> sv;
+    std::vector<int> sdt, rd{src.slot};
+    if (failed || !start_views(n, 1, &sv, &sdt, &rd)) return bad();
+    View y = fresh(n.shape);
+    DynDesc d;
+    d.rank = os.rank();
+    for (int k = 0; k < d.rank; ++k) {
+      d.dims[k] = os.dims[k];
+      d.win[k] = n.shape.dims[k];
+      d.sst[k] = src.strides[k];
+      d.dst[k] = y.strides[k];
+    }
+    const int dt = os.dtype, eb = dtype_size(dt);
+    add_step(fmt("dynamic_slice %s -> %s", os.str().c_str(), n.shape.str().c_str()), rd, {y.slot},
+             [=](ExecState& st, GHipError* e) {
+               DynDesc dd = d;
+               for (int k = 0; k < dd.rank; ++k) {
+                 dd.start[k] = st.ptr(sv[k], sdt[k]);
+                 dd.sdt[k] = sdt[k];
+               }
+               return launch_window_copy(eb, st.ptr(src, dt), st.ptr(y, dt), dd, 0, st.stream, e);
+             });
+    return y;
+  }
+
+  View emit_dyn_update(int v) {
+    const Node n = N[v];
+    const Shape os = n.shape, us = N[n.in[1]].shape;
+    if (os.rank() > kMaxRank) return fail(GHIP_ERR_UNSUPPORTED, "DynamicUpdateSlice: rank > 8");
+    View op = get(n.in[0]);
+    View up = get(n.in[1]);
+    std::vector<View> sv;
+    std::vector<int> sdt, rd{up.slot};
+    if (failed || !start_views(n, 2, &sv, &sdt, &rd)) return bad();
+    View y = fresh(os);
+    emit_copy(os, op, y, "(DynamicUpdateSlice operand)");
+    DynDesc d;
+    d.rank = os.rank();
+    for (int k = 0; k < d.rank; ++k) {
+      d.dims[k] = os.dims[k];
+      d.win[k] = us.dims[k];
+      d.sst[k] = up.strides[k];
+      d.dst[k] = y.strides[k];
+    }
+    const int dt = os.dtype, eb = dtype_size(dt);
+    add_step(fmt("dynamic_update_slice %s <- %s", os.str().c_str(), us.str().c_str()), rd, {y.slot},
+             [=](ExecState& st, GHipError* e) {
+               DynDesc dd = d;
+               for (int k = 0; k < dd.rank; ++k) {
+                 dd.start[k] = st.ptr(sv[k], sdt[k]);
+                 dd.sdt[k] = sdt[k];
+               }
+               return launch_window_copy(eb, st.ptr(up, dt), st.ptr(y, dt), dd, 1, st.stream, e);
+             });
+    return y;
+  }
+
+  View emit_scatter(int v) {
+    const Node n = N[v];
+    const Shape os = n.shape, is = N[n.in[1]].shape, us = N[n.in[2]].shape;
+    if (os.rank() > kMaxRank || us.rank() > kMaxRank || is.rank() > kMaxRank)
+      return fail(GHIP_ERR_UNSUPPORTED, "Scatter: rank > 8");
+    View op = get(n.in[0]);
+    View ix = get(n.in[1]);
+    View up = get(n.in[2]);
+    if (failed) return bad();
+    const int dt = os.dtype, adt = scatter_acc_dtype(dt);
+    View y = fresh(os);
+    View acc = y;
+    CopyDesc cd = copy_desc(os, op, y);
+    if (adt != dt) {
+      Shape as = os;
+      as.dtype = adt;
+      acc = fresh(as);
+      add_step(fmt("convert %s -> %s (scatter accumulator)", os.str().c_str(), dtype_name(adt)), {op.slot}, {acc.slot},
+               [=](ExecState& st, GHipError* e) { return launch_convert(dt, adt, st.ptr(op, dt), st.ptr(acc, adt), cd, st.stream, e); });
+    } else {
+      emit_copy(os, op, y, "(Scatter operand)");
+    }
+    ScatterDesc d;
+    d.ur = us.rank();
+    d.r = os.rank();
+    const int iva = static_cast<int>(n.i0);
+    std::vector<int64_t> non_inserted;
+    for (int k = 0; k < d.r; ++k) {
+      d.odims[k] = os.dims[k];
+      d.ost[k] = acc.strides[k];
+      d.wsize[k] = 1;
+      if (std::find(n.a1.begin(), n.a1.end(), k) == n.a1.end()) non_inserted.push_back(k);
+    }
+    int wi = 0, bi = 0;
+    for (int k = 0; k < d.ur; ++k) {
+      d.udims[k] = us.dims[k];
+      d.ust[k] = up.strides[k];
+      d.ibatch_st[k] = 0;
+      if (std::find(n.a0.begin(), n.a0.end(), k) != n.a0.end()) {
+        const int od = static_cast<int>(non_inserted[wi++]);
+        d.uwin_od[k] = od;
+        d.wsize[od] = us.dims[k];
+      } else {
+        if (bi == iva) ++bi;
+        d.uwin_od[k] = -1;
+        d.ibatch_st[k] = ix.strides[bi++];
+      }
+    }
+    d.nidx = static_cast<int>(n.a2.size());
+    d.ivec_st = iva < is.rank() ? ix.strides[iva] : 0;
+    for (int k = 0; k < d.nidx; ++k) d.sato[k] = static_cast<int>(n.a2[k]);
+    d.idx_dt = is.dtype;
+    d.idx_es = dtype_size(is.dtype);
+    static const char* mn[] = {"sum", "max", "min"};
+    const int mode = n.sub, idt = is.dtype;
+    add_step(fmt("scatter_%s %s updates=%s indices=%s", mn[mode], os.str().c_str(), us.str().c_str(), is.str().c_str()),
+             {up.slot, ix.slot}, {acc.slot}, [=](ExecState& st, GHipError* e) {
+               return launch_scatter(dt, mode, st.ptr(up, dt), st.ptr(ix, idt), st.ptr(acc, adt), d, st.stream, e);
+             });
+    if (adt != dt) {
+      CopyDesc back = copy_desc(os, acc, y);
+      add_step(fmt("convert %s -> %s (scatter result)", dtype_name(adt), os.str().c_str()), {acc.slot}, {y.slot},
+               [=](ExecState& st, GHipError* e) { return launch_convert(adt, dt, st.ptr(acc, adt), st.ptr(y, dt), back, st.stream, e); });
+    }
     return y;
   }
 

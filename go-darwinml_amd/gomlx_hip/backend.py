@@ -122,6 +122,10 @@ _GRAPH_SIGS = {
     "ghip_fn_fused_softmax": ([_vp, _int, _int, _errp], _int),
     "ghip_fn_fused_layer_norm": ([_vp, _int, _intp, _int, _dbl, _int, _int, _errp], _int),
     "ghip_fn_fused_sdpa": ([_vp, _int, _int, _int, _int, _int, _int, _int, _dbl, _int, _errp], _int),
+    "ghip_fn_dynamic_slice": ([_vp, _int, _intp, _int, _i64p, _int, _errp], _int),
+    "ghip_fn_dynamic_update_slice": ([_vp, _int, _int, _intp, _int, _errp], _int),
+    "ghip_fn_scatter": ([_vp, _int, _int, _int, _int, _int, _intp, _int, _intp, _int, _intp, _int, _int, _int,
+                         _errp], _int),
     "ghip_fn_fused_gelu": ([_vp, _int, _int, _errp], _int),
     "ghip_fn_fused_dense": ([_vp, _int, _int, _int, _int, _errp], _int),
     "ghip_fn_fused_qkv_projection": ([_vp, _int, _int, _int, _int, _int, _int, _int, _intp, _intp,
@@ -455,6 +459,33 @@ class Function:
         s, ns = _i64arr(slice_sizes)
         return self._call("ghip_fn_gather", operand.id, start_indices.id, index_vector_axis, o, no,
                           c, nc, m, nm, s, ns, int(indices_are_sorted))
+
+    def DynamicSlice(self, operand, start_indices, slice_sizes) -> Value:
+        s, ns = _intarr([v.id for v in start_indices])
+        z, nz = _i64arr(slice_sizes)
+        return self._call("ghip_fn_dynamic_slice", operand.id, s, ns, z, nz)
+
+    def DynamicUpdateSlice(self, operand, update, start_indices) -> Value:
+        s, ns = _intarr([v.id for v in start_indices])
+        return self._call("ghip_fn_dynamic_update_slice", operand.id, update.id, s, ns)
+
+    def _scatter(self, mode, operand, scatter_indices, updates, index_vector_axis, update_window_axes,
+                 inserted_window_axes, scatter_axes_to_operand_axes, indices_are_sorted=False,
+                 unique_indices=False) -> Value:
+        u, nu = _intarr(update_window_axes)
+        i, ni = _intarr(inserted_window_axes)
+        a, na = _intarr(scatter_axes_to_operand_axes)
+        return self._call("ghip_fn_scatter", mode, operand.id, scatter_indices.id, updates.id, index_vector_axis,
+                          u, nu, i, ni, a, na, int(indices_are_sorted), int(unique_indices))
+
+    def ScatterSum(self, *args, **kw) -> Value:
+        return self._scatter(0, *args, **kw)
+
+    def ScatterMax(self, *args, **kw) -> Value:
+        return self._scatter(1, *args, **kw)
+
+    def ScatterMin(self, *args, **kw) -> Value:
+        return self._scatter(2, *args, **kw)
 
     # fused ops
     def FusedSoftmax(self, x, axis: int) -> Value:

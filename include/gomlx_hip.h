@@ -281,6 +281,25 @@ GHipValue ghip_fn_fused_layer_norm(GHipFunction* f, GHipValue x, const int* axes
 GHipValue ghip_fn_fused_sdpa(GHipFunction* f, GHipValue q, GHipValue k, GHipValue v,
                              GHipValue mask, int num_heads, int num_kv_heads, int layout,
                              double scale, int causal, GHipError* err); /* :2669-2907 */
+/* DynamicSlice (function.go:1571-1594): a `sizes` window of operand at the
+ * run-time start indices `starts` (one integer scalar value per axis), each
+ * clamped to [0, dim - size] (XLA semantics). */
+GHipValue ghip_fn_dynamic_slice(GHipFunction* f, GHipValue operand, const GHipValue* starts,
+                                int nstarts, const int64_t* sizes, int nsizes, GHipError* err);
+/* DynamicUpdateSlice (function.go:1596-1621): operand with `update` written at the
+ * run-time start indices, clamped to [0, dim - update dim]. */
+GHipValue ghip_fn_dynamic_update_slice(GHipFunction* f, GHipValue operand, GHipValue update,
+                                       const GHipValue* starts, int nstarts, GHipError* err);
+/* ScatterSum / ScatterMax / ScatterMin (gather.go:441-640): XLA scatter of
+ * `updates` into `operand` combining with +, max or min.  A window whose start
+ * (from `indices`) does not fit inside the operand is skipped. */
+enum { GHIP_SCATTER_SUM = 0, GHIP_SCATTER_MAX = 1, GHIP_SCATTER_MIN = 2 };
+GHipValue ghip_fn_scatter(GHipFunction* f, int mode, GHipValue operand, GHipValue indices,
+                          GHipValue updates, int index_vector_axis, const int* update_window_axes,
+                          int n_update_window_axes, const int* inserted_window_axes,
+                          int n_inserted_window_axes, const int* scatter_axes_to_operand_axes,
+                          int n_scatter_axes, int indices_are_sorted, int unique_indices,
+                          GHipError* err);
 /* Composite fused ops, built from the primitives above in the order the
  * reference composes them, so the lowering fuses them like any other chain
  * (bias / activation / slicing run in the GEMM epilogue).

@@ -345,6 +345,133 @@ void orc_iota(double* out, int64_t outer, int64_t n, int64_t inner) {
 }
 
 /* ---------------------------------------------------------------------------
+ * DynamicSlice / DynamicUpdateSlice.
+ * Reference: Function.DynamicSlice / DynamicUpdateSlice (mpsgraph/gomlx/
+ * function.go:1571-1621) -> bridge.m:918-1104: a window of the operand at
+ * run-time start indices.  Starts are clamped to [0, dim - window] (XLA's
+ * definition of both ops, which GoMLX's backend API follows; the reference's
+ * tests only use in-range starts, mpsgraph_test.go:993-1131).
+ * ------------------------------------------------------------------------- */
+static int64_t clamp64(int64_t v, int64_t lo, int64_t hi) { return v < lo ? lo : (v > hi ? hi : v); }
+
+void orc_dynamic_slice(const void* x, int elem_bytes, int rank, const int64_t* dims, const int64_t* starts,
+                       const int64_t* sizes, void* out) {
+  int64_t st[ORC_MAX_RANK], xs[ORC_MAX_RANK], n = 1, acc = 1;
+  for (int k = rank - 1; k >= 0; --k) {
+    xs[k] = acc;
+    acc *= dims[k];
+  }
+  for (int k = 0; k < rank; ++k) {
+    st[k] = clamp64(starts[k], 0, dims[k] - sizes[k]);
+    n *= sizes[k];
+  }
+  for (int64_t i = 0; i < n; ++i) {
+    int64_t q = i, off = 0;
+    for (int k = rank - 1; k >= 0; --k) {
+      off += (st[k] + q % sizes[k]) * xs[k];
+      q /= sizes[k];
+    }
+    memcpy((char*)out + i * elem_bytes, (const char*)x + off * elem_bytes, (size_t)elem_bytes);
+  }
+}
+
+void orc_dynamic_update_slice(const void* x, int elem_bytes, int rank, const int64_t* dims, const void* upd,
+                              const int64_t* udims, const int64_t* starts, void* out) {
+  int64_t st[ORC_MAX_RANK], xs[ORC_MAX_RANK], n = 1, total = 1;
+  for (int k = rank - 1; k >= 0; --k) {
+    xs[k] = total;
+    total *= dims[k];
+  }
+  memcpy(out, x, (size_t)(total * elem_bytes));
+  for (int k = 0; k < rank; ++k) {
+    st[k] = clamp64(starts[k], 0, dims[k] - udims[k]);
+    n *= udims[k];
+  }
+  for (int64_t i = 0; i < n; ++i) {
+    int64_t q = i, off = 0;
+    for (int k = rank - 1; k >= 0; --k) {
+      off += (st[k] + q % udims[k]) * xs[k];
+      q /= udims[k];
+    }
+    memcpy((char*)out + off * elem_bytes, (const char*)upd + i * elem_bytes, (size_t)elem_bytes);
+  }
+}
+
+/* ---------------------------------------------------------------------------
+ * Scatter.
+ * Reference: Function.ScatterSum / ScatterMax / ScatterMin (mpsgraph/gomlx/
+ * gather.go:441-640) -> MPSGraph scatterAlongAxis / scatterND with mode add /
+ * max / min (bridge.m:789-815, 1624-1660): XLA scatter.  For update element u:
+ * its scatter coordinates select an index vector in `indices`; component k
+ * gives the start along operand axis sato[k]; its window coordinates (the
+ * update axes listed in uwa) run, in order, over the operand axes not listed
+ * in iwa.  Windows that do not fit are skipped (XLA); out-of-range behaviour is
+ * not fixed by the reference's tests.
+ * ------------------------------------------------------------------------- */
+void orc_scatter(int mode, const double* operand, int r, const int64_t* odims, const int64_t* indices, int ir,
+                 const int64_t* idims, int iva, const double* updates, int ur, const int64_t* udims,
+                 const int* uwa, int n_uwa, const int* iwa, int n_iwa, const int* sato, int n_sato, double* out) {
+  int64_t ostr[ORC_MAX_RANK], istr[ORC_MAX_RANK + 1], total = 1, nu = 1;
+  for (int k = r - 1; k >= 0; --k) {
+    ostr[k] = total;
+    total *= odims[k];
+  }
+  memcpy(out, operand, (size_t)total * sizeof(double));
+  int64_t acc = 1;
+  for (int k = ir - 1; k >= 0; --k) {
+    istr[k] = acc;
+    acc *= idims[k];
+  }
+  for (int k = 0; k < ur; ++k) nu *= udims[k];
+  int win_od[ORC_MAX_RANK];  /* operand axis of each update window axis */
+  int64_t wsize[ORC_MAX_RANK];
+  for (int k = 0; k < r; ++k) wsize[k] = 1;
+  {
+    int j = 0;
+    for (int k = 0; k < r; ++k) {
+      if (in_list(k, iwa, n_iwa)) continue;
+      win_od[j] = k;
+      wsize[k] = udims[uwa[j]];
+      ++j;
+    }
+  }
+  for (int64_t u = 0; u < nu; ++u) {
+    int64_t c[ORC_MAX_RANK], q = u;
+    for (int k = ur - 1; k >= 0; --k) {
+      c[k] = q % udims[k];
+      q /= udims[k];
+    }
+    /* indices position: batch coordinates in order, skipping iva */
+    int64_t ipos = 0;
+    int bi = 0, wj = 0;
+    int64_t w[ORC_MAX_RANK];
+    for (int k = 0; k < r; ++k) w[k] = 0;
+    for (int k = 0; k < ur; ++k) {
+      if (in_list(k, uwa, n_uwa)) {
+        w[win_od[wj++]] = c[k];
+      } else {
+        if (bi == iva) ++bi;
+        ipos += c[k] * istr[bi];
+        ++bi;
+      }
+    }
+    int64_t start[ORC_MAX_RANK];
+    for (int k = 0; k < r; ++k) start[k] = 0;
+    for (int k = 0; k < n_sato; ++k) start[sato[k]] = indices[ipos + (iva < ir ? k * istr[iva] : 0)];
+    int ok = 1;
+    for (int k = 0; k < r; ++k)
+      if (start[k] < 0 || start[k] > odims[k] - wsize[k]) ok = 0;
+    if (!ok) continue;
+    int64_t off = 0;
+    for (int k = 0; k < r; ++k) off += (start[k] + w[k]) * ostr[k];
+    const double v = updates[u], o = out[off];
+    if (mode == 0) out[off] = o + v;
+    else if (isnan(o) || isnan(v)) out[off] = NAN;
+    else out[off] = mode == 1 ? (v > o ? v : o) : (v < o ? v : o);
+  }
+}
+
+/* ---------------------------------------------------------------------------
  * Activations of FusedDense / FusedGelu.
  * Reference: Function.FusedGelu (mpsgraph/gomlx/function.go:2288-2408):
  *   exact:  x * 0.5 * (1 + erf(x / sqrt 2));

@@ -30,6 +30,13 @@
  *   orc_argminmax    reference known answer (mpsgraph_test.go:973-990),
  *                    numpy.argmax/argmin on tie-free data.
  *   orc_iota         reference known answer (mpsgraph_test.go:795-821).
+ *   orc_dynamic_slice / orc_dynamic_update_slice
+ *                    reference known answers (mpsgraph_test.go:993-1062,
+ *                    1064-1131); numpy slicing with the clamped starts.
+ *   orc_scatter      reference known answer (mpsgraph_test.go:1192-1262);
+ *                    numpy.add.at / maximum.at / minimum.at on the embedding
+ *                    pattern; sum invariant and update-order invariance on a
+ *                    general multi-axis case.
  *   orc_activation   reference known answers for GELU (mpsgraph_test.go:2645-2656)
  *                    and ReLU through FusedDense (:2841-2852); odd-part identity
  *                    g(x) - g(-x) = x for both GELU forms; exact GELU against
@@ -103,6 +110,23 @@ void orc_iota(double* out, int64_t outer, int64_t n, int64_t inner);
 enum { ORC_ACT_NONE = 0, ORC_ACT_GELU = 1, ORC_ACT_RELU = 2, ORC_ACT_SILU = 3, ORC_ACT_TANH = 4,
        ORC_ACT_GELU_EXACT = 5 };
 void orc_activation(const double* x, double* y, int64_t n, int act);
+
+/* DynamicSlice: out (dims `sizes`, contiguous) = the window of x (dims, contiguous,
+ * elem_bytes per element) at `starts`, each clamped to [0, dims[k] - sizes[k]]. */
+void orc_dynamic_slice(const void* x, int elem_bytes, int rank, const int64_t* dims, const int64_t* starts,
+                       const int64_t* sizes, void* out);
+/* DynamicUpdateSlice: out = x with `upd` (dims udims) written at `starts`, each
+ * clamped to [0, dims[k] - udims[k]]. */
+void orc_dynamic_update_slice(const void* x, int elem_bytes, int rank, const int64_t* dims, const void* upd,
+                              const int64_t* udims, const int64_t* starts, void* out);
+/* XLA scatter in fp64: out = operand (dims odims, rank r) combined (mode 0 sum,
+ * 1 max, 2 min; NaN propagates through max / min) with every element of updates
+ * (dims udims, rank ur) whose window start fits in the operand.  indices are
+ * int64 (dims idims, rank ir), the index vector along axis iva (iva == ir: an
+ * implicit trailing axis of size 1).  Updates are visited in row-major order. */
+void orc_scatter(int mode, const double* operand, int r, const int64_t* odims, const int64_t* indices, int ir,
+                 const int64_t* idims, int iva, const double* updates, int ur, const int64_t* udims,
+                 const int* uwa, int n_uwa, const int* iwa, int n_iwa, const int* sato, int n_sato, double* out);
 
 /* fp32 -> bf16 (round to nearest even; NaN stays NaN), as 16-bit patterns. */
 void orc_f32_to_bf16(const float* x, uint16_t* y, int64_t n);

@@ -57,6 +57,10 @@ def lib():
         L.orc_iota.argtypes = [_f64p, _i64, _i64, _i64]
         L.orc_f32_to_bf16.argtypes = [_f32p, _u16p, _i64]
         L.orc_activation.argtypes = [_f64p, _f64p, _i64, _int]
+        L.orc_dynamic_slice.argtypes = [_vp, _int, _int, _i64p, _i64p, _i64p, _vp]
+        L.orc_dynamic_update_slice.argtypes = [_vp, _int, _int, _i64p, _vp, _i64p, _i64p, _vp]
+        L.orc_scatter.argtypes = [_int, _f64p, _int, _i64p, _i64p, _int, _i64p, _int, _f64p, _int, _i64p,
+                                  _vp, _int, _vp, _int, _vp, _int, _f64p]
         _lib = L
     return _lib
 
@@ -195,6 +199,53 @@ def iota(shape, axis) -> np.ndarray:
     outer, n, inner = _split(tuple(shape), axis)
     out = np.empty(tuple(shape), np.float64)
     lib().orc_iota(out, outer, n, inner)
+    return out
+
+
+def dynamic_slice(x, starts, sizes) -> np.ndarray:
+    """DynamicSlice (function.go:1571-1594), starts clamped to [0, dim - size]; any dtype, bit-exact."""
+    x = np.ascontiguousarray(x)
+    out = np.empty(tuple(int(s) for s in sizes), x.dtype)
+    lib().orc_dynamic_slice(x.ctypes.data, x.itemsize, x.ndim, np.asarray(x.shape, np.int64),
+                            np.asarray(starts, np.int64).reshape(-1), np.asarray(sizes, np.int64).reshape(-1),
+                            out.ctypes.data)
+    return out
+
+
+def dynamic_update_slice(x, upd, starts) -> np.ndarray:
+    """DynamicUpdateSlice (function.go:1596-1621), starts clamped to [0, dim - update dim]."""
+    x = np.ascontiguousarray(x)
+    upd = np.ascontiguousarray(upd, x.dtype)
+    out = np.empty_like(x)
+    lib().orc_dynamic_update_slice(x.ctypes.data, x.itemsize, x.ndim, np.asarray(x.shape, np.int64), upd.ctypes.data,
+                                   np.asarray(upd.shape, np.int64), np.asarray(starts, np.int64).reshape(-1),
+                                   out.ctypes.data)
+    return out
+
+
+SCATTER_SUM, SCATTER_MAX, SCATTER_MIN = 0, 1, 2
+
+
+def scatter(mode, operand, indices, updates, index_vector_axis, update_window_axes, inserted_window_axes,
+            scatter_axes_to_operand_axes) -> np.ndarray:
+    """ScatterSum / Max / Min (gather.go:441-640) in fp64, XLA semantics; out-of-range windows skipped."""
+    op = np.ascontiguousarray(np.asarray(operand, np.float64))
+    ix = np.ascontiguousarray(np.asarray(indices, np.int64))
+    up = np.ascontiguousarray(np.asarray(updates, np.float64))
+    out = np.empty_like(op)
+    keep = []
+
+    def arr(a):
+        a = np.ascontiguousarray(np.asarray(list(a), np.int32))
+        keep.append(a)
+        return a.ctypes.data_as(ctypes.c_void_p) if a.size else None, len(a)
+
+    u, nu = arr(update_window_axes)
+    i, ni = arr(inserted_window_axes)
+    s, ns = arr(scatter_axes_to_operand_axes)
+    lib().orc_scatter(int(mode), op.reshape(-1), op.ndim, np.asarray(op.shape, np.int64), ix.reshape(-1), ix.ndim,
+                      np.asarray(ix.shape if ix.ndim else (1,), np.int64), int(index_vector_axis), up.reshape(-1),
+                      up.ndim, np.asarray(up.shape if up.ndim else (1,), np.int64), u, nu, i, ni, s, ns, out.reshape(-1))
     return out
 
 

@@ -95,6 +95,24 @@ CASES = {
         "source": "mpsgraph_test.go:1485-1532 (TestConvertDType)",
         "x": [1.7, 2.3, -0.9], "expected": [1, 2, 0],
     },
+    "dynamic_slice": {
+        "source": "mpsgraph_test.go:993-1062 (TestDynamicSlice)",
+        "shape": [3, 4], "x": list(range(1, 13)), "starts": [1, 1], "sizes": [2, 2],
+        "expected": [6, 7, 10, 11],
+    },
+    "dynamic_update_slice": {
+        "source": "mpsgraph_test.go:1064-1131 (TestDynamicUpdateSlice)",
+        "shape": [3, 4], "x": list(range(1, 13)), "update_shape": [2, 2], "update": [100, 200, 300, 400],
+        "starts": [1, 1], "expected": [1, 2, 3, 4, 5, 100, 200, 8, 9, 300, 400, 12],
+    },
+    "scatter_sum": {
+        "source": "mpsgraph_test.go:1192-1262 (TestScatterSum)",
+        "operand_shape": [4, 2], "operand": [0] * 8, "indices_shape": [3, 1], "indices": [0, 2, 0],
+        "updates_shape": [3, 2], "updates": [1, 2, 3, 4, 5, 6],
+        "index_vector_axis": 1, "update_window_axes": [1], "inserted_window_axes": [0],
+        "scatter_axes_to_operand_axes": [0],
+        "expected": [6, 8, 0, 0, 3, 4, 0, 0],
+    },
     "gelu": {
         "source": "mpsgraph_test.go:2645-2656 (TestFusedGelu)",
         "x": [0.0, 1.0, -1.0, 3.0], "tol": 1e-3,

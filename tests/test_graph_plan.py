@@ -215,3 +215,30 @@ def test_fused_dense_and_qkv_plans(be):
     x = f.Parameter("x", make_shape(F32, 2, 3))
     with pytest.raises(BackendError, match="FusedGelu: float input required"):
         f.FusedGelu(f.Parameter("i", make_shape(dtypes.Int32, 3)), False)
+
+
+def test_dynamic_slice_and_scatter_shapes_and_errors(be):
+    f = be.Builder("ds").Main()
+    x = f.Parameter("x", make_shape(F32, 5, 6))
+    i0 = f.Parameter("i0", make_shape(dtypes.Int32))
+    i1 = f.Parameter("i1", make_shape(dtypes.Int64))
+    assert f.OpShape(f.DynamicSlice(x, [i0, i1], [2, 3])).dims == (2, 3)
+    u = f.Parameter("u", make_shape(F32, 2, 6))
+    assert f.OpShape(f.DynamicUpdateSlice(x, u, [i0, i1])).dims == (5, 6)
+    with pytest.raises(BackendError, match="3 start indices for a rank-2"):
+        f.DynamicSlice(x, [i0, i1, i0], [1, 1])
+    with pytest.raises(BackendError, match="slice size 7 out of"):
+        f.DynamicSlice(x, [i0, i1], [2, 7])
+    with pytest.raises(BackendError, match="integer scalar"):
+        f.DynamicSlice(x, [i0, f.Parameter("v", make_shape(dtypes.Int32, 2))], [2, 2])
+    with pytest.raises(BackendError, match="exceeds operand dim"):
+        f.DynamicUpdateSlice(x, f.Parameter("u2", make_shape(F32, 6, 1)), [i0, i1])
+    ids = f.Parameter("ids", make_shape(dtypes.Int32, 7, 1))
+    upd = f.Parameter("upd", make_shape(F32, 7, 6))
+    assert f.OpShape(f.ScatterSum(x, ids, upd, 1, [1], [0], [0])).dims == (5, 6)
+    with pytest.raises(BackendError, match="ScatterMax: updates scatter dim"):
+        f.ScatterMax(x, ids, f.Parameter("upd2", make_shape(F32, 6, 6)), 1, [1], [0], [0])
+    with pytest.raises(BackendError, match="index vector size"):
+        f.ScatterMin(x, ids, upd, 1, [1], [0], [0, 1])
+    with pytest.raises(BackendError, match="window size 9 exceeds"):
+        f.ScatterSum(x, ids, f.Parameter("upd3", make_shape(F32, 7, 9)), 1, [1], [0], [0])

@@ -278,3 +278,81 @@ def test_qkv_projection_known_answers(known, name):
                               c["query_dim"], c["key_value_dim"])
     for o, key in zip(outs, "qkv"):
         assert np.max(np.abs(o.reshape(-1) - np.array(c[key]))) <= c["tol"]
+
+
+# ---------------------------------------------------------------- DynamicSlice / UpdateSlice / Scatter
+def test_dynamic_slice_known_answers(known):
+    c = known["dynamic_slice"]
+    x = np.array(c["x"], np.float32).reshape(c["shape"])
+    assert orc.dynamic_slice(x, c["starts"], c["sizes"]).reshape(-1).tolist() == c["expected"]
+    c = known["dynamic_update_slice"]
+    x = np.array(c["x"], np.float32).reshape(c["shape"])
+    u = np.array(c["update"], np.float32).reshape(c["update_shape"])
+    assert orc.dynamic_update_slice(x, u, c["starts"]).reshape(-1).tolist() == c["expected"]
+
+
+def test_dynamic_slices_against_numpy():
+    rng = np.random.default_rng(3)
+    x = rng.integers(0, 1 << 16, (5, 7, 6)).astype(np.uint16)
+    for starts in ([0, 0, 0], [2, 3, 1], [9, -4, 5], [-1, 100, -100]):
+        sizes = (3, 4, 2)
+        cl = [min(max(s, 0), d - z) for s, d, z in zip(starts, x.shape, sizes)]
+        want = x[cl[0]:cl[0] + 3, cl[1]:cl[1] + 4, cl[2]:cl[2] + 2]
+        assert np.array_equal(orc.dynamic_slice(x, starts, sizes), want)
+        u = rng.integers(0, 1 << 16, sizes).astype(np.uint16)
+        want = x.copy()
+        want[cl[0]:cl[0] + 3, cl[1]:cl[1] + 4, cl[2]:cl[2] + 2] = u
+        assert np.array_equal(orc.dynamic_update_slice(x, u, starts), want)
+
+
+def test_scatter_known_answer(known):
+    c = known["scatter_sum"]
+    out = orc.scatter(orc.SCATTER_SUM, np.array(c["operand"], np.float64).reshape(c["operand_shape"]),
+                      np.array(c["indices"]).reshape(c["indices_shape"]),
+                      np.array(c["updates"], np.float64).reshape(c["updates_shape"]), c["index_vector_axis"],
+                      c["update_window_axes"], c["inserted_window_axes"], c["scatter_axes_to_operand_axes"])
+    assert out.reshape(-1).tolist() == c["expected"]
+
+
+@pytest.mark.parametrize("mode", [0, 1, 2])
+def test_scatter_embedding_pattern_against_numpy(mode):
+    rng = np.random.default_rng(7 + mode)
+    V, D, n = 50, 6, 200
+    op = rng.standard_normal((V, D))
+    ids = rng.integers(-3, V + 3, n)          # some out of range: skipped
+    upd = rng.standard_normal((n, D))
+    got = orc.scatter(mode, op, ids.reshape(n, 1), upd, 1, [1], [0], [0])
+    want = op.copy()
+    ok = (ids >= 0) & (ids < V)
+    fn = [np.add, np.maximum, np.minimum][mode]
+    fn.at(want, ids[ok], upd[ok])
+    assert np.allclose(got, want, rtol=0, atol=1e-12) if mode == 0 else np.array_equal(got, want)
+    # implicit trailing index vector axis (iva == indices rank) gives the same result
+    got2 = orc.scatter(mode, op, ids, upd, 1, [1], [0], [0])
+    assert np.array_equal(got, got2)
+
+
+def test_scatter_general_invariants():
+    rng = np.random.default_rng(11)
+    op = rng.integers(-5, 5, (6, 4, 5)).astype(np.float64)
+    # index vectors of length 2 on axis 0 of indices [2, 3, 4] -> starts on operand axes (2, 0)
+    idx = np.stack([rng.integers(0, 4, (3, 4)), rng.integers(0, 5, (3, 4))])
+    # updates: scatter dims [3, 4] then window dims over operand axes 1 (size 2) and 2 (size 2);
+    # operand axis 0 inserted
+    upd = rng.integers(-9, 9, (3, 2, 4, 2)).astype(np.float64)
+    args = (0, [1, 3], [0], [2, 0])
+    got = orc.scatter(orc.SCATTER_SUM, op, idx, upd, *args)
+    # in-bounds windows: start on axis 2 <= 5-2, on axis 0 <= 6-1
+    starts2, starts0 = idx[0], idx[1]
+    ok = (starts2 <= 3) & (starts0 <= 5)
+    assert got.sum() == op.sum() + upd.transpose(0, 2, 1, 3)[ok].sum()
+    # brute force over the windows, in a different enumeration order
+    want = op.copy()
+    for i in range(3):
+        for j in range(4):
+            if not ok[i, j]:
+                continue
+            for a in range(2):
+                for b in range(2):
+                    want[idx[1, i, j], a, idx[0, i, j] + b] += upd[i, a, j, b]
+    assert np.array_equal(got, want)
