@@ -5,8 +5,9 @@ RMSNorm over the last axis of x [8192, 4096] fp32 (gamma [4096], eps 1e-6) —
 one "step" is one RMSNorm launch over that batch, inputs resident in HBM.
 `value` is GB/s of algorithmic traffic (read x + gamma, write y).  The same line
 carries the other BASELINE workloads under "secondary" (softmax, bf16 RMSNorm,
-LayerNorm, bf16/fp32 DotGeneral, the attention composite), each with its own
-roofline fraction.
+LayerNorm, bf16/fp32 DotGeneral, the attention composite, the transformer block)
+and two widened ops (FusedDense + GELU, the embedding-gradient ScatterSum), each
+with its own roofline fraction.
 
 Timing: W untimed warmup steps plus at least 0.25 s of sustained untimed launches
 (the GPU clock settles only under sustained load; a cold first burst of bf16
@@ -289,6 +290,64 @@ def make_cases(only=None):
         case.keep = (be, ex, bufs)  # keep the backend alive while timing
         return case
 
+    def graph_case(name, build, inputs, **kw):
+        """A workload given as a backend graph: build(f, *params) -> outputs, run
+        through Builder -> Compile -> Execute on the backend's stream."""
+        from gomlx_hip.backend import Backend
+        be = Backend("")
+        b = be.Builder(name)
+        f = b.Main()
+        params = [f.Parameter(f"p{i}", s) for i, (_, s) in enumerate(inputs)]
+        f.Return(build(f, *params))
+        ex = b.Compile()
+        bufs = [be.BufferFromFlatData(0, a, s) for a, s in inputs]
+        stream = torch.cuda.ExternalStream(be.stream())
+
+        def launch(i):
+            for y in ex.Execute(bufs, None, 0):
+                be.BufferFinalize(y)
+        case = Case(name, launch, stream=stream, **kw)
+        case.config["plan"] = [ln for ln in ex.Plan().splitlines()[1:] if ln]
+        case.keep = (be, ex, bufs)
+        return case
+
+    def dense_case():
+        """FusedDense with bias and GELU on the FFN shape of configs[4]: one GEMM whose
+        epilogue adds the bias and evaluates the tanh-GELU chain."""
+        import numpy as np
+        from gomlx_hip import synth
+        from gomlx_hip.backend import ActivationType, dtypes, make_shape
+        T, d, ff = 8192, 2048, 8192
+        bf = lambda seed, shape, std: synth.to_bf16_bits(synth.normal(seed, shape, std=std))  # noqa: E731
+        inputs = [(bf(6001, (8, 1024, d), 1.0), make_shape(dtypes.BFloat16, 8, 1024, d)),
+                  (bf(6002, (d, ff), d ** -0.5), make_shape(dtypes.BFloat16, d, ff)),
+                  (bf(6003, (ff,), 0.1), make_shape(dtypes.BFloat16, ff))]
+        return graph_case("fused_dense_gelu_bf16",
+                          lambda f, x, w, b: [f.FusedDense(x, w, b, ActivationType.GELU)], inputs,
+                          flops_per_step=2 * T * d * ff, bound="mfma", peak=BF16_PEAK_TFLOPS, dtype="bf16",
+                          kernel="gemm_epilogue",
+                          config={"workload": "FusedDense x [8,1024,2048] . W [2048,8192] + bias, tanh-GELU, "
+                                              "bf16 (fp32 accumulate); flops of the product only"})
+
+    def scatter_case():
+        """ScatterSum in the embedding-gradient form: 8192 token rows of width 2048
+        added into a [32000, 2048] bf16 table (ids of configs[4])."""
+        from gomlx_hip import synth
+        from gomlx_hip.backend import dtypes, make_shape
+        V, D, n = 32000, 2048, 8192
+        ids = synth.uniform_int(5001, (n,), 0, V)
+        inputs = [(synth.to_bf16_bits(synth.normal(6101, (V, D), std=0.02)), make_shape(dtypes.BFloat16, V, D)),
+                  (ids, make_shape(dtypes.Int32, n)),
+                  (synth.to_bf16_bits(synth.normal(6102, (n, D), std=1.0)), make_shape(dtypes.BFloat16, n, D))]
+        nbytes = 2 * V * D * 2 + n * D * 2 + n * 4
+        return graph_case("scatter_sum_bf16",
+                          lambda f, t, i, u: [f.ScatterSum(t, i, u, 1, [1], [0], [0])], inputs,
+                          bytes_per_step=nbytes, bound="hbm", peak=HBM_PEAK_GBS, dtype="bf16",
+                          kernel="scatter plan (all kernels)",
+                          config={"workload": "ScatterSum table [32000,2048] bf16 += updates [8192,2048] bf16 at "
+                                              "ids [8192] int32 ~ U[0,32000); bytes: read + write table, read "
+                                              "updates and ids"})
+
     builders = {
         "softmax_f32": softmax_case,
         "rmsnorm_bf16": lambda: rms_case(torch.bfloat16, "bf16"),
@@ -298,6 +357,8 @@ def make_cases(only=None):
         "dot_general_f32": lambda: dot_case(torch.float32, "f32", FP32_PEAK_TFLOPS),
         "attention_bf16": attention_case,
         "transformer_block_bf16": transformer_case,
+        "fused_dense_gelu_bf16": dense_case,
+        "scatter_sum_bf16": scatter_case,
     }
     primary = rms_case(torch.float32, "f32")
     names = [n for n in builders if not only or n in only]

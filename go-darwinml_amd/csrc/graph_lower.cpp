@@ -52,6 +52,18 @@ __device__ __forceinline__ float bf2f(u16 b) { return __uint_as_float(((unsigned
 __device__ __forceinline__ u16 f2bf(float f) { return __builtin_bit_cast(u16, (__bf16)f); }
 __device__ __forceinline__ float rbf(float f) { return bf2f(f2bf(f)); }
 __device__ __forceinline__ float rhf(float f) { return (float)(_Float16)f; }
+// exp / logistic / tanh for ops whose result is rounded to bf16 or f16: the
+// hardware exp2 and reciprocal (relative error below 1e-5 over the whole range,
+// far inside half an ulp of a 16-bit result), instead of the correctly rounded
+// fp32 library routines with their range reductions.
+__device__ __forceinline__ float hexp(float x) { return __builtin_amdgcn_exp2f(x * 1.4426950408889634f); }
+__device__ __forceinline__ float hsigmoid(float x) { return __builtin_amdgcn_rcpf(1.0f + hexp(-x)); }
+__device__ __forceinline__ float htanh(float x) {
+  const float ax = __builtin_fabsf(x), p = x * x;
+  const float small = x + x * p * (-0.33333333f + p * 0.13333333f);  // |x| < 1/16: odd series
+  const float big = __builtin_copysignf(1.0f - 2.0f * __builtin_amdgcn_rcpf(hexp(2.0f * ax) + 1.0f), x);
+  return ax < 0.0625f ? small : big;
+}
 template <typename T> __device__ __forceinline__ T fmax_nan(T a, T b) { return (a > b || a != a) ? a : b; }
 template <typename T> __device__ __forceinline__ T fmin_nan(T a, T b) { return (a < b || a != a) ? a : b; }
 __device__ __forceinline__ long long ipow(long long b, long long e) {
@@ -1302,6 +1314,8 @@ std::string Lowerer::op_expr(const Node& n, const std::vector<std::string>& a, c
   const bool f64 = it == GHIP_DTYPE_FLOAT64;
   const std::string T = ctype(dt);
   auto fn1 = [&](const char* f32, const char* f64n) { return std::string(f64 ? f64n : f32) + "(" + a[0] + ")"; };
+  // 16-bit float results: the hardware transcendental forms (see hexp in the prelude).
+  const bool half = dt == GHIP_DTYPE_BFLOAT16 || dt == GHIP_DTYPE_FLOAT16;
   switch (n.kind) {
     case Kind::Unary:
       switch (n.sub) {
@@ -1309,14 +1323,16 @@ std::string Lowerer::op_expr(const Node& n, const std::vector<std::string>& a, c
         case GHIP_UNARY_NEG: return "(" + T + ")(-" + a[0] + ")";
         case GHIP_UNARY_SQRT: return fn1("sqrtf", "sqrt");
         case GHIP_UNARY_RSQRT: return f64 ? "(1.0 / sqrt(" + a[0] + "))" : "rsqrtf(" + a[0] + ")";
-        case GHIP_UNARY_EXP: return fn1("expf", "exp");
+        case GHIP_UNARY_EXP: return half ? "hexp(" + a[0] + ")" : fn1("expf", "exp");
         case GHIP_UNARY_EXPM1: return fn1("expm1f", "expm1");
         case GHIP_UNARY_LOG: return fn1("logf", "log");
         case GHIP_UNARY_LOG1P: return fn1("log1pf", "log1p");
         case GHIP_UNARY_SIN: return fn1("sinf", "sin");
         case GHIP_UNARY_COS: return fn1("cosf", "cos");
-        case GHIP_UNARY_TANH: return fn1("tanhf", "tanh");
-        case GHIP_UNARY_LOGISTIC: return f64 ? "(1.0 / (1.0 + exp(-" + a[0] + ")))" : "(1.0f / (1.0f + expf(-" + a[0] + ")))";
+        case GHIP_UNARY_TANH: return half ? "htanh(" + a[0] + ")" : fn1("tanhf", "tanh");
+        case GHIP_UNARY_LOGISTIC:
+          if (half) return "hsigmoid(" + a[0] + ")";
+          return f64 ? "(1.0 / (1.0 + exp(-" + a[0] + ")))" : "(1.0f / (1.0f + expf(-" + a[0] + ")))";
         case GHIP_UNARY_ERF: return fn1("erff", "erf");
         case GHIP_UNARY_FLOOR: return fn1("floorf", "floor");
         case GHIP_UNARY_CEIL: return fn1("ceilf", "ceil");
