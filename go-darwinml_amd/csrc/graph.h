@@ -228,6 +228,19 @@ struct ScatterDesc {
 int scatter_acc_dtype(int dtype);
 int launch_scatter(int dtype, int mode, const void* updates, const void* indices, void* acc, const ScatterDesc& d,
                    hipStream_t s, GHipError* err);
+// Deterministic scatter-add of n update rows (row stride upd_row elements) into
+// rows ids[i] (stride id_stride elements, int32 / int64; out of range skipped) of
+// the contiguous [V, D] float32 / bfloat16 / float16 table `out`, each row's
+// updates folded in their original order in fp32 and rounded once.  scratch:
+// scatter_rows_scratch(n) bytes.  n <= kScatterRowsMax, V <= kScatterRowsMaxTable.
+constexpr int64_t kScatterRowsMax = 16384;
+constexpr int64_t kScatterRowsMaxTable = (1 << 18) - 1;
+inline size_t scatter_rows_scratch(int64_t n) { return static_cast<size_t>(2 * n + 2) * 4; }
+// copy_src: when not null, the contiguous operand (16-byte aligned, size a
+// multiple of 16 bytes), copied into `out` by the same launch that sorts.
+int launch_scatter_rows(int dtype, const void* updates, int64_t upd_row, const void* ids, int id_dt, int64_t id_stride,
+                        int64_t n, void* out, int64_t V, int64_t D, void* scratch, const void* copy_src, hipStream_t s,
+                        GHipError* err);
 // dst (contiguous) = convert(src viewed through d.sst); widening / narrowing pairs
 // used around scatter accumulators.
 int launch_convert(int src_dt, int dst_dt, const void* src, void* dst, const CopyDesc& d, hipStream_t s,

@@ -854,6 +854,57 @@ struct Lowerer {
     return y;
   }
 
+  // ScatterSum in the embedding-gradient form (axis 0 of the operand, one index
+  // per update row, whole rows, float data): the deterministic sorted-row path.
+  // Returns a view with slot -1 when the scatter is not of that form.
+  View emit_scatter_rows(const Node& n, const View& op, const View& ix, const View& up) {
+    const Shape os = n.shape, is = N[n.in[1]].shape, us = N[n.in[2]].shape;
+    const int dt = os.dtype, r = os.rank(), ur = us.rank(), iva = static_cast<int>(n.i0);
+    View none;
+    if (n.sub != GHIP_SCATTER_SUM || r < 1) return none;
+    if (dt != GHIP_DTYPE_FLOAT32 && dt != GHIP_DTYPE_BFLOAT16 && dt != GHIP_DTYPE_FLOAT16) return none;
+    if (is.dtype != GHIP_DTYPE_INT32 && is.dtype != GHIP_DTYPE_INT64) return none;
+    if (n.a2 != std::vector<int64_t>{0} || n.a1 != std::vector<int64_t>{0}) return none;
+    const int nw = static_cast<int>(n.a0.size()), nb = ur - nw;  // window / scatter dims of updates
+    int64_t D = 1;
+    for (int k = 0; k < nw; ++k) {
+      if (n.a0[k] != nb + k || us.dims[nb + k] != os.dims[1 + k]) return none;  // trailing, whole rows
+      D *= os.dims[1 + k];
+    }
+    std::vector<int64_t> bax, wax, iax;
+    for (int k = 0; k < nb; ++k) bax.push_back(k);
+    for (int k = nb; k < ur; ++k) wax.push_back(k);
+    for (int k = 0; k < is.rank(); ++k)
+      if (k != iva) iax.push_back(k);
+    int64_t rows = 1, upd_row = 0, dsz = 0, dst_ = 0, isz = 1, ist = 0;
+    if (!merge(us, up, bax, &rows, &upd_row) || !merge(us, up, wax, &dsz, &dst_) || !merge(is, ix, iax, &isz, &ist))
+      return none;
+    if (D > 1 && dst_ != 1) return none;
+    if (rows > 1 && upd_row < D) return none;
+    if (rows == 0 || rows > kScatterRowsMax || os.dims[0] > kScatterRowsMaxTable) return none;
+    View y = fresh(os);
+    // A contiguous operand is copied by the launch that sorts (its other
+    // workgroups), otherwise by a strided copy first.
+    const bool fuse_copy = op.contiguous(os) && os.bytes() % 16 == 0 && op.offset * dtype_size(dt) % 16 == 0;
+    if (!fuse_copy) emit_copy(os, op, y, "(Scatter operand)");
+    Shape ss;
+    ss.dtype = GHIP_DTYPE_INT32;
+    ss.dims = {2 * rows + 2};
+    View sc = fresh(ss);
+    const int64_t V = os.dims[0];
+    const int idt = is.dtype;
+    std::vector<int> rd{up.slot, ix.slot, sc.slot};
+    if (fuse_copy) rd.push_back(op.slot);
+    add_step(fmt("scatter_rows_sum %s updates=%s ids=%s (sorted segments, deterministic%s)", os.str().c_str(),
+                 us.str().c_str(), is.str().c_str(), fuse_copy ? "; operand copied by the sorting launch" : ""),
+             rd, {y.slot, sc.slot}, [=](ExecState& st, GHipError* e) {
+               return launch_scatter_rows(dt, st.ptr(up, dt), upd_row, st.ptr(ix, idt), idt, ist, rows, st.ptr(y, dt), V,
+                                          D, st.ptr(sc, GHIP_DTYPE_INT32), fuse_copy ? st.ptr(op, dt) : nullptr,
+                                          st.stream, e);
+             });
+    return y;
+  }
+
   View emit_scatter(int v) {
     const Node n = N[v];
     const Shape os = n.shape, is = N[n.in[1]].shape, us = N[n.in[2]].shape;
@@ -864,6 +915,7 @@ struct Lowerer {
     View up = get(n.in[2]);
     if (failed) return bad();
     const int dt = os.dtype, adt = scatter_acc_dtype(dt);
+    if (View y = emit_scatter_rows(n, op, ix, up); y.slot >= 0 || failed) return y;
     View y = fresh(os);
     View acc = y;
     CopyDesc cd = copy_desc(os, op, y);

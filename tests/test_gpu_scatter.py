@@ -132,10 +132,18 @@ def test_scatter_embedding_gradient_vs_oracle(be, dt, mode):
                      [(_raw(op, dt), make_shape(dt, V, D)), (ids.reshape(n, 1), make_shape(I32, n, 1)),
                       (_raw(up, dt), make_shape(dt, n, D))])
     ref = orc.scatter(mode, op.astype(np.float64), ids.reshape(n, 1), up.astype(np.float64), 1, [1], [0], [0])
+    if mode == 0 and dt in (F32, BF16):
+        # sorted-row path: each row's updates folded in their original order in fp32 and
+        # rounded once -- exactly numpy's sequential float32 add.at, then one rounding
+        assert "scatter_rows_sum" in plan, plan
+        acc = op.astype(np.float32).copy()
+        ok = (ids >= 0) & (ids < V)
+        np.add.at(acc, ids[ok], up.astype(np.float32)[ok])
+        want = synth.to_bf16_bits(acc) if dt == BF16 else acc
+        assert np.array_equal(y, want)
     if dt == BF16:
         got = synth.bf16_bits_to_f32(y)
         if mode == 0:
-            assert "scatter accumulator" in plan
             # one rounding of an fp32 sum: within 2^-8 relative of the exact sum (RMS floor)
             assert rel_err(got, ref) <= 2.0 ** -8
         else:
@@ -165,6 +173,26 @@ def test_scatter_general_multi_axis_exact(be):
                       [(op, make_shape(dtypes.Float64, 6, 4, 5)), (idx, make_shape(I64, 2, 3, 4)),
                        (upd, make_shape(dtypes.Float64, 3, 2, 4, 2))])
         assert np.array_equal(y, orc.scatter(mode, op, idx, upd, *args)), name
+
+
+def test_scatter_rows_batched_ids_and_atomic_fallback(be):
+    """Ids [B, S] with updates [B, S, D] (the batched embedding-gradient form) take the
+    sorted-row path; more rows than one sort holds fall back to atomics."""
+    rng = np.random.default_rng(9)
+    V, D = 500, 40
+    for B, S, path in ((4, 300, "scatter_rows_sum"), (3, 6000, "scatter_sum")):
+        ids = rng.integers(0, V, (B, S)).astype(np.int64)
+        op = rng.standard_normal((V, D)).astype(np.float32)
+        up = rng.standard_normal((B, S, D)).astype(np.float32)
+        plan, (y,) = run(be, lambda f, o, i, u: [f.ScatterSum(o, i, u, 2, [2], [0], [0])],
+                         [(op, make_shape(F32, V, D)), (ids, make_shape(I64, B, S)), (up, make_shape(F32, B, S, D))])
+        assert path in plan, plan
+        ref = orc.scatter(0, op, ids, up, 2, [2], [0], [0])
+        assert rel_err(y, ref) <= 1e-5
+        if path == "scatter_rows_sum":
+            acc = op.copy()
+            np.add.at(acc, ids.reshape(-1), up.reshape(-1, D))
+            assert np.array_equal(y, acc)
 
 
 def test_scatter_embedding_gradient_large_bf16(be):
