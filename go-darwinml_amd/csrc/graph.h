@@ -11,6 +11,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <deque>
 #include <functional>
 #include <map>
 #include <memory>
@@ -56,6 +57,9 @@ enum class Kind {
   Reshape, Transpose, Broadcast, Slice, Concat, Reverse,
   Reduce, ArgMinMax, Dot, Gather, Softmax, LayerNorm, SDPA,
   DynSlice, DynUpdate, Scatter,
+  Capture,    // a closure's copy of an ancestor's value (an extra input after the params)
+  Call, While, If, Sort,  // control flow: multi-output, read through TupleGet
+  TupleGet,   // output i0 of a control-flow node
 };
 const char* kind_name(Kind k);
 
@@ -69,6 +73,8 @@ struct Node {
   int64_t i0 = 0, i1 = 0, i2 = 0, i3 = 0;
   std::vector<uint8_t> data;   // Const payload
   std::string name;            // Param name
+  std::vector<GHipFunction*> fns;   // control flow: called / cond+body / true+false / comparator
+  std::vector<Shape> outs;          // control flow: output shapes
 };
 
 bool is_elementwise(Kind k);
@@ -101,23 +107,37 @@ struct GHipBuffer {
   bool valid = true;
 };
 
+// Value ids handed out by the graph API are unique within a builder:
+// (function index << kFnShift) | node index, the main function being index 0
+// (so its ids are plain node indices).  Nodes refer to their operands by node
+// index inside their own function.
+constexpr int kFnShift = 24;
+constexpr int kNodeMask = (1 << kFnShift) - 1;
+
 struct GHipFunction {
   GHipBuilder* builder = nullptr;
   std::string name;
-  std::vector<ghip::Node> nodes;
+  int index = 0;                    // position in the builder's function table
+  GHipFunction* parent = nullptr;   // closures: the function that created them
+  std::deque<ghip::Node> nodes;     // stable addresses: nodes are only appended
   std::vector<int> params;
   std::vector<int> outputs;
+  std::vector<int> captures;        // per Capture node: the parent's node index it copies
+  std::map<int, int> capture_of;    // parent node index -> local Capture node
   bool returned = false;
   int add(ghip::Node&& n) {
     nodes.push_back(std::move(n));
     return static_cast<int>(nodes.size()) - 1;
   }
+  int global(int local) const { return (index << kFnShift) | local; }
 };
 
 struct GHipBuilder {
   GHipBackend* backend = nullptr;
   std::string name;
   std::unique_ptr<GHipFunction> main;
+  std::vector<std::unique_ptr<GHipFunction>> others;  // closures and named functions
+  std::vector<GHipFunction*> table;                   // index -> function (main first)
   bool compiled = false;
 };
 
@@ -156,6 +176,7 @@ struct Slot {
 };
 
 struct Plan {
+  std::vector<std::shared_ptr<GHipExecutable>> subs;  // compiled closures / called functions
   std::vector<Slot> slots;
   std::vector<Step> steps;
   size_t arena_bytes = 0;
@@ -166,6 +187,12 @@ struct Plan {
 };
 
 int lower(GHipBackend* be, GHipFunction* fn, Plan* plan, GHipError* err);
+// Compiles one function (main, closure or named function) into an executable:
+// inputs are its params followed by its captures.
+std::shared_ptr<GHipExecutable> compile_function(GHipBackend* be, GHipFunction* fn, GHipError* err);
+// Runs an executable's plan on its backend's stream with the given device
+// pointers for its inputs and (contiguous, pre-allocated) outputs.
+int run_plan(GHipExecutable* e, void* const* in_ptrs, void* const* out_ptrs, GHipError* err);
 
 // Generated elementwise kernels (rtc.cpp).
 struct RtcKernel {

@@ -330,6 +330,7 @@ extern "C" GHipBuilder* ghip_builder_new(GHipBackend* b, const char* name, GHipE
   auto bl = new GHipBuilder();
   bl->backend = b;
   bl->name = name ? name : "";
+  bl->table.push_back(nullptr);  // index 0: the main function, created on demand
   return bl;
 }
 
@@ -341,6 +342,9 @@ extern "C" GHipFunction* ghip_builder_main(GHipBuilder* bl) {
     bl->main = std::make_unique<GHipFunction>();
     bl->main->builder = bl;
     bl->main->name = "main";
+    bl->main->index = 0;
+    if (bl->table.empty()) bl->table.push_back(nullptr);
+    bl->table[0] = bl->main.get();
   }
   return bl->main.get();
 }
@@ -365,16 +369,71 @@ struct Ctx {
     ok = false;
     return -1;
   }
+  // Node index in f of the value with (builder-wide) id v; a value of an
+  // enclosing function is captured (through every function in between).
+  int loc(int v) {
+    if (!f) { fail(GHIP_ERR_INVALID_ARG, "null function"); return -1; }
+    if (v < 0) return v;
+    GHipBuilder* b = f->builder;
+    const int fi = v >> kFnShift, li = v & kNodeMask;
+    GHipFunction* g = b && fi < static_cast<int>(b->table.size()) ? b->table[fi] : (fi == 0 ? f : nullptr);
+    if (!g || li >= static_cast<int>(g->nodes.size())) {
+      fail(GHIP_ERR_INVALID_ARG, "value %d does not belong to this builder", v);
+      return -1;
+    }
+    if (g == f) return li;
+    GHipFunction* p = f->parent;
+    while (p && p != g) p = p->parent;
+    if (!p) {
+      fail(GHIP_ERR_INVALID_ARG, "value %d belongs to function %s, which does not enclose %s", v, g->name.c_str(),
+           f->name.c_str());
+      return -1;
+    }
+    return capture(f, g, li);
+  }
+  static int capture(GHipFunction* h, GHipFunction* g, int li) {
+    if (h == g) return li;
+    const int pl = capture(h->parent, g, li);
+    auto it = h->capture_of.find(pl);
+    if (it != h->capture_of.end()) return it->second;
+    Node cn{Kind::Capture};
+    cn.shape = h->parent->nodes[pl].shape;
+    cn.i0 = static_cast<int64_t>(h->captures.size());
+    const int id = h->add(std::move(cn));
+    h->captures.push_back(pl);
+    h->capture_of[pl] = id;
+    return id;
+  }
   const Node* node(int v) {
     if (!f) { fail(GHIP_ERR_INVALID_ARG, "null function"); return nullptr; }
     if (f->returned) { fail(GHIP_ERR_STATE, "function already returned"); return nullptr; }
-    if (v < 0 || v >= static_cast<int>(f->nodes.size())) {
-      fail(GHIP_ERR_INVALID_ARG, "value %d does not belong to function %s", v, f->name.c_str());
+    const int l = loc(v);
+    if (l < 0) {
+      if (ok) fail(GHIP_ERR_INVALID_ARG, "value %d does not belong to function %s", v, f->name.c_str());
       return nullptr;
     }
-    return &f->nodes[v];
+    return &f->nodes[l];
+  }
+  // Appends n (operands given as value ids) and returns its value id.
+  int add(Node&& n) {
+    for (auto& i : n.in) {
+      if (i < 0) continue;
+      i = loc(i);
+      if (i < 0) return -1;
+    }
+    return f->global(f->add(std::move(n)));
   }
 };
+
+// Shape of the value with id v, looked up in its own function.
+const Node* value_node(GHipFunction* f, int v) {
+  if (!f || v < 0) return nullptr;
+  GHipBuilder* b = f->builder;
+  const int fi = v >> kFnShift, li = v & kNodeMask;
+  GHipFunction* g = b && fi < static_cast<int>(b->table.size()) ? b->table[fi] : (fi == 0 ? f : nullptr);
+  if (!g || li >= static_cast<int>(g->nodes.size())) return nullptr;
+  return &g->nodes[li];
+}
 
 // numpy-style broadcast of two shapes (equal dims, size-1 dims, or rank-0 scalars).
 bool broadcast_dims(const std::vector<int64_t>& a, const std::vector<int64_t>& b,
@@ -419,7 +478,7 @@ extern "C" GHipValue ghip_fn_parameter(GHipFunction* f, const char* name, int dt
   n.i0 = static_cast<int64_t>(f->params.size());
   int id = f->add(std::move(n));
   f->params.push_back(id);
-  return id;
+  return f->global(id);
 }
 
 extern "C" GHipValue ghip_fn_constant(GHipFunction* f, int dtype, const int64_t* dims, int rank,
@@ -433,7 +492,7 @@ extern "C" GHipValue ghip_fn_constant(GHipFunction* f, int dtype, const int64_t*
     return c.fail(GHIP_ERR_INVALID_ARG, "%zu bytes for shape %s", nbytes, n.shape.str().c_str());
   if (nbytes && !data) return c.fail(GHIP_ERR_INVALID_ARG, "null data");
   n.data.assign(static_cast<const uint8_t*>(data), static_cast<const uint8_t*>(data) + nbytes);
-  return f->add(std::move(n));
+  return c.add(std::move(n));
 }
 
 extern "C" GHipValue ghip_fn_iota(GHipFunction* f, int dtype, const int64_t* dims, int rank,
@@ -446,7 +505,7 @@ extern "C" GHipValue ghip_fn_iota(GHipFunction* f, int dtype, const int64_t* dim
   if (axis < 0) axis += rank;
   if (axis < 0 || axis >= rank) return c.fail(GHIP_ERR_INVALID_ARG, "axis out of range");
   n.i0 = axis;
-  return f->add(std::move(n));
+  return c.add(std::move(n));
 }
 
 extern "C" GHipValue ghip_fn_unary(GHipFunction* f, int op, GHipValue x, GHipError* err) {
@@ -481,7 +540,7 @@ extern "C" GHipValue ghip_fn_unary(GHipFunction* f, int op, GHipValue x, GHipErr
       break;
     default: break;
   }
-  return f->add(std::move(n));
+  return c.add(std::move(n));
 }
 
 extern "C" GHipValue ghip_fn_binary(GHipFunction* f, int op, GHipValue lhs, GHipValue rhs,
@@ -507,7 +566,7 @@ extern "C" GHipValue ghip_fn_binary(GHipFunction* f, int op, GHipValue lhs, GHip
   n.shape.dtype = dt;
   if (!broadcast_dims(a->shape.dims, b->shape.dims, &n.shape.dims))
     return c.fail(GHIP_ERR_INVALID_ARG, "incompatible shapes %s and %s", a->shape.str().c_str(), b->shape.str().c_str());
-  return f->add(std::move(n));
+  return c.add(std::move(n));
 }
 
 extern "C" GHipValue ghip_fn_compare(GHipFunction* f, int op, GHipValue lhs, GHipValue rhs,
@@ -525,7 +584,7 @@ extern "C" GHipValue ghip_fn_compare(GHipFunction* f, int op, GHipValue lhs, GHi
   n.shape.dtype = GHIP_DTYPE_BOOL;
   if (!broadcast_dims(a->shape.dims, b->shape.dims, &n.shape.dims))
     return c.fail(GHIP_ERR_INVALID_ARG, "incompatible shapes %s and %s", a->shape.str().c_str(), b->shape.str().c_str());
-  return f->add(std::move(n));
+  return c.add(std::move(n));
 }
 
 extern "C" GHipValue ghip_fn_where(GHipFunction* f, GHipValue cond, GHipValue on_true,
@@ -546,7 +605,7 @@ extern "C" GHipValue ghip_fn_where(GHipFunction* f, GHipValue cond, GHipValue on
   if (!broadcast_dims(t->shape.dims, e->shape.dims, &d1) ||
       !broadcast_dims(p->shape.dims, d1, &n.shape.dims))
     return c.fail(GHIP_ERR_INVALID_ARG, "incompatible shapes");
-  return f->add(std::move(n));
+  return c.add(std::move(n));
 }
 
 extern "C" GHipValue ghip_fn_clamp(GHipFunction* f, GHipValue lo, GHipValue x, GHipValue hi,
@@ -567,7 +626,7 @@ extern "C" GHipValue ghip_fn_clamp(GHipFunction* f, GHipValue lo, GHipValue x, G
   Node n{Kind::Clamp};
   n.in = {lo, x, hi};
   n.shape = v->shape;
-  return f->add(std::move(n));
+  return c.add(std::move(n));
 }
 
 extern "C" GHipValue ghip_fn_convert_dtype(GHipFunction* f, GHipValue x, int dtype, GHipError* err) {
@@ -579,7 +638,7 @@ extern "C" GHipValue ghip_fn_convert_dtype(GHipFunction* f, GHipValue x, int dty
   n.in = {x};
   n.shape = a->shape;
   n.shape.dtype = dtype;
-  return f->add(std::move(n));
+  return c.add(std::move(n));
 }
 
 extern "C" GHipValue ghip_fn_reshape(GHipFunction* f, GHipValue x, const int64_t* dims, int rank,
@@ -592,7 +651,7 @@ extern "C" GHipValue ghip_fn_reshape(GHipFunction* f, GHipValue x, const int64_t
   if (n.shape.size() != a->shape.size())
     return c.fail(GHIP_ERR_INVALID_ARG, "cannot reshape %s to %s", a->shape.str().c_str(), n.shape.str().c_str());
   n.in = {x};
-  return f->add(std::move(n));
+  return c.add(std::move(n));
 }
 
 extern "C" GHipValue ghip_fn_transpose(GHipFunction* f, GHipValue x, const int* perm, int rank,
@@ -608,7 +667,7 @@ extern "C" GHipValue ghip_fn_transpose(GHipFunction* f, GHipValue x, const int* 
   n.a0 = p;
   n.shape.dtype = a->shape.dtype;
   for (auto i : p) n.shape.dims.push_back(a->shape.dims[i]);
-  return f->add(std::move(n));
+  return c.add(std::move(n));
 }
 
 extern "C" GHipValue ghip_fn_broadcast_in_dim(GHipFunction* f, GHipValue x, const int64_t* dims,
@@ -630,7 +689,7 @@ extern "C" GHipValue ghip_fn_broadcast_in_dim(GHipFunction* f, GHipValue x, cons
   }
   n.in = {x};
   n.a0 = ax;
-  return f->add(std::move(n));
+  return c.add(std::move(n));
 }
 
 extern "C" GHipValue ghip_fn_reduce(GHipFunction* f, int op, GHipValue x, const int* axes, int naxes,
@@ -654,7 +713,7 @@ extern "C" GHipValue ghip_fn_reduce(GHipFunction* f, int op, GHipValue x, const 
   n.shape.dtype = a->shape.dtype;
   for (int i = 0; i < a->shape.rank(); ++i)
     if (!std::binary_search(ax.begin(), ax.end(), i)) n.shape.dims.push_back(a->shape.dims[i]);
-  return f->add(std::move(n));
+  return c.add(std::move(n));
 }
 
 extern "C" GHipValue ghip_fn_arg_min_max(GHipFunction* f, GHipValue x, int axis, int out_dtype,
@@ -676,7 +735,7 @@ extern "C" GHipValue ghip_fn_arg_min_max(GHipFunction* f, GHipValue x, int axis,
   n.shape.dtype = out_dtype;
   for (int i = 0; i < r; ++i)
     if (i != axis) n.shape.dims.push_back(a->shape.dims[i]);
-  return f->add(std::move(n));
+  return c.add(std::move(n));
 }
 
 extern "C" GHipValue ghip_fn_dot_general(GHipFunction* f, GHipValue lhs, const int* lc, int nlc,
@@ -720,7 +779,7 @@ extern "C" GHipValue ghip_fn_dot_general(GHipFunction* f, GHipValue lhs, const i
     if (std::find(rca.begin(), rca.end(), i) == rca.end() && std::find(rba.begin(), rba.end(), i) == rba.end())
       n.shape.dims.push_back(b->shape.dims[i]);
   if (n.shape.rank() > kMaxRank) return c.fail(GHIP_ERR_UNSUPPORTED, "output rank too large");
-  return f->add(std::move(n));
+  return c.add(std::move(n));
 }
 
 extern "C" GHipValue ghip_fn_gather(GHipFunction* f, GHipValue operand, GHipValue start_indices,
@@ -770,7 +829,7 @@ extern "C" GHipValue ghip_fn_gather(GHipFunction* f, GHipValue operand, GHipValu
   n.a1 = coll;
   n.a2 = omap;
   n.a3.assign(slice_sizes, slice_sizes + n_sizes);
-  return f->add(std::move(n));
+  return c.add(std::move(n));
 }
 
 extern "C" GHipValue ghip_fn_slice(GHipFunction* f, GHipValue x, const int64_t* starts,
@@ -792,7 +851,7 @@ extern "C" GHipValue ghip_fn_slice(GHipFunction* f, GHipValue x, const int64_t* 
     n.a2.push_back(st);
     n.shape.dims.push_back((limits[i] - starts[i] + st - 1) / st);
   }
-  return f->add(std::move(n));
+  return c.add(std::move(n));
 }
 
 extern "C" GHipValue ghip_fn_concatenate(GHipFunction* f, int axis, const GHipValue* operands, int cnt,
@@ -817,7 +876,7 @@ extern "C" GHipValue ghip_fn_concatenate(GHipFunction* f, int axis, const GHipVa
     n.in.push_back(operands[i]);
   }
   n.i0 = axis;
-  return f->add(std::move(n));
+  return c.add(std::move(n));
 }
 
 extern "C" GHipValue ghip_fn_reverse(GHipFunction* f, GHipValue x, const int* axes, int naxes,
@@ -831,7 +890,7 @@ extern "C" GHipValue ghip_fn_reverse(GHipFunction* f, GHipValue x, const int* ax
   n.in = {x};
   n.a0 = ax;
   n.shape = a->shape;
-  return f->add(std::move(n));
+  return c.add(std::move(n));
 }
 
 extern "C" GHipValue ghip_fn_fused_softmax(GHipFunction* f, GHipValue x, int axis, GHipError* err) {
@@ -846,7 +905,7 @@ extern "C" GHipValue ghip_fn_fused_softmax(GHipFunction* f, GHipValue x, int axi
   n.in = {x};
   n.i0 = axis;
   n.shape = a->shape;
-  return f->add(std::move(n));
+  return c.add(std::move(n));
 }
 
 extern "C" GHipValue ghip_fn_fused_layer_norm(GHipFunction* f, GHipValue x, const int* axes, int naxes,
@@ -876,7 +935,7 @@ extern "C" GHipValue ghip_fn_fused_layer_norm(GHipFunction* f, GHipValue x, cons
     if (p->shape.dtype != a->shape.dtype) return c.fail(GHIP_ERR_INVALID_ARG, "gamma/beta dtype");
     if (p->shape.size() != norm) return c.fail(GHIP_ERR_INVALID_ARG, "gamma/beta must cover the normalized axes");
   }
-  return f->add(std::move(n));
+  return c.add(std::move(n));
 }
 
 extern "C" GHipValue ghip_fn_fused_sdpa(GHipFunction* f, GHipValue q, GHipValue k, GHipValue v,
@@ -917,7 +976,186 @@ extern "C" GHipValue ghip_fn_fused_sdpa(GHipFunction* f, GHipValue q, GHipValue 
   n.f0 = scale;
   n.shape = qn->shape;
   n.shape.dims[3] = vn->shape.dims[3];
-  return f->add(std::move(n));
+  return c.add(std::move(n));
+}
+
+// ===========================================================================
+// Functions and control flow (builder.go:57-70, function.go:120-133, 354-660).
+// A closure is a function whose parent is the function that created it; values
+// of enclosing functions it uses become Capture nodes (extra inputs after its
+// params).  Call / While / If / Sort append one multi-output node and return
+// its outputs as TupleGet values.
+// ===========================================================================
+namespace {
+GHipFunction* new_function(GHipBuilder* bl, const std::string& name, GHipFunction* parent) {
+  auto fn = std::make_unique<GHipFunction>();
+  fn->builder = bl;
+  fn->name = name;
+  fn->parent = parent;
+  fn->index = static_cast<int>(bl->table.size());
+  bl->table.push_back(fn.get());
+  bl->others.push_back(std::move(fn));
+  return bl->table.back();
+}
+
+// Emits the control-flow node and one TupleGet per output; writes the value ids.
+int emit_cf(Ctx& c, Node&& n, GHipValue* outs, int max_outs) {
+  const int k = static_cast<int>(n.outs.size());
+  if (!outs || max_outs < k) {
+    c.fail(GHIP_ERR_INVALID_ARG, "room for %d outputs needed, %d given", k, max_outs);
+    return -1;
+  }
+  std::vector<Shape> shapes = n.outs;
+  const int cf = c.add(std::move(n));
+  if (cf < 0) return -1;
+  for (int i = 0; i < k; ++i) {
+    Node t{Kind::TupleGet};
+    t.in = {cf};
+    t.i0 = i;
+    t.shape = shapes[i];
+    outs[i] = c.add(std::move(t));
+    if (outs[i] < 0) return -1;
+  }
+  return k;
+}
+
+// The reference's validateClosure (function.go:234-248).
+bool check_closure(Ctx& c, GHipFunction* f, GHipFunction* g, const char* what) {
+  if (!g) return c.fail(GHIP_ERR_INVALID_ARG, "%s is null", what), false;
+  if (g->parent != f) return c.fail(GHIP_ERR_INVALID_ARG, "%s must be a closure of the current function", what), false;
+  if (!g->returned) return c.fail(GHIP_ERR_INVALID_ARG, "%s must have Return() called", what), false;
+  return true;
+}
+
+void add_captures(Node& n, const GHipFunction* g, GHipFunction* f) {
+  for (int pl : g->captures) n.in.push_back(f->global(pl));
+}
+}  // namespace
+
+extern "C" GHipFunction* ghip_builder_new_function(GHipBuilder* bl, const char* name, GHipError* err) {
+  if (!bl) {
+    set_error(err, GHIP_ERR_INVALID_ARG, "NewFunction: null builder");
+    return nullptr;
+  }
+  if (bl->compiled) {
+    set_error(err, GHIP_ERR_STATE, "NewFunction: builder already compiled");
+    return nullptr;
+  }
+  return new_function(bl, name ? name : "", nullptr);
+}
+
+extern "C" GHipFunction* ghip_fn_closure(GHipFunction* f, GHipError* err) {
+  if (!f || !f->builder) {
+    set_error(err, GHIP_ERR_INVALID_ARG, "Closure: null function");
+    return nullptr;
+  }
+  if (f->returned) {
+    set_error(err, GHIP_ERR_STATE, "Closure: function %s already returned", f->name.c_str());
+    return nullptr;
+  }
+  return new_function(f->builder, f->name + "/closure", f);
+}
+
+extern "C" int ghip_fn_call(GHipFunction* f, GHipFunction* target, const GHipValue* inputs, int n, GHipValue* outs,
+                            int max_outs, GHipError* err) {
+  FN_BEGIN("Call");
+  if (!f || !target) return c.fail(GHIP_ERR_INVALID_ARG, "null function");
+  if (target->builder != f->builder) return c.fail(GHIP_ERR_INVALID_ARG, "target function must be from the same builder");
+  if (!target->returned) return c.fail(GHIP_ERR_INVALID_ARG, "target function %s must have Return() called", target->name.c_str());
+  if (target->parent && target->parent != f)
+    return c.fail(GHIP_ERR_INVALID_ARG, "target closure must belong to the current function");
+  if (target == f) return c.fail(GHIP_ERR_INVALID_ARG, "a function cannot call itself");
+  if (n != static_cast<int>(target->params.size()))
+    return c.fail(GHIP_ERR_INVALID_ARG, "function %s expects %zu parameters, got %d inputs", target->name.c_str(),
+                  target->params.size(), n);
+  Node node{Kind::Call};
+  for (int i = 0; i < n; ++i) {
+    const Node* a = c.node(inputs[i]);
+    if (!a) return -1;
+    if (a->shape != target->nodes[target->params[i]].shape)
+      return c.fail(GHIP_ERR_INVALID_ARG, "parameter %d shape mismatch: expected %s, got %s", i,
+                    target->nodes[target->params[i]].shape.str().c_str(), a->shape.str().c_str());
+    node.in.push_back(inputs[i]);
+  }
+  add_captures(node, target, f);
+  node.fns = {target};
+  for (int o : target->outputs) node.outs.push_back(target->nodes[o].shape);
+  node.i0 = n;
+  return emit_cf(c, std::move(node), outs, max_outs);
+}
+
+extern "C" int ghip_fn_while(GHipFunction* f, GHipFunction* cond, GHipFunction* body, const GHipValue* init, int n,
+                             GHipValue* outs, int max_outs, GHipError* err) {
+  FN_BEGIN("While");
+  if (n <= 0) return c.fail(GHIP_ERR_INVALID_ARG, "requires at least one initial state value");
+  if (!check_closure(c, f, cond, "cond") || !check_closure(c, f, body, "body")) return -1;
+  Node node{Kind::While};
+  for (int i = 0; i < n; ++i) {
+    const Node* a = c.node(init[i]);
+    if (!a) return -1;
+    node.in.push_back(init[i]);
+    node.outs.push_back(a->shape);
+  }
+  if (static_cast<int>(cond->params.size()) != n)
+    return c.fail(GHIP_ERR_INVALID_ARG, "cond must have %d parameters, got %zu", n, cond->params.size());
+  if (static_cast<int>(body->params.size()) != n)
+    return c.fail(GHIP_ERR_INVALID_ARG, "body must have %d parameters, got %zu", n, body->params.size());
+  for (int i = 0; i < n; ++i) {
+    if (cond->nodes[cond->params[i]].shape != node.outs[i])
+      return c.fail(GHIP_ERR_INVALID_ARG, "cond parameter %d shape %s doesn't match state shape %s", i,
+                    cond->nodes[cond->params[i]].shape.str().c_str(), node.outs[i].str().c_str());
+    if (body->nodes[body->params[i]].shape != node.outs[i])
+      return c.fail(GHIP_ERR_INVALID_ARG, "body parameter %d shape %s doesn't match state shape %s", i,
+                    body->nodes[body->params[i]].shape.str().c_str(), node.outs[i].str().c_str());
+  }
+  if (cond->outputs.size() != 1) return c.fail(GHIP_ERR_INVALID_ARG, "cond must return exactly one value, got %zu", cond->outputs.size());
+  const Shape& cs = cond->nodes[cond->outputs[0]].shape;
+  if (cs.rank() != 0 || cs.dtype != GHIP_DTYPE_BOOL)
+    return c.fail(GHIP_ERR_INVALID_ARG, "cond must return scalar bool, got %s", cs.str().c_str());
+  if (static_cast<int>(body->outputs.size()) != n)
+    return c.fail(GHIP_ERR_INVALID_ARG, "body must return %d values, got %zu", n, body->outputs.size());
+  for (int i = 0; i < n; ++i)
+    if (body->nodes[body->outputs[i]].shape != node.outs[i])
+      return c.fail(GHIP_ERR_INVALID_ARG, "body output %d shape %s must match state shape %s", i,
+                    body->nodes[body->outputs[i]].shape.str().c_str(), node.outs[i].str().c_str());
+  add_captures(node, cond, f);
+  add_captures(node, body, f);
+  node.fns = {cond, body};
+  node.i0 = n;
+  node.i1 = static_cast<int64_t>(cond->captures.size());
+  return emit_cf(c, std::move(node), outs, max_outs);
+}
+
+extern "C" int ghip_fn_if(GHipFunction* f, GHipValue pred, GHipFunction* true_branch, GHipFunction* false_branch,
+                          GHipValue* outs, int max_outs, GHipError* err) {
+  FN_BEGIN("If");
+  const Node* p = c.node(pred);
+  if (!p) return -1;
+  if (p->shape.rank() != 0 || p->shape.dtype != GHIP_DTYPE_BOOL)
+    return c.fail(GHIP_ERR_INVALID_ARG, "pred must be scalar bool, got %s", p->shape.str().c_str());
+  if (!check_closure(c, f, true_branch, "trueBranch") || !check_closure(c, f, false_branch, "falseBranch")) return -1;
+  if (!true_branch->params.empty())
+    return c.fail(GHIP_ERR_INVALID_ARG, "trueBranch must have no parameters, got %zu", true_branch->params.size());
+  if (!false_branch->params.empty())
+    return c.fail(GHIP_ERR_INVALID_ARG, "falseBranch must have no parameters, got %zu", false_branch->params.size());
+  if (true_branch->outputs.size() != false_branch->outputs.size())
+    return c.fail(GHIP_ERR_INVALID_ARG, "branches must return same number of outputs (true=%zu, false=%zu)",
+                  true_branch->outputs.size(), false_branch->outputs.size());
+  Node node{Kind::If};
+  for (size_t i = 0; i < true_branch->outputs.size(); ++i) {
+    const Shape& a = true_branch->nodes[true_branch->outputs[i]].shape;
+    const Shape& b = false_branch->nodes[false_branch->outputs[i]].shape;
+    if (a != b)
+      return c.fail(GHIP_ERR_INVALID_ARG, "output %zu shapes must match (true=%s, false=%s)", i, a.str().c_str(),
+                    b.str().c_str());
+    node.outs.push_back(a);
+  }
+  node.in = {pred};
+  add_captures(node, true_branch, f);
+  add_captures(node, false_branch, f);
+  node.fns = {true_branch, false_branch};
+  node.i0 = static_cast<int64_t>(true_branch->captures.size());
+  return emit_cf(c, std::move(node), outs, max_outs);
 }
 
 // ===========================================================================
@@ -961,7 +1199,7 @@ extern "C" GHipValue ghip_fn_dynamic_slice(GHipFunction* f, GHipValue operand, c
   }
   n.in.push_back(operand);
   n.in.insert(n.in.end(), starts, starts + nstarts);
-  return f->add(std::move(n));
+  return c.add(std::move(n));
 }
 
 extern "C" GHipValue ghip_fn_dynamic_update_slice(GHipFunction* f, GHipValue operand, GHipValue update,
@@ -985,7 +1223,7 @@ extern "C" GHipValue ghip_fn_dynamic_update_slice(GHipFunction* f, GHipValue ope
   n.shape = a->shape;
   n.in = {operand, update};
   n.in.insert(n.in.end(), starts, starts + nstarts);
-  return f->add(std::move(n));
+  return c.add(std::move(n));
 }
 
 extern "C" GHipValue ghip_fn_scatter(GHipFunction* f, int mode, GHipValue operand, GHipValue indices,
@@ -1054,7 +1292,7 @@ extern "C" GHipValue ghip_fn_scatter(GHipFunction* f, int mode, GHipValue operan
   n.a0 = uwa;
   n.a1 = iwa;
   n.a2 = sato;
-  return f->add(std::move(n));
+  return c.add(std::move(n));
 }
 
 // ===========================================================================
@@ -1103,8 +1341,8 @@ GHipValue wrap(GHipValue v, GHipError* err, const char* op) {
 
 // bias broadcast over the trailing axes of `shape_of` and added (function.go:2601-2618).
 GHipValue add_trailing_bias(GHipFunction* f, GHipValue v, GHipValue bias, GHipError* err) {
-  const Shape rs = f->nodes[v].shape;
-  const Shape bs = f->nodes[bias].shape;
+  const Shape rs = value_node(f, v)->shape;
+  const Shape bs = value_node(f, bias)->shape;
   if (bs.rank() > rs.rank()) {
     set_error(err, GHIP_ERR_INVALID_ARG, "bias rank %d exceeds result rank %d", bs.rank(), rs.rank());
     return -1;
@@ -1118,7 +1356,7 @@ GHipValue add_trailing_bias(GHipFunction* f, GHipValue v, GHipValue bias, GHipEr
 
 // x [..., din] . w [din, ...] contracting x's last axis with w's first.
 GHipValue dense_dot(GHipFunction* f, GHipValue x, GHipValue w, GHipError* err) {
-  const int lc = f->nodes[x].shape.rank() - 1, rc = 0;
+  const int lc = value_node(f, x)->shape.rank() - 1, rc = 0;
   return ghip_fn_dot_general(f, x, &lc, 1, nullptr, 0, w, &rc, 1, nullptr, 0, err);
 }
 
@@ -1174,7 +1412,7 @@ extern "C" GHipValue ghip_fn_fused_dense(GHipFunction* f, GHipValue x, GHipValue
     r = wrap(add_trailing_bias(f, r, bias, err), err, "FusedDense: bias");
     if (r < 0) return -1;
   }
-  const int dt = f->nodes[r].shape.dtype;
+  const int dt = value_node(f, r)->shape.dtype;
   switch (activation) {
     case GHIP_ACTIVATION_GELU:
       return wrap(ghip_fn_fused_gelu(f, r, 0, err), err, "FusedDense: GELU activation");
@@ -1220,7 +1458,7 @@ extern "C" int ghip_fn_fused_qkv_projection(GHipFunction* f, GHipValue x, GHipVa
   const char* what[3] = {"FusedAttentionQKVProjection: slice Q", "FusedAttentionQKVProjection: slice K",
                          "FusedAttentionQKVProjection: slice V"};
   auto slice_last = [&](GHipValue t, int64_t a, int64_t b, const char* msg) -> GHipValue {
-    const Shape ts = f->nodes[t].shape;
+    const Shape ts = value_node(f, t)->shape;
     const int r = ts.rank();
     std::vector<int64_t> st(r, 0), lim = ts.dims, str(r, 1);
     st[r - 1] = a;
@@ -1229,7 +1467,7 @@ extern "C" int ghip_fn_fused_qkv_projection(GHipFunction* f, GHipValue x, GHipVa
   };
   GHipValue out[3] = {-1, -1, -1};
   const bool any_bias = bias_q >= 0 || bias_k >= 0 || bias_v >= 0;
-  if (any_bias && f->nodes[w_qkv].shape.rank() >= 2) {
+  if (any_bias && value_node(f, w_qkv)->shape.rank() >= 2) {
     // With biases: one product per output over the matching columns of wQKV.
     // Every output element is the same K-sum as in x . wQKV (the GEMM's
     // summation order does not depend on N), and each product's bias add runs
@@ -1268,17 +1506,26 @@ extern "C" int ghip_fn_return(GHipFunction* f, const GHipValue* outputs, int cnt
   FN_BEGIN("Return");
   if (!f) return c.fail(GHIP_ERR_INVALID_ARG, "null function");
   if (f->returned) return set_error(err, GHIP_ERR_STATE, "Return: called twice");
-  for (int i = 0; i < cnt; ++i)
-    if (outputs[i] < 0 || outputs[i] >= static_cast<int>(f->nodes.size()))
+  std::vector<int> loc(cnt);
+  for (int i = 0; i < cnt; ++i) {
+    loc[i] = outputs[i] < 0 ? -1 : c.loc(outputs[i]);  // a closure may return a captured value
+    if (loc[i] < 0) {
+      ghip_error_clear(err);
       return set_error(err, GHIP_ERR_INVALID_ARG, "Return: output %d is not a value of this function", i);
-  f->outputs.assign(outputs, outputs + cnt);
+    }
+    if (f->nodes[loc[i]].kind == Kind::Call || f->nodes[loc[i]].kind == Kind::While ||
+        f->nodes[loc[i]].kind == Kind::If || f->nodes[loc[i]].kind == Kind::Sort)
+      return set_error(err, GHIP_ERR_INVALID_ARG, "Return: output %d is a control-flow tuple", i);
+  }
+  f->outputs = loc;
   f->returned = true;
   return GHIP_OK;
 }
 
 extern "C" int ghip_fn_value_shape(GHipFunction* f, GHipValue v, int* dtype, int64_t* dims, int max_rank) {
-  if (!f || v < 0 || v >= static_cast<int>(f->nodes.size())) return -1;
-  const Shape& s = f->nodes[v].shape;
+  const Node* n = value_node(f, v);
+  if (!n) return -1;
+  const Shape& s = n->shape;
   if (dtype) *dtype = s.dtype;
   for (int i = 0; i < s.rank() && i < max_rank; ++i) dims[i] = s.dims[i];
   return s.rank();

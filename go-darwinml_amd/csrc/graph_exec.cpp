@@ -17,20 +17,25 @@
 
 using namespace ghip;
 
-extern "C" GHipExecutable* ghip_builder_compile(GHipBuilder* bl, GHipError* err) {
-  if (!bl) { set_error(err, GHIP_ERR_INVALID_ARG, "Compile: null builder"); return nullptr; }
-  if (bl->compiled) { set_error(err, GHIP_ERR_STATE, "Builder already compiled"); return nullptr; }
-  if (!bl->main) { set_error(err, GHIP_ERR_STATE, "Builder has no main function"); return nullptr; }
-  if (!bl->main->returned) { set_error(err, GHIP_ERR_STATE, "Main function has no Return() call"); return nullptr; }
-  GHipBackend* be = bl->backend;
-  if (!be || be->finalized) { set_error(err, GHIP_ERR_STATE, "Compile: backend finalized"); return nullptr; }
-  bl->compiled = true;
+namespace ghip {
+
+// Lowers fn and uploads its constants.  Inputs: fn's params, then its captures.
+static GHipExecutable* compile_raw(GHipBackend* be, GHipFunction* fn, GHipError* err) {
+  if (!fn->returned) {
+    set_error(err, GHIP_ERR_STATE, "Compile: function %s has no Return() call", fn->name.c_str());
+    return nullptr;
+  }
   auto ex = std::make_unique<GHipExecutable>();
   ex->backend = be;
-  GHipFunction* fn = bl->main.get();
   for (int p : fn->params) {
     ex->in_shapes.push_back(fn->nodes[p].shape);
     ex->in_names.push_back(fn->nodes[p].name);
+  }
+  std::vector<int> cap(fn->captures.size(), -1);
+  for (const auto& kv : fn->capture_of) cap[fn->nodes[kv.second].i0] = kv.second;
+  for (int c : cap) {
+    ex->in_shapes.push_back(fn->nodes[c].shape);
+    ex->in_names.push_back("capture");
   }
   for (int o : fn->outputs) ex->out_shapes.push_back(fn->nodes[o].shape);
   if (lower(be, fn, &ex->plan, err) != GHIP_OK) return nullptr;
@@ -59,6 +64,64 @@ extern "C" GHipExecutable* ghip_builder_compile(GHipBuilder* bl, GHipError* err)
     }
   }
   return ex.release();
+}
+
+std::shared_ptr<GHipExecutable> compile_function(GHipBackend* be, GHipFunction* fn, GHipError* err) {
+  GHipExecutable* e = compile_raw(be, fn, err);
+  if (!e) return nullptr;
+  return std::shared_ptr<GHipExecutable>(e, [](GHipExecutable* x) { ghip_exec_finalize(x); });
+}
+
+int run_plan(GHipExecutable* e, void* const* in_ptrs, void* const* out_ptrs, GHipError* err) {
+  GHipBackend* be = e->backend;
+  const Plan& plan = e->plan;
+  if (plan.arena_bytes > e->arena_cap) {
+    if (e->arena) {
+      hipStreamSynchronize(be->stream);
+      be->release(e->arena, e->arena_cap);
+      e->arena = nullptr;
+      e->arena_cap = 0;
+    }
+    if (be->alloc(plan.arena_bytes, &e->arena, err) != GHIP_OK) return err ? err->code : GHIP_ERR_OOM;
+    e->arena_cap = plan.arena_bytes;
+  }
+  ExecState st;
+  st.stream = be->stream;
+  st.slot_ptr.resize(plan.slots.size(), nullptr);
+  for (size_t s = 0; s < plan.slots.size(); ++s) {
+    const Slot& sl = plan.slots[s];
+    switch (sl.kind) {
+      case SlotKind::Input: st.slot_ptr[s] = static_cast<char*>(in_ptrs[sl.index]); break;
+      case SlotKind::Const: st.slot_ptr[s] = static_cast<char*>(sl.const_ptr); break;
+      case SlotKind::Arena: st.slot_ptr[s] = static_cast<char*>(e->arena) + sl.arena_off; break;
+      case SlotKind::Output: st.slot_ptr[s] = static_cast<char*>(out_ptrs[sl.index]); break;
+    }
+  }
+  for (const Step& step : plan.steps) {
+    const int rc = step.run(st, err);
+    if (rc != GHIP_OK) {
+      if (err && err->message) {
+        std::string m = std::string("Execute: ") + step.desc + ": " + err->message;
+        set_error(err, rc, "%s", m.c_str());
+      }
+      hipStreamSynchronize(be->stream);
+      return rc;
+    }
+  }
+  return GHIP_OK;
+}
+
+}  // namespace ghip
+
+extern "C" GHipExecutable* ghip_builder_compile(GHipBuilder* bl, GHipError* err) {
+  if (!bl) { set_error(err, GHIP_ERR_INVALID_ARG, "Compile: null builder"); return nullptr; }
+  if (bl->compiled) { set_error(err, GHIP_ERR_STATE, "Builder already compiled"); return nullptr; }
+  if (!bl->main) { set_error(err, GHIP_ERR_STATE, "Builder has no main function"); return nullptr; }
+  if (!bl->main->returned) { set_error(err, GHIP_ERR_STATE, "Main function has no Return() call"); return nullptr; }
+  GHipBackend* be = bl->backend;
+  if (!be || be->finalized) { set_error(err, GHIP_ERR_STATE, "Compile: backend finalized"); return nullptr; }
+  bl->compiled = true;
+  return compile_raw(be, bl->main.get(), err);
 }
 
 extern "C" int ghip_exec_num_inputs(GHipExecutable* e) { return e ? static_cast<int>(e->in_shapes.size()) : -1; }
@@ -113,17 +176,6 @@ extern "C" int ghip_exec_execute(GHipExecutable* e, GHipBuffer* const* inputs, i
                        e->in_shapes[i].str().c_str(), inputs[i]->shape.str().c_str());
   }
   hipSetDevice(be->device);
-  const Plan& plan = e->plan;
-  if (plan.arena_bytes > e->arena_cap) {
-    if (e->arena) {
-      hipStreamSynchronize(be->stream);
-      be->release(e->arena, e->arena_cap);
-      e->arena = nullptr;
-      e->arena_cap = 0;
-    }
-    if (be->alloc(plan.arena_bytes, &e->arena, err) != GHIP_OK) return err ? err->code : GHIP_ERR_OOM;
-    e->arena_cap = plan.arena_bytes;
-  }
   std::vector<GHipBuffer*> outs(nout, nullptr);
   auto cleanup = [&]() {
     for (auto* b : outs)
@@ -136,29 +188,13 @@ extern "C" int ghip_exec_execute(GHipExecutable* e, GHipBuffer* const* inputs, i
       return err ? err->code : GHIP_ERR_OOM;
     }
   }
-  ExecState st;
-  st.stream = be->stream;
-  st.slot_ptr.resize(plan.slots.size(), nullptr);
-  for (size_t s = 0; s < plan.slots.size(); ++s) {
-    const Slot& sl = plan.slots[s];
-    switch (sl.kind) {
-      case SlotKind::Input: st.slot_ptr[s] = static_cast<char*>(inputs[sl.index]->ptr); break;
-      case SlotKind::Const: st.slot_ptr[s] = static_cast<char*>(sl.const_ptr); break;
-      case SlotKind::Arena: st.slot_ptr[s] = static_cast<char*>(e->arena) + sl.arena_off; break;
-      case SlotKind::Output: st.slot_ptr[s] = static_cast<char*>(outs[sl.index]->ptr); break;
-    }
-  }
-  for (const Step& step : plan.steps) {
-    const int rc = step.run(st, err);
-    if (rc != GHIP_OK) {
-      if (err && err->message) {
-        std::string m = std::string("Execute: ") + step.desc + ": " + err->message;
-        set_error(err, rc, "%s", m.c_str());
-      }
-      hipStreamSynchronize(be->stream);
-      cleanup();
-      return rc;
-    }
+  std::vector<void*> in_ptrs(std::max(n, 1)), out_ptrs(std::max(nout, 1));
+  for (int i = 0; i < n; ++i) in_ptrs[i] = inputs[i]->ptr;
+  for (int i = 0; i < nout; ++i) out_ptrs[i] = outs[i]->ptr;
+  const int rc = run_plan(e, in_ptrs.data(), out_ptrs.data(), err);
+  if (rc != GHIP_OK) {
+    cleanup();
+    return rc;
   }
   for (int i = 0; i < nout; ++i) outputs[i] = outs[i];
   return GHIP_OK;

@@ -138,7 +138,7 @@ struct Lowerer {
   GHipFunction* fn;
   Plan* plan;
   GHipError* err;
-  std::vector<Node>& N;
+  std::deque<Node>& N;
   std::vector<char> live;
   std::vector<std::vector<int>> users;
   std::vector<int> cluster;  // elementwise cluster id (= root node) or -1
@@ -436,6 +436,18 @@ struct Lowerer {
     } else {
       switch (n.kind) {
         case Kind::Param: r = contig(new_slot(SlotKind::Input, n.shape.bytes(), static_cast<int>(n.i0)), n.shape); break;
+        case Kind::Capture:  // inputs after the params, in capture order
+          r = contig(new_slot(SlotKind::Input, n.shape.bytes(), static_cast<int>(fn->params.size() + n.i0)), n.shape);
+          break;
+        case Kind::TupleGet: {
+          const int cf = n.in[0];
+          if (!cf_out.count(cf)) emit_control_flow(cf);
+          if (failed) return bad();
+          r = cf_out[cf][n.i0];
+          break;
+        }
+        case Kind::Call: case Kind::While: case Kind::If: case Kind::Sort:
+          return fail(GHIP_ERR_STATE, "control-flow tuple used as a value");
         case Kind::Const: {
           r = contig(new_slot(SlotKind::Const, n.shape.bytes()), n.shape);
           const_data[r.slot] = n.data;
@@ -779,6 +791,143 @@ struct Lowerer {
                return ghip_argminmax(dt, st.ptr(x, dt), outer, len, inner, is_min, odt, st.ptr(y, odt), st.stream, e);
              });
     return y;
+  }
+
+  // ------------------------------------------------------------------ control flow
+  // Call / While / If run their compiled functions from one step, on the host,
+  // between launches on the stream (executable.go:112-577 orchestrates the same
+  // way); every value stays in device memory and a loop or branch reads back one
+  // bool per decision.  Inputs are passed as contiguous views, outputs land in
+  // fresh contiguous slots.
+  std::map<int, std::vector<View>> cf_out;  // control-flow node -> output views
+  static constexpr long kMaxWhileIterations = 1000000;  // executable.go:269
+
+  void emit_control_flow(int v) {
+    const Node n = N[v];
+    std::vector<GHipExecutable*> subs;
+    for (GHipFunction* g : n.fns) {
+      auto ex = compile_function(be, g, err);
+      if (!ex) {
+        failed = true;
+        return;
+      }
+      plan->subs.push_back(ex);
+      subs.push_back(ex.get());
+    }
+    std::vector<View> ins;
+    std::vector<int> idt, rd, wr;
+    std::vector<size_t> ibytes;
+    for (int o : n.in) {
+      View w = materialize(get(o), N[o].shape, "(control-flow input)");
+      if (failed) return;
+      ins.push_back(w);
+      idt.push_back(N[o].shape.dtype);
+      ibytes.push_back(N[o].shape.bytes());
+      rd.push_back(w.slot);
+    }
+    std::vector<View> outs;
+    std::vector<int> odt;
+    std::vector<size_t> obytes;
+    for (const Shape& s : n.outs) {
+      outs.push_back(fresh(s));
+      odt.push_back(s.dtype);
+      obytes.push_back(s.bytes());
+      wr.push_back(outs.back().slot);
+    }
+    cf_out[v] = outs;
+    auto ptrs = [](ExecState& st, const std::vector<View>& vs, const std::vector<int>& dts, size_t from, size_t to) {
+      std::vector<void*> p;
+      for (size_t i = from; i < to; ++i) p.push_back(st.ptr(vs[i], dts[i]));
+      return p;
+    };
+    // Reads one bool from device memory (the only host round trip per decision).
+    auto read_bool = [](const void* p, hipStream_t s, bool* out, GHipError* e) -> int {
+      uint8_t h = 0;
+      hipError_t he = hipMemcpyAsync(&h, p, 1, hipMemcpyDeviceToHost, s);
+      if (he == hipSuccess) he = hipStreamSynchronize(s);
+      if (he != hipSuccess) return check_hip(he, e, "control flow: reading the predicate");
+      *out = h != 0;
+      return GHIP_OK;
+    };
+    const size_t nin = ins.size();
+    if (n.kind == Kind::Call) {
+      GHipExecutable* sub = subs[0];
+      add_step(fmt("call %s (%zu inputs, %zu outputs)", n.fns[0]->name.c_str(), nin, outs.size()), rd, wr,
+               [=](ExecState& st, GHipError* e) {
+                 auto in = ptrs(st, ins, idt, 0, nin);
+                 auto out = ptrs(st, outs, odt, 0, outs.size());
+                 return run_plan(sub, in.data(), out.data(), e);
+               });
+      return;
+    }
+    if (n.kind == Kind::If) {
+      const size_t ntc = static_cast<size_t>(n.i0);
+      GHipExecutable* tb = subs[0];
+      GHipExecutable* fb = subs[1];
+      add_step(fmt("if (%zu outputs; branches run from the host after reading the predicate)", outs.size()), rd, wr,
+               [=](ExecState& st, GHipError* e) {
+                 bool pred = false;
+                 int rc = read_bool(st.ptr(ins[0], GHIP_DTYPE_BOOL), st.stream, &pred, e);
+                 if (rc != GHIP_OK) return rc;
+                 auto in = pred ? ptrs(st, ins, idt, 1, 1 + ntc) : ptrs(st, ins, idt, 1 + ntc, nin);
+                 auto out = ptrs(st, outs, odt, 0, outs.size());
+                 return run_plan(pred ? tb : fb, in.data(), out.data(), e);
+               });
+      return;
+    }
+    if (n.kind == Kind::While) {
+      const size_t ns = static_cast<size_t>(n.i0), ncc = static_cast<size_t>(n.i1);
+      std::vector<View> A, B;
+      for (size_t i = 0; i < ns; ++i) {
+        A.push_back(fresh(n.outs[i]));
+        B.push_back(fresh(n.outs[i]));
+        wr.push_back(A.back().slot);
+        wr.push_back(B.back().slot);
+      }
+      Shape bs;
+      bs.dtype = GHIP_DTYPE_BOOL;
+      View pv = fresh(bs);
+      wr.push_back(pv.slot);
+      GHipExecutable* cond = subs[0];
+      GHipExecutable* body = subs[1];
+      add_step(fmt("while (%zu state values; cond and body run from the host, one bool read per iteration)", ns), rd,
+               wr, [=](ExecState& st, GHipError* e) -> int {
+                 std::vector<void*> a = ptrs(st, A, odt, 0, ns), b = ptrs(st, B, odt, 0, ns);
+                 for (size_t i = 0; i < ns; ++i) {
+                   const hipError_t he = hipMemcpyAsync(a[i], st.ptr(ins[i], idt[i]), ibytes[i],
+                                                        hipMemcpyDeviceToDevice, st.stream);
+                   if (he != hipSuccess) return check_hip(he, e, "While: initial state");
+                 }
+                 const std::vector<void*> ccap = ptrs(st, ins, idt, ns, ns + ncc);
+                 const std::vector<void*> bcap = ptrs(st, ins, idt, ns + ncc, nin);
+                 void* pp = st.ptr(pv, GHIP_DTYPE_BOOL);
+                 for (long it = 0;; ++it) {
+                   if (it == kMaxWhileIterations)
+                     return set_error(e, GHIP_ERR_STATE, "While: exceeded maximum iterations (%ld)", kMaxWhileIterations);
+                   std::vector<void*> cin(a);
+                   cin.insert(cin.end(), ccap.begin(), ccap.end());
+                   int rc = run_plan(cond, cin.data(), &pp, e);
+                   if (rc != GHIP_OK) return rc;
+                   bool go = false;
+                   rc = read_bool(pp, st.stream, &go, e);
+                   if (rc != GHIP_OK) return rc;
+                   if (!go) break;
+                   std::vector<void*> bin(a);
+                   bin.insert(bin.end(), bcap.begin(), bcap.end());
+                   rc = run_plan(body, bin.data(), b.data(), e);
+                   if (rc != GHIP_OK) return rc;
+                   std::swap(a, b);
+                 }
+                 for (size_t i = 0; i < ns; ++i) {
+                   const hipError_t he = hipMemcpyAsync(st.ptr(outs[i], odt[i]), a[i], obytes[i],
+                                                        hipMemcpyDeviceToDevice, st.stream);
+                   if (he != hipSuccess) return check_hip(he, e, "While: final state");
+                 }
+                 return GHIP_OK;
+               });
+      return;
+    }
+    fail(GHIP_ERR_UNSUPPORTED, "control flow: unsupported operation");
   }
 
   // ------------------------------------------------------------------ DynamicSlice / UpdateSlice / Scatter

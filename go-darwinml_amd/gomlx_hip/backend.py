@@ -130,6 +130,11 @@ _GRAPH_SIGS = {
     "ghip_fn_fused_dense": ([_vp, _int, _int, _int, _int, _errp], _int),
     "ghip_fn_fused_qkv_projection": ([_vp, _int, _int, _int, _int, _int, _int, _int, _intp, _intp,
                                       _intp, _errp], _int),
+    "ghip_builder_new_function": ([_vp, ctypes.c_char_p, _errp], _vp),
+    "ghip_fn_closure": ([_vp, _errp], _vp),
+    "ghip_fn_call": ([_vp, _vp, _intp, _int, _intp, _int, _errp], _int),
+    "ghip_fn_while": ([_vp, _vp, _vp, _intp, _int, _intp, _int, _errp], _int),
+    "ghip_fn_if": ([_vp, _int, _vp, _vp, _intp, _int, _errp], _int),
     "ghip_fn_return": ([_vp, _intp, _int, _errp], _int),
     "ghip_fn_value_shape": ([_vp, _int, _intp, _i64p, _int], _int),
     "ghip_exec_num_inputs": ([_vp], _int),
@@ -330,6 +335,14 @@ class Builder:
     def OpShape(self, v: Value) -> Shape:
         return self.Main().OpShape(v)
 
+    def NewFunction(self, name: str) -> "Function":
+        """Builder.NewFunction (builder.go:57-70): a named function, the target of Call."""
+        err = GHipError(0, None)
+        h = _L().ghip_builder_new_function(self.handle, name.encode(), ctypes.byref(err))
+        if not h:
+            _raise(err)
+        return Function(self, h)
+
     def Compile(self) -> "Executable":
         err = GHipError(0, None)
         h = _L().ghip_builder_compile(self.handle, ctypes.byref(err))
@@ -486,6 +499,34 @@ class Function:
 
     def ScatterMin(self, *args, **kw) -> Value:
         return self._scatter(2, *args, **kw)
+
+    # functions and control flow
+    def Closure(self) -> "Function":
+        """Function.Closure (function.go:120-133)."""
+        err = GHipError(0, None)
+        h = _L().ghip_fn_closure(self.handle, ctypes.byref(err))
+        if not h:
+            _raise(err)
+        return Function(self.builder, h)
+
+    def _cf(self, name, *args, max_outs=64):
+        outs = (ctypes.c_int * max_outs)()
+        err = GHipError(0, None)
+        n = getattr(_L(), name)(self.handle, *args, outs, max_outs, ctypes.byref(err))
+        if n < 0:
+            _raise(err)
+        return [Value(self, outs[i]) for i in range(n)]
+
+    def Call(self, fn: "Function", *inputs):
+        a, n = _intarr([v.id for v in inputs])
+        return self._cf("ghip_fn_call", fn.handle, a, n)
+
+    def While(self, cond: "Function", body: "Function", *initial_state):
+        a, n = _intarr([v.id for v in initial_state])
+        return self._cf("ghip_fn_while", cond.handle, body.handle, a, n)
+
+    def If(self, pred, true_branch: "Function", false_branch: "Function"):
+        return self._cf("ghip_fn_if", pred.id, true_branch.handle, false_branch.handle)
 
     # fused ops
     def FusedSoftmax(self, x, axis: int) -> Value:

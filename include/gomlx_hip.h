@@ -328,6 +328,31 @@ int ghip_fn_return(GHipFunction* f, const GHipValue* outputs, int n, GHipError* 
 /* OpShape (builder.go:63-69): dtype + dims of a value; returns rank or -1. */
 int ghip_fn_value_shape(GHipFunction* f, GHipValue v, int* dtype, int64_t* dims, int max_rank);
 
+/* --- Functions and control flow (builder.go:57-70, function.go:120-133,
+ * 354-660, executable.go:112-577) ------------------------------------------
+ * Value ids are unique within a builder, so a closure may use values of the
+ * functions that enclose it: they are captured (passed to it as extra inputs
+ * after its parameters).  Call / While / If write their outputs' value ids into
+ * outs (room for max_outs) and return the number of outputs, or -1 with err set.
+ * The loops and branches run on the host, between launches of the compiled
+ * closures on the backend's stream; state stays in device memory, and each
+ * While iteration and each If read back one bool. */
+/* NewFunction (builder.go:57-70): a named function, the target of Call. */
+GHipFunction* ghip_builder_new_function(GHipBuilder* bl, const char* name, GHipError* err);
+/* Closure (function.go:120-133): a function nested in f. */
+GHipFunction* ghip_fn_closure(GHipFunction* f, GHipError* err);
+/* Call (function.go:354-405): target's outputs for these inputs. */
+int ghip_fn_call(GHipFunction* f, GHipFunction* target, const GHipValue* inputs, int n,
+                 GHipValue* outs, int max_outs, GHipError* err);
+/* While (function.go:407-493): state = init; while cond(state): state = body(state).
+ * At most 1,000,000 iterations (Execute then fails, as the reference does). */
+int ghip_fn_while(GHipFunction* f, GHipFunction* cond, GHipFunction* body, const GHipValue* init,
+                  int n, GHipValue* outs, int max_outs, GHipError* err);
+/* If (function.go:495-560): the outputs of true_branch or false_branch (closures
+ * without parameters) by the scalar bool pred. */
+int ghip_fn_if(GHipFunction* f, GHipValue pred, GHipFunction* true_branch,
+               GHipFunction* false_branch, GHipValue* outs, int max_outs, GHipError* err);
+
 /* --- Executable (executable.go:19-112) ---------------------------------- */
 int ghip_exec_num_inputs(GHipExecutable* e);
 int ghip_exec_num_outputs(GHipExecutable* e);

@@ -1,0 +1,184 @@
+"""Call / While / If and closures with captured values on the GPU, against the
+reference's known answers (mpsgraph_test.go:3376-3588: sum 1..10 = 55, 5! = 120,
+If(10 > 5) = 1, If(3 > 5) = -1, the captured 3 * 10 = 30, Call(10 + 32) = 42) and
+numpy on tensor-valued loops, nested closures and calls."""
+import numpy as np
+import pytest
+
+from gomlx_hip import synth
+from gomlx_hip.backend import Backend, BackendError, dtypes, make_shape
+from oracle import oracle as orc
+from conftest import rel_err
+
+pytestmark = pytest.mark.gpu
+
+F32, I32, BF16 = dtypes.Float32, dtypes.Int32, dtypes.BFloat16
+
+
+@pytest.fixture(scope="module")
+def be(cuda):
+    b = Backend("")
+    yield b
+    b.Finalize()
+
+
+def run(be, build, inputs):
+    b = be.Builder("cf")
+    f = b.Main()
+    params = [f.Parameter(f"p{i}", s) for i, (_, s) in enumerate(inputs)]
+    f.Return(build(b, f, *params))
+    ex = b.Compile()
+    bufs = [be.BufferFromFlatData(0, np.ascontiguousarray(a), s) for a, s in inputs]
+    outs = [be.BufferToFlatData(r).reshape(be.BufferShape(r).dims).copy() for r in ex.Execute(bufs, None, 0)]
+    plan = ex.Plan()
+    ex.Finalize()
+    return plan, outs
+
+
+def i32(v):
+    return np.array(v, np.int32)
+
+
+def test_while_sum_and_factorial(be):                            # mpsgraph_test.go:3376-3443
+    def sum_1_to_10(b, f, _):
+        cond = f.Closure()
+        counter = cond.Parameter("counter", make_shape(I32))
+        cond.Parameter("sum", make_shape(I32))
+        cond.Return([cond.LessOrEqual(counter, cond.Constant(i32(10)))])
+        body = f.Closure()
+        c, s = body.Parameter("counter", make_shape(I32)), body.Parameter("sum", make_shape(I32))
+        body.Return([body.Add(c, body.Constant(i32(1))), body.Add(s, c)])
+        return [f.While(cond, body, f.Constant(i32(1)), f.Constant(i32(0)))[1]]
+
+    def factorial(b, f, _):
+        cond = f.Closure()
+        n = cond.Parameter("n", make_shape(I32))
+        cond.Parameter("result", make_shape(I32))
+        cond.Return([cond.GreaterThan(n, cond.Constant(i32(1)))])
+        body = f.Closure()
+        n, r = body.Parameter("n", make_shape(I32)), body.Parameter("result", make_shape(I32))
+        body.Return([body.Sub(n, body.Constant(i32(1))), body.Mul(r, n)])
+        return [f.While(cond, body, f.Constant(i32(5)), f.Constant(i32(1)))[1]]
+
+    plan, (y,) = run(be, sum_1_to_10, [(i32(0), make_shape(I32))])
+    assert int(y) == 55 and "while" in plan
+    _, (y,) = run(be, factorial, [(i32(0), make_shape(I32))])
+    assert int(y) == 120
+
+
+@pytest.mark.parametrize("x, want", [(10.0, 1.0), (3.0, -1.0)])
+def test_if_branches(be, x, want):                                # mpsgraph_test.go:3446-3490
+    def build(b, f, xx):
+        pred = f.GreaterThan(xx, f.Constant(np.array(5, np.float32)))
+        t = f.Closure()
+        t.Return([t.Constant(np.array(1, np.float32))])
+        e = f.Closure()
+        e.Return([e.Constant(np.array(-1, np.float32))])
+        return f.If(pred, t, e)
+    _, (y,) = run(be, build, [(np.array(x, np.float32), make_shape(F32))])
+    assert float(y) == want
+
+
+@pytest.mark.parametrize("x", [3.0, -2.0])
+def test_if_with_captured_values(be, x):                          # mpsgraph_test.go:3492-3523
+    def build(b, f, xx):
+        factor = f.Constant(np.array(10, np.float32))
+        pred = f.GreaterThan(xx, f.Constant(np.array(0, np.float32)))
+        t = f.Closure()
+        t.Return([t.Mul(xx, factor)])
+        e = f.Closure()
+        e.Return([e.Neg(e.Mul(xx, factor))])
+        return f.If(pred, t, e)
+    _, (y,) = run(be, build, [(np.array(x, np.float32), make_shape(F32))])
+    assert float(y) == (30.0 if x > 0 else -(x * 10))
+
+
+def test_call_named_function(be):                                 # mpsgraph_test.go:3553-3588
+    def build(b, f, _):
+        add = b.NewFunction("add")
+        a, c = add.Parameter("a", make_shape(F32)), add.Parameter("b", make_shape(F32))
+        add.Return([add.Add(a, c)])
+        return f.Call(add, f.Constant(np.array(10, np.float32)), f.Constant(np.array(32, np.float32)))
+    _, (y,) = run(be, build, [(np.array(0, np.float32), make_shape(F32))])
+    assert float(y) == 42.0
+
+
+def test_while_tensor_state_with_captures(be):
+    """A loop over tensors: x <- W x / ||W x||_inf ... run k times (power iteration with
+    a captured matrix and iteration count), against numpy with the same fp32 steps."""
+    rng = np.random.default_rng(3)
+    n, k = 96, 7
+    W = rng.standard_normal((n, n)).astype(np.float32)
+    x0 = rng.standard_normal((n, 1)).astype(np.float32)
+
+    def build(b, f, w, x, kk):
+        cond = f.Closure()
+        i = cond.Parameter("i", make_shape(I32))
+        cond.Parameter("x", make_shape(F32, n, 1))
+        cond.Return([cond.LessThan(i, kk)])                      # captures kk
+        body = f.Closure()
+        i = body.Parameter("i", make_shape(I32))
+        xv = body.Parameter("x", make_shape(F32, n, 1))
+        y = body.DotGeneral(w, [1], [], xv, [0], [])            # captures W
+        m = body.ReduceMax(body.Abs(y), 0, 1)
+        body.Return([body.Add(i, body.Constant(i32(1))), body.Div(y, body.BroadcastInDim(m, make_shape(F32, n, 1), []))])
+        out = f.While(cond, body, f.Constant(i32(0)), x)
+        return [out[0], out[1]]
+
+    plan, (it, xk) = run(be, build, [(W, make_shape(F32, n, n)), (x0, make_shape(F32, n, 1)), (i32(k), make_shape(I32))])
+    assert int(it) == k
+    want = x0.astype(np.float64)
+    for _ in range(k):
+        y = W.astype(np.float64) @ want
+        want = y / np.max(np.abs(y))
+    assert rel_err(xk, want) <= 1e-4
+
+
+def test_nested_closures_and_calls(be):
+    """If inside a While body, a Call inside the If branch, and a value captured from
+    the main function two levels up (the closures in between capture it too)."""
+    def build(b, f, x, lim):
+        scale = b.NewFunction("scale")
+        a, s = scale.Parameter("a", make_shape(F32, 4)), scale.Parameter("s", make_shape(F32))
+        scale.Return([scale.Mul(a, scale.BroadcastInDim(s, make_shape(F32, 4), []))])
+        two = f.Constant(np.array(2, np.float32))
+        cond = f.Closure()
+        v = cond.Parameter("v", make_shape(F32, 4))
+        cond.Return([cond.LessThan(cond.ReduceSum(v, 0), lim)])      # captures lim
+        body = f.Closure()
+        v = body.Parameter("v", make_shape(F32, 4))
+        big = body.GreaterThan(body.ReduceMax(v, 0), body.Constant(np.array(3, np.float32)))
+        t = body.Closure()
+        t.Return(t.Call(scale, v, two))                              # captures v (body) and two (main)
+        e = body.Closure()
+        e.Return([e.Add(v, e.Constant(np.ones(4, np.float32), 4))])
+        body.Return(body.If(big, t, e))
+        return f.While(cond, body, x)
+
+    x0 = np.array([0.5, -1.0, 0.25, 1.0], np.float32)
+    _, (y,) = run(be, build, [(x0, make_shape(F32, 4)), (np.array(100, np.float32), make_shape(F32))])
+    want = x0.copy()
+    while want.sum() < 100:
+        want = want * 2 if want.max() > 3 else want + 1
+    assert np.array_equal(y, want)
+
+
+def test_control_flow_errors(be):
+    b = be.Builder("err")
+    f = b.Main()
+    x = f.Parameter("x", make_shape(F32, 3))
+    cond = f.Closure()
+    cond.Parameter("v", make_shape(F32, 3))
+    cond.Return([cond.Constant(np.array(1.0, np.float32))])
+    body = f.Closure()
+    v = body.Parameter("v", make_shape(F32, 3))
+    body.Return([v])
+    with pytest.raises(BackendError, match="cond must return scalar bool"):
+        f.While(cond, body, x)
+    unreturned = f.Closure()
+    with pytest.raises(BackendError, match="must have Return"):
+        f.If(f.Constant(np.array(True)), unreturned, unreturned)
+    other = be.Builder("other").Main()
+    with pytest.raises(BackendError, match="does not belong|does not enclose"):
+        other.Add(x, x)
+    b.Finalize()

@@ -242,3 +242,35 @@ def test_dynamic_slice_and_scatter_shapes_and_errors(be):
         f.ScatterMin(x, ids, upd, 1, [1], [0], [0, 1])
     with pytest.raises(BackendError, match="window size 9 exceeds"):
         f.ScatterSum(x, ids, f.Parameter("upd3", make_shape(F32, 7, 9)), 1, [1], [0], [0])
+
+
+def test_control_flow_plans_and_errors(be):
+    b = be.Builder("cf")
+    f = b.Main()
+    x = f.Parameter("x", make_shape(F32, 3))
+    n = f.Parameter("n", make_shape(dtypes.Int32))
+    cond = f.Closure()
+    i = cond.Parameter("i", make_shape(dtypes.Int32))
+    cond.Parameter("v", make_shape(F32, 3))
+    cond.Return([cond.LessThan(i, n)])                  # n captured from main
+    body = f.Closure()
+    i = body.Parameter("i", make_shape(dtypes.Int32))
+    v = body.Parameter("v", make_shape(F32, 3))
+    body.Return([body.Add(i, body.Constant(np.array(1, np.int32))), body.Mul(v, x)])   # x captured
+    outs = f.While(cond, body, f.Constant(np.array(0, np.int32)), x)
+    assert [f.OpShape(o) for o in outs] == [make_shape(dtypes.Int32), make_shape(F32, 3)]
+    with pytest.raises(BackendError, match="body must have 1 parameters|cond must have 1 parameters"):
+        f.While(cond, body, x)
+    with pytest.raises(BackendError, match="pred must be scalar bool"):
+        f.If(x, cond, body)
+    callee = b.NewFunction("callee")
+    a = callee.Parameter("a", make_shape(F32, 3))
+    callee.Return([callee.Neg(a)])
+    with pytest.raises(BackendError, match="expects 1 parameters, got 2"):
+        f.Call(callee, x, x)
+    with pytest.raises(BackendError, match="parameter 0 shape mismatch"):
+        f.Call(callee, n)
+    (neg,) = f.Call(callee, outs[1])
+    f.Return([neg])
+    plan = b.Compile().Plan()
+    assert "while (2 state values" in plan and "call callee" in plan, plan
