@@ -1158,6 +1158,46 @@ extern "C" int ghip_fn_if(GHipFunction* f, GHipValue pred, GHipFunction* true_br
   return emit_cf(c, std::move(node), outs, max_outs);
 }
 
+extern "C" int ghip_fn_sort(GHipFunction* f, GHipFunction* comparator, int axis, int is_stable,
+                            const GHipValue* inputs, int n, GHipValue* outs, int max_outs, GHipError* err) {
+  FN_BEGIN("Sort");
+  if (n <= 0) return c.fail(GHIP_ERR_INVALID_ARG, "requires at least one input tensor");
+  Node node{Kind::Sort};
+  const Node* first = nullptr;
+  for (int i = 0; i < n; ++i) {
+    const Node* a = c.node(inputs[i]);
+    if (!a) return -1;
+    if (!first) first = a;
+    if (a->shape.dims != first->shape.dims) return c.fail(GHIP_ERR_INVALID_ARG, "all inputs must have same dimensions");
+    node.in.push_back(inputs[i]);
+    node.outs.push_back(a->shape);
+  }
+  const int rank = first->shape.rank();
+  if (axis < 0) axis += rank;
+  if (axis < 0 || axis >= rank) return c.fail(GHIP_ERR_INVALID_ARG, "axis %d out of range for rank %d", axis, rank);
+  if (!check_closure(c, f, comparator, "comparator")) return -1;
+  if (static_cast<int>(comparator->params.size()) != 2 * n)
+    return c.fail(GHIP_ERR_INVALID_ARG, "comparator must have %d parameters, got %zu", 2 * n, comparator->params.size());
+  for (int i = 0; i < 2 * n; ++i) {
+    const Shape& ps = comparator->nodes[comparator->params[i]].shape;
+    if (ps.rank() != 0) return c.fail(GHIP_ERR_INVALID_ARG, "comparator parameter %d must be scalar, got %s", i, ps.str().c_str());
+    if (ps.dtype != node.outs[i / 2].dtype)
+      return c.fail(GHIP_ERR_INVALID_ARG, "comparator parameter %d dtype %s must match input dtype %s", i,
+                    dtype_name(ps.dtype), dtype_name(node.outs[i / 2].dtype));
+  }
+  if (comparator->outputs.size() != 1)
+    return c.fail(GHIP_ERR_INVALID_ARG, "comparator must return exactly one value, got %zu", comparator->outputs.size());
+  const Shape& rs = comparator->nodes[comparator->outputs[0]].shape;
+  if (rs.rank() != 0 || rs.dtype != GHIP_DTYPE_BOOL)
+    return c.fail(GHIP_ERR_INVALID_ARG, "comparator must return scalar bool, got %s", rs.str().c_str());
+  add_captures(node, comparator, f);
+  node.fns = {comparator};
+  node.i0 = axis;
+  node.i1 = is_stable ? 1 : 0;
+  node.i2 = n;
+  return emit_cf(c, std::move(node), outs, max_outs);
+}
+
 // ===========================================================================
 // DynamicSlice / DynamicUpdateSlice (function.go:1571-1621) and ScatterSum /
 // ScatterMax / ScatterMin (gather.go:441-640).

@@ -802,8 +802,166 @@ struct Lowerer {
   std::map<int, std::vector<View>> cf_out;  // control-flow node -> output views
   static constexpr long kMaxWhileIterations = 1000000;  // executable.go:269
 
+  // Comparator / scalar closure as device code: statements and the result
+  // expression, its params named p<i>, its captures c<i>.  False when it holds
+  // anything but scalar elementwise ops and constants.
+  bool scalar_fn_source(std::string* body, std::string* result) {
+    std::vector<char> lv(N.size(), 0);
+    std::vector<int> stack(fn->outputs.begin(), fn->outputs.end());
+    while (!stack.empty()) {
+      const int u = stack.back();
+      stack.pop_back();
+      if (u < 0 || lv[u]) continue;
+      lv[u] = 1;
+      for (int o : N[u].in) stack.push_back(o);
+    }
+    std::map<int, std::string> expr;
+    std::ostringstream b;
+    for (int u = 0; u < static_cast<int>(N.size()); ++u) {
+      if (!lv[u]) continue;
+      const Node& n = N[u];
+      if (n.shape.rank() != 0) return false;
+      switch (n.kind) {
+        case Kind::Param: expr[u] = "p" + std::to_string(n.i0); break;
+        case Kind::Capture: expr[u] = "c" + std::to_string(n.i0); break;
+        case Kind::Const: expr[u] = literal(n.shape.dtype, const_as_double(n, 0)); break;
+        case Kind::Reshape: case Kind::Broadcast: expr[u] = expr[n.in[0]]; break;
+        default:
+          if (!is_elementwise(n.kind)) return false;
+          b << member_stmt(u, expr, "t" + std::to_string(u));
+      }
+    }
+    *body = b.str();
+    *result = expr[fn->outputs[0]];
+    return true;
+  }
+
+  // Sort: one workgroup per row along the axis; the row's keys in LDS, a bitonic
+  // network over an index array ordered by the comparator, ties by index (so the
+  // order is total and the sort stable).
+  void emit_sort(int v) {
+    const Node n = N[v];
+    GHipFunction* cf = n.fns[0];
+    const int nin = static_cast<int>(n.i2), axis = static_cast<int>(n.i0);
+    const Shape s0 = n.outs[0];
+    int64_t outer = 1, inner = 1;
+    for (int d = 0; d < axis; ++d) outer *= s0.dims[d];
+    for (int d = axis + 1; d < s0.rank(); ++d) inner *= s0.dims[d];
+    const int64_t L = s0.dims[axis];
+    Plan cplan;
+    Lowerer C(be, cf, &cplan, err);
+    std::string cbody, cres;
+    if (!C.scalar_fn_source(&cbody, &cres)) {
+      fail(GHIP_ERR_UNSUPPORTED, "Sort: the comparator may only use scalar elementwise ops, constants and captured scalars");
+      return;
+    }
+    for (size_t k = nin; k < n.in.size(); ++k)
+      if (N[n.in[k]].shape.rank() != 0) {
+        fail(GHIP_ERR_UNSUPPORTED, "Sort: the comparator may only capture scalars");
+        return;
+      }
+    int64_t P = 2;
+    while (P < L) P <<= 1;
+    int64_t lds = P * 4;
+    for (int i = 0; i < nin; ++i) lds += L * dtype_size(n.outs[i].dtype);
+    if (lds > 150 * 1024) {
+      fail(GHIP_ERR_UNSUPPORTED, "Sort: a row along the sort axis does not fit in one workgroup's LDS");
+      return;
+    }
+    const int NT = static_cast<int>(std::min<int64_t>(1024, std::max<int64_t>(64, P / 2)));
+    std::ostringstream src;
+    src << kRtcPrelude << "extern \"C\" __global__ void __launch_bounds__(" << NT << ") sort_rows(\n";
+    for (int i = 0; i < nin; ++i) src << "    const void* __restrict__ in" << i << ",\n";
+    for (int i = 0; i < nin; ++i) src << "    void* __restrict__ out" << i << ",\n";
+    for (size_t k = nin; k < n.in.size(); ++k) src << "    const void* __restrict__ cap" << (k - nin) << ",\n";
+    src << "    long long inner) {\n";
+    for (int i = 0; i < nin; ++i) src << "  __shared__ " << stype(n.outs[i].dtype) << " k" << i << "[" << L << "];\n";
+    src << "  __shared__ int ix[" << P << "];\n"
+        << "  const long long row = blockIdx.x, o = row / inner, j = row % inner;\n"
+        << "  const long long base = o * " << L << "LL * inner + j;\n"
+        << "  for (int k = threadIdx.x; k < " << L << "; k += " << NT << ") {\n";
+    for (int i = 0; i < nin; ++i)
+      src << "    k" << i << "[k] = ((const " << stype(n.outs[i].dtype) << "*)in" << i << ")[base + k * inner];\n";
+    src << "  }\n  for (int k = threadIdx.x; k < " << P << "; k += " << NT << ") ix[k] = k;\n";
+    for (size_t k = nin; k < n.in.size(); ++k) {
+      const int dt = N[n.in[k]].shape.dtype;
+      src << "  const " << ctype(dt) << " c" << (k - nin) << " = "
+          << load_expr(dt, "((const " + stype(dt) + "*)cap" + std::to_string(k - nin) + ")[0]") << ";\n";
+    }
+    src << "  __syncthreads();\n"
+        << "  auto cmp = [&](int a, int b) -> bool {\n";
+    for (int i = 0; i < nin; ++i) {
+      const int dt = n.outs[i].dtype;
+      src << "    const " << ctype(dt) << " p" << 2 * i << " = " << load_expr(dt, "k" + std::to_string(i) + "[a]") << ";\n"
+          << "    const " << ctype(dt) << " p" << 2 * i + 1 << " = " << load_expr(dt, "k" + std::to_string(i) + "[b]") << ";\n";
+    }
+    src << cbody << "    return " << cres << ";\n  };\n"
+        << "  auto lt = [&](int a, int b) -> bool {\n"
+        << "    if (a >= " << L << ") return false;\n    if (b >= " << L << ") return true;\n"
+        << "    if (cmp(a, b)) return true;\n    if (cmp(b, a)) return false;\n    return a < b;\n  };\n"
+        << "  for (int k = 2; k <= " << P << "; k <<= 1)\n"
+        << "    for (int jj = k >> 1; jj > 0; jj >>= 1) {\n"
+        << "      for (int t = threadIdx.x; t < " << P / 2 << "; t += " << NT << ") {\n"
+        << "        const int a = ((t & ~(jj - 1)) << 1) | (t & (jj - 1)), b = a + jj;\n"
+        << "        const int xa = ix[a], xb = ix[b];\n"
+        << "        if ((a & k) == 0 ? lt(xb, xa) : lt(xa, xb)) { ix[a] = xb; ix[b] = xa; }\n"
+        << "      }\n      __syncthreads();\n    }\n"
+        << "  for (int k = threadIdx.x; k < " << L << "; k += " << NT << ") {\n    const int s = ix[k];\n";
+    for (int i = 0; i < nin; ++i)
+      src << "    ((" << stype(n.outs[i].dtype) << "*)out" << i << ")[base + k * inner] = k" << i << "[s];\n";
+    src << "  }\n}\n";
+    RtcKernel kern;
+    if (rtc_get(be, src.str(), "sort_rows", &kern, err) != GHIP_OK) {
+      failed = true;
+      return;
+    }
+    std::vector<View> ins, outs;
+    std::vector<int> idt, odt, rd, wr;
+    for (int o : n.in) {
+      View w = materialize(get(o), N[o].shape, "(Sort input)");
+      if (failed) return;
+      ins.push_back(w);
+      idt.push_back(N[o].shape.dtype);
+      rd.push_back(w.slot);
+    }
+    for (const Shape& sh : n.outs) {
+      outs.push_back(fresh(sh));
+      odt.push_back(sh.dtype);
+      wr.push_back(outs.back().slot);
+    }
+    cf_out[v] = outs;
+    const int64_t rows = outer * inner;
+    add_step(fmt("sort_rows %s axis=%d inputs=%d (comparator compiled in; bitonic in LDS, stable)", s0.str().c_str(), axis,
+                 nin),
+             rd, wr, [=](ExecState& st, GHipError* e) -> int {
+               if (rows == 0 || L == 0) return GHIP_OK;
+               std::vector<void*> ptr;
+               for (int i = 0; i < nin; ++i) ptr.push_back(st.ptr(ins[i], idt[i]));
+               for (int i = 0; i < nin; ++i) ptr.push_back(st.ptr(outs[i], odt[i]));
+               for (size_t k = nin; k < ins.size(); ++k) ptr.push_back(st.ptr(ins[k], idt[k]));
+               long long in_ = inner;
+               std::vector<void*> args;
+               for (auto& p : ptr) args.push_back(&p);
+               args.push_back(&in_);
+               int64_t done = 0;
+               while (done < rows) {  // grid x <= 2^31 - 1 per launch
+                 const int64_t g = std::min<int64_t>(rows - done, 1 << 30);
+                 if (done) return set_error(e, GHIP_ERR_UNSUPPORTED, "Sort: more than 2^30 rows");
+                 const hipError_t h = hipModuleLaunchKernel(kern.func, static_cast<unsigned>(g), 1, 1, NT, 1, 1, 0,
+                                                            st.stream, args.data(), nullptr);
+                 if (h != hipSuccess) return check_hip(h, e, "sort launch");
+                 done += g;
+               }
+               return GHIP_OK;
+             });
+  }
+
   void emit_control_flow(int v) {
     const Node n = N[v];
+    if (n.kind == Kind::Sort) {
+      emit_sort(v);
+      return;
+    }
     std::vector<GHipExecutable*> subs;
     for (GHipFunction* g : n.fns) {
       auto ex = compile_function(be, g, err);

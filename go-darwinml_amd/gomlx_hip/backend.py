@@ -135,6 +135,7 @@ _GRAPH_SIGS = {
     "ghip_fn_call": ([_vp, _vp, _intp, _int, _intp, _int, _errp], _int),
     "ghip_fn_while": ([_vp, _vp, _vp, _intp, _int, _intp, _int, _errp], _int),
     "ghip_fn_if": ([_vp, _int, _vp, _vp, _intp, _int, _errp], _int),
+    "ghip_fn_sort": ([_vp, _vp, _int, _int, _intp, _int, _intp, _int, _errp], _int),
     "ghip_fn_return": ([_vp, _intp, _int, _errp], _int),
     "ghip_fn_value_shape": ([_vp, _int, _intp, _i64p, _int], _int),
     "ghip_exec_num_inputs": ([_vp], _int),
@@ -527,6 +528,10 @@ class Function:
 
     def If(self, pred, true_branch: "Function", false_branch: "Function"):
         return self._cf("ghip_fn_if", pred.id, true_branch.handle, false_branch.handle)
+
+    def Sort(self, comparator: "Function", axis: int, is_stable: bool, *inputs):
+        a, n = _intarr([v.id for v in inputs])
+        return self._cf("ghip_fn_sort", comparator.handle, int(axis), int(is_stable), a, n)
 
     # fused ops
     def FusedSoftmax(self, x, axis: int) -> Value:

@@ -353,6 +353,16 @@ int ghip_fn_while(GHipFunction* f, GHipFunction* cond, GHipFunction* body, const
 int ghip_fn_if(GHipFunction* f, GHipValue pred, GHipFunction* true_branch,
                GHipFunction* false_branch, GHipValue* outs, int max_outs, GHipError* err);
 
+/* Sort (function.go:562-655): the n inputs (same dims) reordered along `axis` so
+ * that comparator (a closure of 2n scalar parameters lhs_0, rhs_0, lhs_1, rhs_1,
+ * ..., returning a scalar bool "lhs before rhs") holds; ties keep their input
+ * order (every sort is stable).  The comparator is compiled into the sort kernel:
+ * it may use elementwise ops, scalar constants and captured scalars.  Each row
+ * along the axis is sorted in one workgroup's LDS; rows that do not fit (about
+ * 16K elements for one 4-byte key) return GHIP_ERR_UNSUPPORTED at Compile. */
+int ghip_fn_sort(GHipFunction* f, GHipFunction* comparator, int axis, int is_stable,
+                 const GHipValue* inputs, int n, GHipValue* outs, int max_outs, GHipError* err);
+
 /* --- Executable (executable.go:19-112) ---------------------------------- */
 int ghip_exec_num_inputs(GHipExecutable* e);
 int ghip_exec_num_outputs(GHipExecutable* e);

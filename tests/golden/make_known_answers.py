@@ -113,6 +113,11 @@ CASES = {
         "scatter_axes_to_operand_axes": [0],
         "expected": [6, 8, 0, 0, 3, 4, 0, 0],
     },
+    "sort": {
+        "source": "mpsgraph_test.go:3526-3551 (TestSort)",
+        "x": [5, 2, 8, 1, 9, 3],
+        "ascending": [1, 2, 3, 5, 8, 9], "descending": [9, 8, 5, 3, 2, 1],
+    },
     "gelu": {
         "source": "mpsgraph_test.go:2645-2656 (TestFusedGelu)",
         "x": [0.0, 1.0, -1.0, 3.0], "tol": 1e-3,

@@ -182,3 +182,78 @@ def test_control_flow_errors(be):
     with pytest.raises(BackendError, match="does not belong|does not enclose"):
         other.Add(x, x)
     b.Finalize()
+
+
+# ------------------------------------------------------------ Sort
+def _comparator(f, dtypes_, rule):
+    """A comparator closure over len(dtypes_) inputs: rule(c, params) -> bool value."""
+    c = f.Closure()
+    ps = []
+    for i, dt in enumerate(dtypes_):
+        ps.append(c.Parameter(f"lhs{i}", make_shape(dt)))
+        ps.append(c.Parameter(f"rhs{i}", make_shape(dt)))
+    c.Return([rule(c, ps)])
+    return c
+
+
+@pytest.mark.parametrize("ascending", [True, False])
+def test_sort_known_answers(be, known, ascending):                 # mpsgraph_test.go:3526-3551
+    c = known["sort"]
+
+    def build(b, f, x):
+        rule = (lambda k, p: k.LessThan(p[0], p[1])) if ascending else (lambda k, p: k.GreaterThan(p[0], p[1]))
+        return f.Sort(_comparator(f, [F32], rule), 0, True, x)
+    plan, (y,) = run(be, build, [(np.array(c["x"], np.float32), make_shape(F32, 6))])
+    assert "sort_rows" in plan
+    assert y.tolist() == c["ascending" if ascending else "descending"]
+
+
+def test_sort_payload_axis_and_stability(be):
+    """Keys with many ties plus an int32 payload, sorted along the middle axis of
+    [3, 700, 5] (rows strided by 5): equals numpy's stable argsort applied to both."""
+    rng = np.random.default_rng(2)
+    keys = rng.integers(0, 20, (3, 700, 5)).astype(np.float32)
+    payload = np.broadcast_to(np.arange(700, dtype=np.int32)[None, :, None], (3, 700, 5)).copy()
+
+    def build(b, f, k, p):
+        return f.Sort(_comparator(f, [F32, I32], lambda c, q: c.LessThan(q[0], q[1])), 1, True, k, p)
+    _, (ks, ps) = run(be, build, [(keys, make_shape(F32, 3, 700, 5)), (payload, make_shape(I32, 3, 700, 5))])
+    order = np.argsort(keys, axis=1, kind="stable")
+    assert np.array_equal(ks, np.take_along_axis(keys, order, 1))
+    assert np.array_equal(ps, np.take_along_axis(payload, order, 1))
+
+
+def test_sort_bf16_lexicographic_with_captured_scalar(be):
+    """Two keys compared lexicographically (by |a - c|, c captured from the main
+    function, then by b descending), bf16 and int32, rows of 4096 along the last axis."""
+    rng = np.random.default_rng(4)
+    a = synth.round_bf16(rng.standard_normal((2, 4096)).astype(np.float32))
+    bk = rng.integers(0, 8, (2, 4096)).astype(np.int32)
+    center = np.array(0.25, np.float32)
+
+    def build(b, f, aa, bb, cc):
+        def rule(c, q):
+            da, db = c.Abs(c.Sub(q[0], c.ConvertDType(cc, BF16))), c.Abs(c.Sub(q[1], c.ConvertDType(cc, BF16)))
+            first = c.LessThan(da, db)
+            tie = c.Equal(da, db)
+            return c.LogicalOr(first, c.LogicalAnd(tie, c.GreaterThan(q[2], q[3])))
+        return f.Sort(_comparator(f, [BF16, I32], rule), -1, True, aa, bb)
+    _, (ya, yb) = run(be, build, [(synth.to_bf16_bits(a), make_shape(BF16, 2, 4096)), (bk, make_shape(I32, 2, 4096)),
+                                  (center, make_shape(F32))])
+    d = np.abs(synth.round_bf16(a - synth.round_bf16(center)))
+    for r in range(2):
+        order = np.lexsort((np.arange(4096), -bk[r], d[r]))     # primary |a-c|, then b desc, then index
+        assert np.array_equal(synth.bf16_bits_to_f32(ya[r]), a[r][order])
+        assert np.array_equal(yb[r], bk[r][order])
+
+
+def test_sort_errors(be):
+    b = be.Builder("se")
+    f = b.Main()
+    x = f.Parameter("x", make_shape(F32, 8))
+    cmp = _comparator(f, [F32], lambda c, p: c.LessThan(p[0], p[1]))
+    with pytest.raises(BackendError, match="comparator must have 4 parameters"):
+        f.Sort(cmp, 0, True, x, x)
+    with pytest.raises(BackendError, match="axis 1 out of range"):
+        f.Sort(cmp, 1, True, x)
+    b.Finalize()
