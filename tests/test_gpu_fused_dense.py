@@ -203,3 +203,53 @@ def test_qkv_views_feed_fused_attention(be):
     assert got.shape == (B, S, H, D)
     assert np.linalg.norm(got - ref) / np.linalg.norm(ref) <= 1e-2
     assert rel_err(got, ref) <= 2.5e-2
+
+
+@pytest.mark.parametrize("op", ["Exp", "Logistic", "Tanh"])
+def test_bf16_transcendentals_every_input(be, op):
+    """The bf16 forms of exp / logistic / tanh (hardware exp2 and reciprocal) over all
+    65536 bf16 inputs: within one bf16 rounding of the exactly rounded fp64 value
+    (relative 2^-8; results below the smallest normal, 2^-126, may flush to zero as
+    the hardware exp2 does), NaN for NaN, and exact for the saturated values."""
+    bits = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    with np.errstate(invalid="ignore"):
+        x = synth.bf16_bits_to_f32(bits).astype(np.float64)
+    _, (y,) = run(be, lambda f, v: [getattr(f, op)(v)], [(bits, make_shape(BF16, 65536))])
+    got = synth.bf16_bits_to_f32(y[1]).astype(np.float64)
+    with np.errstate(over="ignore", invalid="ignore"):
+        ref = {"Exp": np.exp(x), "Logistic": 1.0 / (1.0 + np.exp(-x)), "Tanh": np.tanh(x)}[op]
+    nan = np.isnan(x)
+    assert np.all(np.isnan(got[nan]))
+    ok = ~nan
+    r, g = ref[ok], got[ok]
+    fin = np.isfinite(r) & (np.abs(r) < 3.3e38)
+    # beyond the largest bf16 / fp32 value the result is the signed infinity
+    assert np.all(g[~fin] == np.where(np.isinf(r[~fin]), r[~fin], np.copysign(np.inf, r[~fin])))
+    err = np.abs(g[fin] - r[fin])
+    bad = err > np.maximum(np.abs(r[fin]) * 2.0 ** -8, 2.0 ** -126)
+    assert not np.any(bad), (x[ok][fin][bad][:8], g[fin][bad][:8], r[fin][bad][:8])
+    # exactly rounded in the vast majority of cases
+    exact = np.mean(synth.round_bf16(r[fin].astype(np.float32)) == g[fin])
+    assert exact > 0.97, exact
+
+
+def test_fused_dense_gelu_full_ffn_shape(be):
+    """The FFN shape of configs[4] (8192 x 2048 . 2048 x 8192): fused == unfused bit for
+    bit, and 4096 sampled outputs against the fp64 oracle."""
+    rng = np.random.default_rng(61)
+    x = _bf16_input((8, 1024, 2048), 1.0, 61)
+    w = _bf16_input((2048, 8192), 2048 ** -0.5, 62)
+    bias = _bf16_input((8192,), 0.1, 63)
+    ins = [(synth.to_bf16_bits(x), make_shape(BF16, 8, 1024, 2048)),
+           (synth.to_bf16_bits(w), make_shape(BF16, 2048, 8192)),
+           (synth.to_bf16_bits(bias), make_shape(BF16, 8192))]
+    build = lambda f, xx, ww, bb: [f.FusedDense(xx, ww, bb, ActivationType.GELU)]
+    _, (y,) = run(be, build, ins)
+    _, (y0,) = run(be, build, ins, fuse=False)
+    assert np.array_equal(y[1], y0[1])
+    ms, ns = rng.integers(0, 8192, 4096), rng.integers(0, 8192, 4096)
+    prod = orc.dot_sampled(x.reshape(1, 8192, 2048), w.reshape(1, 2048, 8192), np.zeros(4096, np.int64), ms, ns)
+    # the product rounds to bf16 first (the graph's DotGeneral output dtype), then bias + GELU
+    ref = orc.gelu(synth.round_bf16(prod.astype(np.float32)).astype(np.float64) + bias[ns], False)
+    got = as_f(y).reshape(8192, 8192)[ms, ns]
+    assert rel_err(got, ref) <= 3e-2
