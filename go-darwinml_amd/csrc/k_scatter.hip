@@ -13,6 +13,7 @@
 // many bf16 updates is rounded once instead of once per update.
 #include <hip/hip_runtime.h>
 
+#include <atomic>
 #include <type_traits>
 
 #include "common.h"
@@ -531,13 +532,13 @@ int launch_scatter_rows(int dtype, const void* updates, int64_t upd_row, const v
     if (table_bytes % 16 || reinterpret_cast<uintptr_t>(copy_src) % 16 || reinterpret_cast<uintptr_t>(out) % 16)
       return set_error(err, GHIP_ERR_INVALID_ARG, "row scatter: table copy needs 16-byte alignment");
     // One workgroup per CU (each holds the sort's LDS): the sort on one, the copy on the rest.
-    static int cus_of[64] = {0};
+    static std::atomic<int> cus_of[64];  // per device; 0 = not queried yet
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
-    int cus = cus_of[dev];
+    int cus = cus_of[dev].load(std::memory_order_relaxed);
     if (cus == 0) {
       if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < 2) cus = 256;
-      cus_of[dev] = cus;
+      cus_of[dev].store(cus, std::memory_order_relaxed);
     }
     hipLaunchKernelGGL(row_sort_copy_kernel, dim3(cus), dim3(kSortThreads), 0, s, sa, static_cast<const uint4*>(copy_src),
                        static_cast<uint4*>(out), table_bytes / 16);
