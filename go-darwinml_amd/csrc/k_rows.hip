@@ -183,13 +183,21 @@ __global__ __launch_bounds__(256) void rows_reg_kernel(RowParams p) {
       for (int j = 0; j < VEC; ++j) mx = fmaxf(mx, f[j]);
     }
     mx = row_reduce_max<WPR>(mx, lds, 0);
+    // fp32 softmax keeps each exp in the register its input came from (a
+    // vector holds 4 fp32 either way), so the store pass only scales.
+    constexpr bool kKeepExp = OP != kLogSoftmax && Elem<T>::kVec == 4;
     float s = 0.f;
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
       float f[VEC];
       val(i, f);
 #pragma unroll
-      for (int j = 0; j < VEC; ++j) s += fast_exp(f[j] - mx);
+      for (int j = 0; j < VEC; ++j) {
+        f[j] = fast_exp(f[j] - mx);
+        s += f[j];
+      }
+      if constexpr (kKeepExp) v[i] = make_uint4(__float_as_uint(f[0]), __float_as_uint(f[1]), __float_as_uint(f[2]),
+                                               __float_as_uint(f[3]));
     }
     s = row_reduce_sum<WPR>(s, lds, 1);
     const float shift = mx + logf(s);
@@ -199,10 +207,17 @@ __global__ __launch_bounds__(256) void rows_reg_kernel(RowParams p) {
       if (!live[i]) continue;
       const int64_t c0 = (static_cast<int64_t>(i) * LANES + l) * VEC;
       float f[VEC];
-      val(i, f);
+      if constexpr (kKeepExp) {
+        f[0] = __uint_as_float(v[i].x) * inv;
+        f[1] = __uint_as_float(v[i].y) * inv;
+        f[2] = __uint_as_float(v[i].z) * inv;
+        f[3] = __uint_as_float(v[i].w) * inv;
+      } else {
+        val(i, f);
 #pragma unroll
-      for (int j = 0; j < VEC; ++j)
-        f[j] = (OP == kLogSoftmax) ? f[j] - shift : fast_exp(f[j] - mx) * inv;
+        for (int j = 0; j < VEC; ++j)
+          f[j] = (OP == kLogSoftmax) ? f[j] - shift : fast_exp(f[j] - mx) * inv;
+      }
       st_nt(yr + c0, pack(f, T{}));
     }
   } else {
