@@ -227,6 +227,10 @@ __global__ __launch_bounds__(256) void rows_reg_kernel(RowParams p) {
       const int64_t c0 = (static_cast<int64_t>(i) * LANES + l) * VEC;
       v[i] = live[i] ? ld_nt(xr + c0) : make_uint4(0, 0, 0, 0);
     }
+    // Unpacked once: the statistics passes and the store pass read these.
+    float xf[NV][VEC];
+#pragma unroll
+    for (int i = 0; i < NV; ++i) unpack(v[i], xf[i], T{});
     const float inv_n = 1.0f / static_cast<float>(n);
     float mean = 0.f, rstd;
     if constexpr (OP == kLayerNorm && WPR > 1) {
@@ -238,8 +242,7 @@ __global__ __launch_bounds__(256) void rows_reg_kernel(RowParams p) {
 #pragma unroll
       for (int i = 0; i < NV; ++i) {
         if (!live[i]) continue;
-        float f[VEC];
-        unpack(v[i], f, T{});
+        const float* f = xf[i];
         cnt += VEC;
 #pragma unroll
         for (int j = 0; j < VEC; ++j) sw += f[j];
@@ -251,8 +254,7 @@ __global__ __launch_bounds__(256) void rows_reg_kernel(RowParams p) {
 #pragma unroll
       for (int i = 0; i < NV; ++i) {
         if (!live[i]) continue;
-        float f[VEC];
-        unpack(v[i], f, T{});
+        const float* f = xf[i];
 #pragma unroll
         for (int j = 0; j < VEC; ++j) {
           const float d = f[j] - mw;
@@ -282,8 +284,7 @@ __global__ __launch_bounds__(256) void rows_reg_kernel(RowParams p) {
       float s = 0.f;
 #pragma unroll
       for (int i = 0; i < NV; ++i) {
-        float f[VEC];
-        unpack(v[i], f, T{});
+        const float* f = xf[i];
 #pragma unroll
         for (int j = 0; j < VEC; ++j) s += (OP == kRmsNorm) ? f[j] * f[j] : f[j];
       }
@@ -296,8 +297,7 @@ __global__ __launch_bounds__(256) void rows_reg_kernel(RowParams p) {
 #pragma unroll
         for (int i = 0; i < NV; ++i) {
           if (!live[i]) continue;
-          float f[VEC];
-          unpack(v[i], f, T{});
+          const float* f = xf[i];
 #pragma unroll
           for (int j = 0; j < VEC; ++j) {
             const float d = f[j] - mean;
@@ -310,23 +310,35 @@ __global__ __launch_bounds__(256) void rows_reg_kernel(RowParams p) {
     }
     const T* g = static_cast<const T*>(p.gamma);
     const T* b = static_cast<const T*>(p.beta);
+    // One copy of the store pass per (gamma, beta) presence: tested per
+    // element, the uniform pointer checks became a select per value.
+    auto store_pass = [&](auto has_g, auto has_b) {
+      constexpr bool G = decltype(has_g)::value, B = decltype(has_b)::value;
 #pragma unroll
-    for (int i = 0; i < NV; ++i) {
-      const int64_t c0 = (static_cast<int64_t>(i) * LANES + l) * VEC;
-      if (!live[i]) continue;
-      float f[VEC], gv[VEC], bv[VEC];
-      unpack(v[i], f, T{});
-      if (g) load_vec(g + c0, gv);
-      if (b) load_vec(b + c0, bv);
+      for (int i = 0; i < NV; ++i) {
+        const int64_t c0 = (static_cast<int64_t>(i) * LANES + l) * VEC;
+        if (!live[i]) continue;
+        const float* x = xf[i];
+        float f[VEC], gv[VEC], bv[VEC];
+        if constexpr (G) load_vec(g + c0, gv);
+        if constexpr (B) load_vec(b + c0, bv);
 #pragma unroll
-      for (int j = 0; j < VEC; ++j) {
-        float o = (f[j] - mean) * rstd;
-        if (g) o *= gv[j];
-        if (b) o += bv[j];
-        f[j] = o;
+        for (int j = 0; j < VEC; ++j) {
+          const float t = (x[j] - mean) * rstd;
+          if constexpr (G && B) f[j] = fmaf(t, gv[j], bv[j]);
+          else if constexpr (G) f[j] = t * gv[j];
+          else if constexpr (B) f[j] = t + bv[j];
+          else f[j] = t;
+        }
+        st_nt(yr + c0, pack(f, T{}));
       }
-      st_nt(yr + c0, pack(f, T{}));
-    }
+    };
+    using yes = std::true_type;
+    using no = std::false_type;
+    if (g && b) store_pass(yes{}, yes{});
+    else if (g) store_pass(yes{}, no{});
+    else if (b) store_pass(no{}, yes{});
+    else store_pass(no{}, no{});
   }
 }
 
