@@ -218,6 +218,31 @@ extern "C" int ghip_backend_description(GHipBackend* b, char* buf, size_t buflen
   return snprintf(buf, buflen, "HIP GPU backend (%s)", b->device_name.c_str());
 }
 
+// Capabilities (capabilities.go:14-166): the GoMLX OpType names (without the
+// "OpType" prefix) this backend builds, and the dtypes it holds.  Ops of the
+// reference's list that are absent here: BatchNorm*, ConvGeneral,
+// ReduceWindow, SelectAndScatterMax and RNGBitGenerator.
+extern "C" int ghip_backend_capabilities(char* buf, size_t buflen) {
+  static const char kCaps[] =
+      "functions=1;ops="
+      "Parameter,Constant,"
+      "Abs,Neg,Sqrt,Rsqrt,Exp,Expm1,Log,Log1p,Sin,Cos,Tanh,Logistic,Erf,Floor,Ceil,Round,Sign,"
+      "LogicalNot,BitwiseNot,IsFinite,IsNaN,Identity,"
+      "Add,Sub,Mul,Div,Rem,Pow,Max,Min,Atan2,LogicalAnd,LogicalOr,LogicalXor,BitwiseAnd,BitwiseOr,"
+      "BitwiseXor,ShiftLeft,ShiftRightArithmetic,ShiftRightLogical,"
+      "Equal,NotEqual,GreaterThan,GreaterOrEqual,LessThan,LessOrEqual,"
+      "EqualTotalOrder,NotEqualTotalOrder,GreaterThanTotalOrder,GreaterOrEqualTotalOrder,"
+      "LessThanTotalOrder,LessOrEqualTotalOrder,"
+      "Reshape,Transpose,ConvertDType,BroadcastInDim,Where,Clamp,Slice,Concatenate,Reverse,Iota,Pad,"
+      "DotGeneral,ReduceSum,ReduceMax,ReduceMin,ReduceProduct,ReduceLogicalAnd,ReduceLogicalOr,"
+      "ArgMinMax,Gather,ScatterSum,ScatterMax,ScatterMin,DynamicSlice,DynamicUpdateSlice,"
+      "FusedSoftmax,FusedLayerNorm,FusedGelu,FusedDense,FusedAttentionQKVProjection,"
+      "FusedScaledDotProductAttention,While,If,Sort,Call;dtypes="
+      "Bool,Int8,Int16,Int32,Int64,Float16,BFloat16,Float32,Float64,Uint8,Uint16,Uint32,Uint64";
+  if (buf && buflen) snprintf(buf, buflen, "%s", kCaps);
+  return static_cast<int>(sizeof(kCaps) - 1);
+}
+
 extern "C" int ghip_backend_num_devices(GHipBackend* b) { return b && !b->plan_only ? 1 : 0; }
 extern "C" void* ghip_backend_stream(GHipBackend* b) { return b ? b->stream : nullptr; }
 
@@ -891,6 +916,77 @@ extern "C" GHipValue ghip_fn_reverse(GHipFunction* f, GHipValue x, const int* ax
   n.a0 = ax;
   n.shape = a->shape;
   return c.add(std::move(n));
+}
+
+namespace {
+GHipValue wrap(GHipValue v, GHipError* err, const char* op);
+}  // namespace
+
+// Pad (function.go:1533-1569): edge padding with a scalar fill value; interior
+// padding is refused as the reference refuses it.  Negative padding crops (XLA
+// semantics).  Composed of a Slice for the crops and, per padded axis, a
+// Concatenate of fill blocks around the operand.
+extern "C" GHipValue ghip_fn_pad(GHipFunction* f, GHipValue x, GHipValue fill, const int64_t* start,
+                                 const int64_t* end, const int64_t* interior, int rank, GHipError* err) {
+  FN_BEGIN("Pad");
+  const Node* a = c.node(x);
+  if (!a) return -1;
+  const Node* fv = c.node(fill);
+  if (!fv) return -1;
+  const Shape xs = a->shape;
+  if (rank != xs.rank()) return c.fail(GHIP_ERR_INVALID_ARG, "%d axis configs for rank-%d operand", rank, xs.rank());
+  if (fv->shape.rank() != 0 || fv->shape.dtype != xs.dtype)
+    return c.fail(GHIP_ERR_INVALID_ARG, "fill value must be a %s scalar, got %s", dtype_name(xs.dtype),
+                  fv->shape.str().c_str());
+  for (int i = 0; i < rank; ++i)
+    if (interior && interior[i] != 0)
+      return c.fail(GHIP_ERR_UNSUPPORTED, "interior padding not supported (axis %d)", i);
+  std::vector<int64_t> s0(rank), s1(rank), st(rank, 1);
+  bool crop = false;
+  for (int i = 0; i < rank; ++i) {
+    s0[i] = start[i] < 0 ? -start[i] : 0;
+    s1[i] = xs.dims[i] - (end[i] < 0 ? -end[i] : 0);
+    if (s1[i] < s0[i]) return c.fail(GHIP_ERR_INVALID_ARG, "axis %d: padding (%lld, %lld) crops more than %lld",
+                                     i, (long long)start[i], (long long)end[i], (long long)xs.dims[i]);
+    crop = crop || start[i] < 0 || end[i] < 0;
+  }
+  GHipValue v = x;
+  if (crop) v = ghip_fn_slice(f, v, s0.data(), s1.data(), st.data(), rank, err);
+  std::vector<int64_t> dims(rank);
+  for (int i = 0; i < rank; ++i) dims[i] = s1[i] - s0[i];
+  for (int i = 0; i < rank && v >= 0; ++i) {
+    const int64_t lo = start[i] > 0 ? start[i] : 0, hi = end[i] > 0 ? end[i] : 0;
+    if (lo == 0 && hi == 0) continue;
+    std::vector<GHipValue> parts;
+    for (int side = 0; side < 3 && v >= 0; ++side) {
+      if (side == 1) { parts.push_back(v); continue; }
+      const int64_t w = side == 0 ? lo : hi;
+      if (w == 0) continue;
+      std::vector<int64_t> bd = dims;
+      bd[i] = w;
+      const GHipValue b = ghip_fn_broadcast_in_dim(f, fill, bd.data(), rank, nullptr, 0, err);
+      if (b < 0) return wrap(b, err, "Pad");
+      parts.push_back(b);
+    }
+    v = ghip_fn_concatenate(f, i, parts.data(), static_cast<int>(parts.size()), err);
+    dims[i] += lo + hi;
+  }
+  return wrap(v, err, "Pad");
+}
+
+// ReduceLogicalAnd / ReduceLogicalOr (function.go:2262-2270): the minimum /
+// maximum of the {0, 1} bytes a Bool holds, read back as Bool.
+extern "C" GHipValue ghip_fn_reduce_logical(GHipFunction* f, int is_or, GHipValue x, const int* axes,
+                                            int naxes, GHipError* err) {
+  FN_BEGIN(is_or ? "ReduceLogicalOr" : "ReduceLogicalAnd");
+  const Node* a = c.node(x);
+  if (!a) return -1;
+  if (a->shape.dtype != GHIP_DTYPE_BOOL)
+    return c.fail(GHIP_ERR_INVALID_ARG, "bool operand required, got %s", dtype_name(a->shape.dtype));
+  GHipValue v = ghip_fn_convert_dtype(f, x, GHIP_DTYPE_UINT8, err);
+  if (v >= 0) v = ghip_fn_reduce(f, is_or ? GHIP_REDUCE_MAX : GHIP_REDUCE_MIN, v, axes, naxes, err);
+  if (v >= 0) v = ghip_fn_convert_dtype(f, v, GHIP_DTYPE_BOOL, err);
+  return wrap(v, err, is_or ? "ReduceLogicalOr" : "ReduceLogicalAnd");
 }
 
 extern "C" GHipValue ghip_fn_fused_softmax(GHipFunction* f, GHipValue x, int axis, GHipError* err) {

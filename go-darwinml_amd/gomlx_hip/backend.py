@@ -52,6 +52,24 @@ class Shape:
         return len(self.dims)
 
 
+@dataclass(frozen=True)
+class PadAxis:
+    """backends.PadAxis: elements added before / after an axis and between its
+    elements (interior)."""
+    start: int = 0
+    end: int = 0
+    interior: int = 0
+
+
+@dataclass(frozen=True)
+class Capabilities:
+    """backends.Capabilities (capabilities.go:14-166): control-flow functions,
+    the OpType names (without the "OpType" prefix) and the DType names."""
+    functions: bool
+    operations: frozenset
+    dtypes: frozenset
+
+
 def make_shape(dtype: int, *dims: int) -> Shape:
     """shapes.Make(dtype, dims...)."""
     return Shape(dtype, tuple(int(d) for d in dims))
@@ -88,6 +106,7 @@ _GRAPH_SIGS = {
     "ghip_backend_description": ([_vp, ctypes.c_char_p, ctypes.c_size_t], _int),
     "ghip_backend_num_devices": ([_vp], _int),
     "ghip_backend_stream": ([_vp], _vp),
+    "ghip_backend_capabilities": ([ctypes.c_char_p, ctypes.c_size_t], _int),
     "ghip_buffer_from_host": ([_vp, _int, _i64p, _int, _vp, ctypes.c_size_t, _errp], _vp),
     "ghip_buffer_new": ([_vp, _int, _i64p, _int, _errp], _vp),
     "ghip_buffer_to_host": ([_vp, _vp, ctypes.c_size_t, _errp], _int),
@@ -119,6 +138,8 @@ _GRAPH_SIGS = {
     "ghip_fn_slice": ([_vp, _int, _i64p, _i64p, _i64p, _int, _errp], _int),
     "ghip_fn_concatenate": ([_vp, _int, _intp, _int, _errp], _int),
     "ghip_fn_reverse": ([_vp, _int, _intp, _int, _errp], _int),
+    "ghip_fn_pad": ([_vp, _int, _int, _i64p, _i64p, _i64p, _int, _errp], _int),
+    "ghip_fn_reduce_logical": ([_vp, _int, _int, _intp, _int, _errp], _int),
     "ghip_fn_fused_softmax": ([_vp, _int, _int, _errp], _int),
     "ghip_fn_fused_layer_norm": ([_vp, _int, _intp, _int, _dbl, _int, _int, _errp], _int),
     "ghip_fn_fused_sdpa": ([_vp, _int, _int, _int, _int, _int, _int, _int, _dbl, _int, _errp], _int),
@@ -229,6 +250,14 @@ class Backend:
     def DeviceDescription(self, device_num: int = 0) -> str:
         return self.Description()
 
+    def Capabilities(self) -> Capabilities:
+        n = _L().ghip_backend_capabilities(None, 0)
+        buf = ctypes.create_string_buffer(n + 1)
+        _L().ghip_backend_capabilities(buf, n + 1)
+        fields = dict(kv.split("=", 1) for kv in buf.value.decode().split(";"))
+        return Capabilities(fields["functions"] == "1", frozenset(fields["ops"].split(",")),
+                            frozenset(fields["dtypes"].split(",")))
+
     def Builder(self, name: str) -> "Builder":
         err = GHipError(0, None)
         h = _L().ghip_builder_new(self.handle, name.encode(), ctypes.byref(err))
@@ -277,6 +306,10 @@ class Backend:
         if r < 0:
             raise BackendError(5, "BufferShape: buffer finalized")
         return Shape(dt.value, tuple(dims[i] for i in range(r)))
+
+    def BufferDeviceNum(self, buf: Buffer) -> int:
+        """Always 0: one device (backend.go:125-128)."""
+        return 0
 
     def BufferToFlatData(self, buf: Buffer, flat: Optional[np.ndarray] = None) -> np.ndarray:
         s = self.BufferShape(buf)
@@ -448,7 +481,23 @@ class Function:
         a, n = _intarr(axes)
         return self._call("ghip_fn_reverse", x.id, a, n)
 
+    def Pad(self, operand, fill_value, *axes_config) -> Value:
+        """axes_config: one PadAxis (or (start, end[, interior]) tuple) per axis."""
+        cfg = [a if isinstance(a, PadAxis) else PadAxis(*a) for a in axes_config]
+        st, r = _i64arr([a.start for a in cfg])
+        en, _ = _i64arr([a.end for a in cfg])
+        it, _ = _i64arr([a.interior for a in cfg])
+        return self._call("ghip_fn_pad", operand.id, fill_value.id, st, en, it, r)
+
     # reductions
+    def ReduceLogicalAnd(self, x, *axes) -> Value:
+        a, n = _intarr(axes)
+        return self._call("ghip_fn_reduce_logical", 0, x.id, a, n)
+
+    def ReduceLogicalOr(self, x, *axes) -> Value:
+        a, n = _intarr(axes)
+        return self._call("ghip_fn_reduce_logical", 1, x.id, a, n)
+
     def _reduce(self, op, x, axes):
         a, n = _intarr(axes)
         return self._call("ghip_fn_reduce", op, x.id, a, n)
@@ -595,6 +644,11 @@ for _i, _n in enumerate(COMPARE):
     _add_binary(_n, _i, "ghip_fn_compare")
 for _n, _c in REDUCE.items():
     _add_reduce(_n, _c)
+# EqualTotalOrder ... LessOrEqualTotalOrder: the plain comparisons, as the
+# reference delegates them (function.go:2227-2256); they differ from a total
+# order only for NaN and for -0 vs +0.
+for _i, _n in enumerate(COMPARE):
+    _add_binary(_n + "TotalOrder", _i, "ghip_fn_compare")
 
 
 # ---------------------------------------------------------------- Executable

@@ -209,6 +209,11 @@ int ghip_backend_is_finalized(GHipBackend* b);            /* IsFinalized (:95-99
 int ghip_backend_description(GHipBackend* b, char* buf, size_t buflen); /* Description */
 int ghip_backend_num_devices(GHipBackend* b);             /* NumDevices (:57) */
 void* ghip_backend_stream(GHipBackend* b);                /* stream Execute uses */
+/* Capabilities (backend.go:64-67, capabilities.go:14-166): writes
+ * "functions=1;ops=<OpType names>;dtypes=<DType names>" (comma-separated, the
+ * GoMLX names without the OpType prefix) into buf, truncated to buflen; returns
+ * the full length. */
+int ghip_backend_capabilities(char* buf, size_t buflen);
 
 /* --- Buffers (buffer.go:20-119, DataInterface backend.go:103-167) ------- */
 /* BufferFromFlatData: device buffer of `shape` holding a copy of host `data`. */
@@ -272,6 +277,15 @@ GHipValue ghip_fn_concatenate(GHipFunction* f, int axis, const GHipValue* operan
                               GHipError* err);                          /* :1093-1113 */
 GHipValue ghip_fn_reverse(GHipFunction* f, GHipValue x, const int* axes, int naxes,
                           GHipError* err);                              /* :1115-1125 */
+/* Pad (:1533-1569): per axis `start` / `end` elements of the scalar `fill`
+ * (negative values crop); a non-zero `interior` (may be NULL) is refused with
+ * GHIP_ERR_UNSUPPORTED, as the reference refuses it. */
+GHipValue ghip_fn_pad(GHipFunction* f, GHipValue x, GHipValue fill, const int64_t* start,
+                      const int64_t* end, const int64_t* interior, int rank, GHipError* err);
+/* ReduceLogicalAnd (is_or = 0) / ReduceLogicalOr (is_or = 1) over a Bool
+ * operand (:2262-2270); empty axes reduce everything. */
+GHipValue ghip_fn_reduce_logical(GHipFunction* f, int is_or, GHipValue x, const int* axes,
+                                 int naxes, GHipError* err);
 GHipValue ghip_fn_fused_softmax(GHipFunction* f, GHipValue x, int axis, GHipError* err); /* :2276 */
 /* gamma / beta may be -1 (absent). */
 GHipValue ghip_fn_fused_layer_norm(GHipFunction* f, GHipValue x, const int* axes, int naxes,

@@ -95,6 +95,11 @@ CASES = {
         "source": "mpsgraph_test.go:1485-1532 (TestConvertDType)",
         "x": [1.7, 2.3, -0.9], "expected": [1, 2, 0],
     },
+    "pad": {
+        "source": "mpsgraph_test.go:876-939 (TestPad)",
+        "shape": [2, 2], "x": [1, 2, 3, 4], "fill": 0, "start": [1, 0], "end": [0, 1],
+        "expected_shape": [3, 3], "expected": [0, 0, 0, 1, 2, 0, 3, 4, 0],
+    },
     "dynamic_slice": {
         "source": "mpsgraph_test.go:993-1062 (TestDynamicSlice)",
         "shape": [3, 4], "x": list(range(1, 13)), "starts": [1, 1], "sizes": [2, 2],

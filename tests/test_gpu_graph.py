@@ -507,3 +507,94 @@ def test_reshape_of_strided_views(be):
     assert np.array_equal(b, x.T.reshape(24) + x.reshape(24))
     want = (np.broadcast_to(x[:, 1][None, :, None], (2, 6, 3)) * np.broadcast_to(x[None, :, :3], (2, 6, 3))).reshape(4, 9)
     assert np.array_equal(c, want)
+
+
+def test_pad_known_answer(be, known):                             # :876-939
+    k = known["pad"]
+    (y,) = run(be, lambda f, x: [f.Pad(x, f.Constant(np.float32(k["fill"])),
+                                       *zip(k["start"], k["end"]))],
+               [(np.array(k["x"], np.float32), make_shape(F32, *k["shape"]))])
+    assert list(y.shape) == k["expected_shape"]
+    assert y.reshape(-1).tolist() == k["expected"]
+
+
+@pytest.mark.parametrize("dt", [F32, BF16, I32, dtypes.Uint8])
+def test_pad_crop_vs_numpy(be, dt):
+    """Edge padding with a non-zero fill on several axes at once, negative
+    padding cropping (XLA semantics), bit-exact against numpy.pad."""
+    rng = np.random.default_rng(11)
+    x = rng.integers(0, 100, (3, 5, 4)).astype(np.float32)
+    cfg = [(1, 2), (0, 0), (-1, 3)]
+    want = np.pad(x[:, :, 1:], [(1, 2), (0, 0), (0, 3)], constant_values=7)
+    host = x if dt in (F32, BF16) else x.astype(np.int32 if dt == I32 else np.uint8)
+    fill = np.array(7, host.dtype)
+    (y,) = run(be, lambda f, p: [f.Pad(p, f.Constant(fill) if dt != BF16 else
+                                       f.ConvertDType(f.Constant(np.float32(7)), BF16), *cfg)],
+               [(host, make_shape(dt, 3, 5, 4))])
+    assert y.shape == want.shape and np.array_equal(y.astype(np.float32), want)
+
+
+def test_pad_errors(be):
+    b = be.Builder("pad_err")
+    f = b.Main()
+    x = f.Parameter("x", make_shape(F32, 2, 3))
+    z = f.Constant(np.float32(0))
+    with pytest.raises(BackendError, match="interior padding not supported"):
+        f.Pad(x, z, (0, 0, 1), (0, 0))
+    with pytest.raises(BackendError, match="scalar"):
+        f.Pad(x, f.Constant(np.zeros(2, np.float32), 2), (0, 0), (0, 0))
+    with pytest.raises(BackendError, match="crops more than"):
+        f.Pad(x, z, (0, 0), (-2, -2))
+    b.Finalize()
+
+
+def test_reduce_logical_and_or(be):                               # function.go:2262-2270
+    rng = np.random.default_rng(12)
+    x = rng.random((4, 5, 6)) < 0.8
+    x[0, :, 0] = True          # a column that is all true
+    x[1, :, 1] = False         # and one that is all false
+    s = make_shape(dtypes.Bool, 4, 5, 6)
+    outs = run(be, lambda f, p: [f.ReduceLogicalAnd(p, 1), f.ReduceLogicalOr(p, 1),
+                                 f.ReduceLogicalAnd(p, 0, 2), f.ReduceLogicalOr(p), f.ReduceLogicalAnd(p)],
+               [(x, s)])
+    wants = [x.all(1), x.any(1), x.all((0, 2)), x.any(), x.all()]
+    for got, want in zip(outs, wants):
+        assert got.dtype == np.bool_ and np.array_equal(got, want)
+
+
+def test_total_order_comparisons_follow_plain_ones(be):           # function.go:2227-2256
+    s = make_shape(F32, 6)
+    l = np.array([1, 2, 3, -0.0, -np.inf, 5], np.float32)
+    r = np.array([2, 2, 2, 0.0, -np.inf, -1], np.float32)
+    outs = run(be, lambda f, a, b: [f.EqualTotalOrder(a, b), f.NotEqualTotalOrder(a, b),
+                                    f.GreaterThanTotalOrder(a, b), f.GreaterOrEqualTotalOrder(a, b),
+                                    f.LessThanTotalOrder(a, b), f.LessOrEqualTotalOrder(a, b)],
+               [(l, s), (r, s)])
+    for got, want in zip(outs, [l == r, l != r, l > r, l >= r, l < r, l <= r]):
+        assert got.astype(bool).tolist() == want.tolist()
+
+
+def test_layer_norm_gradient_known_answer(be):                    # :2625-2642
+    """d/dx sum(LayerNorm(x)) for x = [1, 2, 3, 4] (no gamma / beta) is ~0: the
+    reference's check, here on the backward chain of primitive ops a graph layer
+    emits for it (mean, centre, variance, rsqrt and their adjoints)."""
+    n, eps = 4, 1e-5
+
+    def build(f, x):
+        K = lambda v: f.Constant(np.float32(v))
+        bc = lambda v: f.BroadcastInDim(v, make_shape(F32, 1, n), [0])
+        mean = f.Div(f.ReduceSum(x, 1), K(n))
+        d = f.Sub(x, bc(mean))
+        var = f.Div(f.ReduceSum(f.Mul(d, d), 1), K(n))
+        rstd = f.Rsqrt(f.Add(var, K(eps)))
+        dy = f.BroadcastInDim(K(1.0), make_shape(F32, 1, n), [])
+        g_rstd = f.ReduceSum(f.Mul(dy, d), 1)
+        g_var = f.Mul(f.Mul(g_rstd, K(-0.5)), f.Mul(rstd, f.Mul(rstd, rstd)))
+        g_d = f.Add(f.Mul(dy, bc(rstd)), f.Mul(f.Mul(d, K(2.0 / n)), bc(g_var)))
+        g_x = f.Sub(g_d, bc(f.Div(f.ReduceSum(g_d, 1), K(n))))
+        normed = f.Mul(d, bc(rstd))
+        return [g_x, normed]
+
+    g, y = run(be, build, [(np.array([[1, 2, 3, 4]], np.float32), make_shape(F32, 1, n))])
+    close(y, [-1.3416, -0.4472, 0.4472, 1.3416], 1e-3)
+    assert np.max(np.abs(g)) <= 1e-4

@@ -274,3 +274,51 @@ def test_control_flow_plans_and_errors(be):
     f.Return([neg])
     plan = b.Compile().Plan()
     assert "while (2 state values" in plan and "call callee" in plan, plan
+
+
+# The reference's declared ops (capabilities.go:17-150) minus the ones this
+# backend does not build (CNN / batch-norm / RNG ops, outside the hot path).
+_REFERENCE_OPS = set("""Parameter Constant Abs Neg Sqrt Rsqrt Exp Expm1 Log Log1p Sin Cos Tanh
+Logistic Erf Floor Ceil Round Sign LogicalNot BitwiseNot IsFinite IsNaN Identity Add Sub Mul Div
+Rem Pow Max Min Atan2 LogicalAnd LogicalOr LogicalXor BitwiseAnd BitwiseOr BitwiseXor ShiftLeft
+ShiftRightArithmetic ShiftRightLogical Equal NotEqual GreaterThan GreaterOrEqual LessThan
+LessOrEqual Reshape Transpose ConvertDType BroadcastInDim Where Clamp Slice Concatenate Reverse
+Iota Pad DotGeneral ReduceSum ReduceMax ReduceMin ReduceProduct ArgMinMax BatchNormForInference
+Gather ScatterSum ScatterMax ScatterMin DynamicSlice DynamicUpdateSlice RNGBitGenerator
+ConvGeneral ReduceWindow SelectAndScatterMax EqualTotalOrder NotEqualTotalOrder
+GreaterThanTotalOrder GreaterOrEqualTotalOrder LessThanTotalOrder LessOrEqualTotalOrder
+ReduceLogicalAnd ReduceLogicalOr FusedSoftmax FusedLayerNorm FusedGelu FusedDense
+FusedAttentionQKVProjection FusedScaledDotProductAttention BatchNormForTraining
+BatchNormGradient While If Sort Call""".split())
+_ABSENT = {"BatchNormForInference", "BatchNormForTraining", "BatchNormGradient", "RNGBitGenerator",
+           "ConvGeneral", "ReduceWindow", "SelectAndScatterMax"}
+
+
+def test_capabilities_match_reference_list_and_methods():
+    from gomlx_hip.backend import Backend, Function
+    caps = Backend("plan").Capabilities()
+    assert caps.functions
+    assert caps.operations == _REFERENCE_OPS - _ABSENT
+    # every declared op is a Function method of the same name
+    assert [op for op in caps.operations if not hasattr(Function, op)] == []
+    assert {"Float32", "BFloat16", "Float16", "Bool", "Int32", "Int64", "Uint8"} <= caps.dtypes
+
+
+def test_pad_and_logical_reduce_shapes():
+    from gomlx_hip.backend import Backend, BackendError, dtypes, make_shape
+    import numpy as np
+    b = Backend("plan").Builder("pad")
+    f = b.Main()
+    x = f.Parameter("x", make_shape(dtypes.Float32, 3, 4))
+    z = f.Constant(np.float32(0))
+    assert f.OpShape(f.Pad(x, z, (1, 2), (0, -1))).dims == (6, 3)
+    assert f.OpShape(f.Pad(x, z, (0, 0), (0, 0))).dims == (3, 4)
+    with pytest.raises(BackendError, match="interior"):
+        f.Pad(x, z, (1, 2, 1), (0, 0))
+    with pytest.raises(BackendError, match="2 axis configs for rank-2|axis configs"):
+        f.Pad(x, z, (1, 2))
+    bl = f.Parameter("b", make_shape(dtypes.Bool, 3, 4))
+    assert f.OpShape(f.ReduceLogicalAnd(bl, 1)).dims == (3,)
+    assert f.OpShape(f.ReduceLogicalOr(bl)).dtype == dtypes.Bool
+    with pytest.raises(BackendError, match="bool operand required"):
+        f.ReduceLogicalOr(x)
