@@ -89,22 +89,40 @@ __device__ __forceinline__ void store_vec(bf16_t* p, const float* v) {
 }
 
 // ---------------------------------------------------------------------------
-// Wave64 reductions (butterfly over all 64 lanes; every lane gets the result).
-// ---------------------------------------------------------------------------
+// Wave64 reductions with every lane receiving the result (all 64 lanes active).  Within each row of
+// 16 lanes four DPP steps (quad_perm [1,0,3,2], quad_perm [2,3,0,1],
+// row_half_mirror, row_mirror) leave the row's total in all 16 lanes; the four
+// row totals are then read as scalars (v_readlane) and combined.  Each DPP step
+// is one VALU instruction with its source operand permuted, so a reduction
+// costs ~12 instructions and no LDS round trip (a ds_bpermute butterfly takes
+// six LDS-latency steps).
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float x) {
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), CTRL, 0xf, 0xf, false));
+}
+__device__ __forceinline__ float row_lane(float x, int lane) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), lane));
+}
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
-  return v;
+  v += dpp_f32<0xb1>(v);   // quad_perm [1,0,3,2]
+  v += dpp_f32<0x4e>(v);   // quad_perm [2,3,0,1]
+  v += dpp_f32<0x141>(v);  // row_half_mirror
+  v += dpp_f32<0x140>(v);  // row_mirror
+  return (row_lane(v, 0) + row_lane(v, 16)) + (row_lane(v, 32) + row_lane(v, 48));
 }
 __device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
-  return v;
+  v = fmaxf(v, dpp_f32<0xb1>(v));
+  v = fmaxf(v, dpp_f32<0x4e>(v));
+  v = fmaxf(v, dpp_f32<0x141>(v));
+  v = fmaxf(v, dpp_f32<0x140>(v));
+  return fmaxf(fmaxf(row_lane(v, 0), row_lane(v, 16)), fmaxf(row_lane(v, 32), row_lane(v, 48)));
 }
 
-// exp(x) through the hardware base-2 exponential: exp(x) = 2^(x * log2(e)).
+// exp(x) through the hardware base-2 exponential: exp(x) = 2^(x * log2(e)),
+// one v_exp_f32 (results below 2^-126 flush to zero; exp2f would add a
+// denormal-range rescale of five more instructions per value).
 __device__ __forceinline__ float fast_exp(float x) {
-  return exp2f(x * 1.4426950408889634f);
+  return __builtin_amdgcn_exp2f(x * 1.4426950408889634f);
 }
 
 constexpr int kWave = 64;
