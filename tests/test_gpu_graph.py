@@ -598,3 +598,35 @@ def test_layer_norm_gradient_known_answer(be):                    # :2625-2642
     g, y = run(be, build, [(np.array([[1, 2, 3, 4]], np.float32), make_shape(F32, 1, n))])
     close(y, [-1.3416, -0.4472, 0.4472, 1.3416], 1e-3)
     assert np.max(np.abs(g)) <= 1e-4
+
+
+def test_gomlx_graph_layer_cases(be):                             # :1955-2060
+    """The reference's GoMLX-level tests, as the backend ops the graph layer emits
+    for them (Ones / ZerosLike: constant + broadcast; ExpandDims: reshape;
+    Gather: the XLA gather of an embedding lookup)."""
+    s3 = make_shape(F32, 3)
+    (y,) = run(be, lambda f, a, b: [f.Add(a, b)],
+               [(np.array([1, 2, 3], np.float32), s3), (np.array([10, 20, 30], np.float32), s3)])
+    close(y, [11, 22, 33], 1e-5)                                  # TestGoMLXAdd
+    (y,) = run(be, lambda f, x: [f.Exp(f.Add(f.Log(x), f.BroadcastInDim(f.Constant(np.float32(1)), s3, [])))],
+               [(np.array([1, 2, 4], np.float32), s3)])
+    close(y, [math.e, 2 * math.e, 4 * math.e], 1e-4)              # TestGoMLXMathChain
+    m = np.arange(1, 7, dtype=np.float32)
+    (y,) = run(be, lambda f, a, b: [f.DotGeneral(a, [1], [], b, [0], [])],
+               [(m, make_shape(F32, 2, 3)), (m, make_shape(F32, 3, 2))])
+    close(y, [22, 28, 49, 64], 1e-4)                              # TestGoMLXMatMul
+    (y,) = run(be, lambda f, x: [f.Sub(x, f.BroadcastInDim(
+        f.Reshape(f.Div(f.ReduceSum(x, 1), f.Constant(np.float32(3))), 2, 1), make_shape(F32, 2, 3), [0, 1]))],
+               [(m, make_shape(F32, 2, 3))])
+    close(y, [-1, 0, 1, -1, 0, 1], 1e-4)                          # TestGoMLXReduceAndBroadcast
+    table = np.array([10, 11, 12, 20, 21, 22, 30, 31, 32, 40, 41, 42], np.float32)
+    (y,) = run(be, lambda f, t, i: [f.Gather(t, i, 1, [1], [0], [0], [1, 3], False)],
+               [(table, make_shape(F32, 4, 3)), (np.array([1, 3], np.int32), make_shape(I32, 2, 1))])
+    close(y, [20, 21, 22, 40, 41, 42], 0)                         # TestGoMLXGatherAndSlice
+    s5 = make_shape(F32, 5)
+
+    def relu(f, x):
+        zero = f.BroadcastInDim(f.Constant(np.float32(0)), s5, [])
+        return [f.Where(f.GreaterThan(x, zero), x, zero)]
+    (y,) = run(be, relu, [(np.array([-2, -1, 0, 1, 2], np.float32), s5)])
+    close(y, [0, 0, 0, 1, 2], 1e-5)                               # TestGoMLXWhereAndCompare
