@@ -630,3 +630,12 @@ def test_gomlx_graph_layer_cases(be):                             # :1955-2060
         return [f.Where(f.GreaterThan(x, zero), x, zero)]
     (y,) = run(be, relu, [(np.array([-2, -1, 0, 1, 2], np.float32), s5)])
     close(y, [0, 0, 0, 1, 2], 1e-5)                               # TestGoMLXWhereAndCompare
+
+
+def test_pad_crop_whole_axis_then_pad_back(be):
+    """An axis cropped to nothing and padded back: the empty intermediate slice
+    takes no copy, the output is all fill."""
+    x = np.arange(6, dtype=np.float32).reshape(2, 3)
+    (y,) = run(be, lambda f, p: [f.Pad(p, f.Constant(np.float32(5)), (0, 0), (-3, 2))],
+               [(x, make_shape(F32, 2, 3))])
+    assert y.shape == (2, 2) and np.all(y == 5)
