@@ -11,16 +11,18 @@ with its own roofline fraction.
 
 Timing: W untimed warmup steps plus at least 0.25 s of sustained untimed launches
 (the GPU clock settles only under sustained load; a cold first burst of bf16
-GEMMs runs ~10% slower), then K steps (raised so the timed region holds at least
-30 ms of device work) bracketed by torch.cuda.synchronize()
-on both sides (wall clock -> ms_per_step), and HIP events recorded on the stream
-the kernels run on (-> average launch duration for "roofline").  Working sets
-below 1 GiB rotate through several input/output buffer sets so the 256 MB
-Infinity Cache cannot serve repeat reads (the rotation count is reported).
-HBM-bound cases launch their steps from a captured HIP graph (one graph holds a
-whole rotation cycle and is replayed), so microsecond kernels run back to back
-instead of waiting on the Python launch path; the graph is built, replayed once
-and checked against an eager launch before timing.
+GEMMs runs ~10% slower), then the timed region, bracketed by
+torch.cuda.synchronize() on both sides (wall clock -> ms_per_step) and by HIP
+events recorded on the stream the kernels run on (-> average launch duration for
+"roofline").  The headline line times exactly K = --steps launches; each
+secondary line stretches its own step count to at least 30 ms of device work and
+reports it.  Working sets below 1 GiB rotate through several input/output buffer
+sets so the 256 MB Infinity Cache cannot serve repeat reads (the rotation count
+is reported).  HBM-bound cases launch their steps from a captured HIP graph (one
+graph holds a whole rotation cycle and is replayed; a remainder of K runs as
+single launches), so microsecond kernels run back to back instead of waiting on
+the Python launch path; the graph is built, replayed once and checked against an
+eager launch before timing.
 """
 from __future__ import annotations
 
@@ -103,38 +105,44 @@ MIN_WARM_S = 0.25   # sustained warm-up before each timed region
 MIN_TIMED_S = 0.03  # minimum device time inside each timed region
 
 
-def time_case(case: Case, steps: int, warmup: int, eager: bool = False):
+def time_case(case: Case, steps: int, warmup: int, eager: bool = False, exact_steps: bool = False):
+    """Times `case`.  exact_steps: the timed region holds exactly `steps` launches
+    (the headline line, as --steps asks); otherwise it is stretched to at least
+    MIN_TIMED_S of device work (secondary lines, whose step counts are reported)."""
     import torch
     stream = case.stream or torch.cuda.current_stream()
     runner = graph_runner(case, steps) if case.bound == "hbm" and not eager else None
     if runner is not None:
         replay, per = runner
-        once = lambda i: replay()  # noqa: E731
-        for _ in range(max(1, warmup // per)):
-            replay()
     else:
-        per = 1
-        once = case.launch
-        for i in range(warmup):
-            case.launch(i)
+        replay, per = None, 1
+    for i in range(warmup):
+        case.launch(i)
     # The clock settles only after some 100 ms of sustained load: keep warming up
-    # until that much wall time has passed, and size the timed region to at least
-    # MIN_TIMED_S of work (never fewer steps than asked for).
+    # (untimed) until that much wall time has passed.
     stream.synchronize()
     n, t0 = 0, time.perf_counter()
     while time.perf_counter() - t0 < MIN_WARM_S:
         for _ in range(4):
-            once(n)
-            n += 1
+            if replay is not None:
+                replay()
+                n += per
+            else:
+                case.launch(n)
+                n += 1
         stream.synchronize()
-    est = (time.perf_counter() - t0) / (n * per)
-    steps = max(steps, int(MIN_TIMED_S / est) + 1)
-    reps = max(1, -(-steps // per))
-    steps = reps * per
-    if runner is not None:
-        work = lambda: [replay() for _ in range(reps)]  # noqa: E731
-    else:
-        work = lambda: [case.launch(i) for i in range(steps)]  # noqa: E731
+    settle_steps = n
+    est = (time.perf_counter() - t0) / max(n, 1)
+    if not exact_steps:
+        steps = max(steps, int(MIN_TIMED_S / est) + 1)
+    # whole graph replays first, then single launches for the remainder
+    reps, rest = (steps // per, steps % per) if replay is not None else (0, steps)
+
+    def work():
+        for _ in range(reps):
+            replay()
+        for i in range(rest):
+            case.launch(i)
     torch.cuda.synchronize()
     stream.synchronize()
     ev0 = torch.cuda.Event(enable_timing=True)
@@ -156,7 +164,9 @@ def time_case(case: Case, steps: int, warmup: int, eager: bool = False):
         unit = "TFLOP/s"
     return {
         "steps": steps,
+        "settle_steps": settle_steps,
         "graph": runner is not None,
+        "graph_replays": reps,
         "wall_ms": wall_ms,
         "ms_per_step": wall_ms / steps,
         "launch_us": per_launch_s * 1e6,
@@ -238,6 +248,19 @@ def make_cases(only=None):
                     flops_per_step=2 * B * M * N * K, bound="mfma", peak=peak, dtype=tag,
                     kernel="gemm_bf16_kernel" if tag == "bf16" else "gemm_f32_kernel",
                     config={"workload": f"DotGeneral [8,2048,4096]x[8,4096,4096] lc=[2] lb=[0] rc=[1] rb=[0], {tag} in, fp32 accumulate, {tag} out"})
+
+    def vendor_dot_case():
+        """The same bf16 DotGeneral through torch.matmul (hipBLASLt), timed in the
+        same process for comparison; not part of this backend."""
+        B, M, K, N = 8, 2048, 4096, 4096
+        a = (torch.randn((B, M, K), device=dev, generator=g) * 0.125).to(torch.bfloat16)
+        b = (torch.randn((B, K, N), device=dev, generator=g) * 0.125).to(torch.bfloat16)
+        c = torch.empty((B, M, N), device=dev, dtype=torch.bfloat16)
+        return Case("dot_general_bf16_hipblaslt", lambda i: torch.matmul(a, b, out=c),
+                    flops_per_step=2 * B * M * N * K, bound="mfma", peak=BF16_PEAK_TFLOPS, dtype="bf16",
+                    kernel="hipBLASLt (torch.matmul)",
+                    config={"workload": "comparison only: torch.matmul (hipBLASLt) on the DotGeneral "
+                                        "bf16 config shape, same process"})
 
     def attention_case():
         B, H, S, D = 4, 16, 2048, 128
@@ -355,6 +378,7 @@ def make_cases(only=None):
         "layernorm_bf16": lambda: ln_case(torch.bfloat16, "bf16"),
         "dot_general_bf16": lambda: dot_case(torch.bfloat16, "bf16", BF16_PEAK_TFLOPS),
         "dot_general_f32": lambda: dot_case(torch.float32, "f32", FP32_PEAK_TFLOPS),
+        "dot_general_bf16_hipblaslt": vendor_dot_case,
         "attention_bf16": attention_case,
         "transformer_block_bf16": transformer_case,
         "fused_dense_gelu_bf16": dense_case,
@@ -366,30 +390,33 @@ def make_cases(only=None):
 
 
 def cpu_baseline(seconds_target=10.0):
-    """The oracle's RMSNorm (C, OpenMP, fp64 accumulation) on the host cores, over a
-    bounded sample of the same workload: the first 2048 rows of an [8192, 4096]
-    fp32 input, repeated until ~seconds_target of CPU time has run."""
+    """The CPU restatement of the headline workload (not simplego: GoMLX's pure-Go
+    backend lives in an un-vendored module and there is no Go toolchain): the
+    oracle's fp32 RMSNorm (C, OpenMP over rows, fp32 sequential statistics, fp32
+    output) on the full configs[1] input, x [8192, 4096] fp32, gamma [4096],
+    repeated until ~seconds_target of wall time has run."""
     import numpy as np
     sys.path.insert(0, ROOT)
     from oracle import oracle as orc
     from gomlx_hip import synth
 
-    rows, n = 2048, 4096
+    rows, n = 8192, 4096
     x = synth.normal(2001, (rows, n))
     gam = synth.uniform_f32(2002, (n,), 0.5, 1.5)
-    orc.rmsnorm(x, gam, 1e-6)  # warm
+    y = np.empty_like(x)
+    orc.rmsnorm_f32(x, gam, 1e-6, out=y)  # warm
     reps, t0 = 0, time.perf_counter()
     while time.perf_counter() - t0 < seconds_target:
-        orc.rmsnorm(x, gam, 1e-6)
+        orc.rmsnorm_f32(x, gam, 1e-6, out=y)
         reps += 1
     dt = time.perf_counter() - t0
-    # fp32 in, fp64 out: count the algorithmic fp32 bytes (same unit as the GPU value)
     nbytes = (2 * rows * n + n) * 4
     threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
     return {"value": round(nbytes * reps / dt / 1e9, 3), "unit": "GB/s", "cores": threads,
             "kind": "port",
-            "sample": f"oracle/oracle.c orc_rmsnorm (OpenMP, fp64 accumulate) on rows 0..2047 of "
-                      f"x [8192,4096] fp32, {reps} repetitions in {dt:.1f} s"}
+            "sample": f"CPU restatement, not simplego: oracle/oracle.c orc_rmsnorm_f32 (OpenMP, "
+                      f"{threads} threads, fp32 statistics and output) on the full x [8192,4096] "
+                      f"fp32 + gamma [4096], {reps} repetitions in {dt:.1f} s"}
 
 
 def copy_reference(mib: int, steps: int):
@@ -424,7 +451,7 @@ def main():
         copy_reference(args.copy_ref, args.steps)
         return
     primary, builders, names = make_cases(only)
-    res = time_case(primary, args.steps, args.warmup, args.eager)
+    res = time_case(primary, args.steps, args.warmup, args.eager, exact_steps=True)
     secondary = []
     if not args.no_secondary:
         for name in names:
@@ -461,7 +488,11 @@ def main():
         "dtype": "f32",
         "data": "synthetic (torch.randn on device; inputs resident in HBM)",
         "config": dict(primary.config, rotation=primary.rotation, graph=res["graph"],
-                       kernel=primary.kernel, launch_us=round(res["launch_us"], 2)),
+                       graph_replays=res["graph_replays"], kernel=primary.kernel,
+                       launch_us=round(res["launch_us"], 2),
+                       settle_warmup_steps=res["settle_steps"]),
+        # traffic: HBM bytes per launch from the committed rocprofv3 FETCH_SIZE /
+        # WRITE_SIZE summary of this kernel (counters cannot be read in-process)
         "roofline": dict(res["roofline"], traffic=measured_traffic("rows_reg_kernel<float, 2, 4, 4>")),
         "cpu_baseline": cpu,
         "secondary": secondary,

@@ -47,6 +47,21 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
 #endif
 }
 
+// IEEE binary16 stored as raw 16-bit patterns; conversions through the
+// hardware's v_cvt_f32_f16 / v_cvt_f16_f32 (round to nearest even).
+struct f16_t {
+  uint16_t bits;
+};
+__device__ __forceinline__ float f16_to_f32(uint16_t b) {
+  return static_cast<float>(__builtin_bit_cast(_Float16, b));
+}
+__device__ __forceinline__ uint16_t f32_to_f16(float f) {
+  return __builtin_bit_cast(uint16_t, static_cast<_Float16>(f));
+}
+__device__ __forceinline__ uint32_t pack_f16x2(float lo, float hi) {
+  return static_cast<uint32_t>(f32_to_f16(lo)) | (static_cast<uint32_t>(f32_to_f16(hi)) << 16);
+}
+
 // ---------------------------------------------------------------------------
 // Element traits: how many elements one 16-byte vector holds and how to widen.
 // ---------------------------------------------------------------------------
@@ -60,6 +75,11 @@ template <> struct Elem<bf16_t> {
   static constexpr int kVec = 8;
   __device__ static float load1(const bf16_t* p) { return bf16_to_f32(p->bits); }
   __device__ static void store1(bf16_t* p, float v) { p->bits = f32_to_bf16(v); }
+};
+template <> struct Elem<f16_t> {
+  static constexpr int kVec = 8;
+  __device__ static float load1(const f16_t* p) { return f16_to_f32(p->bits); }
+  __device__ static void store1(f16_t* p, float v) { p->bits = f32_to_f16(v); }
 };
 
 // Loads 16 bytes (kVec elements) and widens them to fp32.
@@ -76,6 +96,15 @@ __device__ __forceinline__ void load_vec(const bf16_t* p, float* out) {
     out[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
   }
 }
+__device__ __forceinline__ void load_vec(const f16_t* p, float* out) {
+  uint4 v = *reinterpret_cast<const uint4*>(p);
+  uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    out[2 * i] = f16_to_f32(static_cast<uint16_t>(w[i]));
+    out[2 * i + 1] = f16_to_f32(static_cast<uint16_t>(w[i] >> 16));
+  }
+}
 __device__ __forceinline__ void store_vec(float* p, const float* v) {
   *reinterpret_cast<float4*>(p) = make_float4(v[0], v[1], v[2], v[3]);
 }
@@ -86,6 +115,10 @@ __device__ __forceinline__ void store_vec(bf16_t* p, const float* v) {
   o.z = pack_bf16x2(v[4], v[5]);
   o.w = pack_bf16x2(v[6], v[7]);
   *reinterpret_cast<uint4*>(p) = o;
+}
+__device__ __forceinline__ void store_vec(f16_t* p, const float* v) {
+  *reinterpret_cast<uint4*>(p) =
+      make_uint4(pack_f16x2(v[0], v[1]), pack_f16x2(v[2], v[3]), pack_f16x2(v[4], v[5]), pack_f16x2(v[6], v[7]));
 }
 
 // ---------------------------------------------------------------------------

@@ -132,10 +132,17 @@ __device__ __forceinline__ i32x4_t make_rsrc(const void* base, uint32_t bytes) {
 // 16 bytes per lane from buffer offset voff straight into LDS byte address
 // la + lane*16 (la wave-uniform; a 32-bit LDS address, so no generic-pointer
 // conversion is needed per load).
+// m0 is set and consumed inside this one asm statement, and no compiler-generated
+// code in these kernels reads or writes m0 (none appears in their ISA apart from
+// these pairs), so clang's warning that a reserved-register clobber is not
+// preserved does not apply here.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
 __device__ __forceinline__ void dma16(i32x4_t rsrc, uint32_t la, uint32_t voff) {
   asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
                ::"s"(la), "v"(voff), "s"(rsrc) : "memory", "m0");
 }
+#pragma clang diagnostic pop
 
 // Wave-instruction i of a wave fills LDS bytes [blk*1024, blk*1024 + 1024),
 // blk = wave * kPerWave + i; lane l writes bytes l*16 .. l*16+15 of that block, so

@@ -90,6 +90,7 @@ const char* kind_name(Kind k) {
     case Kind::SDPA: return "FusedScaledDotProductAttention";
     case Kind::DynSlice: return "DynamicSlice"; case Kind::DynUpdate: return "DynamicUpdateSlice";
     case Kind::Scatter: return "Scatter";
+    default: break;
   }
   return "?";
 }
@@ -221,7 +222,10 @@ extern "C" int ghip_backend_description(GHipBackend* b, char* buf, size_t buflen
 // Capabilities (capabilities.go:14-166): the GoMLX OpType names (without the
 // "OpType" prefix) this backend builds, and the dtypes it holds.  Ops of the
 // reference's list that are absent here: BatchNorm*, ConvGeneral,
-// ReduceWindow, SelectAndScatterMax and RNGBitGenerator.
+// ReduceWindow, SelectAndScatterMax and RNGBitGenerator.  The dtype list is the
+// reference's (capabilities.go:153-166): Float64 is not declared there, so it is
+// not declared here either, although the elementwise, reduce, scatter and copy
+// kernels accept it.
 extern "C" int ghip_backend_capabilities(char* buf, size_t buflen) {
   static const char kCaps[] =
       "functions=1;ops="
@@ -238,7 +242,7 @@ extern "C" int ghip_backend_capabilities(char* buf, size_t buflen) {
       "ArgMinMax,Gather,ScatterSum,ScatterMax,ScatterMin,DynamicSlice,DynamicUpdateSlice,"
       "FusedSoftmax,FusedLayerNorm,FusedGelu,FusedDense,FusedAttentionQKVProjection,"
       "FusedScaledDotProductAttention,While,If,Sort,Call;dtypes="
-      "Bool,Int8,Int16,Int32,Int64,Float16,BFloat16,Float32,Float64,Uint8,Uint16,Uint32,Uint64";
+      "Bool,Int8,Int16,Int32,Int64,Float16,BFloat16,Float32,Uint8,Uint16,Uint32,Uint64";
   if (buf && buflen) snprintf(buf, buflen, "%s", kCaps);
   return static_cast<int>(sizeof(kCaps) - 1);
 }
@@ -1515,14 +1519,14 @@ extern "C" GHipValue ghip_fn_fused_gelu(GHipFunction* f, GHipValue x, int exact,
     const GHipValue e = un(GHIP_UNARY_ERF, mul(x, inv_sqrt2));
     r = mul(mul(half, x), add(one, e));
   } else {
-    // 0.5 x (1 + tanh(u)), u = sqrt(2/pi) (x + 0.044715 x^3) with sqrt(2/pi) as the
-    // reference writes it, evaluated as x logistic(2u): the same function with one
-    // logistic in place of tanh and the (1 + .) / 2 around it (two ops fewer per
-    // element in a GEMM epilogue).
-    const GHipValue coeff = K(0.044715), two_s2pi = K(2.0 * 0.7978845608);
+    // (0.5 x) (1 + tanh(sqrt(2/pi) (x + 0.044715 ((x x) x)))), one op at a time in
+    // the reference's order (function.go:2343-2402): in 16-bit dtypes every op
+    // rounds, so the association decides the result bits.
+    const GHipValue half = K(0.5), one = K(1.0), coeff = K(0.044715), s2pi = K(0.7978845608);
     const GHipValue x3 = mul(mul(x, x), x);
     const GHipValue inner = add(x, mul(coeff, x3));
-    r = mul(x, un(GHIP_UNARY_LOGISTIC, mul(two_s2pi, inner)));
+    const GHipValue t = un(GHIP_UNARY_TANH, mul(s2pi, inner));
+    r = mul(mul(half, x), add(one, t));
   }
   return wrap(r, err, "FusedGelu");
 }

@@ -298,12 +298,18 @@ struct Lowerer {
     return N[v].a0.size() == 1 && N[v].a0[0] == r - 1;
   }
 
+  // The dtypes the row kernels take; a primitive chain in any other float dtype
+  // (Float64) stays unfused and runs as elementwise and reduce kernels.
+  static bool row_dtype(int dt) {
+    return dt == GHIP_DTYPE_FLOAT32 || dt == GHIP_DTYPE_BFLOAT16 || dt == GHIP_DTYPE_FLOAT16;
+  }
+
   // RMSNorm core: v = x * bcast(rsqrt(mean(x*x) + eps)).
   bool rms_core(int v, int* xo, double* eps) {
     if (!is_binary(v, GHIP_BINARY_MUL)) return false;
     for (int o = 0; o < 2; ++o) {
       const int x = N[v].in[o], rb = N[v].in[1 - o];
-      if (N[x].shape.dims != N[v].shape.dims || !dtype_is_float(N[x].shape.dtype)) continue;
+      if (N[x].shape.dims != N[v].shape.dims || !row_dtype(N[x].shape.dtype)) continue;
       int u;
       if (!row_broadcast(rb, N[x].shape, &u) || !is_unary(u, GHIP_UNARY_RSQRT)) continue;
       const int add = strip_reshape(N[u].in[0]);
@@ -342,7 +348,7 @@ struct Lowerer {
     const Node& n = N[v];
     if (n.kind != Kind::Binary) return;
     // RMSNorm, with or without gamma.
-    if (n.sub == GHIP_BINARY_MUL && dtype_is_float(n.shape.dtype) && n.shape.rank() >= 1) {
+    if (n.sub == GHIP_BINARY_MUL && row_dtype(n.shape.dtype) && n.shape.rank() >= 1) {
       int x, g;
       double eps;
       for (int o = 0; o < 2; ++o) {
@@ -357,7 +363,7 @@ struct Lowerer {
       }
     }
     // Softmax: exp(x - bmax) / bcast(sum(exp(x - bmax))).
-    if (n.sub == GHIP_BINARY_DIV && dtype_is_float(n.shape.dtype) && n.shape.rank() >= 1) {
+    if (n.sub == GHIP_BINARY_DIV && row_dtype(n.shape.dtype) && n.shape.rank() >= 1) {
       const int e = n.in[0];
       int s;
       if (is_unary(e, GHIP_UNARY_EXP) && row_broadcast(n.in[1], n.shape, &s) &&
@@ -370,7 +376,7 @@ struct Lowerer {
       }
     }
     // Log-softmax: (x - bmax) - bcast(log(sum(exp(x - bmax)))).
-    if (n.sub == GHIP_BINARY_SUB && dtype_is_float(n.shape.dtype) && n.shape.rank() >= 1) {
+    if (n.sub == GHIP_BINARY_SUB && row_dtype(n.shape.dtype) && n.shape.rank() >= 1) {
       const int d = n.in[0];
       int x, l;
       if (shifted_by_max(d, &x) && row_broadcast(n.in[1], n.shape, &l) && is_unary(l, GHIP_UNARY_LOG)) {
@@ -599,8 +605,8 @@ struct Lowerer {
     const int64_t n = r ? xs.dims[r - 1] : 1;
     const int64_t rows = n ? xs.size() / n : 0;
     const int dt = xs.dtype;
-    if (dt != GHIP_DTYPE_FLOAT32 && dt != GHIP_DTYPE_BFLOAT16)
-      return fail(GHIP_ERR_UNSUPPORTED, "row kernels take float32 / bfloat16");
+    if (!row_dtype(dt))
+      return fail(GHIP_ERR_UNSUPPORTED, fmt("row kernels take float32 / bfloat16 / float16, got %s", dtype_name(dt)).c_str());
     View x = materialize(xv, xs);
     View g, b;
     std::vector<int> rd{x.slot};

@@ -71,10 +71,17 @@ __device__ __forceinline__ i32x4_t make_rsrc(const void* base, uint32_t bytes) {
 }
 // 16 bytes per lane from buffer offset voff straight into LDS byte address
 // la + lane*16 (la wave-uniform).
+// m0 is set and consumed inside this one asm statement, and no compiler-generated
+// code in these kernels reads or writes m0 (none appears in their ISA apart from
+// these pairs), so clang's warning that a reserved-register clobber is not
+// preserved does not apply here.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
 __device__ __forceinline__ void dma16(i32x4_t rsrc, uint32_t la, uint32_t voff) {
   asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
                ::"s"(la), "v"(voff), "s"(rsrc) : "memory", "m0");
 }
+#pragma clang diagnostic pop
 
 // LDS tiles are [64 keys][128 d] bf16: 256-byte rows of 16 chunks of 16 B.
 // K: chunk kc of key row r sits at slot kc ^ (r & 15), so the 16 (8) rows of a

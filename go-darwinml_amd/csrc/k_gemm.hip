@@ -89,10 +89,17 @@ __global__ __launch_bounds__(WM* WN * 64, 1) void gemm_bf16_kernel(GemmParams p)
 constexpr int kBK32 = 32;
 
 // 32-bit LDS address form of dma16 (the generic-pointer form costs SGPRs here).
+// m0 is set and consumed inside this one asm statement, and no compiler-generated
+// code in these kernels reads or writes m0 (none appears in their ISA apart from
+// these pairs), so clang's warning that a reserved-register clobber is not
+// preserved does not apply here.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
 __device__ __forceinline__ void dma16_la(i32x4_t rsrc, uint32_t la, uint32_t voff) {
   asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
                ::"s"(la), "v"(voff), "s"(rsrc) : "memory", "m0");
 }
+#pragma clang diagnostic pop
 
 // R rows x 32 k fp32 tile, split over NW waves in 1 KiB DMA instructions.
 template <int R, bool KC, int NW>

@@ -20,7 +20,7 @@
 //     reduction);
 //   * anything else (unaligned rows, n not a multiple of the vector width, or
 //     rows beyond the register budget) takes a generic multi-pass kernel.
-// Statistics are fp32 for both fp32 and bf16 I/O.
+// Statistics are fp32 for fp32, bf16 and f16 I/O.
 #include <stdarg.h>
 
 #include "common.h"
@@ -68,6 +68,14 @@ __device__ __forceinline__ void unpack(const uint4& r, float* f, bf16_t) {
     f[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
   }
 }
+__device__ __forceinline__ void unpack(const uint4& r, float* f, f16_t) {
+  const uint32_t w[4] = {r.x, r.y, r.z, r.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    f[2 * i] = f16_to_f32(static_cast<uint16_t>(w[i]));
+    f[2 * i + 1] = f16_to_f32(static_cast<uint16_t>(w[i] >> 16));
+  }
+}
 __device__ __forceinline__ uint4 pack(const float* f, float) {
   return make_uint4(__float_as_uint(f[0]), __float_as_uint(f[1]), __float_as_uint(f[2]),
                     __float_as_uint(f[3]));
@@ -75,6 +83,10 @@ __device__ __forceinline__ uint4 pack(const float* f, float) {
 __device__ __forceinline__ uint4 pack(const float* f, bf16_t) {
   return make_uint4(pack_bf16x2(f[0], f[1]), pack_bf16x2(f[2], f[3]), pack_bf16x2(f[4], f[5]),
                     pack_bf16x2(f[6], f[7]));
+}
+__device__ __forceinline__ uint4 pack(const float* f, f16_t) {
+  return make_uint4(pack_f16x2(f[0], f[1]), pack_f16x2(f[2], f[3]), pack_f16x2(f[4], f[5]),
+                    pack_f16x2(f[6], f[7]));
 }
 
 // Sum / max over the WPR waves of a row (slot: which LDS pair to use, so two
@@ -229,17 +241,16 @@ __global__ __launch_bounds__(256) void rows_reg_kernel(RowParams p) {
     }
     // RMSNorm fp32: gamma is fetched with x, so its (L2) latency overlaps the
     // loads of x instead of following the statistics ([8192, 4096]: +3.5..5%).
-    // For bf16 and for LayerNorm (gamma and beta) the extra registers cost more
-    // than the overlap gains (measured -1..2%).
-    constexpr bool kEarlyParams = Elem<T>::kVec == 4 && OP == kRmsNorm;
-    uint4 gr[NV], br[NV];
+    // For 16-bit data and for LayerNorm (gamma and beta) the extra registers cost
+    // more than the overlap gains (measured -1..2%); beyond 4 vectors per lane
+    // they would halve the waves in flight.
+    constexpr bool kEarlyParams = Elem<T>::kVec == 4 && OP == kRmsNorm && NV <= 4;
+    uint4 gr[kEarlyParams ? NV : 1];
 #pragma unroll
     for (int i = 0; i < NV && kEarlyParams; ++i) {
       const int64_t c0 = (static_cast<int64_t>(i) * LANES + l) * VEC;
       gr[i] = (p.gamma && live[i]) ? *reinterpret_cast<const uint4*>(static_cast<const T*>(p.gamma) + c0)
                                    : make_uint4(0, 0, 0, 0);
-      br[i] = (p.beta && live[i]) ? *reinterpret_cast<const uint4*>(static_cast<const T*>(p.beta) + c0)
-                                  : make_uint4(0, 0, 0, 0);
     }
     // Unpacked once: the statistics passes and the store pass read these.
     float xf[NV][VEC];
@@ -338,10 +349,7 @@ __global__ __launch_bounds__(256) void rows_reg_kernel(RowParams p) {
           if constexpr (kEarlyParams) unpack(gr[i], gv, T{});
           else load_vec(g + c0, gv);
         }
-        if constexpr (B) {
-          if constexpr (kEarlyParams) unpack(br[i], bv, T{});
-          else load_vec(b + c0, bv);
-        }
+        if constexpr (B) load_vec(b + c0, bv);
 #pragma unroll
         for (int j = 0; j < VEC; ++j) {
           const float t = (x[j] - mean) * rstd;
@@ -478,6 +486,7 @@ static int dispatch_rows(int dtype, const RowParams& p, void* stream, GHipError*
   hipError_t e;
   if (dtype == GHIP_DTYPE_FLOAT32) e = launch_rows<float, OP>(p, s);
   else if (dtype == GHIP_DTYPE_BFLOAT16) e = launch_rows<bf16_t, OP>(p, s);
+  else if (dtype == GHIP_DTYPE_FLOAT16) e = launch_rows<f16_t, OP>(p, s);
   else return set_error(err, GHIP_ERR_UNSUPPORTED, "%s: dtype %d not supported", what, dtype);
   if (e != hipSuccess) return check_hip(e, err, what);
   return GHIP_OK;

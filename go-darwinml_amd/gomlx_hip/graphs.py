@@ -40,6 +40,16 @@ def softmax_chain(f, x):
     return f.Div(e, f.BroadcastInDim(z, s, list(range(r - 1))))
 
 
+def log_softmax_chain(f, x):
+    """Log-softmax over the last axis as primitives: (x - max) - log(sum(exp(x - max)))."""
+    s = f.OpShape(x)
+    r = len(s.dims)
+    keep = list(range(r - 1))
+    d = f.Sub(x, f.BroadcastInDim(f.ReduceMax(x, r - 1), s, keep))
+    z = f.ReduceSum(f.Exp(d), r - 1)
+    return f.Sub(d, f.BroadcastInDim(f.Log(z), s, keep))
+
+
 def dense(f, x, w):
     """x [..., din] @ w [din, dout] -> [..., dout] (DotGeneral, no batch axes)."""
     rx = len(f.OpShape(x).dims)

@@ -13,6 +13,7 @@ from ._lib import call
 _DT = {
     torch.float32: _lib.DT_FLOAT32,
     torch.bfloat16: _lib.DT_BFLOAT16,
+    torch.float16: _lib.DT_FLOAT16,
     torch.int32: _lib.DT_INT32,
     torch.int64: _lib.DT_INT64,
     torch.bool: _lib.DT_BOOL,

@@ -131,6 +131,27 @@ void orc_rmsnorm(const float* x, const float* gamma, double* y, int64_t rows, in
   }
 }
 
+/* RMSNorm with fp32 output and fp32 sequential statistics: the same arithmetic
+ * as orc_rmsnorm's ORC_MODE_F32SEQ (a plain loop over float32, the way a pure-Go
+ * backend would write it), stored as float32.  This is the CPU baseline that
+ * bench.py times; the parity tests use the fp64 forms. */
+void orc_rmsnorm_f32(const float* x, const float* gamma, float* y, int64_t rows, int64_t n,
+                     double eps) {
+#pragma omp parallel for schedule(static)
+  for (int64_t r = 0; r < rows; ++r) {
+    const float* xr = x + r * n;
+    float* yr = y + r * n;
+    float s = 0.0f;
+    for (int64_t i = 0; i < n; ++i) s += xr[i] * xr[i];
+    const float inv = 1.0f / sqrtf(s / (float)n + (float)eps);
+    for (int64_t i = 0; i < n; ++i) {
+      float o = xr[i] * inv;
+      if (gamma) o *= gamma[i];
+      yr[i] = o;
+    }
+  }
+}
+
 /* ---------------------------------------------------------------------------
  * DotGeneral.
  * Reference: dotGeneralOutputShape (mpsgraph/gomlx/dotgeneral.go:15-53) fixes the

@@ -68,6 +68,11 @@ void orc_layernorm(const float* x, const float* gamma, const float* beta, double
 void orc_rmsnorm(const float* x, const float* gamma, double* y, int64_t rows, int64_t n,
                  double eps, int mode);
 
+/* RMSNorm, fp32 output, fp32 sequential statistics (the CPU baseline's form;
+ * equal to orc_rmsnorm in ORC_MODE_F32SEQ rounded to float32). */
+void orc_rmsnorm_f32(const float* x, const float* gamma, float* y, int64_t rows, int64_t n,
+                     double eps);
+
 /* General DotGeneral with XLA semantics.  Output axis order is
  * [batch..., lhs free..., rhs free...].  Returns 0 on success, -1 on bad axes. */
 int orc_dot_general(const float* lhs, int lrank, const int64_t* ldims,

@@ -45,6 +45,7 @@ def lib():
         L.orc_softmax.argtypes = [_f32p, _f64p, _i64, _i64, _i64, _int, _int]
         L.orc_layernorm.argtypes = [_f32p, _vp, _vp, _f64p, _i64, _i64, ctypes.c_double, _int]
         L.orc_rmsnorm.argtypes = [_f32p, _vp, _f64p, _i64, _i64, ctypes.c_double, _int]
+        L.orc_rmsnorm_f32.argtypes = [_f32p, _vp, _f32p, _i64, _i64, ctypes.c_double]
         L.orc_dot_general.argtypes = [_f32p, _int, _i64p, _vp, _int, _vp, _int,
                                       _f32p, _int, _i64p, _vp, _int, _vp, _int, _f64p, _int]
         L.orc_dot_general.restype = _int
@@ -112,6 +113,16 @@ def rmsnorm(x, gamma=None, eps=1e-6, mode=MODE_F64) -> np.ndarray:
     g, gp = _opt(gamma)
     y = np.empty(x.shape, np.float64)
     lib().orc_rmsnorm(x, gp, y, x.size // n, n, eps, mode)
+    return y
+
+
+def rmsnorm_f32(x, gamma=None, eps=1e-6, out=None) -> np.ndarray:
+    """RMSNorm in fp32 end to end (fp32 sequential statistics, fp32 output)."""
+    x = _f32(x)
+    n = x.shape[-1]
+    g, gp = _opt(gamma)
+    y = np.empty(x.shape, np.float32) if out is None else out
+    lib().orc_rmsnorm_f32(x, gp, y, x.size // n, n, eps)
     return y
 
 
@@ -263,6 +274,55 @@ def activation(x, act: int) -> np.ndarray:
 def gelu(x, exact: bool) -> np.ndarray:
     """FusedGelu (function.go:2288-2408)."""
     return activation(x, ACT_GELU_EXACT if exact else ACT_GELU)
+
+
+def round_16(x, dtype: str) -> np.ndarray:
+    """fp32 -> bf16 / f16 (round to nearest even) -> fp32."""
+    x = np.asarray(x, np.float32)
+    if dtype == "f16":
+        with np.errstate(over="ignore"):
+            return x.astype(np.float16).astype(np.float32)
+    bits = f32_to_bf16_bits(x).astype(np.uint32) << 16
+    return bits.view(np.float32).reshape(x.shape)
+
+
+def _rounded_16_pair(t64, dtype: str, rel: float):
+    """The 16-bit roundings of t * (1 - rel) and t * (1 + rel): any value within
+    relative distance `rel` of t rounds (to nearest even) to one of the two, and
+    they differ only where t lies that close to a rounding midpoint."""
+    lo = round_16((t64 * (1.0 - rel)).astype(np.float32), dtype)
+    hi = round_16((t64 * (1.0 + rel)).astype(np.float32), dtype)
+    return lo, hi
+
+
+def gelu_chain_16(x, exact: bool, dtype: str = "bf16", rel: float = 1e-5):
+    """FusedGelu as the reference composes it (function.go:2343-2402 tanh form,
+    :2299-2341 exact form), with x, every op result and every scalar constant held
+    in the 16-bit dtype: each op is evaluated in fp32 on 16-bit operands and its
+    result rounded to nearest even, in the reference's order.  The scalar constants
+    are float32 values converted to the dtype (makeScalarConst, function.go:210-231).
+    The transcendental (tanh / erf) step is the exact value rounded to the dtype,
+    evaluated by any routine within relative error `rel`: near a rounding midpoint
+    either side is allowed, so two results come back (lo, hi: equal everywhere
+    else).  Returns float32 arrays."""
+    x = round_16(x, dtype)
+    np_err = np.seterr(over="ignore", invalid="ignore")  # x^3 overflows for |x| >~ 2^42, as in the graph
+    r = lambda a: round_16(a, dtype)  # noqa: E731
+    c = lambda v: r(np.float32(v))    # noqa: E731
+    half, one = c(0.5), c(1.0)
+    if exact:
+        xs = r(x * c(0.7071067811865475))
+        from scipy.special import erf
+        tl, th = _rounded_16_pair(erf(xs.astype(np.float64)), dtype, rel)
+    else:
+        x3 = r(r(x * x) * x)
+        inner = r(x + r(c(0.044715) * x3))
+        scaled = r(c(0.7978845608) * inner)
+        tl, th = _rounded_16_pair(np.tanh(scaled.astype(np.float64)), dtype, rel)
+    hx = r(half * x)
+    out = r(hx * r(one + tl)), r(hx * r(one + th))
+    np.seterr(**np_err)
+    return out
 
 
 def dense(x, w, bias=None, act: int = ACT_NONE) -> np.ndarray:

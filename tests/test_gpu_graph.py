@@ -280,6 +280,19 @@ def test_graph_softmax_chain_and_rmsnorm_chain(be):
     assert rel_err(y, orc.rmsnorm(x, g, 1e-6)) <= 1e-5
 
 
+@pytest.mark.parametrize("dt", [F32, BF16])
+def test_graph_log_softmax_chain(be, dt):
+    """The primitive log-softmax chain (one fused row kernel) at configs[0]'s shape."""
+    x = synth.normal(1001, (4096, 1024), std=2.0)
+    if dt == BF16:
+        x = synth.round_bf16(x)
+    (y,) = run(be, lambda f, a: [graphs.log_softmax_chain(f, a)],
+               [(x if dt == F32 else synth.to_bf16_bits(x), make_shape(dt, 4096, 1024))])
+    ref = orc.log_softmax(x)
+    # bf16: one rounding of the fp32 result (RMS-floored)
+    assert rel_err(y, ref) <= (1e-5 if dt == F32 else 2.0 ** -8 + 1e-5)
+
+
 def test_graph_dot_general_layouts(be):
     a = synth.round_bf16(synth.normal(3001, (2, 64, 96), std=0.125))
     b = synth.round_bf16(synth.normal(3002, (96, 2, 80), std=0.125))
@@ -481,17 +494,39 @@ def test_transformer_block_small_stagewise(be):
     assert norm_err(G["out"], exact) <= 1e-2
 
 
+def _tb_reference_tokens(cfg, P, b, toks):
+    """fp64 block output at tokens `toks` of batch row b: K and V for the tokens up
+    to the last one asked for, then attention, the O projection and the FFN for
+    the asked tokens only (each token sees keys 0..t)."""
+    S, d, H, Dh = cfg.seq, cfg.d_model, cfg.heads, cfg.head_dim
+    last = max(toks) + 1
+    x = orc.gather_rows(P["embedding"], P["ids"][b, :last]).astype(np.float64)
+    h = orc.rmsnorm(x.astype(np.float32), P["g_attn"], cfg.eps)
+    proj = lambda a, w: orc.dot_general(np.asarray(a, np.float32), [a.ndim - 1], [], P[w], [0], [])
+    heads = lambda t: np.ascontiguousarray(t.reshape(1, -1, H, Dh).transpose(0, 2, 1, 3), np.float32)
+    k, v = heads(proj(h, "wk")), heads(proj(h, "wv"))
+    q = heads(proj(h[toks], "wq"))
+    a = np.concatenate([orc.sdpa(q[:, :, i:i + 1], k[:, :, :t + 1], v[:, :, :t + 1], scale=Dh ** -0.5, causal=False)
+                        for i, t in enumerate(toks)], axis=2)
+    x2 = x[toks] + proj(a.transpose(0, 2, 1, 3).reshape(len(toks), d), "wo")
+    h2 = orc.rmsnorm(x2.astype(np.float32), P["g_ffn"], cfg.eps)
+    gate, up = proj(h2, "w_gate"), proj(h2, "w_up")
+    return x2 + proj(gate / (1.0 + np.exp(-gate)) * up, "w_down")
+
+
 def test_transformer_block_config_sampled(be):
     """BASELINE configs[4] end to end (ids [8,1024], d_model 2048, 16 heads,
-    FFN 8192), checked on batch row 0 against the oracle composition."""
+    FFN 8192), checked against the fp64 oracle composition on 12 tokens of every
+    one of the 8 batch rows (first, last and seeded positions in between)."""
     cfg = graphs.TransformerBlockConfig()
     P = _tb_inputs(cfg)
     ex, y = _tb_run(be, cfg, P)
     assert np.all(np.isfinite(y))
-    one = graphs.TransformerBlockConfig(batch=1)
-    P1 = dict(P, ids=P["ids"][:1])
-    exact = _tb_reference(one, P1, emulate_bf16=False)
-    assert norm_err(y[:1], exact) <= 1e-2
+    for b in range(cfg.batch):
+        mid = synth.uniform_int(5100 + b, (10,), 1, cfg.seq - 1)
+        toks = sorted({0, cfg.seq - 1, *map(int, mid)})
+        exact = _tb_reference_tokens(cfg, P, b, toks)
+        assert norm_err(y[b, toks], exact) <= 1e-2, (b, toks)
 
 
 def test_reshape_of_strided_views(be):

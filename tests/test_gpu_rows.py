@@ -28,6 +28,16 @@ def bf16_ulps(got_bf16: torch.Tensor, ref: np.ndarray) -> int:
     return int(np.max(np.abs(ordered(g) - ordered(r)))) if g.size else 0
 
 
+def f16_ulps(got_f16: torch.Tensor, ref: np.ndarray) -> int:
+    """Max distance in float16 ulps between a float16 result and the fp64 reference
+    rounded to float16 (numpy's conversion rounds to nearest even)."""
+    g = got_f16.view(torch.int16).cpu().numpy().astype(np.int32)
+    r = ref.astype(np.float16).view(np.int16).astype(np.int32)
+    def ordered(b):
+        return np.where(b < 0, -(b & 0x7FFF), b)
+    return int(np.max(np.abs(ordered(g) - ordered(r)))) if g.size else 0
+
+
 def to_dev(a, dev, dtype=torch.float32):
     return torch.from_numpy(np.ascontiguousarray(a)).to(dev).to(dtype)
 
@@ -191,3 +201,48 @@ def test_norm_invariants_full_size(cuda):
     y = ops.layernorm(x, None, None, 0.0).double()
     assert torch.max(torch.abs(y.mean(-1))).item() < 1e-5
     assert torch.max(torch.abs(y.var(-1, unbiased=False) - 1)).item() < 1e-5
+
+
+# ---------------------------------------------------------------- float16 (declared by the reference)
+@pytest.mark.parametrize("n", [1024, 4096, 20000])
+def test_softmax_and_log_softmax_f16(cuda, n):
+    x = synth.normal(1600 + n, (4096 if n == 1024 else 33, n), std=2.0).astype(np.float16).astype(np.float32)
+    xd = to_dev(x, cuda, torch.float16)
+    assert f16_ulps(ops.softmax(xd), orc.softmax(x)) <= 1
+    # log-softmax values reach |y| ~ 20 where an f16 ulp is 2^-6: one rounding of
+    # the fp32 result, RMS-floored
+    y = ops.softmax(xd, log=True).float().cpu().numpy()
+    assert rel_err(y, orc.log_softmax(x)) <= 2.0 ** -11 + 1e-5
+
+
+def test_norms_config_f16(cuda):
+    """configs[1] shape in float16: RMSNorm within one f16 ulp of the rounded truth,
+    LayerNorm within one f16 rounding (RMS-floored)."""
+    x = synth.normal(2001, (8192, 4096)).astype(np.float16).astype(np.float32)
+    g = synth.uniform_f32(2002, (4096,), 0.5, 1.5).astype(np.float16).astype(np.float32)
+    b = synth.normal(2003, (4096,), std=0.1).astype(np.float16).astype(np.float32)
+    xd, gd, bd = (to_dev(a, cuda, torch.float16) for a in (x, g, b))
+    assert f16_ulps(ops.rmsnorm(xd, gd, 1e-6), orc.rmsnorm(x, g, 1e-6)) <= 1
+    y = ops.layernorm(xd, gd, bd, 1e-5).float().cpu().numpy()
+    assert rel_err(y, orc.layernorm(x, g, b, 1e-5)) <= 2.0 ** -11 + 1e-5
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("n", [4096, 32768])
+def test_norms_16bit_odd_rows(cuda, dtype, n):
+    """Row counts that leave the last workgroup partly empty, at widths that take
+    2 waves per row (n 4096) and 16 vectors per lane over 4 waves (n 32768)."""
+    rows = 13
+    x = synth.normal(2400 + n, (rows, n), std=1.5, mean=0.25)
+    g = synth.uniform_f32(2500 + n, (n,), 0.5, 1.5)
+    b = synth.normal(2600 + n, (n,), std=0.1)
+    if dtype == torch.bfloat16:
+        x, g, b = synth.round_bf16(x), synth.round_bf16(g), synth.round_bf16(b)
+        ulps, tol = bf16_ulps, BF16_TOL
+    else:
+        x, g, b = (a.astype(np.float16).astype(np.float32) for a in (x, g, b))
+        ulps, tol = f16_ulps, 2.0 ** -11 + 1e-5
+    xd, gd, bd = (to_dev(a, cuda, dtype) for a in (x, g, b))
+    assert ulps(ops.rmsnorm(xd, gd, 1e-6), orc.rmsnorm(x, g, 1e-6)) <= 1
+    y = ops.layernorm(xd, gd, bd, 1e-5).float().cpu().numpy()
+    assert rel_err(y, orc.layernorm(x, g, b, 1e-5)) <= tol

@@ -113,6 +113,34 @@ def test_softmax_chain_and_fused_softmax(be):
     assert "reduce" not in p
 
 
+@pytest.mark.parametrize("dt", [F32, BF16, dtypes.Float16])
+def test_log_softmax_chain_is_fused(be, dt):
+    def build(f):
+        x = f.Parameter("x", make_shape(dt, 4096, 1024))
+        return [graphs.log_softmax_chain(f, x)]
+    p = plan_of(be, build)
+    assert p.count("log_softmax_rows") == 1, p
+    assert "(fused primitive log-softmax chain)" in p
+    assert "reduce" not in p and "fused_elementwise" not in p
+
+
+def test_float16_chains_fuse_and_float64_chains_stay_unfused(be):
+    """The row kernels take f32 / bf16 / f16; an f64 chain (a dtype the reference
+    does not declare) must still compile, as plain reduce + elementwise kernels."""
+    def build(dt):
+        def b(f):
+            x = f.Parameter("x", make_shape(dt, 64, 256))
+            g = f.Parameter("g", make_shape(dt, 256))
+            return [graphs.softmax_chain(f, x), graphs.rms_norm(f, x, g, 1e-6), graphs.log_softmax_chain(f, x)]
+        return b
+    p = plan_of(be, build(dtypes.Float16))
+    assert "softmax_rows float16" in p and "rmsnorm_rows float16" in p and "log_softmax_rows float16" in p
+    p = plan_of(be, build(dtypes.Float64))
+    assert "_rows" not in p and "reduce" in p, p
+    with pytest.raises(BackendError, match="row kernels take"):
+        plan_of(be, lambda f: [f.FusedSoftmax(f.Parameter("x", make_shape(dtypes.Float64, 4, 8)), 1)])
+
+
 def test_softmax_other_axis_moves_axis_last(be):
     def build(f):
         x = f.Parameter("x", make_shape(F32, 8, 16, 32))
@@ -301,7 +329,9 @@ def test_capabilities_match_reference_list_and_methods():
     assert caps.operations == _REFERENCE_OPS - _ABSENT
     # every declared op is a Function method of the same name
     assert [op for op in caps.operations if not hasattr(Function, op)] == []
-    assert {"Float32", "BFloat16", "Float16", "Bool", "Int32", "Int64", "Uint8"} <= caps.dtypes
+    # the reference's dtype list exactly (capabilities.go:153-166): no Float64
+    assert caps.dtypes == {"Float32", "Float16", "Bool", "Int8", "Int16", "Int32", "Int64", "Uint8",
+                           "Uint16", "Uint32", "Uint64", "BFloat16"}
 
 
 def test_pad_and_logical_reduce_shapes():

@@ -135,6 +135,19 @@ def test_rmsnorm_invariants():
     assert np.allclose(y, [[3 / r, 8 / r]], atol=1e-12)
 
 
+def test_rmsnorm_f32_output_form():
+    """The CPU baseline's fp32 form: identical to the fp32-sequential mode, within
+    fp32 rounding of the fp64 truth, and the hand-computed row [3, 4]."""
+    x = synth.normal(22, (64, 1024), std=1.5)
+    g = synth.uniform_f32(23, (1024,), 0.5, 1.5)
+    y = orc.rmsnorm_f32(x, g, 1e-6)
+    assert y.dtype == np.float32
+    assert np.array_equal(y, orc.rmsnorm(x, g, 1e-6, mode=orc.MODE_F32SEQ).astype(np.float32))
+    assert np.max(np.abs(y - orc.rmsnorm(x, g, 1e-6))) < 1e-5
+    y = orc.rmsnorm_f32(np.array([[3.0, 4.0]], np.float32), np.array([1.0, 2.0], np.float32), 0.0)
+    assert np.allclose(y, [[3 / np.sqrt(12.5), 8 / np.sqrt(12.5)]], atol=1e-6)
+
+
 DOT_LAYOUTS = [
     # (lhs shape, lc, lb, rhs shape, rc, rb)
     ((5, 7), [1], [], (7, 3), [0], []),
@@ -356,3 +369,41 @@ def test_scatter_general_invariants():
                 for b in range(2):
                     want[idx[1, i, j], a, idx[0, i, j] + b] += upd[i, a, j, b]
     assert np.array_equal(got, want)
+
+
+def _all_bf16(limit=None):
+    x = (np.arange(65536, dtype=np.uint32) << 16).view(np.float32)
+    x = x[np.isfinite(x)]
+    return x if limit is None else x[np.abs(x) <= limit]
+
+
+def test_gelu_chain_16_hand_computed():
+    """The per-op bf16 chain at points worked by hand.  bf16 constants:
+    0.044715 -> 0.044677734375, sqrt(2/pi) 0.7978845608 -> 0.796875.
+    x = -3: x^3 = -27, 0.0446777 * -27 = -1.2063 -> -1.203125, inner -4.203125 ->
+    -4.1875 (tie, even), scaled -3.3369 -> -3.34375, tanh = -0.99751 -> -0.99609375,
+    1 + t = 2^-8, 0.5 x = -1.5, result -1.5 * 2^-8 = -0.005859375.
+    x = 1: inner 1.0447 -> 1.046875, scaled 0.83423 -> 0.8359375, tanh 0.68366 ->
+    0.68359375, 1 + t = 1.68359375 -> 1.6875 (tie, even), result 0.84375.
+    x = -4: scaled -> -5.96875 (bf16), tanh rounds to -1, so the result is -0."""
+    x = np.array([-3.0, 1.0, -4.0], np.float32)
+    lo, hi = orc.gelu_chain_16(x, False)
+    assert lo.tolist() == hi.tolist() == [-0.005859375, 0.84375, -0.0]
+    assert np.signbit(lo[2])
+
+
+def test_gelu_chain_16_tracks_exact_gelu():
+    """Over every bf16 input with |x| <= 8 the chain stays within |x| 2^-7 of the
+    fp64 GELU (both forms), while the tanh form with its cubic term dropped leaves
+    that bound by 2x; only near a rounding midpoint of erf is the step ambiguous."""
+    x = _all_bf16(8.0)
+    for exact in (False, True):
+        lo, hi = orc.gelu_chain_16(x, exact)
+        ref = orc.gelu(x.astype(np.float64), exact)
+        for r in (lo, hi):
+            assert np.all(np.abs(r - ref) <= np.abs(x) * 2.0 ** -7 + 2.0 ** -133)
+    xx = x.astype(np.float64)
+    no_cubic = 0.5 * xx * (1 + np.tanh(0.7978845608 * xx))
+    assert np.max(np.abs(no_cubic - orc.gelu(xx, False)) / (np.abs(xx) * 2.0 ** -7 + 2.0 ** -133)) > 2
+    lo, hi = orc.gelu_chain_16(_all_bf16(), False)
+    assert np.array_equal(lo.view(np.uint32), hi.view(np.uint32))   # tanh never lands near a midpoint
