@@ -470,6 +470,7 @@ def main():
                 entry["executed"] = {"achieved": round(ex_tf, 2), "unit": "TFLOP/s",
                                      "frac": round(ex_tf / case.peak, 4)}
             secondary.append(entry)
+            print(f"bench: {name} {entry['value']} {entry['unit']}", file=sys.stderr, flush=True)
             del case
             torch.cuda.empty_cache()
     cpu = None if args.no_cpu else cpu_baseline()
