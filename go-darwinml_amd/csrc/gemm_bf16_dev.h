@@ -181,6 +181,19 @@ struct OperandTile {
     }
     step = static_cast<uint32_t>(kRPI * (KC ? s_mn : s_k) * 2);
   }
+  // Instruction i of this wave's share (see issue()).
+  template <bool FULL>
+  __device__ __forceinline__ void issue_one(i32x4_t rs, uint32_t lds, int wave, int lane, int k_left, int i) const {
+    const uint32_t v = voff[i & 1] + static_cast<uint32_t>(i & ~1) * step;
+    if constexpr (FULL) {
+      dma16(rs, lds + (wave * kPerWave + i) * 1024, v);
+    } else {
+      const int r = row_of(wave, i, lane);
+      const int c = chunk_of(wave, i, lane);
+      const bool ok = KC ? (r < mn_valid && c * 8 < k_left) : (r < k_left && c * 8 < mn_valid);
+      dma16(rs, lds + (wave * kPerWave + i) * 1024, ok ? v : kOffOOB);
+    }
+  }
   // lds: LDS byte address of the tile.  FULL: the whole tile lies inside the
   // operand (no per-lane masks); otherwise out-of-range rows and k-chunks read
   // zeros.
@@ -222,10 +235,141 @@ __device__ __forceinline__ bf16x8_t frag_mn(const uint16_t* lds, int nbase, int 
   return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
 }
 
+// Half h (k + 0..3 or k + 4..7) of frag_mn's fragment: one transpose read.
+template <int R>
+__device__ __forceinline__ bf16x4_t frag_mn_half(const uint16_t* lds, int nbase, int s, int lane, int h) {
+  const int kl = 16 * s + 8 * (lane >> 5) + ((lane & 15) >> 2);
+  const int nl = nbase + 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+  const uint16_t* p0 = lds + kl * R + (((nl >> 3) ^ swz_n(kl)) * 8) + (nl & 7) + h * 4 * R;
+  return __builtin_amdgcn_ds_read_tr16_b64_v4bf16((GHIP_LDS bf16x4_t*)(p0));
+}
+
 template <bool B>
 struct BoolC {
   static constexpr bool value = B;
 };
+template <int V>
+struct IntC {
+  static constexpr int value = V;
+};
+
+// One 32x32x16 MFMA on 16-bit operands held as raw bits: bf16, or IEEE f16 when
+// F16 (the same operand layout; gfx950 has both instructions).
+template <bool F16>
+__device__ __forceinline__ f32x16_t mma16(const bf16x8_t& a, const bf16x8_t& b, const f32x16_t& c) {
+  if constexpr (F16) {
+    typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8_t, a), __builtin_bit_cast(f16x8_t, b), c,
+                                                  0, 0, 0);
+  } else {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+  }
+}
+
+// sched_barrier(0): the machine scheduler moves nothing across this point, so
+// the source order of MFMAs, LDS reads and loads is the issue order.
+__device__ __forceinline__ void sched_fence() { __builtin_amdgcn_sched_barrier(0); }
+
+// Epilogue through LDS, shared by both cores.  acc[i][j] holds the transposed
+// 32x32 block of wave (wm, wn): lane l, value v -> row m = l % 32, columns
+// n = (v / 4) * 8 + (l / 32) * 4 + v % 4, so storing it directly writes 16 bytes
+// into each of 32 rows per instruction.  Instead the tile is staged in LDS (as
+// Epi::Stage values, 16-byte chunk c of row r at slot c ^ (r % chunks-per-row))
+// and read back row-wise: each lane takes CH = 16 / sizeof(Stage) consecutive
+// columns of one row, so a wave instruction covers whole rows.  Tiles whose stage
+// exceeds the main loop's LDS take 2 passes of half the rows.  The epilogue's own
+// operands for the next row chunk are fetched (prefetch) before the current chunk
+// is stored.
+template <int BM, int BN, int WM, int WN, int NB, class Epi, int kLdsHalfwords, int FM, int FNB>
+__device__ __forceinline__ void tile_epilogue(const GemmParams& p, const Epi& epi, uint16_t (&smem)[kLdsHalfwords],
+                                              const f32x16_t (&acc)[FM][FNB], int64_t bb, int64_t m0, int64_t n0,
+                                              bool mn_full, int lane, int wm, int wn) {
+  constexpr int kLdsBytes = kLdsHalfwords * 2;
+  constexpr int NW = WM * WN;
+  constexpr int TM = BM / WM, TN = BN / WN;
+  constexpr int FN = TN / 32;
+  static_assert(FM == TM / 32 && FNB == NB * FN, "accumulator shape");
+  using Stage = typename Epi::Stage;
+  constexpr int ES = sizeof(Stage);
+  constexpr int CH = 16 / ES;
+  constexpr int kStageBytes = NB * BM * BN * ES;
+  constexpr int P = kStageBytes <= kLdsBytes ? 1 : 2;  // passes
+  static_assert(kStageBytes <= P * kLdsBytes && BM % (32 * P) == 0,
+                "stage must fit the LDS in at most 2 passes of whole 32-row blocks");
+  constexpr int PR = BM / P;          // rows per pass
+  constexpr int CPR = BN * ES / 16;   // 16-byte chunks per staged row (per product)
+  constexpr int NT = NW * 64;
+  static_assert((CPR & (CPR - 1)) == 0 && NT % CPR == 0 && PR % (NT / CPR) == 0, "row-chunk split");
+  constexpr int RPI = NT / CPR;  // rows per read iteration
+  constexpr int NIT = PR / RPI;  // read iterations per pass
+  Stage* stg = reinterpret_cast<Stage*>(smem);
+  auto slot = [](int r, int c) { return c ^ (r & (CPR - 1)); };
+
+  auto epilogue = [&](auto full_c) {
+    constexpr bool FULL = decltype(full_c)::value;
+#pragma unroll
+    for (int pass = 0; pass < P; ++pass) {
+      // LDS is free: every wave has finished its main-loop reads (or the
+      // previous pass's row reads).
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      __syncthreads();
+#pragma unroll
+      for (int i = 0; i < FM; ++i) {
+        const int r = wm * TM + i * 32 + (lane & 31);
+        if ((wm * TM + i * 32) / PR != pass) continue;  // uniform over the wave
+        const int rl = r - pass * PR;
+#pragma unroll
+        for (int h = 0; h < NB; ++h)
+#pragma unroll
+          for (int j = 0; j < FN; ++j)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+              const int n = wn * TN + j * 32 + q * 8 + (lane >> 5) * 4;
+              Stage w[4];
+#pragma unroll
+              for (int e = 0; e < 4; ++e) w[e] = Epi::stage(acc[i][h * FN + j][q * 4 + e]);
+              const int c = n * ES / 16, off = (n * ES) % 16;
+              char* dst = reinterpret_cast<char*>(stg + (h * PR + rl) * BN) + slot(rl, c) * 16 + off;
+              if constexpr (ES == 2) {
+                struct __attribute__((aligned(8))) W8 { Stage x[4]; };
+                *reinterpret_cast<W8*>(dst) = W8{{w[0], w[1], w[2], w[3]}};
+              } else {
+                struct __attribute__((aligned(16))) W16 { Stage x[4]; };
+                *reinterpret_cast<W16*>(dst) = W16{{w[0], w[1], w[2], w[3]}};
+              }
+            }
+      }
+      __syncthreads();
+      const int t = threadIdx.x;
+      const int cl = t % CPR;
+      const int64_t n = n0 + cl * CH;
+      typename Epi::Pre pre[2];
+      auto row_of = [&](int it) { return pass * PR + it * RPI + t / CPR; };
+      if (FULL || m0 + row_of(0) < p.M) epi.template prefetch<FULL>(bb, m0 + row_of(0), n, pre[0]);
+#pragma unroll
+      for (int it = 0; it < NIT; ++it) {
+        if (it + 1 < NIT && (FULL || m0 + row_of(it + 1) < p.M))
+          epi.template prefetch<FULL>(bb, m0 + row_of(it + 1), n, pre[(it + 1) & 1]);
+        const int rl = it * RPI + t / CPR;
+        const int64_t m = m0 + pass * PR + rl;
+        if (!FULL && m >= p.M) continue;
+        Stage v0[CH], v1[CH];
+        struct __attribute__((aligned(16))) C16 { Stage x[CH]; };
+        const C16 a0 = *reinterpret_cast<const C16*>(reinterpret_cast<const char*>(stg + rl * BN) + slot(rl, cl) * 16);
+        const C16 a1 = *reinterpret_cast<const C16*>(reinterpret_cast<const char*>(stg + ((NB - 1) * PR + rl) * BN) +
+                                                     slot(rl, cl) * 16);
+#pragma unroll
+        for (int e = 0; e < CH; ++e) {
+          v0[e] = a0.x[e];
+          v1[e] = a1.x[e];
+        }
+        epi.template store<FULL>(bb, m, n, v0, v1, pre[it & 1]);
+      }
+    }
+  };
+  if (mn_full) epilogue(BoolC<true>{});
+  else epilogue(BoolC<false>{});
+}
 
 // One BM x BN output tile per workgroup of WM x WN waves.  The epilogue functor:
 //   Stage                        how one product value is held in LDS (uint16_t:
@@ -239,7 +383,7 @@ struct BoolC {
 //                                A.B, v1 from A.B1 when NB == 2 (else v1 == v0);
 //                                FULL: the whole tile lies inside the output (no
 //                                column bounds), else columns >= N are ignored.
-template <int BM, int BN, int WM, int WN, bool A_K, bool B_K, int NB, class Epi>
+template <int BM, int BN, int WM, int WN, bool A_K, bool B_K, int NB, class Epi, bool F16 = false>
 __device__ __forceinline__ void gemm_bf16_body(const GemmParams& p, const Epi& epi) {
   static_assert(NB == 1 || NB == 2, "one or two right operands");
   constexpr int NW = WM * WN;
@@ -324,7 +468,7 @@ __device__ __forceinline__ void gemm_bf16_body(const GemmParams& p, const Epi& e
     for (int i = 0; i < FM; ++i)
 #pragma unroll
       for (int j = 0; j < NB * FN; ++j)
-        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb[buf][j], fa[buf][i], acc[i][j], 0, 0, 0);
+        acc[i][j] = mma16<F16>(fb[buf][j], fa[buf][i], acc[i][j]);
   };
 
   // Prologue: tiles 0 and 1 in flight, wait for tile 0.
@@ -362,95 +506,187 @@ __device__ __forceinline__ void gemm_bf16_body(const GemmParams& p, const Epi& e
   }
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
-  // Epilogue through LDS.  acc[i][j] holds the transposed 32x32 block: lane l,
-  // value v -> row m = l % 32, columns n = (v / 4) * 8 + (l / 32) * 4 + v % 4, so
-  // storing it directly writes 16 bytes into each of 32 rows per instruction.
-  // Instead the tile is staged in LDS (as Epi::Stage values, 16-byte chunk c of
-  // row r at slot c ^ (r % chunks-per-row)) and read back row-wise: each lane
-  // takes CH = 16 / sizeof(Stage) consecutive columns of one row, so a wave
-  // instruction covers whole rows.  Tiles whose stage exceeds the LDS take 2
-  // passes of half the rows.  The epilogue's own operands for the next row
-  // chunk are fetched (prefetch) before the current chunk is stored.
-  using Stage = typename Epi::Stage;
-  constexpr int ES = sizeof(Stage);
-  constexpr int CH = 16 / ES;
-  constexpr int kStageBytes = NB * BM * BN * ES;
-  constexpr int P = kStageBytes <= kLdsBytes ? 1 : 2;  // passes
-  static_assert(kStageBytes <= P * kLdsBytes && BM % (32 * P) == 0,
-                "stage must fit the LDS in at most 2 passes of whole 32-row blocks");
-  constexpr int PR = BM / P;          // rows per pass
-  constexpr int CPR = BN * ES / 16;   // 16-byte chunks per staged row (per product)
-  constexpr int NT = NW * 64;
-  static_assert((CPR & (CPR - 1)) == 0 && NT % CPR == 0 && PR % (NT / CPR) == 0, "row-chunk split");
-  constexpr int RPI = NT / CPR;  // rows per read iteration
-  constexpr int NIT = PR / RPI;  // read iterations per pass
-  Stage* stg = reinterpret_cast<Stage*>(smem);
-  auto slot = [](int r, int c) { return c ^ (r & (CPR - 1)); };
+  tile_epilogue<BM, BN, WM, WN, NB>(p, epi, smem, acc, bb, m0, n0, mn_full, lane, wm, wn);
+}
 
-  auto epilogue = [&](auto full_c) {
-    constexpr bool FULL = decltype(full_c)::value;
+
+// 4-wave core: one 256 x 256 tile per workgroup of 2 x 2 waves, each wave a
+// 128 x 128 sub-tile (16 32x32 blocks, 256 accumulators per lane, so one wave per
+// SIMD).  Against the 8-wave core (128 x 64 per wave) a wave reads 8 KiB of LDS per
+// 16-deep k step for twice the MFMA work, which cuts the CU's LDS read traffic by
+// a third.  With one wave per SIMD nothing hides a stall, so the issue order is
+// fixed by sched_fence(): in each k16 step the 16 MFMAs alternate with the 12 LDS
+// reads of the next step's fragments (ordered so that the next step's first MFMAs
+// need only the first reads); in the last step of a k-tile, 8 MFMAs run, then the
+// wait for tile kt+1 and the barrier, then the remaining 8 MFMAs carry the 16
+// loads of tile kt+2 and the reads of tile kt+1's first step.  Products are
+// bit-identical to the 8-wave core (same MFMA, same k order per accumulator).
+template <bool A_K, bool B_K, class Epi, bool F16 = false>
+__device__ __forceinline__ void gemm_bf16_body4(const GemmParams& p, const Epi& epi) {
+  constexpr int BM = 256, BN = 256, WM = 2, WN = 2;
+  constexpr int NW = WM * WN;
+  constexpr int TM = BM / WM, TN = BN / WN;
+  constexpr int FM = TM / 32, FN = TN / 32;
+  constexpr int NS = kBK / 16;
+  using TA = OperandTile<BM, A_K, NW>;
+  using TB = OperandTile<BN, B_K, NW>;
+  constexpr int ND = TA::kPerWave + TB::kPerWave;  // loads per wave per k-tile
+  constexpr int kLdsBytes = 2 * BM * kBK * 2 + 2 * BN * kBK * 2;
+  __shared__ __attribute__((aligned(1024))) uint16_t smem[kLdsBytes / 2];
+  uint16_t(*sa)[BM * kBK] = reinterpret_cast<uint16_t(*)[BM * kBK]>(smem);
+  uint16_t(*sb)[BN * kBK] = reinterpret_cast<uint16_t(*)[BN * kBK]>(smem + 2 * BM * kBK);
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wm = wave / WN, wn = wave % WN;
+
+  int64_t bb;
+  int tm, tn;
+  map_tile(blockIdx.x, p.batch * p.tiles_m * p.tiles_n, p.tiles_m, p.tiles_n, bb, tm, tn);
+  const int64_t m0 = static_cast<int64_t>(tm) * BM, n0 = static_cast<int64_t>(tn) * BN;
+  const uint16_t* A0 = static_cast<const uint16_t*>(p.a) + bb * p.sa_b + m0 * p.sa_m;
+  const uint16_t* B0 = static_cast<const uint16_t*>(p.b) + bb * p.sb_b + n0 * p.sb_n;
+  const uint32_t a_left0 = p.a_extent - static_cast<uint32_t>(m0 * p.sa_m * 2);
+  const uint32_t b_left0 = p.b_extent - static_cast<uint32_t>(n0 * p.sb_n * 2);
+
+  TA ta;
+  TB tb;
+  ta.init(wave, lane, p.sa_m, p.sa_k, p.M - m0);
+  tb.init(wave, lane, p.sb_n, p.sb_k, p.N - n0);
+  const bool mn_full = m0 + BM <= p.M && n0 + BN <= p.N;
+  const int KT = static_cast<int>((p.K + kBK - 1) / kBK);
+  const uint32_t lds_a = static_cast<uint32_t>(reinterpret_cast<uint64_t>((GHIP_LDS void*)smem));
+  const uint32_t lds_b = lds_a + 2 * BM * kBK * 2;
+
+  f32x16_t acc[FM][FN];
 #pragma unroll
-    for (int pass = 0; pass < P; ++pass) {
-      // LDS is free: every wave has finished its main-loop reads (or the
-      // previous pass's row reads).
-      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-      __syncthreads();
+  for (int i = 0; i < FM; ++i)
 #pragma unroll
-      for (int i = 0; i < FM; ++i) {
-        const int r = wm * TM + i * 32 + (lane & 31);
-        if ((wm * TM + i * 32) / PR != pass) continue;  // uniform over the wave
-        const int rl = r - pass * PR;
+    for (int j = 0; j < FN; ++j)
 #pragma unroll
-        for (int h = 0; h < NB; ++h)
-#pragma unroll
-          for (int j = 0; j < FN; ++j)
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-              const int n = wn * TN + j * 32 + q * 8 + (lane >> 5) * 4;
-              Stage w[4];
-#pragma unroll
-              for (int e = 0; e < 4; ++e) w[e] = Epi::stage(acc[i][h * FN + j][q * 4 + e]);
-              const int c = n * ES / 16, off = (n * ES) % 16;
-              char* dst = reinterpret_cast<char*>(stg + (h * PR + rl) * BN) + slot(rl, c) * 16 + off;
-              if constexpr (ES == 2) {
-                struct __attribute__((aligned(8))) W8 { Stage x[4]; };
-                *reinterpret_cast<W8*>(dst) = W8{{w[0], w[1], w[2], w[3]}};
-              } else {
-                struct __attribute__((aligned(16))) W16 { Stage x[4]; };
-                *reinterpret_cast<W16*>(dst) = W16{{w[0], w[1], w[2], w[3]}};
-              }
-            }
+      for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
+
+  // Fragments [buffer][block][half]: a K-contiguous tile gives a fragment in one
+  // ds_read_b128, an MN-contiguous one in two transpose reads (one per half).
+  bf16x4_t fa[2][FM][2], fb[2][FN][2];
+  constexpr int RA = A_K ? 1 : 2, RB = B_K ? 1 : 2;  // LDS reads per fragment
+  constexpr int NR = FM * RA + FN * RB;               // LDS reads per k16 step
+  // Read r of step s (stage st) into buffer nb, in the order A0 B0 A1 B1 ...
+  auto read_op = [&](int st, int s, int nb, int r) {
+    const int blk = r / (RA + RB), q = r % (RA + RB);
+    if (q < RA) {
+      if constexpr (A_K) {
+        const bf16x8_t v = frag_kc(sa[st], wm * TM + blk * 32, s, lane);
+        fa[nb][blk][0] = __builtin_shufflevector(v, v, 0, 1, 2, 3);
+        fa[nb][blk][1] = __builtin_shufflevector(v, v, 4, 5, 6, 7);
+      } else {
+        fa[nb][blk][q] = frag_mn_half<BM>(sa[st], wm * TM + blk * 32, s, lane, q);
       }
-      __syncthreads();
-      const int t = threadIdx.x;
-      const int cl = t % CPR;
-      const int64_t n = n0 + cl * CH;
-      typename Epi::Pre pre[2];
-      auto row_of = [&](int it) { return pass * PR + it * RPI + t / CPR; };
-      if (FULL || m0 + row_of(0) < p.M) epi.template prefetch<FULL>(bb, m0 + row_of(0), n, pre[0]);
-#pragma unroll
-      for (int it = 0; it < NIT; ++it) {
-        if (it + 1 < NIT && (FULL || m0 + row_of(it + 1) < p.M))
-          epi.template prefetch<FULL>(bb, m0 + row_of(it + 1), n, pre[(it + 1) & 1]);
-        const int rl = it * RPI + t / CPR;
-        const int64_t m = m0 + pass * PR + rl;
-        if (!FULL && m >= p.M) continue;
-        Stage v0[CH], v1[CH];
-        struct __attribute__((aligned(16))) C16 { Stage x[CH]; };
-        const C16 a0 = *reinterpret_cast<const C16*>(reinterpret_cast<const char*>(stg + rl * BN) + slot(rl, cl) * 16);
-        const C16 a1 = *reinterpret_cast<const C16*>(reinterpret_cast<const char*>(stg + ((NB - 1) * PR + rl) * BN) +
-                                                     slot(rl, cl) * 16);
-#pragma unroll
-        for (int e = 0; e < CH; ++e) {
-          v0[e] = a0.x[e];
-          v1[e] = a1.x[e];
-        }
-        epi.template store<FULL>(bb, m, n, v0, v1, pre[it & 1]);
+    } else {
+      if constexpr (B_K) {
+        const bf16x8_t v = frag_kc(sb[st], wn * TN + blk * 32, s, lane);
+        fb[nb][blk][0] = __builtin_shufflevector(v, v, 0, 1, 2, 3);
+        fb[nb][blk][1] = __builtin_shufflevector(v, v, 4, 5, 6, 7);
+      } else {
+        fb[nb][blk][q - RA] = frag_mn_half<BN>(sb[st], wn * TN + blk * 32, s, lane, q - RA);
       }
     }
   };
-  if (mn_full) epilogue(BoolC<true>{});
-  else epilogue(BoolC<false>{});
+  // MFMA k of a step; blocks in order of max(i, j), so the first MFMAs of a step
+  // need only the first fragments read.
+  auto mfma_op = [&](int b, int k) {
+    constexpr int ord[16][2] = {{0, 0}, {0, 1}, {1, 0}, {1, 1}, {0, 2}, {1, 2}, {2, 0}, {2, 1},
+                                {2, 2}, {0, 3}, {1, 3}, {2, 3}, {3, 0}, {3, 1}, {3, 2}, {3, 3}};
+    const int i = ord[k][0], j = ord[k][1];
+    const bf16x8_t av = __builtin_shufflevector(fa[b][i][0], fa[b][i][1], 0, 1, 2, 3, 4, 5, 6, 7);
+    const bf16x8_t bv = __builtin_shufflevector(fb[b][j][0], fb[b][j][1], 0, 1, 2, 3, 4, 5, 6, 7);
+    acc[i][j] = mma16<F16>(bv, av, acc[i][j]);
+  };
+
+  auto run = [&](auto full_c) {
+    constexpr bool FULL = decltype(full_c)::value;
+    // Load d (0 .. ND-1) of this wave's share of k-tile kt into stage st.
+    auto dma = [&](int kt, int st, int d) {
+      const int64_t k0 = static_cast<int64_t>(kt) * kBK;
+      const int k_left = static_cast<int>(p.K - k0 < kBK ? p.K - k0 : kBK);
+      if (d < TA::kPerWave) {
+        const i32x4_t ra = make_rsrc(A0 + k0 * p.sa_k, a_left0 - static_cast<uint32_t>(k0 * p.sa_k * 2));
+        ta.template issue_one<FULL>(ra, lds_a + st * (BM * kBK * 2), wave, lane, k_left, d);
+      } else {
+        const i32x4_t rb = make_rsrc(B0 + k0 * p.sb_k, b_left0 - static_cast<uint32_t>(k0 * p.sb_k * 2));
+        tb.template issue_one<FULL>(rb, lds_b + st * (BN * kBK * 2), wave, lane, k_left, d - TA::kPerWave);
+      }
+    };
+    // Prologue: tiles 0 and 1 in flight, wait for tile 0.
+#pragma unroll
+    for (int d = 0; d < ND; ++d) dma(0, 0, d);
+    if (KT > 1) {
+#pragma unroll
+      for (int d = 0; d < ND; ++d) dma(1, 1, d);
+      asm volatile("s_waitcnt vmcnt(%0)" ::"n"(ND) : "memory");
+    } else {
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    }
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < NR; ++r) read_op(0, 0, 0, r);
+
+    // Tile kt in stage ST.  Tile kt+1 (read at its end) and tile kt+2 (loaded at
+    // its end) may not exist: uniform branches.
+    auto tile = [&](int kt, auto st_c) {
+      constexpr int ST = decltype(st_c)::value;
+      const bool nx = kt + 1 < KT, dm = kt + 2 < KT;
+#pragma unroll
+      for (int s = 0; s < NS; ++s) {
+        const int b = s & 1;
+        if (s + 1 < NS) {
+#pragma unroll
+          for (int k = 0; k < 16; ++k) {
+            mfma_op(b, k);
+            if (k < NR) read_op(ST, s + 1, b ^ 1, k);
+            sched_fence();
+          }
+        } else {
+#pragma unroll
+          for (int k = 0; k < 8; ++k) {
+            mfma_op(b, k);
+            sched_fence();
+          }
+          // Tile kt+1 has landed (this wave's loads; the barrier covers the other
+          // waves') and every wave is done reading stage ST (the barrier waits for
+          // the LDS reads), so tile kt+2 may refill it.
+          if (nx) {
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+            __syncthreads();
+          }
+          sched_fence();
+#pragma unroll
+          for (int k = 8; k < 16; ++k) {
+            mfma_op(b, k);
+            const int x = k - 8;
+            if (dm) {
+#pragma unroll
+              for (int d = x * ND / 8; d < (x + 1) * ND / 8; ++d) dma(kt + 2, ST, d);
+            }
+            if (nx) {
+#pragma unroll
+              for (int r = x * NR / 8; r < (x + 1) * NR / 8; ++r) read_op(ST ^ 1, 0, b ^ 1, r);
+            }
+            sched_fence();
+          }
+        }
+      }
+    };
+    for (int kt = 0; kt < KT; kt += 2) {
+      tile(kt, IntC<0>{});
+      if (kt + 1 < KT) tile(kt + 1, IntC<1>{});
+    }
+  };
+  if (mn_full && (p.K % kBK) == 0) run(BoolC<true>{});
+  else run(BoolC<false>{});
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+
+  tile_epilogue<BM, BN, WM, WN, 1>(p, epi, smem, acc, bb, m0, n0, mn_full, lane, wm, wn);
 }
 
 #endif  // __HIP__ || __HIPCC_RTC__

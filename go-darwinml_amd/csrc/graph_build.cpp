@@ -793,8 +793,9 @@ extern "C" GHipValue ghip_fn_dot_general(GHipFunction* f, GHipValue lhs, const i
     if (a->shape.dims[lca[i]] != b->shape.dims[rca[i]]) return c.fail(GHIP_ERR_INVALID_ARG, "contracting dims differ");
   for (int i = 0; i < nlb; ++i)
     if (a->shape.dims[lba[i]] != b->shape.dims[rba[i]]) return c.fail(GHIP_ERR_INVALID_ARG, "batch dims differ");
-  if (!dtype_is_float(a->shape.dtype) || a->shape.dtype == GHIP_DTYPE_FLOAT16 || a->shape.dtype == GHIP_DTYPE_FLOAT64)
-    return c.fail(GHIP_ERR_UNSUPPORTED, "dtype %s (float32 and bfloat16 are lowered)", dtype_name(a->shape.dtype));
+  if (!dtype_is_float(a->shape.dtype) || a->shape.dtype == GHIP_DTYPE_FLOAT64)
+    return c.fail(GHIP_ERR_UNSUPPORTED, "dtype %s (float32, bfloat16 and float16 are lowered)",
+                  dtype_name(a->shape.dtype));
   Node n{Kind::Dot};
   n.in = {lhs, rhs};
   n.a0 = lca; n.a1 = lba; n.a2 = rca; n.a3 = rba;

@@ -2049,10 +2049,12 @@ View Lowerer::emit_gemm_epilogue(int v, const std::vector<int>& mem, bool* fused
 
   // Tile shape: the precompiled kernels' choice for one operand; with two, a
   // 256 x (2 x 128) tile does the MMA work of one 256 x 256 tile.
+  // A single 256 x 256 product runs the 4-wave core (128 x 128 per wave).
   int BM = 128, BN = 128, WM = 2, WN = 2;
+  bool four_wave = false;
   const int64_t t256 = d.B * ((d.M + 255) / 256) * ((d.N + 255) / 256);
   if (NB == 1) {
-    if (d.M >= 256 && d.N >= 256 && t256 >= 128) BM = 256, BN = 256, WM = 2, WN = 4;
+    if (d.M >= 256 && d.N >= 256 && t256 >= 128) BM = 256, BN = 256, WM = 2, WN = 2, four_wave = true;
     else if (d.M >= 256 && d.N >= 128) BM = 256, BN = 128, WM = 2, WN = 2;
   } else if (d.M >= 256 && d.N >= 128) {
     BM = 256, BN = 128, WM = 2, WN = 4;
@@ -2109,9 +2111,12 @@ View Lowerer::emit_gemm_epilogue(int v, const std::vector<int>& mem, bool* fused
   src << "#pragma unroll\n    for (int e = 0; e < " << CHs << "; ++e)\n      if (FULL || n + e < a.N) o[e] = " << store_expr(odt, "r[e]")
       << ";\n  }\n};\n}  // namespace ghip\n";
   src << "extern \"C\" __global__ void __launch_bounds__(" << nt << ", 1) gemm_epilogue(ghip::GemmParams p, ghip::EpiArgs a) {\n"
-      << "  const ghip::GenEpi epi{a};\n"
-      << "  ghip::gemm_bf16_body<" << BM << ", " << BN << ", " << WM << ", " << WN << ", " << (ma ? "true" : "false") << ", "
-      << (mb ? "true" : "false") << ", " << NB << ">(p, epi);\n}\n";
+      << "  const ghip::GenEpi epi{a};\n";
+  if (four_wave)
+    src << "  ghip::gemm_bf16_body4<" << (ma ? "true" : "false") << ", " << (mb ? "true" : "false") << ">(p, epi);\n}\n";
+  else
+    src << "  ghip::gemm_bf16_body<" << BM << ", " << BN << ", " << WM << ", " << WN << ", " << (ma ? "true" : "false") << ", "
+        << (mb ? "true" : "false") << ", " << NB << ">(p, epi);\n}\n";
   RtcKernel kern;
   if (rtc_get(be, src.str(), "gemm_epilogue", &kern, err) != GHIP_OK) {
     failed = true;

@@ -1,8 +1,9 @@
 // Batched GEMM for DotGeneral: c[b] = a[b] (M x K) * b[b] (K x N), fp32 accumulate.
 //
-// bf16 path (the MFMA path the metric is quoted on): the core lives in
+// bf16 / f16 path (the MFMA path the metric is quoted on): the cores live in
 // gemm_bf16_dev.h (shared with the Compile-time generated epilogue GEMMs); the
-// kernels here instantiate it with a plain store epilogue.
+// kernels here instantiate them with a plain store epilogue.  256 x 256 tiles
+// run the 4-wave core, smaller tiles the 8- / 4-wave 128 x 64 core.
 // fp32 path: v_mfma_f32_32x32x2f32 over LDS-DMA tiles (below).
 // Anything the vector paths cannot address (odd strides, unaligned bases,
 // negative strides, > 2 GiB per batch slice) runs a generic LDS-tiled kernel.
@@ -17,19 +18,25 @@ template <>
 __device__ __forceinline__ void store_out<float>(float* p, float v) { *p = v; }
 template <>
 __device__ __forceinline__ void store_out<bf16_t>(bf16_t* p, float v) { p->bits = f32_to_bf16(v); }
+template <>
+__device__ __forceinline__ void store_out<f16_t>(f16_t* p, float v) { p->bits = f32_to_f16(v); }
 
 // Epilogue of the precompiled bf16 kernels: the output value itself is staged
 // (bf16 bits or fp32) and a row chunk is one 16-byte store.
 template <typename OutT>
 struct StoreEpi;
-template <>
-struct StoreEpi<bf16_t> {
+// 16-bit outputs (bf16 / f16): the staged value is the output's bits.
+template <typename OutT>
+struct StoreEpi16 {
   using Stage = uint16_t;
   struct Pre {};
-  bf16_t* c;
+  OutT* c;
   int64_t sc_b, sc_m, N;
   int vec;
-  __device__ __forceinline__ static Stage stage(float v) { return f32_to_bf16(v); }
+  __device__ __forceinline__ static Stage stage(float v) {
+    if constexpr (sizeof(OutT) == 2 && __is_same(OutT, f16_t)) return f32_to_f16(v);
+    else return f32_to_bf16(v);
+  }
   template <bool FULL>
   __device__ __forceinline__ void prefetch(int64_t, int64_t, int64_t, Pre&) const {}
   template <bool FULL>
@@ -46,6 +53,10 @@ struct StoreEpi<bf16_t> {
     }
   }
 };
+template <>
+struct StoreEpi<bf16_t> : StoreEpi16<bf16_t> {};
+template <>
+struct StoreEpi<f16_t> : StoreEpi16<f16_t> {};
 template <>
 struct StoreEpi<float> {
   using Stage = float;
@@ -70,10 +81,28 @@ struct StoreEpi<float> {
   }
 };
 
-template <int BM, int BN, int WM, int WN, bool A_K, bool B_K, typename OutT>
+template <typename OutT>
+__device__ __forceinline__ StoreEpi<OutT> store_epi(const GemmParams& p) {
+  StoreEpi<OutT> e;
+  e.c = static_cast<OutT*>(p.c);
+  e.sc_b = p.sc_b;
+  e.sc_m = p.sc_m;
+  e.N = p.N;
+  e.vec = p.vec_c;
+  return e;
+}
+
+// 16-bit inputs: bf16, or f16 (InT = f16_t selects the f16 MFMA).
+template <int BM, int BN, int WM, int WN, bool A_K, bool B_K, typename InT, typename OutT>
 __global__ __launch_bounds__(WM* WN * 64, 1) void gemm_bf16_kernel(GemmParams p) {
-  const StoreEpi<OutT> epi{static_cast<OutT*>(p.c), p.sc_b, p.sc_m, p.N, p.vec_c};
-  gemm_bf16_body<BM, BN, WM, WN, A_K, B_K, 1>(p, epi);
+  const StoreEpi<OutT> epi = store_epi<OutT>(p);
+  gemm_bf16_body<BM, BN, WM, WN, A_K, B_K, 1, StoreEpi<OutT>, __is_same(InT, f16_t)>(p, epi);
+}
+// The 4-wave 256 x 256 core (128 x 128 per wave).
+template <bool A_K, bool B_K, typename InT, typename OutT>
+__global__ __launch_bounds__(256, 1) void gemm_bf16_kernel4(GemmParams p) {
+  const StoreEpi<OutT> epi = store_epi<OutT>(p);
+  gemm_bf16_body4<A_K, B_K, StoreEpi<OutT>, __is_same(InT, f16_t)>(p, epi);
 }
 
 // ---------------------------------------------------------------------------
@@ -317,16 +346,28 @@ __global__ __launch_bounds__(256) void gemm_generic_kernel(GemmParams p) {
 // ---------------------------------------------------------------------------
 static inline bool al16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15u) == 0; }
 
-template <int BM, int BN, int WM, int WN, typename OutT>
+template <int BM, int BN, int WM, int WN, typename InT, typename OutT>
 static hipError_t launch_bf16(GemmParams p, bool a_k, bool b_k, hipStream_t s) {
   p.tiles_m = static_cast<int>((p.M + BM - 1) / BM);
   p.tiles_n = static_cast<int>((p.N + BN - 1) / BN);
   const int64_t blocks = p.batch * p.tiles_m * p.tiles_n;
   const dim3 grid(static_cast<unsigned>(blocks)), block(WM * WN * 64);
-  if (a_k && b_k) hipLaunchKernelGGL((gemm_bf16_kernel<BM, BN, WM, WN, true, true, OutT>), grid, block, 0, s, p);
-  else if (a_k) hipLaunchKernelGGL((gemm_bf16_kernel<BM, BN, WM, WN, true, false, OutT>), grid, block, 0, s, p);
-  else if (b_k) hipLaunchKernelGGL((gemm_bf16_kernel<BM, BN, WM, WN, false, true, OutT>), grid, block, 0, s, p);
-  else hipLaunchKernelGGL((gemm_bf16_kernel<BM, BN, WM, WN, false, false, OutT>), grid, block, 0, s, p);
+  if (a_k && b_k) hipLaunchKernelGGL((gemm_bf16_kernel<BM, BN, WM, WN, true, true, InT, OutT>), grid, block, 0, s, p);
+  else if (a_k) hipLaunchKernelGGL((gemm_bf16_kernel<BM, BN, WM, WN, true, false, InT, OutT>), grid, block, 0, s, p);
+  else if (b_k) hipLaunchKernelGGL((gemm_bf16_kernel<BM, BN, WM, WN, false, true, InT, OutT>), grid, block, 0, s, p);
+  else hipLaunchKernelGGL((gemm_bf16_kernel<BM, BN, WM, WN, false, false, InT, OutT>), grid, block, 0, s, p);
+  return hipGetLastError();
+}
+
+template <typename InT, typename OutT>
+static hipError_t launch_bf16_4w(GemmParams p, bool a_k, bool b_k, hipStream_t s) {
+  p.tiles_m = static_cast<int>((p.M + 255) / 256);
+  p.tiles_n = static_cast<int>((p.N + 255) / 256);
+  const dim3 grid(static_cast<unsigned>(p.batch * p.tiles_m * p.tiles_n)), block(256);
+  if (a_k && b_k) hipLaunchKernelGGL((gemm_bf16_kernel4<true, true, InT, OutT>), grid, block, 0, s, p);
+  else if (a_k) hipLaunchKernelGGL((gemm_bf16_kernel4<true, false, InT, OutT>), grid, block, 0, s, p);
+  else if (b_k) hipLaunchKernelGGL((gemm_bf16_kernel4<false, true, InT, OutT>), grid, block, 0, s, p);
+  else hipLaunchKernelGGL((gemm_bf16_kernel4<false, false, InT, OutT>), grid, block, 0, s, p);
   return hipGetLastError();
 }
 
@@ -366,7 +407,7 @@ static int64_t slice_bytes(int64_t rows, int64_t s_row, int64_t K, int64_t s_k, 
   return ((rows - 1) * s_row + (K - 1) * s_k + 1) * es;
 }
 
-template <typename OutT>
+template <typename InT, typename OutT>
 static hipError_t dispatch_bf16(GemmParams p, hipStream_t s) {
   const int ma = majorness(p.a, p.sa_b, p.sa_m, p.sa_k, p.M, p.K, 8, p.batch);
   const int mb = majorness(p.b, p.sb_b, p.sb_n, p.sb_k, p.N, p.K, 8, p.batch);
@@ -375,16 +416,16 @@ static hipError_t dispatch_bf16(GemmParams p, hipStream_t s) {
   const int64_t ea = slice_bytes(p.M, p.sa_m, p.K, p.sa_k, 2);
   const int64_t eb = slice_bytes(p.N, p.sb_n, p.K, p.sb_k, 2);
   if (ma < 0 || mb < 0 || !nonneg || ea >= (int64_t{1} << 31) || eb >= (int64_t{1} << 31))
-    return launch_generic<bf16_t, OutT>(p, s);
+    return launch_generic<InT, OutT>(p, s);
   p.a_extent = static_cast<uint32_t>(ea);
   p.b_extent = static_cast<uint32_t>(eb);
   constexpr int64_t kV = 16 / sizeof(OutT);  // elements per 16-byte store
   p.vec_c = (p.sc_m % kV == 0) && (p.sc_b % kV == 0 || p.batch == 1) &&
             (reinterpret_cast<uintptr_t>(p.c) % 16 == 0);
   const int64_t t256 = p.batch * ((p.M + 255) / 256) * ((p.N + 255) / 256);
-  if (p.M >= 256 && p.N >= 256 && t256 >= 128) return launch_bf16<256, 256, 2, 4, OutT>(p, ma, mb, s);
-  if (p.M >= 256 && p.N >= 128) return launch_bf16<256, 128, 2, 2, OutT>(p, ma, mb, s);
-  return launch_bf16<128, 128, 2, 2, OutT>(p, ma, mb, s);
+  if (p.M >= 256 && p.N >= 256 && t256 >= 128) return launch_bf16_4w<InT, OutT>(p, ma, mb, s);
+  if (p.M >= 256 && p.N >= 128) return launch_bf16<256, 128, 2, 2, InT, OutT>(p, ma, mb, s);
+  return launch_bf16<128, 128, 2, 2, InT, OutT>(p, ma, mb, s);
 }
 
 template <typename OutT>
@@ -432,8 +473,12 @@ extern "C" int ghip_gemm_batched(int ab_dtype, int c_dtype, int64_t batch, int64
   hipStream_t s = static_cast<hipStream_t>(stream);
   hipError_t e;
   if (ab_dtype == GHIP_DTYPE_BFLOAT16) {
-    if (c_dtype == GHIP_DTYPE_BFLOAT16) e = dispatch_bf16<bf16_t>(p, s);
-    else if (c_dtype == GHIP_DTYPE_FLOAT32) e = dispatch_bf16<float>(p, s);
+    if (c_dtype == GHIP_DTYPE_BFLOAT16) e = dispatch_bf16<bf16_t, bf16_t>(p, s);
+    else if (c_dtype == GHIP_DTYPE_FLOAT32) e = dispatch_bf16<bf16_t, float>(p, s);
+    else return set_error(err, GHIP_ERR_UNSUPPORTED, "gemm_batched: output dtype %d", c_dtype);
+  } else if (ab_dtype == GHIP_DTYPE_FLOAT16) {
+    if (c_dtype == GHIP_DTYPE_FLOAT16) e = dispatch_bf16<f16_t, f16_t>(p, s);
+    else if (c_dtype == GHIP_DTYPE_FLOAT32) e = dispatch_bf16<f16_t, float>(p, s);
     else return set_error(err, GHIP_ERR_UNSUPPORTED, "gemm_batched: output dtype %d", c_dtype);
   } else if (ab_dtype == GHIP_DTYPE_FLOAT32) {
     if (c_dtype == GHIP_DTYPE_FLOAT32) e = dispatch_f32<float>(p, s);

@@ -73,3 +73,35 @@ def bf16_bits_to_f32(b: np.ndarray) -> np.ndarray:
 def round_bf16(x: np.ndarray) -> np.ndarray:
     """fp32 values rounded to the nearest bf16 (returned as fp32)."""
     return bf16_bits_to_f32(to_bf16_bits(x))
+
+
+def normal_device(seed: int, shape, std: float = 1.0, mean: float = 0.0, device="cuda", dtype=None):
+    """normal() computed with torch on `device` (the same SplitMix64 counters and
+    Box-Muller pairs, in fp64 then cast to fp32 and optionally to `dtype`), for
+    inputs too large to generate on the host in a test's time.  The integer stream
+    is identical; the fp64 log / cos / sin may differ from numpy's in the last
+    bit, so the fp32 values agree with normal() except, rarely, by one ulp."""
+    import torch
+    n = int(np.prod(shape, dtype=np.int64))
+    m = (n + 1) // 2
+    out = torch.empty(2 * m, dtype=torch.float32, device=device)
+    golden, m1, m2 = (int(v.astype(np.int64)) for v in (_GOLDEN, _M1, _M2))
+    mask30, mask27, mask31, mask11 = ((1 << (64 - k)) - 1 for k in (30, 27, 31, 11))
+    chunk = 1 << 24
+    for p0 in range(0, m, chunk):
+        p1 = min(m, p0 + chunk)
+        ctr = torch.arange(2 * p0 + 1, 2 * p1 + 1, dtype=torch.int64, device=device)
+        z = seed + ctr * golden                       # wraps modulo 2^64 like uint64
+        z = (z ^ ((z >> 30) & mask30)) * m1
+        z = (z ^ ((z >> 27) & mask27)) * m2
+        z = z ^ ((z >> 31) & mask31)
+        u = ((z >> 11) & mask11).to(torch.float64) * (1.0 / 9007199254740992.0)
+        u1 = 1.0 - u[0::2]
+        u2 = u[1::2]
+        r = torch.sqrt(-2.0 * torch.log(u1))
+        zz = torch.empty(2 * (p1 - p0), dtype=torch.float64, device=device)
+        zz[0::2] = r * torch.cos(2.0 * np.pi * u2)
+        zz[1::2] = r * torch.sin(2.0 * np.pi * u2)
+        out[2 * p0:2 * p1] = (mean + std * zz).to(torch.float32)
+    out = out[:n].reshape(shape)
+    return out if dtype is None else out.to(dtype)

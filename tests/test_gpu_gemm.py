@@ -93,6 +93,52 @@ def test_f32_layouts_large_tiles(cuda, a_t, b_t):
     assert rel_err(got, ref) <= 1e-4
 
 
+@pytest.mark.parametrize("a_t", [False, True])
+@pytest.mark.parametrize("b_t", [False, True])
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])
+def test_16bit_large_tiles_ragged(cuda, a_t, b_t, dt):
+    """>= 128 tiles of 256 x 256 (the 4-wave core) with ragged M, N and K, every
+    operand majorness, bf16 and f16, 16-bit and fp32 outputs, against fp64 dot
+    products of the same input bytes (4096 sampled entries)."""
+    ta = synth.normal_device(3501, (2, 2056, 200), std=0.125, device=cuda, dtype=dt)
+    tb = synth.normal_device(3502, (2, 200, 2060), std=0.125, device=cuda, dtype=dt)
+    if a_t:
+        ta = ta.transpose(1, 2).contiguous().transpose(1, 2)
+    if b_t:
+        tb = tb.transpose(1, 2).contiguous().transpose(1, 2)
+    c16 = ops.gemm(ta, tb)
+    assert c16.dtype == dt
+    got, ref = _sampled_check(ta, tb, c16, seed=11)
+    # one 16-bit rounding of the fp32 result (bf16 2^-8, f16 2^-11), RMS-floored
+    assert rel_err(got, ref) <= (1e-2 if dt == torch.bfloat16 else 1e-3)
+    c32 = ops.gemm(ta, tb, out_dtype=torch.float32)
+    got, ref = _sampled_check(ta, tb, c32, seed=12)
+    assert rel_err(got, ref) <= 1e-4
+    # the last row / column tiles (ragged edges) in full
+    e32 = c32[:, 2048:, :].cpu().numpy()
+    a = ta.float().cpu().numpy()
+    b = tb.float().cpu().numpy()
+    assert rel_err(e32, orc.dot_general(np.ascontiguousarray(a[:, 2048:]), [2], [0], b, [1], [0])) <= 1e-4
+    e32 = c32[:, :, 2048:].cpu().numpy()
+    assert rel_err(e32, orc.dot_general(a, [2], [0], np.ascontiguousarray(b[:, :, 2048:]), [1], [0])) <= 1e-4
+
+
+@pytest.mark.parametrize("shape", SHAPES)
+def test_f16_layouts(cuda, shape):
+    """f16 DotGeneral (the f16 MFMA) on the small-tile cores and the generic path."""
+    B, M, N, K = shape
+    a = synth.normal(3600 + M, (B, M, K), std=0.125).astype(np.float16).astype(np.float32)
+    b = synth.normal(3700 + N, (B, K, N), std=0.125).astype(np.float16).astype(np.float32)
+    ta, tb = dev(a, cuda, torch.float16), dev(b, cuda, torch.float16)
+    ref = orc.dot_general(a, [2], [0], b, [1], [0])
+    assert rel_err(ops.gemm(ta, tb, out_dtype=torch.float32).cpu().numpy(), ref) <= 1e-4
+    assert rel_err(ops.gemm(ta, tb).float().cpu().numpy(), ref) <= 1e-3
+    # a column view of odd width takes the generic kernel
+    tbo = tb[:, :, : max(1, N - 1)]
+    ref = orc.dot_general(a, [2], [0], np.ascontiguousarray(b[:, :, : max(1, N - 1)]), [1], [0])
+    assert rel_err(ops.gemm(ta, tbo, out_dtype=torch.float32).cpu().numpy(), ref) <= 1e-4
+
+
 def test_generic_path_odd_strides(cuda):
     """Shapes/strides the vector paths cannot address fall back to the generic kernel."""
     a = synth.normal(3400, (2, 33, 19))
@@ -124,10 +170,9 @@ def _sampled_check(ta, tb, c, count=4096, seed=0):
 
 def test_dot_general_config_bf16(cuda):
     """BASELINE config: A [8,2048,4096] x B [8,4096,4096], bf16, fp32 accumulate,
-    bf16 out; entries ~ N(0, 1/64)."""
-    g = torch.Generator(cuda).manual_seed(3001)
-    ta = (torch.randn((8, 2048, 4096), device=cuda, generator=g) * 0.125).to(torch.bfloat16)
-    tb = (torch.randn((8, 4096, 4096), device=cuda, generator=g) * 0.125).to(torch.bfloat16)
+    bf16 out; entries ~ N(0, 1/64) from the SplitMix64 streams 3001 / 3002."""
+    ta = synth.normal_device(3001, (8, 2048, 4096), std=0.125, device=cuda, dtype=torch.bfloat16)
+    tb = synth.normal_device(3002, (8, 4096, 4096), std=0.125, device=cuda, dtype=torch.bfloat16)
     c = ops.gemm(ta, tb)
     got, ref = _sampled_check(ta, tb, c)
     assert rel_err(got, ref) <= 1e-2
@@ -138,9 +183,8 @@ def test_dot_general_config_bf16(cuda):
 
 
 def test_dot_general_config_f32(cuda):
-    g = torch.Generator(cuda).manual_seed(3002)
-    ta = torch.randn((8, 2048, 4096), device=cuda, generator=g) * 0.125
-    tb = torch.randn((8, 4096, 4096), device=cuda, generator=g) * 0.125
+    ta = synth.normal_device(3001, (8, 2048, 4096), std=0.125, device=cuda)
+    tb = synth.normal_device(3002, (8, 4096, 4096), std=0.125, device=cuda)
     c = ops.gemm(ta, tb)
     got, ref = _sampled_check(ta, tb, c)
     assert rel_err(got, ref) <= 1e-4

@@ -293,6 +293,33 @@ def test_graph_log_softmax_chain(be, dt):
     assert rel_err(y, ref) <= (1e-5 if dt == F32 else 2.0 ** -8 + 1e-5)
 
 
+def test_graph_float16_hot_ops(be):
+    """Float16 (a dtype the reference declares, capabilities.go:153-166) through the
+    graph API: FusedSoftmax, FusedLayerNorm, the RMSNorm chain and DotGeneral, each
+    within one f16 rounding (RMS-floored) of the fp64 oracle."""
+    F16 = dtypes.Float16
+    h = lambda a: np.asarray(a, np.float32).astype(np.float16)  # noqa: E731
+    x = h(synth.normal(1901, (512, 1024), std=2.0))
+    g = h(synth.uniform_f32(1902, (1024,), 0.5, 1.5))
+    bt = h(synth.normal(1903, (1024,), std=0.1))
+    s = make_shape(F16, 512, 1024)
+    v = make_shape(F16, 1024)
+    ys = run(be, lambda f, a, gg, bb: [f.FusedSoftmax(a, 1), f.FusedLayerNorm(a, [1], 1e-5, gg, bb),
+                                        graphs.rms_norm(f, a, gg, 1e-6), graphs.log_softmax_chain(f, a)],
+             [(x, s), (g, v), (bt, v)])
+    xf, gf, bf = (a.astype(np.float32) for a in (x, g, bt))
+    refs = [orc.softmax(xf), orc.layernorm(xf, gf, bf, 1e-5), orc.rmsnorm(xf, gf, 1e-6), orc.log_softmax(xf)]
+    for y, r in zip(ys, refs):
+        assert y.dtype == np.float16
+        assert rel_err(y.astype(np.float32), r) <= 2.0 ** -11 + 1e-5
+    a = h(synth.normal(1904, (2, 300, 256), std=0.125))
+    b = h(synth.normal(1905, (2, 256, 520), std=0.125))
+    (y,) = run(be, lambda f, p, q: [f.DotGeneral(p, [2], [0], q, [1], [0])],
+               [(a, make_shape(F16, 2, 300, 256)), (b, make_shape(F16, 2, 256, 520))])
+    assert y.dtype == np.float16
+    assert rel_err(y.astype(np.float32), orc.dot_general(a.astype(np.float32), [2], [0], b.astype(np.float32), [1], [0])) <= 1e-3
+
+
 def test_graph_dot_general_layouts(be):
     a = synth.round_bf16(synth.normal(3001, (2, 64, 96), std=0.125))
     b = synth.round_bf16(synth.normal(3002, (96, 2, 80), std=0.125))

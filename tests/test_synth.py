@@ -23,3 +23,13 @@ def test_normal_moments_and_determinism():
 def test_uniform_int_range():
     v = synth.uniform_int(5001, (8, 1024), 0, 32000)
     assert v.dtype == np.int32 and v.min() >= 0 and v.max() < 32000
+
+
+def test_normal_device_matches_host_stream():
+    """The torch form (run here on the CPU) draws the same SplitMix64 stream: equal
+    to the numpy form value for value on a ragged shape, odd length included."""
+    import torch  # noqa: F401
+    for shape in ((3, 1000, 77), (5,), (1, 1)):
+        a = synth.normal(3001, shape, std=0.125, mean=0.5)
+        b = synth.normal_device(3001, shape, std=0.125, mean=0.5, device="cpu").numpy()
+        assert b.shape == a.shape and np.max(np.abs(a - b)) <= np.spacing(np.abs(a)).max()
