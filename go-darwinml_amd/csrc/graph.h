@@ -193,6 +193,11 @@ std::shared_ptr<GHipExecutable> compile_function(GHipBackend* be, GHipFunction* 
 // Runs an executable's plan on its backend's stream with the given device
 // pointers for its inputs and (contiguous, pre-allocated) outputs.
 int run_plan(GHipExecutable* e, void* const* in_ptrs, void* const* out_ptrs, GHipError* err);
+// The same with the intermediates in `arena` (at least plan.arena_bytes, 256-byte
+// aligned) instead of the executable's own arena.
+int run_plan_in(GHipExecutable* e, void* arena, void* const* in_ptrs, void* const* out_ptrs, GHipError* err);
+// Execute's checks of the input buffers and the input / output counts.
+int check_execute_args(GHipExecutable* e, GHipBuffer* const* inputs, int n, int nout, GHipError* err);
 
 // Generated elementwise kernels (rtc.cpp).
 struct RtcKernel {

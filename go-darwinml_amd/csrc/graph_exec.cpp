@@ -85,6 +85,12 @@ int run_plan(GHipExecutable* e, void* const* in_ptrs, void* const* out_ptrs, GHi
     if (be->alloc(plan.arena_bytes, &e->arena, err) != GHIP_OK) return err ? err->code : GHIP_ERR_OOM;
     e->arena_cap = plan.arena_bytes;
   }
+  return run_plan_in(e, e->arena, in_ptrs, out_ptrs, err);
+}
+
+int run_plan_in(GHipExecutable* e, void* arena, void* const* in_ptrs, void* const* out_ptrs, GHipError* err) {
+  GHipBackend* be = e->backend;
+  const Plan& plan = e->plan;
   ExecState st;
   st.stream = be->stream;
   st.slot_ptr.resize(plan.slots.size(), nullptr);
@@ -93,7 +99,7 @@ int run_plan(GHipExecutable* e, void* const* in_ptrs, void* const* out_ptrs, GHi
     switch (sl.kind) {
       case SlotKind::Input: st.slot_ptr[s] = static_cast<char*>(in_ptrs[sl.index]); break;
       case SlotKind::Const: st.slot_ptr[s] = static_cast<char*>(sl.const_ptr); break;
-      case SlotKind::Arena: st.slot_ptr[s] = static_cast<char*>(e->arena) + sl.arena_off; break;
+      case SlotKind::Arena: st.slot_ptr[s] = static_cast<char*>(arena) + sl.arena_off; break;
       case SlotKind::Output: st.slot_ptr[s] = static_cast<char*>(out_ptrs[sl.index]); break;
     }
   }
@@ -156,11 +162,9 @@ extern "C" size_t ghip_exec_plan(GHipExecutable* e, char* buf, size_t buflen) {
   return s.size();
 }
 
-extern "C" int ghip_exec_execute(GHipExecutable* e, GHipBuffer* const* inputs, int n, const uint8_t* donate,
-                                 GHipBuffer** outputs, int nout, GHipError* err) {
-  (void)donate;  // inputs are never written; donation is accepted and ignored
-  if (!e || e->finalized) return set_error(err, GHIP_ERR_STATE, "Execute: executable finalized");
-  std::lock_guard<std::mutex> lk(e->mu);
+namespace ghip {
+// Execute's argument checks (executable.go:54-68); the caller holds e->mu.
+int check_execute_args(GHipExecutable* e, GHipBuffer* const* inputs, int n, int nout, GHipError* err) {
   GHipBackend* be = e->backend;
   if (!be || be->finalized) return set_error(err, GHIP_ERR_STATE, "Execute: backend finalized");
   if (be->plan_only) return set_error(err, GHIP_ERR_STATE, "Execute: plan-only backend has no device");
@@ -175,6 +179,17 @@ extern "C" int ghip_exec_execute(GHipExecutable* e, GHipBuffer* const* inputs, i
       return set_error(err, GHIP_ERR_INVALID_ARG, "Execute: input #%d shape mismatch: expected %s, got %s", i,
                        e->in_shapes[i].str().c_str(), inputs[i]->shape.str().c_str());
   }
+  return GHIP_OK;
+}
+}  // namespace ghip
+
+extern "C" int ghip_exec_execute(GHipExecutable* e, GHipBuffer* const* inputs, int n, const uint8_t* donate,
+                                 GHipBuffer** outputs, int nout, GHipError* err) {
+  (void)donate;  // inputs are never written; donation is accepted and ignored
+  if (!e || e->finalized) return set_error(err, GHIP_ERR_STATE, "Execute: executable finalized");
+  std::lock_guard<std::mutex> lk(e->mu);
+  GHipBackend* be = e->backend;
+  if (const int rc = check_execute_args(e, inputs, n, nout, err)) return rc;
   hipSetDevice(be->device);
   std::vector<GHipBuffer*> outs(nout, nullptr);
   auto cleanup = [&]() {

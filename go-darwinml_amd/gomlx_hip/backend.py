@@ -165,6 +165,8 @@ _GRAPH_SIGS = {
     "ghip_exec_output_shape": ([_vp, _int, _intp, _i64p, _int], _int),
     "ghip_exec_execute": ([_vp, ctypes.POINTER(_vp), _int, ctypes.POINTER(ctypes.c_uint8),
                            ctypes.POINTER(_vp), _int, _errp], _int),
+    "ghip_exec_execute_noalloc": ([_vp, ctypes.POINTER(_vp), _int, ctypes.POINTER(_vp), _int, _errp], _int),
+    "ghip_exec_noalloc_scratch_bytes": ([], ctypes.c_size_t),
     "ghip_exec_plan": ([_vp, ctypes.c_char_p, ctypes.c_size_t], ctypes.c_size_t),
     "ghip_exec_finalize": ([_vp], None),
 }
@@ -685,6 +687,17 @@ class Executable:
         if rc:
             _raise(err, rc)
         return [Buffer(self.backend, outs[i]) for i in range(nout)]
+
+    def ExecuteNoAlloc(self, inputs: Sequence[Buffer], outputs: Sequence[Buffer]) -> None:
+        """Execute into caller-allocated output buffers with the intermediates in the
+        library's per-GPU scratch array: no device memory is allocated."""
+        n, nout = len(inputs), len(outputs)
+        arr = (ctypes.c_void_p * max(n, 1))(*[b.handle for b in inputs])
+        outs = (ctypes.c_void_p * max(nout, 1))(*[b.handle for b in outputs])
+        err = GHipError(0, None)
+        rc = _L().ghip_exec_execute_noalloc(self.handle, arr, n, outs, nout, ctypes.byref(err))
+        if rc:
+            _raise(err, rc)
 
     def Plan(self) -> str:
         n = _L().ghip_exec_plan(self.handle, None, 0)

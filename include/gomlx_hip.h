@@ -388,6 +388,18 @@ int ghip_exec_output_shape(GHipExecutable* e, int i, int* dtype, int64_t* dims, 
  * Calls on one executable are serialized. */
 int ghip_exec_execute(GHipExecutable* e, GHipBuffer* const* inputs, int n, const uint8_t* donate,
                       GHipBuffer** outputs, int nout, GHipError* err);
+/* Execute without allocating device memory.  No counterpart in the reference:
+ * this is for callers that cannot allocate (serving loops that must not call
+ * hipMalloc, code run under stream capture).  The caller passes the `nout`
+ * output buffers (shapes as ghip_exec_output_shape reports, distinct from the
+ * inputs); the intermediates live in a file-scope device array of
+ * ghip_exec_noalloc_scratch_bytes() (256 MiB) per GPU, shared by every call on
+ * that GPU, so calls that overlap on one GPU race.  A plan needing more than
+ * that, or one with Call / While / If (whose sub-functions have arenas of their
+ * own), is refused with an error.  Inputs are checked like Execute's. */
+int ghip_exec_execute_noalloc(GHipExecutable* e, GHipBuffer* const* inputs, int n,
+                              GHipBuffer* const* outputs, int nout, GHipError* err);
+size_t ghip_exec_noalloc_scratch_bytes(void);
 /* Human-readable lowering plan (one line per launch), for inspection / tests.
  * Returns the full length; writes at most buflen-1 chars. */
 size_t ghip_exec_plan(GHipExecutable* e, char* buf, size_t buflen);
