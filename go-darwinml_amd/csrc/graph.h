@@ -281,7 +281,7 @@ int launch_convert(int src_dt, int dst_dt, const void* src, void* dst, const Cop
 // in elements ordered (batch, head, sequence), head dim contiguous.
 bool sdpa_fused_supported(int dtype, int64_t H, int64_t Hkv, int64_t Sq, int64_t Sk, int64_t D,
                           const int64_t* qs, const int64_t* ks, const int64_t* vs, const int64_t* os,
-                          float scale);
+                          float scale, int mask_dtype);
 
 }  // namespace ghip
 

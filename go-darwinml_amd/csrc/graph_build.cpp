@@ -1067,6 +1067,18 @@ extern "C" GHipValue ghip_fn_fused_sdpa(GHipFunction* f, GHipValue q, GHipValue 
     if (!m) return -1;
     if (m->shape.dtype != GHIP_DTYPE_BOOL && m->shape.dtype != qn->shape.dtype)
       return c.fail(GHIP_ERR_INVALID_ARG, "mask must be bool or additive in q's dtype");
+    // It must broadcast to the scores [B, H, Sq, Sk] over its trailing axes
+    // (broadcastMaskToScores, function.go:2959-2974); a rank-4 mask follows Q's
+    // layout (:2709-2718).
+    std::vector<int64_t> md = m->shape.dims;
+    if (md.size() > 4) return c.fail(GHIP_ERR_INVALID_ARG, "mask rank %zu > 4", md.size());
+    if (layout == GHIP_LAYOUT_BSHD && md.size() == 4) std::swap(md[1], md[2]);
+    const int64_t sd[4] = {qn->shape.dims[0], num_heads, qn->shape.dims[sa], kn->shape.dims[sa]};
+    const size_t off = 4 - md.size();
+    for (size_t i = 0; i < md.size(); ++i)
+      if (md[i] != 1 && md[i] != sd[off + i])
+        return c.fail(GHIP_ERR_INVALID_ARG, "mask %s does not broadcast to the scores [%lld,%lld,%lld,%lld]",
+                      m->shape.str().c_str(), (long long)sd[0], (long long)sd[1], (long long)sd[2], (long long)sd[3]);
   }
   Node n{Kind::SDPA};
   n.in = {q, k, v, mask};

@@ -1463,7 +1463,8 @@ struct Lowerer {
     const bool bshd = n.i2 == GHIP_LAYOUT_BSHD;
     const bool causal = n.i3 != 0;
     const int dt = N[qv_].shape.dtype;
-    if (dt != GHIP_DTYPE_FLOAT32 && dt != GHIP_DTYPE_BFLOAT16) return fail(GHIP_ERR_UNSUPPORTED, "SDPA: float32 / bfloat16 only");
+    if (dt != GHIP_DTYPE_FLOAT32 && dt != GHIP_DTYPE_BFLOAT16 && dt != GHIP_DTYPE_FLOAT16)
+      return fail(GHIP_ERR_UNSUPPORTED, "SDPA: float32 / bfloat16 / float16 only");
     const std::vector<int64_t> to_bhsd{0, 2, 1, 3};
     auto as_bhsd = [&](int id, Shape* s) {
       View w = get(id);
@@ -1478,33 +1479,68 @@ struct Lowerer {
     View q = as_bhsd(qv_, &qs), k = as_bhsd(kv_, &ks), vw = as_bhsd(vv_, &vs);
     if (failed) return bad();
     const int64_t B = qs.dims[0], Sq = qs.dims[2], D = qs.dims[3], Sk = ks.dims[2], Dv = vs.dims[3];
-    // One fused kernel when there is no mask operand and the operands fit it: Q, K,
-    // V are read through their views (BHSD or BSHD, GQA heads shared in place) and
-    // the output is written in the layout the graph expects.
-    if (mv_ < 0 && D == Dv && q.strides[3] == 1 && k.strides[3] == 1 && vw.strides[3] == 1) {
+    // Mask (function.go:2840-2878): a rank-4 mask follows Q's layout (:2709-2718);
+    // any rank broadcasts to the scores [B, H, Sq, Sk] over its trailing axes
+    // (broadcastMaskToScores, :2959-2974): strides 0 on size-1 and missing axes.
+    View mview;
+    int mdt = -1;
+    std::array<int64_t, 4> mst{0, 0, 0, 0};
+    if (mv_ >= 0) {
+      Shape ms = N[mv_].shape;
+      View mw = get(mv_);
+      if (failed) return bad();
+      if (bshd && ms.rank() == 4) {
+        mw = permute(mw, to_bhsd);
+        ms = permute_shape(ms, to_bhsd);
+      }
+      const int64_t sd[4] = {B, H, Sq, Sk};
+      const int off = 4 - ms.rank();
+      for (int i = 0; i < ms.rank(); ++i) {
+        if (ms.dims[i] == 1) continue;
+        if (ms.dims[i] != sd[off + i])
+          return fail(GHIP_ERR_INVALID_ARG, fmt("SDPA: mask %s does not broadcast to the scores [%lld,%lld,%lld,%lld]",
+                                                ms.str().c_str(), (long long)B, (long long)H, (long long)Sq,
+                                                (long long)Sk).c_str());
+        mst[off + i] = mw.strides[i];
+      }
+      mview = mw;
+      mdt = ms.dtype;
+    }
+    const bool has_mask = mv_ >= 0;
+    // One fused kernel when the operands fit it: Q, K, V (and the mask) are read
+    // through their views (BHSD or BSHD, GQA heads shared in place, broadcast mask
+    // axes at stride 0) and the output is written in the layout the graph expects.
+    if (D == Dv && q.strides[3] == 1 && k.strides[3] == 1 && vw.strides[3] == 1) {
       Shape os;
       os.dtype = dt;
       os.dims = {B, H, Sq, Dv};
-      // Output slot in the caller's layout; o_view is its BHSD view.
-      Shape os_layout = bshd ? permute_shape(os, to_bhsd) : os;
-      View out_l = fresh(os_layout);
-      View ov = bshd ? permute(out_l, to_bhsd) : out_l;
       const int64_t qst[3] = {q.strides[0], q.strides[1], q.strides[2]};
       const int64_t kst[3] = {k.strides[0], k.strides[1], k.strides[2]};
       const int64_t vst[3] = {vw.strides[0], vw.strides[1], vw.strides[2]};
-      const int64_t ost[3] = {ov.strides[0], ov.strides[1], ov.strides[2]};
-      const bool al = q.offset % 8 == 0 && k.offset % 8 == 0 && vw.offset % 8 == 0 && ov.offset % 4 == 0;
+      // BHSD strides of the contiguous output in the caller's layout.
+      const int64_t ostr[3] = {H * Sq * Dv, bshd ? Dv : Sq * Dv, bshd ? H * Dv : Dv};
+      bool mask_ok = true;
+      for (int i = 0; i < 4 && has_mask; ++i) mask_ok = mask_ok && mst[i] >= 0;
+      const bool al = q.offset % 8 == 0 && k.offset % 8 == 0 && vw.offset % 8 == 0;
       const float scale = static_cast<float>(n.f0);
-      if (al && sdpa_fused_supported(dt, H, Hkv, Sq, Sk, D, qst, kst, vst, ost, scale)) {
+      if (al && mask_ok && sdpa_fused_supported(dt, H, Hkv, Sq, Sk, D, qst, kst, vst, ostr, scale, mdt)) {
+        Shape os_layout = bshd ? permute_shape(os, to_bhsd) : os;
+        View out_l = fresh(os_layout);
+        View ov = bshd ? permute(out_l, to_bhsd) : out_l;
         std::array<int64_t, 3> aq{qst[0], qst[1], qst[2]}, ak{kst[0], kst[1], kst[2]},
-            av{vst[0], vst[1], vst[2]}, ao{ost[0], ost[1], ost[2]};
-        add_step(fmt("sdpa_fwd %s B=%lld H=%lld Hkv=%d Sq=%lld Sk=%lld D=%lld causal=%d (fused attention)",
+            av{vst[0], vst[1], vst[2]}, ao{ov.strides[0], ov.strides[1], ov.strides[2]};
+        std::vector<int> rd{q.slot, k.slot, vw.slot};
+        if (has_mask) rd.push_back(mview.slot);
+        const View mv = mview;
+        const std::array<int64_t, 4> ms4 = mst;
+        add_step(fmt("sdpa_fwd %s B=%lld H=%lld Hkv=%d Sq=%lld Sk=%lld D=%lld causal=%d mask=%s (fused attention)",
                      dtype_name(dt), (long long)B, (long long)H, Hkv, (long long)Sq, (long long)Sk, (long long)D,
-                     causal ? 1 : 0),
-                 {q.slot, k.slot, vw.slot}, {ov.slot}, [=](ExecState& st, GHipError* e) {
-                   return ghip_sdpa_fwd(dt, st.ptr(q, dt), st.ptr(k, dt), st.ptr(vw, dt), st.ptr(ov, dt), B, H, Hkv,
-                                        Sq, Sk, D, aq.data(), ak.data(), av.data(), ao.data(), scale, causal ? 1 : 0,
-                                        st.stream, e);
+                     causal ? 1 : 0, has_mask ? dtype_name(mdt) : "none"),
+                 rd, {ov.slot}, [=](ExecState& st, GHipError* e) {
+                   const void* mp = has_mask ? st.ptr(mv, mdt) : nullptr;
+                   return ghip_sdpa_fwd_masked(dt, st.ptr(q, dt), st.ptr(k, dt), st.ptr(vw, dt), st.ptr(ov, dt), B, H,
+                                               Hkv, Sq, Sk, D, aq.data(), ak.data(), av.data(), ao.data(), mp, mdt,
+                                               ms4.data(), scale, causal ? 1 : 0, st.stream, e);
                  });
         return out_l;
       }
@@ -1539,28 +1575,6 @@ struct Lowerer {
     if (bstride(q, qs) < 0) q = materialize(q, qs, "(SDPA Q to BHSD)");
     if (bstride(k, ks) < 0) k = materialize(k, ks, "(SDPA K to BHSD)");
     if (bstride(vw, vs) < 0) vw = materialize(vw, vs, "(SDPA V to BHSD)");
-    // Mask: a boolean keep-mask that broadcasts over [B, H] (trailing [Sq, Sk]).
-    View mask;
-    bool has_mask = false;
-    if (mv_ >= 0) {
-      Shape ms = N[mv_].shape;
-      if (ms.dtype != GHIP_DTYPE_BOOL) return fail(GHIP_ERR_UNSUPPORTED, "SDPA: additive masks are not lowered yet");
-      View mw = get(mv_);
-      if (bshd && ms.rank() == 4) {  // rank-4 masks follow Q's layout (function.go:2709-2718)
-        mw = permute(mw, to_bhsd);
-        ms = permute_shape(ms, to_bhsd);
-      }
-      bool lead1 = ms.rank() >= 2;
-      for (int i = 0; lead1 && i < ms.rank() - 2; ++i) lead1 = ms.dims[i] == 1;
-      if (!lead1 || ms.dims[ms.rank() - 2] != Sq || ms.dims[ms.rank() - 1] != Sk)
-        return fail(GHIP_ERR_UNSUPPORTED, "SDPA: boolean mask must be [.., Sq, Sk] with unit leading dims");
-      Shape m2 = ms;
-      m2.dims = {Sq, Sk};
-      View m2v = mw;
-      m2v.strides = {mw.strides[ms.rank() - 2], mw.strides[ms.rank() - 1]};
-      mask = materialize(m2v, m2, "(SDPA mask)");
-      has_mask = true;
-    }
     if (failed) return bad();
     const int64_t BH = B * H;
     Shape ss;
@@ -1583,13 +1597,15 @@ struct Lowerer {
                                         st.ptr(scores, dt), Sq * Sk, Sk, 1, st.stream, e);
              });
     std::vector<int> rd{scores.slot};
-    if (has_mask) rd.push_back(mask.slot);
-    add_step(fmt("scale_mask_softmax_rows %s rows=%lld sk=%lld scale=%g causal=%d mask=%d", dtype_name(dt),
-                 (long long)(BH * Sq), (long long)Sk, n.f0, causal ? 1 : 0, has_mask ? 1 : 0),
+    if (has_mask) rd.push_back(mview.slot);
+    const View mv = mview;
+    const std::array<int64_t, 4> ms4 = mst;
+    add_step(fmt("scale_mask_softmax_rows %s rows=%lld sk=%lld scale=%g causal=%d mask=%s", dtype_name(dt),
+                 (long long)(BH * Sq), (long long)Sk, n.f0, causal ? 1 : 0, has_mask ? dtype_name(mdt) : "none"),
              rd, {probs.slot}, [=](ExecState& st, GHipError* e) {
-               const uint8_t* mp = has_mask ? reinterpret_cast<const uint8_t*>(st.ptr(mask, GHIP_DTYPE_BOOL)) : nullptr;
-               return ghip_scale_mask_softmax_rows(dt, st.ptr(scores, dt), st.ptr(probs, dt), BH * Sq, Sq, Sk, scale,
-                                                   causal ? 1 : 0, mp, st.stream, e);
+               const void* mp = has_mask ? st.ptr(mv, mdt) : nullptr;
+               return ghip_scale_mask_softmax_rows_ex(dt, st.ptr(scores, dt), st.ptr(probs, dt), B, H, Sq, Sk, scale,
+                                                      causal ? 1 : 0, mp, mdt, ms4.data(), st.stream, e);
              });
     add_step(fmt("gemm_batched %s B=%lld M=%lld N=%lld K=%lld (SDPA out = P.V)", dtype_name(dt), (long long)BH,
                  (long long)Sq, (long long)Dv, (long long)Sk),

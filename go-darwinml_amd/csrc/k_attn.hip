@@ -1,8 +1,12 @@
 // Fused scaled-dot-product attention (forward), the single-kernel lowering of
 // Function.FusedScaledDotProductAttention (mpsgraph/gomlx/function.go:2669-2907):
-//   out = softmax(scale * Q K^T  [causal: -inf where key > query]) V
-// for bf16 Q/K/V/O with head dim 128, fp32 softmax statistics and accumulation.
-// GQA reads KV head h / (H / Hkv) directly (function.go:2911-2956 repeats it).
+//   out = softmax(scale * Q K^T + mask  [causal: -inf where key > query]) V
+// for bf16 or f16 Q/K/V/O with head dim 64 or 128, fp32 softmax statistics and
+// accumulation.  The mask is the reference's: a boolean keep-mask (Where(mask,
+// scores, -inf), :2847-2871) or an additive one (scores + mask, :2872-2878), of
+// any rank broadcast to the scores [B, H, Sq, Sk] (:2959-2974), read through
+// element strides (0 on broadcast axes).  GQA reads KV head h / (H / Hkv)
+// directly (function.go:2911-2956 repeats it).
 //
 // Never materialises the [B, H, Sq, Sk] scores (the composite path writes and
 // re-reads them: 1 GiB of bf16 traffic at B4 H16 S2048).  Per workgroup: 128
@@ -35,25 +39,31 @@ namespace attn {
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
 typedef int i32x4_t __attribute__((ext_vector_type(4)));
+
+enum MaskKind { kNoMask = 0, kBoolMask = 1, kAddMask = 2 };
 
 struct Params {
   const void* q;
   const void* k;
   const void* v;
   void* o;
-  int64_t q_sb, q_sh, q_ss;  // element strides of batch, head, sequence (d stride 1)
+  const void* mask;             // bool (uint8) keep-mask, or additive in Q's dtype
+  int64_t q_sb, q_sh, q_ss;     // element strides of batch, head, sequence (d stride 1)
   int64_t k_sb, k_sh, k_ss;
   int64_t v_sb, v_sh, v_ss;
   int64_t o_sb, o_sh, o_ss;
+  int64_t m_sb, m_sh, m_sq, m_sk;  // mask element strides (0 where it broadcasts)
   int B, H, Hkv, Sq, Sk;
   float scale_log2;             // softmax scale * log2(e)
+  float inv_scale;              // 1 / scale (additive masks are added to raw scores / scale)
   int causal;
+  int mask_vec;                 // m_sk == 1 and 4-key groups are aligned: vector mask loads
   uint32_t k_extent, v_extent;  // bytes addressable from one (batch, kv head) slice
 };
 
-constexpr int kD = 128;     // head dim
 constexpr int kBKV = 64;    // keys per tile
 constexpr int kQW = 32;     // queries per wave
 constexpr int kWaves = 4;   // waves per workgroup
@@ -83,37 +93,75 @@ __device__ __forceinline__ void dma16(i32x4_t rsrc, uint32_t la, uint32_t voff) 
 }
 #pragma clang diagnostic pop
 
-// LDS tiles are [64 keys][128 d] bf16: 256-byte rows of 16 chunks of 16 B.
-// K: chunk kc of key row r sits at slot kc ^ (r & 15), so the 16 (8) rows of a
+// LDS tiles are [64 keys][D] 16-bit values: rows of C = D / 8 chunks of 16 B.
+// K: chunk kc of key row r sits at slot kc ^ (r % C), so the 8 or 16 rows of a
 // ds_read_b128 phase land in distinct bank groups.
-__device__ __forceinline__ int swz_k(int r) { return r & 15; }
-// V: chunk j of key row r sits at slot j ^ {0, 6, 10, 12}[r & 3] (a transpose read
-// touches 4 consecutive rows x 2-4 chunks).
-__device__ __forceinline__ int swz_v(int r) { return (0xCA60u >> ((r & 3) * 4)) & 15u; }
+template <int D>
+__device__ __forceinline__ int swz_k(int r) { return r & (D / 8 - 1); }
+// V: chunk j of key row r sits at slot j ^ f(r & 3): a transpose read touches 4
+// consecutive rows x 2 (D = 64) or 2-4 (D = 128) chunks.  D = 128: f = {0, 6, 10,
+// 12}; D = 64 (8 chunks a row): f = {0, 2, 4, 6}, which keeps the chunk pairs of a
+// 32-byte read together and spreads the 4 rows over all 8 bank groups.
+template <int D>
+__device__ __forceinline__ int swz_v(int r) {
+  if constexpr (D == 128) return (0xCA60u >> ((r & 3) * 4)) & 15u;
+  else return 2 * (r & 3);
+}
 
 // K fragment (A operand of S^T = K Q^T): key row kb*32 + lane%32, d = 16s + 8*(lane/32).
+template <int D>
 __device__ __forceinline__ bf16x8_t frag_k(const uint16_t* lds, int kb, int s, int lane) {
   const int row = kb * 32 + (lane & 31);
-  const int slot = (2 * s + (lane >> 5)) ^ swz_k(row);
-  return *reinterpret_cast<const bf16x8_t*>(lds + row * kD + slot * 8);
+  const int slot = (2 * s + (lane >> 5)) ^ swz_k<D>(row);
+  return *reinterpret_cast<const bf16x8_t*>(lds + row * D + slot * 8);
 }
 // V^T fragment (A operand of O^T = V^T P^T), d block db, key step s: lane
 // (d = 32 db + lane%32, h = lane/32) gets keys 16s + 4h + {0..3} and
 // 16s + 8 + 4h + {0..3}.  ds_read_b64_tr_b16 hands lane j of each 16-lane group
 // element j of the four 4-element rows the group points at.
+template <int D>
 __device__ __forceinline__ bf16x8_t frag_v(const uint16_t* lds, int db, int s, int lane) {
   const int kl = 16 * s + 4 * (lane >> 5) + ((lane & 15) >> 2);
   const int nl = db * 32 + 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
-  const uint16_t* p0 = lds + kl * kD + (((nl >> 3) ^ swz_v(kl)) * 8) + (nl & 7);
-  const uint16_t* p1 = p0 + 8 * kD;  // key + 8 keeps key & 3, hence the swizzle
+  const uint16_t* p0 = lds + kl * D + (((nl >> 3) ^ swz_v<D>(kl)) * 8) + (nl & 7);
+  const uint16_t* p1 = p0 + 8 * D;  // key + 8 keeps key & 3, hence the swizzle
   bf16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((GHIP_ALDS bf16x4_t*)(p0));
   bf16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((GHIP_ALDS bf16x4_t*)(p1));
   return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
 }
 
+// 32x32x16 MFMA on 16-bit operands held as bf16 bits: bf16, or f16 when F16.
+template <bool F16>
+__device__ __forceinline__ f32x16_t mma(const bf16x8_t& a, const bf16x8_t& b, const f32x16_t& c) {
+  if constexpr (F16)
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8_t, a), __builtin_bit_cast(f16x8_t, b), c,
+                                                  0, 0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+template <bool F16>
+__device__ __forceinline__ __bf16 to16(float x) {
+  if constexpr (F16) return __builtin_bit_cast(__bf16, static_cast<_Float16>(x));
+  else return static_cast<__bf16>(x);
+}
+template <bool F16>
+__device__ __forceinline__ float from16(uint16_t b) {
+  if constexpr (F16) return f16_to_f32(b);
+  else return bf16_to_f32(b);
+}
+template <bool F16>
+__device__ __forceinline__ uint32_t pack16x2(float lo, float hi) {
+  if constexpr (F16) return pack_f16x2(lo, hi);
+  else return pack_bf16x2(lo, hi);
+}
+
+template <int D, bool F16, int MK>
 __global__ __launch_bounds__(256, 2) void sdpa_fwd_kernel(Params p) {
-  // [stage][K | V][64 keys x 128 d]
-  __shared__ __attribute__((aligned(1024))) uint16_t smem[2][2][kBKV * kD];
+  constexpr int NCH = D / 8;  // 16-byte chunks per key row
+  constexpr int NDMA = kBKV * D * 2 / 1024 / kWaves;  // DMA instructions per wave per K (or V) tile
+  constexpr int RPI = 1024 / (D * 2);                 // key rows per DMA instruction
+  // [stage][K | V][64 keys x D]
+  __shared__ __attribute__((aligned(1024))) uint16_t smem[2][2][kBKV * D];
   const uint32_t lds0 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>((GHIP_ALDS void*)&smem[0][0][0]));
 
   const int lane = threadIdx.x & 63;
@@ -136,14 +184,16 @@ __global__ __launch_bounds__(256, 2) void sdpa_fwd_kernel(Params p) {
   const uint16_t* Vb = static_cast<const uint16_t*>(p.v) + b * p.v_sb + hk * p.v_sh;
 
   // Q fragments (B operand of S^T): query qi, d = 16s + 8*h2 .. +8.
-  bf16x8_t qf[kD / 16];
+  bf16x8_t qf[D / 16];
 #pragma unroll
-  for (int s = 0; s < kD / 16; ++s) {
+  for (int s = 0; s < D / 16; ++s) {
     if (qi < p.Sq)
       qf[s] = *reinterpret_cast<const bf16x8_t*>(Q + static_cast<int64_t>(qi) * p.q_ss + 16 * s + 8 * h2);
     else
       qf[s] = bf16x8_t{};
   }
+  // This lane's mask row (query qi of (b, h)); keys step by m_sk.
+  const int64_t mrow = b * p.m_sb + h * p.m_sh + static_cast<int64_t>(qi < p.Sq ? qi : 0) * p.m_sq;
 
   const int kv_end = p.causal ? min(p.Sk, q0 + kBQ) : p.Sk;
   const int ntiles = (kv_end + kBKV - 1) / kBKV;
@@ -151,37 +201,69 @@ __global__ __launch_bounds__(256, 2) void sdpa_fwd_kernel(Params p) {
   // is folded into one FMA per exponent: exp2(s * c - m * c).
   const float c = p.scale_log2;
 
-  // Per-lane byte offsets of this wave's 4 K and 4 V DMA instructions within a
-  // tile (instruction i fills key rows 4 (4 wave + i) .. +4, 16 lanes per row).
-  // Keys past Sk lie beyond the descriptor's extent and read zeros.
-  uint32_t koff[4], voff[4];
+  // Per-lane byte offsets of this wave's NDMA K and NDMA V DMA instructions within
+  // a tile (instruction i fills key rows RPI (NDMA wave + i) .. +RPI, NCH lanes a
+  // row).  Keys past Sk lie beyond the descriptor's extent and read zeros.
+  uint32_t koff[NDMA], voff[NDMA];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int r = (wave * 4 + i) * 4 + lane / 16;
-    const int cc = lane % 16;
-    koff[i] = static_cast<uint32_t>((static_cast<int64_t>(r) * p.k_ss + (cc ^ swz_k(r)) * 8) * 2);
-    voff[i] = static_cast<uint32_t>((static_cast<int64_t>(r) * p.v_ss + (cc ^ swz_v(r)) * 8) * 2);
+  for (int i = 0; i < NDMA; ++i) {
+    const int r = (wave * NDMA + i) * RPI + lane / NCH;
+    const int cc = lane % NCH;
+    koff[i] = static_cast<uint32_t>((static_cast<int64_t>(r) * p.k_ss + (cc ^ swz_k<D>(r)) * 8) * 2);
+    voff[i] = static_cast<uint32_t>((static_cast<int64_t>(r) * p.v_ss + (cc ^ swz_v<D>(r)) * 8) * 2);
   }
   const uint32_t kstep = static_cast<uint32_t>(kBKV * p.k_ss * 2), vstep = static_cast<uint32_t>(kBKV * p.v_ss * 2);
   auto issue = [&](int t, int st) {
     const uint32_t dk = static_cast<uint32_t>(t) * kstep, dv = static_cast<uint32_t>(t) * vstep;
     const i32x4_t rk = make_rsrc(reinterpret_cast<const char*>(Kb) + dk, p.k_extent - dk);
     const i32x4_t rv = make_rsrc(reinterpret_cast<const char*>(Vb) + dv, p.v_extent - dv);
-    const uint32_t lk = lds0 + static_cast<uint32_t>(st) * (2 * kBKV * kD * 2) + wave * 4 * 1024;
-    const uint32_t lv = lk + kBKV * kD * 2;
+    const uint32_t lk = lds0 + static_cast<uint32_t>(st) * (2 * kBKV * D * 2) + wave * NDMA * 1024;
+    const uint32_t lv = lk + kBKV * D * 2;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) dma16(rk, lk + i * 1024, koff[i]);
+    for (int i = 0; i < NDMA; ++i) dma16(rk, lk + i * 1024, koff[i]);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) dma16(rv, lv + i * 1024, voff[i]);
+    for (int i = 0; i < NDMA; ++i) dma16(rv, lv + i * 1024, voff[i]);
   };
 
-  f32x16_t o[kD / 32];
+  f32x16_t o[D / 32];
 #pragma unroll
-  for (int db = 0; db < kD / 32; ++db)
+  for (int db = 0; db < D / 32; ++db)
 #pragma unroll
     for (int v = 0; v < 16; ++v) o[db][v] = 0.f;
   float m = -INFINITY;  // reference max (raw scores) the exponents are taken against
   float l = 0.f;        // running sum over this half-wave's keys
+
+  // Mask values of the 4-key group g (keys key0 + 32 kb + 4 h2 + 8 g + 0..3) for
+  // score register pair v = 4 g .. 4 g + 3 of s{kb}: keep flags or additive terms.
+  auto mask_group = [&](int key, float* out) {
+    if constexpr (MK == kBoolMask) {
+      const uint8_t* mp = static_cast<const uint8_t*>(p.mask) + mrow;
+      if (p.mask_vec && key + 3 < p.Sk) {
+        const uint32_t w = *reinterpret_cast<const uint32_t*>(mp + key);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) out[e] = ((w >> (8 * e)) & 0xffu) ? 0.f : -INFINITY;
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          out[e] = (key + e < p.Sk && !mp[static_cast<int64_t>(key + e) * p.m_sk]) ? -INFINITY : 0.f;
+      }
+    } else {
+      const uint16_t* mp = static_cast<const uint16_t*>(p.mask) + mrow;
+      if (p.mask_vec && key + 3 < p.Sk) {
+        const uint2 w = *reinterpret_cast<const uint2*>(mp + key);
+        out[0] = from16<F16>(static_cast<uint16_t>(w.x));
+        out[1] = from16<F16>(static_cast<uint16_t>(w.x >> 16));
+        out[2] = from16<F16>(static_cast<uint16_t>(w.y));
+        out[3] = from16<F16>(static_cast<uint16_t>(w.y >> 16));
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          out[e] = key + e < p.Sk ? from16<F16>(mp[static_cast<int64_t>(key + e) * p.m_sk]) : 0.f;
+      }
+#pragma unroll
+      for (int e = 0; e < 4; ++e) out[e] *= p.inv_scale;
+    }
+  };
 
   // One barrier per tile: at the top of tile t every wave has finished tile t-1,
   // so once tile t has landed, stage (t+1) & 1 can take tile t+1.
@@ -193,6 +275,15 @@ __global__ __launch_bounds__(256, 2) void sdpa_fwd_kernel(Params p) {
     // Causal: a wave whose last query precedes the tile's first key has nothing to
     // do here (it still takes part in the barriers and loads).
     if (p.causal && key0 > qw + kQW - 1) return;
+    // The mask terms of this tile, fetched before the MFMAs so their latency
+    // overlaps them.
+    float mk[2][16];
+    if constexpr (MK != kNoMask) {
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) mask_group(key0 + 32 * kb + 4 * h2 + 8 * g, &mk[kb][4 * g]);
+    }
     const uint16_t* sk = &smem[st][0][0];
     const uint16_t* sv = &smem[st][1][0];
     f32x16_t s0, s1;
@@ -202,12 +293,19 @@ __global__ __launch_bounds__(256, 2) void sdpa_fwd_kernel(Params p) {
       s1[v] = 0.f;
     }
 #pragma unroll
-    for (int s = 0; s < kD / 16; ++s) {
-      s0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(frag_k(sk, 0, s, lane), qf[s], s0, 0, 0, 0);
-      s1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(frag_k(sk, 1, s, lane), qf[s], s1, 0, 0, 0);
+    for (int s = 0; s < D / 16; ++s) {
+      s0 = mma<F16>(frag_k<D>(sk, 0, s, lane), qf[s], s0);
+      s1 = mma<F16>(frag_k<D>(sk, 1, s, lane), qf[s], s1);
     }
-    // s{kb}[v] is key key0 + 32 kb + 4 h2 + kv, kv = (v/4)*8 + v%4, for query qi;
-    // only the diagonal tile(s) and a ragged last tile need the element mask:
+    // s{kb}[v] is key key0 + 32 kb + 4 h2 + kv, kv = (v/4)*8 + v%4, for query qi.
+    if constexpr (MK != kNoMask) {
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        s0[v] += mk[0][v];
+        s1[v] += mk[1][v];
+      }
+    }
+    // Only the diagonal tile(s) and a ragged last tile need the element mask:
     // visible iff kv (+32 for s1) < lim.
     if ((p.causal && key0 + kBKV - 1 > qw) || key0 + kBKV > p.Sk) {
       const int lim = min(p.Sk, p.causal ? qi + 1 : p.Sk) - key0 - 4 * h2;
@@ -226,7 +324,7 @@ __global__ __launch_bounds__(256, 2) void sdpa_fwd_kernel(Params p) {
     mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
     // Lazy rescale: the reference max only moves (with o and l rescaled) when
     // some lane's tile max exceeds it by more than kLazyLog2, so exponents stay
-    // <= 2^kLazyLog2 and the 64 multiplies of the rescale are rare.  The result
+    // <= 2^kLazyLog2 and the multiplies of the rescale are rare.  The result
     // o / l does not depend on the reference chosen.
     if (__builtin_amdgcn_ballot_w64((mx - m) * c > kLazyLog2)) {
       const float mnew = fmaxf(m, mx);
@@ -235,7 +333,7 @@ __global__ __launch_bounds__(256, 2) void sdpa_fwd_kernel(Params p) {
       m = mnew;
       l *= alpha;
 #pragma unroll
-      for (int db = 0; db < kD / 32; ++db)
+      for (int db = 0; db < D / 32; ++db)
 #pragma unroll
         for (int v = 0; v < 16; ++v) o[db][v] *= alpha;
     }
@@ -251,20 +349,19 @@ __global__ __launch_bounds__(256, 2) void sdpa_fwd_kernel(Params p) {
       s1[v] = e1;
     }
     l += ls;
-    // P^T operand of key step s: s{s/2}[8 (s%2) .. +8] rounded to bf16.
+    // P^T operand of key step s: s{s/2}[8 (s%2) .. +8] rounded to the 16-bit type.
     bf16x8_t pb[4];
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      pb[0][e] = static_cast<__bf16>(s0[e]);
-      pb[1][e] = static_cast<__bf16>(s0[8 + e]);
-      pb[2][e] = static_cast<__bf16>(s1[e]);
-      pb[3][e] = static_cast<__bf16>(s1[8 + e]);
+      pb[0][e] = to16<F16>(s0[e]);
+      pb[1][e] = to16<F16>(s0[8 + e]);
+      pb[2][e] = to16<F16>(s1[e]);
+      pb[3][e] = to16<F16>(s1[8 + e]);
     }
 #pragma unroll
     for (int s = 0; s < kBKV / 16; ++s)
 #pragma unroll
-      for (int db = 0; db < kD / 32; ++db)
-        o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(frag_v(sv, db, s, lane), pb[s], o[db], 0, 0, 0);
+      for (int db = 0; db < D / 32; ++db) o[db] = mma<F16>(frag_v<D>(sv, db, s, lane), pb[s], o[db]);
     // This stage's LDS reads complete before the next barrier, after which it is
     // refilled.
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
@@ -276,32 +373,45 @@ __global__ __launch_bounds__(256, 2) void sdpa_fwd_kernel(Params p) {
     if (t + 1 < ntiles) tile(t + 1, 1);
   }
 
-  // o[db][v] is d = 32 db + (v/4)*8 + 4 h2 + v%4 of query qi.
+  // o[db][v] is d = 32 db + (v/4)*8 + 4 h2 + v%4 of query qi.  A query whose keys
+  // are all masked has l = 0: its output is NaN, as the reference's softmax of a
+  // row of -inf gives.
   const float lt = l + __shfl_xor(l, 32, 64);
-  const float inv = lt > 0.f ? 1.0f / lt : 0.f;
+  const float inv = 1.0f / lt;
   if (qi < p.Sq) {
     uint16_t* O = static_cast<uint16_t*>(p.o) + b * p.o_sb + h * p.o_sh + static_cast<int64_t>(qi) * p.o_ss;
 #pragma unroll
-    for (int db = 0; db < kD / 32; ++db)
+    for (int db = 0; db < D / 32; ++db)
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
         const int d = db * 32 + g * 8 + 4 * h2;
-        *reinterpret_cast<uint2*>(O + d) =
-            make_uint2(pack_bf16x2(o[db][g * 4 + 0] * inv, o[db][g * 4 + 1] * inv),
-                       pack_bf16x2(o[db][g * 4 + 2] * inv, o[db][g * 4 + 3] * inv));
+        const float r0 = lt > 0.f ? o[db][g * 4 + 0] * inv : __builtin_nanf("");
+        const float r1 = lt > 0.f ? o[db][g * 4 + 1] * inv : __builtin_nanf("");
+        const float r2 = lt > 0.f ? o[db][g * 4 + 2] * inv : __builtin_nanf("");
+        const float r3 = lt > 0.f ? o[db][g * 4 + 3] * inv : __builtin_nanf("");
+        *reinterpret_cast<uint2*>(O + d) = make_uint2(pack16x2<F16>(r0, r1), pack16x2<F16>(r2, r3));
       }
   }
 }
 
+template <int D, bool F16>
+static void launch_d(const Params& p, int mk, dim3 grid, hipStream_t s) {
+  if (mk == kBoolMask) hipLaunchKernelGGL((sdpa_fwd_kernel<D, F16, kBoolMask>), grid, dim3(256), 0, s, p);
+  else if (mk == kAddMask) hipLaunchKernelGGL((sdpa_fwd_kernel<D, F16, kAddMask>), grid, dim3(256), 0, s, p);
+  else hipLaunchKernelGGL((sdpa_fwd_kernel<D, F16, kNoMask>), grid, dim3(256), 0, s, p);
+}
+
 }  // namespace attn
 
-// Whether ghip_sdpa_fwd takes these operands (checked again, with the pointers,
-// by the entry point).  Strides are in elements, ordered (batch, head, sequence);
-// the head dim must be contiguous.
+// Whether ghip_sdpa_fwd_masked takes these operands (checked again, with the
+// pointers, by the entry point).  Strides are in elements, ordered (batch, head,
+// sequence); the head dim must be contiguous.  mask_dtype < 0: no mask.
 bool sdpa_fused_supported(int dtype, int64_t H, int64_t Hkv, int64_t Sq, int64_t Sk, int64_t D,
                           const int64_t* qs, const int64_t* ks, const int64_t* vs, const int64_t* os,
-                          float scale) {
-  if (dtype != GHIP_DTYPE_BFLOAT16 || D != attn::kD || Hkv <= 0 || H % Hkv != 0) return false;
+                          float scale, int mask_dtype) {
+  if (dtype != GHIP_DTYPE_BFLOAT16 && dtype != GHIP_DTYPE_FLOAT16) return false;
+  if ((D != 64 && D != 128) || Hkv <= 0 || H % Hkv != 0) return false;
+  if (mask_dtype >= 0 && mask_dtype != GHIP_DTYPE_BOOL && mask_dtype != dtype) return false;
   if (!(scale > 0.f) || !(scale < 1e30f)) return false;  // positive and finite
   if (Sq <= 0 || Sk <= 0 || Sq > (int64_t{1} << 30) || Sk > (int64_t{1} << 30)) return false;
   for (const int64_t* s : {qs, ks, vs})
@@ -319,11 +429,12 @@ bool sdpa_fused_supported(int dtype, int64_t H, int64_t Hkv, int64_t Sq, int64_t
 
 using namespace ghip;
 
-extern "C" int ghip_sdpa_fwd(int dtype, const void* q, const void* k, const void* v, void* o,
-                             int64_t B, int64_t H, int64_t Hkv, int64_t Sq, int64_t Sk, int64_t D,
-                             const int64_t* q_strides, const int64_t* k_strides,
-                             const int64_t* v_strides, const int64_t* o_strides, float scale,
-                             int causal, void* stream, GHipError* err) {
+extern "C" int ghip_sdpa_fwd_masked(int dtype, const void* q, const void* k, const void* v, void* o,
+                                    int64_t B, int64_t H, int64_t Hkv, int64_t Sq, int64_t Sk, int64_t D,
+                                    const int64_t* q_strides, const int64_t* k_strides,
+                                    const int64_t* v_strides, const int64_t* o_strides, const void* mask,
+                                    int mask_dtype, const int64_t* mask_strides, float scale, int causal,
+                                    void* stream, GHipError* err) {
   if (B < 0 || H <= 0 || Hkv <= 0 || Sq < 0 || Sk < 0 || D <= 0)
     return set_error(err, GHIP_ERR_INVALID_ARG, "sdpa_fwd: bad sizes");
   if (H % Hkv != 0)
@@ -331,12 +442,15 @@ extern "C" int ghip_sdpa_fwd(int dtype, const void* q, const void* k, const void
                      static_cast<long long>(H), static_cast<long long>(Hkv));
   if (!q_strides || !k_strides || !v_strides || !o_strides)
     return set_error(err, GHIP_ERR_INVALID_ARG, "sdpa_fwd: null strides");
+  if (mask && !mask_strides) return set_error(err, GHIP_ERR_INVALID_ARG, "sdpa_fwd: mask without strides");
   if (B == 0 || Sq == 0) return GHIP_OK;
   if (!q || !k || !v || !o) return set_error(err, GHIP_ERR_INVALID_ARG, "sdpa_fwd: null pointer");
-  if (!sdpa_fused_supported(dtype, H, Hkv, Sq, Sk, D, q_strides, k_strides, v_strides, o_strides, scale))
+  const int mdt = mask ? mask_dtype : -1;
+  if (!sdpa_fused_supported(dtype, H, Hkv, Sq, Sk, D, q_strides, k_strides, v_strides, o_strides, scale, mdt))
     return set_error(err, GHIP_ERR_UNSUPPORTED,
-                     "sdpa_fwd: needs bfloat16, head dim 128, a positive finite scale, non-negative strides "
-                     "that are multiples of 8 (4 for the output) and < 2 GiB per K/V head");
+                     "sdpa_fwd: needs bfloat16 or float16, head dim 64 or 128, a bool mask or one in the "
+                     "operands' dtype, a positive finite scale, non-negative strides that are multiples of 8 "
+                     "(4 for the output) and < 2 GiB per K/V head");
   auto al = [](const void* ptr, uintptr_t a) { return (reinterpret_cast<uintptr_t>(ptr) & (a - 1)) == 0; };
   if (!al(q, 16) || !al(k, 16) || !al(v, 16) || !al(o, 8))
     return set_error(err, GHIP_ERR_UNSUPPORTED, "sdpa_fwd: q/k/v must be 16-byte aligned, o 8-byte aligned");
@@ -351,11 +465,39 @@ extern "C" int ghip_sdpa_fwd(int dtype, const void* q, const void* k, const void
   p.B = static_cast<int>(B); p.H = static_cast<int>(H); p.Hkv = static_cast<int>(Hkv);
   p.Sq = static_cast<int>(Sq); p.Sk = static_cast<int>(Sk);
   p.scale_log2 = scale * 1.4426950408889634f;
+  p.inv_scale = 1.0f / scale;
   p.causal = causal ? 1 : 0;
   p.k_extent = static_cast<uint32_t>(((Sk - 1) * p.k_ss + D) * 2);
   p.v_extent = static_cast<uint32_t>(((Sk - 1) * p.v_ss + D) * 2);
-  hipLaunchKernelGGL(attn::sdpa_fwd_kernel, dim3(static_cast<unsigned>(nqb * B * H)), dim3(256), 0,
-                     static_cast<hipStream_t>(stream), p);
+  int mk = attn::kNoMask;
+  if (mask) {
+    mk = mask_dtype == GHIP_DTYPE_BOOL ? attn::kBoolMask : attn::kAddMask;
+    p.mask = mask;
+    p.m_sb = mask_strides[0]; p.m_sh = mask_strides[1]; p.m_sq = mask_strides[2]; p.m_sk = mask_strides[3];
+    // Vector loads of 4-key groups (keys are multiples of 4 apart): unit key stride
+    // and every row start aligned to 4 elements.
+    const int64_t es = mask_dtype == GHIP_DTYPE_BOOL ? 1 : 2;
+    p.mask_vec = p.m_sk == 1 && p.m_sb % 4 == 0 && p.m_sh % 4 == 0 && p.m_sq % 4 == 0 && al(mask, 4 * es);
+  }
+  const dim3 grid(static_cast<unsigned>(nqb * B * H));
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  const bool f16 = dtype == GHIP_DTYPE_FLOAT16;
+  if (D == 64) {
+    if (f16) attn::launch_d<64, true>(p, mk, grid, s);
+    else attn::launch_d<64, false>(p, mk, grid, s);
+  } else {
+    if (f16) attn::launch_d<128, true>(p, mk, grid, s);
+    else attn::launch_d<128, false>(p, mk, grid, s);
+  }
   GHIP_CHECK(hipGetLastError(), err);
   return GHIP_OK;
+}
+
+extern "C" int ghip_sdpa_fwd(int dtype, const void* q, const void* k, const void* v, void* o,
+                             int64_t B, int64_t H, int64_t Hkv, int64_t Sq, int64_t Sk, int64_t D,
+                             const int64_t* q_strides, const int64_t* k_strides,
+                             const int64_t* v_strides, const int64_t* o_strides, float scale,
+                             int causal, void* stream, GHipError* err) {
+  return ghip_sdpa_fwd_masked(dtype, q, k, v, o, B, H, Hkv, Sq, Sk, D, q_strides, k_strides, v_strides, o_strides,
+                              nullptr, -1, nullptr, scale, causal, stream, err);
 }

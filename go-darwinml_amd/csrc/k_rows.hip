@@ -34,10 +34,16 @@ struct RowParams {
   void* y;
   const void* gamma;
   const void* beta;
-  const uint8_t* bmask;  // [sq, sk] keep-mask for kMaskedSoftmax (may be null)
+  // kMaskedSoftmax: a boolean keep-mask (uint8) or an additive mask in the
+  // scores' dtype, addressed as mask + b m_sb + h m_sh + q m_sq + key m_sk for row
+  // (b, h, q) of the [B, H, Sq, Sk] scores (strides 0 where it broadcasts).
+  const void* mask;
+  int mask_kind;         // 0 none, 1 keep-mask, 2 additive
+  int64_t m_sb, m_sh, m_sq, m_sk;
   int64_t rows;
   int64_t n;
   int64_t sq;            // rows per attention matrix (kMaskedSoftmax)
+  int64_t heads;         // H (kMaskedSoftmax)
   float eps;
   float scale;
   int causal;
@@ -157,7 +163,11 @@ __global__ __launch_bounds__(256) void rows_reg_kernel(RowParams p) {
 
   if constexpr (OP == kSoftmax || OP == kLogSoftmax || OP == kMaskedSoftmax) {
     const int64_t qrow = (OP == kMaskedSoftmax) ? ((row_ok ? row : 0) % p.sq) : 0;
-    const uint8_t* mrow = (OP == kMaskedSoftmax && p.bmask) ? p.bmask + qrow * n : nullptr;
+    int64_t moff = 0;
+    if constexpr (OP == kMaskedSoftmax) {
+      const int64_t bh = (row_ok ? row : 0) / p.sq;
+      moff = (bh / p.heads) * p.m_sb + (bh % p.heads) * p.m_sh + qrow * p.m_sq;
+    }
     // Value j of vector i after scale / masks (-inf where masked or not live).
     auto val = [&](int i, float* f) {
       const int64_t c0 = (static_cast<int64_t>(i) * LANES + l) * VEC;
@@ -174,8 +184,9 @@ __global__ __launch_bounds__(256) void rows_reg_kernel(RowParams p) {
 #pragma unroll
         for (int j = 0; j < VEC; ++j) {
           float s = f[j] * p.scale;
+          if (p.mask_kind == 1 && !static_cast<const uint8_t*>(p.mask)[moff + (c0 + j) * p.m_sk]) s = -INFINITY;
+          if (p.mask_kind == 2) s += Elem<T>::load1(static_cast<const T*>(p.mask) + moff + (c0 + j) * p.m_sk);
           if (p.causal && c0 + j > qrow) s = -INFINITY;
-          if (mrow && !mrow[c0 + j]) s = -INFINITY;
           f[j] = s;
         }
       }
@@ -384,13 +395,18 @@ __global__ __launch_bounds__(256) void rows_generic_kernel(RowParams p) {
 
   if constexpr (OP == kSoftmax || OP == kLogSoftmax || OP == kMaskedSoftmax) {
     const int64_t qrow = (OP == kMaskedSoftmax) ? (row % p.sq) : 0;
-    const uint8_t* mrow = (OP == kMaskedSoftmax && p.bmask) ? p.bmask + qrow * n : nullptr;
+    int64_t moff = 0;
+    if constexpr (OP == kMaskedSoftmax) {
+      const int64_t bh = row / p.sq;
+      moff = (bh / p.heads) * p.m_sb + (bh % p.heads) * p.m_sh + qrow * p.m_sq;
+    }
     auto val = [&](int64_t c) -> float {
       float s = Elem<T>::load1(xr + c);
       if constexpr (OP == kMaskedSoftmax) {
         s *= p.scale;
+        if (p.mask_kind == 1 && !static_cast<const uint8_t*>(p.mask)[moff + c * p.m_sk]) s = -INFINITY;
+        if (p.mask_kind == 2) s += Elem<T>::load1(static_cast<const T*>(p.mask) + moff + c * p.m_sk);
         if (p.causal && c > qrow) s = -INFINITY;
-        if (mrow && !mrow[c]) s = -INFINITY;
       }
       return s;
     };
@@ -504,6 +520,26 @@ extern "C" int ghip_softmax_rows(int dtype, const void* x, void* y, int64_t rows
   return dispatch_rows<kSoftmax>(dtype, p, stream, err, "softmax_rows");
 }
 
+extern "C" int ghip_scale_mask_softmax_rows_ex(int dtype, const void* x, void* y, int64_t B, int64_t H,
+                                               int64_t sq, int64_t sk, float scale, int causal, const void* mask,
+                                               int mask_dtype, const int64_t* mask_strides, void* stream,
+                                               GHipError* err) {
+  if (B < 0 || H <= 0 || sq <= 0 || sk < 0)
+    return set_error(err, GHIP_ERR_INVALID_ARG, "scale_mask_softmax_rows: bad sizes");
+  RowParams p{};
+  p.x = x; p.y = y; p.rows = B * H * sq; p.n = sk; p.sq = sq; p.heads = H; p.scale = scale;
+  p.causal = causal;
+  if (mask) {
+    if (!mask_strides) return set_error(err, GHIP_ERR_INVALID_ARG, "scale_mask_softmax_rows: mask without strides");
+    if (mask_dtype != GHIP_DTYPE_BOOL && mask_dtype != dtype)
+      return set_error(err, GHIP_ERR_INVALID_ARG, "scale_mask_softmax_rows: mask must be bool or the scores' dtype");
+    p.mask = mask;
+    p.mask_kind = mask_dtype == GHIP_DTYPE_BOOL ? 1 : 2;
+    p.m_sb = mask_strides[0]; p.m_sh = mask_strides[1]; p.m_sq = mask_strides[2]; p.m_sk = mask_strides[3];
+  }
+  return dispatch_rows<kMaskedSoftmax>(dtype, p, stream, err, "scale_mask_softmax_rows");
+}
+
 extern "C" int ghip_scale_mask_softmax_rows(int dtype, const void* x, void* y, int64_t rows,
                                             int64_t sq, int64_t sk, float scale, int causal,
                                             const uint8_t* bmask, void* stream,
@@ -512,10 +548,9 @@ extern "C" int ghip_scale_mask_softmax_rows(int dtype, const void* x, void* y, i
     return set_error(err, GHIP_ERR_INVALID_ARG,
                      "scale_mask_softmax_rows: rows (%lld) must be a multiple of sq (%lld)",
                      static_cast<long long>(rows), static_cast<long long>(sq));
-  RowParams p{};
-  p.x = x; p.y = y; p.rows = rows; p.n = sk; p.sq = sq; p.scale = scale;
-  p.causal = causal; p.bmask = bmask;
-  return dispatch_rows<kMaskedSoftmax>(dtype, p, stream, err, "scale_mask_softmax_rows");
+  const int64_t ms[4] = {0, 0, sk, 1};
+  return ghip_scale_mask_softmax_rows_ex(dtype, x, y, rows / sq, 1, sq, sk, scale, causal, bmask,
+                                         GHIP_DTYPE_BOOL, ms, stream, err);
 }
 
 extern "C" int ghip_rmsnorm_rows(int dtype, const void* x, const void* gamma, void* y,

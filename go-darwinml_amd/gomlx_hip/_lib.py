@@ -51,6 +51,12 @@ SIGNATURES = {
     "ghip_sdpa_fwd": [_int, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64,
                       ctypes.POINTER(_i64), ctypes.POINTER(_i64), ctypes.POINTER(_i64),
                       ctypes.POINTER(_i64), _f32, _int, _vp, _errp],
+    "ghip_sdpa_fwd_masked": [_int, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64,
+                             ctypes.POINTER(_i64), ctypes.POINTER(_i64), ctypes.POINTER(_i64),
+                             ctypes.POINTER(_i64), _vp, _int, ctypes.POINTER(_i64), _f32, _int, _vp,
+                             _errp],
+    "ghip_scale_mask_softmax_rows_ex": [_int, _vp, _vp, _i64, _i64, _i64, _i64, _f32, _int, _vp, _int,
+                                        ctypes.POINTER(_i64), _vp, _errp],
 }
 
 _lib = None

@@ -133,6 +133,48 @@ def sdpa(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: float, causal
     return o
 
 
+def _mask_strides(mask: torch.Tensor, B, H, Sq, Sk):
+    """Element strides of `mask` broadcast to [B, H, Sq, Sk] over its trailing axes
+    (0 on missing and size-1 axes)."""
+    import ctypes
+    st = [0, 0, 0, 0]
+    off = 4 - mask.dim()
+    for i in range(mask.dim()):
+        if mask.shape[i] != 1:
+            if mask.shape[i] != (B, H, Sq, Sk)[off + i]:
+                raise ValueError(f"mask {tuple(mask.shape)} does not broadcast to {(B, H, Sq, Sk)}")
+            st[off + i] = mask.stride(i)
+    return (ctypes.c_int64 * 4)(*st)
+
+
+def sdpa_masked(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, mask, scale: float, causal: bool,
+                out=None, stream=None):
+    """sdpa with a bool keep-mask or an additive mask (q's dtype) of any rank that
+    broadcasts to the scores [B, H, Sq, Sk]."""
+    _check_dev(q, k, v, mask)
+    B, H, Sq, D = q.shape
+    _, Hkv, Sk, _ = k.shape
+    o = torch.empty((B, H, Sq, D), dtype=q.dtype, device=q.device) if out is None else out
+    mdt = -1 if mask is None else dtype_code(mask.dtype)
+    ms = None if mask is None else _mask_strides(mask, B, H, Sq, Sk)
+    call("ghip_sdpa_fwd_masked", dtype_code(q.dtype), q.data_ptr(), k.data_ptr(), v.data_ptr(),
+         o.data_ptr(), B, H, Hkv, Sq, Sk, D, _strides3(q), _strides3(k), _strides3(v),
+         _strides3(o), _ptr(mask), mdt, ms, float(scale), int(causal), _stream(stream))
+    return o
+
+
+def scale_mask_softmax_ex(x: torch.Tensor, scale: float, causal: bool, mask=None, out=None, stream=None):
+    """softmax(x * scale + mask) over the last axis of scores x [B, H, Sq, Sk]."""
+    _check_dev(x, mask)
+    B, H, Sq, Sk = x.shape
+    y = torch.empty_like(x) if out is None else out
+    mdt = -1 if mask is None else dtype_code(mask.dtype)
+    ms = None if mask is None else _mask_strides(mask, B, H, Sq, Sk)
+    call("ghip_scale_mask_softmax_rows_ex", dtype_code(x.dtype), x.data_ptr(), y.data_ptr(), B, H, Sq, Sk,
+         float(scale), int(causal), _ptr(mask), mdt, ms, _stream(stream))
+    return y
+
+
 def gather_rows(table: torch.Tensor, ids: torch.Tensor, out=None, stream=None):
     """out[i] = table[clamp(ids[i])] for an embedding table [V, ...]."""
     _check_dev(table, ids)

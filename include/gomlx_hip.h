@@ -87,6 +87,16 @@ int ghip_softmax_rows(int dtype, const void* x, void* y, int64_t rows, int64_t n
 int ghip_scale_mask_softmax_rows(int dtype, const void* x, void* y, int64_t rows,
                                  int64_t sq, int64_t sk, float scale, int causal,
                                  const uint8_t* bmask, void* stream, GHipError* err);
+/* The same over scores [B, H, sq, sk] with the reference's full mask surface
+ * (function.go:2840-2878, broadcastMaskToScores :2959-2974): `mask` is a bool
+ * keep-mask (mask_dtype GHIP_DTYPE_BOOL: Where(mask, s, -inf)) or an additive mask
+ * in the scores' dtype (s + mask), read at mask + b*ms[0] + h*ms[1] + q*ms[2] +
+ * key*ms[3] (element strides, 0 on broadcast axes); NULL for none.  Causal keys
+ * are -inf whatever the mask holds. */
+int ghip_scale_mask_softmax_rows_ex(int dtype, const void* x, void* y, int64_t B, int64_t H,
+                                    int64_t sq, int64_t sk, float scale, int causal,
+                                    const void* mask, int mask_dtype, const int64_t* mask_strides,
+                                    void* stream, GHipError* err);
 
 /* RMSNorm over the last axis: y = x * rsqrt(mean(x^2) + eps) * gamma.
  * gamma [n] has x's dtype and may be NULL.  Statistics in fp32.  No reference op:
@@ -122,15 +132,30 @@ int ghip_gemm_batched(int ab_dtype, int c_dtype, int64_t batch, int64_t M, int64
  *                   when causal]) v[b, hk, j, :],   hk = h / (H / Hkv)  (GQA, :2911-2956)
  * Operands are addressed by ELEMENT strides (batch, head, sequence) with the head
  * dim contiguous, so BHSD and BSHD layouts both work without copies.  Supported:
- * dtype BFLOAT16, D == 128, scale > 0, strides multiples of 8 (4 for o), q/k/v
- * 16-byte and o 8-byte aligned; anything else returns GHIP_ERR_UNSUPPORTED (the
- * graph lowering then uses the composite).  Softmax statistics and accumulation
- * are fp32; weights below 2^-126 of a row's largest are flushed to zero. */
+ * dtype BFLOAT16 or FLOAT16, D == 64 or 128, scale > 0, strides multiples of 8
+ * (4 for o), q/k/v 16-byte and o 8-byte aligned; anything else returns
+ * GHIP_ERR_UNSUPPORTED (the graph lowering then uses the composite).  Softmax
+ * statistics and accumulation are fp32; weights below 2^-126 of a row's largest
+ * are flushed to zero. */
 int ghip_sdpa_fwd(int dtype, const void* q, const void* k, const void* v, void* o,
                   int64_t B, int64_t H, int64_t Hkv, int64_t Sq, int64_t Sk, int64_t D,
                   const int64_t* q_strides, const int64_t* k_strides, const int64_t* v_strides,
                   const int64_t* o_strides, float scale, int causal, void* stream,
                   GHipError* err);
+
+/* ghip_sdpa_fwd with the reference's mask operand (function.go:2840-2878): a bool
+ * keep-mask (mask_dtype GHIP_DTYPE_BOOL: scores where false are -inf, :2847-2871)
+ * or an additive mask in the operands' dtype (scale * q.k + mask, :2872-2878), of
+ * any rank broadcast to the scores [B, H, Sq, Sk] (:2959-2974): mask_strides are
+ * its element strides over (b, h, query, key), 0 on broadcast axes.  mask NULL:
+ * no mask.  A query whose keys are all masked gets NaN, as the reference's softmax
+ * of a row of -inf does. */
+int ghip_sdpa_fwd_masked(int dtype, const void* q, const void* k, const void* v, void* o,
+                         int64_t B, int64_t H, int64_t Hkv, int64_t Sq, int64_t Sk, int64_t D,
+                         const int64_t* q_strides, const int64_t* k_strides,
+                         const int64_t* v_strides, const int64_t* o_strides, const void* mask,
+                         int mask_dtype, const int64_t* mask_strides, float scale, int causal,
+                         void* stream, GHipError* err);
 
 /* Embedding lookup: out[i, :] = table[clamp(ids[i], 0, V-1), :] (row_bytes per
  * row, copied bit-exactly).  Replaces the gather fast path

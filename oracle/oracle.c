@@ -263,13 +263,16 @@ void orc_dot_sampled(const float* a, int64_t sa_b, int64_t sa_m, int64_t sa_k,
  * Reference: Function.FusedScaledDotProductAttention (mpsgraph/gomlx/function.go:
  * 2669-2907): scores = DotGeneral(Q, K) contracting D with batch [B,H] (:2746-2753);
  * scores *= scale (:2755-2770); causal keeps rowIota >= colIota over [Sq,Sk]
- * (:2773-2790); boolean mask: Where(mask, scores, -inf) (:2847-2871); softmax over
+ * (:2773-2790); boolean mask: Where(mask, scores, -inf) (:2847-2871); additive
+ * mask: scores + mask (:2872-2878); a mask of any rank broadcasts to the scores
+ * over its trailing axes (broadcastMaskToScores :2959-2974; here element strides
+ * over (b, h, query, key), 0 on broadcast axes); softmax over
  * the last axis (:2880-2886); output = DotGeneral(P, V) (:2888-2897).  GQA repeats
  * each KV head numHeads/numKVHeads times consecutively (repeatHeads :2911-2956),
  * so query head h reads KV head h / (H / Hkv).
  * ------------------------------------------------------------------------- */
-void orc_sdpa(const float* q, const float* k, const float* v, const uint8_t* mask,
-              int64_t B, int64_t H, int64_t Hkv, int64_t Sq, int64_t Sk, int64_t D,
+void orc_sdpa(const float* q, const float* k, const float* v, const void* mask, int mask_kind,
+              const int64_t* mstr, int64_t B, int64_t H, int64_t Hkv, int64_t Sq, int64_t Sk, int64_t D,
               double scale, int causal, double* out) {
   int64_t rep = H / Hkv;
 #pragma omp parallel
@@ -283,17 +286,20 @@ void orc_sdpa(const float* q, const float* k, const float* v, const uint8_t* mas
           const float* qr = q + ((bb * H + h) * Sq + i) * D;
           const float* kb = k + (bb * Hkv + hk) * Sk * D;
           const float* vb = v + (bb * Hkv + hk) * Sk * D;
+          const int64_t mrow = mask_kind ? bb * mstr[0] + h * mstr[1] + i * mstr[2] : 0;
           double mx = -INFINITY;
           for (int64_t j = 0; j < Sk; ++j) {
             double s = 0.0;
             for (int64_t d = 0; d < D; ++d) s += (double)qr[d] * (double)kb[j * D + d];
             s *= scale;
-            int keep = 1;
-            if (causal && !(i >= j)) keep = 0;
-            if (mask && !mask[i * Sk + j]) keep = 0;
-            p[j] = keep ? s : -INFINITY;
+            if (mask_kind == ORC_MASK_BOOL && !((const uint8_t*)mask)[mrow + j * mstr[3]]) s = -INFINITY;
+            if (mask_kind == ORC_MASK_ADD) s += (double)((const float*)mask)[mrow + j * mstr[3]];
+            if (causal && !(i >= j)) s = -INFINITY;
+            p[j] = s;
             if (p[j] > mx) mx = p[j];
           }
+          /* a row with every key masked: exp(-inf - -inf) = NaN, as the reference's
+           * softmax of a row of -inf gives */
           double sum = 0.0;
           for (int64_t j = 0; j < Sk; ++j) { p[j] = exp(p[j] - mx); sum += p[j]; }
           double* orow = out + ((bb * H + h) * Sq + i) * D;

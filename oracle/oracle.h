@@ -92,9 +92,10 @@ void orc_dot_sampled(const float* a, int64_t sa_b, int64_t sa_m, int64_t sa_k,
 /* Scaled dot-product attention in BHSD layout: q [B,H,Sq,D], k/v [B,Hkv,Sk,D].
  * mask (optional, may be NULL) is a boolean [Sq,Sk] (1 = keep).  causal keeps
  * j <= i.  out [B,H,Sq,D]. */
-void orc_sdpa(const float* q, const float* k, const float* v, const uint8_t* mask,
-              int64_t B, int64_t H, int64_t Hkv, int64_t Sq, int64_t Sk, int64_t D,
-              double scale, int causal, double* out);
+enum { ORC_MASK_NONE = 0, ORC_MASK_BOOL = 1, ORC_MASK_ADD = 2 };
+void orc_sdpa(const float* q, const float* k, const float* v, const void* mask, int mask_kind,
+              const int64_t* mask_strides, int64_t B, int64_t H, int64_t Hkv, int64_t Sq, int64_t Sk,
+              int64_t D, double scale, int causal, double* out);
 
 /* Embedding lookup: out[i, :] = table[clamp(ids[i], 0, V-1), :] byte for byte. */
 void orc_gather_rows(const void* table, int64_t V, int64_t row_bytes, const int32_t* ids,

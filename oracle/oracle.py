@@ -51,7 +51,7 @@ def lib():
         L.orc_dot_general.restype = _int
         L.orc_dot_sampled.argtypes = [_vp, _i64, _i64, _i64, _vp, _i64, _i64, _i64, _i64,
                                       _i64p, _i64p, _i64p, _i64, _f64p]
-        L.orc_sdpa.argtypes = [_f32p, _f32p, _f32p, _vp, _i64, _i64, _i64, _i64, _i64, _i64,
+        L.orc_sdpa.argtypes = [_f32p, _f32p, _f32p, _vp, _int, _i64p, _i64, _i64, _i64, _i64, _i64, _i64,
                                ctypes.c_double, _int, _f64p]
         L.orc_gather_rows.argtypes = [_vp, _i64, _i64, _i32p, _i64, _vp]
         L.orc_argminmax.argtypes = [_f32p, _i64, _i64, _i64, _int, _i64p]
@@ -171,19 +171,28 @@ def dot_sampled(a, b, bs, ms, ns) -> np.ndarray:
     return out
 
 
-def sdpa(q, k, v, mask=None, scale=None, causal=False) -> np.ndarray:
-    """Attention in BHSD layout; q [B,H,Sq,D], k/v [B,Hkv,Sk,D]; mask bool [Sq,Sk]."""
+def sdpa(q, k, v, mask=None, scale=None, causal=False, additive=None) -> np.ndarray:
+    """Attention in BHSD layout; q [B,H,Sq,D], k/v [B,Hkv,Sk,D].  mask: a bool
+    keep-mask, additive: an additive mask (fp32); either of any rank that
+    broadcasts (numpy rules, trailing axes) to the scores [B,H,Sq,Sk]."""
     q, k, v = _f32(q), _f32(k), _f32(v)
     B, H, Sq, D = q.shape
     _, Hkv, Sk, _ = k.shape
     if scale is None:
         scale = 1.0 / np.sqrt(D)
-    mp = None
-    if mask is not None:
-        m = np.ascontiguousarray(np.broadcast_to(np.asarray(mask, bool), (Sq, Sk)).astype(np.uint8))
-        mp = m.ctypes.data_as(ctypes.c_void_p)
+    kind, mp, keep = 0, None, None
+    strides = np.zeros(4, np.int64)
+    m = mask if mask is not None else additive
+    if m is not None:
+        kind = 1 if mask is not None else 2
+        keep = np.ascontiguousarray(np.asarray(m, bool if kind == 1 else np.float32))
+        if kind == 1:
+            keep = keep.astype(np.uint8)
+        view = np.broadcast_to(keep, (B, H, Sq, Sk))      # strides 0 on broadcast axes
+        strides = np.asarray([st // keep.itemsize for st in view.strides], np.int64)
+        mp = keep.ctypes.data_as(ctypes.c_void_p)
     out = np.empty((B, H, Sq, D), np.float64)
-    lib().orc_sdpa(q, k, v, mp, B, H, Hkv, Sq, Sk, D, float(scale), int(causal), out)
+    lib().orc_sdpa(q, k, v, mp, kind, strides, B, H, Hkv, Sq, Sk, D, float(scale), int(causal), out)
     return out
 
 

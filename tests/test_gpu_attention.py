@@ -1,11 +1,15 @@
-"""Parity of the fused attention kernel (ghip_sdpa_fwd) against the oracle's
-attention (fp64, oracle/oracle.c orc_sdpa following function.go:2669-2907).
+"""Parity of the fused attention kernel (ghip_sdpa_fwd / ghip_sdpa_fwd_masked)
+against the oracle's attention (fp64, oracle/oracle.c orc_sdpa following
+function.go:2669-2907), for bf16 and f16, head dims 64 and 128, and the
+reference's masks (boolean keep-masks and additive masks of any rank broadcast to
+the scores, function.go:2840-2878, 2959-2974).
 
-Tolerances: bf16 inputs, fp32 softmax / accumulation, P rounded to bf16 before the
-second product and the output rounded to bf16.  Normwise ||got - ref|| / ||ref||
-<= 1e-2 (the north-star bf16 bound).  Elementwise (RMS-floored, conftest.rel_err)
-<= 2.5e-2: two bf16 roundings of up to 2^-9 each (P, then the output) leave the
-worst of ~10^5 outputs just above 1e-2."""
+Tolerances: 16-bit inputs, fp32 softmax / accumulation, P rounded to the 16-bit
+type before the second product and the output rounded once more.  Normwise
+||got - ref|| / ||ref|| <= 1e-2 (the north-star bf16 bound).  Elementwise
+(RMS-floored, conftest.rel_err) <= 2.5e-2: two bf16 roundings of up to 2^-9 each
+(P, then the output) leave the worst of ~10^5 outputs just above 1e-2 (f16 rounds
+8x finer, so the same bounds hold with room)."""
 import numpy as np
 import pytest
 import torch
@@ -22,6 +26,15 @@ def bf16(shape, seed):
     return synth.round_bf16(synth.normal(seed, shape))
 
 
+def r16(a, dt):
+    """fp32 values rounded to the 16-bit dtype dt (returned as fp32)."""
+    return synth.round_bf16(a) if dt == torch.bfloat16 else a.astype(np.float16).astype(np.float32)
+
+
+def dev(a, cuda, dt):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(cuda).to(dt)
+
+
 CASES = [  # (B, H, Hkv, Sq, Sk, causal)
     (1, 2, 2, 128, 128, True),
     (1, 2, 2, 128, 128, False),
@@ -35,18 +48,136 @@ CASES = [  # (B, H, Hkv, Sq, Sk, causal)
 
 
 @pytest.mark.parametrize("case", CASES)
-def test_sdpa_matches_oracle(cuda, case):
+@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])
+def test_sdpa_matches_oracle(cuda, case, D, dt):
     B, H, Hkv, Sq, Sk, causal = case
-    D = 128
-    q = bf16((B, H, Sq, D), 4001 + Sq)
-    k = bf16((B, Hkv, Sk, D), 4002 + Sk)
-    v = bf16((B, Hkv, Sk, D), 4003 + Sk)
+    q = r16(synth.normal(4001 + Sq, (B, H, Sq, D)), dt)
+    k = r16(synth.normal(4002 + Sk, (B, Hkv, Sk, D)), dt)
+    v = r16(synth.normal(4003 + Sk, (B, Hkv, Sk, D)), dt)
     scale = D ** -0.5
     ref = orc.sdpa(q, k, v, scale=scale, causal=causal)
-    tq, tk, tv = (torch.from_numpy(a).to(cuda).to(torch.bfloat16) for a in (q, k, v))
+    tq, tk, tv = (dev(a, cuda, dt) for a in (q, k, v))
     got = ops.sdpa(tq, tk, tv, scale, causal).float().cpu().numpy()
     assert norm_err(got, ref) <= 1e-2
     assert rel_err(got, ref) <= 2.5e-2
+
+
+MASKS = [  # (kind, mask shape as a function of (B, H, Sq, Sk))
+    ("bool", lambda B, H, Sq, Sk: (B, 1, 1, Sk)),      # key padding per batch row
+    ("bool", lambda B, H, Sq, Sk: (B, H, Sq, Sk)),
+    ("bool", lambda B, H, Sq, Sk: (Sq, Sk)),
+    ("add", lambda B, H, Sq, Sk: (B, 1, 1, Sk)),
+    ("add", lambda B, H, Sq, Sk: (B, H, Sq, Sk)),
+    ("add", lambda B, H, Sq, Sk: (1, Sk)),
+    ("add", lambda B, H, Sq, Sk: (1, H, Sq, 1)),       # per-row constant: no effect
+]
+
+
+def _mask(kind, shape, seed, dt):
+    """A boolean keep-mask (key 0 always kept, so no row is empty) or an additive
+    mask in the 16-bit dtype with finite values and some -inf."""
+    if kind == "bool":
+        m = synth.uniform(seed, int(np.prod(shape))).reshape(shape) > 0.35
+        m[..., 0] = True
+        return m
+    a = r16(synth.normal(seed, shape, std=1.5), dt)
+    drop = synth.uniform(seed + 1, int(np.prod(shape))).reshape(shape) > 0.8
+    if shape[-1] > 1:
+        drop[..., 0] = False
+        a = np.where(drop, -np.inf, a).astype(np.float32)
+    return a
+
+
+@pytest.mark.parametrize("mi", range(len(MASKS)))
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("D,dt", [(128, torch.bfloat16), (64, torch.float16)])
+def test_sdpa_masks_match_oracle(cuda, mi, causal, D, dt):
+    """Every mask shape and kind, GQA, ragged query and key tiles."""
+    B, H, Hkv, Sq, Sk = 2, 4, 2, 200, 264
+    kind, fshape = MASKS[mi]
+    q = r16(synth.normal(4401, (B, H, Sq, D)), dt)
+    k = r16(synth.normal(4402, (B, Hkv, Sk, D)), dt)
+    v = r16(synth.normal(4403, (B, Hkv, Sk, D)), dt)
+    m = _mask(kind, fshape(B, H, Sq, Sk), 4404 + mi, dt)
+    scale = D ** -0.5
+    if kind == "bool":
+        ref = orc.sdpa(q, k, v, mask=m, scale=scale, causal=causal)
+        tm = torch.from_numpy(np.ascontiguousarray(m)).to(cuda)
+    else:
+        ref = orc.sdpa(q, k, v, additive=m, scale=scale, causal=causal)
+        tm = dev(m, cuda, dt)
+    got = ops.sdpa_masked(*(dev(a, cuda, dt) for a in (q, k, v)), tm, scale, causal).float().cpu().numpy()
+    assert norm_err(got, ref) <= 1e-2
+    assert rel_err(got, ref) <= 2.5e-2
+
+
+@pytest.mark.parametrize("kind,mshape", [("bool", "b11k"), ("bool", "bhqk"), ("add", "b11k")])
+def test_sdpa_masks_config_shape_rows(cuda, kind, mshape):
+    """BASELINE attention shape B4 H16 S2048 D128 bf16, causal, with a key-padding
+    mask [B,1,1,Sk], a full boolean mask [B,H,Sq,Sk], or an additive float mask
+    [B,1,1,Sk]; sampled rows of every head of two batch rows against the oracle."""
+    B, H, S, D = 4, 16, 2048, 128
+    dt = torch.bfloat16
+    tq = synth.normal_device(4501, (B, H, S, D), device=cuda, dtype=dt)
+    tk = synth.normal_device(4502, (B, H, S, D), device=cuda, dtype=dt)
+    tv = synth.normal_device(4503, (B, H, S, D), device=cuda, dtype=dt)
+    shape = (B, 1, 1, S) if mshape == "b11k" else (B, H, S, S)
+    if kind == "bool":
+        u = synth.normal_device(4504, shape, device=cuda)
+        tm = u > -1.0                                     # keeps ~84%
+        tm[..., 0] = True
+    else:
+        tm = (synth.normal_device(4504, shape, device=cuda) * 2.0).to(dt)
+    got = ops.sdpa_masked(tq, tk, tv, tm, D ** -0.5, True).float().cpu().numpy()
+    rows = np.array([0, 1, 127, 128, 1000, 2047])
+    kmax = rows.max() + 1
+    q, k, v = (t.float().cpu().numpy() for t in (tq, tk, tv))
+    m = (tm if kind == "bool" else tm.float()).cpu().numpy()
+    causal = np.arange(kmax)[None, :] <= rows[:, None]
+    for b in (0, 3):
+        mb = m[b:b + 1, :, :, :kmax] if mshape == "b11k" else m[b:b + 1, :, rows, :kmax]
+        if kind == "bool":
+            ref = orc.sdpa(q[b:b + 1, :, rows], k[b:b + 1, :, :kmax], v[b:b + 1, :, :kmax], scale=D ** -0.5,
+                           mask=mb & causal)
+        else:
+            add = np.where(causal, mb, -np.inf).astype(np.float32)
+            ref = orc.sdpa(q[b:b + 1, :, rows], k[b:b + 1, :, :kmax], v[b:b + 1, :, :kmax], scale=D ** -0.5,
+                           additive=add)
+        assert norm_err(got[b:b + 1, :, rows], ref) <= 1e-2
+
+
+def test_sdpa_fully_masked_row_is_nan(cuda):
+    """A query whose keys are all masked: NaN, like the reference's softmax of -inf
+    (the oracle gives the same)."""
+    B, H, S, D = 1, 2, 128, 128
+    q, k, v = bf16((B, H, S, D), 4601), bf16((B, H, S, D), 4602), bf16((B, H, S, D), 4603)
+    m = np.ones((S, S), bool)
+    m[5] = False
+    got = ops.sdpa_masked(*(dev(a, cuda, torch.bfloat16) for a in (q, k, v)),
+                          torch.from_numpy(m).to(cuda), 0.1, False).float().cpu().numpy()
+    assert np.all(np.isnan(got[:, :, 5])) and np.all(np.isfinite(np.delete(got, 5, axis=2)))
+    assert np.all(np.isnan(orc.sdpa(q, k, v, mask=m, scale=0.1)[:, :, 5]))
+
+
+@pytest.mark.parametrize("kind", ["bool", "add"])
+def test_composite_masked_softmax_general_masks(cuda, kind):
+    """The composite's row kernel (ghip_scale_mask_softmax_rows_ex) with broadcast
+    masks of both kinds, fp32 scores, against numpy."""
+    B, H, Sq, Sk = 2, 3, 40, 70
+    x = synth.normal(4701, (B, H, Sq, Sk))
+    for shape in ((B, 1, 1, Sk), (B, H, Sq, Sk), (Sq, Sk)):
+        m = _mask(kind, shape, 4702, torch.float32)
+        for causal in (False, True):
+            s = x.astype(np.float64) * 0.3
+            s = np.where(m, s, -np.inf) if kind == "bool" else s + m
+            if causal:
+                s = np.where(np.tril(np.ones((Sq, Sk), bool)), s, -np.inf)
+            p = np.exp(s - s.max(-1, keepdims=True))
+            ref = p / p.sum(-1, keepdims=True)
+            tm = torch.from_numpy(np.ascontiguousarray(m)).to(cuda)
+            got = ops.scale_mask_softmax_ex(torch.from_numpy(x).to(cuda), 0.3, causal, tm).cpu().numpy()
+            assert rel_err(got, ref) <= 1e-5
 
 
 def test_sdpa_bshd_strides(cuda):
@@ -90,9 +221,12 @@ def test_sdpa_config_shape_rows(cuda):
 
 
 def test_sdpa_rejects_unsupported(cuda):
-    q = torch.zeros((1, 2, 16, 64), device=cuda, dtype=torch.bfloat16)
+    q = torch.zeros((1, 2, 16, 96), device=cuda, dtype=torch.bfloat16)
     with pytest.raises(BackendError):
-        ops.sdpa(q, q, q, 1.0, False)  # head dim 64: not fused (composite path)
+        ops.sdpa(q, q, q, 1.0, False)  # head dim 96: not fused (composite path)
+    q = torch.zeros((1, 2, 16, 128), device=cuda, dtype=torch.float32)
+    with pytest.raises(BackendError):
+        ops.sdpa(q, q, q, 1.0, False)  # fp32: composite path only
     q = torch.zeros((1, 3, 16, 128), device=cuda, dtype=torch.bfloat16)
     k = torch.zeros((1, 2, 16, 128), device=cuda, dtype=torch.bfloat16)
     with pytest.raises(BackendError):

@@ -349,6 +349,80 @@ def test_graph_sdpa_gqa_causal(be, layout):
     assert rel_err(y, ref) <= 1e-4
 
 
+@pytest.mark.parametrize("layout", [AxesLayout.BHSD, AxesLayout.BSHD])
+@pytest.mark.parametrize("dt,D,kind", [(BF16, 128, "bool"), (BF16, 64, "add"), (dtypes.Float16, 128, "add"),
+                                       (F32, 64, "add"), (F32, 96, "bool")])
+def test_graph_sdpa_masks(be, layout, dt, D, kind):
+    """FusedScaledDotProductAttention with a mask through the graph API: rank-4
+    masks in Q's layout (BSHD masks are [B, Sq, H, Sk], transposed as the reference
+    does, function.go:2709-2718), lower ranks broadcast over the trailing axes;
+    bf16 / f16 with head dim 64 or 128 take the fused kernel, fp32 or head dim 96
+    the composite (GEMM, masked softmax, GEMM)."""
+    B, H, Hkv, S, Sk = 2, 4, 2, 136, 136
+    q = synth.normal(4801, (B, H, S, D))
+    k = synth.normal(4802, (B, Hkv, Sk, D))
+    v = synth.normal(4803, (B, Hkv, Sk, D))
+    if dt == BF16:
+        q, k, v = (synth.round_bf16(a) for a in (q, k, v))
+    elif dt == dtypes.Float16:
+        q, k, v = (a.astype(np.float16).astype(np.float32) for a in (q, k, v))
+    m_bhsd = (synth.uniform(4804, B * H * S * Sk).reshape(B, H, S, Sk) > 0.3) if kind == "bool" else \
+        synth.normal(4804, (B, H, S, Sk), std=1.0)
+    if kind == "bool":
+        m_bhsd[..., 0] = True
+    elif dt == BF16:
+        m_bhsd = synth.round_bf16(m_bhsd)
+    elif dt == dtypes.Float16:
+        m_bhsd = m_bhsd.astype(np.float16).astype(np.float32)
+    ref = orc.sdpa(q, k, v, scale=D ** -0.5, causal=True,
+                   **({"mask": m_bhsd} if kind == "bool" else {"additive": m_bhsd}))
+    t = (lambda a: np.ascontiguousarray(a.transpose(0, 2, 1, 3))) if layout == AxesLayout.BSHD else (lambda a: a)
+    host = lambda a: synth.to_bf16_bits(a) if dt == BF16 else (a.astype(np.float16) if dt == dtypes.Float16 else a)  # noqa: E731
+    mt = t(m_bhsd)
+    mdt = dtypes.Bool if kind == "bool" else dt
+    mh = mt.astype(np.bool_) if kind == "bool" else host(mt)
+    b = be.Builder("sdpa_mask")
+    f = b.Main()
+    ps = [f.Parameter(f"p{i}", make_shape(dt, *t(a).shape)) for i, a in enumerate((q, k, v))]
+    pm = f.Parameter("m", make_shape(mdt, *mt.shape))
+    f.Return([f.FusedScaledDotProductAttention(*ps, pm, H, Hkv, layout, D ** -0.5, True)])
+    ex = b.Compile()
+    plan = ex.Plan()
+    assert ("fused attention" in plan) == (dt != F32 and D in (64, 128)), plan
+    bufs = [be.BufferFromFlatData(0, host(t(a)), make_shape(dt, *t(a).shape)) for a in (q, k, v)]
+    bufs.append(be.BufferFromFlatData(0, mh, make_shape(mdt, *mt.shape)))
+    (r,) = ex.Execute(bufs, None, 0)
+    y = be.BufferToFlatData(r).reshape(be.BufferShape(r).dims)
+    y = synth.bf16_bits_to_f32(y) if dt == BF16 else y.astype(np.float32)
+    if layout == AxesLayout.BSHD:
+        y = y.transpose(0, 2, 1, 3)
+    # fp32 composite: scores and probabilities in fp32; 16-bit: P and the output rounded
+    assert norm_err(y, ref) <= (1e-4 if dt == F32 else 1e-2)
+    ex.Finalize()
+    # a key-padding mask [B, 1, 1, Sk] (rank 4 in BHSD, where BSHD and BHSD agree)
+    if layout == AxesLayout.BHSD and kind == "bool":
+        kp = np.ones((B, 1, 1, Sk), bool)
+        kp[0, ..., 100:] = False
+        ref = orc.sdpa(q, k, v, scale=D ** -0.5, causal=False, mask=kp)
+        (y,) = run(be, lambda f, qq, kk, vv, mm: [f.FusedScaledDotProductAttention(qq, kk, vv, mm, H, Hkv, layout,
+                                                                                    D ** -0.5, False)],
+                   [(host(q), make_shape(dt, *q.shape)), (host(k), make_shape(dt, *k.shape)),
+                    (host(v), make_shape(dt, *v.shape)), (kp, make_shape(dtypes.Bool, B, 1, 1, Sk))])
+        assert norm_err(np.asarray(y, np.float32), ref) <= (1e-4 if dt == F32 else 1e-2)
+
+
+def test_graph_sdpa_mask_shape_errors(be):
+    b = be.Builder("sdpa_bad_mask")
+    f = b.Main()
+    q = f.Parameter("q", make_shape(BF16, 1, 2, 8, 64))
+    with pytest.raises(BackendError, match="does not broadcast"):
+        f.FusedScaledDotProductAttention(q, q, q, f.Parameter("m", make_shape(dtypes.Bool, 3, 8)), 2, 2,
+                                         AxesLayout.BHSD, 0.1, False)
+    with pytest.raises(BackendError, match="bool or additive"):
+        f.FusedScaledDotProductAttention(q, q, q, f.Parameter("m2", make_shape(F32, 8, 8)), 2, 2,
+                                         AxesLayout.BHSD, 0.1, False)
+
+
 def test_graph_elementwise_semantics(be):
     x = np.array([-2.5, -0.5, 0.5, 1.5, 2.5, np.nan, np.inf, -np.inf], np.float32)
     s = make_shape(F32, 8)

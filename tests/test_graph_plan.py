@@ -177,15 +177,21 @@ def test_transformer_block_plan(be, monkeypatch):
     e = graphs.transformer_block(be, cfg)
     p = e.Plan()
     assert p.count("rmsnorm_rows") == 2
-    # Q, K, V and the two attention products stay plain GEMMs; the residual adds
-    # and SiLU(gate) * up run as GEMM epilogues (gate and up in one kernel).
-    assert p.count("gemm_batched bfloat16") == 5
+    # Q, K, V stay plain GEMMs, attention (head dim 64) is one fused kernel; the
+    # residual adds and SiLU(gate) * up run as GEMM epilogues (gate and up in one
+    # kernel).
+    assert p.count("gemm_batched bfloat16") == 3
+    assert p.count("sdpa_fwd bfloat16") == 1 and "causal=1 mask=none (fused attention)" in p
     assert p.count("gemm_batched+epilogue") == 3 and p.count("dots=2") == 1
     assert "fused_elementwise" not in p
-    assert "scale_mask_softmax_rows" in p and "causal=1" in p
+    # head dim 96 has no fused kernel: GEMM, scale + causal softmax, GEMM
+    c96 = graphs.TransformerBlockConfig(batch=2, seq=64, vocab=100, d_model=192, heads=2, head_dim=96, ffn=256)
+    p96 = graphs.transformer_block(be, c96).Plan()
+    assert "sdpa_fwd" not in p96 and "scale_mask_softmax_rows" in p96 and "causal=1" in p96
+    assert p96.count("gemm_batched bfloat16") == 5
     monkeypatch.setenv("GHIP_EPILOGUE_FUSION", "0")
     u = graphs.transformer_block(be, cfg).Plan()
-    assert u.count("gemm_batched bfloat16") == 9 and "gemm_batched+epilogue" not in u
+    assert u.count("gemm_batched bfloat16") == 7 and "gemm_batched+epilogue" not in u
     assert u.count("fused_elementwise") == 3
     assert "gather_rows" in p
     assert e.Outputs()[0].dims == (2, 64, 128)

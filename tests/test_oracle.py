@@ -210,6 +210,52 @@ def test_sdpa_vs_numpy_gqa_causal():
     assert np.max(np.abs(got - p @ vr)) < 1e-12
 
 
+def _np_attention(q, k, v, scale, keep=None, add=None, causal=False):
+    H, Hkv = q.shape[1], k.shape[1]
+    kr = np.repeat(k.astype(np.float64), H // Hkv, axis=1)
+    vr = np.repeat(v.astype(np.float64), H // Hkv, axis=1)
+    s = q.astype(np.float64) @ kr.transpose(0, 1, 3, 2) * scale
+    if add is not None:
+        s = s + np.asarray(add, np.float64)
+    if keep is not None:
+        s = np.where(keep, s, -np.inf)
+    if causal:
+        s = np.where(np.tril(np.ones(s.shape[-2:], bool)), s, -np.inf)
+    p = np.exp(s - s.max(-1, keepdims=True))
+    return (p / p.sum(-1, keepdims=True)) @ vr
+
+
+@pytest.mark.parametrize("mshape", [(5,), (6, 5), (1, 6, 5), (2, 1, 1, 5), (2, 4, 6, 5), (1, 4, 1, 5)])
+def test_sdpa_masks_of_every_rank_vs_numpy(mshape):
+    """Boolean and additive masks of every rank broadcast to [B, H, Sq, Sk]
+    (broadcastMaskToScores, function.go:2959-2974), with and without causal, against
+    a numpy composition; and the closed forms: an all-zero additive mask is no mask,
+    an additive mask of 0 / -inf is the boolean mask, and a per-row additive constant
+    changes nothing (softmax shift invariance)."""
+    B, H, Hkv, Sq, Sk, D = 2, 4, 2, 6, 5, 3
+    q = synth.normal(81, (B, H, Sq, D))
+    k = synth.normal(82, (B, Hkv, Sk, D))
+    v = synth.normal(83, (B, Hkv, Sk, D))
+    keep = synth.uniform(84, int(np.prod(mshape))).reshape(mshape) > 0.3
+    keep[..., 0] = True                                   # every row keeps a key
+    add = synth.normal(85, mshape, std=2.0)
+    for causal in (False, True):
+        got = orc.sdpa(q, k, v, mask=keep, scale=0.4, causal=causal)
+        assert np.max(np.abs(got - _np_attention(q, k, v, 0.4, keep=keep, causal=causal))) < 1e-12
+        got = orc.sdpa(q, k, v, additive=add, scale=0.4, causal=causal)
+        assert np.max(np.abs(got - _np_attention(q, k, v, 0.4, add=add, causal=causal))) < 1e-12
+        zero = orc.sdpa(q, k, v, additive=np.zeros(mshape, np.float32), scale=0.4, causal=causal)
+        assert np.max(np.abs(zero - orc.sdpa(q, k, v, scale=0.4, causal=causal))) < 1e-12
+        as_add = np.where(keep, 0.0, -np.inf).astype(np.float32)
+        assert np.max(np.abs(orc.sdpa(q, k, v, additive=as_add, scale=0.4, causal=causal) -
+                             orc.sdpa(q, k, v, mask=keep, scale=0.4, causal=causal))) < 1e-12
+    row_const = synth.normal(86, (B, H, Sq, 1), std=3.0)
+    assert np.max(np.abs(orc.sdpa(q, k, v, additive=row_const, scale=0.4) - orc.sdpa(q, k, v, scale=0.4))) < 1e-12
+    # a row whose keys are all masked is NaN, as the reference's softmax of -inf is
+    none = np.zeros((Sq, Sk), bool)
+    assert np.all(np.isnan(orc.sdpa(q, k, v, mask=none, scale=0.4)))
+
+
 def test_argminmax_vs_numpy_and_rules():
     x = synth.normal(61, (6, 17, 5))
     for ax in range(3):
