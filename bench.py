@@ -300,7 +300,7 @@ def make_cases(only=None):
 
         def launch(i):
             (y,) = ex.Execute(bufs, None, 0)
-            be.BufferFinalize(y)  # back to the caching allocator; stream order protects reuse
+            be.BufferFinalize(y)  # back to the cache without a sync: reuse is ordered by the stream
         S, causal_attn = cfg.seq, 2 * 2 * cfg.batch * cfg.heads * cfg.seq * cfg.seq * cfg.head_dim
         case = Case("transformer_block_bf16", launch, flops_per_step=cfg.flops(), bound="mfma",
                     executed_flops_per_step=cfg.flops() - causal_attn + causal_attn * (S + 1) // (2 * S),

@@ -182,6 +182,14 @@ struct Plan {
   size_t arena_bytes = 0;
   std::vector<View> out_views;  // where each output value lives
   std::vector<int> out_slot;    // output slot for each output
+  // Donation (Execute's `donate`): the last step that reads each input (-1: none)
+  // and the first step that writes each output; an output may take a donated
+  // input's memory when that input is read only before the output's first write,
+  // or in the same step when that step is elementwise with the input read at the
+  // output's own element index (inplace_inputs of the step).
+  std::vector<int> in_last_read;
+  std::vector<int> out_first_write;
+  std::vector<std::vector<int>> inplace_inputs;  // per step: input indices it may overwrite
   std::vector<std::string> log;
   std::vector<std::vector<uint8_t>> const_data;  // per slot (Const slots only)
 };

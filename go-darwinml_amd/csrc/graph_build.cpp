@@ -341,10 +341,13 @@ extern "C" void* ghip_buffer_device_ptr(GHipBuffer* buf) { return buf && buf->va
 
 extern "C" void ghip_buffer_finalize(GHipBuffer* buf) {
   if (!buf) return;
-  if (buf->valid && buf->backend) {
-    // Work queued on the stream may still read this memory: wait before reuse.
-    hipSetDevice(buf->backend->device);
-    if (buf->backend->stream) hipStreamSynchronize(buf->backend->stream);
+  if (buf->valid && buf->backend && buf->ptr) {
+    // Stream-ordered release: every use of a backend buffer (Execute's kernels,
+    // BufferFromFlatData / BufferToFlatData copies) is enqueued on the backend's
+    // one stream, so the block can go back to the cache now: whatever allocation
+    // takes it next is used by work enqueued after everything already queued
+    // against this buffer.  (A caller that used BufferData's pointer on another
+    // stream must synchronise that stream before finalizing.)
     buf->backend->release(buf->ptr, buf->cap);
   }
   buf->valid = false;

@@ -183,22 +183,61 @@ int check_execute_args(GHipExecutable* e, GHipBuffer* const* inputs, int n, int 
 }
 }  // namespace ghip
 
+// Whether output o may take donated input i's memory: same shape, and the plan
+// reads input i only before it first writes output o, or in that same step
+// when the step is elementwise and reads input i at output o's own indices.
+static bool can_donate(const GHipExecutable* e, int i, int o) {
+  const Plan& plan = e->plan;
+  if (e->in_shapes[i] != e->out_shapes[o]) return false;
+  const int last = plan.in_last_read[i], first = plan.out_first_write[o];
+  if (last < first) return true;
+  if (last != first || first == INT32_MAX) return false;
+  const auto& ip = plan.inplace_inputs[first];
+  return std::find(ip.begin(), ip.end(), i) != ip.end();
+}
+
 extern "C" int ghip_exec_execute(GHipExecutable* e, GHipBuffer* const* inputs, int n, const uint8_t* donate,
                                  GHipBuffer** outputs, int nout, GHipError* err) {
-  (void)donate;  // inputs are never written; donation is accepted and ignored
   if (!e || e->finalized) return set_error(err, GHIP_ERR_STATE, "Execute: executable finalized");
   std::lock_guard<std::mutex> lk(e->mu);
   GHipBackend* be = e->backend;
   if (const int rc = check_execute_args(e, inputs, n, nout, err)) return rc;
   hipSetDevice(be->device);
   std::vector<GHipBuffer*> outs(nout, nullptr);
+  // Donated inputs (executable.go:50): an output of the same shape takes over the
+  // memory of a donated input the plan no longer needs when it writes that output
+  // (the input buffer is consumed: it becomes invalid, and finalizing it is a
+  // no-op).  A buffer passed as several inputs is never taken.
+  std::vector<int> donor(nout, -1);
+  if (donate) {
+    std::vector<char> used(n, 0);
+    for (int o = 0; o < nout; ++o)
+      for (int i = 0; i < n && donor[o] < 0; ++i) {
+        if (!donate[i] || used[i] || !can_donate(e, i, o)) continue;
+        bool shared = false;
+        for (int j = 0; j < n; ++j) shared = shared || (j != i && inputs[j]->ptr == inputs[i]->ptr);
+        if (shared) continue;
+        donor[o] = i;
+        used[i] = 1;
+      }
+  }
   auto cleanup = [&]() {
-    for (auto* b : outs)
-      if (b) ghip_buffer_finalize(b);
+    for (int o = 0; o < nout; ++o)
+      if (outs[o] && donor[o] < 0) ghip_buffer_finalize(outs[o]);
+      else delete outs[o];
   };
-  for (int i = 0; i < nout; ++i) {
-    outs[i] = ghip_buffer_new(be, e->out_shapes[i].dtype, e->out_shapes[i].dims.data(), e->out_shapes[i].rank(), err);
-    if (!outs[i]) {
+  for (int o = 0; o < nout; ++o) {
+    if (donor[o] >= 0) {
+      const GHipBuffer* in = inputs[donor[o]];
+      outs[o] = new GHipBuffer();
+      outs[o]->backend = be;
+      outs[o]->shape = e->out_shapes[o];
+      outs[o]->ptr = in->ptr;
+      outs[o]->cap = in->cap;
+      continue;
+    }
+    outs[o] = ghip_buffer_new(be, e->out_shapes[o].dtype, e->out_shapes[o].dims.data(), e->out_shapes[o].rank(), err);
+    if (!outs[o]) {
       cleanup();
       return err ? err->code : GHIP_ERR_OOM;
     }
@@ -211,7 +250,13 @@ extern "C" int ghip_exec_execute(GHipExecutable* e, GHipBuffer* const* inputs, i
     cleanup();
     return rc;
   }
-  for (int i = 0; i < nout; ++i) outputs[i] = outs[i];
+  for (int o = 0; o < nout; ++o) {
+    if (donor[o] >= 0) {  // the input's memory now belongs to the output
+      inputs[donor[o]]->valid = false;
+      inputs[donor[o]]->ptr = nullptr;
+    }
+    outputs[o] = outs[o];
+  }
   return GHIP_OK;
 }
 

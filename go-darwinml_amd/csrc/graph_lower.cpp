@@ -145,7 +145,8 @@ struct Lowerer {
   std::vector<Fusion> fusion;
   std::vector<char> have;
   std::vector<View> views;
-  std::vector<std::vector<int>> reads, writes;  // per step: slots
+  std::vector<std::vector<int>> reads, writes;
+  std::vector<std::vector<int>> inplace_slots;  // per step: read slots its output may alias
   std::vector<std::vector<uint8_t>> const_data;  // per slot (Const slots)
   bool failed = false;
 
@@ -179,10 +180,12 @@ struct Lowerer {
   }
   View fresh(const Shape& s) { return contig(new_slot(SlotKind::Arena, s.bytes()), s); }
 
-  void add_step(const std::string& desc, std::vector<int> r, std::vector<int> w, StepFn f) {
+  void add_step(const std::string& desc, std::vector<int> r, std::vector<int> w, StepFn f,
+                std::vector<int> inplace = {}) {
     plan->steps.push_back(Step{desc, std::move(f)});
     reads.push_back(std::move(r));
     writes.push_back(std::move(w));
+    inplace_slots.push_back(std::move(inplace));
   }
 
   // ------------------------------------------------------------------ analysis
@@ -1918,6 +1921,16 @@ View Lowerer::emit_cluster(int root, int v) {
     in_views.push_back(in.view);
     in_dt.push_back(N[in.value].shape.dtype);
   }
+  // Slots every read of which is at the output's own element index (linear,
+  // offset 0, same element size): the output may overwrite them in place.
+  std::vector<int> inplace;
+  for (auto& in : ins) {
+    bool ok = true;
+    for (auto& o2 : ins)
+      if (o2.view.slot == in.view.slot)
+        ok = ok && o2.linear && o2.view.offset == 0 && dtype_size(N[o2.value].shape.dtype) == dtype_size(os.dtype);
+    if (ok && std::find(inplace.begin(), inplace.end(), in.view.slot) == inplace.end()) inplace.push_back(in.view.slot);
+  }
   std::ostringstream d;
   d << "fused_elementwise " << os.str() << " ops=" << mem.size() << " inputs=" << ins.size() << " [";
   for (size_t i = 0; i < mem.size(); ++i) {
@@ -1942,7 +1955,7 @@ View Lowerer::emit_cluster(int root, int v) {
     hipError_t h = hipModuleLaunchKernel(kern.func, static_cast<unsigned>(g), 1, 1, 256, 1, 1, 0, st.stream, args.data(), nullptr);
     if (h != hipSuccess) return check_hip(h, e, "generated elementwise kernel launch");
     return GHIP_OK;
-  });
+  }, inplace);
   return y;
 }
 
@@ -2255,6 +2268,22 @@ int Lowerer::finish() {
     arena = std::max(arena, off + sz);
   }
   plan->arena_bytes = arena;
+  // Donation: last read of each input, first write of each output, and per step
+  // the inputs an elementwise step reads at its output's own element index.
+  const int nin = static_cast<int>(fn->params.size() + fn->captures.size());
+  plan->in_last_read.assign(nin, -1);
+  plan->out_first_write.assign(nout, INT32_MAX);
+  plan->inplace_inputs.assign(plan->steps.size(), {});
+  for (size_t st = 0; st < plan->steps.size(); ++st) {
+    for (int s : reads[st])
+      if (plan->slots[s].kind == SlotKind::Input)
+        plan->in_last_read[plan->slots[s].index] = std::max(plan->in_last_read[plan->slots[s].index], static_cast<int>(st));
+    for (int s : writes[st])
+      if (plan->slots[s].kind == SlotKind::Output)
+        plan->out_first_write[plan->slots[s].index] = std::min(plan->out_first_write[plan->slots[s].index], static_cast<int>(st));
+    for (int s : inplace_slots[st])
+      if (plan->slots[s].kind == SlotKind::Input) plan->inplace_inputs[st].push_back(plan->slots[s].index);
+  }
   for (auto& st : plan->steps) plan->log.push_back(st.desc);
   return GHIP_OK;
 }
