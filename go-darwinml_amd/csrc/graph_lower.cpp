@@ -39,8 +39,8 @@ namespace ghip {
 namespace {
 
 struct Fusion {
-  enum Kind { None, RmsNorm, Softmax, LogSoftmax } kind = None;
-  int x = -1, gamma = -1;
+  enum Kind { None, RmsNorm, Softmax, LogSoftmax, LayerNorm } kind = None;
+  int x = -1, gamma = -1, beta = -1;
   double eps = 0;
 };
 
@@ -210,6 +210,7 @@ struct Lowerer {
     for (int v = n - 1; v >= 0; --v)
       if (live[v]) match_patterns(v);
     build_clusters();
+    find_reduce_fusions();
   }
 
   // ------------------------------------------------------------------ patterns
@@ -307,6 +308,52 @@ struct Lowerer {
     return dt == GHIP_DTYPE_FLOAT32 || dt == GHIP_DTYPE_BFLOAT16 || dt == GHIP_DTYPE_FLOAT16;
   }
 
+  // v = ReduceSum(t, last axis) / n, as Div by the constant n or Mul by 1/n
+  // (through reshapes); returns t.
+  int mean_last(int v, double n) {
+    v = strip_reshape(v);
+    int s = -1;
+    if (is_binary(v, GHIP_BINARY_MUL)) {
+      for (int q = 0; q < 2; ++q) {
+        double c;
+        if (scalar_const(N[v].in[q], &c) && fabs(c * n - 1.0) < 1e-5) s = strip_reshape(N[v].in[1 - q]);
+      }
+    } else if (is_binary(v, GHIP_BINARY_DIV)) {
+      double c;
+      if (scalar_const(N[v].in[1], &c) && fabs(c - n) < 1e-6 * n) s = strip_reshape(N[v].in[0]);
+    }
+    if (s < 0 || N[s].kind != Kind::Reduce || N[s].sub != GHIP_REDUCE_SUM) return -1;
+    const int t = N[s].in[0];
+    return is_last_axis_reduce(s, GHIP_REDUCE_SUM, t) ? t : -1;
+  }
+  // LayerNorm core as the reference composes it (function.go:2429-2497):
+  // v = d * bcast(rsqrt(mean(d * d) + eps)) with d = x - bcast(mean(x)).
+  bool ln_core(int v, int* xo, double* eps) {
+    if (!is_binary(v, GHIP_BINARY_MUL)) return false;
+    for (int o = 0; o < 2; ++o) {
+      const int d = N[v].in[o], rb = N[v].in[1 - o];
+      if (!is_binary(d, GHIP_BINARY_SUB) || N[d].shape.dims != N[v].shape.dims) continue;
+      const int x = N[d].in[0];
+      if (N[x].shape.dims != N[v].shape.dims || !row_dtype(N[x].shape.dtype)) continue;
+      const double n = static_cast<double>(N[x].shape.dims.back());
+      int mb, u;
+      if (!row_broadcast(N[d].in[1], N[x].shape, &mb) || mean_last(mb, n) != x) continue;
+      if (!row_broadcast(rb, N[x].shape, &u) || !is_unary(u, GHIP_UNARY_RSQRT)) continue;
+      const int add = strip_reshape(N[u].in[0]);
+      if (!is_binary(add, GHIP_BINARY_ADD)) continue;
+      for (int p = 0; p < 2; ++p) {
+        double e;
+        if (!scalar_const(N[add].in[p], &e)) continue;
+        const int sq = mean_last(N[add].in[1 - p], n);
+        if (!is_binary(sq, GHIP_BINARY_MUL) || N[sq].in[0] != d || N[sq].in[1] != d) continue;
+        *xo = x;
+        *eps = e;
+        return true;
+      }
+    }
+    return false;
+  }
+
   // RMSNorm core: v = x * bcast(rsqrt(mean(x*x) + eps)).
   bool rms_core(int v, int* xo, double* eps) {
     if (!is_binary(v, GHIP_BINARY_MUL)) return false;
@@ -350,18 +397,45 @@ struct Lowerer {
   void match_patterns(int v) {
     const Node& n = N[v];
     if (n.kind != Kind::Binary) return;
+    // LayerNorm: core [* bcast(gamma)] [+ bcast(beta)] (function.go:2429-2562).
+    // Checked first: its core is an RMSNorm of x - mean.
+    if ((n.sub == GHIP_BINARY_ADD || n.sub == GHIP_BINARY_MUL) && row_dtype(n.shape.dtype) && n.shape.rank() >= 1) {
+      int x, g = -1, b = -1, core = -1;
+      double eps;
+      if (n.sub == GHIP_BINARY_ADD) {
+        for (int o = 0; o < 2 && core < 0; ++o) {
+          int bb;
+          if (!col_broadcast(n.in[1 - o], n.shape, &bb)) continue;
+          const int m = n.in[o];
+          int gg;
+          for (int q = 0; q < 2 && is_binary(m, GHIP_BINARY_MUL) && core < 0; ++q)
+            if (col_broadcast(N[m].in[1 - q], n.shape, &gg) && ln_core(N[m].in[q], &x, &eps)) core = N[m].in[q], g = gg, b = bb;
+          if (core < 0 && ln_core(m, &x, &eps)) core = m, b = bb;
+        }
+      } else {
+        for (int o = 0; o < 2 && core < 0; ++o) {
+          int gg;
+          if (col_broadcast(N[v].in[1 - o], n.shape, &gg) && ln_core(N[v].in[o], &x, &eps)) core = N[v].in[o], g = gg;
+        }
+        if (core < 0 && ln_core(v, &x, &eps)) core = v;
+      }
+      if (core >= 0) {
+        fusion[v] = Fusion{Fusion::LayerNorm, x, g, b, eps};
+        return;
+      }
+    }
     // RMSNorm, with or without gamma.
     if (n.sub == GHIP_BINARY_MUL && row_dtype(n.shape.dtype) && n.shape.rank() >= 1) {
       int x, g;
       double eps;
       for (int o = 0; o < 2; ++o) {
         if (col_broadcast(n.in[1 - o], n.shape, &g) && rms_core(n.in[o], &x, &eps)) {
-          fusion[v] = Fusion{Fusion::RmsNorm, x, g, eps};
+          fusion[v] = Fusion{Fusion::RmsNorm, x, g, -1, eps};
           return;
         }
       }
       if (rms_core(v, &x, &eps)) {
-        fusion[v] = Fusion{Fusion::RmsNorm, x, -1, eps};
+        fusion[v] = Fusion{Fusion::RmsNorm, x, -1, -1, eps};
         return;
       }
     }
@@ -429,6 +503,33 @@ struct Lowerer {
           if (!all_in) continue;
           cluster[o] = v;
           work.push_back(o);
+        }
+      }
+    }
+  }
+
+  // Reduce fusion candidates (after the clusters are known).
+  void find_reduce_fusions() {
+    const int n = static_cast<int>(N.size());
+    reduce_prod.assign(n, -1);
+    cons_reduce.assign(n, -1);
+    if (!fuse_reductions) return;
+    std::set<int> outs(fn->outputs.begin(), fn->outputs.end());
+    for (int v = 0; v < n; ++v) {
+      if (!live[v] || N[v].kind != Kind::Reduce || fusion[v].kind != Fusion::None) continue;
+      if (N[v].shape.dtype == GHIP_DTYPE_BOOL) continue;  // no boolean Reduce kernel to mirror
+      const int p = N[v].in[0];
+      if (p >= 0 && cluster[p] == p && users[p].size() == 1 && !outs.count(p)) reduce_prod[v] = p;
+      if (users[v].size() == 1 && !outs.count(v)) {
+        const int u = users[v][0];
+        const int c = u >= 0 ? cluster[u] : -1;
+        if (c >= 0 && cons_reduce[c] < 0 && N[c].shape.dims == N[v].shape.dims) {
+          // a cluster fed by a DotGeneral prefers the GEMM epilogue
+          bool has_dot = false;
+          for (int w = 0; w <= c; ++w)
+            if (cluster[w] == c)
+              for (int o : N[w].in) has_dot = has_dot || (o >= 0 && N[o].kind == Kind::Dot);
+          if (!has_dot) cons_reduce[c] = v;
         }
       }
     }
@@ -655,6 +756,8 @@ struct Lowerer {
       }
       case Fusion::Softmax: return emit_rows(0, xs, xv, Vec{}, Vec{}, 0, "(fused primitive softmax chain)");
       case Fusion::LogSoftmax: return emit_rows(1, xs, xv, Vec{}, Vec{}, 0, "(fused primitive log-softmax chain)");
+      case Fusion::LayerNorm:
+        return emit_rows(3, xs, xv, vec_of(f.gamma), vec_of(f.beta), f.eps, "(fused primitive LayerNorm chain)");
       default: return fail(GHIP_ERR_STATE, "unknown fusion");
     }
   }
@@ -749,6 +852,7 @@ struct Lowerer {
   }
 
   View emit_reduce(int v) {
+    if (reduce_prod[v] >= 0) return emit_reduce_fused(v, reduce_prod[v], -1);
     const Node& n = N[v];
     const Shape& xs = N[n.in[0]].shape;
     View x = get(n.in[0]);
@@ -1413,6 +1517,11 @@ struct Lowerer {
   // members' code is the same generated code the stand-alone cluster kernel
   // runs, so fused and unfused plans give bit-identical results.
   bool fuse_epilogues = true;
+  bool fuse_reductions = true;
+  // Reduce fusion: the elementwise cluster (root) a Reduce absorbs as its
+  // producer, and the consumer cluster (root) a Reduce's value feeds; -1: none.
+  std::vector<int> reduce_prod, cons_reduce;
+  View emit_reduce_fused(int R, int prod_root, int cons_root);
   View emit_gemm_epilogue(int v, const std::vector<int>& mem, bool* fused);
   std::string member_stmt(int u, std::map<int, std::string>& expr, const std::string& name);
 
@@ -1810,10 +1919,208 @@ std::string Lowerer::member_stmt(int u, std::map<int, std::string>& expr, const 
   return "    const " + ctype(n.shape.dtype) + " " + name + " = " + round_expr(n.shape.dtype, op_expr(n, a, sem)) + ";\n";
 }
 
+
+// One generated kernel for Reduce R, evaluating its producer cluster (rooted at
+// prod_root, over R's input shape) on the fly instead of reading it from HBM,
+// and, when cons_root >= 0, the consumer cluster (over R's output shape) on the
+// reduced value before the one store.  The accumulation order is the generic
+// reduce kernels' (one wave per output, lanes striding the reduced index, then a
+// butterfly, when >= 64 values are reduced; else one thread per output in
+// order), and the reduced value is rounded to R's dtype before the consumers
+// see it, so results are bit-identical to the unfused plan.
+View Lowerer::emit_reduce_fused(int R, int prod_root, int cons_root) {
+  const Node& rn = N[R];
+  const int x = rn.in[0];
+  const Shape& xs = N[x].shape;
+  const Shape& rs = rn.shape;
+  const int rx = xs.rank();
+  std::vector<int> kept, red;
+  for (int i = 0; i < rx; ++i)
+    (std::find(rn.a0.begin(), rn.a0.end(), i) != rn.a0.end() ? red : kept).push_back(i);
+  int64_t osize = 1, rsize = 1;
+  for (int i : kept) osize *= xs.dims[i];
+  for (int i : red) rsize *= xs.dims[i];
+  const int rdt = rs.dtype, xdt = xs.dtype;
+  const bool wave = rsize >= 64;
+  // Accumulator type of the generic reduce kernels (RAcc).
+  std::string acc_t = "float";
+  if (rdt == GHIP_DTYPE_FLOAT64) acc_t = "double";
+  else if (dtype_is_int(rdt)) acc_t = dtype_is_unsigned(rdt) ? "unsigned long long" : "long long";
+  struct In {
+    View view;
+    int dt;
+    std::string off;  // element offset expression
+  };
+  std::vector<In> ins;
+  std::ostringstream pbody, cbody;
+  std::map<int, std::string> expr;
+  // Input coordinates: x_i for input axis i (kept axes from the output index,
+  // reduced axes from the reduced index); output coordinates o_k.
+  auto load_input = [&](int o, const std::vector<std::string>& coord, const Shape& cs, std::ostringstream& body) {
+    View w = get(o);
+    if (failed) return;
+    const Shape& sh = N[o].shape;
+    const int off = cs.rank() - sh.rank();
+    std::string e = "0";
+    for (int d = 0; d < sh.rank(); ++d)
+      if (sh.dims[d] != 1 && w.strides[d] != 0) e += " + " + coord[off + d] + " * " + std::to_string(w.strides[d]) + "LL";
+    const int k = static_cast<int>(ins.size());
+    body << "      const " << ctype(sh.dtype) << " in" << k << " = "
+         << load_expr(sh.dtype, "((const " + stype(sh.dtype) + "*)p_in" + std::to_string(k) + ")[" + e + "]") << ";\n";
+    expr[o] = "in" + std::to_string(k);
+    ins.push_back(In{w, sh.dtype, e});
+  };
+  auto cluster_code = [&](int root, const Shape& cs, const std::vector<std::string>& coord, std::ostringstream& body,
+                          const std::set<int>& preset) {
+    std::vector<int> mem;
+    for (int u = 0; u <= root; ++u)
+      if (cluster[u] == root) mem.push_back(u);
+    std::set<int> inset(mem.begin(), mem.end());
+    for (int u : mem) {
+      for (int o : N[u].in) {
+        if (o < 0 || inset.count(o) || expr.count(o) || preset.count(o)) continue;
+        double c;
+        if (scalar_const(o, &c) && (dtype_is_float(N[o].shape.dtype) || fabs(c) < 9007199254740992.0)) {
+          expr[o] = literal(N[o].shape.dtype, c);
+          continue;
+        }
+        if (N[o].kind == Kind::Iota && N[o].shape.dims == cs.dims) {
+          expr[o] = "((" + ctype(N[o].shape.dtype) + ")" + coord[N[o].i0] + ")";
+          continue;
+        }
+        load_input(o, coord, cs, body);
+        if (failed) return;
+      }
+      if (N[u].kind == Kind::Iota) {
+        const std::string name = "v" + std::to_string(u);
+        body << "      const " << ctype(N[u].shape.dtype) << " " << name << " = "
+             << round_expr(N[u].shape.dtype, "((" + ctype(N[u].shape.dtype) + ")" + coord[N[u].i0] + ")") << ";\n";
+        expr[u] = name;
+      } else {
+        body << "  " << member_stmt(u, expr, "v" + std::to_string(u));
+      }
+    }
+  };
+  std::vector<std::string> xc(rx), oc(rs.rank());
+  for (size_t k = 0; k < kept.size(); ++k) xc[kept[k]] = "o" + std::to_string(k);
+  for (size_t k = 0; k < red.size(); ++k) xc[red[k]] = "r" + std::to_string(k);
+  for (int k = 0; k < rs.rank(); ++k) oc[k] = "o" + std::to_string(k);
+  // element value fed to the accumulator
+  std::string val;
+  if (prod_root >= 0) {
+    cluster_code(prod_root, xs, xc, pbody, {});
+    if (failed) return bad();
+    val = round_expr(xdt, expr[prod_root]);
+  } else {
+    load_input(x, xc, xs, pbody);
+    if (failed) return bad();
+    val = expr[x];
+  }
+  // consumer cluster over the output shape, with R's value preset
+  std::string outv = "red", odt_s;
+  int out_v = R, odt = rdt;
+  if (cons_root >= 0) {
+    expr.clear();  // the producer's names are scoped to the reduction loop
+    expr[R] = "red";
+    cluster_code(cons_root, rs, oc, cbody, {R});
+    if (failed) return bad();
+    out_v = cons_root;
+    odt = N[cons_root].shape.dtype;
+    outv = expr[cons_root];
+  }
+  const std::vector<std::string> ops = {"a + b", "a * b", "((a > b || a != a) ? a : b)", "((a < b || a != a) ? a : b)"};
+  std::string init;
+  switch (rn.sub) {
+    case GHIP_REDUCE_SUM: init = "(" + acc_t + ")0"; break;
+    case GHIP_REDUCE_PRODUCT: init = "(" + acc_t + ")1"; break;
+    case GHIP_REDUCE_MAX:
+      init = acc_t == "float" ? "(-__builtin_inff())" : acc_t == "double" ? "(-__builtin_inf())"
+           : acc_t == "long long" ? "(-9223372036854775807LL-1)" : "0ull";
+      break;
+    default:
+      init = acc_t == "float" ? "__builtin_inff()" : acc_t == "double" ? "__builtin_inf()"
+           : acc_t == "long long" ? "9223372036854775807LL" : "18446744073709551615ull";
+  }
+  std::ostringstream src;
+  src << kRtcPrelude << "__device__ __forceinline__ " << acc_t << " comb(" << acc_t << " a, " << acc_t << " b) { return "
+      << ops[rn.sub] << "; }\n";
+  src << "extern \"C\" __global__ void __launch_bounds__(256) fused_reduce(\n";
+  for (size_t k = 0; k < ins.size(); ++k) src << "    const void* __restrict__ p_in" << k << ",\n";
+  src << "    void* __restrict__ p_out) {\n";
+  if (wave)
+    src << "  const long long o = (long long)blockIdx.x * 4 + threadIdx.x / 64;\n  const int lane = threadIdx.x % 64;\n";
+  else
+    src << "  const long long o = (long long)blockIdx.x * 256 + threadIdx.x;\n";
+  src << "  if (o >= " << osize << "LL) return;\n";
+  // output coordinates
+  if (kept.size() == 1) {
+    src << "  const long long o0 = o;\n";
+  } else if (!kept.empty()) {
+    src << "  long long q = o;\n";
+    for (int k = static_cast<int>(kept.size()) - 1; k >= 0; --k)
+      src << "  const long long o" << k << " = q % " << xs.dims[kept[k]] << "LL; q /= " << xs.dims[kept[k]] << "LL;\n";
+  }
+  src << "  " << acc_t << " acc = " << init << ";\n";
+  src << (wave ? "  for (long long r = lane; r < " : "  for (long long r = 0; r < ") << rsize << "LL; r += " << (wave ? 64 : 1)
+      << ") {\n";
+  if (red.size() == 1) {
+    src << "      const long long r0 = r;\n";
+  } else {
+    src << "      long long t = r;\n";
+    for (int k = static_cast<int>(red.size()) - 1; k >= 0; --k)
+      src << "      const long long r" << k << " = t % " << xs.dims[red[k]] << "LL; t /= " << xs.dims[red[k]] << "LL;\n";
+  }
+  src << pbody.str() << "      acc = comb(acc, (" << acc_t << ")(" << val << "));\n  }\n";
+  if (wave) {
+    src << "#pragma unroll\n  for (int off = 32; off >= 1; off >>= 1) acc = comb(acc, __shfl_xor(acc, off, 64));\n"
+        << "  if (lane != 0) return;\n";
+  }
+  // the reduced value as the unfused plan stores it, read back in compute type
+  src << "  const " << ctype(rdt) << " red = " << load_expr(rdt, "(" + stype(rdt) + ")(" + store_expr(rdt, "(" + ctype(rdt) + ")acc") + ")") << ";\n";
+  src << cbody.str();
+  src << "  ((" << stype(odt) << "*)p_out)[o] = " << store_expr(odt, outv) << ";\n}\n";
+  RtcKernel kern;
+  if (rtc_get(be, src.str(), "fused_reduce", &kern, err) != GHIP_OK) return bad();
+  const Shape& os = N[out_v].shape;
+  View y = fresh(os);
+  std::vector<int> rd;
+  std::vector<View> in_views;
+  std::vector<int> in_dt;
+  for (auto& in : ins) {
+    rd.push_back(in.view.slot);
+    in_views.push_back(in.view);
+    in_dt.push_back(in.dt);
+  }
+  static const char* names[] = {"sum", "product", "max", "min"};
+  std::string desc = fmt("fused_reduce_%s %s -> %s", names[rn.sub], xs.str().c_str(), os.str().c_str());
+  if (prod_root >= 0) desc += " (producer fused)";
+  if (cons_root >= 0) desc += " (consumer fused)";
+  const int64_t blocks = wave ? (osize + 3) / 4 : (osize + 255) / 256;
+  add_step(desc, rd, {y.slot}, [=](ExecState& st, GHipError* e) -> int {
+    if (osize == 0) return GHIP_OK;
+    std::vector<void*> ptrs(in_views.size());
+    std::vector<void*> args;
+    for (size_t k = 0; k < in_views.size(); ++k) ptrs[k] = st.ptr(in_views[k], in_dt[k]);
+    void* outp = st.ptr(y, odt);
+    for (size_t k = 0; k < ptrs.size(); ++k) args.push_back(&ptrs[k]);
+    args.push_back(&outp);
+    hipError_t h = hipModuleLaunchKernel(kern.func, static_cast<unsigned>(blocks), 1, 1, 256, 1, 1, 0, st.stream,
+                                         args.data(), nullptr);
+    if (h != hipSuccess) return check_hip(h, e, "generated reduce kernel launch");
+    return GHIP_OK;
+  });
+  if (cons_root >= 0) {
+    views[R] = View{};  // R itself is never materialised
+  }
+  return y;
+}
+
 View Lowerer::emit_cluster(int root, int v) {
   // Members: root's cluster (or, for a value requested outside its cluster, the
   // value alone plus any Iota leaves) in node order.
   std::vector<int> mem;
+  if (root >= 0 && cons_reduce[root] >= 0 && !have[cons_reduce[root]])
+    return emit_reduce_fused(cons_reduce[root], reduce_prod[cons_reduce[root]], root);
   if (root >= 0) {
     for (int u = 0; u <= root; ++u)
       if (cluster[u] == root) mem.push_back(u);
@@ -2296,6 +2603,8 @@ int lower(GHipBackend* be, GHipFunction* fn, Plan* plan, GHipError* err) {
   // unfused plan the fused one is checked against).
   const char* ef = getenv("GHIP_EPILOGUE_FUSION");
   L.fuse_epilogues = !(ef && ef[0] == '0');
+  const char* rf = getenv("GHIP_REDUCE_FUSION");
+  L.fuse_reductions = !(rf && rf[0] == '0');
   L.have.assign(fn->nodes.size(), 0);
   L.views.assign(fn->nodes.size(), View{});
   L.analyse();

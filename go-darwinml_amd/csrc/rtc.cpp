@@ -31,10 +31,13 @@ struct Entry {
 std::mutex g_mu;
 std::map<std::string, Entry> g_cache;
 
-// Options: gfx950, -O3, and packed-fp32 VALU ops disabled (they are not used
-// anywhere in this library).
-const char* kOpts[] = {"--offload-arch=gfx950", "-O3", "-std=c++17", "-Xclang", "-target-feature",
-                       "-Xclang", "-packed-fp32-ops"};
+// Options: gfx950, -O3, packed-fp32 VALU ops disabled (they are not used
+// anywhere in this library), and no floating-point contraction: every generated
+// statement is one graph op rounded on its own, so a multiply is never fused into
+// a following add (a producer's product into a reduction's running sum, say),
+// and a fused kernel computes exactly what the unfused ops would store.
+const char* kOpts[] = {"--offload-arch=gfx950", "-O3", "-std=c++17", "-ffp-contract=off", "-Xclang",
+                       "-target-feature", "-Xclang", "-packed-fp32-ops"};
 }  // namespace
 
 int rtc_get(GHipBackend* be, const std::string& src, const std::string& entry, RtcKernel* out,

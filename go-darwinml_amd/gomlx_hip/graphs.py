@@ -30,6 +30,28 @@ def rms_norm(f, x, gamma, eps: float):
     return y
 
 
+def layer_norm_chain(f, x, gamma, beta, eps: float):
+    """LayerNorm over the last axis as primitives, in the reference's op order
+    (function.go:2429-2562): mean = sum / n, d = x - mean, var = sum(d * d) / n,
+    y = d * rsqrt(var + eps) [* gamma] [+ beta]."""
+    s = f.OpShape(x)
+    dt, dims = s.dtype, s.dims
+    r = len(dims)
+    rows = make_shape(dt, *dims[:-1])
+    keep = list(range(r - 1))
+    count = f.BroadcastInDim(f.Constant(np.array(dims[-1], np.float32), dtype=dt), rows, [])
+    mean = f.Div(f.ReduceSum(x, r - 1), count)
+    d = f.Sub(x, f.BroadcastInDim(mean, s, keep))
+    var = f.Div(f.ReduceSum(f.Mul(d, d), r - 1), count)
+    e = f.BroadcastInDim(f.Constant(np.array(eps, np.float32), dtype=dt), rows, [])
+    y = f.Mul(d, f.BroadcastInDim(f.Rsqrt(f.Add(var, e)), s, keep))
+    if gamma is not None:
+        y = f.Mul(y, f.BroadcastInDim(gamma, s, [r - 1]))
+    if beta is not None:
+        y = f.Add(y, f.BroadcastInDim(beta, s, [r - 1]))
+    return y
+
+
 def softmax_chain(f, x):
     """Softmax over the last axis as the primitive chain (max, sub, exp, sum, div)."""
     s = f.OpShape(x)

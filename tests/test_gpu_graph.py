@@ -293,6 +293,83 @@ def test_graph_log_softmax_chain(be, dt):
     assert rel_err(y, ref) <= (1e-5 if dt == F32 else 2.0 ** -8 + 1e-5)
 
 
+def _reduce_chain_graph(f, x, z, dt):
+    """Elementwise -> Reduce -> elementwise chains that no row pattern matches: the
+    generated fused reduce kernel (wave form, thread form over two axes, strided
+    producer, full reduction with a scalar consumer)."""
+    n = f.BroadcastInDim(f.Constant(np.array(1000, np.float32), dtype=dt), make_shape(dt, 96), [])
+    rms = f.Sqrt(f.Div(f.ReduceSum(f.Mul(x, x), 1), n))
+    two = f.BroadcastInDim(f.Constant(np.array(2, np.float32), dtype=dt), make_shape(dt, 40), [])
+    amax = f.Mul(f.ReduceMax(f.Abs(z), 0, 2), two)
+    t = f.ReduceSum(f.Exp(f.Transpose(x, 1, 0)), 0)
+    tot = f.Mul(f.ReduceSum(f.Mul(z, z)), f.Constant(np.array(0.5, np.float32), dtype=dt))
+    return [rms, amax, t, tot]
+
+
+@pytest.mark.parametrize("dt", [F32, BF16, dtypes.Float16])
+def test_reduce_fusion_matches_unfused_and_oracle(be, dt, monkeypatch):
+    """The fused reduce kernels give the unfused plan's results bit for bit (same
+    accumulation order, the reduced value rounded to its dtype before the
+    consumer), and match a float64 restatement within the dtype's rounding."""
+    x = synth.normal(2101, (96, 1000), std=0.5)
+    z = synth.normal(2102, (6, 40, 5), std=2.0)
+    if dt == BF16:
+        x, z = synth.round_bf16(x), synth.round_bf16(z)
+        feed = synth.to_bf16_bits
+    elif dt == dtypes.Float16:
+        x, z = x.astype(np.float16).astype(np.float32), z.astype(np.float16).astype(np.float32)
+        feed = lambda a: a.astype(np.float16)  # noqa: E731
+    else:
+        feed = lambda a: a  # noqa: E731
+    ins = [(feed(x), make_shape(dt, 96, 1000)), (feed(z), make_shape(dt, 6, 40, 5))]
+    build = lambda f, a, b: _reduce_chain_graph(f, a, b, dt)  # noqa: E731
+    fused = run(be, build, ins)
+    monkeypatch.setenv("GHIP_REDUCE_FUSION", "0")
+    plain = run(be, build, ins)
+    for a, b in zip(fused, plain):
+        assert np.array_equal(np.asarray(a, np.float32), np.asarray(b, np.float32), equal_nan=True)
+    x64, z64 = x.astype(np.float64), z.astype(np.float64)
+    refs = [np.sqrt(np.sum(x64 * x64, 1) / 1000), 2 * np.max(np.abs(z64), (0, 2)), np.sum(np.exp(x64), 1),
+            0.5 * np.sum(z64 * z64)]
+    tol = {F32: 1e-5, BF16: 2.0 ** -6, dtypes.Float16: 2.0 ** -8}[dt]
+    for got, ref in zip(fused, refs):
+        assert rel_err(np.asarray(got, np.float32), ref) <= tol
+
+
+def test_reduce_fusion_integers(be, monkeypatch):
+    """Integer chains accumulate in 64 bits and wrap to the output type, as the
+    unfused reduce does."""
+    x = (synth.uniform_f32(2103, (64, 50), -300, 300)).astype(np.int32)
+    build = lambda f, a: [f.ReduceSum(f.Mul(a, a), 1), f.ReduceMin(f.Neg(a)),  # noqa: E731
+                          f.ReduceMax(f.Mul(a, a), 0)]
+    got = run(be, build, [(x, make_shape(I32, 64, 50))])
+    monkeypatch.setenv("GHIP_REDUCE_FUSION", "0")
+    plain = run(be, build, [(x, make_shape(I32, 64, 50))])
+    x64 = x.astype(np.int64)
+    want = [np.sum(x64 * x64, 1).astype(np.int32), np.min(-x64).astype(np.int32), np.max(x64 * x64, 0).astype(np.int32)]
+    for g, p_, w in zip(got, plain, want):
+        assert np.array_equal(g, w) and np.array_equal(p_, w)
+
+
+@pytest.mark.parametrize("dt", [F32, BF16])
+def test_graph_layer_norm_chain(be, dt):
+    """The reference's LayerNorm composition sent as primitives (one fused row
+    kernel) against the oracle: fp32 within 1e-5, bf16 within one rounding."""
+    x = synth.normal(2201, (512, 2048), std=1.5, mean=0.25)
+    g = synth.uniform_f32(2202, (2048,), 0.5, 1.5)
+    bt = synth.normal(2203, (2048,), std=0.1)
+    if dt == BF16:
+        x, g, bt = synth.round_bf16(x), synth.round_bf16(g), synth.round_bf16(bt)
+        feed = synth.to_bf16_bits
+    else:
+        feed = lambda a: a  # noqa: E731
+    ys = run(be, lambda f, a, gg, bb: [graphs.layer_norm_chain(f, a, gg, bb, 1e-5), graphs.layer_norm_chain(f, a, None, None, 1e-5)],
+             [(feed(x), make_shape(dt, 512, 2048)), (feed(g), make_shape(dt, 2048)), (feed(bt), make_shape(dt, 2048))])
+    tol = 1e-5 if dt == F32 else 2.0 ** -8 + 1e-5
+    assert rel_err(ys[0], orc.layernorm(x, g, bt, 1e-5)) <= tol
+    assert rel_err(ys[1], orc.layernorm(x, None, None, 1e-5)) <= tol
+
+
 def test_graph_float16_hot_ops(be):
     """Float16 (a dtype the reference declares, capabilities.go:153-166) through the
     graph API: FusedSoftmax, FusedLayerNorm, the RMSNorm chain and DotGeneral, each

@@ -104,6 +104,64 @@ def test_rmsnorm_chain_is_fused(be):
     assert "reduce" not in p and "fused_elementwise" not in p
 
 
+@pytest.mark.parametrize("gb", ["both", "gamma", "beta", "none"])
+def test_layernorm_chain_is_fused(be, gb):
+    """The reference's LayerNorm composition (function.go:2429-2562) sent as
+    primitives becomes one layernorm_rows launch, with or without gamma / beta."""
+    def build(f):
+        x = f.Parameter("x", make_shape(BF16, 64, 512))
+        g = f.Parameter("g", make_shape(BF16, 512)) if gb in ("both", "gamma") else None
+        b = f.Parameter("b", make_shape(BF16, 512)) if gb in ("both", "beta") else None
+        return [graphs.layer_norm_chain(f, x, g, b, 1e-5)]
+    p = plan_of(be, build)
+    assert p.count("layernorm_rows bfloat16 rows=64 n=512") == 1, p
+    assert ("+gamma" in p) == (gb in ("both", "gamma")) and ("+beta" in p) == (gb in ("both", "beta"))
+    assert "(fused primitive LayerNorm chain)" in p
+    assert "reduce" not in p and "fused_elementwise" not in p
+
+
+def _reduce_chains(f, dt=F32):
+    """Elementwise -> Reduce -> elementwise chains none of the row patterns match."""
+    x = f.Parameter("x", make_shape(dt, 96, 1000))
+    n = f.BroadcastInDim(f.Constant(np.array(1000, np.float32), dtype=dt), make_shape(dt, 96), [])
+    rms = f.Sqrt(f.Div(f.ReduceSum(f.Mul(x, x), 1), n))                 # producer + consumer, wave form
+    z = f.Parameter("z", make_shape(dt, 6, 40, 5))
+    two = f.BroadcastInDim(f.Constant(np.array(2, np.float32), dtype=dt), make_shape(dt, 40), [])
+    amax = f.Mul(f.ReduceMax(f.Abs(z), 0, 2), two)                      # thread form, two reduced axes
+    t = f.ReduceSum(f.Exp(f.Transpose(x, 1, 0)), 0)                       # strided producer, no consumer
+    return [rms, amax, t]
+
+
+def test_reduce_chains_fuse_into_one_kernel(be, monkeypatch):
+    """Reduce absorbs its elementwise producer and consumer: one launch per chain
+    (the unfused plan runs producer, reduce and consumer as three)."""
+    p = plan_of(be, _reduce_chains)
+    assert p.count("fused_reduce_sum (float32)[96 1000] -> (float32)[96] (producer fused) (consumer fused)") == 1, p
+    assert p.count("fused_reduce_max (float32)[6 40 5] -> (float32)[40] (producer fused) (consumer fused)") == 1, p
+    assert p.count("fused_reduce_sum (float32)[1000 96] -> (float32)[96] (producer fused)") == 1, p
+    assert "fused_elementwise" not in p and "reduce_sum (" not in p.replace("fused_reduce_sum", "")
+    monkeypatch.setenv("GHIP_REDUCE_FUSION", "0")
+    u = plan_of(be, _reduce_chains)
+    assert "fused_reduce" not in u and u.count("fused_elementwise") == 5, u
+
+
+def test_reduce_fusion_leaves_shared_and_output_values(be):
+    """A producer that is also a graph output, or read by a second user, stays
+    materialised; the Reduce then reads it."""
+    def build(f):
+        x = f.Parameter("x", make_shape(F32, 64, 128))
+        sq = f.Mul(x, x)
+        return [f.ReduceSum(sq, 1), sq]
+    p = plan_of(be, build)
+    assert "fused_reduce" not in p and p.count("fused_elementwise") == 1 and "reduce_sum" in p
+    def build2(f):
+        x = f.Parameter("x", make_shape(dtypes.Int32, 64, 50))
+        return [f.ReduceSum(f.Mul(x, x), 1), f.ReduceMin(f.Neg(x))]
+    p = plan_of(be, build2)
+    assert "fused_reduce_sum (int32)[64 50] -> (int32)[64] (producer fused)" in p
+    assert "fused_reduce_min (int32)[64 50] -> (int32)[] (producer fused)" in p
+
+
 def test_softmax_chain_and_fused_softmax(be):
     def build(f):
         x = f.Parameter("x", make_shape(F32, 4096, 1024))
