@@ -55,7 +55,12 @@ struct f16_t {
 __device__ __forceinline__ float f16_to_f32(uint16_t b) {
   return static_cast<float>(__builtin_bit_cast(_Float16, b));
 }
+// Round to nearest even from the fp32 value.  The empty asm makes f an opaque
+// fp32 register, so the compiler cannot fold the rounding into the producing
+// fma / multiply (v_fma_mixlo_f16 rounds the exact product to f16 once, which can
+// differ from rounding the fp32 result): every kernel rounds the same way.
 __device__ __forceinline__ uint16_t f32_to_f16(float f) {
+  asm volatile("" : "+v"(f));
   return __builtin_bit_cast(uint16_t, static_cast<_Float16>(f));
 }
 __device__ __forceinline__ uint32_t pack_f16x2(float lo, float hi) {

@@ -23,6 +23,9 @@
 // Statistics are fp32 for fp32, bf16 and f16 I/O.
 #include <stdarg.h>
 
+#include <atomic>
+#include <type_traits>
+
 #include "common.h"
 
 namespace ghip {
@@ -130,18 +133,142 @@ __device__ __forceinline__ float row_reduce_max(float v, float (*lds)[4], int sl
   }
 }
 
-// One row per WPR waves; a 256-thread workgroup handles 4 / WPR rows.  NV packed
-// 16-byte vectors per lane.
+// Row statistics of RMSNorm (mean 0, rstd = 1/sqrt(mean(x^2) + eps)) or
+// LayerNorm (mean, rstd = 1/sqrt(var + eps)) from the row values of the calling
+// lanes: xget(i, f) gives vector i as fp32 (live[i]: vector i lies on the row).
+template <typename T, int OP, int NV, int WPR, typename XG>
+__device__ __forceinline__ void norm_stats(XG xget, const bool (&live)[NV], int64_t n, float eps, float (*lds)[4],
+                                           float& mean, float& rstd) {
+  // Contraction only within one expression (s += x * x is one fma; a product is
+  // never fused into a later statement's sum): otherwise the backend may fuse
+  // either product of x0*x0 + x1*x1, and the two norm kernels (which must give
+  // identical results for a row whichever of them runs it) would round
+  // differently.
+#pragma clang fp contract(on)
+  constexpr int VEC = Elem<T>::kVec;
+  const float inv_n = 1.0f / static_cast<float>(n);
+  mean = 0.f;
+  if constexpr (OP == kLayerNorm && WPR > 1) {
+    // Each wave reduces its part of the row to (count, mean, M2) in registers
+    // and one LDS exchange combines the WPR parts (Chan, Golub and LeVeque's
+    // pairwise update: M2 = sum M2_w + n_w (mean_w - mean)^2), instead of a
+    // reduction for the mean followed by a second one for the variance.
+    float cnt = 0.f, sw = 0.f;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      if (!live[i]) continue;
+      float f[VEC];
+      xget(i, f);
+      cnt += VEC;
+#pragma unroll
+      for (int j = 0; j < VEC; ++j) sw += f[j];
+    }
+    cnt = wave_sum(cnt);
+    sw = wave_sum(sw);
+    const float mw = cnt > 0.f ? sw / cnt : 0.f;
+    float qw = 0.f;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      if (!live[i]) continue;
+      float f[VEC];
+      xget(i, f);
+#pragma unroll
+      for (int j = 0; j < VEC; ++j) {
+        const float d = f[j] - mw;
+        qw += d * d;
+      }
+    }
+    qw = wave_sum(qw);
+    const int w = threadIdx.x / kWave, first = (w / WPR) * WPR;
+    if ((threadIdx.x % kWave) == 0) {
+      lds[0][w] = cnt;
+      lds[1][w] = mw;
+      lds[2][w] = qw;
+    }
+    __syncthreads();
+    float sum = 0.f;
+#pragma unroll
+    for (int k = 0; k < WPR; ++k) sum += lds[0][first + k] * lds[1][first + k];
+    mean = sum * inv_n;
+    float m2 = 0.f;
+#pragma unroll
+    for (int k = 0; k < WPR; ++k) {
+      const float d = lds[1][first + k] - mean;
+      m2 += lds[2][first + k] + lds[0][first + k] * d * d;
+    }
+    rstd = rsqrtf(m2 * inv_n + eps);
+  } else {
+    float s = 0.f;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      float f[VEC];
+      xget(i, f);
+#pragma unroll
+      for (int j = 0; j < VEC; ++j) s += (OP == kRmsNorm) ? f[j] * f[j] : f[j];
+    }
+    s = row_reduce_sum<WPR>(s, lds, 0);
+    if constexpr (OP == kRmsNorm) {
+      rstd = rsqrtf(s * inv_n + eps);
+    } else {
+      mean = s * inv_n;
+      float q = 0.f;
+#pragma unroll
+      for (int i = 0; i < NV; ++i) {
+        if (!live[i]) continue;
+        float f[VEC];
+      xget(i, f);
+#pragma unroll
+        for (int j = 0; j < VEC; ++j) {
+          const float d = f[j] - mean;
+          q += d * d;
+        }
+      }
+      q = row_reduce_sum<WPR>(q, lds, 1);
+      rstd = rsqrtf(q * inv_n + eps);
+    }
+  }
+}
+
+// Store pass of the norms: y = (x - mean) * rstd [* gamma] [+ beta], one copy per
+// (gamma, beta) presence (tested per element, the uniform pointer checks became a
+// select per value); gfetch / bfetch(i, c0, out) supply vector i of gamma / beta.
+template <typename T, int NV, int LANES, typename XG, typename HG, typename HB, typename GF, typename BF>
+__device__ __forceinline__ void norm_store(XG xget, const bool (&live)[NV], float mean, float rstd, T* yr, int l, HG,
+                                           HB, GF gfetch, BF bfetch) {
+#pragma clang fp contract(on)
+  constexpr int VEC = Elem<T>::kVec;
+  constexpr bool G = HG::value, B = HB::value;
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int64_t c0 = (static_cast<int64_t>(i) * LANES + l) * VEC;
+    if (!live[i]) continue;
+    float x[VEC], f[VEC], gv[VEC], bv[VEC];
+    xget(i, x);
+    if constexpr (G) gfetch(i, c0, gv);
+    if constexpr (B) bfetch(i, c0, bv);
+#pragma unroll
+    for (int j = 0; j < VEC; ++j) {
+      const float t = (x[j] - mean) * rstd;
+      if constexpr (G && B) f[j] = fmaf(t, gv[j], bv[j]);
+      else if constexpr (G) f[j] = t * gv[j];
+      else if constexpr (B) f[j] = t + bv[j];
+      else f[j] = t;
+    }
+    st_nt(yr + c0, pack(f, T{}));
+  }
+}
+
+// One row per WPR waves; a 256-thread workgroup handles 4 / WPR rows (row group
+// `blk`).  NV packed 16-byte vectors per lane.
 template <typename T, int OP, int NV, int WPR>
-__global__ __launch_bounds__(256) void rows_reg_kernel(RowParams p) {
+__device__ __forceinline__ void rows_reg_group(const RowParams& p, int64_t blk, float (*lds)[4]) {
   constexpr int VEC = Elem<T>::kVec;
   constexpr int LANES = kWave * WPR;
   constexpr int ROWS_PER_BLOCK = 4 / WPR;
-  __shared__ float lds[3][4];
 
   const int sub = threadIdx.x / LANES;  // row slot within the block
   const int l = threadIdx.x % LANES;    // lane index within the row
-  const int64_t row = static_cast<int64_t>(blockIdx.x) * ROWS_PER_BLOCK + sub;
+  const int64_t row = blk * ROWS_PER_BLOCK + sub;
   // With WPR > 1 every wave of a row slot shares the row, and the grid covers
   // whole blocks only when rows % ROWS_PER_BLOCK == 0; the early exit is taken
   // by all waves of a row slot together.  Reductions sync the whole block, so a
@@ -263,121 +390,138 @@ __global__ __launch_bounds__(256) void rows_reg_kernel(RowParams p) {
       gr[i] = (p.gamma && live[i]) ? *reinterpret_cast<const uint4*>(static_cast<const T*>(p.gamma) + c0)
                                    : make_uint4(0, 0, 0, 0);
     }
-    // Unpacked once: the statistics passes and the store pass read these.
+    // Kept packed: each pass widens the vectors as it reads them (a shift or a
+    // mask per 16-bit value), which needs half the registers of an fp32 copy.
+    float mean, rstd;
+    auto xget = [&](int i, float* f) { unpack(v[i], f, T{}); };
+    norm_stats<T, OP, NV, WPR>(xget, live, n, p.eps, lds, mean, rstd);
+    const T* g = static_cast<const T*>(p.gamma);
+    const T* b = static_cast<const T*>(p.beta);
+    auto gfetch = [&](int i, int64_t c0, float* gv) {
+      if constexpr (kEarlyParams) unpack(gr[i], gv, T{});
+      else load_vec(g + c0, gv);
+    };
+    auto bfetch = [&](int i, int64_t c0, float* bv) { load_vec(b + c0, bv); };
+    using yes = std::true_type;
+    using no = std::false_type;
+    if (g && b) norm_store<T, NV, LANES>(xget, live, mean, rstd, yr, l, yes{}, yes{}, gfetch, bfetch);
+    else if (g) norm_store<T, NV, LANES>(xget, live, mean, rstd, yr, l, yes{}, no{}, gfetch, bfetch);
+    else if (b) norm_store<T, NV, LANES>(xget, live, mean, rstd, yr, l, no{}, yes{}, gfetch, bfetch);
+    else norm_store<T, NV, LANES>(xget, live, mean, rstd, yr, l, no{}, no{}, gfetch, bfetch);
+  }
+}
+
+template <typename T, int OP, int NV, int WPR>
+__global__ __launch_bounds__(256) void rows_reg_kernel(RowParams p) {
+  __shared__ float lds[3][4];
+  rows_reg_group<T, OP, NV, WPR>(p, blockIdx.x, lds);
+}
+
+// Streaming RMSNorm / LayerNorm for rows that exactly fill NV vectors of every
+// lane (n == NV * 64 * WPR * VEC): a grid of a few workgroups per CU, each looping
+// over row groups with the next group's x loaded (into a second register set)
+// before the current group's statistics, so HBM reads of one row overlap the
+// reduction, scaling and stores of the previous; gamma and beta are read into
+// registers once per workgroup instead of once per row.  The loop has no
+// divergent branch and issues no load between a group's stores and the wait for
+// the next group's x, so that wait never covers the stores (vmcnt counts loads
+// and stores in issue order).  Same arithmetic as rows_reg_group.
+template <typename T, int OP, int NV, int WPR>
+__global__ __launch_bounds__(256) void rows_norm_stream_kernel(RowParams p, int64_t groups) {
+  constexpr int VEC = Elem<T>::kVec;
+  constexpr int LANES = kWave * WPR;
+  constexpr int RPB = 4 / WPR;
+  __shared__ float lds[2][3][4];
+  // The row slot is the same for the whole wave (LANES is a multiple of 64).
+  const int sub = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) / LANES);
+  const int l = threadIdx.x % LANES;
+  const int64_t n = p.n;
+  int64_t blk = blockIdx.x;
+  if (blk >= groups) return;  // whole workgroup
+  const T* g = static_cast<const T*>(p.gamma);
+  const T* b = OP == kLayerNorm ? static_cast<const T*>(p.beta) : nullptr;
+  // gamma / beta widened once (the grid has two workgroups per CU, so registers
+  // are not what limits the waves in flight).
+  float gf[NV][VEC], bfl[NV][VEC];
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int64_t c0 = (static_cast<int64_t>(i) * LANES + l) * VEC;
+    unpack(g ? *reinterpret_cast<const uint4*>(g + c0) : make_uint4(0, 0, 0, 0), gf[i], T{});
+    unpack(b ? *reinterpret_cast<const uint4*>(b + c0) : make_uint4(0, 0, 0, 0), bfl[i], T{});
+  }
+  // Wait for gamma / beta here, once: left pending into the loop, the registers
+  // they land in make the compiler wait for every outstanding load and store at
+  // the top of each iteration (it cannot tell the first iteration apart).
+  __builtin_amdgcn_s_waitcnt(0);
+  bool live[NV];
+#pragma unroll
+  for (int i = 0; i < NV; ++i) live[i] = true;
+  // Rows past the end (the last group of an odd row count) load the last row
+  // again and store nothing.
+  auto load = [&](int64_t k, uint4 (&v)[NV]) {
+    int64_t row = k * RPB + sub;
+    if (row >= p.rows) row = p.rows - 1;
+    const T* xr = static_cast<const T*>(p.x) + row * n;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) v[i] = ld_nt(xr + (static_cast<int64_t>(i) * LANES + l) * VEC);
+  };
+  auto process = [&](int64_t k, const uint4 (&v)[NV], float (*L)[4]) {
+    const int64_t row = k * RPB + sub;
+    // x widened once for the statistics passes and the store pass.
     float xf[NV][VEC];
 #pragma unroll
     for (int i = 0; i < NV; ++i) unpack(v[i], xf[i], T{});
-    const float inv_n = 1.0f / static_cast<float>(n);
-    float mean = 0.f, rstd;
-    if constexpr (OP == kLayerNorm && WPR > 1) {
-      // Each wave reduces its part of the row to (count, mean, M2) in registers
-      // and one LDS exchange combines the WPR parts (Chan, Golub and LeVeque's
-      // pairwise update: M2 = sum M2_w + n_w (mean_w - mean)^2), instead of a
-      // reduction for the mean followed by a second one for the variance.
-      float cnt = 0.f, sw = 0.f;
+    auto xget = [&](int i, float* f) {
 #pragma unroll
-      for (int i = 0; i < NV; ++i) {
-        if (!live[i]) continue;
-        const float* f = xf[i];
-        cnt += VEC;
+      for (int j = 0; j < VEC; ++j) f[j] = xf[i][j];
+    };
+    float mean, rstd;
+    norm_stats<T, OP, NV, WPR>(xget, live, n, p.eps, L, mean, rstd);
+    if (row >= p.rows) return;
+    T* yr = static_cast<T*>(p.y) + row * n;
+    auto gfetch = [&](int i, int64_t, float* gv) {
 #pragma unroll
-        for (int j = 0; j < VEC; ++j) sw += f[j];
-      }
-      cnt = wave_sum(cnt);
-      sw = wave_sum(sw);
-      const float mw = cnt > 0.f ? sw / cnt : 0.f;
-      float qw = 0.f;
+      for (int j = 0; j < VEC; ++j) gv[j] = gf[i][j];
+    };
+    auto bfetch = [&](int i, int64_t, float* bv) {
 #pragma unroll
-      for (int i = 0; i < NV; ++i) {
-        if (!live[i]) continue;
-        const float* f = xf[i];
-#pragma unroll
-        for (int j = 0; j < VEC; ++j) {
-          const float d = f[j] - mw;
-          qw += d * d;
-        }
-      }
-      qw = wave_sum(qw);
-      const int w = threadIdx.x / kWave, first = (w / WPR) * WPR;
-      if ((threadIdx.x % kWave) == 0) {
-        lds[0][w] = cnt;
-        lds[1][w] = mw;
-        lds[2][w] = qw;
-      }
-      __syncthreads();
-      float sum = 0.f;
-#pragma unroll
-      for (int k = 0; k < WPR; ++k) sum += lds[0][first + k] * lds[1][first + k];
-      mean = sum * inv_n;
-      float m2 = 0.f;
-#pragma unroll
-      for (int k = 0; k < WPR; ++k) {
-        const float d = lds[1][first + k] - mean;
-        m2 += lds[2][first + k] + lds[0][first + k] * d * d;
-      }
-      rstd = rsqrtf(m2 * inv_n + p.eps);
-    } else {
-      float s = 0.f;
-#pragma unroll
-      for (int i = 0; i < NV; ++i) {
-        const float* f = xf[i];
-#pragma unroll
-        for (int j = 0; j < VEC; ++j) s += (OP == kRmsNorm) ? f[j] * f[j] : f[j];
-      }
-      s = row_reduce_sum<WPR>(s, lds, 0);
-      if constexpr (OP == kRmsNorm) {
-        rstd = rsqrtf(s * inv_n + p.eps);
-      } else {
-        mean = s * inv_n;
-        float q = 0.f;
-#pragma unroll
-        for (int i = 0; i < NV; ++i) {
-          if (!live[i]) continue;
-          const float* f = xf[i];
-#pragma unroll
-          for (int j = 0; j < VEC; ++j) {
-            const float d = f[j] - mean;
-            q += d * d;
-          }
-        }
-        q = row_reduce_sum<WPR>(q, lds, 1);
-        rstd = rsqrtf(q * inv_n + p.eps);
-      }
-    }
-    const T* g = static_cast<const T*>(p.gamma);
-    const T* b = static_cast<const T*>(p.beta);
-    // One copy of the store pass per (gamma, beta) presence: tested per
-    // element, the uniform pointer checks became a select per value.
-    auto store_pass = [&](auto has_g, auto has_b) {
-      constexpr bool G = decltype(has_g)::value, B = decltype(has_b)::value;
-#pragma unroll
-      for (int i = 0; i < NV; ++i) {
-        const int64_t c0 = (static_cast<int64_t>(i) * LANES + l) * VEC;
-        if (!live[i]) continue;
-        const float* x = xf[i];
-        float f[VEC], gv[VEC], bv[VEC];
-        if constexpr (G) {
-          if constexpr (kEarlyParams) unpack(gr[i], gv, T{});
-          else load_vec(g + c0, gv);
-        }
-        if constexpr (B) load_vec(b + c0, bv);
-#pragma unroll
-        for (int j = 0; j < VEC; ++j) {
-          const float t = (x[j] - mean) * rstd;
-          if constexpr (G && B) f[j] = fmaf(t, gv[j], bv[j]);
-          else if constexpr (G) f[j] = t * gv[j];
-          else if constexpr (B) f[j] = t + bv[j];
-          else f[j] = t;
-        }
-        st_nt(yr + c0, pack(f, T{}));
-      }
+      for (int j = 0; j < VEC; ++j) bv[j] = bfl[i][j];
     };
     using yes = std::true_type;
     using no = std::false_type;
-    if (g && b) store_pass(yes{}, yes{});
-    else if (g) store_pass(yes{}, no{});
-    else if (b) store_pass(no{}, yes{});
-    else store_pass(no{}, no{});
+    if (g && b) norm_store<T, NV, LANES>(xget, live, mean, rstd, yr, l, yes{}, yes{}, gfetch, bfetch);
+    else if (g) norm_store<T, NV, LANES>(xget, live, mean, rstd, yr, l, yes{}, no{}, gfetch, bfetch);
+    else if (b) norm_store<T, NV, LANES>(xget, live, mean, rstd, yr, l, no{}, yes{}, gfetch, bfetch);
+    else norm_store<T, NV, LANES>(xget, live, mean, rstd, yr, l, no{}, no{}, gfetch, bfetch);
+  };
+  // The loop body handles two groups (register sets va, vb) and has no exit in
+  // between, so no path reaches a prefetch with that register set's previous
+  // loads still pending; it runs while both of its prefetches are in range, and
+  // the last one or two groups follow it without a prefetch past the end.  The
+  // scheduling fences keep the compiler from sinking a prefetch below the
+  // statistics or the stores that follow it.
+  const int64_t G = gridDim.x;
+  const int64_t iters = (groups - blk + G - 1) / G;
+  uint4 va[NV], vb[NV];
+  load(blk, va);
+  int64_t it = 0;
+  for (; it + 2 < iters; it += 2) {
+    load(blk + G, vb);
+    __builtin_amdgcn_sched_barrier(0);
+    process(blk, va, lds[0]);
+    blk += G;
+    load(blk + G, va);
+    __builtin_amdgcn_sched_barrier(0);
+    process(blk, vb, lds[1]);
+    blk += G;
+  }
+  if (iters - it == 2) {
+    load(blk + G, vb);
+    __builtin_amdgcn_sched_barrier(0);
+    process(blk, va, lds[0]);
+    process(blk + G, vb, lds[1]);
+  } else {
+    process(blk, va, lds[0]);
   }
 }
 
@@ -458,13 +602,72 @@ static inline bool aligned16(const void* ptr) {
   return (reinterpret_cast<uintptr_t>(ptr) & 15u) == 0;
 }
 
+// CUs of the current device (cached per device).
+static int device_cus() {
+  static std::atomic<int> cache[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  int c = cache[dev].load(std::memory_order_relaxed);
+  if (c == 0) {
+    if (hipDeviceGetAttribute(&c, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || c <= 0) c = 256;
+    cache[dev].store(c, std::memory_order_relaxed);
+  }
+  return c;
+}
+
 template <typename T, int OP, int NV, int WPR>
 static hipError_t launch_reg(const RowParams& p, hipStream_t s) {
   const int rows_per_block = 4 / WPR;
-  const int64_t blocks = (p.rows + rows_per_block - 1) / rows_per_block;
-  hipLaunchKernelGGL((rows_reg_kernel<T, OP, NV, WPR>), dim3(static_cast<unsigned>(blocks)),
-                     dim3(256), 0, s, p);
+  const int64_t groups = (p.rows + rows_per_block - 1) / rows_per_block;
+  hipLaunchKernelGGL((rows_reg_kernel<T, OP, NV, WPR>), dim3(static_cast<unsigned>(groups)), dim3(256), 0, s, p);
   return hipGetLastError();
+}
+
+template <typename T, int OP, int NV, int WPR>
+static hipError_t launch_norm_stream(const RowParams& p, hipStream_t s, int64_t grid_cap) {
+  const int rows_per_block = 4 / WPR;
+  const int64_t groups = (p.rows + rows_per_block - 1) / rows_per_block;
+  const int64_t grid = groups > grid_cap ? grid_cap : groups;
+  hipLaunchKernelGGL((rows_norm_stream_kernel<T, OP, NV, WPR>), dim3(static_cast<unsigned>(grid)), dim3(256), 0, s,
+                     p, groups);
+  return hipGetLastError();
+}
+
+// RMSNorm / LayerNorm rows that exactly fill NV vectors per lane, with at least
+// four row groups per workgroup of a (normally) two-per-CU grid, stream through
+// rows_norm_stream_kernel (measured on MI355X, [8192, 4096]: fp32 71% -> 76% of
+// the HBM peak, bf16 RMSNorm 69% -> 72%, bf16 LayerNorm 67% -> 70%; grids of one
+// or two workgroups per CU beat larger ones and uneven multiples of the CU
+// count); everything else takes one workgroup per row group.
+// Workgroups of rows_norm_stream_kernel<...> per CU for the streaming grid: two,
+// or one where the kernel's registers allow only one (a second, non-resident
+// workgroup per CU would start its share of the rows only after the first ends).
+template <typename T, int OP, int NV, int WPR>
+static int stream_blocks_per_cu() {
+  static std::atomic<int> cached{0};
+  int c = cached.load(std::memory_order_relaxed);
+  if (c == 0) {
+    int b = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&b, rows_norm_stream_kernel<T, OP, NV, WPR>, 256, 0) !=
+            hipSuccess ||
+        b <= 0)
+      b = 1;
+    c = b < 2 ? b : 2;
+    cached.store(c, std::memory_order_relaxed);
+  }
+  return c;
+}
+
+template <typename T, int OP, int NV, int WPR>
+static hipError_t launch_norm(const RowParams& p, hipStream_t s) {
+  if constexpr (NV <= 8) {
+    const int rows_per_block = 4 / WPR;
+    const int64_t groups = (p.rows + rows_per_block - 1) / rows_per_block;
+    const int64_t grid = stream_blocks_per_cu<T, OP, NV, WPR>() * static_cast<int64_t>(device_cus());
+    if (p.n == static_cast<int64_t>(NV) * kWave * WPR * Elem<T>::kVec && groups >= 4 * grid)
+      return launch_norm_stream<T, OP, NV, WPR>(p, s, grid);
+  }
+  return launch_reg<T, OP, NV, WPR>(p, s);
 }
 
 template <typename T, int OP>
@@ -476,13 +679,23 @@ static hipError_t launch_rows(const RowParams& p, hipStream_t s) {
   if (vec_ok) {
     // Waves per row: aim for about four 16-byte vectors per lane.
     const int64_t vecs = p.n / VEC;  // 16-byte vectors per row
-    if (vecs <= 64 * 1) return launch_reg<T, OP, 1, 1>(p, s);
-    if (vecs <= 64 * 2) return launch_reg<T, OP, 2, 1>(p, s);
-    if (vecs <= 64 * 4) return launch_reg<T, OP, 4, 1>(p, s);
-    if (vecs <= 128 * 4) return launch_reg<T, OP, 4, 2>(p, s);
-    if (vecs <= 256 * 4) return launch_reg<T, OP, 4, 4>(p, s);
-    if (vecs <= 256 * 8) return launch_reg<T, OP, 8, 4>(p, s);
-    if (vecs <= 256 * 16) return launch_reg<T, OP, 16, 4>(p, s);
+    constexpr bool kNorm = OP == kRmsNorm || OP == kLayerNorm;
+    auto go = [&](auto nv, auto wpr) {
+      if constexpr (kNorm) return launch_norm<T, OP, decltype(nv)::value, decltype(wpr)::value>(p, s);
+      else return launch_reg<T, OP, decltype(nv)::value, decltype(wpr)::value>(p, s);
+    };
+    using I1 = std::integral_constant<int, 1>;
+    using I2 = std::integral_constant<int, 2>;
+    using I4 = std::integral_constant<int, 4>;
+    using I8 = std::integral_constant<int, 8>;
+    using I16 = std::integral_constant<int, 16>;
+    if (vecs <= 64 * 1) return go(I1{}, I1{});
+    if (vecs <= 64 * 2) return go(I2{}, I1{});
+    if (vecs <= 64 * 4) return go(I4{}, I1{});
+    if (vecs <= 128 * 4) return go(I4{}, I2{});
+    if (vecs <= 256 * 4) return go(I4{}, I4{});
+    if (vecs <= 256 * 8) return go(I8{}, I4{});
+    if (vecs <= 256 * 16) return go(I16{}, I4{});
   }
   hipLaunchKernelGGL((rows_generic_kernel<T, OP>), dim3(static_cast<unsigned>(p.rows)),
                      dim3(256), 0, s, p);

@@ -246,3 +246,41 @@ def test_norms_16bit_odd_rows(cuda, dtype, n):
     assert ulps(ops.rmsnorm(xd, gd, 1e-6), orc.rmsnorm(x, g, 1e-6)) <= 1
     y = ops.layernorm(xd, gd, bd, 1e-5).float().cpu().numpy()
     assert rel_err(y, orc.layernorm(x, g, b, 1e-5)) <= tol
+
+
+@pytest.mark.parametrize("dtype,n,rows", [
+    (torch.float32, 4096, 3001),     # 4 waves per row, one row per workgroup: ragged iteration counts
+    (torch.bfloat16, 4096, 4099),    # 2 waves per row: the last group holds one row
+    (torch.float16, 2048, 8195),     # 1 wave per row, 4 rows per group: last group holds 3 rows
+    (torch.bfloat16, 1024, 8200),    # 2 vectors per lane
+])
+def test_norms_streaming_rows_match_single_group_kernel(cuda, dtype, n, rows):
+    """Row counts large enough for the streaming RMSNorm / LayerNorm kernel (a
+    grid of two workgroups per CU looping over row groups with the next group
+    prefetched): every row is bit-identical to the one-group-per-workgroup kernel,
+    which a launch over 64 rows takes, and within the dtype's rounding of the
+    oracle; gamma / beta in every combination."""
+    x = synth.normal(2700 + n, (rows, n), std=1.5, mean=0.25)
+    g = synth.uniform_f32(2800 + n, (n,), 0.5, 1.5)
+    b = synth.normal(2900 + n, (n,), std=0.1)
+    if dtype == torch.bfloat16:
+        x, g, b = synth.round_bf16(x), synth.round_bf16(g), synth.round_bf16(b)
+        tol = BF16_TOL
+    elif dtype == torch.float16:
+        x, g, b = (a.astype(np.float16).astype(np.float32) for a in (x, g, b))
+        tol = 2.0 ** -11 + 1e-5
+    else:
+        tol = F32_TOL
+    xd, gd, bd = (to_dev(a, cuda, dtype) for a in (x, g, b))
+    picks = np.array([0, 1, 2, 3, 511, 512, 1023, 2047, rows // 2, rows - 3, rows - 2, rows - 1])
+    sub = xd[torch.from_numpy(picks).to(cuda)].contiguous()
+    for gg, bb in [(gd, bd), (gd, None), (None, bd), (None, None)]:
+        ys = [ops.rmsnorm(xd, gg, 1e-6), ops.layernorm(xd, gg, bb, 1e-5)]
+        small = [ops.rmsnorm(sub, gg, 1e-6), ops.layernorm(sub, gg, bb, 1e-5)]
+        for y, s in zip(ys, small):
+            assert torch.equal(y[torch.from_numpy(picks).to(cuda)].view(torch.int16 if dtype != torch.float32 else torch.int32),
+                               s.view(torch.int16 if dtype != torch.float32 else torch.int32))
+        gn = g if gg is not None else None
+        bn = b if bb is not None else None
+        assert rel_err(ys[0].float().cpu().numpy(), orc.rmsnorm(x, gn, 1e-6)) <= tol
+        assert rel_err(ys[1].float().cpu().numpy(), orc.layernorm(x, gn, bn, 1e-5)) <= tol
