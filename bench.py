@@ -208,8 +208,9 @@ def make_cases(only=None):
         xs = [torch.randn((rows, n), device=dev, generator=g).to(dtype) for _ in range(rot)]
         ys = [torch.empty_like(xs[0]) for _ in range(rot)]
         gam = (torch.rand((n,), device=dev, generator=g) + 0.5).to(dtype)
+        kern = "rows_norm_stream_kernel<float, 2, 4, 4>" if tag == "f32" else "rows_norm_stream_kernel<bf16_t, 2, 4, 2>"
         return Case(f"rmsnorm_{tag}", lambda i: ops.rmsnorm(xs[i % rot], gam, 1e-6, out=ys[i % rot]),
-                    bytes_per_step=nbytes, dtype=tag, rotation=rot, kernel="rows_reg_kernel",
+                    bytes_per_step=nbytes, dtype=tag, rotation=rot, kernel=kern,
                     out=lambda i: ys[i % rot],
                     config={"workload": f"RMSNorm last axis, x [8192,4096] {tag}, gamma [4096], eps 1e-6, fp32 statistics"})
 
@@ -222,9 +223,10 @@ def make_cases(only=None):
         ys = [torch.empty_like(xs[0]) for _ in range(rot)]
         gam = (torch.rand((n,), device=dev, generator=g) + 0.5).to(dtype)
         bet = (torch.randn((n,), device=dev, generator=g) * 0.1).to(dtype)
+        kern = "rows_norm_stream_kernel<float, 3, 4, 4>" if tag == "f32" else "rows_norm_stream_kernel<bf16_t, 3, 4, 2>"
         return Case(f"layernorm_{tag}",
                     lambda i: ops.layernorm(xs[i % rot], gam, bet, 1e-5, out=ys[i % rot]),
-                    bytes_per_step=nbytes, dtype=tag, rotation=rot, kernel="rows_reg_kernel",
+                    bytes_per_step=nbytes, dtype=tag, rotation=rot, kernel=kern,
                     out=lambda i: ys[i % rot],
                     config={"workload": f"LayerNorm last axis, x [8192,4096] {tag}, eps 1e-5"})
 
@@ -235,7 +237,7 @@ def make_cases(only=None):
         xs = [torch.randn((rows, n), device=dev, generator=g) * 2 for _ in range(rot)]
         ys = [torch.empty_like(xs[0]) for _ in range(rot)]
         return Case("softmax_f32", lambda i: ops.softmax(xs[i % rot], out=ys[i % rot]),
-                    bytes_per_step=nbytes, dtype="f32", rotation=rot, kernel="rows_reg_kernel",
+                    bytes_per_step=nbytes, dtype="f32", rotation=rot, kernel="rows_reg_kernel<float, 0, 4, 1>",
                     out=lambda i: ys[i % rot],
                     config={"workload": "Softmax last axis, x [4096,1024] fp32 ~ N(0, 2^2)"})
 
@@ -422,15 +424,27 @@ def cpu_baseline(seconds_target=10.0):
 def copy_reference(mib: int, steps: int):
     """A plain device-to-device copy of `mib` MiB, `steps` times: its FETCH_SIZE /
     WRITE_SIZE counters per dispatch, divided by mib * 1024, give the factor that
-    turns those counters into bytes for the kernels measured beside it."""
+    turns those counters into bytes for the kernels measured beside it.  Also
+    times the copies (HIP events; sources and destinations rotate over enough
+    buffers that the 256 MB Infinity Cache cannot serve them) and reports GB/s of
+    bytes read plus written: the copy ceiling at that size."""
     import torch
     n = mib * (1 << 20) // 4
-    x = torch.ones(n, device="cuda", dtype=torch.float32)
-    y = torch.empty_like(x)
-    for _ in range(steps):
-        y.copy_(x)
+    rot = rotation_for(2 * n * 4)
+    xs = [torch.ones(n, device="cuda", dtype=torch.float32) for _ in range(rot)]
+    ys = [torch.empty_like(xs[0]) for _ in range(rot)]
+    for i in range(min(steps, rot)):
+        ys[i].copy_(xs[i])
     torch.cuda.synchronize()
-    print(json.dumps({"copy_ref_mib": mib, "steps": steps}))
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    ev0.record()
+    for i in range(steps):
+        ys[i % rot].copy_(xs[i % rot])
+    ev1.record()
+    torch.cuda.synchronize()
+    us = ev0.elapsed_time(ev1) * 1e3 / max(steps, 1)
+    print(json.dumps({"copy_ref_mib": mib, "steps": steps, "rotation": rot, "us_per_copy": round(us, 2),
+                      "gbs": round(2 * n * 4 / us / 1e3, 1)}))
 
 
 def main():
@@ -462,7 +476,8 @@ def main():
                      "graph": r["graph"],
                      "launch_us": round(r["launch_us"], 2),
                      "value": r["roofline"]["achieved"], "unit": r["roofline"]["unit"],
-                     "roofline": r["roofline"], "rotation": case.rotation,
+                     "roofline": dict(r["roofline"], traffic=measured_traffic(case.kernel)),
+                     "rotation": case.rotation,
                      "kernel": case.kernel, "config": case.config}
             if case.executed_flops:
                 # MFMA utilisation by the work actually executed (causal half only)
@@ -494,7 +509,7 @@ def main():
                        settle_warmup_steps=res["settle_steps"]),
         # traffic: HBM bytes per launch from the committed rocprofv3 FETCH_SIZE /
         # WRITE_SIZE summary of this kernel (counters cannot be read in-process)
-        "roofline": dict(res["roofline"], traffic=measured_traffic("rows_reg_kernel<float, 2, 4, 4>")),
+        "roofline": dict(res["roofline"], traffic=measured_traffic(primary.kernel)),
         "cpu_baseline": cpu,
         "secondary": secondary,
     }

@@ -888,8 +888,8 @@ struct Lowerer {
   View emit_argminmax(int v) {
     const Node& n = N[v];
     const Shape& xs = N[n.in[0]].shape;
-    if (xs.dtype != GHIP_DTYPE_FLOAT32 && xs.dtype != GHIP_DTYPE_BFLOAT16)
-      return fail(GHIP_ERR_UNSUPPORTED, "ArgMinMax lowers float32 / bfloat16 inputs");
+    if (xs.dtype == GHIP_DTYPE_BOOL || xs.dtype == GHIP_DTYPE_FLOAT64)
+      return fail(GHIP_ERR_UNSUPPORTED, "ArgMinMax lowers float32 / bfloat16 / float16 and integer inputs");
     View x = materialize(get(n.in[0]), xs);
     if (failed) return bad();
     const int ax = static_cast<int>(n.i0);

@@ -9,7 +9,9 @@ import ctypes
 import os
 
 _PKG_ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-LIB_PATH = os.path.join(_PKG_ROOT, "lib", "libgomlx_hip.so")
+# GHIP_LIB_PATH selects another build of the same ABI (e.g. the sanitizer build
+# of the host code, `make -C go-darwinml_amd/csrc asan`).
+LIB_PATH = os.environ.get("GHIP_LIB_PATH") or os.path.join(_PKG_ROOT, "lib", "libgomlx_hip.so")
 CSRC_DIR = os.path.join(_PKG_ROOT, "csrc")
 
 # Dtype numbering of include/gomlx_hip.h (the reference's MPSGraphDType).

@@ -18,7 +18,12 @@ _DT = {
     torch.int64: _lib.DT_INT64,
     torch.bool: _lib.DT_BOOL,
     torch.uint8: _lib.DT_UINT8,
+    torch.int8: _lib.DT_INT8,
+    torch.int16: _lib.DT_INT16,
 }
+for _name, _code in (("uint16", "DT_UINT16"), ("uint32", "DT_UINT32"), ("uint64", "DT_UINT64")):
+    if hasattr(torch, _name) and hasattr(_lib, _code):
+        _DT[getattr(torch, _name)] = getattr(_lib, _code)
 
 
 def dtype_code(dt: torch.dtype) -> int:

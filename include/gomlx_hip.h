@@ -166,7 +166,8 @@ int ghip_gather_rows(const void* table, int64_t V, int64_t row_bytes, const int3
 /* ArgMax (is_min = 0) / ArgMin (is_min = 1) of x viewed as [outer, n, inner]
  * along the middle axis; out has out_dtype (INT32 or INT64).  Ties -> lowest
  * index, NaN wins (first NaN).  Replaces Function.ArgMinMax (function.go:
- * 1204-1242). x dtype FLOAT32 or BFLOAT16. */
+ * 1204-1242). x dtype FLOAT32, BFLOAT16, FLOAT16 or any integer type (compared
+ * as int64 / uint64). */
 int ghip_argminmax(int dtype, const void* x, int64_t outer, int64_t n, int64_t inner,
                    int is_min, int out_dtype, void* out, void* stream, GHipError* err);
 

@@ -359,6 +359,27 @@ void orc_argminmax(const float* x, int64_t outer, int64_t n, int64_t inner, int 
     }
 }
 
+/* ArgMin / ArgMax of integers (x widened to int64, or to uint64 when
+ * is_unsigned): the extreme value, ties to the lowest index. */
+void orc_argminmax_int(const int64_t* x, int64_t outer, int64_t n, int64_t inner, int is_min,
+                       int is_unsigned, int64_t* out) {
+  for (int64_t o = 0; o < outer; ++o)
+    for (int64_t j = 0; j < inner; ++j) {
+      const int64_t* xr = x + o * n * inner + j;
+      int64_t best = 0;
+      for (int64_t i = 1; i < n; ++i) {
+        const int64_t v = xr[i * inner], b = xr[best * inner];
+        int better;
+        if (is_unsigned)
+          better = is_min ? ((uint64_t)v < (uint64_t)b) : ((uint64_t)v > (uint64_t)b);
+        else
+          better = is_min ? (v < b) : (v > b);
+        if (better) best = i;
+      }
+      out[o * inner + j] = best;
+    }
+}
+
 /* ---------------------------------------------------------------------------
  * Iota.
  * Reference: Function.Iota (mpsgraph/gomlx/function.go:1127-1135) ->

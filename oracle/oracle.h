@@ -29,6 +29,9 @@
  *   orc_gather_rows  reference known answers (mpsgraph_test.go:648-672).
  *   orc_argminmax    reference known answer (mpsgraph_test.go:973-990),
  *                    numpy.argmax/argmin on tie-free data.
+ *   orc_argminmax_int numpy.argmax/argmin (first occurrence of the extreme) on
+ *                    int8..int64 / uint8..uint64 data with many ties, including
+ *                    uint64 values above INT64_MAX.
  *   orc_iota         reference known answer (mpsgraph_test.go:795-821).
  *   orc_dynamic_slice / orc_dynamic_update_slice
  *                    reference known answers (mpsgraph_test.go:993-1062,
@@ -106,6 +109,8 @@ void orc_gather_rows(const void* table, int64_t V, int64_t row_bytes, const int3
  * every number and the first NaN is returned. */
 void orc_argminmax(const float* x, int64_t outer, int64_t n, int64_t inner, int is_min,
                    int64_t* out);
+void orc_argminmax_int(const int64_t* x, int64_t outer, int64_t n, int64_t inner, int is_min,
+                       int is_unsigned, int64_t* out);
 
 /* Iota: out viewed as [outer, n, inner], out[o, i, j] = i. */
 void orc_iota(double* out, int64_t outer, int64_t n, int64_t inner);

@@ -55,6 +55,7 @@ def lib():
                                ctypes.c_double, _int, _f64p]
         L.orc_gather_rows.argtypes = [_vp, _i64, _i64, _i32p, _i64, _vp]
         L.orc_argminmax.argtypes = [_f32p, _i64, _i64, _i64, _int, _i64p]
+        L.orc_argminmax_int.argtypes = [_i64p, _i64, _i64, _i64, _int, _int, _i64p]
         L.orc_iota.argtypes = [_f64p, _i64, _i64, _i64]
         L.orc_f32_to_bf16.argtypes = [_f32p, _u16p, _i64]
         L.orc_activation.argtypes = [_f64p, _f64p, _i64, _int]
@@ -207,10 +208,18 @@ def gather_rows(table: np.ndarray, ids) -> np.ndarray:
 
 
 def argminmax(x, axis, is_min=False) -> np.ndarray:
-    x = _f32(x)
+    """Index of the max (min) along `axis`: floats compare as fp32 with NaN
+    winning, integers compare exactly (as int64 / uint64); ties -> lowest index."""
+    x = np.asarray(x)
     outer, n, inner = _split(x.shape, axis)
     out = np.empty(outer * inner, np.int64)
-    lib().orc_argminmax(x, outer, n, inner, int(is_min), out)
+    if x.dtype.kind in "iu":
+        unsigned = x.dtype.kind == "u"
+        xi = np.ascontiguousarray(x.astype(np.uint64 if unsigned else np.int64)).view(np.int64)
+        lib().orc_argminmax_int(xi, outer, n, inner, int(is_min), int(unsigned), out)
+    else:
+        x = _f32(x)
+        lib().orc_argminmax(x, outer, n, inner, int(is_min), out)
     ax = axis % x.ndim
     return out.reshape(x.shape[:ax] + x.shape[ax + 1:])
 

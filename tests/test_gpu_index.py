@@ -68,6 +68,34 @@ def test_argminmax_random_with_ties_nans(cuda, shape_axis, is_min, dtype):
         assert np.array_equal(got, orc.argminmax(x, axis, is_min))
 
 
+@pytest.mark.parametrize("dtype", [torch.int8, torch.int16, torch.int32, torch.int64, torch.uint8,
+                                   torch.float16, "uint16", "uint32", "uint64"])
+def test_argminmax_integers_and_f16(cuda, dtype):
+    """The reference passes any dtype to the arg-reduction (function.go:1204-1242):
+    integers compare exactly (int64 / uint64, the type's extremes included, ties to
+    the lowest index), float16 like the other floats."""
+    if isinstance(dtype, str):
+        if not hasattr(torch, dtype):
+            pytest.skip(f"torch has no {dtype}")
+        npdt, dtype = np.dtype(dtype), getattr(torch, dtype)
+    else:
+        npdt = {torch.int8: np.int8, torch.int16: np.int16, torch.int32: np.int32, torch.int64: np.int64,
+                torch.uint8: np.uint8, torch.float16: np.float16}[dtype]
+    rng = np.random.default_rng(23)
+    for shape, axis in [((64, 1000), 1), ((64, 1000), 0), ((3, 200, 7), 1), ((1, 70000), 1)]:
+        if npdt.kind in "iu":
+            info = np.iinfo(npdt)
+            pool = np.array([info.min, info.max, 0, 1, info.max - 1, info.min + 1, 7], dtype=npdt)
+            x = pool[rng.integers(0, len(pool), size=shape)]
+        else:
+            x = (np.round(rng.standard_normal(shape) * 4) / 4).astype(npdt)
+        signed = {1: np.int8, 2: np.int16, 4: np.int32, 8: np.int64}[npdt.itemsize]
+        t = torch.from_numpy(np.ascontiguousarray(x).view(signed)).to(cuda).view(dtype)
+        for is_min in (False, True):
+            got = ops.argminmax(t, axis, is_min, torch.int64).cpu().numpy()
+            assert np.array_equal(got, orc.argminmax(x, axis, is_min))
+
+
 def test_iota_known_answer_and_dtypes(known, cuda):
     c = known["iota"]
     assert ops.iota(c["shape"], c["axis"], torch.float32, cuda).view(-1).tolist() == c["expected"]

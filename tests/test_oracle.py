@@ -256,6 +256,20 @@ def test_sdpa_masks_of_every_rank_vs_numpy(mshape):
     assert np.all(np.isnan(orc.sdpa(q, k, v, mask=none, scale=0.4)))
 
 
+@pytest.mark.parametrize("dt", [np.int8, np.int16, np.int32, np.int64, np.uint8, np.uint16, np.uint32, np.uint64])
+def test_argminmax_integers_vs_numpy(dt):
+    """Integer inputs compare exactly (numpy's argmax / argmin return the first
+    occurrence of the extreme): few distinct values so ties are everywhere, and
+    the type's extremes, including uint64 values above INT64_MAX."""
+    rng = np.random.default_rng(17)
+    info = np.iinfo(dt)
+    pool = np.array([info.min, info.max, 0, 1, info.max - 1, info.min + 1], dtype=dt)
+    x = pool[rng.integers(0, len(pool), size=(5, 37, 3))]
+    for ax in range(3):
+        assert np.array_equal(orc.argminmax(x, ax), np.argmax(x, axis=ax))
+        assert np.array_equal(orc.argminmax(x, ax, is_min=True), np.argmin(x, axis=ax))
+
+
 def test_argminmax_vs_numpy_and_rules():
     x = synth.normal(61, (6, 17, 5))
     for ax in range(3):
