@@ -140,11 +140,6 @@ __device__ __forceinline__ f32x16_t mma(const bf16x8_t& a, const bf16x8_t& b, co
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
 }
 template <bool F16>
-__device__ __forceinline__ __bf16 to16(float x) {
-  if constexpr (F16) return __builtin_bit_cast(__bf16, static_cast<_Float16>(x));
-  else return static_cast<__bf16>(x);
-}
-template <bool F16>
 __device__ __forceinline__ float from16(uint16_t b) {
   if constexpr (F16) return f16_to_f32(b);
   else return bf16_to_f32(b);
@@ -153,6 +148,19 @@ template <bool F16>
 __device__ __forceinline__ uint32_t pack16x2(float lo, float hi) {
   if constexpr (F16) return pack_f16x2(lo, hi);
   else return pack_bf16x2(lo, hi);
+}
+// acc + lo + hi of a packed pair of 16-bit values (v_dot2c against (1, 1)).
+template <bool F16>
+__device__ __forceinline__ float dot2_ones(uint32_t w, float acc) {
+  if constexpr (F16) {
+    typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+    const f16x2_t one = {static_cast<_Float16>(1.0f), static_cast<_Float16>(1.0f)};
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_t, w), one, acc, false);
+  } else {
+    typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+    const bf16x2_t one = {static_cast<__bf16>(1.0f), static_cast<__bf16>(1.0f)};
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, w), one, acc, false);
+  }
 }
 
 template <int D, bool F16, int MK>
@@ -339,25 +347,32 @@ __global__ __launch_bounds__(256, 2) void sdpa_fwd_kernel(Params p) {
     }
     // A query with nothing unmasked yet keeps m = -inf and exponent offset 0.
     const float nb = m == -INFINITY ? 0.f : -m * c;
-    float ls = 0.f;
 #pragma unroll
     for (int v = 0; v < 16; ++v) {
-      const float e0 = __builtin_amdgcn_exp2f(__builtin_fmaf(s0[v], c, nb));
-      const float e1 = __builtin_amdgcn_exp2f(__builtin_fmaf(s1[v], c, nb));
-      ls += e0 + e1;
-      s0[v] = e0;
-      s1[v] = e1;
+      s0[v] = __builtin_amdgcn_exp2f(__builtin_fmaf(s0[v], c, nb));
+      s1[v] = __builtin_amdgcn_exp2f(__builtin_fmaf(s1[v], c, nb));
     }
-    l += ls;
-    // P^T operand of key step s: s{s/2}[8 (s%2) .. +8] rounded to the 16-bit type.
+    // P^T operand of key step s: s{s/2}[8 (s%2) .. +8] rounded to the 16-bit type,
+    // two values per conversion.  The running sum adds the same rounded weights
+    // (one dot2 against (1, 1) per pair), so the normalisation divides by exactly
+    // the weights the P V product used.
+    uint32_t pw[16];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      pw[i] = pack16x2<F16>(s0[2 * i], s0[2 * i + 1]);
+      pw[8 + i] = pack16x2<F16>(s1[2 * i], s1[2 * i + 1]);
+    }
+    float ls0 = 0.f, ls1 = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      ls0 = dot2_ones<F16>(pw[2 * i], ls0);
+      ls1 = dot2_ones<F16>(pw[2 * i + 1], ls1);
+    }
+    l += ls0 + ls1;
     bf16x8_t pb[4];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      pb[0][e] = to16<F16>(s0[e]);
-      pb[1][e] = to16<F16>(s0[8 + e]);
-      pb[2][e] = to16<F16>(s1[e]);
-      pb[3][e] = to16<F16>(s1[8 + e]);
-    }
+    for (int k = 0; k < 4; ++k)
+      pb[k] = __builtin_bit_cast(bf16x8_t, make_uint4(pw[4 * k], pw[4 * k + 1], pw[4 * k + 2], pw[4 * k + 3]));
 #pragma unroll
     for (int s = 0; s < kBKV / 16; ++s)
 #pragma unroll

@@ -655,7 +655,8 @@ def test_transformer_block_small_stagewise(be):
     checks["gate"], checks["up"] = proj(G["h2"], "w_gate"), proj(G["h2"], "w_up")
     g = G["gate"].astype(np.float64)
     checks["act"] = _bf(_bf(g * _bf(1.0 / (1.0 + np.exp(-g)))) * G["up"])
-    checks["out"] = _bf(G["x2"].astype(np.float64) + proj(G["act"], "w_down"))
+    down = orc.dot_general(f32(G["act"]), [2], [], P["w_down"], [0], [])
+    checks["out"] = _bf(G["x2"].astype(np.float64) + _bf(down))
     for name, want in checks.items():
         got = G[name]
         assert got.shape == want.shape, name
@@ -663,6 +664,14 @@ def test_transformer_block_small_stagewise(be):
             # two bf16 roundings (P, output) of up to 2^-9 each
             assert rel_err(got, want) <= 2.5e-2, name
             assert norm_err(got, want) <= 1e-2, name
+            continue
+        if name == "out":
+            # x2 + bf16(act . w_down): the GPU's fp32 sum order may round the
+            # product the other way (one bf16 ulp of the product, <= 2^-7 |down|),
+            # which cancellation against x2 can make large next to the result.
+            err = np.abs(got.astype(np.float64) - want)
+            assert np.all(err <= 2.0 ** -7 * (np.abs(want) + np.abs(down)) + 1e-30), name
+            assert norm_err(got, want) <= 1e-3, name
             continue
         # bf16 results: isolated one-ulp rounding flips only
         assert rel_err(got, want) <= 2.0 ** -7, name

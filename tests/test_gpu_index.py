@@ -79,8 +79,8 @@ def test_argminmax_integers_and_f16(cuda, dtype):
             pytest.skip(f"torch has no {dtype}")
         npdt, dtype = np.dtype(dtype), getattr(torch, dtype)
     else:
-        npdt = {torch.int8: np.int8, torch.int16: np.int16, torch.int32: np.int32, torch.int64: np.int64,
-                torch.uint8: np.uint8, torch.float16: np.float16}[dtype]
+        npdt = np.dtype({torch.int8: np.int8, torch.int16: np.int16, torch.int32: np.int32, torch.int64: np.int64,
+                         torch.uint8: np.uint8, torch.float16: np.float16}[dtype])
     rng = np.random.default_rng(23)
     for shape, axis in [((64, 1000), 1), ((64, 1000), 0), ((3, 200, 7), 1), ((1, 70000), 1)]:
         if npdt.kind in "iu":
