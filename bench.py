@@ -425,9 +425,10 @@ def copy_reference(mib: int, steps: int):
     """A plain device-to-device copy of `mib` MiB, `steps` times: its FETCH_SIZE /
     WRITE_SIZE counters per dispatch, divided by mib * 1024, give the factor that
     turns those counters into bytes for the kernels measured beside it.  Also
-    times the copies (HIP events; sources and destinations rotate over enough
-    buffers that the 256 MB Infinity Cache cannot serve them) and reports GB/s of
-    bytes read plus written: the copy ceiling at that size."""
+    times the copies (HIP events around back-to-back launches; sources and
+    destinations rotate over enough buffers that the 256 MB Infinity Cache cannot
+    serve them) and reports GB/s of bytes read plus written.  Below ~64 MiB the
+    per-copy launch cost from Python shows in the rate."""
     import torch
     n = mib * (1 << 20) // 4
     rot = rotation_for(2 * n * 4)
@@ -436,27 +437,15 @@ def copy_reference(mib: int, steps: int):
     for i in range(steps):
         ys[i % rot].copy_(xs[i % rot])
     torch.cuda.synchronize()
-    # Timed as graph replays of one rotation cycle, so the copies run back to back
-    # (launched one by one from Python, small copies would time the launches).
-    s = torch.cuda.Stream()
-    s.wait_stream(torch.cuda.current_stream())
-    graph = torch.cuda.CUDAGraph()
-    with torch.cuda.stream(s):
-        with torch.cuda.graph(graph, stream=s):
-            for i in range(rot):
-                ys[i].copy_(xs[i])
-    reps = max(1, steps // rot)
-    graph.replay()
-    s.synchronize()
     ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    ev0.record(s)
-    for _ in range(reps):
-        graph.replay()
-    ev1.record(s)
-    s.synchronize()
-    us = ev0.elapsed_time(ev1) * 1e3 / (reps * rot)
-    print(json.dumps({"copy_ref_mib": mib, "steps": steps, "rotation": rot, "timed_copies": reps * rot,
-                      "us_per_copy": round(us, 2), "gbs": round(2 * n * 4 / us / 1e3, 1)}))
+    ev0.record()
+    for i in range(steps):
+        ys[i % rot].copy_(xs[i % rot])
+    ev1.record()
+    torch.cuda.synchronize()
+    us = ev0.elapsed_time(ev1) * 1e3 / max(steps, 1)
+    print(json.dumps({"copy_ref_mib": mib, "steps": steps, "rotation": rot, "us_per_copy": round(us, 2),
+                      "gbs": round(2 * n * 4 / us / 1e3, 1)}))
 
 
 def main():
