@@ -1147,50 +1147,78 @@ struct Lowerer {
       return;
     }
     if (n.kind == Kind::While) {
+      // Speculative batches: cond and body run k iterations ahead on the stream
+      // (each iteration's state in its own slot of a ring of kMaxBatch + 1 state
+      // sets, each predicate in its own byte), then the k predicates come back in
+      // one copy; the state before the first false predicate is the result.  Extra
+      // iterations past the exit only compute (every kernel here is bounds-safe:
+      // clamped indices, skipped out-of-range windows), and their results are
+      // never used.  Batches grow 1, 2, 4, ... up to kMaxBatch, so a loop of N
+      // iterations reads back O(log N + N / kMaxBatch) times and runs at most
+      // about twice its body launches.  The ring's size is bounded by a byte
+      // budget for large states.
       const size_t ns = static_cast<size_t>(n.i0), ncc = static_cast<size_t>(n.i1);
-      std::vector<View> A, B;
-      for (size_t i = 0; i < ns; ++i) {
-        A.push_back(fresh(n.outs[i]));
-        B.push_back(fresh(n.outs[i]));
-        wr.push_back(A.back().slot);
-        wr.push_back(B.back().slot);
-      }
+      size_t state_bytes = 0;
+      for (size_t i = 0; i < ns; ++i) state_bytes += n.outs[i].bytes();
+      constexpr size_t kRingBudget = size_t{256} << 20;
+      int kmax = 8;
+      while (kmax > 1 && (static_cast<size_t>(kmax) + 1) * state_bytes > kRingBudget) kmax /= 2;
+      std::vector<std::vector<View>> H(kmax + 1);
+      for (int r = 0; r <= kmax; ++r)
+        for (size_t i = 0; i < ns; ++i) {
+          H[r].push_back(fresh(n.outs[i]));
+          wr.push_back(H[r].back().slot);
+        }
       Shape bs;
       bs.dtype = GHIP_DTYPE_BOOL;
+      bs.dims = {kmax};
       View pv = fresh(bs);
       wr.push_back(pv.slot);
       GHipExecutable* cond = subs[0];
       GHipExecutable* body = subs[1];
-      add_step(fmt("while (%zu state values; cond and body run from the host, one bool read per iteration)", ns), rd,
-               wr, [=](ExecState& st, GHipError* e) -> int {
-                 std::vector<void*> a = ptrs(st, A, odt, 0, ns), b = ptrs(st, B, odt, 0, ns);
+      add_step(fmt("while (%zu state values; cond and body enqueued in speculative batches of up to %d "
+                   "iterations, one predicate read per batch)", ns, kmax),
+               rd, wr, [=](ExecState& st, GHipError* e) -> int {
+                 std::vector<std::vector<void*>> h(kmax + 1);
+                 for (int r = 0; r <= kmax; ++r) h[r] = ptrs(st, H[r], odt, 0, ns);
                  for (size_t i = 0; i < ns; ++i) {
-                   const hipError_t he = hipMemcpyAsync(a[i], st.ptr(ins[i], idt[i]), ibytes[i],
+                   const hipError_t he = hipMemcpyAsync(h[0][i], st.ptr(ins[i], idt[i]), ibytes[i],
                                                         hipMemcpyDeviceToDevice, st.stream);
                    if (he != hipSuccess) return check_hip(he, e, "While: initial state");
                  }
                  const std::vector<void*> ccap = ptrs(st, ins, idt, ns, ns + ncc);
                  const std::vector<void*> bcap = ptrs(st, ins, idt, ns + ncc, nin);
-                 void* pp = st.ptr(pv, GHIP_DTYPE_BOOL);
-                 for (long it = 0;; ++it) {
-                   if (it == kMaxWhileIterations)
+                 uint8_t* pp = reinterpret_cast<uint8_t*>(st.ptr(pv, GHIP_DTYPE_BOOL));
+                 int base = 0, k = 1, last = -1;
+                 for (long done = 0; last < 0;) {
+                   if (done >= kMaxWhileIterations)
                      return set_error(e, GHIP_ERR_STATE, "While: exceeded maximum iterations (%ld)", kMaxWhileIterations);
-                   std::vector<void*> cin(a);
-                   cin.insert(cin.end(), ccap.begin(), ccap.end());
-                   int rc = run_plan(cond, cin.data(), &pp, e);
-                   if (rc != GHIP_OK) return rc;
-                   bool go = false;
-                   rc = read_bool(pp, st.stream, &go, e);
-                   if (rc != GHIP_OK) return rc;
-                   if (!go) break;
-                   std::vector<void*> bin(a);
-                   bin.insert(bin.end(), bcap.begin(), bcap.end());
-                   rc = run_plan(body, bin.data(), b.data(), e);
-                   if (rc != GHIP_OK) return rc;
-                   std::swap(a, b);
+                   for (int j = 0; j < k; ++j) {
+                     const int cur = (base + j) % (kmax + 1), nxt = (base + j + 1) % (kmax + 1);
+                     std::vector<void*> cin(h[cur]);
+                     cin.insert(cin.end(), ccap.begin(), ccap.end());
+                     void* pj = pp + j;
+                     int rc = run_plan(cond, cin.data(), &pj, e);
+                     if (rc != GHIP_OK) return rc;
+                     std::vector<void*> bin(h[cur]);
+                     bin.insert(bin.end(), bcap.begin(), bcap.end());
+                     rc = run_plan(body, bin.data(), h[nxt].data(), e);
+                     if (rc != GHIP_OK) return rc;
+                   }
+                   uint8_t hp[64];
+                   hipError_t he = hipMemcpyAsync(hp, pp, static_cast<size_t>(k), hipMemcpyDeviceToHost, st.stream);
+                   if (he == hipSuccess) he = hipStreamSynchronize(st.stream);
+                   if (he != hipSuccess) return check_hip(he, e, "While: reading the predicates");
+                   for (int j = 0; j < k && last < 0; ++j)
+                     if (!hp[j]) last = (base + j) % (kmax + 1);
+                   if (last < 0) {
+                     base = (base + k) % (kmax + 1);
+                     done += k;
+                     k = k * 2 > kmax ? kmax : k * 2;
+                   }
                  }
                  for (size_t i = 0; i < ns; ++i) {
-                   const hipError_t he = hipMemcpyAsync(st.ptr(outs[i], odt[i]), a[i], obytes[i],
+                   const hipError_t he = hipMemcpyAsync(st.ptr(outs[i], odt[i]), h[last][i], obytes[i],
                                                         hipMemcpyDeviceToDevice, st.stream);
                    if (he != hipSuccess) return check_hip(he, e, "While: final state");
                  }

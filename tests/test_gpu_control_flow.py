@@ -103,6 +103,56 @@ def test_call_named_function(be):                                 # mpsgraph_tes
     assert float(y) == 42.0
 
 
+@pytest.mark.parametrize("limit", [0, 1, 2, 3, 4, 7, 8, 9, 15, 16, 17, 100])
+def test_while_trip_counts_across_speculative_batches(be, limit):
+    """While runs cond and body in speculative batches (1, 2, 4, 8, 8, ...
+    iterations) and keeps the state before the first false predicate: every trip
+    count, including 0 and counts on either side of a batch boundary, gives
+    exactly the sequential loop's state (a counter, a running sum and a product
+    that any extra iteration would change)."""
+    def build(b, f, lim):
+        cond = f.Closure()
+        c = cond.Parameter("c", make_shape(I32))
+        cond.Parameter("s", make_shape(I32))
+        cond.Parameter("p", make_shape(F32))
+        cond.Return([cond.LessThan(c, lim)])  # lim: a captured value of the enclosing function
+        body = f.Closure()
+        c, s2, pr = (body.Parameter("c", make_shape(I32)), body.Parameter("s", make_shape(I32)),
+                     body.Parameter("p", make_shape(F32)))
+        body.Return([body.Add(c, body.Constant(i32(1))), body.Add(s2, body.Mul(c, c)),
+                     body.Mul(pr, body.Constant(np.array(1.5, np.float32)))])
+        return list(f.While(cond, body, f.Constant(i32(0)), f.Constant(i32(0)),
+                            f.Constant(np.array(1.0, np.float32))))
+    _, outs = run(be, build, [(i32(limit), make_shape(I32))])
+    assert int(outs[0]) == limit
+    assert int(outs[1]) == sum(i * i for i in range(limit))
+    p = np.float32(1.0)
+    for _ in range(limit):
+        p = np.float32(p * np.float32(1.5))
+    assert outs[2].reshape(()) == p
+
+
+def test_while_large_state_uses_a_smaller_batch_ring(be):
+    """A state too large for eight speculative copies within the ring's byte budget
+    runs with a smaller batch and the same result."""
+    n = 40 * (1 << 20) // 4  # 40 MiB of float32 state: 9 copies exceed the 256 MiB budget
+    def build(b, f, x):
+        cond = f.Closure()
+        k = cond.Parameter("k", make_shape(I32))
+        cond.Parameter("v", make_shape(F32, n))
+        cond.Return([cond.LessThan(k, cond.Constant(i32(11)))])
+        body = f.Closure()
+        k, v = body.Parameter("k", make_shape(I32)), body.Parameter("v", make_shape(F32, n))
+        body.Return([body.Add(k, body.Constant(i32(1))),
+                     body.Add(v, body.BroadcastInDim(body.ConvertDType(k, F32), make_shape(F32, n), []))])
+        return [f.While(cond, body, f.Constant(i32(0)), x)[1]]
+    x = synth.normal(77, (n,))
+    plan, outs = run(be, build, [(x, make_shape(F32, n))])
+    assert "speculative batches of up to 4 iterations" in plan, plan
+    want = x.astype(np.float64) + sum(range(11))
+    assert np.max(np.abs(outs[0] - want)) <= 1e-4
+
+
 def test_while_tensor_state_with_captures(be):
     """A loop over tensors: x <- W x / ||W x||_inf ... run k times (power iteration with
     a captured matrix and iteration count), against numpy with the same fp32 steps."""
