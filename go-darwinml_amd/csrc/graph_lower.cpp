@@ -978,7 +978,7 @@ struct Lowerer {
     int64_t lds = P * 4;
     for (int i = 0; i < nin; ++i) lds += L * dtype_size(n.outs[i].dtype);
     if (lds > 150 * 1024) {
-      fail(GHIP_ERR_UNSUPPORTED, "Sort: a row along the sort axis does not fit in one workgroup's LDS");
+      emit_sort_global(v, cbody, cres, outer, inner, L, P);
       return;
     }
     const int NT = static_cast<int>(std::min<int64_t>(1024, std::max<int64_t>(64, P / 2)));
@@ -1064,6 +1064,140 @@ struct Lowerer {
                                                             st.stream, args.data(), nullptr);
                  if (h != hipSuccess) return check_hip(h, e, "sort launch");
                  done += g;
+               }
+               return GHIP_OK;
+             });
+  }
+
+  // Sort of rows too long for one workgroup's LDS: the same bitonic network over an
+  // index array, held per row in an arena scratch buffer.  One workgroup per row;
+  // each chunk of CH indices is sorted in LDS first, then for every larger stage the
+  // exchanges across chunks run in global memory and the ones inside a chunk in LDS.
+  // The comparator reads the keys from the input rows (no copy).  The network, the
+  // tie rule (index order) and so the result are those of the LDS kernel.
+  void emit_sort_global(int v, const std::string& cbody, const std::string& cres, int64_t outer, int64_t inner,
+                        int64_t L, int64_t P) {
+    const Node n = N[v];
+    const int nin = static_cast<int>(n.i2), axis = static_cast<int>(n.i0);
+    const Shape s0 = n.outs[0];
+    const int64_t rows = outer * inner;
+    if (L > (int64_t{1} << 30)) {
+      fail(GHIP_ERR_UNSUPPORTED, "Sort: rows longer than 2^30 elements");
+      return;
+    }
+    const int64_t CH = std::min<int64_t>(P, 16384);  // indices per LDS chunk (64 KiB)
+    const int NT = 1024;
+    // Rows per launch: index scratch of at most 256 MiB.
+    const int64_t batch = std::max<int64_t>(1, std::min<int64_t>(rows, (int64_t{256} << 20) / (P * 4)));
+    std::ostringstream src;
+    src << kRtcPrelude << "extern \"C\" __global__ void __launch_bounds__(" << NT << ") sort_rows_global(\n";
+    for (int i = 0; i < nin; ++i) src << "    const void* __restrict__ in" << i << ",\n";
+    for (int i = 0; i < nin; ++i) src << "    void* __restrict__ out" << i << ",\n";
+    for (size_t k = nin; k < n.in.size(); ++k) src << "    const void* __restrict__ cap" << (k - nin) << ",\n";
+    src << "    int* __restrict__ ixg, long long inner, long long row0) {\n"
+        << "  __shared__ int ix[" << CH << "];\n"
+        << "  const long long row = row0 + blockIdx.x, o = row / inner, j = row % inner;\n"
+        << "  const long long base = o * " << L << "LL * inner + j;\n"
+        << "  int* g = ixg + (long long)blockIdx.x * " << P << "LL;\n";
+    for (size_t k = nin; k < n.in.size(); ++k) {
+      const int dt = N[n.in[k]].shape.dtype;
+      src << "  const " << ctype(dt) << " c" << (k - nin) << " = "
+          << load_expr(dt, "((const " + stype(dt) + "*)cap" + std::to_string(k - nin) + ")[0]") << ";\n";
+    }
+    src << "  auto cmp = [&](int a, int b) -> bool {\n";
+    for (int i = 0; i < nin; ++i) {
+      const int dt = n.outs[i].dtype;
+      const std::string arr = "((const " + stype(dt) + "*)in" + std::to_string(i) + ")";
+      src << "    const " << ctype(dt) << " p" << 2 * i << " = " << load_expr(dt, arr + "[base + (long long)a * inner]")
+          << ";\n"
+          << "    const " << ctype(dt) << " p" << 2 * i + 1 << " = " << load_expr(dt, arr + "[base + (long long)b * inner]")
+          << ";\n";
+    }
+    src << cbody << "    return " << cres << ";\n  };\n"
+        << "  auto lt = [&](int a, int b) -> bool {\n"
+        << "    if (a >= " << L << ") return false;\n    if (b >= " << L << ") return true;\n"
+        << "    if (cmp(a, b)) return true;\n    if (cmp(b, a)) return false;\n    return a < b;\n  };\n"
+        // exchange of the pair at positions (a, a + jj) of stage k, a taken in the whole row
+        << "  auto local = [&](int c, int k, int jtop) {\n"  // stages jj = jtop .. 1 of stage k inside chunk c (in LDS)
+        << "    for (int jj = jtop; jj > 0; jj >>= 1) {\n"
+        << "      for (int t = threadIdx.x; t < " << CH / 2 << "; t += " << NT << ") {\n"
+        << "        const int a = ((t & ~(jj - 1)) << 1) | (t & (jj - 1)), b = a + jj;\n"
+        << "        const int ga = c * " << CH << " + a;\n"
+        << "        const int xa = ix[a], xb = ix[b];\n"
+        << "        if ((ga & k) == 0 ? lt(xb, xa) : lt(xa, xb)) { ix[a] = xb; ix[b] = xa; }\n"
+        << "      }\n      __syncthreads();\n    }\n  };\n"
+        << "  for (int c = 0; c < " << P / CH << "; ++c) {\n"
+        << "    for (int t = threadIdx.x; t < " << CH << "; t += " << NT << ") ix[t] = c * " << CH << " + t;\n"
+        << "    __syncthreads();\n"
+        << "    for (int k = 2; k <= " << CH << "; k <<= 1) local(c, k, k >> 1);\n"
+        << "    for (int t = threadIdx.x; t < " << CH << "; t += " << NT << ") g[c * " << CH << " + t] = ix[t];\n"
+        << "    __syncthreads();\n  }\n"
+        << "  for (int k = " << 2 * CH << "; k <= " << P << "; k <<= 1) {\n"
+        << "    for (int jj = k >> 1; jj >= " << CH << "; jj >>= 1) {\n"
+        << "      for (int t = threadIdx.x; t < " << P / 2 << "; t += " << NT << ") {\n"
+        << "        const int a = ((t & ~(jj - 1)) << 1) | (t & (jj - 1)), b = a + jj;\n"
+        << "        const int xa = g[a], xb = g[b];\n"
+        << "        if ((a & k) == 0 ? lt(xb, xa) : lt(xa, xb)) { g[a] = xb; g[b] = xa; }\n"
+        << "      }\n      __syncthreads();\n    }\n"
+        << "    for (int c = 0; c < " << P / CH << "; ++c) {\n"
+        << "      for (int t = threadIdx.x; t < " << CH << "; t += " << NT << ") ix[t] = g[c * " << CH << " + t];\n"
+        << "      __syncthreads();\n"
+        << "      local(c, k, " << CH / 2 << ");\n"
+        << "      for (int t = threadIdx.x; t < " << CH << "; t += " << NT << ") g[c * " << CH << " + t] = ix[t];\n"
+        << "      __syncthreads();\n    }\n  }\n"
+        << "  for (int t = threadIdx.x; t < " << L << "; t += " << NT << ") {\n"
+        // padding indices sort last, so g[t] < L; the clamp only keeps reads in bounds
+        << "    const long long s = g[t] < " << L << " ? g[t] : " << L - 1 << ";\n";
+    for (int i = 0; i < nin; ++i)
+      src << "    ((" << stype(n.outs[i].dtype) << "*)out" << i << ")[base + t * inner] = ((const "
+          << stype(n.outs[i].dtype) << "*)in" << i << ")[base + s * inner];\n";
+    src << "  }\n}\n";
+    RtcKernel kern;
+    if (rtc_get(be, src.str(), "sort_rows_global", &kern, err) != GHIP_OK) {
+      failed = true;
+      return;
+    }
+    std::vector<View> ins, outs;
+    std::vector<int> idt, odt, rd, wr;
+    for (int o : n.in) {
+      View w = materialize(get(o), N[o].shape, "(Sort input)");
+      if (failed) return;
+      ins.push_back(w);
+      idt.push_back(N[o].shape.dtype);
+      rd.push_back(w.slot);
+    }
+    for (const Shape& sh : n.outs) {
+      outs.push_back(fresh(sh));
+      odt.push_back(sh.dtype);
+      wr.push_back(outs.back().slot);
+    }
+    Shape ish;
+    ish.dtype = GHIP_DTYPE_INT32;
+    ish.dims = {batch, P};
+    const View scratch = fresh(ish);
+    wr.push_back(scratch.slot);
+    cf_out[v] = outs;
+    add_step(fmt("sort_rows_global %s axis=%d inputs=%d (comparator compiled in; bitonic over an index array in "
+                 "global memory, chunks of %lld in LDS, stable)",
+                 s0.str().c_str(), axis, nin, static_cast<long long>(CH)),
+             rd, wr, [=](ExecState& st, GHipError* e) -> int {
+               if (rows == 0 || L == 0) return GHIP_OK;
+               std::vector<void*> ptr;
+               for (int i = 0; i < nin; ++i) ptr.push_back(st.ptr(ins[i], idt[i]));
+               for (int i = 0; i < nin; ++i) ptr.push_back(st.ptr(outs[i], odt[i]));
+               for (size_t k = nin; k < ins.size(); ++k) ptr.push_back(st.ptr(ins[k], idt[k]));
+               void* ixg = st.ptr(scratch, GHIP_DTYPE_INT32);
+               long long in_ = inner, r0 = 0;
+               std::vector<void*> args;
+               for (auto& q : ptr) args.push_back(&q);
+               args.push_back(&ixg);
+               args.push_back(&in_);
+               args.push_back(&r0);
+               for (r0 = 0; r0 < rows; r0 += batch) {
+                 const int64_t gsz = std::min<int64_t>(rows - r0, batch);
+                 const hipError_t h = hipModuleLaunchKernel(kern.func, static_cast<unsigned>(gsz), 1, 1, NT, 1, 1, 0,
+                                                            st.stream, args.data(), nullptr);
+                 if (h != hipSuccess) return check_hip(h, e, "sort launch");
                }
                return GHIP_OK;
              });

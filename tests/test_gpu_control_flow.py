@@ -297,6 +297,56 @@ def test_sort_bf16_lexicographic_with_captured_scalar(be):
         assert np.array_equal(yb[r], bk[r][order])
 
 
+def test_sort_rows_longer_than_lds(be):
+    """Rows of 40000 keys (an index network of 65536: four 16384-index chunks sorted in
+    LDS, then stages 32768 and 65536 with exchanges across chunks in global memory),
+    keys with many ties plus an int32 payload: equal to numpy's stable argsort, both
+    ascending along the last axis and descending along a strided middle axis."""
+    rng = np.random.default_rng(21)
+    L = 40000
+    keys = rng.integers(0, 500, (3, L)).astype(np.float32)
+    payload = np.broadcast_to(np.arange(L, dtype=np.int32)[None, :], (3, L)).copy()
+
+    def build(b, f, k, p):
+        return f.Sort(_comparator(f, [F32, I32], lambda c, q: c.LessThan(q[0], q[1])), 1, True, k, p)
+    plan, (ks, ps) = run(be, build, [(keys, make_shape(F32, 3, L)), (payload, make_shape(I32, 3, L))])
+    assert "sort_rows_global" in plan, plan
+    order = np.argsort(keys, axis=1, kind="stable")
+    assert np.array_equal(ks, np.take_along_axis(keys, order, 1))
+    assert np.array_equal(ps, np.take_along_axis(payload, order, 1))
+
+    x = rng.standard_normal((2, 20001, 3)).astype(np.float32)
+    x[0, ::7, 1] = 0.5                      # a run of ties inside one strided row
+
+    def build_desc(b, f, xx):
+        return f.Sort(_comparator(f, [F32], lambda c, q: c.GreaterThan(q[0], q[1])), 1, True, xx)
+    plan, (y,) = run(be, build_desc, [(x, make_shape(F32, 2, 20001, 3))])
+    assert "sort_rows_global" in plan
+    assert np.array_equal(y, np.take_along_axis(x, np.argsort(-x, axis=1, kind="stable"), 1))
+
+
+def test_sort_wide_keys_take_the_global_path(be):
+    """Three operands of 8000 (int64, int64, int32: 160 KB of keys per row) do not fit
+    one workgroup's LDS with the index array; the global-memory network with a single
+    LDS chunk sorts them lexicographically like numpy.lexsort (ties by index)."""
+    rng = np.random.default_rng(22)
+    a = rng.integers(-3, 3, (2, 8000)).astype(np.int64)
+    bk = rng.integers(0, 1 << 40, (2, 8000)).astype(np.int64)
+    c = np.broadcast_to(np.arange(8000, dtype=np.int32), (2, 8000)).copy()
+
+    def build(b, f, aa, bb, cc):
+        def rule(k, q):
+            return k.LogicalOr(k.LessThan(q[0], q[1]), k.LogicalAnd(k.Equal(q[0], q[1]), k.LessThan(q[2], q[3])))
+        return f.Sort(_comparator(f, [dtypes.Int64, dtypes.Int64, I32], rule), 1, True, aa, bb, cc)
+    plan, (ya, yb, yc) = run(be, build, [(a, make_shape(dtypes.Int64, 2, 8000)), (bk, make_shape(dtypes.Int64, 2, 8000)),
+                                         (c, make_shape(I32, 2, 8000))])
+    assert "sort_rows_global" in plan, plan
+    for r in range(2):
+        order = np.lexsort((np.arange(8000), bk[r], a[r]))
+        assert np.array_equal(ya[r], a[r][order]) and np.array_equal(yb[r], bk[r][order])
+        assert np.array_equal(yc[r], c[r][order])
+
+
 def test_sort_errors(be):
     b = be.Builder("se")
     f = b.Main()

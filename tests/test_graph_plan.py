@@ -368,6 +368,29 @@ def test_control_flow_plans_and_errors(be):
     assert "while (2 state values" in plan and "call callee" in plan, plan
 
 
+def test_sort_picks_lds_or_global_network(be):
+    """Rows whose keys and index array fit one workgroup's LDS use the LDS kernel;
+    longer rows (or wide multi-operand keys) the global-memory network; both
+    generated kernels compile (hipRTC runs on the plan-only backend too)."""
+    def plan_of(dims, dts):
+        b = be.Builder("sort")
+        f = b.Main()
+        xs = [f.Parameter(f"x{i}", make_shape(dt, *dims)) for i, dt in enumerate(dts)]
+        c = f.Closure()
+        ps = []
+        for i, dt in enumerate(dts):
+            ps += [c.Parameter(f"l{i}", make_shape(dt)), c.Parameter(f"r{i}", make_shape(dt))]
+        c.Return([c.LessThan(ps[0], ps[1])])
+        f.Return(f.Sort(c, len(dims) - 1, True, *xs))
+        return b.Compile().Plan()
+    assert "sort_rows " in plan_of((4, 16384), [F32])                     # 64 KiB keys + 64 KiB indices
+    p = plan_of((4, 16385), [F32])
+    assert "sort_rows_global" in p and "chunks of 16384" in p, p
+    p = plan_of((2, 1000000), [F32, dtypes.Int32])
+    assert "sort_rows_global" in p, p
+    assert "sort_rows_global" in plan_of((2, 8000), [dtypes.Int64, dtypes.Int64, dtypes.Int32])
+
+
 # The reference's declared ops (capabilities.go:17-150) minus the ones this
 # backend does not build (CNN / batch-norm / RNG ops, outside the hot path).
 _REFERENCE_OPS = set("""Parameter Constant Abs Neg Sqrt Rsqrt Exp Expm1 Log Log1p Sin Cos Tanh
