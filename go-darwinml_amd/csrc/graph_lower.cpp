@@ -50,7 +50,14 @@ struct Fusion {
 const char kRtcPrelude[] = R"(typedef unsigned short u16;
 __device__ __forceinline__ float bf2f(u16 b) { return __uint_as_float(((unsigned)b) << 16); }
 __device__ __forceinline__ u16 f2bf(float f) { return __builtin_bit_cast(u16, (__bf16)f); }
-__device__ __forceinline__ float rbf(float f) { return bf2f(f2bf(f)); }
+// f rounded to bf16 and widened back, in one v_cvt_pk_bf16_f32: the pair (0, f)
+// converts to the 32-bit word (bf16(f) << 16) | bf16(0), which is that float.
+typedef float rbf_f2 __attribute__((ext_vector_type(2)));
+typedef __bf16 rbf_b2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ float rbf(float f) {
+  const rbf_f2 v = {0.0f, f};
+  return __builtin_bit_cast(float, __builtin_convertvector(v, rbf_b2));
+}
 __device__ __forceinline__ float rhf(float f) { return (float)(_Float16)f; }
 // exp / logistic / tanh for ops whose result is rounded to bf16 or f16: the
 // hardware exp2 and reciprocal (relative error below 1e-5 over the whole range,
