@@ -67,8 +67,12 @@ __device__ __forceinline__ float hexp(float x) { return __builtin_amdgcn_exp2f(x
 __device__ __forceinline__ float hsigmoid(float x) { return __builtin_amdgcn_rcpf(1.0f + hexp(-x)); }
 __device__ __forceinline__ float htanh(float x) {
   const float ax = __builtin_fabsf(x), p = x * x;
-  const float small = x + x * p * (-0.33333333f + p * 0.13333333f);  // |x| < 1/16: odd series
-  const float big = __builtin_copysignf(1.0f - 2.0f * __builtin_amdgcn_rcpf(hexp(2.0f * ax) + 1.0f), x);
+  // |x| < 1/16: the odd series x - x^3/3 + 2x^5/15; else 1 - 2 / (e^(2|x|) + 1) with
+  // e^(2|x|) = exp2(|x| * 2 log2(e)).  Explicit FMAs (generated code compiles without
+  // contraction): 12 instructions.
+  const float small = __builtin_fmaf(x * p, __builtin_fmaf(p, 0.13333333f, -0.33333333f), x);
+  const float e2 = __builtin_amdgcn_exp2f(ax * 2.8853900817779268f);
+  const float big = __builtin_copysignf(__builtin_fmaf(-2.0f, __builtin_amdgcn_rcpf(e2 + 1.0f), 1.0f), x);
   return ax < 0.0625f ? small : big;
 }
 template <typename T> __device__ __forceinline__ T fmax_nan(T a, T b) { return (a > b || a != a) ? a : b; }
