@@ -147,12 +147,14 @@ __device__ __forceinline__ void dma16(i32x4_t rsrc, uint32_t la, uint32_t voff) 
 // Wave-instruction i of a wave fills LDS bytes [blk*1024, blk*1024 + 1024),
 // blk = wave * kPerWave + i; lane l writes bytes l*16 .. l*16+15 of that block, so
 // the swizzle is applied by choosing which global chunk each lane fetches.
-template <int R, bool KC, int NW>
+// BK: k-depth of the tile (64; MN-contiguous tiles may also be 32 deep).
+template <int R, bool KC, int NW, int BK = kBK>
 struct OperandTile {
-  static constexpr int kInstr = R * kBK * 2 / 1024;
+  static_assert(BK == kBK || (!KC && BK == 32), "32-deep tiles are MN-contiguous only");
+  static constexpr int kInstr = R * BK * 2 / 1024;
   static constexpr int kPerWave = kInstr / NW;
   static_assert(kInstr % NW == 0 && kPerWave % 2 == 0, "tile must split evenly over waves");
-  static constexpr int kCPR = KC ? kBK / 8 : R / 8;  // 16-byte chunks per LDS row
+  static constexpr int kCPR = KC ? BK / 8 : R / 8;  // 16-byte chunks per LDS row
   static constexpr int kRPI = 64 / kCPR;             // LDS rows per instruction
   static_assert(KC || R >= 128, "MN-major tiles need >= 16 chunks per LDS row");
 
@@ -683,6 +685,177 @@ __device__ __forceinline__ void gemm_bf16_body4(const GemmParams& p, const Epi& 
     }
   };
   if (mn_full && (p.K % kBK) == 0) run(BoolC<true>{});
+  else run(BoolC<false>{});
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+
+  tile_epilogue<BM, BN, WM, WN, 1>(p, epi, smem, acc, bb, m0, n0, mn_full, lane, wm, wn);
+}
+
+// 4-wave core for both operands MN-contiguous (A [K, M], B [K, N] in memory, e.g.
+// a weight gradient X^T . dY): the same 256 x 256 tile, 2 x 2 waves and MFMA / LDS
+// read order as gemm_bf16_body4, with 32-deep k-tiles in four LDS stages (128 KiB).
+// At the barrier that retires tile kt its stage takes tile kt+4, so three tiles of
+// MFMA work cover a load; the steady state (every tile has a successor and a tile
+// four ahead) runs without runtime branches.  Measured 5% faster than the 64-deep,
+// two-stage core for this layout (K-contiguous rows would fetch half cache lines per
+// 32-deep tile, which is why the other layouts keep 64).  Bit-identical to the other
+// cores: same MFMA, same k order per accumulator.
+template <class Epi, bool F16 = false>
+__device__ __forceinline__ void gemm_bf16_body4mn(const GemmParams& p, const Epi& epi) {
+  constexpr int BM = 256, BN = 256, WM = 2, WN = 2, BK = 32, S = 4;
+  constexpr int NW = WM * WN;
+  constexpr int TM = BM / WM, TN = BN / WN;
+  constexpr int FM = TM / 32, FN = TN / 32;
+  constexpr int NS = BK / 16;
+  using TA = OperandTile<BM, false, NW, BK>;
+  using TB = OperandTile<BN, false, NW, BK>;
+  constexpr int ND = TA::kPerWave + TB::kPerWave;  // loads per wave per k-tile
+  constexpr int kSA = BM * BK * 2, kSB = BN * BK * 2;  // bytes per stage
+  constexpr int kLdsBytes = S * (kSA + kSB);
+  __shared__ __attribute__((aligned(1024))) uint16_t smem[kLdsBytes / 2];
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wm = wave / WN, wn = wave % WN;
+
+  int64_t bb;
+  int tm, tn;
+  map_tile(blockIdx.x, p.batch * p.tiles_m * p.tiles_n, p.tiles_m, p.tiles_n, bb, tm, tn);
+  const int64_t m0 = static_cast<int64_t>(tm) * BM, n0 = static_cast<int64_t>(tn) * BN;
+  const uint16_t* A0 = static_cast<const uint16_t*>(p.a) + bb * p.sa_b + m0 * p.sa_m;
+  const uint16_t* B0 = static_cast<const uint16_t*>(p.b) + bb * p.sb_b + n0 * p.sb_n;
+  const uint32_t a_left0 = p.a_extent - static_cast<uint32_t>(m0 * p.sa_m * 2);
+  const uint32_t b_left0 = p.b_extent - static_cast<uint32_t>(n0 * p.sb_n * 2);
+
+  TA ta;
+  TB tb;
+  ta.init(wave, lane, p.sa_m, p.sa_k, p.M - m0);
+  tb.init(wave, lane, p.sb_n, p.sb_k, p.N - n0);
+  const bool mn_full = m0 + BM <= p.M && n0 + BN <= p.N;
+  const int KT = static_cast<int>((p.K + BK - 1) / BK);
+  const uint32_t lds_a = static_cast<uint32_t>(reinterpret_cast<uint64_t>((GHIP_LDS void*)smem));
+  const uint32_t lds_b = lds_a + S * kSA;
+  const uint16_t* sA = smem;
+  const uint16_t* sB = smem + S * kSA / 2;
+
+  f32x16_t acc[FM][FN];
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
+
+  // Fragments [buffer][block][half], two transpose reads per fragment.
+  bf16x4_t fa[2][FM][2], fb[2][FN][2];
+  constexpr int NR = 2 * (FM + FN);  // LDS reads per k16 step
+  auto read_op = [&](int st, int s, int nb, int r) {
+    const int blk = r / 4, q = r % 4;
+    if (q < 2) fa[nb][blk][q] = frag_mn_half<BM>(sA + st * (kSA / 2), wm * TM + blk * 32, s, lane, q);
+    else fb[nb][blk][q - 2] = frag_mn_half<BN>(sB + st * (kSB / 2), wn * TN + blk * 32, s, lane, q - 2);
+  };
+  auto mfma_op = [&](int b, int k) {
+    constexpr int ord[16][2] = {{0, 0}, {0, 1}, {1, 0}, {1, 1}, {0, 2}, {1, 2}, {2, 0}, {2, 1},
+                                {2, 2}, {0, 3}, {1, 3}, {2, 3}, {3, 0}, {3, 1}, {3, 2}, {3, 3}};
+    const int i = ord[k][0], j = ord[k][1];
+    const bf16x8_t av = __builtin_shufflevector(fa[b][i][0], fa[b][i][1], 0, 1, 2, 3, 4, 5, 6, 7);
+    const bf16x8_t bv = __builtin_shufflevector(fb[b][j][0], fb[b][j][1], 0, 1, 2, 3, 4, 5, 6, 7);
+    acc[i][j] = mma16<F16>(bv, av, acc[i][j]);
+  };
+  // Wait until at most n k-tiles of this wave's loads are in flight (n wave-uniform).
+  auto wait_tiles = [&](int n) {
+    if (n >= 2) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * ND) : "memory");
+    else if (n == 1) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(ND) : "memory");
+    else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  };
+
+  auto run = [&](auto full_c) {
+    constexpr bool FULL = decltype(full_c)::value;
+    auto dma = [&](int kt, int st, int d) {
+      const int64_t k0 = static_cast<int64_t>(kt) * BK;
+      const int k_left = static_cast<int>(p.K - k0 < BK ? p.K - k0 : BK);
+      if (d < TA::kPerWave) {
+        const i32x4_t ra = make_rsrc(A0 + k0 * p.sa_k, a_left0 - static_cast<uint32_t>(k0 * p.sa_k * 2));
+        ta.template issue_one<FULL>(ra, lds_a + st * kSA, wave, lane, k_left, d);
+      } else {
+        const i32x4_t rb = make_rsrc(B0 + k0 * p.sb_k, b_left0 - static_cast<uint32_t>(k0 * p.sb_k * 2));
+        tb.template issue_one<FULL>(rb, lds_b + st * kSB, wave, lane, k_left, d - TA::kPerWave);
+      }
+    };
+    // Prologue: tiles 0 .. S-1 in flight, wait for tile 0.
+#pragma unroll
+    for (int t = 0; t < S; ++t)
+      if (t < KT) {
+#pragma unroll
+        for (int d = 0; d < ND; ++d) dma(t, t, d);
+      }
+    wait_tiles(min(S, KT) - 1);
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < NR; ++r) read_op(0, 0, 0, r);
+
+    // Tile kt in stage ST; STEADY: tiles kt+1 and kt+S exist (no runtime checks).
+    auto tile = [&](int kt, auto st_c, auto steady_c) {
+      constexpr int ST = decltype(st_c)::value;
+      constexpr int SN = (ST + 1) % S;
+      constexpr bool STEADY = decltype(steady_c)::value;
+      const bool nx = STEADY || kt + 1 < KT, dm = STEADY || kt + S < KT;
+#pragma unroll
+      for (int s = 0; s < NS; ++s) {
+        const int b = s & 1;
+        if (s + 1 < NS) {
+#pragma unroll
+          for (int k = 0; k < 16; ++k) {
+            mfma_op(b, k);
+            if (k < NR) read_op(ST, s + 1, b ^ 1, k);
+            sched_fence();
+          }
+        } else {
+#pragma unroll
+          for (int k = 0; k < 8; ++k) {
+            mfma_op(b, k);
+            sched_fence();
+          }
+          // Tile kt+1 has landed (tiles kt+2 .. kt+S-1 may still be in flight) and
+          // every wave is done reading stage ST, so tile kt+S may refill it.
+          if (nx) {
+            if constexpr (STEADY) asm volatile("s_waitcnt vmcnt(%0)" ::"n"((S - 2) * ND) : "memory");
+            else wait_tiles(min(S - 2, KT - kt - 2));
+            __syncthreads();
+          }
+          sched_fence();
+#pragma unroll
+          for (int k = 8; k < 16; ++k) {
+            mfma_op(b, k);
+            const int x = k - 8;
+            if (dm) {
+#pragma unroll
+              for (int d = x * ND / 8; d < (x + 1) * ND / 8; ++d) dma(kt + S, ST, d);
+            }
+            if (nx) {
+#pragma unroll
+              for (int r = x * NR / 8; r < (x + 1) * NR / 8; ++r) read_op(SN, 0, b ^ 1, r);
+            }
+            sched_fence();
+          }
+        }
+      }
+    };
+    int kt = 0;
+    for (; kt + 2 * S - 1 < KT; kt += S) {
+      tile(kt, IntC<0>{}, BoolC<true>{});
+      tile(kt + 1, IntC<1>{}, BoolC<true>{});
+      tile(kt + 2, IntC<2>{}, BoolC<true>{});
+      tile(kt + 3, IntC<3>{}, BoolC<true>{});
+    }
+    for (; kt < KT; kt += S) {
+      tile(kt, IntC<0>{}, BoolC<false>{});
+      if (kt + 1 < KT) tile(kt + 1, IntC<1>{}, BoolC<false>{});
+      if (kt + 2 < KT) tile(kt + 2, IntC<2>{}, BoolC<false>{});
+      if (kt + 3 < KT) tile(kt + 3, IntC<3>{}, BoolC<false>{});
+    }
+  };
+  if (mn_full && (p.K % BK) == 0) run(BoolC<true>{});
   else run(BoolC<false>{});
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 

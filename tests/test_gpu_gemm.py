@@ -123,6 +123,27 @@ def test_16bit_large_tiles_ragged(cuda, a_t, b_t, dt):
     assert rel_err(e32, orc.dot_general(a, [2], [0], np.ascontiguousarray(b[:, :, 2048:]), [1], [0])) <= 1e-4
 
 
+@pytest.mark.parametrize("K", [1024, 1000])
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])
+def test_mn_major_core_matches_k_major_core(cuda, K, dt):
+    """Both operands MN-contiguous (a weight-gradient layout) run the 32-deep,
+    four-stage core; the same values K-contiguous run the 64-deep core.  Same MFMA,
+    same k order per accumulator: bit-identical products, for a K that fills whole
+    k-tiles (steady-state loop) and one that does not, 16-bit and fp32 outputs; and
+    sampled entries against fp64."""
+    ta_k = synth.normal_device(3601, (2, 2048, K), std=0.125, device=cuda, dtype=dt)
+    tb_k = synth.normal_device(3602, (2, K, 2048), std=0.125, device=cuda, dtype=dt).transpose(1, 2).contiguous().transpose(1, 2)
+    ta_mn = ta_k.transpose(1, 2).contiguous().transpose(1, 2)   # [2, 2048, K] with unit M stride
+    tb_mn = tb_k.contiguous()                                   # [2, K, 2048] row-major: unit N stride
+    assert ta_mn.stride(1) == 1 and tb_mn.stride(2) == 1 and ta_k.stride(2) == 1 and tb_k.stride(1) == 1
+    for out_dtype in (dt, torch.float32):
+        c_mn = ops.gemm(ta_mn, tb_mn, out_dtype=out_dtype)
+        c_k = ops.gemm(ta_k, tb_k, out_dtype=out_dtype)
+        assert torch.equal(c_mn, c_k)
+    got, ref = _sampled_check(ta_mn, tb_mn, c_mn, seed=13)
+    assert rel_err(got, ref) <= 1e-4
+
+
 @pytest.mark.parametrize("shape", SHAPES)
 def test_f16_layouts(cuda, shape):
     """f16 DotGeneral (the f16 MFMA) on the small-tile cores and the generic path."""
