@@ -2621,7 +2621,11 @@ View Lowerer::emit_gemm_epilogue(int v, const std::vector<int>& mem, bool* fused
       << ";\n  }\n};\n}  // namespace ghip\n";
   src << "extern \"C\" __global__ void __launch_bounds__(" << nt << ", 1) gemm_epilogue(ghip::GemmParams p, ghip::EpiArgs a) {\n"
       << "  const ghip::GenEpi epi{a};\n";
-  if (four_wave)
+  if (four_wave && ma && !mb)
+    src << "  ghip::gemm_bf16_body4km(p, epi);\n}\n";
+  else if (four_wave && !ma && !mb)
+    src << "  ghip::gemm_bf16_body4mn(p, epi);\n}\n";
+  else if (four_wave)
     src << "  ghip::gemm_bf16_body4<" << (ma ? "true" : "false") << ", " << (mb ? "true" : "false") << ">(p, epi);\n}\n";
   else
     src << "  ghip::gemm_bf16_body<" << BM << ", " << BN << ", " << WM << ", " << WN << ", " << (ma ? "true" : "false") << ", "
