@@ -309,6 +309,18 @@ def test_fused_dense_and_qkv_plans(be):
         f.FusedGelu(f.Parameter("i", make_shape(dtypes.Int32, 3)), False)
 
 
+def test_epilogue_core_follows_epilogue_weight(be):
+    """Large products pick the 8-wave GEMM core when the fused epilogue is VALU-heavy
+    (FusedDense + tanh-GELU: a transcendental in a 10-op chain) and the 4-wave core
+    for a light one (a residual add)."""
+    gelu = _plan(be, lambda f, x, w, b: [f.FusedDense(x, w, b, 1)],
+                 [make_shape(BF16, 8, 1024, 2048), make_shape(BF16, 2048, 8192), make_shape(BF16, 8192)])
+    assert "gemm_batched+epilogue" in gelu and "waves=8" in gelu, gelu
+    resid = _plan(be, lambda f, x, w, r: [f.Add(f.DotGeneral(x, [2], [], w, [0], []), r)],
+                  [make_shape(BF16, 8, 1024, 2048), make_shape(BF16, 2048, 2048), make_shape(BF16, 8, 1024, 2048)])
+    assert "gemm_batched+epilogue" in resid and "waves=4" in resid, resid
+
+
 def test_dynamic_slice_and_scatter_shapes_and_errors(be):
     f = be.Builder("ds").Main()
     x = f.Parameter("x", make_shape(F32, 5, 6))
