@@ -2578,8 +2578,11 @@ View Lowerer::emit_gemm_epilogue(int v, const std::vector<int>& mem, bool* fused
       valu_weight += 6;
   }
   const bool heavy_epilogue = valu_weight >= 8;
+  // A K-contiguous, B MN-contiguous: the 8-wave 32-deep core for any epilogue.
+  bool eight_km = false;
   if (NB == 1) {
-    if (d.M >= 256 && d.N >= 256 && t256 >= 128 && heavy_epilogue) BM = 256, BN = 256, WM = 2, WN = 4;
+    if (d.M >= 256 && d.N >= 256 && t256 >= 128 && ma && !mb) BM = 256, BN = 256, WM = 2, WN = 4, eight_km = true;
+    else if (d.M >= 256 && d.N >= 256 && t256 >= 128 && heavy_epilogue) BM = 256, BN = 256, WM = 2, WN = 4;
     else if (d.M >= 256 && d.N >= 256 && t256 >= 128) BM = 256, BN = 256, WM = 2, WN = 2, four_wave = true;
     else if (d.M >= 256 && d.N >= 128) BM = 256, BN = 128, WM = 2, WN = 2;
   } else if (d.M >= 256 && d.N >= 128) {
@@ -2638,8 +2641,8 @@ View Lowerer::emit_gemm_epilogue(int v, const std::vector<int>& mem, bool* fused
       << ";\n  }\n};\n}  // namespace ghip\n";
   src << "extern \"C\" __global__ void __launch_bounds__(" << nt << ", 1) gemm_epilogue(ghip::GemmParams p, ghip::EpiArgs a) {\n"
       << "  const ghip::GenEpi epi{a};\n";
-  if (four_wave && ma && !mb)
-    src << "  ghip::gemm_bf16_body4km(p, epi);\n}\n";
+  if (eight_km)
+    src << "  ghip::gemm_bf16_body8km(p, epi);\n}\n";
   else if (four_wave && !ma && !mb)
     src << "  ghip::gemm_bf16_body4mn(p, epi);\n}\n";
   else if (four_wave)

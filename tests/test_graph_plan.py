@@ -309,16 +309,25 @@ def test_fused_dense_and_qkv_plans(be):
         f.FusedGelu(f.Parameter("i", make_shape(dtypes.Int32, 3)), False)
 
 
-def test_epilogue_core_follows_epilogue_weight(be):
-    """Large products pick the 8-wave GEMM core when the fused epilogue is VALU-heavy
-    (FusedDense + tanh-GELU: a transcendental in a 10-op chain) and the 4-wave core
-    for a light one (a residual add)."""
-    gelu = _plan(be, lambda f, x, w, b: [f.FusedDense(x, w, b, 1)],
-                 [make_shape(BF16, 8, 1024, 2048), make_shape(BF16, 2048, 8192), make_shape(BF16, 8192)])
+def test_epilogue_core_follows_layout_and_epilogue_weight(be):
+    """Large products with A K-contiguous and B N-contiguous (x . W, the DotGeneral
+    config's layout) run the 8-wave 32-deep core whatever the epilogue; other layouts
+    pick the 8-wave core when the fused epilogue is VALU-heavy (tanh-GELU: a
+    transcendental in a 10-op chain) and the 4-wave core for a light one (a residual
+    add)."""
+    x = make_shape(BF16, 8, 1024, 2048)
+    gelu = _plan(be, lambda f, xx, w, b: [f.FusedDense(xx, w, b, 1)], [x, make_shape(BF16, 2048, 8192), make_shape(BF16, 8192)])
     assert "gemm_batched+epilogue" in gelu and "waves=8" in gelu, gelu
-    resid = _plan(be, lambda f, x, w, r: [f.Add(f.DotGeneral(x, [2], [], w, [0], []), r)],
-                  [make_shape(BF16, 8, 1024, 2048), make_shape(BF16, 2048, 2048), make_shape(BF16, 8, 1024, 2048)])
-    assert "gemm_batched+epilogue" in resid and "waves=4" in resid, resid
+    resid = _plan(be, lambda f, xx, w, r: [f.Add(f.DotGeneral(xx, [2], [], w, [0], []), r)],
+                  [x, make_shape(BF16, 2048, 2048), x])
+    assert "gemm_batched+epilogue" in resid and "waves=8" in resid, resid
+    # W stored [N, K] (x . W^T): B K-contiguous
+    resid_t = _plan(be, lambda f, xx, w, r: [f.Add(f.DotGeneral(xx, [2], [], w, [1], []), r)],
+                    [x, make_shape(BF16, 2048, 2048), x])
+    assert "gemm_batched+epilogue" in resid_t and "waves=4" in resid_t, resid_t
+    gelu_t = _plan(be, lambda f, xx, w: [f.FusedGelu(f.DotGeneral(xx, [2], [], w, [1], []), False)],
+                   [x, make_shape(BF16, 8192, 2048)])
+    assert "gemm_batched+epilogue" in gelu_t and "waves=8" in gelu_t, gelu_t
 
 
 def test_dynamic_slice_and_scatter_shapes_and_errors(be):
