@@ -153,7 +153,9 @@ struct OperandTile {
   static_assert(BK == kBK || (!KC && BK == 32), "32-deep tiles are MN-contiguous only");
   static constexpr int kInstr = R * BK * 2 / 1024;
   static constexpr int kPerWave = kInstr / NW;
-  static_assert(kInstr % NW == 0 && kPerWave % 2 == 0, "tile must split evenly over waves");
+  // An even share repeats the swizzle every two instructions; a share of one uses
+  // voff[0] alone.
+  static_assert(kInstr % NW == 0 && (kPerWave % 2 == 0 || kPerWave == 1), "tile must split evenly over waves");
   static constexpr int kCPR = KC ? BK / 8 : R / 8;  // 16-byte chunks per LDS row
   static constexpr int kRPI = 64 / kCPR;             // LDS rows per instruction
   static_assert(KC || R >= 128, "MN-major tiles need >= 16 chunks per LDS row");
@@ -872,20 +874,25 @@ __device__ __forceinline__ void gemm_bf16_body4mn(const GemmParams& p, const Epi
 // tile kt+1 after an odd kt, B kt+2 and kt+3 may still be in flight (vmcnt 2 NB), after
 // an even kt also A super-tile kt/2+1 (vmcnt 2 NB + NA).  The steady state (tiles kt+1
 // and kt+4 exist) runs without runtime checks; the compiler schedules each step.
+// NP = 2 computes A.B and A.B1 (two products sharing A) on a 256 x (2 x 128) tile:
+// each B stage holds the 128 columns of B, then those of B1, and a wave's 128 x 64
+// sub-tile is 32 columns of each, so the epilogue finds both values of an output in
+// one lane.
 // Bit-identical to the other cores (same MFMA, same k order per accumulator).
 // Measured against the 64-deep two-stage cores at the config shape: 1.5-7% faster
 // than the 8-wave one, 1.5-3% faster than the 4-wave one with this staging.
-template <class Epi, bool F16 = false>
+template <class Epi, bool F16 = false, int NP = 1>
 __device__ __forceinline__ void gemm_bf16_body8km(const GemmParams& p, const Epi& epi) {
-  constexpr int BM = 256, BN = 256, WM = 2, WN = 4, BK = 32;
+  static_assert(NP == 1 || NP == 2, "one or two right operands");
+  constexpr int BM = 256, BN = 256 / NP, WM = 2, WN = 4, BK = 32;  // BN: per product
   constexpr int NW = WM * WN;
   constexpr int TM = BM / WM, TN = BN / WN;
   constexpr int FM = TM / 32, FN = TN / 32;
   using TA = OperandTile<BM, true, NW, 2 * BK>;
   using TB = OperandTile<BN, false, NW, BK>;
-  constexpr int NA = TA::kPerWave;  // A loads per wave per super-tile
-  constexpr int NB = TB::kPerWave;  // B loads per wave per tile
-  constexpr int kSA = BM * 2 * BK * 2, kSB = BN * BK * 2;  // bytes per stage
+  constexpr int NA = TA::kPerWave;       // A loads per wave per super-tile
+  constexpr int NB = NP * TB::kPerWave;  // B loads per wave per tile
+  constexpr int kSA = BM * 2 * BK * 2, kSB1 = BN * BK * 2, kSB = NP * kSB1;  // bytes per stage
   constexpr int kLdsBytes = 2 * kSA + 4 * kSB;
   __shared__ __attribute__((aligned(1024))) uint16_t smem[kLdsBytes / 2];
 
@@ -899,6 +906,7 @@ __device__ __forceinline__ void gemm_bf16_body8km(const GemmParams& p, const Epi
   const int64_t m0 = static_cast<int64_t>(tm) * BM, n0 = static_cast<int64_t>(tn) * BN;
   const uint16_t* A0 = static_cast<const uint16_t*>(p.a) + bb * p.sa_b + m0 * p.sa_m;
   const uint16_t* B0 = static_cast<const uint16_t*>(p.b) + bb * p.sb_b + n0 * p.sb_n;
+  const uint16_t* B1 = static_cast<const uint16_t*>(NP == 2 ? p.b1 : p.b) + bb * p.sb_b + n0 * p.sb_n;
   const uint32_t a_left0 = p.a_extent - static_cast<uint32_t>(m0 * p.sa_m * 2);
   const uint32_t b_left0 = p.b_extent - static_cast<uint32_t>(n0 * p.sb_n * 2);
 
@@ -914,28 +922,31 @@ __device__ __forceinline__ void gemm_bf16_body8km(const GemmParams& p, const Epi
   const uint16_t* sA = smem;
   const uint16_t* sB = smem + kSA;  // after the two A stages (kSA / 2 halfwords each)
 
-  f32x16_t acc[FM][FN];
+  f32x16_t acc[FM][NP * FN];
 #pragma unroll
   for (int i = 0; i < FM; ++i)
 #pragma unroll
-    for (int j = 0; j < FN; ++j)
+    for (int j = 0; j < NP * FN; ++j)
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
 
   // Fragments of A stage sa at k16 step as (0..3 within the super-tile) and of B
   // stage sb at step s (0..1 within the tile), into buffer buf.
-  bf16x8_t fa[2][FM], fb[2][FN];
+  bf16x8_t fa[2][FM], fb[2][NP * FN];
   auto read = [&](int sa, int as, int sb, int s, int buf) {
 #pragma unroll
     for (int i = 0; i < FM; ++i) fa[buf][i] = frag_kc(sA + sa * (kSA / 2), wm * TM + i * 32, as, lane);
 #pragma unroll
-    for (int j = 0; j < FN; ++j) fb[buf][j] = frag_mn<BN>(sB + sb * (kSB / 2), wn * TN + j * 32, s, lane);
+    for (int h = 0; h < NP; ++h)
+#pragma unroll
+      for (int j = 0; j < FN; ++j)
+        fb[buf][h * FN + j] = frag_mn<BN>(sB + sb * (kSB / 2) + h * (kSB1 / 2), wn * TN + j * 32, s, lane);
   };
   auto mfma = [&](int buf) {
 #pragma unroll
     for (int i = 0; i < FM; ++i)
 #pragma unroll
-      for (int j = 0; j < FN; ++j) acc[i][j] = mma16<F16>(fb[buf][j], fa[buf][i], acc[i][j]);
+      for (int j = 0; j < NP * FN; ++j) acc[i][j] = mma16<F16>(fb[buf][j], fa[buf][i], acc[i][j]);
   };
 
   auto run = [&](auto full_c) {
@@ -953,9 +964,17 @@ __device__ __forceinline__ void gemm_bf16_body8km(const GemmParams& p, const Epi
       if (t < KT) {
         const int64_t k0 = static_cast<int64_t>(t) * BK;
         const int k_left = static_cast<int>(p.K - k0 < BK ? p.K - k0 : BK);
-        const i32x4_t rb = make_rsrc(B0 + k0 * p.sb_k, b_left0 - static_cast<uint32_t>(k0 * p.sb_k * 2));
+        const uint32_t b_left = b_left0 - static_cast<uint32_t>(k0 * p.sb_k * 2);
+        const i32x4_t rb = make_rsrc(B0 + k0 * p.sb_k, b_left);
 #pragma unroll
-        for (int d = 0; d < NB; ++d) tb.template issue_one<FULL>(rb, lds_b + (t & 3) * kSB, wave, lane, k_left, d);
+        for (int d = 0; d < TB::kPerWave; ++d)
+          tb.template issue_one<FULL>(rb, lds_b + (t & 3) * kSB, wave, lane, k_left, d);
+        if constexpr (NP == 2) {
+          const i32x4_t rb1 = make_rsrc(B1 + k0 * p.sb_k, b_left);
+#pragma unroll
+          for (int d = 0; d < TB::kPerWave; ++d)
+            tb.template issue_one<FULL>(rb1, lds_b + (t & 3) * kSB + kSB1, wave, lane, k_left, d);
+        }
       }
     };
     // Prologue in the steady state's issue order (as if barriers -4 .. -1 had run).
@@ -1014,7 +1033,7 @@ __device__ __forceinline__ void gemm_bf16_body8km(const GemmParams& p, const Epi
   else run(BoolC<false>{});
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
-  tile_epilogue<BM, BN, WM, WN, 1>(p, epi, smem, acc, bb, m0, n0, mn_full, lane, wm, wn);
+  tile_epilogue<BM, BN, WM, WN, NP>(p, epi, smem, acc, bb, m0, n0, mn_full, lane, wm, wn);
 }
 
 #endif  // __HIP__ || __HIPCC_RTC__

@@ -2578,7 +2578,8 @@ View Lowerer::emit_gemm_epilogue(int v, const std::vector<int>& mem, bool* fused
       valu_weight += 6;
   }
   const bool heavy_epilogue = valu_weight >= 8;
-  // A K-contiguous, B MN-contiguous: the 8-wave 32-deep core for any epilogue.
+  // A K-contiguous, B MN-contiguous: the 8-wave 32-deep core for any epilogue, with
+  // one product or two sharing A.
   bool eight_km = false;
   if (NB == 1) {
     if (d.M >= 256 && d.N >= 256 && t256 >= 128 && ma && !mb) BM = 256, BN = 256, WM = 2, WN = 4, eight_km = true;
@@ -2587,6 +2588,7 @@ View Lowerer::emit_gemm_epilogue(int v, const std::vector<int>& mem, bool* fused
     else if (d.M >= 256 && d.N >= 128) BM = 256, BN = 128, WM = 2, WN = 2;
   } else if (d.M >= 256 && d.N >= 128) {
     BM = 256, BN = 128, WM = 2, WN = 4;
+    eight_km = ma && !mb && d.B * ((d.M + 255) / 256) * ((d.N + 127) / 128) >= 128;
   }
   const int nt = WM * WN * 64;
   const int odt = os.dtype;
@@ -2642,7 +2644,7 @@ View Lowerer::emit_gemm_epilogue(int v, const std::vector<int>& mem, bool* fused
   src << "extern \"C\" __global__ void __launch_bounds__(" << nt << ", 1) gemm_epilogue(ghip::GemmParams p, ghip::EpiArgs a) {\n"
       << "  const ghip::GenEpi epi{a};\n";
   if (eight_km)
-    src << "  ghip::gemm_bf16_body8km(p, epi);\n}\n";
+    src << "  ghip::gemm_bf16_body8km<ghip::GenEpi, false, " << NB << ">(p, epi);\n}\n";
   else if (four_wave && !ma && !mb)
     src << "  ghip::gemm_bf16_body4mn(p, epi);\n}\n";
   else if (four_wave)
@@ -2672,9 +2674,12 @@ View Lowerer::emit_gemm_epilogue(int v, const std::vector<int>& mem, bool* fused
   if (NB == 2) rd.push_back(rv1.slot);
   for (auto& in : ins) rd.push_back(in.view.slot);
   std::ostringstream desc;
-  desc << fmt("gemm_batched+epilogue bf16 B=%lld M=%lld N=%lld K=%lld dots=%d tile=%dx%d waves=%d (%s) ops=%zu inputs=%zu [",
-              (long long)d.B, (long long)d.M, (long long)d.N, (long long)d.K, NB, BM, BN * NB, WM * WN, d.how.c_str(),
-              mem.size(), ins.size());
+  // core: waves and k-depth of the main loop (km32: A in 64-deep, B in 32-deep stages)
+  const char* core = eight_km ? "8w-km32" : four_wave && !ma && !mb ? "4w-mn32" : four_wave ? "4w-k64" : "8w-k64";
+  desc << fmt("gemm_batched+epilogue bf16 B=%lld M=%lld N=%lld K=%lld dots=%d tile=%dx%d waves=%d core=%s (%s) ops=%zu "
+              "inputs=%zu [",
+              (long long)d.B, (long long)d.M, (long long)d.N, (long long)d.K, NB, BM, BN * NB, WM * WN, core,
+              d.how.c_str(), mem.size(), ins.size());
   for (size_t i = 0; i < mem.size(); ++i) {
     const Node& n = N[mem[i]];
     desc << (i ? "," : "") << kind_name(n.kind);

@@ -58,11 +58,12 @@ def _compile_run(be, build, inputs, fuse):
     return plan, outs
 
 
-def _check_fused_equals_unfused(be, build, inputs, dots=1):
+def _check_fused_equals_unfused(be, build, inputs, dots=1, core=None):
     plan_f, out_f = _compile_run(be, build, inputs, True)
     plan_u, out_u = _compile_run(be, build, inputs, False)
     print(plan_f)
     assert f"gemm_batched+epilogue bf16" in plan_f and f"dots={dots}" in plan_f
+    assert core is None or f"core={core}" in plan_f, plan_f
     assert "gemm_batched+epilogue" not in plan_u
     assert len(out_f) == len(out_u)
     for (dt_f, a), (dt_u, b) in zip(out_f, out_u):
@@ -105,17 +106,24 @@ def test_bias_relu_broadcast(be):
     assert rel_err(y, want) <= 2.0 ** -7 and norm_err(y, want) <= 1e-3
 
 
-@pytest.mark.parametrize("rows,cols", [(300, 264), (1024, 512)])
-def test_swiglu_two_products(be, rows, cols):
-    """SiLU(x.Wg) * (x.Wu): both products in one kernel sharing the x tile."""
-    x, sx = _bf16_in(31, (rows, 136))
-    wg, sg = _bf16_in(32, (136, cols), std=136 ** -0.5)
-    wu, su = _bf16_in(33, (136, cols), std=136 ** -0.5)
+@pytest.mark.parametrize("rows,cols,k,core", [(300, 264, 136, "8w-k64"), (1024, 512, 136, "8w-k64"),
+                                              (2000, 2000, 1000, "8w-km32"), (2048, 2048, 512, "8w-km32")])
+def test_swiglu_two_products(be, rows, cols, k, core):
+    """SiLU(x.Wg) * (x.Wu): both products in one kernel sharing the x tile.  Grids
+    of >= 128 tiles run the 8-wave 32-deep core (ragged: rows, cols and k not
+    multiples of the tile), smaller ones the 64-deep core; the large cases are
+    checked bit for bit against the unfused plan, whose products the DotGeneral
+    tests check against the oracle."""
+    x, sx = _bf16_in(31, (rows, k))
+    wg, sg = _bf16_in(32, (k, cols), std=k ** -0.5)
+    wu, su = _bf16_in(33, (k, cols), std=k ** -0.5)
 
     def build(f, x, wg, wu):
         g, u = graphs.dense(f, x, wg), graphs.dense(f, x, wu)
         return [f.Mul(f.Mul(g, f.Logistic(g)), u)]
-    (y,) = _check_fused_equals_unfused(be, build, [(x, sx), (wg, sg), (wu, su)], dots=2)
+    (y,) = _check_fused_equals_unfused(be, build, [(x, sx), (wg, sg), (wu, su)], dots=2, core=core)
+    if rows * cols * k > 1024 * 512 * 136:
+        return
     g = _bf(orc.dot_general(x, [1], [], wg, [0], [])).astype(np.float64)
     u = _bf(orc.dot_general(x, [1], [], wu, [0], []))
     want = _bf(_bf(g * _bf(1.0 / (1.0 + np.exp(-g)))) * u)

@@ -327,7 +327,20 @@ def test_epilogue_core_follows_layout_and_epilogue_weight(be):
     assert "gemm_batched+epilogue" in resid_t and "waves=4" in resid_t, resid_t
     gelu_t = _plan(be, lambda f, xx, w: [f.FusedGelu(f.DotGeneral(xx, [2], [], w, [1], []), False)],
                    [x, make_shape(BF16, 8192, 2048)])
-    assert "gemm_batched+epilogue" in gelu_t and "waves=8" in gelu_t, gelu_t
+    assert "gemm_batched+epilogue" in gelu_t and "waves=8" in gelu_t and "core=8w-k64" in gelu_t, gelu_t
+    assert "core=8w-km32" in gelu and "core=8w-km32" in resid and "core=4w-k64" in resid_t
+
+    # SwiGLU: two products sharing x in one kernel, on the 32-deep core for x . W
+    def swiglu(f, xx, wg, wu):
+        g = f.DotGeneral(xx, [2], [], wg, [0], [])
+        return [f.Mul(f.Mul(g, f.Logistic(g)), f.DotGeneral(xx, [2], [], wu, [0], []))]
+    w = make_shape(BF16, 2048, 8192)
+    sw = _plan(be, swiglu, [x, w, w])
+    assert "dots=2" in sw and "core=8w-km32" in sw and "tile=256x256" in sw, sw
+    small = _plan(be, swiglu, [make_shape(BF16, 1, 1024, 2048), w, w])
+    assert "dots=2" in small and "core=8w-km32" in small, small  # 4 x 64 tiles
+    tiny = _plan(be, swiglu, [make_shape(BF16, 1, 256, 2048), make_shape(BF16, 2048, 1024), make_shape(BF16, 2048, 1024)])
+    assert "dots=2" in tiny and "core=8w-k64" in tiny, tiny  # 8 tiles
 
 
 def test_dynamic_slice_and_scatter_shapes_and_errors(be):
