@@ -51,6 +51,12 @@ def parse():
     p.add_argument("--only", default="", help="comma list of secondary case names")
     p.add_argument("--eager", action="store_true",
                    help="launch every step from Python (no HIP graph); for counter collection")
+    p.add_argument("--warm-s", type=float, default=None, metavar="S",
+                   help="untimed sustained warm-up before each secondary line (default by bound: "
+                        "hbm 0.25 s, mfma 2 s)")
+    p.add_argument("--timed-s", type=float, default=None, metavar="S",
+                   help="minimum device time of each secondary line's timed region (default by "
+                        "bound: hbm 0.03 s, mfma 0.5 s)")
     p.add_argument("--copy-ref", type=int, default=0, metavar="MIB",
                    help="only run a plain device copy of MIB MiB (read + write) `steps` times: "
                         "the reference kernel that scales FETCH_SIZE / WRITE_SIZE to bytes")
@@ -101,14 +107,27 @@ def graph_runner(case: Case, steps: int):
     return g.replay, per
 
 
-MIN_WARM_S = 0.25   # sustained warm-up before each timed region
-MIN_TIMED_S = 0.03  # minimum device time inside each timed region
+# Sustained warm-up before each timed region and minimum device time inside it.
+# HBM-bound kernels draw well under the board's power limit and the clock settles
+# in ~100 ms.  MFMA-bound ones reach the limit (~1.4 kW on MI355X) and the power
+# manager takes ~1-1.5 s to settle the clock (sampled with amd-smi every 0.5 s:
+# 1.59 GHz at 0.5 s, then 2.0 GHz from 1.5 s for hipBLASLt's GEMM; 1.88-1.89 GHz
+# from 0.5 s for this library's); a timed region inside that transient measures the
+# power manager, not the kernel.
+MIN_WARM_S = {"hbm": 0.25, "mfma": 2.0}
+MIN_TIMED_S = {"hbm": 0.03, "mfma": 0.5}
 
 
-def time_case(case: Case, steps: int, warmup: int, eager: bool = False, exact_steps: bool = False):
+def time_case(case: Case, steps: int, warmup: int, eager: bool = False, exact_steps: bool = False,
+              warm_s: float = None, timed_s: float = None):
     """Times `case`.  exact_steps: the timed region holds exactly `steps` launches
     (the headline line, as --steps asks); otherwise it is stretched to at least
-    MIN_TIMED_S of device work (secondary lines, whose step counts are reported)."""
+    MIN_TIMED_S of device work (secondary lines, whose step counts are reported).
+    warm_s / timed_s override MIN_WARM_S / MIN_TIMED_S for the case's bound."""
+    if warm_s is None:
+        warm_s = MIN_WARM_S[case.bound]
+    if timed_s is None:
+        timed_s = MIN_TIMED_S[case.bound]
     import torch
     stream = case.stream or torch.cuda.current_stream()
     runner = graph_runner(case, steps) if case.bound == "hbm" and not eager else None
@@ -118,11 +137,11 @@ def time_case(case: Case, steps: int, warmup: int, eager: bool = False, exact_st
         replay, per = None, 1
     for i in range(warmup):
         case.launch(i)
-    # The clock settles only after some 100 ms of sustained load: keep warming up
-    # (untimed) until that much wall time has passed.
+    # The clock settles only after sustained load: keep warming up (untimed) until
+    # warm_s of wall time has passed.
     stream.synchronize()
     n, t0 = 0, time.perf_counter()
-    while time.perf_counter() - t0 < MIN_WARM_S:
+    while time.perf_counter() - t0 < warm_s:
         for _ in range(4):
             if replay is not None:
                 replay()
@@ -134,7 +153,7 @@ def time_case(case: Case, steps: int, warmup: int, eager: bool = False, exact_st
     settle_steps = n
     est = (time.perf_counter() - t0) / max(n, 1)
     if not exact_steps:
-        steps = max(steps, int(MIN_TIMED_S / est) + 1)
+        steps = max(steps, int(timed_s / est) + 1)
     # whole graph replays first, then single launches for the remainder
     reps, rest = (steps // per, steps % per) if replay is not None else (0, steps)
 
@@ -472,7 +491,8 @@ def main():
         for name in names:
             case = builders[name]()
             steps = args.steps if case.bound == "hbm" else max(5, args.steps // 20)
-            r = time_case(case, steps, max(2, args.warmup // 2), args.eager)
+            r = time_case(case, steps, max(2, args.warmup // 2), args.eager,
+                          warm_s=args.warm_s, timed_s=args.timed_s)
             entry = {"name": name, "dtype": case.dtype, "steps": r["steps"],
                      "graph": r["graph"],
                      "launch_us": round(r["launch_us"], 2),

@@ -52,6 +52,7 @@ namespace ghip {
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
 typedef int i32x4_t __attribute__((ext_vector_type(4)));
 
 struct GemmParams {
@@ -117,6 +118,11 @@ __device__ __forceinline__ int swz_k(int r) { return (r & 7) ^ ((r >> 3) & 1); }
 // by 16 lanes of a transpose read, and the 4 x 64 bytes read by 32 lanes, land
 // in distinct bank groups.
 __device__ __forceinline__ int swz_n(int k) { return (0xCA60u >> ((k & 3) * 4)) & 15u; }
+// Variant for 16x16x32 fragments, whose transpose reads cover k-rows k..k+3 and
+// k+8..k+11 of the same 16 columns in one half-wave: bit 3 of k also flips bit 1 of
+// the slot, so those 8 row pieces (2 chunks each) fill all 16 slots of a 256-byte
+// bank period.
+__device__ __forceinline__ int swz_n2(int k) { return swz_n(k) ^ (((k >> 3) & 1) << 1); }
 
 // Raw buffer descriptor (stride 0): reads at byte offsets >= `bytes` return 0.
 __device__ __forceinline__ i32x4_t make_rsrc(const void* base, uint32_t bytes) {
@@ -147,8 +153,9 @@ __device__ __forceinline__ void dma16(i32x4_t rsrc, uint32_t la, uint32_t voff) 
 // Wave-instruction i of a wave fills LDS bytes [blk*1024, blk*1024 + 1024),
 // blk = wave * kPerWave + i; lane l writes bytes l*16 .. l*16+15 of that block, so
 // the swizzle is applied by choosing which global chunk each lane fetches.
-// BK: k-depth of the tile (64; MN-contiguous tiles may also be 32 deep).
-template <int R, bool KC, int NW, int BK = kBK>
+// BK: k-depth of the tile (64; MN-contiguous tiles may also be 32 deep).  SW2:
+// MN-contiguous tiles use swz_n2 (read by 16x16x32 fragments) instead of swz_n.
+template <int R, bool KC, int NW, int BK = kBK, bool SW2 = false>
 struct OperandTile {
   static_assert(BK == kBK || (!KC && BK == 32), "32-deep tiles are MN-contiguous only");
   static constexpr int kInstr = R * BK * 2 / 1024;
@@ -171,7 +178,7 @@ struct OperandTile {
   }
   __device__ __forceinline__ static int chunk_of(int wave, int i, int lane) {
     const int r = row_of(wave, i, lane);
-    return KC ? (lane % kCPR) ^ swz_k(r) : (lane % kCPR) ^ swz_n(r);
+    return KC ? (lane % kCPR) ^ swz_k(r) : (lane % kCPR) ^ (SW2 ? swz_n2(r) : swz_n(r));
   }
   // s_mn / s_k: element strides of the operand along its rows (m or n) and k.
   __device__ __forceinline__ void init(int wave, int lane, int64_t s_mn, int64_t s_k, int64_t valid) {
@@ -270,13 +277,46 @@ __device__ __forceinline__ f32x16_t mma16(const bf16x8_t& a, const bf16x8_t& b, 
   }
 }
 
+// One 16x16x32 MFMA (bf16, or f16 when F16) accumulating in place.  Lane l of a
+// and b holds k 8 (l / 16) .. +8 of row / column l % 16; lane l of c holds rows
+// 4 (l / 16) .. +4 of column l % 16.  Written as inline asm: with the builtin the
+// register allocator moves 4-register accumulators between MFMAs (dst != srcC) and
+// spills a 128 x 64 wave tile at two waves per SIMD.  The compiler then does not
+// see these as MFMAs, so the callers keep the MFMA data hazards themselves:
+//   * operands come from LDS reads only, waited for with explicit lgkmcnt waits;
+//   * accumulators are written only by these MFMAs (zeroed by VALU long before the
+//     first one), and read only after mfma_drain();
+//   * overwriting an operand register right after the MFMA that reads it is
+//     allowed without wait states (the compiler emits that pattern itself for the
+//     builtin MFMAs).
+template <bool F16>
+__device__ __forceinline__ void mma16x32(f32x4_t& c, const bf16x8_t& a, const bf16x8_t& b) {
+  if constexpr (F16)
+    asm volatile("v_mfma_f32_16x16x32_f16 %0, %1, %2, %0" : "+v"(c) : "v"(a), "v"(b));
+  else
+    asm volatile("v_mfma_f32_16x16x32_bf16 %0, %1, %2, %0" : "+v"(c) : "v"(a), "v"(b));
+}
+// Waits out the last inline-asm MFMAs' result latency (32 wait states, more than an
+// 8-pass MFMA needs before a VALU or memory instruction reads its result) and
+// passes every accumulator through an empty volatile asm ordered after the wait, so
+// nothing that reads them is scheduled before it.
+template <int FM, int FN>
+__device__ __forceinline__ void mfma_drain(f32x4_t (&acc)[FM][FN]) {
+  asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j) asm volatile("" : "+v"(acc[i][j]));
+}
+
 // sched_barrier(0): the machine scheduler moves nothing across this point, so
 // the source order of MFMAs, LDS reads and loads is the issue order.
 __device__ __forceinline__ void sched_fence() { __builtin_amdgcn_sched_barrier(0); }
 
-// Epilogue through LDS, shared by both cores.  acc[i][j] holds the transposed
+// Epilogue through LDS, shared by all cores.  acc[i][j] holds the transposed
 // 32x32 block of wave (wm, wn): lane l, value v -> row m = l % 32, columns
-// n = (v / 4) * 8 + (l / 32) * 4 + v % 4, so storing it directly writes 16 bytes
+// n = (v / 4) * 8 + (l / 32) * 4 + v % 4 (16x16 blocks, f32x4_t: row l % 16,
+// columns 4 (l / 16) + v), so storing it directly writes 16 bytes
 // into each of 32 rows per instruction.  Instead the tile is staged in LDS (as
 // Epi::Stage values, 16-byte chunk c of row r at slot c ^ (r % chunks-per-row))
 // and read back row-wise: each lane takes CH = 16 / sizeof(Stage) consecutive
@@ -284,15 +324,18 @@ __device__ __forceinline__ void sched_fence() { __builtin_amdgcn_sched_barrier(0
 // exceeds the main loop's LDS take 2 passes of half the rows.  The epilogue's own
 // operands for the next row chunk are fetched (prefetch) before the current chunk
 // is stored.
-template <int BM, int BN, int WM, int WN, int NB, class Epi, int kLdsHalfwords, int FM, int FNB>
+template <int BM, int BN, int WM, int WN, int NB, class Epi, int kLdsHalfwords, class AccV, int FM, int FNB>
 __device__ __forceinline__ void tile_epilogue(const GemmParams& p, const Epi& epi, uint16_t (&smem)[kLdsHalfwords],
-                                              const f32x16_t (&acc)[FM][FNB], int64_t bb, int64_t m0, int64_t n0,
+                                              const AccV (&acc)[FM][FNB], int64_t bb, int64_t m0, int64_t n0,
                                               bool mn_full, int lane, int wm, int wn) {
   constexpr int kLdsBytes = kLdsHalfwords * 2;
   constexpr int NW = WM * WN;
   constexpr int TM = BM / WM, TN = BN / WN;
-  constexpr int FN = TN / 32;
-  static_assert(FM == TM / 32 && FNB == NB * FN, "accumulator shape");
+  constexpr int MB = sizeof(AccV) == 64 ? 32 : 16;  // MFMA block: 32x32 (f32x16_t) or 16x16 (f32x4_t)
+  static_assert(sizeof(AccV) == 64 || sizeof(AccV) == 16, "accumulator block");
+  constexpr int FN = TN / MB;
+  constexpr int NQ = MB == 32 ? 4 : 1;  // 4-value column runs per block and lane
+  static_assert(FM == TM / MB && FNB == NB * FN, "accumulator shape");
   using Stage = typename Epi::Stage;
   constexpr int ES = sizeof(Stage);
   constexpr int CH = 16 / ES;
@@ -319,16 +362,16 @@ __device__ __forceinline__ void tile_epilogue(const GemmParams& p, const Epi& ep
       __syncthreads();
 #pragma unroll
       for (int i = 0; i < FM; ++i) {
-        const int r = wm * TM + i * 32 + (lane & 31);
-        if ((wm * TM + i * 32) / PR != pass) continue;  // uniform over the wave
+        const int r = wm * TM + i * MB + (lane & (MB - 1));
+        if ((wm * TM + i * MB) / PR != pass) continue;  // uniform over the wave
         const int rl = r - pass * PR;
 #pragma unroll
         for (int h = 0; h < NB; ++h)
 #pragma unroll
           for (int j = 0; j < FN; ++j)
 #pragma unroll
-            for (int q = 0; q < 4; ++q) {
-              const int n = wn * TN + j * 32 + q * 8 + (lane >> 5) * 4;
+            for (int q = 0; q < NQ; ++q) {
+              const int n = MB == 32 ? wn * TN + j * 32 + q * 8 + (lane >> 5) * 4 : wn * TN + j * 16 + (lane >> 4) * 4;
               Stage w[4];
 #pragma unroll
               for (int e = 0; e < 4; ++e) w[e] = Epi::stage(acc[i][h * FN + j][q * 4 + e]);
@@ -868,32 +911,39 @@ __device__ __forceinline__ void gemm_bf16_body4mn(const GemmParams& p, const Epi
 // with W [K, N] row-major): one 256 x 256 tile per workgroup of 2 x 4 waves (128 x 64
 // each, two waves per SIMD), k-steps of 32 with B in four 32-deep LDS stages and A in
 // two 64-deep "super-tile" stages (a K-contiguous row of 32 k would fetch half cache
-// lines).  B tile kt's stage takes tile kt+4 at the barrier that retires it; the A
-// stage of super-tile j (tiles 2j, 2j+1) takes super-tile j+2 at the barrier that
-// retires tile 2j+1.  Issue order per barrier: A (after odd tiles), then B; so for
-// tile kt+1 after an odd kt, B kt+2 and kt+3 may still be in flight (vmcnt 2 NB), after
-// an even kt also A super-tile kt/2+1 (vmcnt 2 NB + NA).  The steady state (tiles kt+1
-// and kt+4 exist) runs without runtime checks; the compiler schedules each step.
+// lines).  B tile kt's stage takes tile kt+4 at the barrier that starts tile kt; the
+// A stage of super-tile j (tiles 2j, 2j+1) takes super-tile j+2 at the barrier that
+// starts tile 2j+1.  Issue order per barrier: A (at odd tiles), then B; so at the
+// barrier of an odd kt, tile kt+1 is complete once all but B kt+2, kt+3 have landed
+// (vmcnt 2 NB), at an even kt all but those and A super-tile kt/2+1 (vmcnt 2 NB + NA).
+//
+// 16x16x32 MFMAs (32 per tile and wave): under the board's power limit the part
+// clocks ~10-15% higher running them than 32x32x16 MFMAs of the same work (one
+// 16x16 accumulator block moves a quarter of the accumulator data per product), and
+// the products come out bit-identical.  A tile's fragments are in registers when it
+// starts; its MFMAs run row block by row block, each block's A fragment refilled for
+// tile kt+1 right after its last MFMA, and B's in the last block, so one set of
+// fragments (48 VGPRs) serves both tiles.  B stages sit below A in LDS, so every
+// fragment read is one base register plus an immediate offset.
+//
 // NP = 2 computes A.B and A.B1 (two products sharing A) on a 256 x (2 x 128) tile:
 // each B stage holds the 128 columns of B, then those of B1, and a wave's 128 x 64
 // sub-tile is 32 columns of each, so the epilogue finds both values of an output in
 // one lane.
-// Bit-identical to the other cores (same MFMA, same k order per accumulator).
-// Measured against the 64-deep two-stage cores at the config shape: 1.5-7% faster
-// than the 8-wave one, 1.5-3% faster than the 4-wave one with this staging.
 template <class Epi, bool F16 = false, int NP = 1>
 __device__ __forceinline__ void gemm_bf16_body8km(const GemmParams& p, const Epi& epi) {
   static_assert(NP == 1 || NP == 2, "one or two right operands");
   constexpr int BM = 256, BN = 256 / NP, WM = 2, WN = 4, BK = 32;  // BN: per product
   constexpr int NW = WM * WN;
   constexpr int TM = BM / WM, TN = BN / WN;
-  constexpr int FM = TM / 32, FN = TN / 32;
+  constexpr int FM = TM / 16, FN = TN / 16, FB = NP * FN;  // 16x16 blocks per wave
   using TA = OperandTile<BM, true, NW, 2 * BK>;
-  using TB = OperandTile<BN, false, NW, BK>;
+  using TB = OperandTile<BN, false, NW, BK, true>;
   constexpr int NA = TA::kPerWave;       // A loads per wave per super-tile
   constexpr int NB = NP * TB::kPerWave;  // B loads per wave per tile
   constexpr int kSA = BM * 2 * BK * 2, kSB1 = BN * BK * 2, kSB = NP * kSB1;  // bytes per stage
-  constexpr int kLdsBytes = 2 * kSA + 4 * kSB;
+  constexpr int kLdsBytes = 4 * kSB + 2 * kSA;
+  static_assert(4 * kSB <= 65536 && kSA + TM * 2 * BK * 2 <= 65536, "fragment offsets fit the 16-bit immediate");
   __shared__ __attribute__((aligned(1024))) uint16_t smem[kLdsBytes / 2];
 
   const int lane = threadIdx.x & 63;
@@ -917,36 +967,45 @@ __device__ __forceinline__ void gemm_bf16_body8km(const GemmParams& p, const Epi
   const bool mn_full = m0 + BM <= p.M && n0 + BN <= p.N;
   const int KT = static_cast<int>((p.K + BK - 1) / BK);  // 32-deep tiles
   const int KS = (KT + 1) / 2;                             // 64-deep A super-tiles
-  const uint32_t lds_a = static_cast<uint32_t>(reinterpret_cast<uint64_t>((GHIP_LDS void*)smem));
-  const uint32_t lds_b = lds_a + 2 * kSA;
-  const uint16_t* sA = smem;
-  const uint16_t* sB = smem + kSA;  // after the two A stages (kSA / 2 halfwords each)
+  const uint32_t lds_b = static_cast<uint32_t>(reinterpret_cast<uint64_t>((GHIP_LDS void*)smem));
+  const uint32_t lds_a = lds_b + 4 * kSB;
 
-  f32x16_t acc[FM][NP * FN];
+  f32x4_t acc[FM][FB];
 #pragma unroll
   for (int i = 0; i < FM; ++i)
 #pragma unroll
-    for (int j = 0; j < NP * FN; ++j)
+    for (int j = 0; j < FB; ++j)
 #pragma unroll
-      for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
+      for (int v = 0; v < 4; ++v) acc[i][j][v] = 0.f;
 
-  // Fragments of A stage sa at k16 step as (0..3 within the super-tile) and of B
-  // stage sb at step s (0..1 within the tile), into buffer buf.
-  bf16x8_t fa[2][FM], fb[2][NP * FN];
-  auto read = [&](int sa, int as, int sb, int s, int buf) {
+  // Per-lane LDS base pointers (address space 3, so stage and block offsets fold
+  // into the reads' immediate offsets): A for k32 step as (0, 1) of a super-tile
+  // (lane l: row l % 16 of a block, k chunk as * 4 + l / 16), B per column block
+  // (the swizzle mixes the block's chunk bits; lane l: column l % 16 of the block,
+  // k-rows 8 (l / 16) + (l % 16) / 4 and + 4 for the two transpose reads).
+  typedef GHIP_LDS const uint16_t* lds_p;
+  lds_p const lds0 = (lds_p)((GHIP_LDS void*)smem);
+  lds_p abase[2], bbase[FN];
 #pragma unroll
-    for (int i = 0; i < FM; ++i) fa[buf][i] = frag_kc(sA + sa * (kSA / 2), wm * TM + i * 32, as, lane);
+  for (int as = 0; as < 2; ++as) {
+    const int row = wm * TM + (lane & 15);
+    abase[as] = lds0 + 2 * kSB + row * (2 * BK) + (((4 * as + (lane >> 4)) ^ swz_k(row)) * 8);
+  }
 #pragma unroll
-    for (int h = 0; h < NP; ++h)
-#pragma unroll
-      for (int j = 0; j < FN; ++j)
-        fb[buf][h * FN + j] = frag_mn<BN>(sB + sb * (kSB / 2) + h * (kSB1 / 2), wn * TN + j * 32, s, lane);
+  for (int j = 0; j < FN; ++j) {
+    const int kl = 8 * (lane >> 4) + ((lane & 15) >> 2);
+    const int nl = wn * TN + j * 16 + 4 * (lane & 3);
+    bbase[j] = lds0 + kl * BN + (((nl >> 3) ^ swz_n2(kl)) * 8) + (nl & 7);
+  }
+  bf16x8_t fa[FM], fb[FB];
+  auto read_a = [&](int i, int sa, int as) {  // row block i from A stage sa, k32 step as
+    fa[i] = *(GHIP_LDS const bf16x8_t*)(abase[as] + sa * (kSA / 2) + i * 16 * (2 * BK));
   };
-  auto mfma = [&](int buf) {
-#pragma unroll
-    for (int i = 0; i < FM; ++i)
-#pragma unroll
-      for (int j = 0; j < NP * FN; ++j) acc[i][j] = mma16<F16>(fb[buf][j], fa[buf][i], acc[i][j]);
+  auto read_b = [&](int jj, int sb) {  // column block jj (product jj / FN) from B stage sb
+    lds_p p0 = bbase[jj % FN] + sb * (kSB / 2) + (jj / FN) * (kSB1 / 2);
+    const bf16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((GHIP_LDS bf16x4_t*)(p0));
+    const bf16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((GHIP_LDS bf16x4_t*)(p0 + 4 * BN));
+    fb[jj] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
   };
 
   auto run = [&](auto full_c) {
@@ -986,17 +1045,19 @@ __device__ __forceinline__ void gemm_bf16_body8km(const GemmParams& p, const Epi
     issue_b(3);
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
-    read(0, 0, 0, 0, 0);
+#pragma unroll
+    for (int j = 0; j < FB; ++j) read_b(j, 0);
+#pragma unroll
+    for (int i = 0; i < FM; ++i) read_a(i, 0, 0);
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
 
-    // Tile kt in B stage ST = kt % 4 and A stage ST / 2 (steps 2 (ST % 2) and
-    // 2 (ST % 2) + 1 of the super-tile).  STEADY: tiles kt+1 and kt+4 exist.
+    // Tile kt (B stage ST = kt % 4, A stage ST / 2, k32 step ST % 2 of the
+    // super-tile), fragments in registers.  STEADY: tiles kt+1 and kt+4 exist.
     auto tile = [&](int kt, auto st_c, auto steady_c) {
       constexpr int ST = decltype(st_c)::value;
       constexpr int SN = (ST + 1) % 4;
       constexpr bool STEADY = decltype(steady_c)::value;
       const bool nx = STEADY || kt + 1 < KT;
-      read(ST / 2, 2 * (ST % 2) + 1, ST, 1, 1);
-      mfma(0);
       if (nx) {
         if constexpr (STEADY) {
           if constexpr (ST % 2 == 1)
@@ -1006,14 +1067,23 @@ __device__ __forceinline__ void gemm_bf16_body8km(const GemmParams& p, const Epi
         } else {
           asm volatile("s_waitcnt lgkmcnt(0)\n\ts_waitcnt vmcnt(0)" ::: "memory");
         }
+        // Every wave holds tile kt's fragments: its B stage (and after an odd kt
+        // its A stage) is free; tile kt+1 is visible to all.
         __syncthreads();
         if constexpr (ST % 2 == 1) {
           if (STEADY || (kt + 3) / 2 < KS) issue_a(kt / 2 + 2);
         }
         if (STEADY || kt + 4 < KT) issue_b(kt + 4);
-        read(SN / 2, 2 * (SN % 2), SN, 0, 0);
       }
-      mfma(1);
+#pragma unroll
+      for (int i = 0; i < FM; ++i) {
+#pragma unroll
+        for (int j = 0; j < FB; ++j) {
+          mma16x32<F16>(acc[i][j], fb[j], fa[i]);
+          if (i == FM - 1 && nx) read_b(j, SN);
+        }
+        if (nx) read_a(i, SN / 2, SN % 2);
+      }
     };
     int kt = 0;
     for (; kt + 7 < KT; kt += 4) {
@@ -1032,6 +1102,7 @@ __device__ __forceinline__ void gemm_bf16_body8km(const GemmParams& p, const Epi
   if (mn_full && (p.K % (2 * BK)) == 0) run(BoolC<true>{});
   else run(BoolC<false>{});
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  mfma_drain(acc);
 
   tile_epilogue<BM, BN, WM, WN, NP>(p, epi, smem, acc, bb, m0, n0, mn_full, lane, wm, wn);
 }
