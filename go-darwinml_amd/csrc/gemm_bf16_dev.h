@@ -557,188 +557,15 @@ __device__ __forceinline__ void gemm_bf16_body(const GemmParams& p, const Epi& e
 }
 
 
-// 4-wave core: one 256 x 256 tile per workgroup of 2 x 2 waves, each wave a
-// 128 x 128 sub-tile (16 32x32 blocks, 256 accumulators per lane, so one wave per
-// SIMD).  Against the 8-wave core (128 x 64 per wave) a wave reads 8 KiB of LDS per
-// 16-deep k step for twice the MFMA work, which cuts the CU's LDS read traffic by
-// a third.  With one wave per SIMD nothing hides a stall, so the issue order is
-// fixed by sched_fence(): in each k16 step the 16 MFMAs alternate with the 12 LDS
-// reads of the next step's fragments (ordered so that the next step's first MFMAs
-// need only the first reads); in the last step of a k-tile, 8 MFMAs run, then the
-// wait for tile kt+1 and the barrier, then the remaining 8 MFMAs carry the 16
-// loads of tile kt+2 and the reads of tile kt+1's first step.  Products are
-// bit-identical to the 8-wave core (same MFMA, same k order per accumulator).
-template <bool A_K, bool B_K, class Epi, bool F16 = false>
-__device__ __forceinline__ void gemm_bf16_body4(const GemmParams& p, const Epi& epi) {
-  constexpr int BM = 256, BN = 256, WM = 2, WN = 2;
-  constexpr int NW = WM * WN;
-  constexpr int TM = BM / WM, TN = BN / WN;
-  constexpr int FM = TM / 32, FN = TN / 32;
-  constexpr int NS = kBK / 16;
-  using TA = OperandTile<BM, A_K, NW>;
-  using TB = OperandTile<BN, B_K, NW>;
-  constexpr int ND = TA::kPerWave + TB::kPerWave;  // loads per wave per k-tile
-  constexpr int kLdsBytes = 2 * BM * kBK * 2 + 2 * BN * kBK * 2;
-  __shared__ __attribute__((aligned(1024))) uint16_t smem[kLdsBytes / 2];
-  uint16_t(*sa)[BM * kBK] = reinterpret_cast<uint16_t(*)[BM * kBK]>(smem);
-  uint16_t(*sb)[BN * kBK] = reinterpret_cast<uint16_t(*)[BN * kBK]>(smem + 2 * BM * kBK);
-
-  const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int wm = wave / WN, wn = wave % WN;
-
-  int64_t bb;
-  int tm, tn;
-  map_tile(blockIdx.x, p.batch * p.tiles_m * p.tiles_n, p.tiles_m, p.tiles_n, bb, tm, tn);
-  const int64_t m0 = static_cast<int64_t>(tm) * BM, n0 = static_cast<int64_t>(tn) * BN;
-  const uint16_t* A0 = static_cast<const uint16_t*>(p.a) + bb * p.sa_b + m0 * p.sa_m;
-  const uint16_t* B0 = static_cast<const uint16_t*>(p.b) + bb * p.sb_b + n0 * p.sb_n;
-  const uint32_t a_left0 = p.a_extent - static_cast<uint32_t>(m0 * p.sa_m * 2);
-  const uint32_t b_left0 = p.b_extent - static_cast<uint32_t>(n0 * p.sb_n * 2);
-
-  TA ta;
-  TB tb;
-  ta.init(wave, lane, p.sa_m, p.sa_k, p.M - m0);
-  tb.init(wave, lane, p.sb_n, p.sb_k, p.N - n0);
-  const bool mn_full = m0 + BM <= p.M && n0 + BN <= p.N;
-  const int KT = static_cast<int>((p.K + kBK - 1) / kBK);
-  const uint32_t lds_a = static_cast<uint32_t>(reinterpret_cast<uint64_t>((GHIP_LDS void*)smem));
-  const uint32_t lds_b = lds_a + 2 * BM * kBK * 2;
-
-  f32x16_t acc[FM][FN];
-#pragma unroll
-  for (int i = 0; i < FM; ++i)
-#pragma unroll
-    for (int j = 0; j < FN; ++j)
-#pragma unroll
-      for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
-
-  // Fragments [buffer][block][half]: a K-contiguous tile gives a fragment in one
-  // ds_read_b128, an MN-contiguous one in two transpose reads (one per half).
-  bf16x4_t fa[2][FM][2], fb[2][FN][2];
-  constexpr int RA = A_K ? 1 : 2, RB = B_K ? 1 : 2;  // LDS reads per fragment
-  constexpr int NR = FM * RA + FN * RB;               // LDS reads per k16 step
-  // Read r of step s (stage st) into buffer nb, in the order A0 B0 A1 B1 ...
-  auto read_op = [&](int st, int s, int nb, int r) {
-    const int blk = r / (RA + RB), q = r % (RA + RB);
-    if (q < RA) {
-      if constexpr (A_K) {
-        const bf16x8_t v = frag_kc(sa[st], wm * TM + blk * 32, s, lane);
-        fa[nb][blk][0] = __builtin_shufflevector(v, v, 0, 1, 2, 3);
-        fa[nb][blk][1] = __builtin_shufflevector(v, v, 4, 5, 6, 7);
-      } else {
-        fa[nb][blk][q] = frag_mn_half<BM>(sa[st], wm * TM + blk * 32, s, lane, q);
-      }
-    } else {
-      if constexpr (B_K) {
-        const bf16x8_t v = frag_kc(sb[st], wn * TN + blk * 32, s, lane);
-        fb[nb][blk][0] = __builtin_shufflevector(v, v, 0, 1, 2, 3);
-        fb[nb][blk][1] = __builtin_shufflevector(v, v, 4, 5, 6, 7);
-      } else {
-        fb[nb][blk][q - RA] = frag_mn_half<BN>(sb[st], wn * TN + blk * 32, s, lane, q - RA);
-      }
-    }
-  };
-  // MFMA k of a step; blocks in order of max(i, j), so the first MFMAs of a step
-  // need only the first fragments read.
-  auto mfma_op = [&](int b, int k) {
-    constexpr int ord[16][2] = {{0, 0}, {0, 1}, {1, 0}, {1, 1}, {0, 2}, {1, 2}, {2, 0}, {2, 1},
-                                {2, 2}, {0, 3}, {1, 3}, {2, 3}, {3, 0}, {3, 1}, {3, 2}, {3, 3}};
-    const int i = ord[k][0], j = ord[k][1];
-    const bf16x8_t av = __builtin_shufflevector(fa[b][i][0], fa[b][i][1], 0, 1, 2, 3, 4, 5, 6, 7);
-    const bf16x8_t bv = __builtin_shufflevector(fb[b][j][0], fb[b][j][1], 0, 1, 2, 3, 4, 5, 6, 7);
-    acc[i][j] = mma16<F16>(bv, av, acc[i][j]);
-  };
-
-  auto run = [&](auto full_c) {
-    constexpr bool FULL = decltype(full_c)::value;
-    // Load d (0 .. ND-1) of this wave's share of k-tile kt into stage st.
-    auto dma = [&](int kt, int st, int d) {
-      const int64_t k0 = static_cast<int64_t>(kt) * kBK;
-      const int k_left = static_cast<int>(p.K - k0 < kBK ? p.K - k0 : kBK);
-      if (d < TA::kPerWave) {
-        const i32x4_t ra = make_rsrc(A0 + k0 * p.sa_k, a_left0 - static_cast<uint32_t>(k0 * p.sa_k * 2));
-        ta.template issue_one<FULL>(ra, lds_a + st * (BM * kBK * 2), wave, lane, k_left, d);
-      } else {
-        const i32x4_t rb = make_rsrc(B0 + k0 * p.sb_k, b_left0 - static_cast<uint32_t>(k0 * p.sb_k * 2));
-        tb.template issue_one<FULL>(rb, lds_b + st * (BN * kBK * 2), wave, lane, k_left, d - TA::kPerWave);
-      }
-    };
-    // Prologue: tiles 0 and 1 in flight, wait for tile 0.
-#pragma unroll
-    for (int d = 0; d < ND; ++d) dma(0, 0, d);
-    if (KT > 1) {
-#pragma unroll
-      for (int d = 0; d < ND; ++d) dma(1, 1, d);
-      asm volatile("s_waitcnt vmcnt(%0)" ::"n"(ND) : "memory");
-    } else {
-      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    }
-    __syncthreads();
-#pragma unroll
-    for (int r = 0; r < NR; ++r) read_op(0, 0, 0, r);
-
-    // Tile kt in stage ST.  Tile kt+1 (read at its end) and tile kt+2 (loaded at
-    // its end) may not exist: uniform branches.
-    auto tile = [&](int kt, auto st_c) {
-      constexpr int ST = decltype(st_c)::value;
-      const bool nx = kt + 1 < KT, dm = kt + 2 < KT;
-#pragma unroll
-      for (int s = 0; s < NS; ++s) {
-        const int b = s & 1;
-        if (s + 1 < NS) {
-#pragma unroll
-          for (int k = 0; k < 16; ++k) {
-            mfma_op(b, k);
-            if (k < NR) read_op(ST, s + 1, b ^ 1, k);
-            sched_fence();
-          }
-        } else {
-#pragma unroll
-          for (int k = 0; k < 8; ++k) {
-            mfma_op(b, k);
-            sched_fence();
-          }
-          // Tile kt+1 has landed (this wave's loads; the barrier covers the other
-          // waves') and every wave is done reading stage ST (the barrier waits for
-          // the LDS reads), so tile kt+2 may refill it.
-          if (nx) {
-            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-            __syncthreads();
-          }
-          sched_fence();
-#pragma unroll
-          for (int k = 8; k < 16; ++k) {
-            mfma_op(b, k);
-            const int x = k - 8;
-            if (dm) {
-#pragma unroll
-              for (int d = x * ND / 8; d < (x + 1) * ND / 8; ++d) dma(kt + 2, ST, d);
-            }
-            if (nx) {
-#pragma unroll
-              for (int r = x * NR / 8; r < (x + 1) * NR / 8; ++r) read_op(ST ^ 1, 0, b ^ 1, r);
-            }
-            sched_fence();
-          }
-        }
-      }
-    };
-    for (int kt = 0; kt < KT; kt += 2) {
-      tile(kt, IntC<0>{});
-      if (kt + 1 < KT) tile(kt + 1, IntC<1>{});
-    }
-  };
-  if (mn_full && (p.K % kBK) == 0) run(BoolC<true>{});
-  else run(BoolC<false>{});
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-
-  tile_epilogue<BM, BN, WM, WN, 1>(p, epi, smem, acc, bb, m0, n0, mn_full, lane, wm, wn);
-}
-
 // 4-wave core for both operands MN-contiguous (A [K, M], B [K, N] in memory, e.g.
-// a weight gradient X^T . dY): the same 256 x 256 tile, 2 x 2 waves and MFMA / LDS
-// read order as gemm_bf16_body4, with 32-deep k-tiles in four LDS stages (128 KiB).
+// a weight gradient X^T . dY): one 256 x 256 tile per workgroup of 2 x 2 waves, each
+// a 128 x 128 sub-tile (16 32x32 blocks, 256 accumulators per lane, one wave per
+// SIMD, which reads a third less LDS per MFMA than 128 x 64 waves).  With one wave
+// per SIMD nothing hides a stall, so the issue order is fixed by sched_fence(): the
+// MFMAs of a k16 step alternate with the LDS reads of the next step's fragments;
+// in the last step of a k-tile half the MFMAs run, then the wait and the barrier,
+// then the other half carry the refill loads and the next tile's first reads.
+// 32-deep k-tiles in four LDS stages (128 KiB).
 // At the barrier that retires tile kt its stage takes tile kt+4, so three tiles of
 // MFMA work cover a load; the steady state (every tile has a successor and a tile
 // four ahead) runs without runtime branches.  Measured 5% faster than the 64-deep,
@@ -1104,6 +931,178 @@ __device__ __forceinline__ void gemm_bf16_body8km(const GemmParams& p, const Epi
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   mfma_drain(acc);
 
+  tile_epilogue<BM, BN, WM, WN, NP>(p, epi, smem, acc, bb, m0, n0, mn_full, lane, wm, wn);
+}
+
+// 8-wave 16x16x32 core for any operand layout (the A K-contiguous / B MN-contiguous
+// one has its own deeper pipeline, gemm_bf16_body8km): one 256 x 256 tile (256 x
+// (2 x 128) for NP = 2, as there) per workgroup of 2 x 4 waves, 64-deep k-tiles in
+// two LDS stages, two k32 steps per tile.  Fragments roll as in gemm_bf16_body8km:
+// step 0 of tile kt reads step 1 of the same stage; then wait for tile kt+1, barrier
+// (stage kt % 2 is free), refill it with tile kt+2, and step 1 reads step 0 of tile
+// kt+1.  MN-contiguous tiles use swz_n2.  Bit-identical to the other cores; in one
+// process at the config shape 2-3% faster than the 4-wave 32x32x16 cores for B
+// K-contiguous layouts (and 4-6% on [8192,2048].[2048,2048]), 4-5% faster than the
+// 8-wave 32x32x16 64-deep core for two products and heavy epilogues, 4% slower than
+// the 4-wave 32-deep core when both operands are MN-contiguous.
+template <bool A_K, bool B_K, class Epi, bool F16 = false, int NP = 1>
+__device__ __forceinline__ void gemm_bf16_body8x(const GemmParams& p, const Epi& epi) {
+  static_assert(NP == 1 || NP == 2, "one or two right operands");
+  constexpr int BM = 256, BN = 256 / NP, WM = 2, WN = 4, BK = kBK;
+  constexpr int NW = WM * WN;
+  constexpr int TM = BM / WM, TN = BN / WN;
+  constexpr int FM = TM / 16, FN = TN / 16, FB = NP * FN;
+  using TA = OperandTile<BM, A_K, NW, BK, !A_K>;
+  using TB = OperandTile<BN, B_K, NW, BK, !B_K>;
+  constexpr int kSA = BM * BK * 2, kSB1 = BN * BK * 2, kSB = NP * kSB1;  // bytes per stage
+  constexpr int kLdsBytes = 2 * kSA + 2 * kSB;
+  __shared__ __attribute__((aligned(1024))) uint16_t smem[kLdsBytes / 2];
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wm = wave / WN, wn = wave % WN;
+
+  int64_t bb;
+  int tm, tn;
+  map_tile(blockIdx.x, p.batch * p.tiles_m * p.tiles_n, p.tiles_m, p.tiles_n, bb, tm, tn);
+  const int64_t m0 = static_cast<int64_t>(tm) * BM, n0 = static_cast<int64_t>(tn) * BN;
+  const uint16_t* A0 = static_cast<const uint16_t*>(p.a) + bb * p.sa_b + m0 * p.sa_m;
+  const uint16_t* B0 = static_cast<const uint16_t*>(p.b) + bb * p.sb_b + n0 * p.sb_n;
+  const uint16_t* B1 = static_cast<const uint16_t*>(NP == 2 ? p.b1 : p.b) + bb * p.sb_b + n0 * p.sb_n;
+  const uint32_t a_left0 = p.a_extent - static_cast<uint32_t>(m0 * p.sa_m * 2);
+  const uint32_t b_left0 = p.b_extent - static_cast<uint32_t>(n0 * p.sb_n * 2);
+
+  TA ta;
+  TB tb;
+  ta.init(wave, lane, p.sa_m, p.sa_k, p.M - m0);
+  tb.init(wave, lane, p.sb_n, p.sb_k, p.N - n0);
+  const bool mn_full = m0 + BM <= p.M && n0 + BN <= p.N;
+  const int KT = static_cast<int>((p.K + BK - 1) / BK);
+  const uint32_t lds_a = static_cast<uint32_t>(reinterpret_cast<uint64_t>((GHIP_LDS void*)smem));
+  const uint32_t lds_b = lds_a + 2 * kSA;
+
+  f32x4_t acc[FM][FB];
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FB; ++j)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) acc[i][j][v] = 0.f;
+
+  typedef GHIP_LDS const uint16_t* lds_p;
+  lds_p const ldsA = (lds_p)((GHIP_LDS void*)smem);
+  lds_p const ldsB = ldsA + kSA;  // halfwords: after the two A stages
+  // Per-lane LDS base pointers (address space 3, so stage, step and block offsets
+  // fold into the reads' immediate offsets): a K-contiguous operand ([R][64]) has
+  // one per k32 step (lane l: row l % 16 of a block, k chunk 4 s + l / 16), an
+  // MN-contiguous one ([64][R]) one per block (the swizzle mixes the block's chunk
+  // bits; lane l: column l % 16, k-rows 8 (l / 16) + (l % 16) / 4 and + 4).
+  constexpr int NBA = A_K ? 2 : FM, NBB = B_K ? 2 : FN;
+  lds_p abase[NBA], bbase[NBB];
+#pragma unroll
+  for (int q = 0; q < NBA; ++q) {
+    if constexpr (A_K) {
+      const int row = wm * TM + (lane & 15);
+      abase[q] = ldsA + row * BK + (((4 * q + (lane >> 4)) ^ swz_k(row)) * 8);
+    } else {
+      const int kl = 8 * (lane >> 4) + ((lane & 15) >> 2);
+      const int nl = wm * TM + q * 16 + 4 * (lane & 3);
+      abase[q] = ldsA + kl * BM + (((nl >> 3) ^ swz_n2(kl)) * 8) + (nl & 7);
+    }
+  }
+#pragma unroll
+  for (int q = 0; q < NBB; ++q) {
+    if constexpr (B_K) {
+      const int row = wn * TN + (lane & 15);
+      bbase[q] = ldsB + row * BK + (((4 * q + (lane >> 4)) ^ swz_k(row)) * 8);
+    } else {
+      const int kl = 8 * (lane >> 4) + ((lane & 15) >> 2);
+      const int nl = wn * TN + q * 16 + 4 * (lane & 3);
+      bbase[q] = ldsB + kl * BN + (((nl >> 3) ^ swz_n2(kl)) * 8) + (nl & 7);
+    }
+  }
+  bf16x8_t fa[FM], fb[FB];
+  auto rd_tr = [](lds_p p0, int R) {
+    const bf16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((GHIP_LDS bf16x4_t*)(p0));
+    const bf16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((GHIP_LDS bf16x4_t*)(p0 + 4 * R));
+    return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+  };
+  // block i of A / jj of B at k32 step s (0, 1) of stage st
+  auto read_a = [&](int i, int st, int s) {
+    if constexpr (A_K) fa[i] = *(GHIP_LDS const bf16x8_t*)(abase[s] + st * (kSA / 2) + i * 16 * BK);
+    else fa[i] = rd_tr(abase[i] + st * (kSA / 2) + s * 32 * BM, BM);
+  };
+  auto read_b = [&](int jj, int st, int s) {
+    const int h = jj / FN, j = jj % FN;
+    if constexpr (B_K) fb[jj] = *(GHIP_LDS const bf16x8_t*)(bbase[s] + st * (kSB / 2) + h * (kSB1 / 2) + j * 16 * BK);
+    else fb[jj] = rd_tr(bbase[j] + st * (kSB / 2) + h * (kSB1 / 2) + s * 32 * BN, BN);
+  };
+
+  auto run = [&](auto full_c) {
+    constexpr bool FULL = decltype(full_c)::value;
+    auto issue = [&](int kt, int st) {
+      const int64_t k0 = static_cast<int64_t>(kt) * BK;
+      const int k_left = static_cast<int>(p.K - k0 < BK ? p.K - k0 : BK);
+      const i32x4_t ra = make_rsrc(A0 + k0 * p.sa_k, a_left0 - static_cast<uint32_t>(k0 * p.sa_k * 2));
+#pragma unroll
+      for (int d = 0; d < TA::kPerWave; ++d) ta.template issue_one<FULL>(ra, lds_a + st * kSA, wave, lane, k_left, d);
+      const uint32_t b_left = b_left0 - static_cast<uint32_t>(k0 * p.sb_k * 2);
+      const i32x4_t rb = make_rsrc(B0 + k0 * p.sb_k, b_left);
+#pragma unroll
+      for (int d = 0; d < TB::kPerWave; ++d) tb.template issue_one<FULL>(rb, lds_b + st * kSB, wave, lane, k_left, d);
+      if constexpr (NP == 2) {
+        const i32x4_t rb1 = make_rsrc(B1 + k0 * p.sb_k, b_left);
+#pragma unroll
+        for (int d = 0; d < TB::kPerWave; ++d)
+          tb.template issue_one<FULL>(rb1, lds_b + st * kSB + kSB1, wave, lane, k_left, d);
+      }
+    };
+    issue(0, 0);
+    if (KT > 1) issue(1, 1);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < FB; ++j) read_b(j, 0, 0);
+#pragma unroll
+    for (int i = 0; i < FM; ++i) read_a(i, 0, 0);
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+
+    // MFMAs of the fragments in registers, reading (row block by row block, B in
+    // the last one) the fragments of k32 step s of stage st when rd.
+    auto step = [&](bool rd, int st, int s) {
+#pragma unroll
+      for (int i = 0; i < FM; ++i) {
+#pragma unroll
+        for (int j = 0; j < FB; ++j) {
+          mma16x32<F16>(acc[i][j], fb[j], fa[i]);
+          if (i == FM - 1 && rd) read_b(j, st, s);
+        }
+        if (rd) read_a(i, st, s);
+      }
+    };
+    // Tile kt in stage ST: step 0 (reading step 1 of ST), then wait for tile kt+1,
+    // barrier (stage ST is free: every wave holds step 1's fragments), refill ST
+    // with tile kt+2, step 1 (reading step 0 of tile kt+1).
+    auto tile = [&](int kt, auto st_c) {
+      constexpr int ST = decltype(st_c)::value;
+      const bool nx = kt + 1 < KT;
+      step(true, ST, 1);
+      asm volatile("s_waitcnt lgkmcnt(0)\n\ts_waitcnt vmcnt(0)" ::: "memory");
+      if (nx) {
+        __syncthreads();
+        if (kt + 2 < KT) issue(kt + 2, ST);
+      }
+      step(nx, ST ^ 1, 0);
+    };
+    for (int kt = 0; kt < KT; kt += 2) {
+      tile(kt, IntC<0>{});
+      if (kt + 1 < KT) tile(kt + 1, IntC<1>{});
+    }
+  };
+  if (mn_full && (p.K % BK) == 0) run(BoolC<true>{});
+  else run(BoolC<false>{});
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  mfma_drain(acc);
   tile_epilogue<BM, BN, WM, WN, NP>(p, epi, smem, acc, bb, m0, n0, mn_full, lane, wm, wn);
 }
 

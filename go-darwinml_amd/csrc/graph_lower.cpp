@@ -2558,14 +2558,14 @@ View Lowerer::emit_gemm_epilogue(int v, const std::vector<int>& mem, bool* fused
 
   // Tile shape: the precompiled kernels' choice for one operand; with two, a
   // 256 x (2 x 128) tile does the MMA work of one 256 x 256 tile.
-  // A single 256 x 256 product runs the 4-wave core (128 x 128 per wave).
   int BM = 128, BN = 128, WM = 2, WN = 2;
   bool four_wave = false;
   const int64_t t256 = d.B * ((d.M + 255) / 256) * ((d.N + 255) / 256);
-  // A VALU-heavy epilogue (transcendentals, long chains) runs faster on the 8-wave
+  // A VALU-heavy epilogue (transcendentals, long chains) runs faster on an 8-wave
   // core: with one wave per SIMD a wave issues a VALU instruction every few cycles,
-  // with two the SIMD's VALU stays busy (FusedDense + tanh-GELU: 894 -> 953 TFLOP/s),
-  // while the 4-wave core's main loop is a few percent faster for light epilogues.
+  // with two the SIMD's VALU stays busy (FusedDense + tanh-GELU: 894 -> 953 TFLOP/s
+  // against the 4-wave core), while the 4-wave MN-contiguous core's main loop is a
+  // few percent faster for light epilogues.
   int valu_weight = 0;
   for (int u : mem) {
     const Node& n = N[u];
@@ -2579,16 +2579,19 @@ View Lowerer::emit_gemm_epilogue(int v, const std::vector<int>& mem, bool* fused
   }
   const bool heavy_epilogue = valu_weight >= 8;
   // A K-contiguous, B MN-contiguous: the 8-wave 32-deep core for any epilogue, with
-  // one product or two sharing A.
-  bool eight_km = false;
+  // one product or two sharing A.  Other layouts: the 8-wave 64-deep 16x16x32 core,
+  // except both operands MN-contiguous with a light epilogue (4-wave 32-deep core).
+  bool eight_km = false, eight_x = false;
   if (NB == 1) {
     if (d.M >= 256 && d.N >= 256 && t256 >= 128 && ma && !mb) BM = 256, BN = 256, WM = 2, WN = 4, eight_km = true;
-    else if (d.M >= 256 && d.N >= 256 && t256 >= 128 && heavy_epilogue) BM = 256, BN = 256, WM = 2, WN = 4;
+    else if (d.M >= 256 && d.N >= 256 && t256 >= 128 && (mb || heavy_epilogue))
+      BM = 256, BN = 256, WM = 2, WN = 4, eight_x = true;
     else if (d.M >= 256 && d.N >= 256 && t256 >= 128) BM = 256, BN = 256, WM = 2, WN = 2, four_wave = true;
     else if (d.M >= 256 && d.N >= 128) BM = 256, BN = 128, WM = 2, WN = 2;
   } else if (d.M >= 256 && d.N >= 128) {
     BM = 256, BN = 128, WM = 2, WN = 4;
     eight_km = ma && !mb && d.B * ((d.M + 255) / 256) * ((d.N + 127) / 128) >= 128;
+    eight_x = !eight_km;
   }
   const int nt = WM * WN * 64;
   const int odt = os.dtype;
@@ -2645,10 +2648,11 @@ View Lowerer::emit_gemm_epilogue(int v, const std::vector<int>& mem, bool* fused
       << "  const ghip::GenEpi epi{a};\n";
   if (eight_km)
     src << "  ghip::gemm_bf16_body8km<ghip::GenEpi, false, " << NB << ">(p, epi);\n}\n";
-  else if (four_wave && !ma && !mb)
-    src << "  ghip::gemm_bf16_body4mn(p, epi);\n}\n";
+  else if (eight_x)
+    src << "  ghip::gemm_bf16_body8x<" << (ma ? "true" : "false") << ", " << (mb ? "true" : "false")
+        << ", ghip::GenEpi, false, " << NB << ">(p, epi);\n}\n";
   else if (four_wave)
-    src << "  ghip::gemm_bf16_body4<" << (ma ? "true" : "false") << ", " << (mb ? "true" : "false") << ">(p, epi);\n}\n";
+    src << "  ghip::gemm_bf16_body4mn(p, epi);\n}\n";
   else
     src << "  ghip::gemm_bf16_body<" << BM << ", " << BN << ", " << WM << ", " << WN << ", " << (ma ? "true" : "false") << ", "
         << (mb ? "true" : "false") << ", " << NB << ">(p, epi);\n}\n";
@@ -2675,7 +2679,7 @@ View Lowerer::emit_gemm_epilogue(int v, const std::vector<int>& mem, bool* fused
   for (auto& in : ins) rd.push_back(in.view.slot);
   std::ostringstream desc;
   // core: waves and k-depth of the main loop (km32: A in 64-deep, B in 32-deep stages)
-  const char* core = eight_km ? "8w-km32" : four_wave && !ma && !mb ? "4w-mn32" : four_wave ? "4w-k64" : "8w-k64";
+  const char* core = eight_km ? "8w-km32" : eight_x ? "8w-k64" : four_wave ? "4w-mn32" : "small";
   desc << fmt("gemm_batched+epilogue bf16 B=%lld M=%lld N=%lld K=%lld dots=%d tile=%dx%d waves=%d core=%s (%s) ops=%zu "
               "inputs=%zu [",
               (long long)d.B, (long long)d.M, (long long)d.N, (long long)d.K, NB, BM, BN * NB, WM * WN, core,

@@ -110,11 +110,11 @@ __global__ __launch_bounds__(256, 1) void gemm_bf16_kernel4mn(GemmParams p) {
   const StoreEpi<OutT> epi = store_epi<OutT>(p);
   gemm_bf16_body4mn<StoreEpi<OutT>, __is_same(InT, f16_t)>(p, epi);
 }
-// The 4-wave 256 x 256 core (128 x 128 per wave).
+// The 8-wave 256 x 256 16x16x32 core for B K-contiguous layouts (64-deep, two stages).
 template <bool A_K, bool B_K, typename InT, typename OutT>
-__global__ __launch_bounds__(256, 1) void gemm_bf16_kernel4(GemmParams p) {
+__global__ __launch_bounds__(512, 1) void gemm_bf16_kernel8x(GemmParams p) {
   const StoreEpi<OutT> epi = store_epi<OutT>(p);
-  gemm_bf16_body4<A_K, B_K, StoreEpi<OutT>, __is_same(InT, f16_t)>(p, epi);
+  gemm_bf16_body8x<A_K, B_K, StoreEpi<OutT>, __is_same(InT, f16_t)>(p, epi);
 }
 
 // ---------------------------------------------------------------------------
@@ -375,11 +375,11 @@ template <typename InT, typename OutT>
 static hipError_t launch_bf16_4w(GemmParams p, bool a_k, bool b_k, hipStream_t s) {
   p.tiles_m = static_cast<int>((p.M + 255) / 256);
   p.tiles_n = static_cast<int>((p.N + 255) / 256);
-  const dim3 grid(static_cast<unsigned>(p.batch * p.tiles_m * p.tiles_n)), block(256);
-  if (a_k && b_k) hipLaunchKernelGGL((gemm_bf16_kernel4<true, true, InT, OutT>), grid, block, 0, s, p);
+  const dim3 grid(static_cast<unsigned>(p.batch * p.tiles_m * p.tiles_n));
+  if (a_k && b_k) hipLaunchKernelGGL((gemm_bf16_kernel8x<true, true, InT, OutT>), grid, dim3(512), 0, s, p);
   else if (a_k) hipLaunchKernelGGL((gemm_bf16_kernel8km<InT, OutT>), grid, dim3(512), 0, s, p);
-  else if (b_k) hipLaunchKernelGGL((gemm_bf16_kernel4<false, true, InT, OutT>), grid, block, 0, s, p);
-  else hipLaunchKernelGGL((gemm_bf16_kernel4mn<InT, OutT>), grid, block, 0, s, p);
+  else if (b_k) hipLaunchKernelGGL((gemm_bf16_kernel8x<false, true, InT, OutT>), grid, dim3(512), 0, s, p);
+  else hipLaunchKernelGGL((gemm_bf16_kernel4mn<InT, OutT>), grid, dim3(256), 0, s, p);
   return hipGetLastError();
 }
 

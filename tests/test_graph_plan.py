@@ -311,10 +311,10 @@ def test_fused_dense_and_qkv_plans(be):
 
 def test_epilogue_core_follows_layout_and_epilogue_weight(be):
     """Large products with A K-contiguous and B N-contiguous (x . W, the DotGeneral
-    config's layout) run the 8-wave 32-deep core whatever the epilogue; other layouts
-    pick the 8-wave core when the fused epilogue is VALU-heavy (tanh-GELU: a
-    transcendental in a 10-op chain) and the 4-wave core for a light one (a residual
-    add)."""
+    config's layout) run the 8-wave 32-deep core whatever the epilogue; B
+    K-contiguous layouts the 8-wave 64-deep core; both operands MN-contiguous the
+    4-wave 32-deep core for a light epilogue (a residual add) and the 8-wave 64-deep
+    core for a VALU-heavy one (tanh-GELU: a transcendental in a 10-op chain)."""
     x = make_shape(BF16, 8, 1024, 2048)
     gelu = _plan(be, lambda f, xx, w, b: [f.FusedDense(xx, w, b, 1)], [x, make_shape(BF16, 2048, 8192), make_shape(BF16, 8192)])
     assert "gemm_batched+epilogue" in gelu and "waves=8" in gelu, gelu
@@ -324,11 +324,19 @@ def test_epilogue_core_follows_layout_and_epilogue_weight(be):
     # W stored [N, K] (x . W^T): B K-contiguous
     resid_t = _plan(be, lambda f, xx, w, r: [f.Add(f.DotGeneral(xx, [2], [], w, [1], []), r)],
                     [x, make_shape(BF16, 2048, 2048), x])
-    assert "gemm_batched+epilogue" in resid_t and "waves=4" in resid_t, resid_t
+    assert "gemm_batched+epilogue" in resid_t and "waves=8" in resid_t, resid_t
     gelu_t = _plan(be, lambda f, xx, w: [f.FusedGelu(f.DotGeneral(xx, [2], [], w, [1], []), False)],
                    [x, make_shape(BF16, 8192, 2048)])
     assert "gemm_batched+epilogue" in gelu_t and "waves=8" in gelu_t and "core=8w-k64" in gelu_t, gelu_t
-    assert "core=8w-km32" in gelu and "core=8w-km32" in resid and "core=4w-k64" in resid_t
+    assert "core=8w-km32" in gelu and "core=8w-km32" in resid and "core=8w-k64" in resid_t
+    # x^T . dY (both MN-contiguous): light epilogue on 4 waves, heavy on 8
+    xt = make_shape(BF16, 2048, 8192)
+    resid_mm = _plan(be, lambda f, xx, w, r: [f.Add(f.DotGeneral(xx, [0], [], w, [0], []), r)],
+                     [xt, make_shape(BF16, 2048, 2048), make_shape(BF16, 8192, 2048)])
+    assert "core=4w-mn32" in resid_mm and "waves=4" in resid_mm, resid_mm
+    gelu_mm = _plan(be, lambda f, xx, w: [f.FusedGelu(f.DotGeneral(xx, [0], [], w, [0], []), False)],
+                    [xt, make_shape(BF16, 2048, 2048)])
+    assert "core=8w-k64" in gelu_mm, gelu_mm
 
     # SwiGLU: two products sharing x in one kernel, on the 32-deep core for x . W
     def swiglu(f, xx, wg, wu):
