@@ -153,9 +153,11 @@ __device__ __forceinline__ void dma16(i32x4_t rsrc, uint32_t la, uint32_t voff) 
 // Wave-instruction i of a wave fills LDS bytes [blk*1024, blk*1024 + 1024),
 // blk = wave * kPerWave + i; lane l writes bytes l*16 .. l*16+15 of that block, so
 // the swizzle is applied by choosing which global chunk each lane fetches.
-// BK: k-depth of the tile (64; MN-contiguous tiles may also be 32 deep).  SW2:
-// MN-contiguous tiles use swz_n2 (read by 16x16x32 fragments) instead of swz_n.
-template <int R, bool KC, int NW, int BK = kBK, bool SW2 = false>
+// BK: k-depth of the tile (64; MN-contiguous tiles may also be 32 deep).  L16: the
+// tile is read as 16x16x32 fragments: an MN-contiguous tile uses swz_n2 instead of
+// swz_n; a K-contiguous one is laid out so that a fragment read has the access
+// pattern of a 32x32x16 one (see KC16 below).
+template <int R, bool KC, int NW, int BK = kBK, bool L16 = false>
 struct OperandTile {
   static_assert(BK == kBK || (!KC && BK == 32), "32-deep tiles are MN-contiguous only");
   static constexpr int kInstr = R * BK * 2 / 1024;
@@ -166,36 +168,70 @@ struct OperandTile {
   static constexpr int kCPR = KC ? BK / 8 : R / 8;  // 16-byte chunks per LDS row
   static constexpr int kRPI = 64 / kCPR;             // LDS rows per instruction
   static_assert(KC || R >= 128, "MN-major tiles need >= 16 chunks per LDS row");
+  // KC16: K-contiguous [R][64] tile for 16x16x32 fragments.  A 16x16x32 fragment
+  // (16 rows x 4 k-chunks) read from a plain [R][64] tile puts lanes l and l + 16 on
+  // the same row, which the LDS serves with 2-way bank conflicts (measured: 4
+  // conflict cycles per ds_read_b128).  So LDS row rho, chunk slot q ^ swz_k(rho)
+  // holds operand row m = 32 (rho / 32) + 16 (q / 4) + (rho % 32) / 2 and k-chunk
+  // kc = 4 ((q / 2) % 2) + 2 (q % 2) + rho % 2: the fragment of 16-row block b at k32
+  // step s is read as lane l -> LDS row 32 (b / 2) + 2 (l % 16) + (l / 16) % 2, chunk
+  // 4 (b % 2) + 2 s + l / 32 (32 distinct rows per chunk, measured conflict-free),
+  // and each load instruction (8 LDS rows) still fetches 8 whole 128-byte rows.
+  static constexpr bool KC16 = KC && L16;
+  static_assert(!KC16 || (R % 32 == 0 && 32 % (kPerWave * kRPI) == 0),
+                "KC16: a wave's loads stay inside one 32-row group");
 
-  // The swizzle depends on the parity of the instruction only: byte offsets of
-  // this lane's chunk for even / odd i; instruction i adds (i & ~1) * step.
-  uint32_t voff[2];
+  // Byte offsets of this lane's chunk.  The swizzle depends on the parity of the
+  // instruction only: even / odd i; instruction i adds (i & ~1) * step, step being
+  // kRPI operand rows (in the KC16 layout instruction i + 2 holds the operand rows
+  // 8 further on, so kRPI / 2).
+  static constexpr int kNV = 2;
+  uint32_t voff[kNV];
   uint32_t step;
   int mn_valid;
 
-  __device__ __forceinline__ static int row_of(int wave, int i, int lane) {
+  __device__ __forceinline__ static int lds_row(int wave, int i, int lane) {
     return (wave * kPerWave + i) * kRPI + lane / kCPR;
   }
+  // Operand row (m / n for K-contiguous tiles, k for MN-contiguous ones) and
+  // 16-byte chunk that the lane fetches in instruction i.
+  __device__ __forceinline__ static int row_of(int wave, int i, int lane) {
+    const int rho = lds_row(wave, i, lane);
+    if constexpr (KC16) {
+      const int q = (lane % kCPR) ^ swz_k(rho);
+      return 32 * (rho / 32) + 16 * (q / 4) + (rho % 32) / 2;
+    } else {
+      return rho;
+    }
+  }
   __device__ __forceinline__ static int chunk_of(int wave, int i, int lane) {
-    const int r = row_of(wave, i, lane);
-    return KC ? (lane % kCPR) ^ swz_k(r) : (lane % kCPR) ^ (SW2 ? swz_n2(r) : swz_n(r));
+    const int rho = lds_row(wave, i, lane);
+    if constexpr (KC16) {
+      const int q = (lane % kCPR) ^ swz_k(rho);
+      return 4 * ((q / 2) % 2) + 2 * (q % 2) + rho % 2;
+    } else {
+      return KC ? (lane % kCPR) ^ swz_k(rho) : (lane % kCPR) ^ (L16 ? swz_n2(rho) : swz_n(rho));
+    }
   }
   // s_mn / s_k: element strides of the operand along its rows (m or n) and k.
   __device__ __forceinline__ void init(int wave, int lane, int64_t s_mn, int64_t s_k, int64_t valid) {
     mn_valid = valid > R ? R : static_cast<int>(valid);
 #pragma unroll
-    for (int par = 0; par < 2; ++par) {
+    for (int par = 0; par < kNV; ++par) {
       const int r = row_of(wave, par, lane);
       const int c = chunk_of(wave, par, lane);
       voff[par] = KC ? static_cast<uint32_t>((r * s_mn + c * 8) * 2)
                      : static_cast<uint32_t>((r * s_k + c * 8) * 2);
     }
-    step = static_cast<uint32_t>(kRPI * (KC ? s_mn : s_k) * 2);
+    step = static_cast<uint32_t>((KC16 ? kRPI / 2 : kRPI) * (KC ? s_mn : s_k) * 2);
+  }
+  __device__ __forceinline__ uint32_t off(int i) const {
+    return voff[i & 1] + static_cast<uint32_t>(i & ~1) * step;
   }
   // Instruction i of this wave's share (see issue()).
   template <bool FULL>
   __device__ __forceinline__ void issue_one(i32x4_t rs, uint32_t lds, int wave, int lane, int k_left, int i) const {
-    const uint32_t v = voff[i & 1] + static_cast<uint32_t>(i & ~1) * step;
+    const uint32_t v = off(i);
     if constexpr (FULL) {
       dma16(rs, lds + (wave * kPerWave + i) * 1024, v);
     } else {
@@ -212,7 +248,7 @@ struct OperandTile {
   __device__ __forceinline__ void issue(i32x4_t rs, uint32_t lds, int wave, int lane, int k_left) const {
 #pragma unroll
     for (int i = 0; i < kPerWave; ++i) {
-      const uint32_t v = voff[i & 1] + static_cast<uint32_t>(i & ~1) * step;
+      const uint32_t v = off(i);
       if constexpr (FULL) {
         dma16(rs, lds + (wave * kPerWave + i) * 1024, v);
       } else {
@@ -764,7 +800,7 @@ __device__ __forceinline__ void gemm_bf16_body8km(const GemmParams& p, const Epi
   constexpr int NW = WM * WN;
   constexpr int TM = BM / WM, TN = BN / WN;
   constexpr int FM = TM / 16, FN = TN / 16, FB = NP * FN;  // 16x16 blocks per wave
-  using TA = OperandTile<BM, true, NW, 2 * BK>;
+  using TA = OperandTile<BM, true, NW, 2 * BK, true>;
   using TB = OperandTile<BN, false, NW, BK, true>;
   constexpr int NA = TA::kPerWave;       // A loads per wave per super-tile
   constexpr int NB = NP * TB::kPerWave;  // B loads per wave per tile
@@ -806,18 +842,21 @@ __device__ __forceinline__ void gemm_bf16_body8km(const GemmParams& p, const Epi
       for (int v = 0; v < 4; ++v) acc[i][j][v] = 0.f;
 
   // Per-lane LDS base pointers (address space 3, so stage and block offsets fold
-  // into the reads' immediate offsets): A for k32 step as (0, 1) of a super-tile
-  // (lane l: row l % 16 of a block, k chunk as * 4 + l / 16), B per column block
-  // (the swizzle mixes the block's chunk bits; lane l: column l % 16 of the block,
-  // k-rows 8 (l / 16) + (l % 16) / 4 and + 4 for the two transpose reads).
+  // into the reads' immediate offsets): A per block parity and k32 step as (0, 1)
+  // of a super-tile (the KC16 layout: lane l reads LDS row 32 (b / 2) + 2 (l % 16) +
+  // (l / 16) % 2, chunk 4 (b % 2) + 2 as + l / 32 for block b), B per column block (the swizzle
+  // mixes the block's chunk bits; lane l: column l % 16 of the block, k-rows
+  // 8 (l / 16) + (l % 16) / 4 and + 4 for the two transpose reads).
   typedef GHIP_LDS const uint16_t* lds_p;
   lds_p const lds0 = (lds_p)((GHIP_LDS void*)smem);
-  lds_p abase[2], bbase[FN];
+  lds_p abase[2][2], bbase[FN];
 #pragma unroll
-  for (int as = 0; as < 2; ++as) {
-    const int row = wm * TM + (lane & 15);
-    abase[as] = lds0 + 2 * kSB + row * (2 * BK) + (((4 * as + (lane >> 4)) ^ swz_k(row)) * 8);
-  }
+  for (int par = 0; par < 2; ++par)
+#pragma unroll
+    for (int as = 0; as < 2; ++as) {
+      const int rho = wm * TM + 2 * (lane & 15) + ((lane >> 4) & 1);
+      abase[par][as] = lds0 + 2 * kSB + rho * (2 * BK) + (((4 * par + 2 * as + (lane >> 5)) ^ swz_k(rho)) * 8);
+    }
 #pragma unroll
   for (int j = 0; j < FN; ++j) {
     const int kl = 8 * (lane >> 4) + ((lane & 15) >> 2);
@@ -826,7 +865,7 @@ __device__ __forceinline__ void gemm_bf16_body8km(const GemmParams& p, const Epi
   }
   bf16x8_t fa[FM], fb[FB];
   auto read_a = [&](int i, int sa, int as) {  // row block i from A stage sa, k32 step as
-    fa[i] = *(GHIP_LDS const bf16x8_t*)(abase[as] + sa * (kSA / 2) + i * 16 * (2 * BK));
+    fa[i] = *(GHIP_LDS const bf16x8_t*)(abase[i & 1][as] + sa * (kSA / 2) + (i >> 1) * 32 * (2 * BK));
   };
   auto read_b = [&](int jj, int sb) {  // column block jj (product jj / FN) from B stage sb
     lds_p p0 = bbase[jj % FN] + sb * (kSB / 2) + (jj / FN) * (kSB1 / 2);
@@ -952,8 +991,8 @@ __device__ __forceinline__ void gemm_bf16_body8x(const GemmParams& p, const Epi&
   constexpr int NW = WM * WN;
   constexpr int TM = BM / WM, TN = BN / WN;
   constexpr int FM = TM / 16, FN = TN / 16, FB = NP * FN;
-  using TA = OperandTile<BM, A_K, NW, BK, !A_K>;
-  using TB = OperandTile<BN, B_K, NW, BK, !B_K>;
+  using TA = OperandTile<BM, A_K, NW, BK, true>;
+  using TB = OperandTile<BN, B_K, NW, BK, true>;
   constexpr int kSA = BM * BK * 2, kSB1 = BN * BK * 2, kSB = NP * kSB1;  // bytes per stage
   constexpr int kLdsBytes = 2 * kSA + 2 * kSB;
   __shared__ __attribute__((aligned(1024))) uint16_t smem[kLdsBytes / 2];
@@ -993,17 +1032,19 @@ __device__ __forceinline__ void gemm_bf16_body8x(const GemmParams& p, const Epi&
   lds_p const ldsA = (lds_p)((GHIP_LDS void*)smem);
   lds_p const ldsB = ldsA + kSA;  // halfwords: after the two A stages
   // Per-lane LDS base pointers (address space 3, so stage, step and block offsets
-  // fold into the reads' immediate offsets): a K-contiguous operand ([R][64]) has
-  // one per k32 step (lane l: row l % 16 of a block, k chunk 4 s + l / 16), an
-  // MN-contiguous one ([64][R]) one per block (the swizzle mixes the block's chunk
-  // bits; lane l: column l % 16, k-rows 8 (l / 16) + (l % 16) / 4 and + 4).
-  constexpr int NBA = A_K ? 2 : FM, NBB = B_K ? 2 : FN;
+  // fold into the reads' immediate offsets): a K-contiguous operand (KC16 layout)
+  // has one per block parity and k32 step (lane l reads LDS row 32 (b / 2) +
+  // 2 (l % 16) + (l / 16) % 2, chunk 4 (b % 2) + 2 s + l / 32 for block b), an
+  // MN-contiguous one ([64][R]) one
+  // per block (the swizzle mixes the block's chunk bits; lane l: column l % 16,
+  // k-rows 8 (l / 16) + (l % 16) / 4 and + 4).
+  constexpr int NBA = A_K ? 4 : FM, NBB = B_K ? 4 : FN;
   lds_p abase[NBA], bbase[NBB];
 #pragma unroll
   for (int q = 0; q < NBA; ++q) {
     if constexpr (A_K) {
-      const int row = wm * TM + (lane & 15);
-      abase[q] = ldsA + row * BK + (((4 * q + (lane >> 4)) ^ swz_k(row)) * 8);
+      const int rho = wm * TM + 2 * (lane & 15) + ((lane >> 4) & 1);
+      abase[q] = ldsA + rho * BK + (((4 * (q >> 1) + 2 * (q & 1) + (lane >> 5)) ^ swz_k(rho)) * 8);
     } else {
       const int kl = 8 * (lane >> 4) + ((lane & 15) >> 2);
       const int nl = wm * TM + q * 16 + 4 * (lane & 3);
@@ -1013,8 +1054,8 @@ __device__ __forceinline__ void gemm_bf16_body8x(const GemmParams& p, const Epi&
 #pragma unroll
   for (int q = 0; q < NBB; ++q) {
     if constexpr (B_K) {
-      const int row = wn * TN + (lane & 15);
-      bbase[q] = ldsB + row * BK + (((4 * q + (lane >> 4)) ^ swz_k(row)) * 8);
+      const int rho = wn * TN + 2 * (lane & 15) + ((lane >> 4) & 1);
+      bbase[q] = ldsB + rho * BK + (((4 * (q >> 1) + 2 * (q & 1) + (lane >> 5)) ^ swz_k(rho)) * 8);
     } else {
       const int kl = 8 * (lane >> 4) + ((lane & 15) >> 2);
       const int nl = wn * TN + q * 16 + 4 * (lane & 3);
@@ -1029,12 +1070,13 @@ __device__ __forceinline__ void gemm_bf16_body8x(const GemmParams& p, const Epi&
   };
   // block i of A / jj of B at k32 step s (0, 1) of stage st
   auto read_a = [&](int i, int st, int s) {
-    if constexpr (A_K) fa[i] = *(GHIP_LDS const bf16x8_t*)(abase[s] + st * (kSA / 2) + i * 16 * BK);
+    if constexpr (A_K) fa[i] = *(GHIP_LDS const bf16x8_t*)(abase[2 * (i & 1) + s] + st * (kSA / 2) + (i >> 1) * 32 * BK);
     else fa[i] = rd_tr(abase[i] + st * (kSA / 2) + s * 32 * BM, BM);
   };
   auto read_b = [&](int jj, int st, int s) {
     const int h = jj / FN, j = jj % FN;
-    if constexpr (B_K) fb[jj] = *(GHIP_LDS const bf16x8_t*)(bbase[s] + st * (kSB / 2) + h * (kSB1 / 2) + j * 16 * BK);
+    if constexpr (B_K)
+      fb[jj] = *(GHIP_LDS const bf16x8_t*)(bbase[2 * (j & 1) + s] + st * (kSB / 2) + h * (kSB1 / 2) + (j >> 1) * 32 * BK);
     else fb[jj] = rd_tr(bbase[j] + st * (kSB / 2) + h * (kSB1 / 2) + s * 32 * BN, BN);
   };
 
