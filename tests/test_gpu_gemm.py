@@ -144,6 +144,27 @@ def test_mn_major_core_matches_k_major_core(cuda, K, dt):
     assert rel_err(got, ref) <= 1e-4
 
 
+@pytest.mark.parametrize("K", [16, 32, 1000, 1024])
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])
+def test_cores_bit_identical_across_layouts(cuda, K, dt):
+    """The same values in all four operand layouts take four code paths at >= 128
+    tiles of 256 x 256: A K- / B N-contiguous the 8-wave 32-deep 16x16x32 core, B
+    K-contiguous (A either way) the 8-wave 64-deep 16x16x32 core, both MN-contiguous
+    the 4-wave 32x32x16 core.  The products must agree bit for bit, for K inside one
+    k-tile (16, 32: the MFMAs run straight into the epilogue), a ragged K and one that
+    reaches the steady-state loop; plus sampled entries against fp64."""
+    a_k = synth.normal_device(3701, (1, 2048, K), std=0.125, device=cuda, dtype=dt)       # A K-contiguous
+    b_n = synth.normal_device(3702, (1, K, 4096), std=0.125, device=cuda, dtype=dt)       # B N-contiguous
+    a_m = a_k.transpose(1, 2).contiguous().transpose(1, 2)
+    b_k = b_n.transpose(1, 2).contiguous().transpose(1, 2)
+    assert a_k.stride(2) == 1 and a_m.stride(1) == 1 and b_n.stride(2) == 1 and b_k.stride(1) == 1
+    outs = [ops.gemm(a, b) for a, b in ((a_k, b_n), (a_k, b_k), (a_m, b_k), (a_m, b_n))]
+    for c in outs[1:]:
+        assert torch.equal(c, outs[0])
+    got, ref = _sampled_check(a_k, b_n, outs[0], seed=14)
+    assert rel_err(got, ref) <= (1e-2 if dt == torch.bfloat16 else 1e-3)
+
+
 @pytest.mark.parametrize("shape", SHAPES)
 def test_f16_layouts(cuda, shape):
     """f16 DotGeneral (the f16 MFMA) on the small-tile cores and the generic path."""
