@@ -267,7 +267,8 @@ def make_cases(only=None):
         c = torch.empty((B, M, N), device=dev, dtype=dtype)
         return Case(f"dot_general_{tag}", lambda i: ops.gemm(a, b, out=c),
                     flops_per_step=2 * B * M * N * K, bound="mfma", peak=peak, dtype=tag,
-                    kernel="gemm_bf16_kernel" if tag == "bf16" else "gemm_f32_kernel",
+                    kernel="gemm_bf16_kernel8km<bf16_t, bf16_t>" if tag == "bf16"
+                    else "gemm_f32_kernel<256, 256, 2, 4, true, false, float>",
                     config={"workload": f"DotGeneral [8,2048,4096]x[8,4096,4096] lc=[2] lb=[0] rc=[1] rb=[0], {tag} in, fp32 accumulate, {tag} out"})
 
     def vendor_dot_case():
@@ -292,7 +293,7 @@ def make_cases(only=None):
         return Case("attention_bf16", lambda i: ops.sdpa(q, k, v, D ** -0.5, True, out=o),
                     flops_per_step=2 * 2 * B * H * S * S * D, bound="mfma",
                     executed_flops_per_step=2 * 2 * B * H * D * S * (S + 1) // 2,
-                    peak=BF16_PEAK_TFLOPS, dtype="bf16", kernel="sdpa_fwd_kernel",
+                    peak=BF16_PEAK_TFLOPS, dtype="bf16", kernel="sdpa_fwd_kernel<128, false, 0>",
                     config={"workload": "SDPA causal B4 H16 S2048 D128 bf16, one fused kernel "
                                         "(Q.K^T, scale, causal mask, online softmax, P.V); flops "
                                         "counted for both products over the full S x S matrix, "
