@@ -144,6 +144,35 @@ def test_mn_major_core_matches_k_major_core(cuda, K, dt):
     assert rel_err(got, ref) <= 1e-4
 
 
+@pytest.mark.parametrize("shape", [(2, 2056, 2312, 200), (1, 4104, 2056, 72), (3, 1032, 2568, 520)])
+@pytest.mark.parametrize("a_t", [False, True])
+@pytest.mark.parametrize("b_t", [False, True])
+def test_16bit_large_grids_ragged_layouts(cuda, shape, a_t, b_t):
+    """>= 128 tiles of 256 x 256 with ragged M, N and K (k-tiles of 32 and 64 cut
+    short) and batches, every operand majorness: sampled entries and the whole last
+    row tile and column tile against fp64, bf16 and fp32 outputs."""
+    B, M, N, K = shape
+    ta = synth.normal_device(3801 + M, (B, M, K), std=0.125, device=cuda, dtype=torch.bfloat16)
+    tb = synth.normal_device(3802 + N, (B, K, N), std=0.125, device=cuda, dtype=torch.bfloat16)
+    if a_t:
+        ta = ta.transpose(1, 2).contiguous().transpose(1, 2)
+    if b_t:
+        tb = tb.transpose(1, 2).contiguous().transpose(1, 2)
+    c16 = ops.gemm(ta, tb)
+    got, ref = _sampled_check(ta, tb, c16, seed=15)
+    assert rel_err(got, ref) <= 1e-2
+    c32 = ops.gemm(ta, tb, out_dtype=torch.float32)
+    got, ref = _sampled_check(ta, tb, c32, seed=16)
+    assert rel_err(got, ref) <= 1e-4
+    a = ta.float().cpu().numpy()
+    b = tb.float().cpu().numpy()
+    m0, n0 = (M - 1) // 256 * 256, (N - 1) // 256 * 256
+    e = c32[:, m0:, :].cpu().numpy()
+    assert rel_err(e, orc.dot_general(np.ascontiguousarray(a[:, m0:]), [2], [0], b, [1], [0])) <= 1e-4
+    e = c32[:, :, n0:].cpu().numpy()
+    assert rel_err(e, orc.dot_general(a, [2], [0], np.ascontiguousarray(b[:, :, n0:]), [1], [0])) <= 1e-4
+
+
 @pytest.mark.parametrize("K", [16, 32, 1000, 1024])
 @pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])
 def test_cores_bit_identical_across_layouts(cuda, K, dt):
