@@ -2,8 +2,10 @@
 //
 // bf16 / f16 path (the MFMA path the metric is quoted on): the cores live in
 // gemm_bf16_dev.h (shared with the Compile-time generated epilogue GEMMs); the
-// kernels here instantiate them with a plain store epilogue.  256 x 256 tiles
-// run the 4-wave core, smaller tiles the 8- / 4-wave 128 x 64 core.
+// kernels here instantiate them with a plain store epilogue.  Grids of >= 128
+// 256 x 256 tiles run the 8-wave 16x16x32 cores (A K- / B N-contiguous: 32-deep
+// k-steps; B K-contiguous: 64-deep) or, with both operands MN-contiguous, the
+// 4-wave 32-deep core; smaller grids the 8- / 4-wave 32x32x16 core.
 // fp32 path: v_mfma_f32_32x32x2f32 over LDS-DMA tiles (below).
 // Anything the vector paths cannot address (odd strides, unaligned bases,
 // negative strides, > 2 GiB per batch slice) runs a generic LDS-tiled kernel.
