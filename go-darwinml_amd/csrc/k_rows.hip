@@ -33,8 +33,11 @@ namespace ghip {
 enum RowOp { kSoftmax = 0, kLogSoftmax = 1, kRmsNorm = 2, kLayerNorm = 3, kMaskedSoftmax = 4 };
 
 struct RowParams {
+  // The fields every kernel reads first, adjacent (one scalar load fetches them).
   const void* x;
   void* y;
+  int64_t rows;
+  int64_t n;
   const void* gamma;
   const void* beta;
   // kMaskedSoftmax: a boolean keep-mask (uint8) or an additive mask in the
@@ -43,8 +46,6 @@ struct RowParams {
   const void* mask;
   int mask_kind;         // 0 none, 1 keep-mask, 2 additive
   int64_t m_sb, m_sh, m_sq, m_sk;
-  int64_t rows;
-  int64_t n;
   int64_t sq;            // rows per attention matrix (kMaskedSoftmax)
   int64_t heads;         // H (kMaskedSoftmax)
   float eps;
