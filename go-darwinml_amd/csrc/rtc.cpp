@@ -44,17 +44,17 @@ int rtc_get(GHipBackend* be, const std::string& src, const std::string& entry, R
             GHipError* err) {
   std::lock_guard<std::mutex> lk(g_mu);
   Entry& e = g_cache[src];
-  if (e.code.empty()) {
-    // GHIP_RTC_DUMP=<dir>: keep a copy of every generated source (for reading
-    // the generated code and its ISA offline).
-    if (const char* dir = getenv("GHIP_RTC_DUMP")) {
-      const std::string path = std::string(dir) + "/" + entry + "_" +
-                               std::to_string(std::hash<std::string>()(src)) + ".hip";
-      if (FILE* f = fopen(path.c_str(), "w")) {
-        fwrite(src.data(), 1, src.size(), f);
-        fclose(f);
-      }
+  // GHIP_RTC_DUMP=<dir>: keep a copy of every generated source (for reading the
+  // generated code and its ISA offline), also when the compiled code is cached.
+  if (const char* dir = getenv("GHIP_RTC_DUMP")) {
+    const std::string path = std::string(dir) + "/" + entry + "_" +
+                             std::to_string(std::hash<std::string>()(src)) + ".hip";
+    if (FILE* f = fopen(path.c_str(), "w")) {
+      fwrite(src.data(), 1, src.size(), f);
+      fclose(f);
     }
+  }
+  if (e.code.empty()) {
     hiprtcProgram prog;
     if (hiprtcCreateProgram(&prog, src.c_str(), "fused.hip", 0, nullptr, nullptr) != HIPRTC_SUCCESS) {
       g_cache.erase(src);
