@@ -56,6 +56,8 @@ extern "C" int ghip_exec_execute_noalloc(GHipExecutable* e, GHipBuffer* const* i
   for (int i = 0; i < nout; ++i) {
     if (!outputs || !outputs[i] || !outputs[i]->valid)
       return set_error(err, GHIP_ERR_INVALID_ARG, "ExecuteNoAlloc: output #%d is not a valid buffer", i);
+    if (outputs[i]->backend != e->backend)
+      return set_error(err, GHIP_ERR_INVALID_ARG, "ExecuteNoAlloc: output #%d belongs to another backend", i);
     if (outputs[i]->shape != e->out_shapes[i])
       return set_error(err, GHIP_ERR_INVALID_ARG, "ExecuteNoAlloc: output #%d shape mismatch: expected %s, got %s",
                        i, e->out_shapes[i].str().c_str(), outputs[i]->shape.str().c_str());

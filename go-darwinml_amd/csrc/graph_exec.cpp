@@ -175,6 +175,11 @@ int check_execute_args(GHipExecutable* e, GHipBuffer* const* inputs, int n, int 
   for (int i = 0; i < n; ++i) {
     if (!inputs[i] || !inputs[i]->valid)
       return set_error(err, GHIP_ERR_INVALID_ARG, "Execute: input #%d is not a valid buffer", i);
+    // A buffer of another backend lives on another stream (and maybe device):
+    // reading it, or taking it over by donation into this backend's allocator,
+    // would race with that stream's work.
+    if (inputs[i]->backend != be)
+      return set_error(err, GHIP_ERR_INVALID_ARG, "Execute: input #%d belongs to another backend", i);
     if (inputs[i]->shape != e->in_shapes[i])
       return set_error(err, GHIP_ERR_INVALID_ARG, "Execute: input #%d shape mismatch: expected %s, got %s", i,
                        e->in_shapes[i].str().c_str(), inputs[i]->shape.str().c_str());

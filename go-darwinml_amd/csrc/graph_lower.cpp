@@ -1302,11 +1302,21 @@ struct Lowerer {
       // iterations reads back O(log N + N / kMaxBatch) times and runs at most
       // about twice its body launches.  The ring's size is bounded by a byte
       // budget for large states.
+      //
+      // When cond or body itself runs host-driven steps (a nested While, If or
+      // Call, i.e. a plan with sub-plans), an iteration past the exit is not just
+      // computation: a nested loop on post-exit state may not terminate, and an
+      // error from it would fail a program the sequential loop completes.  Such
+      // loops run without speculation: cond, read its predicate, then the body
+      // only when it is true.
       const size_t ns = static_cast<size_t>(n.i0), ncc = static_cast<size_t>(n.i1);
+      GHipExecutable* cond = subs[0];
+      GHipExecutable* body = subs[1];
+      const bool speculate = cond->plan.subs.empty() && body->plan.subs.empty();
       size_t state_bytes = 0;
       for (size_t i = 0; i < ns; ++i) state_bytes += n.outs[i].bytes();
       constexpr size_t kRingBudget = size_t{256} << 20;
-      int kmax = 8;
+      int kmax = speculate ? 8 : 1;
       while (kmax > 1 && (static_cast<size_t>(kmax) + 1) * state_bytes > kRingBudget) kmax /= 2;
       std::vector<std::vector<View>> H(kmax + 1);
       for (int r = 0; r <= kmax; ++r)
@@ -1319,11 +1329,12 @@ struct Lowerer {
       bs.dims = {kmax};
       View pv = fresh(bs);
       wr.push_back(pv.slot);
-      GHipExecutable* cond = subs[0];
-      GHipExecutable* body = subs[1];
-      add_step(fmt("while (%zu state values; cond and body enqueued in speculative batches of up to %d "
-                   "iterations, one predicate read per batch)", ns, kmax),
-               rd, wr, [=](ExecState& st, GHipError* e) -> int {
+      const std::string desc =
+          speculate ? fmt("while (%zu state values; cond and body enqueued in speculative batches of up to %d "
+                          "iterations, one predicate read per batch)", ns, kmax)
+                    : fmt("while (%zu state values; cond or body runs host-driven control flow, so no "
+                          "speculation: one predicate read per iteration, body only when it is true)", ns);
+      add_step(desc, rd, wr, [=](ExecState& st, GHipError* e) -> int {
                  std::vector<std::vector<void*>> h(kmax + 1);
                  for (int r = 0; r <= kmax; ++r) h[r] = ptrs(st, H[r], odt, 0, ns);
                  for (size_t i = 0; i < ns; ++i) {
@@ -1335,6 +1346,31 @@ struct Lowerer {
                  const std::vector<void*> bcap = ptrs(st, ins, idt, ns + ncc, nin);
                  uint8_t* pp = reinterpret_cast<uint8_t*>(st.ptr(pv, GHIP_DTYPE_BOOL));
                  int base = 0, k = 1, last = -1;
+                 if (!speculate) {
+                   for (long done = 0; last < 0; ++done) {
+                     if (done >= kMaxWhileIterations)
+                       return set_error(e, GHIP_ERR_STATE, "While: exceeded maximum iterations (%ld)",
+                                        kMaxWhileIterations);
+                     const int cur = base, nxt = base ^ 1;
+                     std::vector<void*> cin(h[cur]);
+                     cin.insert(cin.end(), ccap.begin(), ccap.end());
+                     void* p0 = pp;
+                     int rc = run_plan(cond, cin.data(), &p0, e);
+                     if (rc != GHIP_OK) return rc;
+                     bool pred = false;
+                     rc = read_bool(pp, st.stream, &pred, e);
+                     if (rc != GHIP_OK) return rc;
+                     if (!pred) {
+                       last = cur;
+                       break;
+                     }
+                     std::vector<void*> bin(h[cur]);
+                     bin.insert(bin.end(), bcap.begin(), bcap.end());
+                     rc = run_plan(body, bin.data(), h[nxt].data(), e);
+                     if (rc != GHIP_OK) return rc;
+                     base = nxt;
+                   }
+                 }
                  for (long done = 0; last < 0;) {
                    if (done >= kMaxWhileIterations)
                      return set_error(e, GHIP_ERR_STATE, "While: exceeded maximum iterations (%ld)", kMaxWhileIterations);
@@ -2372,11 +2408,25 @@ View Lowerer::emit_cluster(int root, int v) {
       body << member_stmt(u, expr, "v" + std::to_string(u));
     }
   }
+  // Slots every read of which is at the output's own element index (linear,
+  // offset 0, same element size): the output may overwrite them in place (a
+  // donated input), so those operands and the output are not declared
+  // __restrict__: with donation they are one buffer.
+  std::vector<int> inplace;
+  for (auto& in : ins) {
+    bool ok = true;
+    for (auto& o2 : ins)
+      if (o2.view.slot == in.view.slot)
+        ok = ok && o2.linear && o2.view.offset == 0 && dtype_size(N[o2.value].shape.dtype) == dtype_size(os.dtype);
+    if (ok && std::find(inplace.begin(), inplace.end(), in.view.slot) == inplace.end()) inplace.push_back(in.view.slot);
+  }
+  auto may_alias = [&](const View& w) { return std::find(inplace.begin(), inplace.end(), w.slot) != inplace.end(); };
   std::ostringstream src;
   src << kRtcPrelude << R"(extern "C" __global__ void __launch_bounds__(256) fused(
 )";
-  for (size_t k = 0; k < ins.size(); ++k) src << "    const void* __restrict__ p_in" << k << ",\n";
-  src << "    void* __restrict__ p_out, long long n) {\n";
+  for (size_t k = 0; k < ins.size(); ++k)
+    src << "    const void* " << (may_alias(ins[k].view) ? "" : "__restrict__ ") << "p_in" << k << ",\n";
+  src << "    void* " << (inplace.empty() ? "__restrict__ " : "") << "p_out, long long n) {\n";
   src << "  for (long long i = (long long)blockIdx.x * 256 + threadIdx.x; i < n; i += (long long)gridDim.x * 256) {\n";
   if (need_idx) {
     src << "    long long q = i;\n";
@@ -2400,16 +2450,6 @@ View Lowerer::emit_cluster(int root, int v) {
     rd.push_back(in.view.slot);
     in_views.push_back(in.view);
     in_dt.push_back(N[in.value].shape.dtype);
-  }
-  // Slots every read of which is at the output's own element index (linear,
-  // offset 0, same element size): the output may overwrite them in place.
-  std::vector<int> inplace;
-  for (auto& in : ins) {
-    bool ok = true;
-    for (auto& o2 : ins)
-      if (o2.view.slot == in.view.slot)
-        ok = ok && o2.linear && o2.view.offset == 0 && dtype_size(N[o2.value].shape.dtype) == dtype_size(os.dtype);
-    if (ok && std::find(inplace.begin(), inplace.end(), in.view.slot) == inplace.end()) inplace.push_back(in.view.slot);
   }
   std::ostringstream d;
   d << "fused_elementwise " << os.str() << " ops=" << mem.size() << " inputs=" << ins.size() << " [";

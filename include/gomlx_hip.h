@@ -70,7 +70,8 @@ int ghip_device_name(int device, char* buf, size_t buflen, GHipError* err);
  * Direct op entry points (device pointers, async on `stream`).
  * These are the kernels the graph lowering launches; they are exported so a
  * host without Go (tests, benchmarks) can drive them through the same ABI.
- * dtype: GHIP_DTYPE_FLOAT32 or GHIP_DTYPE_BFLOAT16 unless stated.
+ * dtype: GHIP_DTYPE_FLOAT32, GHIP_DTYPE_BFLOAT16 or GHIP_DTYPE_FLOAT16 unless
+ * stated (16-bit values are raw bit patterns; statistics and accumulation fp32).
  * ======================================================================== */
 
 /* Softmax (log_softmax != 0: log-softmax) of each length-n row of x [rows, n].
@@ -115,8 +116,9 @@ int ghip_layernorm_rows(int dtype, const void* x, const void* gamma, const void*
  * (dotgeneral.go:65-164 -> mpsgraph_matmul, bridge.m:684-700):
  *   c[b, m, n] = sum_k a[b, m, k] * b[b, k, n]
  * with every operand addressed by ELEMENT strides (so transposed / permuted
- * views need no copy).  ab_dtype is the dtype of a and b (FLOAT32 or BFLOAT16);
- * c_dtype the output dtype (FLOAT32 or BFLOAT16).  Accumulation is fp32.
+ * views need no copy).  ab_dtype is the dtype of a and b (FLOAT32, BFLOAT16 or
+ * FLOAT16); c_dtype the output dtype (FLOAT32, or ab_dtype when that is 16-bit).
+ * Accumulation is fp32.
  * Requires sc_n == 1. */
 int ghip_gemm_batched(int ab_dtype, int c_dtype, int64_t batch, int64_t M, int64_t N,
                       int64_t K, const void* a, int64_t sa_b, int64_t sa_m, int64_t sa_k,
@@ -189,8 +191,10 @@ int ghip_iota(int dtype, void* out, int64_t outer, int64_t n, int64_t inner, voi
  * whole graph once: it fuses softmax / RMSNorm / LayerNorm / attention patterns
  * into the row kernels above, DotGeneral into the batched GEMM with operand
  * transposes folded into strides, and chains of elementwise ops into generated
- * kernels (hipRTC, gfx950).  Execute launches the plan on the backend's stream
- * with device-resident buffers and synchronizes once at the end.
+ * kernels (hipRTC, gfx950).  Execute enqueues the plan on the backend's stream
+ * with device-resident buffers and returns without synchronizing (results are
+ * ordered on that stream; BufferToFlatData waits for them).  Graphs with While /
+ * If synchronize inside Execute to read their predicates.
  * ======================================================================== */
 typedef struct GHipBackend GHipBackend;
 typedef struct GHipBuilder GHipBuilder;
@@ -375,8 +379,12 @@ int ghip_fn_value_shape(GHipFunction* f, GHipValue v, int* dtype, int64_t* dims,
  * after its parameters).  Call / While / If write their outputs' value ids into
  * outs (room for max_outs) and return the number of outputs, or -1 with err set.
  * The loops and branches run on the host, between launches of the compiled
- * closures on the backend's stream; state stays in device memory, and each
- * While iteration and each If read back one bool. */
+ * closures on the backend's stream; state stays in device memory.  An If reads
+ * back one bool.  A While enqueues cond and body in speculative batches (1, 2,
+ * 4, then up to 8 iterations) and reads back each batch's predicates in one
+ * copy, keeping the state before the first false one; a While whose cond or body
+ * itself contains Call / While / If runs without speculation (one predicate read
+ * per iteration, the body only when it is true). */
 /* NewFunction (builder.go:57-70): a named function, the target of Call. */
 GHipFunction* ghip_builder_new_function(GHipBuilder* bl, const char* name, GHipError* err);
 /* Closure (function.go:120-133): a function nested in f. */
@@ -398,8 +406,10 @@ int ghip_fn_if(GHipFunction* f, GHipValue pred, GHipFunction* true_branch,
  * ..., returning a scalar bool "lhs before rhs") holds; ties keep their input
  * order (every sort is stable).  The comparator is compiled into the sort kernel:
  * it may use elementwise ops, scalar constants and captured scalars.  Each row
- * along the axis is sorted in one workgroup's LDS; rows that do not fit (about
- * 16K elements for one 4-byte key) return GHIP_ERR_UNSUPPORTED at Compile. */
+ * along the axis is sorted by one workgroup: in LDS when its keys and indices fit
+ * (about 16K elements for one 4-byte key), otherwise over an index array in the
+ * executable's arena (chunks sorted in LDS, larger stages in global memory), for
+ * rows of up to 2^30 elements. */
 int ghip_fn_sort(GHipFunction* f, GHipFunction* comparator, int axis, int is_stable,
                  const GHipValue* inputs, int n, GHipValue* outs, int max_outs, GHipError* err);
 

@@ -131,3 +131,27 @@ def test_finalize_does_not_wait_and_reuse_is_ordered(be):
     for t, y in keep:
         assert np.all(be.BufferToFlatData(y) == np.float32(3 * t))
         be.BufferFinalize(y)
+
+
+def test_buffers_of_another_backend_are_refused(be):
+    """A buffer made by a second backend lives on that backend's stream: Execute
+    refuses it as an input (donated or not) instead of reading it, or moving it
+    into this backend's allocator, unordered with the other stream."""
+    s = make_shape(F32, 64, 64)
+    ex = _compile(be, "neg", lambda f, x: [f.Neg(x)], [s])
+    other = Backend("")
+    try:
+        host = synth.normal(5301, (64, 64))
+        xo = other.BufferFromFlatData(0, host, s)
+        for donate in (None, [True]):
+            with pytest.raises(BackendError, match="another backend"):
+                ex.Execute([xo], donate, 0)
+        assert np.array_equal(other.BufferToFlatData(xo).reshape(64, 64), host)  # still valid
+        other.BufferFinalize(xo)
+        x = be.BufferFromFlatData(0, host, s)
+        (y,) = ex.Execute([x], None, 0)
+        assert np.array_equal(be.BufferToFlatData(y).reshape(64, 64), -host)
+        be.BufferFinalize(y)
+        be.BufferFinalize(x)
+    finally:
+        other.Finalize()

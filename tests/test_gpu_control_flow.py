@@ -213,6 +213,34 @@ def test_nested_closures_and_calls(be):
     assert np.array_equal(y, want)
 
 
+def test_while_with_nested_loop_runs_without_speculation(be):
+    """An outer loop whose body runs an inner While that terminates for every state
+    the sequential loop reaches (i = 0, 1, 2: count j up from i to 2) but not on the
+    state after the exit (i = 3: j never equals 2, so the inner loop would hit the
+    iteration limit).  The outer loop must not evaluate its body past the exit: the
+    result is the sequential loop's, with no error."""
+    def build(b, f, _):
+        cond = f.Closure()
+        i = cond.Parameter("i", make_shape(I32))
+        cond.Parameter("total", make_shape(I32))
+        cond.Return([cond.LessThan(i, cond.Constant(i32(3)))])
+        body = f.Closure()
+        i, tot = body.Parameter("i", make_shape(I32)), body.Parameter("total", make_shape(I32))
+        icond = body.Closure()
+        j = icond.Parameter("j", make_shape(I32))
+        icond.Return([icond.NotEqual(j, icond.Constant(i32(2)))])
+        ibody = body.Closure()
+        j = ibody.Parameter("j", make_shape(I32))
+        ibody.Return([ibody.Add(j, ibody.Constant(i32(1)))])
+        (jend,) = body.While(icond, ibody, i)
+        body.Return([body.Add(i, body.Constant(i32(1))), body.Add(tot, jend)])
+        return list(f.While(cond, body, f.Constant(i32(0)), f.Constant(i32(0))))
+
+    plan, (i_end, total) = run(be, build, [(i32(0), make_shape(I32))])
+    assert "no speculation" in plan, plan
+    assert int(i_end) == 3 and int(total) == 6
+
+
 def test_control_flow_errors(be):
     b = be.Builder("err")
     f = b.Main()

@@ -208,3 +208,30 @@ def test_transformer_block_fused_equals_unfused(be):
         outs[fuse] = be.BufferToFlatData(out).copy()
         ex.Finalize()
     assert np.array_equal(outs[True], outs[False])
+
+
+@pytest.mark.parametrize("rows,cols,k", [(2048, 4096, 512), (2000, 4104, 520)])
+def test_gelu_both_operands_mn_contiguous(be, rows, cols, k):
+    """FusedGelu(DotGeneral(x, [0], [], w, [0], [])) with x stored [K, M] and w
+    [K, N]: both operands MN-contiguous and a VALU-heavy (tanh) epilogue, which
+    runs on the 8-wave 64-deep core with both tiles read by transpose reads.  At
+    least 128 tiles of 256 x 256, even and ragged (rows, cols and k not multiples
+    of the tile); bit for bit against the unfused plan and 2048 sampled outputs
+    against the reference's bf16 GELU chain on the fp64 product (row strides stay
+    multiples of 8 elements, which the MFMA path needs)."""
+    xt, sx = _bf16_in(81, (k, rows))
+    w, sw = _bf16_in(82, (k, cols), std=k ** -0.5)
+
+    def build(f, xt, w):
+        return [f.FusedGelu(f.DotGeneral(xt, [0], [], w, [0], []), False)]
+    (y,) = _check_fused_equals_unfused(be, build, [(xt, sx), (w, sw)], core="8w-k64")
+    rng = np.random.default_rng(rows + cols)
+    mi, ni = rng.integers(0, rows, 2048), rng.integers(0, cols, 2048)
+    dot = _bf(np.einsum("km,km->m", xt[:, mi].astype(np.float64), w[:, ni].astype(np.float64)))
+    lo, hi = orc.gelu_chain_16(dot, False)
+    got = y[mi, ni]
+    want = lo.astype(np.float64)
+    assert rel_err(got, want) <= 3e-2 and norm_err(got, want) <= 1e-2
+    # the chain's result exactly, except where the fp32-accumulated product rounds
+    # to the other bf16 neighbour of the fp64 one
+    assert np.mean((got == lo) | (got == hi)) >= 0.95

@@ -86,6 +86,12 @@ def test_noalloc_errors(be):
         ex.ExecuteNoAlloc(bufs, [bufs[0], outs[1]])
     with pytest.raises(BackendError, match="expected 2 outputs"):
         ex.ExecuteNoAlloc(bufs, outs[:1])
+    other = Backend("")
+    try:
+        with pytest.raises(BackendError, match="another backend"):
+            ex.ExecuteNoAlloc(bufs, [other.NewSharedBuffer(0, ex.Outputs()[0]), outs[1]])
+    finally:
+        other.Finalize()
     # While runs sub-functions with arenas of their own: refused, Execute still works
     b = be.Builder("loop")
     f = b.Main()
