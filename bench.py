@@ -23,6 +23,14 @@ graph holds a whole rotation cycle and is replayed; a remainder of K runs as
 single launches), so microsecond kernels run back to back instead of waiting on
 the Python launch path; the graph is built, replayed once and checked against an
 eager launch before timing.
+
+Inputs: every workload's tensors come from the SplitMix64 / Box-Muller streams of
+gomlx_hip.synth (seeded, generated on the device or on the host for the graph
+cases).  CPU baselines: every line but the vendor comparison carries a
+cpu_baseline, the C oracle (oracle/oracle.c, OpenMP on the host's cores: a CPU
+restatement, not GoMLX's simplego, which cannot be built here) timed on a bounded
+slice of the same input bytes, copied back from the device; the headline's leg
+runs 10 s on the full input, the others --cpu-s each.
 """
 from __future__ import annotations
 
@@ -46,7 +54,9 @@ def parse():
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=200)
     p.add_argument("--warmup", type=int, default=10)
-    p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline legs")
+    p.add_argument("--cpu-s", type=float, default=2.0, metavar="S",
+                   help="wall time of each secondary line's CPU leg (the headline's takes 10 s)")
     p.add_argument("--no-secondary", action="store_true")
     p.add_argument("--only", default="", help="comma list of secondary case names")
     p.add_argument("--eager", action="store_true",
@@ -58,8 +68,9 @@ def parse():
                    help="minimum device time of each secondary line's timed region (default by "
                         "bound: hbm 0.03 s, mfma 0.5 s)")
     p.add_argument("--copy-ref", type=int, default=0, metavar="MIB",
-                   help="only run a plain device copy of MIB MiB (read + write) `steps` times: "
-                        "the reference kernel that scales FETCH_SIZE / WRITE_SIZE to bytes")
+                   help="only run a plain device copy of MIB MiB (read, and the same written), "
+                        "graph-launched like the HBM lines: the ceiling the row kernels are held "
+                        "against, and the kernel that scales FETCH_SIZE / WRITE_SIZE to bytes")
     return p.parse_args()
 
 
@@ -69,8 +80,11 @@ class Case:
 
     def __init__(self, name, launch, bytes_per_step=0, flops_per_step=0, bound="hbm",
                  peak=HBM_PEAK_GBS, dtype="f32", rotation=1, config=None, kernel="",
-                 out=None, stream=None, executed_flops_per_step=None):
+                 out=None, stream=None, executed_flops_per_step=None, cpu=None):
         self.name, self.launch = name, launch
+        # cpu(budget_s) -> cpu_baseline dict: the oracle on a bounded sample of the
+        # same input bytes (None: no CPU leg, e.g. the vendor comparison line).
+        self.cpu = cpu
         self.bytes, self.flops = bytes_per_step, flops_per_step
         # MFMA work actually executed when it is less than the algorithmic flops
         # (causal attention skips the masked half of the score matrix).
@@ -201,10 +215,40 @@ def measured_traffic(kernel_key):
     path = os.path.join(ROOT, "profiles", "traffic.json")
     try:
         with open(path) as f:
-            entry = json.load(f).get(kernel_key)
-    except (OSError, ValueError):
+            table = json.load(f)
+    except (OSError, ValueError) as e:
+        print(f"bench: WARNING: cannot read {path}: {e}", file=sys.stderr, flush=True)
         return None
-    return None if entry is None else entry["traffic_bytes"]
+    entry = table.get(kernel_key)
+    if entry is None:
+        if kernel_key.startswith(("rows_", "gemm_", "sdpa_")):
+            print(f"bench: WARNING: no traffic measurement for kernel '{kernel_key}' in "
+                  f"profiles/traffic.json (renamed kernel?): roofline.traffic is null",
+                  file=sys.stderr, flush=True)
+        return None
+    return entry["traffic_bytes"]
+
+
+def cpu_rate(fn, budget_s):
+    """Runs fn() once untimed, then repeatedly until budget_s of wall time has
+    passed; returns (repetitions, seconds)."""
+    fn()
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        fn()
+        reps += 1
+        dt = time.perf_counter() - t0
+        if dt >= budget_s:
+            return reps, dt
+
+
+def cpu_threads():
+    return int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+
+
+def cpu_entry(value, unit, sample):
+    return {"value": round(value, 3), "unit": unit, "cores": cpu_threads(), "kind": "port",
+            "sample": "CPU restatement, not simplego: " + sample}
 
 
 def rotation_for(nbytes):
@@ -212,89 +256,159 @@ def rotation_for(nbytes):
 
 
 def make_cases(only=None):
+    """Every workload's inputs come from the SplitMix64 / Box-Muller streams of
+    gomlx_hip.synth, generated on the device (synth.normal_device, or synth on the
+    host for the graph cases); each CPU leg runs the oracle on a bounded slice of
+    those same bytes, copied back from the device."""
+    import numpy as np
     import torch
-    from gomlx_hip import ops
+    from gomlx_hip import ops, synth
+    sys.path.insert(0, ROOT)
+    from oracle import oracle as orc
 
     dev = torch.device("cuda:0")
-    g = torch.Generator(dev).manual_seed(2001)
     cases = {}
+
+    def nd(seed, shape, std=1.0, dtype=None):
+        return synth.normal_device(seed, shape, std=std, device=dev, dtype=dtype)
+
+    def host32(t):
+        return t.float().cpu().numpy()
+
+    def rotated(x, rot):
+        return [x] + [x.clone() for _ in range(rot - 1)]
+
+    def norm_cpu(tag, op, x, gam, bet, nbytes_row, rows_sample):
+        """The oracle's RMSNorm (fp32 end to end, as the headline's CPU leg) or
+        LayerNorm (fp64 output) on the first rows_sample rows of the device input."""
+        xs = host32(x[:rows_sample])
+        gs = host32(gam)
+        bs = None if bet is None else host32(bet)
+        def leg(budget_s):
+            y = np.empty_like(xs)
+            fn = (lambda: orc.rmsnorm_f32(xs, gs, 1e-6, out=y)) if op == "rms" else \
+                (lambda: orc.layernorm(xs, gs, bs, 1e-5))
+            reps, dt = cpu_rate(fn, budget_s)
+            what = "orc_rmsnorm_f32 (fp32 statistics and output)" if op == "rms" else "orc_layernorm (fp64)"
+            return cpu_entry(nbytes_row * rows_sample * reps / dt / 1e9, "GB/s",
+                             f"oracle/oracle.c {what}, OpenMP {cpu_threads()} threads, on rows 0..{rows_sample} "
+                             f"of the same [8192,4096] {tag} input (values widened to fp32), {reps} repetitions "
+                             f"in {dt:.1f} s; bytes counted as on the GPU line")
+        return leg
 
     def rms_case(dtype, tag):
         rows, n = 8192, 4096
         es = 4 if dtype == torch.float32 else 2
         nbytes = (2 * rows * n + n) * es
         rot = rotation_for(nbytes)
-        xs = [torch.randn((rows, n), device=dev, generator=g).to(dtype) for _ in range(rot)]
-        ys = [torch.empty_like(xs[0]) for _ in range(rot)]
-        gam = (torch.rand((n,), device=dev, generator=g) + 0.5).to(dtype)
+        x = nd(2001, (rows, n), dtype=dtype)
+        xs = rotated(x, rot)
+        ys = [torch.empty_like(x) for _ in range(rot)]
+        gam = synth_uniform_device(2002, (n,), 0.5, 1.5, dev).to(dtype)
         kern = "rows_norm_stream_kernel<float, 2, 4, 4>" if tag == "f32" else "rows_norm_stream_kernel<bf16_t, 2, 4, 2>"
         return Case(f"rmsnorm_{tag}", lambda i: ops.rmsnorm(xs[i % rot], gam, 1e-6, out=ys[i % rot]),
                     bytes_per_step=nbytes, dtype=tag, rotation=rot, kernel=kern,
                     out=lambda i: ys[i % rot],
-                    config={"workload": f"RMSNorm last axis, x [8192,4096] {tag}, gamma [4096], eps 1e-6, fp32 statistics"})
+                    cpu=norm_cpu(tag, "rms", x, gam, None, (2 * n) * es, rows if tag == "f32" else 2048),
+                    config={"workload": f"RMSNorm last axis, x [8192,4096] {tag} ~ N(0,1), gamma [4096] ~ "
+                                        f"U(0.5,1.5), eps 1e-6, fp32 statistics"})
 
     def ln_case(dtype, tag):
         rows, n = 8192, 4096
         es = 4 if dtype == torch.float32 else 2
         nbytes = (2 * rows * n + 2 * n) * es
         rot = rotation_for(nbytes)
-        xs = [torch.randn((rows, n), device=dev, generator=g).to(dtype) for _ in range(rot)]
-        ys = [torch.empty_like(xs[0]) for _ in range(rot)]
-        gam = (torch.rand((n,), device=dev, generator=g) + 0.5).to(dtype)
-        bet = (torch.randn((n,), device=dev, generator=g) * 0.1).to(dtype)
+        x = nd(2001, (rows, n), dtype=dtype)
+        xs = rotated(x, rot)
+        ys = [torch.empty_like(x) for _ in range(rot)]
+        gam = synth_uniform_device(2002, (n,), 0.5, 1.5, dev).to(dtype)
+        bet = nd(2003, (n,), std=0.1, dtype=dtype)
         kern = "rows_norm_stream_kernel<float, 3, 4, 4>" if tag == "f32" else "rows_norm_stream_kernel<bf16_t, 3, 4, 2>"
         return Case(f"layernorm_{tag}",
                     lambda i: ops.layernorm(xs[i % rot], gam, bet, 1e-5, out=ys[i % rot]),
                     bytes_per_step=nbytes, dtype=tag, rotation=rot, kernel=kern,
                     out=lambda i: ys[i % rot],
-                    config={"workload": f"LayerNorm last axis, x [8192,4096] {tag}, eps 1e-5"})
+                    cpu=norm_cpu(tag, "ln", x, gam, bet, (2 * n) * es, 2048),
+                    config={"workload": f"LayerNorm last axis, x [8192,4096] {tag} ~ N(0,1), gamma ~ U(0.5,1.5), "
+                                        f"beta ~ N(0,0.1), eps 1e-5"})
 
     def softmax_case():
         rows, n = 4096, 1024
         nbytes = 2 * rows * n * 4
         rot = rotation_for(nbytes)
-        xs = [torch.randn((rows, n), device=dev, generator=g) * 2 for _ in range(rot)]
-        ys = [torch.empty_like(xs[0]) for _ in range(rot)]
+        x = nd(1001, (rows, n), std=2.0)
+        xs = rotated(x, rot)
+        ys = [torch.empty_like(x) for _ in range(rot)]
+        xh = host32(x)
+
+        def leg(budget_s):
+            reps, dt = cpu_rate(lambda: orc.softmax(xh), budget_s)
+            return cpu_entry(nbytes * reps / dt / 1e9, "GB/s",
+                             f"oracle/oracle.c orc_softmax (fp64), OpenMP {cpu_threads()} threads, on the full "
+                             f"[4096,1024] fp32 input, {reps} repetitions in {dt:.1f} s")
         return Case("softmax_f32", lambda i: ops.softmax(xs[i % rot], out=ys[i % rot]),
                     bytes_per_step=nbytes, dtype="f32", rotation=rot, kernel="rows_reg_kernel<float, 0, 4, 1>",
-                    out=lambda i: ys[i % rot],
+                    out=lambda i: ys[i % rot], cpu=leg,
                     config={"workload": "Softmax last axis, x [4096,1024] fp32 ~ N(0, 2^2)"})
+
+    def dot_inputs(dtype):
+        B, M, K, N = 8, 2048, 4096, 4096
+        std = K ** -0.25  # entries ~ N(0, 1/sqrt(K)) (configs[2])
+        return nd(3001, (B, M, K), std=std, dtype=dtype), nd(3002, (B, K, N), std=std, dtype=dtype)
 
     def dot_case(dtype, tag, peak):
         B, M, K, N = 8, 2048, 4096, 4096
-        a = (torch.randn((B, M, K), device=dev, generator=g) * 0.125).to(dtype)
-        b = (torch.randn((B, K, N), device=dev, generator=g) * 0.125).to(dtype)
+        a, b = dot_inputs(dtype)
         c = torch.empty((B, M, N), device=dev, dtype=dtype)
+        rows = 16
+        ah, bh = host32(a[0, :rows]), host32(b[0])
+
+        def leg(budget_s):
+            reps, dt = cpu_rate(lambda: orc.dot_general(ah, [1], [], bh, [0], []), budget_s)
+            return cpu_entry(2 * rows * N * K * reps / dt / 1e12, "TFLOP/s",
+                             f"oracle/oracle.c orc_dot_general (fp64 accumulation), OpenMP {cpu_threads()} "
+                             f"threads, on rows 0..{rows} of batch 0 of the same {tag} A times batch 0 of B "
+                             f"([{rows},4096] x [4096,4096]), {reps} repetitions in {dt:.1f} s")
         return Case(f"dot_general_{tag}", lambda i: ops.gemm(a, b, out=c),
                     flops_per_step=2 * B * M * N * K, bound="mfma", peak=peak, dtype=tag,
                     kernel="gemm_bf16_kernel8km<bf16_t, bf16_t>" if tag == "bf16"
-                    else "gemm_f32_kernel<256, 256, 2, 4, true, false, float>",
-                    config={"workload": f"DotGeneral [8,2048,4096]x[8,4096,4096] lc=[2] lb=[0] rc=[1] rb=[0], {tag} in, fp32 accumulate, {tag} out"})
+                    else "gemm_f32_kernel<256, 256, 2, 4, true, false, float>", cpu=leg,
+                    config={"workload": f"DotGeneral [8,2048,4096]x[8,4096,4096] lc=[2] lb=[0] rc=[1] rb=[0], "
+                                        f"{tag} in ~ N(0, 1/sqrt(4096)), fp32 accumulate, {tag} out"})
 
     def vendor_dot_case():
         """The same bf16 DotGeneral through torch.matmul (hipBLASLt), timed in the
         same process for comparison; not part of this backend."""
         B, M, K, N = 8, 2048, 4096, 4096
-        a = (torch.randn((B, M, K), device=dev, generator=g) * 0.125).to(torch.bfloat16)
-        b = (torch.randn((B, K, N), device=dev, generator=g) * 0.125).to(torch.bfloat16)
+        a, b = dot_inputs(torch.bfloat16)
         c = torch.empty((B, M, N), device=dev, dtype=torch.bfloat16)
         return Case("dot_general_bf16_hipblaslt", lambda i: torch.matmul(a, b, out=c),
                     flops_per_step=2 * B * M * N * K, bound="mfma", peak=BF16_PEAK_TFLOPS, dtype="bf16",
                     kernel="hipBLASLt (torch.matmul)",
                     config={"workload": "comparison only: torch.matmul (hipBLASLt) on the DotGeneral "
-                                        "bf16 config shape, same process"})
+                                        "bf16 config shape and inputs, same process"})
 
     def attention_case():
         B, H, S, D = 4, 16, 2048, 128
-        q = torch.randn((B, H, S, D), device=dev, generator=g).to(torch.bfloat16)
-        k = torch.randn((B, H, S, D), device=dev, generator=g).to(torch.bfloat16)
-        v = torch.randn((B, H, S, D), device=dev, generator=g).to(torch.bfloat16)
+        q = nd(4001, (B, H, S, D), dtype=torch.bfloat16)
+        k = nd(4002, (B, H, S, D), dtype=torch.bfloat16)
+        v = nd(4003, (B, H, S, D), dtype=torch.bfloat16)
         o = torch.empty_like(q)
+        qh, kh, vh = host32(q[:1, :1]), host32(k[:1, :1]), host32(v[:1, :1])
+        ex1 = 2 * 2 * D * S * (S + 1) // 2
+
+        def leg(budget_s):
+            reps, dt = cpu_rate(lambda: orc.sdpa(qh, kh, vh, scale=D ** -0.5, causal=True), budget_s)
+            return cpu_entry(ex1 * reps / dt / 1e12, "TFLOP/s",
+                             f"oracle/oracle.c orc_sdpa (fp64, scores materialised per query), OpenMP "
+                             f"{cpu_threads()} threads, on (batch 0, head 0) of the same bf16 Q, K, V "
+                             f"([2048,128] each, causal); executed flops as on the GPU line; {reps} "
+                             f"repetitions in {dt:.1f} s")
         return Case("attention_bf16", lambda i: ops.sdpa(q, k, v, D ** -0.5, True, out=o),
                     flops_per_step=2 * 2 * B * H * S * S * D, bound="mfma",
                     executed_flops_per_step=2 * 2 * B * H * D * S * (S + 1) // 2,
-                    peak=BF16_PEAK_TFLOPS, dtype="bf16", kernel="sdpa_fwd_kernel<128, false, 0>",
-                    config={"workload": "SDPA causal B4 H16 S2048 D128 bf16, one fused kernel "
+                    peak=BF16_PEAK_TFLOPS, dtype="bf16", kernel="sdpa_fwd_kernel<128, false, 0>", cpu=leg,
+                    config={"workload": "SDPA causal B4 H16 S2048 D128 bf16 ~ N(0,1), one fused kernel "
                                         "(Q.K^T, scale, causal mask, online softmax, P.V); flops "
                                         "counted for both products over the full S x S matrix, "
                                         "the causal half above the diagonal is skipped"})
@@ -303,13 +417,12 @@ def make_cases(only=None):
         """BASELINE configs[4] through the graph API: Builder -> Compile -> Execute of
         the whole decoder block (gather, RMSNorm, QKV/O projections, fused causal
         attention, residual, RMSNorm, SwiGLU FFN, residual) on the backend's stream."""
-        import numpy as np
-        from gomlx_hip import graphs, synth
+        from gomlx_hip import graphs
         from gomlx_hip.backend import Backend
         be = Backend("")
         cfg = graphs.TransformerBlockConfig()
         ex = graphs.transformer_block(be, cfg)
-        bufs = []
+        bufs, P = [], {}
         for i, (name, shape) in enumerate(cfg.param_shapes()):
             if name == "ids":
                 host = synth.uniform_int(5001, (cfg.batch, cfg.seq), 0, cfg.vocab)
@@ -317,8 +430,20 @@ def make_cases(only=None):
                 host = np.ones(shape.dims, np.float32)
             else:
                 host = synth.round_bf16(synth.normal(5002 + i, shape.dims, std=0.02))
+            P[name] = host
             bufs.append(be.BufferFromFlatData(0, host, shape))
         stream = torch.cuda.ExternalStream(be.stream())
+        toks = [0, 255, 511, 767, 1023]
+
+        def leg(budget_s):
+            fl = orc.block_tokens(P, 0, toks, cfg.d_model, cfg.heads, cfg.head_dim, cfg.eps)[1]
+            reps, dt = cpu_rate(lambda: orc.block_tokens(P, 0, toks, cfg.d_model, cfg.heads, cfg.head_dim,
+                                                         cfg.eps), budget_s)
+            return cpu_entry(fl * reps / dt / 1e12, "TFLOP/s",
+                             f"oracle composition of the block (oracle.block_tokens: orc_gather_rows, "
+                             f"orc_rmsnorm, orc_dot_general, orc_sdpa, fp64), OpenMP {cpu_threads()} threads, "
+                             f"on the same parameters and ids: batch row 0, K/V for tokens 0..1023, the rest "
+                             f"for tokens {toks} ({fl / 1e9:.1f} GFLOP each), {reps} repetitions in {dt:.1f} s")
 
         def launch(i):
             (y,) = ex.Execute(bufs, None, 0)
@@ -327,7 +452,7 @@ def make_cases(only=None):
         case = Case("transformer_block_bf16", launch, flops_per_step=cfg.flops(), bound="mfma",
                     executed_flops_per_step=cfg.flops() - causal_attn + causal_attn * (S + 1) // (2 * S),
                     peak=BF16_PEAK_TFLOPS, dtype="bf16", kernel="graph Execute (all kernels)",
-                    stream=stream,
+                    stream=stream, cpu=leg,
                     config={"workload": "decoder block B8 S1024 d2048 H16 Dh128 FFN 8192 bf16 "
                                         "(configs[4]) through Builder/Compile/Execute; flops: "
                                         "projections + both attention products over the full "
@@ -359,25 +484,32 @@ def make_cases(only=None):
     def dense_case():
         """FusedDense with bias and GELU on the FFN shape of configs[4]: one GEMM whose
         epilogue adds the bias and evaluates the tanh-GELU chain."""
-        import numpy as np
-        from gomlx_hip import synth
         from gomlx_hip.backend import ActivationType, dtypes, make_shape
         T, d, ff = 8192, 2048, 8192
         bf = lambda seed, shape, std: synth.to_bf16_bits(synth.normal(seed, shape, std=std))  # noqa: E731
         inputs = [(bf(6001, (8, 1024, d), 1.0), make_shape(dtypes.BFloat16, 8, 1024, d)),
                   (bf(6002, (d, ff), d ** -0.5), make_shape(dtypes.BFloat16, d, ff)),
                   (bf(6003, (ff,), 0.1), make_shape(dtypes.BFloat16, ff))]
+        rows = 32
+        xh = synth.bf16_bits_to_f32(inputs[0][0][0, :rows])
+        wh, bh = synth.bf16_bits_to_f32(inputs[1][0]), synth.bf16_bits_to_f32(inputs[2][0])
+
+        def leg(budget_s):
+            reps, dt = cpu_rate(lambda: orc.dense(xh, wh, bh, orc.ACT_GELU), budget_s)
+            return cpu_entry(2 * rows * d * ff * reps / dt / 1e12, "TFLOP/s",
+                             f"oracle FusedDense (orc_dot_general fp64 + bias + tanh-GELU), OpenMP "
+                             f"{cpu_threads()} threads, on tokens 0..{rows} of the same x, W and bias, "
+                             f"{reps} repetitions in {dt:.1f} s; flops of the product only")
         return graph_case("fused_dense_gelu_bf16",
                           lambda f, x, w, b: [f.FusedDense(x, w, b, ActivationType.GELU)], inputs,
                           flops_per_step=2 * T * d * ff, bound="mfma", peak=BF16_PEAK_TFLOPS, dtype="bf16",
-                          kernel="gemm_epilogue",
+                          kernel="gemm_epilogue", cpu=leg,
                           config={"workload": "FusedDense x [8,1024,2048] . W [2048,8192] + bias, tanh-GELU, "
                                               "bf16 (fp32 accumulate); flops of the product only"})
 
     def scatter_case():
         """ScatterSum in the embedding-gradient form: 8192 token rows of width 2048
         added into a [32000, 2048] bf16 table (ids of configs[4])."""
-        from gomlx_hip import synth
         from gomlx_hip.backend import dtypes, make_shape
         V, D, n = 32000, 2048, 8192
         ids = synth.uniform_int(5001, (n,), 0, V)
@@ -385,10 +517,22 @@ def make_cases(only=None):
                   (ids, make_shape(dtypes.Int32, n)),
                   (synth.to_bf16_bits(synth.normal(6102, (n, D), std=1.0)), make_shape(dtypes.BFloat16, n, D))]
         nbytes = 2 * V * D * 2 + n * D * 2 + n * 4
+        cols = 64
+        th = synth.bf16_bits_to_f32(inputs[0][0][:, :cols]).astype(np.float64)
+        uh = synth.bf16_bits_to_f32(inputs[2][0][:, :cols]).astype(np.float64)
+        ih = ids.reshape(n, 1).astype(np.int64)
+        nb_s = 2 * V * cols * 2 + n * cols * 2 + n * 4
+
+        def leg(budget_s):
+            reps, dt = cpu_rate(lambda: orc.scatter(0, th, ih, uh, 1, [1], [0], [0]), budget_s)
+            return cpu_entry(nb_s * reps / dt / 1e9, "GB/s",
+                             f"oracle/oracle.c orc_scatter (ScatterSum, fp64, sequential), on columns "
+                             f"0..{cols} of the same table, updates and ids ([32000,{cols}] += [8192,{cols}]), "
+                             f"{reps} repetitions in {dt:.1f} s; bytes counted as on the GPU line")
         return graph_case("scatter_sum_bf16",
                           lambda f, t, i, u: [f.ScatterSum(t, i, u, 1, [1], [0], [0])], inputs,
                           bytes_per_step=nbytes, bound="hbm", peak=HBM_PEAK_GBS, dtype="bf16",
-                          kernel="scatter plan (all kernels)",
+                          kernel="scatter plan (all kernels)", cpu=leg,
                           config={"workload": "ScatterSum table [32000,2048] bf16 += updates [8192,2048] bf16 at "
                                               "ids [8192] int32 ~ U[0,32000); bytes: read + write table, read "
                                               "updates and ids"})
@@ -411,61 +555,53 @@ def make_cases(only=None):
     return primary, builders, names
 
 
-def cpu_baseline(seconds_target=10.0):
-    """The CPU restatement of the headline workload (not simplego: GoMLX's pure-Go
-    backend lives in an un-vendored module and there is no Go toolchain): the
-    oracle's fp32 RMSNorm (C, OpenMP over rows, fp32 sequential statistics, fp32
-    output) on the full configs[1] input, x [8192, 4096] fp32, gamma [4096],
-    repeated until ~seconds_target of wall time has run."""
-    import numpy as np
-    sys.path.insert(0, ROOT)
-    from oracle import oracle as orc
+def synth_uniform_device(seed, shape, lo, hi, dev):
+    """synth.uniform_f32 values (host SplitMix64, small) uploaded to the device."""
+    import torch
     from gomlx_hip import synth
-
-    rows, n = 8192, 4096
-    x = synth.normal(2001, (rows, n))
-    gam = synth.uniform_f32(2002, (n,), 0.5, 1.5)
-    y = np.empty_like(x)
-    orc.rmsnorm_f32(x, gam, 1e-6, out=y)  # warm
-    reps, t0 = 0, time.perf_counter()
-    while time.perf_counter() - t0 < seconds_target:
-        orc.rmsnorm_f32(x, gam, 1e-6, out=y)
-        reps += 1
-    dt = time.perf_counter() - t0
-    nbytes = (2 * rows * n + n) * 4
-    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
-    return {"value": round(nbytes * reps / dt / 1e9, 3), "unit": "GB/s", "cores": threads,
-            "kind": "port",
-            "sample": f"CPU restatement, not simplego: oracle/oracle.c orc_rmsnorm_f32 (OpenMP, "
-                      f"{threads} threads, fp32 statistics and output) on the full x [8192,4096] "
-                      f"fp32 + gamma [4096], {reps} repetitions in {dt:.1f} s"}
+    return torch.from_numpy(synth.uniform_f32(seed, shape, lo, hi)).to(dev)
 
 
 def copy_reference(mib: int, steps: int):
-    """A plain device-to-device copy of `mib` MiB, `steps` times: its FETCH_SIZE /
-    WRITE_SIZE counters per dispatch, divided by mib * 1024, give the factor that
-    turns those counters into bytes for the kernels measured beside it.  Also
-    times the copies (HIP events around back-to-back launches; sources and
-    destinations rotate over enough buffers that the 256 MB Infinity Cache cannot
-    serve them) and reports GB/s of bytes read plus written.  Below ~64 MiB the
-    per-copy launch cost from Python shows in the rate."""
+    """A plain device-to-device copy of `mib` MiB (mib read and mib written: the
+    bytes the softmax line moves at mib = 16): its FETCH_SIZE / WRITE_SIZE counters
+    per dispatch give the factor that turns those counters into bytes for the
+    kernels measured beside it, and its launch time is the ceiling the row kernels
+    are held against.  Timed like a secondary HBM line: the copies of one rotation
+    cycle (sources and destinations rotate past the 256 MB Infinity Cache) are
+    captured in a HIP graph, warmed up for 0.25 s, then replayed for >= 30 ms
+    between HIP events; reports the average per copy and GB/s of bytes read plus
+    written."""
     import torch
-    n = mib * (1 << 20) // 4
+    n = mib * (1 << 20) // 4  # fp32 elements per side
     rot = rotation_for(2 * n * 4)
     xs = [torch.ones(n, device="cuda", dtype=torch.float32) for _ in range(rot)]
     ys = [torch.empty_like(xs[0]) for _ in range(rot)]
-    for i in range(steps):
-        ys[i % rot].copy_(xs[i % rot])
-    torch.cuda.synchronize()
-    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    ev0.record()
-    for i in range(steps):
-        ys[i % rot].copy_(xs[i % rot])
-    ev1.record()
-    torch.cuda.synchronize()
-    us = ev0.elapsed_time(ev1) * 1e3 / max(steps, 1)
-    print(json.dumps({"copy_ref_mib": mib, "steps": steps, "rotation": rot, "us_per_copy": round(us, 2),
-                      "gbs": round(2 * n * 4 / us / 1e3, 1)}))
+    per = rot * max(1, -(-16 // rot))
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for i in range(per):
+            ys[i % rot].copy_(xs[i % rot])
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < 0.25:
+        g.replay()
+        torch.cuda.synchronize()
+    reps = max(1, steps // per)
+    while True:
+        ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        ev0.record()
+        for _ in range(reps):
+            g.replay()
+        ev1.record()
+        torch.cuda.synchronize()
+        ms = ev0.elapsed_time(ev1)
+        if ms >= 30.0:
+            break
+        reps *= 2
+    us = ms * 1e3 / (reps * per)
+    print(json.dumps({"copy_ref_mib": mib, "copies": reps * per, "rotation": rot, "graph": True,
+                      "us_per_copy": round(us, 2), "gbs": round(2 * n * 4 / us / 1e3, 1),
+                      "frac_of_hbm_peak": round(2 * n * 4 / us / 1e3 / HBM_PEAK_GBS, 4)}))
 
 
 def main():
@@ -512,11 +648,15 @@ def main():
                 entry["value"] = round(ex_tf, 2)
                 entry["full_matrix"] = {"achieved": round(full_tf, 2), "unit": "TFLOP/s",
                                         "frac": round(full_tf / case.peak, 4)}
+            if case.cpu is not None and not args.no_cpu:
+                entry["cpu_baseline"] = case.cpu(args.cpu_s)
             secondary.append(entry)
-            print(f"bench: {name} {entry['value']} {entry['unit']}", file=sys.stderr, flush=True)
+            print(f"bench: {name} {entry['value']} {entry['unit']}"
+                  + (f" (cpu {entry['cpu_baseline']['value']} {entry['cpu_baseline']['unit']})"
+                     if "cpu_baseline" in entry else ""), file=sys.stderr, flush=True)
             del case
             torch.cuda.empty_cache()
-    cpu = None if args.no_cpu else cpu_baseline()
+    cpu = None if args.no_cpu else primary.cpu(10.0)
     gbs = primary.bytes * res["steps"] / (res["wall_ms"] / 1e3) / 1e9
     line = {
         "metric": "softmax/RMSNorm GB/s (% HBM peak); bf16 DotGeneral TFLOP/s (% MFMA peak)",
@@ -530,7 +670,8 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "f32",
-        "data": "synthetic (torch.randn on device; inputs resident in HBM)",
+        "data": "synthetic (SplitMix64 / Box-Muller streams of gomlx_hip.synth generated on the device, "
+                "resident in HBM; each CPU leg reads the same bytes)",
         "config": dict(primary.config, rotation=primary.rotation, graph=res["graph"],
                        graph_replays=res["graph_replays"], kernel=primary.kernel,
                        launch_us=round(res["launch_us"], 2),

@@ -427,8 +427,15 @@ __global__ __launch_bounds__(256) void rows_reg_kernel(RowParams p) {
 // divergent branch and issues no load between a group's stores and the wait for
 // the next group's x, so that wait never covers the stores (vmcnt counts loads
 // and stores in issue order).  Same arithmetic as rows_reg_group.
+//
+// x, y, the row count and the group count are the first kernel arguments, which
+// this file preloads into SGPRs (-amdgpu-kernarg-preload-count), and the row width
+// is a compile-time constant: a wave issues its first group's loads before any
+// kernel-argument fetch, and gamma / beta follow them, so their latency overlaps
+// instead of preceding the first loads.
 template <typename T, int OP, int NV, int WPR>
-__global__ __launch_bounds__(256) void rows_norm_stream_kernel(RowParams p, int64_t groups) {
+__global__ __launch_bounds__(256) void rows_norm_stream_kernel(const void* x, void* y, int64_t rows,
+                                                               int64_t groups, RowParams p) {
   constexpr int VEC = Elem<T>::kVec;
   constexpr int LANES = kWave * WPR;
   constexpr int RPB = 4 / WPR;
@@ -436,9 +443,23 @@ __global__ __launch_bounds__(256) void rows_norm_stream_kernel(RowParams p, int6
   // The row slot is the same for the whole wave (LANES is a multiple of 64).
   const int sub = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) / LANES);
   const int l = threadIdx.x % LANES;
-  const int64_t n = p.n;
+  constexpr int64_t n = static_cast<int64_t>(NV) * LANES * VEC;
   int64_t blk = blockIdx.x;
   if (blk >= groups) return;  // whole workgroup
+  bool live[NV];
+#pragma unroll
+  for (int i = 0; i < NV; ++i) live[i] = true;
+  // Rows past the end (the last group of an odd row count) load the last row
+  // again and store nothing.
+  auto load = [&](int64_t k, uint4 (&v)[NV]) {
+    int64_t row = k * RPB + sub;
+    if (row >= rows) row = rows - 1;
+    const T* xr = static_cast<const T*>(x) + row * n;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) v[i] = ld_nt(xr + (static_cast<int64_t>(i) * LANES + l) * VEC);
+  };
+  uint4 va[NV], vb[NV];
+  load(blk, va);
   const T* g = static_cast<const T*>(p.gamma);
   const T* b = OP == kLayerNorm ? static_cast<const T*>(p.beta) : nullptr;
   // gamma / beta widened once (the grid has two workgroups per CU, so registers
@@ -450,22 +471,11 @@ __global__ __launch_bounds__(256) void rows_norm_stream_kernel(RowParams p, int6
     unpack(g ? *reinterpret_cast<const uint4*>(g + c0) : make_uint4(0, 0, 0, 0), gf[i], T{});
     unpack(b ? *reinterpret_cast<const uint4*>(b + c0) : make_uint4(0, 0, 0, 0), bfl[i], T{});
   }
-  // Wait for gamma / beta here, once: left pending into the loop, the registers
-  // they land in make the compiler wait for every outstanding load and store at
-  // the top of each iteration (it cannot tell the first iteration apart).
+  // Wait for the first group and gamma / beta here, once: left pending into the
+  // loop, the registers gamma / beta land in make the compiler wait for every
+  // outstanding load and store at the top of each iteration (it cannot tell the
+  // first iteration apart).
   __builtin_amdgcn_s_waitcnt(0);
-  bool live[NV];
-#pragma unroll
-  for (int i = 0; i < NV; ++i) live[i] = true;
-  // Rows past the end (the last group of an odd row count) load the last row
-  // again and store nothing.
-  auto load = [&](int64_t k, uint4 (&v)[NV]) {
-    int64_t row = k * RPB + sub;
-    if (row >= p.rows) row = p.rows - 1;
-    const T* xr = static_cast<const T*>(p.x) + row * n;
-#pragma unroll
-    for (int i = 0; i < NV; ++i) v[i] = ld_nt(xr + (static_cast<int64_t>(i) * LANES + l) * VEC);
-  };
   auto process = [&](int64_t k, const uint4 (&v)[NV], float (*L)[4]) {
     const int64_t row = k * RPB + sub;
     // x widened once for the statistics passes and the store pass.
@@ -478,8 +488,8 @@ __global__ __launch_bounds__(256) void rows_norm_stream_kernel(RowParams p, int6
     };
     float mean, rstd;
     norm_stats<T, OP, NV, WPR>(xget, live, n, p.eps, L, mean, rstd);
-    if (row >= p.rows) return;
-    T* yr = static_cast<T*>(p.y) + row * n;
+    if (row >= rows) return;
+    T* yr = static_cast<T*>(y) + row * n;
     auto gfetch = [&](int i, int64_t, float* gv) {
 #pragma unroll
       for (int j = 0; j < VEC; ++j) gv[j] = gf[i][j];
@@ -503,8 +513,6 @@ __global__ __launch_bounds__(256) void rows_norm_stream_kernel(RowParams p, int6
   // statistics or the stores that follow it.
   const int64_t G = gridDim.x;
   const int64_t iters = (groups - blk + G - 1) / G;
-  uint4 va[NV], vb[NV];
-  load(blk, va);
   int64_t it = 0;
   for (; it + 2 < iters; it += 2) {
     load(blk + G, vb);
@@ -630,7 +638,7 @@ static hipError_t launch_norm_stream(const RowParams& p, hipStream_t s, int64_t 
   const int64_t groups = (p.rows + rows_per_block - 1) / rows_per_block;
   const int64_t grid = groups > grid_cap ? grid_cap : groups;
   hipLaunchKernelGGL((rows_norm_stream_kernel<T, OP, NV, WPR>), dim3(static_cast<unsigned>(grid)), dim3(256), 0, s,
-                     p, groups);
+                     p.x, p.y, p.rows, groups, p);
   return hipGetLastError();
 }
 

@@ -368,3 +368,32 @@ def f32_to_bf16_bits(x) -> np.ndarray:
     y = np.empty(x.shape, np.uint16)
     lib().orc_f32_to_bf16(x.reshape(-1), y.reshape(-1), x.size)
     return y
+
+
+def block_tokens(P, b, toks, d_model, heads, head_dim, eps):
+    """fp64 output of the decoder block (gather, RMSNorm, Q/K/V projections, causal
+    attention, O projection + residual, RMSNorm, SwiGLU FFN + residual: the graph
+    gomlx_hip.graphs.transformer_block builds) at tokens `toks` of batch row b.  K
+    and V are computed for the tokens up to the last one asked for, then attention,
+    the O projection and the FFN for the asked tokens only (token t sees keys
+    0..t).  P: "ids" [B, S] int32, "embedding", "wq", "wk", "wv", "wo", "w_gate",
+    "w_up", "w_down" (values widened to fp32), "g_attn", "g_ffn".  Returns
+    (out [len(toks), d_model], flops of this evaluation)."""
+    d, H, Dh = d_model, heads, head_dim
+    last = max(toks) + 1
+    x = gather_rows(P["embedding"], P["ids"][b, :last]).astype(np.float64)
+    h = rmsnorm(x.astype(np.float32), P["g_attn"], eps)
+    proj = lambda a, w: dot_general(np.asarray(a, np.float32), [a.ndim - 1], [], P[w], [0], [])  # noqa: E731
+    hd = lambda t: np.ascontiguousarray(t.reshape(1, -1, H, Dh).transpose(0, 2, 1, 3), np.float32)  # noqa: E731
+    k, v = hd(proj(h, "wk")), hd(proj(h, "wv"))
+    q = hd(proj(h[toks], "wq"))
+    a = np.concatenate([sdpa(q[:, :, i:i + 1], k[:, :, :t + 1], v[:, :, :t + 1], scale=Dh ** -0.5, causal=False)
+                        for i, t in enumerate(toks)], axis=2)
+    x2 = x[toks] + proj(a.transpose(0, 2, 1, 3).reshape(len(toks), d), "wo")
+    h2 = rmsnorm(x2.astype(np.float32), P["g_ffn"], eps)
+    gate, up = proj(h2, "w_gate"), proj(h2, "w_up")
+    out = x2 + proj(gate / (1.0 + np.exp(-gate)) * up, "w_down")
+    ff = P["w_up"].shape[1]
+    n = len(toks)
+    flops = 2 * 2 * last * d * d + n * (2 * 2 * d * d + 3 * 2 * d * ff) + sum(4 * H * Dh * (t + 1) for t in toks)
+    return out, flops

@@ -682,23 +682,9 @@ def test_transformer_block_small_stagewise(be):
 
 
 def _tb_reference_tokens(cfg, P, b, toks):
-    """fp64 block output at tokens `toks` of batch row b: K and V for the tokens up
-    to the last one asked for, then attention, the O projection and the FFN for
-    the asked tokens only (each token sees keys 0..t)."""
-    S, d, H, Dh = cfg.seq, cfg.d_model, cfg.heads, cfg.head_dim
-    last = max(toks) + 1
-    x = orc.gather_rows(P["embedding"], P["ids"][b, :last]).astype(np.float64)
-    h = orc.rmsnorm(x.astype(np.float32), P["g_attn"], cfg.eps)
-    proj = lambda a, w: orc.dot_general(np.asarray(a, np.float32), [a.ndim - 1], [], P[w], [0], [])
-    heads = lambda t: np.ascontiguousarray(t.reshape(1, -1, H, Dh).transpose(0, 2, 1, 3), np.float32)
-    k, v = heads(proj(h, "wk")), heads(proj(h, "wv"))
-    q = heads(proj(h[toks], "wq"))
-    a = np.concatenate([orc.sdpa(q[:, :, i:i + 1], k[:, :, :t + 1], v[:, :, :t + 1], scale=Dh ** -0.5, causal=False)
-                        for i, t in enumerate(toks)], axis=2)
-    x2 = x[toks] + proj(a.transpose(0, 2, 1, 3).reshape(len(toks), d), "wo")
-    h2 = orc.rmsnorm(x2.astype(np.float32), P["g_ffn"], cfg.eps)
-    gate, up = proj(h2, "w_gate"), proj(h2, "w_up")
-    return x2 + proj(gate / (1.0 + np.exp(-gate)) * up, "w_down")
+    """fp64 block output at tokens `toks` of batch row b (the oracle's composition
+    of the block; token t sees keys 0..t)."""
+    return orc.block_tokens(P, b, toks, cfg.d_model, cfg.heads, cfg.head_dim, cfg.eps)[0]
 
 
 def test_transformer_block_config_sampled(be):
