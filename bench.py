@@ -371,7 +371,7 @@ def make_cases(only=None):
                              f"([{rows},4096] x [4096,4096]), {reps} repetitions in {dt:.1f} s")
         return Case(f"dot_general_{tag}", lambda i: ops.gemm(a, b, out=c),
                     flops_per_step=2 * B * M * N * K, bound="mfma", peak=peak, dtype=tag,
-                    kernel="gemm_bf16_kernel8km<bf16_t, bf16_t>" if tag == "bf16"
+                    kernel="gemm_bf16_kernel4km<bf16_t, bf16_t>" if tag == "bf16"
                     else "gemm_f32_kernel<256, 256, 2, 4, true, false, float>", cpu=leg,
                     config={"workload": f"DotGeneral [8,2048,4096]x[8,4096,4096] lc=[2] lb=[0] rc=[1] rb=[0], "
                                         f"{tag} in ~ N(0, 1/sqrt(4096)), fp32 accumulate, {tag} out"})

@@ -157,7 +157,12 @@ __device__ __forceinline__ void dma16(i32x4_t rsrc, uint32_t la, uint32_t voff) 
 // tile is read as 16x16x32 fragments: an MN-contiguous tile uses swz_n2 instead of
 // swz_n; a K-contiguous one is laid out so that a fragment read has the access
 // pattern of a 32x32x16 one (see KC16 below).
-template <int R, bool KC, int NW, int BK = kBK, bool L16 = false>
+//
+// IL (interleaved, KC16 tiles of four waves): instruction i of wave w fills the 1 KiB
+// block i * NW + w instead of w * kPerWave + i, so the NW waves' instruction i
+// together fill the 32-row group i (NW * kRPI == 32) and a wave's instructions
+// step through the groups, 32 operand rows apart.
+template <int R, bool KC, int NW, int BK = kBK, bool L16 = false, bool IL = false>
 struct OperandTile {
   static_assert(BK == kBK || (!KC && BK == 32), "32-deep tiles are MN-contiguous only");
   static constexpr int kInstr = R * BK * 2 / 1024;
@@ -168,6 +173,9 @@ struct OperandTile {
   static constexpr int kCPR = KC ? BK / 8 : R / 8;  // 16-byte chunks per LDS row
   static constexpr int kRPI = 64 / kCPR;             // LDS rows per instruction
   static_assert(KC || R >= 128, "MN-major tiles need >= 16 chunks per LDS row");
+  static_assert(!IL || (KC && L16 && NW * kRPI == 32), "interleaved: KC16 tiles whose waves fill 32 rows");
+  // 1 KiB LDS block written by instruction i of `wave`.
+  __device__ __forceinline__ static int block(int wave, int i) { return IL ? i * NW + wave : wave * kPerWave + i; }
   // KC16: K-contiguous [R][64] tile for 16x16x32 fragments.  A 16x16x32 fragment
   // (16 rows x 4 k-chunks) read from a plain [R][64] tile puts lanes l and l + 16 on
   // the same row, which the LDS serves with 2-way bank conflicts (measured: 4
@@ -178,8 +186,8 @@ struct OperandTile {
   // 4 (b % 2) + 2 s + l / 32 (32 distinct rows per chunk, measured conflict-free),
   // and each load instruction (8 LDS rows) still fetches 8 whole 128-byte rows.
   static constexpr bool KC16 = KC && L16;
-  static_assert(!KC16 || (R % 32 == 0 && 32 % (kPerWave * kRPI) == 0),
-                "KC16: a wave's loads stay inside one 32-row group");
+  static_assert(!KC16 || (R % 32 == 0 && (IL || 32 % (kPerWave * kRPI) == 0)),
+                "KC16: a wave's loads stay inside one 32-row group (or interleave)");
 
   // Byte offsets of this lane's chunk.  The swizzle depends on the parity of the
   // instruction only: even / odd i; instruction i adds (i & ~1) * step, step being
@@ -191,7 +199,7 @@ struct OperandTile {
   int mn_valid;
 
   __device__ __forceinline__ static int lds_row(int wave, int i, int lane) {
-    return (wave * kPerWave + i) * kRPI + lane / kCPR;
+    return block(wave, i) * kRPI + lane / kCPR;
   }
   // Operand row (m / n for K-contiguous tiles, k for MN-contiguous ones) and
   // 16-byte chunk that the lane fetches in instruction i.
@@ -223,22 +231,23 @@ struct OperandTile {
       voff[par] = KC ? static_cast<uint32_t>((r * s_mn + c * 8) * 2)
                      : static_cast<uint32_t>((r * s_k + c * 8) * 2);
     }
-    step = static_cast<uint32_t>((KC16 ? kRPI / 2 : kRPI) * (KC ? s_mn : s_k) * 2);
+    step = static_cast<uint32_t>((IL ? 32 : KC16 ? kRPI / 2 : kRPI) * (KC ? s_mn : s_k) * 2);
   }
   __device__ __forceinline__ uint32_t off(int i) const {
-    return voff[i & 1] + static_cast<uint32_t>(i & ~1) * step;
+    if constexpr (IL) return voff[0] + static_cast<uint32_t>(i) * step;
+    else return voff[i & 1] + static_cast<uint32_t>(i & ~1) * step;
   }
   // Instruction i of this wave's share (see issue()).
   template <bool FULL>
   __device__ __forceinline__ void issue_one(i32x4_t rs, uint32_t lds, int wave, int lane, int k_left, int i) const {
     const uint32_t v = off(i);
     if constexpr (FULL) {
-      dma16(rs, lds + (wave * kPerWave + i) * 1024, v);
+      dma16(rs, lds + block(wave, i) * 1024, v);
     } else {
       const int r = row_of(wave, i, lane);
       const int c = chunk_of(wave, i, lane);
       const bool ok = KC ? (r < mn_valid && c * 8 < k_left) : (r < k_left && c * 8 < mn_valid);
-      dma16(rs, lds + (wave * kPerWave + i) * 1024, ok ? v : kOffOOB);
+      dma16(rs, lds + block(wave, i) * 1024, ok ? v : kOffOOB);
     }
   }
   // lds: LDS byte address of the tile.  FULL: the whole tile lies inside the
@@ -250,12 +259,12 @@ struct OperandTile {
     for (int i = 0; i < kPerWave; ++i) {
       const uint32_t v = off(i);
       if constexpr (FULL) {
-        dma16(rs, lds + (wave * kPerWave + i) * 1024, v);
+        dma16(rs, lds + block(wave, i) * 1024, v);
       } else {
         const int r = row_of(wave, i, lane);
         const int c = chunk_of(wave, i, lane);
         const bool ok = KC ? (r < mn_valid && c * 8 < k_left) : (r < k_left && c * 8 < mn_valid);
-        dma16(rs, lds + (wave * kPerWave + i) * 1024, ok ? v : kOffOOB);
+        dma16(rs, lds + block(wave, i) * 1024, ok ? v : kOffOOB);
       }
     }
   }
@@ -971,6 +980,238 @@ __device__ __forceinline__ void gemm_bf16_body8km(const GemmParams& p, const Epi
   mfma_drain(acc);
 
   tile_epilogue<BM, BN, WM, WN, NP>(p, epi, smem, acc, bb, m0, n0, mn_full, lane, wm, wn);
+}
+
+// One 16x16x32 MFMA accumulating in place in AGPRs (the 4-wave cores keep 256
+// accumulators a lane); otherwise as mma16x32.
+template <bool F16>
+__device__ __forceinline__ void mma16x32a(f32x4_t& c, const bf16x8_t& a, const bf16x8_t& b) {
+  if constexpr (F16)
+    asm volatile("v_mfma_f32_16x16x32_f16 %0, %1, %2, %0" : "+a"(c) : "v"(a), "v"(b));
+  else
+    asm volatile("v_mfma_f32_16x16x32_bf16 %0, %1, %2, %0" : "+a"(c) : "v"(a), "v"(b));
+}
+template <int FM, int FN>
+__device__ __forceinline__ void mfma_drain_a(f32x4_t (&acc)[FM][FN]) {
+  asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j) asm volatile("" : "+a"(acc[i][j]));
+}
+
+// 4-wave core for A K-contiguous and B MN-contiguous (the DotGeneral config): one
+// 256 x 256 tile per workgroup of 2 x 2 waves, each 128 x 128 (64 16x16x32 MFMAs per
+// k32 step, 256 accumulators a lane in AGPRs, one wave per SIMD).  A wave reads 16
+// fragments per 64 MFMAs from LDS, a third less than the 8-wave core's 128 x 64
+// waves (12 per 32), for the same DMA traffic; under the board's power limit the
+// LDS bytes are energy the MFMAs do not get.
+//
+// LDS staging as in gemm_bf16_body8km (B in four 32-deep stages, A in two 64-deep
+// super-tile stages; the A DMA interleaves the waves so each instruction fills one
+// 32-row group).  With one wave per SIMD nothing hides a stall, so the issue order is
+// fixed (sched_fence) and no wait sits where the MFMA queue would drain:
+//   * tile kt's fragments are in registers when it starts (A rolling: fa[i] is
+//     refilled for tile kt+1 right after row block i's last MFMA; B double-buffered);
+//   * the wait and barrier of tile kt come after its first two row blocks: by then
+//     this wave's reads of stage kt (issued during tile kt-1) have completed, and
+//     the wait for tile kt+1's DMA (issued three tiles earlier) is normally a no-op;
+//   * after the barrier, stage kt takes tile kt+4 (and an odd kt's A stage the
+//     super-tile two ahead) by DMA spread over the remaining MFMAs, and tile kt+1's
+//     B fragments are read, two per row block.
+// DMA issue order per tile is A (odd tiles) then B, as in gemm_bf16_body8km, so the
+// same vmcnt counts hold.  Bit-identical to the other cores (same MFMA, same k order
+// per accumulator).
+template <class Epi, bool F16 = false>
+__device__ __forceinline__ void gemm_bf16_body4km(const GemmParams& p, const Epi& epi) {
+  constexpr int BM = 256, BN = 256, WM = 2, WN = 2, BK = 32;
+  constexpr int NW = WM * WN;
+  constexpr int TM = BM / WM, TN = BN / WN;
+  constexpr int FM = TM / 16, FN = TN / 16;  // 8 x 8 blocks of 16 x 16
+  using TA = OperandTile<BM, true, NW, 2 * BK, true, true>;
+  using TB = OperandTile<BN, false, NW, BK, true>;
+  constexpr int NA = TA::kPerWave;  // A loads per wave per super-tile (8)
+  constexpr int NB = TB::kPerWave;  // B loads per wave per tile (4)
+  constexpr int kSA = BM * 2 * BK * 2, kSB = BN * BK * 2;  // bytes per stage
+  constexpr int kLdsBytes = 4 * kSB + 2 * kSA;
+  static_assert(4 * kSB <= 65536 && kSA + TM * 2 * BK * 2 <= 65536, "fragment offsets fit the 16-bit immediate");
+  static_assert(NA + NB <= 12 && FM == 8 && FN == 8, "DMA slots of one tile");
+  __shared__ __attribute__((aligned(1024))) uint16_t smem[kLdsBytes / 2];
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wm = wave / WN, wn = wave % WN;
+
+  int64_t bb;
+  int tm, tn;
+  map_tile(blockIdx.x, p.batch * p.tiles_m * p.tiles_n, p.tiles_m, p.tiles_n, bb, tm, tn);
+  const int64_t m0 = static_cast<int64_t>(tm) * BM, n0 = static_cast<int64_t>(tn) * BN;
+  const uint16_t* A0 = static_cast<const uint16_t*>(p.a) + bb * p.sa_b + m0 * p.sa_m;
+  const uint16_t* B0 = static_cast<const uint16_t*>(p.b) + bb * p.sb_b + n0 * p.sb_n;
+  const uint32_t a_left0 = p.a_extent - static_cast<uint32_t>(m0 * p.sa_m * 2);
+  const uint32_t b_left0 = p.b_extent - static_cast<uint32_t>(n0 * p.sb_n * 2);
+
+  TA ta;
+  TB tb;
+  ta.init(wave, lane, p.sa_m, p.sa_k, p.M - m0);
+  tb.init(wave, lane, p.sb_n, p.sb_k, p.N - n0);
+  const bool mn_full = m0 + BM <= p.M && n0 + BN <= p.N;
+  const int KT = static_cast<int>((p.K + BK - 1) / BK);  // 32-deep tiles
+  const int KS = (KT + 1) / 2;                             // 64-deep A super-tiles
+  const uint32_t lds_b = static_cast<uint32_t>(reinterpret_cast<uint64_t>((GHIP_LDS void*)smem));
+  const uint32_t lds_a = lds_b + 4 * kSB;
+
+  f32x4_t acc[FM][FN];
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) acc[i][j][v] = 0.f;
+
+  // Per-lane LDS base pointers, as in gemm_bf16_body8km.
+  typedef GHIP_LDS const uint16_t* lds_p;
+  lds_p const lds0 = (lds_p)((GHIP_LDS void*)smem);
+  lds_p abase[2][2], bbase[FN];
+#pragma unroll
+  for (int par = 0; par < 2; ++par)
+#pragma unroll
+    for (int as = 0; as < 2; ++as) {
+      const int rho = wm * TM + 2 * (lane & 15) + ((lane >> 4) & 1);
+      abase[par][as] = lds0 + 2 * kSB + rho * (2 * BK) + (((4 * par + 2 * as + (lane >> 5)) ^ swz_k(rho)) * 8);
+    }
+#pragma unroll
+  for (int j = 0; j < FN; ++j) {
+    const int kl = 8 * (lane >> 4) + ((lane & 15) >> 2);
+    const int nl = wn * TN + j * 16 + 4 * (lane & 3);
+    bbase[j] = lds0 + kl * BN + (((nl >> 3) ^ swz_n2(kl)) * 8) + (nl & 7);
+  }
+  bf16x8_t fa[FM], fb[2][FN];
+  auto read_a = [&](int i, int sa, int as) {  // row block i from A stage sa, k32 step as
+    fa[i] = *(GHIP_LDS const bf16x8_t*)(abase[i & 1][as] + sa * (kSA / 2) + (i >> 1) * 32 * (2 * BK));
+  };
+  auto read_b = [&](int buf, int j, int sb) {  // column block j from B stage sb into buffer buf
+    lds_p p0 = bbase[j] + sb * (kSB / 2);
+    const bf16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((GHIP_LDS bf16x4_t*)(p0));
+    const bf16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((GHIP_LDS bf16x4_t*)(p0 + 4 * BN));
+    fb[buf][j] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+  };
+
+  auto run = [&](auto full_c) {
+    constexpr bool FULL = decltype(full_c)::value;
+    auto dma_a = [&](int j, int d) {  // instruction d of A super-tile j (k 64j ..) into A stage j % 2
+      const int64_t k0 = static_cast<int64_t>(j) * 2 * BK;
+      const int k_left = static_cast<int>(p.K - k0 < 2 * BK ? p.K - k0 : 2 * BK);
+      const i32x4_t ra = make_rsrc(A0 + k0 * p.sa_k, a_left0 - static_cast<uint32_t>(k0 * p.sa_k * 2));
+      ta.template issue_one<FULL>(ra, lds_a + (j & 1) * kSA, wave, lane, k_left, d);
+    };
+    auto dma_b = [&](int t, int d) {  // instruction d of B tile t into B stage t % 4
+      const int64_t k0 = static_cast<int64_t>(t) * BK;
+      const int k_left = static_cast<int>(p.K - k0 < BK ? p.K - k0 : BK);
+      const i32x4_t rb = make_rsrc(B0 + k0 * p.sb_k, b_left0 - static_cast<uint32_t>(k0 * p.sb_k * 2));
+      tb.template issue_one<FULL>(rb, lds_b + (t & 3) * kSB, wave, lane, k_left, d);
+    };
+    auto issue_a = [&](int j) {
+      if (j < KS) {
+#pragma unroll
+        for (int d = 0; d < NA; ++d) dma_a(j, d);
+      }
+    };
+    auto issue_b = [&](int t) {
+      if (t < KT) {
+#pragma unroll
+        for (int d = 0; d < NB; ++d) dma_b(t, d);
+      }
+    };
+    // Prologue in the steady state's issue order (as if barriers -4 .. -1 had run).
+    issue_b(0);
+    issue_a(0);
+    issue_b(1);
+    issue_b(2);
+    issue_a(1);
+    issue_b(3);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < FN; ++j) read_b(0, j, 0);
+#pragma unroll
+    for (int i = 0; i < FM; ++i) read_a(i, 0, 0);
+
+    // Tile kt (B stage ST = kt % 4, A stage ST / 2, k32 step ST % 2 of the
+    // super-tile; B fragments in fb[ST % 2]).  STEADY: tiles kt+1 and kt+4 exist.
+    auto tile = [&](int kt, auto st_c, auto steady_c) {
+      constexpr int ST = decltype(st_c)::value;
+      constexpr int SN = (ST + 1) % 4;
+      constexpr int CB = ST & 1;
+      constexpr bool STEADY = decltype(steady_c)::value;
+      const bool nx = STEADY || kt + 1 < KT;
+      const bool do_b = STEADY || kt + 4 < KT;
+      const bool do_a = ST % 2 == 1 && (STEADY || (kt + 3) / 2 < KS);
+      constexpr int ND = (ST % 2 == 1 ? NA : 0) + NB;  // DMA instructions of this tile
+#pragma unroll
+      for (int i = 0; i < FM; ++i) {
+#pragma unroll
+        for (int j = 0; j < FN; ++j) {
+          mma16x32a<F16>(acc[i][j], fb[CB][j], fa[i]);
+          if (i >= 2 && nx) {
+            // After the barrier: one DMA instruction every 4th MFMA, tile kt+1's B
+            // fragments two per row block (rows 2-5).
+            const int q = (i - 2) * FN + j;  // 0 .. 47
+            if (q % 4 == 0 && q / 4 < ND) {
+              const int d = q / 4;
+              if (ST % 2 == 1 && d < NA) {
+                if (do_a) dma_a(kt / 2 + 2, d);
+              } else if (do_b) {
+                dma_b(kt + 4, ST % 2 == 1 ? d - NA : d);
+              }
+            }
+            if (q % 4 == 2 && q / 4 < FN) read_b(CB ^ 1, q / 4, SN);
+          }
+          sched_fence();
+        }
+        if (i == 1 && nx) {
+          // Tile kt+1 has landed (this wave's loads, then everyone's through the
+          // barrier), and every wave has finished reading stage ST (its fragments
+          // were read during tile kt-1), which may now be refilled.
+          if constexpr (STEADY) {
+            if constexpr (ST % 2 == 1)
+              asm volatile("s_waitcnt lgkmcnt(0)\n\ts_waitcnt vmcnt(%0)" ::"n"(2 * NB) : "memory");
+            else
+              asm volatile("s_waitcnt lgkmcnt(0)\n\ts_waitcnt vmcnt(%0)" ::"n"(2 * NB + NA) : "memory");
+          } else {
+            asm volatile("s_waitcnt lgkmcnt(0)\n\ts_waitcnt vmcnt(0)" ::: "memory");
+          }
+          __syncthreads();
+          read_a(0, SN / 2, SN % 2);
+          read_a(1, SN / 2, SN % 2);
+          sched_fence();
+        }
+        if (i >= 2 && nx) {
+          read_a(i, SN / 2, SN % 2);
+          sched_fence();
+        }
+      }
+    };
+    int kt = 0;
+    for (; kt + 7 < KT; kt += 4) {
+      tile(kt, IntC<0>{}, BoolC<true>{});
+      tile(kt + 1, IntC<1>{}, BoolC<true>{});
+      tile(kt + 2, IntC<2>{}, BoolC<true>{});
+      tile(kt + 3, IntC<3>{}, BoolC<true>{});
+    }
+    for (; kt < KT; kt += 4) {
+      tile(kt, IntC<0>{}, BoolC<false>{});
+      if (kt + 1 < KT) tile(kt + 1, IntC<1>{}, BoolC<false>{});
+      if (kt + 2 < KT) tile(kt + 2, IntC<2>{}, BoolC<false>{});
+      if (kt + 3 < KT) tile(kt + 3, IntC<3>{}, BoolC<false>{});
+    }
+  };
+  if (mn_full && (p.K % (2 * BK)) == 0) run(BoolC<true>{});
+  else run(BoolC<false>{});
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  mfma_drain_a(acc);
+
+  tile_epilogue<BM, BN, WM, WN, 1>(p, epi, smem, acc, bb, m0, n0, mn_full, lane, wm, wn);
 }
 
 // 8-wave 16x16x32 core for any operand layout (the A K-contiguous / B MN-contiguous

@@ -100,11 +100,12 @@ __global__ __launch_bounds__(WM* WN * 64, 1) void gemm_bf16_kernel(GemmParams p)
   const StoreEpi<OutT> epi = store_epi<OutT>(p);
   gemm_bf16_body<BM, BN, WM, WN, A_K, B_K, 1, StoreEpi<OutT>, __is_same(InT, f16_t)>(p, epi);
 }
-// The 8-wave 256 x 256 core for A K-contiguous, B MN-contiguous (32-deep k-steps).
+// The 4-wave 256 x 256 16x16x32 core for A K-contiguous, B MN-contiguous (128 x 128
+// waves, AGPR accumulators).
 template <typename InT, typename OutT>
-__global__ __launch_bounds__(512, 1) void gemm_bf16_kernel8km(GemmParams p) {
+__global__ __launch_bounds__(256, 1) void gemm_bf16_kernel4km(GemmParams p) {
   const StoreEpi<OutT> epi = store_epi<OutT>(p);
-  gemm_bf16_body8km<StoreEpi<OutT>, __is_same(InT, f16_t)>(p, epi);
+  gemm_bf16_body4km<StoreEpi<OutT>, __is_same(InT, f16_t)>(p, epi);
 }
 // The 4-wave 256 x 256 core for both operands MN-contiguous (32-deep, four stages).
 template <typename InT, typename OutT>
@@ -379,7 +380,7 @@ static hipError_t launch_bf16_4w(GemmParams p, bool a_k, bool b_k, hipStream_t s
   p.tiles_n = static_cast<int>((p.N + 255) / 256);
   const dim3 grid(static_cast<unsigned>(p.batch * p.tiles_m * p.tiles_n));
   if (a_k && b_k) hipLaunchKernelGGL((gemm_bf16_kernel8x<true, true, InT, OutT>), grid, dim3(512), 0, s, p);
-  else if (a_k) hipLaunchKernelGGL((gemm_bf16_kernel8km<InT, OutT>), grid, dim3(512), 0, s, p);
+  else if (a_k) hipLaunchKernelGGL((gemm_bf16_kernel4km<InT, OutT>), grid, dim3(256), 0, s, p);
   else if (b_k) hipLaunchKernelGGL((gemm_bf16_kernel8x<false, true, InT, OutT>), grid, dim3(512), 0, s, p);
   else hipLaunchKernelGGL((gemm_bf16_kernel4mn<InT, OutT>), grid, dim3(256), 0, s, p);
   return hipGetLastError();

@@ -5,8 +5,8 @@ reads behind explicit waits, accumulators touched only by the MFMAs until a drai
 of 32 wait states); this checks the compiled code for it: in every kernel that
 instantiates the cores, no instruction other than an MFMA accumulating into the
 same registers reads or writes an MFMA's destination within the next 12
-instructions on any path (branches followed), for the precompiled kernels and for a
-generated epilogue (FusedDense + tanh-GELU).  CPU only: hipcc cross-compiles for gfx950 here."""
+instructions on any path (branches followed), for the precompiled kernels (VGPR or
+AGPR accumulators) and for a generated epilogue (FusedDense + tanh-GELU).  CPU only: hipcc cross-compiles for gfx950 here."""
 import os
 import re
 import subprocess
@@ -23,12 +23,14 @@ pytestmark = pytest.mark.skipif(not os.path.exists(HIPCC), reason="hipcc not ins
 
 
 def _regs(tok):
+    """Registers named by an operand: ("v", n) for VGPRs, ("a", n) for AGPRs (the
+    4-wave cores accumulate in AGPRs)."""
     tok = tok.strip()
-    m = re.match(r"v\[(\d+):(\d+)\]$", tok)
+    m = re.match(r"([va])\[(\d+):(\d+)\]$", tok)
     if m:
-        return set(range(int(m.group(1)), int(m.group(2)) + 1))
-    m = re.match(r"v(\d+)$", tok)
-    return {int(m.group(1))} if m else set()
+        return {(m.group(1), r) for r in range(int(m.group(2)), int(m.group(3)) + 1)}
+    m = re.match(r"([va])(\d+)$", tok)
+    return {(m.group(1), int(m.group(2)))} if m else set()
 
 
 def _violations(asm_lines, kernel_names, window=12):
@@ -90,8 +92,8 @@ def _compile(src, out, extra=()):
 
 def test_precompiled_cores_keep_mfma_hazards(tmp_path):
     lines = _compile(os.path.join(CSRC, "k_gemm.hip"), str(tmp_path / "k_gemm.s"))
-    count, bad = _violations(lines, ["kernel8km", "kernel8x"])
-    assert count >= 1024, count  # every instantiation, unrolled
+    count, bad = _violations(lines, ["kernel4km", "kernel8x"])
+    assert count >= 2048, count  # every instantiation, unrolled
     assert not bad, bad[:5]
 
 
