@@ -1022,20 +1022,26 @@ __device__ __forceinline__ void mfma_drain_a(f32x4_t (&acc)[FM][FN]) {
 // DMA issue order per tile is A (odd tiles) then B, as in gemm_bf16_body8km, so the
 // same vmcnt counts hold.  Bit-identical to the other cores (same MFMA, same k order
 // per accumulator).
-template <class Epi, bool F16 = false>
+//
+// NP = 2 computes A.B and A.B1 (two products sharing A) on a 256 x (2 x 128) tile,
+// as gemm_bf16_body8km does: each B stage holds 128 columns of B, then those of B1,
+// and a wave's 128 x 128 sub-tile is 64 columns of each.
+template <class Epi, bool F16 = false, int NP = 1>
 __device__ __forceinline__ void gemm_bf16_body4km(const GemmParams& p, const Epi& epi) {
-  constexpr int BM = 256, BN = 256, WM = 2, WN = 2, BK = 32;
+  static_assert(NP == 1 || NP == 2, "one or two right operands");
+  constexpr int BM = 256, BN = 256 / NP, WM = 2, WN = 2, BK = 32;  // BN: per product
   constexpr int NW = WM * WN;
   constexpr int TM = BM / WM, TN = BN / WN;
-  constexpr int FM = TM / 16, FN = TN / 16;  // 8 x 8 blocks of 16 x 16
+  constexpr int FM = TM / 16, FN = TN / 16, FB = NP * FN;  // 8 x 8 blocks of 16 x 16
   using TA = OperandTile<BM, true, NW, 2 * BK, true, true>;
   using TB = OperandTile<BN, false, NW, BK, true>;
-  constexpr int NA = TA::kPerWave;  // A loads per wave per super-tile (8)
-  constexpr int NB = TB::kPerWave;  // B loads per wave per tile (4)
-  constexpr int kSA = BM * 2 * BK * 2, kSB = BN * BK * 2;  // bytes per stage
+  constexpr int NA = TA::kPerWave;          // A loads per wave per super-tile (8)
+  constexpr int NBP = TB::kPerWave;         // B loads per wave per tile and product
+  constexpr int NB = NP * NBP;              // B loads per wave per tile (4)
+  constexpr int kSA = BM * 2 * BK * 2, kSB1 = BN * BK * 2, kSB = NP * kSB1;  // bytes per stage
   constexpr int kLdsBytes = 4 * kSB + 2 * kSA;
   static_assert(4 * kSB <= 65536 && kSA + TM * 2 * BK * 2 <= 65536, "fragment offsets fit the 16-bit immediate");
-  static_assert(NA + NB <= 12 && FM == 8 && FN == 8, "DMA slots of one tile");
+  static_assert(NA + NB <= 12 && FM == 8 && FB == 8, "DMA slots of one tile");
   __shared__ __attribute__((aligned(1024))) uint16_t smem[kLdsBytes / 2];
 
   const int lane = threadIdx.x & 63;
@@ -1048,6 +1054,7 @@ __device__ __forceinline__ void gemm_bf16_body4km(const GemmParams& p, const Epi
   const int64_t m0 = static_cast<int64_t>(tm) * BM, n0 = static_cast<int64_t>(tn) * BN;
   const uint16_t* A0 = static_cast<const uint16_t*>(p.a) + bb * p.sa_b + m0 * p.sa_m;
   const uint16_t* B0 = static_cast<const uint16_t*>(p.b) + bb * p.sb_b + n0 * p.sb_n;
+  const uint16_t* B1 = static_cast<const uint16_t*>(NP == 2 ? p.b1 : p.b) + bb * p.sb_b + n0 * p.sb_n;
   const uint32_t a_left0 = p.a_extent - static_cast<uint32_t>(m0 * p.sa_m * 2);
   const uint32_t b_left0 = p.b_extent - static_cast<uint32_t>(n0 * p.sb_n * 2);
 
@@ -1061,11 +1068,11 @@ __device__ __forceinline__ void gemm_bf16_body4km(const GemmParams& p, const Epi
   const uint32_t lds_b = static_cast<uint32_t>(reinterpret_cast<uint64_t>((GHIP_LDS void*)smem));
   const uint32_t lds_a = lds_b + 4 * kSB;
 
-  f32x4_t acc[FM][FN];
+  f32x4_t acc[FM][FB];
 #pragma unroll
   for (int i = 0; i < FM; ++i)
 #pragma unroll
-    for (int j = 0; j < FN; ++j)
+    for (int j = 0; j < FB; ++j)
 #pragma unroll
       for (int v = 0; v < 4; ++v) acc[i][j][v] = 0.f;
 
@@ -1086,15 +1093,15 @@ __device__ __forceinline__ void gemm_bf16_body4km(const GemmParams& p, const Epi
     const int nl = wn * TN + j * 16 + 4 * (lane & 3);
     bbase[j] = lds0 + kl * BN + (((nl >> 3) ^ swz_n2(kl)) * 8) + (nl & 7);
   }
-  bf16x8_t fa[FM], fb[2][FN];
+  bf16x8_t fa[FM], fb[2][FB];
   auto read_a = [&](int i, int sa, int as) {  // row block i from A stage sa, k32 step as
     fa[i] = *(GHIP_LDS const bf16x8_t*)(abase[i & 1][as] + sa * (kSA / 2) + (i >> 1) * 32 * (2 * BK));
   };
-  auto read_b = [&](int buf, int j, int sb) {  // column block j from B stage sb into buffer buf
-    lds_p p0 = bbase[j] + sb * (kSB / 2);
+  auto read_b = [&](int buf, int jj, int sb) {  // column block jj (product jj / FN) from B stage sb
+    lds_p p0 = bbase[jj % FN] + sb * (kSB / 2) + (jj / FN) * (kSB1 / 2);
     const bf16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((GHIP_LDS bf16x4_t*)(p0));
     const bf16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((GHIP_LDS bf16x4_t*)(p0 + 4 * BN));
-    fb[buf][j] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+    fb[buf][jj] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
   };
 
   auto run = [&](auto full_c) {
@@ -1105,11 +1112,12 @@ __device__ __forceinline__ void gemm_bf16_body4km(const GemmParams& p, const Epi
       const i32x4_t ra = make_rsrc(A0 + k0 * p.sa_k, a_left0 - static_cast<uint32_t>(k0 * p.sa_k * 2));
       ta.template issue_one<FULL>(ra, lds_a + (j & 1) * kSA, wave, lane, k_left, d);
     };
-    auto dma_b = [&](int t, int d) {  // instruction d of B tile t into B stage t % 4
+    auto dma_b = [&](int t, int d) {  // instruction d of B tile t into B stage t % 4 (d / NBP: product)
       const int64_t k0 = static_cast<int64_t>(t) * BK;
       const int k_left = static_cast<int>(p.K - k0 < BK ? p.K - k0 : BK);
-      const i32x4_t rb = make_rsrc(B0 + k0 * p.sb_k, b_left0 - static_cast<uint32_t>(k0 * p.sb_k * 2));
-      tb.template issue_one<FULL>(rb, lds_b + (t & 3) * kSB, wave, lane, k_left, d);
+      const uint16_t* Bp = (NP == 2 && d >= NBP) ? B1 : B0;
+      const i32x4_t rb = make_rsrc(Bp + k0 * p.sb_k, b_left0 - static_cast<uint32_t>(k0 * p.sb_k * 2));
+      tb.template issue_one<FULL>(rb, lds_b + (t & 3) * kSB + (d / NBP) * kSB1, wave, lane, k_left, d % NBP);
     };
     auto issue_a = [&](int j) {
       if (j < KS) {
@@ -1133,7 +1141,7 @@ __device__ __forceinline__ void gemm_bf16_body4km(const GemmParams& p, const Epi
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
 #pragma unroll
-    for (int j = 0; j < FN; ++j) read_b(0, j, 0);
+    for (int j = 0; j < FB; ++j) read_b(0, j, 0);
 #pragma unroll
     for (int i = 0; i < FM; ++i) read_a(i, 0, 0);
 
@@ -1151,12 +1159,12 @@ __device__ __forceinline__ void gemm_bf16_body4km(const GemmParams& p, const Epi
 #pragma unroll
       for (int i = 0; i < FM; ++i) {
 #pragma unroll
-        for (int j = 0; j < FN; ++j) {
+        for (int j = 0; j < FB; ++j) {
           mma16x32a<F16>(acc[i][j], fb[CB][j], fa[i]);
           if (i >= 2 && nx) {
             // After the barrier: one DMA instruction every 4th MFMA, tile kt+1's B
             // fragments two per row block (rows 2-5).
-            const int q = (i - 2) * FN + j;  // 0 .. 47
+            const int q = (i - 2) * FB + j;  // 0 .. 47
             if (q % 4 == 0 && q / 4 < ND) {
               const int d = q / 4;
               if (ST % 2 == 1 && d < NA) {
@@ -1165,7 +1173,7 @@ __device__ __forceinline__ void gemm_bf16_body4km(const GemmParams& p, const Epi
                 dma_b(kt + 4, ST % 2 == 1 ? d - NA : d);
               }
             }
-            if (q % 4 == 2 && q / 4 < FN) read_b(CB ^ 1, q / 4, SN);
+            if (q % 4 == 2 && q / 4 < FB) read_b(CB ^ 1, q / 4, SN);
           }
           sched_fence();
         }
@@ -1211,7 +1219,7 @@ __device__ __forceinline__ void gemm_bf16_body4km(const GemmParams& p, const Epi
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   mfma_drain_a(acc);
 
-  tile_epilogue<BM, BN, WM, WN, 1>(p, epi, smem, acc, bb, m0, n0, mn_full, lane, wm, wn);
+  tile_epilogue<BM, BN, WM, WN, NP>(p, epi, smem, acc, bb, m0, n0, mn_full, lane, wm, wn);
 }
 
 // 8-wave 16x16x32 core for any operand layout (the A K-contiguous / B MN-contiguous

@@ -107,10 +107,10 @@ def test_bias_relu_broadcast(be):
 
 
 @pytest.mark.parametrize("rows,cols,k,core", [(300, 264, 136, "8w-k64"), (1024, 512, 136, "8w-k64"),
-                                              (2000, 2000, 1000, "8w-km32"), (2048, 2048, 512, "8w-km32")])
+                                              (2000, 2000, 1000, "4w-km32"), (2048, 2048, 512, "4w-km32")])
 def test_swiglu_two_products(be, rows, cols, k, core):
     """SiLU(x.Wg) * (x.Wu): both products in one kernel sharing the x tile.  Grids
-    of >= 128 tiles run the 8-wave 32-deep core (ragged: rows, cols and k not
+    of >= 128 tiles run the 4-wave 128 x 128-wave core (ragged: rows, cols and k not
     multiples of the tile), smaller ones the 64-deep core; the large cases are
     checked bit for bit against the unfused plan, whose products the DotGeneral
     tests check against the oracle."""

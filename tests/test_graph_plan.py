@@ -311,16 +311,18 @@ def test_fused_dense_and_qkv_plans(be):
 
 def test_epilogue_core_follows_layout_and_epilogue_weight(be):
     """Large products with A K-contiguous and B N-contiguous (x . W, the DotGeneral
-    config's layout) run the 8-wave 32-deep core whatever the epilogue; B
-    K-contiguous layouts the 8-wave 64-deep core; both operands MN-contiguous the
-    4-wave 32-deep core for a light epilogue (a residual add) and the 8-wave 64-deep
-    core for a VALU-heavy one (tanh-GELU: a transcendental in a 10-op chain)."""
+    config's layout) run the 4-wave 128 x 128-wave core for a light epilogue (a
+    residual add) or two products (SwiGLU) and the 8-wave 32-deep core for a
+    VALU-heavy epilogue of one product (tanh-GELU: a transcendental in a 10-op
+    chain); B K-contiguous layouts the 8-wave 64-deep core; both operands
+    MN-contiguous the 4-wave 32-deep core for a light epilogue and the 8-wave 64-deep
+    core for a VALU-heavy one."""
     x = make_shape(BF16, 8, 1024, 2048)
     gelu = _plan(be, lambda f, xx, w, b: [f.FusedDense(xx, w, b, 1)], [x, make_shape(BF16, 2048, 8192), make_shape(BF16, 8192)])
     assert "gemm_batched+epilogue" in gelu and "waves=8" in gelu, gelu
     resid = _plan(be, lambda f, xx, w, r: [f.Add(f.DotGeneral(xx, [2], [], w, [0], []), r)],
                   [x, make_shape(BF16, 2048, 2048), x])
-    assert "gemm_batched+epilogue" in resid and "waves=8" in resid, resid
+    assert "gemm_batched+epilogue" in resid and "waves=4" in resid, resid
     # W stored [N, K] (x . W^T): B K-contiguous
     resid_t = _plan(be, lambda f, xx, w, r: [f.Add(f.DotGeneral(xx, [2], [], w, [1], []), r)],
                     [x, make_shape(BF16, 2048, 2048), x])
@@ -328,7 +330,7 @@ def test_epilogue_core_follows_layout_and_epilogue_weight(be):
     gelu_t = _plan(be, lambda f, xx, w: [f.FusedGelu(f.DotGeneral(xx, [2], [], w, [1], []), False)],
                    [x, make_shape(BF16, 8192, 2048)])
     assert "gemm_batched+epilogue" in gelu_t and "waves=8" in gelu_t and "core=8w-k64" in gelu_t, gelu_t
-    assert "core=8w-km32" in gelu and "core=8w-km32" in resid and "core=8w-k64" in resid_t
+    assert "core=8w-km32" in gelu and "core=4w-km32" in resid and "core=8w-k64" in resid_t
     # x^T . dY (both MN-contiguous): light epilogue on 4 waves, heavy on 8
     xt = make_shape(BF16, 2048, 8192)
     resid_mm = _plan(be, lambda f, xx, w, r: [f.Add(f.DotGeneral(xx, [0], [], w, [0], []), r)],
@@ -338,15 +340,15 @@ def test_epilogue_core_follows_layout_and_epilogue_weight(be):
                     [xt, make_shape(BF16, 2048, 2048)])
     assert "core=8w-k64" in gelu_mm, gelu_mm
 
-    # SwiGLU: two products sharing x in one kernel, on the 32-deep core for x . W
+    # SwiGLU: two products sharing x in one kernel, on the 4-wave core for x . W
     def swiglu(f, xx, wg, wu):
         g = f.DotGeneral(xx, [2], [], wg, [0], [])
         return [f.Mul(f.Mul(g, f.Logistic(g)), f.DotGeneral(xx, [2], [], wu, [0], []))]
     w = make_shape(BF16, 2048, 8192)
     sw = _plan(be, swiglu, [x, w, w])
-    assert "dots=2" in sw and "core=8w-km32" in sw and "tile=256x256" in sw, sw
+    assert "dots=2" in sw and "core=4w-km32" in sw and "tile=256x256" in sw, sw
     small = _plan(be, swiglu, [make_shape(BF16, 1, 1024, 2048), w, w])
-    assert "dots=2" in small and "core=8w-km32" in small, small  # 4 x 64 tiles
+    assert "dots=2" in small and "core=4w-km32" in small, small  # 4 x 64 tiles
     tiny = _plan(be, swiglu, [make_shape(BF16, 1, 256, 2048), make_shape(BF16, 2048, 1024), make_shape(BF16, 2048, 1024)])
     assert "dots=2" in tiny and "core=8w-k64" in tiny, tiny  # 8 tiles
 

@@ -97,17 +97,26 @@ def test_precompiled_cores_keep_mfma_hazards(tmp_path):
     assert not bad, bad[:5]
 
 
-def test_generated_epilogue_keeps_mfma_hazards(tmp_path, monkeypatch):
+@pytest.mark.parametrize("case", ["gelu", "residual"])
+def test_generated_epilogue_keeps_mfma_hazards(tmp_path, monkeypatch, case):
+    """FusedDense + tanh-GELU (8-wave core, VGPR accumulators) and x . W + r
+    (4-wave core, AGPR accumulators)."""
     from gomlx_hip.backend import Backend, ActivationType, dtypes, make_shape
     monkeypatch.setenv("GHIP_RTC_DUMP", str(tmp_path))
     be = Backend("plan")
     b = be.Builder("dense")
     f = b.Main()
     x = f.Parameter("x", make_shape(dtypes.BFloat16, 8, 1024, 2048))
-    w = f.Parameter("w", make_shape(dtypes.BFloat16, 2048, 8192))
-    bias = f.Parameter("b", make_shape(dtypes.BFloat16, 8192))
-    f.Return([f.FusedDense(x, w, bias, ActivationType.GELU)])
-    b.Compile()
+    if case == "gelu":
+        w = f.Parameter("w", make_shape(dtypes.BFloat16, 2048, 8192))
+        bias = f.Parameter("b", make_shape(dtypes.BFloat16, 8192))
+        f.Return([f.FusedDense(x, w, bias, ActivationType.GELU)])
+    else:
+        w = f.Parameter("w", make_shape(dtypes.BFloat16, 2048, 2048))
+        r = f.Parameter("r", make_shape(dtypes.BFloat16, 8, 1024, 2048))
+        f.Return([f.Add(f.DotGeneral(x, [2], [], w, [0], []), r)])
+    plan = b.Compile().Plan()
+    assert ("core=8w-km32" if case == "gelu" else "core=4w-km32") in plan, plan
     srcs = [p for p in os.listdir(tmp_path) if p.startswith("gemm_epilogue") and p.endswith(".hip")]
     assert srcs, os.listdir(tmp_path)
     lines = _compile(str(tmp_path / srcs[0]), str(tmp_path / "epi.s"), ("-ffp-contract=off",))
