@@ -27,6 +27,22 @@ __global__ __launch_bounds__(256) void strided_copy_kernel(const E* __restrict__
   }
 }
 
+// Dense copy of n 16-byte vectors: each thread moves kPer vectors, all loads
+// issued before the stores, nontemporal both ways (the data is streamed once).
+constexpr int kCopyPer = 4;
+typedef unsigned u32x4_nt __attribute__((ext_vector_type(4)));
+__global__ __launch_bounds__(256) void copy_dense16_kernel(const u32x4_nt* __restrict__ src,
+                                                          u32x4_nt* __restrict__ dst, int64_t n) {
+  const int64_t base = static_cast<int64_t>(blockIdx.x) * (256 * kCopyPer) + threadIdx.x;
+  u32x4_nt v[kCopyPer];
+#pragma unroll
+  for (int k = 0; k < kCopyPer; ++k)
+    if (base + k * 256 < n) v[k] = __builtin_nontemporal_load(src + base + k * 256);
+#pragma unroll
+  for (int k = 0; k < kCopyPer; ++k)
+    if (base + k * 256 < n) __builtin_nontemporal_store(v[k], dst + base + k * 256);
+}
+
 static unsigned grid_for(int64_t total) {
   int64_t g = (total + 255) / 256;
   if (g > 65536) g = 65536;
@@ -35,10 +51,45 @@ static unsigned grid_for(int64_t total) {
 
 int launch_strided_copy(int elem_bytes, const void* src, void* dst, const CopyDesc& din,
                         hipStream_t s, GHipError* err) {
-  CopyDesc d = din;
+  // Drop unit axes and merge an axis into the next one when both sides step
+  // through them as one run (stride[k] == stride[k+1] * dims[k+1]): fewer
+  // divisions per element, and a dense copy becomes rank 1.
+  CopyDesc d;
+  d.rank = 0;
   int64_t total = 1;
-  for (int k = 0; k < d.rank; ++k) total *= d.dims[k];
+  for (int k = 0; k < din.rank; ++k) {
+    total *= din.dims[k];
+    if (din.dims[k] == 1) continue;
+    if (d.rank > 0 && d.sst[d.rank - 1] == din.sst[k] * din.dims[k] && d.dst[d.rank - 1] == din.dst[k] * din.dims[k]) {
+      d.dims[d.rank - 1] *= din.dims[k];
+      d.sst[d.rank - 1] = din.sst[k];
+      d.dst[d.rank - 1] = din.dst[k];
+      continue;
+    }
+    d.dims[d.rank] = din.dims[k];
+    d.sst[d.rank] = din.sst[k];
+    d.dst[d.rank] = din.dst[k];
+    ++d.rank;
+  }
   if (total == 0) return GHIP_OK;
+  if (d.rank == 0) {  // a single element
+    d.rank = 1;
+    d.dims[0] = 1;
+    d.sst[0] = d.dst[0] = 1;
+  }
+  // Dense on both sides: 16-byte vectors when the size and both bases allow.
+  if (d.rank == 1 && d.sst[0] == 1 && d.dst[0] == 1) {
+    const int64_t bytes = total * elem_bytes;
+    if (bytes % 16 == 0 && reinterpret_cast<uintptr_t>(src) % 16 == 0 && reinterpret_cast<uintptr_t>(dst) % 16 == 0) {
+      const int64_t n = bytes / 16;
+      const int64_t g = (n + 256 * kCopyPer - 1) / (256 * kCopyPer);
+      if (g > 0x7fffffffLL) return set_error(err, GHIP_ERR_INVALID_ARG, "copy: too large");
+      hipLaunchKernelGGL(copy_dense16_kernel, dim3(static_cast<unsigned>(g)), dim3(256), 0, s,
+                         static_cast<const u32x4_nt*>(src), static_cast<u32x4_nt*>(dst), n);
+      GHIP_CHECK(hipGetLastError(), err);
+      return GHIP_OK;
+    }
+  }
   // Widen the element when the innermost axis is unit-stride on both sides and
   // its extent, both base pointers and all other strides allow it.
   int eb = elem_bytes;
@@ -258,3 +309,27 @@ int launch_gather_rows(const void* table, int64_t V_, int64_t row_bytes, const v
 }
 
 }  // namespace ghip
+
+extern "C" int ghip_copy_strided(int elem_bytes, const void* src, void* dst, int rank, const int64_t* dims,
+                                 const int64_t* src_strides, const int64_t* dst_strides, void* stream,
+                                 GHipError* err) {
+  using namespace ghip;
+  if (elem_bytes != 1 && elem_bytes != 2 && elem_bytes != 4 && elem_bytes != 8 && elem_bytes != 16)
+    return set_error(err, GHIP_ERR_INVALID_ARG, "copy: element size %d", elem_bytes);
+  if (rank < 0 || rank > kMaxRank) return set_error(err, GHIP_ERR_INVALID_ARG, "copy: rank %d", rank);
+  if (rank > 0 && (!dims || !src_strides || !dst_strides))
+    return set_error(err, GHIP_ERR_INVALID_ARG, "copy: null dims or strides");
+  CopyDesc d;
+  d.rank = rank;
+  int64_t total = 1;
+  for (int k = 0; k < rank; ++k) {
+    if (dims[k] < 0) return set_error(err, GHIP_ERR_INVALID_ARG, "copy: negative size");
+    d.dims[k] = dims[k];
+    d.sst[k] = src_strides[k];
+    d.dst[k] = dst_strides[k];
+    total *= dims[k];
+  }
+  if (total == 0) return GHIP_OK;
+  if (!src || !dst) return set_error(err, GHIP_ERR_INVALID_ARG, "copy: null pointer");
+  return launch_strided_copy(elem_bytes, src, dst, d, static_cast<hipStream_t>(stream), err);
+}

@@ -59,6 +59,8 @@ SIGNATURES = {
                              _errp],
     "ghip_scale_mask_softmax_rows_ex": [_int, _vp, _vp, _i64, _i64, _i64, _i64, _f32, _int, _vp, _int,
                                         ctypes.POINTER(_i64), _vp, _errp],
+    "ghip_copy_strided": [_int, _vp, _vp, _int, ctypes.POINTER(_i64), ctypes.POINTER(_i64),
+                          ctypes.POINTER(_i64), _vp, _errp],
 }
 
 _lib = None

@@ -116,6 +116,19 @@ def gemm(a: torch.Tensor, b: torch.Tensor, out_dtype=None, out=None, stream=None
     return c[0] if squeeze else c
 
 
+def copy(src: torch.Tensor, out: torch.Tensor, stream=None) -> torch.Tensor:
+    """out[...] = src[...] for tensors of one shape and element size, any strides."""
+    import ctypes
+    _check_dev(src, out)
+    if tuple(src.shape) != tuple(out.shape) or src.element_size() != out.element_size():
+        raise ValueError(f"copy: {tuple(src.shape)} x{src.element_size()} -> {tuple(out.shape)} x{out.element_size()}")
+    r = src.dim()
+    arr = ctypes.c_int64 * max(r, 1)
+    call("ghip_copy_strided", src.element_size(), src.data_ptr(), out.data_ptr(), r,
+         arr(*src.shape), arr(*src.stride()), arr(*out.stride()), _stream(stream))
+    return out
+
+
 def _strides3(t: torch.Tensor):
     """(batch, head, sequence) element strides of a [B, H, S, D] view."""
     import ctypes

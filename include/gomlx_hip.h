@@ -112,6 +112,17 @@ int ghip_layernorm_rows(int dtype, const void* x, const void* gamma, const void*
                         void* y, int64_t rows, int64_t n, float eps, void* stream,
                         GHipError* err);
 
+/* dst[i] = src[i] over `dims` (rank <= 8), both sides addressed by ELEMENT strides
+ * of elem_bytes-byte elements (1, 2, 4, 8 or 16): the copy that materialises
+ * transposed, broadcast, sliced or reversed views and writes outputs.  Axes that
+ * both sides step through as one run are merged first; a dense copy moves
+ * 16-byte vectors with nontemporal loads and stores.  No reference op:
+ * MPSGraph does these copies inside the graph (e.g. the rhs transposes of
+ * dotgeneral.go:116-145). */
+int ghip_copy_strided(int elem_bytes, const void* src, void* dst, int rank, const int64_t* dims,
+                      const int64_t* src_strides, const int64_t* dst_strides, void* stream,
+                      GHipError* err);
+
 /* Batched matrix product, the lowering target of Function.DotGeneral
  * (dotgeneral.go:65-164 -> mpsgraph_matmul, bridge.m:684-700):
  *   c[b, m, n] = sum_k a[b, m, k] * b[b, k, n]
