@@ -773,6 +773,46 @@ struct Lowerer {
     }
   }
 
+  // Softmax (op 0) or LayerNorm (op 3) over axis `axis` of x, which is not the
+  // last one: the column kernels on x read as dense [outer, n, inner], writing y in
+  // x's own layout (no transposing copy of x, none of y).
+  View emit_cols(int op, const Shape& xs, const View& xv, int axis, const Vec& gamma, const Vec& beta,
+                 double eps, const char* why) {
+    const int dt = xs.dtype;
+    if (!row_dtype(dt))
+      return fail(GHIP_ERR_UNSUPPORTED, fmt("row kernels take float32 / bfloat16 / float16, got %s", dtype_name(dt)).c_str());
+    int64_t outer = 1, inner = 1;
+    for (int i = 0; i < axis; ++i) outer *= xs.dims[i];
+    for (int i = axis + 1; i < xs.rank(); ++i) inner *= xs.dims[i];
+    const int64_t n = xs.dims[axis];
+    View x = materialize(xv, xs);
+    View g, b;
+    std::vector<int> rd{x.slot};
+    if (gamma.present) {
+      g = materialize(gamma.view, gamma.shape);
+      rd.push_back(g.slot);
+    }
+    if (beta.present) {
+      b = materialize(beta.view, beta.shape);
+      rd.push_back(b.slot);
+    }
+    if (failed) return bad();
+    View y = fresh(xs);
+    const bool hg = gamma.present, hb = beta.present;
+    const float fe = static_cast<float>(eps);
+    add_step(fmt("%s %s outer=%lld n=%lld inner=%lld%s%s %s", op == 0 ? "softmax_cols" : "layernorm_cols",
+                 dtype_name(dt), (long long)outer, (long long)n, (long long)inner, hg ? " +gamma" : "",
+                 hb ? " +beta" : "", why),
+             rd, {y.slot}, [=](ExecState& st, GHipError* e) {
+               const void* xp = st.ptr(x, dt);
+               void* yp = st.ptr(y, dt);
+               if (op == 0) return ghip_softmax_cols(dt, xp, yp, outer, n, inner, 0, st.stream, e);
+               return ghip_layernorm_cols(dt, xp, hg ? st.ptr(g, dt) : nullptr, hb ? st.ptr(b, dt) : nullptr, yp,
+                                          outer, n, inner, fe, st.stream, e);
+             });
+    return y;
+  }
+
   View emit_softmax(int v) {
     const Node& n = N[v];
     const Shape& xs = N[n.in[0]].shape;
@@ -780,13 +820,7 @@ struct Lowerer {
     if (failed) return bad();
     const int r = xs.rank(), axis = static_cast<int>(n.i0);
     if (axis == r - 1) return emit_rows(0, xs, xv, Vec{}, Vec{}, 0, "(FusedSoftmax)");
-    std::vector<int64_t> perm;
-    for (int i = 0; i < r; ++i)
-      if (i != axis) perm.push_back(i);
-    perm.push_back(axis);
-    View y = emit_rows(0, permute_shape(xs, perm), permute(xv, perm), Vec{}, Vec{}, 0, "(FusedSoftmax, axis moved last)");
-    if (failed) return bad();
-    return permute(y, inverse(perm));
+    return emit_cols(0, xs, xv, axis, Vec{}, Vec{}, 0, "(FusedSoftmax over a middle axis)");
   }
 
   View emit_layernorm(int v) {
@@ -798,6 +832,20 @@ struct Lowerer {
     const int k = static_cast<int>(n.a0.size());
     bool trailing = true;
     for (int i = 0; i < k; ++i) trailing = trailing && n.a0[i] == r - k + i;
+    if (k == 1 && !trailing) {
+      // One normalized axis before the last: the column kernel, when gamma / beta
+      // hold exactly that axis's n values (shape [n], or x's rank with every other
+      // axis of size 1).
+      const int ax = static_cast<int>(n.a0[0]);
+      auto along_axis = [&](int w) {
+        if (w < 0) return true;
+        const Shape& gs = N[w].shape;
+        if (gs.size() != xs.dims[ax]) return false;
+        return gs.rank() == 1 || (gs.rank() == r && gs.dims[ax] == xs.dims[ax]);
+      };
+      if (along_axis(n.in[1]) && along_axis(n.in[2]))
+        return emit_cols(3, xs, xv, ax, vec_of(n.in[1]), vec_of(n.in[2]), n.f0, "(FusedLayerNorm over a middle axis)");
+    }
     std::vector<int64_t> perm;
     for (int i = 0; i < r; ++i)
       if (std::find(n.a0.begin(), n.a0.end(), i) == n.a0.end()) perm.push_back(i);

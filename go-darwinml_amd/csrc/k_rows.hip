@@ -730,6 +730,126 @@ static int dispatch_rows(int dtype, const RowParams& p, void* stream, GHipError*
   return GHIP_OK;
 }
 
+// ---------------------------------------------------------------------------
+// Column kernels: softmax / log-softmax / LayerNorm over a middle axis of a dense
+// [outer, n, inner] tensor (inner > 1), in place of moving the axis last with a
+// transposing copy (and copying the result back).  A workgroup takes 64 adjacent
+// columns i of one outer index as 64 lanes x 4 row phases: lane c of phase ph
+// walks rows ph, ph + 4, ... of column i0 + c, so each wave instruction reads 64
+// consecutive elements of one row.  Per-column statistics in fp32 (softmax: a
+// running max and a sum of exponents rescaled when the max moves; LayerNorm: a
+// running count, mean and squared-deviation sum, Welford's update), combined
+// over the 4 phases through LDS (Chan, Golub and LeVeque's pairwise update for
+// LayerNorm), then a second pass writes y in the same layout (its reads of x
+// are mostly served by the L2 / Infinity Cache).  -inf inputs contribute nothing
+// to the sums; a column of -inf gives NaN, as the row kernels do.
+struct ColParams {
+  const void* x;
+  void* y;
+  const void* gamma;  // [n] or null (LayerNorm)
+  const void* beta;   // [n] or null (LayerNorm)
+  int64_t n, inner, col_blocks;
+  float eps;
+};
+
+template <typename T, int OP>
+__global__ __launch_bounds__(256) void cols_kernel(ColParams p) {
+  __shared__ float red[3][4][64];
+  const int c = threadIdx.x & 63, ph = threadIdx.x >> 6;
+  const int64_t o = blockIdx.x / p.col_blocks;
+  const int64_t i = (blockIdx.x % p.col_blocks) * 64 + c;
+  const bool ok = i < p.inner;
+  const int64_t n = p.n, inner = p.inner;
+  const T* x = static_cast<const T*>(p.x) + o * n * inner + (ok ? i : 0);
+  T* y = static_cast<T*>(p.y) + o * n * inner + (ok ? i : 0);
+  if constexpr (OP == kSoftmax || OP == kLogSoftmax) {
+    float m = -INFINITY, s = 0.f;
+    if (ok)
+      for (int64_t k = ph; k < n; k += 4) {
+        const float v = Elem<T>::load1(x + k * inner);
+        if (v == -INFINITY) continue;
+        if (v > m) {
+          s = m == -INFINITY ? 0.f : s * fast_exp(m - v);
+          m = v;
+        }
+        s += fast_exp(v - m);  // NaN inputs make s NaN
+      }
+    red[0][ph][c] = m;
+    red[1][ph][c] = s;
+    __syncthreads();
+    float M = red[0][0][c];
+#pragma unroll
+    for (int q = 1; q < 4; ++q) M = fmaxf(M, red[0][q][c]);
+    float S = 0.f;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const float mq = red[0][q][c];
+      if (mq != -INFINITY) S += red[1][q][c] * fast_exp(mq - M);
+    }
+    if (!ok) return;
+    const float inv = 1.0f / S, shift = M + logf(S);
+    for (int64_t k = ph; k < n; k += 4) {
+      const float v = Elem<T>::load1(x + k * inner);
+      Elem<T>::store1(y + k * inner, OP == kLogSoftmax ? v - shift : fast_exp(v - M) * inv);
+    }
+  } else {
+    static_assert(OP == kLayerNorm, "softmax, log-softmax or LayerNorm");
+    float cnt = 0.f, mean = 0.f, m2 = 0.f;
+    if (ok)
+      for (int64_t k = ph; k < n; k += 4) {
+        const float v = Elem<T>::load1(x + k * inner);
+        cnt += 1.f;
+        const float d = v - mean;
+        mean += d / cnt;
+        m2 += d * (v - mean);
+      }
+    red[0][ph][c] = cnt;
+    red[1][ph][c] = mean;
+    red[2][ph][c] = m2;
+    __syncthreads();
+    float na = red[0][0][c], ma = red[1][0][c], qa = red[2][0][c];
+#pragma unroll
+    for (int q = 1; q < 4; ++q) {
+      const float nb = red[0][q][c], mb = red[1][q][c], qb = red[2][q][c];
+      const float nt = na + nb;
+      if (nb > 0.f) {
+        const float d = mb - ma;
+        ma += d * (nb / nt);
+        qa += qb + d * d * (na * nb / nt);
+        na = nt;
+      }
+    }
+    if (!ok) return;
+    const float rstd = 1.0f / sqrtf(qa / static_cast<float>(n) + p.eps);
+    const T* g = static_cast<const T*>(p.gamma);
+    const T* b = static_cast<const T*>(p.beta);
+    for (int64_t k = ph; k < n; k += 4) {
+      float r = (Elem<T>::load1(x + k * inner) - ma) * rstd;
+      if (g) r *= Elem<T>::load1(g + k);
+      if (b) r += Elem<T>::load1(b + k);
+      Elem<T>::store1(y + k * inner, r);
+    }
+  }
+}
+
+template <int OP>
+static int dispatch_cols(int dtype, ColParams p, int64_t outer, void* stream, GHipError* err, const char* what) {
+  if (outer < 0 || p.n < 0 || p.inner < 0) return set_error(err, GHIP_ERR_INVALID_ARG, "%s: negative size", what);
+  if (outer == 0 || p.n == 0 || p.inner == 0) return GHIP_OK;
+  if (!p.x || !p.y) return set_error(err, GHIP_ERR_INVALID_ARG, "%s: null pointer", what);
+  p.col_blocks = (p.inner + 63) / 64;
+  const int64_t grid = outer * p.col_blocks;
+  if (grid > 0x7fffffffLL) return set_error(err, GHIP_ERR_INVALID_ARG, "%s: too many columns", what);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const dim3 g(static_cast<unsigned>(grid));
+  if (dtype == GHIP_DTYPE_FLOAT32) hipLaunchKernelGGL((cols_kernel<float, OP>), g, dim3(256), 0, s, p);
+  else if (dtype == GHIP_DTYPE_BFLOAT16) hipLaunchKernelGGL((cols_kernel<bf16_t, OP>), g, dim3(256), 0, s, p);
+  else if (dtype == GHIP_DTYPE_FLOAT16) hipLaunchKernelGGL((cols_kernel<f16_t, OP>), g, dim3(256), 0, s, p);
+  else return set_error(err, GHIP_ERR_UNSUPPORTED, "%s: dtype %d not supported", what, dtype);
+  GHIP_CHECK(hipGetLastError(), err);
+  return GHIP_OK;
+}
+
 }  // namespace ghip
 
 using namespace ghip;
@@ -789,4 +909,20 @@ extern "C" int ghip_layernorm_rows(int dtype, const void* x, const void* gamma, 
   RowParams p{};
   p.x = x; p.y = y; p.gamma = gamma; p.beta = beta; p.rows = rows; p.n = n; p.eps = eps;
   return dispatch_rows<kLayerNorm>(dtype, p, stream, err, "layernorm_rows");
+}
+
+extern "C" int ghip_softmax_cols(int dtype, const void* x, void* y, int64_t outer, int64_t n, int64_t inner,
+                                 int log_softmax, void* stream, GHipError* err) {
+  ColParams p{};
+  p.x = x; p.y = y; p.n = n; p.inner = inner;
+  if (log_softmax) return dispatch_cols<kLogSoftmax>(dtype, p, outer, stream, err, "softmax_cols");
+  return dispatch_cols<kSoftmax>(dtype, p, outer, stream, err, "softmax_cols");
+}
+
+extern "C" int ghip_layernorm_cols(int dtype, const void* x, const void* gamma, const void* beta, void* y,
+                                   int64_t outer, int64_t n, int64_t inner, float eps, void* stream,
+                                   GHipError* err) {
+  ColParams p{};
+  p.x = x; p.y = y; p.gamma = gamma; p.beta = beta; p.n = n; p.inner = inner; p.eps = eps;
+  return dispatch_cols<kLayerNorm>(dtype, p, outer, stream, err, "layernorm_cols");
 }

@@ -61,6 +61,8 @@ SIGNATURES = {
                                         ctypes.POINTER(_i64), _vp, _errp],
     "ghip_copy_strided": [_int, _vp, _vp, _int, ctypes.POINTER(_i64), ctypes.POINTER(_i64),
                           ctypes.POINTER(_i64), _vp, _errp],
+    "ghip_softmax_cols": [_int, _vp, _vp, _i64, _i64, _i64, _int, _vp, _errp],
+    "ghip_layernorm_cols": [_int, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _f32, _vp, _errp],
 }
 
 _lib = None

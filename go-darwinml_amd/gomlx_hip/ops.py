@@ -116,6 +116,25 @@ def gemm(a: torch.Tensor, b: torch.Tensor, out_dtype=None, out=None, stream=None
     return c[0] if squeeze else c
 
 
+def softmax_axis(x: torch.Tensor, axis: int, log: bool = False, out=None, stream=None) -> torch.Tensor:
+    """Softmax (log-softmax) over a middle axis of a contiguous tensor (the column
+    kernel: x read as [outer, n, inner])."""
+    _check_dev(x)
+    if not x.is_contiguous():
+        raise ValueError("softmax_axis: contiguous input required")
+    axis = axis % x.dim()
+    outer = 1
+    for d in x.shape[:axis]:
+        outer *= d
+    inner = 1
+    for d in x.shape[axis + 1:]:
+        inner *= d
+    y = torch.empty_like(x) if out is None else out
+    call("ghip_softmax_cols", dtype_code(x.dtype), x.data_ptr(), y.data_ptr(), outer, x.shape[axis], inner,
+         int(log), _stream(stream))
+    return y
+
+
 def copy(src: torch.Tensor, out: torch.Tensor, stream=None) -> torch.Tensor:
     """out[...] = src[...] for tensors of one shape and element size, any strides."""
     import ctypes

@@ -99,6 +99,19 @@ int ghip_scale_mask_softmax_rows_ex(int dtype, const void* x, void* y, int64_t B
                                     const void* mask, int mask_dtype, const int64_t* mask_strides,
                                     void* stream, GHipError* err);
 
+/* Softmax (log_softmax != 0: log-softmax) over the middle axis of a dense
+ * x [outer, n, inner] (the axis of length n; y in the same layout).  Replaces
+ * Function.FusedSoftmax with an axis other than the last (function.go:2276-2286,
+ * bridge.m:1448-1461: MPSGraph takes any axis) without moving the axis last. */
+int ghip_softmax_cols(int dtype, const void* x, void* y, int64_t outer, int64_t n, int64_t inner,
+                      int log_softmax, void* stream, GHipError* err);
+/* LayerNorm over the middle axis of a dense x [outer, n, inner], fp32 statistics;
+ * gamma / beta [n] in x's dtype, each may be NULL.  Replaces Function.FusedLayerNorm
+ * with one normalized axis that is not the last (function.go:2416-2427). */
+int ghip_layernorm_cols(int dtype, const void* x, const void* gamma, const void* beta, void* y,
+                        int64_t outer, int64_t n, int64_t inner, float eps, void* stream,
+                        GHipError* err);
+
 /* RMSNorm over the last axis: y = x * rsqrt(mean(x^2) + eps) * gamma.
  * gamma [n] has x's dtype and may be NULL.  Statistics in fp32.  No reference op:
  * replaces the primitive Mul/ReduceSum/Div/Add/Rsqrt/Mul chain (function.go:

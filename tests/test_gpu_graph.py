@@ -370,6 +370,58 @@ def test_graph_layer_norm_chain(be, dt):
     assert rel_err(ys[1], orc.layernorm(x, None, None, 1e-5)) <= tol
 
 
+@pytest.mark.parametrize("dt", [F32, BF16, dtypes.Float16])
+@pytest.mark.parametrize("shape,axis", [((6, 700, 130), 1), ((300, 5, 7), 0), ((2, 3, 257, 64), 2)])
+def test_graph_softmax_layernorm_middle_axis(be, dt, shape, axis):
+    """FusedSoftmax and FusedLayerNorm over an axis before the last (the column
+    kernels: 64 adjacent columns per workgroup, ragged column counts) against the
+    fp64 oracle on the same values: fp32 within 1e-5, 16-bit outputs within one
+    rounding of the dtype (RMS-floored)."""
+    np_dt = {F32: np.float32, BF16: None, dtypes.Float16: np.float16}[dt]
+    x = synth.normal(2101, shape, std=2.0)
+    n = shape[axis]
+    g = synth.uniform_f32(2102, (n,), 0.5, 1.5)
+    bt = synth.normal(2103, (n,), std=0.1)
+    if dt == BF16:
+        x, g, bt = _bf(x), _bf(g), _bf(bt)
+        host = lambda a: synth.to_bf16_bits(a)  # noqa: E731
+    else:
+        x, g, bt = (a.astype(np_dt).astype(np.float32) for a in (x, g, bt))
+        host = lambda a: a.astype(np_dt)  # noqa: E731
+    bshape = [1] * len(shape)
+    bshape[axis] = n
+    ys = run(be, lambda f, a, gg, bb: [f.FusedSoftmax(a, axis), f.FusedLayerNorm(a, [axis], 1e-5, gg, bb)],
+             [(host(x), make_shape(dt, *shape)), (host(g), make_shape(dt, n)),
+              (host(bt.reshape(bshape)), make_shape(dt, *bshape))])
+    ys = [y.astype(np.float32) for y in ys]  # run() has widened bf16 already
+    ref_sm = orc.softmax(x, axis)
+    ref_ln = np.moveaxis(orc.layernorm(np.ascontiguousarray(np.moveaxis(x, axis, -1)), g, bt, 1e-5), -1, axis)
+    tol = 1e-5 if dt == F32 else (2.0 ** -8 if dt == BF16 else 2.0 ** -11) + 1e-5
+    assert rel_err(ys[0], ref_sm) <= tol
+    assert rel_err(ys[1], ref_ln) <= tol
+
+
+def test_softmax_columns_direct_log_and_masked(cuda):
+    """ghip_softmax_cols through the C ABI: log-softmax, a column of -inf (NaN, as
+    the row kernels give), and columns with some -inf entries (those get 0)."""
+    import torch
+    from gomlx_hip import ops
+    x = synth.normal(2111, (4, 96, 200), std=3.0)
+    x[1, :, 7] = -np.inf
+    x[2, ::3, 9] = -np.inf
+    t = torch.from_numpy(x).cuda()
+    y = ops.softmax_axis(t, 1).cpu().numpy()
+    ly = ops.softmax_axis(t, 1, log=True).cpu().numpy()
+    assert np.all(np.isnan(y[1, :, 7]))
+    assert np.all(y[2, ::3, 9] == 0) and abs(y[2, :, 9].sum() - 1) < 1e-5
+    ok = np.ones(x.shape, bool)
+    ok[1, :, 7] = False
+    ref = orc.softmax(x, 1)
+    assert rel_err(y[ok], ref[ok]) <= 1e-5
+    finite = ok & np.isfinite(x)
+    assert rel_err(ly[finite], orc.log_softmax(x, 1)[finite]) <= 1e-5
+
+
 def test_graph_float16_hot_ops(be):
     """Float16 (a dtype the reference declares, capabilities.go:153-166) through the
     graph API: FusedSoftmax, FusedLayerNorm, the RMSNorm chain and DotGeneral, each

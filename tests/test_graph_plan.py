@@ -171,6 +171,22 @@ def test_softmax_chain_and_fused_softmax(be):
     assert "reduce" not in p
 
 
+def test_middle_axis_softmax_and_layernorm_use_column_kernels(be):
+    """FusedSoftmax / FusedLayerNorm over an axis before the last run the column
+    kernels on x as it lies in memory: one step each, no transposing copy of x or
+    of the result."""
+    def build(f):
+        x = f.Parameter("x", make_shape(F32, 8, 300, 64))
+        g = f.Parameter("g", make_shape(F32, 300))
+        b = f.Parameter("b", make_shape(F32, 1, 300, 1))
+        return [f.FusedSoftmax(x, 1), f.FusedLayerNorm(x, [1], 1e-5, g, b), f.FusedSoftmax(x, 0)]
+    p = plan_of(be, build)
+    assert "softmax_cols float32 outer=8 n=300 inner=64" in p, p
+    assert "layernorm_cols float32 outer=8 n=300 inner=64 +gamma +beta" in p, p
+    assert "softmax_cols float32 outer=1 n=8 inner=19200" in p, p
+    assert "strided_copy" not in p, p
+
+
 @pytest.mark.parametrize("dt", [F32, BF16, dtypes.Float16])
 def test_log_softmax_chain_is_fused(be, dt):
     def build(f):
@@ -197,14 +213,6 @@ def test_float16_chains_fuse_and_float64_chains_stay_unfused(be):
     assert "_rows" not in p and "reduce" in p, p
     with pytest.raises(BackendError, match="row kernels take"):
         plan_of(be, lambda f: [f.FusedSoftmax(f.Parameter("x", make_shape(dtypes.Float64, 4, 8)), 1)])
-
-
-def test_softmax_other_axis_moves_axis_last(be):
-    def build(f):
-        x = f.Parameter("x", make_shape(F32, 8, 16, 32))
-        return [f.FusedSoftmax(x, 1)]
-    p = plan_of(be, build)
-    assert "softmax_rows float32 rows=256 n=16" in p
 
 
 def test_dot_general_folds_transposes(be):
