@@ -1890,7 +1890,8 @@ struct Lowerer {
       const int64_t ostr[3] = {H * Sq * Dv, bshd ? Dv : Sq * Dv, bshd ? H * Dv : Dv};
       bool mask_ok = true;
       for (int i = 0; i < 4 && has_mask; ++i) mask_ok = mask_ok && mst[i] >= 0;
-      const bool al = q.offset % 8 == 0 && k.offset % 8 == 0 && vw.offset % 8 == 0;
+      const int64_t a16 = 16 / dtype_size(dt);  // elements in 16 bytes
+      const bool al = q.offset % a16 == 0 && k.offset % a16 == 0 && vw.offset % a16 == 0;
       const float scale = static_cast<float>(n.f0);
       if (al && mask_ok && sdpa_fused_supported(dt, H, Hkv, Sq, Sk, D, qst, kst, vst, ostr, scale, mdt)) {
         Shape os_layout = bshd ? permute_shape(os, to_bhsd) : os;

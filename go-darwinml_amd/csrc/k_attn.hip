@@ -1,8 +1,9 @@
 // Fused scaled-dot-product attention (forward), the single-kernel lowering of
 // Function.FusedScaledDotProductAttention (mpsgraph/gomlx/function.go:2669-2907):
 //   out = softmax(scale * Q K^T + mask  [causal: -inf where key > query]) V
-// for bf16 or f16 Q/K/V/O with head dim 64 or 128, fp32 softmax statistics and
-// accumulation.  The mask is the reference's: a boolean keep-mask (Where(mask,
+// for bf16 or f16 Q/K/V/O with a head dim that is a multiple of 8 up to 256, or
+// fp32 with a multiple of 4 up to 128 (a second kernel, at the end), fp32 softmax
+// statistics and accumulation.  The mask is the reference's: a boolean keep-mask (Where(mask,
 // scores, -inf), :2847-2871) or an additive one (scores + mask, :2872-2878), of
 // any rank broadcast to the scores [B, H, Sq, Sk] (:2959-2974), read through
 // element strides (0 on broadcast axes).  GQA reads KV head h / (H / Hkv)
@@ -62,6 +63,7 @@ struct Params {
   int64_t o_sb, o_sh, o_ss;
   int64_t m_sb, m_sh, m_sq, m_sk;  // mask element strides (0 where it broadcasts)
   int B, H, Hkv, Sq, Sk;
+  int D;                        // head dim (<= the kernel's padded width DP)
   float scale_log2;             // softmax scale * log2(e)
   float inv_scale;              // 1 / scale (additive masks are added to raw scores / scale)
   int causal;
@@ -74,6 +76,9 @@ constexpr int kQW = 32;     // queries per wave
 constexpr int kWaves = 4;   // waves per workgroup
 constexpr int kBQ = kQW * kWaves;
 constexpr float kLazyLog2 = 8.f;  // the reference max may trail the true max by 2^8
+// A buffer offset past every descriptor's extent (extents are < 2 GiB): a DMA lane
+// given it loads zeros.
+constexpr uint32_t kPastEnd = 0x80000000u;
 
 __device__ __forceinline__ i32x4_t make_rsrc(const void* base, uint32_t bytes) {
   const uint64_t b = reinterpret_cast<uint64_t>(base);
@@ -98,38 +103,40 @@ __device__ __forceinline__ void dma16(i32x4_t rsrc, uint32_t la, uint32_t voff) 
 }
 #pragma clang diagnostic pop
 
-// LDS tiles are [64 keys][D] 16-bit values: rows of C = D / 8 chunks of 16 B.
+// LDS tiles are [64 keys][DP] 16-bit values: rows of C = DP / 8 chunks of 16 B.
 // K: chunk kc of key row r sits at slot kc ^ (r % C), so the 8 or 16 rows of a
 // ds_read_b128 phase land in distinct bank groups.
-template <int D>
-__device__ __forceinline__ int swz_k(int r) { return r & (D / 8 - 1); }
+template <int DP>
+__device__ __forceinline__ int swz_k(int r) { return r & (DP / 8 - 1); }
 // V: chunk j of key row r sits at slot j ^ f(r & 3): a transpose read touches 4
-// consecutive rows x 2 (D = 64) or 2-4 (D = 128) chunks.  D = 128: f = {0, 6, 10,
-// 12}; D = 64 (8 chunks a row): f = {0, 2, 4, 6}, which keeps the chunk pairs of a
-// 32-byte read together and spreads the 4 rows over all 8 bank groups.
-template <int D>
+// consecutive rows x 2 (DP = 64) or 2-4 (DP >= 128) chunks.  DP >= 128: f = {0, 6,
+// 10, 12} (rows are whole multiples of the 128-byte bank period, so the bank group
+// is the slot mod 8 at DP = 256 as at 128); DP = 64 (8 chunks a row): f = {0, 2, 4,
+// 6}, which keeps the chunk pairs of a 32-byte read together and spreads the 4 rows
+// over all 8 bank groups.
+template <int DP>
 __device__ __forceinline__ int swz_v(int r) {
-  if constexpr (D == 128) return (0xCA60u >> ((r & 3) * 4)) & 15u;
+  if constexpr (DP >= 128) return (0xCA60u >> ((r & 3) * 4)) & 15u;
   else return 2 * (r & 3);
 }
 
 // K fragment (A operand of S^T = K Q^T): key row kb*32 + lane%32, d = 16s + 8*(lane/32).
-template <int D>
+template <int DP>
 __device__ __forceinline__ bf16x8_t frag_k(const uint16_t* lds, int kb, int s, int lane) {
   const int row = kb * 32 + (lane & 31);
-  const int slot = (2 * s + (lane >> 5)) ^ swz_k<D>(row);
-  return *reinterpret_cast<const bf16x8_t*>(lds + row * D + slot * 8);
+  const int slot = (2 * s + (lane >> 5)) ^ swz_k<DP>(row);
+  return *reinterpret_cast<const bf16x8_t*>(lds + row * DP + slot * 8);
 }
 // V^T fragment (A operand of O^T = V^T P^T), d block db, key step s: lane
 // (d = 32 db + lane%32, h = lane/32) gets keys 16s + 4h + {0..3} and
 // 16s + 8 + 4h + {0..3}.  ds_read_b64_tr_b16 hands lane j of each 16-lane group
 // element j of the four 4-element rows the group points at.
-template <int D>
+template <int DP>
 __device__ __forceinline__ bf16x8_t frag_v(const uint16_t* lds, int db, int s, int lane) {
   const int kl = 16 * s + 4 * (lane >> 5) + ((lane & 15) >> 2);
   const int nl = db * 32 + 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
-  const uint16_t* p0 = lds + kl * D + (((nl >> 3) ^ swz_v<D>(kl)) * 8) + (nl & 7);
-  const uint16_t* p1 = p0 + 8 * D;  // key + 8 keeps key & 3, hence the swizzle
+  const uint16_t* p0 = lds + kl * DP + (((nl >> 3) ^ swz_v<DP>(kl)) * 8) + (nl & 7);
+  const uint16_t* p1 = p0 + 8 * DP;  // key + 8 keeps key & 3, hence the swizzle
   bf16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((GHIP_ALDS bf16x4_t*)(p0));
   bf16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((GHIP_ALDS bf16x4_t*)(p1));
   return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
@@ -168,18 +175,25 @@ __device__ __forceinline__ float dot2_ones(uint32_t w, float acc) {
   }
 }
 
-template <int D, bool F16, int MK>
-__global__ __launch_bounds__(256, 2) void sdpa_fwd_kernel(Params p) {
-  constexpr int NCH = D / 8;  // 16-byte chunks per key row
-  constexpr int NDMA = kBKV * D * 2 / 1024 / kWaves;  // DMA instructions per wave per K (or V) tile
-  constexpr int RPI = 1024 / (D * 2);                 // key rows per DMA instruction
-  // [stage][K | V][64 keys x D]
-  __shared__ __attribute__((aligned(1024))) uint16_t smem[1][2][kBKV * D];
+// DP: the padded head dim the LDS tiles, Q fragments and output accumulators are
+// laid out for (64, 128 or 256); the head dim D = p.D is any multiple of 8 up to
+// DP.  The 16-byte chunks of a row past D are loaded as zeros (their DMA offsets lie
+// beyond the buffer's extent) and Q's are zero, so they add nothing to the scores
+// and their output columns are not stored.  The MFMAs still run over the full DP
+// (no branch in the tile loop: at D = DP the loop is exactly the unpadded one).
+template <int DP, bool F16, int MK>
+__global__ __launch_bounds__(256, DP >= 256 ? 1 : 2) void sdpa_fwd_kernel(Params p) {
+  constexpr int NCH = DP / 8;  // 16-byte chunks per key row
+  constexpr int NDMA = kBKV * DP * 2 / 1024 / kWaves;  // DMA instructions per wave per K (or V) tile
+  constexpr int RPI = 1024 / (DP * 2);                 // key rows per DMA instruction
+  // [stage][K | V][64 keys x DP]
+  __shared__ __attribute__((aligned(1024))) uint16_t smem[1][2][kBKV * DP];
   const uint32_t lds0 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>((GHIP_ALDS void*)&smem[0][0][0]));
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int h2 = lane >> 5;  // half of the wave
+  const int D = p.D;
   const int nqb = (p.Sq + kBQ - 1) / kBQ;
   const int nbh = p.B * p.H;
   // Longest first over the whole grid: every (batch, head) of the last query
@@ -197,10 +211,10 @@ __global__ __launch_bounds__(256, 2) void sdpa_fwd_kernel(Params p) {
   const uint16_t* Vb = static_cast<const uint16_t*>(p.v) + b * p.v_sb + hk * p.v_sh;
 
   // Q fragments (B operand of S^T): query qi, d = 16s + 8*h2 .. +8.
-  bf16x8_t qf[D / 16];
+  bf16x8_t qf[DP / 16];
 #pragma unroll
-  for (int s = 0; s < D / 16; ++s) {
-    if (qi < p.Sq)
+  for (int s = 0; s < DP / 16; ++s) {
+    if (qi < p.Sq && 16 * s + 8 * h2 < D)
       qf[s] = *reinterpret_cast<const bf16x8_t*>(Q + static_cast<int64_t>(qi) * p.q_ss + 16 * s + 8 * h2);
     else
       qf[s] = bf16x8_t{};
@@ -222,25 +236,26 @@ __global__ __launch_bounds__(256, 2) void sdpa_fwd_kernel(Params p) {
   for (int i = 0; i < NDMA; ++i) {
     const int r = (wave * NDMA + i) * RPI + lane / NCH;
     const int cc = lane % NCH;
-    koff[i] = static_cast<uint32_t>((static_cast<int64_t>(r) * p.k_ss + (cc ^ swz_k<D>(r)) * 8) * 2);
-    voff[i] = static_cast<uint32_t>((static_cast<int64_t>(r) * p.v_ss + (cc ^ swz_v<D>(r)) * 8) * 2);
+    const int gk = cc ^ swz_k<DP>(r), gv = cc ^ swz_v<DP>(r);  // global chunks this lane loads
+    koff[i] = 8 * gk < D ? static_cast<uint32_t>((static_cast<int64_t>(r) * p.k_ss + gk * 8) * 2) : kPastEnd;
+    voff[i] = 8 * gv < D ? static_cast<uint32_t>((static_cast<int64_t>(r) * p.v_ss + gv * 8) * 2) : kPastEnd;
   }
   const uint32_t kstep = static_cast<uint32_t>(kBKV * p.k_ss * 2), vstep = static_cast<uint32_t>(kBKV * p.v_ss * 2);
   auto issue = [&](int t, int st) {
     const uint32_t dk = static_cast<uint32_t>(t) * kstep, dv = static_cast<uint32_t>(t) * vstep;
     const i32x4_t rk = make_rsrc(reinterpret_cast<const char*>(Kb) + dk, p.k_extent - dk);
     const i32x4_t rv = make_rsrc(reinterpret_cast<const char*>(Vb) + dv, p.v_extent - dv);
-    const uint32_t lk = lds0 + static_cast<uint32_t>(st) * (2 * kBKV * D * 2) + wave * NDMA * 1024;
-    const uint32_t lv = lk + kBKV * D * 2;
+    const uint32_t lk = lds0 + static_cast<uint32_t>(st) * (2 * kBKV * DP * 2) + wave * NDMA * 1024;
+    const uint32_t lv = lk + kBKV * DP * 2;
 #pragma unroll
     for (int i = 0; i < NDMA; ++i) dma16(rk, lk + i * 1024, koff[i]);
 #pragma unroll
     for (int i = 0; i < NDMA; ++i) dma16(rv, lv + i * 1024, voff[i]);
   };
 
-  f32x16_t o[D / 32];
+  f32x16_t o[DP / 32];
 #pragma unroll
-  for (int db = 0; db < D / 32; ++db)
+  for (int db = 0; db < DP / 32; ++db)
 #pragma unroll
     for (int v = 0; v < 16; ++v) o[db][v] = 0.f;
   float m = -INFINITY;  // reference max (raw scores) the exponents are taken against
@@ -307,9 +322,9 @@ __global__ __launch_bounds__(256, 2) void sdpa_fwd_kernel(Params p) {
       s1[v] = 0.f;
     }
 #pragma unroll
-    for (int s = 0; s < D / 16; ++s) {
-      s0 = mma<F16>(frag_k<D>(sk, 0, s, lane), qf[s], s0);
-      s1 = mma<F16>(frag_k<D>(sk, 1, s, lane), qf[s], s1);
+    for (int s = 0; s < DP / 16; ++s) {
+      s0 = mma<F16>(frag_k<DP>(sk, 0, s, lane), qf[s], s0);
+      s1 = mma<F16>(frag_k<DP>(sk, 1, s, lane), qf[s], s1);
     }
     // s{kb}[v] is key key0 + 32 kb + 4 h2 + kv, kv = (v/4)*8 + v%4, for query qi.
     if constexpr (MK != kNoMask) {
@@ -347,7 +362,7 @@ __global__ __launch_bounds__(256, 2) void sdpa_fwd_kernel(Params p) {
       m = mnew;
       l *= alpha;
 #pragma unroll
-      for (int db = 0; db < D / 32; ++db)
+      for (int db = 0; db < DP / 32; ++db)
 #pragma unroll
         for (int v = 0; v < 16; ++v) o[db][v] *= alpha;
     }
@@ -382,7 +397,7 @@ __global__ __launch_bounds__(256, 2) void sdpa_fwd_kernel(Params p) {
 #pragma unroll
     for (int s = 0; s < kBKV / 16; ++s)
 #pragma unroll
-      for (int db = 0; db < D / 32; ++db) o[db] = mma<F16>(frag_v<D>(sv, db, s, lane), pb[s], o[db]);
+      for (int db = 0; db < DP / 32; ++db) o[db] = mma<F16>(frag_v<DP>(sv, db, s, lane), pb[s], o[db]);
     // The stage's LDS reads complete before the next barrier, after which it is
     // refilled.
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
@@ -401,10 +416,11 @@ __global__ __launch_bounds__(256, 2) void sdpa_fwd_kernel(Params p) {
   if (qi < p.Sq) {
     uint16_t* O = static_cast<uint16_t*>(p.o) + b * p.o_sb + h * p.o_sh + static_cast<int64_t>(qi) * p.o_ss;
 #pragma unroll
-    for (int db = 0; db < D / 32; ++db)
+    for (int db = 0; db < DP / 32; ++db)
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
         const int d = db * 32 + g * 8 + 4 * h2;
+        if (d >= D) continue;  // D is a multiple of 8: d < D covers d .. d + 3
         const float r0 = lt > 0.f ? o[db][g * 4 + 0] * inv : __builtin_nanf("");
         const float r1 = lt > 0.f ? o[db][g * 4 + 1] * inv : __builtin_nanf("");
         const float r2 = lt > 0.f ? o[db][g * 4 + 2] * inv : __builtin_nanf("");
@@ -414,11 +430,229 @@ __global__ __launch_bounds__(256, 2) void sdpa_fwd_kernel(Params p) {
   }
 }
 
-template <int D, bool F16>
+template <int DP, bool F16>
 static void launch_d(const Params& p, int mk, dim3 grid, hipStream_t s) {
-  if (mk == kBoolMask) hipLaunchKernelGGL((sdpa_fwd_kernel<D, F16, kBoolMask>), grid, dim3(256), 0, s, p);
-  else if (mk == kAddMask) hipLaunchKernelGGL((sdpa_fwd_kernel<D, F16, kAddMask>), grid, dim3(256), 0, s, p);
-  else hipLaunchKernelGGL((sdpa_fwd_kernel<D, F16, kNoMask>), grid, dim3(256), 0, s, p);
+  if (mk == kBoolMask) hipLaunchKernelGGL((sdpa_fwd_kernel<DP, F16, kBoolMask>), grid, dim3(256), 0, s, p);
+  else if (mk == kAddMask) hipLaunchKernelGGL((sdpa_fwd_kernel<DP, F16, kAddMask>), grid, dim3(256), 0, s, p);
+  else hipLaunchKernelGGL((sdpa_fwd_kernel<DP, F16, kNoMask>), grid, dim3(256), 0, s, p);
+}
+
+
+// fp32 Q / K / V / O: the same structure on v_mfma_f32_32x32x2_f32 (fp32 products
+// and sums throughout, P never rounded), with 32-key K / V tiles held as fp32 in LDS
+// (32 KiB at DP = 128).  Each lane again owns one query column:
+//   * S^T = K Q^T: MFMA step (g, e), g < DP / 8, e < 4, takes head dim d = 8g + 4h +
+//     e in lane half h.  A lane reads those 4 values of its key row with one
+//     ds_read_b128 (16-byte chunk c of row r sits at slot c ^ (r % 8), so the 8 rows
+//     of a b128 phase land in distinct bank groups) and holds Q's in registers;
+//   * O^T = V^T P^T: MFMA step j < 16 takes key 8 (j / 4) + 4h + j % 4 in lane half
+//     h, which is where register j of that lane's S^T accumulator lies, so P enters
+//     the MFMA straight from the accumulator; V^T is read one value a lane (the 32
+//     lanes of a half on 32 consecutive head-dim values of one key row).
+// Head dims below DP are padded as in the 16-bit kernel (zero chunks, unstored
+// output columns); D is a multiple of 4.
+constexpr int kKT32 = 32;  // keys per fp32 tile
+
+// Two workgroups a CU, except DP = 128 with a boolean mask, whose ~260 registers
+// a lane need the accumulation registers of a one-wave-per-SIMD launch.
+template <int DP, int MK>
+__global__ __launch_bounds__(256, DP >= 128 && MK == kBoolMask ? 1 : 2) void sdpa_fwd_f32_kernel(Params p) {
+  constexpr int KT = kKT32;
+  constexpr int NCH = DP / 4;                         // 16-byte chunks per row
+  constexpr int NDMA = KT * DP * 4 / 1024 / kWaves;   // DMA instructions per wave per K (or V) tile
+  constexpr int RPI = 256 / DP;                       // rows per DMA instruction
+  __shared__ __attribute__((aligned(1024))) float smem[2][KT * DP];  // K | V
+  const uint32_t lds0 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>((GHIP_ALDS void*)&smem[0][0]));
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int h2 = lane >> 5;
+  const int D = p.D;
+  const int nqb = (p.Sq + kBQ - 1) / kBQ;
+  const int nbh = p.B * p.H;
+  const int qb = p.causal ? (nqb - 1 - static_cast<int>(blockIdx.x / nbh)) : static_cast<int>(blockIdx.x / nbh);
+  const int bh = blockIdx.x % nbh;
+  const int b = bh / p.H, h = bh % p.H;
+  const int hk = h / (p.H / p.Hkv);
+  const int q0 = qb * kBQ;
+  const int qw = q0 + wave * kQW;
+  const int qi = qw + (lane & 31);
+
+  const float* Q = static_cast<const float*>(p.q) + b * p.q_sb + h * p.q_sh;
+  const float* Kb = static_cast<const float*>(p.k) + b * p.k_sb + hk * p.k_sh;
+  const float* Vb = static_cast<const float*>(p.v) + b * p.v_sb + hk * p.v_sh;
+
+  // Q values of this lane: query qi, d = 8g + 4 h2 .. +4.
+  float4 qf[DP / 8];
+#pragma unroll
+  for (int g = 0; g < DP / 8; ++g) {
+    const int d = 8 * g + 4 * h2;
+    qf[g] = qi < p.Sq && d < D ? *reinterpret_cast<const float4*>(Q + static_cast<int64_t>(qi) * p.q_ss + d)
+                               : make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+  const int64_t mrow = b * p.m_sb + h * p.m_sh + static_cast<int64_t>(qi < p.Sq ? qi : 0) * p.m_sq;
+
+  const int kv_end = p.causal ? min(p.Sk, q0 + kBQ) : p.Sk;
+  const int ntiles = (kv_end + KT - 1) / KT;
+  const float c = p.scale_log2;
+
+  uint32_t koff[NDMA], voff[NDMA];
+#pragma unroll
+  for (int i = 0; i < NDMA; ++i) {
+    const int r = (wave * NDMA + i) * RPI + lane / NCH;
+    const int cc = lane % NCH;
+    const int gk = cc ^ (r & 7);
+    koff[i] = 4 * gk < D ? static_cast<uint32_t>((static_cast<int64_t>(r) * p.k_ss + gk * 4) * 4) : kPastEnd;
+    voff[i] = 4 * cc < D ? static_cast<uint32_t>((static_cast<int64_t>(r) * p.v_ss + cc * 4) * 4) : kPastEnd;
+  }
+  const uint32_t kstep = static_cast<uint32_t>(KT * p.k_ss * 4), vstep = static_cast<uint32_t>(KT * p.v_ss * 4);
+  auto issue = [&](int t) {
+    const uint32_t dk = static_cast<uint32_t>(t) * kstep, dv = static_cast<uint32_t>(t) * vstep;
+    const i32x4_t rk = make_rsrc(reinterpret_cast<const char*>(Kb) + dk, p.k_extent - dk);
+    const i32x4_t rv = make_rsrc(reinterpret_cast<const char*>(Vb) + dv, p.v_extent - dv);
+    const uint32_t lk = lds0 + wave * NDMA * 1024;
+    const uint32_t lv = lk + KT * DP * 4;
+#pragma unroll
+    for (int i = 0; i < NDMA; ++i) dma16(rk, lk + i * 1024, koff[i]);
+#pragma unroll
+    for (int i = 0; i < NDMA; ++i) dma16(rv, lv + i * 1024, voff[i]);
+  };
+
+  f32x16_t o[DP / 32];
+#pragma unroll
+  for (int db = 0; db < DP / 32; ++db)
+#pragma unroll
+    for (int v = 0; v < 16; ++v) o[db][v] = 0.f;
+  float m = -INFINITY, l = 0.f;
+
+  // Keep flags of keys key .. key + 3 (score registers 4g .. 4g + 3), one byte each
+  // of a word (keys past Sk are kept: the element mask drops them).
+  auto keep_group = [&](int key) -> uint32_t {
+    const uint8_t* mp = static_cast<const uint8_t*>(p.mask) + mrow;
+    if (p.mask_vec && key + 3 < p.Sk) return *reinterpret_cast<const uint32_t*>(mp + key);
+    uint32_t w = 0;
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      w |= (key + e >= p.Sk || mp[static_cast<int64_t>(key + e) * p.m_sk]) ? (1u << (8 * e)) : 0u;
+    return w;
+  };
+  // Additive terms of keys key .. key + 3, divided by the scale.
+  auto add_group = [&](int key, float* out) {
+    {
+      const float* mp = static_cast<const float*>(p.mask) + mrow;
+      if (p.mask_vec && key + 3 < p.Sk) {
+        const float4 w = *reinterpret_cast<const float4*>(mp + key);
+        out[0] = w.x; out[1] = w.y; out[2] = w.z; out[3] = w.w;
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) out[e] = key + e < p.Sk ? mp[static_cast<int64_t>(key + e) * p.m_sk] : 0.f;
+      }
+#pragma unroll
+      for (int e = 0; e < 4; ++e) out[e] *= p.inv_scale;
+    }
+  };
+
+  const float* sk = &smem[0][0];
+  const float* sv = &smem[1][0];
+  for (int t = 0; t < ntiles; ++t) {
+    __syncthreads();
+    issue(t);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    const int key0 = t * KT;
+    if (p.causal && key0 > qw + kQW - 1) continue;
+    float mk[MK == kAddMask ? 16 : 1];
+    uint32_t mw[4];
+    if constexpr (MK == kAddMask) {
+#pragma unroll
+      for (int g = 0; g < 4; ++g) add_group(key0 + 4 * h2 + 8 * g, &mk[4 * g]);
+    } else if constexpr (MK == kBoolMask) {
+#pragma unroll
+      for (int g = 0; g < 4; ++g) mw[g] = keep_group(key0 + 4 * h2 + 8 * g);
+    }
+    f32x16_t sc;
+#pragma unroll
+    for (int v = 0; v < 16; ++v) sc[v] = 0.f;
+    const int row = lane & 31;
+#pragma unroll
+    for (int g = 0; g < DP / 8; ++g) {
+      const float4 kf = *reinterpret_cast<const float4*>(sk + row * DP + (((2 * g + h2) ^ (row & 7)) * 4));
+      sc = __builtin_amdgcn_mfma_f32_32x32x2f32(kf.x, qf[g].x, sc, 0, 0, 0);
+      sc = __builtin_amdgcn_mfma_f32_32x32x2f32(kf.y, qf[g].y, sc, 0, 0, 0);
+      sc = __builtin_amdgcn_mfma_f32_32x32x2f32(kf.z, qf[g].z, sc, 0, 0, 0);
+      sc = __builtin_amdgcn_mfma_f32_32x32x2f32(kf.w, qf[g].w, sc, 0, 0, 0);
+    }
+    // sc[v] is key key0 + 4 h2 + kv, kv = (v/4)*8 + v%4, for query qi.
+    if constexpr (MK == kAddMask) {
+#pragma unroll
+      for (int v = 0; v < 16; ++v) sc[v] += mk[v];
+    } else if constexpr (MK == kBoolMask) {
+#pragma unroll
+      for (int v = 0; v < 16; ++v) sc[v] = (mw[v >> 2] >> (8 * (v & 3))) & 0xffu ? sc[v] : -INFINITY;
+    }
+    if ((p.causal && key0 + KT - 1 > qw) || key0 + KT > p.Sk) {
+      const int lim = min(p.Sk, p.causal ? qi + 1 : p.Sk) - key0 - 4 * h2;
+#pragma unroll
+      for (int v = 0; v < 16; ++v) sc[v] = (v >> 2) * 8 + (v & 3) < lim ? sc[v] : -INFINITY;
+    }
+    float mx = -INFINITY;
+#pragma unroll
+    for (int v = 0; v < 16; v += 2) asm("v_max3_f32 %0, %1, %2, %3" : "=v"(mx) : "v"(mx), "v"(sc[v]), "v"(sc[v + 1]));
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    if (__builtin_amdgcn_ballot_w64((mx - m) * c > kLazyLog2)) {
+      const float mnew = fmaxf(m, mx);
+      const float alpha = mnew == -INFINITY ? 1.f : __builtin_amdgcn_exp2f((m - mnew) * c);
+      m = mnew;
+      l *= alpha;
+#pragma unroll
+      for (int db = 0; db < DP / 32; ++db)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) o[db][v] *= alpha;
+    }
+    const float nb = m == -INFINITY ? 0.f : -m * c;
+    float ls = 0.f;
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+      sc[v] = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[v], c, nb));
+      ls += sc[v];
+    }
+    l += ls;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const int key = 8 * (j >> 2) + 4 * h2 + (j & 3);
+#pragma unroll
+      for (int db = 0; db < DP / 32; ++db)
+        o[db] = __builtin_amdgcn_mfma_f32_32x32x2f32(sv[key * DP + 32 * db + row], sc[j], o[db], 0, 0, 0);
+      // V reads are not hoisted more than 4 keys ahead (registers: 2 waves a SIMD).
+      if ((j & 3) == 3) __builtin_amdgcn_sched_barrier(0);
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  }
+
+  // o[db][v] is d = 32 db + (v/4)*8 + 4 h2 + v%4 of query qi.
+  const float lt = l + __shfl_xor(l, 32, 64);
+  const float inv = 1.0f / lt;
+  if (qi < p.Sq) {
+    float* O = static_cast<float*>(p.o) + b * p.o_sb + h * p.o_sh + static_cast<int64_t>(qi) * p.o_ss;
+#pragma unroll
+    for (int db = 0; db < DP / 32; ++db)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int d = db * 32 + g * 8 + 4 * h2;
+        if (d >= D) continue;  // D is a multiple of 4
+        const float nan = __builtin_nanf("");
+        *reinterpret_cast<float4*>(O + d) =
+            make_float4(lt > 0.f ? o[db][g * 4 + 0] * inv : nan, lt > 0.f ? o[db][g * 4 + 1] * inv : nan,
+                        lt > 0.f ? o[db][g * 4 + 2] * inv : nan, lt > 0.f ? o[db][g * 4 + 3] * inv : nan);
+      }
+  }
+}
+
+template <int DP>
+static void launch_f32(const Params& p, int mk, dim3 grid, hipStream_t s) {
+  if (mk == kBoolMask) hipLaunchKernelGGL((sdpa_fwd_f32_kernel<DP, kBoolMask>), grid, dim3(256), 0, s, p);
+  else if (mk == kAddMask) hipLaunchKernelGGL((sdpa_fwd_f32_kernel<DP, kAddMask>), grid, dim3(256), 0, s, p);
+  else hipLaunchKernelGGL((sdpa_fwd_f32_kernel<DP, kNoMask>), grid, dim3(256), 0, s, p);
 }
 
 }  // namespace attn
@@ -426,22 +660,29 @@ static void launch_d(const Params& p, int mk, dim3 grid, hipStream_t s) {
 // Whether ghip_sdpa_fwd_masked takes these operands (checked again, with the
 // pointers, by the entry point).  Strides are in elements, ordered (batch, head,
 // sequence); the head dim must be contiguous.  mask_dtype < 0: no mask.
+//   bf16 / f16: head dim a multiple of 8 up to 256; strides multiples of 8 (4 for
+//   the output).  fp32: head dim a multiple of 4 up to 128; strides multiples of 4.
 bool sdpa_fused_supported(int dtype, int64_t H, int64_t Hkv, int64_t Sq, int64_t Sk, int64_t D,
                           const int64_t* qs, const int64_t* ks, const int64_t* vs, const int64_t* os,
                           float scale, int mask_dtype) {
-  if (dtype != GHIP_DTYPE_BFLOAT16 && dtype != GHIP_DTYPE_FLOAT16) return false;
-  if ((D != 64 && D != 128) || Hkv <= 0 || H % Hkv != 0) return false;
+  const bool f32 = dtype == GHIP_DTYPE_FLOAT32;
+  if (!f32 && dtype != GHIP_DTYPE_BFLOAT16 && dtype != GHIP_DTYPE_FLOAT16) return false;
+  const int64_t es = f32 ? 4 : 2;
+  const int64_t in_al = 16 / es;  // 16-byte rows for the DMA and Q loads
+  const int64_t out_al = 4;  // 16 bytes (fp32) or 8 (16-bit): the output stores
+  if (D <= 0 || D % in_al != 0 || D > (f32 ? 128 : 256)) return false;
+  if (Hkv <= 0 || H % Hkv != 0) return false;
   if (mask_dtype >= 0 && mask_dtype != GHIP_DTYPE_BOOL && mask_dtype != dtype) return false;
   if (!(scale > 0.f) || !(scale < 1e30f)) return false;  // positive and finite
   if (Sq <= 0 || Sk <= 0 || Sq > (int64_t{1} << 30) || Sk > (int64_t{1} << 30)) return false;
   for (const int64_t* s : {qs, ks, vs})
     for (int i = 0; i < 3; ++i)
-      if (s[i] < 0 || s[i] % 8 != 0) return false;
+      if (s[i] < 0 || s[i] % in_al != 0) return false;
   for (int i = 0; i < 3; ++i)
-    if (os[i] < 0 || os[i] % 4 != 0) return false;
+    if (os[i] < 0 || os[i] % out_al != 0) return false;
   // One (batch, kv head) slice of K / V must fit the 2 GiB buffer-offset range.
-  if (((Sk - 1) * ks[2] + D) * 2 >= (int64_t{1} << 31)) return false;
-  if (((Sk - 1) * vs[2] + D) * 2 >= (int64_t{1} << 31)) return false;
+  if (((Sk - 1) * ks[2] + D) * es >= (int64_t{1} << 31)) return false;
+  if (((Sk - 1) * vs[2] + D) * es >= (int64_t{1} << 31)) return false;
   return true;
 }
 
@@ -468,12 +709,16 @@ extern "C" int ghip_sdpa_fwd_masked(int dtype, const void* q, const void* k, con
   const int mdt = mask ? mask_dtype : -1;
   if (!sdpa_fused_supported(dtype, H, Hkv, Sq, Sk, D, q_strides, k_strides, v_strides, o_strides, scale, mdt))
     return set_error(err, GHIP_ERR_UNSUPPORTED,
-                     "sdpa_fwd: needs bfloat16 or float16, head dim 64 or 128, a bool mask or one in the "
-                     "operands' dtype, a positive finite scale, non-negative strides that are multiples of 8 "
-                     "(4 for the output) and < 2 GiB per K/V head");
+                     "sdpa_fwd: needs bfloat16 or float16 with a head dim that is a multiple of 8 up to 256, "
+                     "or float32 with a multiple of 4 up to 128; a bool mask or one in the operands' dtype, a "
+                     "positive finite scale, non-negative strides that are multiples of 16 bytes (8 bytes for "
+                     "a 16-bit output) and < 2 GiB per K/V head");
+  const bool f32 = dtype == GHIP_DTYPE_FLOAT32;
+  const int64_t es = f32 ? 4 : 2;
   auto al = [](const void* ptr, uintptr_t a) { return (reinterpret_cast<uintptr_t>(ptr) & (a - 1)) == 0; };
-  if (!al(q, 16) || !al(k, 16) || !al(v, 16) || !al(o, 8))
-    return set_error(err, GHIP_ERR_UNSUPPORTED, "sdpa_fwd: q/k/v must be 16-byte aligned, o 8-byte aligned");
+  if (!al(q, 16) || !al(k, 16) || !al(v, 16) || !al(o, 4 * es))
+    return set_error(err, GHIP_ERR_UNSUPPORTED, "sdpa_fwd: q/k/v must be 16-byte aligned, o %d-byte aligned",
+                     static_cast<int>(4 * es));
   const int64_t nqb = (Sq + attn::kBQ - 1) / attn::kBQ;
   if (nqb * B * H > 0x7fffffffLL) return set_error(err, GHIP_ERR_INVALID_ARG, "sdpa_fwd: problem too large");
   attn::Params p{};
@@ -487,8 +732,9 @@ extern "C" int ghip_sdpa_fwd_masked(int dtype, const void* q, const void* k, con
   p.scale_log2 = scale * 1.4426950408889634f;
   p.inv_scale = 1.0f / scale;
   p.causal = causal ? 1 : 0;
-  p.k_extent = static_cast<uint32_t>(((Sk - 1) * p.k_ss + D) * 2);
-  p.v_extent = static_cast<uint32_t>(((Sk - 1) * p.v_ss + D) * 2);
+  p.D = static_cast<int>(D);
+  p.k_extent = static_cast<uint32_t>(((Sk - 1) * p.k_ss + D) * es);
+  p.v_extent = static_cast<uint32_t>(((Sk - 1) * p.v_ss + D) * es);
   int mk = attn::kNoMask;
   if (mask) {
     mk = mask_dtype == GHIP_DTYPE_BOOL ? attn::kBoolMask : attn::kAddMask;
@@ -496,18 +742,25 @@ extern "C" int ghip_sdpa_fwd_masked(int dtype, const void* q, const void* k, con
     p.m_sb = mask_strides[0]; p.m_sh = mask_strides[1]; p.m_sq = mask_strides[2]; p.m_sk = mask_strides[3];
     // Vector loads of 4-key groups (keys are multiples of 4 apart): unit key stride
     // and every row start aligned to 4 elements.
-    const int64_t es = mask_dtype == GHIP_DTYPE_BOOL ? 1 : 2;
-    p.mask_vec = p.m_sk == 1 && p.m_sb % 4 == 0 && p.m_sh % 4 == 0 && p.m_sq % 4 == 0 && al(mask, 4 * es);
+    const int64_t mes = mask_dtype == GHIP_DTYPE_BOOL ? 1 : es;
+    p.mask_vec = p.m_sk == 1 && p.m_sb % 4 == 0 && p.m_sh % 4 == 0 && p.m_sq % 4 == 0 && al(mask, 4 * mes);
   }
   const dim3 grid(static_cast<unsigned>(nqb * B * H));
   const hipStream_t s = static_cast<hipStream_t>(stream);
   const bool f16 = dtype == GHIP_DTYPE_FLOAT16;
-  if (D == 64) {
+  // The smallest padded width that holds D.
+  if (f32) {
+    if (D <= 64) attn::launch_f32<64>(p, mk, grid, s);
+    else attn::launch_f32<128>(p, mk, grid, s);
+  } else if (D <= 64) {
     if (f16) attn::launch_d<64, true>(p, mk, grid, s);
     else attn::launch_d<64, false>(p, mk, grid, s);
-  } else {
+  } else if (D <= 128) {
     if (f16) attn::launch_d<128, true>(p, mk, grid, s);
     else attn::launch_d<128, false>(p, mk, grid, s);
+  } else {
+    if (f16) attn::launch_d<256, true>(p, mk, grid, s);
+    else attn::launch_d<256, false>(p, mk, grid, s);
   }
   GHIP_CHECK(hipGetLastError(), err);
   return GHIP_OK;

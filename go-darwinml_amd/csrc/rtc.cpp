@@ -2,8 +2,8 @@
 //
 // Compile turns each elementwise cluster into HIP source (graph_lower.cpp) and
 // this file compiles it once per process with hipRTC for gfx950, caching the
-// loaded module by source text, so identical clusters across graphs share one
-// code object.  A plan-only backend compiles (which validates the generated
+// code object by source text (identical clusters across graphs share one) and
+// loading it once on each device that runs it.  A plan-only backend compiles (which validates the generated
 // source) but never loads modules.
 #include <hip/hip_runtime.h>
 #include <hip/hiprtc.h>
@@ -23,10 +23,11 @@
 namespace ghip {
 
 namespace {
+// One code object per source; one loaded module per device that has run it (a
+// module loaded while device d is current holds functions of d's context only).
 struct Entry {
   std::vector<char> code;
-  RtcKernel k;
-  bool loaded = false;
+  std::map<int, RtcKernel> loaded;
 };
 std::mutex g_mu;
 std::map<std::string, Entry> g_cache;
@@ -81,15 +82,20 @@ int rtc_get(GHipBackend* be, const std::string& src, const std::string& entry, R
     *out = RtcKernel{};
     return GHIP_OK;
   }
-  if (!e.loaded) {
+  auto it = e.loaded.find(be->device);
+  if (it == e.loaded.end()) {
     hipSetDevice(be->device);
-    hipError_t h = hipModuleLoadData(&e.k.module, e.code.data());
+    RtcKernel k{};
+    hipError_t h = hipModuleLoadData(&k.module, e.code.data());
     if (h != hipSuccess) return check_hip(h, err, "hipModuleLoadData(generated kernel)");
-    h = hipModuleGetFunction(&e.k.func, e.k.module, entry.c_str());
-    if (h != hipSuccess) return check_hip(h, err, "hipModuleGetFunction(generated kernel)");
-    e.loaded = true;
+    h = hipModuleGetFunction(&k.func, k.module, entry.c_str());
+    if (h != hipSuccess) {
+      hipModuleUnload(k.module);
+      return check_hip(h, err, "hipModuleGetFunction(generated kernel)");
+    }
+    it = e.loaded.emplace(be->device, k).first;
   }
-  *out = e.k;
+  *out = it->second;
   return GHIP_OK;
 }
 

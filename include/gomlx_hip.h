@@ -158,11 +158,12 @@ int ghip_gemm_batched(int ab_dtype, int c_dtype, int64_t batch, int64_t M, int64
  *                   when causal]) v[b, hk, j, :],   hk = h / (H / Hkv)  (GQA, :2911-2956)
  * Operands are addressed by ELEMENT strides (batch, head, sequence) with the head
  * dim contiguous, so BHSD and BSHD layouts both work without copies.  Supported:
- * dtype BFLOAT16 or FLOAT16, D == 64 or 128, scale > 0, strides multiples of 8
- * (4 for o), q/k/v 16-byte and o 8-byte aligned; anything else returns
- * GHIP_ERR_UNSUPPORTED (the graph lowering then uses the composite).  Softmax
- * statistics and accumulation are fp32; weights below 2^-126 of a row's largest
- * are flushed to zero. */
+ * dtype BFLOAT16 or FLOAT16 with D a multiple of 8 up to 256, strides multiples of
+ * 8 (4 for o), o 8-byte aligned; or FLOAT32 with D a multiple of 4 up to 128,
+ * strides multiples of 4, o 16-byte aligned; scale > 0 and q/k/v 16-byte aligned.
+ * Anything else returns GHIP_ERR_UNSUPPORTED (the graph lowering then uses the
+ * composite).  Softmax statistics and accumulation are fp32 (fp32 products too for
+ * FLOAT32); weights below 2^-126 of a row's largest are flushed to zero. */
 int ghip_sdpa_fwd(int dtype, const void* q, const void* k, const void* v, void* o,
                   int64_t B, int64_t H, int64_t Hkv, int64_t Sq, int64_t Sk, int64_t D,
                   const int64_t* q_strides, const int64_t* k_strides, const int64_t* v_strides,

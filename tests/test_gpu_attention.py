@@ -1,10 +1,14 @@
-"""Parity of the fused attention kernel (ghip_sdpa_fwd / ghip_sdpa_fwd_masked)
+"""Parity of the fused attention kernels (ghip_sdpa_fwd / ghip_sdpa_fwd_masked)
 against the oracle's attention (fp64, oracle/oracle.c orc_sdpa following
-function.go:2669-2907), for bf16 and f16, head dims 64 and 128, and the
-reference's masks (boolean keep-masks and additive masks of any rank broadcast to
-the scores, function.go:2840-2878, 2959-2974).
+function.go:2669-2907), for bf16 and f16 with head dims that are multiples of 8 up
+to 256 (64 and 128 exactly, the others padded to 64 / 128 / 256), fp32 with head
+dims that are multiples of 4 up to 128, and the reference's masks (boolean
+keep-masks and additive masks of any rank broadcast to the scores,
+function.go:2840-2878, 2959-2974).
 
-Tolerances: 16-bit inputs, fp32 softmax / accumulation, P rounded to the 16-bit
+Tolerances, fp32: fp32 products, sums and softmax (exponents by v_exp_f32, within
+1 ulp), P unrounded: normwise <= 1e-5, elementwise <= 1e-4.
+Tolerances, 16-bit: 16-bit inputs, fp32 softmax / accumulation, P rounded to the 16-bit
 type before the second product and the output rounded once more.  Normwise
 ||got - ref|| / ||ref|| <= 1e-2 (the north-star bf16 bound).  Elementwise
 (RMS-floored, conftest.rel_err) <= 2.5e-2: two bf16 roundings of up to 2^-9 each
@@ -27,8 +31,15 @@ def bf16(shape, seed):
 
 
 def r16(a, dt):
-    """fp32 values rounded to the 16-bit dtype dt (returned as fp32)."""
+    """fp32 values rounded to dt (returned as fp32; fp32 unchanged)."""
+    if dt == torch.float32:
+        return np.asarray(a, np.float32)
     return synth.round_bf16(a) if dt == torch.bfloat16 else a.astype(np.float16).astype(np.float32)
+
+
+def tols(dt):
+    """(normwise, elementwise) bounds: fp32 or a 16-bit dtype (module docstring)."""
+    return (1e-5, 1e-4) if dt == torch.float32 else (1e-2, 2.5e-2)
 
 
 def dev(a, cuda, dt):
@@ -63,6 +74,75 @@ def test_sdpa_matches_oracle(cuda, case, D, dt):
     assert rel_err(got, ref) <= 2.5e-2
 
 
+@pytest.mark.parametrize("case", [CASES[0], CASES[2], CASES[3], CASES[4], CASES[5], CASES[6]])
+@pytest.mark.parametrize("D,dt", [(8, torch.bfloat16), (32, torch.bfloat16), (80, torch.float16),
+                                  (96, torch.bfloat16), (96, torch.float16), (160, torch.bfloat16),
+                                  (256, torch.bfloat16), (256, torch.float16)])
+def test_sdpa_head_dims_match_oracle(cuda, case, D, dt):
+    """16-bit head dims other than 64 / 128: padded to the next of 64 / 128 / 256
+    (zero chunks past D, output columns past D never written)."""
+    B, H, Hkv, Sq, Sk, causal = case
+    q = r16(synth.normal(4021 + D, (B, H, Sq, D)), dt)
+    k = r16(synth.normal(4022 + D, (B, Hkv, Sk, D)), dt)
+    v = r16(synth.normal(4023 + D, (B, Hkv, Sk, D)), dt)
+    scale = D ** -0.5
+    ref = orc.sdpa(q, k, v, scale=scale, causal=causal)
+    # Output in a wider buffer: columns past D must stay as they were.
+    wide = torch.full((B, H, Sq, D + 8), 7.0, device=cuda, dtype=dt)
+    ops.sdpa(*(dev(a, cuda, dt) for a in (q, k, v)), scale, causal, out=wide[..., :D])
+    got = wide[..., :D].float().cpu().numpy()
+    assert torch.all(wide[..., D:] == 7.0)
+    assert norm_err(got, ref) <= 1e-2
+    assert rel_err(got, ref) <= 2.5e-2
+
+
+@pytest.mark.parametrize("case", CASES)
+@pytest.mark.parametrize("D", [4, 32, 64, 96, 128])
+def test_sdpa_f32_matches_oracle(cuda, case, D):
+    """fp32 Q / K / V / O on fp32 MFMAs: every case, head dims 4 .. 128."""
+    B, H, Hkv, Sq, Sk, causal = case
+    q = synth.normal(4031 + Sq, (B, H, Sq, D))
+    k = synth.normal(4032 + Sk, (B, Hkv, Sk, D))
+    v = synth.normal(4033 + Sk, (B, Hkv, Sk, D))
+    scale = D ** -0.5
+    ref = orc.sdpa(q, k, v, scale=scale, causal=causal)
+    got = ops.sdpa(*(dev(a, cuda, torch.float32) for a in (q, k, v)), scale, causal).cpu().numpy()
+    assert norm_err(got, ref) <= 1e-5
+    assert rel_err(got, ref) <= 1e-4
+
+
+def test_sdpa_f32_large_scores(cuda):
+    """fp32 with scores spread over ~±300 (scale 1, |q|, |k| ~ 4): exercises the
+    lazy rescale of the running max and very small weights."""
+    B, H, S, D = 1, 2, 520, 64
+    q = synth.normal(4041, (B, H, S, D), std=2.2)
+    k = synth.normal(4042, (B, H, S, D), std=2.2)
+    v = synth.normal(4043, (B, H, S, D))
+    for causal in (False, True):
+        ref = orc.sdpa(q, k, v, scale=1.0, causal=causal)
+        got = ops.sdpa(*(dev(a, cuda, torch.float32) for a in (q, k, v)), 1.0, causal).cpu().numpy()
+        assert norm_err(got, ref) <= 1e-5
+        assert rel_err(got, ref) <= 1e-4
+
+
+def test_sdpa_head_dim_256_long(cuda):
+    """Head dim 256 (one workgroup a CU) over many key tiles: B2 H4 S1536 causal,
+    GQA 2:1, sampled rows against the oracle."""
+    B, H, Hkv, S, D = 2, 4, 2, 1536, 256
+    dt = torch.bfloat16
+    q = bf16((B, H, S, D), 4051)
+    k = bf16((B, Hkv, S, D), 4052)
+    v = bf16((B, Hkv, S, D), 4053)
+    got = ops.sdpa(*(dev(a, cuda, dt) for a in (q, k, v)), D ** -0.5, True).float().cpu().numpy()
+    rows = np.array([0, 63, 64, 700, 1535])
+    kmax = rows.max() + 1
+    kr, vr = np.repeat(k, 2, axis=1), np.repeat(v, 2, axis=1)
+    ref = orc.sdpa(q[:, :, rows], kr[:, :, :kmax], vr[:, :, :kmax], scale=D ** -0.5,
+                   mask=np.arange(kmax)[None, :] <= rows[:, None])
+    assert norm_err(got[:, :, rows], ref) <= 1e-2
+    assert rel_err(got[:, :, rows], ref) <= 2.5e-2
+
+
 MASKS = [  # (kind, mask shape as a function of (B, H, Sq, Sk))
     ("bool", lambda B, H, Sq, Sk: (B, 1, 1, Sk)),      # key padding per batch row
     ("bool", lambda B, H, Sq, Sk: (B, H, Sq, Sk)),
@@ -91,7 +171,8 @@ def _mask(kind, shape, seed, dt):
 
 @pytest.mark.parametrize("mi", range(len(MASKS)))
 @pytest.mark.parametrize("causal", [False, True])
-@pytest.mark.parametrize("D,dt", [(128, torch.bfloat16), (64, torch.float16)])
+@pytest.mark.parametrize("D,dt", [(128, torch.bfloat16), (64, torch.float16), (96, torch.bfloat16),
+                                  (128, torch.float32), (64, torch.float32), (96, torch.float32)])
 def test_sdpa_masks_match_oracle(cuda, mi, causal, D, dt):
     """Every mask shape and kind, GQA, ragged query and key tiles."""
     B, H, Hkv, Sq, Sk = 2, 4, 2, 200, 264
@@ -108,8 +189,9 @@ def test_sdpa_masks_match_oracle(cuda, mi, causal, D, dt):
         ref = orc.sdpa(q, k, v, additive=m, scale=scale, causal=causal)
         tm = dev(m, cuda, dt)
     got = ops.sdpa_masked(*(dev(a, cuda, dt) for a in (q, k, v)), tm, scale, causal).float().cpu().numpy()
-    assert norm_err(got, ref) <= 1e-2
-    assert rel_err(got, ref) <= 2.5e-2
+    nt, et = tols(dt)
+    assert norm_err(got, ref) <= nt
+    assert rel_err(got, ref) <= et
 
 
 @pytest.mark.parametrize("kind,mshape", [("bool", "b11k"), ("bool", "bhqk"), ("add", "b11k")])
@@ -147,14 +229,16 @@ def test_sdpa_masks_config_shape_rows(cuda, kind, mshape):
         assert norm_err(got[b:b + 1, :, rows], ref) <= 1e-2
 
 
-def test_sdpa_fully_masked_row_is_nan(cuda):
+@pytest.mark.parametrize("D,dt", [(128, torch.bfloat16), (96, torch.float16), (128, torch.float32),
+                                  (40, torch.float32)])
+def test_sdpa_fully_masked_row_is_nan(cuda, D, dt):
     """A query whose keys are all masked: NaN, like the reference's softmax of -inf
     (the oracle gives the same)."""
-    B, H, S, D = 1, 2, 128, 128
+    B, H, S = 1, 2, 128
     q, k, v = bf16((B, H, S, D), 4601), bf16((B, H, S, D), 4602), bf16((B, H, S, D), 4603)
     m = np.ones((S, S), bool)
     m[5] = False
-    got = ops.sdpa_masked(*(dev(a, cuda, torch.bfloat16) for a in (q, k, v)),
+    got = ops.sdpa_masked(*(dev(a, cuda, dt) for a in (q, k, v)),
                           torch.from_numpy(m).to(cuda), 0.1, False).float().cpu().numpy()
     assert np.all(np.isnan(got[:, :, 5])) and np.all(np.isfinite(np.delete(got, 5, axis=2)))
     assert np.all(np.isnan(orc.sdpa(q, k, v, mask=m, scale=0.1)[:, :, 5]))
@@ -195,6 +279,20 @@ def test_sdpa_bshd_strides(cuda):
     assert norm_err(got, ref) <= 1e-2
 
 
+@pytest.mark.parametrize("D,dt", [(96, torch.bfloat16), (96, torch.float32), (64, torch.float32)])
+def test_sdpa_bshd_strides_other_dims(cuda, D, dt):
+    """BSHD storage through strides for a padded 16-bit head dim and for fp32."""
+    B, S, H = 2, 160, 4
+    q, k, v = (r16(synth.normal(4111 + i, (B, S, H, D)), dt) for i in range(3))
+    to_bhsd = lambda a: np.ascontiguousarray(a.transpose(0, 2, 1, 3))  # noqa: E731
+    ref = orc.sdpa(to_bhsd(q), to_bhsd(k), to_bhsd(v), scale=0.09, causal=True)
+    tq, tk, tv = (torch.from_numpy(a).to(cuda).to(dt).transpose(1, 2) for a in (q, k, v))
+    out = torch.empty((B, S, H, D), device=cuda, dtype=dt)
+    ops.sdpa(tq, tk, tv, 0.09, True, out=out.transpose(1, 2))
+    got = out.float().cpu().numpy().transpose(0, 2, 1, 3)
+    assert norm_err(got, ref) <= tols(dt)[0]
+
+
 def test_sdpa_causal_row0_is_v0(cuda):
     """Causal row 0 attends to key 0 only: out[.., 0, :] == v[.., 0, :] (function.go
     causal mask, the reference's known answer mpsgraph_test.go:2996-3015)."""
@@ -221,12 +319,18 @@ def test_sdpa_config_shape_rows(cuda):
 
 
 def test_sdpa_rejects_unsupported(cuda):
-    q = torch.zeros((1, 2, 16, 96), device=cuda, dtype=torch.bfloat16)
+    q = torch.zeros((1, 2, 16, 100), device=cuda, dtype=torch.bfloat16)
     with pytest.raises(BackendError):
-        ops.sdpa(q, q, q, 1.0, False)  # head dim 96: not fused (composite path)
-    q = torch.zeros((1, 2, 16, 128), device=cuda, dtype=torch.float32)
+        ops.sdpa(q, q, q, 1.0, False)  # 16-bit head dim not a multiple of 8: composite path
+    q = torch.zeros((1, 2, 16, 264), device=cuda, dtype=torch.bfloat16)
     with pytest.raises(BackendError):
-        ops.sdpa(q, q, q, 1.0, False)  # fp32: composite path only
+        ops.sdpa(q, q, q, 1.0, False)  # 16-bit head dim above 256
+    q = torch.zeros((1, 2, 16, 256), device=cuda, dtype=torch.float32)
+    with pytest.raises(BackendError):
+        ops.sdpa(q, q, q, 1.0, False)  # fp32 head dim above 128
+    q = torch.zeros((1, 2, 16, 6), device=cuda, dtype=torch.float32)
+    with pytest.raises(BackendError):
+        ops.sdpa(q, q, q, 1.0, False)  # fp32 head dim not a multiple of 4
     q = torch.zeros((1, 3, 16, 128), device=cuda, dtype=torch.bfloat16)
     k = torch.zeros((1, 2, 16, 128), device=cuda, dtype=torch.bfloat16)
     with pytest.raises(BackendError):

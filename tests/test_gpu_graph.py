@@ -480,12 +480,14 @@ def test_graph_sdpa_gqa_causal(be, layout):
 
 @pytest.mark.parametrize("layout", [AxesLayout.BHSD, AxesLayout.BSHD])
 @pytest.mark.parametrize("dt,D,kind", [(BF16, 128, "bool"), (BF16, 64, "add"), (dtypes.Float16, 128, "add"),
-                                       (F32, 64, "add"), (F32, 96, "bool")])
+                                       (BF16, 96, "bool"), (F32, 64, "add"), (F32, 96, "bool"),
+                                       (BF16, 100, "add"), (F32, 144, "bool")])
 def test_graph_sdpa_masks(be, layout, dt, D, kind):
     """FusedScaledDotProductAttention with a mask through the graph API: rank-4
     masks in Q's layout (BSHD masks are [B, Sq, H, Sk], transposed as the reference
     does, function.go:2709-2718), lower ranks broadcast over the trailing axes;
-    bf16 / f16 with head dim 64 or 128 take the fused kernel, fp32 or head dim 96
+    bf16 / f16 with a head dim that is a multiple of 8 up to 256 and fp32 with a
+    multiple of 4 up to 128 take the fused kernel, the others (bf16 100, fp32 144)
     the composite (GEMM, masked softmax, GEMM)."""
     B, H, Hkv, S, Sk = 2, 4, 2, 136, 136
     q = synth.normal(4801, (B, H, S, D))
@@ -517,7 +519,8 @@ def test_graph_sdpa_masks(be, layout, dt, D, kind):
     f.Return([f.FusedScaledDotProductAttention(*ps, pm, H, Hkv, layout, D ** -0.5, True)])
     ex = b.Compile()
     plan = ex.Plan()
-    assert ("fused attention" in plan) == (dt != F32 and D in (64, 128)), plan
+    fused = (D % 8 == 0 and D <= 256) if dt != F32 else (D % 4 == 0 and D <= 128)
+    assert ("fused attention" in plan) == fused, plan
     bufs = [be.BufferFromFlatData(0, host(t(a)), make_shape(dt, *t(a).shape)) for a in (q, k, v)]
     bufs.append(be.BufferFromFlatData(0, mh, make_shape(mdt, *mt.shape)))
     (r,) = ex.Execute(bufs, None, 0)
@@ -525,7 +528,7 @@ def test_graph_sdpa_masks(be, layout, dt, D, kind):
     y = synth.bf16_bits_to_f32(y) if dt == BF16 else y.astype(np.float32)
     if layout == AxesLayout.BSHD:
         y = y.transpose(0, 2, 1, 3)
-    # fp32 composite: scores and probabilities in fp32; 16-bit: P and the output rounded
+    # fp32: scores and probabilities in fp32; 16-bit: P and the output rounded
     assert norm_err(y, ref) <= (1e-4 if dt == F32 else 1e-2)
     ex.Finalize()
     # a key-padding mask [B, 1, 1, Sk] (rank 4 in BHSD, where BSHD and BHSD agree)

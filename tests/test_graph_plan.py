@@ -250,11 +250,17 @@ def test_transformer_block_plan(be, monkeypatch):
     assert p.count("sdpa_fwd bfloat16") == 1 and "causal=1 mask=none (fused attention)" in p
     assert p.count("gemm_batched+epilogue") == 3 and p.count("dots=2") == 1
     assert "fused_elementwise" not in p
-    # head dim 96 has no fused kernel: GEMM, scale + causal softmax, GEMM
+    # head dim 96: the fused kernel (padded to 128)
     c96 = graphs.TransformerBlockConfig(batch=2, seq=64, vocab=100, d_model=192, heads=2, head_dim=96, ffn=256)
     p96 = graphs.transformer_block(be, c96).Plan()
-    assert "sdpa_fwd" not in p96 and "scale_mask_softmax_rows" in p96 and "causal=1" in p96
-    assert p96.count("gemm_batched bfloat16") == 5
+    assert "sdpa_fwd bfloat16" in p96 and "D=96 causal=1 mask=none (fused attention)" in p96
+    assert "scale_mask_softmax_rows" not in p96 and p96.count("gemm_batched bfloat16") == 3
+    # head dim 100 (not a multiple of 8) has no fused kernel: GEMM, scale + causal
+    # softmax, GEMM
+    c100 = graphs.TransformerBlockConfig(batch=2, seq=64, vocab=100, d_model=200, heads=2, head_dim=100, ffn=256)
+    p100 = graphs.transformer_block(be, c100).Plan()
+    assert "sdpa_fwd" not in p100 and "scale_mask_softmax_rows" in p100 and "causal=1" in p100
+    assert p100.count("gemm_batched bfloat16") == 5
     monkeypatch.setenv("GHIP_EPILOGUE_FUSION", "0")
     u = graphs.transformer_block(be, cfg).Plan()
     assert u.count("gemm_batched bfloat16") == 7 and "gemm_batched+epilogue" not in u
