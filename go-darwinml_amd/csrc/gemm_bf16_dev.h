@@ -67,7 +67,13 @@ struct GemmParams {
   uint32_t a_extent, b_extent;  // bytes addressable from one batch slice's base
   int vec_c;                    // C rows allow 4-element vector stores
   const void* b1;               // second right operand (NB = 2), B's strides and extent
+  // Grouped launch (4-wave K-contiguous-A core): groups > 0 products A.B_g -> C_g
+  // sharing A, one per "batch" index g; b_g / c_g replace b + g sb_b / c + g sc_b.
+  int groups;
+  const void* b_g[4];
+  void* c_g[4];
 };
+constexpr int kGemmMaxGroups = 4;
 
 // Generated epilogues read up to kEpiMaxIn extra operands, each addressed as
 // in[k] + bb * s_b[k] + m * s_m[k] + n * s_n[k] (elements), and write `out`
@@ -84,6 +90,13 @@ struct EpiArgs {
 
 #if defined(__HIP__) || defined(__HIPCC_RTC__)
 // (The structs above are also used by host-only translation units.)
+
+// ptrs[g] for a wave-uniform g < kGemmMaxGroups, by selects (an indexed read of a
+// kernel-argument array would be copied to scratch memory first).
+template <typename P>
+__device__ __forceinline__ P pick_group(const P (&ptrs)[kGemmMaxGroups], int64_t g) {
+  return g == 0 ? ptrs[0] : g == 1 ? ptrs[1] : g == 2 ? ptrs[2] : ptrs[3];
+}
 
 // Maps a linear workgroup id to (batch, tile_m, tile_n).
 __device__ __forceinline__ void map_tile(int64_t bid, int64_t total, int tiles_m, int tiles_n,
@@ -827,7 +840,9 @@ __device__ __forceinline__ void gemm_bf16_body8km(const GemmParams& p, const Epi
   map_tile(blockIdx.x, p.batch * p.tiles_m * p.tiles_n, p.tiles_m, p.tiles_n, bb, tm, tn);
   const int64_t m0 = static_cast<int64_t>(tm) * BM, n0 = static_cast<int64_t>(tn) * BN;
   const uint16_t* A0 = static_cast<const uint16_t*>(p.a) + bb * p.sa_b + m0 * p.sa_m;
-  const uint16_t* B0 = static_cast<const uint16_t*>(p.b) + bb * p.sb_b + n0 * p.sb_n;
+  const uint16_t* B0 = (NP == 1 && p.groups ? static_cast<const uint16_t*>(pick_group(p.b_g, bb))
+                                             : static_cast<const uint16_t*>(p.b) + bb * p.sb_b) +
+                       n0 * p.sb_n;
   const uint16_t* B1 = static_cast<const uint16_t*>(NP == 2 ? p.b1 : p.b) + bb * p.sb_b + n0 * p.sb_n;
   const uint32_t a_left0 = p.a_extent - static_cast<uint32_t>(m0 * p.sa_m * 2);
   const uint32_t b_left0 = p.b_extent - static_cast<uint32_t>(n0 * p.sb_n * 2);
@@ -1053,7 +1068,9 @@ __device__ __forceinline__ void gemm_bf16_body4km(const GemmParams& p, const Epi
   map_tile(blockIdx.x, p.batch * p.tiles_m * p.tiles_n, p.tiles_m, p.tiles_n, bb, tm, tn);
   const int64_t m0 = static_cast<int64_t>(tm) * BM, n0 = static_cast<int64_t>(tn) * BN;
   const uint16_t* A0 = static_cast<const uint16_t*>(p.a) + bb * p.sa_b + m0 * p.sa_m;
-  const uint16_t* B0 = static_cast<const uint16_t*>(p.b) + bb * p.sb_b + n0 * p.sb_n;
+  const uint16_t* B0 = (NP == 1 && p.groups ? static_cast<const uint16_t*>(pick_group(p.b_g, bb))
+                                             : static_cast<const uint16_t*>(p.b) + bb * p.sb_b) +
+                       n0 * p.sb_n;
   const uint16_t* B1 = static_cast<const uint16_t*>(NP == 2 ? p.b1 : p.b) + bb * p.sb_b + n0 * p.sb_n;
   const uint32_t a_left0 = p.a_extent - static_cast<uint32_t>(m0 * p.sa_m * 2);
   const uint32_t b_left0 = p.b_extent - static_cast<uint32_t>(n0 * p.sb_n * 2);
@@ -1255,7 +1272,9 @@ __device__ __forceinline__ void gemm_bf16_body8x(const GemmParams& p, const Epi&
   map_tile(blockIdx.x, p.batch * p.tiles_m * p.tiles_n, p.tiles_m, p.tiles_n, bb, tm, tn);
   const int64_t m0 = static_cast<int64_t>(tm) * BM, n0 = static_cast<int64_t>(tn) * BN;
   const uint16_t* A0 = static_cast<const uint16_t*>(p.a) + bb * p.sa_b + m0 * p.sa_m;
-  const uint16_t* B0 = static_cast<const uint16_t*>(p.b) + bb * p.sb_b + n0 * p.sb_n;
+  const uint16_t* B0 = (NP == 1 && p.groups ? static_cast<const uint16_t*>(pick_group(p.b_g, bb))
+                                             : static_cast<const uint16_t*>(p.b) + bb * p.sb_b) +
+                       n0 * p.sb_n;
   const uint16_t* B1 = static_cast<const uint16_t*>(NP == 2 ? p.b1 : p.b) + bb * p.sb_b + n0 * p.sb_n;
   const uint32_t a_left0 = p.a_extent - static_cast<uint32_t>(m0 * p.sa_m * 2);
   const uint32_t b_left0 = p.b_extent - static_cast<uint32_t>(n0 * p.sb_n * 2);

@@ -1746,10 +1746,87 @@ struct Lowerer {
     return true;
   }
 
+  // Dots that share Dot v's left operand view, sizes and right-operand strides run
+  // as one grouped launch (ghip_gemm_grouped: the Q, K, V projections of an
+  // attention block).  A sibling joins when no elementwise cluster uses it (one
+  // could absorb it as a GEMM epilogue), its right operand is a leaf or already
+  // lowered (lowering it here cannot reach back to v), and it folds without an
+  // operand copy.  Returns an empty view when v has no sibling.
+  bool group_dots = true;
+  View emit_dot_group(int v, const DotPlan& d) {
+    const Node& n = N[v];
+    const int L = n.in[0];
+    const int dt = N[L].shape.dtype, odt = n.shape.dtype;
+    if (d.B != 1 || (dt != GHIP_DTYPE_BFLOAT16 && dt != GHIP_DTYPE_FLOAT16)) return View{};
+    std::vector<int> grp{v};
+    std::vector<DotPlan> plans{d};
+    for (int u : users[L]) {
+      if (static_cast<int>(grp.size()) == kGemmMaxGroups) break;
+      if (u == v || !live[u] || have[u] || N[u].kind != Kind::Dot || fusion[u].kind != Fusion::None) continue;
+      const Node& m = N[u];
+      if (m.in[0] != L || m.a0 != n.a0 || m.a1 != n.a1 || m.a2 != n.a2 || m.a3 != n.a3 || m.shape.dtype != odt ||
+          m.shape.dims != n.shape.dims || N[m.in[1]].shape.dims != N[n.in[1]].shape.dims ||
+          N[m.in[1]].shape.dtype != N[n.in[1]].shape.dtype)
+        continue;
+      bool absorbable = false;
+      for (int w : users[u]) absorbable = absorbable || cluster[w] >= 0;
+      if (absorbable || std::find(grp.begin(), grp.end(), u) != grp.end()) continue;
+      const Kind rk = N[m.in[1]].kind;
+      if (!have[m.in[1]] && rk != Kind::Param && rk != Kind::Const && rk != Kind::Capture) continue;
+      DotPlan du;
+      if (!plan_dot(u, false, &du)) {
+        if (failed) return bad();
+        continue;
+      }
+      if (du.lv.slot != d.lv.slot || du.lv.offset != d.lv.offset || du.lv.strides != d.lv.strides ||
+          du.sam != d.sam || du.sak != d.sak || du.B != 1 || du.M != d.M || du.N != d.N || du.K != d.K ||
+          du.sbk != d.sbk || du.sbn != d.sbn)
+        continue;
+      grp.push_back(u);
+      plans.push_back(du);
+    }
+    if (grp.size() < 2) return View{};
+    const int G = static_cast<int>(grp.size());
+    std::vector<View> ys, rvs;
+    std::vector<int> rd{d.lv.slot}, wr;
+    for (int g = 0; g < G; ++g) {
+      ys.push_back(fresh(N[grp[g]].shape));
+      rvs.push_back(plans[g].rv);
+      rd.push_back(plans[g].rv.slot);
+      wr.push_back(ys.back().slot);
+    }
+    const View lv = d.lv;
+    const int64_t M = d.M, N_ = d.N, K = d.K, sam = d.sam, sak = d.sak, sbk = d.sbk, sbn = d.sbn;
+    add_step(fmt("gemm_grouped %s G=%d M=%lld N=%lld K=%lld (products sharing a; a strides m=%lld k=%lld, b strides "
+                 "k=%lld n=%lld)",
+                 dtype_name(dt), G, (long long)M, (long long)N_, (long long)K, (long long)sam, (long long)sak,
+                 (long long)sbk, (long long)sbn),
+             rd, wr, [=](ExecState& st, GHipError* e) {
+               const void* bp[kGemmMaxGroups];
+               void* cp[kGemmMaxGroups];
+               for (int g = 0; g < G; ++g) {
+                 bp[g] = st.ptr(rvs[g], dt);
+                 cp[g] = st.ptr(ys[g], odt);
+               }
+               return ghip_gemm_grouped(dt, odt, G, M, N_, K, st.ptr(lv, dt), sam, sak, bp, sbk, sbn, cp, N_,
+                                        st.stream, e);
+             });
+    for (int g = 1; g < G; ++g) {
+      views[grp[g]] = ys[g];
+      have[grp[g]] = 1;
+    }
+    return ys[0];
+  }
+
   View emit_dot(int v) {
     const Node& n = N[v];
     DotPlan d;
     if (!plan_dot(v, true, &d)) return bad();
+    if (group_dots) {
+      const View y = emit_dot_group(v, d);
+      if (failed) return bad();
+      if (y.slot >= 0) return y;
+    }
     const View lv = d.lv, rv = d.rv;
     const int64_t B = d.B, sab = d.sab, sbb = d.sbb, M = d.M, sam = d.sam, K = d.K, sak = d.sak, N_ = d.N,
                   sbn = d.sbn, sbk = d.sbk;
@@ -2911,6 +2988,9 @@ int lower(GHipBackend* be, GHipFunction* fn, Plan* plan, GHipError* err) {
   L.fuse_epilogues = !(ef && ef[0] == '0');
   const char* rf = getenv("GHIP_REDUCE_FUSION");
   L.fuse_reductions = !(rf && rf[0] == '0');
+  // GHIP_DOT_GROUPING=0 keeps DotGenerals that share a left operand separate.
+  const char* gf = getenv("GHIP_DOT_GROUPING");
+  L.group_dots = !(gf && gf[0] == '0');
   L.have.assign(fn->nodes.size(), 0);
   L.views.assign(fn->nodes.size(), View{});
   L.analyse();

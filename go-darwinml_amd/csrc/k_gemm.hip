@@ -107,6 +107,28 @@ __global__ __launch_bounds__(256, 1) void gemm_bf16_kernel4km(GemmParams p) {
   const StoreEpi<OutT> epi = store_epi<OutT>(p);
   gemm_bf16_body4km<StoreEpi<OutT>, __is_same(InT, f16_t)>(p, epi);
 }
+// Products sharing A, one per "batch" index g of the grid (gemm_bf16_kernel4km's
+// core): the output base of tile group g is c_g[g].
+template <typename OutT>
+struct GroupStoreEpi : StoreEpi<OutT> {
+  void* cg[kGemmMaxGroups];
+  template <bool FULL>
+  __device__ __forceinline__ void store(int64_t bb, int64_t m, int64_t n, const typename StoreEpi<OutT>::Stage* v,
+                                        const typename StoreEpi<OutT>::Stage* v1,
+                                        const typename StoreEpi<OutT>::Pre& pre) const {
+    StoreEpi<OutT> e = *this;
+    e.c = static_cast<OutT*>(pick_group(cg, bb));
+    e.template store<FULL>(0, m, n, v, v1, pre);
+  }
+};
+template <typename InT, typename OutT>
+__global__ __launch_bounds__(256, 1) void gemm_bf16_kernel4km_grouped(GemmParams p) {
+  GroupStoreEpi<OutT> epi;
+  static_cast<StoreEpi<OutT>&>(epi) = store_epi<OutT>(p);
+#pragma unroll
+  for (int g = 0; g < kGemmMaxGroups; ++g) epi.cg[g] = p.c_g[g];
+  gemm_bf16_body4km<GroupStoreEpi<OutT>, __is_same(InT, f16_t)>(p, epi);
+}
 // The 4-wave 256 x 256 core for both operands MN-contiguous (32-deep, four stages).
 template <typename InT, typename OutT>
 __global__ __launch_bounds__(256, 1) void gemm_bf16_kernel4mn(GemmParams p) {
@@ -443,6 +465,52 @@ static hipError_t dispatch_bf16(GemmParams p, hipStream_t s) {
   return launch_bf16<128, 128, 2, 2, InT, OutT>(p, ma, mb, s);
 }
 
+// G products A.B_g -> C_g sharing A (same sizes and strides): one launch of G x
+// tiles workgroups on the 4-wave core when A is K-contiguous and every B_g is
+// MN-contiguous (the layouts of x . W); otherwise one dispatch per product.  Each
+// product's result is the one the stand-alone dispatch would give (the same core
+// and k order).
+template <typename InT, typename OutT>
+static hipError_t dispatch_grouped(GemmParams p, int G, const void* const* b, void* const* c, hipStream_t s) {
+  bool ok = majorness(p.a, 0, p.sa_m, p.sa_k, p.M, p.K, 8, 1) == 1 && p.sa_m >= 0 && p.sa_k >= 0 &&
+            p.sb_k >= 0 && p.sb_n >= 0;
+  for (int g = 0; g < G && ok; ++g) ok = majorness(b[g], 0, p.sb_n, p.sb_k, p.N, p.K, 8, 1) == 0;
+  const int64_t ea = slice_bytes(p.M, p.sa_m, p.K, p.sa_k, 2);
+  const int64_t eb = slice_bytes(p.N, p.sb_n, p.K, p.sb_k, 2);
+  const int64_t tiles = ((p.M + 255) / 256) * ((p.N + 255) / 256);
+  ok = ok && ea < (int64_t{1} << 31) && eb < (int64_t{1} << 31) && p.M >= 256 && p.N >= 256 && G * tiles >= 128;
+  if (!ok) {
+    for (int g = 0; g < G; ++g) {
+      GemmParams q = p;
+      q.batch = 1;
+      q.b = b[g];
+      q.c = c[g];
+      const hipError_t e = dispatch_bf16<InT, OutT>(q, s);
+      if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
+  }
+  p.a_extent = static_cast<uint32_t>(ea);
+  p.b_extent = static_cast<uint32_t>(eb);
+  constexpr int64_t kV = 16 / sizeof(OutT);
+  p.vec_c = p.sc_m % kV == 0;
+  for (int g = 0; g < G; ++g) p.vec_c = p.vec_c && reinterpret_cast<uintptr_t>(c[g]) % 16 == 0;
+  p.batch = G;
+  p.sa_b = p.sb_b = p.sc_b = 0;
+  p.groups = G;
+  for (int g = 0; g < kGemmMaxGroups; ++g) {
+    p.b_g[g] = b[g < G ? g : 0];
+    p.c_g[g] = c[g < G ? g : 0];
+  }
+  p.b = b[0];
+  p.c = c[0];
+  p.tiles_m = static_cast<int>((p.M + 255) / 256);
+  p.tiles_n = static_cast<int>((p.N + 255) / 256);
+  hipLaunchKernelGGL((gemm_bf16_kernel4km_grouped<InT, OutT>), dim3(static_cast<unsigned>(G * tiles)), dim3(256), 0,
+                     s, p);
+  return hipGetLastError();
+}
+
 template <typename OutT>
 static hipError_t dispatch_f32(GemmParams p, hipStream_t s) {
   const int ma = majorness(p.a, p.sa_b, p.sa_m, p.sa_k, p.M, p.K, 4, p.batch);
@@ -502,6 +570,47 @@ extern "C" int ghip_gemm_batched(int ab_dtype, int c_dtype, int64_t batch, int64
   } else {
     return set_error(err, GHIP_ERR_UNSUPPORTED, "gemm_batched: input dtype %d", ab_dtype);
   }
+  GHIP_CHECK(e, err);
+  return GHIP_OK;
+}
+
+extern "C" int ghip_gemm_grouped(int ab_dtype, int c_dtype, int groups, int64_t M, int64_t N, int64_t K,
+                                 const void* a, int64_t sa_m, int64_t sa_k, const void* const* b, int64_t sb_k,
+                                 int64_t sb_n, void* const* c, int64_t sc_m, void* stream, GHipError* err) {
+  if (groups < 1 || groups > kGemmMaxGroups)
+    return set_error(err, GHIP_ERR_INVALID_ARG, "gemm_grouped: groups must be 1..%d", kGemmMaxGroups);
+  if (M < 0 || N < 0 || K < 0) return set_error(err, GHIP_ERR_INVALID_ARG, "gemm_grouped: negative size");
+  if (M == 0 || N == 0) return GHIP_OK;
+  if (!b || !c) return set_error(err, GHIP_ERR_INVALID_ARG, "gemm_grouped: null pointer array");
+  for (int g = 0; g < groups; ++g)
+    if (!c[g] || (K > 0 && (!a || !b[g]))) return set_error(err, GHIP_ERR_INVALID_ARG, "gemm_grouped: null pointer");
+  const bool in16 = ab_dtype == GHIP_DTYPE_BFLOAT16 || ab_dtype == GHIP_DTYPE_FLOAT16;
+  if (!in16 || K == 0 || (c_dtype != ab_dtype && c_dtype != GHIP_DTYPE_FLOAT32)) {
+    // fp32 operands, an empty contraction or an output dtype the batched entry
+    // rejects: product by product.
+    for (int g = 0; g < groups; ++g) {
+      const int rc = ghip_gemm_batched(ab_dtype, c_dtype, 1, M, N, K, a, 0, sa_m, sa_k, b[g], 0, sb_k, sb_n, c[g], 0,
+                                       sc_m, 1, stream, err);
+      if (rc != GHIP_OK) return rc;
+    }
+    return GHIP_OK;
+  }
+  if (((M + 127) / 128) * ((N + 127) / 128) > 0x7fffffffLL / groups)
+    return set_error(err, GHIP_ERR_INVALID_ARG, "gemm_grouped: problem too large");
+  GemmParams p{};
+  p.a = a;
+  p.sa_m = sa_m; p.sa_k = sa_k;
+  p.sb_k = sb_k; p.sb_n = sb_n;
+  p.sc_m = sc_m;
+  p.batch = 1; p.M = M; p.N = N; p.K = K;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  hipError_t e;
+  if (ab_dtype == GHIP_DTYPE_BFLOAT16)
+    e = c_dtype == GHIP_DTYPE_FLOAT32 ? dispatch_grouped<bf16_t, float>(p, groups, b, c, s)
+                                      : dispatch_grouped<bf16_t, bf16_t>(p, groups, b, c, s);
+  else
+    e = c_dtype == GHIP_DTYPE_FLOAT32 ? dispatch_grouped<f16_t, float>(p, groups, b, c, s)
+                                      : dispatch_grouped<f16_t, f16_t>(p, groups, b, c, s);
   GHIP_CHECK(e, err);
   return GHIP_OK;
 }

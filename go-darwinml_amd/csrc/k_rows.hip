@@ -412,10 +412,20 @@ __device__ __forceinline__ void rows_reg_group(const RowParams& p, int64_t blk, 
   }
 }
 
+// x, y, the row count and the row width come first as kernel arguments of their
+// own, preloaded into SGPRs like rows_norm_stream_kernel's: the row's loads are
+// addressed without waiting for a kernel-argument fetch (at the config's 6 us per
+// launch, that fetch is a visible part of the kernel).
 template <typename T, int OP, int NV, int WPR>
-__global__ __launch_bounds__(256) void rows_reg_kernel(RowParams p) {
+__global__ __launch_bounds__(256) void rows_reg_kernel(const void* x, void* y, int64_t rows, int64_t n,
+                                                       RowParams p) {
   __shared__ float lds[3][4];
-  rows_reg_group<T, OP, NV, WPR>(p, blockIdx.x, lds);
+  RowParams q = p;
+  q.x = x;
+  q.y = y;
+  q.rows = rows;
+  q.n = n;
+  rows_reg_group<T, OP, NV, WPR>(q, blockIdx.x, lds);
 }
 
 // Streaming RMSNorm / LayerNorm for rows that exactly fill NV vectors of every
@@ -628,7 +638,8 @@ template <typename T, int OP, int NV, int WPR>
 static hipError_t launch_reg(const RowParams& p, hipStream_t s) {
   const int rows_per_block = 4 / WPR;
   const int64_t groups = (p.rows + rows_per_block - 1) / rows_per_block;
-  hipLaunchKernelGGL((rows_reg_kernel<T, OP, NV, WPR>), dim3(static_cast<unsigned>(groups)), dim3(256), 0, s, p);
+  hipLaunchKernelGGL((rows_reg_kernel<T, OP, NV, WPR>), dim3(static_cast<unsigned>(groups)), dim3(256), 0, s, p.x, p.y,
+                     p.rows, p.n, p);
   return hipGetLastError();
 }
 

@@ -46,6 +46,8 @@ SIGNATURES = {
     "ghip_layernorm_rows": [_int, _vp, _vp, _vp, _vp, _i64, _i64, _f32, _vp, _errp],
     "ghip_gemm_batched": [_int, _int, _i64, _i64, _i64, _i64, _vp, _i64, _i64, _i64,
                           _vp, _i64, _i64, _i64, _vp, _i64, _i64, _i64, _vp, _errp],
+    "ghip_gemm_grouped": [_int, _int, _int, _i64, _i64, _i64, _vp, _i64, _i64, ctypes.POINTER(_vp), _i64, _i64,
+                          ctypes.POINTER(_vp), _i64, _vp, _errp],
     "ghip_gather_rows": [_vp, _i64, _i64, _vp, _i64, _vp, _vp, _errp],
     "ghip_argminmax": [_int, _vp, _i64, _i64, _i64, _int, _int, _vp, _vp, _errp],
     "ghip_iota": [_int, _vp, _i64, _i64, _i64, _vp, _errp],

@@ -116,6 +116,26 @@ def gemm(a: torch.Tensor, b: torch.Tensor, out_dtype=None, out=None, stream=None
     return c[0] if squeeze else c
 
 
+def gemm_grouped(a: torch.Tensor, bs, out_dtype=None, outs=None, stream=None):
+    """[a @ b for b in bs] in one call (ghip_gemm_grouped): a [M,K], every b [K,N]
+    with the same strides; returns the list of [M,N] results."""
+    import ctypes
+    _check_dev(a, *bs)
+    M, K = a.shape
+    K2, N = bs[0].shape
+    if K != K2 or any(b.shape != bs[0].shape or b.stride() != bs[0].stride() for b in bs):
+        raise ValueError("gemm_grouped: every b must be [K, N] with the same strides")
+    odt = out_dtype or a.dtype
+    cs = [torch.empty((M, N), dtype=odt, device=a.device) for _ in bs] if outs is None else list(outs)
+    if any(c.stride() != cs[0].stride() or c.stride(1) != 1 for c in cs):
+        raise ValueError("gemm_grouped: outputs need one row stride and unit column stride")
+    bp = (ctypes.c_void_p * len(bs))(*[b.data_ptr() for b in bs])
+    cp = (ctypes.c_void_p * len(cs))(*[c.data_ptr() for c in cs])
+    call("ghip_gemm_grouped", dtype_code(a.dtype), dtype_code(odt), len(bs), M, N, K, a.data_ptr(),
+         a.stride(0), a.stride(1), bp, bs[0].stride(0), bs[0].stride(1), cp, cs[0].stride(0), _stream(stream))
+    return cs
+
+
 def softmax_axis(x: torch.Tensor, axis: int, log: bool = False, out=None, stream=None) -> torch.Tensor:
     """Softmax (log-softmax) over a middle axis of a contiguous tensor (the column
     kernel: x read as [outer, n, inner])."""

@@ -150,6 +150,19 @@ int ghip_gemm_batched(int ab_dtype, int c_dtype, int64_t batch, int64_t M, int64
                       int64_t sc_b, int64_t sc_m, int64_t sc_n, void* stream,
                       GHipError* err);
 
+/* Several DotGenerals that share the left operand (dotgeneral.go:65-164 once per
+ * product; the projections Q, K, V of an attention block, function.go:2976-3075,
+ * are such a set), in one launch:
+ *   c[g][m, n] = sum_k a[m, k] * b[g][k, n],   g < groups (1 .. 4)
+ * with one set of element strides for a, for every b[g] and every c[g] (unit n
+ * stride).  Each c[g] equals what ghip_gemm_batched gives for that product alone
+ * (the same kernel core and summation order).  16-bit a / b with a K-contiguous
+ * and every b[g] N-contiguous run as one grid of groups x tiles workgroups; other
+ * layouts and dtypes run product by product. */
+int ghip_gemm_grouped(int ab_dtype, int c_dtype, int groups, int64_t M, int64_t N, int64_t K,
+                      const void* a, int64_t sa_m, int64_t sa_k, const void* const* b, int64_t sb_k,
+                      int64_t sb_n, void* const* c, int64_t sc_m, void* stream, GHipError* err);
+
 /* Fused attention forward, the one-kernel lowering of
  * Function.FusedScaledDotProductAttention (function.go:2669-2907; the composite
  * it replaces is DotGeneral -> scale -> causal Where -> FusedSoftmax -> DotGeneral,

@@ -235,3 +235,44 @@ def test_gelu_both_operands_mn_contiguous(be, rows, cols, k):
     # the chain's result exactly, except where the fp32-accumulated product rounds
     # to the other bf16 neighbour of the fp64 one
     assert np.mean((got == lo) | (got == hi)) >= 0.95
+
+
+def test_grouped_projections_equal_separate(be):
+    """Three DotGenerals sharing x (the Q, K, V projections of a block) compile to
+    one grouped launch (gemm_grouped G=3) whose outputs equal the stand-alone GEMMs
+    (GHIP_DOT_GROUPING=0) bit for bit; a fourth Dot on x with an elementwise user
+    stays outside the group (it is the residual epilogue's)."""
+    M, D = 2048, 1024
+    x, sx = _bf16_in(5101, (M, D), std=0.5)
+    ws = [_bf16_in(5102 + i, (D, D), std=0.03) for i in range(4)]
+    r, sr = _bf16_in(5110, (M, D))
+
+    def build(f, xx, w0, w1, w2, w3, rr):
+        dots = [graphs.dense(f, xx, w) for w in (w0, w1, w2)]
+        return dots + [f.Add(rr, graphs.dense(f, xx, w3))]
+
+    inputs = [(x, sx)] + ws + [(r, sr)]
+    outs = {}
+    for grouping in ("1", "0"):
+        old = os.environ.get("GHIP_DOT_GROUPING")
+        os.environ["GHIP_DOT_GROUPING"] = grouping
+        try:
+            plan, out = _compile_run(be, build, inputs, True)
+        finally:
+            if old is None:
+                del os.environ["GHIP_DOT_GROUPING"]
+            else:
+                os.environ["GHIP_DOT_GROUPING"] = old
+        outs[grouping] = out
+        if grouping == "1":
+            assert plan.count("gemm_grouped bfloat16 G=3") == 1 and "gemm_batched+epilogue" in plan, plan
+        else:
+            assert "gemm_grouped" not in plan and plan.count("gemm_batched bfloat16") == 3, plan
+    for (dt_g, a), (dt_s, b) in zip(outs["1"], outs["0"]):
+        assert dt_g == dt_s and np.array_equal(a.view(np.uint8), b.view(np.uint8))
+    for i in range(3):
+        y = synth.bf16_bits_to_f32(outs["1"][i][1])
+        rows = np.arange(0, M, 97)
+        ref = orc.dot_general(x[rows], [1], [], ws[i][0], [0], [])
+        assert rel_err(y[rows], ref) <= 1e-2
+

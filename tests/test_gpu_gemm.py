@@ -284,3 +284,35 @@ def test_empty_and_k0(cuda):
     b = torch.empty((1, 0, 8), device=cuda)
     c = ops.gemm(a, b)
     assert torch.count_nonzero(c).item() == 0
+
+
+@pytest.mark.parametrize("G,M,N,K", [(3, 2048, 2048, 1024), (2, 2000, 2056, 520), (4, 1032, 2312, 200),
+                                     (3, 300, 264, 72), (2, 256, 256, 40)])
+@pytest.mark.parametrize("dt,odt", [(torch.bfloat16, torch.bfloat16), (torch.float16, torch.float16),
+                                    (torch.bfloat16, torch.float32)])
+def test_gemm_grouped_equals_separate(cuda, G, M, N, K, dt, odt):
+    """ghip_gemm_grouped: G products sharing A in one launch (>= 128 tiles of 256 x
+    256: the grouped 4-wave grid; fewer: one dispatch per product) equal the
+    stand-alone ghip_gemm_batched results bit for bit, ragged M, N and K included;
+    plus sampled entries of every product against fp64."""
+    a = synth.normal_device(3901 + M, (M, K), std=0.125, device=cuda, dtype=dt)
+    bs = [synth.normal_device(3902 + g, (K, N), std=0.125, device=cuda, dtype=dt) for g in range(G)]
+    got = ops.gemm_grouped(a, bs, out_dtype=odt)
+    torch.cuda.synchronize()
+    for g in range(G):
+        ref_c = ops.gemm(a, bs[g], out_dtype=odt)
+        assert torch.equal(got[g], ref_c), f"product {g} differs from the stand-alone GEMM"
+        s_got, s_ref = _sampled_check(a[None], bs[g][None], got[g][None], count=1024, seed=20 + g)
+        assert rel_err(s_got, s_ref) <= (1e-4 if odt == torch.float32 else 1e-2)
+
+
+def test_gemm_grouped_f32_and_rejects(cuda):
+    """fp32 operands run product by product (equal to the batched entry); groups
+    outside 1..4 are rejected."""
+    a = synth.normal_device(3911, (300, 130), device=cuda)
+    bs = [synth.normal_device(3912 + g, (130, 270), device=cuda) for g in range(3)]
+    got = ops.gemm_grouped(a, bs)
+    for g in range(3):
+        assert torch.equal(got[g], ops.gemm(a, bs[g]))
+    with pytest.raises(Exception):
+        ops.gemm_grouped(a, bs + bs)  # 6 groups

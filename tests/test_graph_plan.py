@@ -243,10 +243,10 @@ def test_transformer_block_plan(be, monkeypatch):
     e = graphs.transformer_block(be, cfg)
     p = e.Plan()
     assert p.count("rmsnorm_rows") == 2
-    # Q, K, V stay plain GEMMs, attention (head dim 64) is one fused kernel; the
-    # residual adds and SiLU(gate) * up run as GEMM epilogues (gate and up in one
-    # kernel).
-    assert p.count("gemm_batched bfloat16") == 3
+    # Q, K, V are one grouped launch (three products sharing the normed x),
+    # attention (head dim 64) is one fused kernel; the residual adds and
+    # SiLU(gate) * up run as GEMM epilogues (gate and up in one kernel).
+    assert p.count("gemm_grouped bfloat16 G=3") == 1 and "gemm_batched bfloat16" not in p
     assert p.count("sdpa_fwd bfloat16") == 1 and "causal=1 mask=none (fused attention)" in p
     assert p.count("gemm_batched+epilogue") == 3 and p.count("dots=2") == 1
     assert "fused_elementwise" not in p
@@ -254,16 +254,20 @@ def test_transformer_block_plan(be, monkeypatch):
     c96 = graphs.TransformerBlockConfig(batch=2, seq=64, vocab=100, d_model=192, heads=2, head_dim=96, ffn=256)
     p96 = graphs.transformer_block(be, c96).Plan()
     assert "sdpa_fwd bfloat16" in p96 and "D=96 causal=1 mask=none (fused attention)" in p96
-    assert "scale_mask_softmax_rows" not in p96 and p96.count("gemm_batched bfloat16") == 3
+    assert "scale_mask_softmax_rows" not in p96 and p96.count("gemm_grouped bfloat16 G=3") == 1
     # head dim 100 (not a multiple of 8) has no fused kernel: GEMM, scale + causal
     # softmax, GEMM
     c100 = graphs.TransformerBlockConfig(batch=2, seq=64, vocab=100, d_model=200, heads=2, head_dim=100, ffn=256)
     p100 = graphs.transformer_block(be, c100).Plan()
     assert "sdpa_fwd" not in p100 and "scale_mask_softmax_rows" in p100 and "causal=1" in p100
-    assert p100.count("gemm_batched bfloat16") == 5
+    assert p100.count("gemm_batched bfloat16") == 2 and p100.count("gemm_grouped bfloat16 G=3") == 1
     monkeypatch.setenv("GHIP_EPILOGUE_FUSION", "0")
     u = graphs.transformer_block(be, cfg).Plan()
-    assert u.count("gemm_batched bfloat16") == 7 and "gemm_batched+epilogue" not in u
+    assert u.count("gemm_batched bfloat16") == 4 and "gemm_batched+epilogue" not in u
+    assert u.count("gemm_grouped bfloat16 G=3") == 1
+    monkeypatch.setenv("GHIP_DOT_GROUPING", "0")
+    g0 = graphs.transformer_block(be, cfg).Plan()
+    assert g0.count("gemm_batched bfloat16") == 7 and "gemm_grouped" not in g0
     assert u.count("fused_elementwise") == 3
     assert "gather_rows" in p
     assert e.Outputs()[0].dims == (2, 64, 128)
