@@ -262,10 +262,15 @@ int launch_reduce(int dtype, int op, const void* src, const ReduceDesc& d, void*
 // ---------------------------------------------------------------------------
 // Row gather with int32 / int64 ids (the public ghip_gather_rows takes int32).
 // ---------------------------------------------------------------------------
+// One wave per output row.  A wave issues the loads of up to 4 vectors per lane
+// (a 4 KiB bf16 row of 2048 values at 16-byte vectors) before their stores, so a
+// row's reads are in flight together.  ids and n are the first kernel arguments
+// (preloaded into SGPRs, -amdgpu-kernarg-preload-count for this file): the id
+// load, on which every row load depends, is issued without a kernel-argument fetch.
 template <typename V, typename I>
-__global__ __launch_bounds__(256) void gather_any_kernel(const V* __restrict__ table, int64_t nrows,
-                                                         int64_t row_vecs, const I* __restrict__ ids,
-                                                         int64_t n, V* __restrict__ out) {
+__global__ __launch_bounds__(256) void gather_any_kernel(const I* __restrict__ ids, int64_t n,
+                                                         const V* __restrict__ table, int64_t nrows,
+                                                         int64_t row_vecs, V* __restrict__ out) {
   const int64_t r = static_cast<int64_t>(blockIdx.x) * 4 + threadIdx.x / 64;
   if (r >= n) return;
   const int lane = threadIdx.x % 64;
@@ -273,7 +278,15 @@ __global__ __launch_bounds__(256) void gather_any_kernel(const V* __restrict__ t
   id = id < 0 ? 0 : (id > nrows - 1 ? nrows - 1 : id);
   const V* srcp = table + id * row_vecs;
   V* dstp = out + r * row_vecs;
-  for (int64_t c = lane; c < row_vecs; c += 64) dstp[c] = srcp[c];
+  int64_t c0 = 0;
+  for (; c0 + 4 * 64 <= row_vecs; c0 += 4 * 64) {
+    const V a0 = srcp[c0 + lane], a1 = srcp[c0 + 64 + lane], a2 = srcp[c0 + 128 + lane], a3 = srcp[c0 + 192 + lane];
+    dstp[c0 + lane] = a0;
+    dstp[c0 + 64 + lane] = a1;
+    dstp[c0 + 128 + lane] = a2;
+    dstp[c0 + 192 + lane] = a3;
+  }
+  for (int64_t c = c0 + lane; c < row_vecs; c += 64) dstp[c] = srcp[c];
 }
 
 template <typename I>
@@ -282,11 +295,14 @@ static hipError_t gather_t(const void* table, int64_t V_, int64_t row_bytes, con
   const unsigned grid = static_cast<unsigned>((n + 3) / 4);
   auto al = [](const void* p, unsigned a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; };
   if (row_bytes % 16 == 0 && al(table, 16) && al(out, 16))
-    hipLaunchKernelGGL((gather_any_kernel<uint4, I>), dim3(grid), dim3(256), 0, s, (const uint4*)table, V_, row_bytes / 16, ids, n, (uint4*)out);
+    hipLaunchKernelGGL((gather_any_kernel<uint4, I>), dim3(grid), dim3(256), 0, s, ids, n, (const uint4*)table, V_,
+                       row_bytes / 16, (uint4*)out);
   else if (row_bytes % 4 == 0 && al(table, 4) && al(out, 4))
-    hipLaunchKernelGGL((gather_any_kernel<uint32_t, I>), dim3(grid), dim3(256), 0, s, (const uint32_t*)table, V_, row_bytes / 4, ids, n, (uint32_t*)out);
+    hipLaunchKernelGGL((gather_any_kernel<uint32_t, I>), dim3(grid), dim3(256), 0, s, ids, n, (const uint32_t*)table,
+                       V_, row_bytes / 4, (uint32_t*)out);
   else
-    hipLaunchKernelGGL((gather_any_kernel<uint8_t, I>), dim3(grid), dim3(256), 0, s, (const uint8_t*)table, V_, row_bytes, ids, n, (uint8_t*)out);
+    hipLaunchKernelGGL((gather_any_kernel<uint8_t, I>), dim3(grid), dim3(256), 0, s, ids, n, (const uint8_t*)table, V_,
+                       row_bytes, (uint8_t*)out);
   return hipGetLastError();
 }
 

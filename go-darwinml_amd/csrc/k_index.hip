@@ -1,30 +1,13 @@
-// Integer / indexing kernels: embedding gather, argmin/argmax, iota.
+// Integer / indexing kernels: argmin/argmax, iota, and the embedding-gather entry
+// point (its kernel is the graph Gather's, in k_generic.hip).
 // All three are bit-exact by construction (copies and integer arithmetic).
 #include <limits>
 #include <type_traits>
 
 #include "common.h"
+#include "graph.h"
 
 namespace ghip {
-
-// ---------------------------------------------------------------------------
-// Embedding gather: out[i] = table[clamp(ids[i])], one wave per output row,
-// 16-byte accesses when the row size and both base pointers allow it.
-// ---------------------------------------------------------------------------
-template <typename V>
-__global__ __launch_bounds__(256) void gather_rows_kernel(const V* __restrict__ table, int64_t nrows,
-                                                          int64_t row_vecs,
-                                                          const int32_t* __restrict__ ids, int64_t n,
-                                                          V* __restrict__ out) {
-  const int64_t r = static_cast<int64_t>(blockIdx.x) * 4 + threadIdx.x / kWave;
-  if (r >= n) return;
-  const int lane = threadIdx.x % kWave;
-  int64_t id = ids[r];
-  id = id < 0 ? 0 : (id > nrows - 1 ? nrows - 1 : id);
-  const V* src = table + id * row_vecs;
-  V* dst = out + r * row_vecs;
-  for (int64_t c = lane; c < row_vecs; c += kWave) dst[c] = src[c];
-}
 
 // ---------------------------------------------------------------------------
 // ArgMin / ArgMax along the middle axis of [outer, n, inner].
@@ -151,24 +134,9 @@ extern "C" int ghip_gather_rows(const void* table, int64_t V, int64_t row_bytes,
                      (long long)V, (long long)row_bytes, (long long)n);
   if (n == 0) return GHIP_OK;
   if (!table || !ids || !out) return set_error(err, GHIP_ERR_INVALID_ARG, "gather_rows: null pointer");
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  const unsigned grid = blocks_for(n, 4);
-  auto al = [](const void* p, unsigned a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; };
-  if (row_bytes % 16 == 0 && al(table, 16) && al(out, 16)) {
-    hipLaunchKernelGGL(gather_rows_kernel<uint4>, dim3(grid), dim3(256), 0, s,
-                       static_cast<const uint4*>(table), V, row_bytes / 16, ids, n,
-                       static_cast<uint4*>(out));
-  } else if (row_bytes % 4 == 0 && al(table, 4) && al(out, 4)) {
-    hipLaunchKernelGGL(gather_rows_kernel<uint32_t>, dim3(grid), dim3(256), 0, s,
-                       static_cast<const uint32_t*>(table), V, row_bytes / 4, ids, n,
-                       static_cast<uint32_t*>(out));
-  } else {
-    hipLaunchKernelGGL(gather_rows_kernel<uint8_t>, dim3(grid), dim3(256), 0, s,
-                       static_cast<const uint8_t*>(table), V, row_bytes, ids, n,
-                       static_cast<uint8_t*>(out));
-  }
-  GHIP_CHECK(hipGetLastError(), err);
-  return GHIP_OK;
+  // The graph's Gather kernel (k_generic.hip): one wave per row, clamped ids.
+  return launch_gather_rows(table, V, row_bytes, ids, GHIP_DTYPE_INT32, n, out, static_cast<hipStream_t>(stream),
+                            err);
 }
 
 template <typename T, typename O>
