@@ -501,3 +501,36 @@ def test_pad_and_logical_reduce_shapes():
     assert f.OpShape(f.ReduceLogicalOr(bl)).dtype == dtypes.Bool
     with pytest.raises(BackendError, match="bool operand required"):
         f.ReduceLogicalOr(x)
+
+
+def test_dot_grouping_rule(be):
+    """DotGenerals sharing a left operand run as one grouped launch when none feeds
+    an elementwise op (which may absorb it as a GEMM epilogue), they fold without
+    copies, and their right operands are leaves; the rest stay separate steps."""
+    sx, sw = make_shape(BF16, 512, 256), make_shape(BF16, 256, 384)
+    dense = graphs.dense
+    # three plain products + one feeding an Add: G=3 and a fused epilogue
+    p = _plan(be, lambda f, x, a, b, c, d, r: [dense(f, x, a), dense(f, x, b), dense(f, x, c),
+                                                f.Add(r, dense(f, x, d))],
+              [sx, sw, sw, sw, sw, make_shape(BF16, 512, 384)])
+    assert p.count("gemm_grouped bfloat16 G=3 M=512 N=384 K=256") == 1 and "gemm_batched+epilogue" in p, p
+    # a right operand computed from another product's output is not a leaf: that
+    # product runs alone, the other two are grouped
+    def chained(f, x, a, b):
+        y = dense(f, x, a)
+        return [y, dense(f, x, b), dense(f, x, f.Slice(y, [0, 0], [256, 384], [1, 1]))]
+    p = _plan(be, chained, [sx, sw, sw])
+    assert p.count("gemm_grouped bfloat16 G=2") == 1 and p.count("gemm_batched bfloat16") == 1, p
+    w_sq = make_shape(BF16, 256, 256)
+    p = _plan(be, lambda f, x, a, b: [dense(f, x, a), dense(f, x, f.Mul(b, b))], [sx, w_sq, w_sq])
+    assert "gemm_grouped" not in p and p.count("gemm_batched bfloat16") == 2, p
+    # different right-operand layouts (one transposed view): separate
+    p = _plan(be, lambda f, x, a, b: [dense(f, x, a), f.DotGeneral(x, [1], [], b, [1], [])], [sx, w_sq, w_sq])
+    assert "gemm_grouped" not in p and p.count("gemm_batched bfloat16") == 2, p
+    # fp32 products: not grouped (the grouped core is the 16-bit one)
+    p = _plan(be, lambda f, x, a, b: [dense(f, x, a), dense(f, x, b)],
+              [make_shape(F32, 512, 256), make_shape(F32, 256, 384), make_shape(F32, 256, 384)])
+    assert "gemm_grouped" not in p and p.count("gemm_batched float32") == 2, p
+    # more than four siblings: groups of at most four
+    p = _plan(be, lambda f, x, *ws: [dense(f, x, w) for w in ws], [sx] + [sw] * 6)
+    assert p.count("gemm_grouped bfloat16 G=4") == 1 and p.count("gemm_grouped bfloat16 G=2") == 1, p
