@@ -24,12 +24,14 @@
 //   * K / V tiles arrive by buffer_load ... lds (16 B per lane; keys past Sk lie
 //     beyond the buffer descriptor's extent and read zeros) into one 32 KiB LDS
 //     stage per workgroup, XOR-swizzled so the ds_read_b128 (K) and transpose
-//     reads (V) are bank-conflict free.  Each tile is loaded at its start and
-//     waited for before its first LDS read, so the DMA's LDS writes never compete
-//     with the tile's reads; the other workgroups resident on the CU (up to five at
-//     32 KiB of LDS; two at the D = 128 kernels' 168-206 VGPRs) compute meanwhile.
-//     Against a two-stage prefetch in one process this measured 0-2.5% faster, and
-//     letting the prefetch run under the reads 2.5% slower than waiting for it;
+//     reads (V) are bank-conflict free.  Two schedules: (plain) each tile's K and
+//     V are loaded at its start and waited for before its first LDS read, the
+//     other workgroups resident on the CU (three at the D = 128 kernel's 168
+//     VGPRs) computing meanwhile; (split, unmasked) V_t loads while the scores of
+//     tile t are computed and K_{t+1} while P V of tile t is, in the same 32 KiB,
+//     at three barriers a tile instead of two: 4% faster at B4 H16 S2048 causal,
+//     6-7% at longer or non-causal shapes, 6% slower when every causal workgroup
+//     is short (<= 16 key tiles: the block's S1024), where the plain one is used;
 //   * the output rescale of the online softmax is lazy: the reference max moves
 //     only when a tile's max exceeds it by more than 2^8 (exponents stay <= 2^8);
 //   * causal: tiles past a workgroup's last query are never loaded, a wave skips
@@ -181,7 +183,10 @@ __device__ __forceinline__ float dot2_ones(uint32_t w, float acc) {
 // beyond the buffer's extent) and Q's are zero, so they add nothing to the scores
 // and their output columns are not stored.  The MFMAs still run over the full DP
 // (no branch in the tile loop: at D = DP the loop is exactly the unpadded one).
-template <int DP, bool F16, int MK>
+// SPLIT: the split K / V load schedule (below); the host picks it unless the
+// mask is causal and no workgroup has more than 16 key tiles, where the plain
+// schedule measured faster (short workgroups).
+template <int DP, bool F16, int MK, bool SPLIT>
 __global__ __launch_bounds__(256, DP >= 256 ? 1 : 2) void sdpa_fwd_kernel(Params p) {
   constexpr int NCH = DP / 8;  // 16-byte chunks per key row
   constexpr int NDMA = kBKV * DP * 2 / 1024 / kWaves;  // DMA instructions per wave per K (or V) tile
@@ -252,6 +257,20 @@ __global__ __launch_bounds__(256, DP >= 256 ? 1 : 2) void sdpa_fwd_kernel(Params
 #pragma unroll
     for (int i = 0; i < NDMA; ++i) dma16(rv, lv + i * 1024, voff[i]);
   };
+  auto issue_k = [&](int t) {
+    const uint32_t dk = static_cast<uint32_t>(t) * kstep;
+    const i32x4_t rk = make_rsrc(reinterpret_cast<const char*>(Kb) + dk, p.k_extent - dk);
+    const uint32_t lk = lds0 + wave * NDMA * 1024;
+#pragma unroll
+    for (int i = 0; i < NDMA; ++i) dma16(rk, lk + i * 1024, koff[i]);
+  };
+  auto issue_v = [&](int t) {
+    const uint32_t dv = static_cast<uint32_t>(t) * vstep;
+    const i32x4_t rv = make_rsrc(reinterpret_cast<const char*>(Vb) + dv, p.v_extent - dv);
+    const uint32_t lv = lds0 + kBKV * DP * 2 + wave * NDMA * 1024;
+#pragma unroll
+    for (int i = 0; i < NDMA; ++i) dma16(rv, lv + i * 1024, voff[i]);
+  };
 
   f32x16_t o[DP / 32];
 #pragma unroll
@@ -293,17 +312,10 @@ __global__ __launch_bounds__(256, DP >= 256 ? 1 : 2) void sdpa_fwd_kernel(Params
     }
   };
 
-  // Two barriers per tile: the first once every wave has finished reading tile
-  // t-1 (the stage may be refilled), the second once tile t has landed.
-  auto tile = [&](int t, int st) {
-    __syncthreads();
-    issue(t, st);
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
+  // Scores, softmax and the P^T operand of tile t (keys t * 64 ..) from the K tile
+  // in LDS; the caller has checked that the wave has keys to process there.
+  auto scores = [&](int t, bf16x8_t (&pb)[4]) {
     const int key0 = t * kBKV;
-    // Causal: a wave whose last query precedes the tile's first key has nothing to
-    // do here (it still takes part in the barriers and loads).
-    if (p.causal && key0 > qw + kQW - 1) return;
     // The mask terms of this tile, fetched before the MFMAs so their latency
     // overlaps them.
     float mk[2][16];
@@ -313,8 +325,7 @@ __global__ __launch_bounds__(256, DP >= 256 ? 1 : 2) void sdpa_fwd_kernel(Params
 #pragma unroll
         for (int g = 0; g < 4; ++g) mask_group(key0 + 32 * kb + 4 * h2 + 8 * g, &mk[kb][4 * g]);
     }
-    const uint16_t* sk = &smem[st][0][0];
-    const uint16_t* sv = &smem[st][1][0];
+    const uint16_t* sk = &smem[0][0][0];
     f32x16_t s0, s1;
 #pragma unroll
     for (int v = 0; v < 16; ++v) {
@@ -390,22 +401,72 @@ __global__ __launch_bounds__(256, DP >= 256 ? 1 : 2) void sdpa_fwd_kernel(Params
       ls1 = dot2_ones<F16>(pw[2 * i + 1], ls1);
     }
     l += ls0 + ls1;
-    bf16x8_t pb[4];
 #pragma unroll
     for (int k = 0; k < 4; ++k)
       pb[k] = __builtin_bit_cast(bf16x8_t, make_uint4(pw[4 * k], pw[4 * k + 1], pw[4 * k + 2], pw[4 * k + 3]));
+  };
+  // O^T += V^T P^T over the V tile in LDS.
+  auto pv = [&](const bf16x8_t (&pb)[4]) {
+    const uint16_t* sv = &smem[0][1][0];
 #pragma unroll
     for (int s = 0; s < kBKV / 16; ++s)
 #pragma unroll
       for (int db = 0; db < DP / 32; ++db) o[db] = mma<F16>(frag_v<DP>(sv, db, s, lane), pb[s], o[db]);
-    // The stage's LDS reads complete before the next barrier, after which it is
-    // refilled.
-    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
   };
+  // Causal: a wave whose last query precedes tile t's first key has nothing to do
+  // there (it still takes part in the barriers and loads).
+  auto skip = [&](int t) { return p.causal && t * kBKV > qw + kQW - 1; };
 
-  for (int t = 0; t < ntiles; t += 2) {
-    tile(t, 0);
-    if (t + 1 < ntiles) tile(t + 1, 0);
+  if constexpr (!SPLIT) {
+    // Two barriers per tile: the first once every wave has finished reading tile
+    // t-1 (the stage may be refilled), the second once tile t has landed.
+    auto tile = [&](int t) {
+      __syncthreads();
+      issue(t, 0);
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      __syncthreads();
+      if (!skip(t)) {
+        bf16x8_t pb[4];
+        scores(t, pb);
+        pv(pb);
+      }
+      // The stage's LDS reads complete before the next barrier, after which it is
+      // refilled.
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    };
+    for (int t = 0; t < ntiles; t += 2) {
+      tile(t);
+      if (t + 1 < ntiles) tile(t + 1);
+    }
+  } else {
+    // K and V load separately, each under the other half of the tile: V_t during
+    // the scores of tile t, K_{t+1} during P V of tile t (three barriers a tile; the
+    // first tile's K and V are both issued up front).  vmcnt counts this wave's
+    // DMA instructions in issue order: NDMA of them per K or V tile.
+    constexpr int kWaitOneTile = NDMA | (7 << 4) | (15 << 8);  // vmcnt(NDMA), other counters not waited
+    static_assert(NDMA < 16, "vmcnt immediate");
+    issue_k(0);
+    issue_v(0);
+    for (int t = 0; t < ntiles; ++t) {
+      if (t == 0) __builtin_amdgcn_s_waitcnt(kWaitOneTile);  // K_0 landed (V_0 may be in flight)
+      else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // K_t landed
+      __syncthreads();  // K_t visible; every wave done with P V of tile t-1
+      if (t > 0) issue_v(t);
+      bf16x8_t pb[4];
+      const bool sk = skip(t);
+      if (!sk) scores(t, pb);
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      __syncthreads();  // every wave done reading K_t
+      if (t + 1 < ntiles) {
+        issue_k(t + 1);
+        __builtin_amdgcn_s_waitcnt(kWaitOneTile);  // V_t landed, K_{t+1} in flight
+      } else {
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      }
+      __syncthreads();  // V_t visible
+      if (!sk) pv(pb);
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    }
   }
 
   // o[db][v] is d = 32 db + (v/4)*8 + 4 h2 + v%4 of query qi.  A query whose keys
@@ -430,11 +491,20 @@ __global__ __launch_bounds__(256, DP >= 256 ? 1 : 2) void sdpa_fwd_kernel(Params
   }
 }
 
+template <int DP, bool F16, bool SPLIT>
+static void launch_dm(const Params& p, int mk, dim3 grid, hipStream_t s) {
+  static_assert(!SPLIT, "masked kernels use the plain schedule");
+  if (mk == kBoolMask) hipLaunchKernelGGL((sdpa_fwd_kernel<DP, F16, kBoolMask, SPLIT>), grid, dim3(256), 0, s, p);
+  else if (mk == kAddMask) hipLaunchKernelGGL((sdpa_fwd_kernel<DP, F16, kAddMask, SPLIT>), grid, dim3(256), 0, s, p);
+  else hipLaunchKernelGGL((sdpa_fwd_kernel<DP, F16, kNoMask, SPLIT>), grid, dim3(256), 0, s, p);
+}
+// The split schedule only without a mask: with one, the compiler's waits for the
+// mask loads also wait for the K / V DMA (vmcnt counts both in issue order), and
+// the masked variants would spill at the extra barrier.
 template <int DP, bool F16>
-static void launch_d(const Params& p, int mk, dim3 grid, hipStream_t s) {
-  if (mk == kBoolMask) hipLaunchKernelGGL((sdpa_fwd_kernel<DP, F16, kBoolMask>), grid, dim3(256), 0, s, p);
-  else if (mk == kAddMask) hipLaunchKernelGGL((sdpa_fwd_kernel<DP, F16, kAddMask>), grid, dim3(256), 0, s, p);
-  else hipLaunchKernelGGL((sdpa_fwd_kernel<DP, F16, kNoMask>), grid, dim3(256), 0, s, p);
+static void launch_d(const Params& p, int mk, dim3 grid, bool split, hipStream_t s) {
+  if (split && mk == kNoMask) hipLaunchKernelGGL((sdpa_fwd_kernel<DP, F16, kNoMask, true>), grid, dim3(256), 0, s, p);
+  else launch_dm<DP, F16, false>(p, mk, grid, s);
 }
 
 
@@ -748,19 +818,24 @@ extern "C" int ghip_sdpa_fwd_masked(int dtype, const void* q, const void* k, con
   const dim3 grid(static_cast<unsigned>(nqb * B * H));
   const hipStream_t s = static_cast<hipStream_t>(stream);
   const bool f16 = dtype == GHIP_DTYPE_FLOAT16;
+  // Key tiles of the longest workgroup: the split K / V schedule (no mask) unless
+  // causal workgroups are all short (<= 16 tiles: B8 H16 S1024 measured 6% faster
+  // with the plain schedule, S2048 4% and S4096 / S8192 6-7% slower).
+  const int64_t kv_max = causal ? std::min<int64_t>(Sk, nqb * attn::kBQ) : Sk;
+  const bool split = !causal || (kv_max + attn::kBKV - 1) / attn::kBKV > 16;
   // The smallest padded width that holds D.
   if (f32) {
     if (D <= 64) attn::launch_f32<64>(p, mk, grid, s);
     else attn::launch_f32<128>(p, mk, grid, s);
   } else if (D <= 64) {
-    if (f16) attn::launch_d<64, true>(p, mk, grid, s);
-    else attn::launch_d<64, false>(p, mk, grid, s);
+    if (f16) attn::launch_d<64, true>(p, mk, grid, split, s);
+    else attn::launch_d<64, false>(p, mk, grid, split, s);
   } else if (D <= 128) {
-    if (f16) attn::launch_d<128, true>(p, mk, grid, s);
-    else attn::launch_d<128, false>(p, mk, grid, s);
+    if (f16) attn::launch_d<128, true>(p, mk, grid, split, s);
+    else attn::launch_d<128, false>(p, mk, grid, split, s);
   } else {
-    if (f16) attn::launch_d<256, true>(p, mk, grid, s);
-    else attn::launch_d<256, false>(p, mk, grid, s);
+    if (f16) attn::launch_d<256, true>(p, mk, grid, split, s);
+    else attn::launch_d<256, false>(p, mk, grid, split, s);
   }
   GHIP_CHECK(hipGetLastError(), err);
   return GHIP_OK;

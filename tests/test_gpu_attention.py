@@ -55,6 +55,7 @@ CASES = [  # (B, H, Hkv, Sq, Sk, causal)
     (1, 2, 1, 64, 300, True),      # causal with Sk > Sq (top-left aligned mask)
     (1, 1, 1, 1, 1, True),
     (2, 3, 3, 1, 70, False),       # single query row
+    (1, 2, 2, 1100, 1100, True),   # causal with > 16 key tiles (the split K / V schedule), ragged
 ]
 
 
