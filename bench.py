@@ -407,7 +407,7 @@ def make_cases(only=None):
         return Case("attention_bf16", lambda i: ops.sdpa(q, k, v, D ** -0.5, True, out=o),
                     flops_per_step=2 * 2 * B * H * S * S * D, bound="mfma",
                     executed_flops_per_step=2 * 2 * B * H * D * S * (S + 1) // 2,
-                    peak=BF16_PEAK_TFLOPS, dtype="bf16", kernel="sdpa_fwd_kernel<128, false, 0>", cpu=leg,
+                    peak=BF16_PEAK_TFLOPS, dtype="bf16", kernel="sdpa_fwd_kernel<128, false, 0, true>", cpu=leg,
                     config={"workload": "SDPA causal B4 H16 S2048 D128 bf16 ~ N(0,1), one fused kernel "
                                         "(Q.K^T, scale, causal mask, online softmax, P.V); flops "
                                         "counted for both products over the full S x S matrix, "
