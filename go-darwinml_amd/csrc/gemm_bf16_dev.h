@@ -64,7 +64,7 @@ struct GemmParams {
   int64_t sc_b, sc_m;
   int64_t batch, M, N, K;
   int tiles_m, tiles_n;
-  uint32_t a_extent, b_extent;  // bytes addressable from one batch slice's base
+  uint32_t a_extent, b_extent;  // bytes addressable from one batch slice's base (< 2 GiB)
   int vec_c;                    // C rows allow 4-element vector stores
   const void* b1;               // second right operand (NB = 2), B's strides and extent
   // Grouped launch (4-wave K-contiguous-A core): groups > 0 products A.B_g -> C_g
@@ -72,8 +72,19 @@ struct GemmParams {
   int groups;
   const void* b_g[4];
   void* c_g[4];
+  // Slices of 2 GiB or more (the BIG instantiations): their byte extents.
+  int64_t a_extent64, b_extent64;
 };
 constexpr int kGemmMaxGroups = 4;
+
+// A tile's DMA reads at most 256 rows of an operand (m or n rows of a K-contiguous
+// operand, k rows of an MN-contiguous one) from a descriptor based at the tile and
+// k step, at byte offsets that must stay below 2 GiB; s_mn / s_k are element
+// strides, es the element size.  The operand slice itself may be of any size.
+__host__ __device__ inline bool gemm_rows_fit(int64_t s_mn, int64_t s_k, int64_t es) {
+  const int64_t s = s_mn > s_k ? s_mn : s_k;
+  return s >= 0 && (s * 256 + 256) * es < (int64_t{1} << 31);
+}
 
 // Generated epilogues read up to kEpiMaxIn extra operands, each addressed as
 // in[k] + bb * s_b[k] + m * s_m[k] + n * s_n[k] (elements), and write `out`
@@ -147,6 +158,41 @@ __device__ __forceinline__ i32x4_t make_rsrc(const void* base, uint32_t bytes) {
   r.w = 0x00020000;
   return r;
 }
+
+// Records of a descriptor based `left` bytes before the end of an operand slice:
+// the rest of the slice, capped at kOffOOB.  A slice may span more than 4 GiB; a
+// tile's loads stay below 2 GiB from the descriptor's base (gemm_rows_fit), so
+// the cap cuts nothing a tile reads and a masked lane's kOffOOB still reads zeros.
+__device__ __forceinline__ uint32_t left_bytes(int64_t left) {
+  return left <= 0 ? 0u : left >= static_cast<int64_t>(kOffOOB) ? kOffOOB : static_cast<uint32_t>(left);
+}
+
+// Records of the descriptors a tile bases at its rows and k step, from the bytes
+// of the operand slice left after the tile's base.  Ext32 (BIG = false: slices
+// below 2 GiB) keeps the arithmetic in 32 bits; Ext64 (BIG = true: any slice)
+// subtracts in 64 bits and caps with left_bytes.  They are separate
+// instantiations because Ext64's extra scalar registers made the 32-bit cases'
+// cores spill SGPRs (1.5-9% slower, measured).
+struct Ext32 {
+  uint32_t left;
+  __device__ __forceinline__ Ext32(uint32_t extent, int64_t used) : left(extent - static_cast<uint32_t>(used)) {}
+  __device__ __forceinline__ uint32_t at(int64_t d) const { return left - static_cast<uint32_t>(d); }
+};
+struct Ext64 {
+  int64_t left;
+  __device__ __forceinline__ Ext64(int64_t extent, int64_t used) : left(extent - used) {}
+  __device__ __forceinline__ uint32_t at(int64_t d) const { return left_bytes(left - d); }
+};
+template <bool BIG>
+struct ExtSel {
+  __device__ __forceinline__ static Ext32 a(const GemmParams& p, int64_t used) { return Ext32(p.a_extent, used); }
+  __device__ __forceinline__ static Ext32 b(const GemmParams& p, int64_t used) { return Ext32(p.b_extent, used); }
+};
+template <>
+struct ExtSel<true> {
+  __device__ __forceinline__ static Ext64 a(const GemmParams& p, int64_t used) { return Ext64(p.a_extent64, used); }
+  __device__ __forceinline__ static Ext64 b(const GemmParams& p, int64_t used) { return Ext64(p.b_extent64, used); }
+};
 
 // 16 bytes per lane from buffer offset voff straight into LDS byte address
 // la + lane*16 (la wave-uniform; a 32-bit LDS address, so no generic-pointer
@@ -488,7 +534,7 @@ __device__ __forceinline__ void tile_epilogue(const GemmParams& p, const Epi& ep
 //                                A.B, v1 from A.B1 when NB == 2 (else v1 == v0);
 //                                FULL: the whole tile lies inside the output (no
 //                                column bounds), else columns >= N are ignored.
-template <int BM, int BN, int WM, int WN, bool A_K, bool B_K, int NB, class Epi, bool F16 = false>
+template <int BM, int BN, int WM, int WN, bool A_K, bool B_K, int NB, class Epi, bool F16 = false, bool BIG = false>
 __device__ __forceinline__ void gemm_bf16_body(const GemmParams& p, const Epi& epi) {
   static_assert(NB == 1 || NB == 2, "one or two right operands");
   constexpr int NW = WM * WN;
@@ -516,8 +562,8 @@ __device__ __forceinline__ void gemm_bf16_body(const GemmParams& p, const Epi& e
   const uint16_t* A0 = static_cast<const uint16_t*>(p.a) + bb * p.sa_b + m0 * p.sa_m;
   const uint16_t* B0 = static_cast<const uint16_t*>(p.b) + bb * p.sb_b + n0 * p.sb_n;
   const uint16_t* B1 = static_cast<const uint16_t*>(NB == 2 ? p.b1 : p.b) + bb * p.sb_b + n0 * p.sb_n;
-  const uint32_t a_left0 = p.a_extent - static_cast<uint32_t>(m0 * p.sa_m * 2);
-  const uint32_t b_left0 = p.b_extent - static_cast<uint32_t>(n0 * p.sb_n * 2);
+  const auto a_left0 = ExtSel<BIG>::a(p, m0 * p.sa_m * 2);
+  const auto b_left0 = ExtSel<BIG>::b(p, n0 * p.sb_n * 2);
 
   TA ta;
   TB tb;
@@ -531,8 +577,8 @@ __device__ __forceinline__ void gemm_bf16_body(const GemmParams& p, const Epi& e
   auto issue = [&](int kt, int st) {
     const int64_t k0 = static_cast<int64_t>(kt) * kBK;
     const int k_left = static_cast<int>(p.K - k0 < kBK ? p.K - k0 : kBK);
-    const uint32_t b_left = b_left0 - static_cast<uint32_t>(k0 * p.sb_k * 2);
-    const i32x4_t ra = make_rsrc(A0 + k0 * p.sa_k, a_left0 - static_cast<uint32_t>(k0 * p.sa_k * 2));
+    const uint32_t b_left = b_left0.at(k0 * p.sb_k * 2);
+    const i32x4_t ra = make_rsrc(A0 + k0 * p.sa_k, a_left0.at(k0 * p.sa_k * 2));
     const i32x4_t rb = make_rsrc(B0 + k0 * p.sb_k, b_left);
     const uint32_t la = lds_a + st * (BM * kBK * 2), lb = lds_b + st * (NB * BN * kBK * 2);
     if (mn_full && k_left == kBK) {
@@ -630,7 +676,7 @@ __device__ __forceinline__ void gemm_bf16_body(const GemmParams& p, const Epi& e
 // two-stage core for this layout (K-contiguous rows would fetch half cache lines per
 // 32-deep tile, which is why the other layouts keep 64).  Bit-identical to the other
 // cores: same MFMA, same k order per accumulator.
-template <class Epi, bool F16 = false>
+template <class Epi, bool F16 = false, bool BIG = false>
 __device__ __forceinline__ void gemm_bf16_body4mn(const GemmParams& p, const Epi& epi) {
   constexpr int BM = 256, BN = 256, WM = 2, WN = 2, BK = 32, S = 4;
   constexpr int NW = WM * WN;
@@ -654,8 +700,8 @@ __device__ __forceinline__ void gemm_bf16_body4mn(const GemmParams& p, const Epi
   const int64_t m0 = static_cast<int64_t>(tm) * BM, n0 = static_cast<int64_t>(tn) * BN;
   const uint16_t* A0 = static_cast<const uint16_t*>(p.a) + bb * p.sa_b + m0 * p.sa_m;
   const uint16_t* B0 = static_cast<const uint16_t*>(p.b) + bb * p.sb_b + n0 * p.sb_n;
-  const uint32_t a_left0 = p.a_extent - static_cast<uint32_t>(m0 * p.sa_m * 2);
-  const uint32_t b_left0 = p.b_extent - static_cast<uint32_t>(n0 * p.sb_n * 2);
+  const auto a_left0 = ExtSel<BIG>::a(p, m0 * p.sa_m * 2);
+  const auto b_left0 = ExtSel<BIG>::b(p, n0 * p.sb_n * 2);
 
   TA ta;
   TB tb;
@@ -705,10 +751,10 @@ __device__ __forceinline__ void gemm_bf16_body4mn(const GemmParams& p, const Epi
       const int64_t k0 = static_cast<int64_t>(kt) * BK;
       const int k_left = static_cast<int>(p.K - k0 < BK ? p.K - k0 : BK);
       if (d < TA::kPerWave) {
-        const i32x4_t ra = make_rsrc(A0 + k0 * p.sa_k, a_left0 - static_cast<uint32_t>(k0 * p.sa_k * 2));
+        const i32x4_t ra = make_rsrc(A0 + k0 * p.sa_k, a_left0.at(k0 * p.sa_k * 2));
         ta.template issue_one<FULL>(ra, lds_a + st * kSA, wave, lane, k_left, d);
       } else {
-        const i32x4_t rb = make_rsrc(B0 + k0 * p.sb_k, b_left0 - static_cast<uint32_t>(k0 * p.sb_k * 2));
+        const i32x4_t rb = make_rsrc(B0 + k0 * p.sb_k, b_left0.at(k0 * p.sb_k * 2));
         tb.template issue_one<FULL>(rb, lds_b + st * kSB, wave, lane, k_left, d - TA::kPerWave);
       }
     };
@@ -815,7 +861,7 @@ __device__ __forceinline__ void gemm_bf16_body4mn(const GemmParams& p, const Epi
 // each B stage holds the 128 columns of B, then those of B1, and a wave's 128 x 64
 // sub-tile is 32 columns of each, so the epilogue finds both values of an output in
 // one lane.
-template <class Epi, bool F16 = false, int NP = 1>
+template <class Epi, bool F16 = false, int NP = 1, bool BIG = false>
 __device__ __forceinline__ void gemm_bf16_body8km(const GemmParams& p, const Epi& epi) {
   static_assert(NP == 1 || NP == 2, "one or two right operands");
   constexpr int BM = 256, BN = 256 / NP, WM = 2, WN = 4, BK = 32;  // BN: per product
@@ -844,8 +890,8 @@ __device__ __forceinline__ void gemm_bf16_body8km(const GemmParams& p, const Epi
                                              : static_cast<const uint16_t*>(p.b) + bb * p.sb_b) +
                        n0 * p.sb_n;
   const uint16_t* B1 = static_cast<const uint16_t*>(NP == 2 ? p.b1 : p.b) + bb * p.sb_b + n0 * p.sb_n;
-  const uint32_t a_left0 = p.a_extent - static_cast<uint32_t>(m0 * p.sa_m * 2);
-  const uint32_t b_left0 = p.b_extent - static_cast<uint32_t>(n0 * p.sb_n * 2);
+  const auto a_left0 = ExtSel<BIG>::a(p, m0 * p.sa_m * 2);
+  const auto b_left0 = ExtSel<BIG>::b(p, n0 * p.sb_n * 2);
 
   TA ta;
   TB tb;
@@ -904,7 +950,7 @@ __device__ __forceinline__ void gemm_bf16_body8km(const GemmParams& p, const Epi
       if (j < KS) {
         const int64_t k0 = static_cast<int64_t>(j) * 2 * BK;
         const int k_left = static_cast<int>(p.K - k0 < 2 * BK ? p.K - k0 : 2 * BK);
-        const i32x4_t ra = make_rsrc(A0 + k0 * p.sa_k, a_left0 - static_cast<uint32_t>(k0 * p.sa_k * 2));
+        const i32x4_t ra = make_rsrc(A0 + k0 * p.sa_k, a_left0.at(k0 * p.sa_k * 2));
 #pragma unroll
         for (int d = 0; d < NA; ++d) ta.template issue_one<FULL>(ra, lds_a + (j & 1) * kSA, wave, lane, k_left, d);
       }
@@ -913,7 +959,7 @@ __device__ __forceinline__ void gemm_bf16_body8km(const GemmParams& p, const Epi
       if (t < KT) {
         const int64_t k0 = static_cast<int64_t>(t) * BK;
         const int k_left = static_cast<int>(p.K - k0 < BK ? p.K - k0 : BK);
-        const uint32_t b_left = b_left0 - static_cast<uint32_t>(k0 * p.sb_k * 2);
+        const uint32_t b_left = b_left0.at(k0 * p.sb_k * 2);
         const i32x4_t rb = make_rsrc(B0 + k0 * p.sb_k, b_left);
 #pragma unroll
         for (int d = 0; d < TB::kPerWave; ++d)
@@ -1041,7 +1087,7 @@ __device__ __forceinline__ void mfma_drain_a(f32x4_t (&acc)[FM][FN]) {
 // NP = 2 computes A.B and A.B1 (two products sharing A) on a 256 x (2 x 128) tile,
 // as gemm_bf16_body8km does: each B stage holds 128 columns of B, then those of B1,
 // and a wave's 128 x 128 sub-tile is 64 columns of each.
-template <class Epi, bool F16 = false, int NP = 1>
+template <class Epi, bool F16 = false, int NP = 1, bool BIG = false>
 __device__ __forceinline__ void gemm_bf16_body4km(const GemmParams& p, const Epi& epi) {
   static_assert(NP == 1 || NP == 2, "one or two right operands");
   constexpr int BM = 256, BN = 256 / NP, WM = 2, WN = 2, BK = 32;  // BN: per product
@@ -1072,8 +1118,8 @@ __device__ __forceinline__ void gemm_bf16_body4km(const GemmParams& p, const Epi
                                              : static_cast<const uint16_t*>(p.b) + bb * p.sb_b) +
                        n0 * p.sb_n;
   const uint16_t* B1 = static_cast<const uint16_t*>(NP == 2 ? p.b1 : p.b) + bb * p.sb_b + n0 * p.sb_n;
-  const uint32_t a_left0 = p.a_extent - static_cast<uint32_t>(m0 * p.sa_m * 2);
-  const uint32_t b_left0 = p.b_extent - static_cast<uint32_t>(n0 * p.sb_n * 2);
+  const auto a_left0 = ExtSel<BIG>::a(p, m0 * p.sa_m * 2);
+  const auto b_left0 = ExtSel<BIG>::b(p, n0 * p.sb_n * 2);
 
   TA ta;
   TB tb;
@@ -1126,14 +1172,14 @@ __device__ __forceinline__ void gemm_bf16_body4km(const GemmParams& p, const Epi
     auto dma_a = [&](int j, int d) {  // instruction d of A super-tile j (k 64j ..) into A stage j % 2
       const int64_t k0 = static_cast<int64_t>(j) * 2 * BK;
       const int k_left = static_cast<int>(p.K - k0 < 2 * BK ? p.K - k0 : 2 * BK);
-      const i32x4_t ra = make_rsrc(A0 + k0 * p.sa_k, a_left0 - static_cast<uint32_t>(k0 * p.sa_k * 2));
+      const i32x4_t ra = make_rsrc(A0 + k0 * p.sa_k, a_left0.at(k0 * p.sa_k * 2));
       ta.template issue_one<FULL>(ra, lds_a + (j & 1) * kSA, wave, lane, k_left, d);
     };
     auto dma_b = [&](int t, int d) {  // instruction d of B tile t into B stage t % 4 (d / NBP: product)
       const int64_t k0 = static_cast<int64_t>(t) * BK;
       const int k_left = static_cast<int>(p.K - k0 < BK ? p.K - k0 : BK);
       const uint16_t* Bp = (NP == 2 && d >= NBP) ? B1 : B0;
-      const i32x4_t rb = make_rsrc(Bp + k0 * p.sb_k, b_left0 - static_cast<uint32_t>(k0 * p.sb_k * 2));
+      const i32x4_t rb = make_rsrc(Bp + k0 * p.sb_k, b_left0.at(k0 * p.sb_k * 2));
       tb.template issue_one<FULL>(rb, lds_b + (t & 3) * kSB + (d / NBP) * kSB1, wave, lane, k_left, d % NBP);
     };
     auto issue_a = [&](int j) {
@@ -1250,7 +1296,7 @@ __device__ __forceinline__ void gemm_bf16_body4km(const GemmParams& p, const Epi
 // K-contiguous layouts (and 4-6% on [8192,2048].[2048,2048]), 4-5% faster than the
 // 8-wave 32x32x16 64-deep core for two products and heavy epilogues, 4% slower than
 // the 4-wave 32-deep core when both operands are MN-contiguous.
-template <bool A_K, bool B_K, class Epi, bool F16 = false, int NP = 1>
+template <bool A_K, bool B_K, class Epi, bool F16 = false, int NP = 1, bool BIG = false>
 __device__ __forceinline__ void gemm_bf16_body8x(const GemmParams& p, const Epi& epi) {
   static_assert(NP == 1 || NP == 2, "one or two right operands");
   constexpr int BM = 256, BN = 256 / NP, WM = 2, WN = 4, BK = kBK;
@@ -1276,8 +1322,8 @@ __device__ __forceinline__ void gemm_bf16_body8x(const GemmParams& p, const Epi&
                                              : static_cast<const uint16_t*>(p.b) + bb * p.sb_b) +
                        n0 * p.sb_n;
   const uint16_t* B1 = static_cast<const uint16_t*>(NP == 2 ? p.b1 : p.b) + bb * p.sb_b + n0 * p.sb_n;
-  const uint32_t a_left0 = p.a_extent - static_cast<uint32_t>(m0 * p.sa_m * 2);
-  const uint32_t b_left0 = p.b_extent - static_cast<uint32_t>(n0 * p.sb_n * 2);
+  const auto a_left0 = ExtSel<BIG>::a(p, m0 * p.sa_m * 2);
+  const auto b_left0 = ExtSel<BIG>::b(p, n0 * p.sb_n * 2);
 
   TA ta;
   TB tb;
@@ -1353,10 +1399,10 @@ __device__ __forceinline__ void gemm_bf16_body8x(const GemmParams& p, const Epi&
     auto issue = [&](int kt, int st) {
       const int64_t k0 = static_cast<int64_t>(kt) * BK;
       const int k_left = static_cast<int>(p.K - k0 < BK ? p.K - k0 : BK);
-      const i32x4_t ra = make_rsrc(A0 + k0 * p.sa_k, a_left0 - static_cast<uint32_t>(k0 * p.sa_k * 2));
+      const i32x4_t ra = make_rsrc(A0 + k0 * p.sa_k, a_left0.at(k0 * p.sa_k * 2));
 #pragma unroll
       for (int d = 0; d < TA::kPerWave; ++d) ta.template issue_one<FULL>(ra, lds_a + st * kSA, wave, lane, k_left, d);
-      const uint32_t b_left = b_left0 - static_cast<uint32_t>(k0 * p.sb_k * 2);
+      const uint32_t b_left = b_left0.at(k0 * p.sb_k * 2);
       const i32x4_t rb = make_rsrc(B0 + k0 * p.sb_k, b_left);
 #pragma unroll
       for (int d = 0; d < TB::kPerWave; ++d) tb.template issue_one<FULL>(rb, lds_b + st * kSB, wave, lane, k_left, d);

@@ -2665,7 +2665,10 @@ View Lowerer::emit_gemm_epilogue(int v, const std::vector<int>& mem, bool* fused
   if (ma < 0 || mb < 0) return View{};
   const int64_t ea = ((d.M - 1) * d.sam + (d.K - 1) * d.sak + 1) * 2;
   const int64_t eb = ((d.N - 1) * d.sbn + (d.K - 1) * d.sbk + 1) * 2;
-  if (ea >= (int64_t{1} << 31) || eb >= (int64_t{1} << 31)) return View{};
+  if (!gemm_rows_fit(d.sam, d.sak, 2) || !gemm_rows_fit(d.sbn, d.sbk, 2)) return View{};
+  // Operand slices of 2 GiB or more: the cores' 64-bit-records form (BIG).
+  const bool big = ea >= (int64_t{1} << 31) || eb >= (int64_t{1} << 31);
+  const char* big_arg = big ? ", true" : "";
 
   // Extra operands: each must fold to one stride per (batch, m, n) group of the
   // output dims [batch (nbatch), lhs free (nlfree), rhs free].
@@ -2822,17 +2825,17 @@ View Lowerer::emit_gemm_epilogue(int v, const std::vector<int>& mem, bool* fused
   src << "extern \"C\" __global__ void __launch_bounds__(" << nt << ", 1) gemm_epilogue(ghip::GemmParams p, ghip::EpiArgs a) {\n"
       << "  const ghip::GenEpi epi{a};\n";
   if (four_km)
-    src << "  ghip::gemm_bf16_body4km<ghip::GenEpi, false, " << NB << ">(p, epi);\n}\n";
+    src << "  ghip::gemm_bf16_body4km<ghip::GenEpi, false, " << NB << big_arg << ">(p, epi);\n}\n";
   else if (eight_km)
-    src << "  ghip::gemm_bf16_body8km<ghip::GenEpi, false, " << NB << ">(p, epi);\n}\n";
+    src << "  ghip::gemm_bf16_body8km<ghip::GenEpi, false, " << NB << big_arg << ">(p, epi);\n}\n";
   else if (eight_x)
     src << "  ghip::gemm_bf16_body8x<" << (ma ? "true" : "false") << ", " << (mb ? "true" : "false")
-        << ", ghip::GenEpi, false, " << NB << ">(p, epi);\n}\n";
+        << ", ghip::GenEpi, false, " << NB << big_arg << ">(p, epi);\n}\n";
   else if (four_wave)
-    src << "  ghip::gemm_bf16_body4mn(p, epi);\n}\n";
+    src << "  ghip::gemm_bf16_body4mn<ghip::GenEpi, false" << big_arg << ">(p, epi);\n}\n";
   else
     src << "  ghip::gemm_bf16_body<" << BM << ", " << BN << ", " << WM << ", " << WN << ", " << (ma ? "true" : "false") << ", "
-        << (mb ? "true" : "false") << ", " << NB << ">(p, epi);\n}\n";
+        << (mb ? "true" : "false") << ", " << NB << ", ghip::GenEpi, false" << big_arg << ">(p, epi);\n}\n";
   RtcKernel kern;
   if (rtc_get(be, src.str(), "gemm_epilogue", &kern, err) != GHIP_OK) {
     failed = true;
@@ -2846,8 +2849,10 @@ View Lowerer::emit_gemm_epilogue(int v, const std::vector<int>& mem, bool* fused
   gp.batch = d.B; gp.M = d.M; gp.N = d.N; gp.K = d.K;
   gp.tiles_m = static_cast<int>((d.M + BM - 1) / BM);
   gp.tiles_n = static_cast<int>((d.N + BN - 1) / BN);
-  gp.a_extent = static_cast<uint32_t>(ea);
-  gp.b_extent = static_cast<uint32_t>(eb);
+  gp.a_extent = big ? 0u : static_cast<uint32_t>(ea);
+  gp.b_extent = big ? 0u : static_cast<uint32_t>(eb);
+  gp.a_extent64 = ea;
+  gp.b_extent64 = eb;
   const int64_t blocks = d.B * gp.tiles_m * gp.tiles_n;
   const int64_t so_b = d.M * d.N, so_m = d.N;
   const View lv = d.lv, rv0 = d.rv, rv1 = dp[NB - 1].rv;

@@ -70,7 +70,8 @@ struct Params {
   float inv_scale;              // 1 / scale (additive masks are added to raw scores / scale)
   int causal;
   int mask_vec;                 // m_sk == 1 and 4-key groups are aligned: vector mask loads
-  uint32_t k_extent, v_extent;  // bytes addressable from one (batch, kv head) slice
+  uint32_t k_extent, v_extent;  // bytes addressable from one (batch, kv head) slice (< 2 GiB)
+  int64_t k_extent64, v_extent64;  // the same for the BIG kernels (any size)
 };
 
 constexpr int kBKV = 64;    // keys per tile
@@ -78,8 +79,8 @@ constexpr int kQW = 32;     // queries per wave
 constexpr int kWaves = 4;   // waves per workgroup
 constexpr int kBQ = kQW * kWaves;
 constexpr float kLazyLog2 = 8.f;  // the reference max may trail the true max by 2^8
-// A buffer offset past every descriptor's extent (extents are < 2 GiB): a DMA lane
-// given it loads zeros.
+// A buffer offset past every descriptor's records (< 2 GiB, or capped at it in the
+// BIG kernels): a DMA lane given it loads zeros.
 constexpr uint32_t kPastEnd = 0x80000000u;
 
 __device__ __forceinline__ i32x4_t make_rsrc(const void* base, uint32_t bytes) {
@@ -91,6 +92,26 @@ __device__ __forceinline__ i32x4_t make_rsrc(const void* base, uint32_t bytes) {
   r.w = 0x00020000;
   return r;
 }
+// Byte offsets of a key tile within a K / V slice, and the records of a descriptor
+// based there.  BIG = false (slices below 2 GiB): 32-bit arithmetic.  BIG = true
+// (16-bit kernels, slices of any size): 64-bit offsets and the bytes left in the
+// slice capped at kPastEnd; a key tile lies within 2 GiB of its first row (the
+// host checks the sequence strides), so the cap cuts nothing a tile reads.  Kept
+// as separate instantiations: the 64-bit arithmetic made the 32-bit cases 3-8%
+// slower (measured).
+template <bool BIG>
+struct KvOff {
+  using T = uint32_t;
+  __device__ __forceinline__ static uint32_t rec(uint32_t ext, int64_t, T d) { return ext - d; }
+};
+template <>
+struct KvOff<true> {
+  using T = int64_t;
+  __device__ __forceinline__ static uint32_t rec(uint32_t, int64_t ext64, T d) {
+    const int64_t left = ext64 - d;
+    return left <= 0 ? 0u : left >= static_cast<int64_t>(kPastEnd) ? kPastEnd : static_cast<uint32_t>(left);
+  }
+};
 // 16 bytes per lane from buffer offset voff straight into LDS byte address
 // la + lane*16 (la wave-uniform).
 // m0 is set and consumed inside this one asm statement, and no compiler-generated
@@ -186,7 +207,7 @@ __device__ __forceinline__ float dot2_ones(uint32_t w, float acc) {
 // SPLIT: the split K / V load schedule (below); the host picks it unless the
 // mask is causal and no workgroup has more than 16 key tiles, where the plain
 // schedule measured faster (short workgroups).
-template <int DP, bool F16, int MK, bool SPLIT>
+template <int DP, bool F16, int MK, bool SPLIT, bool BIG = false>
 __global__ __launch_bounds__(256, DP >= 256 ? 1 : 2) void sdpa_fwd_kernel(Params p) {
   constexpr int NCH = DP / 8;  // 16-byte chunks per key row
   constexpr int NDMA = kBKV * DP * 2 / 1024 / kWaves;  // DMA instructions per wave per K (or V) tile
@@ -245,11 +266,12 @@ __global__ __launch_bounds__(256, DP >= 256 ? 1 : 2) void sdpa_fwd_kernel(Params
     koff[i] = 8 * gk < D ? static_cast<uint32_t>((static_cast<int64_t>(r) * p.k_ss + gk * 8) * 2) : kPastEnd;
     voff[i] = 8 * gv < D ? static_cast<uint32_t>((static_cast<int64_t>(r) * p.v_ss + gv * 8) * 2) : kPastEnd;
   }
-  const uint32_t kstep = static_cast<uint32_t>(kBKV * p.k_ss * 2), vstep = static_cast<uint32_t>(kBKV * p.v_ss * 2);
+  using Off = typename KvOff<BIG>::T;
+  const Off kstep = static_cast<Off>(kBKV * p.k_ss * 2), vstep = static_cast<Off>(kBKV * p.v_ss * 2);
   auto issue = [&](int t, int st) {
-    const uint32_t dk = static_cast<uint32_t>(t) * kstep, dv = static_cast<uint32_t>(t) * vstep;
-    const i32x4_t rk = make_rsrc(reinterpret_cast<const char*>(Kb) + dk, p.k_extent - dk);
-    const i32x4_t rv = make_rsrc(reinterpret_cast<const char*>(Vb) + dv, p.v_extent - dv);
+    const Off dk = static_cast<Off>(t) * kstep, dv = static_cast<Off>(t) * vstep;
+    const i32x4_t rk = make_rsrc(reinterpret_cast<const char*>(Kb) + dk, KvOff<BIG>::rec(p.k_extent, p.k_extent64, dk));
+    const i32x4_t rv = make_rsrc(reinterpret_cast<const char*>(Vb) + dv, KvOff<BIG>::rec(p.v_extent, p.v_extent64, dv));
     const uint32_t lk = lds0 + static_cast<uint32_t>(st) * (2 * kBKV * DP * 2) + wave * NDMA * 1024;
     const uint32_t lv = lk + kBKV * DP * 2;
 #pragma unroll
@@ -258,15 +280,15 @@ __global__ __launch_bounds__(256, DP >= 256 ? 1 : 2) void sdpa_fwd_kernel(Params
     for (int i = 0; i < NDMA; ++i) dma16(rv, lv + i * 1024, voff[i]);
   };
   auto issue_k = [&](int t) {
-    const uint32_t dk = static_cast<uint32_t>(t) * kstep;
-    const i32x4_t rk = make_rsrc(reinterpret_cast<const char*>(Kb) + dk, p.k_extent - dk);
+    const Off dk = static_cast<Off>(t) * kstep;
+    const i32x4_t rk = make_rsrc(reinterpret_cast<const char*>(Kb) + dk, KvOff<BIG>::rec(p.k_extent, p.k_extent64, dk));
     const uint32_t lk = lds0 + wave * NDMA * 1024;
 #pragma unroll
     for (int i = 0; i < NDMA; ++i) dma16(rk, lk + i * 1024, koff[i]);
   };
   auto issue_v = [&](int t) {
-    const uint32_t dv = static_cast<uint32_t>(t) * vstep;
-    const i32x4_t rv = make_rsrc(reinterpret_cast<const char*>(Vb) + dv, p.v_extent - dv);
+    const Off dv = static_cast<Off>(t) * vstep;
+    const i32x4_t rv = make_rsrc(reinterpret_cast<const char*>(Vb) + dv, KvOff<BIG>::rec(p.v_extent, p.v_extent64, dv));
     const uint32_t lv = lds0 + kBKV * DP * 2 + wave * NDMA * 1024;
 #pragma unroll
     for (int i = 0; i < NDMA; ++i) dma16(rv, lv + i * 1024, voff[i]);
@@ -491,20 +513,26 @@ __global__ __launch_bounds__(256, DP >= 256 ? 1 : 2) void sdpa_fwd_kernel(Params
   }
 }
 
-template <int DP, bool F16, bool SPLIT>
+template <int DP, bool F16, bool SPLIT, bool BIG>
 static void launch_dm(const Params& p, int mk, dim3 grid, hipStream_t s) {
   static_assert(!SPLIT, "masked kernels use the plain schedule");
-  if (mk == kBoolMask) hipLaunchKernelGGL((sdpa_fwd_kernel<DP, F16, kBoolMask, SPLIT>), grid, dim3(256), 0, s, p);
-  else if (mk == kAddMask) hipLaunchKernelGGL((sdpa_fwd_kernel<DP, F16, kAddMask, SPLIT>), grid, dim3(256), 0, s, p);
-  else hipLaunchKernelGGL((sdpa_fwd_kernel<DP, F16, kNoMask, SPLIT>), grid, dim3(256), 0, s, p);
+  if (mk == kBoolMask) hipLaunchKernelGGL((sdpa_fwd_kernel<DP, F16, kBoolMask, SPLIT, BIG>), grid, dim3(256), 0, s, p);
+  else if (mk == kAddMask) hipLaunchKernelGGL((sdpa_fwd_kernel<DP, F16, kAddMask, SPLIT, BIG>), grid, dim3(256), 0, s, p);
+  else hipLaunchKernelGGL((sdpa_fwd_kernel<DP, F16, kNoMask, SPLIT, BIG>), grid, dim3(256), 0, s, p);
 }
 // The split schedule only without a mask: with one, the compiler's waits for the
 // mask loads also wait for the K / V DMA (vmcnt counts both in issue order), and
 // the masked variants would spill at the extra barrier.
+// BIG: K / V slices of 2 GiB or more (KvOff).
+template <int DP, bool F16, bool BIG>
+static void launch_db(const Params& p, int mk, dim3 grid, bool split, hipStream_t s) {
+  if (split && mk == kNoMask) hipLaunchKernelGGL((sdpa_fwd_kernel<DP, F16, kNoMask, true, BIG>), grid, dim3(256), 0, s, p);
+  else launch_dm<DP, F16, false, BIG>(p, mk, grid, s);
+}
 template <int DP, bool F16>
-static void launch_d(const Params& p, int mk, dim3 grid, bool split, hipStream_t s) {
-  if (split && mk == kNoMask) hipLaunchKernelGGL((sdpa_fwd_kernel<DP, F16, kNoMask, true>), grid, dim3(256), 0, s, p);
-  else launch_dm<DP, F16, false>(p, mk, grid, s);
+static void launch_d(const Params& p, int mk, dim3 grid, bool split, bool big, hipStream_t s) {
+  if (big) launch_db<DP, F16, true>(p, mk, grid, split, s);
+  else launch_db<DP, F16, false>(p, mk, grid, split, s);
 }
 
 
@@ -750,9 +778,12 @@ bool sdpa_fused_supported(int dtype, int64_t H, int64_t Hkv, int64_t Sq, int64_t
       if (s[i] < 0 || s[i] % in_al != 0) return false;
   for (int i = 0; i < 3; ++i)
     if (os[i] < 0 || os[i] % out_al != 0) return false;
-  // One (batch, kv head) slice of K / V must fit the 2 GiB buffer-offset range.
-  if (((Sk - 1) * ks[2] + D) * es >= (int64_t{1} << 31)) return false;
-  if (((Sk - 1) * vs[2] + D) * es >= (int64_t{1} << 31)) return false;
+  // A key tile (64 keys) of K / V lies within 2 GiB of its first row; the slice of
+  // one (batch, kv head) may be any size with 16-bit operands (the BIG kernels),
+  // below 2 GiB with fp32 ones.
+  if ((64 * ks[2] + 256) * es >= (int64_t{1} << 31) || (64 * vs[2] + 256) * es >= (int64_t{1} << 31)) return false;
+  if (f32 && (((Sk - 1) * ks[2] + D) * es >= (int64_t{1} << 31) || ((Sk - 1) * vs[2] + D) * es >= (int64_t{1} << 31)))
+    return false;
   return true;
 }
 
@@ -782,7 +813,8 @@ extern "C" int ghip_sdpa_fwd_masked(int dtype, const void* q, const void* k, con
                      "sdpa_fwd: needs bfloat16 or float16 with a head dim that is a multiple of 8 up to 256, "
                      "or float32 with a multiple of 4 up to 128; a bool mask or one in the operands' dtype, a "
                      "positive finite scale, non-negative strides that are multiples of 16 bytes (8 bytes for "
-                     "a 16-bit output) and < 2 GiB per K/V head");
+                     "a 16-bit output), K / V sequence strides below 32 MiB and, for float32, < 2 GiB per "
+                     "K/V head");
   const bool f32 = dtype == GHIP_DTYPE_FLOAT32;
   const int64_t es = f32 ? 4 : 2;
   auto al = [](const void* ptr, uintptr_t a) { return (reinterpret_cast<uintptr_t>(ptr) & (a - 1)) == 0; };
@@ -803,8 +835,11 @@ extern "C" int ghip_sdpa_fwd_masked(int dtype, const void* q, const void* k, con
   p.inv_scale = 1.0f / scale;
   p.causal = causal ? 1 : 0;
   p.D = static_cast<int>(D);
-  p.k_extent = static_cast<uint32_t>(((Sk - 1) * p.k_ss + D) * es);
-  p.v_extent = static_cast<uint32_t>(((Sk - 1) * p.v_ss + D) * es);
+  p.k_extent64 = ((Sk - 1) * p.k_ss + D) * es;
+  p.v_extent64 = ((Sk - 1) * p.v_ss + D) * es;
+  const bool big = p.k_extent64 >= (int64_t{1} << 31) || p.v_extent64 >= (int64_t{1} << 31);
+  p.k_extent = big ? 0u : static_cast<uint32_t>(p.k_extent64);
+  p.v_extent = big ? 0u : static_cast<uint32_t>(p.v_extent64);
   int mk = attn::kNoMask;
   if (mask) {
     mk = mask_dtype == GHIP_DTYPE_BOOL ? attn::kBoolMask : attn::kAddMask;
@@ -828,14 +863,14 @@ extern "C" int ghip_sdpa_fwd_masked(int dtype, const void* q, const void* k, con
     if (D <= 64) attn::launch_f32<64>(p, mk, grid, s);
     else attn::launch_f32<128>(p, mk, grid, s);
   } else if (D <= 64) {
-    if (f16) attn::launch_d<64, true>(p, mk, grid, split, s);
-    else attn::launch_d<64, false>(p, mk, grid, split, s);
+    if (f16) attn::launch_d<64, true>(p, mk, grid, split, big, s);
+    else attn::launch_d<64, false>(p, mk, grid, split, big, s);
   } else if (D <= 128) {
-    if (f16) attn::launch_d<128, true>(p, mk, grid, split, s);
-    else attn::launch_d<128, false>(p, mk, grid, split, s);
+    if (f16) attn::launch_d<128, true>(p, mk, grid, split, big, s);
+    else attn::launch_d<128, false>(p, mk, grid, split, big, s);
   } else {
-    if (f16) attn::launch_d<256, true>(p, mk, grid, split, s);
-    else attn::launch_d<256, false>(p, mk, grid, split, s);
+    if (f16) attn::launch_d<256, true>(p, mk, grid, split, big, s);
+    else attn::launch_d<256, false>(p, mk, grid, split, big, s);
   }
   GHIP_CHECK(hipGetLastError(), err);
   return GHIP_OK;

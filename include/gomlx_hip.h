@@ -142,7 +142,10 @@ int ghip_copy_strided(int elem_bytes, const void* src, void* dst, int rank, cons
  * with every operand addressed by ELEMENT strides (so transposed / permuted
  * views need no copy).  ab_dtype is the dtype of a and b (FLOAT32, BFLOAT16 or
  * FLOAT16); c_dtype the output dtype (FLOAT32, or ab_dtype when that is 16-bit).
- * Accumulation is fp32.
+ * Accumulation is fp32.  Operands of any size: a batch slice may span more than
+ * 4 GiB (the MFMA cores then run their 64-bit-addressing form, bit-identical);
+ * row strides of 2^22 elements (16-bit) / 2^21 (fp32) or more, unaligned or
+ * negative strides run a generic (non-MFMA) kernel.
  * Requires sc_n == 1. */
 int ghip_gemm_batched(int ab_dtype, int c_dtype, int64_t batch, int64_t M, int64_t N,
                       int64_t K, const void* a, int64_t sa_b, int64_t sa_m, int64_t sa_k,
@@ -173,8 +176,10 @@ int ghip_gemm_grouped(int ab_dtype, int c_dtype, int groups, int64_t M, int64_t 
  * dim contiguous, so BHSD and BSHD layouts both work without copies.  Supported:
  * dtype BFLOAT16 or FLOAT16 with D a multiple of 8 up to 256, strides multiples of
  * 8 (4 for o), o 8-byte aligned; or FLOAT32 with D a multiple of 4 up to 128,
- * strides multiples of 4, o 16-byte aligned; scale > 0 and q/k/v 16-byte aligned.
- * Anything else returns GHIP_ERR_UNSUPPORTED (the graph lowering then uses the
+ * strides multiples of 4, o 16-byte aligned; scale > 0 and q/k/v 16-byte aligned;
+ * K / V sequence strides below 32 MiB.  One (batch, kv head) slice of K / V may
+ * span more than 4 GiB with 16-bit operands (long contexts), below 2 GiB with
+ * FLOAT32 ones.  Anything else returns GHIP_ERR_UNSUPPORTED (the graph lowering then uses the
  * composite).  Softmax statistics and accumulation are fp32 (fp32 products too for
  * FLOAT32); weights below 2^-126 of a row's largest are flushed to zero. */
 int ghip_sdpa_fwd(int dtype, const void* q, const void* k, const void* v, void* o,
