@@ -5,7 +5,8 @@ RMSNorm over the last axis of x [8192, 4096] fp32 (gamma [4096], eps 1e-6) —
 one "step" is one RMSNorm launch over that batch, inputs resident in HBM.
 `value` is GB/s of algorithmic traffic (read x + gamma, write y).  The same line
 carries the other BASELINE workloads under "secondary" (softmax, bf16 RMSNorm,
-LayerNorm, bf16/fp32 DotGeneral, the attention composite, the transformer block)
+LayerNorm, bf16/fp32 DotGeneral, the bf16 DotGeneral's per-GPU shard under 8-way
+data parallelism (batch 0 alone), the attention composite, the transformer block)
 and two widened ops (FusedDense + GELU, the embedding-gradient ScatterSum), each
 with its own roofline fraction.
 
@@ -26,8 +27,8 @@ eager launch before timing.
 
 Inputs: every workload's tensors come from the SplitMix64 / Box-Muller streams of
 gomlx_hip.synth (seeded, generated on the device or on the host for the graph
-cases).  CPU baselines: every line but the vendor comparison carries a
-cpu_baseline, the C oracle (oracle/oracle.c, OpenMP on the host's cores: a CPU
+cases).  CPU baselines: every line but the vendor comparisons and the shard line
+(whose CPU work per row is the DotGeneral line's) carries a cpu_baseline, the C oracle (oracle/oracle.c, OpenMP on the host's cores: a CPU
 restatement, not GoMLX's simplego, which cannot be built here) timed on a bounded
 slice of the same input bytes, copied back from the device; the headline's leg
 runs 10 s on the full input, the others --cpu-s each.
@@ -388,6 +389,27 @@ def make_cases(only=None):
                     config={"workload": "comparison only: torch.matmul (hipBLASLt) on the DotGeneral "
                                         "bf16 config shape and inputs, same process"})
 
+    def shard_dot_case(vendor):
+        """Batch 0 of the bf16 DotGeneral config, [2048,4096] x [4096,4096]: one GPU's
+        shard when the 8 batches are spread over 8 GPUs (data parallel over the batch
+        axis, no exchange).  128 tiles of 256 x 256, half the CUs; this backend runs
+        it on the 128 x 128 core.  vendor: torch.matmul (hipBLASLt), for comparison."""
+        a8, b8 = dot_inputs(torch.bfloat16)
+        a, b = a8[0], b8[0]
+        c = torch.empty((2048, 4096), device=dev, dtype=torch.bfloat16)
+        fl = 2 * 2048 * 4096 * 4096
+        shape = "DotGeneral [2048,4096]x[4096,4096] (batch 0 of the config: the per-GPU shard of 8-way data parallelism)"
+        if vendor:
+            return Case("dot_general_bf16_shard_hipblaslt", lambda i: torch.matmul(a, b, out=c),
+                        flops_per_step=fl, bound="mfma", peak=BF16_PEAK_TFLOPS, dtype="bf16",
+                        kernel="hipBLASLt (torch.matmul)",
+                        config={"workload": f"comparison only: torch.matmul (hipBLASLt) on the {shape}, same process"})
+        return Case("dot_general_bf16_shard", lambda i: ops.gemm(a, b, out=c),
+                    flops_per_step=fl, bound="mfma", peak=BF16_PEAK_TFLOPS, dtype="bf16",
+                    kernel="gemm_bf16_kernel<128, 128, 2, 2, true, false, bf16_t, bf16_t>",
+                    config={"workload": f"{shape}, bf16 in ~ N(0, 1/sqrt(4096)), fp32 accumulate, bf16 out; "
+                                        f"CPU rate: as dot_general_bf16 (same rows, same work per row)"})
+
     def attention_case():
         B, H, S, D = 4, 16, 2048, 128
         q = nd(4001, (B, H, S, D), dtype=torch.bfloat16)
@@ -545,6 +567,8 @@ def make_cases(only=None):
         "dot_general_bf16": lambda: dot_case(torch.bfloat16, "bf16", BF16_PEAK_TFLOPS),
         "dot_general_f32": lambda: dot_case(torch.float32, "f32", FP32_PEAK_TFLOPS),
         "dot_general_bf16_hipblaslt": vendor_dot_case,
+        "dot_general_bf16_shard": lambda: shard_dot_case(False),
+        "dot_general_bf16_shard_hipblaslt": lambda: shard_dot_case(True),
         "attention_bf16": attention_case,
         "transformer_block_bf16": transformer_case,
         "fused_dense_gelu_bf16": dense_case,

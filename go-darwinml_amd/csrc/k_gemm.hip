@@ -2,10 +2,11 @@
 //
 // bf16 / f16 path (the MFMA path the metric is quoted on): the cores live in
 // gemm_bf16_dev.h (shared with the Compile-time generated epilogue GEMMs); the
-// kernels here instantiate them with a plain store epilogue.  Grids of >= 128
-// 256 x 256 tiles run the 8-wave 16x16x32 cores (A K- / B N-contiguous: 32-deep
-// k-steps; B K-contiguous: 64-deep) or, with both operands MN-contiguous, the
-// 4-wave 32-deep core; smaller grids the 8- / 4-wave 32x32x16 core.
+// kernels here instantiate them with a plain store epilogue.  Grids of more than
+// 128 256 x 256 tiles run the 256 x 256 cores (A K- / B N-contiguous: the 4-wave
+// 16x16x32 core; B K-contiguous: the 8-wave 64-deep 16x16x32 core; both
+// MN-contiguous: the 4-wave 32-deep core); smaller grids the 4-wave 128 x 128
+// 32x32x16 core, two workgroups per CU.
 // fp32 path: v_mfma_f32_32x32x2f32 over LDS-DMA tiles (below).
 // Anything the vector paths cannot address (odd strides, unaligned bases,
 // negative strides, a row stride of 4M elements (bf16) / 2M (fp32) or more) runs
@@ -95,11 +96,11 @@ static hipError_t dispatch_bf16(GemmParams p, hipStream_t s) {
   const int64_t ea = slice_bytes(p.M, p.sa_m, p.K, p.sa_k, 2);
   const int64_t eb = slice_bytes(p.N, p.sb_n, p.K, p.sb_k, 2);
   const int64_t t256 = p.batch * ((p.M + 255) / 256) * ((p.N + 255) / 256);
-  const bool grid256 = p.M >= 256 && p.N >= 256 && t256 >= 128;
   // Slices of 2 GiB or more: the 256 x 256 cores' 64-bit-records forms.
   const bool big = ea >= (int64_t{1} << 31) || eb >= (int64_t{1} << 31);
+  const bool big_ok = p.M >= 256 && p.N >= 256 && t256 >= 128;
   if (ma < 0 || mb < 0 || !nonneg || !gemm_rows_fit(p.sa_m, p.sa_k, 2) || !gemm_rows_fit(p.sb_n, p.sb_k, 2) ||
-      (big && !grid256))
+      (big && !big_ok))
     return launch_generic<InT, OutT>(p, s);
   p.a_extent = big ? 0u : static_cast<uint32_t>(ea);
   p.b_extent = big ? 0u : static_cast<uint32_t>(eb);
@@ -109,8 +110,13 @@ static hipError_t dispatch_bf16(GemmParams p, hipStream_t s) {
   p.vec_c = (p.sc_m % kV == 0) && (p.sc_b % kV == 0 || p.batch == 1) &&
             (reinterpret_cast<uintptr_t>(p.c) % 16 == 0);
   if (big) return launch_bf16_4w<true, InT, OutT>(p, ma, mb, s);
-  if (grid256) return launch_bf16_4w<false, InT, OutT>(p, ma, mb, s);
-  if (p.M >= 256 && p.N >= 128) return launch_bf16<256, 128, 2, 2, InT, OutT>(p, ma, mb, s);
+  // Grids of more than 128 256 x 256 tiles: the 256 x 256 cores (one workgroup per
+  // CU).  Up to 128 such tiles they would leave half the 256 CUs or more idle, and
+  // the 128 x 128 core (two workgroups per CU, so up to 512 tiles in one round) is
+  // faster in every layout: 11-33% at 128 tiles ([2048,4096,4096], [8192,1024,2048]),
+  // 12-43% against the 256 x 128 core below that (A/B, one box).  All cores give
+  // the same bits.
+  if (p.M >= 256 && p.N >= 256 && t256 > 128) return launch_bf16_4w<false, InT, OutT>(p, ma, mb, s);
   return launch_bf16<128, 128, 2, 2, InT, OutT>(p, ma, mb, s);
 }
 

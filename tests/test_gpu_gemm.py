@@ -131,9 +131,10 @@ def test_mn_major_core_matches_k_major_core(cuda, K, dt):
     same k order per accumulator: bit-identical products, for a K that fills whole
     k-tiles (steady-state loop) and one that does not, 16-bit and fp32 outputs; and
     sampled entries against fp64."""
-    ta_k = synth.normal_device(3601, (2, 2048, K), std=0.125, device=cuda, dtype=dt)
+    # [2, 2304, K] x [2, K, 2048]: 144 tiles of 256 x 256 (the 256 x 256 cores)
+    ta_k = synth.normal_device(3601, (2, 2304, K), std=0.125, device=cuda, dtype=dt)
     tb_k = synth.normal_device(3602, (2, K, 2048), std=0.125, device=cuda, dtype=dt).transpose(1, 2).contiguous().transpose(1, 2)
-    ta_mn = ta_k.transpose(1, 2).contiguous().transpose(1, 2)   # [2, 2048, K] with unit M stride
+    ta_mn = ta_k.transpose(1, 2).contiguous().transpose(1, 2)   # [2, 2304, K] with unit M stride
     tb_mn = tb_k.contiguous()                                   # [2, K, 2048] row-major: unit N stride
     assert ta_mn.stride(1) == 1 and tb_mn.stride(2) == 1 and ta_k.stride(2) == 1 and tb_k.stride(1) == 1
     for out_dtype in (dt, torch.float32):
@@ -176,14 +177,14 @@ def test_16bit_large_grids_ragged_layouts(cuda, shape, a_t, b_t):
 @pytest.mark.parametrize("K", [16, 32, 1000, 1024])
 @pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])
 def test_cores_bit_identical_across_layouts(cuda, K, dt):
-    """The same values in all four operand layouts take four code paths at >= 128
-    tiles of 256 x 256: A K- / B N-contiguous the 8-wave 32-deep 16x16x32 core, B
-    K-contiguous (A either way) the 8-wave 64-deep 16x16x32 core, both MN-contiguous
+    """The same values in all four operand layouts take three code paths at more than
+    128 tiles of 256 x 256 (here 136): A K- / B N-contiguous the 4-wave 16x16x32 core,
+    B K-contiguous (A either way) the 8-wave 64-deep 16x16x32 core, both MN-contiguous
     the 4-wave 32x32x16 core.  The products must agree bit for bit, for K inside one
     k-tile (16, 32: the MFMAs run straight into the epilogue), a ragged K and one that
     reaches the steady-state loop; plus sampled entries against fp64."""
     a_k = synth.normal_device(3701, (1, 2048, K), std=0.125, device=cuda, dtype=dt)       # A K-contiguous
-    b_n = synth.normal_device(3702, (1, K, 4096), std=0.125, device=cuda, dtype=dt)       # B N-contiguous
+    b_n = synth.normal_device(3702, (1, K, 4352), std=0.125, device=cuda, dtype=dt)       # B N-contiguous
     a_m = a_k.transpose(1, 2).contiguous().transpose(1, 2)
     b_k = b_n.transpose(1, 2).contiguous().transpose(1, 2)
     assert a_k.stride(2) == 1 and a_m.stride(1) == 1 and b_n.stride(2) == 1 and b_k.stride(1) == 1
@@ -192,6 +193,27 @@ def test_cores_bit_identical_across_layouts(cuda, K, dt):
         assert torch.equal(c, outs[0])
     got, ref = _sampled_check(a_k, b_n, outs[0], seed=14)
     assert rel_err(got, ref) <= (1e-2 if dt == torch.bfloat16 else 1e-3)
+
+
+@pytest.mark.parametrize("K", [1000, 4096])
+@pytest.mark.parametrize("layout", ["km", "kk", "mm", "mk"])
+def test_small_grid_core_matches_large_grid_cores(cuda, K, layout):
+    """A grid of 128 tiles of 256 x 256 ([2048, K] x [K, 4096]) runs the 128 x 128
+    core (two workgroups per CU); the same product as batch 0 of a two-batch call
+    (256 tiles) runs a 256 x 256 core.  Both must give the same bits, in every
+    operand layout, with bf16 and fp32 outputs."""
+    a2 = synth.normal_device(3801, (2, 2048, K), std=0.125, device=cuda, dtype=torch.bfloat16)
+    b2 = synth.normal_device(3802, (2, K, 4096), std=0.125, device=cuda, dtype=torch.bfloat16)
+    if layout[0] == "m":
+        a2 = a2.transpose(1, 2).contiguous().transpose(1, 2)
+    if layout[1] == "k":
+        b2 = b2.transpose(1, 2).contiguous().transpose(1, 2)
+    for odt in (torch.bfloat16, torch.float32):
+        c2 = ops.gemm(a2, b2, out_dtype=odt)
+        c1 = ops.gemm(a2[:1], b2[:1], out_dtype=odt)
+        assert torch.equal(c1[0], c2[0])
+    got, ref = _sampled_check(a2[:1], b2[:1], c1, seed=15)
+    assert rel_err(got, ref) <= 1e-4
 
 
 @pytest.mark.parametrize("shape", SHAPES)
