@@ -2756,16 +2756,19 @@ View Lowerer::emit_gemm_epilogue(int v, const std::vector<int>& mem, bool* fused
   // reads per MFMA; on the block's residual and SwiGLU epilogues 2.5% faster than
   // the 8-wave core under sustained load).  A VALU-heavy epilogue of one product
   // (FusedDense + tanh-GELU) stays on the 8-wave core (4% faster there).
+  //
+  // One product on a grid of at most 128 256 x 256 tiles: the 128 x 128 core (two
+  // workgroups per CU), as the precompiled GEMMs do (a 256 x 256 grid that small
+  // leaves half the CUs or more idle).
   bool eight_km = false, eight_x = false, four_km = false;
-  if (ma && !mb && d.M >= 256 && d.N >= 256 / NB && (NB == 2 || !heavy_epilogue) &&
-      d.B * ((d.M + 255) / 256) * ((d.N + 256 / NB - 1) / (256 / NB)) >= 128) {
+  const int64_t t4 = d.B * ((d.M + 255) / 256) * ((d.N + 256 / NB - 1) / (256 / NB));
+  if (ma && !mb && d.M >= 256 && d.N >= 256 / NB && (NB == 2 || !heavy_epilogue) && (NB == 2 ? t4 >= 128 : t4 > 128)) {
     BM = 256, BN = 256 / NB, WM = 2, WN = 2, four_km = true;
   } else if (NB == 1) {
-    if (d.M >= 256 && d.N >= 256 && t256 >= 128 && ma && !mb) BM = 256, BN = 256, WM = 2, WN = 4, eight_km = true;
-    else if (d.M >= 256 && d.N >= 256 && t256 >= 128 && (mb || heavy_epilogue))
+    if (d.M >= 256 && d.N >= 256 && t256 > 128 && ma && !mb) BM = 256, BN = 256, WM = 2, WN = 4, eight_km = true;
+    else if (d.M >= 256 && d.N >= 256 && t256 > 128 && (mb || heavy_epilogue))
       BM = 256, BN = 256, WM = 2, WN = 4, eight_x = true;
-    else if (d.M >= 256 && d.N >= 256 && t256 >= 128) BM = 256, BN = 256, WM = 2, WN = 2, four_wave = true;
-    else if (d.M >= 256 && d.N >= 128) BM = 256, BN = 128, WM = 2, WN = 2;
+    else if (d.M >= 256 && d.N >= 256 && t256 > 128) BM = 256, BN = 256, WM = 2, WN = 2, four_wave = true;
   } else if (d.M >= 256 && d.N >= 128) {
     BM = 256, BN = 128, WM = 2, WN = 4;
     eight_km = ma && !mb && d.B * ((d.M + 255) / 256) * ((d.N + 127) / 128) >= 128;
