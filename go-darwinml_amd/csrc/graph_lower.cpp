@@ -1980,14 +1980,27 @@ struct Lowerer {
         if (has_mask) rd.push_back(mview.slot);
         const View mv = mview;
         const std::array<int64_t, 4> ms4 = mst;
-        add_step(fmt("sdpa_fwd %s B=%lld H=%lld Hkv=%d Sq=%lld Sk=%lld D=%lld causal=%d mask=%s (fused attention)",
+        // Few (batch, head, query block) workgroups: the key range splits over a
+        // workspace in the arena (partial outputs merged by log-sum-exp).
+        const int64_t ws_bytes = ghip_sdpa_workspace_bytes(dt, B, H, Hkv, Sq, Sk, D, causal ? 1 : 0);
+        std::vector<int> wr{ov.slot};
+        View wsv;
+        if (ws_bytes > 0) {
+          Shape wss;
+          wss.dtype = GHIP_DTYPE_FLOAT32;
+          wss.dims = {(ws_bytes + 3) / 4};
+          wsv = fresh(wss);
+          wr.push_back(wsv.slot);
+        }
+        add_step(fmt("sdpa_fwd %s B=%lld H=%lld Hkv=%d Sq=%lld Sk=%lld D=%lld causal=%d mask=%s (fused attention%s)",
                      dtype_name(dt), (long long)B, (long long)H, Hkv, (long long)Sq, (long long)Sk, (long long)D,
-                     causal ? 1 : 0, has_mask ? dtype_name(mdt) : "none"),
-                 rd, {ov.slot}, [=](ExecState& st, GHipError* e) {
+                     causal ? 1 : 0, has_mask ? dtype_name(mdt) : "none", ws_bytes > 0 ? ", key range split" : ""),
+                 rd, wr, [=](ExecState& st, GHipError* e) {
                    const void* mp = has_mask ? st.ptr(mv, mdt) : nullptr;
-                   return ghip_sdpa_fwd_masked(dt, st.ptr(q, dt), st.ptr(k, dt), st.ptr(vw, dt), st.ptr(ov, dt), B, H,
-                                               Hkv, Sq, Sk, D, aq.data(), ak.data(), av.data(), ao.data(), mp, mdt,
-                                               ms4.data(), scale, causal ? 1 : 0, st.stream, e);
+                   void* ws = ws_bytes > 0 ? st.ptr(wsv, GHIP_DTYPE_FLOAT32) : nullptr;
+                   return ghip_sdpa_fwd_masked_ws(dt, st.ptr(q, dt), st.ptr(k, dt), st.ptr(vw, dt), st.ptr(ov, dt), B,
+                                                  H, Hkv, Sq, Sk, D, aq.data(), ak.data(), av.data(), ao.data(), mp, mdt,
+                                                  ms4.data(), scale, causal ? 1 : 0, ws, ws_bytes, st.stream, e);
                  });
         return out_l;
       }

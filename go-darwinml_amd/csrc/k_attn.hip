@@ -72,6 +72,16 @@ struct Params {
   int mask_vec;                 // m_sk == 1 and 4-key groups are aligned: vector mask loads
   uint32_t k_extent, v_extent;  // bytes addressable from one (batch, kv head) slice (< 2 GiB)
   int64_t k_extent64, v_extent64;  // the same for the BIG kernels (any size)
+  // Key range split over blockIdx.y (16-bit kernels): kv_chunk keys per split (a
+  // multiple of the 64-key tile), each split writing its normalised output and its
+  // log2-sum-exp of the scaled scores for the combine kernel; 0: no split.
+  int kv_chunk;
+  float* part_o;    // [split][b][h][query][D]
+  float* part_lse;  // [split][b][h][query]
+  // Grouped-query rows (16-bit kernels, no causal mask): a workgroup holds up to
+  // 128 (head, query) rows of one kv head's group of H / Hkv heads, head-major, so
+  // the group's heads read each K / V tile once; grid (row blocks, b, kv head).
+  int gqa_pack;
 };
 
 constexpr int kBKV = 64;    // keys per tile
@@ -220,17 +230,38 @@ __global__ __launch_bounds__(256, DP >= 256 ? 1 : 2) void sdpa_fwd_kernel(Params
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int h2 = lane >> 5;  // half of the wave
   const int D = p.D;
-  const int nqb = (p.Sq + kBQ - 1) / kBQ;
-  const int nbh = p.B * p.H;
-  // Longest first over the whole grid: every (batch, head) of the last query
-  // block, then of the one before it, ... (causal: later blocks see more keys).
-  const int qb = p.causal ? (nqb - 1 - static_cast<int>(blockIdx.x / nbh)) : static_cast<int>(blockIdx.x / nbh);
-  const int bh = blockIdx.x % nbh;
-  const int b = bh / p.H, h = bh % p.H;
-  const int hk = h / (p.H / p.Hkv);
-  const int q0 = qb * kBQ;
-  const int qw = q0 + wave * kQW;    // first query of this wave
-  const int qi = qw + (lane & 31);   // this lane's query
+  int b, h, hk, q0, qw, qi;
+  bool qv;  // this lane's row exists
+  if (p.gqa_pack) {
+    // Row r of the group (head hk * G + r / Sq, query r % Sq); no causal mask, so
+    // q0 / qw (the causal bounds) go unused.
+    const int G = p.H / p.Hkv;
+    const int nbk = p.B * p.Hkv;
+    const int bk = static_cast<int>(blockIdx.x % nbk);
+    b = bk / p.Hkv;
+    hk = bk % p.Hkv;
+    const int r = static_cast<int>(blockIdx.x / nbk) * kBQ + wave * kQW + (lane & 31);
+    qv = r < G * p.Sq;
+    const int rc = qv ? r : 0;
+    h = hk * G + rc / p.Sq;
+    qi = rc % p.Sq;
+    q0 = 0;
+    qw = 0;
+  } else {
+    const int nqb = (p.Sq + kBQ - 1) / kBQ;
+    const int nbh = p.B * p.H;
+    // Longest first over the whole grid: every (batch, head) of the last query
+    // block, then of the one before it, ... (causal: later blocks see more keys).
+    const int qb = p.causal ? (nqb - 1 - static_cast<int>(blockIdx.x / nbh)) : static_cast<int>(blockIdx.x / nbh);
+    const int bh = blockIdx.x % nbh;
+    b = bh / p.H;
+    h = bh % p.H;
+    hk = h / (p.H / p.Hkv);
+    q0 = qb * kBQ;
+    qw = q0 + wave * kQW;    // first query of this wave
+    qi = qw + (lane & 31);   // this lane's query
+    qv = qi < p.Sq;
+  }
 
   const uint16_t* Q = static_cast<const uint16_t*>(p.q) + b * p.q_sb + h * p.q_sh;
   const uint16_t* Kb = static_cast<const uint16_t*>(p.k) + b * p.k_sb + hk * p.k_sh;
@@ -240,15 +271,21 @@ __global__ __launch_bounds__(256, DP >= 256 ? 1 : 2) void sdpa_fwd_kernel(Params
   bf16x8_t qf[DP / 16];
 #pragma unroll
   for (int s = 0; s < DP / 16; ++s) {
-    if (qi < p.Sq && 16 * s + 8 * h2 < D)
+    if (qv && 16 * s + 8 * h2 < D)
       qf[s] = *reinterpret_cast<const bf16x8_t*>(Q + static_cast<int64_t>(qi) * p.q_ss + 16 * s + 8 * h2);
     else
       qf[s] = bf16x8_t{};
   }
   // This lane's mask row (query qi of (b, h)); keys step by m_sk.
-  const int64_t mrow = b * p.m_sb + h * p.m_sh + static_cast<int64_t>(qi < p.Sq ? qi : 0) * p.m_sq;
+  const int64_t mrow = b * p.m_sb + h * p.m_sh + static_cast<int64_t>(qv ? qi : 0) * p.m_sq;
 
-  const int kv_end = p.causal ? min(p.Sk, q0 + kBQ) : p.Sk;
+  // Keys [kv_beg, kv_end) in tiles t0 .. ntiles-1; with a split key range the
+  // chunk bounds are multiples of the tile, so a split's tiles hold its keys only.
+  const int split = static_cast<int>(blockIdx.y);
+  const int kv_all = p.causal ? min(p.Sk, q0 + kBQ) : p.Sk;
+  const int kv_beg = p.kv_chunk ? split * p.kv_chunk : 0;
+  const int kv_end = p.kv_chunk ? min(kv_all, kv_beg + p.kv_chunk) : kv_all;
+  const int t0 = kv_beg / kBKV;
   const int ntiles = (kv_end + kBKV - 1) / kBKV;
   // scale_log2 > 0, so the running max is kept on the raw scores and the scale
   // is folded into one FMA per exponent: exp2(s * c - m * c).
@@ -456,7 +493,7 @@ __global__ __launch_bounds__(256, DP >= 256 ? 1 : 2) void sdpa_fwd_kernel(Params
       // refilled.
       asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     };
-    for (int t = 0; t < ntiles; t += 2) {
+    for (int t = t0; t < ntiles; t += 2) {
       tile(t);
       if (t + 1 < ntiles) tile(t + 1);
     }
@@ -467,13 +504,16 @@ __global__ __launch_bounds__(256, DP >= 256 ? 1 : 2) void sdpa_fwd_kernel(Params
     // DMA instructions in issue order: NDMA of them per K or V tile.
     constexpr int kWaitOneTile = NDMA | (7 << 4) | (15 << 8);  // vmcnt(NDMA), other counters not waited
     static_assert(NDMA < 16, "vmcnt immediate");
-    issue_k(0);
-    issue_v(0);
-    for (int t = 0; t < ntiles; ++t) {
-      if (t == 0) __builtin_amdgcn_s_waitcnt(kWaitOneTile);  // K_0 landed (V_0 may be in flight)
+    // (A split with no keys for this query block issues nothing.)
+    if (t0 < ntiles) {
+      issue_k(t0);
+      issue_v(t0);
+    }
+    for (int t = t0; t < ntiles; ++t) {
+      if (t == t0) __builtin_amdgcn_s_waitcnt(kWaitOneTile);  // K_t0 landed (V_t0 may be in flight)
       else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // K_t landed
       __syncthreads();  // K_t visible; every wave done with P V of tile t-1
-      if (t > 0) issue_v(t);
+      if (t > t0) issue_v(t);
       bf16x8_t pb[4];
       const bool sk = skip(t);
       if (!sk) scores(t, pb);
@@ -495,8 +535,28 @@ __global__ __launch_bounds__(256, DP >= 256 ? 1 : 2) void sdpa_fwd_kernel(Params
   // are all masked has l = 0: its output is NaN, as the reference's softmax of a
   // row of -inf gives.
   const float lt = l + __shfl_xor(l, 32, 64);
+  if (p.kv_chunk) {
+    // One split's share: o / l in fp32 and the log2-sum-exp m c + log2 l of its
+    // scaled scores (-inf, with o = 0, when none of its keys is visible).
+    if (qv) {
+      const int64_t row = ((static_cast<int64_t>(split) * p.B + b) * p.H + h) * p.Sq + qi;
+      const float winv = lt > 0.f ? 1.0f / lt : 0.f;
+      float* po = p.part_o + row * D;
+#pragma unroll
+      for (int db = 0; db < DP / 32; ++db)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int d = db * 32 + g * 8 + 4 * h2;
+          if (d >= D) continue;
+          *reinterpret_cast<float4*>(po + d) = make_float4(o[db][g * 4 + 0] * winv, o[db][g * 4 + 1] * winv,
+                                                           o[db][g * 4 + 2] * winv, o[db][g * 4 + 3] * winv);
+        }
+      if (h2 == 0) p.part_lse[row] = lt > 0.f ? m * c + __builtin_amdgcn_logf(lt) : -INFINITY;
+    }
+    return;
+  }
   const float inv = 1.0f / lt;
-  if (qi < p.Sq) {
+  if (qv) {
     uint16_t* O = static_cast<uint16_t*>(p.o) + b * p.o_sb + h * p.o_sh + static_cast<int64_t>(qi) * p.o_ss;
 #pragma unroll
     for (int db = 0; db < DP / 32; ++db)
@@ -753,6 +813,77 @@ static void launch_f32(const Params& p, int mk, dim3 grid, hipStream_t s) {
   else hipLaunchKernelGGL((sdpa_fwd_f32_kernel<DP, kNoMask>), grid, dim3(256), 0, s, p);
 }
 
+// Combine of a split key range (16-bit outputs): for each (b, h, query) row the
+// splits' outputs weighted by 2^(lse_i - max lse), summed in split order (the same
+// bits every run); a row none of whose keys is visible gets NaN, as without the
+// split.  One wave per row, four head-dim values a lane (D <= 256).
+template <bool F16>
+__global__ __launch_bounds__(256) void sdpa_combine_kernel(Params p, int ns) {
+  const int64_t rows = static_cast<int64_t>(p.B) * p.H * p.Sq;
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + threadIdx.x / 64;
+  const int d = (threadIdx.x % 64) * 4;
+  if (row >= rows || d >= p.D) return;
+  float mx = -INFINITY;
+  for (int i = 0; i < ns; ++i) mx = fmaxf(mx, p.part_lse[i * rows + row]);
+  float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f, wsum = 0.f;
+  for (int i = 0; i < ns; ++i) {
+    const float lse = p.part_lse[i * rows + row];
+    if (lse == -INFINITY) continue;
+    const float w = __builtin_amdgcn_exp2f(lse - mx);
+    const float4 v = *reinterpret_cast<const float4*>(p.part_o + (i * rows + row) * p.D + d);
+    a0 += w * v.x;
+    a1 += w * v.y;
+    a2 += w * v.z;
+    a3 += w * v.w;
+    wsum += w;
+  }
+  const bool none = mx == -INFINITY;
+  const float inv = none ? 0.f : 1.0f / wsum;
+  const float nan = __builtin_nanf("");
+  const int qi = static_cast<int>(row % p.Sq);
+  const int64_t bh = row / p.Sq;
+  const int h = static_cast<int>(bh % p.H), b = static_cast<int>(bh / p.H);
+  uint16_t* O = static_cast<uint16_t*>(p.o) + b * p.o_sb + h * p.o_sh + static_cast<int64_t>(qi) * p.o_ss + d;
+  *reinterpret_cast<uint2*>(O) = make_uint2(pack16x2<F16>(none ? nan : a0 * inv, none ? nan : a1 * inv),
+                                            pack16x2<F16>(none ? nan : a2 * inv, none ? nan : a3 * inv));
+}
+
+// Key-range splits for grids of few workgroups (decoding, short prefills), 16-bit
+// operands: below 384 (b, h, query block) workgroups (half of the 768 that fit at
+// three per CU) each one's keys are split so that the grid comes near 768, every
+// split keeping at least 4 key tiles (at most 64 splits).  ns = 1: no split.
+struct KvSplit {
+  int ns;
+  int chunk;  // keys per split (a multiple of kBKV)
+};
+// Workgroups of the kernel's grid (x): (query block, b, h), or with grouped-query
+// rows (16-bit, no causal mask, GQA, Sq < 128: decoding) (row block, b, kv head).
+struct SdpaGrid {
+  int64_t wgs;
+  bool pack;
+};
+static SdpaGrid sdpa_grid(int dtype, int64_t B, int64_t H, int64_t Hkv, int64_t Sq, int causal) {
+  const bool pack = dtype != GHIP_DTYPE_FLOAT32 && !causal && Hkv > 0 && Hkv < H && H % Hkv == 0 && Sq < kBQ;
+  if (pack) return SdpaGrid{(H / Hkv * Sq + kBQ - 1) / kBQ * B * Hkv, true};
+  return SdpaGrid{(Sq + kBQ - 1) / kBQ * B * H, false};
+}
+static KvSplit kv_split(int dtype, int64_t grid, int64_t Sk) {
+  const KvSplit none{1, 0};
+  if (dtype == GHIP_DTYPE_FLOAT32 || grid <= 0 || Sk <= 0) return none;
+  const int64_t tiles = (Sk + kBKV - 1) / kBKV;
+  if (grid >= 384 || tiles < 8) return none;
+  int64_t ns = std::min<int64_t>((768 + grid - 1) / grid, tiles / 4);
+  ns = std::min<int64_t>(ns, 64);
+  if (ns < 2) return none;
+  const int64_t per = (tiles + ns - 1) / ns;
+  ns = (tiles + per - 1) / per;
+  if (ns < 2) return none;
+  return KvSplit{static_cast<int>(ns), static_cast<int>(per * kBKV)};
+}
+static int64_t kv_split_bytes(const KvSplit& ks, int64_t B, int64_t H, int64_t Sq, int64_t D) {
+  return ks.ns > 1 ? static_cast<int64_t>(ks.ns) * B * H * Sq * (D + 1) * 4 : 0;
+}
+
 }  // namespace attn
 
 // Whether ghip_sdpa_fwd_masked takes these operands (checked again, with the
@@ -791,12 +922,19 @@ bool sdpa_fused_supported(int dtype, int64_t H, int64_t Hkv, int64_t Sq, int64_t
 
 using namespace ghip;
 
-extern "C" int ghip_sdpa_fwd_masked(int dtype, const void* q, const void* k, const void* v, void* o,
-                                    int64_t B, int64_t H, int64_t Hkv, int64_t Sq, int64_t Sk, int64_t D,
-                                    const int64_t* q_strides, const int64_t* k_strides,
-                                    const int64_t* v_strides, const int64_t* o_strides, const void* mask,
-                                    int mask_dtype, const int64_t* mask_strides, float scale, int causal,
-                                    void* stream, GHipError* err) {
+extern "C" int64_t ghip_sdpa_workspace_bytes(int dtype, int64_t B, int64_t H, int64_t Hkv, int64_t Sq, int64_t Sk,
+                                             int64_t D, int causal) {
+  if (B <= 0 || H <= 0 || Hkv <= 0 || Sq <= 0 || Sk <= 0 || D <= 0) return 0;
+  const attn::SdpaGrid g = attn::sdpa_grid(dtype, B, H, Hkv, Sq, causal);
+  return attn::kv_split_bytes(attn::kv_split(dtype, g.wgs, Sk), B, H, Sq, D);
+}
+
+extern "C" int ghip_sdpa_fwd_masked_ws(int dtype, const void* q, const void* k, const void* v, void* o,
+                                       int64_t B, int64_t H, int64_t Hkv, int64_t Sq, int64_t Sk, int64_t D,
+                                       const int64_t* q_strides, const int64_t* k_strides,
+                                       const int64_t* v_strides, const int64_t* o_strides, const void* mask,
+                                       int mask_dtype, const int64_t* mask_strides, float scale, int causal,
+                                       void* workspace, int64_t workspace_bytes, void* stream, GHipError* err) {
   if (B < 0 || H <= 0 || Hkv <= 0 || Sq < 0 || Sk < 0 || D <= 0)
     return set_error(err, GHIP_ERR_INVALID_ARG, "sdpa_fwd: bad sizes");
   if (H % Hkv != 0)
@@ -822,7 +960,9 @@ extern "C" int ghip_sdpa_fwd_masked(int dtype, const void* q, const void* k, con
     return set_error(err, GHIP_ERR_UNSUPPORTED, "sdpa_fwd: q/k/v must be 16-byte aligned, o %d-byte aligned",
                      static_cast<int>(4 * es));
   const int64_t nqb = (Sq + attn::kBQ - 1) / attn::kBQ;
-  if (nqb * B * H > 0x7fffffffLL) return set_error(err, GHIP_ERR_INVALID_ARG, "sdpa_fwd: problem too large");
+  const attn::SdpaGrid sg = attn::sdpa_grid(dtype, B, H, Hkv, Sq, causal);
+  if (nqb * B * H > 0x7fffffffLL || sg.wgs > 0x7fffffffLL)
+    return set_error(err, GHIP_ERR_INVALID_ARG, "sdpa_fwd: problem too large");
   attn::Params p{};
   p.q = q; p.k = k; p.v = v; p.o = o;
   p.q_sb = q_strides[0]; p.q_sh = q_strides[1]; p.q_ss = q_strides[2];
@@ -850,7 +990,21 @@ extern "C" int ghip_sdpa_fwd_masked(int dtype, const void* q, const void* k, con
     const int64_t mes = mask_dtype == GHIP_DTYPE_BOOL ? 1 : es;
     p.mask_vec = p.m_sk == 1 && p.m_sb % 4 == 0 && p.m_sh % 4 == 0 && p.m_sq % 4 == 0 && al(mask, 4 * mes);
   }
-  const dim3 grid(static_cast<unsigned>(nqb * B * H));
+  // A split key range when a workspace is given and the grid is small.
+  p.gqa_pack = sg.pack ? 1 : 0;
+  const attn::KvSplit kvs = workspace ? attn::kv_split(dtype, sg.wgs, Sk) : attn::KvSplit{1, 0};
+  const int64_t rows = B * H * Sq;
+  if (kvs.ns > 1) {
+    const int64_t need = attn::kv_split_bytes(kvs, B, H, Sq, D);
+    if (workspace_bytes < need)
+      return set_error(err, GHIP_ERR_INVALID_ARG, "sdpa_fwd: workspace of %lld bytes, %lld needed",
+                       static_cast<long long>(workspace_bytes), static_cast<long long>(need));
+    if (!al(workspace, 16)) return set_error(err, GHIP_ERR_INVALID_ARG, "sdpa_fwd: workspace must be 16-byte aligned");
+    p.kv_chunk = kvs.chunk;
+    p.part_o = static_cast<float*>(workspace);
+    p.part_lse = p.part_o + static_cast<int64_t>(kvs.ns) * rows * D;
+  }
+  const dim3 grid(static_cast<unsigned>(sg.wgs), static_cast<unsigned>(kvs.ns));
   const hipStream_t s = static_cast<hipStream_t>(stream);
   const bool f16 = dtype == GHIP_DTYPE_FLOAT16;
   // Key tiles of the longest workgroup: the split K / V schedule (no mask) unless
@@ -873,7 +1027,23 @@ extern "C" int ghip_sdpa_fwd_masked(int dtype, const void* q, const void* k, con
     else attn::launch_d<256, false>(p, mk, grid, split, big, s);
   }
   GHIP_CHECK(hipGetLastError(), err);
+  if (kvs.ns > 1) {
+    const dim3 cgrid(static_cast<unsigned>((rows + 3) / 4));
+    if (f16) hipLaunchKernelGGL((attn::sdpa_combine_kernel<true>), cgrid, dim3(256), 0, s, p, kvs.ns);
+    else hipLaunchKernelGGL((attn::sdpa_combine_kernel<false>), cgrid, dim3(256), 0, s, p, kvs.ns);
+    GHIP_CHECK(hipGetLastError(), err);
+  }
   return GHIP_OK;
+}
+
+extern "C" int ghip_sdpa_fwd_masked(int dtype, const void* q, const void* k, const void* v, void* o,
+                                    int64_t B, int64_t H, int64_t Hkv, int64_t Sq, int64_t Sk, int64_t D,
+                                    const int64_t* q_strides, const int64_t* k_strides,
+                                    const int64_t* v_strides, const int64_t* o_strides, const void* mask,
+                                    int mask_dtype, const int64_t* mask_strides, float scale, int causal,
+                                    void* stream, GHipError* err) {
+  return ghip_sdpa_fwd_masked_ws(dtype, q, k, v, o, B, H, Hkv, Sq, Sk, D, q_strides, k_strides, v_strides, o_strides,
+                                 mask, mask_dtype, mask_strides, scale, causal, nullptr, 0, stream, err);
 }
 
 extern "C" int ghip_sdpa_fwd(int dtype, const void* q, const void* k, const void* v, void* o,

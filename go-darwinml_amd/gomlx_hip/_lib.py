@@ -59,12 +59,21 @@ SIGNATURES = {
                              ctypes.POINTER(_i64), ctypes.POINTER(_i64), ctypes.POINTER(_i64),
                              ctypes.POINTER(_i64), _vp, _int, ctypes.POINTER(_i64), _f32, _int, _vp,
                              _errp],
+    "ghip_sdpa_fwd_masked_ws": [_int, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64,
+                                ctypes.POINTER(_i64), ctypes.POINTER(_i64), ctypes.POINTER(_i64),
+                                ctypes.POINTER(_i64), _vp, _int, ctypes.POINTER(_i64), _f32, _int, _vp, _i64,
+                                _vp, _errp],
     "ghip_scale_mask_softmax_rows_ex": [_int, _vp, _vp, _i64, _i64, _i64, _i64, _f32, _int, _vp, _int,
                                         ctypes.POINTER(_i64), _vp, _errp],
     "ghip_copy_strided": [_int, _vp, _vp, _int, ctypes.POINTER(_i64), ctypes.POINTER(_i64),
                           ctypes.POINTER(_i64), _vp, _errp],
     "ghip_softmax_cols": [_int, _vp, _vp, _i64, _i64, _i64, _int, _vp, _errp],
     "ghip_layernorm_cols": [_int, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _f32, _vp, _errp],
+}
+
+# name -> argtypes of the entry points that return int64_t.
+SIGNATURES_I64 = {
+    "ghip_sdpa_workspace_bytes": [_int, _i64, _i64, _i64, _i64, _i64, _i64, _int],
 }
 
 _lib = None
@@ -84,6 +93,10 @@ def load():
         fn = getattr(L, name)
         fn.argtypes = argtypes
         fn.restype = ctypes.c_int
+    for name, argtypes in SIGNATURES_I64.items():
+        fn = getattr(L, name)
+        fn.argtypes = argtypes
+        fn.restype = ctypes.c_int64
     L.ghip_version.argtypes = []
     L.ghip_version.restype = ctypes.c_char_p
     L.ghip_error_clear.argtypes = [_errp]

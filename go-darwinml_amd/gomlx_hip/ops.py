@@ -176,18 +176,19 @@ def _strides3(t: torch.Tensor):
     return (ctypes.c_int64 * 3)(t.stride(0), t.stride(1), t.stride(2))
 
 
-def sdpa(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: float, causal: bool,
-         out=None, stream=None):
-    """Fused attention: q [B,H,Sq,D], k / v [B,Hkv,Sk,D] (any strides with a contiguous
-    head dim, e.g. BSHD storage viewed as BHSD) -> out [B,H,Sq,D]."""
-    _check_dev(q, k, v)
+def sdpa_workspace(q: torch.Tensor, Hkv: int, Sk: int, causal: bool):
+    """Workspace for ghip_sdpa_fwd_masked_ws (None when the shape takes no key split)."""
     B, H, Sq, D = q.shape
-    _, Hkv, Sk, _ = k.shape
-    o = torch.empty((B, H, Sq, D), dtype=q.dtype, device=q.device) if out is None else out
-    call("ghip_sdpa_fwd", dtype_code(q.dtype), q.data_ptr(), k.data_ptr(), v.data_ptr(),
-         o.data_ptr(), B, H, Hkv, Sq, Sk, D, _strides3(q), _strides3(k), _strides3(v),
-         _strides3(o), float(scale), int(causal), _stream(stream))
-    return o
+    n = _lib.load().ghip_sdpa_workspace_bytes(dtype_code(q.dtype), B, H, Hkv, Sq, Sk, D, int(causal))
+    return torch.empty((n,), dtype=torch.uint8, device=q.device) if n > 0 else None
+
+
+def sdpa(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: float, causal: bool,
+         out=None, stream=None, kv_split: bool = True):
+    """Fused attention: q [B,H,Sq,D], k / v [B,Hkv,Sk,D] (any strides with a contiguous
+    head dim, e.g. BSHD storage viewed as BHSD) -> out [B,H,Sq,D].  kv_split: with a
+    workspace, so small grids split their key range (ghip_sdpa_fwd_masked_ws)."""
+    return sdpa_masked(q, k, v, None, scale, causal, out=out, stream=stream, kv_split=kv_split)
 
 
 def _mask_strides(mask: torch.Tensor, B, H, Sq, Sk):
@@ -205,18 +206,20 @@ def _mask_strides(mask: torch.Tensor, B, H, Sq, Sk):
 
 
 def sdpa_masked(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, mask, scale: float, causal: bool,
-                out=None, stream=None):
+                out=None, stream=None, kv_split: bool = True):
     """sdpa with a bool keep-mask or an additive mask (q's dtype) of any rank that
-    broadcasts to the scores [B, H, Sq, Sk]."""
-    _check_dev(q, k, v, mask)
+    broadcasts to the scores [B, H, Sq, Sk] (mask None: none)."""
+    _check_dev(q, k, v, *([mask] if mask is not None else []))
     B, H, Sq, D = q.shape
     _, Hkv, Sk, _ = k.shape
     o = torch.empty((B, H, Sq, D), dtype=q.dtype, device=q.device) if out is None else out
     mdt = -1 if mask is None else dtype_code(mask.dtype)
     ms = None if mask is None else _mask_strides(mask, B, H, Sq, Sk)
-    call("ghip_sdpa_fwd_masked", dtype_code(q.dtype), q.data_ptr(), k.data_ptr(), v.data_ptr(),
+    ws = sdpa_workspace(q, Hkv, Sk, causal) if kv_split else None
+    call("ghip_sdpa_fwd_masked_ws", dtype_code(q.dtype), q.data_ptr(), k.data_ptr(), v.data_ptr(),
          o.data_ptr(), B, H, Hkv, Sq, Sk, D, _strides3(q), _strides3(k), _strides3(v),
-         _strides3(o), _ptr(mask), mdt, ms, float(scale), int(causal), _stream(stream))
+         _strides3(o), _ptr(mask), mdt, ms, float(scale), int(causal), _ptr(ws),
+         0 if ws is None else ws.numel(), _stream(stream))
     return o
 
 

@@ -202,6 +202,25 @@ int ghip_sdpa_fwd_masked(int dtype, const void* q, const void* k, const void* v,
                          int mask_dtype, const int64_t* mask_strides, float scale, int causal,
                          void* stream, GHipError* err);
 
+/* ghip_sdpa_fwd_masked with a caller-provided workspace (the same
+ * FusedScaledDotProductAttention, function.go:2669-2907).  With a workspace of
+ * ghip_sdpa_workspace_bytes() bytes (16-byte aligned) a grid of few (batch, head,
+ * 128-query block) workgroups (decoding, short prefills; 16-bit operands) splits
+ * each workgroup's key range over several workgroups and merges their outputs by
+ * log-sum-exp in a second kernel (without a causal mask, grouped-query heads of
+ * one kv head also share workgroups when Sq < 128, with or without a workspace): the result agrees with the unsplit one to
+ * rounding (same tolerance against the reference), and is the same bits every
+ * run.  workspace NULL or ghip_sdpa_workspace_bytes() == 0: no split.  Calls that
+ * share one workspace on different streams race. */
+int64_t ghip_sdpa_workspace_bytes(int dtype, int64_t B, int64_t H, int64_t Hkv, int64_t Sq, int64_t Sk,
+                                  int64_t D, int causal);
+int ghip_sdpa_fwd_masked_ws(int dtype, const void* q, const void* k, const void* v, void* o,
+                            int64_t B, int64_t H, int64_t Hkv, int64_t Sq, int64_t Sk, int64_t D,
+                            const int64_t* q_strides, const int64_t* k_strides,
+                            const int64_t* v_strides, const int64_t* o_strides, const void* mask,
+                            int mask_dtype, const int64_t* mask_strides, float scale, int causal,
+                            void* workspace, int64_t workspace_bytes, void* stream, GHipError* err);
+
 /* Embedding lookup: out[i, :] = table[clamp(ids[i], 0, V-1), :] (row_bytes per
  * row, copied bit-exactly).  Replaces the gather fast path
  * (gather.go:61-203 -> mpsgraph_gather_along_axis, bridge.m:764-782). */

@@ -35,7 +35,8 @@ def test_library_exports_every_declared_symbol():
 def test_python_signatures_cover_header():
     # Every declared entry point has a ctypes signature, so no call goes untyped.
     from gomlx_hip import backend
-    sigs = set(_lib.SIGNATURES) | set(backend._GRAPH_SIGS) | {"ghip_version", "ghip_error_clear"}
+    sigs = set(_lib.SIGNATURES) | set(_lib.SIGNATURES_I64) | set(backend._GRAPH_SIGS) | {"ghip_version",
+                                                                                          "ghip_error_clear"}
     extra = declared_symbols() - sigs
     assert not extra, f"no ctypes signature for {sorted(extra)}"
 
@@ -54,3 +55,23 @@ def test_error_path_without_gpu():
     with pytest.raises(_lib.BackendError) as ei:
         _lib.call("ghip_softmax_rows", 99, None, None, 4, 4, 0, None)
     assert ei.value.code in (1, 2)
+
+
+def test_sdpa_workspace_policy():
+    """Host-side policy of the split key range (no GPU call): a workspace only for
+    16-bit grids of few workgroups with at least 8 key tiles, its size covering
+    every split's partial rows (D + 1 floats a row).  Without a causal mask,
+    grouped-query heads of one kv head share workgroups when Sq < 128 (decoding):
+    B8 H32 Hkv8 Sq1 is 64 workgroups, so 12 splits."""
+    L = _lib.load()
+    ws = L.ghip_sdpa_workspace_bytes
+    BF16, F32 = _lib.DT_BFLOAT16, _lib.DT_FLOAT32
+    assert ws(BF16, 8, 32, 8, 1, 8192, 128, 0) == 12 * 8 * 32 * 1 * 129 * 4
+    assert ws(BF16, 8, 32, 8, 1, 8192, 128, 1) == 3 * 8 * 32 * 1 * 129 * 4   # causal: 256 workgroups
+    assert ws(BF16, 8, 32, 32, 1, 8192, 128, 0) == 3 * 8 * 32 * 1 * 129 * 4  # no GQA: 256 workgroups
+    assert ws(BF16, 1, 32, 8, 1, 32768, 128, 0) == 64 * 32 * 1 * 129 * 4     # 8 workgroups, at most 64 splits
+    assert ws(BF16, 4, 16, 16, 2048, 2048, 128, 1) == 0     # the config: 1024 workgroups
+    assert ws(F32, 1, 2, 2, 1, 8192, 128, 0) == 0           # fp32 never splits
+    assert ws(BF16, 1, 2, 2, 1, 448, 128, 0) == 0           # fewer than 8 key tiles
+    assert ws(BF16, 1, 4, 4, 1, 777, 128, 0) == 3 * 4 * 1 * 129 * 4
+    assert ws(BF16, 0, 4, 4, 1, 777, 128, 0) == 0

@@ -62,7 +62,10 @@ CASES = [  # (B, H, Hkv, Sq, Sk, causal)
 @pytest.mark.parametrize("case", CASES)
 @pytest.mark.parametrize("D", [64, 128])
 @pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])
-def test_sdpa_matches_oracle(cuda, case, D, dt):
+@pytest.mark.parametrize("kv_split", [True, False])
+def test_sdpa_matches_oracle(cuda, case, D, dt, kv_split):
+    """kv_split: with a workspace (ghip_sdpa_fwd_masked_ws), so the grids small
+    enough split their key range; without one every case runs unsplit."""
     B, H, Hkv, Sq, Sk, causal = case
     q = r16(synth.normal(4001 + Sq, (B, H, Sq, D)), dt)
     k = r16(synth.normal(4002 + Sk, (B, Hkv, Sk, D)), dt)
@@ -70,9 +73,98 @@ def test_sdpa_matches_oracle(cuda, case, D, dt):
     scale = D ** -0.5
     ref = orc.sdpa(q, k, v, scale=scale, causal=causal)
     tq, tk, tv = (dev(a, cuda, dt) for a in (q, k, v))
-    got = ops.sdpa(tq, tk, tv, scale, causal).float().cpu().numpy()
+    got = ops.sdpa(tq, tk, tv, scale, causal, kv_split=kv_split).float().cpu().numpy()
     assert norm_err(got, ref) <= 1e-2
     assert rel_err(got, ref) <= 2.5e-2
+
+
+# Grids of few (batch, head, query block) workgroups with long key ranges: the key
+# range splits over several workgroups (ghip_sdpa_workspace_bytes > 0) and a second
+# kernel merges them by log-sum-exp.
+SPLIT_CASES = [  # (B, H, Hkv, Sq, Sk, causal)
+    (2, 8, 2, 1, 4096, False),     # decoding, GQA 4:1
+    (1, 4, 4, 16, 2048, False),    # a few queries
+    (1, 4, 1, 1, 777, False),      # ragged last split (keys 640 .. 776)
+    (1, 2, 2, 200, 1500, True),    # causal, Sq < Sk: splits past the diagonal hold no keys
+    (3, 2, 1, 130, 3000, False),   # two query blocks, ragged
+    (1, 8, 2, 40, 1024, False),    # grouped-query rows: 4 heads x 40 queries, two row blocks
+    (2, 6, 3, 5, 700, False),      # grouped-query rows: 2 heads x 5 queries, ragged keys
+]
+
+
+@pytest.mark.parametrize("case", [(2, 8, 2, 3, 300, False), (1, 12, 4, 50, 200, False), (1, 16, 1, 1, 64, False)])
+@pytest.mark.parametrize("D,dt", [(64, torch.bfloat16), (128, torch.float16), (256, torch.bfloat16)])
+@pytest.mark.parametrize("kv_split", [True, False])
+def test_sdpa_grouped_query_rows_match_oracle(cuda, case, D, dt, kv_split):
+    """GQA without a causal mask and Sq < 128: the (head, query) rows of each kv
+    head's group share workgroups (3 heads x 50 queries span two row blocks; 16
+    heads of one query), with and without a workspace."""
+    B, H, Hkv, Sq, Sk, causal = case
+    q = r16(synth.normal(4121 + Sq, (B, H, Sq, D)), dt)
+    k = r16(synth.normal(4122 + Sk, (B, Hkv, Sk, D)), dt)
+    v = r16(synth.normal(4123 + Sk, (B, Hkv, Sk, D)), dt)
+    scale = D ** -0.5
+    ref = orc.sdpa(q, k, v, scale=scale, causal=causal)
+    got = ops.sdpa(*(dev(a, cuda, dt) for a in (q, k, v)), scale, causal, kv_split=kv_split)
+    got = got.float().cpu().numpy()
+    assert norm_err(got, ref) <= 1e-2
+    assert rel_err(got, ref) <= 2.5e-2
+
+
+@pytest.mark.parametrize("case", SPLIT_CASES)
+@pytest.mark.parametrize("D,dt", [(64, torch.bfloat16), (128, torch.bfloat16), (128, torch.float16),
+                                  (256, torch.bfloat16), (96, torch.float16)])
+def test_sdpa_split_key_range_matches_oracle(cuda, case, D, dt):
+    B, H, Hkv, Sq, Sk, causal = case
+    assert ops.sdpa_workspace(torch.empty((B, H, Sq, D), dtype=dt, device=cuda), Hkv, Sk, causal) is not None
+    q = r16(synth.normal(4101 + Sq, (B, H, Sq, D)), dt)
+    k = r16(synth.normal(4102 + Sk, (B, Hkv, Sk, D)), dt)
+    v = r16(synth.normal(4103 + Sk, (B, Hkv, Sk, D)), dt)
+    scale = D ** -0.5
+    ref = orc.sdpa(q, k, v, scale=scale, causal=causal)
+    tq, tk, tv = (dev(a, cuda, dt) for a in (q, k, v))
+    got = ops.sdpa(tq, tk, tv, scale, causal)
+    again = ops.sdpa(tq, tk, tv, scale, causal)
+    assert torch.equal(got, again)  # the merge is in a fixed order
+    got = got.float().cpu().numpy()
+    assert norm_err(got, ref) <= 1e-2
+    assert rel_err(got, ref) <= 2.5e-2
+    unsplit = ops.sdpa(tq, tk, tv, scale, causal, kv_split=False).float().cpu().numpy()
+    assert norm_err(got, unsplit) <= 1e-2
+
+
+@pytest.mark.parametrize("kind", ["bool", "add"])
+@pytest.mark.parametrize("mh", [1, 4])
+def test_sdpa_split_key_range_masks(cuda, kind, mh):
+    """Decoding shapes (grouped-query rows, split key range) with a bool keep-mask or
+    an additive mask, broadcast over heads (mh 1) or per head (mh 4), one query row
+    fully masked (NaN, as unsplit)."""
+    B, H, Hkv, Sq, Sk, D = 2, 4, 2, 2, 3000, 128
+    dt = torch.bfloat16
+    q = r16(synth.normal(4111, (B, H, Sq, D)), dt)
+    k = r16(synth.normal(4112, (B, Hkv, Sk, D)), dt)
+    v = r16(synth.normal(4113, (B, Hkv, Sk, D)), dt)
+    rng = np.random.default_rng(4114 + mh)
+    keep = rng.random((B, mh, Sq, Sk)) > 0.3
+    keep[1, :, 1, :] = False
+    if kind == "bool":
+        mask = keep
+        tm = torch.from_numpy(keep).to(cuda)
+    else:
+        mask = r16(np.where(keep, rng.normal(0.0, 1.0, keep.shape), -np.inf).astype(np.float32), dt)
+        tm = dev(mask, cuda, dt)
+    scale = D ** -0.5
+    if kind == "bool":
+        ref = orc.sdpa(q, k, v, scale=scale, causal=False, mask=mask)
+    else:
+        ref = orc.sdpa(q, k, v, scale=scale, causal=False, additive=mask)
+    tq, tk, tv = (dev(a, cuda, dt) for a in (q, k, v))
+    got = ops.sdpa_masked(tq, tk, tv, tm, scale, False).float().cpu().numpy()
+    assert np.all(np.isnan(got[1, :, 1]))
+    ok = ~np.isnan(ref)
+    assert np.array_equal(ok, ~np.isnan(got))
+    assert norm_err(got[ok], ref[ok]) <= 1e-2
+    assert rel_err(got[ok], ref[ok]) <= 2.5e-2
 
 
 @pytest.mark.parametrize("case", [CASES[0], CASES[2], CASES[3], CASES[4], CASES[5], CASES[6]])
