@@ -6,7 +6,8 @@ one "step" is one RMSNorm launch over that batch, inputs resident in HBM.
 `value` is GB/s of algorithmic traffic (read x + gamma, write y).  The same line
 carries the other BASELINE workloads under "secondary" (softmax, bf16 RMSNorm,
 LayerNorm, bf16/fp32 DotGeneral, the bf16 DotGeneral's per-GPU shard under 8-way
-data parallelism (batch 0 alone), the attention composite, the transformer block)
+data parallelism (batch 0 alone), the attention composite, a decoding step of
+grouped-query attention over an 8192-token KV cache, the transformer block)
 and two widened ops (FusedDense + GELU, the embedding-gradient ScatterSum), each
 with its own roofline fraction.
 
@@ -435,6 +436,39 @@ def make_cases(only=None):
                                         "counted for both products over the full S x S matrix, "
                                         "the causal half above the diagonal is skipped"})
 
+    def decode_case():
+        """One decoding step of grouped-query attention: B8 H32 (8 kv heads) over an
+        8192-token KV cache, D128, bf16, no causal mask (the new token sees the whole
+        cache).  HBM-bound: bytes = K and V read + Q read + O written.  The four query
+        heads of a kv head share workgroups and each key range is split over
+        several (12 splits, a log-sum-exp combine kernel after)."""
+        B, H, Hkv, Sk, D = 8, 32, 8, 8192, 128
+        nbytes = 2 * B * Hkv * Sk * D * 2 + 2 * B * H * D * 2
+        rot = rotation_for(nbytes)
+        q = nd(4501, (B, H, 1, D), dtype=torch.bfloat16)
+        k = nd(4502, (B, Hkv, Sk, D), dtype=torch.bfloat16)
+        v = nd(4503, (B, Hkv, Sk, D), dtype=torch.bfloat16)
+        ks, vs = rotated(k, rot), rotated(v, rot)
+        outs = [torch.empty_like(q) for _ in range(rot)]
+        ws = ops.sdpa_workspace(q, Hkv, Sk, False)
+        qh, kh, vh = host32(q[:1]), host32(k[:1]), host32(v[:1])
+        b1 = nbytes // B
+
+        def leg(budget_s):
+            reps, dt = cpu_rate(lambda: orc.sdpa(qh, kh, vh, scale=D ** -0.5, causal=False), budget_s)
+            return cpu_entry(b1 * reps / dt / 1e9, "GB/s",
+                             f"oracle/oracle.c orc_sdpa (fp64), OpenMP {cpu_threads()} threads, on batch 0 "
+                             f"(32 heads over 8 kv heads of 8192 keys) of the same bf16 Q, K, V; bytes as on "
+                             f"the GPU line; {reps} repetitions in {dt:.1f} s")
+        return Case("attention_decode_bf16",
+                    lambda i: ops.sdpa(q, ks[i % rot], vs[i % rot], D ** -0.5, False, out=outs[i % rot],
+                                       workspace=ws),
+                    bytes_per_step=nbytes, dtype="bf16", rotation=rot,
+                    kernel="sdpa_fwd_kernel<128, false, 0, true> + sdpa_combine_kernel<false> (decode)",
+                    out=lambda i: outs[i % rot], cpu=leg,
+                    config={"workload": "SDPA decoding step: Q [8,32,1,128], K / V [8,8,8192,128] bf16 ~ N(0,1) "
+                                        "(GQA 4:1), no causal mask; bytes: K + V + Q read, O written"})
+
     def transformer_case():
         """BASELINE configs[4] through the graph API: Builder -> Compile -> Execute of
         the whole decoder block (gather, RMSNorm, QKV/O projections, fused causal
@@ -570,6 +604,7 @@ def make_cases(only=None):
         "dot_general_bf16_shard": lambda: shard_dot_case(False),
         "dot_general_bf16_shard_hipblaslt": lambda: shard_dot_case(True),
         "attention_bf16": attention_case,
+        "attention_decode_bf16": decode_case,
         "transformer_block_bf16": transformer_case,
         "fused_dense_gelu_bf16": dense_case,
         "scatter_sum_bf16": scatter_case,

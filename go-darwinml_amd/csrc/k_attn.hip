@@ -473,8 +473,10 @@ __global__ __launch_bounds__(256, DP >= 256 ? 1 : 2) void sdpa_fwd_kernel(Params
       for (int db = 0; db < DP / 32; ++db) o[db] = mma<F16>(frag_v<DP>(sv, db, s, lane), pb[s], o[db]);
   };
   // Causal: a wave whose last query precedes tile t's first key has nothing to do
-  // there (it still takes part in the barriers and loads).
-  auto skip = [&](int t) { return p.causal && t * kBKV > qw + kQW - 1; };
+  // there; neither has a wave without rows (decoding: a handful of rows in the
+  // first wave).  It still takes part in the barriers and loads.
+  const bool wave_rows = __builtin_amdgcn_ballot_w64(qv) != 0;
+  auto skip = [&](int t) { return !wave_rows || (p.causal && t * kBKV > qw + kQW - 1); };
 
   if constexpr (!SPLIT) {
     // Two barriers per tile: the first once every wave has finished reading tile

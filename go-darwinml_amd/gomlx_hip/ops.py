@@ -184,11 +184,13 @@ def sdpa_workspace(q: torch.Tensor, Hkv: int, Sk: int, causal: bool):
 
 
 def sdpa(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: float, causal: bool,
-         out=None, stream=None, kv_split: bool = True):
+         out=None, stream=None, kv_split: bool = True, workspace=None):
     """Fused attention: q [B,H,Sq,D], k / v [B,Hkv,Sk,D] (any strides with a contiguous
     head dim, e.g. BSHD storage viewed as BHSD) -> out [B,H,Sq,D].  kv_split: with a
-    workspace, so small grids split their key range (ghip_sdpa_fwd_masked_ws)."""
-    return sdpa_masked(q, k, v, None, scale, causal, out=out, stream=stream, kv_split=kv_split)
+    workspace (`workspace`, or one allocated here), so small grids split their key
+    range (ghip_sdpa_fwd_masked_ws)."""
+    return sdpa_masked(q, k, v, None, scale, causal, out=out, stream=stream, kv_split=kv_split,
+                       workspace=workspace)
 
 
 def _mask_strides(mask: torch.Tensor, B, H, Sq, Sk):
@@ -206,7 +208,7 @@ def _mask_strides(mask: torch.Tensor, B, H, Sq, Sk):
 
 
 def sdpa_masked(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, mask, scale: float, causal: bool,
-                out=None, stream=None, kv_split: bool = True):
+                out=None, stream=None, kv_split: bool = True, workspace=None):
     """sdpa with a bool keep-mask or an additive mask (q's dtype) of any rank that
     broadcasts to the scores [B, H, Sq, Sk] (mask None: none)."""
     _check_dev(q, k, v, *([mask] if mask is not None else []))
@@ -215,7 +217,7 @@ def sdpa_masked(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, mask, scale: 
     o = torch.empty((B, H, Sq, D), dtype=q.dtype, device=q.device) if out is None else out
     mdt = -1 if mask is None else dtype_code(mask.dtype)
     ms = None if mask is None else _mask_strides(mask, B, H, Sq, Sk)
-    ws = sdpa_workspace(q, Hkv, Sk, causal) if kv_split else None
+    ws = (workspace if workspace is not None else sdpa_workspace(q, Hkv, Sk, causal)) if kv_split else None
     call("ghip_sdpa_fwd_masked_ws", dtype_code(q.dtype), q.data_ptr(), k.data_ptr(), v.data_ptr(),
          o.data_ptr(), B, H, Hkv, Sq, Sk, D, _strides3(q), _strides3(k), _strides3(v),
          _strides3(o), _ptr(mask), mdt, ms, float(scale), int(causal), _ptr(ws),
