@@ -479,6 +479,35 @@ def test_graph_sdpa_gqa_causal(be, layout):
 
 
 @pytest.mark.parametrize("layout", [AxesLayout.BHSD, AxesLayout.BSHD])
+def test_graph_sdpa_decoding(be, layout):
+    """One decoding step through the graph API: Q of one query against a 3000-token
+    KV cache, GQA 4:1, no causal mask.  The plan splits each workgroup's key range
+    (its workspace in the arena) and packs the four query heads of a kv head into
+    one workgroup; the result against the oracle."""
+    B, H, Hkv, Sq, Sk, D = 2, 8, 2, 1, 3000, 128
+    q = _bf(synth.normal(4901, (B, H, Sq, D)))
+    k = _bf(synth.normal(4902, (B, Hkv, Sk, D)))
+    v = _bf(synth.normal(4903, (B, Hkv, Sk, D)))
+    ref = orc.sdpa(q, k, v, scale=D ** -0.5, causal=False)
+    t = (lambda a: np.ascontiguousarray(a.transpose(0, 2, 1, 3))) if layout == AxesLayout.BSHD else (lambda a: a)
+    b = be.Builder("decode")
+    f = b.Main()
+    ps = [f.Parameter(n, make_shape(BF16, *t(a).shape)) for n, a in (("q", q), ("k", k), ("v", v))]
+    f.Return([f.FusedScaledDotProductAttention(*ps, None, H, Hkv, layout, D ** -0.5, False)])
+    ex = b.Compile()
+    plan = ex.Plan()
+    assert "fused attention, key range split" in plan, plan
+    (r,) = ex.Execute([be.BufferFromFlatData(0, t(a), make_shape(BF16, *t(a).shape)) for a in (q, k, v)], None, 0)
+    s = be.BufferShape(r)
+    y = synth.bf16_bits_to_f32(be.BufferToFlatData(r).reshape(s.dims))
+    ex.Finalize()
+    if layout == AxesLayout.BSHD:
+        y = y.transpose(0, 2, 1, 3)
+    assert norm_err(y, ref) <= 1e-2
+    assert rel_err(y, ref) <= 2.5e-2
+
+
+@pytest.mark.parametrize("layout", [AxesLayout.BHSD, AxesLayout.BSHD])
 @pytest.mark.parametrize("dt,D,kind", [(BF16, 128, "bool"), (BF16, 64, "add"), (dtypes.Float16, 128, "add"),
                                        (BF16, 96, "bool"), (F32, 64, "add"), (F32, 96, "bool"),
                                        (BF16, 100, "add"), (F32, 144, "bool")])

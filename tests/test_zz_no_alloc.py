@@ -7,7 +7,7 @@ import numpy as np
 import pytest
 
 from gomlx_hip import graphs, synth
-from gomlx_hip.backend import Backend, BackendError, dtypes, make_shape
+from gomlx_hip.backend import AxesLayout, Backend, BackendError, dtypes, make_shape
 
 pytestmark = pytest.mark.gpu
 
@@ -52,6 +52,22 @@ def _scatter_case(be, V, D, n, seed):
     return ex, [be.BufferFromFlatData(0, a, sh) for a, sh in host]
 
 
+def _decode_case(be, B, H, Hkv, Sk, D, seed):
+    """One decoding step of grouped-query attention: its key range splits over a
+    workspace in the arena (the scratch array here)."""
+    b = be.Builder("decode_noalloc")
+    f = b.Main()
+    q = f.Parameter("q", make_shape(BF16, B, H, 1, D))
+    k = f.Parameter("k", make_shape(BF16, B, Hkv, Sk, D))
+    v = f.Parameter("v", make_shape(BF16, B, Hkv, Sk, D))
+    f.Return([f.FusedScaledDotProductAttention(q, k, v, None, H, Hkv, AxesLayout.BHSD, D ** -0.5, False)])
+    ex = b.Compile()
+    assert "key range split" in ex.Plan(), ex.Plan()
+    host = [synth.normal(seed, (B, H, 1, D)), synth.normal(seed + 1, (B, Hkv, Sk, D)),
+            synth.normal(seed + 2, (B, Hkv, Sk, D))]
+    return ex, [be.BufferFromFlatData(0, a, make_shape(BF16, *a.shape)) for a in host]
+
+
 def _compare(be, ex, bufs):
     ref = ex.Execute(bufs, None, 0)
     outs = [be.NewSharedBuffer(0, s) for s in ex.Outputs()]
@@ -64,8 +80,8 @@ def _compare(be, ex, bufs):
 
 def test_noalloc_matches_execute_two_calls_second_smaller(be):
     """A transformer block (intermediates in the scratch array), then a smaller one;
-    then a scatter graph, then a smaller scatter graph: each bit-identical to
-    Execute on the same executable and inputs."""
+    then a scatter graph, then a smaller scatter graph, then two decoding attention
+    steps: each bit-identical to Execute on the same executable and inputs."""
     big = graphs.TransformerBlockConfig(batch=2, seq=256, vocab=2000, d_model=512, heads=4, head_dim=128, ffn=2048)
     small = graphs.TransformerBlockConfig(batch=1, seq=128, vocab=1000, d_model=256, heads=2, head_dim=128, ffn=1024)
     for cfg, seed in ((big, 7100), (small, 7200)):
@@ -74,6 +90,10 @@ def test_noalloc_matches_execute_two_calls_second_smaller(be):
         _compare(be, ex, bufs)
     for (V, D, n), seed in (((4000, 512, 3000), 7300), ((500, 256, 700), 7400)):
         ex, bufs = _scatter_case(be, V, D, n, seed)
+        _compare(be, ex, bufs)
+    # decoding attention: the split key range's partial outputs in the arena
+    for (B, H, Hkv, Sk, D), seed in (((4, 16, 4, 6000, 128), 7500), ((1, 8, 2, 1500, 64), 7600)):
+        ex, bufs = _decode_case(be, B, H, Hkv, Sk, D, seed)
         _compare(be, ex, bufs)
 
 
