@@ -62,12 +62,16 @@ def test_sdpa_workspace_policy():
     16-bit grids of few workgroups with at least 8 key tiles, its size covering
     every split's partial rows (D + 1 floats a row).  Without a causal mask,
     grouped-query heads of one kv head share workgroups when Sq < 128 (decoding):
-    B8 H32 Hkv8 Sq1 is 64 workgroups, so 12 splits."""
+    B8 H32 Hkv8 Sq1 is 64 workgroups, so 12 splits.  Grids of several row blocks
+    per (b, h) split only with 64 key tiles or more (counted to the causal bound)."""
     L = _lib.load()
     ws = L.ghip_sdpa_workspace_bytes
     BF16, F32 = _lib.DT_BFLOAT16, _lib.DT_FLOAT32
     assert ws(BF16, 8, 32, 8, 1, 8192, 128, 0) == 12 * 8 * 32 * 1 * 129 * 4
-    assert ws(BF16, 8, 32, 8, 1, 8192, 128, 1) == 3 * 8 * 32 * 1 * 129 * 4   # causal: 256 workgroups
+    assert ws(BF16, 8, 32, 8, 1, 8192, 128, 1) == 0        # causal, one query: it sees key 0 only
+    assert ws(BF16, 1, 16, 16, 2048, 2048, 128, 0) == 0    # prefill, 32 key tiles: no split
+    assert ws(BF16, 2, 8, 8, 1024, 8192, 128, 0) == 6 * 2 * 8 * 1024 * 129 * 4  # 128 tiles: 6 splits
+    assert ws(BF16, 1, 16, 16, 512, 8192, 64, 1) == 0      # causal: its queries see 512 keys
     assert ws(BF16, 8, 32, 32, 1, 8192, 128, 0) == 3 * 8 * 32 * 1 * 129 * 4  # no GQA: 256 workgroups
     assert ws(BF16, 1, 32, 8, 1, 32768, 128, 0) == 64 * 32 * 1 * 129 * 4     # 8 workgroups, at most 64 splits
     assert ws(BF16, 4, 16, 16, 2048, 2048, 128, 1) == 0     # the config: 1024 workgroups

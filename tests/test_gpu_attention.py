@@ -85,9 +85,9 @@ SPLIT_CASES = [  # (B, H, Hkv, Sq, Sk, causal)
     (2, 8, 2, 1, 4096, False),     # decoding, GQA 4:1
     (1, 4, 4, 16, 2048, False),    # a few queries
     (1, 4, 1, 1, 777, False),      # ragged last split (keys 640 .. 776)
-    (1, 2, 2, 200, 1500, True),    # causal, Sq < Sk: splits past the diagonal hold no keys
-    (3, 2, 1, 130, 3000, False),   # two query blocks, ragged
-    (1, 8, 2, 40, 1024, False),    # grouped-query rows: 4 heads x 40 queries, two row blocks
+    (1, 2, 2, 4200, 4200, True),   # causal prefill of 66 key tiles: later splits of early blocks hold no keys
+    (3, 2, 1, 130, 4500, False),   # two query blocks, ragged
+    (1, 8, 2, 40, 4500, False),    # grouped-query rows: 4 heads x 40 queries, two row blocks
     (2, 6, 3, 5, 700, False),      # grouped-query rows: 2 heads x 5 queries, ragged keys
 ]
 
