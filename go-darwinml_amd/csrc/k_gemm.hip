@@ -187,7 +187,10 @@ static hipError_t dispatch_f32(GemmParams p, hipStream_t s) {
   p.vec_c = (p.sc_m % 4 == 0) && (p.sc_b % 4 == 0 || p.batch == 1) &&
             (reinterpret_cast<uintptr_t>(p.c) % (4 * sizeof(OutT)) == 0);
   if (big) return launch_f32<256, 256, 2, 4, OutT, true>(p, ma, mb, s);
-  if (grid256) return launch_f32<256, 256, 2, 4, OutT>(p, ma, mb, s);
+  // The 8-wave 256 x 256 fp32 core only from one full round of its tiles: below
+  // that the 4-wave 128 x 128 core (two workgroups per CU) is faster, 1.9x at 128
+  // tiles of 256 x 256 ([2048,4096,4096]), 1.3x at 144 and 192, even at 256.
+  if (p.M >= 256 && p.N >= 256 && t256 >= 256) return launch_f32<256, 256, 2, 4, OutT>(p, ma, mb, s);
   return launch_f32<128, 128, 2, 2, OutT>(p, ma, mb, s);
 }
 
