@@ -403,7 +403,7 @@ def make_cases(only=None):
         if vendor:
             return Case("dot_general_bf16_shard_hipblaslt", lambda i: torch.matmul(a, b, out=c),
                         flops_per_step=fl, bound="mfma", peak=BF16_PEAK_TFLOPS, dtype="bf16",
-                        kernel="hipBLASLt (torch.matmul)",
+                        kernel="hipBLASLt (torch.matmul, shard shape)",
                         config={"workload": f"comparison only: torch.matmul (hipBLASLt) on the {shape}, same process"})
         return Case("dot_general_bf16_shard", lambda i: ops.gemm(a, b, out=c),
                     flops_per_step=fl, bound="mfma", peak=BF16_PEAK_TFLOPS, dtype="bf16",
