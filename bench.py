@@ -6,8 +6,9 @@ one "step" is one RMSNorm launch over that batch, inputs resident in HBM.
 `value` is GB/s of algorithmic traffic (read x + gamma, write y).  The same line
 carries the other BASELINE workloads under "secondary" (softmax, bf16 RMSNorm,
 LayerNorm, bf16/fp32 DotGeneral, the bf16 DotGeneral's per-GPU shard under 8-way
-data parallelism (batch 0 alone), the attention composite, a decoding step of
-grouped-query attention over an 8192-token KV cache, the transformer block)
+data parallelism (batch 0 alone), a decoding step's few-row DotGeneral (an FFN
+down projection over 16 sequences, HBM-bound), the attention composite, a decoding
+step of grouped-query attention over an 8192-token KV cache, the transformer block)
 and two widened ops (FusedDense + GELU, the embedding-gradient ScatterSum), each
 with its own roofline fraction.
 
@@ -411,6 +412,41 @@ def make_cases(only=None):
                     config={"workload": f"{shape}, bf16 in ~ N(0, 1/sqrt(4096)), fp32 accumulate, bf16 out; "
                                         f"CPU rate: as dot_general_bf16 (same rows, same work per row)"})
 
+    def decode_dot_case(vendor):
+        """A decoding step's FFN down projection for 16 sequences: x [16,14336] .
+        W [14336,4096] bf16, fp32 accumulate, bf16 out.  HBM-bound: W (117 MB) is
+        read once (rotated over enough copies to leave the Infinity Cache).  32 tiles
+        of 128 x 128: this backend splits the contraction into 14 ranges of 1024
+        (fp32 partials in a workspace sized by ghip_gemm_workspace_bytes), summed by a
+        second kernel.  vendor: torch.matmul (hipBLASLt), for comparison."""
+        M, K, N = 16, 14336, 4096
+        x = nd(3101, (M, K), std=K ** -0.25, dtype=torch.bfloat16)
+        w = nd(3102, (K, N), std=K ** -0.25, dtype=torch.bfloat16)
+        nbytes = (M * K + K * N + M * N) * 2
+        rot = rotation_for(nbytes)
+        ws_ = rotated(w, rot)
+        cs = [torch.empty((M, N), device=dev, dtype=torch.bfloat16) for _ in range(rot)]
+        shape = "DotGeneral [16,14336]x[14336,4096] (a decoding step's FFN down projection, 16 sequences)"
+        if vendor:
+            return Case("dot_general_bf16_decode_hipblaslt", lambda i: torch.matmul(x, ws_[i % rot], out=cs[i % rot]),
+                        bytes_per_step=nbytes, dtype="bf16", rotation=rot, out=lambda i: cs[i % rot],
+                        kernel="hipBLASLt (torch.matmul, decode shape)",
+                        config={"workload": f"comparison only: torch.matmul (hipBLASLt) on the {shape}, same process"})
+        work = ops.gemm_workspace(torch.bfloat16, torch.bfloat16, 1, M, N, K, dev)
+        xh, wh = host32(x), host32(w)
+
+        def leg(budget_s):
+            reps, dt = cpu_rate(lambda: orc.dot_general(xh, [1], [], wh, [0], []), budget_s)
+            return cpu_entry(nbytes * reps / dt / 1e9, "GB/s",
+                             f"oracle/oracle.c orc_dot_general (fp64 accumulation), OpenMP {cpu_threads()} threads, "
+                             f"on the whole product from the same bf16 x and W; bytes as on the GPU line; "
+                             f"{reps} repetitions in {dt:.1f} s")
+        return Case("dot_general_bf16_decode", lambda i: ops.gemm(x, ws_[i % rot], out=cs[i % rot], workspace=work),
+                    bytes_per_step=nbytes, dtype="bf16", rotation=rot, cpu=leg, out=lambda i: cs[i % rot],
+                    kernel="gemm_bf16_kernel<128, 128, 2, 2, true, false, bf16_t, float> + gemm_split_sum_kernel",
+                    config={"workload": f"{shape}, bf16 in ~ N(0, 1/sqrt(14336)), fp32 accumulate, bf16 out; "
+                                        f"bytes: x and W read, the output written"})
+
     def attention_case():
         B, H, S, D = 4, 16, 2048, 128
         q = nd(4001, (B, H, S, D), dtype=torch.bfloat16)
@@ -603,6 +639,8 @@ def make_cases(only=None):
         "dot_general_bf16_hipblaslt": vendor_dot_case,
         "dot_general_bf16_shard": lambda: shard_dot_case(False),
         "dot_general_bf16_shard_hipblaslt": lambda: shard_dot_case(True),
+        "dot_general_bf16_decode": lambda: decode_dot_case(False),
+        "dot_general_bf16_decode_hipblaslt": lambda: decode_dot_case(True),
         "attention_bf16": attention_case,
         "attention_decode_bf16": decode_case,
         "transformer_block_bf16": transformer_case,

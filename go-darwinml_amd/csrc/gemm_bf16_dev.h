@@ -86,6 +86,53 @@ __host__ __device__ inline bool gemm_rows_fit(int64_t s_mn, int64_t s_k, int64_t
   return s >= 0 && (s * 256 + 256) * es < (int64_t{1} << 31);
 }
 
+#if !defined(__HIPCC_RTC__)
+// Contraction split for 16-bit products whose grid leaves most of the chip idle
+// (the 128 x 128 core, two workgroups per CU: 512 slots).  s ranges of kc = K / s
+// contraction steps (kc a multiple of 64) run as s slices of one grid, each
+// writing its fp32 partial product; a second kernel sums the s partials in split
+// order and rounds once.  s = 1: no split.  The rule is a cost model of measured
+// figures: a lone 128 x 128 tile takes ~14.6 ns per contraction step at any grid
+// up to one round of 512, a split grid cannot beat the operands' own read time
+// (A + B at ~5 TB/s), and the partials cost s x M x N x 8 bytes of traffic plus
+// ~2 us for the summing launch; a split must save 15%.  One batch only.
+struct GemmSplit {
+  int s;
+  int64_t kc;
+};
+constexpr int kGemmMaxSplit = 16;
+inline GemmSplit gemm_k_split(int64_t batch, int64_t M, int64_t N, int64_t K) {
+  GemmSplit r{1, K};
+  if (batch != 1 || M <= 0 || N <= 0 || K < 1024) return r;
+  const int64_t t = ((M + 127) / 128) * ((N + 127) / 128);
+  if (t > 256) return r;
+  int64_t smax = 512 / t;
+  if (smax > K / 512) smax = K / 512;
+  if (smax > kGemmMaxSplit) smax = kGemmMaxSplit;
+  const double floor_us = static_cast<double>(M * K + K * N) * 2 / 5e6;
+  auto cost = [&](int64_t s) {
+    const double k_us = static_cast<double>(K / s) * 0.0146;
+    const double part_us = s > 1 ? static_cast<double>(s) * M * N * 8 / 5e6 + 2.0 : 0.0;
+    return (k_us > floor_us ? k_us : floor_us) + part_us;
+  };
+  double best = 0.85 * cost(1);
+  for (int64_t s = 2; s <= smax; ++s) {
+    if (K % (s * 64) != 0) continue;
+    const double c = cost(s);
+    if (c < best) {
+      best = c;
+      r.s = static_cast<int>(s);
+      r.kc = K / s;
+    }
+  }
+  return r;
+}
+// Workspace bytes of a split (0 for s = 1): s fp32 partial products [M, N].
+inline int64_t gemm_split_bytes(const GemmSplit& sp, int64_t M, int64_t N) {
+  return sp.s > 1 ? static_cast<int64_t>(sp.s) * M * N * 4 : 0;
+}
+#endif
+
 // Generated epilogues read up to kEpiMaxIn extra operands, each addressed as
 // in[k] + bb * s_b[k] + m * s_m[k] + n * s_n[k] (elements), and write `out`
 // ([batch, M, N] with strides so_b, so_m, 1).

@@ -1797,10 +1797,14 @@ struct Lowerer {
     }
     const View lv = d.lv;
     const int64_t M = d.M, N_ = d.N, K = d.K, sam = d.sam, sak = d.sak, sbk = d.sbk, sbn = d.sbn;
+    // Products that split their contraction run one after another, sharing one
+    // workspace in the arena.
+    const int64_t ws_bytes = ghip_gemm_workspace_bytes(dt, odt, 1, M, N_, K);
+    const View wsv = gemm_workspace_view(ws_bytes, &wr);
     add_step(fmt("gemm_grouped %s G=%d M=%lld N=%lld K=%lld (products sharing a; a strides m=%lld k=%lld, b strides "
-                 "k=%lld n=%lld)",
+                 "k=%lld n=%lld%s)",
                  dtype_name(dt), G, (long long)M, (long long)N_, (long long)K, (long long)sam, (long long)sak,
-                 (long long)sbk, (long long)sbn),
+                 (long long)sbk, (long long)sbn, split_note(ws_bytes, 1, M, N_, K).c_str()),
              rd, wr, [=](ExecState& st, GHipError* e) {
                const void* bp[kGemmMaxGroups];
                void* cp[kGemmMaxGroups];
@@ -1808,8 +1812,9 @@ struct Lowerer {
                  bp[g] = st.ptr(rvs[g], dt);
                  cp[g] = st.ptr(ys[g], odt);
                }
-               return ghip_gemm_grouped(dt, odt, G, M, N_, K, st.ptr(lv, dt), sam, sak, bp, sbk, sbn, cp, N_,
-                                        st.stream, e);
+               void* ws = ws_bytes > 0 ? st.ptr(wsv, GHIP_DTYPE_FLOAT32) : nullptr;
+               return ghip_gemm_grouped_ws(dt, odt, G, M, N_, K, st.ptr(lv, dt), sam, sak, bp, sbk, sbn, cp, N_, ws,
+                                           ws_bytes, st.stream, e);
              });
     for (int g = 1; g < G; ++g) {
       views[grp[g]] = ys[g];
@@ -1833,14 +1838,35 @@ struct Lowerer {
     View y = fresh(n.shape);
     const int dt = N[n.in[0]].shape.dtype, odt = n.shape.dtype;
     const int64_t scb = M * N_, scm = N_;
-    add_step(fmt("gemm_batched %s B=%lld M=%lld N=%lld K=%lld (%s; a strides b=%lld m=%lld k=%lld, b strides b=%lld k=%lld n=%lld)",
+    std::vector<int> wr{y.slot};
+    const int64_t ws_bytes = ghip_gemm_workspace_bytes(dt, odt, B, M, N_, K);
+    const View wsv = gemm_workspace_view(ws_bytes, &wr);
+    add_step(fmt("gemm_batched %s B=%lld M=%lld N=%lld K=%lld (%s; a strides b=%lld m=%lld k=%lld, b strides b=%lld k=%lld n=%lld%s)",
                  dtype_name(dt), (long long)B, (long long)M, (long long)N_, (long long)K, d.how.c_str(), (long long)sab,
-                 (long long)sam, (long long)sak, (long long)sbb, (long long)sbk, (long long)sbn),
-             {lv.slot, rv.slot}, {y.slot}, [=](ExecState& st, GHipError* e) {
-               return ghip_gemm_batched(dt, odt, B, M, N_, K, st.ptr(lv, dt), sab, sam, sak, st.ptr(rv, dt), sbb, sbk, sbn,
-                                        st.ptr(y, odt), scb, scm, 1, st.stream, e);
+                 (long long)sam, (long long)sak, (long long)sbb, (long long)sbk, (long long)sbn,
+                 split_note(ws_bytes, B, M, N_, K).c_str()),
+             {lv.slot, rv.slot}, wr, [=](ExecState& st, GHipError* e) {
+               void* ws = ws_bytes > 0 ? st.ptr(wsv, GHIP_DTYPE_FLOAT32) : nullptr;
+               return ghip_gemm_batched_ws(dt, odt, B, M, N_, K, st.ptr(lv, dt), sab, sam, sak, st.ptr(rv, dt), sbb, sbk,
+                                           sbn, st.ptr(y, odt), scb, scm, 1, ws, ws_bytes, st.stream, e);
              });
     return y;
+  }
+
+  // The arena view of a GEMM step's contraction-split workspace (none for 0
+  // bytes), appended to the step's written slots.
+  View gemm_workspace_view(int64_t ws_bytes, std::vector<int>* wr) {
+    if (ws_bytes <= 0) return View{};
+    Shape wss;
+    wss.dtype = GHIP_DTYPE_FLOAT32;
+    wss.dims = {(ws_bytes + 3) / 4};
+    const View w = fresh(wss);
+    wr->push_back(w.slot);
+    return w;
+  }
+  static std::string split_note(int64_t ws_bytes, int64_t B, int64_t M, int64_t N_, int64_t K) {
+    if (ws_bytes <= 0) return "";
+    return fmt("; contraction split in %d", gemm_k_split(B, M, N_, K).s);
   }
 
   // ------------------------------------------------------------------ GEMM epilogue fusion
@@ -2668,6 +2694,10 @@ View Lowerer::emit_gemm_epilogue(int v, const std::vector<int>& mem, bool* fused
   }
   const DotPlan& d = dp[0];
   if (NB == 2 && (dp[1].sbb != d.sbb || dp[1].sbk != d.sbk || dp[1].sbn != d.sbn)) return View{};
+  // A product the stand-alone GEMM step would run with its contraction split stays
+  // unfused (the split's fp32 partials are summed by a kernel of their own, which
+  // the generated epilogue kernel does not reproduce).
+  if (ghip_gemm_workspace_bytes(GHIP_DTYPE_BFLOAT16, N[dots[0]].shape.dtype, d.B, d.M, d.N, d.K) > 0) return View{};
   // The bf16 MFMA path's operand conditions, decided here because the fused
   // kernel has no generic fallback.
   if (d.B > 65535 || d.M == 0 || d.N == 0 || d.K == 0) return View{};

@@ -63,6 +63,61 @@ static hipError_t launch_bf16(GemmParams p, bool a_k, bool b_k, hipStream_t s) {
 
 
 
+// Sum of the s fp32 partial products of a split contraction (gemm_k_split),
+// ws[j][m][n] (dense [M, N] each), in split order j = 0, 1, .., s - 1, rounded
+// once to the output c[m * sc_m + n].  V4: a thread takes 4 consecutive n of one
+// row (N % 4 == 0: one 16-byte load per partial; vec_out: one store); else one
+// element.
+template <typename OutT, bool V4>
+__global__ __launch_bounds__(256) void gemm_split_sum_kernel(const float* __restrict__ ws, OutT* __restrict__ c,
+                                                             int64_t M, int64_t N, int64_t sc_m, int s, int vec_out) {
+  const int64_t slice = M * N;
+  constexpr int W = V4 ? 4 : 1;
+  const int64_t nw = N / W;
+  const int64_t groups = M * nw;
+  for (int64_t g = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; g < groups;
+       g += static_cast<int64_t>(gridDim.x) * 256) {
+    const int64_t m = g / nw, n = (g % nw) * W;
+    const float* src = ws + m * N + n;
+    OutT* dst = c + m * sc_m + n;
+    if constexpr (V4) {
+      // Every partial's load is issued before the first add (one memory latency
+      // per thread, not s); the adds then run in split order.
+      float4 v[kGemmMaxSplit];
+#pragma unroll
+      for (int j = 0; j < kGemmMaxSplit; ++j)
+        if (j < s) v[j] = *reinterpret_cast<const float4*>(src + j * slice);
+      float4 acc = v[0];
+#pragma unroll
+      for (int j = 1; j < kGemmMaxSplit; ++j)
+        if (j < s) {
+          acc.x += v[j].x;
+          acc.y += v[j].y;
+          acc.z += v[j].z;
+          acc.w += v[j].w;
+        }
+      if (vec_out) {
+        if constexpr (__is_same(OutT, float)) {
+          *reinterpret_cast<float4*>(dst) = acc;
+        } else if constexpr (__is_same(OutT, bf16_t)) {
+          *reinterpret_cast<uint2*>(dst) = make_uint2(pack_bf16x2(acc.x, acc.y), pack_bf16x2(acc.z, acc.w));
+        } else {
+          *reinterpret_cast<uint2*>(dst) = make_uint2(pack_f16x2(acc.x, acc.y), pack_f16x2(acc.z, acc.w));
+        }
+      } else {
+        store_out<OutT>(dst, acc.x);
+        store_out<OutT>(dst + 1, acc.y);
+        store_out<OutT>(dst + 2, acc.z);
+        store_out<OutT>(dst + 3, acc.w);
+      }
+    } else {
+      float acc = src[0];
+      for (int j = 1; j < s; ++j) acc += src[j * slice];
+      store_out<OutT>(dst, acc);
+    }
+  }
+}
+
 template <typename InT, typename OutT>
 static hipError_t launch_generic(const GemmParams& p, hipStream_t s) {
   const dim3 grid(static_cast<unsigned>((p.N + 15) / 16), static_cast<unsigned>((p.M + 15) / 16),
@@ -87,8 +142,51 @@ static int64_t slice_bytes(int64_t rows, int64_t s_row, int64_t K, int64_t s_k, 
   return ((rows - 1) * s_row + (K - 1) * s_k + 1) * es;
 }
 
+// Workspace of a split contraction (16-byte aligned, large enough: checked by the
+// entry points); ptr null: no split.
+struct GemmWs {
+  float* ptr = nullptr;
+  int64_t bytes = 0;
+};
+
+// A split contraction (gemm_k_split): the s ranges of kc steps run as s "batches"
+// of the 128 x 128 core (range j: a + j kc sa_k, b + j kc sb_k) writing fp32
+// partials into the workspace, then gemm_split_sum_kernel adds them in range order.
 template <typename InT, typename OutT>
-static hipError_t dispatch_bf16(GemmParams p, hipStream_t s) {
+static hipError_t launch_split(const GemmParams& p, int ma, int mb, const GemmSplit& sp, float* ws, hipStream_t s) {
+  GemmParams q = p;
+  q.batch = sp.s;
+  q.K = sp.kc;
+  q.sa_b = sp.kc * p.sa_k;
+  q.sb_b = sp.kc * p.sb_k;
+  q.c = ws;
+  q.sc_b = p.M * p.N;
+  q.sc_m = p.N;
+  const int64_t ea = slice_bytes(p.M, p.sa_m, sp.kc, p.sa_k, 2);
+  const int64_t eb = slice_bytes(p.N, p.sb_n, sp.kc, p.sb_k, 2);
+  q.a_extent = static_cast<uint32_t>(ea);
+  q.b_extent = static_cast<uint32_t>(eb);
+  q.a_extent64 = ea;
+  q.b_extent64 = eb;
+  q.vec_c = p.N % 4 == 0;
+  hipError_t e = launch_bf16<128, 128, 2, 2, InT, float>(q, ma == 1, mb == 1, s);
+  if (e != hipSuccess) return e;
+  const bool v4 = p.N % 4 == 0;
+  const int64_t groups = p.M * (v4 ? p.N / 4 : p.N);
+  const int64_t blocks = (groups + 255) / 256 < 4096 ? (groups + 255) / 256 : 4096;
+  const int vec_out = p.sc_m % 4 == 0 && reinterpret_cast<uintptr_t>(p.c) % (4 * sizeof(OutT)) == 0;
+  OutT* c = static_cast<OutT*>(p.c);
+  if (v4)
+    hipLaunchKernelGGL((gemm_split_sum_kernel<OutT, true>), dim3(static_cast<unsigned>(blocks)), dim3(256), 0, s, ws,
+                       c, p.M, p.N, p.sc_m, sp.s, vec_out);
+  else
+    hipLaunchKernelGGL((gemm_split_sum_kernel<OutT, false>), dim3(static_cast<unsigned>(blocks)), dim3(256), 0, s, ws,
+                       c, p.M, p.N, p.sc_m, sp.s, vec_out);
+  return hipGetLastError();
+}
+
+template <typename InT, typename OutT>
+static hipError_t dispatch_bf16(GemmParams p, hipStream_t s, GemmWs ws = {}) {
   const int ma = majorness(p.a, p.sa_b, p.sa_m, p.sa_k, p.M, p.K, 8, p.batch);
   const int mb = majorness(p.b, p.sb_b, p.sb_n, p.sb_k, p.N, p.K, 8, p.batch);
   const bool nonneg = p.sa_b >= 0 && p.sa_m >= 0 && p.sa_k >= 0 && p.sb_b >= 0 && p.sb_k >= 0 &&
@@ -110,6 +208,11 @@ static hipError_t dispatch_bf16(GemmParams p, hipStream_t s) {
   p.vec_c = (p.sc_m % kV == 0) && (p.sc_b % kV == 0 || p.batch == 1) &&
             (reinterpret_cast<uintptr_t>(p.c) % 16 == 0);
   if (big) return launch_bf16_4w<true, InT, OutT>(p, ma, mb, s);
+  // Few tiles and a long contraction, with a workspace: the contraction split.
+  if (ws.ptr) {
+    const GemmSplit sp = gemm_k_split(p.batch, p.M, p.N, p.K);
+    if (sp.s > 1 && gemm_split_bytes(sp, p.M, p.N) <= ws.bytes) return launch_split<InT, OutT>(p, ma, mb, sp, ws.ptr, s);
+  }
   // Grids of more than 128 256 x 256 tiles: the 256 x 256 cores (one workgroup per
   // CU).  Up to 128 such tiles they would leave half the 256 CUs or more idle, and
   // the 128 x 128 core (two workgroups per CU, so up to 512 tiles in one round) is
@@ -126,7 +229,8 @@ static hipError_t dispatch_bf16(GemmParams p, hipStream_t s) {
 // product's result is the one the stand-alone dispatch would give (the same core
 // and k order).
 template <typename InT, typename OutT>
-static hipError_t dispatch_grouped(GemmParams p, int G, const void* const* b, void* const* c, hipStream_t s) {
+static hipError_t dispatch_grouped(GemmParams p, int G, const void* const* b, void* const* c, hipStream_t s,
+                                   GemmWs ws = {}) {
   bool ok = majorness(p.a, 0, p.sa_m, p.sa_k, p.M, p.K, 8, 1) == 1 && p.sa_m >= 0 && p.sa_k >= 0 &&
             p.sb_k >= 0 && p.sb_n >= 0;
   for (int g = 0; g < G && ok; ++g) ok = majorness(b[g], 0, p.sb_n, p.sb_k, p.N, p.K, 8, 1) == 0;
@@ -134,13 +238,16 @@ static hipError_t dispatch_grouped(GemmParams p, int G, const void* const* b, vo
   const int64_t eb = slice_bytes(p.N, p.sb_n, p.K, p.sb_k, 2);
   const int64_t tiles = ((p.M + 255) / 256) * ((p.N + 255) / 256);
   ok = ok && ea < (int64_t{1} << 31) && eb < (int64_t{1} << 31) && p.M >= 256 && p.N >= 256 && G * tiles >= 128;
+  // Products the stand-alone entry splits (given the workspace) run as that split,
+  // one after another in the same workspace, so each keeps the stand-alone bits.
+  if (ws.ptr && gemm_k_split(1, p.M, p.N, p.K).s > 1) ok = false;
   if (!ok) {
     for (int g = 0; g < G; ++g) {
       GemmParams q = p;
       q.batch = 1;
       q.b = b[g];
       q.c = c[g];
-      const hipError_t e = dispatch_bf16<InT, OutT>(q, s);
+      const hipError_t e = dispatch_bf16<InT, OutT>(q, s, ws);
       if (e != hipSuccess) return e;
     }
     return hipSuccess;
@@ -198,11 +305,47 @@ static hipError_t dispatch_f32(GemmParams p, hipStream_t s) {
 
 using namespace ghip;
 
+// Workspace bytes a split of this product needs (0: never split): 16-bit operands
+// only.
+static int64_t split_ws_bytes(int ab_dtype, int64_t batch, int64_t M, int64_t N, int64_t K) {
+  if (ab_dtype != GHIP_DTYPE_BFLOAT16 && ab_dtype != GHIP_DTYPE_FLOAT16) return 0;
+  return gemm_split_bytes(gemm_k_split(batch, M, N, K), M, N);
+}
+
+// A workspace given for a product that splits must hold the split's partials and
+// be 16-byte aligned.
+static int check_split_ws(const char* who, int64_t need, const void* workspace, int64_t workspace_bytes,
+                          GHipError* err) {
+  if (!workspace || need == 0) return GHIP_OK;
+  if (workspace_bytes < need)
+    return set_error(err, GHIP_ERR_INVALID_ARG, "%s: workspace of %lld bytes, %lld needed", who,
+                     static_cast<long long>(workspace_bytes), static_cast<long long>(need));
+  if (reinterpret_cast<uintptr_t>(workspace) % 16 != 0)
+    return set_error(err, GHIP_ERR_INVALID_ARG, "%s: workspace must be 16-byte aligned", who);
+  return GHIP_OK;
+}
+
+extern "C" int64_t ghip_gemm_workspace_bytes(int ab_dtype, int c_dtype, int64_t batch, int64_t M, int64_t N,
+                                             int64_t K) {
+  (void)c_dtype;
+  if (batch < 0 || M < 0 || N < 0 || K < 0) return 0;
+  return split_ws_bytes(ab_dtype, batch, M, N, K);
+}
+
 extern "C" int ghip_gemm_batched(int ab_dtype, int c_dtype, int64_t batch, int64_t M, int64_t N,
                                  int64_t K, const void* a, int64_t sa_b, int64_t sa_m,
                                  int64_t sa_k, const void* b, int64_t sb_b, int64_t sb_k,
                                  int64_t sb_n, void* c, int64_t sc_b, int64_t sc_m, int64_t sc_n,
                                  void* stream, GHipError* err) {
+  return ghip_gemm_batched_ws(ab_dtype, c_dtype, batch, M, N, K, a, sa_b, sa_m, sa_k, b, sb_b, sb_k, sb_n, c, sc_b,
+                              sc_m, sc_n, nullptr, 0, stream, err);
+}
+
+extern "C" int ghip_gemm_batched_ws(int ab_dtype, int c_dtype, int64_t batch, int64_t M, int64_t N,
+                                    int64_t K, const void* a, int64_t sa_b, int64_t sa_m,
+                                    int64_t sa_k, const void* b, int64_t sb_b, int64_t sb_k,
+                                    int64_t sb_n, void* c, int64_t sc_b, int64_t sc_m, int64_t sc_n,
+                                    void* workspace, int64_t workspace_bytes, void* stream, GHipError* err) {
   if (batch < 0 || M < 0 || N < 0 || K < 0)
     return set_error(err, GHIP_ERR_INVALID_ARG, "gemm_batched: negative size");
   if (sc_n != 1) return set_error(err, GHIP_ERR_INVALID_ARG, "gemm_batched: sc_n must be 1");
@@ -211,6 +354,11 @@ extern "C" int ghip_gemm_batched(int ab_dtype, int c_dtype, int64_t batch, int64
   const int64_t tiles = batch * ((M + 127) / 128) * ((N + 127) / 128);
   if (tiles > 0x7fffffffLL || batch > 65535)
     return set_error(err, GHIP_ERR_INVALID_ARG, "gemm_batched: problem too large");
+  const int rc = check_split_ws("gemm_batched", split_ws_bytes(ab_dtype, batch, M, N, K), workspace, workspace_bytes, err);
+  if (rc != GHIP_OK) return rc;
+  GemmWs ws;
+  ws.ptr = static_cast<float*>(workspace);
+  ws.bytes = workspace ? workspace_bytes : 0;
   GemmParams p{};
   p.a = a; p.b = b; p.c = c;
   p.sa_b = sa_b; p.sa_m = sa_m; p.sa_k = sa_k;
@@ -220,12 +368,12 @@ extern "C" int ghip_gemm_batched(int ab_dtype, int c_dtype, int64_t batch, int64
   hipStream_t s = static_cast<hipStream_t>(stream);
   hipError_t e;
   if (ab_dtype == GHIP_DTYPE_BFLOAT16) {
-    if (c_dtype == GHIP_DTYPE_BFLOAT16) e = dispatch_bf16<bf16_t, bf16_t>(p, s);
-    else if (c_dtype == GHIP_DTYPE_FLOAT32) e = dispatch_bf16<bf16_t, float>(p, s);
+    if (c_dtype == GHIP_DTYPE_BFLOAT16) e = dispatch_bf16<bf16_t, bf16_t>(p, s, ws);
+    else if (c_dtype == GHIP_DTYPE_FLOAT32) e = dispatch_bf16<bf16_t, float>(p, s, ws);
     else return set_error(err, GHIP_ERR_UNSUPPORTED, "gemm_batched: output dtype %d", c_dtype);
   } else if (ab_dtype == GHIP_DTYPE_FLOAT16) {
-    if (c_dtype == GHIP_DTYPE_FLOAT16) e = dispatch_bf16<f16_t, f16_t>(p, s);
-    else if (c_dtype == GHIP_DTYPE_FLOAT32) e = dispatch_bf16<f16_t, float>(p, s);
+    if (c_dtype == GHIP_DTYPE_FLOAT16) e = dispatch_bf16<f16_t, f16_t>(p, s, ws);
+    else if (c_dtype == GHIP_DTYPE_FLOAT32) e = dispatch_bf16<f16_t, float>(p, s, ws);
     else return set_error(err, GHIP_ERR_UNSUPPORTED, "gemm_batched: output dtype %d", c_dtype);
   } else if (ab_dtype == GHIP_DTYPE_FLOAT32) {
     if (c_dtype == GHIP_DTYPE_FLOAT32) e = dispatch_f32<float>(p, s);
@@ -241,6 +389,14 @@ extern "C" int ghip_gemm_batched(int ab_dtype, int c_dtype, int64_t batch, int64
 extern "C" int ghip_gemm_grouped(int ab_dtype, int c_dtype, int groups, int64_t M, int64_t N, int64_t K,
                                  const void* a, int64_t sa_m, int64_t sa_k, const void* const* b, int64_t sb_k,
                                  int64_t sb_n, void* const* c, int64_t sc_m, void* stream, GHipError* err) {
+  return ghip_gemm_grouped_ws(ab_dtype, c_dtype, groups, M, N, K, a, sa_m, sa_k, b, sb_k, sb_n, c, sc_m, nullptr, 0,
+                              stream, err);
+}
+
+extern "C" int ghip_gemm_grouped_ws(int ab_dtype, int c_dtype, int groups, int64_t M, int64_t N, int64_t K,
+                                    const void* a, int64_t sa_m, int64_t sa_k, const void* const* b, int64_t sb_k,
+                                    int64_t sb_n, void* const* c, int64_t sc_m, void* workspace,
+                                    int64_t workspace_bytes, void* stream, GHipError* err) {
   if (groups < 1 || groups > kGemmMaxGroups)
     return set_error(err, GHIP_ERR_INVALID_ARG, "gemm_grouped: groups must be 1..%d", kGemmMaxGroups);
   if (M < 0 || N < 0 || K < 0) return set_error(err, GHIP_ERR_INVALID_ARG, "gemm_grouped: negative size");
@@ -253,14 +409,19 @@ extern "C" int ghip_gemm_grouped(int ab_dtype, int c_dtype, int groups, int64_t 
     // fp32 operands, an empty contraction or an output dtype the batched entry
     // rejects: product by product.
     for (int g = 0; g < groups; ++g) {
-      const int rc = ghip_gemm_batched(ab_dtype, c_dtype, 1, M, N, K, a, 0, sa_m, sa_k, b[g], 0, sb_k, sb_n, c[g], 0,
-                                       sc_m, 1, stream, err);
+      const int rc = ghip_gemm_batched_ws(ab_dtype, c_dtype, 1, M, N, K, a, 0, sa_m, sa_k, b[g], 0, sb_k, sb_n, c[g],
+                                          0, sc_m, 1, workspace, workspace_bytes, stream, err);
       if (rc != GHIP_OK) return rc;
     }
     return GHIP_OK;
   }
   if (((M + 127) / 128) * ((N + 127) / 128) > 0x7fffffffLL / groups)
     return set_error(err, GHIP_ERR_INVALID_ARG, "gemm_grouped: problem too large");
+  const int rc = check_split_ws("gemm_grouped", split_ws_bytes(ab_dtype, 1, M, N, K), workspace, workspace_bytes, err);
+  if (rc != GHIP_OK) return rc;
+  GemmWs ws;
+  ws.ptr = static_cast<float*>(workspace);
+  ws.bytes = workspace ? workspace_bytes : 0;
   GemmParams p{};
   p.a = a;
   p.sa_m = sa_m; p.sa_k = sa_k;
@@ -270,11 +431,11 @@ extern "C" int ghip_gemm_grouped(int ab_dtype, int c_dtype, int groups, int64_t 
   hipStream_t s = static_cast<hipStream_t>(stream);
   hipError_t e;
   if (ab_dtype == GHIP_DTYPE_BFLOAT16)
-    e = c_dtype == GHIP_DTYPE_FLOAT32 ? dispatch_grouped<bf16_t, float>(p, groups, b, c, s)
-                                      : dispatch_grouped<bf16_t, bf16_t>(p, groups, b, c, s);
+    e = c_dtype == GHIP_DTYPE_FLOAT32 ? dispatch_grouped<bf16_t, float>(p, groups, b, c, s, ws)
+                                      : dispatch_grouped<bf16_t, bf16_t>(p, groups, b, c, s, ws);
   else
-    e = c_dtype == GHIP_DTYPE_FLOAT32 ? dispatch_grouped<f16_t, float>(p, groups, b, c, s)
-                                      : dispatch_grouped<f16_t, f16_t>(p, groups, b, c, s);
+    e = c_dtype == GHIP_DTYPE_FLOAT32 ? dispatch_grouped<f16_t, float>(p, groups, b, c, s, ws)
+                                      : dispatch_grouped<f16_t, f16_t>(p, groups, b, c, s, ws);
   GHIP_CHECK(e, err);
   return GHIP_OK;
 }

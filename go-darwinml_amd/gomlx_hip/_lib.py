@@ -48,6 +48,10 @@ SIGNATURES = {
                           _vp, _i64, _i64, _i64, _vp, _i64, _i64, _i64, _vp, _errp],
     "ghip_gemm_grouped": [_int, _int, _int, _i64, _i64, _i64, _vp, _i64, _i64, ctypes.POINTER(_vp), _i64, _i64,
                           ctypes.POINTER(_vp), _i64, _vp, _errp],
+    "ghip_gemm_batched_ws": [_int, _int, _i64, _i64, _i64, _i64, _vp, _i64, _i64, _i64,
+                             _vp, _i64, _i64, _i64, _vp, _i64, _i64, _i64, _vp, _i64, _vp, _errp],
+    "ghip_gemm_grouped_ws": [_int, _int, _int, _i64, _i64, _i64, _vp, _i64, _i64, ctypes.POINTER(_vp), _i64,
+                             _i64, ctypes.POINTER(_vp), _i64, _vp, _i64, _vp, _errp],
     "ghip_gather_rows": [_vp, _i64, _i64, _vp, _i64, _vp, _vp, _errp],
     "ghip_argminmax": [_int, _vp, _i64, _i64, _i64, _int, _int, _vp, _vp, _errp],
     "ghip_iota": [_int, _vp, _i64, _i64, _i64, _vp, _errp],
@@ -74,6 +78,7 @@ SIGNATURES = {
 # name -> argtypes of the entry points that return int64_t.
 SIGNATURES_I64 = {
     "ghip_sdpa_workspace_bytes": [_int, _i64, _i64, _i64, _i64, _i64, _i64, _int],
+    "ghip_gemm_workspace_bytes": [_int, _int, _i64, _i64, _i64, _i64],
 }
 
 _lib = None

@@ -96,8 +96,18 @@ def layernorm(x: torch.Tensor, gamma=None, beta=None, eps: float = 1e-5, out=Non
     return y
 
 
-def gemm(a: torch.Tensor, b: torch.Tensor, out_dtype=None, out=None, stream=None):
-    """c[b] = a[b] @ b[b] for a [B,M,K] / [M,K], b [B,K,N] / [K,N]; any strides."""
+def gemm_workspace(a_dtype, out_dtype, B: int, M: int, N: int, K: int, device):
+    """Workspace for ghip_gemm_batched_ws / ghip_gemm_grouped_ws (None when a
+    product of these sizes never splits its contraction)."""
+    n = _lib.load().ghip_gemm_workspace_bytes(dtype_code(a_dtype), dtype_code(out_dtype or a_dtype), B, M, N, K)
+    return torch.empty((n,), dtype=torch.uint8, device=device) if n > 0 else None
+
+
+def gemm(a: torch.Tensor, b: torch.Tensor, out_dtype=None, out=None, stream=None, k_split: bool = True,
+         workspace=None):
+    """c[b] = a[b] @ b[b] for a [B,M,K] / [M,K], b [B,K,N] / [K,N]; any strides.
+    k_split: with a workspace (`workspace`, or one allocated here), so few-tile
+    products with a long contraction split it (ghip_gemm_batched_ws)."""
     _check_dev(a, b)
     squeeze = a.dim() == 2
     a3 = a.unsqueeze(0) if a.dim() == 2 else a
@@ -109,16 +119,21 @@ def gemm(a: torch.Tensor, b: torch.Tensor, out_dtype=None, out=None, stream=None
     odt = out_dtype or a.dtype
     c = torch.empty((B, M, N), dtype=odt, device=a.device) if out is None else out.view(B, M, N)
     sb_b = b3.stride(0) if B2 == B else 0
-    call("ghip_gemm_batched", dtype_code(a.dtype), dtype_code(odt), B, M, N, K,
+    if k_split and workspace is None:
+        workspace = gemm_workspace(a.dtype, odt, B, M, N, K, a.device)
+    ws_ptr = workspace.data_ptr() if (k_split and workspace is not None) else None
+    ws_bytes = workspace.numel() * workspace.element_size() if ws_ptr is not None else 0
+    call("ghip_gemm_batched_ws", dtype_code(a.dtype), dtype_code(odt), B, M, N, K,
          a3.data_ptr(), a3.stride(0), a3.stride(1), a3.stride(2),
          b3.data_ptr(), sb_b, b3.stride(1), b3.stride(2),
-         c.data_ptr(), c.stride(0), c.stride(1), c.stride(2), _stream(stream))
+         c.data_ptr(), c.stride(0), c.stride(1), c.stride(2), ws_ptr, ws_bytes, _stream(stream))
     return c[0] if squeeze else c
 
 
-def gemm_grouped(a: torch.Tensor, bs, out_dtype=None, outs=None, stream=None):
-    """[a @ b for b in bs] in one call (ghip_gemm_grouped): a [M,K], every b [K,N]
-    with the same strides; returns the list of [M,N] results."""
+def gemm_grouped(a: torch.Tensor, bs, out_dtype=None, outs=None, stream=None, k_split: bool = True,
+                 workspace=None):
+    """[a @ b for b in bs] in one call (ghip_gemm_grouped_ws): a [M,K], every b [K,N]
+    with the same strides; returns the list of [M,N] results.  k_split as in gemm."""
     import ctypes
     _check_dev(a, *bs)
     M, K = a.shape
@@ -131,8 +146,13 @@ def gemm_grouped(a: torch.Tensor, bs, out_dtype=None, outs=None, stream=None):
         raise ValueError("gemm_grouped: outputs need one row stride and unit column stride")
     bp = (ctypes.c_void_p * len(bs))(*[b.data_ptr() for b in bs])
     cp = (ctypes.c_void_p * len(cs))(*[c.data_ptr() for c in cs])
-    call("ghip_gemm_grouped", dtype_code(a.dtype), dtype_code(odt), len(bs), M, N, K, a.data_ptr(),
-         a.stride(0), a.stride(1), bp, bs[0].stride(0), bs[0].stride(1), cp, cs[0].stride(0), _stream(stream))
+    if k_split and workspace is None:
+        workspace = gemm_workspace(a.dtype, odt, 1, M, N, K, a.device)
+    ws_ptr = workspace.data_ptr() if (k_split and workspace is not None) else None
+    ws_bytes = workspace.numel() * workspace.element_size() if ws_ptr is not None else 0
+    call("ghip_gemm_grouped_ws", dtype_code(a.dtype), dtype_code(odt), len(bs), M, N, K, a.data_ptr(),
+         a.stride(0), a.stride(1), bp, bs[0].stride(0), bs[0].stride(1), cp, cs[0].stride(0), ws_ptr, ws_bytes,
+         _stream(stream))
     return cs
 
 

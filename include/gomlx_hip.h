@@ -166,6 +166,40 @@ int ghip_gemm_grouped(int ab_dtype, int c_dtype, int groups, int64_t M, int64_t 
                       const void* a, int64_t sa_m, int64_t sa_k, const void* const* b, int64_t sb_k,
                       int64_t sb_n, void* const* c, int64_t sc_m, void* stream, GHipError* err);
 
+/* Device workspace bytes ghip_gemm_batched_ws / ghip_gemm_grouped_ws can use for a
+ * product of these sizes (per product), or 0 when such a product never splits.
+ * A split applies to 16-bit operands, batch 1, at most 256 output tiles of
+ * 128 x 128 and a long contraction (K >= 1024, K / s a multiple of 64): the
+ * contraction runs as s ranges in one grid, each writing its fp32 partial
+ * product [M, N] into the workspace (s x M x N x 4 bytes), and a second kernel
+ * adds the s partials in range order and rounds once.  The result is
+ * deterministic, but its rounding differs from the unsplit product's (another
+ * fp32 summation order).  Same DotGeneral as ghip_gemm_batched
+ * (dotgeneral.go:65-164); the reference has no workspace. */
+int64_t ghip_gemm_workspace_bytes(int ab_dtype, int c_dtype, int64_t batch, int64_t M, int64_t N,
+                                  int64_t K);
+
+/* ghip_gemm_batched with a caller-owned device workspace (16-byte aligned) that
+ * allows the contraction split described above.  workspace NULL: exactly
+ * ghip_gemm_batched (no split).  A workspace smaller than
+ * ghip_gemm_workspace_bytes reports for a product that splits is an error
+ * (GHIP_ERR_INVALID_ARG).  The workspace is written on `stream`: calls sharing
+ * one workspace must be ordered (one stream). */
+int ghip_gemm_batched_ws(int ab_dtype, int c_dtype, int64_t batch, int64_t M, int64_t N,
+                         int64_t K, const void* a, int64_t sa_b, int64_t sa_m, int64_t sa_k,
+                         const void* b, int64_t sb_b, int64_t sb_k, int64_t sb_n, void* c,
+                         int64_t sc_b, int64_t sc_m, int64_t sc_n, void* workspace,
+                         int64_t workspace_bytes, void* stream, GHipError* err);
+
+/* ghip_gemm_grouped with a workspace: products that split (per
+ * ghip_gemm_workspace_bytes with batch 1) run one after another, each as
+ * ghip_gemm_batched_ws gives it with the same workspace, so c[g] keeps the
+ * stand-alone bits; others as ghip_gemm_grouped. */
+int ghip_gemm_grouped_ws(int ab_dtype, int c_dtype, int groups, int64_t M, int64_t N, int64_t K,
+                         const void* a, int64_t sa_m, int64_t sa_k, const void* const* b,
+                         int64_t sb_k, int64_t sb_n, void* const* c, int64_t sc_m, void* workspace,
+                         int64_t workspace_bytes, void* stream, GHipError* err);
+
 /* Fused attention forward, the one-kernel lowering of
  * Function.FusedScaledDotProductAttention (function.go:2669-2907; the composite
  * it replaces is DotGeneral -> scale -> causal Where -> FusedSoftmax -> DotGeneral,

@@ -79,3 +79,25 @@ def test_sdpa_workspace_policy():
     assert ws(BF16, 1, 2, 2, 1, 448, 128, 0) == 0           # fewer than 8 key tiles
     assert ws(BF16, 1, 4, 4, 1, 777, 128, 0) == 3 * 4 * 1 * 129 * 4
     assert ws(BF16, 0, 4, 4, 1, 777, 128, 0) == 0
+
+
+def test_gemm_workspace_policy():
+    """Host-side policy of the contraction split (no GPU call): 16-bit, batch 1, at
+    most 256 tiles of 128 x 128, K >= 1024 with K / s a multiple of 64, and a
+    modelled saving of 15% or more; the workspace holds s fp32 partials [M, N]."""
+    L = _lib.load()
+    ws = L.ghip_gemm_workspace_bytes
+    BF16, F16, F32 = _lib.DT_BFLOAT16, _lib.DT_FLOAT16, _lib.DT_FLOAT32
+    assert ws(BF16, BF16, 1, 16, 4096, 4096) == 8 * 16 * 4096 * 4      # decoding-size rows: 8 ranges of 512
+    assert ws(F16, F32, 1, 16, 4096, 4096) == 8 * 16 * 4096 * 4
+    assert ws(BF16, BF16, 1, 1024, 1024, 8192) == 8 * 1024 * 1024 * 4  # 64 tiles: 8 ranges
+    assert ws(BF16, BF16, 1, 2048, 2048, 8192) == 2 * 2048 * 2048 * 4  # 256 tiles: 2 ranges
+    # 14 ranges of 1024: reading W bounds 14 and 16 ranges alike, and 14 write fewer partials
+    assert ws(BF16, BF16, 1, 16, 4096, 14336) == 14 * 16 * 4096 * 4
+    assert ws(BF16, BF16, 1, 2048, 4096, 4096) == 0   # 512 tiles: one full round already
+    assert ws(BF16, BF16, 1, 2048, 2048, 2048) == 0   # the partials' traffic would eat the saving
+    assert ws(BF16, BF16, 2, 16, 4096, 4096) == 0     # batched products never split
+    assert ws(BF16, BF16, 1, 16, 4096, 1000) == 0     # short contraction
+    assert ws(BF16, BF16, 1, 16, 4096, 1096) == 0     # no split of K into multiples of 64
+    assert ws(F32, F32, 1, 16, 4096, 4096) == 0       # fp32 never splits
+    assert ws(BF16, BF16, 1, 0, 4096, 4096) == 0

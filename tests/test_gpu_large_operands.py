@@ -70,7 +70,7 @@ def test_gemm_rows_past_4gib(cuda):
     assert a.numel() * 2 > 4 * GiB
     _log(f"gemm A{tuple(a.shape)} x B{tuple(b.shape)}")
     c = ops.gemm(a, b)
-    c0 = ops.gemm(a0, b)
+    c0 = ops.gemm(a0, b, k_split=False)  # (128 tiles would split the contraction: another summation order)
     torch.cuda.synchronize()
     cv = c.view(reps, mb, N)
     for r in range(reps):
@@ -157,8 +157,10 @@ def test_gemm_f32_strided_past_4gib(cuda):
 def test_graph_epilogue_rows_past_4gib(cuda):
     """DotGeneral + bias through Builder / Compile / Execute with x [270336, 8192]
     bf16 (a 4.4 GB parameter): the generated epilogue kernel's 64-bit form.  Every
-    8192-row block of the result equals the small graph's result."""
-    reps, mb, K, N = 33, 8192, 8192, 256
+    8192-row block of the result equals the small graph's result (N = 1024, so the
+    small graph's 512 tiles of 128 x 128 run the fused epilogue too rather than a
+    contraction split)."""
+    reps, mb, K, N = 33, 8192, 8192, 1024
     rng = np.random.default_rng(5)
     x0 = synth.to_bf16_bits(rng.standard_normal((mb, K), dtype=np.float32) * 0.05)
     w = synth.to_bf16_bits(rng.standard_normal((K, N), dtype=np.float32) * 0.05)
@@ -188,7 +190,7 @@ def test_graph_epilogue_rows_past_4gib(cuda):
         _log(f"graph DotGeneral+bias x[{reps * mb},{K}]")
         plan, y = run(xb, reps * mb)
         del xb
-        assert "gemm_batched+epilogue" in plan, plan
+        assert "gemm_batched+epilogue" in plan and "gemm_batched+epilogue" in plan0, (plan, plan0)
         yv = y.reshape(reps, mb, N)
         for r in range(reps):
             assert np.array_equal(yv[r], y0), f"row block {r} differs"

@@ -68,6 +68,23 @@ def _decode_case(be, B, H, Hkv, Sk, D, seed):
     return ex, [be.BufferFromFlatData(0, a, make_shape(BF16, *a.shape)) for a in host]
 
 
+def _dot_case(be, M, N, K, seed):
+    """A few-tile DotGeneral with a long contraction plus a bias: the contraction
+    splits over a workspace in the arena (the scratch array here)."""
+    b = be.Builder("dot_split_noalloc")
+    f = b.Main()
+    x = f.Parameter("x", make_shape(BF16, M, K))
+    w = f.Parameter("w", make_shape(BF16, K, N))
+    c = f.Parameter("c", make_shape(BF16, N))
+    d = f.DotGeneral(x, [1], [], w, [0], [])
+    f.Return([f.Add(d, f.BroadcastInDim(c, make_shape(BF16, M, N), [1]))])
+    ex = b.Compile()
+    assert "contraction split" in ex.Plan(), ex.Plan()
+    host = [synth.round_bf16(synth.normal(seed, (M, K), std=0.125)),
+            synth.round_bf16(synth.normal(seed + 1, (K, N), std=0.125)), synth.round_bf16(synth.normal(seed + 2, (N,)))]
+    return ex, [be.BufferFromFlatData(0, a, make_shape(BF16, *a.shape)) for a in host]
+
+
 def _compare(be, ex, bufs):
     ref = ex.Execute(bufs, None, 0)
     outs = [be.NewSharedBuffer(0, s) for s in ex.Outputs()]
@@ -81,7 +98,8 @@ def _compare(be, ex, bufs):
 def test_noalloc_matches_execute_two_calls_second_smaller(be):
     """A transformer block (intermediates in the scratch array), then a smaller one;
     then a scatter graph, then a smaller scatter graph, then two decoding attention
-    steps: each bit-identical to Execute on the same executable and inputs."""
+    steps, then two few-tile products with a split contraction: each bit-identical
+    to Execute on the same executable and inputs."""
     big = graphs.TransformerBlockConfig(batch=2, seq=256, vocab=2000, d_model=512, heads=4, head_dim=128, ffn=2048)
     small = graphs.TransformerBlockConfig(batch=1, seq=128, vocab=1000, d_model=256, heads=2, head_dim=128, ffn=1024)
     for cfg, seed in ((big, 7100), (small, 7200)):
@@ -94,6 +112,10 @@ def test_noalloc_matches_execute_two_calls_second_smaller(be):
     # decoding attention: the split key range's partial outputs in the arena
     for (B, H, Hkv, Sk, D), seed in (((4, 16, 4, 6000, 128), 7500), ((1, 8, 2, 1500, 64), 7600)):
         ex, bufs = _decode_case(be, B, H, Hkv, Sk, D, seed)
+        _compare(be, ex, bufs)
+    # few-tile products: the contraction split's fp32 partials in the arena
+    for (M, N, K), seed in (((16, 4096, 4096), 7700), ((8, 2048, 2048), 7800)):
+        ex, bufs = _dot_case(be, M, N, K, seed)
         _compare(be, ex, bufs)
 
 
