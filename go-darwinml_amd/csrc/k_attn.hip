@@ -829,27 +829,45 @@ __global__ __launch_bounds__(256) void sdpa_combine_kernel(Params p, int ns) {
   const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + threadIdx.x / 64;
   const int d = (threadIdx.x % 64) * 4;
   if (row >= rows || d >= p.D) return;
-  // The row is the same for the whole wave; the loads of the splits do not depend
-  // on each other, so the unrolled loops issue them back to back.
+  // The row is the same for the whole wave.  The splits' loads do not depend on
+  // each other: they are issued kC at a time before any of them is used (the max
+  // pass, then the weighted sum), so a row waits for ceil(ns / kC) + 1 memory
+  // latencies rather than one per split.
+  constexpr int kC = 16;
   const float* lse = p.part_lse + row;
   const float* po = p.part_o + row * p.D + d;
   const int64_t so = rows * p.D;  // one split's outputs
   float mx = -INFINITY;
-#pragma unroll 4
-  for (int i = 0; i < ns; ++i) mx = fmaxf(mx, lse[i * rows]);
+  for (int i0 = 0; i0 < ns; i0 += kC) {
+    float l[kC];
+#pragma unroll
+    for (int j = 0; j < kC; ++j) l[j] = i0 + j < ns ? lse[(i0 + j) * rows] : -INFINITY;
+#pragma unroll
+    for (int j = 0; j < kC; ++j) mx = fmaxf(mx, l[j]);
+  }
   float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f, wsum = 0.f;
-#pragma unroll 4
-  for (int i = 0; i < ns; ++i) {
-    const float li = lse[i * rows];
-    const float4 v = *reinterpret_cast<const float4*>(po + i * so);
-    // A split with no visible key (lse -inf) adds nothing, whatever its o holds.
-    const bool live = li != -INFINITY;
-    const float w = live ? __builtin_amdgcn_exp2f(li - mx) : 0.f;
-    a0 += live ? w * v.x : 0.f;
-    a1 += live ? w * v.y : 0.f;
-    a2 += live ? w * v.z : 0.f;
-    a3 += live ? w * v.w : 0.f;
-    wsum += w;
+  for (int i0 = 0; i0 < ns; i0 += kC) {
+    float l[kC];
+    float4 v[kC];
+#pragma unroll
+    for (int j = 0; j < kC; ++j)
+      if (i0 + j < ns) {
+        l[j] = lse[(i0 + j) * rows];
+        v[j] = *reinterpret_cast<const float4*>(po + (i0 + j) * so);
+      }
+    // Split order: the same sums every run.
+#pragma unroll
+    for (int j = 0; j < kC; ++j)
+      if (i0 + j < ns) {
+        // A split with no visible key (lse -inf) adds nothing, whatever its o holds.
+        const bool live = l[j] != -INFINITY;
+        const float w = live ? __builtin_amdgcn_exp2f(l[j] - mx) : 0.f;
+        a0 += live ? w * v[j].x : 0.f;
+        a1 += live ? w * v[j].y : 0.f;
+        a2 += live ? w * v[j].z : 0.f;
+        a3 += live ? w * v[j].w : 0.f;
+        wsum += w;
+      }
   }
   const bool none = mx == -INFINITY;
   const float inv = none ? 0.f : 1.0f / wsum;
