@@ -87,31 +87,37 @@ __host__ __device__ inline bool gemm_rows_fit(int64_t s_mn, int64_t s_k, int64_t
 }
 
 #if !defined(__HIPCC_RTC__)
-// Contraction split for 16-bit products whose grid leaves most of the chip idle
-// (the 128 x 128 core, two workgroups per CU: 512 slots).  s ranges of kc = K / s
-// contraction steps (kc a multiple of 64) run as s slices of one grid, each
-// writing its fp32 partial product; a second kernel sums the s partials in split
-// order and rounds once.  s = 1: no split.  The rule is a cost model of measured
-// figures: a lone 128 x 128 tile takes ~14.6 ns per contraction step at any grid
-// up to one round of 512, a split grid cannot beat the operands' own read time
-// (A + B at ~5 TB/s), and the partials cost s x M x N x 8 bytes of traffic plus
-// ~2 us for the summing launch; a split must save 15%.  One batch only.
+// Contraction split for products whose grid leaves most of the chip idle.  s
+// ranges of kc = K / s contraction steps (kc a multiple of 64) run as s slices of
+// one grid, each writing its fp32 partial product; a second kernel sums the s
+// partials in split order and rounds once.  s = 1: no split.  The rule is a cost
+// model of measured figures: a 128 x 128 tile takes ~14.6 ns per contraction step
+// with 16-bit operands, latency-bound, so two workgroups per CU each keep that
+// pace (512 slots); with fp32 operands ~65 ns, which is already ~80% of a CU's
+// fp32 MFMA rate, so only one tile per CU counts (256 slots).  A split grid cannot
+// beat the operands' own read time (A + B at ~5 TB/s), and the partials cost
+// s x M x N x 8 bytes of traffic plus ~2 us for the summing launch; a split must
+// save 15%, and a range keeps at least 512 (16-bit) or 256 (fp32) steps.  es: the
+// operands' element size (2 or 4).  One batch only.
 struct GemmSplit {
   int s;
   int64_t kc;
 };
 constexpr int kGemmMaxSplit = 16;
-inline GemmSplit gemm_k_split(int64_t batch, int64_t M, int64_t N, int64_t K) {
+inline GemmSplit gemm_k_split(int64_t batch, int64_t M, int64_t N, int64_t K, int es) {
   GemmSplit r{1, K};
-  if (batch != 1 || M <= 0 || N <= 0 || K < 1024) return r;
+  if (batch != 1 || M <= 0 || N <= 0 || K < 1024 || (es != 2 && es != 4)) return r;
   const int64_t t = ((M + 127) / 128) * ((N + 127) / 128);
-  if (t > 256) return r;
-  int64_t smax = 512 / t;
-  if (smax > K / 512) smax = K / 512;
+  const int64_t slots = es == 4 ? 256 : 512;
+  if (2 * t > slots) return r;
+  const int64_t kc_min = es == 4 ? 256 : 512;
+  const double step_us = es == 4 ? 0.065 : 0.0146;
+  int64_t smax = slots / t;
+  if (smax > K / kc_min) smax = K / kc_min;
   if (smax > kGemmMaxSplit) smax = kGemmMaxSplit;
-  const double floor_us = static_cast<double>(M * K + K * N) * 2 / 5e6;
+  const double floor_us = static_cast<double>(M * K + K * N) * es / 5e6;
   auto cost = [&](int64_t s) {
-    const double k_us = static_cast<double>(K / s) * 0.0146;
+    const double k_us = static_cast<double>(K / s) * step_us;
     const double part_us = s > 1 ? static_cast<double>(s) * M * N * 8 / 5e6 + 2.0 : 0.0;
     return (k_us > floor_us ? k_us : floor_us) + part_us;
   };

@@ -1804,7 +1804,7 @@ struct Lowerer {
     add_step(fmt("gemm_grouped %s G=%d M=%lld N=%lld K=%lld (products sharing a; a strides m=%lld k=%lld, b strides "
                  "k=%lld n=%lld%s)",
                  dtype_name(dt), G, (long long)M, (long long)N_, (long long)K, (long long)sam, (long long)sak,
-                 (long long)sbk, (long long)sbn, split_note(ws_bytes, 1, M, N_, K).c_str()),
+                 (long long)sbk, (long long)sbn, split_note(ws_bytes, 1, M, N_, K, dt).c_str()),
              rd, wr, [=](ExecState& st, GHipError* e) {
                const void* bp[kGemmMaxGroups];
                void* cp[kGemmMaxGroups];
@@ -1844,7 +1844,7 @@ struct Lowerer {
     add_step(fmt("gemm_batched %s B=%lld M=%lld N=%lld K=%lld (%s; a strides b=%lld m=%lld k=%lld, b strides b=%lld k=%lld n=%lld%s)",
                  dtype_name(dt), (long long)B, (long long)M, (long long)N_, (long long)K, d.how.c_str(), (long long)sab,
                  (long long)sam, (long long)sak, (long long)sbb, (long long)sbk, (long long)sbn,
-                 split_note(ws_bytes, B, M, N_, K).c_str()),
+                 split_note(ws_bytes, B, M, N_, K, dt).c_str()),
              {lv.slot, rv.slot}, wr, [=](ExecState& st, GHipError* e) {
                void* ws = ws_bytes > 0 ? st.ptr(wsv, GHIP_DTYPE_FLOAT32) : nullptr;
                return ghip_gemm_batched_ws(dt, odt, B, M, N_, K, st.ptr(lv, dt), sab, sam, sak, st.ptr(rv, dt), sbb, sbk,
@@ -1864,9 +1864,9 @@ struct Lowerer {
     wr->push_back(w.slot);
     return w;
   }
-  static std::string split_note(int64_t ws_bytes, int64_t B, int64_t M, int64_t N_, int64_t K) {
+  static std::string split_note(int64_t ws_bytes, int64_t B, int64_t M, int64_t N_, int64_t K, int dt) {
     if (ws_bytes <= 0) return "";
-    return fmt("; contraction split in %d", gemm_k_split(B, M, N_, K).s);
+    return fmt("; contraction split in %d", gemm_k_split(B, M, N_, K, dt == GHIP_DTYPE_FLOAT32 ? 4 : 2).s);
   }
 
   // ------------------------------------------------------------------ GEMM epilogue fusion

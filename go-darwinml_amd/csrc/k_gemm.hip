@@ -150,10 +150,12 @@ struct GemmWs {
 };
 
 // A split contraction (gemm_k_split): the s ranges of kc steps run as s "batches"
-// of the 128 x 128 core (range j: a + j kc sa_k, b + j kc sb_k) writing fp32
-// partials into the workspace, then gemm_split_sum_kernel adds them in range order.
+// of the 128 x 128 core (16-bit operands: the 32x32x16 core; fp32: the fp32 MFMA
+// core; range j: a + j kc sa_k, b + j kc sb_k) writing fp32 partials into the
+// workspace, then gemm_split_sum_kernel adds them in range order.
 template <typename InT, typename OutT>
 static hipError_t launch_split(const GemmParams& p, int ma, int mb, const GemmSplit& sp, float* ws, hipStream_t s) {
+  constexpr int64_t es = sizeof(InT);
   GemmParams q = p;
   q.batch = sp.s;
   q.K = sp.kc;
@@ -162,14 +164,16 @@ static hipError_t launch_split(const GemmParams& p, int ma, int mb, const GemmSp
   q.c = ws;
   q.sc_b = p.M * p.N;
   q.sc_m = p.N;
-  const int64_t ea = slice_bytes(p.M, p.sa_m, sp.kc, p.sa_k, 2);
-  const int64_t eb = slice_bytes(p.N, p.sb_n, sp.kc, p.sb_k, 2);
+  const int64_t ea = slice_bytes(p.M, p.sa_m, sp.kc, p.sa_k, es);
+  const int64_t eb = slice_bytes(p.N, p.sb_n, sp.kc, p.sb_k, es);
   q.a_extent = static_cast<uint32_t>(ea);
   q.b_extent = static_cast<uint32_t>(eb);
   q.a_extent64 = ea;
   q.b_extent64 = eb;
   q.vec_c = p.N % 4 == 0;
-  hipError_t e = launch_bf16<128, 128, 2, 2, InT, float>(q, ma == 1, mb == 1, s);
+  hipError_t e;
+  if constexpr (es == 4) e = launch_f32<128, 128, 2, 2, float>(q, ma == 1, mb == 1, s);
+  else e = launch_bf16<128, 128, 2, 2, InT, float>(q, ma == 1, mb == 1, s);
   if (e != hipSuccess) return e;
   const bool v4 = p.N % 4 == 0;
   const int64_t groups = p.M * (v4 ? p.N / 4 : p.N);
@@ -210,7 +214,7 @@ static hipError_t dispatch_bf16(GemmParams p, hipStream_t s, GemmWs ws = {}) {
   if (big) return launch_bf16_4w<true, InT, OutT>(p, ma, mb, s);
   // Few tiles and a long contraction, with a workspace: the contraction split.
   if (ws.ptr) {
-    const GemmSplit sp = gemm_k_split(p.batch, p.M, p.N, p.K);
+    const GemmSplit sp = gemm_k_split(p.batch, p.M, p.N, p.K, 2);
     if (sp.s > 1 && gemm_split_bytes(sp, p.M, p.N) <= ws.bytes) return launch_split<InT, OutT>(p, ma, mb, sp, ws.ptr, s);
   }
   // Grids of more than 128 256 x 256 tiles: the 256 x 256 cores (one workgroup per
@@ -240,7 +244,7 @@ static hipError_t dispatch_grouped(GemmParams p, int G, const void* const* b, vo
   ok = ok && ea < (int64_t{1} << 31) && eb < (int64_t{1} << 31) && p.M >= 256 && p.N >= 256 && G * tiles >= 128;
   // Products the stand-alone entry splits (given the workspace) run as that split,
   // one after another in the same workspace, so each keeps the stand-alone bits.
-  if (ws.ptr && gemm_k_split(1, p.M, p.N, p.K).s > 1) ok = false;
+  if (ws.ptr && gemm_k_split(1, p.M, p.N, p.K, 2).s > 1) ok = false;
   if (!ok) {
     for (int g = 0; g < G; ++g) {
       GemmParams q = p;
@@ -274,7 +278,7 @@ static hipError_t dispatch_grouped(GemmParams p, int G, const void* const* b, vo
 }
 
 template <typename OutT>
-static hipError_t dispatch_f32(GemmParams p, hipStream_t s) {
+static hipError_t dispatch_f32(GemmParams p, hipStream_t s, GemmWs ws = {}) {
   const int ma = majorness(p.a, p.sa_b, p.sa_m, p.sa_k, p.M, p.K, 4, p.batch);
   const int mb = majorness(p.b, p.sb_b, p.sb_n, p.sb_k, p.N, p.K, 4, p.batch);
   const bool nonneg = p.sa_b >= 0 && p.sa_m >= 0 && p.sa_k >= 0 && p.sb_b >= 0 && p.sb_k >= 0 &&
@@ -294,6 +298,11 @@ static hipError_t dispatch_f32(GemmParams p, hipStream_t s) {
   p.vec_c = (p.sc_m % 4 == 0) && (p.sc_b % 4 == 0 || p.batch == 1) &&
             (reinterpret_cast<uintptr_t>(p.c) % (4 * sizeof(OutT)) == 0);
   if (big) return launch_f32<256, 256, 2, 4, OutT, true>(p, ma, mb, s);
+  // Few tiles and a long contraction, with a workspace: the contraction split.
+  if (ws.ptr) {
+    const GemmSplit sp = gemm_k_split(p.batch, p.M, p.N, p.K, 4);
+    if (sp.s > 1 && gemm_split_bytes(sp, p.M, p.N) <= ws.bytes) return launch_split<float, OutT>(p, ma, mb, sp, ws.ptr, s);
+  }
   // The 8-wave 256 x 256 fp32 core only from one full round of its tiles: below
   // that the 4-wave 128 x 128 core (two workgroups per CU) is faster, 1.9x at 128
   // tiles of 256 x 256 ([2048,4096,4096]), 1.3x at 144 and 192, even at 256.
@@ -308,8 +317,10 @@ using namespace ghip;
 // Workspace bytes a split of this product needs (0: never split): 16-bit operands
 // only.
 static int64_t split_ws_bytes(int ab_dtype, int64_t batch, int64_t M, int64_t N, int64_t K) {
-  if (ab_dtype != GHIP_DTYPE_BFLOAT16 && ab_dtype != GHIP_DTYPE_FLOAT16) return 0;
-  return gemm_split_bytes(gemm_k_split(batch, M, N, K), M, N);
+  const int es = ab_dtype == GHIP_DTYPE_FLOAT32 ? 4
+                 : (ab_dtype == GHIP_DTYPE_BFLOAT16 || ab_dtype == GHIP_DTYPE_FLOAT16) ? 2 : 0;
+  if (es == 0) return 0;
+  return gemm_split_bytes(gemm_k_split(batch, M, N, K, es), M, N);
 }
 
 // A workspace given for a product that splits must hold the split's partials and
@@ -376,8 +387,8 @@ extern "C" int ghip_gemm_batched_ws(int ab_dtype, int c_dtype, int64_t batch, in
     else if (c_dtype == GHIP_DTYPE_FLOAT32) e = dispatch_bf16<f16_t, float>(p, s, ws);
     else return set_error(err, GHIP_ERR_UNSUPPORTED, "gemm_batched: output dtype %d", c_dtype);
   } else if (ab_dtype == GHIP_DTYPE_FLOAT32) {
-    if (c_dtype == GHIP_DTYPE_FLOAT32) e = dispatch_f32<float>(p, s);
-    else if (c_dtype == GHIP_DTYPE_BFLOAT16) e = dispatch_f32<bf16_t>(p, s);
+    if (c_dtype == GHIP_DTYPE_FLOAT32) e = dispatch_f32<float>(p, s, ws);
+    else if (c_dtype == GHIP_DTYPE_BFLOAT16) e = dispatch_f32<bf16_t>(p, s, ws);
     else return set_error(err, GHIP_ERR_UNSUPPORTED, "gemm_batched: output dtype %d", c_dtype);
   } else {
     return set_error(err, GHIP_ERR_UNSUPPORTED, "gemm_batched: input dtype %d", ab_dtype);

@@ -168,8 +168,8 @@ int ghip_gemm_grouped(int ab_dtype, int c_dtype, int groups, int64_t M, int64_t 
 
 /* Device workspace bytes ghip_gemm_batched_ws / ghip_gemm_grouped_ws can use for a
  * product of these sizes (per product), or 0 when such a product never splits.
- * A split applies to 16-bit operands, batch 1, at most 256 output tiles of
- * 128 x 128 and a long contraction (K >= 1024, K / s a multiple of 64): the
+ * A split applies to batch 1, at most 256 (16-bit operands) or 128 (fp32) output
+ * tiles of 128 x 128 and a long contraction (K >= 1024, K / s a multiple of 64): the
  * contraction runs as s ranges in one grid, each writing its fp32 partial
  * product [M, N] into the workspace (s x M x N x 4 bytes), and a second kernel
  * adds the s partials in range order and rounds once.  The result is

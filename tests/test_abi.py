@@ -82,9 +82,11 @@ def test_sdpa_workspace_policy():
 
 
 def test_gemm_workspace_policy():
-    """Host-side policy of the contraction split (no GPU call): 16-bit, batch 1, at
-    most 256 tiles of 128 x 128, K >= 1024 with K / s a multiple of 64, and a
-    modelled saving of 15% or more; the workspace holds s fp32 partials [M, N]."""
+    """Host-side policy of the contraction split (no GPU call): batch 1, at most 256
+    (16-bit) or 128 (fp32) tiles of 128 x 128, K >= 1024 with K / s a multiple of 64
+    (at least 512 steps a range for 16-bit operands, 256 for fp32, whose steps are
+    ~4.5x slower), and a modelled saving of 15% or more; the workspace holds s fp32
+    partials [M, N]."""
     L = _lib.load()
     ws = L.ghip_gemm_workspace_bytes
     BF16, F16, F32 = _lib.DT_BFLOAT16, _lib.DT_FLOAT16, _lib.DT_FLOAT32
@@ -99,5 +101,11 @@ def test_gemm_workspace_policy():
     assert ws(BF16, BF16, 2, 16, 4096, 4096) == 0     # batched products never split
     assert ws(BF16, BF16, 1, 16, 4096, 1000) == 0     # short contraction
     assert ws(BF16, BF16, 1, 16, 4096, 1096) == 0     # no split of K into multiples of 64
-    assert ws(F32, F32, 1, 16, 4096, 4096) == 0       # fp32 never splits
+    # fp32: one 128 x 128 tile per CU already runs near the CU's fp32 MFMA rate, so a
+    # split only fills idle CUs (t x s <= 256)
+    assert ws(F32, F32, 1, 16, 4096, 4096) == 8 * 16 * 4096 * 4
+    assert ws(F32, BF16, 1, 1024, 1024, 8192) == 4 * 1024 * 1024 * 4
+    assert ws(F32, F32, 1, 2048, 2048, 2048) == 0    # 256 tiles: every CU busy
+    assert ws(F32, F32, 1, 2048, 4096, 4096) == 0
+    assert ws(_lib.DT_FLOAT64, _lib.DT_FLOAT64, 1, 16, 4096, 4096) == 0
     assert ws(BF16, BF16, 1, 0, 4096, 4096) == 0

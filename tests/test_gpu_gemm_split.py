@@ -63,18 +63,43 @@ def test_split_matches_oracle(cuda, M, N, K, S, dt, odt):
     assert rel_err(got, ref) <= tol
 
 
+# fp32 operands (the fp32 MFMA core's ranges, 256-step ranges allowed; a split only
+# fills idle CUs): (M, N, K, splits)
+F32_SHAPES = [(16, 4096, 4096, 8), (300, 264, 2048, 8), (1024, 1024, 8192, 4), (512, 4096, 4096, 2),
+              (16, 4100, 14336, 7)]
+
+
+@pytest.mark.parametrize("M,N,K,S", F32_SHAPES)
+@pytest.mark.parametrize("odt", [F32, BF16])
+def test_split_f32_matches_oracle(cuda, M, N, K, S, odt):
+    ws = ops.gemm_workspace(F32, odt, 1, M, N, K, cuda)
+    assert ws is not None and ws.numel() == S * M * N * 4, "the shape must take the split"
+    print(f"split gemm f32 M={M} N={N} K={K} s={S} -> {odt}", flush=True)
+    a, b = _ab(cuda, M, N, K, F32, 5601 + M)
+    c = ops.gemm(a, b, out_dtype=odt, workspace=ws)
+    c2 = ops.gemm(a, b, out_dtype=odt, workspace=ws)
+    torch.cuda.synchronize()
+    assert torch.equal(c, c2)
+    rows = np.arange(M) if M <= 64 else np.random.default_rng(M).choice(M, 64, replace=False)
+    ref = _ref(a, b, rows)
+    got = c.float().cpu().numpy()[rows]
+    assert rel_err(got, ref) <= (1e-4 if odt == F32 else 1e-2)
+
+
 @pytest.mark.parametrize("M,N,K", [(16, 4096, 4096), (304, 264, 4096), (1024, 1024, 8192)])
 def test_split_bit_identical_across_layouts(cuda, M, N, K):
     """All four operand layouts run the 128 x 128 core over the same ranges: the
-    same bits, 16-bit and fp32 outputs (M and N multiples of 8, which MN-contiguous
-    operands need for the vector path; ragged against the 128 x 128 tiles)."""
-    outs = {}
-    for layout in ("km", "kk", "mk", "mm"):
-        a, b = _ab(cuda, M, N, K, BF16, 5201, layout)
-        outs[layout] = [ops.gemm(a, b), ops.gemm(a, b, out_dtype=F32)]
-    for layout in ("kk", "mk", "mm"):
-        for i in range(2):
-            assert torch.equal(outs[layout][i], outs["km"][i]), layout
+    same bits, bf16 and fp32 operands, 16-bit and fp32 outputs (M and N multiples
+    of 8, which MN-contiguous operands need for the vector path; ragged against the
+    128 x 128 tiles)."""
+    for dt in (BF16, F32):
+        outs = {}
+        for layout in ("km", "kk", "mk", "mm"):
+            a, b = _ab(cuda, M, N, K, dt, 5201, layout)
+            outs[layout] = [ops.gemm(a, b, out_dtype=BF16), ops.gemm(a, b, out_dtype=F32)]
+        for layout in ("kk", "mk", "mm"):
+            for i in range(2):
+                assert torch.equal(outs[layout][i], outs["km"][i]), (dt, layout)
 
 
 def test_split_deterministic_and_close_to_unsplit(cuda):
