@@ -8,7 +8,8 @@ carries the other BASELINE workloads under "secondary" (softmax, bf16 RMSNorm,
 LayerNorm, bf16/fp32 DotGeneral, the bf16 DotGeneral's per-GPU shard under 8-way
 data parallelism (batch 0 alone), a decoding step's few-row DotGeneral (an FFN
 down projection over 16 sequences, HBM-bound), the attention composite, a decoding
-step of grouped-query attention over an 8192-token KV cache, the transformer block)
+step of grouped-query attention over an 8192-token KV cache, the transformer block,
+a whole decoding step of an 8B-class block for 16 sequences through the graph API)
 and two widened ops (FusedDense + GELU, the embedding-gradient ScatterSum), each
 with its own roofline fraction.
 
@@ -552,6 +553,61 @@ def make_cases(only=None):
         case.keep = (be, ex, bufs)  # keep the backend alive while timing
         return case
 
+    def decode_step_case():
+        """One decoding step of a decoder block (d 4096, 32 heads over 8 kv heads of
+        128, FFN 14336: an 8B-class model) for 16 sequences with 4096-position KV
+        caches, through Builder -> Compile -> Execute (gomlx_hip.graphs.decode_step):
+        RMSNorm, Q / K / V projections, grouped-query attention over the caches,
+        O projection + residual, RMSNorm, SwiGLU FFN + residual.  HBM-bound: bytes
+        = every weight and both caches read once, x read, x' and the new K / V
+        written (705 MB a step)."""
+        from gomlx_hip import graphs
+        from gomlx_hip.backend import Backend
+        be = Backend("")
+        cfg = graphs.DecodeStepConfig()
+        ex = graphs.decode_step(be, cfg)
+        bufs, P32 = [], {}
+        for i, (name, shape) in enumerate(cfg.param_shapes()):
+            if name.startswith("g_"):
+                host32_ = synth.round_bf16(synth.uniform_f32(6001 + i, shape.dims, 0.5, 1.5))
+                bufs.append(be.BufferFromFlatData(0, host32_, shape))
+                P32[name] = host32_
+                continue
+            std = 1.0 if name in ("x", "k_cache", "v_cache") else shape.dims[0] ** -0.5
+            t = nd(6001 + i, shape.dims, std=std, dtype=torch.bfloat16)
+            bufs.append(be.BufferFromFlatData(0, t.cpu().view(torch.int16).numpy().view(np.uint16), shape))
+            # the CPU leg evaluates sequence 0: its x row and caches, every weight
+            P32[name] = host32(t[:1] if name in ("x", "k_cache", "v_cache") else t)
+            del t
+        stream = torch.cuda.ExternalStream(be.stream())
+        nb = cfg.bytes()
+        w_bytes = 2 * sum(int(np.prod(sh.dims)) for n_, sh in cfg.param_shapes()
+                          if n_ not in ("x", "k_cache", "v_cache"))
+        one = w_bytes + 2 * (2 * cfg.kv_heads * cfg.cache * cfg.head_dim + 2 * cfg.d_model
+                             + 2 * cfg.kv_heads * cfg.head_dim)
+
+        def leg(budget_s):
+            reps, dt = cpu_rate(lambda: orc.decode_step(P32, [0], cfg.heads, cfg.kv_heads, cfg.head_dim, cfg.eps),
+                                budget_s)
+            return cpu_entry(one * reps / dt / 1e9, "GB/s",
+                             f"oracle composition of the step (oracle.decode_step: orc_rmsnorm, orc_dot_general, "
+                             f"orc_sdpa, fp64), OpenMP {cpu_threads()} threads, on sequence 0 of the same "
+                             f"parameters (every weight, its caches; {one / 1e6:.0f} MB as bf16 a step), "
+                             f"{reps} repetitions in {dt:.1f} s")
+
+        def launch(i):
+            for y in ex.Execute(bufs, None, 0):
+                be.BufferFinalize(y)
+        case = Case("decode_step_bf16", launch, bytes_per_step=nb, dtype="bf16", kernel="graph Execute (all kernels)",
+                    stream=stream, cpu=leg,
+                    config={"workload": "decoding step of a decoder block, 16 sequences x 4096 cached positions, "
+                                        "d 4096, H 32 / Hkv 8 x 128, FFN 14336 bf16, through "
+                                        "Builder/Compile/Execute; bytes: weights + KV caches + x read, x' and "
+                                        "the new K / V written", "tokens_per_step": cfg.batch,
+                            "steps_in_plan": ex.Plan().count("\n")})
+        case.keep = (be, ex, bufs)
+        return case
+
     def graph_case(name, build, inputs, **kw):
         """A workload given as a backend graph: build(f, *params) -> outputs, run
         through Builder -> Compile -> Execute on the backend's stream."""
@@ -644,6 +700,7 @@ def make_cases(only=None):
         "attention_bf16": attention_case,
         "attention_decode_bf16": decode_case,
         "transformer_block_bf16": transformer_case,
+        "decode_step_bf16": decode_step_case,
         "fused_dense_gelu_bf16": dense_case,
         "scatter_sum_bf16": scatter_case,
     }

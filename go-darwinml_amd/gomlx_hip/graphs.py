@@ -131,3 +131,67 @@ def transformer_block(backend: Backend, cfg: TransformerBlockConfig):
     out = f.Add(x2, dense(f, act, P["w_down"]))
     f.Return([out])
     return b.Compile()
+
+
+class DecodeStepConfig:
+    """One decoding step of a decoder block for `batch` sequences, each with a KV
+    cache of `cache` positions (grouped-query attention, kv_heads <= heads)."""
+
+    def __init__(self, batch=16, cache=4096, d_model=4096, heads=32, kv_heads=8, head_dim=128, ffn=14336,
+                 eps=1e-6, dtype=dtypes.BFloat16):
+        self.batch, self.cache, self.d_model = batch, cache, d_model
+        self.heads, self.kv_heads, self.head_dim, self.ffn = heads, kv_heads, head_dim, ffn
+        self.eps, self.dtype = eps, dtype
+
+    def param_shapes(self):
+        dt, d, f = self.dtype, self.d_model, self.ffn
+        B, S, H, Hkv, Dh = self.batch, self.cache, self.heads, self.kv_heads, self.head_dim
+        return [
+            ("x", make_shape(dt, B, d)),
+            ("g_attn", make_shape(dt, d)),
+            ("wq", make_shape(dt, d, H * Dh)), ("wk", make_shape(dt, d, Hkv * Dh)),
+            ("wv", make_shape(dt, d, Hkv * Dh)),
+            ("k_cache", make_shape(dt, B, Hkv, S, Dh)), ("v_cache", make_shape(dt, B, Hkv, S, Dh)),
+            ("wo", make_shape(dt, H * Dh, d)),
+            ("g_ffn", make_shape(dt, d)),
+            ("w_gate", make_shape(dt, d, f)), ("w_up", make_shape(dt, d, f)),
+            ("w_down", make_shape(dt, f, d)),
+        ]
+
+    def bytes(self) -> int:
+        """HBM bytes a step must move at least: every parameter read once (weights,
+        caches, x, gammas) and the outputs (x', new K, new V) written; 2 bytes an
+        element."""
+        n = sum(int(np.prod(s.dims)) for _, s in self.param_shapes())
+        out = self.batch * (self.d_model + 2 * self.kv_heads * self.head_dim)
+        return 2 * (n + out)
+
+
+def decode_step(backend: Backend, cfg: DecodeStepConfig):
+    """One decoding step: x [B, d] (the sequences' current hidden states) ->
+    RMSNorm -> Q, K, V projections -> grouped-query attention of the B queries
+    over their K / V caches [B, Hkv, S, Dh] (BHSD; the caller has already written
+    the current position into them) -> O projection + residual -> RMSNorm ->
+    SwiGLU FFN + residual.  Returns the compiled Executable, whose outputs are
+    (x' [B, d], k_new [B, Hkv*Dh], v_new [B, Hkv*Dh]): the projections of the
+    current position, for the caller to write into the caches for the next step.
+    Every product has B rows (decoding), so the GEMMs are few-tile products."""
+    b = backend.Builder("decode_step")
+    f = b.Main()
+    P = {name: f.Parameter(name, shape) for name, shape in cfg.param_shapes()}
+    B, d, H, Hkv, Dh = cfg.batch, cfg.d_model, cfg.heads, cfg.kv_heads, cfg.head_dim
+    x = P["x"]
+    h = rms_norm(f, x, P["g_attn"], cfg.eps)
+    q = f.Reshape(dense(f, h, P["wq"]), B, H, 1, Dh)
+    k_new = dense(f, h, P["wk"])
+    v_new = dense(f, h, P["wv"])
+    a = f.FusedScaledDotProductAttention(q, P["k_cache"], P["v_cache"], None, H, Hkv, AxesLayout.BHSD,
+                                         Dh ** -0.5, False)
+    x2 = f.Add(x, dense(f, f.Reshape(a, B, H * Dh), P["wo"]))
+    h2 = rms_norm(f, x2, P["g_ffn"], cfg.eps)
+    gate = dense(f, h2, P["w_gate"])
+    up = dense(f, h2, P["w_up"])
+    act = f.Mul(f.Mul(gate, f.Logistic(gate)), up)
+    out = f.Add(x2, dense(f, act, P["w_down"]))
+    f.Return([out, k_new, v_new])
+    return b.Compile()

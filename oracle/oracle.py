@@ -397,3 +397,28 @@ def block_tokens(P, b, toks, d_model, heads, head_dim, eps):
     n = len(toks)
     flops = 2 * 2 * last * d * d + n * (2 * 2 * d * d + 3 * 2 * d * ff) + sum(4 * H * Dh * (t + 1) for t in toks)
     return out, flops
+
+
+def decode_step(P, rows, heads, kv_heads, head_dim, eps):
+    """fp64 outputs of the decoding step gomlx_hip.graphs.decode_step builds, for
+    the sequences `rows`: RMSNorm, Q / K / V projections, grouped-query attention of
+    each sequence's query over its whole K / V cache (no mask), O projection +
+    residual, RMSNorm, SwiGLU FFN + residual.  P: "x" [B, d], "wq", "wk", "wv",
+    "k_cache" / "v_cache" [B, Hkv, S, Dh], "wo", "w_gate", "w_up", "w_down" (values
+    widened to fp32), "g_attn", "g_ffn".  Returns (x' [n, d], k_new, v_new
+    [n, Hkv*Dh])."""
+    H, Hkv, Dh = heads, kv_heads, head_dim
+    x = np.asarray(P["x"][rows], np.float64)
+    n, d = x.shape
+    h = rmsnorm(x.astype(np.float32), P["g_attn"], eps)
+    proj = lambda a, w: dot_general(np.asarray(a, np.float32), [a.ndim - 1], [], P[w], [0], [])  # noqa: E731
+    q = proj(h, "wq").reshape(n, H, 1, Dh)
+    k_new, v_new = proj(h, "wk"), proj(h, "wv")
+    kc = np.ascontiguousarray(P["k_cache"][rows], np.float32)  # [n, Hkv, S, Dh]: head h reads kv head h // (H / Hkv)
+    vc = np.ascontiguousarray(P["v_cache"][rows], np.float32)
+    a = sdpa(np.ascontiguousarray(q, np.float32), kc, vc, scale=Dh ** -0.5, causal=False)
+    x2 = x + proj(a.reshape(n, H * Dh), "wo")
+    h2 = rmsnorm(x2.astype(np.float32), P["g_ffn"], eps)
+    gate, up = proj(h2, "w_gate"), proj(h2, "w_up")
+    out = x2 + proj(gate / (1.0 + np.exp(-gate)) * up, "w_down")
+    return out, k_new, v_new
