@@ -91,14 +91,15 @@ __host__ __device__ inline bool gemm_rows_fit(int64_t s_mn, int64_t s_k, int64_t
 // ranges of kc = K / s contraction steps (kc a multiple of 64) run as s slices of
 // one grid, each writing its fp32 partial product; a second kernel sums the s
 // partials in split order and rounds once.  s = 1: no split.  The rule is a cost
-// model of measured figures: a 128 x 128 tile takes ~14.6 ns per contraction step
-// with 16-bit operands, latency-bound, so two workgroups per CU each keep that
-// pace (512 slots); with fp32 operands ~65 ns, which is already ~80% of a CU's
-// fp32 MFMA rate, so only one tile per CU counts (256 slots).  A split grid cannot
-// beat the operands' own read time (A + B at ~5 TB/s), and the partials cost
-// s x M x N x 8 bytes of traffic plus ~2 us for the summing launch; a split must
-// save 15%, and a range keeps at least 512 (16-bit) or 256 (fp32) steps.  es: the
-// operands' element size (2 or 4).  One batch only.
+// model fitted to split-count sweeps (graph-replayed launches, one box): a 128 x
+// 128 tile takes ~2 us plus ~14.6 ns per contraction step with 16-bit operands,
+// latency-bound, so two workgroups per CU each keep that pace (512 slots); with
+// fp32 operands ~65 ns a step, which is already ~80% of a CU's fp32 MFMA rate, so
+// only one tile per CU counts (256 slots).  A split grid cannot beat the operands'
+// own read time (A + B at ~5 TB/s), and the partials cost s x M x N x 8 bytes
+// (written, then read by the sum) at ~3 TB/s plus ~2 us for the summing launch; a
+// split must save 15%, and a range keeps at least 128 steps.  es: the operands'
+// element size (2 or 4).  One batch only.
 struct GemmSplit {
   int s;
   int64_t kc;
@@ -110,15 +111,15 @@ inline GemmSplit gemm_k_split(int64_t batch, int64_t M, int64_t N, int64_t K, in
   const int64_t t = ((M + 127) / 128) * ((N + 127) / 128);
   const int64_t slots = es == 4 ? 256 : 512;
   if (2 * t > slots) return r;
-  const int64_t kc_min = es == 4 ? 256 : 512;
+  const int64_t kc_min = 128;
   const double step_us = es == 4 ? 0.065 : 0.0146;
   int64_t smax = slots / t;
   if (smax > K / kc_min) smax = K / kc_min;
   if (smax > kGemmMaxSplit) smax = kGemmMaxSplit;
   const double floor_us = static_cast<double>(M * K + K * N) * es / 5e6;
   auto cost = [&](int64_t s) {
-    const double k_us = static_cast<double>(K / s) * step_us;
-    const double part_us = s > 1 ? static_cast<double>(s) * M * N * 8 / 5e6 + 2.0 : 0.0;
+    const double k_us = 2.0 + static_cast<double>(K / s) * step_us;
+    const double part_us = s > 1 ? static_cast<double>(s) * M * N * 8 / 3e6 + 2.0 : 0.0;
     return (k_us > floor_us ? k_us : floor_us) + part_us;
   };
   double best = 0.85 * cost(1);

@@ -84,14 +84,15 @@ def test_sdpa_workspace_policy():
 def test_gemm_workspace_policy():
     """Host-side policy of the contraction split (no GPU call): batch 1, at most 256
     (16-bit) or 128 (fp32) tiles of 128 x 128, K >= 1024 with K / s a multiple of 64
-    (at least 512 steps a range for 16-bit operands, 256 for fp32, whose steps are
-    ~4.5x slower), and a modelled saving of 15% or more; the workspace holds s fp32
-    partials [M, N]."""
+    and at least 128 steps a range, and a modelled saving of 15% or more; the
+    workspace holds s fp32 partials [M, N]."""
     L = _lib.load()
     ws = L.ghip_gemm_workspace_bytes
     BF16, F16, F32 = _lib.DT_BFLOAT16, _lib.DT_FLOAT16, _lib.DT_FLOAT32
-    assert ws(BF16, BF16, 1, 16, 4096, 4096) == 8 * 16 * 4096 * 4      # decoding-size rows: 8 ranges of 512
-    assert ws(F16, F32, 1, 16, 4096, 4096) == 8 * 16 * 4096 * 4
+    assert ws(BF16, BF16, 1, 16, 4096, 4096) == 16 * 16 * 4096 * 4     # decoding-size rows: 16 ranges of 256
+    assert ws(F16, F32, 1, 16, 4096, 4096) == 16 * 16 * 4096 * 4
+    assert ws(BF16, BF16, 1, 256, 4096, 4096) == 4 * 256 * 4096 * 4   # 64 tiles: the partials' traffic caps it at 4
+    assert ws(BF16, BF16, 1, 4, 2048, 1024) == 8 * 4 * 2048 * 4       # ranges of 128 steps
     assert ws(BF16, BF16, 1, 1024, 1024, 8192) == 8 * 1024 * 1024 * 4  # 64 tiles: 8 ranges
     assert ws(BF16, BF16, 1, 2048, 2048, 8192) == 2 * 2048 * 2048 * 4  # 256 tiles: 2 ranges
     # 14 ranges of 1024: reading W bounds 14 and 16 ranges alike, and 14 write fewer partials

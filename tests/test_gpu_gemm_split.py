@@ -41,10 +41,11 @@ def _ref(a, b, rows=None):
     return orc.dot_general(np.ascontiguousarray(an), [1], [], np.ascontiguousarray(b.float().cpu().numpy()), [0], [])
 
 
-# (M, N, K, splits): decoding-size rows, ragged M / N, a 64-tile and a 256-tile grid,
-# a K that 16 ranges of a multiple of 64 do not divide evenly into powers of two
-SPLIT_SHAPES = [(16, 4096, 4096, 8), (1, 4096, 4096, 8), (300, 264, 4096, 8), (1024, 1024, 8192, 8),
-                (2048, 2048, 8192, 2), (16, 4096, 14336, 14), (8, 4104, 11008, 4)]
+# (M, N, K, splits): decoding-size rows, ragged M / N, 64-tile grids and a 256-tile
+# one, a K that is not a power of two (14 ranges), ranges of 128 steps
+SPLIT_SHAPES = [(16, 4096, 4096, 16), (1, 4096, 4096, 16), (300, 264, 4096, 16), (1024, 1024, 8192, 8),
+                (2048, 2048, 8192, 2), (16, 4096, 14336, 14), (8, 4104, 11008, 4), (256, 4096, 4096, 4),
+                (4, 2048, 1024, 8)]
 
 
 @pytest.mark.parametrize("M,N,K,S", SPLIT_SHAPES)
@@ -63,9 +64,9 @@ def test_split_matches_oracle(cuda, M, N, K, S, dt, odt):
     assert rel_err(got, ref) <= tol
 
 
-# fp32 operands (the fp32 MFMA core's ranges, 256-step ranges allowed; a split only
-# fills idle CUs): (M, N, K, splits)
-F32_SHAPES = [(16, 4096, 4096, 8), (300, 264, 2048, 8), (1024, 1024, 8192, 4), (512, 4096, 4096, 2),
+# fp32 operands (the fp32 MFMA core's ranges; a split only fills idle CUs):
+# (M, N, K, splits)
+F32_SHAPES = [(16, 4096, 4096, 8), (300, 264, 2048, 16), (1024, 1024, 8192, 4), (512, 4096, 4096, 2),
               (16, 4100, 14336, 7)]
 
 
@@ -167,7 +168,7 @@ def test_graph_dot_bias_split(cuda):
         f.Return([d, f.Add(d, f.BroadcastInDim(pb, make_shape(dtypes.BFloat16, M, N), [1]))])
         ex = b.Compile()
         plan = ex.Plan()
-        assert "contraction split in 8" in plan and "epilogue" not in plan, plan
+        assert "contraction split in 16" in plan and "epilogue" not in plan, plan
         bufs = [be.BufferFromFlatData(0, x, make_shape(dtypes.BFloat16, M, K)),
                 be.BufferFromFlatData(0, w, make_shape(dtypes.BFloat16, K, N)),
                 be.BufferFromFlatData(0, bias, make_shape(dtypes.BFloat16, N))]

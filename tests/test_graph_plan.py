@@ -369,12 +369,12 @@ def test_epilogue_core_follows_layout_and_epilogue_weight(be):
     assert "dots=2" in small and "core=4w-km32" in small, small  # 4 x 64 tiles
     tiny = _plan(be, swiglu, [make_shape(BF16, 1, 256, 512), make_shape(BF16, 512, 1024), make_shape(BF16, 512, 1024)])
     assert "dots=2" in tiny and "core=8w-k64" in tiny, tiny  # 8 tiles
-    # The same 8 tiles with K = 2048: each product splits its contraction (4 ranges
-    # in 64 workgroups), so the products stay unfused and the gate runs as its own
+    # The same 8 tiles with K = 2048: each product splits its contraction (8 ranges
+    # of 256 steps), so the products stay unfused and the gate runs as its own
     # elementwise kernel.
     split = _plan(be, swiglu, [make_shape(BF16, 1, 256, 2048), make_shape(BF16, 2048, 1024),
                                make_shape(BF16, 2048, 1024)])
-    assert split.count("contraction split in 4") == 2 and "epilogue" not in split, split
+    assert split.count("contraction split in 8") == 2 and "epilogue" not in split, split
     assert "fused_elementwise" in split, split
 
 
