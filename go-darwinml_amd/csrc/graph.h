@@ -29,6 +29,16 @@ struct GHipBuffer;
 
 namespace ghip {
 
+// The first half of a split contraction (k_gemm.hip), for the graph lowering,
+// which folds the sum of the partials into the consumer's generated kernel:
+// writes the s fp32 partial products [s][M][N] of a (batch 1, 16-bit operands)
+// into ws, exactly as ghip_gemm_batched_ws does before its sum kernel.  Reports
+// an error when the product would not take that path with s ranges (the
+// lowering checks the same conditions when it compiles the plan).
+int gemm_split_partials(int ab_dtype, int64_t M, int64_t N, int64_t K, const void* a, int64_t sa_m, int64_t sa_k,
+                        const void* b, int64_t sb_k, int64_t sb_n, float* ws, int64_t ws_bytes, int s, void* stream,
+                        GHipError* err);
+
 int dtype_size(int dt);
 bool dtype_is_float(int dt);
 bool dtype_is_int(int dt);      // signed or unsigned integer (not bool)

@@ -1883,6 +1883,7 @@ struct Lowerer {
   std::vector<int> reduce_prod, cons_reduce;
   View emit_reduce_fused(int R, int prod_root, int cons_root);
   View emit_gemm_epilogue(int v, const std::vector<int>& mem, bool* fused);
+  bool emit_split_partials(int o, const Shape& os, const std::set<int>& inset, View* wsv, int* splits);
   std::string member_stmt(int u, std::map<int, std::string>& expr, const std::string& name);
 
   // ------------------------------------------------------------------ Gather
@@ -2516,8 +2517,10 @@ View Lowerer::emit_cluster(int root, int v) {
     View view;
     std::vector<int64_t> eff;  // effective strides over os.dims
     bool linear;
+    bool partial = false;      // a split Dot's fp32 partials, read at i + j * size
   };
   std::vector<In> ins;
+  int n_partial = 0;
   std::map<int, std::string> expr;  // value -> C expression
   std::ostringstream body;
   bool need_idx = false;
@@ -2539,6 +2542,29 @@ View Lowerer::emit_cluster(int root, int v) {
         expr[o] = iota_expr(o);
         continue;
       }
+      // A DotGeneral read only here whose contraction splits: its fp32 partials
+      // come from a GEMM step of their own and are summed here, in range order,
+      // then rounded to the Dot's dtype: the value the stand-alone sum kernel
+      // stores, without its launch.
+      View pw;
+      int ps = 0;
+      if (fuse_epilogues && emit_split_partials(o, os, inset, &pw, &ps)) {
+        const int k = static_cast<int>(ins.size());
+        In in{o, pw, contiguous_strides(os.dims), true};
+        in.partial = true;
+        const std::string pk = "((const float*)p_in" + std::to_string(k) + ")";
+        const std::string acc = "acc" + std::to_string(k);
+        body << "    float " << acc << " = " << pk << "[i];\n";
+        body << "    for (int j = 1; j < " << ps << "; ++j) " << acc << " += " << pk << "[i + (long long)j * "
+             << os.size() << "LL];\n";
+        body << "    const " << ctype(N[o].shape.dtype) << " in" << k << " = " << round_expr(N[o].shape.dtype, acc)
+             << ";\n";
+        expr[o] = "in" + std::to_string(k);
+        ins.push_back(in);
+        ++n_partial;
+        continue;
+      }
+      if (failed) return bad();
       View w = get(o);
       if (failed) return bad();
       In in{o, w, {}, true};
@@ -2579,10 +2605,11 @@ View Lowerer::emit_cluster(int root, int v) {
   // __restrict__: with donation they are one buffer.
   std::vector<int> inplace;
   for (auto& in : ins) {
-    bool ok = true;
+    bool ok = !in.partial;
     for (auto& o2 : ins)
       if (o2.view.slot == in.view.slot)
-        ok = ok && o2.linear && o2.view.offset == 0 && dtype_size(N[o2.value].shape.dtype) == dtype_size(os.dtype);
+        ok = ok && !o2.partial && o2.linear && o2.view.offset == 0 &&
+             dtype_size(N[o2.value].shape.dtype) == dtype_size(os.dtype);
     if (ok && std::find(inplace.begin(), inplace.end(), in.view.slot) == inplace.end()) inplace.push_back(in.view.slot);
   }
   auto may_alias = [&](const View& w) { return std::find(inplace.begin(), inplace.end(), w.slot) != inplace.end(); };
@@ -2614,7 +2641,7 @@ View Lowerer::emit_cluster(int root, int v) {
   for (auto& in : ins) {
     rd.push_back(in.view.slot);
     in_views.push_back(in.view);
-    in_dt.push_back(N[in.value].shape.dtype);
+    in_dt.push_back(in.partial ? GHIP_DTYPE_FLOAT32 : N[in.value].shape.dtype);
   }
   std::ostringstream d;
   d << "fused_elementwise " << os.str() << " ops=" << mem.size() << " inputs=" << ins.size() << " [";
@@ -2624,6 +2651,7 @@ View Lowerer::emit_cluster(int root, int v) {
     if (n.kind == Kind::Unary || n.kind == Kind::Binary || n.kind == Kind::Compare) d << "#" << n.sub;
   }
   d << "]";
+  if (n_partial) d << " (sums the split partials of " << n_partial << " product" << (n_partial > 1 ? "s" : "") << ")";
   const int odt = os.dtype;
   add_step(d.str(), rd, {y.slot}, [=](ExecState& st, GHipError* e) -> int {
     if (total == 0) return GHIP_OK;
@@ -2654,6 +2682,54 @@ static int mfma_majorness(int64_t offset, int64_t s_b, int64_t s_mn, int64_t s_k
   if (s_k == 1 && K % 8 == 0 && (MN == 1 || s_mn % 8 == 0) && b_ok) return 1;
   if (s_mn == 1 && MN % 8 == 0 && (K == 1 || s_k % 8 == 0) && b_ok) return 0;
   return -1;
+}
+
+// A DotGeneral o that only the elementwise cluster being emitted reads (its
+// members: inset), with 16-bit operands on the MFMA path, batch 1, o's shape the
+// cluster's, and a contraction that splits: emits the GEMM step that writes o's
+// fp32 partials into a fresh workspace view (*wsv, *splits ranges) and returns
+// true; otherwise emits nothing of o and returns false.
+bool Lowerer::emit_split_partials(int o, const Shape& os, const std::set<int>& inset, View* wsv, int* splits) {
+  const Node& n = N[o];
+  if (n.kind != Kind::Dot || !live[o] || have[o] || fusion[o].kind != Fusion::None || n.shape.dims != os.dims)
+    return false;
+  for (int r : fn->outputs)
+    if (r == o) return false;
+  for (int w : users[o])
+    if (!inset.count(w)) return false;
+  const int dt = N[n.in[0]].shape.dtype, odt = n.shape.dtype;
+  if ((dt != GHIP_DTYPE_BFLOAT16 && dt != GHIP_DTYPE_FLOAT16) || N[n.in[1]].shape.dtype != dt) return false;
+  if (odt != dt && odt != GHIP_DTYPE_FLOAT32) return false;
+  DotPlan d;
+  if (!plan_dot(o, false, &d)) return false;
+  if (d.B != 1 || d.M <= 0 || d.N <= 0 || d.K <= 0) return false;
+  const int64_t wsb = ghip_gemm_workspace_bytes(dt, odt, 1, d.M, d.N, d.K);
+  if (wsb <= 0 || d.sam < 0 || d.sak < 0 || d.sbk < 0 || d.sbn < 0) return false;
+  if (mfma_majorness(d.lv.offset, 0, d.sam, d.sak, d.M, d.K, 1) < 0 ||
+      mfma_majorness(d.rv.offset, 0, d.sbn, d.sbk, d.N, d.K, 1) < 0)
+    return false;
+  if (!gemm_rows_fit(d.sam, d.sak, 2) || !gemm_rows_fit(d.sbn, d.sbk, 2)) return false;
+  const int64_t ea = ((d.M - 1) * d.sam + (d.K - 1) * d.sak + 1) * 2;
+  const int64_t eb = ((d.N - 1) * d.sbn + (d.K - 1) * d.sbk + 1) * 2;
+  if (ea >= (int64_t{1} << 31) || eb >= (int64_t{1} << 31)) return false;
+  const int S = gemm_k_split(1, d.M, d.N, d.K, 2).s;
+  Shape wss;
+  wss.dtype = GHIP_DTYPE_FLOAT32;
+  wss.dims = {(wsb + 3) / 4};
+  const View w = fresh(wss);
+  const View lv = d.lv, rv = d.rv;
+  const int64_t M = d.M, N_ = d.N, K = d.K, sam = d.sam, sak = d.sak, sbk = d.sbk, sbn = d.sbn;
+  add_step(fmt("gemm_split_partials %s M=%lld N=%lld K=%lld (%s; a strides m=%lld k=%lld, b strides k=%lld n=%lld; "
+               "contraction split in %d, summed by the consumer)",
+               dtype_name(dt), (long long)M, (long long)N_, (long long)K, d.how.c_str(), (long long)sam,
+               (long long)sak, (long long)sbk, (long long)sbn, S),
+           {lv.slot, rv.slot}, {w.slot}, [=](ExecState& st, GHipError* e) {
+             return gemm_split_partials(dt, M, N_, K, st.ptr(lv, dt), sam, sak, st.ptr(rv, dt), sbk, sbn,
+                                        reinterpret_cast<float*>(st.ptr(w, GHIP_DTYPE_FLOAT32)), wsb, S, st.stream, e);
+           });
+  *wsv = w;
+  *splits = S;
+  return true;
 }
 
 View Lowerer::emit_gemm_epilogue(int v, const std::vector<int>& mem, bool* fused) {

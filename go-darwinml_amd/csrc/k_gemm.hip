@@ -153,8 +153,9 @@ struct GemmWs {
 // of the 128 x 128 core (16-bit operands: the 32x32x16 core; fp32: the fp32 MFMA
 // core; range j: a + j kc sa_k, b + j kc sb_k) writing fp32 partials into the
 // workspace, then gemm_split_sum_kernel adds them in range order.
-template <typename InT, typename OutT>
-static hipError_t launch_split(const GemmParams& p, int ma, int mb, const GemmSplit& sp, float* ws, hipStream_t s) {
+template <typename InT>
+static hipError_t launch_split_partials(const GemmParams& p, int ma, int mb, const GemmSplit& sp, float* ws,
+                                        hipStream_t s) {
   constexpr int64_t es = sizeof(InT);
   GemmParams q = p;
   q.batch = sp.s;
@@ -171,9 +172,13 @@ static hipError_t launch_split(const GemmParams& p, int ma, int mb, const GemmSp
   q.a_extent64 = ea;
   q.b_extent64 = eb;
   q.vec_c = p.N % 4 == 0;
-  hipError_t e;
-  if constexpr (es == 4) e = launch_f32<128, 128, 2, 2, float>(q, ma == 1, mb == 1, s);
-  else e = launch_bf16<128, 128, 2, 2, InT, float>(q, ma == 1, mb == 1, s);
+  if constexpr (es == 4) return launch_f32<128, 128, 2, 2, float>(q, ma == 1, mb == 1, s);
+  else return launch_bf16<128, 128, 2, 2, InT, float>(q, ma == 1, mb == 1, s);
+}
+
+template <typename InT, typename OutT>
+static hipError_t launch_split(const GemmParams& p, int ma, int mb, const GemmSplit& sp, float* ws, hipStream_t s) {
+  const hipError_t e = launch_split_partials<InT>(p, ma, mb, sp, ws, s);
   if (e != hipSuccess) return e;
   const bool v4 = p.N % 4 == 0;
   const int64_t groups = p.M * (v4 ? p.N / 4 : p.N);
@@ -308,6 +313,36 @@ static hipError_t dispatch_f32(GemmParams p, hipStream_t s, GemmWs ws = {}) {
   // tiles of 256 x 256 ([2048,4096,4096]), 1.3x at 144 and 192, even at 256.
   if (p.M >= 256 && p.N >= 256 && t256 >= 256) return launch_f32<256, 256, 2, 4, OutT>(p, ma, mb, s);
   return launch_f32<128, 128, 2, 2, OutT>(p, ma, mb, s);
+}
+
+int gemm_split_partials(int ab_dtype, int64_t M, int64_t N, int64_t K, const void* a, int64_t sa_m, int64_t sa_k,
+                        const void* b, int64_t sb_k, int64_t sb_n, float* ws, int64_t ws_bytes, int s, void* stream,
+                        GHipError* err) {
+  if (ab_dtype != GHIP_DTYPE_BFLOAT16 && ab_dtype != GHIP_DTYPE_FLOAT16)
+    return set_error(err, GHIP_ERR_INVALID_ARG, "gemm_split_partials: 16-bit operands only");
+  if (M <= 0 || N <= 0 || K <= 0 || !a || !b || !ws)
+    return set_error(err, GHIP_ERR_INVALID_ARG, "gemm_split_partials: empty product or null pointer");
+  GemmParams p{};
+  p.a = a;
+  p.b = b;
+  p.sa_m = sa_m; p.sa_k = sa_k;
+  p.sb_k = sb_k; p.sb_n = sb_n;
+  p.batch = 1; p.M = M; p.N = N; p.K = K;
+  const int ma = majorness(a, 0, sa_m, sa_k, M, K, 8, 1);
+  const int mb = majorness(b, 0, sb_n, sb_k, N, K, 8, 1);
+  const bool ok = ma >= 0 && mb >= 0 && sa_m >= 0 && sa_k >= 0 && sb_k >= 0 && sb_n >= 0 &&
+                  gemm_rows_fit(sa_m, sa_k, 2) && gemm_rows_fit(sb_n, sb_k, 2) &&
+                  slice_bytes(M, sa_m, K, sa_k, 2) < (int64_t{1} << 31) && slice_bytes(N, sb_n, K, sb_k, 2) < (int64_t{1} << 31);
+  const GemmSplit sp = gemm_k_split(1, M, N, K, 2);
+  if (!ok || sp.s != s)
+    return set_error(err, GHIP_ERR_STATE, "gemm_split_partials: the product does not take a %d-range split", s);
+  if (ws_bytes < gemm_split_bytes(sp, M, N) || reinterpret_cast<uintptr_t>(ws) % 16 != 0)
+    return set_error(err, GHIP_ERR_INVALID_ARG, "gemm_split_partials: workspace too small or misaligned");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const hipError_t e = ab_dtype == GHIP_DTYPE_BFLOAT16 ? launch_split_partials<bf16_t>(p, ma, mb, sp, ws, st)
+                                                       : launch_split_partials<f16_t>(p, ma, mb, sp, ws, st);
+  GHIP_CHECK(e, err);
+  return GHIP_OK;
 }
 
 }  // namespace ghip

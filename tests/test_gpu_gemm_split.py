@@ -186,3 +186,65 @@ def test_graph_dot_bias_split(cuda):
     wf = synth.bf16_bits_to_f32(w).astype(np.float64)
     ref = xf @ wf + synth.bf16_bits_to_f32(bias).astype(np.float64)
     assert rel_err(synth.bf16_bits_to_f32(yn), ref) <= 1e-2
+
+
+@pytest.mark.parametrize("dt", [dtypes.BFloat16, dtypes.Float16])
+def test_graph_split_sums_fold_into_consumers(cuda, dt):
+    """A residual add after a split product, and SiLU(x.Wg) * (x.Wu) over two split
+    products: the products' partials are summed by the consumers' generated
+    kernels (no sum launches), bit for bit the plan compiled with
+    GHIP_EPILOGUE_FUSION=0 (sum kernels, then the elementwise kernels); and
+    against fp64 with the graph's rounding points."""
+    import os
+    M, K, N, F = 16, 4096, 2048, 4096
+    rng = np.random.default_rng(11)
+
+    # host storage: bf16 as its uint16 bit pattern, f16 as numpy float16
+    def bits(a):
+        return synth.to_bf16_bits(a) if dt == dtypes.BFloat16 else a.astype(np.float16)
+
+    def val(b):
+        return synth.bf16_bits_to_f32(b) if dt == dtypes.BFloat16 else b.astype(np.float32)
+    x = bits(rng.standard_normal((M, K), dtype=np.float32))
+    w1 = bits(rng.standard_normal((K, N), dtype=np.float32) * K ** -0.5)
+    r = bits(rng.standard_normal((M, N), dtype=np.float32))
+    wg = bits(rng.standard_normal((K, F), dtype=np.float32) * K ** -0.5)
+    wu = bits(rng.standard_normal((K, F), dtype=np.float32) * K ** -0.5)
+    shapes = [make_shape(dt, M, K), make_shape(dt, K, N), make_shape(dt, M, N), make_shape(dt, K, F),
+              make_shape(dt, K, F)]
+    host = [x, w1, r, wg, wu]
+    be = Backend("")
+    outs, plans = {}, {}
+    try:
+        for fuse in (True, False):
+            os.environ["GHIP_EPILOGUE_FUSION"] = "1" if fuse else "0"
+            try:
+                b = be.Builder("split_fold")
+                f = b.Main()
+                px, pw1, pr, pwg, pwu = [f.Parameter(f"p{i}", s) for i, s in enumerate(shapes)]
+                y1 = f.Add(f.DotGeneral(px, [1], [], pw1, [0], []), pr)
+                g = f.DotGeneral(px, [1], [], pwg, [0], [])
+                y2 = f.Mul(f.Mul(g, f.Logistic(g)), f.DotGeneral(px, [1], [], pwu, [0], []))
+                f.Return([y1, y2])
+                ex = b.Compile()
+            finally:
+                del os.environ["GHIP_EPILOGUE_FUSION"]
+            plans[fuse] = ex.Plan()
+            bufs = [be.BufferFromFlatData(0, a, s) for a, s in zip(host, shapes)]
+            outs[fuse] = [be.BufferToFlatData(o).copy() for o in ex.Execute(bufs, None, 0)]
+            ex.Finalize()
+    finally:
+        be.Finalize()
+    assert plans[True].count("gemm_split_partials") == 3 and "sums the split partials of 2 products" in plans[True], \
+        plans[True]
+    assert "gemm_split_partials" not in plans[False] and plans[False].count("contraction split in") == 3, plans[False]
+    for a, b in zip(outs[True], outs[False]):
+        assert np.array_equal(a, b)
+    xf, w1f, rf, wgf, wuf = (val(a).astype(np.float64) for a in host)
+    rnd = (lambda a: synth.round_bf16(a.astype(np.float32)).astype(np.float64)) if dt == dtypes.BFloat16 else \
+        (lambda a: a.astype(np.float16).astype(np.float64))
+    ref1 = rnd(rnd(xf @ w1f) + rf)
+    gq, uq = rnd(xf @ wgf), rnd(xf @ wuf)
+    ref2 = rnd(rnd(gq * rnd(1 / (1 + np.exp(-gq)))) * uq)
+    assert rel_err(val(outs[True][0]).reshape(M, N), ref1) <= 1e-2
+    assert rel_err(val(outs[True][1]).reshape(M, F), ref2) <= 2e-2
