@@ -418,8 +418,9 @@ def make_cases(only=None):
         W [14336,4096] bf16, fp32 accumulate, bf16 out.  HBM-bound: W (117 MB) is
         read once (rotated over enough copies to leave the Infinity Cache).  32 tiles
         of 128 x 128: this backend splits the contraction into 14 ranges of 1024
-        (fp32 partials in a workspace sized by ghip_gemm_workspace_bytes), summed by a
-        second kernel.  vendor: torch.matmul (hipBLASLt), for comparison."""
+        (fp32 partials in a workspace sized by ghip_gemm_workspace_bytes; 32 x 128
+        tiles for these 16 rows), summed by a second kernel.  vendor: torch.matmul
+        (hipBLASLt), for comparison."""
         M, K, N = 16, 14336, 4096
         x = nd(3101, (M, K), std=K ** -0.25, dtype=torch.bfloat16)
         w = nd(3102, (K, N), std=K ** -0.25, dtype=torch.bfloat16)
@@ -444,7 +445,7 @@ def make_cases(only=None):
                              f"{reps} repetitions in {dt:.1f} s")
         return Case("dot_general_bf16_decode", lambda i: ops.gemm(x, ws_[i % rot], out=cs[i % rot], workspace=work),
                     bytes_per_step=nbytes, dtype="bf16", rotation=rot, cpu=leg, out=lambda i: cs[i % rot],
-                    kernel="gemm_bf16_kernel<128, 128, 2, 2, true, false, bf16_t, float> + gemm_split_sum_kernel",
+                    kernel="gemm_bf16_kernel<32, 128, 1, 4, true, false, bf16_t, float> + gemm_split_sum_kernel",
                     config={"workload": f"{shape}, bf16 in ~ N(0, 1/sqrt(14336)), fp32 accumulate, bf16 out; "
                                         f"bytes: x and W read, the output written"})
 

@@ -118,6 +118,19 @@ __global__ __launch_bounds__(256) void gemm_split_sum_kernel(const float* __rest
   }
 }
 
+// The same core for a K-contiguous A only (the two B layouts): tiles of 32 rows,
+// whose A tile is too short for the MN-contiguous DMA pattern.
+template <int BM, int BN, int WM, int WN, typename InT, typename OutT>
+static hipError_t launch_bf16_ak(GemmParams p, bool b_k, hipStream_t s) {
+  p.tiles_m = static_cast<int>((p.M + BM - 1) / BM);
+  p.tiles_n = static_cast<int>((p.N + BN - 1) / BN);
+  const int64_t blocks = p.batch * p.tiles_m * p.tiles_n;
+  const dim3 grid(static_cast<unsigned>(blocks)), block(WM * WN * 64);
+  if (b_k) hipLaunchKernelGGL((gemm_bf16_kernel<BM, BN, WM, WN, true, true, InT, OutT>), grid, block, 0, s, p);
+  else hipLaunchKernelGGL((gemm_bf16_kernel<BM, BN, WM, WN, true, false, InT, OutT>), grid, block, 0, s, p);
+  return hipGetLastError();
+}
+
 template <typename InT, typename OutT>
 static hipError_t launch_generic(const GemmParams& p, hipStream_t s) {
   const dim3 grid(static_cast<unsigned>((p.N + 15) / 16), static_cast<unsigned>((p.M + 15) / 16),
@@ -172,8 +185,16 @@ static hipError_t launch_split_partials(const GemmParams& p, int ma, int mb, con
   q.a_extent64 = ea;
   q.b_extent64 = eb;
   q.vec_c = p.N % 4 == 0;
-  if constexpr (es == 4) return launch_f32<128, 128, 2, 2, float>(q, ma == 1, mb == 1, s);
-  else return launch_bf16<128, 128, 2, 2, InT, float>(q, ma == 1, mb == 1, s);
+  if constexpr (es == 4) {
+    return launch_f32<128, 128, 2, 2, float>(q, ma == 1, mb == 1, s);
+  } else {
+    // At most 32 rows (decoding) and A K-contiguous: 32 x 128 tiles (four waves of
+    // 32 x 32), a quarter of the 128-row tile's wasted MFMA work and LDS, more
+    // workgroups resident per CU: 4-13% faster at [16, 1024..14336, 4096..14336]
+    // (graph-replayed A/B).  Same MFMA and k order per accumulator: the same bits.
+    if (p.M <= 32 && ma == 1) return launch_bf16_ak<32, 128, 1, 4, InT, float>(q, mb == 1, s);
+    return launch_bf16<128, 128, 2, 2, InT, float>(q, ma == 1, mb == 1, s);
+  }
 }
 
 template <typename InT, typename OutT>
