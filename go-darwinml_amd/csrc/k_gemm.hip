@@ -186,6 +186,10 @@ static hipError_t launch_split_partials(const GemmParams& p, int ma, int mb, con
   q.b_extent64 = eb;
   q.vec_c = p.N % 4 == 0;
   if constexpr (es == 4) {
+    // At most 32 rows: 32 x 128 fp32 tiles (four waves of 32 x 32), a quarter of
+    // the 128-row tile's MFMA work, which the slow fp32 MFMAs feel.  Same MFMA and k
+    // order per accumulator: the same bits.
+    if (p.M <= 32) return launch_f32<32, 128, 1, 4, float>(q, ma == 1, mb == 1, s);
     return launch_f32<128, 128, 2, 2, float>(q, ma == 1, mb == 1, s);
   } else {
     // At most 32 rows (decoding) and A K-contiguous: 32 x 128 tiles (four waves of
