@@ -87,6 +87,22 @@ def test_split_f32_matches_oracle(cuda, M, N, K, S, odt):
     assert rel_err(got, ref) <= (1e-4 if odt == F32 else 1e-2)
 
 
+@pytest.mark.parametrize("dt", [BF16, F32])
+def test_split_columns_not_multiple_of_4(cuda, dt):
+    """N = 1030 with B K-contiguous ([N, K] storage; an N-contiguous B needs N to be
+    a multiple of the vector width): the partials' stores and the sum run their
+    scalar forms; against fp64, and two calls give the same bits."""
+    M, N, K = 16, 1030, 4096
+    ws = ops.gemm_workspace(dt, dt, 1, M, N, K, cuda)
+    assert ws is not None
+    a, b = _ab(cuda, M, N, K, dt, 5701, "kk")
+    c = ops.gemm(a, b, workspace=ws)
+    c2 = ops.gemm(a, b, workspace=ws)
+    torch.cuda.synchronize()
+    assert torch.equal(c, c2)
+    assert rel_err(c.float().cpu().numpy(), _ref(a, b)) <= (1e-4 if dt == F32 else 1e-2)
+
+
 @pytest.mark.parametrize("M,N,K", [(16, 4096, 4096), (304, 264, 4096), (1024, 1024, 8192)])
 def test_split_bit_identical_across_layouts(cuda, M, N, K):
     """All four operand layouts run the 128 x 128 core over the same ranges: the
