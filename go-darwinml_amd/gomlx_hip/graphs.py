@@ -149,8 +149,7 @@ class DecodeStepConfig:
         return [
             ("x", make_shape(dt, B, d)),
             ("g_attn", make_shape(dt, d)),
-            ("wq", make_shape(dt, d, H * Dh)), ("wk", make_shape(dt, d, Hkv * Dh)),
-            ("wv", make_shape(dt, d, Hkv * Dh)),
+            ("w_qkv", make_shape(dt, d, (H + 2 * Hkv) * Dh)),  # [Wq | Wk | Wv]
             ("k_cache", make_shape(dt, B, Hkv, S, Dh)), ("v_cache", make_shape(dt, B, Hkv, S, Dh)),
             ("wo", make_shape(dt, H * Dh, d)),
             ("g_ffn", make_shape(dt, d)),
@@ -169,7 +168,8 @@ class DecodeStepConfig:
 
 def decode_step(backend: Backend, cfg: DecodeStepConfig):
     """One decoding step: x [B, d] (the sequences' current hidden states) ->
-    RMSNorm -> Q, K, V projections -> grouped-query attention of the B queries
+    RMSNorm -> Q, K, V projections (FusedAttentionQKVProjection over one [Wq | Wk |
+    Wv] weight: one product, Q / K / V its column views) -> grouped-query attention of the B queries
     over their K / V caches [B, Hkv, S, Dh] (BHSD; the caller has already written
     the current position into them) -> O projection + residual -> RMSNorm ->
     SwiGLU FFN + residual.  Returns the compiled Executable, whose outputs are
@@ -182,9 +182,8 @@ def decode_step(backend: Backend, cfg: DecodeStepConfig):
     B, d, H, Hkv, Dh = cfg.batch, cfg.d_model, cfg.heads, cfg.kv_heads, cfg.head_dim
     x = P["x"]
     h = rms_norm(f, x, P["g_attn"], cfg.eps)
-    q = f.Reshape(dense(f, h, P["wq"]), B, H, 1, Dh)
-    k_new = dense(f, h, P["wk"])
-    v_new = dense(f, h, P["wv"])
+    q, k_new, v_new = f.FusedAttentionQKVProjection(h, P["w_qkv"], None, None, None, H * Dh, Hkv * Dh)
+    q = f.Reshape(q, B, H, 1, Dh)
     a = f.FusedScaledDotProductAttention(q, P["k_cache"], P["v_cache"], None, H, Hkv, AxesLayout.BHSD,
                                          Dh ** -0.5, False)
     x2 = f.Add(x, dense(f, f.Reshape(a, B, H * Dh), P["wo"]))

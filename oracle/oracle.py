@@ -403,17 +403,18 @@ def decode_step(P, rows, heads, kv_heads, head_dim, eps):
     """fp64 outputs of the decoding step gomlx_hip.graphs.decode_step builds, for
     the sequences `rows`: RMSNorm, Q / K / V projections, grouped-query attention of
     each sequence's query over its whole K / V cache (no mask), O projection +
-    residual, RMSNorm, SwiGLU FFN + residual.  P: "x" [B, d], "wq", "wk", "wv",
-    "k_cache" / "v_cache" [B, Hkv, S, Dh], "wo", "w_gate", "w_up", "w_down" (values
-    widened to fp32), "g_attn", "g_ffn".  Returns (x' [n, d], k_new, v_new
-    [n, Hkv*Dh])."""
+    residual, RMSNorm, SwiGLU FFN + residual.  P: "x" [B, d], "w_qkv" ([Wq | Wk |
+    Wv], [d, (H + 2 Hkv) Dh]), "k_cache" / "v_cache" [B, Hkv, S, Dh], "wo", "w_gate",
+    "w_up", "w_down" (values widened to fp32), "g_attn", "g_ffn".  Returns
+    (x' [n, d], k_new, v_new [n, Hkv*Dh])."""
     H, Hkv, Dh = heads, kv_heads, head_dim
     x = np.asarray(P["x"][rows], np.float64)
     n, d = x.shape
     h = rmsnorm(x.astype(np.float32), P["g_attn"], eps)
     proj = lambda a, w: dot_general(np.asarray(a, np.float32), [a.ndim - 1], [], P[w], [0], [])  # noqa: E731
-    q = proj(h, "wq").reshape(n, H, 1, Dh)
-    k_new, v_new = proj(h, "wk"), proj(h, "wv")
+    qkv = proj(h, "w_qkv")
+    q = qkv[:, :H * Dh].reshape(n, H, 1, Dh)
+    k_new, v_new = qkv[:, H * Dh:(H + Hkv) * Dh], qkv[:, (H + Hkv) * Dh:]
     kc = np.ascontiguousarray(P["k_cache"][rows], np.float32)  # [n, Hkv, S, Dh]: head h reads kv head h // (H / Hkv)
     vc = np.ascontiguousarray(P["v_cache"][rows], np.float32)
     a = sdpa(np.ascontiguousarray(q, np.float32), kc, vc, scale=Dh ** -0.5, causal=False)
