@@ -558,11 +558,11 @@ def make_cases(only=None):
         """One decoding step of a decoder block (d 4096, 32 heads over 8 kv heads of
         128, FFN 14336: an 8B-class model) for 16 sequences with 4096-position KV
         caches, through Builder -> Compile -> Execute (gomlx_hip.graphs.decode_step):
-        RMSNorm, Q / K / V projections (FusedAttentionQKVProjection: one product with
-        a [Wq | Wk | Wv] weight), grouped-query attention over the caches,
+        RMSNorm, Q / K / V projections (one product with a [Wq | Wk | Wv] weight,
+        returned whole), grouped-query attention over the caches,
         O projection + residual, RMSNorm, SwiGLU FFN + residual.  HBM-bound: bytes
-        = every weight and both caches read once, x read, x' and the new K / V
-        written (705 MB a step)."""
+        = every weight and both caches read once, x read, x' and the Q / K / V
+        projections written (705 MB a step)."""
         from gomlx_hip import graphs
         from gomlx_hip.backend import Backend
         be = Backend("")
@@ -603,9 +603,9 @@ def make_cases(only=None):
         case = Case("decode_step_bf16", launch, bytes_per_step=nb, dtype="bf16", kernel="graph Execute (all kernels)",
                     stream=stream, cpu=leg,
                     config={"workload": "decoding step of a decoder block, 16 sequences x 4096 cached positions, "
-                                        "d 4096, H 32 / Hkv 8 x 128 (one fused QKV weight), FFN 14336 bf16, "
+                                        "d 4096, H 32 / Hkv 8 x 128 (one [Wq | Wk | Wv] weight), FFN 14336 bf16, "
                                         "through Builder/Compile/Execute; bytes: weights + KV caches + x read, "
-                                        "x' and the new K / V written", "tokens_per_step": cfg.batch,
+                                        "x' and the Q / K / V projections written", "tokens_per_step": cfg.batch,
                             "steps_in_plan": ex.Plan().count("\n")})
         case.keep = (be, ex, bufs)
         return case

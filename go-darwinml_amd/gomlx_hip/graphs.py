@@ -159,31 +159,32 @@ class DecodeStepConfig:
 
     def bytes(self) -> int:
         """HBM bytes a step must move at least: every parameter read once (weights,
-        caches, x, gammas) and the outputs (x', new K, new V) written; 2 bytes an
-        element."""
+        caches, x, gammas) and the outputs (x' and the Q / K / V projections) written;
+        2 bytes an element."""
         n = sum(int(np.prod(s.dims)) for _, s in self.param_shapes())
-        out = self.batch * (self.d_model + 2 * self.kv_heads * self.head_dim)
+        out = self.batch * (self.d_model + (self.heads + 2 * self.kv_heads) * self.head_dim)
         return 2 * (n + out)
 
 
 def decode_step(backend: Backend, cfg: DecodeStepConfig):
     """One decoding step: x [B, d] (the sequences' current hidden states) ->
-    RMSNorm -> Q, K, V projections (FusedAttentionQKVProjection over one [Wq | Wk |
-    Wv] weight: one product, Q / K / V its column views) -> grouped-query attention of the B queries
-    over their K / V caches [B, Hkv, S, Dh] (BHSD; the caller has already written
-    the current position into them) -> O projection + residual -> RMSNorm ->
-    SwiGLU FFN + residual.  Returns the compiled Executable, whose outputs are
-    (x' [B, d], k_new [B, Hkv*Dh], v_new [B, Hkv*Dh]): the projections of the
-    current position, for the caller to write into the caches for the next step.
-    Every product has B rows (decoding), so the GEMMs are few-tile products."""
+    RMSNorm -> Q, K, V projections (one product with the [Wq | Wk | Wv] weight, Q a
+    column view of it, as FusedAttentionQKVProjection lowers) -> grouped-query
+    attention of the B queries over their K / V caches [B, Hkv, S, Dh] (BHSD; the
+    caller has already written the current position into them) -> O projection +
+    residual -> RMSNorm -> SwiGLU FFN + residual.  Returns the compiled Executable,
+    whose outputs are (x' [B, d], qkv [B, (H + 2 Hkv) Dh]): the current position's
+    projections, whose K columns [H Dh, (H + Hkv) Dh) and V columns [(H + Hkv) Dh,
+    (H + 2 Hkv) Dh) the caller writes into the caches for the next step.  Every
+    product has B rows (decoding), so the GEMMs are few-tile products."""
     b = backend.Builder("decode_step")
     f = b.Main()
     P = {name: f.Parameter(name, shape) for name, shape in cfg.param_shapes()}
     B, d, H, Hkv, Dh = cfg.batch, cfg.d_model, cfg.heads, cfg.kv_heads, cfg.head_dim
     x = P["x"]
     h = rms_norm(f, x, P["g_attn"], cfg.eps)
-    q, k_new, v_new = f.FusedAttentionQKVProjection(h, P["w_qkv"], None, None, None, H * Dh, Hkv * Dh)
-    q = f.Reshape(q, B, H, 1, Dh)
+    qkv = dense(f, h, P["w_qkv"])
+    q = f.Reshape(f.Slice(qkv, [0, 0], [B, H * Dh]), B, H, 1, Dh)
     a = f.FusedScaledDotProductAttention(q, P["k_cache"], P["v_cache"], None, H, Hkv, AxesLayout.BHSD,
                                          Dh ** -0.5, False)
     x2 = f.Add(x, dense(f, f.Reshape(a, B, H * Dh), P["wo"]))
@@ -192,5 +193,5 @@ def decode_step(backend: Backend, cfg: DecodeStepConfig):
     up = dense(f, h2, P["w_up"])
     act = f.Mul(f.Mul(gate, f.Logistic(gate)), up)
     out = f.Add(x2, dense(f, act, P["w_down"]))
-    f.Return([out, k_new, v_new])
+    f.Return([out, qkv])
     return b.Compile()

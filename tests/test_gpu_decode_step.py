@@ -1,10 +1,10 @@
 """One decoding step of a decoder block through Builder / Compile / Execute
 (gomlx_hip.graphs.decode_step): every product has B rows, so the projections run
 as contraction splits, and the attention of the B queries over their K / V caches
-as grouped-query rows with a split key range.  Outputs (x', new K, new V) against
-the fp64 composition of the same step (oracle.decode_step) on the same parameter
-bytes, normwise <= 1e-2 (bf16 rounding at every op of the graph, as in the block
-test); two Executes give the same bits."""
+as grouped-query rows with a split key range.  Outputs (x', and the new K / V
+columns of the QKV projection) against the fp64 composition of the same step
+(oracle.decode_step) on the same parameter bytes, normwise <= 1e-2 (bf16 rounding
+at every op of the graph, as in the block test); two Executes give the same bits."""
 import numpy as np
 import pytest
 import torch
@@ -59,9 +59,11 @@ def test_decode_step_matches_oracle(be, cuda, kw):
     ex.Finalize()
     for a, b in zip(outs, again):
         assert np.array_equal(a, b)
-    B, d, kv = cfg.batch, cfg.d_model, cfg.kv_heads * cfg.head_dim
-    got = [synth.bf16_bits_to_f32(o) for o in outs]
+    B, d, q, kv = cfg.batch, cfg.d_model, cfg.heads * cfg.head_dim, cfg.kv_heads * cfg.head_dim
+    x2 = synth.bf16_bits_to_f32(outs[0]).reshape(B, d)
+    qkv = synth.bf16_bits_to_f32(outs[1]).reshape(B, q + 2 * kv)
     rows = np.arange(B) if B <= 4 else np.array([0, 5, B - 1])
     ref = orc.decode_step(P, rows, cfg.heads, cfg.kv_heads, cfg.head_dim, cfg.eps)
-    for g, r, shape, name in zip(got, ref, [(B, d), (B, kv), (B, kv)], ["x'", "k_new", "v_new"]):
-        assert norm_err(g.reshape(shape)[rows], r) <= 1e-2, name
+    got = [x2[rows], qkv[rows, q:q + kv], qkv[rows, q + kv:]]
+    for g, r, name in zip(got, ref, ["x'", "k_new", "v_new"]):
+        assert norm_err(g, r) <= 1e-2, name
