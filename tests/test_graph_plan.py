@@ -541,3 +541,18 @@ def test_dot_grouping_rule(be):
     # more than four siblings: groups of at most four
     p = _plan(be, lambda f, x, *ws: [dense(f, x, w) for w in ws], [sx] + [sw] * 6)
     assert p.count("gemm_grouped bfloat16 G=4") == 1 and p.count("gemm_grouped bfloat16 G=2") == 1, p
+
+
+def test_decode_step_plan(be):
+    """The decoding block step (16 sequences, 8B-class shapes) plans every projection
+    as a contraction split: the QKV product with its own sum (a graph output, Q read
+    by the attention), the O / gate / up / down partials summed inside the residual
+    and SwiGLU kernels; the attention as one fused launch with a split key range."""
+    from gomlx_hip import graphs
+    plan = graphs.decode_step(be, graphs.DecodeStepConfig()).Plan()
+    assert plan.startswith("# 11 steps"), plan
+    assert "gemm_batched bfloat16 B=1 M=16 N=6144 K=4096" in plan and "contraction split in 8)" in plan, plan
+    assert plan.count("gemm_split_partials") == 4, plan
+    assert "sums the split partials of 2 products" in plan and plan.count("sums the split partials of 1 product") == 2
+    assert plan.count("sdpa_fwd") == 1 and "key range split" in plan, plan
+    assert "strided_copy" not in plan and "epilogue" not in plan, plan
