@@ -103,6 +103,24 @@ def test_split_columns_not_multiple_of_4(cuda, dt):
     assert rel_err(c.float().cpu().numpy(), _ref(a, b)) <= (1e-4 if dt == F32 else 1e-2)
 
 
+@pytest.mark.parametrize("dt", [BF16, F32])
+def test_split_32_row_tiles_match_128_row_tiles(cuda, dt):
+    """At most 32 rows run the split on 32 x 128 tiles, more rows on 128 x 128 ones
+    (same MFMA, same k order per accumulator): the 16-row product equals the first 16
+    rows of the 33-row product that extends it, bit for bit (both split into the same
+    ranges: 16 tiles of 128 x 128 either way)."""
+    N, K = 2048, 4096
+    a33 = synth.normal_device(5801, (33, K), std=0.125, device=cuda, dtype=dt)
+    b = synth.normal_device(5802, (K, N), std=0.125, device=cuda, dtype=dt)
+    w16 = ops.gemm_workspace(dt, dt, 1, 16, N, K, cuda)
+    w33 = ops.gemm_workspace(dt, dt, 1, 33, N, K, cuda)
+    assert w16.numel() // (16 * N * 4) == w33.numel() // (33 * N * 4) > 1
+    for odt in (dt, F32):
+        c16 = ops.gemm(a33[:16], b, out_dtype=odt)
+        c33 = ops.gemm(a33, b, out_dtype=odt)
+        assert torch.equal(c16, c33[:16])
+
+
 @pytest.mark.parametrize("M,N,K", [(16, 4096, 4096), (304, 264, 4096), (1024, 1024, 8192)])
 def test_split_bit_identical_across_layouts(cuda, M, N, K):
     """All four operand layouts run the 128 x 128 core over the same ranges: the
